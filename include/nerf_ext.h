@@ -1,0 +1,216 @@
+/*
+ * nerf_ext.h — additive C interface of the MI355X NeRF backend.
+ *
+ * nerf.h (the reference ABI) fixes the model shape at compile time, renders
+ * only uploaded cameras and caps training at 256 steps per ray.  The benchmark
+ * configurations need more: hash-grid shapes, an analytic scene, novel views,
+ * multi-view batches and kernel-level calls on device buffers.  Those live
+ * here, in a separate header that never changes nerf.h.  None of these entry
+ * points has a counterpart in the reference's nerf.h; each comment names the
+ * reference code whose behaviour the kernel behind it follows, or the
+ * publication that defines it where the reference has no such stage.
+ *
+ * Conventions
+ *   - Plain pointers and sizes; "device" pointers come from nerf_ext_malloc
+ *     (or any HIP allocation on the current device), "host" pointers are
+ *     ordinary process memory.
+ *   - stream: a hipStream_t passed as void*; NULL is the null stream.
+ *     Kernel launches are asynchronous; nothing synchronises unless stated.
+ *   - Every function returns a NerfStatus.  On failure nerf_ext_last_error()
+ *     returns a message for the calling thread.
+ *   - Arithmetic contract: hash indices, occupancy bits and sample counts are
+ *     bit-exact with the scalar CPU oracle (oracle/nerf_oracle.cpp); MLP
+ *     outputs and RGB agree within 1e-3 relative.
+ */
+#ifndef NERF_EXT_H
+#define NERF_EXT_H
+
+#include "nerf.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { NERF_EXT_F32 = 0, NERF_EXT_F16 = 1 };
+enum { NERF_EXT_H2D = 1, NERF_EXT_D2H = 2, NERF_EXT_D2D = 3 };
+enum { NERF_EXT_DENSITY_PARAMS = 3072, NERF_EXT_COLOR_PARAMS = 7168 };
+enum { NERF_EXT_MAX_LEVELS = 16 };
+
+/* ---------------------------------------------------------------- runtime */
+typedef struct NerfExtDeviceInfo {
+    char name[64];
+    char arch[32];              /* e.g. "gfx950" */
+    uint32_t compute_units;
+    uint32_t lds_bytes_per_block;
+    uint64_t global_mem_bytes;
+    uint32_t clock_khz;
+    uint32_t memory_clock_khz;
+    uint32_t memory_bus_bits;
+    uint32_t l2_bytes;
+} NerfExtDeviceInfo;
+
+NERF_API const char* nerf_ext_last_error(void);
+NERF_API NerfStatus nerf_ext_device_info(NerfExtDeviceInfo* out);
+NERF_API NerfStatus nerf_ext_malloc(void** out_ptr, uint64_t bytes);
+NERF_API NerfStatus nerf_ext_free(void* ptr);
+NERF_API NerfStatus nerf_ext_memcpy(void* dst, const void* src, uint64_t bytes, uint32_t kind);
+NERF_API NerfStatus nerf_ext_memset(void* dst, int value, uint64_t bytes);
+NERF_API NerfStatus nerf_ext_synchronize(void);
+NERF_API NerfStatus nerf_ext_stream_create(void** out_stream);
+NERF_API NerfStatus nerf_ext_stream_destroy(void* stream);
+NERF_API NerfStatus nerf_ext_stream_synchronize(void* stream);
+NERF_API NerfStatus nerf_ext_event_create(void** out_event);
+NERF_API NerfStatus nerf_ext_event_destroy(void* event);
+NERF_API NerfStatus nerf_ext_event_record(void* event, void* stream);
+NERF_API NerfStatus nerf_ext_event_elapsed_ms(void* start, void* stop, float* out_ms);
+
+/* ------------------------------------------------------ hash-grid encoding */
+/* Multiresolution hash encoding of Mueller et al., "Instant Neural Graphics
+ * Primitives", SIGGRAPH 2022, section 3 (no counterpart in the reference,
+ * whose encoder is the frequency encoding of backend-cuda.cu:252-277).
+ * Level l has resolution N_l = floor(N_min * b^l + 1e-9), with
+ * b = (finest / N_min)^(1 / (L - 1)) when finest_resolution != 0 and
+ * b = per_level_scale otherwise.  A point x in [0,1]^3 (clamped) maps to
+ * p = x * N_l; corners floor(p) (clamped to N_l - 1) + {0,1}^3; index
+ * cx + cy (N_l+1) + cz (N_l+1)^2 when (N_l+1)^3 <= T, else
+ * (cx * 1 ^ cy * 2654435761 ^ cz * 805459861) mod T; trilinear weights. */
+typedef struct NerfExtGridDesc {
+    uint32_t n_levels;          /* L, at most 16 */
+    uint32_t n_features;        /* F, must be 2 */
+    uint32_t log2_table_size;   /* log2 T, 1..24 */
+    uint32_t base_resolution;   /* N_min >= 1 */
+    float per_level_scale;      /* b, used when finest_resolution == 0 */
+    uint32_t finest_resolution; /* optional N_max */
+    uint32_t table_dtype;       /* NERF_EXT_F32 or NERF_EXT_F16 */
+    uint32_t reserved;
+} NerfExtGridDesc;
+
+typedef struct NerfExtGridLevels {
+    uint32_t n_levels;
+    uint32_t table_size;
+    uint32_t resolution[NERF_EXT_MAX_LEVELS];
+    uint32_t dense[NERF_EXT_MAX_LEVELS];
+} NerfExtGridLevels;
+
+NERF_API NerfStatus nerf_ext_grid_levels(const NerfExtGridDesc* grid, NerfExtGridLevels* out);
+/* Table of L * T * F elements of grid->table_dtype, layout [level][entry][feature],
+ * filled with U(-range, range) from the splitmix64 stream keyed by
+ * (0x7ab1e, seed), element order = memory order (bit-exact with the oracle). */
+NERF_API NerfStatus nerf_ext_grid_init_table(const NerfExtGridDesc* grid, uint64_t seed, float range, void* table, void* stream);
+/* features: [n][L*F] of features_dtype. */
+NERF_API NerfStatus nerf_ext_encode_forward(const NerfExtGridDesc* grid, const void* table, const float* positions, uint32_t n, void* features, uint32_t features_dtype, void* stream);
+/* Debug view of the gather: indices [n][L][8] and trilinear weights [n][L][8]. */
+NERF_API NerfStatus nerf_ext_encode_indices(const NerfExtGridDesc* grid, const float* positions, uint32_t n, uint32_t* indices, float* weights, void* stream);
+
+/* ------------------------------------------------------------------- MLPs */
+/* Density network 32 -> 64 -> 16 and colour network [geo 15 | SH4 16 | 0]
+ * -> 64 -> 64 -> 16 (3 used), no biases, ReLU, fp16 weights packed [out][in]
+ * input layer first (reference semantics backend-cuda.cu:668-835, packing
+ * :828-834), fp32 MFMA accumulation.  Weight init: the reference's
+ * splitmix64 Xavier (backend-cuda.cu:1810-1847) on the target shapes. */
+NERF_API NerfStatus nerf_ext_mlp_init(uint32_t network /* 0 density, 1 colour */, float* params_host);
+NERF_API NerfStatus nerf_ext_float_to_half(const float* src, uint16_t* dst, uint64_t n, void* stream);
+/* Density MLP on fp16 features [n][32]: raw outputs [n][16] fp32. */
+NERF_API NerfStatus nerf_ext_density_mlp(const uint16_t* params, const uint16_t* features, uint32_t n, float* out, void* stream);
+/* Fused hash encode + density MLP; out [n][16] = (exp(raw0), raw1..raw15). */
+NERF_API NerfStatus nerf_ext_density_forward(const NerfExtGridDesc* grid, const void* table, const uint16_t* params, const float* positions, uint32_t n, float* out, void* stream);
+
+typedef struct NerfExtModel {
+    NerfExtGridDesc grid;
+    const void* table;              /* device, [L][T][F] */
+    const uint16_t* density_params; /* device, 3072 fp16 */
+    const uint16_t* color_params;   /* device, 7168 fp16 */
+} NerfExtModel;
+
+/* Full field at points with view directions: out [n][4] = (sigma, r, g, b),
+ * sigma = exp(density raw 0), rgb = sigmoid(colour raw 0..2). */
+NERF_API NerfStatus nerf_ext_field_forward(const NerfExtModel* model, const float* positions, const float* directions, uint32_t n, float* out, void* stream);
+
+/* ---------------------------------------------------------- analytic scene */
+typedef struct NerfExtGaussian {
+    float cx, cy, cz;   /* centre */
+    float sigma;        /* isotropic standard deviation */
+    float amplitude;    /* peak density */
+    float r, g, b;      /* albedo */
+} NerfExtGaussian;
+
+/* count Gaussians from the splitmix64 stream (0x6a55, seed): per Gaussian
+ * centre = lo + (hi - lo) u (3 draws), sigma = s0 + (s1 - s0) u,
+ * amplitude = a0 + (a1 - a0) u, albedo u (3 draws); 8 draws per Gaussian. */
+typedef struct NerfExtSceneDesc {
+    uint32_t count;
+    uint32_t reserved;
+    uint64_t seed;
+    float centre_lo, centre_hi;
+    float sigma_lo, sigma_hi;
+    float amplitude_lo, amplitude_hi;
+} NerfExtSceneDesc;
+
+NERF_API NerfStatus nerf_ext_scene_gaussians(const NerfExtSceneDesc* desc, NerfExtGaussian* out_host);
+/* density(p) = sum_g A_g exp(-|p - c_g|^2 / (2 sigma_g^2)), host/device bit-identical. */
+NERF_API NerfStatus nerf_ext_scene_density(const NerfExtGaussian* gaussians, uint32_t count, const float* positions, uint32_t n, float* out, void* stream);
+
+typedef struct NerfExtOccupancy {
+    uint32_t* bitfield;  /* device, ceil(res^3 / 32) words, bit x + y res + z res^2, LSB first */
+    uint32_t resolution;
+    float aabb_min[3];
+    float aabb_max[3];
+} NerfExtOccupancy;
+
+/* Bit set iff density(cell centre) > threshold (reference cell centres
+ * backend-cuda.cu:1607-1608, strict threshold :1632). */
+NERF_API NerfStatus nerf_ext_occupancy_from_scene(const NerfExtGaussian* gaussians, uint32_t count, float threshold, const NerfExtOccupancy* occupancy, void* stream);
+
+/* ----------------------------------------------------------- rays and march */
+typedef struct NerfExtCamera {
+    float c2w[12];          /* rows 0..2 of the row-major camera-to-world 4x4 */
+    float fx, fy, cx, cy;
+    uint32_t width, height;
+} NerfExtCamera;
+
+/* Camera on a sphere of the given radius around centre, looking at it, +y up,
+ * direction from the splitmix64 stream (0xca3e, seed), draw index 2*index. */
+NERF_API NerfStatus nerf_ext_camera_orbit(uint64_t seed, uint32_t index, float radius, const float* centre3, uint32_t width, uint32_t height, float focal, NerfExtCamera* out);
+
+/* Per-ray occupied-step counts of the pixel rays of one view (pixel centres,
+ * y flipped: backend-cuda.cu:561-563; march :448-469).  counts [W*H]. */
+NERF_API NerfStatus nerf_ext_march_count(const NerfExtCamera* camera, const NerfExtOccupancy* occupancy, uint32_t max_steps, uint32_t* counts, void* stream);
+
+/* ------------------------------------------------------------------ render */
+typedef struct NerfExtRenderer NerfExtRenderer;
+
+typedef struct NerfExtRenderDesc {
+    const NerfExtModel* model;
+    const NerfExtOccupancy* occupancy;
+    const NerfExtCamera* cameras;   /* host array of view_count cameras */
+    uint32_t view_count;
+    uint32_t max_steps;             /* march steps per ray */
+    float min_transmittance;        /* early stop threshold, e.g. 1e-4 */
+    float background[3];            /* composited as C + T * background */
+    void* stream;
+} NerfExtRenderDesc;
+
+typedef struct NerfExtRenderStats {
+    uint64_t rays;
+    uint64_t samples;          /* occupied samples marched (before early stop) */
+    float ms_count;            /* march count pass */
+    float ms_scan;             /* exclusive scan of counts */
+    float ms_samples;          /* march write pass */
+    float ms_field;            /* fused encode + MLP */
+    float ms_composite;
+    float ms_total;
+} NerfExtRenderStats;
+
+NERF_API NerfStatus nerf_ext_renderer_create(NerfExtRenderer** out);
+NERF_API NerfStatus nerf_ext_renderer_destroy(NerfExtRenderer* renderer);
+/* Renders view_count views into rgba8 [view][H][W] (device).  Optional device
+ * outputs: rgb_f32 [view][H][W][3] (unclamped composite) and counts
+ * [view][H][W] (occupied samples per ray).  With stats != NULL the call
+ * synchronises and times each stage with HIP events on desc->stream. */
+NERF_API NerfStatus nerf_ext_render(NerfExtRenderer* renderer, const NerfExtRenderDesc* desc, uint32_t* rgba8, float* rgb_f32, uint32_t* counts, NerfExtRenderStats* stats);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NERF_EXT_H */

@@ -1,0 +1,181 @@
+// common.hpp — internal declarations shared by the HIP translation units of
+// libnerf.so.  Not a public header: the C interface is include/nerf.h and
+// include/nerf_ext.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#ifndef NERF_BUILD_SHARED
+#define NERF_BUILD_SHARED 1
+#endif
+#include "../../include/nerf.h"
+#include "../../include/nerf_ext.h"
+#include "nerf_math.h"
+
+namespace nerf_hip {
+
+// ------------------------------------------------------------------ errors
+void set_error(const std::string& msg);
+void clear_error();
+
+// Records a HIP failure as the thread's last error and maps it to the ABI code.
+NerfStatus hip_fail(hipError_t e, const char* what);
+
+#define NERF_HIP_TRY(expr)                                       \
+    do {                                                         \
+        const hipError_t nerf_e_ = (expr);                       \
+        if (nerf_e_ != hipSuccess) return ::nerf_hip::hip_fail(nerf_e_, #expr); \
+    } while (0)
+
+#define NERF_CHECK_ARG(cond, msg)                        \
+    do {                                                 \
+        if (!(cond)) {                                   \
+            ::nerf_hip::set_error(msg);                  \
+            return NERF_STATUS_INVALID_USAGE;            \
+        }                                                \
+    } while (0)
+
+// Launch error check: kernel launches report configuration errors through
+// hipGetLastError().
+#define NERF_LAUNCH_CHECK(name) NERF_HIP_TRY(hipGetLastError())
+
+// ------------------------------------------------------------ vector types
+typedef _Float16 half_t;
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// ------------------------------------------------------------- hash grid
+// Per-level parameters of a hash grid, passed by value to kernels.
+struct GridParams {
+    uint32_t n_levels;
+    uint32_t n_features;
+    uint32_t table_size;   // T
+    uint32_t table_dtype;  // NERF_EXT_F32 / NERF_EXT_F16
+    uint32_t resolution[NERF_EXT_MAX_LEVELS];
+    uint32_t dense[NERF_EXT_MAX_LEVELS];
+};
+
+// Validates a descriptor and computes its level table (host, fp64).
+NerfStatus make_grid(const NerfExtGridDesc* desc, GridParams& out);
+
+// Index and trilinear weight of corner c (bit 0 = x, 1 = y, 2 = z) for one
+// level; shared by every kernel that touches the table.  All arithmetic is the
+// scalar fp32/u32 sequence of the oracle's encode_point().
+struct LevelCell {
+    uint32_t i0[3];
+    float w[3];
+};
+
+__device__ __forceinline__ LevelCell level_cell(const float p[3], uint32_t N) {
+    LevelCell c;
+    const float s = (float)N;
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+        const float x   = fminf(fmaxf(p[a], 0.0f), 1.0f);
+        const float pos = x * s;
+        uint32_t i      = (uint32_t)floorf(pos);
+        i               = i >= N ? N - 1u : i;
+        c.i0[a]         = i;
+        c.w[a]          = pos - (float)i;
+    }
+    return c;
+}
+
+__device__ __forceinline__ uint32_t corner_index(const LevelCell& c, uint32_t corner, uint32_t N, bool dense, uint32_t mask) {
+    const uint32_t cx = c.i0[0] + (corner & 1u);
+    const uint32_t cy = c.i0[1] + ((corner >> 1) & 1u);
+    const uint32_t cz = c.i0[2] + ((corner >> 2) & 1u);
+    if (dense) {
+        const uint32_t stride = N + 1u;
+        return cx + cy * stride + cz * stride * stride;
+    }
+    return ((cx * nerf_math::kPrime1) ^ (cy * nerf_math::kPrime2) ^ (cz * nerf_math::kPrime3)) & mask;
+}
+
+__device__ __forceinline__ float corner_weight(const LevelCell& c, uint32_t corner) {
+    const float wx = (corner & 1u) ? c.w[0] : 1.0f - c.w[0];
+    const float wy = (corner & 2u) ? c.w[1] : 1.0f - c.w[1];
+    const float wz = (corner & 4u) ? c.w[2] : 1.0f - c.w[2];
+    return (wx * wy) * wz;
+}
+
+// --------------------------------------------------------------- cameras
+struct Ray {
+    float o[3];
+    float d[3];
+    float tn, tf;
+};
+
+// Pixel ray of backend-cuda.cu:373-408 with 1/sqrtf in place of rsqrtf; all
+// scalar IEEE fp32 (the library is built with -ffp-contract=off).
+__device__ __forceinline__ bool make_ray(const NerfExtCamera& c, float px, float py_flipped, const float* bmin, const float* bmax, Ray& r) {
+    const float dcx = (px - c.cx) / c.fx;
+    const float dcy = (py_flipped - c.cy) / c.fy;
+    const float dcz = -1.0f;
+    float d[3];
+#pragma unroll
+    for (int a = 0; a < 3; ++a) d[a] = c.c2w[4 * a + 0] * dcx + c.c2w[4 * a + 1] * dcy + c.c2w[4 * a + 2] * dcz;
+    const float len2 = d[0] * d[0] + d[1] * d[1] + d[2] * d[2];
+    if (len2 <= 1e-16f) return false;
+    const float inv = 1.0f / sqrtf(len2);
+    float tmins[3], tmaxs[3];
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+        r.d[a]            = d[a] * inv;
+        r.o[a]            = c.c2w[4 * a + 3];
+        const float inv_d = fabsf(r.d[a]) > 1e-8f ? 1.0f / r.d[a] : (r.d[a] >= 0.0f ? 1e8f : -1e8f);
+        const float t0    = (bmin[a] - r.o[a]) * inv_d;
+        const float t1    = (bmax[a] - r.o[a]) * inv_d;
+        tmins[a]          = fminf(t0, t1);
+        tmaxs[a]          = fmaxf(t0, t1);
+    }
+    float tn       = fmaxf(fmaxf(tmins[0], tmins[1]), tmins[2]);
+    const float tf = fminf(fminf(tmaxs[0], tmaxs[1]), tmaxs[2]);
+    if (!(tn <= tf && tf > 0.0f)) return false;
+    if (tn < 0.0f) tn = 0.0f;
+    r.tn = tn;
+    r.tf = tf;
+    return true;
+}
+
+// Inference pixel ray (pixel centre, y flipped: backend-cuda.cu:561-563).
+__device__ __forceinline__ bool pixel_ray(const NerfExtCamera& c, uint32_t pix, const float* bmin, const float* bmax, Ray& r) {
+    const uint32_t x = pix % c.width;
+    const uint32_t y = pix / c.width;
+    const float px   = (float)x + 0.5f;
+    const float py   = (float)y + 0.5f;
+    return make_ray(c, px, (float)c.height - 1.0f - py, bmin, bmax, r);
+}
+
+// ------------------------------------------------------------ field eval
+// Where the fused field kernel gets its sample positions and directions.
+struct FieldInputs {
+    // Mode A: explicit positions [n][3] and directions [n][3].
+    const float* positions;
+    const float* directions;
+    // Mode B: march output — (t_mid, dt) per sample, owning ray per sample and
+    // per-ray origin/direction records (float4 o, float4 d).
+    const float2* samples;
+    const uint32_t* sample_ray;
+    const float4* rays;  // [ray][2]: (o.xyz, tn), (d.xyz, tf)
+};
+
+struct FieldWeights {
+    const half_t* density;  // 3072
+    const half_t* color;    // 7168
+};
+
+// out4 [n] float4 (sigma, r, g, b).
+hipError_t launch_field(const GridParams& g, const void* table, const FieldWeights& w, const FieldInputs& in, uint32_t n, float4* out4, hipStream_t stream);
+// Density-only (config 1): out [n][16] = (exp(raw0), raw1..15).
+hipError_t launch_density(const GridParams& g, const void* table, const half_t* dparams, const float* positions, const half_t* features, uint32_t n, float* out, hipStream_t stream);
+
+// Number of compute units of the current device (cached).
+uint32_t device_cu_count();
+
+}  // namespace nerf_hip

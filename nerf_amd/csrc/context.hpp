@@ -1,0 +1,64 @@
+// context.hpp — the object behind the opaque void* context of include/nerf.h.
+#pragma once
+
+#include <mutex>
+#include <vector>
+
+#include "common.hpp"
+
+namespace nerf_hip {
+
+struct TrainState;  // training buffers and schedule (train.hip)
+
+NerfExtGridDesc abi_grid_desc();
+
+struct Context {
+    std::mutex mutex;  // serialises all GPU work of one context (backend-cuda.cu:1407)
+    hipStream_t stream = nullptr;
+
+    // dataset (deep copies, backend-cuda.cu:1970-1977)
+    uint8_t* images = nullptr;
+    std::vector<float> cameras;  // host, 16 floats per image
+    uint32_t image_count = 0, width = 0, height = 0;
+    float fx = 0, fy = 0, cx = 0, cy = 0;
+    uint32_t* rgba = nullptr;  // last inference image
+    bool scene_ready = false;
+
+    // occupancy
+    uint32_t occupancy_res = 0;
+    uint32_t* bitfield     = nullptr;
+    float* density_grid    = nullptr;
+
+    // capacities from NerfCreateDesc
+    uint32_t max_sample_steps = 0, max_batch_rays = 0;
+    uint64_t alignment = 0;
+
+    // model: fp32 masters + fp16 working copies
+    NerfExtGridDesc grid{};
+    GridParams grid_params{};
+    uint64_t table_elems = 0;
+    void* table          = nullptr;  // fp16 [L][T][2]
+    float* table_f32     = nullptr;
+    uint16_t* dparams    = nullptr;
+    uint16_t* cparams    = nullptr;
+    float* dparams_f32   = nullptr;
+    float* cparams_f32   = nullptr;
+
+    NerfExtRenderer* renderer = nullptr;
+
+    // training
+    bool training_configured = false;
+    NerfTrainingConfig train_config{};
+    uint32_t host_generation = 0;
+    TrainState* train        = nullptr;
+
+    ~Context();
+    void release();
+    NerfStatus init_model();
+    NerfStatus upload_weights(const float* d32, const float* c32, const float* t32);
+    // Zeroes optimiser moments, gradients, occupancy and the step counter.
+    NerfStatus train_reset_state();
+    void train_release();
+};
+
+}  // namespace nerf_hip

@@ -1,0 +1,176 @@
+// hashgrid.hip — multiresolution hash-grid encoding (Mueller et al., "Instant
+// Neural Graphics Primitives", SIGGRAPH 2022, section 3).  The reference has no
+// hash grid (its encoder is the frequency encoding of backend-cuda.cu:252-277);
+// the semantics below are the published ones, fixed in detail by
+// include/nerf_ext.h and restated scalar by the CPU oracle.
+//
+// Standalone forward kernel layout: grid.y = level, so at any moment the
+// resident workgroups gather from one or two levels' tables and each XCD's L2
+// holds the level being read (C1: 512 KiB per level, C2: 2 MiB).
+#include <math.h>
+
+#include "common.hpp"
+
+namespace nerf_hip {
+
+NerfStatus make_grid(const NerfExtGridDesc* d, GridParams& g) {
+    NERF_CHECK_ARG(d, "grid descriptor is null");
+    NERF_CHECK_ARG(d->n_levels >= 1u && d->n_levels <= NERF_EXT_MAX_LEVELS, "grid: n_levels must be 1..16");
+    NERF_CHECK_ARG(d->n_features == 2u, "grid: n_features must be 2");
+    NERF_CHECK_ARG(d->log2_table_size >= 1u && d->log2_table_size <= 24u, "grid: log2_table_size must be 1..24");
+    NERF_CHECK_ARG(d->base_resolution >= 1u, "grid: base_resolution must be >= 1");
+    NERF_CHECK_ARG(d->table_dtype == NERF_EXT_F32 || d->table_dtype == NERF_EXT_F16, "grid: table_dtype must be F32 or F16");
+    double b = (double)d->per_level_scale;
+    if (d->finest_resolution > 0u && d->n_levels > 1u) b = exp(log((double)d->finest_resolution / (double)d->base_resolution) / (double)(d->n_levels - 1u));
+    NERF_CHECK_ARG(b >= 1.0, "grid: per-level scale must be >= 1");
+    g.n_levels    = d->n_levels;
+    g.n_features  = d->n_features;
+    g.table_size  = 1u << d->log2_table_size;
+    g.table_dtype = d->table_dtype;
+    for (uint32_t l = 0; l < NERF_EXT_MAX_LEVELS; ++l) {
+        g.resolution[l] = 0u;
+        g.dense[l]      = 0u;
+    }
+    for (uint32_t l = 0; l < d->n_levels; ++l) {
+        const double nl = floor((double)d->base_resolution * pow(b, (double)l) + 1e-9);
+        NERF_CHECK_ARG(nl >= 1.0 && nl < 16777216.0, "grid: level resolution out of range (must be < 2^24)");
+        g.resolution[l]  = (uint32_t)nl;
+        const uint64_t v = (uint64_t)g.resolution[l] + 1ull;
+        g.dense[l]       = (v * v * v <= (uint64_t)g.table_size) ? 1u : 0u;
+    }
+    return NERF_STATUS_OK;
+}
+
+// Table init: element i (memory order) = U(-range, range) from splitmix64
+// stream (0x7ab1e, seed), the same generator as the reference's weight init
+// (backend-cuda.cu:1819-1824) evaluated at its closed form per element.
+template <typename T>
+__global__ __launch_bounds__(256) void k_init_table(T* table, uint64_t count, uint64_t state0, float range) {
+    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += stride) {
+        const float u = nerf_math::unit24(nerf_math::splitmix_at(state0, i));
+        table[i]      = (T)((u * 2.0f - 1.0f) * range);
+    }
+}
+
+// One thread per (point, level); blockIdx.y = level.
+template <typename TableT, typename OutT>
+__global__ __launch_bounds__(256) void k_encode_forward(GridParams g, const TableT* __restrict__ table, const float* __restrict__ pos, uint32_t n, OutT* __restrict__ out) {
+    const uint32_t level = blockIdx.y;
+    const uint32_t i     = blockIdx.x * 256u + threadIdx.x;
+    if (i >= n) return;
+    const float p[3]      = {pos[3ull * i], pos[3ull * i + 1], pos[3ull * i + 2]};
+    const uint32_t N      = g.resolution[level];
+    const bool dense      = g.dense[level] != 0u;
+    const uint32_t mask   = g.table_size - 1u;
+    const LevelCell c     = level_cell(p, N);
+    const TableT* base    = table + (uint64_t)level * g.table_size * 2u;
+    uint32_t idx[8];
+#pragma unroll
+    for (uint32_t k = 0; k < 8u; ++k) idx[k] = corner_index(c, k, N, dense, mask);
+    float v0[8], v1[8];
+#pragma unroll
+    for (uint32_t k = 0; k < 8u; ++k) {
+        v0[k] = (float)base[2u * idx[k]];
+        v1[k] = (float)base[2u * idx[k] + 1u];
+    }
+    float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+    for (uint32_t k = 0; k < 8u; ++k) {
+        const float w = corner_weight(c, k);
+        a0            = a0 + w * v0[k];
+        a1            = a1 + w * v1[k];
+    }
+    OutT* o = out + (uint64_t)i * (g.n_levels * 2u) + level * 2u;
+    o[0]    = (OutT)a0;
+    o[1]    = (OutT)a1;
+}
+
+__global__ __launch_bounds__(256) void k_encode_indices(GridParams g, const float* __restrict__ pos, uint32_t n, uint32_t* __restrict__ indices, float* __restrict__ weights) {
+    const uint32_t level = blockIdx.y;
+    const uint32_t i     = blockIdx.x * 256u + threadIdx.x;
+    if (i >= n) return;
+    const float p[3]  = {pos[3ull * i], pos[3ull * i + 1], pos[3ull * i + 2]};
+    const uint32_t N  = g.resolution[level];
+    const LevelCell c = level_cell(p, N);
+    const uint64_t o  = ((uint64_t)i * g.n_levels + level) * 8u;
+#pragma unroll
+    for (uint32_t k = 0; k < 8u; ++k) {
+        if (indices) indices[o + k] = corner_index(c, k, N, g.dense[level] != 0u, g.table_size - 1u);
+        if (weights) weights[o + k] = corner_weight(c, k);
+    }
+}
+
+}  // namespace nerf_hip
+
+using namespace nerf_hip;
+
+extern "C" {
+
+NERF_API NerfStatus nerf_ext_grid_levels(const NerfExtGridDesc* grid, NerfExtGridLevels* out) {
+    NERF_CHECK_ARG(out, "nerf_ext_grid_levels: null output");
+    GridParams g;
+    const NerfStatus s = make_grid(grid, g);
+    if (s != NERF_STATUS_OK) return s;
+    out->n_levels   = g.n_levels;
+    out->table_size = g.table_size;
+    for (uint32_t l = 0; l < NERF_EXT_MAX_LEVELS; ++l) {
+        out->resolution[l] = g.resolution[l];
+        out->dense[l]      = g.dense[l];
+    }
+    return NERF_STATUS_OK;
+}
+
+NERF_API NerfStatus nerf_ext_grid_init_table(const NerfExtGridDesc* grid, uint64_t seed, float range, void* table, void* stream) {
+    GridParams g;
+    const NerfStatus s = make_grid(grid, g);
+    if (s != NERF_STATUS_OK) return s;
+    NERF_CHECK_ARG(table, "nerf_ext_grid_init_table: null table");
+    const uint64_t count  = (uint64_t)g.n_levels * g.table_size * g.n_features;
+    const uint64_t state0 = nerf_math::stream_state(0x7ab1eull, seed);
+    const uint32_t blocks = (uint32_t)((count + 255u) / 256u < 65536u ? (count + 255u) / 256u : 65536u);
+    if (g.table_dtype == NERF_EXT_F32)
+        k_init_table<float><<<blocks, 256, 0, (hipStream_t)stream>>>((float*)table, count, state0, range);
+    else
+        k_init_table<half_t><<<blocks, 256, 0, (hipStream_t)stream>>>((half_t*)table, count, state0, range);
+    NERF_LAUNCH_CHECK("k_init_table");
+    return NERF_STATUS_OK;
+}
+
+NERF_API NerfStatus nerf_ext_encode_forward(const NerfExtGridDesc* grid, const void* table, const float* positions, uint32_t n, void* features, uint32_t features_dtype, void* stream) {
+    GridParams g;
+    const NerfStatus s = make_grid(grid, g);
+    if (s != NERF_STATUS_OK) return s;
+    if (n == 0u) return NERF_STATUS_OK;
+    NERF_CHECK_ARG(table && positions && features, "nerf_ext_encode_forward: null pointer");
+    NERF_CHECK_ARG(features_dtype == NERF_EXT_F32 || features_dtype == NERF_EXT_F16, "nerf_ext_encode_forward: bad features dtype");
+    const dim3 grid_dim((n + 255u) / 256u, g.n_levels);
+    hipStream_t st = (hipStream_t)stream;
+    if (g.table_dtype == NERF_EXT_F32) {
+        if (features_dtype == NERF_EXT_F32)
+            k_encode_forward<float, float><<<grid_dim, 256, 0, st>>>(g, (const float*)table, positions, n, (float*)features);
+        else
+            k_encode_forward<float, half_t><<<grid_dim, 256, 0, st>>>(g, (const float*)table, positions, n, (half_t*)features);
+    } else {
+        if (features_dtype == NERF_EXT_F32)
+            k_encode_forward<half_t, float><<<grid_dim, 256, 0, st>>>(g, (const half_t*)table, positions, n, (float*)features);
+        else
+            k_encode_forward<half_t, half_t><<<grid_dim, 256, 0, st>>>(g, (const half_t*)table, positions, n, (half_t*)features);
+    }
+    NERF_LAUNCH_CHECK("k_encode_forward");
+    return NERF_STATUS_OK;
+}
+
+NERF_API NerfStatus nerf_ext_encode_indices(const NerfExtGridDesc* grid, const float* positions, uint32_t n, uint32_t* indices, float* weights, void* stream) {
+    GridParams g;
+    const NerfStatus s = make_grid(grid, g);
+    if (s != NERF_STATUS_OK) return s;
+    if (n == 0u) return NERF_STATUS_OK;
+    NERF_CHECK_ARG(positions && (indices || weights), "nerf_ext_encode_indices: null pointer");
+    const dim3 grid_dim((n + 255u) / 256u, g.n_levels);
+    k_encode_indices<<<grid_dim, 256, 0, (hipStream_t)stream>>>(g, positions, n, indices, weights);
+    NERF_LAUNCH_CHECK("k_encode_indices");
+    return NERF_STATUS_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,429 @@
+// render.hip — inference rendering: occupancy march with compacted sample
+// streams, fused field evaluation, front-to-back compositing to RGBA8.
+//
+// Stages (one HIP stream):
+//   1. k_march_count   one thread per ray: pixel ray + AABB (backend-cuda.cu
+//                      :373-408, :561-563), occupancy march (:448-469),
+//                      per-ray occupied-step count; ray record (o, tn, d, tf).
+//   2. scan            exclusive prefix sum of counts -> sample offsets.
+//   3. k_march_samples re-marches from the stored ray record and writes the
+//                      compacted stream (t_mid, dt) + owning ray, ray-major.
+//   4. field           fused hash encode + MFMA MLPs -> (sigma, r, g, b).
+//   5. k_composite     per ray, front to back (:601-635) with early stop at
+//                      T < min_transmittance, background C + T * bg, RGBA8.
+// The reference instead samples spp uniform steps per ray with no occupancy
+// test and no early stop (:534-600) and writes 28 B per step whether or not
+// the step is occupied.
+#include <algorithm>
+#include <vector>
+
+#include "common.hpp"
+
+namespace nerf_hip {
+
+namespace {
+
+struct OccView {
+    const uint32_t* bits;
+    uint32_t res;
+    float bmin[3], bmax[3];
+};
+
+// backend-cuda.cu:338-351 (a null bitfield marks every cell of the box occupied).
+__device__ __forceinline__ bool occupied(const OccView& o, const float p[3]) {
+    const float sx = o.bmax[0] - o.bmin[0], sy = o.bmax[1] - o.bmin[1], sz = o.bmax[2] - o.bmin[2];
+    const float rx = (p[0] - o.bmin[0]) / sx, ry = (p[1] - o.bmin[1]) / sy, rz = (p[2] - o.bmin[2]) / sz;
+    if (rx < 0.0f || rx >= 1.0f || ry < 0.0f || ry >= 1.0f || rz < 0.0f || rz >= 1.0f) return false;
+    if (!o.bits) return true;
+    const uint32_t ix  = min(o.res - 1u, (uint32_t)(rx * (float)o.res));
+    const uint32_t iy  = min(o.res - 1u, (uint32_t)(ry * (float)o.res));
+    const uint32_t iz  = min(o.res - 1u, (uint32_t)(rz * (float)o.res));
+    const uint32_t idx = ix + iy * o.res + iz * o.res * o.res;
+    return (o.bits[idx >> 5] >> (idx & 31u)) & 1u;
+}
+
+__device__ __forceinline__ float cone_angle(const NerfExtCamera& c) {
+    const float ifx = c.fx > 0.0f ? 1.0f / c.fx : 0.0f;
+    const float ify = c.fy > 0.0f ? 1.0f / c.fy : 0.0f;
+    return 0.5f * (ifx + ify);
+}
+
+// The march loop of backend-cuda.cu:450-469, one scalar fp32 op at a time.
+template <typename Emit>
+__device__ __forceinline__ uint32_t march_ray(const float4 ro, const float4 rd, float cone, uint32_t max_steps, const OccView& occ, Emit emit) {
+    const float tn = ro.w, tf = rd.w;
+    const float t_range = tf - tn;
+    if (!(t_range > 0.0f)) return 0u;
+    const float dt_min = t_range / (float)max_steps;
+    uint32_t count = 0u, i = 0u;
+    float t = tn;
+    while (t < tf && i < max_steps) {
+        const float dt   = fminf(fmaxf(dt_min, t * cone), tf - t);
+        const float tm   = t + 0.5f * dt;
+        const float p[3] = {ro.x + tm * rd.x, ro.y + tm * rd.y, ro.z + tm * rd.z};
+        if (occupied(occ, p)) {
+            emit(count, tm, dt);
+            ++count;
+        }
+        t += dt;
+        ++i;
+    }
+    return count;
+}
+
+__global__ __launch_bounds__(256) void k_march_count(const NerfExtCamera* __restrict__ cams, uint32_t pixels_per_view, uint32_t n_rays, OccView occ, uint32_t max_steps, float4* __restrict__ rays, uint32_t* __restrict__ counts) {
+    const uint32_t ray = blockIdx.x * 256u + threadIdx.x;
+    if (ray >= n_rays) return;
+    const uint32_t view     = ray / pixels_per_view;
+    const NerfExtCamera cam = cams[view];
+    Ray r;
+    float4 ro = make_float4(0.0f, 0.0f, 0.0f, 0.0f), rd = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    uint32_t count = 0u;
+    if (pixel_ray(cam, ray - view * pixels_per_view, occ.bmin, occ.bmax, r)) {
+        ro    = make_float4(r.o[0], r.o[1], r.o[2], r.tn);
+        rd    = make_float4(r.d[0], r.d[1], r.d[2], r.tf);
+        count = march_ray(ro, rd, cone_angle(cam), max_steps, occ, [](uint32_t, float, float) {});
+    }
+    rays[2ull * ray]      = ro;
+    rays[2ull * ray + 1u] = rd;
+    counts[ray]           = count;
+}
+
+__global__ __launch_bounds__(256) void k_march_samples(const NerfExtCamera* __restrict__ cams, uint32_t pixels_per_view, uint32_t n_rays, OccView occ, uint32_t max_steps, const float4* __restrict__ rays, const uint32_t* __restrict__ counts,
+    const uint32_t* __restrict__ offsets, float2* __restrict__ samples, uint32_t* __restrict__ sample_ray) {
+    const uint32_t ray = blockIdx.x * 256u + threadIdx.x;
+    if (ray >= n_rays) return;
+    const uint32_t count = counts[ray];
+    if (count == 0u) return;
+    const uint32_t view = ray / pixels_per_view;
+    const float cone    = cone_angle(cams[view]);
+    const uint32_t base = offsets[ray];
+    // The re-march is the same scalar sequence as the count pass, so it emits
+    // exactly `count` samples; the k < count test keeps every write inside
+    // this ray's slice regardless.
+    march_ray(rays[2ull * ray], rays[2ull * ray + 1u], cone, max_steps, occ, [&](uint32_t k, float tm, float dt) {
+        if (k < count) {
+            samples[base + k]    = make_float2(tm, dt);
+            sample_ray[base + k] = ray;
+        }
+    });
+}
+
+// Front-to-back composite with early stop (reference :601-635 plus the stop).
+__global__ __launch_bounds__(256) void k_composite(uint32_t n_rays, const uint32_t* __restrict__ counts, const uint32_t* __restrict__ offsets, const float2* __restrict__ samples, const float4* __restrict__ field, float t_stop, float3 bg,
+    uint32_t* __restrict__ rgba8, float* __restrict__ rgb_out) {
+    const uint32_t ray = blockIdx.x * 256u + threadIdx.x;
+    if (ray >= n_rays) return;
+    const uint32_t count = counts[ray];
+    const uint32_t base  = count ? offsets[ray] : 0u;
+    float T = 1.0f, cr = 0.0f, cg = 0.0f, cb = 0.0f;
+    for (uint32_t i = 0; i < count; ++i) {
+        const float4 f = field[base + i];
+        const float dt = fmaxf(samples[base + i].y, 0.0f);
+        const float a  = 1.0f - __expf(-(f.x * dt));
+        const float w  = T * a;
+        cr += w * f.y;
+        cg += w * f.z;
+        cb += w * f.w;
+        T *= 1.0f - a;
+        if (T < t_stop) break;
+    }
+    const float r = cr + T * bg.x, g = cg + T * bg.y, b = cb + T * bg.z;
+    if (rgb_out) {
+        rgb_out[3ull * ray]      = r;
+        rgb_out[3ull * ray + 1u] = g;
+        rgb_out[3ull * ray + 2u] = b;
+    }
+    const uint32_t ur = (uint32_t)rintf(fminf(1.0f, fmaxf(0.0f, r)) * 255.0f);
+    const uint32_t ug = (uint32_t)rintf(fminf(1.0f, fmaxf(0.0f, g)) * 255.0f);
+    const uint32_t ub = (uint32_t)rintf(fminf(1.0f, fmaxf(0.0f, b)) * 255.0f);
+    rgba8[ray]        = (255u << 24) | (ub << 16) | (ug << 8) | ur;
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------- scan
+// Exclusive prefix sum of n u32 values (n < 2^32 total).  Three passes over
+// 1024-element blocks: block sums, scan of the sums in one workgroup, then
+// the per-block scan with the block's base added.  total (device) receives the
+// grand total as u64 so that overflow of the u32 offsets is detectable.
+namespace {
+
+constexpr uint32_t kScanBlock = 1024u;  // elements per workgroup (256 threads x 4)
+
+__device__ __forceinline__ uint32_t wave_inclusive_scan(uint32_t v) {
+    const uint32_t lane = threadIdx.x & 63u;
+#pragma unroll
+    for (uint32_t d = 1; d < 64u; d <<= 1) {
+        const uint32_t o = __shfl_up(v, d, 64);
+        if (lane >= d) v += o;
+    }
+    return v;
+}
+
+// Block-wide exclusive scan of one value per thread (256 threads); returns the
+// exclusive prefix and writes the block total to *total.
+__device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* lds4, uint32_t* total) {
+    const uint32_t inc  = wave_inclusive_scan(v);
+    const uint32_t wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63u) == 63u) lds4[wave] = inc;
+    __syncthreads();
+    uint32_t wave_base = 0u;
+    for (uint32_t w = 0; w < wave; ++w) wave_base += lds4[w];
+    *total = lds4[0] + lds4[1] + lds4[2] + lds4[3];
+    __syncthreads();
+    return wave_base + inc - v;
+}
+
+__global__ __launch_bounds__(256) void k_scan_reduce(const uint32_t* __restrict__ in, uint32_t n, uint32_t* __restrict__ block_sums) {
+    __shared__ uint32_t lds4[4];
+    const uint64_t base = (uint64_t)blockIdx.x * kScanBlock + 4u * threadIdx.x;
+    uint32_t v          = 0u;
+#pragma unroll
+    for (uint32_t k = 0; k < 4u; ++k) v += base + k < n ? in[base + k] : 0u;
+    uint32_t total;
+    block_exclusive_scan(v, lds4, &total);
+    if (threadIdx.x == 0u) block_sums[blockIdx.x] = total;
+}
+
+__global__ __launch_bounds__(256) void k_scan_sums(uint32_t* __restrict__ block_sums, uint32_t n_blocks, unsigned long long* __restrict__ total_out) {
+    __shared__ uint32_t lds4[4];
+    uint64_t carry = 0u;
+    for (uint32_t b0 = 0; b0 < n_blocks; b0 += 256u) {
+        const uint32_t i = b0 + threadIdx.x;
+        const uint32_t v = i < n_blocks ? block_sums[i] : 0u;
+        uint32_t total;
+        const uint32_t ex = block_exclusive_scan(v, lds4, &total);
+        if (i < n_blocks) block_sums[i] = (uint32_t)(carry + ex);
+        carry += total;
+        __syncthreads();
+    }
+    if (threadIdx.x == 0u) *total_out = carry;
+}
+
+__global__ __launch_bounds__(256) void k_scan_apply(const uint32_t* __restrict__ in, uint32_t n, const uint32_t* __restrict__ block_sums, uint32_t* __restrict__ out) {
+    __shared__ uint32_t lds4[4];
+    const uint64_t base = (uint64_t)blockIdx.x * kScanBlock + 4u * threadIdx.x;
+    uint32_t v[4], s = 0u;
+#pragma unroll
+    for (uint32_t k = 0; k < 4u; ++k) {
+        v[k] = base + k < n ? in[base + k] : 0u;
+        s += v[k];
+    }
+    uint32_t total;
+    uint32_t run = block_exclusive_scan(s, lds4, &total) + block_sums[blockIdx.x];
+#pragma unroll
+    for (uint32_t k = 0; k < 4u; ++k) {
+        if (base + k < n) out[base + k] = run;
+        run += v[k];
+    }
+}
+
+}  // namespace
+
+uint64_t scan_tmp_words(uint32_t n) { return (n + kScanBlock - 1u) / kScanBlock + 2u; }
+
+hipError_t exclusive_scan_u32(const uint32_t* in, uint32_t* out, uint32_t n, uint32_t* tmp, unsigned long long* total, hipStream_t stream) {
+    const uint32_t blocks = (n + kScanBlock - 1u) / kScanBlock;
+    if (blocks == 0u) return hipMemsetAsync(total, 0, sizeof(unsigned long long), stream);
+    k_scan_reduce<<<blocks, 256, 0, stream>>>(in, n, tmp);
+    k_scan_sums<<<1, 256, 0, stream>>>(tmp, blocks, total);
+    k_scan_apply<<<blocks, 256, 0, stream>>>(in, n, tmp, out);
+    return hipGetLastError();
+}
+
+}  // namespace nerf_hip
+
+// ----------------------------------------------------------------- renderer
+struct NerfExtRenderer {
+    template <typename T>
+    struct Buf {
+        T* ptr       = nullptr;
+        uint64_t cap = 0;
+        hipError_t reserve(uint64_t n) {
+            if (n <= cap) return hipSuccess;
+            if (ptr) (void)hipFree(ptr);
+            ptr = nullptr;
+            cap = 0;
+            const uint64_t want = n + n / 8u + 256u;
+            hipError_t e        = hipMalloc(&ptr, want * sizeof(T));
+            if (e == hipSuccess) cap = want;
+            return e;
+        }
+        void release() {
+            if (ptr) (void)hipFree(ptr);
+            ptr = nullptr;
+            cap = 0;
+        }
+    };
+    Buf<NerfExtCamera> cams;
+    Buf<float4> rays;
+    Buf<uint32_t> counts, offsets, scan_tmp;
+    Buf<unsigned long long> total;
+    Buf<float2> samples;
+    Buf<uint32_t> sample_ray;
+    Buf<float4> field;
+    hipEvent_t ev[6] = {};
+    unsigned long long* host_total = nullptr;
+
+    ~NerfExtRenderer() {
+        cams.release();
+        rays.release();
+        counts.release();
+        offsets.release();
+        scan_tmp.release();
+        total.release();
+        samples.release();
+        sample_ray.release();
+        field.release();
+        for (hipEvent_t& e : ev)
+            if (e) (void)hipEventDestroy(e);
+        if (host_total) (void)hipHostFree(host_total);
+    }
+};
+
+using namespace nerf_hip;
+
+extern "C" {
+
+NERF_API NerfStatus nerf_ext_renderer_create(NerfExtRenderer** out) {
+    NERF_CHECK_ARG(out, "nerf_ext_renderer_create: null output");
+    *out = nullptr;
+    NerfExtRenderer* r = new (std::nothrow) NerfExtRenderer();
+    if (!r) {
+        set_error("nerf_ext_renderer_create: out of host memory");
+        return NERF_STATUS_FAILURE;
+    }
+    for (hipEvent_t& e : r->ev) {
+        const hipError_t err = hipEventCreate(&e);
+        if (err != hipSuccess) {
+            delete r;
+            return hip_fail(err, "hipEventCreate");
+        }
+    }
+    const hipError_t err = hipHostMalloc((void**)&r->host_total, sizeof(unsigned long long), hipHostMallocDefault);
+    if (err != hipSuccess) {
+        delete r;
+        return hip_fail(err, "hipHostMalloc");
+    }
+    *out = r;
+    return NERF_STATUS_OK;
+}
+
+NERF_API NerfStatus nerf_ext_renderer_destroy(NerfExtRenderer* renderer) {
+    if (!renderer) return NERF_STATUS_OK;
+    (void)hipDeviceSynchronize();
+    delete renderer;
+    return NERF_STATUS_OK;
+}
+
+NERF_API NerfStatus nerf_ext_march_count(const NerfExtCamera* camera, const NerfExtOccupancy* occupancy, uint32_t max_steps, uint32_t* counts, void* stream) {
+    NERF_CHECK_ARG(camera && occupancy && counts, "nerf_ext_march_count: null pointer");
+    NERF_CHECK_ARG(max_steps > 0u, "nerf_ext_march_count: max_steps must be > 0");
+    NERF_CHECK_ARG(camera->width > 0u && camera->height > 0u, "nerf_ext_march_count: empty image");
+    const uint64_t n64 = (uint64_t)camera->width * camera->height;
+    NERF_CHECK_ARG(n64 < (1ull << 31), "nerf_ext_march_count: too many rays");
+    const uint32_t n = (uint32_t)n64;
+    hipStream_t st   = (hipStream_t)stream;
+    NerfExtCamera* dcam = nullptr;
+    float4* rays        = nullptr;
+    NERF_HIP_TRY(hipMallocAsync((void**)&dcam, sizeof(NerfExtCamera), st));
+    NERF_HIP_TRY(hipMallocAsync((void**)&rays, sizeof(float4) * 2ull * n, st));
+    NERF_HIP_TRY(hipMemcpyAsync(dcam, camera, sizeof(NerfExtCamera), hipMemcpyHostToDevice, st));
+    OccView occ{occupancy->bitfield, occupancy->resolution, {occupancy->aabb_min[0], occupancy->aabb_min[1], occupancy->aabb_min[2]}, {occupancy->aabb_max[0], occupancy->aabb_max[1], occupancy->aabb_max[2]}};
+    k_march_count<<<(n + 255u) / 256u, 256, 0, st>>>(dcam, n, n, occ, max_steps, rays, counts);
+    NERF_LAUNCH_CHECK("k_march_count");
+    NERF_HIP_TRY(hipFreeAsync(rays, st));
+    NERF_HIP_TRY(hipFreeAsync(dcam, st));
+    return NERF_STATUS_OK;
+}
+
+NERF_API NerfStatus nerf_ext_render(NerfExtRenderer* R, const NerfExtRenderDesc* d, uint32_t* rgba8, float* rgb_f32, uint32_t* counts_out, NerfExtRenderStats* stats) {
+    NERF_CHECK_ARG(R && d && d->model && d->occupancy && d->cameras && rgba8, "nerf_ext_render: null argument");
+    NERF_CHECK_ARG(d->view_count >= 1u, "nerf_ext_render: view_count must be >= 1");
+    NERF_CHECK_ARG(d->max_steps >= 1u, "nerf_ext_render: max_steps must be >= 1");
+    GridParams g;
+    const NerfStatus gs = make_grid(&d->model->grid, g);
+    if (gs != NERF_STATUS_OK) return gs;
+    NERF_CHECK_ARG(g.n_levels * g.n_features == 32u, "nerf_ext_render: the density MLP takes 32 features (16 levels x 2)");
+    NERF_CHECK_ARG(d->model->table && d->model->density_params && d->model->color_params, "nerf_ext_render: model has null buffers");
+    const uint32_t W = d->cameras[0].width, H = d->cameras[0].height;
+    for (uint32_t v = 0; v < d->view_count; ++v) NERF_CHECK_ARG(d->cameras[v].width == W && d->cameras[v].height == H && W > 0u && H > 0u, "nerf_ext_render: all views must share a non-empty image size");
+    const uint64_t n64 = (uint64_t)W * H * d->view_count;
+    NERF_CHECK_ARG(n64 < (1ull << 31), "nerf_ext_render: too many rays");
+    const uint32_t n_rays = (uint32_t)n64;
+    hipStream_t st        = (hipStream_t)d->stream;
+
+    NERF_HIP_TRY(R->cams.reserve(d->view_count));
+    NERF_HIP_TRY(R->rays.reserve(2ull * n_rays));
+    NERF_HIP_TRY(R->counts.reserve(n_rays));
+    NERF_HIP_TRY(R->offsets.reserve(n_rays));
+    NERF_HIP_TRY(R->scan_tmp.reserve(scan_tmp_words(n_rays)));
+    NERF_HIP_TRY(R->total.reserve(1));
+    NERF_HIP_TRY(hipMemcpyAsync(R->cams.ptr, d->cameras, sizeof(NerfExtCamera) * d->view_count, hipMemcpyHostToDevice, st));
+
+    const NerfExtOccupancy& o = *d->occupancy;
+    const OccView occ{o.bitfield, o.resolution, {o.aabb_min[0], o.aabb_min[1], o.aabb_min[2]}, {o.aabb_max[0], o.aabb_max[1], o.aabb_max[2]}};
+    const uint32_t ppv    = W * H;
+    const uint32_t blocks = (n_rays + 255u) / 256u;
+    const bool timed      = stats != nullptr;
+
+    if (timed) NERF_HIP_TRY(hipEventRecord(R->ev[0], st));
+    k_march_count<<<blocks, 256, 0, st>>>(R->cams.ptr, ppv, n_rays, occ, d->max_steps, R->rays.ptr, R->counts.ptr);
+    NERF_LAUNCH_CHECK("k_march_count");
+    if (timed) NERF_HIP_TRY(hipEventRecord(R->ev[1], st));
+    NERF_HIP_TRY(exclusive_scan_u32(R->counts.ptr, R->offsets.ptr, n_rays, R->scan_tmp.ptr, R->total.ptr, st));
+    if (timed) NERF_HIP_TRY(hipEventRecord(R->ev[2], st));
+    NERF_HIP_TRY(hipMemcpyAsync(R->host_total, R->total.ptr, sizeof(unsigned long long), hipMemcpyDeviceToHost, st));
+    NERF_HIP_TRY(hipStreamSynchronize(st));
+    const uint64_t total = *R->host_total;
+    if (total >= (1ull << 32)) {
+        set_error("nerf_ext_render: more than 2^32 samples in one call; render fewer views per call");
+        return NERF_STATUS_INVALID_USAGE;
+    }
+    const uint32_t n_samples = (uint32_t)total;
+    NERF_HIP_TRY(R->samples.reserve(n_samples));
+    NERF_HIP_TRY(R->sample_ray.reserve(n_samples));
+    NERF_HIP_TRY(R->field.reserve(n_samples));
+
+    if (timed) NERF_HIP_TRY(hipEventRecord(R->ev[3], st));
+    k_march_samples<<<blocks, 256, 0, st>>>(R->cams.ptr, ppv, n_rays, occ, d->max_steps, R->rays.ptr, R->counts.ptr, R->offsets.ptr, R->samples.ptr, R->sample_ray.ptr);
+    NERF_LAUNCH_CHECK("k_march_samples");
+    if (timed) NERF_HIP_TRY(hipEventRecord(R->ev[4], st));
+    FieldInputs in{};
+    in.samples    = R->samples.ptr;
+    in.sample_ray = R->sample_ray.ptr;
+    in.rays       = R->rays.ptr;
+    const FieldWeights w{(const half_t*)d->model->density_params, (const half_t*)d->model->color_params};
+    NERF_HIP_TRY(launch_field(g, d->model->table, w, in, n_samples, R->field.ptr, st));
+    if (timed) NERF_HIP_TRY(hipEventRecord(R->ev[5], st));
+    k_composite<<<blocks, 256, 0, st>>>(n_rays, R->counts.ptr, R->offsets.ptr, R->samples.ptr, R->field.ptr, d->min_transmittance, make_float3(d->background[0], d->background[1], d->background[2]), rgba8, rgb_f32);
+    NERF_LAUNCH_CHECK("k_composite");
+    if (counts_out) NERF_HIP_TRY(hipMemcpyAsync(counts_out, R->counts.ptr, sizeof(uint32_t) * n_rays, hipMemcpyDeviceToDevice, st));
+    if (timed) {
+        hipEvent_t end = nullptr;
+        NERF_HIP_TRY(hipEventCreate(&end));
+        NERF_HIP_TRY(hipEventRecord(end, st));
+        NERF_HIP_TRY(hipEventSynchronize(end));
+        float ms[5];
+        NERF_HIP_TRY(hipEventElapsedTime(&ms[0], R->ev[0], R->ev[1]));
+        NERF_HIP_TRY(hipEventElapsedTime(&ms[1], R->ev[1], R->ev[2]));
+        NERF_HIP_TRY(hipEventElapsedTime(&ms[2], R->ev[3], R->ev[4]));
+        NERF_HIP_TRY(hipEventElapsedTime(&ms[3], R->ev[4], R->ev[5]));
+        NERF_HIP_TRY(hipEventElapsedTime(&ms[4], R->ev[5], end));
+        float total_ms = 0.0f;
+        NERF_HIP_TRY(hipEventElapsedTime(&total_ms, R->ev[0], end));
+        (void)hipEventDestroy(end);
+        stats->rays         = n_rays;
+        stats->samples      = n_samples;
+        stats->ms_count     = ms[0];
+        stats->ms_scan      = ms[1];
+        stats->ms_samples   = ms[2];
+        stats->ms_field     = ms[3];
+        stats->ms_composite = ms[4];
+        stats->ms_total     = total_ms;
+    }
+    return NERF_STATUS_OK;
+}
+
+}  // extern "C"

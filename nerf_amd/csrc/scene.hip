@@ -1,0 +1,164 @@
+// scene.hip — analytic Gaussian scene, its occupancy bitfield, and orbit
+// cameras.  The Gaussian density is evaluated with nerf_math::det_expf so that
+// the bitfield is bit-identical to a CPU evaluation of the same field.
+//
+// Occupancy packing follows backend-cuda.cu:347-350 (cell x + y res + z res^2,
+// word idx >> 5, bit idx & 31) and the strict threshold of :1632; cell centres
+// follow :1607-1608.  The reference builds its bitfield with one atomicOr per
+// cell (:1628-1634); here each wavefront ballots its 64 cells and one lane
+// stores the two resulting words, so there are no atomics.
+#include <math.h>
+
+#include "common.hpp"
+
+namespace nerf_hip {
+namespace {
+
+constexpr uint32_t kMaxSceneLds = 1024;  // Gaussians staged in LDS per pass
+
+struct GaussLds {
+    float cx, cy, cz, k, a;
+};
+
+__device__ __forceinline__ float eval_density(const GaussLds* gs, uint32_t count, const float p[3], float acc) {
+    for (uint32_t i = 0; i < count; ++i) {
+        const float dx = p[0] - gs[i].cx;
+        const float dy = p[1] - gs[i].cy;
+        const float dz = p[2] - gs[i].cz;
+        const float d2 = (dx * dx + dy * dy) + dz * dz;
+        acc            = acc + gs[i].a * nerf_math::det_expf(d2 * gs[i].k);
+    }
+    return acc;
+}
+
+__device__ __forceinline__ void stage_gaussians(GaussLds* lds, const NerfExtGaussian* g, uint32_t begin, uint32_t count) {
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < count; i += blockDim.x) {
+        const NerfExtGaussian q = g[begin + i];
+        lds[i]                  = GaussLds{q.cx, q.cy, q.cz, -0.5f / (q.sigma * q.sigma), q.amplitude};
+    }
+    __syncthreads();
+}
+
+__global__ __launch_bounds__(256) void k_scene_density(const NerfExtGaussian* __restrict__ gaussians, uint32_t count, const float* __restrict__ pos, uint32_t n, float* __restrict__ out) {
+    __shared__ GaussLds lds[kMaxSceneLds];
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    const uint32_t q = i < n ? i : n - 1u;
+    const float p[3] = {pos[3ull * q], pos[3ull * q + 1], pos[3ull * q + 2]};
+    float acc        = 0.0f;
+    for (uint32_t b = 0; b < count; b += kMaxSceneLds) {
+        const uint32_t c = count - b < kMaxSceneLds ? count - b : kMaxSceneLds;
+        stage_gaussians(lds, gaussians, b, c);
+        acc = eval_density(lds, c, p, acc);
+    }
+    if (i < n) out[i] = acc;
+}
+
+__global__ __launch_bounds__(256) void k_occupancy_from_scene(const NerfExtGaussian* __restrict__ gaussians, uint32_t count, float threshold, uint32_t res, float3 bmin, float3 bmax, uint32_t* __restrict__ bits, uint64_t cells, uint64_t words) {
+    __shared__ GaussLds lds[kMaxSceneLds];
+    const uint64_t cell = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+    const uint64_t rr   = (uint64_t)res * res;
+    const uint64_t cq   = cell < cells ? cell : cells - 1u;
+    const uint32_t z    = (uint32_t)(cq / rr);
+    const uint32_t rem  = (uint32_t)(cq - (uint64_t)z * rr);
+    const uint32_t y    = rem / res;
+    const uint32_t x    = rem - y * res;
+    const float sx = (bmax.x - bmin.x) / (float)res, sy = (bmax.y - bmin.y) / (float)res, sz = (bmax.z - bmin.z) / (float)res;
+    const float p[3] = {bmin.x + ((float)x + 0.5f) * sx, bmin.y + ((float)y + 0.5f) * sy, bmin.z + ((float)z + 0.5f) * sz};
+    float acc        = 0.0f;
+    for (uint32_t b = 0; b < count; b += kMaxSceneLds) {
+        const uint32_t c = count - b < kMaxSceneLds ? count - b : kMaxSceneLds;
+        stage_gaussians(lds, gaussians, b, c);
+        acc = eval_density(lds, c, p, acc);
+    }
+    const bool occ          = cell < cells && acc > threshold;
+    const uint64_t ballot   = __ballot(occ);
+    const uint32_t lane     = threadIdx.x & 63u;
+    const uint64_t wave_base = ((uint64_t)blockIdx.x * 256u + (threadIdx.x & ~63u)) >> 5;  // first word of this wave
+    if (lane == 0u) {
+        if (wave_base < words) bits[wave_base] = (uint32_t)ballot;
+        if (wave_base + 1u < words) bits[wave_base + 1u] = (uint32_t)(ballot >> 32);
+    }
+}
+
+}  // namespace
+}  // namespace nerf_hip
+
+using namespace nerf_hip;
+
+extern "C" {
+
+NERF_API NerfStatus nerf_ext_scene_gaussians(const NerfExtSceneDesc* d, NerfExtGaussian* out) {
+    NERF_CHECK_ARG(d && out, "nerf_ext_scene_gaussians: null argument");
+    const uint64_t s0 = nerf_math::stream_state(0x6a55ull, d->seed);
+    for (uint32_t i = 0; i < d->count; ++i) {
+        float u[8];
+        for (uint32_t k = 0; k < 8u; ++k) u[k] = nerf_math::unit24(nerf_math::splitmix_at(s0, 8ull * i + k));
+        NerfExtGaussian& g = out[i];
+        g.cx               = d->centre_lo + (d->centre_hi - d->centre_lo) * u[0];
+        g.cy               = d->centre_lo + (d->centre_hi - d->centre_lo) * u[1];
+        g.cz               = d->centre_lo + (d->centre_hi - d->centre_lo) * u[2];
+        g.sigma            = d->sigma_lo + (d->sigma_hi - d->sigma_lo) * u[3];
+        g.amplitude        = d->amplitude_lo + (d->amplitude_hi - d->amplitude_lo) * u[4];
+        g.r                = u[5];
+        g.g                = u[6];
+        g.b                = u[7];
+    }
+    return NERF_STATUS_OK;
+}
+
+NERF_API NerfStatus nerf_ext_scene_density(const NerfExtGaussian* gaussians, uint32_t count, const float* positions, uint32_t n, float* out, void* stream) {
+    if (n == 0u) return NERF_STATUS_OK;
+    NERF_CHECK_ARG(gaussians && positions && out, "nerf_ext_scene_density: null pointer");
+    k_scene_density<<<(n + 255u) / 256u, 256, 0, (hipStream_t)stream>>>(gaussians, count, positions, n, out);
+    NERF_LAUNCH_CHECK("k_scene_density");
+    return NERF_STATUS_OK;
+}
+
+NERF_API NerfStatus nerf_ext_occupancy_from_scene(const NerfExtGaussian* gaussians, uint32_t count, float threshold, const NerfExtOccupancy* occ, void* stream) {
+    NERF_CHECK_ARG(occ && occ->bitfield && gaussians, "nerf_ext_occupancy_from_scene: null pointer");
+    NERF_CHECK_ARG(occ->resolution >= 1u && occ->resolution <= 2048u, "nerf_ext_occupancy_from_scene: resolution must be 1..2048");
+    const uint64_t cells  = (uint64_t)occ->resolution * occ->resolution * occ->resolution;
+    const uint64_t words  = (cells + 31u) / 32u;
+    const uint64_t blocks = (cells + 255u) / 256u;
+    k_occupancy_from_scene<<<(uint32_t)blocks, 256, 0, (hipStream_t)stream>>>(gaussians, count, threshold, occ->resolution, make_float3(occ->aabb_min[0], occ->aabb_min[1], occ->aabb_min[2]),
+        make_float3(occ->aabb_max[0], occ->aabb_max[1], occ->aabb_max[2]), occ->bitfield, cells, words);
+    NERF_LAUNCH_CHECK("k_occupancy_from_scene");
+    return NERF_STATUS_OK;
+}
+
+NERF_API NerfStatus nerf_ext_camera_orbit(uint64_t seed, uint32_t index, float radius, const float* centre3, uint32_t width, uint32_t height, float focal, NerfExtCamera* out) {
+    NERF_CHECK_ARG(centre3 && out, "nerf_ext_camera_orbit: null argument");
+    NERF_CHECK_ARG(width > 0u && height > 0u && focal > 0.0f, "nerf_ext_camera_orbit: bad image size or focal");
+    const uint64_t s0 = nerf_math::stream_state(0xca3eull, seed);
+    const double u    = (double)nerf_math::unit24(nerf_math::splitmix_at(s0, 2ull * index));
+    const double v    = (double)nerf_math::unit24(nerf_math::splitmix_at(s0, 2ull * index + 1ull));
+    const double cz   = 1.0 - 2.0 * u;  // uniform on the sphere
+    const double sz   = sqrt(fmax(0.0, 1.0 - cz * cz));
+    const double phi  = 2.0 * 3.14159265358979323846 * v;
+    const double back[3] = {sz * cos(phi), cz, sz * sin(phi)};  // camera +z (it looks along -z)
+    double upw[3]        = {0.0, 1.0, 0.0};
+    if (fabs(back[1]) > 0.999) {
+        upw[1] = 0.0;
+        upw[2] = 1.0;
+    }
+    double right[3] = {upw[1] * back[2] - upw[2] * back[1], upw[2] * back[0] - upw[0] * back[2], upw[0] * back[1] - upw[1] * back[0]};
+    const double rn = sqrt(right[0] * right[0] + right[1] * right[1] + right[2] * right[2]);
+    for (double& c : right) c /= rn;
+    const double up[3] = {back[1] * right[2] - back[2] * right[1], back[2] * right[0] - back[0] * right[2], back[0] * right[1] - back[1] * right[0]};
+    for (int a = 0; a < 3; ++a) {
+        out->c2w[4 * a + 0] = (float)right[a];
+        out->c2w[4 * a + 1] = (float)up[a];
+        out->c2w[4 * a + 2] = (float)back[a];
+        out->c2w[4 * a + 3] = (float)((double)centre3[a] + (double)radius * back[a]);
+    }
+    out->fx     = focal;
+    out->fy     = focal;
+    out->cx     = 0.5f * ((float)width - 1.0f);   // benchmark.cpp:213-214 convention
+    out->cy     = 0.5f * ((float)height - 1.0f);
+    out->width  = width;
+    out->height = height;
+    return NERF_STATUS_OK;
+}
+
+}  // extern "C"

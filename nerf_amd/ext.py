@@ -1,0 +1,134 @@
+"""Python mirror of include/nerf_ext.h: hash grids, MLP weights, the analytic
+scene, cameras and rendering, all on device buffers.
+
+The configurations of the benchmark plan are named here by their contents
+(hash-grid shape, scene size, image size), not by number.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import _lib as L
+from .device import DeviceArray, Stream
+
+# 16 levels x 2 features, N_min 16, b 1.3819, uniform table init in +-1e-4.
+HASH_PRIMES = (1, 2654435761, 805459861)
+
+
+def grid_desc(log2_table_size: int, dtype: int, n_levels: int = 16, base: int = 16, per_level_scale: float = 1.3819, finest: int = 0) -> L.NerfExtGridDesc:
+    return L.NerfExtGridDesc(n_levels, 2, log2_table_size, base, per_level_scale, finest, dtype, 0)
+
+
+def grid_levels(desc: L.NerfExtGridDesc) -> tuple[np.ndarray, np.ndarray]:
+    out = L.NerfExtGridLevels()
+    L.call("nerf_ext_grid_levels", C.byref(desc), C.byref(out))
+    n = out.n_levels
+    return np.array(out.resolution[:n], np.uint32), np.array(out.dense[:n], np.uint32)
+
+
+def table_elements(desc: L.NerfExtGridDesc) -> int:
+    return desc.n_levels * (1 << desc.log2_table_size) * desc.n_features
+
+
+def init_table(desc: L.NerfExtGridDesc, seed: int = 0, value_range: float = 1e-4) -> DeviceArray:
+    dtype = np.float32 if desc.table_dtype == L.NERF_EXT_F32 else np.float16
+    table = DeviceArray((table_elements(desc),), dtype)
+    L.call("nerf_ext_grid_init_table", C.byref(desc), seed, value_range, table.ptr, None)
+    return table
+
+
+def mlp_init(network: int) -> np.ndarray:
+    n = L.NERF_EXT_DENSITY_PARAMS if network == 0 else L.NERF_EXT_COLOR_PARAMS
+    out = np.empty(n, np.float32)
+    L.call("nerf_ext_mlp_init", network, out.ctypes.data)
+    return out
+
+
+def encode_forward(desc, table: DeviceArray, positions: DeviceArray, n: int, out: DeviceArray, stream: Stream | None = None) -> None:
+    dt = L.NERF_EXT_F32 if out.dtype == np.float32 else L.NERF_EXT_F16
+    L.call("nerf_ext_encode_forward", C.byref(desc), table.ptr, positions.ptr, n, out.ptr, dt, stream.handle if stream else None)
+
+
+@dataclass
+class Model:
+    """Hash grid + density/colour MLP weights resident on the device."""
+
+    grid: L.NerfExtGridDesc
+    table: DeviceArray
+    density_f32: np.ndarray
+    color_f32: np.ndarray
+    density: DeviceArray
+    color: DeviceArray
+
+    @classmethod
+    def create(cls, grid: L.NerfExtGridDesc, seed: int = 0, table_range: float = 1e-4) -> "Model":
+        table = init_table(grid, seed, table_range)
+        d32 = mlp_init(0)
+        c32 = mlp_init(1)
+        return cls(grid, table, d32, c32, DeviceArray.from_numpy(d32.astype(np.float16)), DeviceArray.from_numpy(c32.astype(np.float16)))
+
+    def struct(self) -> L.NerfExtModel:
+        return L.NerfExtModel(self.grid, self.table.ptr, self.density.ptr, self.color.ptr)
+
+
+def scene_gaussians(count: int, seed: int = 0, centre=(0.2, 0.8), sigma=(0.02, 0.1), amplitude=(5.0, 50.0)) -> np.ndarray:
+    """Analytic scene records as a structured array (cx cy cz sigma A r g b)."""
+    desc = L.NerfExtSceneDesc(count, 0, seed, centre[0], centre[1], sigma[0], sigma[1], amplitude[0], amplitude[1])
+    out = (L.NerfExtGaussian * count)()
+    L.call("nerf_ext_scene_gaussians", C.byref(desc), C.cast(out, C.c_void_p))
+    return np.frombuffer(out, dtype=np.float32).reshape(count, 8).copy()
+
+
+def occupancy_struct(bits: DeviceArray, res: int, aabb_min=(0.0, 0.0, 0.0), aabb_max=(1.0, 1.0, 1.0)) -> L.NerfExtOccupancy:
+    return L.NerfExtOccupancy(bits.ptr, res, (C.c_float * 3)(*aabb_min), (C.c_float * 3)(*aabb_max))
+
+
+def occupancy_from_scene(gaussians: np.ndarray, res: int, threshold: float = 0.01, aabb_min=(0.0, 0.0, 0.0), aabb_max=(1.0, 1.0, 1.0)) -> DeviceArray:
+    words = (res ** 3 + 31) // 32
+    bits = DeviceArray.zeros((words,), np.uint32)
+    g = DeviceArray.from_numpy(np.ascontiguousarray(gaussians, np.float32))
+    occ = occupancy_struct(bits, res, aabb_min, aabb_max)
+    L.call("nerf_ext_occupancy_from_scene", g.ptr, gaussians.shape[0], threshold, C.byref(occ), None)
+    return bits
+
+
+def camera_orbit(seed: int, index: int, radius: float, centre, width: int, height: int, focal: float) -> L.NerfExtCamera:
+    cam = L.NerfExtCamera()
+    c3 = (C.c_float * 3)(*centre)
+    L.call("nerf_ext_camera_orbit", seed, index, radius, C.cast(c3, C.c_void_p), width, height, focal, C.byref(cam))
+    return cam
+
+
+def camera_array(cam: L.NerfExtCamera) -> np.ndarray:
+    """Camera as the 18-word host record the oracle takes (floats then u32s)."""
+    buf = np.frombuffer(bytes(cam), dtype=np.uint8).copy()
+    return buf
+
+
+class Renderer:
+    def __init__(self):
+        self._h = C.c_void_p()
+        L.call("nerf_ext_renderer_create", C.byref(self._h))
+
+    def render(self, model: Model, occupancy: L.NerfExtOccupancy, cameras: list, max_steps: int, min_transmittance: float = 1e-4, background=(1.0, 1.0, 1.0), rgba8: DeviceArray | None = None, rgb: DeviceArray | None = None,
+               counts: DeviceArray | None = None, stream: Stream | None = None, timed: bool = False):
+        n_views = len(cameras)
+        w, h = cameras[0].width, cameras[0].height
+        if rgba8 is None:
+            rgba8 = DeviceArray((n_views, h, w), np.uint32)
+        cams = (L.NerfExtCamera * n_views)(*cameras)
+        ms = model.struct()
+        desc = L.NerfExtRenderDesc(C.pointer(ms), C.pointer(occupancy), cams, n_views, max_steps, min_transmittance, (C.c_float * 3)(*background), stream.handle if stream else None)
+        stats = L.NerfExtRenderStats()
+        L.call("nerf_ext_render", self._h, C.byref(desc), rgba8.ptr, rgb.ptr if rgb else None, counts.ptr if counts else None, C.byref(stats) if timed else None)
+        return rgba8, (stats if timed else None)
+
+    def __del__(self):
+        try:
+            if self._h.value and L._lib is not None:
+                L._lib.nerf_ext_renderer_destroy(self._h)
+        except Exception:
+            pass

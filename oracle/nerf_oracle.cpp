@@ -1,0 +1,610 @@
+// nerf_oracle.cpp — scalar C++ CPU oracle of the NeRF hot path.
+//
+// TEST INFRASTRUCTURE ONLY.  This file is the checker: tests/, the smoke check
+// in __graft_entry__.py and the cpu_baseline leg of bench.py call it through
+// ctypes (oracle/liboracle.so).  The product (nerf_amd/libnerf.so) never links,
+// loads or calls it.
+//
+// It restates, one scalar operation at a time, the semantics of each stage:
+//   * stages the reference has (ray generation, AABB clip, occupancy lookup,
+//     march, composite, RGBA8 packing, RNG, weight init) follow
+//     Xayah-Graphics/NeRF backend-cuda.cu at the cited lines, with two
+//     documented substitutions: 1/sqrtf replaces rsqrtf (:384) so that the
+//     result is correctly rounded on every target, and libm expf replaces
+//     __expf;
+//   * stages the reference lacks (hash-grid encoding, SH degree-4 direction
+//     encoding, exp density activation, analytic Gaussian scene) follow their
+//     published definitions, cited at each function.
+// Build flags: -O2 -ffp-contract=off, no SIMD intrinsics (oracle/Makefile).
+//
+// How each part is pinned (tests/test_oracle_*.py): fp16 conversion against
+// numpy's IEEE conversion; splitmix64 against Vigna's published seed-0
+// outputs; hash indices against brute-force closed forms and dense-level
+// injectivity; trilinear interpolation against exact reproduction of linear
+// tables; MLP against an fp64 numpy GEMM with the same rounding points; SH
+// against quadrature orthonormality; rays, AABB and march against analytic
+// axis-aligned cases; composite against the closed form for constant density.
+// hash_u32 (:321-328) has no published test vector: it is checked for
+// bijectivity through its inverse and for avalanche only ("parity unpinned"
+// beyond that; it is not on the inference path).
+
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+#include <algorithm>
+#include <thread>
+#include <vector>
+
+#include "../nerf_amd/csrc/nerf_math.h"  // det_expf only (shared on purpose: bit-exact occupancy)
+
+// ---------------------------------------------------------------------------
+// IEEE binary16 conversion (round to nearest even), written from the format
+// definition (IEEE 754-2008, section 3.6).
+// ---------------------------------------------------------------------------
+extern "C" uint16_t orc_f32_to_f16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const uint32_t a    = x & 0x7fffffffu;
+    if (a > 0x7f800000u) return (uint16_t)(sign | 0x7e00u);  // NaN
+    if (a >= 0x47800000u) return (uint16_t)(sign | 0x7c00u); // >= 2^16: inf
+    if (a >= 0x38800000u) {                                   // normal half
+        const uint32_t mant = a & 0x7fffffu;
+        const uint32_t exp  = (a >> 23) - 127u + 15u;
+        uint32_t h          = (exp << 10) | (mant >> 13);
+        const uint32_t rem  = mant & 0x1fffu;
+        if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h += 1u;  // may carry into inf
+        return (uint16_t)(sign | h);
+    }
+    if (a < 0x33000000u) return (uint16_t)sign;  // below 2^-25: rounds to zero
+    const uint32_t mant  = (a & 0x7fffffu) | 0x800000u;
+    const uint32_t shift = 126u - (a >> 23);      // 14..24
+    uint32_t h           = mant >> shift;
+    const uint32_t rem   = mant & ((1u << shift) - 1u);
+    const uint32_t half  = 1u << (shift - 1u);
+    if (rem > half || (rem == half && (h & 1u))) h += 1u;
+    return (uint16_t)(sign | h);
+}
+
+extern "C" float orc_f16_to_f32(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    const uint32_t e    = (h >> 10) & 0x1fu;
+    uint32_t m          = h & 0x3ffu;
+    uint32_t x;
+    if (e == 0u) {
+        if (m == 0u) {
+            x = sign;
+        } else {  // subnormal: normalise
+            uint32_t ee = 113u;
+            while (!(m & 0x400u)) {
+                m <<= 1;
+                --ee;
+            }
+            x = sign | (ee << 23) | ((m & 0x3ffu) << 13);
+        }
+    } else if (e == 31u) {
+        x = sign | 0x7f800000u | (m << 13);
+    } else {
+        x = sign | ((e + 112u) << 23) | (m << 13);
+    }
+    float f;
+    memcpy(&f, &x, 4);
+    return f;
+}
+
+extern "C" void orc_f32_to_f16_array(const float* src, uint16_t* dst, uint64_t n) {
+    for (uint64_t i = 0; i < n; ++i) dst[i] = orc_f32_to_f16(src[i]);
+}
+
+static inline float r16(float x) { return orc_f16_to_f32(orc_f32_to_f16(x)); }
+
+// ---------------------------------------------------------------------------
+// Integer RNG.
+// ---------------------------------------------------------------------------
+// backend-cuda.cu:321-328 (== :1439-1446).
+extern "C" uint32_t orc_hash_u32(uint32_t x) {
+    x ^= x >> 16;
+    x *= 0x7feb352du;
+    x ^= x >> 15;
+    x *= 0x846ca68bu;
+    x ^= x >> 16;
+    return x;
+}
+// backend-cuda.cu:329-332.
+extern "C" float orc_rand01(uint32_t seed) {
+    return (float)(orc_hash_u32(seed) & 0x00ffffffu) / (float)0x01000000u;
+}
+
+// Sequential splitmix64 exactly as the reference's init loop runs it
+// (backend-cuda.cu:1811, :1819-1823): state += golden; mix.
+extern "C" void orc_splitmix_sequence(uint64_t state, uint64_t n, uint64_t* out) {
+    for (uint64_t i = 0; i < n; ++i) {
+        state += 0x9e3779b97f4a7c15ull;
+        uint64_t z = state;
+        z          = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+        z          = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+        out[i]     = z ^ (z >> 31);
+    }
+}
+
+// State seeding of backend-cuda.cu:1811 / :1830.
+extern "C" uint64_t orc_stream_state(uint64_t a, uint64_t b) {
+    return (a + 0x9e3779b97f4a7c15ull) ^ (b * 0xbf58476d1ce4e5b9ull);
+}
+
+// n uniforms lo + (hi - lo) * u24, u24 = ((u32)(z >> 32) >> 8) / 2^24, from the
+// sequential stream (a, b).  Used for the hash table init U(-1e-4, 1e-4) and for
+// all synthetic inputs; written as (2u - 1) * half_range + mid to mirror
+// backend-cuda.cu:1824 when lo = -hi.
+extern "C" void orc_uniform_fill(uint64_t a, uint64_t b, uint64_t n, float lo, float hi, float* out) {
+    uint64_t state = orc_stream_state(a, b);
+    for (uint64_t i = 0; i < n; ++i) {
+        state += 0x9e3779b97f4a7c15ull;
+        uint64_t z     = state;
+        z              = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+        z              = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+        z              = z ^ (z >> 31);
+        const float u  = (float)((uint32_t)(z >> 32) >> 8) * (1.0f / 16777216.0f);
+        if (lo == -hi)
+            out[i] = (u * 2.0f - 1.0f) * hi;
+        else
+            out[i] = lo + (hi - lo) * u;
+    }
+}
+
+// Xavier-uniform MLP init of backend-cuda.cu:1810-1847 applied to the target
+// shapes: density 32->64->16 (seeds 0x1234/0x5678), colour 32->64->64->16
+// (seeds 0x9abc/0xdef0).  Matrices are packed [out][in], input layer first.
+extern "C" uint32_t orc_mlp_param_count(uint32_t network) { return network == 0u ? 3072u : 7168u; }
+
+extern "C" void orc_mlp_init(uint32_t network, float* out) {
+    const uint32_t dens_shape[2][2] = {{64u, 32u}, {16u, 64u}};
+    const uint32_t col_shape[3][2]  = {{64u, 32u}, {64u, 64u}, {16u, 64u}};
+    const uint32_t n_mat            = network == 0u ? 2u : 3u;
+    uint64_t state = network == 0u ? orc_stream_state(0x1234ull, 0x5678ull) : orc_stream_state(0x9abcull, 0xdef0ull);
+    uint64_t off   = 0;
+    for (uint32_t m = 0; m < n_mat; ++m) {
+        const uint32_t fan_out = network == 0u ? dens_shape[m][0] : col_shape[m][0];
+        const uint32_t fan_in  = network == 0u ? dens_shape[m][1] : col_shape[m][1];
+        const float scale      = sqrtf(6.0f / (float)(fan_in + fan_out));
+        for (uint64_t i = 0; i < (uint64_t)fan_in * fan_out; ++i) {
+            state += 0x9e3779b97f4a7c15ull;
+            uint64_t z = state;
+            z          = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+            z          = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+            z ^= z >> 31;
+            out[off + i] = ((float)((uint32_t)(z >> 32) >> 8) * (1.0f / 16777216.0f) * 2.0f - 1.0f) * scale;
+        }
+        off += (uint64_t)fan_in * fan_out;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Multiresolution hash grid (Mueller et al. 2022, section 3).
+// ---------------------------------------------------------------------------
+struct OrcGrid {
+    uint32_t n_levels;
+    uint32_t n_features;
+    uint32_t table_size;  // T, a power of two
+    uint32_t table_dtype; // 0 f32, 1 f16
+    uint32_t resolution[16];
+    uint32_t dense[16];
+};
+
+// N_l = floor(N_min * b^l + 1e-9) in double; b = (finest / base)^(1 / (L - 1))
+// when finest > 0.  A level is dense (1:1 indexing) when (N_l + 1)^3 <= T.
+extern "C" void orc_grid_levels(uint32_t n_levels, uint32_t base, float per_level_scale, uint32_t finest, uint32_t log2_table_size, uint32_t* resolution, uint32_t* dense) {
+    double b = (double)per_level_scale;
+    if (finest > 0u && n_levels > 1u) b = exp(log((double)finest / (double)base) / (double)(n_levels - 1u));
+    const uint64_t T = 1ull << log2_table_size;
+    for (uint32_t l = 0; l < n_levels; ++l) {
+        const double nl   = floor((double)base * pow(b, (double)l) + 1e-9);
+        resolution[l]     = (uint32_t)nl;
+        const uint64_t v  = (uint64_t)resolution[l] + 1ull;
+        dense[l]          = (v * v * v <= T) ? 1u : 0u;
+    }
+}
+
+static inline float table_value(const OrcGrid& g, const void* table, uint32_t level, uint32_t idx, uint32_t f) {
+    const uint64_t off = ((uint64_t)level * g.table_size + idx) * g.n_features + f;
+    if (g.table_dtype == 0u) return ((const float*)table)[off];
+    return orc_f16_to_f32(((const uint16_t*)table)[off]);
+}
+
+static void encode_point(const OrcGrid& g, const void* table, const float* p, float* feat, uint32_t* idx_out, float* w_out) {
+    for (uint32_t l = 0; l < g.n_levels; ++l) {
+        const uint32_t N = g.resolution[l];
+        const float s    = (float)N;
+        uint32_t i0[3];
+        float w[3];
+        for (int a = 0; a < 3; ++a) {
+            const float x   = fminf(fmaxf(p[a], 0.0f), 1.0f);
+            const float pos = x * s;
+            uint32_t c      = (uint32_t)floorf(pos);
+            if (c >= N) c = N - 1u;
+            i0[a] = c;
+            w[a]  = pos - (float)c;
+        }
+        float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        for (uint32_t c = 0; c < 8u; ++c) {
+            const uint32_t cx = i0[0] + (c & 1u);
+            const uint32_t cy = i0[1] + ((c >> 1) & 1u);
+            const uint32_t cz = i0[2] + ((c >> 2) & 1u);
+            uint32_t idx;
+            if (g.dense[l]) {
+                const uint32_t stride = N + 1u;
+                idx                   = cx + cy * stride + cz * stride * stride;
+            } else {
+                idx = ((cx * 1u) ^ (cy * 2654435761u) ^ (cz * 805459861u)) & (g.table_size - 1u);
+            }
+            const float wx     = (c & 1u) ? w[0] : 1.0f - w[0];
+            const float wy     = (c & 2u) ? w[1] : 1.0f - w[1];
+            const float wz     = (c & 4u) ? w[2] : 1.0f - w[2];
+            const float weight = (wx * wy) * wz;
+            if (idx_out) idx_out[l * 8u + c] = idx;
+            if (w_out) w_out[l * 8u + c] = weight;
+            for (uint32_t f = 0; f < g.n_features; ++f) acc[f] += weight * table_value(g, table, l, idx, f);
+        }
+        for (uint32_t f = 0; f < g.n_features; ++f) feat[l * g.n_features + f] = acc[f];
+    }
+}
+
+// features: [n][L*F] f32; optional indices/weights: [n][L][8].
+extern "C" void orc_encode(const OrcGrid* g, const void* table, const float* pos, uint32_t n, float* features, uint32_t* indices, float* weights) {
+    const uint32_t width = g->n_levels * g->n_features;
+    for (uint32_t i = 0; i < n; ++i)
+        encode_point(*g, table, pos + 3ull * i, features + (uint64_t)i * width, indices ? indices + (uint64_t)i * g->n_levels * 8u : nullptr,
+            weights ? weights + (uint64_t)i * g->n_levels * 8u : nullptr);
+}
+
+// ---------------------------------------------------------------------------
+// MLPs: no biases, ReLU hidden layers, W row-major [out][in] (backend-cuda.cu
+// :668-783 semantics), fp16 operands and fp16-rounded hidden activations,
+// accumulation carried in fp64 and rounded once to fp32.
+// ---------------------------------------------------------------------------
+static void matvec(const uint16_t* W, uint32_t n_out, uint32_t n_in, const float* x, float* y) {
+    for (uint32_t o = 0; o < n_out; ++o) {
+        double acc = 0.0;
+        for (uint32_t k = 0; k < n_in; ++k) acc += (double)orc_f16_to_f32(W[(uint64_t)o * n_in + k]) * (double)x[k];
+        y[o] = (float)acc;
+    }
+}
+
+// Density network 32 -> 64 -> 16 on one feature row; out16 = raw outputs.
+static void density_row(const uint16_t* params, const float* feat32, float* out16) {
+    float x[32], h[64];
+    for (int k = 0; k < 32; ++k) x[k] = r16(feat32[k]);
+    matvec(params, 64, 32, x, h);
+    for (int k = 0; k < 64; ++k) h[k] = r16(fmaxf(h[k], 0.0f));
+    matvec(params + 2048, 16, 64, h, out16);
+}
+
+// Real spherical harmonics, bands 0..3 (16 values) with the Condon-Shortley
+// phase, of a unit direction (Sloan, "Stupid Spherical Harmonics Tricks", 2008).
+extern "C" void orc_sh4(const float* d, float* out) {
+    const float x = d[0], y = d[1], z = d[2];
+    const float xy = x * y, yz = y * z, xz = x * z;
+    const float x2 = x * x, y2 = y * y, z2 = z * z;
+    out[0]  = 0.28209479177387814f;
+    out[1]  = -0.48860251190291987f * y;
+    out[2]  = 0.48860251190291987f * z;
+    out[3]  = -0.48860251190291987f * x;
+    out[4]  = 1.0925484305920792f * xy;
+    out[5]  = -1.0925484305920792f * yz;
+    out[6]  = 0.94617469575755997f * z2 - 0.31539156525251999f;
+    out[7]  = -1.0925484305920792f * xz;
+    out[8]  = 0.54627421529603959f * (x2 - y2);
+    out[9]  = 0.59004358992664352f * y * (3.0f * x2 - y2) * -1.0f;
+    out[10] = 2.8906114426405538f * xy * z;
+    out[11] = 0.45704579946446572f * y * (1.0f - 5.0f * z2);
+    out[12] = 0.3731763325901154f * z * (5.0f * z2 - 3.0f);
+    out[13] = 0.45704579946446572f * x * (1.0f - 5.0f * z2);
+    out[14] = 1.4453057213202769f * z * (x2 - y2);
+    out[15] = 0.59004358992664352f * x * (3.0f * y2 - x2);
+}
+
+// Colour network [geo 15 | SH 16 | 0] -> 64 -> 64 -> 16 (3 used), sigmoid.
+static void color_row(const uint16_t* params, const float* dens_out16, const float* dir, float* rgb) {
+    float sh[16], x[32], h1[64], h2[64], o[16];
+    orc_sh4(dir, sh);
+    for (int k = 0; k < 15; ++k) x[k] = r16(dens_out16[1 + k]);
+    for (int k = 0; k < 16; ++k) x[15 + k] = r16(sh[k]);
+    x[31] = 0.0f;
+    matvec(params, 64, 32, x, h1);
+    for (int k = 0; k < 64; ++k) h1[k] = r16(fmaxf(h1[k], 0.0f));
+    matvec(params + 2048, 64, 64, h1, h2);
+    for (int k = 0; k < 64; ++k) h2[k] = r16(fmaxf(h2[k], 0.0f));
+    matvec(params + 2048 + 4096, 16, 64, h2, o);
+    for (int c = 0; c < 3; ++c) rgb[c] = 1.0f / (1.0f + expf(-o[c]));
+}
+
+// Density MLP on given features (rounded to fp16 inside): raw outputs [n][16].
+extern "C" void orc_density_mlp(const uint16_t* params, const float* features, uint32_t n, float* out) {
+    for (uint32_t i = 0; i < n; ++i) density_row(params, features + 32ull * i, out + 16ull * i);
+}
+
+// Config-1 pipeline: encode -> density MLP -> exp on channel 0.  out [n][16].
+extern "C" void orc_density_forward(const OrcGrid* g, const void* table, const uint16_t* params, const float* pos, uint32_t n, float* out) {
+    float feat[32];
+    for (uint32_t i = 0; i < n; ++i) {
+        encode_point(*g, table, pos + 3ull * i, feat, nullptr, nullptr);
+        float* o = out + 16ull * i;
+        density_row(params, feat, o);
+        o[0] = expf(o[0]);
+    }
+}
+
+// Full field: out [n][4] = (sigma = exp(raw), r, g, b).
+static void field_point(const OrcGrid& g, const void* table, const uint16_t* dparams, const uint16_t* cparams, const float* p, const float* d, float* out4) {
+    float feat[32], o[16], rgb[3];
+    encode_point(g, table, p, feat, nullptr, nullptr);
+    density_row(dparams, feat, o);
+    color_row(cparams, o, d, rgb);
+    out4[0] = expf(o[0]);
+    out4[1] = rgb[0];
+    out4[2] = rgb[1];
+    out4[3] = rgb[2];
+}
+
+extern "C" void orc_field_forward(const OrcGrid* g, const void* table, const uint16_t* dparams, const uint16_t* cparams, const float* pos, const float* dirs, uint32_t n, float* out) {
+    for (uint32_t i = 0; i < n; ++i) field_point(*g, table, dparams, cparams, pos + 3ull * i, dirs + 3ull * i, out + 4ull * i);
+}
+
+// ---------------------------------------------------------------------------
+// Analytic Gaussian scene: density(p) = sum_g A_g exp(k_g |p - c_g|^2) with
+// k_g = -0.5 / sigma_g^2.  Record per Gaussian: cx cy cz sigma A r g b.
+// ---------------------------------------------------------------------------
+extern "C" float orc_det_expf(float x) { return nerf_math::det_expf(x); }
+extern "C" void orc_det_expf_array(const float* x, uint64_t n, float* out) {
+    for (uint64_t i = 0; i < n; ++i) out[i] = nerf_math::det_expf(x[i]);
+}
+
+static inline float scene_density(const float* gs, uint32_t count, const float* p) {
+    float acc = 0.0f;
+    for (uint32_t i = 0; i < count; ++i) {
+        const float* g = gs + 8ull * i;
+        const float dx = p[0] - g[0];
+        const float dy = p[1] - g[1];
+        const float dz = p[2] - g[2];
+        const float d2 = (dx * dx + dy * dy) + dz * dz;
+        const float k  = -0.5f / (g[3] * g[3]);
+        acc            = acc + g[4] * nerf_math::det_expf(d2 * k);
+    }
+    return acc;
+}
+
+extern "C" void orc_scene_density(const float* gs, uint32_t count, const float* pos, uint32_t n, float* out) {
+    for (uint32_t i = 0; i < n; ++i) out[i] = scene_density(gs, count, pos + 3ull * i);
+}
+
+// Bit (x + y*res + z*res^2) is set iff density(cell centre) > threshold, with
+// centre = min + (i + 0.5) * ((max - min) / res) per axis (backend-cuda.cu
+// :1607-1608 cell centres, :1632-1633 strict threshold, :347-350 packing).
+extern "C" void orc_occupancy_from_scene(const float* gs, uint32_t count, uint32_t res, const float* aabb, float threshold, uint32_t* bits) {
+    const uint64_t cells = (uint64_t)res * res * res;
+    memset(bits, 0, ((cells + 31) / 32) * 4);
+    const float step[3] = {(aabb[3] - aabb[0]) / (float)res, (aabb[4] - aabb[1]) / (float)res, (aabb[5] - aabb[2]) / (float)res};
+    for (uint64_t c = 0; c < cells; ++c) {
+        const uint32_t z = (uint32_t)(c / ((uint64_t)res * res));
+        const uint32_t r = (uint32_t)(c - (uint64_t)z * res * res);
+        const uint32_t y = r / res;
+        const uint32_t x = r - y * res;
+        const float p[3] = {aabb[0] + ((float)x + 0.5f) * step[0], aabb[1] + ((float)y + 0.5f) * step[1], aabb[2] + ((float)z + 0.5f) * step[2]};
+        if (scene_density(gs, count, p) > threshold) bits[c >> 5] |= 1u << (c & 31u);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Cameras, rays, AABB and occupancy march.
+// ---------------------------------------------------------------------------
+struct OrcCamera {
+    float c2w[12];  // rows 0..2 of the row-major camera-to-world matrix
+    float fx, fy, cx, cy;
+    uint32_t width, height;
+};
+
+struct OrcRay {
+    float o[3], d[3], tn, tf;
+};
+
+// backend-cuda.cu:373-390 (ray direction; 1/sqrtf instead of rsqrtf) and
+// :391-408 (slab test).
+static bool make_ray(const OrcCamera& c, float px, float py_flipped, const float* aabb, OrcRay& r) {
+    const float dcx = (px - c.cx) / c.fx;
+    const float dcy = (py_flipped - c.cy) / c.fy;
+    const float dcz = -1.0f;
+    float d[3];
+    for (int a = 0; a < 3; ++a) d[a] = c.c2w[4 * a + 0] * dcx + c.c2w[4 * a + 1] * dcy + c.c2w[4 * a + 2] * dcz;
+    const float len2 = d[0] * d[0] + d[1] * d[1] + d[2] * d[2];
+    if (len2 <= 1e-16f) return false;
+    const float inv = 1.0f / sqrtf(len2);
+    for (int a = 0; a < 3; ++a) {
+        r.d[a] = d[a] * inv;
+        r.o[a] = c.c2w[4 * a + 3];
+    }
+    float tmin = -INFINITY, tmax = INFINITY;
+    float tmins[3], tmaxs[3];
+    for (int a = 0; a < 3; ++a) {
+        const float inv_d = fabsf(r.d[a]) > 1e-8f ? 1.0f / r.d[a] : (r.d[a] >= 0.0f ? 1e8f : -1e8f);
+        const float t0    = (aabb[a] - r.o[a]) * inv_d;
+        const float t1    = (aabb[3 + a] - r.o[a]) * inv_d;
+        tmins[a]          = fminf(t0, t1);
+        tmaxs[a]          = fmaxf(t0, t1);
+    }
+    tmin = fmaxf(fmaxf(tmins[0], tmins[1]), tmins[2]);
+    tmax = fminf(fminf(tmaxs[0], tmaxs[1]), tmaxs[2]);
+    if (!(tmin <= tmax && tmax > 0.0f)) return false;
+    if (tmin < 0.0f) tmin = 0.0f;
+    r.tn = tmin;
+    r.tf = tmax;
+    return true;
+}
+
+// backend-cuda.cu:338-351.  A null bitfield marks every cell of the box occupied.
+static inline bool occupied(const uint32_t* bits, uint32_t res, const float* aabb, const float* p) {
+    const float sx = aabb[3] - aabb[0], sy = aabb[4] - aabb[1], sz = aabb[5] - aabb[2];
+    const float rx = (p[0] - aabb[0]) / sx, ry = (p[1] - aabb[1]) / sy, rz = (p[2] - aabb[2]) / sz;
+    if (rx < 0.0f || rx >= 1.0f || ry < 0.0f || ry >= 1.0f || rz < 0.0f || rz >= 1.0f) return false;
+    if (!bits) return true;  // no bitfield: every cell of the box is occupied
+    const uint32_t ix  = std::min(res - 1u, (uint32_t)(rx * (float)res));
+    const uint32_t iy  = std::min(res - 1u, (uint32_t)(ry * (float)res));
+    const uint32_t iz  = std::min(res - 1u, (uint32_t)(rz * (float)res));
+    const uint32_t idx = ix + iy * res + iz * res * res;
+    return (bits[idx >> 5] & (1u << (idx & 31u))) != 0u;
+}
+
+// Inference ray of pixel (x, y): pixel centre, y flipped (backend-cuda.cu:561-563).
+static bool pixel_ray(const OrcCamera& c, uint32_t x, uint32_t y, const float* aabb, OrcRay& r) {
+    const float px = (float)x + 0.5f;
+    const float py = (float)y + 0.5f;
+    return make_ray(c, px, (float)c.height - 1.0f - py, aabb, r);
+}
+
+// March of backend-cuda.cu:448-469; emit(t_mid, dt) for occupied steps.
+template <typename Emit>
+static uint32_t march(const OrcCamera& c, const OrcRay& r, const uint32_t* bits, uint32_t res, const float* aabb, uint32_t max_steps, Emit emit) {
+    const float t_range = r.tf - r.tn;
+    if (!(t_range > 0.0f)) return 0u;
+    const float dt_min = t_range / (float)max_steps;
+    const float ifx    = c.fx > 0.0f ? 1.0f / c.fx : 0.0f;
+    const float ify    = c.fy > 0.0f ? 1.0f / c.fy : 0.0f;
+    const float cone   = 0.5f * (ifx + ify);
+    uint32_t count = 0, i = 0;
+    float t = r.tn;
+    while (t < r.tf && i < max_steps) {
+        const float dt    = fminf(fmaxf(dt_min, t * cone), r.tf - t);
+        const float tm    = t + 0.5f * dt;
+        const float p[3]  = {r.o[0] + tm * r.d[0], r.o[1] + tm * r.d[1], r.o[2] + tm * r.d[2]};
+        if (occupied(bits, res, aabb, p)) {
+            emit(count, tm, dt);
+            ++count;
+        }
+        t += dt;
+        ++i;
+    }
+    return count;
+}
+
+// Per-ray occupied-sample counts for rays [ray_begin, ray_begin + n) of one view.
+extern "C" void orc_march_count(const OrcCamera* cam, const uint32_t* bits, uint32_t res, const float* aabb, uint32_t max_steps, uint32_t ray_begin, uint32_t n, uint32_t* counts) {
+    for (uint32_t k = 0; k < n; ++k) {
+        const uint32_t ray = ray_begin + k;
+        OrcRay r;
+        counts[k] = 0u;
+        if (!pixel_ray(*cam, ray % cam->width, ray / cam->width, aabb, r)) continue;
+        counts[k] = march(*cam, r, bits, res, aabb, max_steps, [](uint32_t, float, float) {});
+    }
+}
+
+// Samples (t_mid, dt) of one ray, up to cap; returns the count.
+extern "C" uint32_t orc_march_ray(const OrcCamera* cam, const uint32_t* bits, uint32_t res, const float* aabb, uint32_t max_steps, uint32_t ray, float* t_dt, uint32_t cap) {
+    OrcRay r;
+    if (!pixel_ray(*cam, ray % cam->width, ray / cam->width, aabb, r)) return 0u;
+    return march(*cam, r, bits, res, aabb, max_steps, [&](uint32_t k, float tm, float dt) {
+        if (k < cap) {
+            t_dt[2 * k]     = tm;
+            t_dt[2 * k + 1] = dt;
+        }
+    });
+}
+
+// Ray origin/direction/t-range of one pixel ray; returns 0 if it misses.
+extern "C" int orc_pixel_ray(const OrcCamera* cam, uint32_t ray, const float* aabb, float* out8) {
+    OrcRay r;
+    if (!pixel_ray(*cam, ray % cam->width, ray / cam->width, aabb, r)) return 0;
+    for (int a = 0; a < 3; ++a) {
+        out8[a]     = r.o[a];
+        out8[3 + a] = r.d[a];
+    }
+    out8[6] = r.tn;
+    out8[7] = r.tf;
+    return 1;
+}
+
+// ---------------------------------------------------------------------------
+// Composite (backend-cuda.cu:601-635) with early stop: after sample i updates
+// T, stop when T < t_stop.  Background bg added as C + T * bg; clamp; RGBA8 by
+// round-to-nearest-even of x * 255 (:628-634).
+// ---------------------------------------------------------------------------
+static uint32_t pack_rgba8(const float* rgb) {
+    uint32_t u[3];
+    for (int c = 0; c < 3; ++c) u[c] = (uint32_t)nearbyintf(fminf(1.0f, fmaxf(0.0f, rgb[c])) * 255.0f);
+    return (255u << 24) | (u[2] << 16) | (u[1] << 8) | u[0];
+}
+
+// sigma_rgb: [count][4]; dt: [count].  Writes rgb[3]; returns samples used.
+extern "C" uint32_t orc_composite_ray(const float* sigma_rgb, const float* dt, uint32_t count, float t_stop, const float* bg, float* rgb_out, uint32_t* rgba8_out) {
+    float T = 1.0f, C[3] = {0, 0, 0};
+    uint32_t used = 0;
+    for (uint32_t i = 0; i < count; ++i) {
+        const float a = 1.0f - expf(-(sigma_rgb[4 * i] * fmaxf(dt[i], 0.0f)));
+        const float w = T * a;
+        for (int c = 0; c < 3; ++c) C[c] += w * sigma_rgb[4 * i + 1 + c];
+        T *= 1.0f - a;
+        ++used;
+        if (T < t_stop) break;
+    }
+    for (int c = 0; c < 3; ++c) rgb_out[c] = C[c] + T * bg[c];
+    if (rgba8_out) *rgba8_out = pack_rgba8(rgb_out);
+    return used;
+}
+
+// ---------------------------------------------------------------------------
+// Whole render of a list of rays of one view: march -> field -> composite.
+// Rays are split statically over n_threads std::threads.
+// ---------------------------------------------------------------------------
+struct OrcModel {
+    OrcGrid grid;
+    const void* table;
+    const uint16_t* density_params;
+    const uint16_t* color_params;
+};
+
+extern "C" void orc_render_rays(const OrcModel* model, const OrcCamera* cam, const uint32_t* bits, uint32_t res, const float* aabb, uint32_t max_steps, float t_stop, const float* bg, const uint32_t* rays, uint32_t n_rays, float* rgb_out, uint32_t* rgba8_out,
+    uint32_t* counts_out, uint32_t n_threads) {
+    if (n_threads == 0u) n_threads = 1u;
+    auto work = [&](uint32_t begin, uint32_t end) {
+        std::vector<float> t_dt, sig, dts;
+        for (uint32_t k = begin; k < end; ++k) {
+            const uint32_t ray = rays[k];
+            OrcRay r;
+            uint32_t count = 0;
+            t_dt.clear();
+            if (pixel_ray(*cam, ray % cam->width, ray / cam->width, aabb, r)) {
+                count = march(*cam, r, bits, res, aabb, max_steps, [&](uint32_t, float tm, float dt) {
+                    t_dt.push_back(tm);
+                    t_dt.push_back(dt);
+                });
+            }
+            float T = 1.0f, C[3] = {0, 0, 0};
+            for (uint32_t i = 0; i < count; ++i) {
+                const float tm   = t_dt[2 * i];
+                const float dt   = t_dt[2 * i + 1];
+                const float p[3] = {r.o[0] + tm * r.d[0], r.o[1] + tm * r.d[1], r.o[2] + tm * r.d[2]};
+                float s4[4];
+                field_point(model->grid, model->table, model->density_params, model->color_params, p, r.d, s4);
+                const float a = 1.0f - expf(-(s4[0] * fmaxf(dt, 0.0f)));
+                const float w = T * a;
+                for (int c = 0; c < 3; ++c) C[c] += w * s4[1 + c];
+                T *= 1.0f - a;
+                if (T < t_stop) break;
+            }
+            float rgb[3];
+            for (int c = 0; c < 3; ++c) rgb[c] = C[c] + T * bg[c];
+            if (rgb_out)
+                for (int c = 0; c < 3; ++c) rgb_out[3ull * k + c] = rgb[c];
+            if (rgba8_out) rgba8_out[k] = pack_rgba8(rgb);
+            if (counts_out) counts_out[k] = count;
+        }
+    };
+    std::vector<std::thread> pool;
+    const uint32_t chunk = (n_rays + n_threads - 1u) / n_threads;
+    for (uint32_t t = 0; t < n_threads; ++t) {
+        const uint32_t b = t * chunk, e = std::min(n_rays, b + chunk);
+        if (b >= e) break;
+        pool.emplace_back(work, b, e);
+    }
+    for (auto& th : pool) th.join();
+}
+

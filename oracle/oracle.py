@@ -1,0 +1,288 @@
+"""ctypes binding of oracle/liboracle.so — the scalar CPU checker.
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, by the smoke check of
+__graft_entry__.py and by the cpu_baseline leg of bench.py.  The product
+(nerf_amd) never imports it.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "liboracle.so"
+
+
+class OrcGrid(C.Structure):
+    _fields_ = [
+        ("n_levels", C.c_uint32),
+        ("n_features", C.c_uint32),
+        ("table_size", C.c_uint32),
+        ("table_dtype", C.c_uint32),
+        ("resolution", C.c_uint32 * 16),
+        ("dense", C.c_uint32 * 16),
+    ]
+
+
+class OrcCamera(C.Structure):
+    _fields_ = [
+        ("c2w", C.c_float * 12),
+        ("fx", C.c_float),
+        ("fy", C.c_float),
+        ("cx", C.c_float),
+        ("cy", C.c_float),
+        ("width", C.c_uint32),
+        ("height", C.c_uint32),
+    ]
+
+
+class OrcModel(C.Structure):
+    _fields_ = [
+        ("grid", OrcGrid),
+        ("table", C.c_void_p),
+        ("density_params", C.c_void_p),
+        ("color_params", C.c_void_p),
+    ]
+
+
+_P = C.c_void_p
+_U32 = C.c_uint32
+_U64 = C.c_uint64
+_F = C.c_float
+
+_PROTOS = {
+    "orc_f32_to_f16": (C.c_uint16, [_F]),
+    "orc_f16_to_f32": (_F, [C.c_uint16]),
+    "orc_f32_to_f16_array": (None, [_P, _P, _U64]),
+    "orc_hash_u32": (_U32, [_U32]),
+    "orc_rand01": (_F, [_U32]),
+    "orc_splitmix_sequence": (None, [_U64, _U64, _P]),
+    "orc_stream_state": (_U64, [_U64, _U64]),
+    "orc_uniform_fill": (None, [_U64, _U64, _U64, _F, _F, _P]),
+    "orc_mlp_param_count": (_U32, [_U32]),
+    "orc_mlp_init": (None, [_U32, _P]),
+    "orc_grid_levels": (None, [_U32, _U32, _F, _U32, _U32, _P, _P]),
+    "orc_encode": (None, [C.POINTER(OrcGrid), _P, _P, _U32, _P, _P, _P]),
+    "orc_density_mlp": (None, [_P, _P, _U32, _P]),
+    "orc_density_forward": (None, [C.POINTER(OrcGrid), _P, _P, _P, _U32, _P]),
+    "orc_sh4": (None, [_P, _P]),
+    "orc_field_forward": (None, [C.POINTER(OrcGrid), _P, _P, _P, _P, _P, _U32, _P]),
+    "orc_det_expf": (_F, [_F]),
+    "orc_det_expf_array": (None, [_P, _U64, _P]),
+    "orc_scene_density": (None, [_P, _U32, _P, _U32, _P]),
+    "orc_occupancy_from_scene": (None, [_P, _U32, _U32, _P, _F, _P]),
+    "orc_march_count": (None, [C.POINTER(OrcCamera), _P, _U32, _P, _U32, _U32, _U32, _P]),
+    "orc_march_ray": (_U32, [C.POINTER(OrcCamera), _P, _U32, _P, _U32, _U32, _P, _U32]),
+    "orc_pixel_ray": (C.c_int, [C.POINTER(OrcCamera), _U32, _P, _P]),
+    "orc_composite_ray": (_U32, [_P, _P, _U32, _F, _P, _P, _P]),
+    "orc_render_rays": (None, [C.POINTER(OrcModel), C.POINTER(OrcCamera), _P, _U32, _P, _U32, _F, _P, _P, _U32, _P, _P, _P, _U32]),
+}
+
+_lib = None
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build()
+        L = C.CDLL(str(LIB_PATH))
+        for name, (res, args) in _PROTOS.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+# ------------------------------------------------------------------ helpers
+def f32_to_f16_bits(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty(x.shape, np.uint16)
+    lib().orc_f32_to_f16_array(_p(x), _p(out), x.size)
+    return out
+
+
+def f16_bits_to_f32(h: np.ndarray) -> np.ndarray:
+    f = lib().orc_f16_to_f32
+    return np.array([f(int(v)) for v in np.asarray(h).ravel()], np.float32).reshape(np.shape(h))
+
+
+def splitmix_sequence(state: int, n: int) -> np.ndarray:
+    out = np.empty(n, np.uint64)
+    lib().orc_splitmix_sequence(state, n, _p(out))
+    return out
+
+
+def uniform_fill(a: int, b: int, n: int, lo: float, hi: float) -> np.ndarray:
+    out = np.empty(n, np.float32)
+    lib().orc_uniform_fill(a, b, n, lo, hi, _p(out))
+    return out
+
+
+def mlp_init(network: int) -> np.ndarray:
+    out = np.empty(lib().orc_mlp_param_count(network), np.float32)
+    lib().orc_mlp_init(network, _p(out))
+    return out
+
+
+def grid_levels(n_levels: int, base: int, scale: float, finest: int, log2_t: int) -> tuple[np.ndarray, np.ndarray]:
+    res = np.zeros(16, np.uint32)
+    dense = np.zeros(16, np.uint32)
+    lib().orc_grid_levels(n_levels, base, scale, finest, log2_t, _p(res), _p(dense))
+    return res[:n_levels], dense[:n_levels]
+
+
+def make_grid(n_levels: int, log2_t: int, table_dtype: int, base: int = 16, scale: float = 1.3819, finest: int = 0) -> OrcGrid:
+    res, dense = grid_levels(n_levels, base, scale, finest, log2_t)
+    g = OrcGrid()
+    g.n_levels = n_levels
+    g.n_features = 2
+    g.table_size = 1 << log2_t
+    g.table_dtype = table_dtype
+    for i in range(n_levels):
+        g.resolution[i] = int(res[i])
+        g.dense[i] = int(dense[i])
+    return g
+
+
+def encode(grid: OrcGrid, table: np.ndarray, pos: np.ndarray, with_indices: bool = False):
+    pos = np.ascontiguousarray(pos, np.float32)
+    n = pos.shape[0]
+    feat = np.empty((n, grid.n_levels * 2), np.float32)
+    idx = np.empty((n, grid.n_levels, 8), np.uint32) if with_indices else None
+    w = np.empty((n, grid.n_levels, 8), np.float32) if with_indices else None
+    lib().orc_encode(C.byref(grid), _p(table), _p(pos), n, _p(feat), _p(idx) if with_indices else None, _p(w) if with_indices else None)
+    return (feat, idx, w) if with_indices else feat
+
+
+def density_mlp(params_f16_bits: np.ndarray, features: np.ndarray) -> np.ndarray:
+    features = np.ascontiguousarray(features, np.float32)
+    out = np.empty((features.shape[0], 16), np.float32)
+    lib().orc_density_mlp(_p(params_f16_bits), _p(features), features.shape[0], _p(out))
+    return out
+
+
+def density_forward(grid: OrcGrid, table: np.ndarray, params_f16_bits: np.ndarray, pos: np.ndarray) -> np.ndarray:
+    pos = np.ascontiguousarray(pos, np.float32)
+    out = np.empty((pos.shape[0], 16), np.float32)
+    lib().orc_density_forward(C.byref(grid), _p(table), _p(params_f16_bits), _p(pos), pos.shape[0], _p(out))
+    return out
+
+
+def sh4(d: np.ndarray) -> np.ndarray:
+    d = np.ascontiguousarray(d, np.float32).reshape(-1, 3)
+    out = np.empty((d.shape[0], 16), np.float32)
+    for i in range(d.shape[0]):
+        lib().orc_sh4(_p(d[i]), out[i].ctypes.data)
+    return out
+
+
+def field_forward(grid: OrcGrid, table: np.ndarray, dparams_bits: np.ndarray, cparams_bits: np.ndarray, pos: np.ndarray, dirs: np.ndarray) -> np.ndarray:
+    pos = np.ascontiguousarray(pos, np.float32)
+    dirs = np.ascontiguousarray(dirs, np.float32)
+    out = np.empty((pos.shape[0], 4), np.float32)
+    lib().orc_field_forward(C.byref(grid), _p(table), _p(dparams_bits), _p(cparams_bits), _p(pos), _p(dirs), pos.shape[0], _p(out))
+    return out
+
+
+def det_expf(x) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty_like(x)
+    lib().orc_det_expf_array(_p(x), x.size, _p(out))
+    return out
+
+
+def scene_density(gaussians: np.ndarray, pos: np.ndarray) -> np.ndarray:
+    g = np.ascontiguousarray(gaussians, np.float32)
+    pos = np.ascontiguousarray(pos, np.float32)
+    out = np.empty(pos.shape[0], np.float32)
+    lib().orc_scene_density(_p(g), g.shape[0], _p(pos), pos.shape[0], _p(out))
+    return out
+
+
+def occupancy_from_scene(gaussians: np.ndarray, res: int, aabb=(0, 0, 0, 1, 1, 1), threshold: float = 0.01) -> np.ndarray:
+    g = np.ascontiguousarray(gaussians, np.float32)
+    box = np.array(aabb, np.float32)
+    bits = np.zeros((res ** 3 + 31) // 32, np.uint32)
+    lib().orc_occupancy_from_scene(_p(g), g.shape[0], res, _p(box), threshold, _p(bits))
+    return bits
+
+
+def camera(c2w12, fx, fy, cx, cy, width, height) -> OrcCamera:
+    cam = OrcCamera()
+    for i in range(12):
+        cam.c2w[i] = float(c2w12[i])
+    cam.fx, cam.fy, cam.cx, cam.cy = fx, fy, cx, cy
+    cam.width, cam.height = width, height
+    return cam
+
+
+def camera_from_bytes(raw: bytes) -> OrcCamera:
+    """An OrcCamera from the bytes of a layout-identical NerfExtCamera."""
+    cam = OrcCamera()
+    C.memmove(C.addressof(cam), raw, C.sizeof(OrcCamera))
+    return cam
+
+
+def march_count(cam: OrcCamera, bits: np.ndarray | None, res: int, aabb, max_steps: int, ray_begin: int = 0, n: int | None = None) -> np.ndarray:
+    if n is None:
+        n = cam.width * cam.height - ray_begin
+    box = np.array(aabb, np.float32)
+    out = np.empty(n, np.uint32)
+    lib().orc_march_count(C.byref(cam), _p(bits) if bits is not None else None, res, _p(box), max_steps, ray_begin, n, _p(out))
+    return out
+
+
+def march_ray(cam: OrcCamera, bits: np.ndarray | None, res: int, aabb, max_steps: int, ray: int) -> np.ndarray:
+    box = np.array(aabb, np.float32)
+    cap = max_steps
+    buf = np.empty((cap, 2), np.float32)
+    k = lib().orc_march_ray(C.byref(cam), _p(bits) if bits is not None else None, res, _p(box), max_steps, ray, _p(buf), cap)
+    return buf[:k].copy()
+
+
+def pixel_ray(cam: OrcCamera, ray: int, aabb) -> np.ndarray | None:
+    box = np.array(aabb, np.float32)
+    out = np.empty(8, np.float32)
+    ok = lib().orc_pixel_ray(C.byref(cam), ray, _p(box), _p(out))
+    return out if ok else None
+
+
+def composite_ray(sigma_rgb: np.ndarray, dt: np.ndarray, t_stop: float = 1e-4, bg=(1.0, 1.0, 1.0)):
+    s = np.ascontiguousarray(sigma_rgb, np.float32)
+    d = np.ascontiguousarray(dt, np.float32)
+    b = np.array(bg, np.float32)
+    rgb = np.empty(3, np.float32)
+    rgba = np.empty(1, np.uint32)
+    used = lib().orc_composite_ray(_p(s), _p(d), s.shape[0], t_stop, _p(b), _p(rgb), _p(rgba))
+    return rgb, int(rgba[0]), int(used)
+
+
+def render_rays(grid: OrcGrid, table: np.ndarray, dparams_bits: np.ndarray, cparams_bits: np.ndarray, cam: OrcCamera, bits: np.ndarray | None, res: int, aabb, max_steps: int, rays: np.ndarray, t_stop: float = 1e-4, bg=(1.0, 1.0, 1.0),
+                threads: int = 1):
+    model = OrcModel()
+    model.grid = grid
+    model.table = _p(table)
+    model.density_params = _p(dparams_bits)
+    model.color_params = _p(cparams_bits)
+    rays = np.ascontiguousarray(rays, np.uint32)
+    box = np.array(aabb, np.float32)
+    b = np.array(bg, np.float32)
+    rgb = np.empty((rays.size, 3), np.float32)
+    rgba = np.empty(rays.size, np.uint32)
+    counts = np.empty(rays.size, np.uint32)
+    lib().orc_render_rays(C.byref(model), C.byref(cam), _p(bits) if bits is not None else None, res, _p(box), max_steps, t_stop, _p(b), _p(rays), rays.size, _p(rgb), _p(rgba), _p(counts), threads)
+    return rgb, rgba, counts

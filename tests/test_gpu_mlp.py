@@ -1,0 +1,93 @@
+"""GPU MLP parity (fp16 MFMA, fp32 accumulate) against the oracle (fp16
+rounding points, fp64 accumulation): within 1e-3 relative."""
+import numpy as np
+import pytest
+
+from conftest import announce
+from helpers import L, ext, orc, DeviceArray, synchronize, byref, oracle_grid, host_table, host_params, points, unit_dirs, assert_rel
+
+pytestmark = pytest.mark.gpu
+
+
+def test_density_mlp_on_features():
+    n = 4099  # ragged: not a multiple of 16
+    announce(f"density mlp n={n}")
+    rng = np.random.default_rng(11)
+    feat = rng.normal(0, 1, (n, 32)).astype(np.float16)
+    w = ext.mlp_init(0).astype(np.float16)
+    d_w = DeviceArray.from_numpy(w)
+    d_f = DeviceArray.from_numpy(feat)
+    d_o = DeviceArray((n, 16), np.float32)
+    L.call("nerf_ext_density_mlp", d_w.ptr, d_f.ptr, n, d_o.ptr, None)
+    synchronize()
+    want = orc.density_mlp(w.view(np.uint16), feat.astype(np.float32))
+    assert_rel(d_o.numpy(), want, what="density mlp")
+
+
+def test_density_mlp_structured_weights():
+    """Identity-like weights: output k is relu(feature k) — checks MFMA operand layouts row by row."""
+    n = 64
+    announce("density mlp identity weights")
+    W1 = np.zeros((64, 32), np.float32)
+    W1[:32, :32] = np.eye(32)
+    W1[32:, :] = -np.eye(32)
+    W2 = np.zeros((16, 64), np.float32)
+    W2[:, :16] = np.eye(16)
+    W2[:, 32:48] += 0.5 * np.eye(16)[:, :16][:, ::-1]
+    w = np.concatenate([W1.ravel(), W2.ravel()]).astype(np.float16)
+    rng = np.random.default_rng(12)
+    feat = rng.normal(0, 2, (n, 32)).astype(np.float16)
+    d_w, d_f, d_o = DeviceArray.from_numpy(w), DeviceArray.from_numpy(feat), DeviceArray((n, 16), np.float32)
+    L.call("nerf_ext_density_mlp", d_w.ptr, d_f.ptr, n, d_o.ptr, None)
+    synchronize()
+    x = feat.astype(np.float32)
+    want = np.maximum(x[:, :16], 0) + 0.5 * np.maximum(-x[:, 15::-1], 0)
+    np.testing.assert_allclose(d_o.numpy(), want, rtol=1e-3, atol=1e-3)
+    np.testing.assert_allclose(d_o.numpy(), orc.density_mlp(w.view(np.uint16), x), rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("n", [1 << 16, 1000])
+def test_density_forward_hash_grid_f32_2p16(n):
+    """Hash encode + density MLP, 16 levels x 2 fp32 features, T = 2^16, points
+    from seed 0; output (exp(raw0), raw1..15)."""
+    announce(f"density forward n={n}")
+    desc = ext.grid_desc(16, L.NERF_EXT_F32)
+    model = ext.Model.create(desc, seed=0)
+    pos = points(n, seed=0)
+    d_pos = DeviceArray.from_numpy(pos)
+    d_o = DeviceArray((n, 16), np.float32)
+    L.call("nerf_ext_density_forward", byref(desc), model.table.ptr, model.density.ptr, d_pos.ptr, n, d_o.ptr, None)
+    synchronize()
+    want = orc.density_forward(oracle_grid(desc), host_table(model), host_params(model)[0], pos)
+    assert_rel(d_o.numpy(), want, what="density forward")
+
+
+def test_density_forward_large_table_values():
+    """A table with O(1) entries drives hidden activations across the fp16 range."""
+    n = 8192
+    announce(f"density forward O(1) table n={n}")
+    desc = ext.grid_desc(16, L.NERF_EXT_F32)
+    model = ext.Model.create(desc, seed=5, table_range=1.0)
+    pos = points(n, seed=2)
+    d_pos, d_o = DeviceArray.from_numpy(pos), DeviceArray((n, 16), np.float32)
+    L.call("nerf_ext_density_forward", byref(desc), model.table.ptr, model.density.ptr, d_pos.ptr, n, d_o.ptr, None)
+    synchronize()
+    want = orc.density_forward(oracle_grid(desc), host_table(model), host_params(model)[0], pos)
+    assert_rel(d_o.numpy(), want, what="density forward O(1) table")
+
+
+@pytest.mark.parametrize("log2_t,dtype", [(19, L.NERF_EXT_F16), (16, L.NERF_EXT_F32)])
+def test_field_forward(log2_t, dtype):
+    n = 8195
+    announce(f"field forward n={n} log2_t={log2_t}")
+    desc = ext.grid_desc(log2_t, dtype)
+    model = ext.Model.create(desc, seed=1, table_range=0.5)
+    pos = points(n, seed=3)
+    dirs = unit_dirs(n, seed=4)
+    d_pos, d_dir, d_o = DeviceArray.from_numpy(pos), DeviceArray.from_numpy(dirs), DeviceArray((n, 4), np.float32)
+    ms = model.struct()
+    L.call("nerf_ext_field_forward", byref(ms), d_pos.ptr, d_dir.ptr, n, d_o.ptr, None)
+    synchronize()
+    dp, cp = host_params(model)
+    want = orc.field_forward(oracle_grid(desc), host_table(model), dp, cp, pos, dirs)
+    assert_rel(d_o.numpy(), want, what="field forward")
