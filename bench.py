@@ -98,6 +98,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain fp32->fp16 conversion over MIB MiB of input (reads 4 B, writes 2 B per element) to calibrate HBM counters, then exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this backend runs on one GPU; --gpus {args.gpus} is not supported (multi-GPU sharding is design-only)", file=sys.stderr)
@@ -107,6 +109,15 @@ def main() -> int:
     from nerf_amd.device import DeviceArray, Event, Stream, device_info, synchronize
 
     L.load()
+    if args.copy_calibration:
+        n = args.copy_calibration * (1 << 20) // 4
+        src, dst = DeviceArray((n,), np.float32), DeviceArray((n,), np.float16)
+        src.fill_bytes(0)
+        for _ in range(3):
+            L.call("nerf_ext_float_to_half", src.ptr, dst.ptr, n, None)
+        synchronize()
+        print(json.dumps({"copy_calibration": {"elements": n, "read_bytes": 4 * n, "write_bytes": 2 * n, "kernel": "k_float_to_half", "launches": 3}}), flush=True)
+        return 0
     info = device_info()
     scene, bits, desc, model, cam, occ = build_workload()
     stream = Stream()
