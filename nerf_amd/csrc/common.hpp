@@ -49,6 +49,16 @@ typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
+// fp32 -> fp16, round to nearest even, of an fp32 value that has been rounded
+// to fp32 first.  The empty asm makes the value opaque, which stops the
+// compiler from fusing a preceding multiply into the conversion
+// (v_fma_mixlo_f16 rounds the exact product once, straight to fp16, which can
+// differ from rounding to fp32 and then to fp16).
+__device__ __forceinline__ half_t to_half_rne(float x) {
+    asm volatile("" : "+v"(x));
+    return (half_t)x;
+}
+
 // ------------------------------------------------------------- hash grid
 // Per-level parameters of a hash grid, passed by value to kernels.
 struct GridParams {

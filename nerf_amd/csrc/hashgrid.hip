@@ -44,12 +44,15 @@ NerfStatus make_grid(const NerfExtGridDesc* d, GridParams& g) {
 // Table init: element i (memory order) = U(-range, range) from splitmix64
 // stream (0x7ab1e, seed), the same generator as the reference's weight init
 // (backend-cuda.cu:1819-1824) evaluated at its closed form per element.
+__device__ __forceinline__ void store_value(float* p, float v) { *p = v; }
+__device__ __forceinline__ void store_value(half_t* p, float v) { *p = to_half_rne(v); }
+
 template <typename T>
 __global__ __launch_bounds__(256) void k_init_table(T* table, uint64_t count, uint64_t state0, float range) {
     const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += stride) {
         const float u = nerf_math::unit24(nerf_math::splitmix_at(state0, i));
-        table[i]      = (T)((u * 2.0f - 1.0f) * range);
+        store_value(table + i, (u * 2.0f - 1.0f) * range);
     }
 }
 
@@ -82,8 +85,8 @@ __global__ __launch_bounds__(256) void k_encode_forward(GridParams g, const Tabl
         a1            = a1 + w * v1[k];
     }
     OutT* o = out + (uint64_t)i * (g.n_levels * 2u) + level * 2u;
-    o[0]    = (OutT)a0;
-    o[1]    = (OutT)a1;
+    store_value(o, a0);
+    store_value(o + 1, a1);
 }
 
 __global__ __launch_bounds__(256) void k_encode_indices(GridParams g, const float* __restrict__ pos, uint32_t n, uint32_t* __restrict__ indices, float* __restrict__ weights) {
