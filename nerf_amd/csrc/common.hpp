@@ -182,7 +182,7 @@ struct FieldWeights {
 
 // out4 [n] float4 (sigma, r, g, b).
 hipError_t launch_field(const GridParams& g, const void* table, const FieldWeights& w, const FieldInputs& in, uint32_t n, float4* out4, hipStream_t stream);
-// Density-only (config 1): out [n][16] = (exp(raw0), raw1..15).
+// Density network only, on points or on fp16 features: out [n][16] = (exp(raw0), raw1..15).
 hipError_t launch_density(const GridParams& g, const void* table, const half_t* dparams, const float* positions, const half_t* features, uint32_t n, float* out, hipStream_t stream);
 
 // Number of compute units of the current device (cached).

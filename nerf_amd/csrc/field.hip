@@ -239,7 +239,7 @@ __global__ __launch_bounds__(kBlockThreads) void k_density_mlp(const half_t* __r
     }
 }
 
-// Fused encode + density MLP (config 1): out [n][16] = (exp(raw0), raw1..15).
+// Fused encode + density MLP on points: out [n][16] = (exp(raw0), raw1..15).
 template <typename TableT>
 __global__ __launch_bounds__(kBlockThreads) void k_density_forward(GridParams g, const TableT* __restrict__ table, const half_t* __restrict__ params, const float* __restrict__ pos, uint32_t n, float* __restrict__ out) {
     __shared__ half_t sp[NERF_EXT_DENSITY_PARAMS];

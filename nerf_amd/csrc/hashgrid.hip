@@ -6,7 +6,8 @@
 //
 // Standalone forward kernel layout: grid.y = level, so at any moment the
 // resident workgroups gather from one or two levels' tables and each XCD's L2
-// holds the level being read (C1: 512 KiB per level, C2: 2 MiB).
+// holds the level being read (512 KiB per level for T = 2^16 fp32, 2 MiB for
+// T = 2^19 fp16).
 #include <math.h>
 
 #include "common.hpp"

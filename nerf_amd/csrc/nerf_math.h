@@ -68,7 +68,7 @@ NERF_HD float unit24(uint64_t z) {
 // Deterministic exp for binary32, used where host and device must agree bit for
 // bit (the analytic Gaussian density that feeds the occupancy bitfield).
 // Method: Cody & Waite argument reduction x = k ln2 + r with ln2 split into
-// C1 = 0.693359375 (exact in 9 bits) and C2 = -2.12194440e-4, followed by the
+// ln2_hi = 0.693359375 (exact in 9 bits) and ln2_lo = -2.12194440e-4, followed by the
 // degree-7 minimax polynomial for exp(r) on [-ln2/2, ln2/2] from S. L. Moshier's
 // Cephes library (expf.c), and scaling by 2^k through the exponent field.
 // Inputs below -87 return 0 (results that would be subnormal are flushed) and
