@@ -608,3 +608,195 @@ extern "C" void orc_render_rays(const OrcModel* model, const OrcCamera* cam, con
     for (auto& th : pool) th.join();
 }
 
+
+// ===========================================================================
+// Training: composite backward with Huber loss, MLP backward, hash-grid
+// scatter-add, Adam.
+// ===========================================================================
+
+// Huber loss of x with threshold delta (Huber 1964): 0.5 x^2 for |x| <= delta,
+// delta (|x| - delta / 2) otherwise; derivative clamp(x, -delta, delta).
+static inline double huber(double x, double d) { return fabs(x) <= d ? 0.5 * x * x : d * (fabs(x) - 0.5 * d); }
+
+// Forward + backward of front-to-back compositing for one ray (reference
+// backend-cuda.cu:1095-1182 generalised to exp density, Huber loss and a
+// background colour).  sigma = exp(raw), c = sigmoid(raw_rgb),
+// alpha_i = 1 - exp(-sigma_i max(dt_i, 0)), T_{i+1} = T_i (1 - alpha_i),
+// pred = sum_i T_i alpha_i c_i + T_n bg.  Loss = inv_norm * sum_c huber(pred_c
+// - gt_c).  Gradients wrt the raw network outputs, with the suffix
+// S_i = sum_{j>i} w_j c_j + T_n bg (:1140-1170):
+//   d raw_rgb_ic   = w_i g_c c_ic (1 - c_ic)
+//   d raw_sigma_i  = dt_i sigma_i sum_c g_c (T_{i+1} c_ic - S_ic)
+// (the reference's T_i c - S / (1 - alpha) times d alpha / d raw =
+// dt sigma (1 - alpha)).  Evaluated in fp64; returns the un-normalised loss.
+extern "C" double orc_composite_backward_ray(const float* sraw, const float* rgbraw, const float* dt, uint32_t n, const float* gt, const float* bg, float delta, float inv_norm, float* dsraw, float* drgbraw, float* pred_out) {
+    std::vector<double> sig(n), a(n), T(n + 1), c(3 * (size_t)n);
+    T[0] = 1.0;
+    double pred[3] = {0, 0, 0};
+    for (uint32_t i = 0; i < n; ++i) {
+        sig[i]           = exp((double)sraw[i]);
+        const double dti = dt[i] > 0.0f ? (double)dt[i] : 0.0;
+        a[i]             = 1.0 - exp(-sig[i] * dti);
+        for (int k = 0; k < 3; ++k) {
+            c[3 * i + k] = 1.0 / (1.0 + exp(-(double)rgbraw[3 * i + k]));
+            pred[k] += T[i] * a[i] * c[3 * i + k];
+        }
+        T[i + 1] = T[i] * (1.0 - a[i]);
+    }
+    double loss = 0.0, g[3];
+    for (int k = 0; k < 3; ++k) {
+        pred[k] += T[n] * bg[k];
+        const double x = pred[k] - gt[k];
+        loss += huber(x, delta);
+        g[k] = (x > delta ? delta : (x < -delta ? -delta : x)) * inv_norm;
+        if (pred_out) pred_out[k] = (float)pred[k];
+    }
+    double S[3] = {T[n] * bg[0], T[n] * bg[1], T[n] * bg[2]};
+    for (int i = (int)n - 1; i >= 0; --i) {
+        const double dti = dt[i] > 0.0f ? (double)dt[i] : 0.0;
+        const double w   = T[i] * a[i];
+        double ds        = 0.0;
+        for (int k = 0; k < 3; ++k) {
+            const double ci        = c[3 * i + k];
+            drgbraw[3 * i + k]     = (float)(w * g[k] * ci * (1.0 - ci));
+            ds += g[k] * (T[i + 1] * ci - S[k]);
+            S[k] += w * ci;
+        }
+        dsraw[i] = (float)(dti * sig[i] * ds);
+    }
+    return loss;
+}
+
+// MLP backward for n samples with the GPU's fp16 rounding points.
+// Inputs: features [n][32] (fp16 values), directions [n][3], upstream
+// d_sigma_raw [n] and d_rgb_raw [n][3], loss_scale.  Forward activations are
+// recomputed exactly as in density_row / color_row.  Deltas are scaled by
+// loss_scale and rounded to fp16 where the GPU feeds them to MFMA:
+//   do3 = f16(ls * d_rgb_raw) (rows 0..2), dh2 = f16(mask(h2) C3^T do3),
+//   dh1 = f16(mask(h1) C2^T dh2), dgeo = (C1^T dh1)[geo],
+//   do = f16(ls * d_sigma_raw | dgeo), dhd = f16(mask(hd) D2^T do),
+//   dfeat = D1^T dhd (fp32, still scaled by ls).
+// Weight gradients (scaled by ls) accumulate in fp64: dW = sum delta (x) act.
+// Layouts of dD (3072) and dC (7168) follow the parameter packing.
+extern "C" void orc_mlp_backward(const uint16_t* dp, const uint16_t* cp, const float* features, const float* dirs, const float* dsraw, const float* drgbraw, uint32_t n, float loss_scale, float* dfeat, double* dD, double* dC) {
+    auto W = [](const uint16_t* P, uint32_t off, uint32_t n_in, uint32_t o, uint32_t k) { return (double)orc_f16_to_f32(P[off + o * n_in + k]); };
+    for (uint32_t s = 0; s < n; ++s) {
+        float x[32], hd[64], o[16], xc[32], h1[64], h2[64], sh[16];
+        for (int k = 0; k < 32; ++k) x[k] = r16(features[32ull * s + k]);
+        matvec(dp, 64, 32, x, hd);
+        for (int k = 0; k < 64; ++k) hd[k] = r16(fmaxf(hd[k], 0.0f));
+        matvec(dp + 2048, 16, 64, hd, o);
+        orc_sh4(dirs + 3ull * s, sh);
+        for (int k = 0; k < 15; ++k) xc[k] = r16(o[1 + k]);
+        for (int k = 0; k < 16; ++k) xc[15 + k] = r16(sh[k]);
+        xc[31] = 0.0f;
+        matvec(cp, 64, 32, xc, h1);
+        for (int k = 0; k < 64; ++k) h1[k] = r16(fmaxf(h1[k], 0.0f));
+        matvec(cp + 2048, 64, 64, h1, h2);
+        for (int k = 0; k < 64; ++k) h2[k] = r16(fmaxf(h2[k], 0.0f));
+        // colour backward
+        float do3[16] = {0};
+        for (int c = 0; c < 3; ++c) do3[c] = r16(loss_scale * drgbraw[3ull * s + c]);
+        float dh2[64], dh1[64];
+        for (int k = 0; k < 64; ++k) {
+            double acc = 0.0;
+            for (int q = 0; q < 16; ++q) acc += W(cp, 6144, 64, q, k) * do3[q];
+            dh2[k] = h2[k] > 0.0f ? r16((float)acc) : 0.0f;
+        }
+        for (int k = 0; k < 64; ++k) {
+            double acc = 0.0;
+            for (int q = 0; q < 64; ++q) acc += W(cp, 2048, 64, q, k) * dh2[q];
+            dh1[k] = h1[k] > 0.0f ? r16((float)acc) : 0.0f;
+        }
+        float dgeo[15];
+        for (int k = 0; k < 15; ++k) {
+            double acc = 0.0;
+            for (int q = 0; q < 64; ++q) acc += W(cp, 0, 32, q, k) * dh1[q];
+            dgeo[k] = (float)acc;
+        }
+        // density backward
+        float dout[16];
+        dout[0] = r16(loss_scale * dsraw[s]);
+        for (int k = 0; k < 15; ++k) dout[1 + k] = r16(dgeo[k]);
+        float dhd[64];
+        for (int k = 0; k < 64; ++k) {
+            double acc = 0.0;
+            for (int q = 0; q < 16; ++q) acc += W(dp, 2048, 64, q, k) * dout[q];
+            dhd[k] = hd[k] > 0.0f ? r16((float)acc) : 0.0f;
+        }
+        for (int k = 0; k < 32; ++k) {
+            double acc = 0.0;
+            for (int q = 0; q < 64; ++q) acc += W(dp, 0, 32, q, k) * dhd[q];
+            dfeat[32ull * s + k] = (float)acc;
+        }
+        // weight gradients
+        for (int q = 0; q < 64; ++q)
+            for (int k = 0; k < 32; ++k) dD[q * 32 + k] += (double)dhd[q] * x[k];
+        for (int q = 0; q < 16; ++q)
+            for (int k = 0; k < 64; ++k) dD[2048 + q * 64 + k] += (double)dout[q] * hd[k];
+        for (int q = 0; q < 64; ++q)
+            for (int k = 0; k < 32; ++k) dC[q * 32 + k] += (double)dh1[q] * xc[k];
+        for (int q = 0; q < 64; ++q)
+            for (int k = 0; k < 64; ++k) dC[2048 + q * 64 + k] += (double)dh2[q] * h1[k];
+        for (int q = 0; q < 16; ++q)
+            for (int k = 0; k < 64; ++k) dC[6144 + q * 64 + k] += (double)do3[q] * h2[k];
+    }
+}
+
+// Hash-grid backward: dtable[l][idx_c][f] += w_c * dfeat[2l + f] over the 8
+// corners of every level of every point (fp64 accumulation, so the result does
+// not depend on summation order).  dtable: [L][T][F] doubles.
+extern "C" void orc_encode_backward(const OrcGrid* g, const float* pos, const float* dfeat, uint32_t n, double* dtable) {
+    for (uint32_t s = 0; s < n; ++s) {
+        for (uint32_t l = 0; l < g->n_levels; ++l) {
+            const uint32_t N = g->resolution[l];
+            const float sc   = (float)N;
+            uint32_t i0[3];
+            float wa[3];
+            for (int a = 0; a < 3; ++a) {
+                const float x = fminf(fmaxf(pos[3ull * s + a], 0.0f), 1.0f);
+                const float p = x * sc;
+                uint32_t cidx = (uint32_t)floorf(p);
+                if (cidx >= N) cidx = N - 1u;
+                i0[a] = cidx;
+                wa[a] = p - (float)cidx;
+            }
+            for (uint32_t c = 0; c < 8u; ++c) {
+                const uint32_t cx = i0[0] + (c & 1u), cy = i0[1] + ((c >> 1) & 1u), cz = i0[2] + ((c >> 2) & 1u);
+                uint32_t id;
+                if (g->dense[l]) {
+                    const uint32_t st = N + 1u;
+                    id                = cx + cy * st + cz * st * st;
+                } else {
+                    id = ((cx * 1u) ^ (cy * 2654435761u) ^ (cz * 805459861u)) & (g->table_size - 1u);
+                }
+                const float wx  = (c & 1u) ? wa[0] : 1.0f - wa[0];
+                const float wy  = (c & 2u) ? wa[1] : 1.0f - wa[1];
+                const float wz  = (c & 4u) ? wa[2] : 1.0f - wa[2];
+                const double wt = (double)((wx * wy) * wz);
+                for (uint32_t f = 0; f < g->n_features; ++f)
+                    dtable[((uint64_t)l * g->table_size + id) * g->n_features + f] += wt * (double)dfeat[(uint64_t)s * g->n_levels * g->n_features + l * g->n_features + f];
+            }
+        }
+    }
+}
+
+// Adam step of backend-cuda.cu:1513-1554 on n parameters: grads are scaled by
+// loss_scale; skip when non-finite or norm > guard; lr decays by 0.1 per
+// decay_ksteps * 1000 steps; global-norm clip; bias corrections 1/(1 - b^t).
+// step is the 1-based optimizer step t.  Returns 1 if the update was skipped.
+extern "C" int orc_adam(float* w, float* m, float* v, const float* g, uint64_t n, float lr, float b1, float b2, float eps, float clip, float guard, float loss_scale, uint32_t decay_ksteps, uint32_t step, double grad_norm, int nonfinite) {
+    if (nonfinite || !(grad_norm == grad_norm) || grad_norm > guard) return 1;
+    const float decay = (float)decay_ksteps * 1000.0f;
+    const float lr_t  = decay > 0.0f ? lr * powf(0.1f, (float)step / decay) : lr;
+    const float scale = (grad_norm > clip && grad_norm > 0.0) ? (float)(clip / grad_norm) : 1.0f;
+    const float bc1   = 1.0f / (1.0f - powf(b1, (float)step));
+    const float bc2   = 1.0f / (1.0f - powf(b2, (float)step));
+    for (uint64_t i = 0; i < n; ++i) {
+        const float gr = g[i] / loss_scale * scale;
+        m[i]           = b1 * m[i] + (1.0f - b1) * gr;
+        v[i]           = b2 * v[i] + (1.0f - b2) * gr * gr;
+        w[i] -= lr_t * (m[i] * bc1) / (sqrtf(v[i] * bc2) + eps);
+    }
+    return 0;
+}

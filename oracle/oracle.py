@@ -78,6 +78,10 @@ _PROTOS = {
     "orc_march_ray": (_U32, [C.POINTER(OrcCamera), _P, _U32, _P, _U32, _U32, _P, _U32]),
     "orc_pixel_ray": (C.c_int, [C.POINTER(OrcCamera), _U32, _P, _P]),
     "orc_composite_ray": (_U32, [_P, _P, _U32, _F, _P, _P, _P]),
+    "orc_composite_backward_ray": (C.c_double, [_P, _P, _P, _U32, _P, _P, _F, _F, _P, _P, _P]),
+    "orc_mlp_backward": (None, [_P, _P, _P, _P, _P, _P, _U32, _F, _P, _P, _P]),
+    "orc_encode_backward": (None, [C.POINTER(OrcGrid), _P, _P, _U32, _P]),
+    "orc_adam": (C.c_int, [_P, _P, _P, _P, _U64, _F, _F, _F, _F, _F, _F, _F, _U32, _U32, C.c_double, C.c_int]),
     "orc_render_rays": (None, [C.POINTER(OrcModel), C.POINTER(OrcCamera), _P, _U32, _P, _U32, _F, _P, _P, _U32, _P, _P, _P, _U32]),
 }
 
@@ -286,3 +290,46 @@ def render_rays(grid: OrcGrid, table: np.ndarray, dparams_bits: np.ndarray, cpar
     counts = np.empty(rays.size, np.uint32)
     lib().orc_render_rays(C.byref(model), C.byref(cam), _p(bits) if bits is not None else None, res, _p(box), max_steps, t_stop, _p(b), _p(rays), rays.size, _p(rgb), _p(rgba), _p(counts), threads)
     return rgb, rgba, counts
+
+
+# ------------------------------------------------------------------ training
+def composite_backward_ray(sraw, rgbraw, dt, gt, bg=(1.0, 1.0, 1.0), delta=0.1, inv_norm=1.0):
+    sraw = np.ascontiguousarray(sraw, np.float32)
+    rgbraw = np.ascontiguousarray(rgbraw, np.float32).reshape(-1, 3)
+    dt = np.ascontiguousarray(dt, np.float32)
+    gt = np.array(gt, np.float32)
+    b = np.array(bg, np.float32)
+    n = sraw.size
+    ds = np.empty(n, np.float32)
+    drgb = np.empty((n, 3), np.float32)
+    pred = np.empty(3, np.float32)
+    loss = lib().orc_composite_backward_ray(_p(sraw), _p(rgbraw), _p(dt), n, _p(gt), _p(b), delta, inv_norm, _p(ds), _p(drgb), _p(pred))
+    return float(loss), ds, drgb, pred
+
+
+def mlp_backward(dparams_bits, cparams_bits, features, dirs, dsraw, drgbraw, loss_scale):
+    features = np.ascontiguousarray(features, np.float32)
+    dirs = np.ascontiguousarray(dirs, np.float32)
+    dsraw = np.ascontiguousarray(dsraw, np.float32)
+    drgbraw = np.ascontiguousarray(drgbraw, np.float32)
+    n = features.shape[0]
+    dfeat = np.empty((n, 32), np.float32)
+    dD = np.zeros(3072, np.float64)
+    dC = np.zeros(7168, np.float64)
+    lib().orc_mlp_backward(_p(dparams_bits), _p(cparams_bits), _p(features), _p(dirs), _p(dsraw), _p(drgbraw), n, loss_scale, _p(dfeat), _p(dD), _p(dC))
+    return dfeat, dD, dC
+
+
+def encode_backward(grid: OrcGrid, pos, dfeat):
+    pos = np.ascontiguousarray(pos, np.float32)
+    dfeat = np.ascontiguousarray(dfeat, np.float32)
+    out = np.zeros(grid.n_levels * grid.table_size * 2, np.float64)
+    lib().orc_encode_backward(C.byref(grid), _p(pos), _p(dfeat), pos.shape[0], _p(out))
+    return out
+
+
+def adam(w, m, v, g, lr, b1, b2, eps, clip, guard, loss_scale, decay_ksteps, step, grad_norm, nonfinite=0):
+    for a in (w, m, v):
+        assert a.dtype == np.float32 and a.flags["C_CONTIGUOUS"]
+    g = np.ascontiguousarray(g, np.float32)
+    return lib().orc_adam(_p(w), _p(m), _p(v), _p(g), w.size, lr, b1, b2, eps, clip, guard, loss_scale, decay_ksteps, step, grad_norm, nonfinite)
