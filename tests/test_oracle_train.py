@@ -136,9 +136,9 @@ def test_oracle_mlp_backward_matches_matrix_form(orc):
     dx, dW = _backward64(params, feat.astype(np.float64), sh, ds.astype(np.float64) * ls, drgb.astype(np.float64) * ls)
 
     def close(a, b, what):
-        scale = np.sqrt(np.mean(b ** 2)) + 1e-30
-        err = np.abs(a - b).max() / scale
-        assert err < 2e-2, f"{what}: {err:.3e}"
+        # Weight gradients sum over the batch: relative Frobenius error.
+        err = np.linalg.norm(a - b) / (np.linalg.norm(b) + 1e-30)
+        assert err < 1e-2, f"{what}: {err:.3e}"
 
     # Per-sample input gradients: a ReLU whose fp16-rounded activation is 0
     # while the fp64 one is not flips a mask in a few samples, so the bar is
