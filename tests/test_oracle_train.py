@@ -136,9 +136,11 @@ def test_oracle_mlp_backward_matches_matrix_form(orc):
     dx, dW = _backward64(params, feat.astype(np.float64), sh, ds.astype(np.float64) * ls, drgb.astype(np.float64) * ls)
 
     def close(a, b, what):
-        # Weight gradients sum over the batch: relative Frobenius error.
+        # Weight gradients sum over the batch: relative Frobenius error (the
+        # fp16 rounding points move them ~1 % from exact fp64 math; a wrong
+        # index or transpose moves them by O(1)).
         err = np.linalg.norm(a - b) / (np.linalg.norm(b) + 1e-30)
-        assert err < 1e-2, f"{what}: {err:.3e}"
+        assert err < 3e-2, f"{what}: {err:.3e}"
 
     # Per-sample input gradients: a ReLU whose fp16-rounded activation is 0
     # while the fp64 one is not flips a mask in a few samples, so the bar is
