@@ -209,6 +209,107 @@ NERF_API NerfStatus nerf_ext_renderer_destroy(NerfExtRenderer* renderer);
  * synchronises and times each stage with HIP events on desc->stream. */
 NERF_API NerfStatus nerf_ext_render(NerfExtRenderer* renderer, const NerfExtRenderDesc* desc, uint32_t* rgba8, float* rgb_f32, uint32_t* counts, NerfExtRenderStats* stats);
 
+/* Ground truth of the analytic scene: volume rendering of density(p) with
+ * colour(p) = sum_g A_g G_g(p) albedo_g / density(p), uniform steps of
+ * (t_far - t_near) / steps over the AABB, white background; RGBA8 with
+ * alpha = 1 - T.  rgba8: device [view][H][W]. */
+NERF_API NerfStatus nerf_ext_scene_render(const NerfExtGaussian* gaussians, uint32_t count, const NerfExtCamera* cameras, uint32_t view_count, const float* aabb6, uint32_t steps, uint32_t* rgba8, void* stream);
+
+/* ---------------------------------------------------------------- training */
+/* One training step (the reference's nerf_train_step, backend-cuda.cu:2405,
+ * with the graph of :2199-2402): pick a camera (hash of the step, :1482),
+ * occupancy maintenance on its schedule (:1479-1634), random pixels per ray
+ * (:438-441), occupancy march with compaction (:422-533) into a sample stream
+ * of fixed capacity, fused field forward, composite forward/backward with a
+ * Huber loss on white-composited RGB, MLP backward on MFMA, hash-grid
+ * scatter-add, global-norm clip / skip guard / Adam (:1447-1554) on fp32
+ * masters with fp16 working copies.  With target_samples != 0 the ray count
+ * adapts so that each step marches about target_samples samples. */
+typedef struct NerfExtTrainer NerfExtTrainer;
+
+typedef struct NerfExtTrainDesc {
+    NerfExtGridDesc grid;            /* table_dtype must be NERF_EXT_F16 */
+    const uint8_t* images_rgba8;     /* host, image_count * W * H * 4 */
+    const NerfExtCamera* cameras;    /* host, image_count (all of size W x H) */
+    uint32_t image_count;
+    uint32_t occupancy_res;
+    float aabb_min[3];
+    float aabb_max[3];
+    NerfHyperParams hyper;
+    NerfOccupancyParams occupancy;
+    uint32_t initial_rays;           /* rays of the first step */
+    uint32_t max_rays;               /* ray-buffer capacity */
+    uint32_t target_samples;         /* 0: keep the ray count fixed */
+    uint32_t sample_capacity;        /* sample-stream capacity */
+    uint32_t max_steps_per_ray;      /* march step budget */
+    float huber_delta;
+    float table_init_range;          /* hash table init U(-r, r) */
+    uint32_t reserved;
+    uint64_t seed;                   /* hash table init seed */
+} NerfExtTrainDesc;
+
+typedef struct NerfExtTrainStats {
+    NerfTrainStats last;             /* last completed step */
+    uint32_t rays;                   /* rays marched in the last step */
+    uint32_t samples;                /* samples kept in the last step */
+    uint32_t active_rays;
+    uint32_t skipped;                /* Adam update skipped */
+    uint64_t occupied_samples;       /* before the capacity cut */
+} NerfExtTrainStats;
+
+/* Device buffers of a trainer, for inspection (read-only use by callers). */
+typedef struct NerfExtTrainBuffers {
+    void* state;                     /* opaque device state */
+    float* rays;                     /* [max_rays][2][4]: (o, t_near), (d, t_far) */
+    float* gt;                       /* [max_rays][4] */
+    uint32_t* counts;                /* [max_rays] occupied samples per ray */
+    uint32_t* kept;                  /* [max_rays] samples kept */
+    uint32_t* offsets;               /* [max_rays] */
+    float* samples;                  /* [cap][2] (t_mid, dt) */
+    uint32_t* sample_ray;            /* [cap] */
+    float* field;                    /* [cap][4] (sigma, r, g, b) */
+    uint16_t* features;              /* [cap][32] fp16 */
+    float* draw;                     /* [cap][4] d loss / d raw outputs */
+    float* table_grad;               /* [L][T][2] fp32, loss-scaled */
+    float* mlp_grad;                 /* [3072 + 7168] fp32, loss-scaled */
+    float* table_f32;                /* fp32 master table */
+    float* mlp_f32;                  /* fp32 master MLP weights */
+    float* table_m;
+    float* table_v;
+    float* mlp_m;
+    float* mlp_v;
+    uint32_t* bitfield;
+    float* density_grid;
+    uint32_t max_rays;
+    uint32_t sample_capacity;
+    uint64_t table_elems;
+} NerfExtTrainBuffers;
+
+enum {
+    NERF_EXT_STAGE_BEGIN = 0,     /* camera, occupancy schedule, counters */
+    NERF_EXT_STAGE_OCCUPANCY = 1, /* occupancy maintenance (if scheduled) */
+    NERF_EXT_STAGE_SAMPLE = 2,    /* rays, march, scan, sample stream */
+    NERF_EXT_STAGE_FORWARD = 3,   /* field forward (+ fp16 features) */
+    NERF_EXT_STAGE_COMPOSITE = 4, /* composite fwd/bwd + loss */
+    NERF_EXT_STAGE_BACKWARD = 5,  /* MLP backward, hash scatter-add, dW */
+    NERF_EXT_STAGE_ADAM = 6,      /* grad stats, Adam, fp16 copies */
+    NERF_EXT_STAGE_END = 7        /* stats, ray-count adaptation, step++ */
+};
+
+NERF_API NerfStatus nerf_ext_trainer_create(const NerfExtTrainDesc* desc, NerfExtTrainer** out);
+NERF_API NerfStatus nerf_ext_trainer_destroy(NerfExtTrainer* trainer);
+/* Enqueues `steps` full training steps (asynchronous). */
+NERF_API NerfStatus nerf_ext_trainer_step(NerfExtTrainer* trainer, uint32_t steps);
+/* Enqueues stages first..last of the current step (parity tests). */
+NERF_API NerfStatus nerf_ext_trainer_run_stages(NerfExtTrainer* trainer, uint32_t first, uint32_t last);
+NERF_API NerfStatus nerf_ext_trainer_synchronize(NerfExtTrainer* trainer);
+NERF_API NerfStatus nerf_ext_trainer_stats(NerfExtTrainer* trainer, NerfExtTrainStats* out);
+NERF_API NerfStatus nerf_ext_trainer_buffers(NerfExtTrainer* trainer, NerfExtTrainBuffers* out);
+/* Current fp16 model and occupancy (device pointers owned by the trainer). */
+NERF_API NerfStatus nerf_ext_trainer_model(NerfExtTrainer* trainer, NerfExtModel* model, NerfExtOccupancy* occupancy);
+/* The trainer's stream (hipStream_t as void*). */
+NERF_API void* nerf_ext_trainer_stream(NerfExtTrainer* trainer);
+
 #ifdef __cplusplus
 }
 #endif

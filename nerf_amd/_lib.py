@@ -239,6 +239,47 @@ class NerfExtRenderStats(C.Structure):
     ]
 
 
+class NerfExtTrainDesc(C.Structure):
+    _fields_ = [
+        ("grid", NerfExtGridDesc),
+        ("images_rgba8", C.c_void_p),
+        ("cameras", C.POINTER(NerfExtCamera)),
+        ("image_count", C.c_uint32),
+        ("occupancy_res", C.c_uint32),
+        ("aabb_min", C.c_float * 3),
+        ("aabb_max", C.c_float * 3),
+        ("hyper", NerfHyperParams),
+        ("occupancy", NerfOccupancyParams),
+        ("initial_rays", C.c_uint32),
+        ("max_rays", C.c_uint32),
+        ("target_samples", C.c_uint32),
+        ("sample_capacity", C.c_uint32),
+        ("max_steps_per_ray", C.c_uint32),
+        ("huber_delta", C.c_float),
+        ("table_init_range", C.c_float),
+        ("reserved", C.c_uint32),
+        ("seed", C.c_uint64),
+    ]
+
+
+class NerfExtTrainStats(C.Structure):
+    _fields_ = [
+        ("last", NerfTrainStats),
+        ("rays", C.c_uint32),
+        ("samples", C.c_uint32),
+        ("active_rays", C.c_uint32),
+        ("skipped", C.c_uint32),
+        ("occupied_samples", C.c_uint64),
+    ]
+
+
+class NerfExtTrainBuffers(C.Structure):
+    _fields_ = [(k, C.c_void_p) for k in ("state", "rays", "gt", "counts", "kept", "offsets", "samples", "sample_ray", "field", "features", "draw", "table_grad", "mlp_grad", "table_f32", "mlp_f32",
+                                          "table_m", "table_v", "mlp_m", "mlp_v", "bitfield", "density_grid")] + [("max_rays", C.c_uint32), ("sample_capacity", C.c_uint32), ("table_elems", C.c_uint64)]
+
+
+NERF_EXT_STAGE_BEGIN, NERF_EXT_STAGE_OCCUPANCY, NERF_EXT_STAGE_SAMPLE, NERF_EXT_STAGE_FORWARD, NERF_EXT_STAGE_COMPOSITE, NERF_EXT_STAGE_BACKWARD, NERF_EXT_STAGE_ADAM, NERF_EXT_STAGE_END = range(8)
+
 _S = C.c_int  # NerfStatus
 _P = C.c_void_p
 _U32 = C.c_uint32
@@ -294,6 +335,17 @@ PROTOTYPES: dict[str, tuple] = {
     "nerf_ext_renderer_create": (_S, [C.POINTER(_P)]),
     "nerf_ext_renderer_destroy": (_S, [_P]),
     "nerf_ext_render": (_S, [_P, C.POINTER(NerfExtRenderDesc), _P, _P, _P, C.POINTER(NerfExtRenderStats)]),
+    "nerf_ext_scene_render": (_S, [_P, _U32, C.POINTER(NerfExtCamera), _U32, _P, _U32, _P, _P]),
+    # training
+    "nerf_ext_trainer_create": (_S, [C.POINTER(NerfExtTrainDesc), C.POINTER(_P)]),
+    "nerf_ext_trainer_destroy": (_S, [_P]),
+    "nerf_ext_trainer_step": (_S, [_P, _U32]),
+    "nerf_ext_trainer_run_stages": (_S, [_P, _U32, _U32]),
+    "nerf_ext_trainer_synchronize": (_S, [_P]),
+    "nerf_ext_trainer_stats": (_S, [_P, C.POINTER(NerfExtTrainStats)]),
+    "nerf_ext_trainer_buffers": (_S, [_P, C.POINTER(NerfExtTrainBuffers)]),
+    "nerf_ext_trainer_model": (_S, [_P, C.POINTER(NerfExtModel), C.POINTER(NerfExtOccupancy)]),
+    "nerf_ext_trainer_stream": (_P, [_P]),
 }
 
 

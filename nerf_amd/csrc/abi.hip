@@ -45,7 +45,7 @@ void Context::release() {
     if (renderer) (void)nerf_ext_renderer_destroy(renderer);
     renderer = nullptr;
     train_release();
-    for (void* p : {(void*)images, (void*)rgba, (void*)bitfield, (void*)density_grid, (void*)table, (void*)table_f32, (void*)dparams, (void*)cparams, (void*)dparams_f32, (void*)cparams_f32})
+    for (void* p : {(void*)images, (void*)rgba, (void*)bitfield, (void*)density_grid, (void*)table, (void*)table_f32, (void*)dparams, (void*)cparams, (void*)mlp_f32})
         if (p) (void)hipFree(p);
     images = nullptr;
     rgba   = nullptr;
@@ -54,19 +54,18 @@ void Context::release() {
     table = nullptr;
     table_f32 = nullptr;
     dparams = cparams = nullptr;
-    dparams_f32 = cparams_f32 = nullptr;
+    mlp_f32 = nullptr;
     if (stream) (void)hipStreamDestroy(stream);
     stream = nullptr;
 }
 
 // Uploads fp32 master weights and refreshes their fp16 working copies.
-NerfStatus Context::upload_weights(const float* d32, const float* c32, const float* t32) {
-    NERF_HIP_TRY(hipMemcpyAsync(dparams_f32, d32, sizeof(float) * NERF_EXT_DENSITY_PARAMS, hipMemcpyHostToDevice, stream));
-    NERF_HIP_TRY(hipMemcpyAsync(cparams_f32, c32, sizeof(float) * NERF_EXT_COLOR_PARAMS, hipMemcpyHostToDevice, stream));
+NerfStatus Context::upload_weights(const float* mlp32, const float* t32) {
+    NERF_HIP_TRY(hipMemcpyAsync(mlp_f32, mlp32, sizeof(float) * (NERF_EXT_DENSITY_PARAMS + NERF_EXT_COLOR_PARAMS), hipMemcpyHostToDevice, stream));
     if (t32) NERF_HIP_TRY(hipMemcpyAsync(table_f32, t32, sizeof(float) * table_elems, hipMemcpyHostToDevice, stream));
     NERF_HIP_TRY(hipStreamSynchronize(stream));
-    NerfStatus s = nerf_ext_float_to_half(dparams_f32, dparams, NERF_EXT_DENSITY_PARAMS, stream);
-    if (s == NERF_STATUS_OK) s = nerf_ext_float_to_half(cparams_f32, cparams, NERF_EXT_COLOR_PARAMS, stream);
+    NerfStatus s = nerf_ext_float_to_half(mlp_f32, dparams, NERF_EXT_DENSITY_PARAMS, stream);
+    if (s == NERF_STATUS_OK) s = nerf_ext_float_to_half(mlp_f32 + NERF_EXT_DENSITY_PARAMS, cparams, NERF_EXT_COLOR_PARAMS, stream);
     if (s == NERF_STATUS_OK) s = nerf_ext_float_to_half(table_f32, (uint16_t*)table, table_elems, stream);
     if (s != NERF_STATUS_OK) return s;
     NERF_HIP_TRY(hipStreamSynchronize(stream));
@@ -82,16 +81,15 @@ NerfStatus Context::init_model() {
     NERF_HIP_TRY(hipMalloc(&table_f32, table_elems * sizeof(float)));
     NERF_HIP_TRY(hipMalloc(&dparams, NERF_EXT_DENSITY_PARAMS * sizeof(uint16_t)));
     NERF_HIP_TRY(hipMalloc(&cparams, NERF_EXT_COLOR_PARAMS * sizeof(uint16_t)));
-    NERF_HIP_TRY(hipMalloc(&dparams_f32, NERF_EXT_DENSITY_PARAMS * sizeof(float)));
-    NERF_HIP_TRY(hipMalloc(&cparams_f32, NERF_EXT_COLOR_PARAMS * sizeof(float)));
+    NERF_HIP_TRY(hipMalloc(&mlp_f32, (NERF_EXT_DENSITY_PARAMS + NERF_EXT_COLOR_PARAMS) * sizeof(float)));
     NerfExtGridDesc g32 = grid;
     g32.table_dtype     = NERF_EXT_F32;
     s                   = nerf_ext_grid_init_table(&g32, 0u, 1e-4f, table_f32, stream);
     if (s != NERF_STATUS_OK) return s;
-    std::vector<float> d32(NERF_EXT_DENSITY_PARAMS), c32(NERF_EXT_COLOR_PARAMS);
-    nerf_ext_mlp_init(0u, d32.data());
-    nerf_ext_mlp_init(1u, c32.data());
-    return upload_weights(d32.data(), c32.data(), nullptr);
+    std::vector<float> w(NERF_EXT_DENSITY_PARAMS + NERF_EXT_COLOR_PARAMS);
+    nerf_ext_mlp_init(0u, w.data());
+    nerf_ext_mlp_init(1u, w.data() + NERF_EXT_DENSITY_PARAMS);
+    return upload_weights(w.data(), nullptr);
 }
 
 }  // namespace nerf_hip
@@ -231,16 +229,17 @@ NERF_API NerfStatus nerf_inference(void* context, const NerfInferenceRequest* re
     return NERF_STATUS_OK;
 }
 
-static std::vector<nerf_ckpt::Tensor> checkpoint_tensors(std::vector<float>& d32, std::vector<float>& c32, std::vector<float>& t32, const Context& ctx) {
-    d32.resize(NERF_EXT_DENSITY_PARAMS);
-    c32.resize(NERF_EXT_COLOR_PARAMS);
+static std::vector<nerf_ckpt::Tensor> checkpoint_tensors(std::vector<float>& w32, std::vector<float>& t32, const Context& ctx) {
+    w32.resize(NERF_EXT_DENSITY_PARAMS + NERF_EXT_COLOR_PARAMS);
     t32.resize(ctx.table_elems);
+    float* d32 = w32.data();
+    float* c32 = w32.data() + NERF_EXT_DENSITY_PARAMS;
     return {
-        {"density.input.weight", {64, 32}, d32.data()},
-        {"density.output.weight", {16, 64}, d32.data() + 2048},
-        {"color.input.weight", {64, 32}, c32.data()},
-        {"color.hidden.0.weight", {64, 64}, c32.data() + 2048},
-        {"color.output.weight", {16, 64}, c32.data() + 2048 + 4096},
+        {"density.input.weight", {64, 32}, d32},
+        {"density.output.weight", {16, 64}, d32 + 2048},
+        {"color.input.weight", {64, 32}, c32},
+        {"color.hidden.0.weight", {64, 64}, c32 + 2048},
+        {"color.output.weight", {16, 64}, c32 + 2048 + 4096},
         {"encoding.hash_table", {ctx.grid.n_levels, 1ull << ctx.grid.log2_table_size, ctx.grid.n_features}, t32.data()},
     };
 }
@@ -251,10 +250,9 @@ NERF_API NerfStatus nerf_save_network_weights(void* context, const NerfCheckpoin
     Context* ctx = static_cast<Context*>(context);
     std::scoped_lock lock(ctx->mutex);
     if (hipStreamSynchronize(ctx->stream) != hipSuccess) return NERF_STATUS_CUDA_ERROR;
-    std::vector<float> d32, c32, t32;
-    auto tensors = checkpoint_tensors(d32, c32, t32, *ctx);
-    if (hipMemcpy(d32.data(), ctx->dparams_f32, d32.size() * 4u, hipMemcpyDeviceToHost) != hipSuccess) return NERF_STATUS_CUDA_ERROR;
-    if (hipMemcpy(c32.data(), ctx->cparams_f32, c32.size() * 4u, hipMemcpyDeviceToHost) != hipSuccess) return NERF_STATUS_CUDA_ERROR;
+    std::vector<float> w32, t32;
+    auto tensors = checkpoint_tensors(w32, t32, *ctx);
+    if (hipMemcpy(w32.data(), ctx->mlp_f32, w32.size() * 4u, hipMemcpyDeviceToHost) != hipSuccess) return NERF_STATUS_CUDA_ERROR;
     if (hipMemcpy(t32.data(), ctx->table_f32, t32.size() * 4u, hipMemcpyDeviceToHost) != hipSuccess) return NERF_STATUS_CUDA_ERROR;
     const std::vector<std::pair<std::string, std::string>> ms = {{"format", "nerf/hashgrid-network-v1"}};
     const std::vector<std::pair<std::string, uint64_t>> mn    = {{"density_input_dim", 32}, {"density_hidden_layers", 1}, {"density_width", 64}, {"density_output_dim", 16}, {"color_input_dim", 32}, {"color_hidden_layers", 2},
@@ -268,8 +266,8 @@ NERF_API NerfStatus nerf_save_network_weights(void* context, const NerfCheckpoin
 NERF_API NerfStatus nerf_load_network_weights(void* context, const NerfCheckpointFileDesc* desc) {
     if (!context || !desc || !desc->path_utf8) return NERF_STATUS_INVALID_USAGE;
     Context* ctx = static_cast<Context*>(context);
-    std::vector<float> d32, c32, t32;
-    auto tensors = checkpoint_tensors(d32, c32, t32, *ctx);
+    std::vector<float> w32, t32;
+    auto tensors = checkpoint_tensors(w32, t32, *ctx);
     std::string err;
     if (!nerf_ckpt::load(desc->path_utf8, tensors, err)) {
         set_error("nerf_load_network_weights: " + err);
@@ -277,7 +275,7 @@ NERF_API NerfStatus nerf_load_network_weights(void* context, const NerfCheckpoin
     }
     std::scoped_lock lock(ctx->mutex);
     if (hipStreamSynchronize(ctx->stream) != hipSuccess) return NERF_STATUS_CUDA_ERROR;
-    if (ctx->upload_weights(d32.data(), c32.data(), t32.data()) != NERF_STATUS_OK) return NERF_STATUS_CUDA_ERROR;
+    if (ctx->upload_weights(w32.data(), t32.data()) != NERF_STATUS_OK) return NERF_STATUS_CUDA_ERROR;
     const NerfStatus s = ctx->train_reset_state();
     if (s != NERF_STATUS_OK) return s;
     ctx->host_generation = 0u;

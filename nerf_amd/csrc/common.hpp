@@ -173,6 +173,14 @@ struct FieldInputs {
     const float2* samples;
     const uint32_t* sample_ray;
     const float4* rays;  // [ray][2]: (o.xyz, tn), (d.xyz, tf)
+    // Optional: sample count read on the device (clamped to the launch's
+    // capacity) and an fp16 copy of the hash features [n][32] for training.
+    const uint32_t* n_dev;
+    half_t* features_out;
+    // Mode B positions are world positions inside [bmin, bmax]; the grid
+    // encodes the unit cube, so they are mapped by (p - bmin) / (bmax - bmin).
+    float bmin[3];
+    float bmax[3];
 };
 
 struct FieldWeights {

@@ -8,7 +8,7 @@
 
 namespace nerf_hip {
 
-struct TrainState;  // training buffers and schedule (train.hip)
+struct Trainer;  // training run (trainer.hip)
 
 NerfExtGridDesc abi_grid_desc();
 
@@ -41,8 +41,7 @@ struct Context {
     float* table_f32     = nullptr;
     uint16_t* dparams    = nullptr;
     uint16_t* cparams    = nullptr;
-    float* dparams_f32   = nullptr;
-    float* cparams_f32   = nullptr;
+    float* mlp_f32       = nullptr;  // 3072 density then 7168 colour fp32 masters
 
     NerfExtRenderer* renderer = nullptr;
 
@@ -50,12 +49,12 @@ struct Context {
     bool training_configured = false;
     NerfTrainingConfig train_config{};
     uint32_t host_generation = 0;
-    TrainState* train        = nullptr;
+    Trainer* train           = nullptr;
 
     ~Context();
     void release();
     NerfStatus init_model();
-    NerfStatus upload_weights(const float* d32, const float* c32, const float* t32);
+    NerfStatus upload_weights(const float* mlp32, const float* t32);
     // Zeroes optimiser moments, gradients, occupancy and the step counter.
     NerfStatus train_reset_state();
     void train_release();

@@ -24,191 +24,13 @@
 //   * Weights are staged once per workgroup into LDS, then each wave keeps its
 //     A fragments in VGPRs (80 VGPRs for both networks) and loops over tiles
 //     of 16 samples (persistent grid).
-#include "common.hpp"
+#include "mlp_device.hpp"
 
 namespace nerf_hip {
 
+using namespace mlp;
+
 namespace {
-
-constexpr uint32_t kWaveSize    = 64;
-constexpr uint32_t kBlockWaves  = 4;
-constexpr uint32_t kBlockThreads = kWaveSize * kBlockWaves;
-
-__device__ __forceinline__ floatx4 mfma16x16x32(const half8_t a, const half8_t b, const floatx4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-}
-
-// k-index maps (see file header).  Returns -1 for a padded slot.
-enum class KMap { Identity, Hidden, ColorIn };
-
-__device__ __forceinline__ int logical_k(KMap m, uint32_t t, uint32_t g, uint32_t e) {
-    switch (m) {
-    case KMap::Identity: return (int)(32u * t + 8u * g + e);
-    case KMap::Hidden: return (int)(32u * t + (e < 4u ? 4u * g + e : 16u + 4u * g + (e - 4u)));
-    case KMap::ColorIn:
-    default:
-        if (e < 4u) {
-            const uint32_t slot = 4u * g + e;  // density output neuron
-            return slot == 0u ? -1 : (int)(slot - 1u);
-        }
-        return (int)(15u + 4u * g + (e - 4u));  // SH coefficient
-    }
-}
-
-// A fragment of W [n_out][n_in] for output block b, k-step t.
-__device__ __forceinline__ half8_t load_a(const half_t* W, uint32_t n_in, uint32_t b, uint32_t t, KMap m, uint32_t lane) {
-    const uint32_t i = lane & 15u, g = lane >> 4;
-    const half_t* row = W + (16u * b + i) * n_in;
-    half8_t a;
-#pragma unroll
-    for (uint32_t e = 0; e < 8u; ++e) {
-        const int k = logical_k(m, t, g, e);
-        a[e]        = k < 0 ? (half_t)0.0f : row[k];
-    }
-    return a;
-}
-
-struct DensityFrags {
-    half8_t w1[4];  // 64 x 32: blocks 0..3, one k-step
-    half8_t w2[2];  // 16 x 64: one block, k-steps 0..1
-};
-struct ColorFrags {
-    half8_t w1[4];  // 64 x 32
-    half8_t w2[8];  // 64 x 64: [block * 2 + kstep]
-    half8_t w3[2];  // 16 x 64
-};
-
-__device__ __forceinline__ void load_density(const half_t* P, DensityFrags& f, uint32_t lane) {
-#pragma unroll
-    for (uint32_t b = 0; b < 4u; ++b) f.w1[b] = load_a(P, 32u, b, 0u, KMap::Identity, lane);
-#pragma unroll
-    for (uint32_t t = 0; t < 2u; ++t) f.w2[t] = load_a(P + 2048, 64u, 0u, t, KMap::Hidden, lane);
-}
-
-__device__ __forceinline__ void load_color(const half_t* P, ColorFrags& f, uint32_t lane) {
-#pragma unroll
-    for (uint32_t b = 0; b < 4u; ++b) f.w1[b] = load_a(P, 32u, b, 0u, KMap::ColorIn, lane);
-#pragma unroll
-    for (uint32_t b = 0; b < 4u; ++b)
-#pragma unroll
-        for (uint32_t t = 0; t < 2u; ++t) f.w2[2u * b + t] = load_a(P + 2048, 64u, b, t, KMap::Hidden, lane);
-#pragma unroll
-    for (uint32_t t = 0; t < 2u; ++t) f.w3[t] = load_a(P + 2048 + 4096, 64u, 0u, t, KMap::Hidden, lane);
-}
-
-__device__ __forceinline__ half4_t relu_half(const floatx4 v) {
-    half4_t h;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) h[e] = (half_t)fmaxf(v[e], 0.0f);
-    return h;
-}
-
-__device__ __forceinline__ half8_t cat(const half4_t a, const half4_t b) {
-    return half8_t{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-}
-
-// 64 hidden neurons from a 32-wide B operand (4 output blocks, ReLU, fp16).
-__device__ __forceinline__ void layer_32_64(const half8_t* w, const half8_t x, half4_t h[4]) {
-    const floatx4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (uint32_t b = 0; b < 4u; ++b) h[b] = relu_half(mfma16x16x32(w[b], x, zero));
-}
-
-// 16 linear outputs from 64 hidden (one block, two k-steps).
-__device__ __forceinline__ floatx4 layer_64_16(const half8_t* w, const half4_t h[4]) {
-    const floatx4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
-    floatx4 o          = mfma16x16x32(w[0], cat(h[0], h[1]), zero);
-    return mfma16x16x32(w[1], cat(h[2], h[3]), o);
-}
-
-__device__ __forceinline__ floatx4 density_mlp(const DensityFrags& f, const half8_t x) {
-    half4_t h[4];
-    layer_32_64(f.w1, x, h);
-    return layer_64_16(f.w2, h);
-}
-
-__device__ __forceinline__ floatx4 color_mlp(const ColorFrags& f, const half8_t x) {
-    half4_t h1[4], h2[4];
-    layer_32_64(f.w1, x, h1);
-    const floatx4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (uint32_t b = 0; b < 4u; ++b) {
-        floatx4 a = mfma16x16x32(f.w2[2u * b], cat(h1[0], h1[1]), zero);
-        a         = mfma16x16x32(f.w2[2u * b + 1u], cat(h1[2], h1[3]), a);
-        h2[b]     = relu_half(a);
-    }
-    return layer_64_16(f.w3, h2);
-}
-
-// Hash encoding of levels 4g..4g+3 of one point: features 8g..8g+7 as fp32.
-// Corner order, weights and accumulation order are those of the oracle.
-template <typename TableT>
-__device__ __forceinline__ void encode_quad(const GridParams& g, const TableT* __restrict__ table, const float p[3], uint32_t grp, float feat[8]) {
-    const uint32_t mask = g.table_size - 1u;
-#pragma unroll
-    for (uint32_t j = 0; j < 4u; ++j) {
-        // Level 4*grp + j, selected without dynamic indexing of the kernel argument.
-        const uint32_t l0 = j, l1 = 4u + j, l2 = 8u + j, l3 = 12u + j;
-        const uint32_t N  = grp == 0u ? g.resolution[l0] : grp == 1u ? g.resolution[l1] : grp == 2u ? g.resolution[l2] : g.resolution[l3];
-        const uint32_t dn = grp == 0u ? g.dense[l0] : grp == 1u ? g.dense[l1] : grp == 2u ? g.dense[l2] : g.dense[l3];
-        const uint32_t level = 4u * grp + j;
-        float a0 = 0.0f, a1 = 0.0f;
-        if (level < g.n_levels) {
-            const LevelCell c  = level_cell(p, N);
-            const TableT* base = table + (uint64_t)level * g.table_size * 2u;
-            uint32_t idx[8];
-#pragma unroll
-            for (uint32_t k = 0; k < 8u; ++k) idx[k] = corner_index(c, k, N, dn != 0u, mask);
-            float v0[8], v1[8];
-#pragma unroll
-            for (uint32_t k = 0; k < 8u; ++k) {
-                v0[k] = (float)base[2u * idx[k]];
-                v1[k] = (float)base[2u * idx[k] + 1u];
-            }
-#pragma unroll
-            for (uint32_t k = 0; k < 8u; ++k) {
-                const float w = corner_weight(c, k);
-                a0            = a0 + w * v0[k];
-                a1            = a1 + w * v1[k];
-            }
-        }
-        feat[2u * j]      = a0;
-        feat[2u * j + 1u] = a1;
-    }
-}
-
-__device__ __forceinline__ half8_t to_half8(const float f[8]) {
-    half8_t h;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) h[e] = (half_t)f[e];
-    return h;
-}
-
-// Real SH bands 0..3 (Sloan 2008), coefficients 4g..4g+3 of a unit direction.
-__device__ __forceinline__ void sh4_quad(const float d[3], uint32_t grp, float out[4]) {
-    const float x = d[0], y = d[1], z = d[2];
-    const float xy = x * y, yz = y * z, xz = x * z;
-    const float x2 = x * x, y2 = y * y, z2 = z * z;
-    float s[16];
-    s[0]  = 0.28209479177387814f;
-    s[1]  = -0.48860251190291987f * y;
-    s[2]  = 0.48860251190291987f * z;
-    s[3]  = -0.48860251190291987f * x;
-    s[4]  = 1.0925484305920792f * xy;
-    s[5]  = -1.0925484305920792f * yz;
-    s[6]  = 0.94617469575755997f * z2 - 0.31539156525251999f;
-    s[7]  = -1.0925484305920792f * xz;
-    s[8]  = 0.54627421529603959f * (x2 - y2);
-    s[9]  = 0.59004358992664352f * y * (3.0f * x2 - y2) * -1.0f;
-    s[10] = 2.8906114426405538f * xy * z;
-    s[11] = 0.45704579946446572f * y * (1.0f - 5.0f * z2);
-    s[12] = 0.3731763325901154f * z * (5.0f * z2 - 3.0f);
-    s[13] = 0.45704579946446572f * x * (1.0f - 5.0f * z2);
-    s[14] = 1.4453057213202769f * z * (x2 - y2);
-    s[15] = 0.59004358992664352f * x * (3.0f * y2 - x2);
-#pragma unroll
-    for (uint32_t e = 0; e < 4u; ++e) out[e] = grp == 0u ? s[e] : grp == 1u ? s[4u + e] : grp == 2u ? s[8u + e] : s[12u + e];
-}
 
 __device__ __forceinline__ void stage_params(half_t* lds, const half_t* src, uint32_t count) {
     for (uint32_t i = threadIdx.x; i < count; i += blockDim.x) lds[i] = src[i];
@@ -264,7 +86,8 @@ __global__ __launch_bounds__(kBlockThreads) void k_density_forward(GridParams g,
 // Full field: sigma, rgb per sample.  Inputs either explicit (positions,
 // directions) or march samples (t_mid, dt, ray) with per-ray o, d.
 template <typename TableT, bool kFromSamples>
-__global__ __launch_bounds__(kBlockThreads) void k_field_forward(GridParams g, const TableT* __restrict__ table, const half_t* __restrict__ dparams, const half_t* __restrict__ cparams, FieldInputs in, uint32_t n, float4* __restrict__ out) {
+__global__ __launch_bounds__(kBlockThreads) void k_field_forward(GridParams g, const TableT* __restrict__ table, const half_t* __restrict__ dparams, const half_t* __restrict__ cparams, FieldInputs in, uint32_t n_cap, float4* __restrict__ out) {
+    const uint32_t n = in.n_dev ? min(*in.n_dev, n_cap) : n_cap;
     __shared__ half_t sp[NERF_EXT_DENSITY_PARAMS + NERF_EXT_COLOR_PARAMS];
     for (uint32_t i = threadIdx.x; i < NERF_EXT_DENSITY_PARAMS; i += blockDim.x) sp[i] = dparams[i];
     for (uint32_t i = threadIdx.x; i < NERF_EXT_COLOR_PARAMS; i += blockDim.x) sp[NERF_EXT_DENSITY_PARAMS + i] = cparams[i];
@@ -288,9 +111,9 @@ __global__ __launch_bounds__(kBlockThreads) void k_field_forward(GridParams g, c
             d[0]             = rd.x;
             d[1]             = rd.y;
             d[2]             = rd.z;
-            p[0]             = ro.x + td.x * rd.x;
-            p[1]             = ro.y + td.x * rd.y;
-            p[2]             = ro.z + td.x * rd.z;
+            const float w[3] = {ro.x + td.x * rd.x, ro.y + td.x * rd.y, ro.z + td.x * rd.z};
+#pragma unroll
+            for (int a = 0; a < 3; ++a) p[a] = (w[a] - in.bmin[a]) / (in.bmax[a] - in.bmin[a]);
         } else {
 #pragma unroll
             for (int a = 0; a < 3; ++a) {
@@ -300,7 +123,9 @@ __global__ __launch_bounds__(kBlockThreads) void k_field_forward(GridParams g, c
         }
         float feat[8];
         encode_quad(g, table, p, grp, feat);
-        const floatx4 o = density_mlp(fd, to_half8(feat));
+        const half8_t x = to_half8(feat);
+        if (in.features_out && s < n) *reinterpret_cast<half8_t*>(in.features_out + (uint64_t)s * 32u + 8u * grp) = x;
+        const floatx4 o = density_mlp(fd, x);
         // Colour input: (density outputs 4g..4g+3, SH 4g..4g+3); the slot of
         // density output 0 (sigma) carries a zero weight and a zero value.
         float sh[4];

@@ -394,6 +394,10 @@ NERF_API NerfStatus nerf_ext_render(NerfExtRenderer* R, const NerfExtRenderDesc*
     in.samples    = R->samples.ptr;
     in.sample_ray = R->sample_ray.ptr;
     in.rays       = R->rays.ptr;
+    for (int a = 0; a < 3; ++a) {
+        in.bmin[a] = o.aabb_min[a];
+        in.bmax[a] = o.aabb_max[a];
+    }
     const FieldWeights w{(const half_t*)d->model->density_params, (const half_t*)d->model->color_params};
     NERF_HIP_TRY(launch_field(g, d->model->table, w, in, n_samples, R->field.ptr, st));
     if (timed) NERF_HIP_TRY(hipEventRecord(R->ev[5], st));

@@ -81,6 +81,58 @@ __global__ __launch_bounds__(256) void k_occupancy_from_scene(const NerfExtGauss
     }
 }
 
+struct GaussColorLds {
+    float cx, cy, cz, k, a, r, g, b;
+};
+
+// Ground-truth volume rendering of the analytic scene: uniform steps, colour
+// = density-weighted albedo, white background, alpha = 1 - T; stops once
+// T < 1e-4.  Gaussians (<= kMaxSceneLds) staged in LDS.
+__global__ __launch_bounds__(256) void k_scene_render(const NerfExtGaussian* __restrict__ gs, uint32_t count, const NerfExtCamera* __restrict__ cams, uint32_t ppv, uint32_t n_rays, float3 bmin3, float3 bmax3, uint32_t steps,
+                                                      uint32_t* __restrict__ rgba) {
+    __shared__ GaussColorLds lds[kMaxSceneLds];
+    for (uint32_t i = threadIdx.x; i < count; i += blockDim.x) {
+        const NerfExtGaussian q = gs[i];
+        lds[i]                  = GaussColorLds{q.cx, q.cy, q.cz, -0.5f / (q.sigma * q.sigma), q.amplitude, q.r, q.g, q.b};
+    }
+    __syncthreads();
+    const uint32_t ray = blockIdx.x * 256u + threadIdx.x;
+    if (ray >= n_rays) return;
+    const uint32_t view = ray / ppv;
+    const float bmin[3] = {bmin3.x, bmin3.y, bmin3.z}, bmax[3] = {bmax3.x, bmax3.y, bmax3.z};
+    Ray r;
+    float T = 1.0f, C[3] = {0.0f, 0.0f, 0.0f};
+    if (pixel_ray(cams[view], ray - view * ppv, bmin, bmax, r)) {
+        const float dt = (r.tf - r.tn) / (float)steps;
+        for (uint32_t i = 0; i < steps && dt > 0.0f; ++i) {
+            const float t    = r.tn + ((float)i + 0.5f) * dt;
+            const float p[3] = {r.o[0] + t * r.d[0], r.o[1] + t * r.d[1], r.o[2] + t * r.d[2]};
+            float sig = 0.0f, cr = 0.0f, cg = 0.0f, cb = 0.0f;
+            for (uint32_t k = 0; k < count; ++k) {
+                const float dx = p[0] - lds[k].cx, dy = p[1] - lds[k].cy, dz = p[2] - lds[k].cz;
+                const float v  = lds[k].a * nerf_math::det_expf(((dx * dx + dy * dy) + dz * dz) * lds[k].k);
+                sig += v;
+                cr += v * lds[k].r;
+                cg += v * lds[k].g;
+                cb += v * lds[k].b;
+            }
+            if (sig <= 0.0f) continue;
+            const float a = 1.0f - expf(-sig * dt);
+            const float w = T * a / sig;
+            C[0] += w * cr;
+            C[1] += w * cg;
+            C[2] += w * cb;
+            T *= 1.0f - a;
+            if (T < 1e-4f) break;
+        }
+    }
+    uint32_t u[3];
+#pragma unroll
+    for (int c = 0; c < 3; ++c) u[c] = (uint32_t)rintf(fminf(1.0f, fmaxf(0.0f, C[c] + T)) * 255.0f);
+    const uint32_t ua = (uint32_t)rintf(fminf(1.0f, fmaxf(0.0f, 1.0f - T)) * 255.0f);
+    rgba[ray]         = (ua << 24) | (u[2] << 16) | (u[1] << 8) | u[0];
+}
+
 }  // namespace
 }  // namespace nerf_hip
 
@@ -124,6 +176,25 @@ NERF_API NerfStatus nerf_ext_occupancy_from_scene(const NerfExtGaussian* gaussia
     k_occupancy_from_scene<<<(uint32_t)blocks, 256, 0, (hipStream_t)stream>>>(gaussians, count, threshold, occ->resolution, make_float3(occ->aabb_min[0], occ->aabb_min[1], occ->aabb_min[2]),
         make_float3(occ->aabb_max[0], occ->aabb_max[1], occ->aabb_max[2]), occ->bitfield, cells, words);
     NERF_LAUNCH_CHECK("k_occupancy_from_scene");
+    return NERF_STATUS_OK;
+}
+
+NERF_API NerfStatus nerf_ext_scene_render(const NerfExtGaussian* gaussians, uint32_t count, const NerfExtCamera* cameras, uint32_t view_count, const float* aabb6, uint32_t steps, uint32_t* rgba8, void* stream) {
+    NERF_CHECK_ARG(gaussians && cameras && aabb6 && rgba8, "nerf_ext_scene_render: null pointer");
+    NERF_CHECK_ARG(count >= 1u && count <= kMaxSceneLds, "nerf_ext_scene_render: 1..1024 Gaussians");
+    NERF_CHECK_ARG(view_count >= 1u && steps >= 1u, "nerf_ext_scene_render: need views and steps");
+    const uint32_t W = cameras[0].width, H = cameras[0].height;
+    for (uint32_t v = 0; v < view_count; ++v) NERF_CHECK_ARG(cameras[v].width == W && cameras[v].height == H && W > 0u && H > 0u, "nerf_ext_scene_render: views must share a size");
+    const uint64_t n64 = (uint64_t)W * H * view_count;
+    NERF_CHECK_ARG(n64 < (1ull << 31), "nerf_ext_scene_render: too many rays");
+    hipStream_t st      = (hipStream_t)stream;
+    NerfExtCamera* dcam = nullptr;
+    NERF_HIP_TRY(hipMallocAsync((void**)&dcam, sizeof(NerfExtCamera) * view_count, st));
+    NERF_HIP_TRY(hipMemcpyAsync(dcam, cameras, sizeof(NerfExtCamera) * view_count, hipMemcpyHostToDevice, st));
+    const uint32_t n = (uint32_t)n64;
+    k_scene_render<<<(n + 255u) / 256u, 256, 0, st>>>(gaussians, count, dcam, W * H, n, make_float3(aabb6[0], aabb6[1], aabb6[2]), make_float3(aabb6[3], aabb6[4], aabb6[5]), steps, rgba8);
+    NERF_LAUNCH_CHECK("k_scene_render");
+    NERF_HIP_TRY(hipFreeAsync(dcam, st));
     return NERF_STATUS_OK;
 }
 

@@ -1,22 +1,22 @@
-// train.hip — training entry points of include/nerf.h.
+// train.hip — training entry points of include/nerf.h on the trainer.
 //
 // Argument and state validation follow backend-cuda.cu:2125-2140 and
-// :2405-2435.  The training step itself (march, field forward, composite
-// backward with Huber loss, MLP backward on MFMA, hash-grid scatter-add,
-// fused Adam, occupancy schedule) is not in this build yet: nerf_train_step
-// reports NERF_STATUS_FAILURE with an explanatory last-error message.
-#include "common.hpp"
+// :2405-2435.  nerf_configure_training builds a trainer that borrows the
+// context's model and occupancy buffers, with the configured AABB, Adam
+// hyper-parameters, occupancy schedule, a fixed rays_per_batch and
+// max_sample_steps_per_ray as the march budget; the sample stream holds
+// rays_per_batch * max_sample_steps_per_ray samples, so no ray is ever cut.
+// nerf_train_step enqueues one step asynchronously (:2417);
+// nerf_read_train_stats synchronises (:2431).  The loss is the Huber loss
+// (delta 0.1) of the hash-grid model, not the reference's alpha-weighted MSE.
 #include "context.hpp"
+#include "trainer.hpp"
 
 namespace nerf_hip {
 
-struct TrainState {
-    NerfTrainStats stats{};
-};
-
 void Context::train_release() {
     delete train;
-    train = nullptr;
+    train               = nullptr;
     training_configured = false;
 }
 
@@ -26,9 +26,9 @@ NerfStatus Context::train_reset_state() {
         NERF_HIP_TRY(hipMemsetAsync(bitfield, 0, (cells + 31u) / 32u * 4u, stream));
         NERF_HIP_TRY(hipMemsetAsync(density_grid, 0, cells * sizeof(float), stream));
     }
-    if (train) train->stats = NerfTrainStats{};
     NERF_HIP_TRY(hipStreamSynchronize(stream));
-    return NERF_STATUS_OK;
+    // Training stays configured; moments, gradients and the step counter restart.
+    return train ? train->reset() : NERF_STATUS_OK;
 }
 
 }  // namespace nerf_hip
@@ -47,12 +47,60 @@ NERF_API NerfStatus nerf_configure_training(void* context, const NerfTrainingCon
     if (c.rays_per_batch == 0u || c.max_sample_steps_per_ray == 0u || c.max_sample_steps_per_ray > 256u) return NERF_STATUS_INVALID_USAGE;
     if (c.occupancy_params.update_interval == 0u || ctx->image_count == 0u) return NERF_STATUS_INVALID_USAGE;
     if (c.rays_per_batch > ctx->max_batch_rays || total > ctx->max_sample_steps || total > 0xffffffffull) return NERF_STATUS_INVALID_USAGE;
+    if (!(c.aabb_max_x > c.aabb_min_x && c.aabb_max_y > c.aabb_min_y && c.aabb_max_z > c.aabb_min_z)) {
+        set_error("nerf_configure_training: empty AABB");
+        return NERF_STATUS_INVALID_USAGE;
+    }
+    if (ctx->occupancy_res == 0u) {
+        set_error("nerf_configure_training: the context has no occupancy grid (occupancy_grid_res 0)");
+        return NERF_STATUS_INVALID_USAGE;
+    }
     std::scoped_lock lock(ctx->mutex);
-    if (!ctx->train) ctx->train = new TrainState();
+    ctx->train_release();
+    std::vector<NerfExtCamera> cams(ctx->image_count);
+    for (uint32_t i = 0; i < ctx->image_count; ++i) {
+        const float* m = ctx->cameras.data() + 16ull * i;
+        for (int r = 0; r < 3; ++r)
+            for (int k = 0; k < 4; ++k) cams[i].c2w[4 * r + k] = m[4 * r + k];
+        cams[i].fx     = ctx->fx;
+        cams[i].fy     = ctx->fy;
+        cams[i].cx     = ctx->cx;
+        cams[i].cy     = ctx->cy;
+        cams[i].width  = ctx->width;
+        cams[i].height = ctx->height;
+    }
+    // The trainer takes the dataset from host memory; the context keeps its
+    // own device copy only for its lifetime, so copy the images back once.
+    std::vector<uint8_t> images((uint64_t)ctx->image_count * ctx->width * ctx->height * 4u);
+    if (!images.empty() && hipMemcpy(images.data(), ctx->images, images.size(), hipMemcpyDeviceToHost) != hipSuccess) return NERF_STATUS_CUDA_ERROR;
+    NerfExtTrainDesc d{};
+    d.grid         = ctx->grid;
+    d.images_rgba8 = images.data();
+    d.cameras      = cams.data();
+    d.image_count  = ctx->image_count;
+    d.occupancy_res = ctx->occupancy_res;
+    d.aabb_min[0] = c.aabb_min_x;
+    d.aabb_min[1] = c.aabb_min_y;
+    d.aabb_min[2] = c.aabb_min_z;
+    d.aabb_max[0] = c.aabb_max_x;
+    d.aabb_max[1] = c.aabb_max_y;
+    d.aabb_max[2] = c.aabb_max_z;
+    d.hyper             = c.hyper_params;
+    d.occupancy         = c.occupancy_params;
+    d.initial_rays      = c.rays_per_batch;
+    d.max_rays          = c.rays_per_batch;
+    d.target_samples    = 0u;
+    d.sample_capacity   = (uint32_t)total;
+    d.max_steps_per_ray = c.max_sample_steps_per_ray;
+    d.huber_delta       = 0.1f;
+    if (d.hyper.loss_scale <= 0.0f) d.hyper.loss_scale = 1.0f;
+    const BorrowedModel bm{(half_t*)ctx->table, ctx->table_f32, (half_t*)ctx->dparams, (half_t*)ctx->cparams, ctx->mlp_f32, ctx->bitfield, ctx->density_grid};
+    Trainer* t = nullptr;
+    const NerfStatus s = trainer_create(&d, &bm, ctx->stream, &t);
+    if (s != NERF_STATUS_OK) return s == NERF_STATUS_INVALID_USAGE ? s : NERF_STATUS_CUDA_ERROR;
+    ctx->train               = t;
     ctx->train_config        = c;
     ctx->host_generation     = 0u;
-    const NerfStatus s       = ctx->train_reset_state();
-    if (s != NERF_STATUS_OK) return s;
     ctx->training_configured = true;
     return NERF_STATUS_OK;
 }
@@ -61,9 +109,12 @@ NERF_API NerfStatus nerf_configure_training(void* context, const NerfTrainingCon
 NERF_API NerfStatus nerf_train_step(void* context) {
     if (!context) return NERF_STATUS_INVALID_USAGE;
     Context* ctx = static_cast<Context*>(context);
-    if (!ctx->scene_ready || !ctx->training_configured) return NERF_STATUS_STATE_ERROR;
-    set_error("nerf_train_step: the training step is not part of this build yet");
-    return NERF_STATUS_FAILURE;
+    if (!ctx->scene_ready || !ctx->training_configured || !ctx->train) return NERF_STATUS_STATE_ERROR;
+    std::scoped_lock lock(ctx->mutex);
+    const NerfStatus s = ctx->train->run_stages(NERF_EXT_STAGE_BEGIN, NERF_EXT_STAGE_END);
+    if (s != NERF_STATUS_OK) return NERF_STATUS_CUDA_ERROR;
+    ++ctx->host_generation;
+    return NERF_STATUS_OK;
 }
 
 // backend-cuda.cu:2421-2435.
@@ -72,8 +123,9 @@ NERF_API NerfStatus nerf_read_train_stats(void* context, NerfTrainStats* out_sta
     Context* ctx = static_cast<Context*>(context);
     if (!ctx->training_configured || !ctx->train) return NERF_STATUS_STATE_ERROR;
     std::scoped_lock lock(ctx->mutex);
-    if (hipStreamSynchronize(ctx->stream) != hipSuccess) return NERF_STATUS_CUDA_ERROR;
-    *out_stats           = ctx->train->stats;
+    TrainDevState st{};
+    if (ctx->train->read_state(st) != NERF_STATUS_OK) return NERF_STATUS_CUDA_ERROR;
+    *out_stats           = st.stats;
     ctx->host_generation = out_stats->completed_steps;
     return NERF_STATUS_OK;
 }

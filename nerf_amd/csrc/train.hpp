@@ -1,0 +1,102 @@
+// train.hpp — device-resident training state and the kernels of one step.
+#pragma once
+
+#include "common.hpp"
+
+namespace nerf_hip {
+
+enum : uint32_t { kOccNone = 0u, kOccWarmupInit = 1u, kOccRefresh = 2u };
+
+// Per-step scalars kept in device memory, so that every kernel of a step reads
+// its counts on the device (fixed launch shapes: the step can be captured in
+// a HIP graph).  Mirrors the reference's TrainingDeviceState
+// (backend-cuda.cu:79-85) plus the batch counters and Adam scalars.
+struct TrainDevState {
+    uint32_t frame;       // steps completed so far (reference frame_index)
+    uint32_t camera;      // camera of the current step
+    uint32_t occ_mode;    // kOcc* of the current step
+    uint32_t n_rays;      // rays marched this step
+    uint32_t n_samples;   // samples kept this step (a prefix of the stream)
+    uint32_t n_active;    // rays with at least one kept sample
+    uint32_t nonfinite;   // gradient contains inf/nan
+    uint32_t skip;        // Adam update skipped
+    unsigned long long total;  // occupied samples before the capacity cut
+    double grad_sumsq;    // sum of squared (loss-scaled) gradients
+    float loss_sum;       // sum of per-ray Huber losses
+    float rays_f;         // adaptive ray count
+    float lr, grad_scale, inv_bc1, inv_bc2, inv_ls;
+    uint32_t pad;
+    NerfTrainStats stats; // last completed step
+};
+
+// Fixed parameters of a configured run (kernel argument).
+struct TrainParams {
+    uint32_t image_count, width, height;
+    uint32_t occ_res;
+    float bmin[3], bmax[3];
+    uint32_t max_steps;       // march steps per ray
+    uint32_t max_rays;        // capacity of the ray buffers
+    uint32_t sample_cap;      // capacity of the sample stream
+    uint32_t target_samples;  // adaptive ray count target (0: fixed)
+    uint32_t min_rays;
+    float huber_delta;
+    float loss_scale;
+    float lr, beta1, beta2, eps, clip, guard;
+    uint32_t lr_decay_ksteps;
+    float occ_decay, occ_threshold;
+    uint32_t occ_cells_per_update, occ_interval, occ_warmup;
+    uint32_t occ_cells;
+};
+
+// Device buffers of a run.
+struct TrainBuffers {
+    TrainDevState* state;
+    const NerfExtCamera* cams;   // [image_count]
+    const uint8_t* images;       // [image_count][H][W][4]
+    uint32_t* bits;              // occupancy bitfield
+    float* density;              // occupancy density grid
+    float4* rays;                // [max_rays][2]
+    float4* gt;                  // [max_rays] (r, g, b, a)
+    uint32_t* counts;            // [max_rays] occupied samples
+    uint32_t* kept;              // [max_rays] samples kept (0 if cut)
+    uint32_t* offsets;           // [max_rays]
+    uint32_t* scan_tmp;
+    float2* samples;             // [sample_cap] (t_mid, dt)
+    uint32_t* sample_ray;        // [sample_cap]
+    float4* field;               // [sample_cap] (sigma, r, g, b)
+    half_t* features;            // [sample_cap][32]
+    float4* draw;                // [sample_cap] (d sigma_raw, d r, d g, d b)
+    // model
+    GridParams grid;
+    half_t* table;               // fp16 working copy [L][T][2]
+    float* table_f32;            // fp32 master
+    float* table_grad;           // fp32, loss-scaled
+    float* table_m;
+    float* table_v;
+    half_t* dparams;             // 3072 fp16
+    half_t* cparams;             // 7168 fp16
+    float* mlp_f32;              // 10240 fp32 masters (density then colour)
+    float* mlp_grad;             // 10240, loss-scaled
+    float* mlp_m;
+    float* mlp_v;
+    float* dw_partials;          // [kDwBlocks][10240]
+    uint64_t table_elems;
+};
+
+constexpr uint32_t kDwBlocks   = 256;   // workgroups of the weight-gradient passes
+constexpr uint32_t kMlpParams  = NERF_EXT_DENSITY_PARAMS + NERF_EXT_COLOR_PARAMS;
+
+// Launches one stage (NERF_EXT_STAGE_*) of a training step on `stream`.
+// `occupancy_update` selects the occupancy-maintenance kernels (the schedule
+// is a function of the step index, which the host tracks).
+hipError_t launch_train_stage(const TrainParams& P, const TrainBuffers& B, uint32_t stage, bool occupancy_update, hipStream_t stream);
+
+// Individual stages, exposed for the parity tests through nerf_ext.h.
+hipError_t launch_composite_train(const TrainParams& P, const TrainBuffers& B, hipStream_t stream);
+hipError_t launch_mlp_backward(const TrainParams& P, const TrainBuffers& B, hipStream_t stream);
+hipError_t launch_adam(const TrainParams& P, const TrainBuffers& B, hipStream_t stream);
+
+uint64_t scan_tmp_words(uint32_t n);
+hipError_t exclusive_scan_u32(const uint32_t* in, uint32_t* out, uint32_t n, uint32_t* tmp, unsigned long long* total, hipStream_t stream);
+
+}  // namespace nerf_hip

@@ -1,0 +1,827 @@
+// train_kernels.hip — one training step of the hash-grid NeRF on gfx950.
+//
+// Stage                     reference                      here
+// begin step / camera       backend-cuda.cu:1479-1488      k_step_begin
+// occupancy maintenance     :1555-1634                     k_occ_decay, k_occ_eval, k_occ_bits
+// ray sampling + march      :422-533                       k_train_rays, scan, k_train_samples
+// field forward             :1328-1339                     launch_field (field.hip)
+// composite fwd/bwd + loss  :1095-1182 (MSE)               k_composite_train (Huber)
+// MLP backward              :784-909, 1267-1301 (cuBLAS)   k_bwd_dx (+ hash scatter), k_bwd_dw, k_dw_reduce
+// grad stats, Adam          :1447-1554                     k_grad_stats, k_adam_prepare, k_adam
+// end step                  :1495-1512                     k_step_end
+//
+// MI355X choices: every count lives in device memory and every launch has a
+// fixed shape, so a whole step is one stream of kernels (graph-capturable;
+// HIP has no conditional graph nodes, so the reference's bucket switch
+// (:1489-1494) becomes kernels that read their counts and exit early).  The
+// MLP backward recomputes the forward per 16-sample tile in registers (MFMA
+// is cheap next to moving activations through HBM); the input-gradient pass
+// scatters straight into the hash-table gradient; the weight gradients run as
+// three recompute passes whose per-tile sample axis is moved onto the MFMA
+// reduction axis through a per-wave LDS transpose, with deterministic
+// per-workgroup partials.
+#include "mlp_device.hpp"
+#include "train.hpp"
+
+namespace nerf_hip {
+
+using namespace mlp;
+
+namespace {
+
+constexpr uint32_t kWave   = 64;
+constexpr uint32_t kWaves  = 4;
+constexpr uint32_t kThreads = kWave * kWaves;
+
+__device__ __forceinline__ uint32_t hash_u32(uint32_t x) {  // backend-cuda.cu:321-328
+    x ^= x >> 16;
+    x *= 0x7feb352du;
+    x ^= x >> 15;
+    x *= 0x846ca68bu;
+    x ^= x >> 16;
+    return x;
+}
+__device__ __forceinline__ float rand01(uint32_t seed) {  // :329-332
+    return (float)(hash_u32(seed) & 0x00ffffffu) / (float)0x01000000u;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// Orders LDS traffic of one wavefront (writes by some lanes, reads by others)
+// without a workgroup barrier.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+// ------------------------------------------------------------ step control
+__global__ void k_step_begin(TrainParams P, TrainDevState* S) {
+    if (threadIdx.x != 0u || blockIdx.x != 0u) return;
+    const uint32_t f = S->frame;
+    S->camera        = hash_u32(f * 747796405u + 2891336453u) % P.image_count;  // :1482
+    if (f < P.occ_warmup)
+        S->occ_mode = f == 0u ? kOccWarmupInit : kOccNone;                     // :1483-1485
+    else
+        S->occ_mode = (P.occ_interval != 0u && f % P.occ_interval == 0u) ? kOccRefresh : kOccNone;
+    uint32_t rays = (uint32_t)(S->rays_f + 0.5f);
+    rays          = rays < P.min_rays ? P.min_rays : (rays > P.max_rays ? P.max_rays : rays);
+    S->n_rays     = rays;
+    S->n_samples  = 0u;
+    S->n_active   = 0u;
+    S->nonfinite  = 0u;
+    S->total      = 0ull;
+    S->grad_sumsq = 0.0;
+    S->loss_sum   = 0.0f;
+}
+
+__global__ void k_step_end(TrainParams P, TrainDevState* S) {
+    if (threadIdx.x != 0u || blockIdx.x != 0u) return;
+    const float inv = S->n_active ? 1.0f / (float)S->n_active : 0.0f;
+    const float loss = S->loss_sum * inv;                                          // :1499
+    const float gn   = (float)sqrt(S->grad_sumsq > 0.0 ? S->grad_sumsq : 0.0) / P.loss_scale;
+    S->stats.loss              = loss;
+    S->stats.grad_norm         = gn;
+    S->stats.has_nonfinite     = (S->nonfinite || !isfinite(loss) || !isfinite(gn)) ? 1u : 0u;
+    S->stats.completed_steps   = S->frame + 1u;
+    S->stats.last_train_camera = S->camera;
+    if (P.target_samples != 0u && S->n_samples > 0u) {
+        // Aim the next batch at target_samples (exponentially smoothed).
+        const float want = S->rays_f * (float)P.target_samples / (float)S->n_samples;
+        S->rays_f        = 0.5f * S->rays_f + 0.5f * want;
+        S->rays_f        = fminf(fmaxf(S->rays_f, (float)P.min_rays), (float)P.max_rays);
+    }
+    S->frame = S->frame + 1u;
+}
+
+// ----------------------------------------------------------- occupancy grid
+__global__ __launch_bounds__(256) void k_occ_decay(TrainParams P, const TrainDevState* S, float* density) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i >= P.occ_cells) return;
+    const uint32_t mode = S->occ_mode;
+    if (mode == kOccWarmupInit) density[i] = 1.0f;          // :1559-1561
+    else if (mode == kOccRefresh) density[i] *= P.occ_decay; // :1563
+}
+
+// density[cell] = max(density[cell], exp(raw sigma(cell centre))) over the
+// rotating window of cells_per_update cells (:1575-1627).
+template <typename TableT>
+__global__ __launch_bounds__(kThreads) void k_occ_eval(TrainParams P, GridParams g, const TableT* __restrict__ table, const half_t* __restrict__ dparams, const TrainDevState* S, float* density) {
+    __shared__ half_t sp[NERF_EXT_DENSITY_PARAMS];
+    for (uint32_t i = threadIdx.x; i < NERF_EXT_DENSITY_PARAMS; i += blockDim.x) sp[i] = dparams[i];
+    __syncthreads();
+    if (S->occ_mode != kOccRefresh) return;  // uniform across the grid
+    const uint32_t lane = threadIdx.x & 63u, grp = lane >> 4, s16 = lane & 15u;
+    DensityFrags f;
+    load_density(sp, f, lane);
+    const uint32_t count = P.occ_cells_per_update < P.occ_cells ? P.occ_cells_per_update : P.occ_cells;
+    const uint32_t start = (uint32_t)((uint64_t)S->frame * count % P.occ_cells);
+    const uint32_t res   = P.occ_res;
+    const float step[3]  = {(P.bmax[0] - P.bmin[0]) / (float)res, (P.bmax[1] - P.bmin[1]) / (float)res, (P.bmax[2] - P.bmin[2]) / (float)res};
+    const uint32_t tiles = (count + 15u) / 16u;
+    for (uint32_t tile = blockIdx.x * kWaves + (threadIdx.x >> 6); tile < tiles; tile += gridDim.x * kWaves) {
+        const uint32_t k    = tile * 16u + s16;
+        const uint32_t kq   = k < count ? k : count - 1u;
+        const uint32_t cell = (start + kq) % P.occ_cells;
+        const uint32_t z = cell / (res * res), rem = cell - z * res * res, y = rem / res, x = rem - y * res;
+        float p[3] = {P.bmin[0] + ((float)x + 0.5f) * step[0], P.bmin[1] + ((float)y + 0.5f) * step[1], P.bmin[2] + ((float)z + 0.5f) * step[2]};
+        // The hash grid encodes the unit cube: normalise by the AABB.
+#pragma unroll
+        for (int a = 0; a < 3; ++a) p[a] = (p[a] - P.bmin[a]) / (P.bmax[a] - P.bmin[a]);
+        float feat[8];
+        encode_quad(g, table, p, grp, feat);
+        const floatx4 o = density_mlp(f, to_half8(feat));
+        if (grp == 0u && k < count) {
+            const float sigma = expf(o[0]);
+            density[cell]     = fmaxf(density[cell], sigma);
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void k_occ_bits(TrainParams P, const TrainDevState* S, const float* density, uint32_t* bits) {
+    if (S->occ_mode == kOccNone) return;
+    const uint32_t cell = blockIdx.x * 256u + threadIdx.x;
+    const bool occ      = cell < P.occ_cells && density[cell > P.occ_cells - 1u ? P.occ_cells - 1u : cell] > P.occ_threshold;  // :1632
+    const uint64_t b    = __ballot(occ);
+    const uint32_t words = (P.occ_cells + 31u) / 32u;
+    const uint32_t w0    = (blockIdx.x * 256u + (threadIdx.x & ~63u)) >> 5;
+    if ((threadIdx.x & 63u) == 0u) {
+        if (w0 < words) bits[w0] = (uint32_t)b;
+        if (w0 + 1u < words) bits[w0 + 1u] = (uint32_t)(b >> 32);
+    }
+}
+
+// ---------------------------------------------------------------- sampling
+__device__ __forceinline__ bool occupied_at(const TrainParams& P, const uint32_t* bits, const float p[3]) {
+    const float sx = P.bmax[0] - P.bmin[0], sy = P.bmax[1] - P.bmin[1], sz = P.bmax[2] - P.bmin[2];
+    const float rx = (p[0] - P.bmin[0]) / sx, ry = (p[1] - P.bmin[1]) / sy, rz = (p[2] - P.bmin[2]) / sz;
+    if (rx < 0.0f || rx >= 1.0f || ry < 0.0f || ry >= 1.0f || rz < 0.0f || rz >= 1.0f) return false;
+    const uint32_t res = P.occ_res;
+    const uint32_t ix = min(res - 1u, (uint32_t)(rx * (float)res)), iy = min(res - 1u, (uint32_t)(ry * (float)res)), iz = min(res - 1u, (uint32_t)(rz * (float)res));
+    const uint32_t idx = ix + iy * res + iz * res * res;
+    return (bits[idx >> 5] >> (idx & 31u)) & 1u;
+}
+
+template <typename Emit>
+__device__ __forceinline__ uint32_t march_train(const TrainParams& P, const uint32_t* bits, float4 ro, float4 rd, float cone, Emit emit) {
+    const float tn = ro.w, tf = rd.w, t_range = tf - tn;
+    if (!(t_range > 0.0f)) return 0u;
+    const float dt_min = t_range / (float)P.max_steps;
+    uint32_t count = 0u, i = 0u;
+    float t = tn;
+    while (t < tf && i < P.max_steps) {  // :457-469
+        const float dt   = fminf(fmaxf(dt_min, t * cone), tf - t);
+        const float tm   = t + 0.5f * dt;
+        const float p[3] = {ro.x + tm * rd.x, ro.y + tm * rd.y, ro.z + tm * rd.z};
+        if (occupied_at(P, bits, p)) {
+            emit(count, tm, dt);
+            ++count;
+        }
+        t += dt;
+        ++i;
+    }
+    return count;
+}
+
+__device__ __forceinline__ float cone_of(const NerfExtCamera& c) {  // :333-337
+    const float ifx = c.fx > 0.0f ? 1.0f / c.fx : 0.0f, ify = c.fy > 0.0f ? 1.0f / c.fy : 0.0f;
+    return 0.5f * (ifx + ify);
+}
+
+// Random pixel per ray (:438-441), ray, march count, bilinear ground truth
+// composited over white (:471-499).
+__global__ __launch_bounds__(256) void k_train_rays(TrainParams P, const TrainDevState* S, const NerfExtCamera* __restrict__ cams, const uint8_t* __restrict__ images, const uint32_t* __restrict__ bits, float4* __restrict__ rays, float4* __restrict__ gt,
+                                                     uint32_t* __restrict__ counts) {
+    const uint32_t r = blockIdx.x * 256u + threadIdx.x;
+    if (r >= P.max_rays) return;
+    uint32_t count = 0u;
+    float4 ro = make_float4(0.0f, 0.0f, 0.0f, 0.0f), rd = make_float4(0.0f, 0.0f, 0.0f, 0.0f), g4 = make_float4(1.0f, 1.0f, 1.0f, 0.0f);
+    if (r < S->n_rays) {
+        const uint32_t cam_idx  = S->camera;
+        const NerfExtCamera cam = cams[cam_idx];
+        const uint32_t seed     = S->frame * 1315423911u ^ r * 9781u;
+        const float px          = rand01(seed ^ 0xA511E9B3u) * (float)P.width;
+        const float py          = rand01(seed ^ 0x63D83595u) * (float)P.height;
+        const float pyf         = (float)P.height - 1.0f - py;
+        Ray ray;
+        if (make_ray(cam, px, pyf, P.bmin, P.bmax, ray)) {
+            ro    = make_float4(ray.o[0], ray.o[1], ray.o[2], ray.tn);
+            rd    = make_float4(ray.d[0], ray.d[1], ray.d[2], ray.tf);
+            count = march_train(P, bits, ro, rd, cone_of(cam), [](uint32_t, float, float) {});
+        }
+        if (count > 0u) {
+            const uint8_t* img = images + (uint64_t)cam_idx * P.width * P.height * 4u;
+            const float cx = fmaxf(0.0f, fminf(px, (float)P.width - 1.0f)), cy = fmaxf(0.0f, fminf(py, (float)P.height - 1.0f));
+            const int x0 = (int)floorf(cx), y0 = (int)floorf(cy);
+            const int x1 = min(x0 + 1, (int)P.width - 1), y1 = min(y0 + 1, (int)P.height - 1);
+            const float tx = cx - (float)x0, ty = cy - (float)y0;
+            const int stride = (int)P.width * 4;
+            const uint8_t* p00 = img + y0 * stride + x0 * 4;
+            const uint8_t* p10 = img + y0 * stride + x1 * 4;
+            const uint8_t* p01 = img + y1 * stride + x0 * 4;
+            const uint8_t* p11 = img + y1 * stride + x1 * 4;
+            const float inv255 = 1.0f / 255.0f;
+            float c[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float a = (float)p00[k] * inv255 * (1.0f - tx) + (float)p10[k] * inv255 * tx;
+                const float b = (float)p01[k] * inv255 * (1.0f - tx) + (float)p11[k] * inv255 * tx;
+                c[k]          = a * (1.0f - ty) + b * ty;
+            }
+            const float alpha = c[3];
+            g4 = make_float4(c[0] * alpha + (1.0f - alpha), c[1] * alpha + (1.0f - alpha), c[2] * alpha + (1.0f - alpha), alpha);
+        }
+    }
+    rays[2ull * r]      = ro;
+    rays[2ull * r + 1u] = rd;
+    gt[r]               = g4;
+    counts[r]           = count;
+}
+
+// Writes the samples of every ray whose whole range fits the stream capacity;
+// kept[r] is its count or 0.  The kept rays form a prefix (offsets grow with
+// r), so n_samples = max(offset + count) over kept rays.
+__global__ __launch_bounds__(256) void k_train_samples(TrainParams P, TrainDevState* S, const NerfExtCamera* __restrict__ cams, const uint32_t* __restrict__ bits, const float4* __restrict__ rays, const uint32_t* __restrict__ counts,
+                                                        const uint32_t* __restrict__ offsets, uint32_t* __restrict__ kept, float2* __restrict__ samples, uint32_t* __restrict__ sample_ray) {
+    const uint32_t r = blockIdx.x * 256u + threadIdx.x;
+    if (r >= P.max_rays) return;
+    const uint32_t count = counts[r];
+    const uint32_t base  = offsets[r];
+    const bool fits      = count > 0u && (uint64_t)base + count <= (uint64_t)P.sample_cap;
+    kept[r]              = fits ? count : 0u;
+    if (!fits) return;
+    const float cone = cone_of(cams[S->camera]);
+    march_train(P, bits, rays[2ull * r], rays[2ull * r + 1u], cone, [&](uint32_t k, float tm, float dt) {
+        if (k < count) {
+            samples[base + k]    = make_float2(tm, dt);
+            sample_ray[base + k] = r;
+        }
+    });
+    atomicMax(&S->n_samples, base + count);
+    atomicAdd(&S->n_active, 1u);
+}
+
+// ----------------------------------------------------- composite fwd + bwd
+// Huber loss (Huber 1964) on the white-composited RGB; gradients with respect
+// to the raw network outputs (see the oracle's orc_composite_backward_ray for
+// the derivation).  The suffix S_i is formed as pred - prefix_i so that both
+// passes run front to back.
+__global__ __launch_bounds__(256) void k_composite_train(TrainParams P, TrainDevState* S, const uint32_t* __restrict__ kept, const uint32_t* __restrict__ offsets, const float2* __restrict__ samples, const float4* __restrict__ field,
+                                                          const float4* __restrict__ gt, float4* __restrict__ draw) {
+    __shared__ float wsum[kWaves];
+    const uint32_t r = blockIdx.x * 256u + threadIdx.x;
+    float ray_loss   = 0.0f;
+    const uint32_t active = S->n_active;
+    const float inv_norm  = active ? 1.0f / (float)active : 0.0f;
+    if (r < P.max_rays && r < S->n_rays) {
+        const uint32_t count = kept[r];
+        if (count > 0u) {
+            const uint32_t base = offsets[r];
+            float T = 1.0f, C[3] = {0.0f, 0.0f, 0.0f};
+            for (uint32_t i = 0; i < count; ++i) {
+                const float4 f = field[base + i];
+                const float dt = fmaxf(samples[base + i].y, 0.0f);
+                const float a  = 1.0f - __expf(-(f.x * dt));
+                const float w  = T * a;
+                C[0] += w * f.y;
+                C[1] += w * f.z;
+                C[2] += w * f.w;
+                T *= 1.0f - a;
+            }
+            const float4 g4 = gt[r];
+            const float gtv[3] = {g4.x, g4.y, g4.z};
+            float pred[3], gr[3];
+            const float d = P.huber_delta;
+#pragma unroll
+            for (int c = 0; c < 3; ++c) {
+                pred[c]      = C[c] + T;  // white background
+                const float x = pred[c] - gtv[c];
+                const float ax = fabsf(x);
+                ray_loss += ax <= d ? 0.5f * x * x : d * (ax - 0.5f * d);
+                gr[c] = fminf(fmaxf(x, -d), d) * inv_norm;
+            }
+            T = 1.0f;
+            float Cp[3] = {0.0f, 0.0f, 0.0f};
+            for (uint32_t i = 0; i < count; ++i) {
+                const float4 f   = field[base + i];
+                const float dt   = fmaxf(samples[base + i].y, 0.0f);
+                const float a    = 1.0f - __expf(-(f.x * dt));
+                const float w    = T * a;
+                const float Tn   = T * (1.0f - a);
+                const float c3[3] = {f.y, f.z, f.w};
+                float ds = 0.0f, dc[3];
+#pragma unroll
+                for (int c = 0; c < 3; ++c) {
+                    Cp[c] += w * c3[c];
+                    const float suffix = pred[c] - Cp[c];
+                    ds += gr[c] * (Tn * c3[c] - suffix);
+                    dc[c] = w * gr[c] * c3[c] * (1.0f - c3[c]);
+                }
+                draw[base + i] = make_float4(dt * f.x * ds, dc[0], dc[1], dc[2]);
+                T = Tn;
+            }
+        }
+    }
+    const float wl = wave_sum(ray_loss);
+    if ((threadIdx.x & 63u) == 0u) wsum[threadIdx.x >> 6] = wl;
+    __syncthreads();
+    if (threadIdx.x == 0u) {
+        const float b = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+        if (b != 0.0f) atomicAdd(&S->loss_sum, b);
+    }
+}
+
+// ------------------------------------------------------------ MLP backward
+// Transposed-weight fragments (A operands of the backward products).
+// C3^T: rows = h2 neurons, k = colour output neuron (identity map, < 16).
+__device__ __forceinline__ half8_t frag_c3t(const half_t* cp, uint32_t b, uint32_t lane) {
+    const uint32_t i = lane & 15u, g = lane >> 4;
+    half8_t a;
+#pragma unroll
+    for (uint32_t e = 0; e < 8u; ++e) {
+        const uint32_t k = 8u * g + e;
+        a[e]             = k < 16u ? cp[6144u + k * 64u + 16u * b + i] : (half_t)0.0f;
+    }
+    return a;
+}
+// W^T for a 64-output layer W [64][n_in] (C2: n_in 64, D1/C1 handled below):
+// rows = W's input index 16b + i, k = W's output index via the Hidden map.
+__device__ __forceinline__ half8_t frag_hidden_t(const half_t* W, uint32_t n_in, uint32_t b, uint32_t t, uint32_t lane) {
+    const uint32_t i = lane & 15u, g = lane >> 4;
+    half8_t a;
+#pragma unroll
+    for (uint32_t e = 0; e < 8u; ++e) {
+        const int k = logical_k(KMap::Hidden, t, g, e);
+        a[e]        = W[(uint32_t)k * n_in + 16u * b + i];
+    }
+    return a;
+}
+// C1^T with rows = density-output slots 0..15 (slot 0 -> zero row, slot j ->
+// colour input j - 1), k = h1 neuron via the Hidden map.
+__device__ __forceinline__ half8_t frag_c1t(const half_t* cp, uint32_t t, uint32_t lane) {
+    const uint32_t i = lane & 15u, g = lane >> 4;
+    half8_t a;
+#pragma unroll
+    for (uint32_t e = 0; e < 8u; ++e) {
+        const int k = logical_k(KMap::Hidden, t, g, e);
+        a[e]        = i == 0u ? (half_t)0.0f : cp[(uint32_t)k * 32u + (i - 1u)];
+    }
+    return a;
+}
+// D2^T: rows = hd neurons 16b + i, k = density output slot 4g + e (e < 4).
+__device__ __forceinline__ half8_t frag_d2t(const half_t* dp, uint32_t b, uint32_t lane) {
+    const uint32_t i = lane & 15u, g = lane >> 4;
+    half8_t a;
+#pragma unroll
+    for (uint32_t e = 0; e < 8u; ++e) a[e] = e < 4u ? dp[2048u + (4u * g + e) * 64u + 16u * b + i] : (half_t)0.0f;
+    return a;
+}
+
+__device__ __forceinline__ half4_t mask_half(const floatx4 v, const half4_t act) {
+    half4_t h;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) h[e] = act[e] > (half_t)0.0f ? (half_t)v[e] : (half_t)0.0f;
+    return h;
+}
+
+// Everything one 16-sample tile needs in the backward passes.
+struct TileGrad {
+    half8_t x;        // density input (hash features), B layout
+    half4_t hd[4];    // density hidden
+    half4_t dhd[4];   // its delta
+    half4_t dout;     // density output delta (slots 4g..4g+3)
+    half8_t xc;       // colour input, B layout (ColorIn map)
+    half4_t h1[4], dh1[4], h2[4], dh2[4];
+    half8_t do3;      // colour output delta, identity map
+    floatx4 dx[2];    // hash-feature gradient: features 16b + 4g + e
+};
+
+// Recomputes the forward of one tile and back-propagates (loss-scaled fp16
+// deltas, fp32 MFMA accumulation): the chain of the oracle's orc_mlp_backward.
+__device__ __forceinline__ void tile_backward(const half_t* dp, const half_t* cp, const DensityFrags& fd, const half8_t x, const float d[3], const float4 g, float ls, uint32_t grp, TileGrad& T) {
+    const floatx4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+    const uint32_t lane = threadIdx.x & 63u;
+    T.x = x;
+    layer_32_64(fd.w1, x, T.hd);
+    const floatx4 o = layer_64_16(fd.w2, T.hd);
+    float sh[4];
+    sh4_quad(d, grp, sh);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        T.xc[e]     = (half_t)o[e];
+        T.xc[4 + e] = (half_t)sh[e];
+    }
+    if (grp == 0u) T.xc[0] = (half_t)0.0f;
+    // colour forward (weights straight from LDS)
+#pragma unroll
+    for (uint32_t b = 0; b < 4u; ++b) T.h1[b] = relu_half(mfma16x16x32(load_a(cp, 32u, b, 0u, KMap::ColorIn, lane), T.xc, zero));
+#pragma unroll
+    for (uint32_t b = 0; b < 4u; ++b) {
+        floatx4 a = mfma16x16x32(load_a(cp + 2048, 64u, b, 0u, KMap::Hidden, lane), cat(T.h1[0], T.h1[1]), zero);
+        a         = mfma16x16x32(load_a(cp + 2048, 64u, b, 1u, KMap::Hidden, lane), cat(T.h1[2], T.h1[3]), a);
+        T.h2[b]   = relu_half(a);
+    }
+    // colour backward
+#pragma unroll
+    for (uint32_t e = 0; e < 8u; ++e) {
+        const uint32_t k = 8u * grp + e;
+        const float v    = k == 0u ? g.y : (k == 1u ? g.z : (k == 2u ? g.w : 0.0f));
+        T.do3[e]         = to_half_rne(ls * v);
+    }
+#pragma unroll
+    for (uint32_t b = 0; b < 4u; ++b) T.dh2[b] = mask_half(mfma16x16x32(frag_c3t(cp, b, lane), T.do3, zero), T.h2[b]);
+#pragma unroll
+    for (uint32_t b = 0; b < 4u; ++b) {
+        floatx4 a = mfma16x16x32(frag_hidden_t(cp + 2048, 64u, b, 0u, lane), cat(T.dh2[0], T.dh2[1]), zero);
+        a         = mfma16x16x32(frag_hidden_t(cp + 2048, 64u, b, 1u, lane), cat(T.dh2[2], T.dh2[3]), a);
+        T.dh1[b]  = mask_half(a, T.h1[b]);
+    }
+    floatx4 dgeo = mfma16x16x32(frag_c1t(cp, 0u, lane), cat(T.dh1[0], T.dh1[1]), zero);
+    dgeo         = mfma16x16x32(frag_c1t(cp, 1u, lane), cat(T.dh1[2], T.dh1[3]), dgeo);
+    // density backward
+#pragma unroll
+    for (int e = 0; e < 4; ++e) T.dout[e] = (half_t)dgeo[e];
+    if (grp == 0u) T.dout[0] = to_half_rne(ls * g.x);
+    const half4_t z4 = {(half_t)0.0f, (half_t)0.0f, (half_t)0.0f, (half_t)0.0f};
+#pragma unroll
+    for (uint32_t b = 0; b < 4u; ++b) T.dhd[b] = mask_half(mfma16x16x32(frag_d2t(dp, b, lane), cat(T.dout, z4), zero), T.hd[b]);
+#pragma unroll
+    for (uint32_t b = 0; b < 2u; ++b) {
+        floatx4 a = mfma16x16x32(frag_hidden_t(dp, 32u, b, 0u, lane), cat(T.dhd[0], T.dhd[1]), zero);
+        T.dx[b]   = mfma16x16x32(frag_hidden_t(dp, 32u, b, 1u, lane), cat(T.dhd[2], T.dhd[3]), a);
+    }
+}
+
+__device__ __forceinline__ void sample_geometry(const float2* samples, const uint32_t* sample_ray, const float4* rays, const float* bmin, const float* bmax, uint32_t q, float p[3], float d[3]) {
+    const float2 td  = samples[q];
+    const uint32_t r = sample_ray[q];
+    const float4 ro = rays[2ull * r], rd = rays[2ull * r + 1u];
+    d[0] = rd.x;
+    d[1] = rd.y;
+    d[2] = rd.z;
+    const float w[3] = {ro.x + td.x * rd.x, ro.y + td.x * rd.y, ro.z + td.x * rd.z};
+#pragma unroll
+    for (int a = 0; a < 3; ++a) p[a] = (w[a] - bmin[a]) / (bmax[a] - bmin[a]);
+}
+
+// Scatter-add of d(feature) into the fp32 table gradient for one level.
+__device__ __forceinline__ void scatter_level(const GridParams& g, float* __restrict__ grad, uint32_t level, const float p[3], float d0, float d1) {
+    const uint32_t N  = g.resolution[level];
+    const bool dense  = g.dense[level] != 0u;
+    const LevelCell c = level_cell(p, N);
+    float* base       = grad + (uint64_t)level * g.table_size * 2u;
+#pragma unroll
+    for (uint32_t k = 0; k < 8u; ++k) {
+        const uint32_t idx = corner_index(c, k, N, dense, g.table_size - 1u);
+        const float w      = corner_weight(c, k);
+        atomicAdd(base + 2u * idx, w * d0);
+        atomicAdd(base + 2u * idx + 1u, w * d1);
+    }
+}
+
+__device__ __forceinline__ uint32_t select4(const uint32_t* a, uint32_t grp, uint32_t off) {
+    return grp == 0u ? a[off] : grp == 1u ? a[off + 2u] : grp == 2u ? a[off + 4u] : a[off + 6u];
+}
+
+// Input-gradient pass: d(features) of each tile, scattered into the table
+// gradient.  Lane (g, s) holds features 16b + 4g + e, i.e. levels 2g, 2g+1
+// (b = 0) and 8+2g, 9+2g (b = 1) of sample s.
+__global__ __launch_bounds__(kThreads) void k_bwd_dx(TrainParams P, GridParams g, const TrainDevState* S, const half_t* __restrict__ dparams, const half_t* __restrict__ cparams, const half_t* __restrict__ features,
+                                                     const float4* __restrict__ draw, const float2* __restrict__ samples, const uint32_t* __restrict__ sample_ray, const float4* __restrict__ rays, float* __restrict__ table_grad) {
+    __shared__ half_t sp[kMlpParams];
+    for (uint32_t i = threadIdx.x; i < NERF_EXT_DENSITY_PARAMS; i += blockDim.x) sp[i] = dparams[i];
+    for (uint32_t i = threadIdx.x; i < NERF_EXT_COLOR_PARAMS; i += blockDim.x) sp[NERF_EXT_DENSITY_PARAMS + i] = cparams[i];
+    __syncthreads();
+    const uint32_t n = min(S->n_samples, P.sample_cap);
+    const uint32_t lane = threadIdx.x & 63u, grp = lane >> 4, s16 = lane & 15u;
+    DensityFrags fd;
+    load_density(sp, fd, lane);
+    const uint32_t tiles = (n + 15u) / 16u;
+    for (uint32_t tile = blockIdx.x * kWaves + (threadIdx.x >> 6); tile < tiles; tile += gridDim.x * kWaves) {
+        const uint32_t s = tile * 16u + s16;
+        const uint32_t q = s < n ? s : n - 1u;
+        float p[3], d[3];
+        sample_geometry(samples, sample_ray, rays, P.bmin, P.bmax, q, p, d);
+        const half8_t x = *reinterpret_cast<const half8_t*>(features + (uint64_t)q * 32u + 8u * grp);
+        const float4 gr = draw[q];
+        TileGrad T;
+        tile_backward(sp, sp + NERF_EXT_DENSITY_PARAMS, fd, x, d, gr, P.loss_scale, grp, T);
+        if (s < n) {
+#pragma unroll
+            for (uint32_t b = 0; b < 2u; ++b) {
+                const uint32_t l0 = 8u * b + 2u * grp;
+                if (l0 < g.n_levels) scatter_level(g, table_grad, l0, p, T.dx[b][0], T.dx[b][1]);
+                if (l0 + 1u < g.n_levels) scatter_level(g, table_grad, l0 + 1u, p, T.dx[b][2], T.dx[b][3]);
+            }
+        }
+    }
+}
+
+// Weight-gradient passes.  Group 0: colour hidden (64x64).  Group 1: colour
+// input (64x32) and output (16x64).  Group 2: density input (64x32) and
+// output (16x64).  Per wave and per 32 samples (two tiles), deltas and
+// activations are written to LDS as [neuron][32 samples]; dW blocks are then
+// MFMAs with the 32 samples on the reduction axis.
+constexpr uint32_t kDwScratch = 5632;  // halfs per wave (largest group)
+
+__device__ __forceinline__ void lds_put_c(half_t* L, const half4_t v[4], uint32_t nblocks, uint32_t col, uint32_t grp) {
+#pragma unroll
+    for (uint32_t b = 0; b < 4u; ++b)
+        if (b < nblocks)
+#pragma unroll
+            for (uint32_t e = 0; e < 4u; ++e) L[(16u * b + 4u * grp + e) * 32u + col] = v[b][e];
+}
+
+__device__ __forceinline__ half8_t lds_row8(const half_t* L, uint32_t row, uint32_t grp) { return *reinterpret_cast<const half8_t*>(L + row * 32u + 8u * grp); }
+
+template <uint32_t kGroup>
+__global__ __launch_bounds__(kThreads) void k_bwd_dw(TrainParams P, const TrainDevState* S, const half_t* __restrict__ dparams, const half_t* __restrict__ cparams, const half_t* __restrict__ features, const float4* __restrict__ draw,
+                                                     const float2* __restrict__ samples, const uint32_t* __restrict__ sample_ray, const float4* __restrict__ rays, float* __restrict__ partials) {
+    __shared__ half_t sp[kMlpParams];
+    __shared__ __align__(16) half_t scratch[kWaves * kDwScratch];
+    for (uint32_t i = threadIdx.x; i < NERF_EXT_DENSITY_PARAMS; i += blockDim.x) sp[i] = dparams[i];
+    for (uint32_t i = threadIdx.x; i < NERF_EXT_COLOR_PARAMS; i += blockDim.x) sp[NERF_EXT_DENSITY_PARAMS + i] = cparams[i];
+    __syncthreads();
+    const uint32_t n = min(S->n_samples, P.sample_cap);
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u, grp = lane >> 4, s16 = lane & 15u;
+    half_t* L = scratch + wave * kDwScratch;
+    DensityFrags fd;
+    load_density(sp, fd, lane);
+    const half_t* dp = sp;
+    const half_t* cp = sp + NERF_EXT_DENSITY_PARAMS;
+    // Accumulators: group 0 uses 16 blocks (64x64); groups 1 and 2 use 8 + 4.
+    floatx4 acc[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    // LDS regions, rows of 32 halfs (one per sample of the pair):
+    //   group 0: R0 = 64-row delta, R1 = 64-row activation            (4096 halfs)
+    //   group 1/2: R0 = 64-row delta of the input layer, R1 = 32-row input,
+    //              R2 = 16-row delta of the output layer, R3 = 64-row hidden  (5632 halfs)
+    half_t* R0 = L;
+    half_t* R1 = L + 64u * 32u;
+    half_t* R2 = L + 96u * 32u;
+    half_t* R3 = L + 112u * 32u;
+    const uint32_t pairs = (n + 31u) / 32u;
+    for (uint32_t pair = blockIdx.x * kWaves + wave; pair < pairs; pair += gridDim.x * kWaves) {
+        wave_lds_sync();
+#pragma unroll
+        for (uint32_t h = 0; h < 2u; ++h) {
+            const uint32_t s   = pair * 32u + 16u * h + s16;
+            const bool valid   = s < n;
+            const uint32_t q   = valid ? s : n - 1u;
+            float p[3], d[3];
+            sample_geometry(samples, sample_ray, rays, P.bmin, P.bmax, q, p, d);
+            const half8_t x = *reinterpret_cast<const half8_t*>(features + (uint64_t)q * 32u + 8u * grp);
+            float4 gr       = draw[q];
+            if (!valid) gr = make_float4(0.0f, 0.0f, 0.0f, 0.0f);  // zero deltas for padding samples
+            TileGrad T;
+            tile_backward(dp, cp, fd, x, d, gr, P.loss_scale, grp, T);
+            const uint32_t col = 16u * h + s16;
+            if constexpr (kGroup == 0u) {
+                lds_put_c(R0, T.dh2, 4u, col, grp);
+                lds_put_c(R1, T.h1, 4u, col, grp);
+            } else if constexpr (kGroup == 1u) {
+                lds_put_c(R0, T.dh1, 4u, col, grp);
+#pragma unroll
+                for (uint32_t e = 0; e < 8u; ++e) {  // colour input, logical order; row 31 is the zero pad
+                    const int k = logical_k(KMap::ColorIn, 0u, grp, e);
+                    R1[(k < 0 ? 31u : (uint32_t)k) * 32u + col] = k < 0 ? (half_t)0.0f : T.xc[e];
+                }
+#pragma unroll
+                for (uint32_t e = 0; e < 8u; ++e)
+                    if (8u * grp + e < 16u) R2[(8u * grp + e) * 32u + col] = T.do3[e];
+                lds_put_c(R3, T.h2, 4u, col, grp);
+            } else {
+                lds_put_c(R0, T.dhd, 4u, col, grp);
+#pragma unroll
+                for (uint32_t e = 0; e < 8u; ++e) R1[(8u * grp + e) * 32u + col] = T.x[e];
+#pragma unroll
+                for (uint32_t e = 0; e < 4u; ++e) R2[(4u * grp + e) * 32u + col] = T.dout[e];
+                lds_put_c(R3, T.hd, 4u, col, grp);
+            }
+        }
+        wave_lds_sync();
+        if constexpr (kGroup == 0u) {
+#pragma unroll
+            for (uint32_t ob = 0; ob < 4u; ++ob) {
+                const half8_t a = lds_row8(R0, 16u * ob + s16, grp);
+#pragma unroll
+                for (uint32_t ib = 0; ib < 4u; ++ib) acc[4u * ob + ib] = mfma16x16x32(a, lds_row8(R1, 16u * ib + s16, grp), acc[4u * ob + ib]);
+            }
+        } else {
+            // 64 x 32 input layer: 4 x 2 blocks; 16 x 64 output layer: 1 x 4 blocks.
+#pragma unroll
+            for (uint32_t ob = 0; ob < 4u; ++ob) {
+                const half8_t a = lds_row8(R0, 16u * ob + s16, grp);
+#pragma unroll
+                for (uint32_t ib = 0; ib < 2u; ++ib) acc[2u * ob + ib] = mfma16x16x32(a, lds_row8(R1, 16u * ib + s16, grp), acc[2u * ob + ib]);
+            }
+            const half8_t a2 = lds_row8(R2, s16, grp);
+#pragma unroll
+            for (uint32_t ib = 0; ib < 4u; ++ib) acc[8u + ib] = mfma16x16x32(a2, lds_row8(R3, 16u * ib + s16, grp), acc[8u + ib]);
+        }
+    }
+    // Deterministic reduction of the 4 waves in LDS, then one partial per block.
+    __syncthreads();
+    float* red            = reinterpret_cast<float*>(scratch);
+    const uint32_t count  = kGroup == 0u ? 4096u : 3072u;
+    for (uint32_t i = threadIdx.x; i < count; i += blockDim.x) red[i] = 0.0f;
+    __syncthreads();
+    for (uint32_t w = 0; w < kWaves; ++w) {
+        if (wave == w) {
+            if constexpr (kGroup == 0u) {
+#pragma unroll
+                for (uint32_t ob = 0; ob < 4u; ++ob)
+#pragma unroll
+                    for (uint32_t ib = 0; ib < 4u; ++ib)
+#pragma unroll
+                        for (uint32_t e = 0; e < 4u; ++e) red[(16u * ob + 4u * grp + e) * 64u + 16u * ib + s16] += acc[4u * ob + ib][e];
+            } else {
+#pragma unroll
+                for (uint32_t ob = 0; ob < 4u; ++ob)
+#pragma unroll
+                    for (uint32_t ib = 0; ib < 2u; ++ib)
+#pragma unroll
+                        for (uint32_t e = 0; e < 4u; ++e) red[(16u * ob + 4u * grp + e) * 32u + 16u * ib + s16] += acc[2u * ob + ib][e];
+#pragma unroll
+                for (uint32_t ib = 0; ib < 4u; ++ib)
+#pragma unroll
+                    for (uint32_t e = 0; e < 4u; ++e) red[2048u + (4u * grp + e) * 64u + 16u * ib + s16] += acc[8u + ib][e];
+            }
+        }
+        __syncthreads();
+    }
+    // Partial layout: [block][10240] in parameter order (density 0..3071, colour 3072..).
+    float* out = partials + (uint64_t)blockIdx.x * kMlpParams;
+    for (uint32_t i = threadIdx.x; i < count; i += blockDim.x) {
+        uint32_t dst;
+        if constexpr (kGroup == 0u) dst = NERF_EXT_DENSITY_PARAMS + 2048u + i;                          // colour hidden
+        else if constexpr (kGroup == 1u) dst = NERF_EXT_DENSITY_PARAMS + (i < 2048u ? i : 6144u + (i - 2048u));  // colour input | output
+        else dst = i;                                                                                     // density input | output
+        out[dst] = red[i];
+    }
+}
+
+__global__ __launch_bounds__(256) void k_dw_reduce(const float* __restrict__ partials, uint32_t blocks, float* __restrict__ grad) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i >= kMlpParams) return;
+    float s = 0.0f;
+    for (uint32_t b = 0; b < blocks; ++b) s += partials[(uint64_t)b * kMlpParams + i];
+    grad[i] = s;
+}
+
+// ------------------------------------------------------------------ Adam
+__global__ __launch_bounds__(256) void k_grad_stats(const float* __restrict__ g, uint64_t n, TrainDevState* S) {
+    __shared__ double ws[kWaves];
+    __shared__ uint32_t bad;
+    if (threadIdx.x == 0u) bad = 0u;
+    __syncthreads();
+    double acc          = 0.0;
+    uint32_t nonfinite  = 0u;
+    const uint64_t step = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += step) {
+        const float v = g[i];
+        if (!isfinite(v)) nonfinite = 1u;
+        else acc += (double)v * (double)v;
+    }
+    const double w = wave_sum_d(acc);
+    if ((threadIdx.x & 63u) == 0u) ws[threadIdx.x >> 6] = w;
+    if (nonfinite) atomicOr(&bad, 1u);
+    __syncthreads();
+    if (threadIdx.x == 0u) {
+        const double b = ws[0] + ws[1] + ws[2] + ws[3];
+        if (b != 0.0) atomicAdd(&S->grad_sumsq, b);
+        if (bad) atomicOr(&S->nonfinite, 1u);
+    }
+}
+
+// :1513-1536: skip guard, lr decay, clip factor, bias corrections.
+__global__ void k_adam_prepare(TrainParams P, TrainDevState* S) {
+    if (threadIdx.x != 0u || blockIdx.x != 0u) return;
+    const float gn        = (float)sqrt(S->grad_sumsq > 0.0 ? S->grad_sumsq : 0.0) / P.loss_scale;
+    const uint32_t t      = S->frame + 1u;  // optimizer step
+    const bool skip       = S->nonfinite != 0u || !isfinite(gn) || gn > P.guard;
+    S->skip               = skip ? 1u : 0u;
+    S->inv_ls             = 1.0f / P.loss_scale;
+    if (skip) {
+        S->lr = 0.0f;
+        S->grad_scale = 1.0f;
+        S->inv_bc1 = 1.0f;
+        S->inv_bc2 = 1.0f;
+        return;
+    }
+    const float decay = (float)P.lr_decay_ksteps * 1000.0f;
+    S->lr             = decay > 0.0f ? P.lr * powf(0.1f, (float)t / decay) : P.lr;
+    S->grad_scale     = (gn > P.clip && gn > 0.0f) ? P.clip / gn : 1.0f;
+    S->inv_bc1        = 1.0f / (1.0f - powf(P.beta1, (float)t));
+    S->inv_bc2        = 1.0f / (1.0f - powf(P.beta2, (float)t));
+}
+
+// :1537-1554 on fp32 masters with fp16 working copies; the gradient is
+// consumed and zeroed whether or not the update is applied.
+__global__ __launch_bounds__(256) void k_adam(TrainParams P, const TrainDevState* S, float* __restrict__ w, half_t* __restrict__ w16, float* __restrict__ g, float* __restrict__ m, float* __restrict__ v, uint64_t n) {
+    const bool skip       = S->skip != 0u;
+    const float lr = S->lr, gs = S->grad_scale * S->inv_ls, bc1 = S->inv_bc1, bc2 = S->inv_bc2;
+    const float b1 = P.beta1, b2 = P.beta2, eps = P.eps;
+    const uint64_t step = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += step) {
+        const float gr = g[i] * gs;
+        g[i]           = 0.0f;
+        if (skip) continue;
+        const float mi = b1 * m[i] + (1.0f - b1) * gr;
+        const float vi = b2 * v[i] + (1.0f - b2) * gr * gr;
+        const float wi = w[i] - lr * (mi * bc1) / (sqrtf(vi * bc2) + eps);
+        m[i]           = mi;
+        v[i]           = vi;
+        w[i]           = wi;
+        w16[i]         = to_half_rne(wi);
+    }
+}
+
+uint32_t grid_for(uint64_t n, uint32_t cap) {
+    const uint64_t b = (n + 255u) / 256u;
+    return (uint32_t)(b < cap ? (b > 0u ? b : 1u) : cap);
+}
+
+}  // namespace
+
+hipError_t launch_composite_train(const TrainParams& P, const TrainBuffers& B, hipStream_t st) {
+    k_composite_train<<<(P.max_rays + 255u) / 256u, 256, 0, st>>>(P, B.state, B.kept, B.offsets, B.samples, B.field, B.gt, B.draw);
+    return hipGetLastError();
+}
+
+hipError_t launch_mlp_backward(const TrainParams& P, const TrainBuffers& B, hipStream_t st) {
+    const uint32_t cus = device_cu_count();
+    if (B.grid.table_dtype != NERF_EXT_F16) return hipErrorInvalidValue;
+    k_bwd_dx<<<cus * 4u, kThreads, 0, st>>>(P, B.grid, B.state, B.dparams, B.cparams, B.features, B.draw, B.samples, B.sample_ray, B.rays, B.table_grad);
+    k_bwd_dw<0><<<kDwBlocks, kThreads, 0, st>>>(P, B.state, B.dparams, B.cparams, B.features, B.draw, B.samples, B.sample_ray, B.rays, B.dw_partials);
+    k_bwd_dw<1><<<kDwBlocks, kThreads, 0, st>>>(P, B.state, B.dparams, B.cparams, B.features, B.draw, B.samples, B.sample_ray, B.rays, B.dw_partials);
+    k_bwd_dw<2><<<kDwBlocks, kThreads, 0, st>>>(P, B.state, B.dparams, B.cparams, B.features, B.draw, B.samples, B.sample_ray, B.rays, B.dw_partials);
+    k_dw_reduce<<<(kMlpParams + 255u) / 256u, 256, 0, st>>>(B.dw_partials, kDwBlocks, B.mlp_grad);
+    return hipGetLastError();
+}
+
+hipError_t launch_adam(const TrainParams& P, const TrainBuffers& B, hipStream_t st) {
+    const uint32_t cap = device_cu_count() * 16u;
+    k_grad_stats<<<grid_for(B.table_elems, cap), 256, 0, st>>>(B.table_grad, B.table_elems, B.state);
+    k_grad_stats<<<grid_for(kMlpParams, cap), 256, 0, st>>>(B.mlp_grad, kMlpParams, B.state);
+    k_adam_prepare<<<1, 64, 0, st>>>(P, B.state);
+    k_adam<<<grid_for(B.table_elems, cap), 256, 0, st>>>(P, B.state, B.table_f32, B.table, B.table_grad, B.table_m, B.table_v, B.table_elems);
+    // MLP masters: density then colour, fp16 copies in two separate arrays.
+    k_adam<<<grid_for(NERF_EXT_DENSITY_PARAMS, cap), 256, 0, st>>>(P, B.state, B.mlp_f32, B.dparams, B.mlp_grad, B.mlp_m, B.mlp_v, NERF_EXT_DENSITY_PARAMS);
+    k_adam<<<grid_for(NERF_EXT_COLOR_PARAMS, cap), 256, 0, st>>>(P, B.state, B.mlp_f32 + NERF_EXT_DENSITY_PARAMS, B.cparams, B.mlp_grad + NERF_EXT_DENSITY_PARAMS, B.mlp_m + NERF_EXT_DENSITY_PARAMS,
+                                                                B.mlp_v + NERF_EXT_DENSITY_PARAMS, NERF_EXT_COLOR_PARAMS);
+    return hipGetLastError();
+}
+
+hipError_t launch_train_stage(const TrainParams& P, const TrainBuffers& B, uint32_t stage, bool occupancy_update, hipStream_t st) {
+    const uint32_t cus        = device_cu_count();
+    const uint32_t ray_blocks = (P.max_rays + 255u) / 256u;
+    switch (stage) {
+    case NERF_EXT_STAGE_BEGIN: k_step_begin<<<1, 64, 0, st>>>(P, B.state); break;
+    case NERF_EXT_STAGE_OCCUPANCY:
+        if (occupancy_update) {
+            k_occ_decay<<<(P.occ_cells + 255u) / 256u, 256, 0, st>>>(P, B.state, B.density);
+            k_occ_eval<half_t><<<cus * 4u, kThreads, 0, st>>>(P, B.grid, B.table, B.dparams, B.state, B.density);
+            k_occ_bits<<<(P.occ_cells + 255u) / 256u, 256, 0, st>>>(P, B.state, B.density, B.bits);
+        }
+        break;
+    case NERF_EXT_STAGE_SAMPLE: {
+        k_train_rays<<<ray_blocks, 256, 0, st>>>(P, B.state, B.cams, B.images, B.bits, B.rays, B.gt, B.counts);
+        const hipError_t e = exclusive_scan_u32(B.counts, B.offsets, P.max_rays, B.scan_tmp, &B.state->total, st);
+        if (e != hipSuccess) return e;
+        k_train_samples<<<ray_blocks, 256, 0, st>>>(P, B.state, B.cams, B.bits, B.rays, B.counts, B.offsets, B.kept, B.samples, B.sample_ray);
+        break;
+    }
+    case NERF_EXT_STAGE_FORWARD: {
+        FieldInputs in{};
+        in.samples      = B.samples;
+        in.sample_ray   = B.sample_ray;
+        in.rays         = B.rays;
+        in.n_dev        = &B.state->n_samples;
+        in.features_out = B.features;
+        for (int a = 0; a < 3; ++a) {
+            in.bmin[a] = P.bmin[a];
+            in.bmax[a] = P.bmax[a];
+        }
+        return launch_field(B.grid, B.table, FieldWeights{B.dparams, B.cparams}, in, P.sample_cap, B.field, st);
+    }
+    case NERF_EXT_STAGE_COMPOSITE: return launch_composite_train(P, B, st);
+    case NERF_EXT_STAGE_BACKWARD: return launch_mlp_backward(P, B, st);
+    case NERF_EXT_STAGE_ADAM: return launch_adam(P, B, st);
+    case NERF_EXT_STAGE_END: k_step_end<<<1, 64, 0, st>>>(P, B.state); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace nerf_hip

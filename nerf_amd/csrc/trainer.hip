@@ -1,0 +1,313 @@
+// trainer.hip — the training run object behind nerf_ext_trainer_* and the
+// reference ABI's nerf_configure_training / nerf_train_step.
+//
+// Owns the device state, the ray/sample buffers of one step and (unless the
+// caller lends them) the model: fp32 master table and MLP weights, their
+// fp16 working copies, Adam moments and gradients, and the occupancy grid.
+#include <string.h>
+
+#include <vector>
+
+#include "trainer.hpp"
+
+namespace nerf_hip {
+
+Trainer::~Trainer() {
+    if (stream) (void)hipStreamSynchronize(stream);
+    for (void* p : owned)
+        if (p) (void)hipFree(p);
+    if (stream && own_stream) (void)hipStreamDestroy(stream);
+}
+
+template <typename T>
+static hipError_t alloc(Trainer& t, T*& ptr, uint64_t count) {
+    void* p        = nullptr;
+    const hipError_t e = hipMalloc(&p, count * sizeof(T) > 0 ? count * sizeof(T) : 16u);
+    if (e != hipSuccess) return e;
+    t.owned.push_back(p);
+    ptr = static_cast<T*>(p);
+    return hipSuccess;
+}
+
+bool Trainer::occupancy_due(uint32_t frame) const {
+    if (frame < P.occ_warmup) return frame == 0u;                      // backend-cuda.cu:1483-1485
+    return P.occ_interval != 0u && frame % P.occ_interval == 0u;       // :1487
+}
+
+NerfStatus Trainer::run_stages(uint32_t first, uint32_t last) {
+    for (uint32_t s = first; s <= last; ++s) {
+        NERF_HIP_TRY(launch_train_stage(P, B, s, occupancy_due(host_frame), stream));
+        if (s == NERF_EXT_STAGE_END) ++host_frame;
+    }
+    return NERF_STATUS_OK;
+}
+
+NerfStatus trainer_create(const NerfExtTrainDesc* d, const BorrowedModel* borrowed, hipStream_t stream, Trainer** out) {
+    NERF_CHECK_ARG(d && out, "trainer: null argument");
+    *out = nullptr;
+    NERF_CHECK_ARG(d->image_count >= 1u && d->cameras && d->images_rgba8, "trainer: a dataset of at least one image is required");
+    NERF_CHECK_ARG(d->grid.table_dtype == NERF_EXT_F16, "trainer: the hash table must be fp16");
+    NERF_CHECK_ARG(d->max_rays >= 1u && d->sample_capacity >= 1u && d->max_steps_per_ray >= 1u, "trainer: capacities must be >= 1");
+    NERF_CHECK_ARG(d->occupancy_res >= 1u && d->occupancy_res <= 1024u, "trainer: occupancy_res must be 1..1024");
+    NERF_CHECK_ARG(d->hyper.loss_scale > 0.0f, "trainer: loss_scale must be > 0");
+    const uint32_t W = d->cameras[0].width, H = d->cameras[0].height;
+    for (uint32_t i = 0; i < d->image_count; ++i) NERF_CHECK_ARG(d->cameras[i].width == W && d->cameras[i].height == H && W > 0u && H > 0u, "trainer: all images must share one non-empty size");
+    for (int a = 0; a < 3; ++a) NERF_CHECK_ARG(d->aabb_max[a] > d->aabb_min[a], "trainer: empty AABB");
+
+    auto t = std::make_unique<Trainer>();
+    GridParams g;
+    NerfStatus st = make_grid(&d->grid, g);
+    if (st != NERF_STATUS_OK) return st;
+    NERF_CHECK_ARG(g.n_levels * g.n_features == 32u, "trainer: the density MLP takes 32 features (16 levels x 2)");
+    if (stream) {
+        t->stream = stream;
+    } else {
+        NERF_HIP_TRY(hipStreamCreateWithFlags(&t->stream, hipStreamNonBlocking));
+        t->own_stream = true;
+    }
+    TrainParams& P = t->P;
+    P.image_count  = d->image_count;
+    P.width        = W;
+    P.height       = H;
+    P.occ_res      = d->occupancy_res;
+    for (int a = 0; a < 3; ++a) {
+        P.bmin[a] = d->aabb_min[a];
+        P.bmax[a] = d->aabb_max[a];
+    }
+    P.max_steps            = d->max_steps_per_ray;
+    P.max_rays             = d->max_rays;
+    P.sample_cap           = d->sample_capacity;
+    P.target_samples       = d->target_samples;
+    P.min_rays             = d->target_samples ? 64u : 1u;
+    if (P.min_rays > P.max_rays) P.min_rays = P.max_rays;
+    P.huber_delta          = d->huber_delta > 0.0f ? d->huber_delta : 0.1f;
+    P.loss_scale           = d->hyper.loss_scale;
+    P.lr                   = d->hyper.learning_rate;
+    P.beta1                = d->hyper.adam_beta1;
+    P.beta2                = d->hyper.adam_beta2;
+    P.eps                  = d->hyper.adam_eps;
+    P.clip                 = d->hyper.grad_clip_norm;
+    P.guard                = d->hyper.update_guard_grad_norm;
+    P.lr_decay_ksteps      = d->hyper.lr_decay_ksteps;
+    P.occ_decay            = d->occupancy.decay;
+    P.occ_threshold        = d->occupancy.threshold;
+    P.occ_cells_per_update = d->occupancy.cells_per_update;
+    P.occ_interval         = d->occupancy.update_interval;
+    P.occ_warmup           = d->occupancy.warmup_steps;
+    P.occ_cells            = d->occupancy_res * d->occupancy_res * d->occupancy_res;
+
+    TrainBuffers& B = t->B;
+    B.grid          = g;
+    B.table_elems   = (uint64_t)g.n_levels * g.table_size * g.n_features;
+    Trainer& T      = *t;
+    NERF_HIP_TRY(alloc(T, B.state, 1));
+    NerfExtCamera* cams = nullptr;
+    NERF_HIP_TRY(alloc(T, cams, d->image_count));
+    B.cams = cams;
+    uint8_t* images = nullptr;
+    NERF_HIP_TRY(alloc(T, images, (uint64_t)d->image_count * W * H * 4u));
+    B.images = images;
+    NERF_HIP_TRY(alloc(T, B.rays, 2ull * P.max_rays));
+    NERF_HIP_TRY(alloc(T, B.gt, P.max_rays));
+    NERF_HIP_TRY(alloc(T, B.counts, P.max_rays));
+    NERF_HIP_TRY(alloc(T, B.kept, P.max_rays));
+    NERF_HIP_TRY(alloc(T, B.offsets, P.max_rays));
+    NERF_HIP_TRY(alloc(T, B.scan_tmp, scan_tmp_words(P.max_rays)));
+    NERF_HIP_TRY(alloc(T, B.samples, P.sample_cap));
+    NERF_HIP_TRY(alloc(T, B.sample_ray, P.sample_cap));
+    NERF_HIP_TRY(alloc(T, B.field, P.sample_cap));
+    NERF_HIP_TRY(alloc(T, B.features, 32ull * P.sample_cap));
+    NERF_HIP_TRY(alloc(T, B.draw, P.sample_cap));
+    NERF_HIP_TRY(alloc(T, B.table_grad, B.table_elems));
+    NERF_HIP_TRY(alloc(T, B.table_m, B.table_elems));
+    NERF_HIP_TRY(alloc(T, B.table_v, B.table_elems));
+    NERF_HIP_TRY(alloc(T, B.mlp_grad, kMlpParams));
+    NERF_HIP_TRY(alloc(T, B.mlp_m, kMlpParams));
+    NERF_HIP_TRY(alloc(T, B.mlp_v, kMlpParams));
+    NERF_HIP_TRY(alloc(T, B.dw_partials, (uint64_t)kDwBlocks * kMlpParams));
+    if (borrowed) {
+        B.table     = borrowed->table;
+        B.table_f32 = borrowed->table_f32;
+        B.dparams   = borrowed->dparams;
+        B.cparams   = borrowed->cparams;
+        B.mlp_f32   = borrowed->mlp_f32;
+        B.bits      = borrowed->bits;
+        B.density   = borrowed->density;
+    } else {
+        NERF_HIP_TRY(alloc(T, B.table, B.table_elems));
+        NERF_HIP_TRY(alloc(T, B.table_f32, B.table_elems));
+        NERF_HIP_TRY(alloc(T, B.dparams, NERF_EXT_DENSITY_PARAMS));
+        NERF_HIP_TRY(alloc(T, B.cparams, NERF_EXT_COLOR_PARAMS));
+        NERF_HIP_TRY(alloc(T, B.mlp_f32, kMlpParams));
+        NERF_HIP_TRY(alloc(T, B.bits, (P.occ_cells + 31u) / 32u));
+        NERF_HIP_TRY(alloc(T, B.density, P.occ_cells));
+    }
+    hipStream_t s = T.stream;
+    NERF_HIP_TRY(hipMemcpyAsync(cams, d->cameras, sizeof(NerfExtCamera) * d->image_count, hipMemcpyHostToDevice, s));
+    NERF_HIP_TRY(hipMemcpyAsync(images, d->images_rgba8, (uint64_t)d->image_count * W * H * 4u, hipMemcpyHostToDevice, s));
+    T.initial_rays = (float)(d->initial_rays ? d->initial_rays : 1u);
+    st             = T.reset();
+    if (st != NERF_STATUS_OK) return st;
+    if (!borrowed) {
+        NerfExtGridDesc g32 = d->grid;
+        g32.table_dtype     = NERF_EXT_F32;
+        st                  = nerf_ext_grid_init_table(&g32, d->seed, d->table_init_range, B.table_f32, s);
+        if (st != NERF_STATUS_OK) return st;
+        st = nerf_ext_float_to_half(B.table_f32, (uint16_t*)B.table, B.table_elems, s);
+        if (st != NERF_STATUS_OK) return st;
+        std::vector<float> w(kMlpParams);
+        nerf_ext_mlp_init(0u, w.data());
+        nerf_ext_mlp_init(1u, w.data() + NERF_EXT_DENSITY_PARAMS);
+        NERF_HIP_TRY(hipMemcpyAsync(B.mlp_f32, w.data(), sizeof(float) * kMlpParams, hipMemcpyHostToDevice, s));
+        NERF_HIP_TRY(hipStreamSynchronize(s));
+        st = nerf_ext_float_to_half(B.mlp_f32, (uint16_t*)B.dparams, NERF_EXT_DENSITY_PARAMS, s);
+        if (st == NERF_STATUS_OK) st = nerf_ext_float_to_half(B.mlp_f32 + NERF_EXT_DENSITY_PARAMS, (uint16_t*)B.cparams, NERF_EXT_COLOR_PARAMS, s);
+        if (st != NERF_STATUS_OK) return st;
+    }
+    NERF_HIP_TRY(hipStreamSynchronize(s));
+    T.grid_desc = d->grid;
+    *out       = t.release();
+    return NERF_STATUS_OK;
+}
+
+NerfStatus Trainer::reset() {
+    hipStream_t s = stream;
+    NERF_HIP_TRY(hipMemsetAsync(B.table_grad, 0, B.table_elems * 4u, s));
+    NERF_HIP_TRY(hipMemsetAsync(B.table_m, 0, B.table_elems * 4u, s));
+    NERF_HIP_TRY(hipMemsetAsync(B.table_v, 0, B.table_elems * 4u, s));
+    NERF_HIP_TRY(hipMemsetAsync(B.mlp_grad, 0, kMlpParams * 4u, s));
+    NERF_HIP_TRY(hipMemsetAsync(B.mlp_m, 0, kMlpParams * 4u, s));
+    NERF_HIP_TRY(hipMemsetAsync(B.mlp_v, 0, kMlpParams * 4u, s));
+    NERF_HIP_TRY(hipMemsetAsync(B.bits, 0, (P.occ_cells + 31u) / 32u * 4u, s));
+    NERF_HIP_TRY(hipMemsetAsync(B.density, 0, (uint64_t)P.occ_cells * 4u, s));
+    TrainDevState init{};
+    init.rays_f = initial_rays;
+    NERF_HIP_TRY(hipMemcpyAsync(B.state, &init, sizeof(init), hipMemcpyHostToDevice, s));
+    NERF_HIP_TRY(hipStreamSynchronize(s));
+    host_frame = 0u;
+    return NERF_STATUS_OK;
+}
+
+NerfStatus Trainer::read_state(TrainDevState& host) {
+    NERF_HIP_TRY(hipStreamSynchronize(stream));
+    NERF_HIP_TRY(hipMemcpy(&host, B.state, sizeof(host), hipMemcpyDeviceToHost));
+    return NERF_STATUS_OK;
+}
+
+}  // namespace nerf_hip
+
+using namespace nerf_hip;
+
+struct NerfExtTrainer {
+    nerf_hip::Trainer* t = nullptr;
+};
+
+extern "C" {
+
+NERF_API NerfStatus nerf_ext_trainer_create(const NerfExtTrainDesc* desc, NerfExtTrainer** out) {
+    NERF_CHECK_ARG(out, "nerf_ext_trainer_create: null output");
+    *out       = nullptr;
+    Trainer* t = nullptr;
+    const NerfStatus s = trainer_create(desc, nullptr, nullptr, &t);
+    if (s != NERF_STATUS_OK) return s;
+    *out      = new NerfExtTrainer();
+    (*out)->t = t;
+    return NERF_STATUS_OK;
+}
+
+NERF_API NerfStatus nerf_ext_trainer_destroy(NerfExtTrainer* trainer) {
+    if (!trainer) return NERF_STATUS_OK;
+    delete trainer->t;
+    delete trainer;
+    return NERF_STATUS_OK;
+}
+
+NERF_API NerfStatus nerf_ext_trainer_step(NerfExtTrainer* trainer, uint32_t steps) {
+    NERF_CHECK_ARG(trainer && trainer->t, "nerf_ext_trainer_step: null trainer");
+    for (uint32_t i = 0; i < steps; ++i) {
+        const NerfStatus s = trainer->t->run_stages(NERF_EXT_STAGE_BEGIN, NERF_EXT_STAGE_END);
+        if (s != NERF_STATUS_OK) return s;
+    }
+    return NERF_STATUS_OK;
+}
+
+NERF_API NerfStatus nerf_ext_trainer_run_stages(NerfExtTrainer* trainer, uint32_t first, uint32_t last) {
+    NERF_CHECK_ARG(trainer && trainer->t, "nerf_ext_trainer_run_stages: null trainer");
+    NERF_CHECK_ARG(first <= last && last <= NERF_EXT_STAGE_END, "nerf_ext_trainer_run_stages: bad stage range");
+    return trainer->t->run_stages(first, last);
+}
+
+NERF_API NerfStatus nerf_ext_trainer_synchronize(NerfExtTrainer* trainer) {
+    NERF_CHECK_ARG(trainer && trainer->t, "nerf_ext_trainer_synchronize: null trainer");
+    NERF_HIP_TRY(hipStreamSynchronize(trainer->t->stream));
+    return NERF_STATUS_OK;
+}
+
+NERF_API NerfStatus nerf_ext_trainer_stats(NerfExtTrainer* trainer, NerfExtTrainStats* out) {
+    NERF_CHECK_ARG(trainer && trainer->t && out, "nerf_ext_trainer_stats: null argument");
+    TrainDevState s{};
+    const NerfStatus st = trainer->t->read_state(s);
+    if (st != NERF_STATUS_OK) return st;
+    out->last             = s.stats;
+    out->rays             = s.n_rays;
+    out->samples          = s.n_samples;
+    out->active_rays      = s.n_active;
+    out->skipped          = s.skip;
+    out->occupied_samples = s.total;
+    return NERF_STATUS_OK;
+}
+
+NERF_API NerfStatus nerf_ext_trainer_buffers(NerfExtTrainer* trainer, NerfExtTrainBuffers* o) {
+    NERF_CHECK_ARG(trainer && trainer->t && o, "nerf_ext_trainer_buffers: null argument");
+    const TrainBuffers& B = trainer->t->B;
+    memset(o, 0, sizeof(*o));
+    o->state           = B.state;
+    o->rays            = (float*)B.rays;
+    o->gt              = (float*)B.gt;
+    o->counts          = B.counts;
+    o->kept            = B.kept;
+    o->offsets         = B.offsets;
+    o->samples         = (float*)B.samples;
+    o->sample_ray      = B.sample_ray;
+    o->field           = (float*)B.field;
+    o->features        = (uint16_t*)B.features;
+    o->draw            = (float*)B.draw;
+    o->table_grad      = B.table_grad;
+    o->mlp_grad        = B.mlp_grad;
+    o->table_f32       = B.table_f32;
+    o->mlp_f32         = B.mlp_f32;
+    o->table_m         = B.table_m;
+    o->table_v         = B.table_v;
+    o->mlp_m           = B.mlp_m;
+    o->mlp_v           = B.mlp_v;
+    o->bitfield        = B.bits;
+    o->density_grid    = B.density;
+    o->max_rays        = trainer->t->P.max_rays;
+    o->sample_capacity = trainer->t->P.sample_cap;
+    o->table_elems     = B.table_elems;
+    return NERF_STATUS_OK;
+}
+
+NERF_API NerfStatus nerf_ext_trainer_model(NerfExtTrainer* trainer, NerfExtModel* model, NerfExtOccupancy* occ) {
+    NERF_CHECK_ARG(trainer && trainer->t, "nerf_ext_trainer_model: null trainer");
+    const Trainer& t = *trainer->t;
+    if (model) {
+        model->grid           = t.grid_desc;
+        model->table          = t.B.table;
+        model->density_params = (const uint16_t*)t.B.dparams;
+        model->color_params   = (const uint16_t*)t.B.cparams;
+    }
+    if (occ) {
+        occ->bitfield   = t.B.bits;
+        occ->resolution = t.P.occ_res;
+        for (int a = 0; a < 3; ++a) {
+            occ->aabb_min[a] = t.P.bmin[a];
+            occ->aabb_max[a] = t.P.bmax[a];
+        }
+    }
+    return NERF_STATUS_OK;
+}
+
+NERF_API void* nerf_ext_trainer_stream(NerfExtTrainer* trainer) { return trainer && trainer->t ? (void*)trainer->t->stream : nullptr; }
+
+}  // extern "C"

@@ -1,0 +1,44 @@
+// trainer.hpp — host object of a training run (trainer.hip).
+#pragma once
+
+#include <memory>
+#include <vector>
+
+#include "train.hpp"
+
+namespace nerf_hip {
+
+// Model buffers lent by the owner of a model (the nerf.h context) instead of
+// being allocated by the trainer.
+struct BorrowedModel {
+    half_t* table;
+    float* table_f32;
+    half_t* dparams;
+    half_t* cparams;
+    float* mlp_f32;
+    uint32_t* bits;
+    float* density;
+};
+
+struct Trainer {
+    TrainParams P{};
+    TrainBuffers B{};
+    NerfExtGridDesc grid_desc{};
+    hipStream_t stream = nullptr;
+    bool own_stream    = false;
+    uint32_t host_frame = 0;  // steps enqueued so far (drives the occupancy schedule)
+    float initial_rays  = 1.0f;
+    std::vector<void*> owned;
+
+    ~Trainer();
+    bool occupancy_due(uint32_t frame) const;
+    NerfStatus run_stages(uint32_t first, uint32_t last);
+    NerfStatus read_state(TrainDevState& host);
+    // Zeroes gradients, Adam moments, the occupancy grid and the step state
+    // (frame 0, initial ray count); the weights are left as they are.
+    NerfStatus reset();
+};
+
+NerfStatus trainer_create(const NerfExtTrainDesc* desc, const BorrowedModel* borrowed, hipStream_t stream, Trainer** out);
+
+}  // namespace nerf_hip

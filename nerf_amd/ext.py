@@ -132,3 +132,113 @@ class Renderer:
                 L._lib.nerf_ext_renderer_destroy(self._h)
         except Exception:
             pass
+
+
+def read_device(ptr: int, shape, dtype) -> np.ndarray:
+    """Copies `shape` elements of `dtype` from a raw device pointer."""
+    out = np.empty(shape, dtype)
+    if out.nbytes:
+        L.call("nerf_ext_memcpy", out.ctypes.data, int(ptr), out.nbytes, L.NERF_EXT_D2H)
+    return out
+
+
+def scene_render(gaussians: np.ndarray, cameras: list, steps: int, aabb=(0.0, 0.0, 0.0, 1.0, 1.0, 1.0), stream: Stream | None = None) -> DeviceArray:
+    """Renders the analytic scene into RGBA8 images [views][H][W] (alpha =
+    1 - transmittance, composited over white)."""
+    g = DeviceArray.from_numpy(np.ascontiguousarray(gaussians, np.float32))
+    n_views = len(cameras)
+    w, h = cameras[0].width, cameras[0].height
+    out = DeviceArray((n_views, h, w), np.uint32)
+    cams = (L.NerfExtCamera * n_views)(*cameras)
+    box = (C.c_float * 6)(*aabb)
+    L.call("nerf_ext_scene_render", g.ptr, gaussians.shape[0], cams, n_views, C.cast(box, C.c_void_p), steps, out.ptr, stream.handle if stream else None)
+    if stream is not None:
+        stream.synchronize()
+    else:
+        from .device import synchronize
+
+        synchronize()
+    return out
+
+
+def hyper_params(lr=1e-2, beta1=0.9, beta2=0.99, eps=1e-15, clip=1e30, guard=1e30, loss_scale=1.0, lr_decay_ksteps=0) -> L.NerfHyperParams:
+    return L.NerfHyperParams(lr, beta1, beta2, eps, clip, guard, loss_scale, lr_decay_ksteps)
+
+
+def occupancy_params(decay=0.95, threshold=0.01, cells_per_update=1 << 30, update_interval=16, warmup_steps=256) -> L.NerfOccupancyParams:
+    return L.NerfOccupancyParams(decay, threshold, cells_per_update, update_interval, warmup_steps)
+
+
+class Trainer:
+    """One training run (nerf_ext_trainer_*): dataset, model, optimiser state
+    and the buffers of one step, all on the device."""
+
+    def __init__(self, grid: L.NerfExtGridDesc, images_rgba8: np.ndarray, cameras: list, *, occupancy_res=128, aabb_min=(0.0, 0.0, 0.0), aabb_max=(1.0, 1.0, 1.0), hyper: L.NerfHyperParams | None = None,
+                 occupancy: L.NerfOccupancyParams | None = None, initial_rays=4096, max_rays=1 << 18, target_samples=0, sample_capacity=1 << 20, max_steps_per_ray=1024, huber_delta=0.1, table_init_range=1e-4, seed=0):
+        images = np.ascontiguousarray(images_rgba8)
+        n = len(cameras)
+        self._cams = (L.NerfExtCamera * n)(*cameras)
+        d = L.NerfExtTrainDesc()
+        d.grid = grid
+        d.images_rgba8 = images.ctypes.data
+        d.cameras = self._cams
+        d.image_count = n
+        d.occupancy_res = occupancy_res
+        d.aabb_min = (C.c_float * 3)(*aabb_min)
+        d.aabb_max = (C.c_float * 3)(*aabb_max)
+        d.hyper = hyper or hyper_params()
+        d.occupancy = occupancy or occupancy_params()
+        d.initial_rays = initial_rays
+        d.max_rays = max_rays
+        d.target_samples = target_samples
+        d.sample_capacity = sample_capacity
+        d.max_steps_per_ray = max_steps_per_ray
+        d.huber_delta = huber_delta
+        d.table_init_range = table_init_range
+        d.seed = seed
+        self.desc = d
+        self._h = C.c_void_p()
+        L.call("nerf_ext_trainer_create", C.byref(d), C.byref(self._h))
+
+    @property
+    def handle(self) -> int:
+        return int(self._h.value or 0)
+
+    def step(self, steps: int = 1) -> None:
+        L.call("nerf_ext_trainer_step", self._h, steps)
+
+    def run_stages(self, first: int, last: int) -> None:
+        L.call("nerf_ext_trainer_run_stages", self._h, first, last)
+
+    def synchronize(self) -> None:
+        L.call("nerf_ext_trainer_synchronize", self._h)
+
+    def stats(self) -> L.NerfExtTrainStats:
+        out = L.NerfExtTrainStats()
+        L.call("nerf_ext_trainer_stats", self._h, C.byref(out))
+        return out
+
+    def buffers(self) -> L.NerfExtTrainBuffers:
+        out = L.NerfExtTrainBuffers()
+        L.call("nerf_ext_trainer_buffers", self._h, C.byref(out))
+        return out
+
+    def model(self) -> tuple[L.NerfExtModel, L.NerfExtOccupancy]:
+        m, o = L.NerfExtModel(), L.NerfExtOccupancy()
+        L.call("nerf_ext_trainer_model", self._h, C.byref(m), C.byref(o))
+        return m, o
+
+    def stream(self) -> int:
+        return int(L.load().nerf_ext_trainer_stream(self._h) or 0)
+
+    def close(self) -> None:
+        if self._h.value:
+            L.call("nerf_ext_trainer_destroy", self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            if self._h.value and L._lib is not None:
+                L._lib.nerf_ext_trainer_destroy(self._h)
+        except Exception:
+            pass

@@ -629,18 +629,15 @@ static inline double huber(double x, double d) { return fabs(x) <= d ? 0.5 * x *
 //   d raw_sigma_i  = dt_i sigma_i sum_c g_c (T_{i+1} c_ic - S_ic)
 // (the reference's T_i c - S / (1 - alpha) times d alpha / d raw =
 // dt sigma (1 - alpha)).  Evaluated in fp64; returns the un-normalised loss.
-extern "C" double orc_composite_backward_ray(const float* sraw, const float* rgbraw, const float* dt, uint32_t n, const float* gt, const float* bg, float delta, float inv_norm, float* dsraw, float* drgbraw, float* pred_out) {
-    std::vector<double> sig(n), a(n), T(n + 1), c(3 * (size_t)n);
+static double composite_backward_core(const std::vector<double>& sig, const std::vector<double>& c, const float* dt, uint32_t n, const float* gt, const float* bg, float delta, float inv_norm, float* dsraw, float* drgbraw,
+                                      float* pred_out) {
+    std::vector<double> a(n), T(n + 1);
     T[0] = 1.0;
     double pred[3] = {0, 0, 0};
     for (uint32_t i = 0; i < n; ++i) {
-        sig[i]           = exp((double)sraw[i]);
         const double dti = dt[i] > 0.0f ? (double)dt[i] : 0.0;
         a[i]             = 1.0 - exp(-sig[i] * dti);
-        for (int k = 0; k < 3; ++k) {
-            c[3 * i + k] = 1.0 / (1.0 + exp(-(double)rgbraw[3 * i + k]));
-            pred[k] += T[i] * a[i] * c[3 * i + k];
-        }
+        for (int k = 0; k < 3; ++k) pred[k] += T[i] * a[i] * c[3 * i + k];
         T[i + 1] = T[i] * (1.0 - a[i]);
     }
     double loss = 0.0, g[3];
@@ -657,14 +654,34 @@ extern "C" double orc_composite_backward_ray(const float* sraw, const float* rgb
         const double w   = T[i] * a[i];
         double ds        = 0.0;
         for (int k = 0; k < 3; ++k) {
-            const double ci        = c[3 * i + k];
-            drgbraw[3 * i + k]     = (float)(w * g[k] * ci * (1.0 - ci));
+            const double ci    = c[3 * i + k];
+            drgbraw[3 * i + k] = (float)(w * g[k] * ci * (1.0 - ci));
             ds += g[k] * (T[i + 1] * ci - S[k]);
             S[k] += w * ci;
         }
         dsraw[i] = (float)(dti * sig[i] * ds);
     }
     return loss;
+}
+
+extern "C" double orc_composite_backward_ray(const float* sraw, const float* rgbraw, const float* dt, uint32_t n, const float* gt, const float* bg, float delta, float inv_norm, float* dsraw, float* drgbraw, float* pred_out) {
+    std::vector<double> sig(n), c(3 * (size_t)n);
+    for (uint32_t i = 0; i < n; ++i) {
+        sig[i] = exp((double)sraw[i]);
+        for (int k = 0; k < 3; ++k) c[3 * i + k] = 1.0 / (1.0 + exp(-(double)rgbraw[3 * i + k]));
+    }
+    return composite_backward_core(sig, c, dt, n, gt, bg, delta, inv_norm, dsraw, drgbraw, pred_out);
+}
+
+// The same with the activations given (sigma, rgb in [0, 1]) instead of raw
+// outputs; gradients are still with respect to the raw outputs.
+extern "C" double orc_composite_backward_act(const float* sigma, const float* rgb, const float* dt, uint32_t n, const float* gt, const float* bg, float delta, float inv_norm, float* dsraw, float* drgbraw, float* pred_out) {
+    std::vector<double> sig(n), c(3 * (size_t)n);
+    for (uint32_t i = 0; i < n; ++i) {
+        sig[i] = (double)sigma[i];
+        for (int k = 0; k < 3; ++k) c[3 * i + k] = (double)rgb[3 * i + k];
+    }
+    return composite_backward_core(sig, c, dt, n, gt, bg, delta, inv_norm, dsraw, drgbraw, pred_out);
 }
 
 // MLP backward for n samples with the GPU's fp16 rounding points.
@@ -799,4 +816,107 @@ extern "C" int orc_adam(float* w, float* m, float* v, const float* g, uint64_t n
         w[i] -= lr_t * (m[i] * bc1) / (sqrtf(v[i] * bc2) + eps);
     }
     return 0;
+}
+
+// Training rays of one step (backend-cuda.cu:438-499): random pixel of ray r,
+// ray through (px, H - 1 - py), march, ground truth bilinear over the
+// RGBA8 image (top row first) composited over white.  Outputs per ray:
+// counts[r], gt[r][4] (r, g, b, alpha), pixel[r][2]; samples (t_mid, dt) are
+// written ray-major into t_dt (capacity cap), offsets[r] = start of ray r.
+extern "C" void orc_train_rays(const OrcCamera* cam, const uint8_t* image, const uint32_t* bits, uint32_t res, const float* aabb, uint32_t max_steps, uint32_t frame, uint32_t n_rays, uint32_t* counts, float* gt, float* pixel, uint32_t* offsets,
+                               float* t_dt, uint32_t cap) {
+    uint32_t off = 0;
+    const uint32_t W = cam->width, H = cam->height;
+    for (uint32_t r = 0; r < n_rays; ++r) {
+        const uint32_t seed = frame * 1315423911u ^ r * 9781u;
+        const float px      = orc_rand01(seed ^ 0xA511E9B3u) * (float)W;
+        const float py      = orc_rand01(seed ^ 0x63D83595u) * (float)H;
+        pixel[2 * r]        = px;
+        pixel[2 * r + 1]    = py;
+        OrcRay ray;
+        uint32_t count = 0;
+        offsets[r]     = off;
+        if (make_ray(*cam, px, (float)H - 1.0f - py, aabb, ray)) {
+            count = march(*cam, ray, bits, res, aabb, max_steps, [&](uint32_t k, float tm, float dt) {
+                if (off + k < cap) {
+                    t_dt[2 * (off + k)]     = tm;
+                    t_dt[2 * (off + k) + 1] = dt;
+                }
+            });
+        }
+        counts[r] = count;
+        off += count;
+        float g4[4] = {1.0f, 1.0f, 1.0f, 0.0f};
+        if (count > 0) {
+            const float cx = fmaxf(0.0f, fminf(px, (float)W - 1.0f)), cy = fmaxf(0.0f, fminf(py, (float)H - 1.0f));
+            const int x0 = (int)floorf(cx), y0 = (int)floorf(cy);
+            const int x1 = std::min(x0 + 1, (int)W - 1), y1 = std::min(y0 + 1, (int)H - 1);
+            const float tx = cx - (float)x0, ty = cy - (float)y0;
+            const float inv255 = 1.0f / 255.0f;
+            const uint8_t* p00 = image + ((uint64_t)y0 * W + x0) * 4;
+            const uint8_t* p10 = image + ((uint64_t)y0 * W + x1) * 4;
+            const uint8_t* p01 = image + ((uint64_t)y1 * W + x0) * 4;
+            const uint8_t* p11 = image + ((uint64_t)y1 * W + x1) * 4;
+            float c[4];
+            for (int k = 0; k < 4; ++k) {
+                const float a = (float)p00[k] * inv255 * (1.0f - tx) + (float)p10[k] * inv255 * tx;
+                const float b = (float)p01[k] * inv255 * (1.0f - tx) + (float)p11[k] * inv255 * tx;
+                c[k]          = a * (1.0f - ty) + b * ty;
+            }
+            const float al = c[3];
+            g4[0] = c[0] * al + (1.0f - al);
+            g4[1] = c[1] * al + (1.0f - al);
+            g4[2] = c[2] * al + (1.0f - al);
+            g4[3] = al;
+        }
+        for (int k = 0; k < 4; ++k) gt[4 * r + k] = g4[k];
+    }
+}
+
+// Camera index of training step `frame` (backend-cuda.cu:1482).
+extern "C" uint32_t orc_train_camera(uint32_t frame, uint32_t image_count) { return orc_hash_u32(frame * 747796405u + 2891336453u) % image_count; }
+
+// Ground-truth images of the analytic scene: `steps` uniform steps over the
+// ray's AABB interval, emission = density-weighted Gaussian albedo,
+// alpha = 1 - exp(-density dt), stop below transmittance 1e-4, RGB over white,
+// A = 1 - T; RGBA8 packed little-endian (R in the low byte), pixel (x, y) at
+// index y * W + x with the reference's pixel-centre and row flip.
+extern "C" void orc_scene_render(const float* gs, uint32_t count, const OrcCamera* cam, const float* aabb, uint32_t steps, uint32_t* rgba) {
+    const uint32_t W = cam->width, H = cam->height;
+    for (uint32_t y = 0; y < H; ++y) {
+        for (uint32_t x = 0; x < W; ++x) {
+            OrcRay r;
+            float T = 1.0f, Cc[3] = {0.0f, 0.0f, 0.0f};
+            if (pixel_ray(*cam, x, y, aabb, r)) {
+                const float dt = (r.tf - r.tn) / (float)steps;
+                for (uint32_t i = 0; i < steps && dt > 0.0f; ++i) {
+                    const float t    = r.tn + ((float)i + 0.5f) * dt;
+                    const float p[3] = {r.o[0] + t * r.d[0], r.o[1] + t * r.d[1], r.o[2] + t * r.d[2]};
+                    float sig = 0.0f, cr = 0.0f, cg = 0.0f, cb = 0.0f;
+                    for (uint32_t k = 0; k < count; ++k) {
+                        const float* g = gs + 8ull * k;
+                        const float dx = p[0] - g[0], dy = p[1] - g[1], dz = p[2] - g[2];
+                        const float kk = -0.5f / (g[3] * g[3]);
+                        const float v  = g[4] * nerf_math::det_expf(((dx * dx + dy * dy) + dz * dz) * kk);
+                        sig += v;
+                        cr += v * g[5];
+                        cg += v * g[6];
+                        cb += v * g[7];
+                    }
+                    if (sig <= 0.0f) continue;
+                    const float a = 1.0f - expf(-sig * dt);
+                    const float w = T * a / sig;
+                    Cc[0] += w * cr;
+                    Cc[1] += w * cg;
+                    Cc[2] += w * cb;
+                    T *= 1.0f - a;
+                    if (T < 1e-4f) break;
+                }
+            }
+            uint32_t u[3];
+            for (int c = 0; c < 3; ++c) u[c] = (uint32_t)rintf(fminf(1.0f, fmaxf(0.0f, Cc[c] + T)) * 255.0f);
+            const uint32_t ua     = (uint32_t)rintf(fminf(1.0f, fmaxf(0.0f, 1.0f - T)) * 255.0f);
+            rgba[(uint64_t)y * W + x] = (ua << 24) | (u[2] << 16) | (u[1] << 8) | u[0];
+        }
+    }
 }

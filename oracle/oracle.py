@@ -79,9 +79,13 @@ _PROTOS = {
     "orc_pixel_ray": (C.c_int, [C.POINTER(OrcCamera), _U32, _P, _P]),
     "orc_composite_ray": (_U32, [_P, _P, _U32, _F, _P, _P, _P]),
     "orc_composite_backward_ray": (C.c_double, [_P, _P, _P, _U32, _P, _P, _F, _F, _P, _P, _P]),
+    "orc_composite_backward_act": (C.c_double, [_P, _P, _P, _U32, _P, _P, _F, _F, _P, _P, _P]),
     "orc_mlp_backward": (None, [_P, _P, _P, _P, _P, _P, _U32, _F, _P, _P, _P]),
     "orc_encode_backward": (None, [C.POINTER(OrcGrid), _P, _P, _U32, _P]),
     "orc_adam": (C.c_int, [_P, _P, _P, _P, _U64, _F, _F, _F, _F, _F, _F, _F, _U32, _U32, C.c_double, C.c_int]),
+    "orc_train_rays": (None, [C.POINTER(OrcCamera), _P, _P, _U32, _P, _U32, _U32, _U32, _P, _P, _P, _P, _P, _U32]),
+    "orc_train_camera": (_U32, [_U32, _U32]),
+    "orc_scene_render": (None, [_P, _U32, C.POINTER(OrcCamera), _P, _U32, _P]),
     "orc_render_rays": (None, [C.POINTER(OrcModel), C.POINTER(OrcCamera), _P, _U32, _P, _U32, _F, _P, _P, _U32, _P, _P, _P, _U32]),
 }
 
@@ -307,6 +311,21 @@ def composite_backward_ray(sraw, rgbraw, dt, gt, bg=(1.0, 1.0, 1.0), delta=0.1, 
     return float(loss), ds, drgb, pred
 
 
+def composite_backward_act(sigma, rgb, dt, gt, bg=(1.0, 1.0, 1.0), delta=0.1, inv_norm=1.0):
+    """Composite backward from activations (sigma, rgb); gradients wrt raw outputs."""
+    sigma = np.ascontiguousarray(sigma, np.float32)
+    rgb = np.ascontiguousarray(rgb, np.float32).reshape(-1, 3)
+    dt = np.ascontiguousarray(dt, np.float32)
+    gt = np.array(gt, np.float32)
+    b = np.array(bg, np.float32)
+    n = sigma.size
+    ds = np.empty(n, np.float32)
+    drgb = np.empty((n, 3), np.float32)
+    pred = np.empty(3, np.float32)
+    loss = lib().orc_composite_backward_act(_p(sigma), _p(rgb), _p(dt), n, _p(gt), _p(b), delta, inv_norm, _p(ds), _p(drgb), _p(pred))
+    return float(loss), ds, drgb, pred
+
+
 def mlp_backward(dparams_bits, cparams_bits, features, dirs, dsraw, drgbraw, loss_scale):
     features = np.ascontiguousarray(features, np.float32)
     dirs = np.ascontiguousarray(dirs, np.float32)
@@ -333,3 +352,28 @@ def adam(w, m, v, g, lr, b1, b2, eps, clip, guard, loss_scale, decay_ksteps, ste
         assert a.dtype == np.float32 and a.flags["C_CONTIGUOUS"]
     g = np.ascontiguousarray(g, np.float32)
     return lib().orc_adam(_p(w), _p(m), _p(v), _p(g), w.size, lr, b1, b2, eps, clip, guard, loss_scale, decay_ksteps, step, grad_norm, nonfinite)
+
+
+def train_rays(cam: OrcCamera, image: np.ndarray, bits, res: int, aabb, max_steps: int, frame: int, n_rays: int, cap: int):
+    image = np.ascontiguousarray(image, np.uint8)
+    box = np.array(aabb, np.float32)
+    counts = np.empty(n_rays, np.uint32)
+    gt = np.empty((n_rays, 4), np.float32)
+    pix = np.empty((n_rays, 2), np.float32)
+    offs = np.empty(n_rays, np.uint32)
+    tdt = np.zeros((cap, 2), np.float32)
+    lib().orc_train_rays(C.byref(cam), _p(image), _p(bits) if bits is not None else None, res, _p(box), max_steps, frame, n_rays, _p(counts), _p(gt), _p(pix), _p(offs), _p(tdt), cap)
+    return counts, gt, pix, offs, tdt
+
+
+def train_camera(frame: int, image_count: int) -> int:
+    return int(lib().orc_train_camera(frame, image_count))
+
+
+def scene_render(gaussians: np.ndarray, cam: OrcCamera, steps: int, aabb=(0, 0, 0, 1, 1, 1)) -> np.ndarray:
+    """RGBA8 image [H][W] as uint32 words (R in the low byte)."""
+    g = np.ascontiguousarray(gaussians, np.float32)
+    box = np.array(aabb, np.float32)
+    out = np.empty((cam.height, cam.width), np.uint32)
+    lib().orc_scene_render(_p(g), g.shape[0], C.byref(cam), _p(box), steps, _p(out))
+    return out

@@ -1,0 +1,282 @@
+"""GPU training-step parity, stage by stage, against the oracle.
+
+Bars: sample counts, offsets and (t_mid, dt) bit-exact; ground truth within
+1e-6; field outputs, composite gradients and the loss within 1e-3 relative;
+MLP weight gradients and hash-table gradients within 1e-2 relative (Frobenius
+norm; fp16 ReLU masks may flip on a few activations); Adam within 1e-5 on the
+GPU's own gradients.  The dataset is the analytic Gaussian scene rendered by
+nerf_ext_scene_render (itself checked against the oracle to 1 LSB).
+"""
+import numpy as np
+import pytest
+
+from conftest import announce
+from helpers import L, ext, orc, oracle_grid, assert_rel
+
+pytestmark = pytest.mark.gpu
+
+W = H = 64
+VIEWS = 4
+FOCAL = 1111.0 * W / 800.0
+CENTRE = (0.5, 0.5, 0.5)
+BOX = (0.0, 0.0, 0.0, 1.0, 1.0, 1.0)
+OCC_RES = 32
+RAYS = 256
+STEPS = 64
+LOSS_SCALE = 128.0
+
+
+@pytest.fixture(scope="module")
+def dataset():
+    g = ext.scene_gaussians(16, seed=3)
+    cams = [ext.camera_orbit(7, i, 1.32, CENTRE, W, H, FOCAL) for i in range(VIEWS)]
+    imgs = ext.scene_render(g, cams, 128).numpy()
+    return g, cams, imgs
+
+
+def _trainer(dataset, capacity=RAYS * STEPS, rays=RAYS, **kw):
+    _, cams, imgs = dataset
+    grid = ext.grid_desc(14, L.NERF_EXT_F16)
+    occ = ext.occupancy_params(warmup_steps=2, update_interval=4, cells_per_update=OCC_RES ** 3, threshold=0.01, decay=0.95)
+    hyper = ext.hyper_params(loss_scale=LOSS_SCALE)
+    t = ext.Trainer(grid, imgs.view(np.uint8), cams, occupancy_res=OCC_RES, hyper=hyper, occupancy=occ, initial_rays=rays, max_rays=rays, sample_capacity=capacity, max_steps_per_ray=STEPS, seed=5,
+                    table_init_range=1e-1, **kw)
+    return t, grid
+
+
+def _model_host(t):
+    m, _ = t.model()
+    elems = ext.table_elements(m.grid)
+    table = ext.read_device(m.table, (elems,), np.uint16)
+    dp = ext.read_device(m.density_params, (L.NERF_EXT_DENSITY_PARAMS,), np.uint16)
+    cp = ext.read_device(m.color_params, (L.NERF_EXT_COLOR_PARAMS,), np.uint16)
+    return table, dp, cp
+
+
+def _sample_state(t):
+    """Device buffers after the SAMPLE stage, as host arrays."""
+    B = t.buffers()
+    st = t.stats()
+    n = st.samples
+    return dict(
+        stats=st,
+        counts=ext.read_device(B.counts, (RAYS,), np.uint32),
+        kept=ext.read_device(B.kept, (RAYS,), np.uint32),
+        offsets=ext.read_device(B.offsets, (RAYS,), np.uint32),
+        gt=ext.read_device(B.gt, (RAYS, 4), np.float32),
+        rays=ext.read_device(B.rays, (RAYS, 2, 4), np.float32),
+        samples=ext.read_device(B.samples, (n, 2), np.float32),
+        sample_ray=ext.read_device(B.sample_ray, (n,), np.uint32),
+    )
+
+
+def _positions(s):
+    """Normalised sample positions and directions, in the fp32 order the field kernel uses."""
+    r = s["sample_ray"]
+    ro, rd = s["rays"][r, 0], s["rays"][r, 1]
+    t = s["samples"][:, 0:1]
+    w = ro[:, :3] + t * rd[:, :3]
+    box_min, box_max = np.array(BOX[:3], np.float32), np.array(BOX[3:], np.float32)
+    p = ((w - box_min) / (box_max - box_min)).astype(np.float32)
+    return p, np.ascontiguousarray(rd[:, :3])
+
+
+def test_scene_render_matches_oracle(dataset):
+    announce("scene render 4 views 64x64")
+    g, cams, imgs = dataset
+    for v in range(VIEWS):
+        want = orc.scene_render(g, orc.camera_from_bytes(bytes(cams[v])), 128).view(np.uint8).astype(int)
+        got = imgs[v].view(np.uint8).astype(int)
+        diff = np.abs(got - want)
+        assert diff.max() <= 1, f"view {v}: max diff {diff.max()}"
+        assert (diff == 0).mean() > 0.99
+        assert (got[..., 3] > 0).mean() > 0.05, "scene not visible"
+
+
+def test_occupancy_warmup_marks_every_cell(dataset):
+    announce("train occupancy warmup")
+    t, _ = _trainer(dataset)
+    t.run_stages(L.NERF_EXT_STAGE_BEGIN, L.NERF_EXT_STAGE_OCCUPANCY)
+    t.synchronize()
+    B = t.buffers()
+    cells = OCC_RES ** 3
+    assert np.all(ext.read_device(B.density_grid, (cells,), np.float32) == 1.0)
+    assert np.all(ext.read_device(B.bitfield, (cells // 32,), np.uint32) == 0xFFFFFFFF)
+
+
+@pytest.mark.parametrize("capacity", [RAYS * STEPS, 3000])
+def test_sample_stage_bit_exact(dataset, capacity):
+    announce(f"train sample stage capacity={capacity}")
+    _, cams, imgs = dataset
+    t, _ = _trainer(dataset, capacity=capacity)
+    t.run_stages(L.NERF_EXT_STAGE_BEGIN, L.NERF_EXT_STAGE_SAMPLE)
+    s = _sample_state(t)
+    cam = orc.train_camera(0, VIEWS)
+    bits = ext.read_device(t.buffers().bitfield, (OCC_RES ** 3 // 32,), np.uint32)
+    counts, gt, _, offs, tdt = orc.train_rays(orc.camera_from_bytes(bytes(cams[cam])), imgs[cam].view(np.uint8), bits, OCC_RES, BOX, STEPS, 0, RAYS, RAYS * STEPS)
+    assert s["stats"].rays == RAYS
+    assert np.array_equal(s["counts"], counts)
+    assert np.array_equal(s["offsets"], offs)
+    hit = counts > 0
+    np.testing.assert_allclose(s["gt"][hit], gt[hit], rtol=0, atol=1e-6)
+    # Kept rays: the prefix whose samples fit the capacity.
+    fits = hit & (offs.astype(np.int64) + counts <= capacity)
+    assert np.array_equal(s["kept"], np.where(fits, counts, 0))
+    n = int((offs + counts)[fits].max()) if fits.any() else 0
+    assert s["stats"].samples == n
+    assert s["stats"].active_rays == int(fits.sum())
+    assert np.array_equal(s["samples"].view(np.uint32), tdt[:n].view(np.uint32))
+    want_ray = np.repeat(np.arange(RAYS, dtype=np.uint32)[fits], counts[fits])
+    assert np.array_equal(s["sample_ray"], want_ray)
+
+
+def test_forward_stage(dataset):
+    announce("train forward stage")
+    t, grid = _trainer(dataset)
+    t.run_stages(L.NERF_EXT_STAGE_BEGIN, L.NERF_EXT_STAGE_FORWARD)
+    s = _sample_state(t)
+    n = s["stats"].samples
+    B = t.buffers()
+    field = ext.read_device(B.field, (n, 4), np.float32)
+    feats = ext.read_device(B.features, (n, 32), np.float16).astype(np.float32)
+    table, dp, cp = _model_host(t)
+    p, d = _positions(s)
+    og = oracle_grid(grid)
+    want_feat = orc.encode(og, table, p)
+    assert_rel(feats, want_feat, what="training features (fp16)")
+    assert (feats == want_feat.astype(np.float16).astype(np.float32)).mean() > 0.999, "features are not the fp16 rounding of the encoding"
+    want = orc.field_forward(og, table, dp, cp, p, d)
+    assert_rel(field[:, 0], want[:, 0], what="sigma")
+    assert_rel(field[:, 1:], want[:, 1:], what="rgb")
+
+
+def _composite_oracle(s, field, inv_norm):
+    n = s["stats"].samples
+    ds = np.zeros(n, np.float32)
+    drgb = np.zeros((n, 3), np.float32)
+    loss = 0.0
+    for r in np.nonzero(s["kept"])[0]:
+        b, c = int(s["offsets"][r]), int(s["kept"][r])
+        sl = slice(b, b + c)
+        l, d1, d3, _ = orc.composite_backward_act(field[sl, 0], field[sl, 1:], s["samples"][sl, 1], s["gt"][r, :3], delta=0.1, inv_norm=inv_norm)
+        ds[sl], drgb[sl] = d1, d3
+        loss += l
+    return loss * inv_norm, ds, drgb
+
+
+def test_composite_stage(dataset):
+    announce("train composite stage")
+    t, _ = _trainer(dataset)
+    t.run_stages(L.NERF_EXT_STAGE_BEGIN, L.NERF_EXT_STAGE_COMPOSITE)
+    s = _sample_state(t)
+    n = s["stats"].samples
+    B = t.buffers()
+    field = ext.read_device(B.field, (n, 4), np.float32)
+    draw = ext.read_device(B.draw, (n, 4), np.float32)
+    _, ds, drgb = _composite_oracle(s, field, 1.0 / s["stats"].active_rays)
+    assert_rel(draw[:, 0], ds, what="d sigma_raw")
+    assert_rel(draw[:, 1:], drgb, what="d rgb_raw")
+
+
+def _frob(got, want):
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    return float(np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-30))
+
+
+def test_backward_stage(dataset):
+    announce("train backward stage")
+    t, grid = _trainer(dataset)
+    t.run_stages(L.NERF_EXT_STAGE_BEGIN, L.NERF_EXT_STAGE_BACKWARD)
+    s = _sample_state(t)
+    n = s["stats"].samples
+    B = t.buffers()
+    feats = ext.read_device(B.features, (n, 32), np.float16).astype(np.float32)
+    draw = ext.read_device(B.draw, (n, 4), np.float32)
+    mlp_grad = ext.read_device(B.mlp_grad, (10240,), np.float32)
+    table_grad = ext.read_device(B.table_grad, (B.table_elems,), np.float32)
+    _, dp, cp = _model_host(t)
+    p, d = _positions(s)
+    dfeat, dD, dC = orc.mlp_backward(dp, cp, feats, d, draw[:, 0], draw[:, 1:], LOSS_SCALE)
+    assert np.isfinite(mlp_grad).all() and np.isfinite(table_grad).all()
+    for name, got, want in (("density input", mlp_grad[:2048], dD[:2048]), ("density output", mlp_grad[2048:3072], dD[2048:]), ("colour input", mlp_grad[3072:5120], dC[:2048]),
+                            ("colour hidden", mlp_grad[5120:9216], dC[2048:6144]), ("colour output", mlp_grad[9216:], dC[6144:])):
+        err = _frob(got, want)
+        assert err < 1e-2, f"{name} dW: relative Frobenius error {err:.3e}"
+    want_t = orc.encode_backward(oracle_grid(grid), p, dfeat)
+    err = _frob(table_grad, want_t)
+    assert err < 1e-2, f"table gradient: relative Frobenius error {err:.3e}"
+    # Support: every touched entry is touched on both sides.
+    assert np.array_equal(table_grad != 0, want_t != 0) or (np.count_nonzero((table_grad != 0) != (want_t != 0)) < 1e-4 * table_grad.size)
+
+
+def test_adam_stage_and_step_end(dataset):
+    announce("train adam stage")
+    t, _ = _trainer(dataset)
+    t.run_stages(L.NERF_EXT_STAGE_BEGIN, L.NERF_EXT_STAGE_BACKWARD)
+    t.synchronize()
+    B = t.buffers()
+    E = int(B.table_elems)
+    tw = ext.read_device(B.table_f32, (E,), np.float32)
+    tg = ext.read_device(B.table_grad, (E,), np.float32)
+    mw = ext.read_device(B.mlp_f32, (10240,), np.float32)
+    mg = ext.read_device(B.mlp_grad, (10240,), np.float32)
+    s = _sample_state(t)
+    field = ext.read_device(B.field, (s["stats"].samples, 4), np.float32)
+    want_loss, _, _ = _composite_oracle(s, field, 1.0 / s["stats"].active_rays)
+    gn = float(np.sqrt(np.sum(tg.astype(np.float64) ** 2) + np.sum(mg.astype(np.float64) ** 2))) / LOSS_SCALE
+    t.run_stages(L.NERF_EXT_STAGE_ADAM, L.NERF_EXT_STAGE_END)
+    st = t.stats()
+    hp = t.desc.hyper
+    for name, w0, g, ptr, p16, count in (("table", tw, tg, B.table_f32, t.model()[0].table, E), ("mlp", mw, mg, B.mlp_f32, None, 10240)):
+        w, m, v = w0.copy(), np.zeros_like(w0), np.zeros_like(w0)
+        skipped = orc.adam(w, m, v, g, hp.learning_rate, hp.adam_beta1, hp.adam_beta2, hp.adam_eps, hp.grad_clip_norm, hp.update_guard_grad_norm, LOSS_SCALE, hp.lr_decay_ksteps, 1, gn)
+        assert skipped == 0
+        got = ext.read_device(ptr, (count,), np.float32)
+        np.testing.assert_allclose(got - w0, w - w0, rtol=1e-5, atol=1e-8, err_msg=f"{name} Adam update")
+        if p16 is not None:
+            assert np.array_equal(ext.read_device(p16, (count,), np.float16), got.astype(np.float16)), "fp16 working copy != RNE(master)"
+    assert not ext.read_device(B.table_grad, (E,), np.float32).any(), "table gradient not consumed"
+    assert not ext.read_device(B.mlp_grad, (10240,), np.float32).any(), "MLP gradient not consumed"
+    assert st.last.completed_steps == 1
+    assert st.last.last_train_camera == orc.train_camera(0, VIEWS)
+    assert st.last.has_nonfinite == 0
+    assert abs(st.last.loss - want_loss) <= 1e-3 * want_loss
+    assert abs(st.last.grad_norm - gn) <= 1e-4 * gn
+
+
+def test_occupancy_refresh(dataset):
+    announce("train occupancy refresh at step 4")
+    t, grid = _trainer(dataset)
+    t.step(4)
+    t.synchronize()
+    table, dp, _ = _model_host(t)
+    B = t.buffers()
+    cells = OCC_RES ** 3
+    before = ext.read_device(B.density_grid, (cells,), np.float32)
+    t.run_stages(L.NERF_EXT_STAGE_BEGIN, L.NERF_EXT_STAGE_OCCUPANCY)
+    t.synchronize()
+    got = ext.read_device(B.density_grid, (cells,), np.float32)
+    bits = ext.read_device(B.bitfield, (cells // 32,), np.uint32)
+    idx = np.arange(cells)
+    x, y, z = idx % OCC_RES, (idx // OCC_RES) % OCC_RES, idx // (OCC_RES * OCC_RES)
+    step = np.float32(1.0 / OCC_RES)
+    centres = np.stack([(x + 0.5) * step, (y + 0.5) * step, (z + 0.5) * step], 1).astype(np.float32)
+    sigma = orc.density_forward(oracle_grid(grid), table, dp, centres)[:, 0]
+    want = np.maximum(before * np.float32(0.95), sigma)
+    assert_rel(got, want, what="density grid after refresh")
+    occ = got > 0.01
+    want_bits = np.packbits(occ.reshape(-1, 32)[:, ::-1], axis=1).view(">u4").ravel().astype(np.uint32)
+    assert np.array_equal(bits, want_bits), "bitfield != density > threshold"
+
+
+def test_training_reduces_loss(dataset):
+    announce("train 300 steps")
+    t, _ = _trainer(dataset, rays=RAYS)
+    losses = []
+    for _ in range(30):
+        t.step(10)
+        st = t.stats()
+        assert st.last.has_nonfinite == 0
+        losses.append(st.last.loss)
+    assert st.last.completed_steps == 300
+    assert np.mean(losses[-5:]) < 0.5 * np.mean(losses[:2]), losses
