@@ -18,7 +18,15 @@ kernel (the fused field kernel, HBM-bound by its algorithmic bytes) timed with
 HIP events on the render stream, and the scalar CPU oracle timed on a bounded
 ray subset of the same view on the host cores.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+Training (reported in the same line as "train"): 100 800x800 target views of
+the same scene rendered on the GPU from seeded poses on the same orbit; each
+step marches a batch whose ray count adapts to 2^18 samples (hard cap 2^18),
+Huber loss, full backward through composite, MLPs and hash grid, Adam (lr
+1e-2, betas 0.9/0.99, eps 1e-15, loss scale 128), occupancy refresh every 16
+steps with decay 0.95.  Train samples/s = samples trained on in the timed
+steps / wall time of those steps.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--train-steps K2]
 """
 from __future__ import annotations
 
@@ -42,6 +50,7 @@ MAX_STEPS = 1024
 T_STOP = 1e-4
 CENTRE = (0.5, 0.5, 0.5)
 RADIUS = 1.32
+TRAIN_W = TRAIN_H = 800
 # Algorithmic bytes of the fused field kernel per sample: sample record
 # (t_mid, dt, ray id) 12 B + 16 levels x 8 corners x 2 fp16 features 512 B +
 # (sigma, r, g, b) fp32 16 B.
@@ -58,9 +67,48 @@ def build_workload():
     bits = ext.occupancy_from_scene(scene, 128, threshold=0.01)
     desc = ext.grid_desc(19, L.NERF_EXT_F16)
     model = ext.Model.create(desc, seed=0)
-    cam = ext.camera_orbit(0, 0, RADIUS, CENTRE, W, H, FOCAL)
+    cam = ext.camera_orbit(0, 0, RADIUS, CENTRE, W, H, FOCAL * W / 800.0)  # field of view of the 800-px view
     occ = ext.occupancy_struct(bits, 128)
     return scene, bits, desc, model, cam, occ
+
+
+def train_bench(steps: int, warmup: int, views: int = 100):
+    """Training throughput on the analytic scene (2^18-sample batches)."""
+    from nerf_amd import _lib as L, ext
+    from nerf_amd.device import Event
+
+    scene = ext.scene_gaussians(32, seed=0)
+    cams = [ext.camera_orbit(1, i, RADIUS, CENTRE, TRAIN_W, TRAIN_H, FOCAL) for i in range(views)]
+    images = ext.scene_render(scene, cams, 512).numpy()
+    desc = ext.grid_desc(19, L.NERF_EXT_F16)
+    hyper = ext.hyper_params(lr=1e-2, beta1=0.9, beta2=0.99, eps=1e-15, loss_scale=128.0)
+    occ = ext.occupancy_params(decay=0.95, threshold=0.01, cells_per_update=128 ** 3, update_interval=16, warmup_steps=16)
+    batch = 1 << 18
+    tr = ext.Trainer(desc, images.view(np.uint8), cams, occupancy_res=128, hyper=hyper, occupancy=occ, initial_rays=4096, max_rays=batch, target_samples=batch, sample_capacity=batch,
+                     max_steps_per_ray=MAX_STEPS, seed=0)
+    del images
+
+    class _On:
+        handle = tr.stream()
+
+    tr.step(warmup)
+    s0 = tr.stats()
+    ev0, ev1 = Event(), Event()
+    t0 = time.perf_counter()
+    ev0.record(_On)
+    tr.step(steps)
+    ev1.record(_On)
+    s1 = tr.stats()  # synchronises the trainer's stream
+    wall = time.perf_counter() - t0
+    gpu_ms = ev0.elapsed_ms(ev1)
+    samples = s1.samples_total - s0.samples_total
+    out = {"samples_per_s": round(samples / wall, 1), "unit": "train samples/s", "steps": steps, "warmup": warmup, "ms_per_step": round(wall * 1e3 / steps, 4),
+           "gpu_ms_per_step": round(gpu_ms / steps, 4), "mean_samples_per_step": round(samples / steps, 1), "rays_last_step": s1.rays, "loss_first_timed": None,
+           "loss_last": round(float(s1.last.loss), 6), "nonfinite": int(s1.last.has_nonfinite), "batch_target": batch, "views": views,
+           "workload": f"{views} 800x800 views, 32-Gaussian scene, hash grid T=2^19 fp16, 128^3 occupancy, 2^18-sample batches, <=1024 steps/ray"}
+    out["loss_first_timed"] = round(float(s0.last.loss), 6)
+    tr.close()
+    return out
 
 
 def cpu_baseline(desc, model, cam, bits, budget_s: float = 15.0):
@@ -89,18 +137,24 @@ def cpu_baseline(desc, model, cam, bits, budget_s: float = 15.0):
     orc.render_rays(g, table, dp, cp, ocam, b, 128, (0, 0, 0, 1, 1, 1), MAX_STEPS, rays, T_STOP, threads=threads)
     dt = time.perf_counter() - t0
     return {"value": rays.size / dt / 1e6, "unit": "Mrays/s", "cores": threads, "kind": "port",
-            "sample": f"{rays.size} rays (every {stride}th ray of the 800x800 view, full march+field+composite per ray), {dt:.1f} s"}
+            "sample": f"{rays.size} rays (every {stride}th ray of the {W}x{H} view, full march+field+composite per ray), {dt:.1f} s"}
 
 
 def main() -> int:
+    global W, H
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--train-steps", type=int, default=100, help="timed training steps (0: skip the training leg)")
+    ap.add_argument("--train-warmup", type=int, default=30)
+    ap.add_argument("--width", type=int, default=W, help="render width (the metric is quoted at 800)")
+    ap.add_argument("--height", type=int, default=H, help="render height (the metric is quoted at 800)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain fp32->fp16 conversion over MIB MiB of input (reads 4 B, writes 2 B per element) to calibrate HBM counters, then exit")
     args = ap.parse_args()
+    W, H = args.width, args.height
     if args.gpus != 1:
         print(f"bench.py: this backend runs on one GPU; --gpus {args.gpus} is not supported (multi-GPU sharding is design-only)", file=sys.stderr)
         return 2
@@ -171,7 +225,7 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "f16 MFMA (fp32 accumulate), f32 march/composite",
         "data": "synthetic: analytic 32-Gaussian scene, random-init hash grid and MLPs",
-        "config": {"workload": "800x800 inference render, 32-Gaussian scene, 128^3 occupancy, hash grid T=2^19 fp16, <=1024 steps/ray, early stop T<1e-4",
+        "config": {"workload": f"{W}x{H} inference render, 32-Gaussian scene, 128^3 occupancy, hash grid T=2^19 fp16, <=1024 steps/ray, early stop T<1e-4",
                    "rays": rays, "samples_per_render": int(samples), "gpu_ms_per_render": round(gpu_ms, 4), "parallelism": "single GPU"},
         "stages_ms": {k: round(v, 4) for k, v in stage.items()},
         "roofline": {"kernel": "k_field_forward (fused hash encode + density/colour MLP)", "bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -179,6 +233,8 @@ def main() -> int:
                      "bytes_per_sample": FIELD_BYTES_PER_SAMPLE, "flops_per_sample": FIELD_FLOPS_PER_SAMPLE},
         "device": {"name": info.name.decode(), "arch": info.arch.decode(), "cus": info.compute_units},
     }
+    if args.train_steps > 0:
+        line["train"] = train_bench(args.train_steps, args.train_warmup)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(desc, model, cam, bits)
     print(json.dumps(line), flush=True)

@@ -255,6 +255,7 @@ typedef struct NerfExtTrainStats {
     uint32_t active_rays;
     uint32_t skipped;                /* Adam update skipped */
     uint64_t occupied_samples;       /* before the capacity cut */
+    uint64_t samples_total;          /* samples trained on since creation or the last reset */
 } NerfExtTrainStats;
 
 /* Device buffers of a trainer, for inspection (read-only use by callers). */

@@ -270,6 +270,7 @@ class NerfExtTrainStats(C.Structure):
         ("active_rays", C.c_uint32),
         ("skipped", C.c_uint32),
         ("occupied_samples", C.c_uint64),
+        ("samples_total", C.c_uint64),
     ]
 
 

@@ -21,6 +21,7 @@ struct TrainDevState {
     uint32_t nonfinite;   // gradient contains inf/nan
     uint32_t skip;        // Adam update skipped
     unsigned long long total;  // occupied samples before the capacity cut
+    unsigned long long samples_done;  // samples trained on since the last reset
     double grad_sumsq;    // sum of squared (loss-scaled) gradients
     float loss_sum;       // sum of per-ray Huber losses
     float rays_f;         // adaptive ray count

@@ -94,6 +94,7 @@ __global__ void k_step_end(TrainParams P, TrainDevState* S) {
     S->stats.has_nonfinite     = (S->nonfinite || !isfinite(loss) || !isfinite(gn)) ? 1u : 0u;
     S->stats.completed_steps   = S->frame + 1u;
     S->stats.last_train_camera = S->camera;
+    S->samples_done            = S->samples_done + S->n_samples;
     if (P.target_samples != 0u && S->n_samples > 0u) {
         // Aim the next batch at target_samples (exponentially smoothed).
         const float want = S->rays_f * (float)P.target_samples / (float)S->n_samples;

@@ -254,6 +254,7 @@ NERF_API NerfStatus nerf_ext_trainer_stats(NerfExtTrainer* trainer, NerfExtTrain
     out->active_rays      = s.n_active;
     out->skipped          = s.skip;
     out->occupied_samples = s.total;
+    out->samples_total    = s.samples_done;
     return NERF_STATUS_OK;
 }
 

@@ -85,8 +85,8 @@ def test_scene_render_matches_oracle(dataset):
     announce("scene render 4 views 64x64")
     g, cams, imgs = dataset
     for v in range(VIEWS):
-        want = orc.scene_render(g, orc.camera_from_bytes(bytes(cams[v])), 128).view(np.uint8).astype(int)
-        got = imgs[v].view(np.uint8).astype(int)
+        want = orc.scene_render(g, orc.camera_from_bytes(bytes(cams[v])), 128).view(np.uint8).reshape(H, W, 4).astype(int)
+        got = imgs[v].view(np.uint8).reshape(H, W, 4).astype(int)
         diff = np.abs(got - want)
         assert diff.max() <= 1, f"view {v}: max diff {diff.max()}"
         assert (diff == 0).mean() > 0.99
