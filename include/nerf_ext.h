@@ -77,7 +77,7 @@ NERF_API NerfStatus nerf_ext_event_elapsed_ms(void* start, void* stop, float* ou
 typedef struct NerfExtGridDesc {
     uint32_t n_levels;          /* L, at most 16 */
     uint32_t n_features;        /* F, must be 2 */
-    uint32_t log2_table_size;   /* log2 T, 1..24 */
+    uint32_t log2_table_size;   /* log2 T, 2..24 */
     uint32_t base_resolution;   /* N_min >= 1 */
     float per_level_scale;      /* b, used when finest_resolution == 0 */
     uint32_t finest_resolution; /* optional N_max */

@@ -114,6 +114,31 @@ __device__ __forceinline__ float corner_weight(const LevelCell& c, uint32_t corn
     return (wx * wy) * wz;
 }
 
+// Hash encoding of one level of one point: features (a0, a1) as fp32.
+// Corner order, weights and accumulation order are those of the oracle.
+template <typename TableT>
+__device__ __forceinline__ void encode_level(const GridParams& g, const TableT* __restrict__ table, const float p[3], uint32_t level, uint32_t N, bool dense, float& a0, float& a1) {
+    const LevelCell c  = level_cell(p, N);
+    const TableT* base = table + (uint64_t)level * g.table_size * 2u;
+    uint32_t idx[8];
+#pragma unroll
+    for (uint32_t k = 0; k < 8u; ++k) idx[k] = corner_index(c, k, N, dense, g.table_size - 1u);
+    float v0[8], v1[8];
+#pragma unroll
+    for (uint32_t k = 0; k < 8u; ++k) {
+        v0[k] = (float)base[2u * idx[k]];
+        v1[k] = (float)base[2u * idx[k] + 1u];
+    }
+    a0 = 0.0f;
+    a1 = 0.0f;
+#pragma unroll
+    for (uint32_t k = 0; k < 8u; ++k) {
+        const float w = corner_weight(c, k);
+        a0            = a0 + w * v0[k];
+        a1            = a1 + w * v1[k];
+    }
+}
+
 // --------------------------------------------------------------- cameras
 struct Ray {
     float o[3];

@@ -37,6 +37,44 @@ __device__ __forceinline__ void stage_params(half_t* lds, const half_t* src, uin
     __syncthreads();
 }
 
+// Position (normalised by the AABB) and direction of march sample q.
+__device__ __forceinline__ void sample_point(const FieldInputs& in, uint32_t q, float p[3], float d[3]) {
+    const float2 td  = in.samples[q];
+    const uint32_t r = in.sample_ray[q];
+    const float4 ro  = in.rays[2ull * r];
+    const float4 rd  = in.rays[2ull * r + 1ull];
+    d[0]             = rd.x;
+    d[1]             = rd.y;
+    d[2]             = rd.z;
+    const float w[3] = {ro.x + td.x * rd.x, ro.y + td.x * rd.y, ro.z + td.x * rd.z};
+#pragma unroll
+    for (int a = 0; a < 3; ++a) p[a] = (w[a] - in.bmin[a]) / (in.bmax[a] - in.bmin[a]);
+}
+
+// Colour input of lane group grp from density outputs 4g..4g+3 and SH
+// coefficients 4g..4g+3; the slot of density output 0 (sigma) carries a zero
+// weight and a zero value.
+__device__ __forceinline__ half8_t color_input(const floatx4 o, const float d[3], uint32_t grp) {
+    float sh[4];
+    sh4_quad(d, grp, sh);
+    half8_t xc;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        xc[e]     = (half_t)o[e];
+        xc[4 + e] = (half_t)sh[e];
+    }
+    if (grp == 0u) xc[0] = (half_t)0.0f;
+    return xc;
+}
+
+__device__ __forceinline__ float4 field_output(const floatx4 o, const floatx4 c) {
+    const float sigma = expf(o[0]);
+    const float r     = 1.0f / (1.0f + expf(-c[0]));
+    const float gg    = 1.0f / (1.0f + expf(-c[1]));
+    const float b     = 1.0f / (1.0f + expf(-c[2]));
+    return make_float4(sigma, r, gg, b);
+}
+
 // ---------------------------------------------------------------- kernels
 // Density MLP on fp16 features [n][32] -> raw outputs [n][16].
 __global__ __launch_bounds__(kBlockThreads) void k_density_mlp(const half_t* __restrict__ params, const half_t* __restrict__ features, uint32_t n, float* __restrict__ out) {
@@ -104,16 +142,7 @@ __global__ __launch_bounds__(kBlockThreads) void k_field_forward(GridParams g, c
         const uint32_t q = s < n ? s : n - 1u;
         float p[3], d[3];
         if constexpr (kFromSamples) {
-            const float2 td  = in.samples[q];
-            const uint32_t r = in.sample_ray[q];
-            const float4 ro  = in.rays[2ull * r];
-            const float4 rd  = in.rays[2ull * r + 1ull];
-            d[0]             = rd.x;
-            d[1]             = rd.y;
-            d[2]             = rd.z;
-            const float w[3] = {ro.x + td.x * rd.x, ro.y + td.x * rd.y, ro.z + td.x * rd.z};
-#pragma unroll
-            for (int a = 0; a < 3; ++a) p[a] = (w[a] - in.bmin[a]) / (in.bmax[a] - in.bmin[a]);
+            sample_point(in, q, p, d);
         } else {
 #pragma unroll
             for (int a = 0; a < 3; ++a) {
@@ -126,25 +155,8 @@ __global__ __launch_bounds__(kBlockThreads) void k_field_forward(GridParams g, c
         const half8_t x = to_half8(feat);
         if (in.features_out && s < n) *reinterpret_cast<half8_t*>(in.features_out + (uint64_t)s * 32u + 8u * grp) = x;
         const floatx4 o = density_mlp(fd, x);
-        // Colour input: (density outputs 4g..4g+3, SH 4g..4g+3); the slot of
-        // density output 0 (sigma) carries a zero weight and a zero value.
-        float sh[4];
-        sh4_quad(d, grp, sh);
-        half8_t xc;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            xc[e]     = (half_t)o[e];
-            xc[4 + e] = (half_t)sh[e];
-        }
-        if (grp == 0u) xc[0] = (half_t)0.0f;
-        const floatx4 c = color_mlp(fc, xc);
-        if (grp == 0u && s < n) {
-            const float sigma = expf(o[0]);
-            const float r     = 1.0f / (1.0f + expf(-c[0]));
-            const float gg    = 1.0f / (1.0f + expf(-c[1]));
-            const float b     = 1.0f / (1.0f + expf(-c[2]));
-            out[s]            = make_float4(sigma, r, gg, b);
-        }
+        const floatx4 c = color_mlp(fc, color_input(o, d, grp));
+        if (grp == 0u && s < n) out[s] = field_output(o, c);
     }
 }
 
@@ -159,7 +171,7 @@ uint32_t persistent_blocks(uint32_t n, uint32_t per_cu) {
 
 hipError_t launch_field(const GridParams& g, const void* table, const FieldWeights& w, const FieldInputs& in, uint32_t n, float4* out4, hipStream_t stream) {
     if (n == 0u) return hipSuccess;
-    const uint32_t blocks = persistent_blocks(n, 8u);
+    const uint32_t blocks   = persistent_blocks(n, 8u);
     const bool from_samples = in.samples != nullptr;
     if (g.table_dtype == NERF_EXT_F32) {
         if (from_samples)

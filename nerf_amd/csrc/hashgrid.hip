@@ -18,7 +18,7 @@ NerfStatus make_grid(const NerfExtGridDesc* d, GridParams& g) {
     NERF_CHECK_ARG(d, "grid descriptor is null");
     NERF_CHECK_ARG(d->n_levels >= 1u && d->n_levels <= NERF_EXT_MAX_LEVELS, "grid: n_levels must be 1..16");
     NERF_CHECK_ARG(d->n_features == 2u, "grid: n_features must be 2");
-    NERF_CHECK_ARG(d->log2_table_size >= 1u && d->log2_table_size <= 24u, "grid: log2_table_size must be 1..24");
+    NERF_CHECK_ARG(d->log2_table_size >= 2u && d->log2_table_size <= 24u, "grid: log2_table_size must be 2..24");
     NERF_CHECK_ARG(d->base_resolution >= 1u, "grid: base_resolution must be >= 1");
     NERF_CHECK_ARG(d->table_dtype == NERF_EXT_F32 || d->table_dtype == NERF_EXT_F16, "grid: table_dtype must be F32 or F16");
     double b = (double)d->per_level_scale;
@@ -66,25 +66,8 @@ __global__ __launch_bounds__(256) void k_encode_forward(GridParams g, const Tabl
     const float p[3]      = {pos[3ull * i], pos[3ull * i + 1], pos[3ull * i + 2]};
     const uint32_t N      = g.resolution[level];
     const bool dense      = g.dense[level] != 0u;
-    const uint32_t mask   = g.table_size - 1u;
-    const LevelCell c     = level_cell(p, N);
-    const TableT* base    = table + (uint64_t)level * g.table_size * 2u;
-    uint32_t idx[8];
-#pragma unroll
-    for (uint32_t k = 0; k < 8u; ++k) idx[k] = corner_index(c, k, N, dense, mask);
-    float v0[8], v1[8];
-#pragma unroll
-    for (uint32_t k = 0; k < 8u; ++k) {
-        v0[k] = (float)base[2u * idx[k]];
-        v1[k] = (float)base[2u * idx[k] + 1u];
-    }
-    float a0 = 0.0f, a1 = 0.0f;
-#pragma unroll
-    for (uint32_t k = 0; k < 8u; ++k) {
-        const float w = corner_weight(c, k);
-        a0            = a0 + w * v0[k];
-        a1            = a1 + w * v1[k];
-    }
+    float a0, a1;
+    encode_level(g, table, p, level, N, dense, a0, a1);
     OutT* o = out + (uint64_t)i * (g.n_levels * 2u) + level * 2u;
     store_value(o, a0);
     store_value(o + 1, a1);

@@ -120,10 +120,8 @@ __device__ __forceinline__ floatx4 color_mlp(const ColorFrags& f, const half8_t 
 }
 
 // Hash encoding of levels 4g..4g+3 of one point: features 8g..8g+7 as fp32.
-// Corner order, weights and accumulation order are those of the oracle.
 template <typename TableT>
 __device__ __forceinline__ void encode_quad(const GridParams& g, const TableT* __restrict__ table, const float p[3], uint32_t grp, float feat[8]) {
-    const uint32_t mask = g.table_size - 1u;
 #pragma unroll
     for (uint32_t j = 0; j < 4u; ++j) {
         // Level 4*grp + j, selected without dynamic indexing of the kernel argument.
@@ -132,25 +130,7 @@ __device__ __forceinline__ void encode_quad(const GridParams& g, const TableT* _
         const uint32_t dn = grp == 0u ? g.dense[l0] : grp == 1u ? g.dense[l1] : grp == 2u ? g.dense[l2] : g.dense[l3];
         const uint32_t level = 4u * grp + j;
         float a0 = 0.0f, a1 = 0.0f;
-        if (level < g.n_levels) {
-            const LevelCell c  = level_cell(p, N);
-            const TableT* base = table + (uint64_t)level * g.table_size * 2u;
-            uint32_t idx[8];
-#pragma unroll
-            for (uint32_t k = 0; k < 8u; ++k) idx[k] = corner_index(c, k, N, dn != 0u, mask);
-            float v0[8], v1[8];
-#pragma unroll
-            for (uint32_t k = 0; k < 8u; ++k) {
-                v0[k] = (float)base[2u * idx[k]];
-                v1[k] = (float)base[2u * idx[k] + 1u];
-            }
-#pragma unroll
-            for (uint32_t k = 0; k < 8u; ++k) {
-                const float w = corner_weight(c, k);
-                a0            = a0 + w * v0[k];
-                a1            = a1 + w * v1[k];
-            }
-        }
+        if (level < g.n_levels) encode_level(g, table, p, level, N, dn != 0u, a0, a1);
         feat[2u * j]      = a0;
         feat[2u * j + 1u] = a1;
     }

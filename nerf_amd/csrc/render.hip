@@ -6,11 +6,14 @@
 //                      :373-408, :561-563), occupancy march (:448-469),
 //                      per-ray occupied-step count; ray record (o, tn, d, tf).
 //   2. scan            exclusive prefix sum of counts -> sample offsets.
-//   3. k_march_samples re-marches from the stored ray record and writes the
-//                      compacted stream (t_mid, dt) + owning ray, ray-major.
+//   3. k_march_samples eight lanes per ray: re-marches from the stored ray
+//                      record 8 steps at a time and writes the compacted
+//                      stream (t_mid, dt) + owning ray, ray-major, in
+//                      contiguous segments.
 //   4. field           fused hash encode + MFMA MLPs -> (sigma, r, g, b).
-//   5. k_composite     per ray, front to back (:601-635) with early stop at
-//                      T < min_transmittance, background C + T * bg, RGBA8.
+//   5. k_composite     one wave per ray, front to back (:601-635) over groups
+//                      of 64 samples with early stop at T < min_transmittance,
+//                      background C + T * bg, RGBA8.
 // The reference instead samples spp uniform steps per ray with no occupancy
 // test and no early stop (:534-600) and writes 28 B per step whether or not
 // the step is occupied.
@@ -18,6 +21,7 @@
 #include <vector>
 
 #include "common.hpp"
+#include "wave.hpp"
 
 namespace nerf_hip {
 
@@ -89,45 +93,68 @@ __global__ __launch_bounds__(256) void k_march_count(const NerfExtCamera* __rest
     counts[ray]           = count;
 }
 
+// Eight rays per wave, eight lanes per ray (wave::march<8>): the step
+// sequence is bit-identical to the count pass and the occupied steps of each
+// run of 8 are written contiguously, so samples leave in 64-byte segments
+// instead of one 8-byte store per ray and step; k < count keeps every write
+// inside the ray's slice.
+constexpr uint32_t kMarchGroup = 8u;
+
 __global__ __launch_bounds__(256) void k_march_samples(const NerfExtCamera* __restrict__ cams, uint32_t pixels_per_view, uint32_t n_rays, OccView occ, uint32_t max_steps, const float4* __restrict__ rays, const uint32_t* __restrict__ counts,
     const uint32_t* __restrict__ offsets, float2* __restrict__ samples, uint32_t* __restrict__ sample_ray) {
-    const uint32_t ray = blockIdx.x * 256u + threadIdx.x;
+    const uint32_t ray = (blockIdx.x * 256u + threadIdx.x) / kMarchGroup;
     if (ray >= n_rays) return;
     const uint32_t count = counts[ray];
     if (count == 0u) return;
     const uint32_t view = ray / pixels_per_view;
     const float cone    = cone_angle(cams[view]);
     const uint32_t base = offsets[ray];
-    // The re-march is the same scalar sequence as the count pass, so it emits
-    // exactly `count` samples; the k < count test keeps every write inside
-    // this ray's slice regardless.
-    march_ray(rays[2ull * ray], rays[2ull * ray + 1u], cone, max_steps, occ, [&](uint32_t k, float tm, float dt) {
-        if (k < count) {
-            samples[base + k]    = make_float2(tm, dt);
-            sample_ray[base + k] = ray;
-        }
+    wave::march<kMarchGroup>(rays[2ull * ray], rays[2ull * ray + 1u], cone, max_steps, count, [&](const float p[3]) { return occupied(occ, p); }, [&](uint32_t k, float tm, float dt) {
+        samples[base + k]    = make_float2(tm, dt);
+        sample_ray[base + k] = ray;
     });
 }
 
-// Front-to-back composite with early stop (reference :601-635 plus the stop).
+// Front-to-back composite with early stop (reference :601-635 plus the
+// stop), one wave per ray over groups of 64 samples: transmittance before
+// each sample is the carried T times the exclusive product of (1 - alpha)
+// across the group; the first sample after which T falls below t_stop is the
+// last one composited.
 __global__ __launch_bounds__(256) void k_composite(uint32_t n_rays, const uint32_t* __restrict__ counts, const uint32_t* __restrict__ offsets, const float2* __restrict__ samples, const float4* __restrict__ field, float t_stop, float3 bg,
     uint32_t* __restrict__ rgba8, float* __restrict__ rgb_out) {
-    const uint32_t ray = blockIdx.x * 256u + threadIdx.x;
+    const uint32_t ray  = blockIdx.x * 4u + (threadIdx.x >> 6);
+    const uint32_t lane = threadIdx.x & 63u;
     if (ray >= n_rays) return;
     const uint32_t count = counts[ray];
     const uint32_t base  = count ? offsets[ray] : 0u;
     float T = 1.0f, cr = 0.0f, cg = 0.0f, cb = 0.0f;
-    for (uint32_t i = 0; i < count; ++i) {
-        const float4 f = field[base + i];
-        const float dt = fmaxf(samples[base + i].y, 0.0f);
-        const float a  = 1.0f - __expf(-(f.x * dt));
-        const float w  = T * a;
+    for (uint32_t c0 = 0; c0 < count; c0 += 64u) {
+        const uint32_t i = c0 + lane;
+        const bool valid = i < count;
+        float4 f         = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        float dt         = 0.0f;
+        if (valid) {
+            f  = field[base + i];
+            dt = fmaxf(samples[base + i].y, 0.0f);
+        }
+        const float a     = valid ? 1.0f - __expf(-(f.x * dt)) : 0.0f;
+        const float incl  = wave::inclusive_product(1.0f - a);
+        float excl        = __shfl_up(incl, 1, 64);
+        excl              = lane == 0u ? 1.0f : excl;
+        const float Ti    = T * excl;
+        const uint64_t st = __ballot(valid && T * incl < t_stop);
+        const uint32_t last = st ? (uint32_t)__ffsll((long long)st) - 1u : 63u;
+        const float w     = lane <= last ? Ti * a : 0.0f;
         cr += w * f.y;
         cg += w * f.z;
         cb += w * f.w;
-        T *= 1.0f - a;
-        if (T < t_stop) break;
+        T *= wave::broadcast(incl, last);
+        if (st) break;
     }
+    cr = wave::sum(cr);
+    cg = wave::sum(cg);
+    cb = wave::sum(cb);
+    if (lane != 0u) return;
     const float r = cr + T * bg.x, g = cg + T * bg.y, b = cb + T * bg.z;
     if (rgb_out) {
         rgb_out[3ull * ray]      = r;
@@ -387,7 +414,8 @@ NERF_API NerfStatus nerf_ext_render(NerfExtRenderer* R, const NerfExtRenderDesc*
     NERF_HIP_TRY(R->field.reserve(n_samples));
 
     if (timed) NERF_HIP_TRY(hipEventRecord(R->ev[3], st));
-    k_march_samples<<<blocks, 256, 0, st>>>(R->cams.ptr, ppv, n_rays, occ, d->max_steps, R->rays.ptr, R->counts.ptr, R->offsets.ptr, R->samples.ptr, R->sample_ray.ptr);
+    const uint32_t wave_blocks = (n_rays + 3u) / 4u;  // one wave per ray
+    k_march_samples<<<(n_rays + 256u / kMarchGroup - 1u) / (256u / kMarchGroup), 256, 0, st>>>(R->cams.ptr, ppv, n_rays, occ, d->max_steps, R->rays.ptr, R->counts.ptr, R->offsets.ptr, R->samples.ptr, R->sample_ray.ptr);
     NERF_LAUNCH_CHECK("k_march_samples");
     if (timed) NERF_HIP_TRY(hipEventRecord(R->ev[4], st));
     FieldInputs in{};
@@ -401,7 +429,7 @@ NERF_API NerfStatus nerf_ext_render(NerfExtRenderer* R, const NerfExtRenderDesc*
     const FieldWeights w{(const half_t*)d->model->density_params, (const half_t*)d->model->color_params};
     NERF_HIP_TRY(launch_field(g, d->model->table, w, in, n_samples, R->field.ptr, st));
     if (timed) NERF_HIP_TRY(hipEventRecord(R->ev[5], st));
-    k_composite<<<blocks, 256, 0, st>>>(n_rays, R->counts.ptr, R->offsets.ptr, R->samples.ptr, R->field.ptr, d->min_transmittance, make_float3(d->background[0], d->background[1], d->background[2]), rgba8, rgb_f32);
+    k_composite<<<wave_blocks, 256, 0, st>>>(n_rays, R->counts.ptr, R->offsets.ptr, R->samples.ptr, R->field.ptr, d->min_transmittance, make_float3(d->background[0], d->background[1], d->background[2]), rgba8, rgb_f32);
     NERF_LAUNCH_CHECK("k_composite");
     if (counts_out) NERF_HIP_TRY(hipMemcpyAsync(counts_out, R->counts.ptr, sizeof(uint32_t) * n_rays, hipMemcpyDeviceToDevice, st));
     if (timed) {

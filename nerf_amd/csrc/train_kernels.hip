@@ -21,6 +21,7 @@
 // reduction axis through a per-wave LDS transpose, with deterministic
 // per-workgroup partials.
 #include "mlp_device.hpp"
+#include "wave.hpp"
 #include "train.hpp"
 
 namespace nerf_hip {
@@ -172,168 +173,167 @@ __device__ __forceinline__ bool occupied_at(const TrainParams& P, const uint32_t
     return (bits[idx >> 5] >> (idx & 31u)) & 1u;
 }
 
-template <typename Emit>
-__device__ __forceinline__ uint32_t march_train(const TrainParams& P, const uint32_t* bits, float4 ro, float4 rd, float cone, Emit emit) {
-    const float tn = ro.w, tf = rd.w, t_range = tf - tn;
-    if (!(t_range > 0.0f)) return 0u;
-    const float dt_min = t_range / (float)P.max_steps;
-    uint32_t count = 0u, i = 0u;
-    float t = tn;
-    while (t < tf && i < P.max_steps) {  // :457-469
-        const float dt   = fminf(fmaxf(dt_min, t * cone), tf - t);
-        const float tm   = t + 0.5f * dt;
-        const float p[3] = {ro.x + tm * rd.x, ro.y + tm * rd.y, ro.z + tm * rd.z};
-        if (occupied_at(P, bits, p)) {
-            emit(count, tm, dt);
-            ++count;
-        }
-        t += dt;
-        ++i;
-    }
-    return count;
-}
-
 __device__ __forceinline__ float cone_of(const NerfExtCamera& c) {  // :333-337
     const float ifx = c.fx > 0.0f ? 1.0f / c.fx : 0.0f, ify = c.fy > 0.0f ? 1.0f / c.fy : 0.0f;
     return 0.5f * (ifx + ify);
 }
 
 // Random pixel per ray (:438-441), ray, march count, bilinear ground truth
-// composited over white (:471-499).
+// composited over white (:471-499).  One wave per ray (wave::march<64>); ray
+// slots from n_rays to max_rays get a zero count so the scan over all slots
+// stays valid.
 __global__ __launch_bounds__(256) void k_train_rays(TrainParams P, const TrainDevState* S, const NerfExtCamera* __restrict__ cams, const uint8_t* __restrict__ images, const uint32_t* __restrict__ bits, float4* __restrict__ rays, float4* __restrict__ gt,
                                                      uint32_t* __restrict__ counts) {
-    const uint32_t r = blockIdx.x * 256u + threadIdx.x;
-    if (r >= P.max_rays) return;
-    uint32_t count = 0u;
-    float4 ro = make_float4(0.0f, 0.0f, 0.0f, 0.0f), rd = make_float4(0.0f, 0.0f, 0.0f, 0.0f), g4 = make_float4(1.0f, 1.0f, 1.0f, 0.0f);
-    if (r < S->n_rays) {
-        const uint32_t cam_idx  = S->camera;
-        const NerfExtCamera cam = cams[cam_idx];
-        const uint32_t seed     = S->frame * 1315423911u ^ r * 9781u;
-        const float px          = rand01(seed ^ 0xA511E9B3u) * (float)P.width;
-        const float py          = rand01(seed ^ 0x63D83595u) * (float)P.height;
-        const float pyf         = (float)P.height - 1.0f - py;
-        Ray ray;
-        if (make_ray(cam, px, pyf, P.bmin, P.bmax, ray)) {
-            ro    = make_float4(ray.o[0], ray.o[1], ray.o[2], ray.tn);
-            rd    = make_float4(ray.d[0], ray.d[1], ray.d[2], ray.tf);
-            count = march_train(P, bits, ro, rd, cone_of(cam), [](uint32_t, float, float) {});
-        }
-        if (count > 0u) {
-            const uint8_t* img = images + (uint64_t)cam_idx * P.width * P.height * 4u;
-            const float cx = fmaxf(0.0f, fminf(px, (float)P.width - 1.0f)), cy = fmaxf(0.0f, fminf(py, (float)P.height - 1.0f));
-            const int x0 = (int)floorf(cx), y0 = (int)floorf(cy);
-            const int x1 = min(x0 + 1, (int)P.width - 1), y1 = min(y0 + 1, (int)P.height - 1);
-            const float tx = cx - (float)x0, ty = cy - (float)y0;
-            const int stride = (int)P.width * 4;
-            const uint8_t* p00 = img + y0 * stride + x0 * 4;
-            const uint8_t* p10 = img + y0 * stride + x1 * 4;
-            const uint8_t* p01 = img + y1 * stride + x0 * 4;
-            const uint8_t* p11 = img + y1 * stride + x1 * 4;
-            const float inv255 = 1.0f / 255.0f;
-            float c[4];
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const float a = (float)p00[k] * inv255 * (1.0f - tx) + (float)p10[k] * inv255 * tx;
-                const float b = (float)p01[k] * inv255 * (1.0f - tx) + (float)p11[k] * inv255 * tx;
-                c[k]          = a * (1.0f - ty) + b * ty;
+    const uint32_t lane = threadIdx.x & 63u, nw = gridDim.x * kWaves;
+    const uint32_t n_rays = S->n_rays, cam_idx = S->camera, frame = S->frame;
+    const NerfExtCamera cam = cams[cam_idx];
+    const float cone        = cone_of(cam);
+    for (uint32_t r = blockIdx.x * kWaves + (threadIdx.x >> 6); r < P.max_rays; r += nw) {
+        uint32_t count = 0u;
+        float4 ro = make_float4(0.0f, 0.0f, 0.0f, 0.0f), rd = make_float4(0.0f, 0.0f, 0.0f, 0.0f), g4 = make_float4(1.0f, 1.0f, 1.0f, 0.0f);
+        if (r < n_rays) {
+            const uint32_t seed = frame * 1315423911u ^ r * 9781u;
+            const float px      = rand01(seed ^ 0xA511E9B3u) * (float)P.width;
+            const float py      = rand01(seed ^ 0x63D83595u) * (float)P.height;
+            const float pyf     = (float)P.height - 1.0f - py;
+            Ray ray;
+            if (make_ray(cam, px, pyf, P.bmin, P.bmax, ray)) {
+                ro    = make_float4(ray.o[0], ray.o[1], ray.o[2], ray.tn);
+                rd    = make_float4(ray.d[0], ray.d[1], ray.d[2], ray.tf);
+                count = wave::march<64>(ro, rd, cone, P.max_steps, ~0u, [&](const float p[3]) { return occupied_at(P, bits, p); }, [](uint32_t, float, float) {});
             }
-            const float alpha = c[3];
-            g4 = make_float4(c[0] * alpha + (1.0f - alpha), c[1] * alpha + (1.0f - alpha), c[2] * alpha + (1.0f - alpha), alpha);
+            if (count > 0u) {
+                const uint8_t* img = images + (uint64_t)cam_idx * P.width * P.height * 4u;
+                const float cx = fmaxf(0.0f, fminf(px, (float)P.width - 1.0f)), cy = fmaxf(0.0f, fminf(py, (float)P.height - 1.0f));
+                const int x0 = (int)floorf(cx), y0 = (int)floorf(cy);
+                const int x1 = min(x0 + 1, (int)P.width - 1), y1 = min(y0 + 1, (int)P.height - 1);
+                const float tx = cx - (float)x0, ty = cy - (float)y0;
+                const int stride = (int)P.width * 4;
+                const uint8_t* p00 = img + y0 * stride + x0 * 4;
+                const uint8_t* p10 = img + y0 * stride + x1 * 4;
+                const uint8_t* p01 = img + y1 * stride + x0 * 4;
+                const uint8_t* p11 = img + y1 * stride + x1 * 4;
+                const float inv255 = 1.0f / 255.0f;
+                float c[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const float a = (float)p00[k] * inv255 * (1.0f - tx) + (float)p10[k] * inv255 * tx;
+                    const float b = (float)p01[k] * inv255 * (1.0f - tx) + (float)p11[k] * inv255 * tx;
+                    c[k]          = a * (1.0f - ty) + b * ty;
+                }
+                const float alpha = c[3];
+                g4 = make_float4(c[0] * alpha + (1.0f - alpha), c[1] * alpha + (1.0f - alpha), c[2] * alpha + (1.0f - alpha), alpha);
+            }
+        }
+        if (lane == 0u) {
+            rays[2ull * r]      = ro;
+            rays[2ull * r + 1u] = rd;
+            gt[r]               = g4;
+            counts[r]           = count;
         }
     }
-    rays[2ull * r]      = ro;
-    rays[2ull * r + 1u] = rd;
-    gt[r]               = g4;
-    counts[r]           = count;
 }
 
 // Writes the samples of every ray whose whole range fits the stream capacity;
 // kept[r] is its count or 0.  The kept rays form a prefix (offsets grow with
-// r), so n_samples = max(offset + count) over kept rays.
+// r), so n_samples = max(offset + count) over kept rays.  One wave per ray.
 __global__ __launch_bounds__(256) void k_train_samples(TrainParams P, TrainDevState* S, const NerfExtCamera* __restrict__ cams, const uint32_t* __restrict__ bits, const float4* __restrict__ rays, const uint32_t* __restrict__ counts,
                                                         const uint32_t* __restrict__ offsets, uint32_t* __restrict__ kept, float2* __restrict__ samples, uint32_t* __restrict__ sample_ray) {
-    const uint32_t r = blockIdx.x * 256u + threadIdx.x;
-    if (r >= P.max_rays) return;
-    const uint32_t count = counts[r];
-    const uint32_t base  = offsets[r];
-    const bool fits      = count > 0u && (uint64_t)base + count <= (uint64_t)P.sample_cap;
-    kept[r]              = fits ? count : 0u;
-    if (!fits) return;
-    const float cone = cone_of(cams[S->camera]);
-    march_train(P, bits, rays[2ull * r], rays[2ull * r + 1u], cone, [&](uint32_t k, float tm, float dt) {
-        if (k < count) {
+    const uint32_t lane = threadIdx.x & 63u, nw = gridDim.x * kWaves;
+    const float cone    = cone_of(cams[S->camera]);
+    for (uint32_t r = blockIdx.x * kWaves + (threadIdx.x >> 6); r < P.max_rays; r += nw) {
+        const uint32_t count = counts[r];
+        const uint32_t base  = offsets[r];
+        const bool fits      = count > 0u && (uint64_t)base + count <= (uint64_t)P.sample_cap;
+        if (lane == 0u) kept[r] = fits ? count : 0u;
+        if (!fits) continue;
+        wave::march<64>(rays[2ull * r], rays[2ull * r + 1u], cone, P.max_steps, count, [&](const float p[3]) { return occupied_at(P, bits, p); }, [&](uint32_t k, float tm, float dt) {
             samples[base + k]    = make_float2(tm, dt);
             sample_ray[base + k] = r;
+        });
+        if (lane == 0u) {
+            atomicMax(&S->n_samples, base + count);
+            atomicAdd(&S->n_active, 1u);
         }
-    });
-    atomicMax(&S->n_samples, base + count);
-    atomicAdd(&S->n_active, 1u);
+    }
 }
 
 // ----------------------------------------------------- composite fwd + bwd
 // Huber loss (Huber 1964) on the white-composited RGB; gradients with respect
 // to the raw network outputs (see the oracle's orc_composite_backward_ray for
-// the derivation).  The suffix S_i is formed as pred - prefix_i so that both
-// passes run front to back.
+// the derivation).  One wave per ray over groups of 64 samples: transmittance
+// from the carried T times the exclusive product of (1 - alpha) across the
+// group; the backward pass forms the suffix S_i = pred - prefix_i from an
+// inclusive scan of w c, so both passes run front to back.
 __global__ __launch_bounds__(256) void k_composite_train(TrainParams P, TrainDevState* S, const uint32_t* __restrict__ kept, const uint32_t* __restrict__ offsets, const float2* __restrict__ samples, const float4* __restrict__ field,
                                                           const float4* __restrict__ gt, float4* __restrict__ draw) {
     __shared__ float wsum[kWaves];
-    const uint32_t r = blockIdx.x * 256u + threadIdx.x;
-    float ray_loss   = 0.0f;
+    const uint32_t lane = threadIdx.x & 63u, nw = gridDim.x * kWaves;
     const uint32_t active = S->n_active;
     const float inv_norm  = active ? 1.0f / (float)active : 0.0f;
-    if (r < P.max_rays && r < S->n_rays) {
+    const uint32_t n_rays = min(S->n_rays, P.max_rays);
+    const float d         = P.huber_delta;
+    float wave_loss       = 0.0f;
+    for (uint32_t r = blockIdx.x * kWaves + (threadIdx.x >> 6); r < n_rays; r += nw) {
         const uint32_t count = kept[r];
-        if (count > 0u) {
-            const uint32_t base = offsets[r];
-            float T = 1.0f, C[3] = {0.0f, 0.0f, 0.0f};
-            for (uint32_t i = 0; i < count; ++i) {
-                const float4 f = field[base + i];
-                const float dt = fmaxf(samples[base + i].y, 0.0f);
-                const float a  = 1.0f - __expf(-(f.x * dt));
-                const float w  = T * a;
-                C[0] += w * f.y;
-                C[1] += w * f.z;
-                C[2] += w * f.w;
-                T *= 1.0f - a;
-            }
-            const float4 g4 = gt[r];
-            const float gtv[3] = {g4.x, g4.y, g4.z};
-            float pred[3], gr[3];
-            const float d = P.huber_delta;
+        if (count == 0u) continue;
+        const uint32_t base = offsets[r];
+        float T = 1.0f, C[3] = {0.0f, 0.0f, 0.0f};
+        for (uint32_t c0 = 0; c0 < count; c0 += 64u) {
+            const uint32_t i = c0 + lane;
+            const bool valid = i < count;
+            const float4 f   = valid ? field[base + i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            const float dt   = valid ? fmaxf(samples[base + i].y, 0.0f) : 0.0f;
+            const float a    = valid ? 1.0f - __expf(-(f.x * dt)) : 0.0f;
+            const float incl = wave::inclusive_product(1.0f - a);
+            float excl       = __shfl_up(incl, 1, 64);
+            excl             = lane == 0u ? 1.0f : excl;
+            const float w    = T * excl * a;
+            C[0] += w * f.y;
+            C[1] += w * f.z;
+            C[2] += w * f.w;
+            T *= wave::broadcast(incl, 63u);
+        }
+        const float4 g4    = gt[r];
+        const float gtv[3] = {g4.x, g4.y, g4.z};
+        float pred[3], gr[3];
+        float ray_loss = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+            pred[c]        = wave::sum(C[c]) + T;  // white background
+            const float x  = pred[c] - gtv[c];
+            const float ax = fabsf(x);
+            ray_loss += ax <= d ? 0.5f * x * x : d * (ax - 0.5f * d);
+            gr[c] = fminf(fmaxf(x, -d), d) * inv_norm;
+        }
+        wave_loss += ray_loss;
+        T = 1.0f;
+        float carry[3] = {0.0f, 0.0f, 0.0f};
+        for (uint32_t c0 = 0; c0 < count; c0 += 64u) {
+            const uint32_t i  = c0 + lane;
+            const bool valid  = i < count;
+            const float4 f    = valid ? field[base + i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            const float dt    = valid ? fmaxf(samples[base + i].y, 0.0f) : 0.0f;
+            const float a     = valid ? 1.0f - __expf(-(f.x * dt)) : 0.0f;
+            const float incl  = wave::inclusive_product(1.0f - a);
+            float excl        = __shfl_up(incl, 1, 64);
+            excl              = lane == 0u ? 1.0f : excl;
+            const float w     = T * excl * a;
+            const float Tn    = T * incl;
+            const float c3[3] = {f.y, f.z, f.w};
+            float ds = 0.0f, dc[3];
 #pragma unroll
             for (int c = 0; c < 3; ++c) {
-                pred[c]      = C[c] + T;  // white background
-                const float x = pred[c] - gtv[c];
-                const float ax = fabsf(x);
-                ray_loss += ax <= d ? 0.5f * x * x : d * (ax - 0.5f * d);
-                gr[c] = fminf(fmaxf(x, -d), d) * inv_norm;
+                const float prefix = carry[c] + wave::inclusive_sum(w * c3[c]);
+                ds += gr[c] * (Tn * c3[c] - (pred[c] - prefix));
+                dc[c]    = w * gr[c] * c3[c] * (1.0f - c3[c]);
+                carry[c] = wave::broadcast(prefix, 63u);
             }
-            T = 1.0f;
-            float Cp[3] = {0.0f, 0.0f, 0.0f};
-            for (uint32_t i = 0; i < count; ++i) {
-                const float4 f   = field[base + i];
-                const float dt   = fmaxf(samples[base + i].y, 0.0f);
-                const float a    = 1.0f - __expf(-(f.x * dt));
-                const float w    = T * a;
-                const float Tn   = T * (1.0f - a);
-                const float c3[3] = {f.y, f.z, f.w};
-                float ds = 0.0f, dc[3];
-#pragma unroll
-                for (int c = 0; c < 3; ++c) {
-                    Cp[c] += w * c3[c];
-                    const float suffix = pred[c] - Cp[c];
-                    ds += gr[c] * (Tn * c3[c] - suffix);
-                    dc[c] = w * gr[c] * c3[c] * (1.0f - c3[c]);
-                }
-                draw[base + i] = make_float4(dt * f.x * ds, dc[0], dc[1], dc[2]);
-                T = Tn;
-            }
+            if (valid) draw[base + i] = make_float4(dt * f.x * ds, dc[0], dc[1], dc[2]);
+            T *= wave::broadcast(incl, 63u);
         }
     }
-    const float wl = wave_sum(ray_loss);
-    if ((threadIdx.x & 63u) == 0u) wsum[threadIdx.x >> 6] = wl;
+    if (lane == 0u) wsum[threadIdx.x >> 6] = wave_loss;
     __syncthreads();
     if (threadIdx.x == 0u) {
         const float b = wsum[0] + wsum[1] + wsum[2] + wsum[3];
@@ -474,18 +474,71 @@ __device__ __forceinline__ void sample_geometry(const float2* samples, const uin
     for (int a = 0; a < 3; ++a) p[a] = (w[a] - bmin[a]) / (bmax[a] - bmin[a]);
 }
 
-// Scatter-add of d(feature) into the fp32 table gradient for one level.
-__device__ __forceinline__ void scatter_level(const GridParams& g, float* __restrict__ grad, uint32_t level, const float p[3], float d0, float d1) {
-    const uint32_t N  = g.resolution[level];
-    const bool dense  = g.dense[level] != 0u;
-    const LevelCell c = level_cell(p, N);
-    float* base       = grad + (uint64_t)level * g.table_size * 2u;
+// Value of lane i + o of the same 16-lane row (0 past the row's end): DPP
+// row_shl:o.
+template <int o>
+__device__ __forceinline__ float row_next(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x100 + o, 0xF, 0xF, false));
+}
+template <int o>
+__device__ __forceinline__ uint32_t row_next_u(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x100 + o, 0xF, 0xF, false);
+}
+
+template <int o>
+__device__ __forceinline__ void combine_step(float v[16], uint32_t seg) {
+    const uint32_t ns = row_next_u<o>(seg);
+    const bool same   = ns == seg;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        const float nv = row_next<o>(v[k]);
+        v[k]           = same ? v[k] + nv : v[k];
+    }
+}
+
+// Scatter-add of d(feature) into the fp32 table gradient for one level, with
+// the contributions of a 16-lane row combined first.  Each row holds 16
+// consecutive samples (mostly of one ray) at the same level; runs of samples
+// in the same grid cell touch the same 8 corners, so their 16 corner values
+// (8 corners x 2 features) are summed across the run with a segmented suffix
+// scan over DPP row shifts and only the run's first lane issues atomics.
+// Runs are long on coarse levels, where the atomics would otherwise queue on
+// a few hot addresses.  All 64 lanes must call this (the level may differ
+// between rows); lanes with live == false contribute nothing.
+__device__ __forceinline__ void scatter_level(const GridParams& g, float* __restrict__ grad, uint32_t level, const float p[3], float d0, float d1, bool live) {
+    const uint32_t lane = threadIdx.x & 63u, s16 = lane & 15u;
+    const uint32_t lv   = level < g.n_levels ? level : 0u;
+    const uint32_t N    = g.resolution[lv];
+    const bool dense    = g.dense[lv] != 0u;
+    live                = live && level < g.n_levels;
+    const LevelCell c   = level_cell(p, N);
+    // Cell key; dead lanes get a key no live lane has.
+    const uint32_t kx = live ? c.i0[0] : 0xFFFFFFFFu, ky = c.i0[1], kz = c.i0[2];
+    const uint32_t px = __shfl_up(kx, 1, 16), py = __shfl_up(ky, 1, 16), pz = __shfl_up(kz, 1, 16);
+    const bool head   = s16 == 0u || kx != px || ky != py || kz != pz || !live;
+    const uint64_t heads = __ballot(head);
+    float v[16];
+#pragma unroll
+    for (uint32_t k = 0; k < 8u; ++k) {
+        const float w = live ? corner_weight(c, k) : 0.0f;
+        v[2u * k]      = w * d0;
+        v[2u * k + 1u] = w * d1;
+    }
+    if (heads != ~0ull) {  // some run longer than one sample somewhere in the wave
+        const uint32_t row_heads = (uint32_t)(heads >> (lane & 48u)) & 0xFFFFu;
+        const uint32_t seg       = (uint32_t)__popc(row_heads & ((2u << s16) - 1u));
+        combine_step<1>(v, seg);
+        combine_step<2>(v, seg);
+        combine_step<4>(v, seg);
+        combine_step<8>(v, seg);
+    }
+    if (!(live && head)) return;
+    float* base = grad + (uint64_t)lv * g.table_size * 2u;
 #pragma unroll
     for (uint32_t k = 0; k < 8u; ++k) {
         const uint32_t idx = corner_index(c, k, N, dense, g.table_size - 1u);
-        const float w      = corner_weight(c, k);
-        atomicAdd(base + 2u * idx, w * d0);
-        atomicAdd(base + 2u * idx + 1u, w * d1);
+        atomicAdd(base + 2u * idx, v[2u * k]);
+        atomicAdd(base + 2u * idx + 1u, v[2u * k + 1u]);
     }
 }
 
@@ -516,13 +569,12 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dx(TrainParams P, GridParams g
         const float4 gr = draw[q];
         TileGrad T;
         tile_backward(sp, sp + NERF_EXT_DENSITY_PARAMS, fd, x, d, gr, P.loss_scale, grp, T);
-        if (s < n) {
+        const bool live = s < n;
 #pragma unroll
-            for (uint32_t b = 0; b < 2u; ++b) {
-                const uint32_t l0 = 8u * b + 2u * grp;
-                if (l0 < g.n_levels) scatter_level(g, table_grad, l0, p, T.dx[b][0], T.dx[b][1]);
-                if (l0 + 1u < g.n_levels) scatter_level(g, table_grad, l0 + 1u, p, T.dx[b][2], T.dx[b][3]);
-            }
+        for (uint32_t b = 0; b < 2u; ++b) {
+            const uint32_t l0 = 8u * b + 2u * grp;
+            scatter_level(g, table_grad, l0, p, T.dx[b][0], T.dx[b][1], live);
+            scatter_level(g, table_grad, l0 + 1u, p, T.dx[b][2], T.dx[b][3], live);
         }
     }
 }
@@ -748,6 +800,14 @@ __global__ __launch_bounds__(256) void k_adam(TrainParams P, const TrainDevState
     }
 }
 
+// Workgroups of a one-wave-per-ray kernel: one wave per ray slot, at most
+// 16 workgroups (64 waves) per CU; the kernels loop over the remaining slots.
+uint32_t ray_wave_blocks(uint32_t max_rays) {
+    const uint32_t need = (max_rays + kWaves - 1u) / kWaves;
+    const uint32_t cap  = device_cu_count() * 16u;
+    return need < cap ? (need > 0u ? need : 1u) : cap;
+}
+
 uint32_t grid_for(uint64_t n, uint32_t cap) {
     const uint64_t b = (n + 255u) / 256u;
     return (uint32_t)(b < cap ? (b > 0u ? b : 1u) : cap);
@@ -756,7 +816,7 @@ uint32_t grid_for(uint64_t n, uint32_t cap) {
 }  // namespace
 
 hipError_t launch_composite_train(const TrainParams& P, const TrainBuffers& B, hipStream_t st) {
-    k_composite_train<<<(P.max_rays + 255u) / 256u, 256, 0, st>>>(P, B.state, B.kept, B.offsets, B.samples, B.field, B.gt, B.draw);
+    k_composite_train<<<ray_wave_blocks(P.max_rays), 256, 0, st>>>(P, B.state, B.kept, B.offsets, B.samples, B.field, B.gt, B.draw);
     return hipGetLastError();
 }
 
@@ -786,7 +846,6 @@ hipError_t launch_adam(const TrainParams& P, const TrainBuffers& B, hipStream_t 
 
 hipError_t launch_train_stage(const TrainParams& P, const TrainBuffers& B, uint32_t stage, bool occupancy_update, hipStream_t st) {
     const uint32_t cus        = device_cu_count();
-    const uint32_t ray_blocks = (P.max_rays + 255u) / 256u;
     switch (stage) {
     case NERF_EXT_STAGE_BEGIN: k_step_begin<<<1, 64, 0, st>>>(P, B.state); break;
     case NERF_EXT_STAGE_OCCUPANCY:
@@ -797,10 +856,10 @@ hipError_t launch_train_stage(const TrainParams& P, const TrainBuffers& B, uint3
         }
         break;
     case NERF_EXT_STAGE_SAMPLE: {
-        k_train_rays<<<ray_blocks, 256, 0, st>>>(P, B.state, B.cams, B.images, B.bits, B.rays, B.gt, B.counts);
+        k_train_rays<<<ray_wave_blocks(P.max_rays), 256, 0, st>>>(P, B.state, B.cams, B.images, B.bits, B.rays, B.gt, B.counts);
         const hipError_t e = exclusive_scan_u32(B.counts, B.offsets, P.max_rays, B.scan_tmp, &B.state->total, st);
         if (e != hipSuccess) return e;
-        k_train_samples<<<ray_blocks, 256, 0, st>>>(P, B.state, B.cams, B.bits, B.rays, B.counts, B.offsets, B.kept, B.samples, B.sample_ray);
+        k_train_samples<<<ray_wave_blocks(P.max_rays), 256, 0, st>>>(P, B.state, B.cams, B.bits, B.rays, B.counts, B.offsets, B.kept, B.samples, B.sample_ray);
         break;
     }
     case NERF_EXT_STAGE_FORWARD: {
