@@ -67,6 +67,18 @@ struct TrainBuffers {
     float4* field;               // [sample_cap] (sigma, r, g, b)
     half_t* features;            // [sample_cap][32]
     float4* draw;                // [sample_cap] (d sigma_raw, d r, d g, d b)
+    float* dfeat;                // [sample_cap][32] d(features), loss-scaled
+    // binned hash-grid scatter: records (entry within bin, 2 values) grouped
+    // by bin of kBinEntries table entries
+    uint32_t* bin_hist;          // [n_bins][kBinBlocks] record counts
+    uint32_t* bin_off;           // [n_bins][kBinBlocks] exclusive scan of bin_hist
+    uint32_t* bin_scan_tmp;
+    unsigned long long* bin_total;
+    uint32_t* rec_idx;           // [rec_cap]
+    float2* rec_val;             // [rec_cap]
+    uint32_t n_bins;             // bins of the hashed levels
+    uint32_t n_dense;            // leading dense levels (scattered with atomics)
+    uint64_t rec_cap;
     // model
     GridParams grid;
     half_t* table;               // fp16 working copy [L][T][2]
@@ -85,6 +97,9 @@ struct TrainBuffers {
 };
 
 constexpr uint32_t kDwBlocks   = 256;   // workgroups of the weight-gradient passes
+constexpr uint32_t kBinEntries = 8192;  // table entries per scatter bin (64 KiB of fp32 pairs in LDS)
+constexpr uint32_t kBinBlocks  = 256;   // workgroups of the bin count / fill passes
+constexpr uint32_t kMaxBins    = 16384; // bin counters per workgroup in LDS (64 KiB)
 constexpr uint32_t kMlpParams  = NERF_EXT_DENSITY_PARAMS + NERF_EXT_COLOR_PARAMS;
 
 // Launches one stage (NERF_EXT_STAGE_*) of a training step on `stream`.

@@ -496,8 +496,8 @@ __device__ __forceinline__ void combine_step(float v[16], uint32_t seg) {
     }
 }
 
-// Scatter-add of d(feature) into the fp32 table gradient for one level, with
-// the contributions of a 16-lane row combined first.  Each row holds 16
+// Scatter-add of d(feature) into the fp32 table gradient for one dense level,
+// with the contributions of a 16-lane row combined first.  Each row holds 16
 // consecutive samples (mostly of one ray) at the same level; runs of samples
 // in the same grid cell touch the same 8 corners, so their 16 corner values
 // (8 corners x 2 features) are summed across the run with a segmented suffix
@@ -542,15 +542,14 @@ __device__ __forceinline__ void scatter_level(const GridParams& g, float* __rest
     }
 }
 
-__device__ __forceinline__ uint32_t select4(const uint32_t* a, uint32_t grp, uint32_t off) {
-    return grp == 0u ? a[off] : grp == 1u ? a[off + 2u] : grp == 2u ? a[off + 4u] : a[off + 6u];
-}
-
-// Input-gradient pass: d(features) of each tile, scattered into the table
-// gradient.  Lane (g, s) holds features 16b + 4g + e, i.e. levels 2g, 2g+1
-// (b = 0) and 8+2g, 9+2g (b = 1) of sample s.
+// Input-gradient pass: d(features) of each tile, loss-scaled, to dfeat
+// [n][32] for the binned scatter of the hashed levels; the dense (coarse)
+// levels, where runs of consecutive samples share cells, are scattered here
+// with row-combined atomics.  Lane (g, s) holds features 16b + 4g + e of
+// sample s, i.e. levels 2g, 2g+1 (b = 0) and 8+2g, 9+2g (b = 1).
 __global__ __launch_bounds__(kThreads) void k_bwd_dx(TrainParams P, GridParams g, const TrainDevState* S, const half_t* __restrict__ dparams, const half_t* __restrict__ cparams, const half_t* __restrict__ features,
-                                                     const float4* __restrict__ draw, const float2* __restrict__ samples, const uint32_t* __restrict__ sample_ray, const float4* __restrict__ rays, float* __restrict__ table_grad) {
+                                                     const float4* __restrict__ draw, const float2* __restrict__ samples, const uint32_t* __restrict__ sample_ray, const float4* __restrict__ rays, float* __restrict__ dfeat, uint32_t n_dense,
+                                                     float* __restrict__ table_grad) {
     __shared__ half_t sp[kMlpParams];
     for (uint32_t i = threadIdx.x; i < NERF_EXT_DENSITY_PARAMS; i += blockDim.x) sp[i] = dparams[i];
     for (uint32_t i = threadIdx.x; i < NERF_EXT_COLOR_PARAMS; i += blockDim.x) sp[NERF_EXT_DENSITY_PARAMS + i] = cparams[i];
@@ -570,13 +569,90 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dx(TrainParams P, GridParams g
         TileGrad T;
         tile_backward(sp, sp + NERF_EXT_DENSITY_PARAMS, fd, x, d, gr, P.loss_scale, grp, T);
         const bool live = s < n;
+        if (live) {
+            float4* o = reinterpret_cast<float4*>(dfeat + (uint64_t)s * 32u);
+            o[grp]      = make_float4(T.dx[0][0], T.dx[0][1], T.dx[0][2], T.dx[0][3]);
+            o[4u + grp] = make_float4(T.dx[1][0], T.dx[1][1], T.dx[1][2], T.dx[1][3]);
+        }
+        if (n_dense > 0u) {  // uniform: the dense levels are the first n_dense levels
 #pragma unroll
-        for (uint32_t b = 0; b < 2u; ++b) {
-            const uint32_t l0 = 8u * b + 2u * grp;
-            scatter_level(g, table_grad, l0, p, T.dx[b][0], T.dx[b][1], live);
-            scatter_level(g, table_grad, l0 + 1u, p, T.dx[b][2], T.dx[b][3], live);
+            for (uint32_t b = 0; b < 2u; ++b) {
+                const uint32_t l0 = 8u * b + 2u * grp;
+                scatter_level(g, table_grad, l0, p, T.dx[b][0], T.dx[b][1], live && l0 < n_dense);
+                scatter_level(g, table_grad, l0 + 1u, p, T.dx[b][2], T.dx[b][3], live && l0 + 1u < n_dense);
+            }
         }
     }
+}
+
+// Hash-grid backward of the hashed levels, binned.  Entry e = (level -
+// n_dense) * T + index of the hashed levels belongs to bin e / kBinEntries.  k_bin_pass<false> counts each workgroup's records per
+// bin (LDS histogram, stored as hist[bin][workgroup]); an exclusive scan of
+// that matrix gives every (bin, workgroup) its record range; k_bin_pass<true>
+// revisits the same samples in the same order and writes each record
+// (entry within the bin, w * d(feature 0), w * d(feature 1)) into its range;
+// k_bin_accumulate then sums one bin per workgroup in LDS and writes the
+// bin's slice of the gradient once.  No global atomics, and the gradient is
+// overwritten rather than accumulated, so it needs no clearing.
+template <bool kFill>
+__global__ __launch_bounds__(256) void k_bin_pass(TrainParams P, GridParams g, const TrainDevState* S, const float2* __restrict__ samples, const uint32_t* __restrict__ sample_ray, const float4* __restrict__ rays,
+                                                  const float* __restrict__ dfeat, uint32_t n_dense, uint32_t n_bins, uint32_t* __restrict__ hist, uint32_t* __restrict__ rec_idx, float2* __restrict__ rec_val) {
+    __shared__ uint32_t cursor[kMaxBins];
+    for (uint32_t i = threadIdx.x; i < n_bins; i += blockDim.x) cursor[i] = kFill ? hist[(uint64_t)i * gridDim.x + blockIdx.x] : 0u;
+    __syncthreads();
+    const uint32_t n    = min(S->n_samples, P.sample_cap);
+    const uint32_t mask = g.table_size - 1u;
+    for (uint32_t s = blockIdx.x * blockDim.x + threadIdx.x; s < n; s += gridDim.x * blockDim.x) {
+        float p[3], d[3];
+        sample_geometry(samples, sample_ray, rays, P.bmin, P.bmax, s, p, d);
+        const float* df = dfeat + (uint64_t)s * 32u;
+        for (uint32_t l = n_dense; l < g.n_levels; ++l) {
+            const uint32_t N  = g.resolution[l];
+            const bool dense  = g.dense[l] != 0u;
+            const LevelCell c = level_cell(p, N);
+            const uint32_t e0 = (l - n_dense) * g.table_size;
+            float d0 = 0.0f, d1 = 0.0f;
+            if constexpr (kFill) {
+                d0 = df[2u * l];
+                d1 = df[2u * l + 1u];
+            }
+#pragma unroll
+            for (uint32_t k = 0; k < 8u; ++k) {
+                const uint32_t e    = e0 + corner_index(c, k, N, dense, mask);
+                const uint32_t slot = atomicAdd(&cursor[e / kBinEntries], 1u);
+                if constexpr (kFill) {
+                    const float w = corner_weight(c, k);
+                    rec_idx[slot] = e % kBinEntries;
+                    rec_val[slot] = make_float2(w * d0, w * d1);
+                }
+            }
+        }
+    }
+    if constexpr (!kFill) {
+        __syncthreads();
+        for (uint32_t i = threadIdx.x; i < n_bins; i += blockDim.x) hist[(uint64_t)i * gridDim.x + blockIdx.x] = cursor[i];
+    }
+}
+
+// grad points at the first hashed level; entries = hashed levels x T.
+__global__ __launch_bounds__(512) void k_bin_accumulate(const uint32_t* __restrict__ offsets, uint32_t n_blocks, uint32_t n_bins, const unsigned long long* __restrict__ total, const uint32_t* __restrict__ rec_idx, const float2* __restrict__ rec_val,
+                                                        uint64_t entries, float2* __restrict__ grad) {
+    __shared__ float acc[2u * kBinEntries];
+    for (uint32_t i = threadIdx.x; i < 2u * kBinEntries; i += blockDim.x) acc[i] = 0.0f;
+    __syncthreads();
+    const uint32_t bin   = blockIdx.x;
+    const uint32_t begin = offsets[(uint64_t)bin * n_blocks];
+    const uint32_t end   = bin + 1u < n_bins ? offsets[(uint64_t)(bin + 1u) * n_blocks] : (uint32_t)*total;
+    for (uint32_t r = begin + threadIdx.x; r < end; r += blockDim.x) {
+        const uint32_t i = rec_idx[r] % kBinEntries;
+        const float2 v   = rec_val[r];
+        atomicAdd(&acc[2u * i], v.x);
+        atomicAdd(&acc[2u * i + 1u], v.y);
+    }
+    __syncthreads();
+    const uint64_t base = (uint64_t)bin * kBinEntries;
+    for (uint32_t i = threadIdx.x; i < kBinEntries; i += blockDim.x)
+        if (base + i < entries) grad[base + i] = make_float2(acc[2u * i], acc[2u * i + 1u]);
 }
 
 // Weight-gradient passes.  Group 0: colour hidden (64x64).  Group 1: colour
@@ -724,6 +800,11 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dw(TrainParams P, const TrainD
     }
 }
 
+__global__ __launch_bounds__(256) void k_fill_zero(float* __restrict__ p, uint64_t n) {
+    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) p[i] = 0.0f;
+}
+
 __global__ __launch_bounds__(256) void k_dw_reduce(const float* __restrict__ partials, uint32_t blocks, float* __restrict__ grad) {
     const uint32_t i = blockIdx.x * 256u + threadIdx.x;
     if (i >= kMlpParams) return;
@@ -779,17 +860,16 @@ __global__ void k_adam_prepare(TrainParams P, TrainDevState* S) {
     S->inv_bc2        = 1.0f / (1.0f - powf(P.beta2, (float)t));
 }
 
-// :1537-1554 on fp32 masters with fp16 working copies; the gradient is
-// consumed and zeroed whether or not the update is applied.
-__global__ __launch_bounds__(256) void k_adam(TrainParams P, const TrainDevState* S, float* __restrict__ w, half_t* __restrict__ w16, float* __restrict__ g, float* __restrict__ m, float* __restrict__ v, uint64_t n) {
+// :1537-1554 on fp32 masters with fp16 working copies.  The backward pass
+// overwrites both gradients every step, so they are not cleared here.
+__global__ __launch_bounds__(256) void k_adam(TrainParams P, const TrainDevState* S, float* __restrict__ w, half_t* __restrict__ w16, const float* __restrict__ g, float* __restrict__ m, float* __restrict__ v, uint64_t n) {
     const bool skip       = S->skip != 0u;
     const float lr = S->lr, gs = S->grad_scale * S->inv_ls, bc1 = S->inv_bc1, bc2 = S->inv_bc2;
     const float b1 = P.beta1, b2 = P.beta2, eps = P.eps;
     const uint64_t step = (uint64_t)gridDim.x * blockDim.x;
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += step) {
+        if (skip) break;
         const float gr = g[i] * gs;
-        g[i]           = 0.0f;
-        if (skip) continue;
         const float mi = b1 * m[i] + (1.0f - b1) * gr;
         const float vi = b2 * v[i] + (1.0f - b2) * gr * gr;
         const float wi = w[i] - lr * (mi * bc1) / (sqrtf(vi * bc2) + eps);
@@ -823,7 +903,19 @@ hipError_t launch_composite_train(const TrainParams& P, const TrainBuffers& B, h
 hipError_t launch_mlp_backward(const TrainParams& P, const TrainBuffers& B, hipStream_t st) {
     const uint32_t cus = device_cu_count();
     if (B.grid.table_dtype != NERF_EXT_F16) return hipErrorInvalidValue;
-    k_bwd_dx<<<cus * 4u, kThreads, 0, st>>>(P, B.grid, B.state, B.dparams, B.cparams, B.features, B.draw, B.samples, B.sample_ray, B.rays, B.table_grad);
+    // Dense levels: cleared, then row-combined atomics inside k_bwd_dx.
+    const uint64_t dense_elems = (uint64_t)B.n_dense * B.grid.table_size * 2u;
+    if (dense_elems) k_fill_zero<<<grid_for(dense_elems, cus * 4u), 256, 0, st>>>(B.table_grad, dense_elems);
+    k_bwd_dx<<<cus * 4u, kThreads, 0, st>>>(P, B.grid, B.state, B.dparams, B.cparams, B.features, B.draw, B.samples, B.sample_ray, B.rays, B.dfeat, B.n_dense, B.table_grad);
+    // Hashed levels: binned.
+    if (B.n_bins) {
+        k_bin_pass<false><<<kBinBlocks, 256, 0, st>>>(P, B.grid, B.state, B.samples, B.sample_ray, B.rays, B.dfeat, B.n_dense, B.n_bins, B.bin_hist, nullptr, nullptr);
+        const hipError_t e = exclusive_scan_u32(B.bin_hist, B.bin_off, B.n_bins * kBinBlocks, B.bin_scan_tmp, B.bin_total, st);
+        if (e != hipSuccess) return e;
+        k_bin_pass<true><<<kBinBlocks, 256, 0, st>>>(P, B.grid, B.state, B.samples, B.sample_ray, B.rays, B.dfeat, B.n_dense, B.n_bins, B.bin_off, B.rec_idx, B.rec_val);
+        k_bin_accumulate<<<B.n_bins, 512, 0, st>>>(B.bin_off, kBinBlocks, B.n_bins, B.bin_total, B.rec_idx, B.rec_val, (uint64_t)(B.grid.n_levels - B.n_dense) * B.grid.table_size,
+                                                   reinterpret_cast<float2*>(B.table_grad) + (uint64_t)B.n_dense * B.grid.table_size);
+    }
     k_bwd_dw<0><<<kDwBlocks, kThreads, 0, st>>>(P, B.state, B.dparams, B.cparams, B.features, B.draw, B.samples, B.sample_ray, B.rays, B.dw_partials);
     k_bwd_dw<1><<<kDwBlocks, kThreads, 0, st>>>(P, B.state, B.dparams, B.cparams, B.features, B.draw, B.samples, B.sample_ray, B.rays, B.dw_partials);
     k_bwd_dw<2><<<kDwBlocks, kThreads, 0, st>>>(P, B.state, B.dparams, B.cparams, B.features, B.draw, B.samples, B.sample_ray, B.rays, B.dw_partials);

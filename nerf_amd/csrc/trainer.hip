@@ -59,6 +59,8 @@ NerfStatus trainer_create(const NerfExtTrainDesc* d, const BorrowedModel* borrow
     NerfStatus st = make_grid(&d->grid, g);
     if (st != NERF_STATUS_OK) return st;
     NERF_CHECK_ARG(g.n_levels * g.n_features == 32u, "trainer: the density MLP takes 32 features (16 levels x 2)");
+    NERF_CHECK_ARG((uint64_t)g.n_levels * g.table_size <= (uint64_t)kMaxBins * kBinEntries, "trainer: at most 2^27 table entries (16 levels x 2^23)");
+    NERF_CHECK_ARG((uint64_t)d->sample_capacity * g.n_levels * 8u < (1ull << 32), "trainer: sample_capacity x 128 must stay below 2^32 gradient records");
     if (stream) {
         t->stream = stream;
     } else {
@@ -118,6 +120,17 @@ NerfStatus trainer_create(const NerfExtTrainDesc* d, const BorrowedModel* borrow
     NERF_HIP_TRY(alloc(T, B.field, P.sample_cap));
     NERF_HIP_TRY(alloc(T, B.features, 32ull * P.sample_cap));
     NERF_HIP_TRY(alloc(T, B.draw, P.sample_cap));
+    NERF_HIP_TRY(alloc(T, B.dfeat, 32ull * P.sample_cap));
+    B.n_dense = 0u;
+    while (B.n_dense < g.n_levels && g.dense[B.n_dense]) ++B.n_dense;
+    B.n_bins  = (uint32_t)(((uint64_t)(g.n_levels - B.n_dense) * g.table_size + kBinEntries - 1u) / kBinEntries);
+    B.rec_cap = (uint64_t)P.sample_cap * (g.n_levels - B.n_dense) * 8u;
+    NERF_HIP_TRY(alloc(T, B.bin_hist, (uint64_t)B.n_bins * kBinBlocks));
+    NERF_HIP_TRY(alloc(T, B.bin_off, (uint64_t)B.n_bins * kBinBlocks));
+    NERF_HIP_TRY(alloc(T, B.bin_scan_tmp, scan_tmp_words(B.n_bins * kBinBlocks + 1u)));
+    NERF_HIP_TRY(alloc(T, B.bin_total, 1));
+    NERF_HIP_TRY(alloc(T, B.rec_idx, B.rec_cap));
+    NERF_HIP_TRY(alloc(T, B.rec_val, B.rec_cap));
     NERF_HIP_TRY(alloc(T, B.table_grad, B.table_elems));
     NERF_HIP_TRY(alloc(T, B.table_m, B.table_elems));
     NERF_HIP_TRY(alloc(T, B.table_v, B.table_elems));

@@ -235,8 +235,8 @@ def test_adam_stage_and_step_end(dataset):
         np.testing.assert_allclose(got - w0, w - w0, rtol=1e-5, atol=1e-8, err_msg=f"{name} Adam update")
         if p16 is not None:
             assert np.array_equal(ext.read_device(p16, (count,), np.float16), got.astype(np.float16)), "fp16 working copy != RNE(master)"
-    assert not ext.read_device(B.table_grad, (E,), np.float32).any(), "table gradient not consumed"
-    assert not ext.read_device(B.mlp_grad, (10240,), np.float32).any(), "MLP gradient not consumed"
+    # Adam reads the gradients and leaves them as they are (the next backward overwrites them).
+    assert np.array_equal(ext.read_device(B.table_grad, (E,), np.float32), tg)
     assert st.last.completed_steps == 1
     assert st.last.last_train_camera == orc.train_camera(0, VIEWS)
     assert st.last.has_nonfinite == 0
