@@ -602,28 +602,52 @@ __global__ __launch_bounds__(256) void k_bin_pass(TrainParams P, GridParams g, c
     __syncthreads();
     const uint32_t n    = min(S->n_samples, P.sample_cap);
     const uint32_t mask = g.table_size - 1u;
-    for (uint32_t s = blockIdx.x * blockDim.x + threadIdx.x; s < n; s += gridDim.x * blockDim.x) {
+    const uint32_t lane = threadIdx.x & 63u, s16 = lane & 15u;
+    // Waves take 64 consecutive samples; all lanes stay active (rows of 16
+    // combine runs of samples in the same cell, as in scatter_level, and only
+    // a run's first lane emits its 8 records).
+    for (uint32_t base = blockIdx.x * blockDim.x + (threadIdx.x & ~63u); base < n; base += gridDim.x * blockDim.x) {
+        const uint32_t s = base + lane;
+        const bool live  = s < n;
+        const uint32_t q = live ? s : n - 1u;
         float p[3], d[3];
-        sample_geometry(samples, sample_ray, rays, P.bmin, P.bmax, s, p, d);
-        const float* df = dfeat + (uint64_t)s * 32u;
+        sample_geometry(samples, sample_ray, rays, P.bmin, P.bmax, q, p, d);
+        const float* df = dfeat + (uint64_t)q * 32u;
         for (uint32_t l = n_dense; l < g.n_levels; ++l) {
             const uint32_t N  = g.resolution[l];
             const bool dense  = g.dense[l] != 0u;
             const LevelCell c = level_cell(p, N);
             const uint32_t e0 = (l - n_dense) * g.table_size;
-            float d0 = 0.0f, d1 = 0.0f;
+            const uint32_t kx = live ? c.i0[0] : 0xFFFFFFFFu, ky = c.i0[1], kz = c.i0[2];
+            const uint32_t px = __shfl_up(kx, 1, 16), py = __shfl_up(ky, 1, 16), pz = __shfl_up(kz, 1, 16);
+            const bool head   = s16 == 0u || kx != px || ky != py || kz != pz || !live;
+            float v[16];
             if constexpr (kFill) {
-                d0 = df[2u * l];
-                d1 = df[2u * l + 1u];
+                const float d0 = live ? df[2u * l] : 0.0f, d1 = live ? df[2u * l + 1u] : 0.0f;
+#pragma unroll
+                for (uint32_t k = 0; k < 8u; ++k) {
+                    const float w  = corner_weight(c, k);
+                    v[2u * k]      = w * d0;
+                    v[2u * k + 1u] = w * d1;
+                }
+                const uint64_t heads = __ballot(head);
+                if (heads != ~0ull) {
+                    const uint32_t row_heads = (uint32_t)(heads >> (lane & 48u)) & 0xFFFFu;
+                    const uint32_t seg       = (uint32_t)__popc(row_heads & ((2u << s16) - 1u));
+                    combine_step<1>(v, seg);
+                    combine_step<2>(v, seg);
+                    combine_step<4>(v, seg);
+                    combine_step<8>(v, seg);
+                }
             }
+            if (!(live && head)) continue;
 #pragma unroll
             for (uint32_t k = 0; k < 8u; ++k) {
                 const uint32_t e    = e0 + corner_index(c, k, N, dense, mask);
                 const uint32_t slot = atomicAdd(&cursor[e / kBinEntries], 1u);
                 if constexpr (kFill) {
-                    const float w = corner_weight(c, k);
                     rec_idx[slot] = e % kBinEntries;
-                    rec_val[slot] = make_float2(w * d0, w * d1);
+                    rec_val[slot] = make_float2(v[2u * k], v[2u * k + 1u]);
                 }
             }
         }
@@ -643,11 +667,25 @@ __global__ __launch_bounds__(512) void k_bin_accumulate(const uint32_t* __restri
     const uint32_t bin   = blockIdx.x;
     const uint32_t begin = offsets[(uint64_t)bin * n_blocks];
     const uint32_t end   = bin + 1u < n_bins ? offsets[(uint64_t)(bin + 1u) * n_blocks] : (uint32_t)*total;
-    for (uint32_t r = begin + threadIdx.x; r < end; r += blockDim.x) {
-        const uint32_t i = rec_idx[r] % kBinEntries;
-        const float2 v   = rec_val[r];
-        atomicAdd(&acc[2u * i], v.x);
-        atomicAdd(&acc[2u * i + 1u], v.y);
+    // Batches of 8 coalesced record loads per thread are issued before their
+    // LDS atomics, so the loads of a batch are in flight together.
+    constexpr uint32_t kBatch = 8u;
+    for (uint32_t r0 = begin; r0 < end; r0 += kBatch * blockDim.x) {
+        uint32_t idx[kBatch];
+        float2 val[kBatch];
+#pragma unroll
+        for (uint32_t k = 0; k < kBatch; ++k) {
+            const uint32_t r = r0 + k * blockDim.x + threadIdx.x;
+            idx[k]           = r < end ? rec_idx[r] % kBinEntries : 0u;
+            val[k]           = r < end ? rec_val[r] : make_float2(0.0f, 0.0f);
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < kBatch; ++k) {
+            if (r0 + k * blockDim.x + threadIdx.x < end) {
+                atomicAdd(&acc[2u * idx[k]], val[k].x);
+                atomicAdd(&acc[2u * idx[k] + 1u], val[k].y);
+            }
+        }
     }
     __syncthreads();
     const uint64_t base = (uint64_t)bin * kBinEntries;
@@ -805,12 +843,19 @@ __global__ __launch_bounds__(256) void k_fill_zero(float* __restrict__ p, uint64
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) p[i] = 0.0f;
 }
 
+// Sum of the per-workgroup partials: workgroup x sums 64 parameters, its 4
+// waves each a quarter of the partials (independent loads in flight), then
+// the quarters are added in a fixed order.
 __global__ __launch_bounds__(256) void k_dw_reduce(const float* __restrict__ partials, uint32_t blocks, float* __restrict__ grad) {
-    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
-    if (i >= kMlpParams) return;
-    float s = 0.0f;
-    for (uint32_t b = 0; b < blocks; ++b) s += partials[(uint64_t)b * kMlpParams + i];
-    grad[i] = s;
+    __shared__ float part[4][64];
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t i    = blockIdx.x * 64u + lane;
+    float s             = 0.0f;
+    if (i < kMlpParams)
+        for (uint32_t b = wave; b < blocks; b += 4u) s += partials[(uint64_t)b * kMlpParams + i];
+    part[wave][lane] = s;
+    __syncthreads();
+    if (wave == 0u && i < kMlpParams) grad[i] = (part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]);
 }
 
 // ------------------------------------------------------------------ Adam
@@ -919,7 +964,7 @@ hipError_t launch_mlp_backward(const TrainParams& P, const TrainBuffers& B, hipS
     k_bwd_dw<0><<<kDwBlocks, kThreads, 0, st>>>(P, B.state, B.dparams, B.cparams, B.features, B.draw, B.samples, B.sample_ray, B.rays, B.dw_partials);
     k_bwd_dw<1><<<kDwBlocks, kThreads, 0, st>>>(P, B.state, B.dparams, B.cparams, B.features, B.draw, B.samples, B.sample_ray, B.rays, B.dw_partials);
     k_bwd_dw<2><<<kDwBlocks, kThreads, 0, st>>>(P, B.state, B.dparams, B.cparams, B.features, B.draw, B.samples, B.sample_ray, B.rays, B.dw_partials);
-    k_dw_reduce<<<(kMlpParams + 255u) / 256u, 256, 0, st>>>(B.dw_partials, kDwBlocks, B.mlp_grad);
+    k_dw_reduce<<<(kMlpParams + 63u) / 64u, 256, 0, st>>>(B.dw_partials, kDwBlocks, B.mlp_grad);
     return hipGetLastError();
 }
 
