@@ -135,9 +135,15 @@ __global__ __launch_bounds__(kBlockThreads) void k_field_forward(GridParams g, c
     ColorFrags fc;
     load_density(sp, fd, lane);
     load_color(sp + NERF_EXT_DENSITY_PARAMS, fc, lane);
-    const uint32_t tiles  = (n + 15u) / 16u;
-    const uint32_t nwaves = gridDim.x * kBlockWaves;
-    for (uint32_t tile = blockIdx.x * kBlockWaves + (threadIdx.x >> 6); tile < tiles; tile += nwaves) {
+    // Round r covers tiles [r * W, (r + 1) * W) of the stream (W = all waves),
+    // XCD x (workgroups b with b % 8 == x) taking the x-th eighth of it, so
+    // a ray's consecutive tiles share one XCD's L2 while the whole device
+    // works on one band of neighbouring rays.
+    const uint32_t tiles   = (n + 15u) / 16u;
+    const uint32_t per_xcd = (gridDim.x >> 3) * kBlockWaves;
+    const uint32_t lw      = (blockIdx.x >> 3) * kBlockWaves + (threadIdx.x >> 6);
+    const uint32_t first   = (blockIdx.x & 7u) * per_xcd + lw;
+    for (uint32_t tile = first; tile < tiles; tile += 8u * per_xcd) {
         const uint32_t s = tile * 16u + s16;
         const uint32_t q = s < n ? s : n - 1u;
         float p[3], d[3];
@@ -171,7 +177,7 @@ uint32_t persistent_blocks(uint32_t n, uint32_t per_cu) {
 
 hipError_t launch_field(const GridParams& g, const void* table, const FieldWeights& w, const FieldInputs& in, uint32_t n, float4* out4, hipStream_t stream) {
     if (n == 0u) return hipSuccess;
-    const uint32_t blocks   = persistent_blocks(n, 8u);
+    const uint32_t blocks   = (persistent_blocks(n, 8u) + 7u) / 8u * 8u;  // whole XCD rounds
     const bool from_samples = in.samples != nullptr;
     if (g.table_dtype == NERF_EXT_F32) {
         if (from_samples)
