@@ -31,6 +31,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--train-steps K2]
 from __future__ import annotations
 
 import argparse
+import ctypes as C
 import json
 import os
 import sys
@@ -70,6 +71,69 @@ def build_workload():
     cam = ext.camera_orbit(0, 0, RADIUS, CENTRE, W, H, FOCAL * W / 800.0)  # field of view of the 800-px view
     occ = ext.occupancy_struct(bits, 128)
     return scene, bits, desc, model, cam, occ
+
+
+# Hash-encode forward, 16 levels x 2 fp32 features, T = 2^16: position 12 B
+# + 16 levels x 8 corners x 2 features x 4 B + 32 fp32 outputs = 1,164 B/point.
+ENCODE_BYTES_PER_POINT = 12 + 16 * 8 * 2 * 4 + 32 * 4
+
+
+def unit_points(n: int, seed: int) -> np.ndarray:
+    """n points in [0,1)^3: draws 0..3n-1 of the library's splitmix64 stream
+    keyed (0x9017, seed), 24-bit uniforms (the points of the parity tests)."""
+    m = np.uint64(0xFFFFFFFFFFFFFFFF)
+    golden, mix1, mix2 = np.uint64(0x9E3779B97F4A7C15), np.uint64(0xBF58476D1CE4E5B9), np.uint64(0x94D049BB133111EB)
+    with np.errstate(over="ignore"):
+        state0 = (np.uint64(0x9017) + golden) ^ (np.uint64(seed) * mix1)
+        z = state0 + (np.arange(3 * n, dtype=np.uint64) + np.uint64(1)) * golden
+        z = (z ^ (z >> np.uint64(30))) * mix1
+        z = (z ^ (z >> np.uint64(27))) * mix2
+        z = (z ^ (z >> np.uint64(31))) & m
+    u = ((z >> np.uint64(40)).astype(np.float32)) * np.float32(1.0 / 16777216.0)
+    return u.reshape(n, 3)
+
+
+def kernel_rooflines(reps_small: int = 200):
+    """Stage rooflines of the hash encode (HBM) and the fused MLP (MFMA)."""
+    from nerf_amd import _lib as L, ext
+    from nerf_amd.device import DeviceArray, Event, Stream
+    out = {}
+    st = Stream()
+
+    def timed(fn, reps):
+        fn()
+        st.synchronize()
+        e0, e1 = Event(), Event()
+        e0.record(st)
+        for _ in range(reps):
+            fn()
+        e1.record(st)
+        st.synchronize()
+        return e0.elapsed_ms(e1) / reps
+
+    desc = ext.grid_desc(16, L.NERF_EXT_F32)
+    table = ext.init_table(desc, 0, 1e-4)
+    for n, reps, label in ((1 << 16, reps_small, "encode_forward_2p16"), (1 << 24, 20, "encode_forward_2p24")):
+        pos = DeviceArray.from_numpy(unit_points(n, seed=0))
+        feats = DeviceArray((n, 32), np.float32)
+        ms = timed(lambda: L.call("nerf_ext_encode_forward", C.byref(desc), table.ptr, pos.ptr, n, feats.ptr, L.NERF_EXT_F32, st.handle), reps)
+        gbs = n * ENCODE_BYTES_PER_POINT / (ms / 1e3) / 1e9
+        out[label] = {"kernel": "k_encode_forward", "points": n, "table": "16 x 2^16 x 2 fp32", "ms": round(ms, 5), "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                      "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_point": ENCODE_BYTES_PER_POINT, "reps": reps}
+    n = 1 << 22
+    rng = np.random.default_rng(0)
+    feats = DeviceArray.from_numpy(rng.uniform(-1.0, 1.0, size=(n, 32)).astype(np.float16))
+    d = rng.normal(size=(n, 3)).astype(np.float32)
+    dirs = DeviceArray.from_numpy(d / np.linalg.norm(d, axis=1, keepdims=True))
+    res = DeviceArray((n, 4), np.float32)
+    dp = DeviceArray.from_numpy(ext.mlp_init(0).astype(np.float16))
+    cp = DeviceArray.from_numpy(ext.mlp_init(1).astype(np.float16))
+    ms = timed(lambda: L.call("nerf_ext_field_mlp", dp.ptr, cp.ptr, feats.ptr, dirs.ptr, n, res.ptr, st.handle), 20)
+    tfs = n * FIELD_FLOPS_PER_SAMPLE / (ms / 1e3) / 1e12
+    io_gbs = n * (64 + 12 + 16) / (ms / 1e3) / 1e9
+    out["field_mlp"] = {"kernel": "k_field_mlp (density 32-64-16 + colour 32-64-64-16, fp16 MFMA)", "samples": n, "ms": round(ms, 4), "bound": "mfma", "achieved": round(tfs, 1), "peak": MFMA_FP16_PEAK_TFS, "unit": "TFLOP/s",
+                        "frac": round(tfs / MFMA_FP16_PEAK_TFS, 4), "flops_per_sample": FIELD_FLOPS_PER_SAMPLE, "io_GBps": round(io_gbs, 1)}
+    return out
 
 
 def train_bench(steps: int, warmup: int, views: int = 100):
@@ -147,6 +211,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-stage-rooflines", action="store_true", help="skip the encode / MLP stage measurements")
     ap.add_argument("--train-steps", type=int, default=100, help="timed training steps (0: skip the training leg)")
     ap.add_argument("--train-warmup", type=int, default=30)
     ap.add_argument("--width", type=int, default=W, help="render width (the metric is quoted at 800)")
@@ -233,6 +298,8 @@ def main() -> int:
                      "bytes_per_sample": FIELD_BYTES_PER_SAMPLE, "flops_per_sample": FIELD_FLOPS_PER_SAMPLE},
         "device": {"name": info.name.decode(), "arch": info.arch.decode(), "cus": info.compute_units},
     }
+    if not args.no_stage_rooflines:
+        line["stage_rooflines"] = kernel_rooflines()
     if args.train_steps > 0:
         line["train"] = train_bench(args.train_steps, args.train_warmup)
     if not args.no_cpu_baseline:

@@ -125,6 +125,10 @@ typedef struct NerfExtModel {
 /* Full field at points with view directions: out [n][4] = (sigma, r, g, b),
  * sigma = exp(density raw 0), rgb = sigmoid(colour raw 0..2). */
 NERF_API NerfStatus nerf_ext_field_forward(const NerfExtModel* model, const float* positions, const float* directions, uint32_t n, float* out, void* stream);
+/* The density and colour MLPs of nerf_ext_field_forward on given encodings:
+ * features fp16 [n][32], unit directions [n][3] -> out [n][4] = (sigma, r, g, b).
+ * The fused fp16-MFMA MLP pass on its own (no table gathers). */
+NERF_API NerfStatus nerf_ext_field_mlp(const uint16_t* density_params, const uint16_t* color_params, const uint16_t* features, const float* directions, uint32_t n, float* out, void* stream);
 
 /* ---------------------------------------------------------- analytic scene */
 typedef struct NerfExtGaussian {

@@ -325,6 +325,7 @@ PROTOTYPES: dict[str, tuple] = {
     "nerf_ext_float_to_half": (_S, [_P, _P, _U64, _P]),
     "nerf_ext_density_mlp": (_S, [_P, _P, _U32, _P, _P]),
     "nerf_ext_density_forward": (_S, [C.POINTER(NerfExtGridDesc), _P, _P, _P, _U32, _P, _P]),
+    "nerf_ext_field_mlp": (_S, [_P, _P, _P, _P, _U32, _P, _P]),
     "nerf_ext_field_forward": (_S, [C.POINTER(NerfExtModel), _P, _P, _U32, _P, _P]),
     # scene
     "nerf_ext_scene_gaussians": (_S, [C.POINTER(NerfExtSceneDesc), _P]),

@@ -32,6 +32,8 @@ HIPCC_FLAGS = [
     "-DNERF_BUILD_SHARED",
     "-DNERF_BUILD_EXPORTS",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in VGPRs: no accumulator-register copies before the VALU uses them.
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wall",
     "-Wno-unused-function",
 ]

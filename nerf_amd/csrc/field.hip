@@ -67,12 +67,18 @@ __device__ __forceinline__ half8_t color_input(const floatx4 o, const float d[3]
     return xc;
 }
 
-__device__ __forceinline__ float4 field_output(const floatx4 o, const floatx4 c) {
-    const float sigma = expf(o[0]);
-    const float r     = 1.0f / (1.0f + expf(-c[0]));
-    const float gg    = 1.0f / (1.0f + expf(-c[1]));
-    const float b     = 1.0f / (1.0f + expf(-c[2]));
-    return make_float4(sigma, r, gg, b);
+// Output activation spread over the wave: the raw outputs of sample s sit in
+// lane (0, s) (density output 0, colour outputs 0..2); lane (g, s) takes
+// channel g (g = 0: sigma = exp, g = 1..3: sigmoid of colour g - 1), so each
+// lane evaluates one transcendental and the 16 samples leave in one 256-byte
+// store.
+__device__ __forceinline__ float field_channel(const floatx4 o, const floatx4 c, uint32_t grp, uint32_t s16) {
+    const float v0 = __shfl(o[0], (int)s16, 64);
+    const float v1 = __shfl(c[0], (int)s16, 64);
+    const float v2 = __shfl(c[1], (int)s16, 64);
+    const float v3 = __shfl(c[2], (int)s16, 64);
+    const float x  = grp == 0u ? v0 : grp == 1u ? v1 : grp == 2u ? v2 : v3;
+    return grp == 0u ? __expf(x) : __frcp_rn(1.0f + __expf(-x));
 }
 
 // ---------------------------------------------------------------- kernels
@@ -162,7 +168,35 @@ __global__ __launch_bounds__(kBlockThreads) void k_field_forward(GridParams g, c
         if (in.features_out && s < n) *reinterpret_cast<half8_t*>(in.features_out + (uint64_t)s * 32u + 8u * grp) = x;
         const floatx4 o = density_mlp(fd, x);
         const floatx4 c = color_mlp(fc, color_input(o, d, grp));
-        if (grp == 0u && s < n) out[s] = field_output(o, c);
+        const float v = field_channel(o, c, grp, s16);
+        if (s < n) reinterpret_cast<float*>(out)[4ull * s + grp] = v;
+    }
+}
+
+// MLP pass on given encodings: lane (g, s) loads features 8g..8g+7 of
+// sample s (one 16-byte load), the B operand of the density MLP.
+__global__ __launch_bounds__(kBlockThreads) void k_field_mlp(const half_t* __restrict__ dparams, const half_t* __restrict__ cparams, const half_t* __restrict__ features, const float* __restrict__ dirs, uint32_t n,
+                                                            float4* __restrict__ out) {
+    __shared__ half_t sp[NERF_EXT_DENSITY_PARAMS + NERF_EXT_COLOR_PARAMS];
+    for (uint32_t i = threadIdx.x; i < NERF_EXT_DENSITY_PARAMS; i += blockDim.x) sp[i] = dparams[i];
+    for (uint32_t i = threadIdx.x; i < NERF_EXT_COLOR_PARAMS; i += blockDim.x) sp[NERF_EXT_DENSITY_PARAMS + i] = cparams[i];
+    __syncthreads();
+    const uint32_t lane = threadIdx.x & 63u, grp = lane >> 4, s16 = lane & 15u;
+    DensityFrags fd;
+    ColorFrags fc;
+    load_density(sp, fd, lane);
+    load_color(sp + NERF_EXT_DENSITY_PARAMS, fc, lane);
+    const uint32_t tiles  = (n + 15u) / 16u;
+    const uint32_t nwaves = gridDim.x * kBlockWaves;
+    for (uint32_t tile = blockIdx.x * kBlockWaves + (threadIdx.x >> 6); tile < tiles; tile += nwaves) {
+        const uint32_t s = tile * 16u + s16;
+        const uint32_t q = s < n ? s : n - 1u;
+        const half8_t x  = *reinterpret_cast<const half8_t*>(features + (uint64_t)q * 32u + 8u * grp);
+        const float d[3] = {dirs[3ull * q], dirs[3ull * q + 1u], dirs[3ull * q + 2u]};
+        const floatx4 o  = density_mlp(fd, x);
+        const floatx4 c  = color_mlp(fc, color_input(o, d, grp));
+        const float v = field_channel(o, c, grp, s16);
+        if (s < n) reinterpret_cast<float*>(out)[4ull * s + grp] = v;
     }
 }
 
@@ -270,6 +304,15 @@ NERF_API NerfStatus nerf_ext_density_forward(const NerfExtGridDesc* grid, const 
     if (n == 0u) return NERF_STATUS_OK;
     NERF_CHECK_ARG(table && params && positions && out, "nerf_ext_density_forward: null pointer");
     NERF_HIP_TRY(launch_density(g, table, (const half_t*)params, positions, nullptr, n, out, (hipStream_t)stream));
+    return NERF_STATUS_OK;
+}
+
+NERF_API NerfStatus nerf_ext_field_mlp(const uint16_t* density_params, const uint16_t* color_params, const uint16_t* features, const float* directions, uint32_t n, float* out, void* stream) {
+    if (n == 0u) return NERF_STATUS_OK;
+    NERF_CHECK_ARG(density_params && color_params && features && directions && out, "nerf_ext_field_mlp: null pointer");
+    NERF_CHECK_ARG(((uintptr_t)features & 15u) == 0u, "nerf_ext_field_mlp: features must be 16-byte aligned");
+    k_field_mlp<<<persistent_blocks(n, 8u), kBlockThreads, 0, (hipStream_t)stream>>>((const half_t*)density_params, (const half_t*)color_params, (const half_t*)features, directions, n, reinterpret_cast<float4*>(out));
+    NERF_LAUNCH_CHECK("k_field_mlp");
     return NERF_STATUS_OK;
 }
 

@@ -57,20 +57,32 @@ __global__ __launch_bounds__(256) void k_init_table(T* table, uint64_t count, ui
     }
 }
 
-// One thread per (point, level); blockIdx.y = level.
+// Workgroup of 16 points x 16 level slots: thread (level l, point p) =
+// threadIdx.x = 16 l + p gathers the 8 corners of one level of one point.
+// The 16 positions are staged in LDS once, and the 16 x 2L features go out
+// through an LDS tile as one contiguous store of the workgroup's points.
+constexpr uint32_t kEncPoints = 16u;
+
 template <typename TableT, typename OutT>
 __global__ __launch_bounds__(256) void k_encode_forward(GridParams g, const TableT* __restrict__ table, const float* __restrict__ pos, uint32_t n, OutT* __restrict__ out) {
-    const uint32_t level = blockIdx.y;
-    const uint32_t i     = blockIdx.x * 256u + threadIdx.x;
-    if (i >= n) return;
-    const float p[3]      = {pos[3ull * i], pos[3ull * i + 1], pos[3ull * i + 2]};
-    const uint32_t N      = g.resolution[level];
-    const bool dense      = g.dense[level] != 0u;
-    float a0, a1;
-    encode_level(g, table, p, level, N, dense, a0, a1);
-    OutT* o = out + (uint64_t)i * (g.n_levels * 2u) + level * 2u;
-    store_value(o, a0);
-    store_value(o + 1, a1);
+    __shared__ float sp[3u * kEncPoints];
+    __shared__ OutT tile[kEncPoints * 2u * NERF_EXT_MAX_LEVELS];
+    const uint32_t first = blockIdx.x * kEncPoints;
+    const uint32_t count = n - first < kEncPoints ? n - first : kEncPoints;
+    if (threadIdx.x < 3u * count) sp[threadIdx.x] = pos[3ull * first + threadIdx.x];
+    __syncthreads();
+    const uint32_t p = threadIdx.x & (kEncPoints - 1u), level = threadIdx.x / kEncPoints;
+    const uint32_t width = 2u * g.n_levels;
+    if (p < count && level < g.n_levels) {
+        const float x[3] = {sp[3u * p], sp[3u * p + 1u], sp[3u * p + 2u]};
+        float a0, a1;
+        encode_level(g, table, x, level, g.resolution[level], g.dense[level] != 0u, a0, a1);
+        store_value(&tile[p * width + 2u * level], a0);
+        store_value(&tile[p * width + 2u * level + 1u], a1);
+    }
+    __syncthreads();
+    OutT* o = out + (uint64_t)first * width;
+    for (uint32_t i = threadIdx.x; i < count * width; i += blockDim.x) o[i] = tile[i];
 }
 
 __global__ __launch_bounds__(256) void k_encode_indices(GridParams g, const float* __restrict__ pos, uint32_t n, uint32_t* __restrict__ indices, float* __restrict__ weights) {
@@ -131,7 +143,7 @@ NERF_API NerfStatus nerf_ext_encode_forward(const NerfExtGridDesc* grid, const v
     if (n == 0u) return NERF_STATUS_OK;
     NERF_CHECK_ARG(table && positions && features, "nerf_ext_encode_forward: null pointer");
     NERF_CHECK_ARG(features_dtype == NERF_EXT_F32 || features_dtype == NERF_EXT_F16, "nerf_ext_encode_forward: bad features dtype");
-    const dim3 grid_dim((n + 255u) / 256u, g.n_levels);
+    const dim3 grid_dim((n + kEncPoints - 1u) / kEncPoints);
     hipStream_t st = (hipStream_t)stream;
     if (g.table_dtype == NERF_EXT_F32) {
         if (features_dtype == NERF_EXT_F32)

@@ -920,3 +920,18 @@ extern "C" void orc_scene_render(const float* gs, uint32_t count, const OrcCamer
         }
     }
 }
+
+// Field MLPs on given features (rounded to fp16 inside) and unit directions:
+// out [n][4] = (sigma = exp(raw), r, g, b), the network part of field_point.
+extern "C" void orc_field_mlp(const uint16_t* dparams, const uint16_t* cparams, const float* features, const float* dirs, uint32_t n, float* out) {
+    for (uint32_t i = 0; i < n; ++i) {
+        float o[16], rgb[3];
+        density_row(dparams, features + 32ull * i, o);
+        color_row(cparams, o, dirs + 3ull * i, rgb);
+        float* out4 = out + 4ull * i;
+        out4[0]     = expf(o[0]);
+        out4[1]     = rgb[0];
+        out4[2]     = rgb[1];
+        out4[3]     = rgb[2];
+    }
+}

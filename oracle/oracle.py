@@ -85,6 +85,7 @@ _PROTOS = {
     "orc_adam": (C.c_int, [_P, _P, _P, _P, _U64, _F, _F, _F, _F, _F, _F, _F, _U32, _U32, C.c_double, C.c_int]),
     "orc_train_rays": (None, [C.POINTER(OrcCamera), _P, _P, _U32, _P, _U32, _U32, _U32, _P, _P, _P, _P, _P, _U32]),
     "orc_train_camera": (_U32, [_U32, _U32]),
+    "orc_field_mlp": (None, [_P, _P, _P, _P, _U32, _P]),
     "orc_scene_render": (None, [_P, _U32, C.POINTER(OrcCamera), _P, _U32, _P]),
     "orc_render_rays": (None, [C.POINTER(OrcModel), C.POINTER(OrcCamera), _P, _U32, _P, _U32, _F, _P, _P, _U32, _P, _P, _P, _U32]),
 }
@@ -376,4 +377,13 @@ def scene_render(gaussians: np.ndarray, cam: OrcCamera, steps: int, aabb=(0, 0, 
     box = np.array(aabb, np.float32)
     out = np.empty((cam.height, cam.width), np.uint32)
     lib().orc_scene_render(_p(g), g.shape[0], C.byref(cam), _p(box), steps, _p(out))
+    return out
+
+
+def field_mlp(dparams_bits, cparams_bits, features, dirs) -> np.ndarray:
+    """Field MLPs on [n][32] features (fp16-rounded inside) and [n][3] unit directions -> [n][4]."""
+    features = np.ascontiguousarray(features, np.float32)
+    dirs = np.ascontiguousarray(dirs, np.float32)
+    out = np.empty((features.shape[0], 4), np.float32)
+    lib().orc_field_mlp(_p(dparams_bits), _p(cparams_bits), _p(features), _p(dirs), features.shape[0], _p(out))
     return out

@@ -91,3 +91,19 @@ def test_field_forward(log2_t, dtype):
     dp, cp = host_params(model)
     want = orc.field_forward(oracle_grid(desc), host_table(model), dp, cp, pos, dirs)
     assert_rel(d_o.numpy(), want, what="field forward")
+
+
+@pytest.mark.parametrize("n", [65536, 1000])
+def test_field_mlp_on_features(n):
+    announce(f"field mlp on features n={n}")
+    rng = np.random.default_rng(11)
+    feats = rng.uniform(-1.0, 1.0, size=(n, 32)).astype(np.float16)
+    dirs = unit_dirs(n, seed=12)
+    dp = orc.f32_to_f16_bits(orc.mlp_init(0))
+    cp = orc.f32_to_f16_bits(orc.mlp_init(1))
+    d_f, d_d, d_o = DeviceArray.from_numpy(feats), DeviceArray.from_numpy(dirs), DeviceArray((n, 4), np.float32)
+    d_dp, d_cp = DeviceArray.from_numpy(dp), DeviceArray.from_numpy(cp)
+    L.call("nerf_ext_field_mlp", d_dp.ptr, d_cp.ptr, d_f.ptr, d_d.ptr, n, d_o.ptr, None)
+    synchronize()
+    want = orc.field_mlp(dp, cp, feats.astype(np.float32), dirs)
+    assert_rel(d_o.numpy(), want, what="field mlp")

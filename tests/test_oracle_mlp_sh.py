@@ -62,3 +62,17 @@ def test_sh4_axis_values(orc):
     np.testing.assert_allclose(y[1, 3], -c1, rtol=1e-6)                                # Y11 = -c x (Condon-Shortley)
     np.testing.assert_allclose(y[2, 1], -c1, rtol=1e-6)                                # Y1-1 = -c y
     np.testing.assert_allclose(y[1, 8], 0.25 * np.sqrt(15 / np.pi), rtol=1e-6)         # Y22(x=1)
+
+
+def test_field_mlp_composes_with_encode(orc):
+    """field_mlp(encode(x), d) reproduces field_forward(x, d) exactly."""
+    g = orc.make_grid(16, 12, 0)
+    table = orc.uniform_fill(0x7ab1e, 5, 16 * 4096 * 2, -0.5, 0.5)
+    rng = np.random.default_rng(3)
+    pos = rng.random((500, 3), dtype=np.float32)
+    d = rng.normal(size=(500, 3)).astype(np.float32)
+    d /= np.linalg.norm(d, axis=1, keepdims=True)
+    dp = orc.f32_to_f16_bits(orc.mlp_init(0))
+    cp = orc.f32_to_f16_bits(orc.mlp_init(1))
+    feats = orc.encode(g, table, pos)
+    assert np.array_equal(orc.field_mlp(dp, cp, feats, d), orc.field_forward(g, table, dp, cp, pos, d))
