@@ -59,6 +59,13 @@ FIELD_BYTES_PER_SAMPLE = 12 + 16 * 8 * 2 * 2 + 16
 # Algorithmic MLP flops per sample: density 32x64 + 64x16, colour 31x64 +
 # 64x64 + 64x3, two flops per multiply-add.
 FIELD_FLOPS_PER_SAMPLE = 2 * (32 * 64 + 64 * 16) + 2 * (31 * 64 + 64 * 64 + 64 * 3)
+# HBM traffic of the field kernel per sample on this workload, from rocprofv3
+# FETCH_SIZE (x 2.0) + WRITE_SIZE (x 1.0) on one 800x800 render, the factors
+# being what the same counters read on a plain conversion kernel of known
+# size (profiles/field_forward_800x800_hbm_traffic.md): 894.3 GB + 7.8 GB over
+# 486,308,861 samples.  Every 4-byte table gather pulls a whole line from
+# beyond L2, hence the gap to the 540 algorithmic bytes.
+FIELD_TRAFFIC_BYTES_PER_SAMPLE = 1855
 
 
 def build_workload():
@@ -294,7 +301,8 @@ def main() -> int:
                    "rays": rays, "samples_per_render": int(samples), "gpu_ms_per_render": round(gpu_ms, 4), "parallelism": "single GPU"},
         "stages_ms": {k: round(v, 4) for k, v in stage.items()},
         "roofline": {"kernel": "k_field_forward (fused hash encode + density/colour MLP)", "bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved_gbs / HBM_PEAK_GBS, 4), "traffic": None, "mfma_tflops": round(field_tflops, 2), "mfma_frac": round(field_tflops / MFMA_FP16_PEAK_TFS, 4),
+                     "frac": round(achieved_gbs / HBM_PEAK_GBS, 4), "traffic": int(samples * FIELD_TRAFFIC_BYTES_PER_SAMPLE),
+                     "traffic_GBps": round(samples * FIELD_TRAFFIC_BYTES_PER_SAMPLE / field_s / 1e9, 1), "mfma_tflops": round(field_tflops, 2), "mfma_frac": round(field_tflops / MFMA_FP16_PEAK_TFS, 4),
                      "bytes_per_sample": FIELD_BYTES_PER_SAMPLE, "flops_per_sample": FIELD_FLOPS_PER_SAMPLE},
         "device": {"name": info.name.decode(), "arch": info.arch.decode(), "cus": info.compute_units},
     }
