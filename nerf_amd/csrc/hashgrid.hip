@@ -57,14 +57,15 @@ __global__ __launch_bounds__(256) void k_init_table(T* table, uint64_t count, ui
     }
 }
 
-// Workgroup of 16 points x 16 level slots: thread (level l, point p) =
+// Tile encode, for tables too large for the level split: workgroup of 16
+// points x 16 level slots, thread (level l, point p) =
 // threadIdx.x = 16 l + p gathers the 8 corners of one level of one point.
 // The 16 positions are staged in LDS once, and the 16 x 2L features go out
 // through an LDS tile as one contiguous store of the workgroup's points.
 constexpr uint32_t kEncPoints = 16u;
 
 template <typename TableT, typename OutT>
-__global__ __launch_bounds__(256) void k_encode_forward(GridParams g, const TableT* __restrict__ table, const float* __restrict__ pos, uint32_t n, OutT* __restrict__ out) {
+__global__ __launch_bounds__(256) void k_encode_tile(GridParams g, const TableT* __restrict__ table, const float* __restrict__ pos, uint32_t n, OutT* __restrict__ out) {
     __shared__ float sp[3u * kEncPoints];
     __shared__ OutT tile[kEncPoints * 2u * NERF_EXT_MAX_LEVELS];
     const uint32_t first = blockIdx.x * kEncPoints;
@@ -83,6 +84,40 @@ __global__ __launch_bounds__(256) void k_encode_forward(GridParams g, const Tabl
     __syncthreads();
     OutT* o = out + (uint64_t)first * width;
     for (uint32_t i = threadIdx.x; i < count * width; i += blockDim.x) o[i] = tile[i];
+}
+
+// XCD-aware encode.  Workgroup b runs on XCD b % 8 (the dispatcher's round
+// robin) and gathers only the levels of pair b % 8 (levels 2x, 2x + 1), so
+// each XCD's L2 holds two levels of the table rather than all of them; the
+// workgroups of one XCD stride over the points, one point per thread, and
+// each thread writes its 4 features as one vector store.  The placement is
+// a locality choice only: any workgroup-to-XCD mapping gives the same
+// result.
+template <typename TableT, typename OutT>
+__global__ __launch_bounds__(256) void k_encode_split(GridParams g, const TableT* __restrict__ table, const float* __restrict__ pos, uint32_t n, OutT* __restrict__ out) {
+    const uint32_t pair = blockIdx.x & 7u, slot = blockIdx.x >> 3, slots = gridDim.x >> 3;
+    const uint32_t l0 = 2u * pair, l1 = l0 + 1u;
+    if (l0 >= g.n_levels) return;  // uniform per workgroup
+    const bool has1   = l1 < g.n_levels;
+    const uint32_t N0 = g.resolution[l0], N1 = has1 ? g.resolution[l1] : 1u;
+    const bool d0 = g.dense[l0] != 0u, d1 = has1 && g.dense[l1] != 0u;
+    const uint32_t width = 2u * g.n_levels;
+    for (uint32_t i = slot * blockDim.x + threadIdx.x; i < n; i += slots * blockDim.x) {
+        const float x[3] = {pos[3ull * i], pos[3ull * i + 1], pos[3ull * i + 2]};
+        float a0, a1, b0 = 0.0f, b1 = 0.0f;
+        encode_level(g, table, x, l0, N0, d0, a0, a1);
+        if (has1) encode_level(g, table, x, l1, N1, d1, b0, b1);
+        OutT* o = out + (uint64_t)i * width + 2u * l0;
+        if (has1) {
+            store_value(o, a0);
+            store_value(o + 1, a1);
+            store_value(o + 2, b0);
+            store_value(o + 3, b1);
+        } else {
+            store_value(o, a0);
+            store_value(o + 1, a1);
+        }
+    }
 }
 
 __global__ __launch_bounds__(256) void k_encode_indices(GridParams g, const float* __restrict__ pos, uint32_t n, uint32_t* __restrict__ indices, float* __restrict__ weights) {
@@ -143,19 +178,29 @@ NERF_API NerfStatus nerf_ext_encode_forward(const NerfExtGridDesc* grid, const v
     if (n == 0u) return NERF_STATUS_OK;
     NERF_CHECK_ARG(table && positions && features, "nerf_ext_encode_forward: null pointer");
     NERF_CHECK_ARG(features_dtype == NERF_EXT_F32 || features_dtype == NERF_EXT_F16, "nerf_ext_encode_forward: bad features dtype");
-    const dim3 grid_dim((n + kEncPoints - 1u) / kEncPoints);
     hipStream_t st = (hipStream_t)stream;
+    // Level split when two levels of the table fit in half of one XCD's L2
+    // (4 MiB); otherwise every workgroup gathers all levels.
+    const uint64_t pair_bytes = 2ull * g.table_size * g.n_features * (g.table_dtype == NERF_EXT_F32 ? 4u : 2u);
+    const bool split          = pair_bytes <= (2ull << 20);
+    const uint32_t per_xcd    = (n + 255u) / 256u;
+    const uint32_t cap        = device_cu_count() / 8u * 8u;  // 8 workgroups per CU of one XCD
+    const dim3 grid_dim = split ? dim3(8u * (per_xcd < cap ? per_xcd : (cap > 0u ? cap : 1u))) : dim3((n + kEncPoints - 1u) / kEncPoints);
+#define NERF_ENC(TT, OT)                                                                                                   \
+    do {                                                                                                                   \
+        if (split)                                                                                                         \
+            k_encode_split<TT, OT><<<grid_dim, 256, 0, st>>>(g, (const TT*)table, positions, n, (OT*)features);            \
+        else                                                                                                               \
+            k_encode_tile<TT, OT><<<grid_dim, 256, 0, st>>>(g, (const TT*)table, positions, n, (OT*)features);             \
+    } while (0)
     if (g.table_dtype == NERF_EXT_F32) {
-        if (features_dtype == NERF_EXT_F32)
-            k_encode_forward<float, float><<<grid_dim, 256, 0, st>>>(g, (const float*)table, positions, n, (float*)features);
-        else
-            k_encode_forward<float, half_t><<<grid_dim, 256, 0, st>>>(g, (const float*)table, positions, n, (half_t*)features);
+        if (features_dtype == NERF_EXT_F32) NERF_ENC(float, float);
+        else NERF_ENC(float, half_t);
     } else {
-        if (features_dtype == NERF_EXT_F32)
-            k_encode_forward<half_t, float><<<grid_dim, 256, 0, st>>>(g, (const half_t*)table, positions, n, (float*)features);
-        else
-            k_encode_forward<half_t, half_t><<<grid_dim, 256, 0, st>>>(g, (const half_t*)table, positions, n, (half_t*)features);
+        if (features_dtype == NERF_EXT_F32) NERF_ENC(half_t, float);
+        else NERF_ENC(half_t, half_t);
     }
+#undef NERF_ENC
     NERF_LAUNCH_CHECK("k_encode_forward");
     return NERF_STATUS_OK;
 }
