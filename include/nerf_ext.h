@@ -200,9 +200,10 @@ typedef struct NerfExtRenderStats {
     float ms_count;            /* march count pass */
     float ms_scan;             /* exclusive scan of counts */
     float ms_samples;          /* march write pass */
-    float ms_field;            /* fused encode + MLP */
-    float ms_composite;
+    float ms_field;            /* fused encode + MLP, summed over the rounds */
+    float ms_composite;        /* composite rounds and their bookkeeping */
     float ms_total;
+    uint64_t samples_shaded;   /* samples evaluated by the field (rays retire early) */
 } NerfExtRenderStats;
 
 NERF_API NerfStatus nerf_ext_renderer_create(NerfExtRenderer** out);

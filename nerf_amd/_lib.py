@@ -236,6 +236,7 @@ class NerfExtRenderStats(C.Structure):
         ("ms_field", C.c_float),
         ("ms_composite", C.c_float),
         ("ms_total", C.c_float),
+        ("samples_shaded", C.c_uint64),
     ]
 
 

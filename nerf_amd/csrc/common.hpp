@@ -202,6 +202,9 @@ struct FieldInputs {
     // capacity) and an fp16 copy of the hash features [n][32] for training.
     const uint32_t* n_dev;
     half_t* features_out;
+    // Optional (mode B): the j-th sample evaluated is stream sample
+    // sample_index[j], and its output goes to out[sample_index[j]].
+    const uint32_t* sample_index;
     // Mode B positions are world positions inside [bmin, bmax]; the grid
     // encodes the unit cube, so they are mapped by (p - bmin) / (bmax - bmin).
     float bmin[3];

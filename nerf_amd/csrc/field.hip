@@ -153,8 +153,11 @@ __global__ __launch_bounds__(kBlockThreads) void k_field_forward(GridParams g, c
         const uint32_t s = tile * 16u + s16;
         const uint32_t q = s < n ? s : n - 1u;
         float p[3], d[3];
+        uint32_t dst = s;  // output slot
         if constexpr (kFromSamples) {
-            sample_point(in, q, p, d);
+            const uint32_t qs = in.sample_index ? in.sample_index[q] : q;
+            dst               = in.sample_index ? qs : s;
+            sample_point(in, qs, p, d);
         } else {
 #pragma unroll
             for (int a = 0; a < 3; ++a) {
@@ -169,7 +172,7 @@ __global__ __launch_bounds__(kBlockThreads) void k_field_forward(GridParams g, c
         const floatx4 o = density_mlp(fd, x);
         const floatx4 c = color_mlp(fc, color_input(o, d, grp));
         const float v = field_channel(o, c, grp, s16);
-        if (s < n) reinterpret_cast<float*>(out)[4ull * s + grp] = v;
+        if (s < n) reinterpret_cast<float*>(out)[4ull * dst + grp] = v;
     }
 }
 

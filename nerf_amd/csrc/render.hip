@@ -115,46 +115,20 @@ __global__ __launch_bounds__(256) void k_march_samples(const NerfExtCamera* __re
     });
 }
 
-// Front-to-back composite with early stop (reference :601-635 plus the
-// stop), one wave per ray over groups of 64 samples: transmittance before
-// each sample is the carried T times the exclusive product of (1 - alpha)
-// across the group; the first sample after which T falls below t_stop is the
-// last one composited.
-__global__ __launch_bounds__(256) void k_composite(uint32_t n_rays, const uint32_t* __restrict__ counts, const uint32_t* __restrict__ offsets, const float2* __restrict__ samples, const float4* __restrict__ field, float t_stop, float3 bg,
-    uint32_t* __restrict__ rgba8, float* __restrict__ rgb_out) {
-    const uint32_t ray  = blockIdx.x * 4u + (threadIdx.x >> 6);
-    const uint32_t lane = threadIdx.x & 63u;
-    if (ray >= n_rays) return;
-    const uint32_t count = counts[ray];
-    const uint32_t base  = count ? offsets[ray] : 0u;
-    float T = 1.0f, cr = 0.0f, cg = 0.0f, cb = 0.0f;
-    for (uint32_t c0 = 0; c0 < count; c0 += 64u) {
-        const uint32_t i = c0 + lane;
-        const bool valid = i < count;
-        float4 f         = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        float dt         = 0.0f;
-        if (valid) {
-            f  = field[base + i];
-            dt = fmaxf(samples[base + i].y, 0.0f);
-        }
-        const float a     = valid ? 1.0f - __expf(-(f.x * dt)) : 0.0f;
-        const float incl  = wave::inclusive_product(1.0f - a);
-        float excl        = __shfl_up(incl, 1, 64);
-        excl              = lane == 0u ? 1.0f : excl;
-        const float Ti    = T * excl;
-        const uint64_t st = __ballot(valid && T * incl < t_stop);
-        const uint32_t last = st ? (uint32_t)__ffsll((long long)st) - 1u : 63u;
-        const float w     = lane <= last ? Ti * a : 0.0f;
-        cr += w * f.y;
-        cg += w * f.z;
-        cb += w * f.w;
-        T *= wave::broadcast(incl, last);
-        if (st) break;
-    }
-    cr = wave::sum(cr);
-    cg = wave::sum(cg);
-    cb = wave::sum(cb);
-    if (lane != 0u) return;
+__global__ void k_fill_u32(uint32_t* __restrict__ p, uint32_t n, uint32_t v) {
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) p[i] = v;
+}
+
+// -------------------------------------------------------------- rounds
+// Shading and compositing run in rounds over slices of each ray's sample
+// stream: round r shades samples [S_r, S_r + K_r) of every active ray
+// (K = 256, 256, 512, ...: every S_r is a multiple of 64), composites them
+// front to back onto the ray's carried (T, C) (reference :601-635) and
+// retires the rays whose transmittance fell below t_stop or whose samples
+// are exhausted.  Only active rays are shaded: an opaque surface ends a ray's
+// field work within the round it is reached.
+
+__device__ __forceinline__ void write_pixel(uint32_t ray, float cr, float cg, float cb, float T, float3 bg, uint32_t* __restrict__ rgba8, float* __restrict__ rgb_out) {
     const float r = cr + T * bg.x, g = cg + T * bg.y, b = cb + T * bg.z;
     if (rgb_out) {
         rgb_out[3ull * ray]      = r;
@@ -165,6 +139,121 @@ __global__ __launch_bounds__(256) void k_composite(uint32_t n_rays, const uint32
     const uint32_t ug = (uint32_t)rintf(fminf(1.0f, fmaxf(0.0f, g)) * 255.0f);
     const uint32_t ub = (uint32_t)rintf(fminf(1.0f, fmaxf(0.0f, b)) * 255.0f);
     rgba8[ray]        = (255u << 24) | (ub << 16) | (ug << 8) | ur;
+}
+
+// Rays without samples get the background; the others start the first
+// round's list (wave-aggregated appends) with T = 1, C = 0.
+__global__ __launch_bounds__(256) void k_round_init(uint32_t n_rays, const uint32_t* __restrict__ counts, float3 bg, uint32_t* __restrict__ rgba8, float* __restrict__ rgb_out, float4* __restrict__ state,
+                                                   uint32_t* __restrict__ list, uint32_t* __restrict__ n_active) {
+    const uint32_t ray = blockIdx.x * 256u + threadIdx.x;
+    const bool valid   = ray < n_rays;
+    const bool take    = valid && counts[ray] > 0u;
+    const uint64_t m   = __ballot(take);
+    const uint32_t lane = threadIdx.x & 63u;
+    uint32_t base       = 0u;
+    const uint32_t lead = m ? (uint32_t)__ffsll((long long)m) - 1u : 0u;
+    if (m && lane == lead) base = atomicAdd(n_active, (uint32_t)__popcll(m));
+    base = (uint32_t)__shfl((int)base, (int)lead, 64);
+    if (take) {
+        list[base + wave::rank_below(m)] = ray;
+        state[ray]                       = make_float4(1.0f, 0.0f, 0.0f, 0.0f);
+    } else if (valid) {
+        write_pixel(ray, 0.0f, 0.0f, 0.0f, 1.0f, bg, rgba8, rgb_out);
+    }
+}
+
+// Samples of this round per list slot (zero past the active count, so the
+// scan runs over a fixed length); also clears the next round's counter.
+__global__ __launch_bounds__(256) void k_round_counts(uint32_t n_slots, const uint32_t* __restrict__ list, const uint32_t* __restrict__ n_active, const uint32_t* __restrict__ counts, uint32_t S, uint32_t K, uint32_t* __restrict__ cnt,
+                                                     uint32_t* __restrict__ n_next) {
+    const uint32_t a = blockIdx.x * 256u + threadIdx.x;
+    if (a == 0u) *n_next = 0u;
+    if (a >= n_slots) return;
+    uint32_t v = 0u;
+    if (a < *n_active) {
+        const uint32_t c = counts[list[a]];
+        v                = c > S ? min(K, c - S) : 0u;
+    }
+    cnt[a] = v;
+}
+
+// Stream indices of this round's samples, slot by slot (one wave per slot).
+__global__ __launch_bounds__(256) void k_round_list(const uint32_t* __restrict__ list, const uint32_t* __restrict__ n_active, const uint32_t* __restrict__ offsets, uint32_t S, const uint32_t* __restrict__ cnt,
+                                                   const uint32_t* __restrict__ off, uint32_t* __restrict__ qlist) {
+    const uint32_t lane = threadIdx.x & 63u, nw = gridDim.x * 4u;
+    const uint32_t n    = *n_active;
+    for (uint32_t a = blockIdx.x * 4u + (threadIdx.x >> 6); a < n; a += nw) {
+        const uint32_t q0 = offsets[list[a]] + S, dst = off[a], m = cnt[a];
+        for (uint32_t k = lane; k < m; k += 64u) qlist[dst + k] = q0 + k;
+    }
+}
+
+// One wave per active ray: composite samples [S, min(count, S + K)) in
+// groups of 64 (transmittance = carried T x exclusive product of 1 - alpha;
+// the first sample after which T < t_stop is the last one composited), then
+// write the pixel or carry (T, C) into the next round.  Kept rays are
+// buffered one per lane and appended 64 at a time.
+__global__ __launch_bounds__(256) void k_round_composite(const uint32_t* __restrict__ list, const uint32_t* __restrict__ n_active, const uint32_t* __restrict__ counts, const uint32_t* __restrict__ offsets,
+                                                        const float2* __restrict__ samples, const float4* __restrict__ field, uint32_t S, uint32_t K, float t_stop, float3 bg, float4* __restrict__ state,
+                                                        uint32_t* __restrict__ rgba8, float* __restrict__ rgb_out, uint32_t* __restrict__ next_list, uint32_t* __restrict__ n_next) {
+    const uint32_t lane = threadIdx.x & 63u, nw = gridDim.x * 4u;
+    const uint32_t n    = *n_active;
+    uint32_t kept_ray   = 0u, n_kept = 0u;  // lane j holds the j-th kept ray
+    for (uint32_t a = blockIdx.x * 4u + (threadIdx.x >> 6); a < n; a += nw) {
+        const uint32_t ray   = list[a];
+        const uint32_t count = counts[ray];
+        const uint32_t base  = offsets[ray];
+        const uint32_t end   = min(count, S + K);
+        const float4 st0     = state[ray];
+        float T = st0.x, cr = 0.0f, cg = 0.0f, cb = 0.0f;
+        bool stopped = false;
+        for (uint32_t c0 = S; c0 < end; c0 += 64u) {
+            const uint32_t i = c0 + lane;
+            const bool valid = i < end;
+            float4 f         = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            float dt         = 0.0f;
+            if (valid) {
+                f  = field[base + i];
+                dt = fmaxf(samples[base + i].y, 0.0f);
+            }
+            const float al      = valid ? 1.0f - __expf(-(f.x * dt)) : 0.0f;
+            const float incl    = wave::inclusive_product(1.0f - al);
+            float excl          = __shfl_up(incl, 1, 64);
+            excl                = lane == 0u ? 1.0f : excl;
+            const uint64_t stop = __ballot(valid && T * incl < t_stop);
+            const uint32_t last = stop ? (uint32_t)__ffsll((long long)stop) - 1u : 63u;
+            const float w       = lane <= last ? T * excl * al : 0.0f;
+            cr += w * f.y;
+            cg += w * f.z;
+            cb += w * f.w;
+            T *= wave::broadcast(incl, last);
+            if (stop) {
+                stopped = true;
+                break;
+            }
+        }
+        cr = st0.y + wave::sum(cr);
+        cg = st0.z + wave::sum(cg);
+        cb = st0.w + wave::sum(cb);
+        if (stopped || end >= count) {
+            if (lane == 0u) write_pixel(ray, cr, cg, cb, T, bg, rgba8, rgb_out);
+        } else {
+            if (lane == 0u) state[ray] = make_float4(T, cr, cg, cb);
+            if (lane == n_kept) kept_ray = ray;
+            if (++n_kept == 64u) {
+                uint32_t at = 0u;
+                if (lane == 0u) at = atomicAdd(n_next, 64u);
+                next_list[(uint32_t)__shfl((int)at, 0, 64) + lane] = kept_ray;
+                n_kept = 0u;
+            }
+        }
+    }
+    if (n_kept) {
+        uint32_t at = 0u;
+        if (lane == 0u) at = atomicAdd(n_next, n_kept);
+        at = (uint32_t)__shfl((int)at, 0, 64);
+        if (lane < n_kept) next_list[at + lane] = kept_ray;
+    }
 }
 
 }  // namespace
@@ -262,6 +351,9 @@ hipError_t exclusive_scan_u32(const uint32_t* in, uint32_t* out, uint32_t n, uin
 }  // namespace nerf_hip
 
 // ----------------------------------------------------------------- renderer
+constexpr uint32_t kFirstRound = 256u;  // samples per ray in the first round (a multiple of 64)
+constexpr uint32_t kMaxRounds  = 24u;   // K doubles from 256: covers any max_steps < 2^24
+
 struct NerfExtRenderer {
     template <typename T>
     struct Buf {
@@ -290,7 +382,13 @@ struct NerfExtRenderer {
     Buf<float2> samples;
     Buf<uint32_t> sample_ray;
     Buf<float4> field;
+    // rounds
+    Buf<float4> state;                 // per ray (T, C.rgb)
+    Buf<uint32_t> list[2], n_active;   // active rays of this / the next round, and their counts
+    Buf<uint32_t> cnt, off, qlist;     // samples per slot, their offsets, stream indices
+    Buf<unsigned long long> round_total;
     hipEvent_t ev[6] = {};
+    hipEvent_t fev[2 * kMaxRounds] = {};
     unsigned long long* host_total = nullptr;
 
     ~NerfExtRenderer() {
@@ -303,6 +401,16 @@ struct NerfExtRenderer {
         samples.release();
         sample_ray.release();
         field.release();
+        state.release();
+        list[0].release();
+        list[1].release();
+        n_active.release();
+        cnt.release();
+        off.release();
+        qlist.release();
+        round_total.release();
+        for (hipEvent_t& e : fev)
+            if (e) (void)hipEventDestroy(e);
         for (hipEvent_t& e : ev)
             if (e) (void)hipEventDestroy(e);
         if (host_total) (void)hipHostFree(host_total);
@@ -320,6 +428,13 @@ NERF_API NerfStatus nerf_ext_renderer_create(NerfExtRenderer** out) {
     if (!r) {
         set_error("nerf_ext_renderer_create: out of host memory");
         return NERF_STATUS_FAILURE;
+    }
+    for (hipEvent_t& e : r->fev) {
+        const hipError_t err = hipEventCreate(&e);
+        if (err != hipSuccess) {
+            delete r;
+            return hip_fail(err, "hipEventCreate");
+        }
     }
     for (hipEvent_t& e : r->ev) {
         const hipError_t err = hipEventCreate(&e);
@@ -414,7 +529,6 @@ NERF_API NerfStatus nerf_ext_render(NerfExtRenderer* R, const NerfExtRenderDesc*
     NERF_HIP_TRY(R->field.reserve(n_samples));
 
     if (timed) NERF_HIP_TRY(hipEventRecord(R->ev[3], st));
-    const uint32_t wave_blocks = (n_rays + 3u) / 4u;  // one wave per ray
     k_march_samples<<<(n_rays + 256u / kMarchGroup - 1u) / (256u / kMarchGroup), 256, 0, st>>>(R->cams.ptr, ppv, n_rays, occ, d->max_steps, R->rays.ptr, R->counts.ptr, R->offsets.ptr, R->samples.ptr, R->sample_ray.ptr);
     NERF_LAUNCH_CHECK("k_march_samples");
     if (timed) NERF_HIP_TRY(hipEventRecord(R->ev[4], st));
@@ -427,33 +541,79 @@ NERF_API NerfStatus nerf_ext_render(NerfExtRenderer* R, const NerfExtRenderDesc*
         in.bmax[a] = o.aabb_max[a];
     }
     const FieldWeights w{(const half_t*)d->model->density_params, (const half_t*)d->model->color_params};
-    NERF_HIP_TRY(launch_field(g, d->model->table, w, in, n_samples, R->field.ptr, st));
-    if (timed) NERF_HIP_TRY(hipEventRecord(R->ev[5], st));
-    k_composite<<<wave_blocks, 256, 0, st>>>(n_rays, R->counts.ptr, R->offsets.ptr, R->samples.ptr, R->field.ptr, d->min_transmittance, make_float3(d->background[0], d->background[1], d->background[2]), rgba8, rgb_f32);
-    NERF_LAUNCH_CHECK("k_composite");
+    const float3 bg = make_float3(d->background[0], d->background[1], d->background[2]);
+    // Rounds: slices of 256, 256, 512, 1024, ... samples per active ray until
+    // every ray's stream (at most max_steps samples) is covered.
+    uint32_t n_rounds = 0u;
+    uint32_t Ks[kMaxRounds], Ss[kMaxRounds];
+    for (uint64_t S = 0, K = kFirstRound; S < d->max_steps && n_rounds < kMaxRounds; S += K, K = S < kFirstRound ? kFirstRound : S) {
+        Ss[n_rounds] = (uint32_t)S;
+        Ks[n_rounds] = (uint32_t)K;
+        ++n_rounds;
+    }
+    NERF_HIP_TRY(R->state.reserve(n_rays));
+    NERF_HIP_TRY(R->list[0].reserve(n_rays));
+    NERF_HIP_TRY(R->list[1].reserve(n_rays));
+    NERF_HIP_TRY(R->n_active.reserve(2));
+    NERF_HIP_TRY(R->cnt.reserve(n_rays));
+    NERF_HIP_TRY(R->off.reserve(n_rays));
+    NERF_HIP_TRY(R->qlist.reserve(n_samples));
+    NERF_HIP_TRY(R->round_total.reserve(kMaxRounds));
+    in.sample_index = R->qlist.ptr;
+    uint32_t* n_cur  = R->n_active.ptr;
+    uint32_t* n_nxt  = R->n_active.ptr + 1;
+    uint32_t* l_cur  = R->list[0].ptr;
+    uint32_t* l_nxt  = R->list[1].ptr;
+    k_fill_u32<<<1, 64, 0, st>>>(n_cur, 2u, 0u);
+    k_round_init<<<blocks, 256, 0, st>>>(n_rays, R->counts.ptr, bg, rgba8, rgb_f32, R->state.ptr, l_cur, n_cur);
+    NERF_LAUNCH_CHECK("k_round_init");
+    const uint32_t ray_waves = std::min<uint32_t>((n_rays + 3u) / 4u, device_cu_count() * 16u);  // workgroups of one-wave-per-slot kernels
+    for (uint32_t r = 0; r < n_rounds; ++r) {
+        k_round_counts<<<blocks, 256, 0, st>>>(n_rays, l_cur, n_cur, R->counts.ptr, Ss[r], Ks[r], R->cnt.ptr, n_nxt);
+        NERF_HIP_TRY(exclusive_scan_u32(R->cnt.ptr, R->off.ptr, n_rays, R->scan_tmp.ptr, R->round_total.ptr + r, st));
+        k_round_list<<<ray_waves, 256, 0, st>>>(l_cur, n_cur, R->offsets.ptr, Ss[r], R->cnt.ptr, R->off.ptr, R->qlist.ptr);
+        NERF_LAUNCH_CHECK("k_round_list");
+        // The field reads this round's sample count on the device: the low
+        // word of the 64-bit scan total (little-endian; totals < 2^32).
+        in.n_dev = reinterpret_cast<const uint32_t*>(R->round_total.ptr + r);
+        if (timed) NERF_HIP_TRY(hipEventRecord(R->fev[2u * r], st));
+        NERF_HIP_TRY(launch_field(g, d->model->table, w, in, n_samples, R->field.ptr, st));
+        if (timed) NERF_HIP_TRY(hipEventRecord(R->fev[2u * r + 1u], st));
+        k_round_composite<<<ray_waves, 256, 0, st>>>(l_cur, n_cur, R->counts.ptr, R->offsets.ptr, R->samples.ptr, R->field.ptr, Ss[r], Ks[r], d->min_transmittance, bg, R->state.ptr, rgba8, rgb_f32, l_nxt, n_nxt);
+        NERF_LAUNCH_CHECK("k_round_composite");
+        std::swap(l_cur, l_nxt);
+        std::swap(n_cur, n_nxt);
+    }
     if (counts_out) NERF_HIP_TRY(hipMemcpyAsync(counts_out, R->counts.ptr, sizeof(uint32_t) * n_rays, hipMemcpyDeviceToDevice, st));
     if (timed) {
         hipEvent_t end = nullptr;
         NERF_HIP_TRY(hipEventCreate(&end));
         NERF_HIP_TRY(hipEventRecord(end, st));
         NERF_HIP_TRY(hipEventSynchronize(end));
-        float ms[5];
+        float ms[3], field_ms = 0.0f, total_ms = 0.0f;
         NERF_HIP_TRY(hipEventElapsedTime(&ms[0], R->ev[0], R->ev[1]));
         NERF_HIP_TRY(hipEventElapsedTime(&ms[1], R->ev[1], R->ev[2]));
         NERF_HIP_TRY(hipEventElapsedTime(&ms[2], R->ev[3], R->ev[4]));
-        NERF_HIP_TRY(hipEventElapsedTime(&ms[3], R->ev[4], R->ev[5]));
-        NERF_HIP_TRY(hipEventElapsedTime(&ms[4], R->ev[5], end));
-        float total_ms = 0.0f;
+        for (uint32_t r = 0; r < n_rounds; ++r) {
+            float f = 0.0f;
+            NERF_HIP_TRY(hipEventElapsedTime(&f, R->fev[2u * r], R->fev[2u * r + 1u]));
+            field_ms += f;
+        }
         NERF_HIP_TRY(hipEventElapsedTime(&total_ms, R->ev[0], end));
         (void)hipEventDestroy(end);
-        stats->rays         = n_rays;
-        stats->samples      = n_samples;
-        stats->ms_count     = ms[0];
-        stats->ms_scan      = ms[1];
-        stats->ms_samples   = ms[2];
-        stats->ms_field     = ms[3];
-        stats->ms_composite = ms[4];
-        stats->ms_total     = total_ms;
+        std::vector<unsigned long long> totals(n_rounds);
+        NERF_HIP_TRY(hipMemcpy(totals.data(), R->round_total.ptr, sizeof(unsigned long long) * n_rounds, hipMemcpyDeviceToHost));
+        uint64_t shaded = 0;
+        for (unsigned long long t : totals) shaded += t;
+        stats->rays           = n_rays;
+        stats->samples        = n_samples;
+        stats->samples_shaded = shaded;
+        stats->ms_count       = ms[0];
+        stats->ms_scan        = ms[1];
+        stats->ms_samples     = ms[2];
+        stats->ms_field       = field_ms;
+        stats->ms_composite   = total_ms - ms[0] - ms[1] - ms[2] - field_ms;
+        stats->ms_total       = total_ms;
     }
     return NERF_STATUS_OK;
 }
