@@ -97,7 +97,7 @@ struct TrainBuffers {
 };
 
 constexpr uint32_t kDwBlocks   = 256;   // workgroups of the weight-gradient passes
-constexpr uint32_t kBinEntries = 8192;  // table entries per scatter bin (64 KiB of fp32 pairs in LDS)
+constexpr uint32_t kBinEntries = 4096;  // table entries per scatter bin (64 KiB of int64 pairs in LDS)
 constexpr uint32_t kBinBlocks  = 256;   // workgroups of the bin count / fill passes
 constexpr uint32_t kMaxBins    = 16384; // bin counters per workgroup in LDS (64 KiB)
 constexpr uint32_t kMlpParams  = NERF_EXT_DENSITY_PARAMS + NERF_EXT_COLOR_PARAMS;

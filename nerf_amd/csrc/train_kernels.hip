@@ -658,15 +658,46 @@ __global__ __launch_bounds__(256) void k_bin_pass(TrainParams P, GridParams g, c
     }
 }
 
+// One bin per workgroup.  fp32 LDS atomics run at a twelfth of the rate of
+// 64-bit integer ones on gfx950, so the bin is accumulated in fixed point:
+// a first pass over the bin's records finds max |v|, every value is scaled
+// by the power of two 2^e that puts that maximum at 2^40 and rounded to an
+// int64, and the int64 sums (exact, so independent of the order of the
+// records) are scaled back once.  Contributions below 2^-40 of the bin's
+// largest one round to zero.  A non-finite record makes the whole slice
+// NaN, which the gradient statistics report as non-finite.
 // grad points at the first hashed level; entries = hashed levels x T.
 __global__ __launch_bounds__(512) void k_bin_accumulate(const uint32_t* __restrict__ offsets, uint32_t n_blocks, uint32_t n_bins, const unsigned long long* __restrict__ total, const uint32_t* __restrict__ rec_idx, const float2* __restrict__ rec_val,
                                                         uint64_t entries, float2* __restrict__ grad) {
-    __shared__ float acc[2u * kBinEntries];
-    for (uint32_t i = threadIdx.x; i < 2u * kBinEntries; i += blockDim.x) acc[i] = 0.0f;
-    __syncthreads();
+    __shared__ unsigned long long acc[2u * kBinEntries];
+    __shared__ float wmax[16];
+    for (uint32_t i = threadIdx.x; i < 2u * kBinEntries; i += blockDim.x) acc[i] = 0ull;
     const uint32_t bin   = blockIdx.x;
     const uint32_t begin = offsets[(uint64_t)bin * n_blocks];
     const uint32_t end   = bin + 1u < n_bins ? offsets[(uint64_t)(bin + 1u) * n_blocks] : (uint32_t)*total;
+    float mx = 0.0f;  // NaN-propagating max: a non-finite record poisons it
+    for (uint32_t r = begin + threadIdx.x; r < end; r += blockDim.x) {
+        const float2 v = rec_val[r];
+        const float a  = fmaxf(fabsf(v.x), fabsf(v.y));
+        mx             = (a != a || mx != mx) ? __builtin_nanf("") : fmaxf(mx, a);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float other = __shfl_xor(mx, o, 64);
+        mx                = (other != other || mx != mx) ? __builtin_nanf("") : fmaxf(mx, other);
+    }
+    if ((threadIdx.x & 63u) == 0u) wmax[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    mx = 0.0f;
+    for (uint32_t w = 0; w < blockDim.x / 64u; ++w) mx = (wmax[w] != wmax[w] || mx != mx) ? __builtin_nanf("") : fmaxf(mx, wmax[w]);
+    const uint64_t base = (uint64_t)bin * kBinEntries;
+    if (!(mx <= 3.0e38f)) {  // NaN or inf among the records
+        for (uint32_t i = threadIdx.x; i < kBinEntries; i += blockDim.x)
+            if (base + i < entries) grad[base + i] = make_float2(__builtin_nanf(""), __builtin_nanf(""));
+        return;
+    }
+    const int e        = mx > 0.0f ? 39 - ilogbf(mx) : 0;  // mx * 2^e in [2^39, 2^40)
+    const double scale = ldexp(1.0, e);
     // Batches of 8 coalesced record loads per thread are issued before their
     // LDS atomics, so the loads of a batch are in flight together.
     constexpr uint32_t kBatch = 8u;
@@ -682,15 +713,15 @@ __global__ __launch_bounds__(512) void k_bin_accumulate(const uint32_t* __restri
 #pragma unroll
         for (uint32_t k = 0; k < kBatch; ++k) {
             if (r0 + k * blockDim.x + threadIdx.x < end) {
-                atomicAdd(&acc[2u * idx[k]], val[k].x);
-                atomicAdd(&acc[2u * idx[k] + 1u], val[k].y);
+                atomicAdd(&acc[2u * idx[k]], (unsigned long long)llrint((double)val[k].x * scale));
+                atomicAdd(&acc[2u * idx[k] + 1u], (unsigned long long)llrint((double)val[k].y * scale));
             }
         }
     }
     __syncthreads();
-    const uint64_t base = (uint64_t)bin * kBinEntries;
+    const double inv = ldexp(1.0, -e);
     for (uint32_t i = threadIdx.x; i < kBinEntries; i += blockDim.x)
-        if (base + i < entries) grad[base + i] = make_float2(acc[2u * i], acc[2u * i + 1u]);
+        if (base + i < entries) grad[base + i] = make_float2((float)((double)(long long)acc[2u * i] * inv), (float)((double)(long long)acc[2u * i + 1u] * inv));
 }
 
 // Weight-gradient passes.  Group 0: colour hidden (64x64).  Group 1: colour

@@ -59,7 +59,7 @@ NerfStatus trainer_create(const NerfExtTrainDesc* d, const BorrowedModel* borrow
     NerfStatus st = make_grid(&d->grid, g);
     if (st != NERF_STATUS_OK) return st;
     NERF_CHECK_ARG(g.n_levels * g.n_features == 32u, "trainer: the density MLP takes 32 features (16 levels x 2)");
-    NERF_CHECK_ARG((uint64_t)g.n_levels * g.table_size <= (uint64_t)kMaxBins * kBinEntries, "trainer: at most 2^27 table entries (16 levels x 2^23)");
+    NERF_CHECK_ARG((uint64_t)g.n_levels * g.table_size <= (uint64_t)kMaxBins * kBinEntries, "trainer: at most 2^26 table entries (16 levels x 2^22)");
     NERF_CHECK_ARG((uint64_t)d->sample_capacity * g.n_levels * 8u < (1ull << 32), "trainer: sample_capacity x 128 must stay below 2^32 gradient records");
     if (stream) {
         t->stream = stream;
