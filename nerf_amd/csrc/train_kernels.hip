@@ -6,7 +6,7 @@
 // ray sampling + march      :422-533                       k_train_rays, scan, k_train_samples
 // field forward             :1328-1339                     launch_field (field.hip)
 // composite fwd/bwd + loss  :1095-1182 (MSE)               k_composite_train (Huber)
-// MLP backward              :784-909, 1267-1301 (cuBLAS)   k_bwd_dx (+ hash scatter), k_bwd_dw, k_dw_reduce
+// MLP backward              :784-909, 1267-1301 (cuBLAS)   k_bwd_dx (+ hash scatter, dW operands), k_dw_gemm, k_dw_reduce
 // grad stats, Adam          :1447-1554                     k_grad_stats, k_adam_prepare, k_adam
 // end step                  :1495-1512                     k_step_end
 //
@@ -547,33 +547,68 @@ __device__ __forceinline__ void scatter_level(const GridParams& g, float* __rest
 // levels, where runs of consecutive samples share cells, are scattered here
 // with row-combined atomics.  Lane (g, s) holds features 16b + 4g + e of
 // sample s, i.e. levels 2g, 2g+1 (b = 0) and 8+2g, 9+2g (b = 1).
+// Rows 16b + 4g + e, column s16 of a 16-column tile region.
+__device__ __forceinline__ void put16(half_t* L, uint32_t row0, const half4_t v[4], uint32_t s16, uint32_t grp) {
+#pragma unroll
+    for (uint32_t b = 0; b < 4u; ++b)
+#pragma unroll
+        for (uint32_t e = 0; e < 4u; ++e) L[(row0 + 16u * b + 4u * grp + e) * 16u + s16] = v[b][e];
+}
+
+constexpr uint32_t kDxLds = (kMlpParams + kWaves * kStageRows * 16u) * 2u;  // bytes of dynamic LDS
+
 __global__ __launch_bounds__(kThreads) void k_bwd_dx(TrainParams P, GridParams g, const TrainDevState* S, const half_t* __restrict__ dparams, const half_t* __restrict__ cparams, const half_t* __restrict__ features,
                                                      const float4* __restrict__ draw, const float2* __restrict__ samples, const uint32_t* __restrict__ sample_ray, const float4* __restrict__ rays, float* __restrict__ dfeat, uint32_t n_dense,
-                                                     float* __restrict__ table_grad) {
-    __shared__ half_t sp[kMlpParams];
+                                                     float* __restrict__ table_grad, half_t* __restrict__ dw_stage) {
+    extern __shared__ __align__(16) half_t dyn[];
+    half_t* sp = dyn;
     for (uint32_t i = threadIdx.x; i < NERF_EXT_DENSITY_PARAMS; i += blockDim.x) sp[i] = dparams[i];
     for (uint32_t i = threadIdx.x; i < NERF_EXT_COLOR_PARAMS; i += blockDim.x) sp[NERF_EXT_DENSITY_PARAMS + i] = cparams[i];
     __syncthreads();
     const uint32_t n = min(S->n_samples, P.sample_cap);
     const uint32_t lane = threadIdx.x & 63u, grp = lane >> 4, s16 = lane & 15u;
+    half_t* W = dyn + kMlpParams + (threadIdx.x >> 6) * kStageRows * 16u;  // this wave's staging tile
     DensityFrags fd;
     load_density(sp, fd, lane);
     const uint32_t tiles = (n + 15u) / 16u;
     for (uint32_t tile = blockIdx.x * kWaves + (threadIdx.x >> 6); tile < tiles; tile += gridDim.x * kWaves) {
         const uint32_t s = tile * 16u + s16;
-        const uint32_t q = s < n ? s : n - 1u;
+        const bool live  = s < n;
+        const uint32_t q = live ? s : n - 1u;
         float p[3], d[3];
         sample_geometry(samples, sample_ray, rays, P.bmin, P.bmax, q, p, d);
         const half8_t x = *reinterpret_cast<const half8_t*>(features + (uint64_t)q * 32u + 8u * grp);
-        const float4 gr = draw[q];
+        float4 gr       = draw[q];
+        if (!live) gr = make_float4(0.0f, 0.0f, 0.0f, 0.0f);  // padding samples add nothing to the weight gradients
         TileGrad T;
         tile_backward(sp, sp + NERF_EXT_DENSITY_PARAMS, fd, x, d, gr, P.loss_scale, grp, T);
-        const bool live = s < n;
         if (live) {
             float4* o = reinterpret_cast<float4*>(dfeat + (uint64_t)s * 32u);
             o[grp]      = make_float4(T.dx[0][0], T.dx[0][1], T.dx[0][2], T.dx[0][3]);
             o[4u + grp] = make_float4(T.dx[1][0], T.dx[1][1], T.dx[1][2], T.dx[1][3]);
         }
+        // Weight-gradient operands of this tile, neuron-major through LDS,
+        // then one contiguous 15 KB copy to dw_stage.
+        wave_lds_sync();
+        put16(W, kRowDh2, T.dh2, s16, grp);
+        put16(W, kRowH1, T.h1, s16, grp);
+        put16(W, kRowDh1, T.dh1, s16, grp);
+        put16(W, kRowH2, T.h2, s16, grp);
+        put16(W, kRowDhd, T.dhd, s16, grp);
+        put16(W, kRowHd, T.hd, s16, grp);
+#pragma unroll
+        for (uint32_t e = 0; e < 8u; ++e) {  // colour input in logical order; row 31 is the zero pad
+            const int k = logical_k(KMap::ColorIn, 0u, grp, e);
+            W[(kRowXc + (k < 0 ? 31u : (uint32_t)k)) * 16u + s16] = k < 0 ? (half_t)0.0f : T.xc[e];
+            if (8u * grp + e < 16u) W[(kRowDo3 + 8u * grp + e) * 16u + s16] = T.do3[e];
+            W[(kRowX + 8u * grp + e) * 16u + s16] = T.x[e];
+        }
+#pragma unroll
+        for (uint32_t e = 0; e < 4u; ++e) W[(kRowDout + 4u * grp + e) * 16u + s16] = T.dout[e];
+        wave_lds_sync();
+        const uint4* src = reinterpret_cast<const uint4*>(W);
+        uint4* dst       = reinterpret_cast<uint4*>(dw_stage + (uint64_t)tile * kStageRows * 16u);
+        for (uint32_t i = lane; i < kStageRows * 2u; i += 64u) dst[i] = src[i];
         if (n_dense > 0u) {  // uniform: the dense levels are the first n_dense levels
 #pragma unroll
             for (uint32_t b = 0; b < 2u; ++b) {
@@ -724,149 +759,96 @@ __global__ __launch_bounds__(512) void k_bin_accumulate(const uint32_t* __restri
         if (base + i < entries) grad[base + i] = make_float2((float)((double)(long long)acc[2u * i] * inv), (float)((double)(long long)acc[2u * i + 1u] * inv));
 }
 
-// Weight-gradient passes.  Group 0: colour hidden (64x64).  Group 1: colour
-// input (64x32) and output (16x64).  Group 2: density input (64x32) and
-// output (16x64).  Per wave and per 32 samples (two tiles), deltas and
-// activations are written to LDS as [neuron][32 samples]; dW blocks are then
-// MFMAs with the 32 samples on the reduction axis.
-constexpr uint32_t kDwScratch = 5632;  // halfs per wave (largest group)
-
-__device__ __forceinline__ void lds_put_c(half_t* L, const half4_t v[4], uint32_t nblocks, uint32_t col, uint32_t grp) {
-#pragma unroll
-    for (uint32_t b = 0; b < 4u; ++b)
-        if (b < nblocks)
-#pragma unroll
-            for (uint32_t e = 0; e < 4u; ++e) L[(16u * b + 4u * grp + e) * 32u + col] = v[b][e];
+// Weight gradients as one pass of products over samples: dW = sum_s delta_s
+// act_s^T for the five layers, on the operands k_bwd_dx staged per tile.  A
+// wave takes pairs of tiles (32 samples = the k of one 16x16x32 MFMA); lane
+// (r, g) loads row r, samples 8g..8g+7 of the pair, which is both the A
+// fragment (deltas, rows = neurons) and the B fragment (activations, rows =
+// inputs).  40 accumulator blocks: colour hidden 16, colour input 8 + output
+// 4, density input 8 + output 4.  The 4 waves of a workgroup are reduced in
+// LDS in a fixed order, one partial per workgroup.
+__device__ __forceinline__ half8_t stage_frag(const half_t* __restrict__ stage, uint32_t tiles, uint32_t pair, uint32_t row0, uint32_t lane) {
+    const uint32_t r = lane & 15u, g = lane >> 4;
+    const uint32_t tile = 2u * pair + (g >> 1);
+    if (tile >= tiles) return half8_t{};
+    return *reinterpret_cast<const half8_t*>(stage + ((uint64_t)tile * kStageRows + row0 + r) * 16u + 8u * (g & 1u));
 }
 
-__device__ __forceinline__ half8_t lds_row8(const half_t* L, uint32_t row, uint32_t grp) { return *reinterpret_cast<const half8_t*>(L + row * 32u + 8u * grp); }
-
-template <uint32_t kGroup>
-__global__ __launch_bounds__(kThreads) void k_bwd_dw(TrainParams P, const TrainDevState* S, const half_t* __restrict__ dparams, const half_t* __restrict__ cparams, const half_t* __restrict__ features, const float4* __restrict__ draw,
-                                                     const float2* __restrict__ samples, const uint32_t* __restrict__ sample_ray, const float4* __restrict__ rays, float* __restrict__ partials) {
-    __shared__ half_t sp[kMlpParams];
-    __shared__ __align__(16) half_t scratch[kWaves * kDwScratch];
-    for (uint32_t i = threadIdx.x; i < NERF_EXT_DENSITY_PARAMS; i += blockDim.x) sp[i] = dparams[i];
-    for (uint32_t i = threadIdx.x; i < NERF_EXT_COLOR_PARAMS; i += blockDim.x) sp[NERF_EXT_DENSITY_PARAMS + i] = cparams[i];
-    __syncthreads();
-    const uint32_t n = min(S->n_samples, P.sample_cap);
+__global__ __launch_bounds__(kThreads) void k_dw_gemm(TrainParams P, const TrainDevState* S, const half_t* __restrict__ stage, float* __restrict__ partials) {
+    __shared__ float red[kMlpParams];
+    const uint32_t n     = min(S->n_samples, P.sample_cap);
+    const uint32_t tiles = (n + 15u) / 16u, pairs = (tiles + 1u) / 2u;
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u, grp = lane >> 4, s16 = lane & 15u;
-    half_t* L = scratch + wave * kDwScratch;
-    DensityFrags fd;
-    load_density(sp, fd, lane);
-    const half_t* dp = sp;
-    const half_t* cp = sp + NERF_EXT_DENSITY_PARAMS;
-    // Accumulators: group 0 uses 16 blocks (64x64); groups 1 and 2 use 8 + 4.
-    floatx4 acc[16];
+    floatx4 a0[16], a1[12], a2[12];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) acc[i] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-    // LDS regions, rows of 32 halfs (one per sample of the pair):
-    //   group 0: R0 = 64-row delta, R1 = 64-row activation            (4096 halfs)
-    //   group 1/2: R0 = 64-row delta of the input layer, R1 = 32-row input,
-    //              R2 = 16-row delta of the output layer, R3 = 64-row hidden  (5632 halfs)
-    half_t* R0 = L;
-    half_t* R1 = L + 64u * 32u;
-    half_t* R2 = L + 96u * 32u;
-    half_t* R3 = L + 112u * 32u;
-    const uint32_t pairs = (n + 31u) / 32u;
+    for (int i = 0; i < 16; ++i) a0[i] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < 12; ++i) a1[i] = a2[i] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     for (uint32_t pair = blockIdx.x * kWaves + wave; pair < pairs; pair += gridDim.x * kWaves) {
-        wave_lds_sync();
+        half8_t bh1[4], bh2[4], bhd[4], bxc[2], bx[2];
 #pragma unroll
-        for (uint32_t h = 0; h < 2u; ++h) {
-            const uint32_t s   = pair * 32u + 16u * h + s16;
-            const bool valid   = s < n;
-            const uint32_t q   = valid ? s : n - 1u;
-            float p[3], d[3];
-            sample_geometry(samples, sample_ray, rays, P.bmin, P.bmax, q, p, d);
-            const half8_t x = *reinterpret_cast<const half8_t*>(features + (uint64_t)q * 32u + 8u * grp);
-            float4 gr       = draw[q];
-            if (!valid) gr = make_float4(0.0f, 0.0f, 0.0f, 0.0f);  // zero deltas for padding samples
-            TileGrad T;
-            tile_backward(dp, cp, fd, x, d, gr, P.loss_scale, grp, T);
-            const uint32_t col = 16u * h + s16;
-            if constexpr (kGroup == 0u) {
-                lds_put_c(R0, T.dh2, 4u, col, grp);
-                lds_put_c(R1, T.h1, 4u, col, grp);
-            } else if constexpr (kGroup == 1u) {
-                lds_put_c(R0, T.dh1, 4u, col, grp);
+        for (uint32_t i = 0; i < 4u; ++i) {
+            bh1[i] = stage_frag(stage, tiles, pair, kRowH1 + 16u * i, lane);
+            bh2[i] = stage_frag(stage, tiles, pair, kRowH2 + 16u * i, lane);
+            bhd[i] = stage_frag(stage, tiles, pair, kRowHd + 16u * i, lane);
+        }
 #pragma unroll
-                for (uint32_t e = 0; e < 8u; ++e) {  // colour input, logical order; row 31 is the zero pad
-                    const int k = logical_k(KMap::ColorIn, 0u, grp, e);
-                    R1[(k < 0 ? 31u : (uint32_t)k) * 32u + col] = k < 0 ? (half_t)0.0f : T.xc[e];
-                }
+        for (uint32_t i = 0; i < 2u; ++i) {
+            bxc[i] = stage_frag(stage, tiles, pair, kRowXc + 16u * i, lane);
+            bx[i]  = stage_frag(stage, tiles, pair, kRowX + 16u * i, lane);
+        }
 #pragma unroll
-                for (uint32_t e = 0; e < 8u; ++e)
-                    if (8u * grp + e < 16u) R2[(8u * grp + e) * 32u + col] = T.do3[e];
-                lds_put_c(R3, T.h2, 4u, col, grp);
-            } else {
-                lds_put_c(R0, T.dhd, 4u, col, grp);
+        for (uint32_t ob = 0; ob < 4u; ++ob) {
+            const half8_t dh2 = stage_frag(stage, tiles, pair, kRowDh2 + 16u * ob, lane);
+            const half8_t dh1 = stage_frag(stage, tiles, pair, kRowDh1 + 16u * ob, lane);
+            const half8_t dhd = stage_frag(stage, tiles, pair, kRowDhd + 16u * ob, lane);
 #pragma unroll
-                for (uint32_t e = 0; e < 8u; ++e) R1[(8u * grp + e) * 32u + col] = T.x[e];
+            for (uint32_t ib = 0; ib < 4u; ++ib) a0[4u * ob + ib] = mfma16x16x32(dh2, bh1[ib], a0[4u * ob + ib]);
 #pragma unroll
-                for (uint32_t e = 0; e < 4u; ++e) R2[(4u * grp + e) * 32u + col] = T.dout[e];
-                lds_put_c(R3, T.hd, 4u, col, grp);
+            for (uint32_t ib = 0; ib < 2u; ++ib) {
+                a1[2u * ob + ib] = mfma16x16x32(dh1, bxc[ib], a1[2u * ob + ib]);
+                a2[2u * ob + ib] = mfma16x16x32(dhd, bx[ib], a2[2u * ob + ib]);
             }
         }
-        wave_lds_sync();
-        if constexpr (kGroup == 0u) {
+        const half8_t do3  = stage_frag(stage, tiles, pair, kRowDo3, lane);
+        const half8_t dout = stage_frag(stage, tiles, pair, kRowDout, lane);
 #pragma unroll
-            for (uint32_t ob = 0; ob < 4u; ++ob) {
-                const half8_t a = lds_row8(R0, 16u * ob + s16, grp);
-#pragma unroll
-                for (uint32_t ib = 0; ib < 4u; ++ib) acc[4u * ob + ib] = mfma16x16x32(a, lds_row8(R1, 16u * ib + s16, grp), acc[4u * ob + ib]);
-            }
-        } else {
-            // 64 x 32 input layer: 4 x 2 blocks; 16 x 64 output layer: 1 x 4 blocks.
-#pragma unroll
-            for (uint32_t ob = 0; ob < 4u; ++ob) {
-                const half8_t a = lds_row8(R0, 16u * ob + s16, grp);
-#pragma unroll
-                for (uint32_t ib = 0; ib < 2u; ++ib) acc[2u * ob + ib] = mfma16x16x32(a, lds_row8(R1, 16u * ib + s16, grp), acc[2u * ob + ib]);
-            }
-            const half8_t a2 = lds_row8(R2, s16, grp);
-#pragma unroll
-            for (uint32_t ib = 0; ib < 4u; ++ib) acc[8u + ib] = mfma16x16x32(a2, lds_row8(R3, 16u * ib + s16, grp), acc[8u + ib]);
+        for (uint32_t ib = 0; ib < 4u; ++ib) {
+            a1[8u + ib] = mfma16x16x32(do3, bh2[ib], a1[8u + ib]);
+            a2[8u + ib] = mfma16x16x32(dout, bhd[ib], a2[8u + ib]);
         }
     }
-    // Deterministic reduction of the 4 waves in LDS, then one partial per block.
-    __syncthreads();
-    float* red            = reinterpret_cast<float*>(scratch);
-    const uint32_t count  = kGroup == 0u ? 4096u : 3072u;
-    for (uint32_t i = threadIdx.x; i < count; i += blockDim.x) red[i] = 0.0f;
+    // Fixed-order reduction of the 4 waves, in parameter order (density
+    // 0..3071, colour 3072..10239).
+    for (uint32_t i = threadIdx.x; i < kMlpParams; i += blockDim.x) red[i] = 0.0f;
     __syncthreads();
     for (uint32_t w = 0; w < kWaves; ++w) {
         if (wave == w) {
-            if constexpr (kGroup == 0u) {
 #pragma unroll
-                for (uint32_t ob = 0; ob < 4u; ++ob)
+            for (uint32_t e = 0; e < 4u; ++e) {
 #pragma unroll
-                    for (uint32_t ib = 0; ib < 4u; ++ib)
+                for (uint32_t ob = 0; ob < 4u; ++ob) {
+                    const uint32_t o = 16u * ob + 4u * grp + e;
 #pragma unroll
-                        for (uint32_t e = 0; e < 4u; ++e) red[(16u * ob + 4u * grp + e) * 64u + 16u * ib + s16] += acc[4u * ob + ib][e];
-            } else {
+                    for (uint32_t ib = 0; ib < 4u; ++ib) red[NERF_EXT_DENSITY_PARAMS + 2048u + o * 64u + 16u * ib + s16] += a0[4u * ob + ib][e];
 #pragma unroll
-                for (uint32_t ob = 0; ob < 4u; ++ob)
+                    for (uint32_t ib = 0; ib < 2u; ++ib) {
+                        red[NERF_EXT_DENSITY_PARAMS + o * 32u + 16u * ib + s16] += a1[2u * ob + ib][e];
+                        red[o * 32u + 16u * ib + s16] += a2[2u * ob + ib][e];
+                    }
+                }
+                const uint32_t o = 4u * grp + e;
 #pragma unroll
-                    for (uint32_t ib = 0; ib < 2u; ++ib)
-#pragma unroll
-                        for (uint32_t e = 0; e < 4u; ++e) red[(16u * ob + 4u * grp + e) * 32u + 16u * ib + s16] += acc[2u * ob + ib][e];
-#pragma unroll
-                for (uint32_t ib = 0; ib < 4u; ++ib)
-#pragma unroll
-                    for (uint32_t e = 0; e < 4u; ++e) red[2048u + (4u * grp + e) * 64u + 16u * ib + s16] += acc[8u + ib][e];
+                for (uint32_t ib = 0; ib < 4u; ++ib) {
+                    red[NERF_EXT_DENSITY_PARAMS + 6144u + o * 64u + 16u * ib + s16] += a1[8u + ib][e];
+                    red[2048u + o * 64u + 16u * ib + s16] += a2[8u + ib][e];
+                }
             }
         }
         __syncthreads();
     }
-    // Partial layout: [block][10240] in parameter order (density 0..3071, colour 3072..).
     float* out = partials + (uint64_t)blockIdx.x * kMlpParams;
-    for (uint32_t i = threadIdx.x; i < count; i += blockDim.x) {
-        uint32_t dst;
-        if constexpr (kGroup == 0u) dst = NERF_EXT_DENSITY_PARAMS + 2048u + i;                          // colour hidden
-        else if constexpr (kGroup == 1u) dst = NERF_EXT_DENSITY_PARAMS + (i < 2048u ? i : 6144u + (i - 2048u));  // colour input | output
-        else dst = i;                                                                                     // density input | output
-        out[dst] = red[i];
-    }
+    for (uint32_t i = threadIdx.x; i < kMlpParams; i += blockDim.x) out[i] = red[i];
 }
 
 __global__ __launch_bounds__(256) void k_fill_zero(float* __restrict__ p, uint64_t n) {
@@ -982,7 +964,13 @@ hipError_t launch_mlp_backward(const TrainParams& P, const TrainBuffers& B, hipS
     // Dense levels: cleared, then row-combined atomics inside k_bwd_dx.
     const uint64_t dense_elems = (uint64_t)B.n_dense * B.grid.table_size * 2u;
     if (dense_elems) k_fill_zero<<<grid_for(dense_elems, cus * 4u), 256, 0, st>>>(B.table_grad, dense_elems);
-    k_bwd_dx<<<cus * 4u, kThreads, 0, st>>>(P, B.grid, B.state, B.dparams, B.cparams, B.features, B.draw, B.samples, B.sample_ray, B.rays, B.dfeat, B.n_dense, B.table_grad);
+    static bool lds_set = false;  // once per process: the kernel's dynamic LDS exceeds the 64 KiB default
+    if (!lds_set) {
+        const hipError_t e = hipFuncSetAttribute((const void*)k_bwd_dx, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDxLds);
+        if (e != hipSuccess) return e;
+        lds_set = true;
+    }
+    k_bwd_dx<<<cus * 2u, kThreads, kDxLds, st>>>(P, B.grid, B.state, B.dparams, B.cparams, B.features, B.draw, B.samples, B.sample_ray, B.rays, B.dfeat, B.n_dense, B.table_grad, B.dw_stage);
     // Hashed levels: binned.
     if (B.n_bins) {
         k_bin_pass<false><<<kBinBlocks, 256, 0, st>>>(P, B.grid, B.state, B.samples, B.sample_ray, B.rays, B.dfeat, B.n_dense, B.n_bins, B.bin_hist, nullptr, nullptr);
@@ -992,9 +980,7 @@ hipError_t launch_mlp_backward(const TrainParams& P, const TrainBuffers& B, hipS
         k_bin_accumulate<<<B.n_bins, 512, 0, st>>>(B.bin_off, kBinBlocks, B.n_bins, B.bin_total, B.rec_idx, B.rec_val, (uint64_t)(B.grid.n_levels - B.n_dense) * B.grid.table_size,
                                                    reinterpret_cast<float2*>(B.table_grad) + (uint64_t)B.n_dense * B.grid.table_size);
     }
-    k_bwd_dw<0><<<kDwBlocks, kThreads, 0, st>>>(P, B.state, B.dparams, B.cparams, B.features, B.draw, B.samples, B.sample_ray, B.rays, B.dw_partials);
-    k_bwd_dw<1><<<kDwBlocks, kThreads, 0, st>>>(P, B.state, B.dparams, B.cparams, B.features, B.draw, B.samples, B.sample_ray, B.rays, B.dw_partials);
-    k_bwd_dw<2><<<kDwBlocks, kThreads, 0, st>>>(P, B.state, B.dparams, B.cparams, B.features, B.draw, B.samples, B.sample_ray, B.rays, B.dw_partials);
+    k_dw_gemm<<<kDwBlocks, kThreads, 0, st>>>(P, B.state, B.dw_stage, B.dw_partials);
     k_dw_reduce<<<(kMlpParams + 63u) / 64u, 256, 0, st>>>(B.dw_partials, kDwBlocks, B.mlp_grad);
     return hipGetLastError();
 }

@@ -121,6 +121,7 @@ NerfStatus trainer_create(const NerfExtTrainDesc* d, const BorrowedModel* borrow
     NERF_HIP_TRY(alloc(T, B.features, 32ull * P.sample_cap));
     NERF_HIP_TRY(alloc(T, B.draw, P.sample_cap));
     NERF_HIP_TRY(alloc(T, B.dfeat, 32ull * P.sample_cap));
+    NERF_HIP_TRY(alloc(T, B.dw_stage, (uint64_t)(P.sample_cap + 15u) / 16u * kStageRows * 16u));
     B.n_dense = 0u;
     while (B.n_dense < g.n_levels && g.dense[B.n_dense]) ++B.n_dense;
     B.n_bins  = (uint32_t)(((uint64_t)(g.n_levels - B.n_dense) * g.table_size + kBinEntries - 1u) / kBinEntries);
