@@ -33,17 +33,23 @@ struct OccView {
     float bmin[3], bmax[3];
 };
 
-// backend-cuda.cu:338-351 (a null bitfield marks every cell of the box occupied).
-__device__ __forceinline__ bool occupied(const OccView& o, const float p[3]) {
+// Cell index of p in the grid over the box, or wave::kOutside
+// (backend-cuda.cu:338-351).
+__device__ __forceinline__ uint32_t occ_cell(const OccView& o, const float p[3]) {
     const float sx = o.bmax[0] - o.bmin[0], sy = o.bmax[1] - o.bmin[1], sz = o.bmax[2] - o.bmin[2];
     const float rx = (p[0] - o.bmin[0]) / sx, ry = (p[1] - o.bmin[1]) / sy, rz = (p[2] - o.bmin[2]) / sz;
-    if (rx < 0.0f || rx >= 1.0f || ry < 0.0f || ry >= 1.0f || rz < 0.0f || rz >= 1.0f) return false;
-    if (!o.bits) return true;
-    const uint32_t ix  = min(o.res - 1u, (uint32_t)(rx * (float)o.res));
-    const uint32_t iy  = min(o.res - 1u, (uint32_t)(ry * (float)o.res));
-    const uint32_t iz  = min(o.res - 1u, (uint32_t)(rz * (float)o.res));
-    const uint32_t idx = ix + iy * o.res + iz * o.res * o.res;
-    return (o.bits[idx >> 5] >> (idx & 31u)) & 1u;
+    if (rx < 0.0f || rx >= 1.0f || ry < 0.0f || ry >= 1.0f || rz < 0.0f || rz >= 1.0f) return wave::kOutside;
+    const uint32_t ix = min(o.res - 1u, (uint32_t)(rx * (float)o.res));
+    const uint32_t iy = min(o.res - 1u, (uint32_t)(ry * (float)o.res));
+    const uint32_t iz = min(o.res - 1u, (uint32_t)(rz * (float)o.res));
+    return ix + iy * o.res + iz * o.res * o.res;
+}
+
+// backend-cuda.cu:338-351 (a null bitfield marks every cell of the box occupied).
+__device__ __forceinline__ bool occupied(const OccView& o, const float p[3]) {
+    const uint32_t idx = occ_cell(o, p);
+    if (idx == wave::kOutside) return false;
+    return !o.bits || ((o.bits[idx >> 5] >> (idx & 31u)) & 1u);
 }
 
 __device__ __forceinline__ float cone_angle(const NerfExtCamera& c) {
@@ -109,7 +115,7 @@ __global__ __launch_bounds__(256) void k_march_samples(const NerfExtCamera* __re
     const uint32_t view = ray / pixels_per_view;
     const float cone    = cone_angle(cams[view]);
     const uint32_t base = offsets[ray];
-    wave::march<kMarchGroup>(rays[2ull * ray], rays[2ull * ray + 1u], cone, max_steps, count, [&](const float p[3]) { return occupied(occ, p); }, [&](uint32_t k, float tm, float dt) {
+    wave::march<kMarchGroup>(rays[2ull * ray], rays[2ull * ray + 1u], cone, max_steps, count, occ.bits, [&](const float p[3]) { return occ_cell(occ, p); }, [&](uint32_t k, float tm, float dt) {
         samples[base + k]    = make_float2(tm, dt);
         sample_ray[base + k] = ray;
     });

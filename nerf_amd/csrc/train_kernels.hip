@@ -163,14 +163,14 @@ __global__ __launch_bounds__(256) void k_occ_bits(TrainParams P, const TrainDevS
 }
 
 // ---------------------------------------------------------------- sampling
-__device__ __forceinline__ bool occupied_at(const TrainParams& P, const uint32_t* bits, const float p[3]) {
+// Occupancy cell of p (backend-cuda.cu:338-351), or wave::kOutside.
+__device__ __forceinline__ uint32_t occ_cell_at(const TrainParams& P, const float p[3]) {
     const float sx = P.bmax[0] - P.bmin[0], sy = P.bmax[1] - P.bmin[1], sz = P.bmax[2] - P.bmin[2];
     const float rx = (p[0] - P.bmin[0]) / sx, ry = (p[1] - P.bmin[1]) / sy, rz = (p[2] - P.bmin[2]) / sz;
-    if (rx < 0.0f || rx >= 1.0f || ry < 0.0f || ry >= 1.0f || rz < 0.0f || rz >= 1.0f) return false;
+    if (rx < 0.0f || rx >= 1.0f || ry < 0.0f || ry >= 1.0f || rz < 0.0f || rz >= 1.0f) return wave::kOutside;
     const uint32_t res = P.occ_res;
     const uint32_t ix = min(res - 1u, (uint32_t)(rx * (float)res)), iy = min(res - 1u, (uint32_t)(ry * (float)res)), iz = min(res - 1u, (uint32_t)(rz * (float)res));
-    const uint32_t idx = ix + iy * res + iz * res * res;
-    return (bits[idx >> 5] >> (idx & 31u)) & 1u;
+    return ix + iy * res + iz * res * res;
 }
 
 __device__ __forceinline__ float cone_of(const NerfExtCamera& c) {  // :333-337
@@ -179,16 +179,19 @@ __device__ __forceinline__ float cone_of(const NerfExtCamera& c) {  // :333-337
 }
 
 // Random pixel per ray (:438-441), ray, march count, bilinear ground truth
-// composited over white (:471-499).  One wave per ray (wave::march<64>); ray
+// composited over white (:471-499).  kTrainGroup lanes per ray (wave::march); ray
 // slots from n_rays to max_rays get a zero count so the scan over all slots
 // stays valid.
+constexpr uint32_t kTrainGroup = 16u;  // lanes per ray in the training march (4 rays per wave)
+
 __global__ __launch_bounds__(256) void k_train_rays(TrainParams P, const TrainDevState* S, const NerfExtCamera* __restrict__ cams, const uint8_t* __restrict__ images, const uint32_t* __restrict__ bits, float4* __restrict__ rays, float4* __restrict__ gt,
                                                      uint32_t* __restrict__ counts) {
-    const uint32_t lane = threadIdx.x & 63u, nw = gridDim.x * kWaves;
+    constexpr uint32_t kPer = 64u / kTrainGroup;  // rays per wave
+    const uint32_t lane = threadIdx.x & 63u, stride = gridDim.x * kWaves * kPer;
     const uint32_t n_rays = S->n_rays, cam_idx = S->camera, frame = S->frame;
     const NerfExtCamera cam = cams[cam_idx];
     const float cone        = cone_of(cam);
-    for (uint32_t r = blockIdx.x * kWaves + (threadIdx.x >> 6); r < P.max_rays; r += nw) {
+    for (uint32_t r = (blockIdx.x * kWaves + (threadIdx.x >> 6)) * kPer + lane / kTrainGroup; r < P.max_rays; r += stride) {
         uint32_t count = 0u;
         float4 ro = make_float4(0.0f, 0.0f, 0.0f, 0.0f), rd = make_float4(0.0f, 0.0f, 0.0f, 0.0f), g4 = make_float4(1.0f, 1.0f, 1.0f, 0.0f);
         if (r < n_rays) {
@@ -200,7 +203,7 @@ __global__ __launch_bounds__(256) void k_train_rays(TrainParams P, const TrainDe
             if (make_ray(cam, px, pyf, P.bmin, P.bmax, ray)) {
                 ro    = make_float4(ray.o[0], ray.o[1], ray.o[2], ray.tn);
                 rd    = make_float4(ray.d[0], ray.d[1], ray.d[2], ray.tf);
-                count = wave::march<64>(ro, rd, cone, P.max_steps, ~0u, [&](const float p[3]) { return occupied_at(P, bits, p); }, [](uint32_t, float, float) {});
+                count = wave::march<kTrainGroup>(ro, rd, cone, P.max_steps, ~0u, bits, [&](const float p[3]) { return occ_cell_at(P, p); }, [](uint32_t, float, float) {});
             }
             if (count > 0u) {
                 const uint8_t* img = images + (uint64_t)cam_idx * P.width * P.height * 4u;
@@ -225,7 +228,7 @@ __global__ __launch_bounds__(256) void k_train_rays(TrainParams P, const TrainDe
                 g4 = make_float4(c[0] * alpha + (1.0f - alpha), c[1] * alpha + (1.0f - alpha), c[2] * alpha + (1.0f - alpha), alpha);
             }
         }
-        if (lane == 0u) {
+        if (lane % kTrainGroup == 0u) {
             rays[2ull * r]      = ro;
             rays[2ull * r + 1u] = rd;
             gt[r]               = g4;
@@ -236,22 +239,25 @@ __global__ __launch_bounds__(256) void k_train_rays(TrainParams P, const TrainDe
 
 // Writes the samples of every ray whose whole range fits the stream capacity;
 // kept[r] is its count or 0.  The kept rays form a prefix (offsets grow with
-// r), so n_samples = max(offset + count) over kept rays.  One wave per ray.
+// r), so n_samples = max(offset + count) over kept rays.  kTrainGroup lanes
+// per ray.
 __global__ __launch_bounds__(256) void k_train_samples(TrainParams P, TrainDevState* S, const NerfExtCamera* __restrict__ cams, const uint32_t* __restrict__ bits, const float4* __restrict__ rays, const uint32_t* __restrict__ counts,
                                                         const uint32_t* __restrict__ offsets, uint32_t* __restrict__ kept, float2* __restrict__ samples, uint32_t* __restrict__ sample_ray) {
-    const uint32_t lane = threadIdx.x & 63u, nw = gridDim.x * kWaves;
+    constexpr uint32_t kPer = 64u / kTrainGroup;
+    const uint32_t lane = threadIdx.x & 63u, stride = gridDim.x * kWaves * kPer;
     const float cone    = cone_of(cams[S->camera]);
-    for (uint32_t r = blockIdx.x * kWaves + (threadIdx.x >> 6); r < P.max_rays; r += nw) {
+    for (uint32_t r = (blockIdx.x * kWaves + (threadIdx.x >> 6)) * kPer + lane / kTrainGroup; r < P.max_rays; r += stride) {
         const uint32_t count = counts[r];
         const uint32_t base  = offsets[r];
         const bool fits      = count > 0u && (uint64_t)base + count <= (uint64_t)P.sample_cap;
-        if (lane == 0u) kept[r] = fits ? count : 0u;
+        const bool leader    = lane % kTrainGroup == 0u;
+        if (leader) kept[r] = fits ? count : 0u;
         if (!fits) continue;
-        wave::march<64>(rays[2ull * r], rays[2ull * r + 1u], cone, P.max_steps, count, [&](const float p[3]) { return occupied_at(P, bits, p); }, [&](uint32_t k, float tm, float dt) {
+        wave::march<kTrainGroup>(rays[2ull * r], rays[2ull * r + 1u], cone, P.max_steps, count, bits, [&](const float p[3]) { return occ_cell_at(P, p); }, [&](uint32_t k, float tm, float dt) {
             samples[base + k]    = make_float2(tm, dt);
             sample_ray[base + k] = r;
         });
-        if (lane == 0u) {
+        if (leader) {
             atomicMax(&S->n_samples, base + count);
             atomicAdd(&S->n_active, 1u);
         }

@@ -45,18 +45,21 @@ __device__ __forceinline__ uint32_t rank_below(uint64_t mask) {
     return (uint32_t)__popcll(below);
 }
 
+constexpr uint32_t kOutside = 0xFFFFFFFFu;
+
 // Occupancy march of one ray by a group of G lanes (G divides 64; the wave
 // marches 64 / G rays), with the step rule of backend-cuda.cu:450-469.  The
 // lanes of a group run the same scalar recurrence for t, so t and dt are
 // bit-identical to a one-thread march; lane j of the group keeps step i + j of
-// each run of G steps, the G occupancy tests run in parallel, and
-// emit(k, t_mid, dt) is called by the lanes holding the k-th occupied step
-// with k < limit, consecutive k on consecutive lanes.  Returns the number of
-// occupied steps seen (all of them when limit is ~0u).  Larger G shortens a
-// ray's latency chain; smaller G shares each recurrence instruction among
-// more rays.
-template <uint32_t G, typename Occupied, typename Emit>
-__device__ __forceinline__ uint32_t march(float4 ro, float4 rd, float cone, uint32_t max_steps, uint32_t limit, Occupied occupied, Emit emit) {
+// each run of G steps and tests its cell: cell(p) gives the cell index or
+// kOutside, and bit (index & 31) of bits[index >> 5] marks it occupied (a
+// null bitfield marks every cell inside the box).  The loads of run k + 1 are
+// issued before the cells of run k are consumed, so their latency overlaps
+// the recurrence.  emit(k, t_mid, dt) is called by the lanes holding the k-th
+// occupied step with k < limit, consecutive k on consecutive lanes.  Returns
+// the number of occupied steps seen (all of them when limit is ~0u).
+template <uint32_t G, typename Cell, typename Emit>
+__device__ __forceinline__ uint32_t march(float4 ro, float4 rd, float cone, uint32_t max_steps, uint32_t limit, const uint32_t* __restrict__ bits, Cell cell, Emit emit) {
     static_assert(G >= 1u && G <= 64u && 64u % G == 0u, "group size must divide 64");
     const uint32_t lane = lane_id(), j_own = lane % G, shift = lane - j_own;
     const uint64_t group_bits = G == 64u ? ~0ull : ((1ull << G) - 1ull);
@@ -65,25 +68,53 @@ __device__ __forceinline__ uint32_t march(float4 ro, float4 rd, float cone, uint
     const float dt_min = (tf - tn) / (float)max_steps;
     float t = tn;
     uint32_t i = 0u, seen = 0u;
-    while (t < tf && i < max_steps && seen < limit) {
+    // One run of G steps: this lane's step (if any) and its cell word in flight.
+    // The G steps run unconditionally, branch-free: once t reaches tf the
+    // step is clamped to zero, so t stays put and every later step of the run
+    // is marked dead, which leaves t and dt of the live steps bit-identical
+    // to the conditional loop.
+    auto run = [&](float& tm_out, float& dt_out, bool& has_out, uint32_t& idx_out, uint32_t& word_out) {
         float my_tm = 0.0f, my_dt = 0.0f;
-        bool has = false;
-        for (uint32_t j = 0; j < G && t < tf && i < max_steps; ++j, ++i) {
-            const float dt = fminf(fmaxf(dt_min, t * cone), tf - t);
-            const float tm = t + 0.5f * dt;
+        bool live = false;
+#pragma unroll
+        for (uint32_t j = 0; j < G; ++j) {
+            const float dt = fminf(fmaxf(dt_min, t * cone), fmaxf(tf - t, 0.0f));
             if (j_own == j) {
-                my_tm = tm;
+                my_tm = t + 0.5f * dt;
                 my_dt = dt;
-                has   = true;
+                live  = t < tf;
             }
             t += dt;
         }
+        const bool has      = live && i + j_own < max_steps;
+        i += G;
         const float p[3]    = {ro.x + my_tm * rd.x, ro.y + my_tm * rd.y, ro.z + my_tm * rd.z};
-        const bool hit      = has && occupied(p);
+        const uint32_t idx  = has ? cell(p) : kOutside;
+        tm_out              = my_tm;
+        dt_out              = my_dt;
+        has_out             = has;
+        idx_out             = idx;
+        word_out            = (idx != kOutside && bits) ? bits[idx >> 5] : 0u;
+    };
+    float tm0 = 0.0f, dt0 = 0.0f, tm1 = 0.0f, dt1 = 0.0f;
+    bool has0 = false, has1 = false;
+    uint32_t idx0 = kOutside, idx1 = kOutside, word0 = 0u, word1 = 0u;
+    bool more = t < tf && i < max_steps;  // uniform per group
+    if (more) run(tm0, dt0, has0, idx0, word0);
+    while (more) {
+        const bool next = t < tf && i < max_steps;
+        if (next) run(tm1, dt1, has1, idx1, word1);
+        const bool hit      = has0 && idx0 != kOutside && (!bits || ((word0 >> (idx0 & 31u)) & 1u));
         const uint64_t mask = (__ballot(hit) >> shift) & group_bits;
         const uint32_t k    = seen + (uint32_t)__popcll(mask & ((1ull << j_own) - 1ull));
-        if (hit && k < limit) emit(k, my_tm, my_dt);
+        if (hit && k < limit) emit(k, tm0, dt0);
         seen += (uint32_t)__popcll(mask);
+        more = next && seen < limit;
+        tm0 = tm1;
+        dt0 = dt1;
+        has0 = has1;
+        idx0 = idx1;
+        word0 = word1;
     }
     return seen;
 }
