@@ -709,9 +709,10 @@ __global__ __launch_bounds__(256) void k_bin_pass(TrainParams P, GridParams g, c
 // NaN, which the gradient statistics report as non-finite.
 // grad points at the first hashed level; entries = hashed levels x T.
 __global__ __launch_bounds__(512) void k_bin_accumulate(const uint32_t* __restrict__ offsets, uint32_t n_blocks, uint32_t n_bins, const unsigned long long* __restrict__ total, const uint32_t* __restrict__ rec_idx, const float2* __restrict__ rec_val,
-                                                        uint64_t entries, float2* __restrict__ grad) {
+                                                        uint64_t entries, float2* __restrict__ grad, TrainDevState* S) {
     __shared__ unsigned long long acc[2u * kBinEntries];
     __shared__ float wmax[16];
+    __shared__ double wsq[16];
     for (uint32_t i = threadIdx.x; i < 2u * kBinEntries; i += blockDim.x) acc[i] = 0ull;
     const uint32_t bin   = blockIdx.x;
     const uint32_t begin = offsets[(uint64_t)bin * n_blocks];
@@ -735,6 +736,7 @@ __global__ __launch_bounds__(512) void k_bin_accumulate(const uint32_t* __restri
     if (!(mx <= 3.0e38f)) {  // NaN or inf among the records
         for (uint32_t i = threadIdx.x; i < kBinEntries; i += blockDim.x)
             if (base + i < entries) grad[base + i] = make_float2(__builtin_nanf(""), __builtin_nanf(""));
+        if (threadIdx.x == 0u) atomicOr(&S->nonfinite, 1u);
         return;
     }
     const int e        = mx > 0.0f ? 39 - ilogbf(mx) : 0;  // mx * 2^e in [2^39, 2^40)
@@ -760,9 +762,24 @@ __global__ __launch_bounds__(512) void k_bin_accumulate(const uint32_t* __restri
         }
     }
     __syncthreads();
+    // The bin's gradient, and its share of the squared gradient norm (the
+    // statistics k_grad_stats takes of the other gradients).
     const double inv = ldexp(1.0, -e);
+    double sq        = 0.0;
     for (uint32_t i = threadIdx.x; i < kBinEntries; i += blockDim.x)
-        if (base + i < entries) grad[base + i] = make_float2((float)((double)(long long)acc[2u * i] * inv), (float)((double)(long long)acc[2u * i + 1u] * inv));
+        if (base + i < entries) {
+            const float gx = (float)((double)(long long)acc[2u * i] * inv), gy = (float)((double)(long long)acc[2u * i + 1u] * inv);
+            grad[base + i] = make_float2(gx, gy);
+            sq += (double)gx * (double)gx + (double)gy * (double)gy;
+        }
+    sq = wave_sum_d(sq);
+    if ((threadIdx.x & 63u) == 0u) wsq[threadIdx.x >> 6] = sq;
+    __syncthreads();
+    if (threadIdx.x == 0u) {
+        double b = 0.0;
+        for (uint32_t w = 0; w < blockDim.x / 64u; ++w) b += wsq[w];
+        if (b != 0.0) atomicAdd(&S->grad_sumsq, b);
+    }
 }
 
 // Weight gradients as one pass of products over samples: dW = sum_s delta_s
@@ -857,7 +874,14 @@ __global__ __launch_bounds__(kThreads) void k_dw_gemm(TrainParams P, const Train
     for (uint32_t i = threadIdx.x; i < kMlpParams; i += blockDim.x) out[i] = red[i];
 }
 
-__global__ __launch_bounds__(256) void k_fill_zero(float* __restrict__ p, uint64_t n) {
+// Start of the backward stage: clears the dense-level gradient slab (its
+// atomics accumulate into it) and the gradient statistics, which the hashed-
+// level accumulation and k_grad_stats then add to.
+__global__ __launch_bounds__(256) void k_backward_clear(float* __restrict__ p, uint64_t n, TrainDevState* S) {
+    if (blockIdx.x == 0u && threadIdx.x == 0u) {
+        S->grad_sumsq = 0.0;
+        S->nonfinite  = 0u;
+    }
     const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) p[i] = 0.0f;
 }
@@ -878,6 +902,9 @@ __global__ __launch_bounds__(256) void k_dw_reduce(const float* __restrict__ par
 }
 
 // ------------------------------------------------------------------ Adam
+// Squared norm and non-finite flag of the gradients accumulated with atomics
+// (dense hash levels, MLP); the hashed levels' share comes from
+// k_bin_accumulate.  Four-wide loads, fp32 per load, fp64 across loads.
 __global__ __launch_bounds__(256) void k_grad_stats(const float* __restrict__ g, uint64_t n, TrainDevState* S) {
     __shared__ double ws[kWaves];
     __shared__ uint32_t bad;
@@ -886,7 +913,14 @@ __global__ __launch_bounds__(256) void k_grad_stats(const float* __restrict__ g,
     double acc          = 0.0;
     uint32_t nonfinite  = 0u;
     const uint64_t step = (uint64_t)gridDim.x * blockDim.x;
-    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += step) {
+    const uint64_t n4   = n / 4u;
+    const float4* g4    = reinterpret_cast<const float4*>(g);
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += step) {
+        const float4 v = g4[i];
+        if (!isfinite(v.x) || !isfinite(v.y) || !isfinite(v.z) || !isfinite(v.w)) nonfinite = 1u;
+        else acc += (double)v.x * (double)v.x + (double)v.y * (double)v.y + (double)v.z * (double)v.z + (double)v.w * (double)v.w;
+    }
+    for (uint64_t i = 4u * n4 + (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += step) {
         const float v = g[i];
         if (!isfinite(v)) nonfinite = 1u;
         else acc += (double)v * (double)v;
@@ -969,7 +1003,7 @@ hipError_t launch_mlp_backward(const TrainParams& P, const TrainBuffers& B, hipS
     if (B.grid.table_dtype != NERF_EXT_F16) return hipErrorInvalidValue;
     // Dense levels: cleared, then row-combined atomics inside k_bwd_dx.
     const uint64_t dense_elems = (uint64_t)B.n_dense * B.grid.table_size * 2u;
-    if (dense_elems) k_fill_zero<<<grid_for(dense_elems, cus * 4u), 256, 0, st>>>(B.table_grad, dense_elems);
+    k_backward_clear<<<grid_for(dense_elems, cus * 4u), 256, 0, st>>>(B.table_grad, dense_elems, B.state);
     static bool lds_set = false;  // once per process: the kernel's dynamic LDS exceeds the 64 KiB default
     if (!lds_set) {
         const hipError_t e = hipFuncSetAttribute((const void*)k_bwd_dx, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDxLds);
@@ -984,7 +1018,7 @@ hipError_t launch_mlp_backward(const TrainParams& P, const TrainBuffers& B, hipS
         if (e != hipSuccess) return e;
         k_bin_pass<true><<<kBinBlocks, 256, 0, st>>>(P, B.grid, B.state, B.samples, B.sample_ray, B.rays, B.dfeat, B.n_dense, B.n_bins, B.bin_off, B.rec_idx, B.rec_val);
         k_bin_accumulate<<<B.n_bins, 512, 0, st>>>(B.bin_off, kBinBlocks, B.n_bins, B.bin_total, B.rec_idx, B.rec_val, (uint64_t)(B.grid.n_levels - B.n_dense) * B.grid.table_size,
-                                                   reinterpret_cast<float2*>(B.table_grad) + (uint64_t)B.n_dense * B.grid.table_size);
+                                                   reinterpret_cast<float2*>(B.table_grad) + (uint64_t)B.n_dense * B.grid.table_size, B.state);
     }
     k_dw_gemm<<<kDwBlocks, kThreads, 0, st>>>(P, B.state, B.dw_stage, B.dw_partials);
     k_dw_reduce<<<(kMlpParams + 63u) / 64u, 256, 0, st>>>(B.dw_partials, kDwBlocks, B.mlp_grad);
@@ -993,7 +1027,8 @@ hipError_t launch_mlp_backward(const TrainParams& P, const TrainBuffers& B, hipS
 
 hipError_t launch_adam(const TrainParams& P, const TrainBuffers& B, hipStream_t st) {
     const uint32_t cap = device_cu_count() * 16u;
-    k_grad_stats<<<grid_for(B.table_elems, cap), 256, 0, st>>>(B.table_grad, B.table_elems, B.state);
+    const uint64_t dense_elems = (uint64_t)B.n_dense * B.grid.table_size * 2u;  // hashed levels: counted by k_bin_accumulate
+    if (dense_elems) k_grad_stats<<<grid_for(dense_elems / 4u, cap), 256, 0, st>>>(B.table_grad, dense_elems, B.state);
     k_grad_stats<<<grid_for(kMlpParams, cap), 256, 0, st>>>(B.mlp_grad, kMlpParams, B.state);
     k_adam_prepare<<<1, 64, 0, st>>>(P, B.state);
     k_adam<<<grid_for(B.table_elems, cap), 256, 0, st>>>(P, B.state, B.table_f32, B.table, B.table_grad, B.table_m, B.table_v, B.table_elems);
