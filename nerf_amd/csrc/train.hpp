@@ -73,6 +73,7 @@ struct TrainBuffers {
     // by bin of kBinEntries table entries
     uint32_t* bin_hist;          // [n_bins][kBinBlocks] record counts
     uint32_t* bin_off;           // [n_bins][kBinBlocks] exclusive scan of bin_hist
+    uint32_t* bin_max;           // [n_bins][kBinBlocks] bits of the largest |record value|
     uint32_t* bin_scan_tmp;
     unsigned long long* bin_total;
     uint32_t* rec_idx;           // [rec_cap]

@@ -637,9 +637,14 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dx(TrainParams P, GridParams g
 // overwritten rather than accumulated, so it needs no clearing.
 template <bool kFill>
 __global__ __launch_bounds__(256) void k_bin_pass(TrainParams P, GridParams g, const TrainDevState* S, const float2* __restrict__ samples, const uint32_t* __restrict__ sample_ray, const float4* __restrict__ rays,
-                                                  const float* __restrict__ dfeat, uint32_t n_dense, uint32_t n_bins, uint32_t* __restrict__ hist, uint32_t* __restrict__ rec_idx, float2* __restrict__ rec_val) {
+                                                  const float* __restrict__ dfeat, uint32_t n_dense, uint32_t n_bins, uint32_t* __restrict__ hist, uint32_t* __restrict__ rec_idx, float2* __restrict__ rec_val,
+                                                  uint32_t* __restrict__ bin_max) {
     __shared__ uint32_t cursor[kMaxBins];
-    for (uint32_t i = threadIdx.x; i < n_bins; i += blockDim.x) cursor[i] = kFill ? hist[(uint64_t)i * gridDim.x + blockIdx.x] : 0u;
+    __shared__ uint32_t vmax[kFill ? kMaxBins : 1u];  // bits of the largest |record value| per bin
+    for (uint32_t i = threadIdx.x; i < n_bins; i += blockDim.x) {
+        cursor[i] = kFill ? hist[(uint64_t)i * gridDim.x + blockIdx.x] : 0u;
+        if constexpr (kFill) vmax[i] = 0u;
+    }
     __syncthreads();
     const uint32_t n    = min(S->n_samples, P.sample_cap);
     const uint32_t mask = g.table_size - 1u;
@@ -653,17 +658,17 @@ __global__ __launch_bounds__(256) void k_bin_pass(TrainParams P, GridParams g, c
         const uint32_t q = live ? s : n - 1u;
         float p[3], d[3];
         sample_geometry(samples, sample_ray, rays, P.bmin, P.bmax, q, p, d);
-        const float* df = dfeat + (uint64_t)q * 32u;
         for (uint32_t l = n_dense; l < g.n_levels; ++l) {
             const uint32_t N  = g.resolution[l];
             const bool dense  = g.dense[l] != 0u;
-            const LevelCell c = level_cell(p, N);
             const uint32_t e0 = (l - n_dense) * g.table_size;
+            const LevelCell c = level_cell(p, N);
             const uint32_t kx = live ? c.i0[0] : 0xFFFFFFFFu, ky = c.i0[1], kz = c.i0[2];
             const uint32_t px = __shfl_up(kx, 1, 16), py = __shfl_up(ky, 1, 16), pz = __shfl_up(kz, 1, 16);
             const bool head   = s16 == 0u || kx != px || ky != py || kz != pz || !live;
             float v[16];
             if constexpr (kFill) {
+                const float* df = dfeat + (uint64_t)q * 32u;
                 const float d0 = live ? df[2u * l] : 0.0f, d1 = live ? df[2u * l + 1u] : 0.0f;
 #pragma unroll
                 for (uint32_t k = 0; k < 8u; ++k) {
@@ -689,13 +694,16 @@ __global__ __launch_bounds__(256) void k_bin_pass(TrainParams P, GridParams g, c
                 if constexpr (kFill) {
                     rec_idx[slot] = e % kBinEntries;
                     rec_val[slot] = make_float2(v[2u * k], v[2u * k + 1u]);
+                    // |x| as bits orders like |x| for finite x; NaN and inf compare above every finite value.
+                    atomicMax(&vmax[e / kBinEntries], max(__float_as_uint(v[2u * k]) & 0x7FFFFFFFu, __float_as_uint(v[2u * k + 1u]) & 0x7FFFFFFFu));
                 }
             }
         }
     }
-    if constexpr (!kFill) {
-        __syncthreads();
-        for (uint32_t i = threadIdx.x; i < n_bins; i += blockDim.x) hist[(uint64_t)i * gridDim.x + blockIdx.x] = cursor[i];
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < n_bins; i += blockDim.x) {
+        if constexpr (kFill) bin_max[(uint64_t)i * gridDim.x + blockIdx.x] = vmax[i];
+        else hist[(uint64_t)i * gridDim.x + blockIdx.x] = cursor[i];
     }
 }
 
@@ -709,31 +717,28 @@ __global__ __launch_bounds__(256) void k_bin_pass(TrainParams P, GridParams g, c
 // NaN, which the gradient statistics report as non-finite.
 // grad points at the first hashed level; entries = hashed levels x T.
 __global__ __launch_bounds__(512) void k_bin_accumulate(const uint32_t* __restrict__ offsets, uint32_t n_blocks, uint32_t n_bins, const unsigned long long* __restrict__ total, const uint32_t* __restrict__ rec_idx, const float2* __restrict__ rec_val,
-                                                        uint64_t entries, float2* __restrict__ grad, TrainDevState* S) {
+                                                        const uint32_t* __restrict__ bin_max, uint64_t entries, float2* __restrict__ grad, TrainDevState* S) {
     __shared__ unsigned long long acc[2u * kBinEntries];
-    __shared__ float wmax[16];
+    __shared__ uint32_t wmax[16];
     __shared__ double wsq[16];
     for (uint32_t i = threadIdx.x; i < 2u * kBinEntries; i += blockDim.x) acc[i] = 0ull;
     const uint32_t bin   = blockIdx.x;
     const uint32_t begin = offsets[(uint64_t)bin * n_blocks];
     const uint32_t end   = bin + 1u < n_bins ? offsets[(uint64_t)(bin + 1u) * n_blocks] : (uint32_t)*total;
-    float mx = 0.0f;  // NaN-propagating max: a non-finite record poisons it
-    for (uint32_t r = begin + threadIdx.x; r < end; r += blockDim.x) {
-        const float2 v = rec_val[r];
-        const float a  = fmaxf(fabsf(v.x), fabsf(v.y));
-        mx             = (a != a || mx != mx) ? __builtin_nanf("") : fmaxf(mx, a);
-    }
+    // Largest |record value| of the bin, as bits: the maximum of the fill
+    // pass's per-workgroup maxima (bits above 0x7F800000 - NaN - or equal to
+    // it - inf - mark a non-finite record).
+    uint32_t mb = 0u;
+    for (uint32_t i = threadIdx.x; i < n_blocks; i += blockDim.x) mb = max(mb, bin_max[(uint64_t)bin * n_blocks + i]);
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float other = __shfl_xor(mx, o, 64);
-        mx                = (other != other || mx != mx) ? __builtin_nanf("") : fmaxf(mx, other);
-    }
-    if ((threadIdx.x & 63u) == 0u) wmax[threadIdx.x >> 6] = mx;
+    for (int o = 32; o > 0; o >>= 1) mb = max(mb, (uint32_t)__shfl_xor((int)mb, o, 64));
+    if ((threadIdx.x & 63u) == 0u) wmax[threadIdx.x >> 6] = mb;
     __syncthreads();
-    mx = 0.0f;
-    for (uint32_t w = 0; w < blockDim.x / 64u; ++w) mx = (wmax[w] != wmax[w] || mx != mx) ? __builtin_nanf("") : fmaxf(mx, wmax[w]);
+    mb = 0u;
+    for (uint32_t w = 0; w < blockDim.x / 64u; ++w) mb = max(mb, wmax[w]);
+    const float mx      = __uint_as_float(mb);
     const uint64_t base = (uint64_t)bin * kBinEntries;
-    if (!(mx <= 3.0e38f)) {  // NaN or inf among the records
+    if (mb >= 0x7F800000u) {  // NaN or inf among the records
         for (uint32_t i = threadIdx.x; i < kBinEntries; i += blockDim.x)
             if (base + i < entries) grad[base + i] = make_float2(__builtin_nanf(""), __builtin_nanf(""));
         if (threadIdx.x == 0u) atomicOr(&S->nonfinite, 1u);
@@ -1013,11 +1018,11 @@ hipError_t launch_mlp_backward(const TrainParams& P, const TrainBuffers& B, hipS
     k_bwd_dx<<<cus * 2u, kThreads, kDxLds, st>>>(P, B.grid, B.state, B.dparams, B.cparams, B.features, B.draw, B.samples, B.sample_ray, B.rays, B.dfeat, B.n_dense, B.table_grad, B.dw_stage);
     // Hashed levels: binned.
     if (B.n_bins) {
-        k_bin_pass<false><<<kBinBlocks, 256, 0, st>>>(P, B.grid, B.state, B.samples, B.sample_ray, B.rays, B.dfeat, B.n_dense, B.n_bins, B.bin_hist, nullptr, nullptr);
+        k_bin_pass<false><<<kBinBlocks, 256, 0, st>>>(P, B.grid, B.state, B.samples, B.sample_ray, B.rays, B.dfeat, B.n_dense, B.n_bins, B.bin_hist, nullptr, nullptr, nullptr);
         const hipError_t e = exclusive_scan_u32(B.bin_hist, B.bin_off, B.n_bins * kBinBlocks, B.bin_scan_tmp, B.bin_total, st);
         if (e != hipSuccess) return e;
-        k_bin_pass<true><<<kBinBlocks, 256, 0, st>>>(P, B.grid, B.state, B.samples, B.sample_ray, B.rays, B.dfeat, B.n_dense, B.n_bins, B.bin_off, B.rec_idx, B.rec_val);
-        k_bin_accumulate<<<B.n_bins, 512, 0, st>>>(B.bin_off, kBinBlocks, B.n_bins, B.bin_total, B.rec_idx, B.rec_val, (uint64_t)(B.grid.n_levels - B.n_dense) * B.grid.table_size,
+        k_bin_pass<true><<<kBinBlocks, 256, 0, st>>>(P, B.grid, B.state, B.samples, B.sample_ray, B.rays, B.dfeat, B.n_dense, B.n_bins, B.bin_off, B.rec_idx, B.rec_val, B.bin_max);
+        k_bin_accumulate<<<B.n_bins, 512, 0, st>>>(B.bin_off, kBinBlocks, B.n_bins, B.bin_total, B.rec_idx, B.rec_val, B.bin_max, (uint64_t)(B.grid.n_levels - B.n_dense) * B.grid.table_size,
                                                    reinterpret_cast<float2*>(B.table_grad) + (uint64_t)B.n_dense * B.grid.table_size, B.state);
     }
     k_dw_gemm<<<kDwBlocks, kThreads, 0, st>>>(P, B.state, B.dw_stage, B.dw_partials);

@@ -128,6 +128,7 @@ NerfStatus trainer_create(const NerfExtTrainDesc* d, const BorrowedModel* borrow
     B.rec_cap = (uint64_t)P.sample_cap * (g.n_levels - B.n_dense) * 8u;
     NERF_HIP_TRY(alloc(T, B.bin_hist, (uint64_t)B.n_bins * kBinBlocks));
     NERF_HIP_TRY(alloc(T, B.bin_off, (uint64_t)B.n_bins * kBinBlocks));
+    NERF_HIP_TRY(alloc(T, B.bin_max, (uint64_t)B.n_bins * kBinBlocks));
     NERF_HIP_TRY(alloc(T, B.bin_scan_tmp, scan_tmp_words(B.n_bins * kBinBlocks + 1u)));
     NERF_HIP_TRY(alloc(T, B.bin_total, 1));
     NERF_HIP_TRY(alloc(T, B.rec_idx, B.rec_cap));
