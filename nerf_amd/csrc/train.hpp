@@ -76,8 +76,7 @@ struct TrainBuffers {
     uint32_t* bin_max;           // [n_bins][kBinBlocks] bits of the largest |record value|
     uint32_t* bin_scan_tmp;
     unsigned long long* bin_total;
-    uint32_t* rec_idx;           // [rec_cap]
-    float2* rec_val;             // [rec_cap]
+    uint2* rec;                  // [rec_cap] packed (entry within bin, 2 values)
     uint32_t n_bins;             // bins of the hashed levels
     uint32_t n_dense;            // leading dense levels (scattered with atomics)
     uint64_t rec_cap;

@@ -635,9 +635,20 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dx(TrainParams P, GridParams g
 // k_bin_accumulate then sums one bin per workgroup in LDS and writes the
 // bin's slice of the gradient once.  No global atomics, and the gradient is
 // overwritten rather than accumulated, so it needs no clearing.
+// A record is 8 bytes: the two values, each rounded to 17 explicit mantissa
+// bits (relative change at most 2^-18), with the entry's 12-bit index within
+// its bin in their low 6 bits.  Non-finite values stay non-finite or are
+// caught by the bin's maximum, which is taken before packing.
+static_assert(kBinEntries == 4096u, "records hold 12 bits of entry index");
+__device__ __forceinline__ uint2 pack_record(float v0, float v1, uint32_t entry) {
+    return make_uint2(((__float_as_uint(v0) + 32u) & ~63u) | (entry & 63u), ((__float_as_uint(v1) + 32u) & ~63u) | (entry >> 6));
+}
+__device__ __forceinline__ uint32_t record_entry(uint2 r) { return (r.x & 63u) | ((r.y & 63u) << 6); }
+__device__ __forceinline__ float2 record_value(uint2 r) { return make_float2(__uint_as_float(r.x & ~63u), __uint_as_float(r.y & ~63u)); }
+
 template <bool kFill>
 __global__ __launch_bounds__(256) void k_bin_pass(TrainParams P, GridParams g, const TrainDevState* S, const float2* __restrict__ samples, const uint32_t* __restrict__ sample_ray, const float4* __restrict__ rays,
-                                                  const float* __restrict__ dfeat, uint32_t n_dense, uint32_t n_bins, uint32_t* __restrict__ hist, uint32_t* __restrict__ rec_idx, float2* __restrict__ rec_val,
+                                                  const float* __restrict__ dfeat, uint32_t n_dense, uint32_t n_bins, uint32_t* __restrict__ hist, uint2* __restrict__ rec,
                                                   uint32_t* __restrict__ bin_max) {
     __shared__ uint32_t cursor[kMaxBins];
     __shared__ uint32_t vmax[kFill ? kMaxBins : 1u];  // bits of the largest |record value| per bin
@@ -692,8 +703,7 @@ __global__ __launch_bounds__(256) void k_bin_pass(TrainParams P, GridParams g, c
                 const uint32_t e    = e0 + corner_index(c, k, N, dense, mask);
                 const uint32_t slot = atomicAdd(&cursor[e / kBinEntries], 1u);
                 if constexpr (kFill) {
-                    rec_idx[slot] = e % kBinEntries;
-                    rec_val[slot] = make_float2(v[2u * k], v[2u * k + 1u]);
+                    rec[slot] = pack_record(v[2u * k], v[2u * k + 1u], e % kBinEntries);
                     // |x| as bits orders like |x| for finite x; NaN and inf compare above every finite value.
                     atomicMax(&vmax[e / kBinEntries], max(__float_as_uint(v[2u * k]) & 0x7FFFFFFFu, __float_as_uint(v[2u * k + 1u]) & 0x7FFFFFFFu));
                 }
@@ -716,7 +726,7 @@ __global__ __launch_bounds__(256) void k_bin_pass(TrainParams P, GridParams g, c
 // largest one round to zero.  A non-finite record makes the whole slice
 // NaN, which the gradient statistics report as non-finite.
 // grad points at the first hashed level; entries = hashed levels x T.
-__global__ __launch_bounds__(512) void k_bin_accumulate(const uint32_t* __restrict__ offsets, uint32_t n_blocks, uint32_t n_bins, const unsigned long long* __restrict__ total, const uint32_t* __restrict__ rec_idx, const float2* __restrict__ rec_val,
+__global__ __launch_bounds__(512) void k_bin_accumulate(const uint32_t* __restrict__ offsets, uint32_t n_blocks, uint32_t n_bins, const unsigned long long* __restrict__ total, const uint2* __restrict__ rec,
                                                         const uint32_t* __restrict__ bin_max, uint64_t entries, float2* __restrict__ grad, TrainDevState* S) {
     __shared__ unsigned long long acc[2u * kBinEntries];
     __shared__ uint32_t wmax[16];
@@ -755,8 +765,9 @@ __global__ __launch_bounds__(512) void k_bin_accumulate(const uint32_t* __restri
 #pragma unroll
         for (uint32_t k = 0; k < kBatch; ++k) {
             const uint32_t r = r0 + k * blockDim.x + threadIdx.x;
-            idx[k]           = r < end ? rec_idx[r] % kBinEntries : 0u;
-            val[k]           = r < end ? rec_val[r] : make_float2(0.0f, 0.0f);
+            const uint2 w    = r < end ? rec[r] : make_uint2(0u, 0u);
+            idx[k]           = record_entry(w);
+            val[k]           = record_value(w);
         }
 #pragma unroll
         for (uint32_t k = 0; k < kBatch; ++k) {
@@ -1018,11 +1029,11 @@ hipError_t launch_mlp_backward(const TrainParams& P, const TrainBuffers& B, hipS
     k_bwd_dx<<<cus * 2u, kThreads, kDxLds, st>>>(P, B.grid, B.state, B.dparams, B.cparams, B.features, B.draw, B.samples, B.sample_ray, B.rays, B.dfeat, B.n_dense, B.table_grad, B.dw_stage);
     // Hashed levels: binned.
     if (B.n_bins) {
-        k_bin_pass<false><<<kBinBlocks, 256, 0, st>>>(P, B.grid, B.state, B.samples, B.sample_ray, B.rays, B.dfeat, B.n_dense, B.n_bins, B.bin_hist, nullptr, nullptr, nullptr);
+        k_bin_pass<false><<<kBinBlocks, 256, 0, st>>>(P, B.grid, B.state, B.samples, B.sample_ray, B.rays, B.dfeat, B.n_dense, B.n_bins, B.bin_hist, nullptr, nullptr);
         const hipError_t e = exclusive_scan_u32(B.bin_hist, B.bin_off, B.n_bins * kBinBlocks, B.bin_scan_tmp, B.bin_total, st);
         if (e != hipSuccess) return e;
-        k_bin_pass<true><<<kBinBlocks, 256, 0, st>>>(P, B.grid, B.state, B.samples, B.sample_ray, B.rays, B.dfeat, B.n_dense, B.n_bins, B.bin_off, B.rec_idx, B.rec_val, B.bin_max);
-        k_bin_accumulate<<<B.n_bins, 512, 0, st>>>(B.bin_off, kBinBlocks, B.n_bins, B.bin_total, B.rec_idx, B.rec_val, B.bin_max, (uint64_t)(B.grid.n_levels - B.n_dense) * B.grid.table_size,
+        k_bin_pass<true><<<kBinBlocks, 256, 0, st>>>(P, B.grid, B.state, B.samples, B.sample_ray, B.rays, B.dfeat, B.n_dense, B.n_bins, B.bin_off, B.rec, B.bin_max);
+        k_bin_accumulate<<<B.n_bins, 512, 0, st>>>(B.bin_off, kBinBlocks, B.n_bins, B.bin_total, B.rec, B.bin_max, (uint64_t)(B.grid.n_levels - B.n_dense) * B.grid.table_size,
                                                    reinterpret_cast<float2*>(B.table_grad) + (uint64_t)B.n_dense * B.grid.table_size, B.state);
     }
     k_dw_gemm<<<kDwBlocks, kThreads, 0, st>>>(P, B.state, B.dw_stage, B.dw_partials);

@@ -131,8 +131,7 @@ NerfStatus trainer_create(const NerfExtTrainDesc* d, const BorrowedModel* borrow
     NERF_HIP_TRY(alloc(T, B.bin_max, (uint64_t)B.n_bins * kBinBlocks));
     NERF_HIP_TRY(alloc(T, B.bin_scan_tmp, scan_tmp_words(B.n_bins * kBinBlocks + 1u)));
     NERF_HIP_TRY(alloc(T, B.bin_total, 1));
-    NERF_HIP_TRY(alloc(T, B.rec_idx, B.rec_cap));
-    NERF_HIP_TRY(alloc(T, B.rec_val, B.rec_cap));
+    NERF_HIP_TRY(alloc(T, B.rec, B.rec_cap));
     NERF_HIP_TRY(alloc(T, B.table_grad, B.table_elems));
     NERF_HIP_TRY(alloc(T, B.table_m, B.table_elems));
     NERF_HIP_TRY(alloc(T, B.table_v, B.table_elems));
