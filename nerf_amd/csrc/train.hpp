@@ -78,7 +78,7 @@ struct TrainBuffers {
     unsigned long long* bin_total;
     uint2* rec;                  // [rec_cap] packed (entry within bin, 2 values)
     uint32_t n_bins;             // bins of the hashed levels
-    uint32_t n_dense;            // leading dense levels (scattered with atomics)
+    uint32_t n_dense;            // leading levels scattered with atomics (dense, <= kAtomicMaxEntries entries)
     uint64_t rec_cap;
     // model
     GridParams grid;
@@ -104,7 +104,8 @@ constexpr uint32_t kDwBlocks   = 256;   // workgroups of the weight-gradient pas
 constexpr uint32_t kRowDh2 = 0, kRowH1 = 64, kRowDh1 = 128, kRowXc = 192, kRowDo3 = 224, kRowH2 = 240, kRowDhd = 304, kRowX = 368, kRowDout = 400, kRowHd = 416, kStageRows = 480;
 constexpr uint32_t kBinEntries = 4096;  // table entries per scatter bin (64 KiB of int64 pairs in LDS)
 constexpr uint32_t kBinBlocks  = 256;   // workgroups of the bin count / fill passes
-constexpr uint32_t kMaxBins    = 16384; // bin counters per workgroup in LDS (64 KiB)
+constexpr uint32_t kAtomicMaxEntries = 1u << 15;  // largest level scattered with atomics
+constexpr uint32_t kMaxBins    = 16384; // bins; the fill pass keeps a cursor and a maximum per bin in LDS (128 KiB)
 constexpr uint32_t kMlpParams  = NERF_EXT_DENSITY_PARAMS + NERF_EXT_COLOR_PARAMS;
 
 // Launches one stage (NERF_EXT_STAGE_*) of a training step on `stream`.

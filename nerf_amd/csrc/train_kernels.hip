@@ -549,9 +549,10 @@ __device__ __forceinline__ void scatter_level(const GridParams& g, float* __rest
 }
 
 // Input-gradient pass: d(features) of each tile, loss-scaled, to dfeat
-// [n][32] for the binned scatter of the hashed levels; the dense (coarse)
-// levels, where runs of consecutive samples share cells, are scattered here
-// with row-combined atomics.  Lane (g, s) holds features 16b + 4g + e of
+// [n][32] for the binned scatter; the first n_dense levels (the coarsest
+// dense ones, where runs of consecutive samples share cells and a few bins
+// would take every sample's records) are scattered here with row-combined
+// atomics.  Lane (g, s) holds features 16b + 4g + e of
 // sample s, i.e. levels 2g, 2g+1 (b = 0) and 8+2g, 9+2g (b = 1).
 // Rows 16b + 4g + e, column s16 of a 16-column tile region.
 __device__ __forceinline__ void put16(half_t* L, uint32_t row0, const half4_t v[4], uint32_t s16, uint32_t grp) {
@@ -626,9 +627,10 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dx(TrainParams P, GridParams g
     }
 }
 
-// Hash-grid backward of the hashed levels, binned.  Entry e = (level -
-// n_dense) * T + index of the hashed levels belongs to bin e / kBinEntries.  k_bin_pass<false> counts each workgroup's records per
-// bin (LDS histogram, stored as hist[bin][workgroup]); an exclusive scan of
+// Hash-grid backward of the levels past the first n_dense (hashed levels and
+// the finer dense ones), binned.  Entry e = (level - n_dense) * T + index
+// belongs to bin e / kBinEntries.  k_bin_pass<false> counts each workgroup's
+// records per bin (LDS histogram, stored as hist[bin][workgroup]); an exclusive scan of
 // that matrix gives every (bin, workgroup) its record range; k_bin_pass<true>
 // revisits the same samples in the same order and writes each record
 // (entry within the bin, w * d(feature 0), w * d(feature 1)) into its range;

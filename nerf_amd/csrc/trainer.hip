@@ -122,8 +122,15 @@ NerfStatus trainer_create(const NerfExtTrainDesc* d, const BorrowedModel* borrow
     NERF_HIP_TRY(alloc(T, B.draw, P.sample_cap));
     NERF_HIP_TRY(alloc(T, B.dfeat, 32ull * P.sample_cap));
     NERF_HIP_TRY(alloc(T, B.dw_stage, (uint64_t)(P.sample_cap + 15u) / 16u * kStageRows * 16u));
+    // Leading dense levels of at most kAtomicMaxEntries entries take row-
+    // combined atomics; binned, the records of every sample would crowd into
+    // their few bins.  Every other level is binned.
     B.n_dense = 0u;
-    while (B.n_dense < g.n_levels && g.dense[B.n_dense]) ++B.n_dense;
+    while (B.n_dense < g.n_levels && g.dense[B.n_dense]) {
+        const uint64_t v = (uint64_t)g.resolution[B.n_dense] + 1u;
+        if (v * v * v > kAtomicMaxEntries) break;
+        ++B.n_dense;
+    }
     B.n_bins  = (uint32_t)(((uint64_t)(g.n_levels - B.n_dense) * g.table_size + kBinEntries - 1u) / kBinEntries);
     B.rec_cap = (uint64_t)P.sample_cap * (g.n_levels - B.n_dense) * 8u;
     NERF_HIP_TRY(alloc(T, B.bin_hist, (uint64_t)B.n_bins * kBinBlocks));

@@ -34,9 +34,9 @@ def dataset():
     return g, cams, imgs
 
 
-def _trainer(dataset, capacity=RAYS * STEPS, rays=RAYS, **kw):
+def _trainer(dataset, capacity=RAYS * STEPS, rays=RAYS, log2_table=14, **kw):
     _, cams, imgs = dataset
-    grid = ext.grid_desc(14, L.NERF_EXT_F16)
+    grid = ext.grid_desc(log2_table, L.NERF_EXT_F16)
     occ = ext.occupancy_params(warmup_steps=2, update_interval=4, cells_per_update=OCC_RES ** 3, threshold=0.01, decay=0.95)
     hyper = ext.hyper_params(loss_scale=LOSS_SCALE)
     t = ext.Trainer(grid, imgs.view(np.uint8), cams, occupancy_res=OCC_RES, hyper=hyper, occupancy=occ, initial_rays=rays, max_rays=rays, sample_capacity=capacity, max_steps_per_ray=STEPS, seed=5,
@@ -183,9 +183,12 @@ def _frob(got, want):
     return float(np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-30))
 
 
-def test_backward_stage(dataset):
-    announce("train backward stage")
-    t, grid = _trainer(dataset)
+# T = 2^14: the dense levels take atomics, the hashed ones bins.  T = 2^17:
+# the coarsest dense levels take atomics, the finer dense ones bins as well.
+@pytest.mark.parametrize("log2_table", [14, 17])
+def test_backward_stage(dataset, log2_table):
+    announce(f"train backward stage, T=2^{log2_table}")
+    t, grid = _trainer(dataset, log2_table=log2_table)
     t.run_stages(L.NERF_EXT_STAGE_BEGIN, L.NERF_EXT_STAGE_BACKWARD)
     s = _sample_state(t)
     n = s["stats"].samples
@@ -209,9 +212,10 @@ def test_backward_stage(dataset):
     assert np.array_equal(table_grad != 0, want_t != 0) or (np.count_nonzero((table_grad != 0) != (want_t != 0)) < 1e-4 * table_grad.size)
 
 
-def test_adam_stage_and_step_end(dataset):
-    announce("train adam stage")
-    t, _ = _trainer(dataset)
+@pytest.mark.parametrize("log2_table", [14, 17])
+def test_adam_stage_and_step_end(dataset, log2_table):
+    announce(f"train adam stage, T=2^{log2_table}")
+    t, _ = _trainer(dataset, log2_table=log2_table)
     t.run_stages(L.NERF_EXT_STAGE_BEGIN, L.NERF_EXT_STAGE_BACKWARD)
     t.synchronize()
     B = t.buffers()
