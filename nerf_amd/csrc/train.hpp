@@ -25,8 +25,6 @@ struct TrainDevState {
     double grad_sumsq;    // sum of squared (loss-scaled) gradients
     float loss_sum;       // sum of per-ray Huber losses
     float rays_f;         // adaptive ray count
-    float lr, grad_scale, inv_bc1, inv_bc2, inv_ls;
-    uint32_t pad;
     NerfTrainStats stats; // last completed step
 };
 

@@ -907,7 +907,9 @@ __global__ __launch_bounds__(256) void k_backward_clear(float* __restrict__ p, u
 // Sum of the per-workgroup partials: workgroup x sums 64 parameters, its 4
 // waves each a quarter of the partials (independent loads in flight), then
 // the quarters are added in a fixed order.
-__global__ __launch_bounds__(256) void k_dw_reduce(const float* __restrict__ partials, uint32_t blocks, float* __restrict__ grad) {
+// The MLP gradient's share of the squared norm and the non-finite flag are
+// taken here, from the values written.
+__global__ __launch_bounds__(256) void k_dw_reduce(const float* __restrict__ partials, uint32_t blocks, float* __restrict__ grad, TrainDevState* S) {
     __shared__ float part[4][64];
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t i    = blockIdx.x * 64u + lane;
@@ -916,7 +918,18 @@ __global__ __launch_bounds__(256) void k_dw_reduce(const float* __restrict__ par
         for (uint32_t b = wave; b < blocks; b += 4u) s += partials[(uint64_t)b * kMlpParams + i];
     part[wave][lane] = s;
     __syncthreads();
-    if (wave == 0u && i < kMlpParams) grad[i] = (part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]);
+    if (wave != 0u) return;
+    double sq = 0.0;
+    bool bad  = false;
+    if (i < kMlpParams) {
+        const float gi = (part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]);
+        grad[i]        = gi;
+        if (isfinite(gi)) sq = (double)gi * (double)gi;
+        else bad = true;
+    }
+    sq = wave_sum_d(sq);
+    if (__ballot(bad) != 0ull && lane == 0u) atomicOr(&S->nonfinite, 1u);
+    if (lane == 0u && sq != 0.0) atomicAdd(&S->grad_sumsq, sq);
 }
 
 // ------------------------------------------------------------------ Adam
@@ -954,45 +967,87 @@ __global__ __launch_bounds__(256) void k_grad_stats(const float* __restrict__ g,
     }
 }
 
-// :1513-1536: skip guard, lr decay, clip factor, bias corrections.
-__global__ void k_adam_prepare(TrainParams P, TrainDevState* S) {
-    if (threadIdx.x != 0u || blockIdx.x != 0u) return;
-    const float gn        = (float)sqrt(S->grad_sumsq > 0.0 ? S->grad_sumsq : 0.0) / P.loss_scale;
-    const uint32_t t      = S->frame + 1u;  // optimizer step
-    const bool skip       = S->nonfinite != 0u || !isfinite(gn) || gn > P.guard;
-    S->skip               = skip ? 1u : 0u;
-    S->inv_ls             = 1.0f / P.loss_scale;
-    if (skip) {
-        S->lr = 0.0f;
-        S->grad_scale = 1.0f;
-        S->inv_bc1 = 1.0f;
-        S->inv_bc2 = 1.0f;
-        return;
+// :1513-1536: skip guard, lr decay, clip factor, bias corrections, from the
+// step's gradient statistics.
+struct AdamCoef {
+    float lr, gs, bc1, bc2;  // gs: clip factor / loss scale
+    uint32_t skip;
+};
+__device__ AdamCoef adam_coef(const TrainParams& P, const TrainDevState* S) {
+    const float gn   = (float)sqrt(S->grad_sumsq > 0.0 ? S->grad_sumsq : 0.0) / P.loss_scale;
+    const uint32_t t = S->frame + 1u;  // optimizer step
+    AdamCoef c;
+    c.skip = (S->nonfinite != 0u || !isfinite(gn) || gn > P.guard) ? 1u : 0u;
+    if (c.skip) {
+        c.lr = 0.0f;
+        c.gs = 1.0f / P.loss_scale;
+        c.bc1 = c.bc2 = 1.0f;
+        return c;
     }
     const float decay = (float)P.lr_decay_ksteps * 1000.0f;
-    S->lr             = decay > 0.0f ? P.lr * powf(0.1f, (float)t / decay) : P.lr;
-    S->grad_scale     = (gn > P.clip && gn > 0.0f) ? P.clip / gn : 1.0f;
-    S->inv_bc1        = 1.0f / (1.0f - powf(P.beta1, (float)t));
-    S->inv_bc2        = 1.0f / (1.0f - powf(P.beta2, (float)t));
+    c.lr              = decay > 0.0f ? P.lr * powf(0.1f, (float)t / decay) : P.lr;
+    c.gs              = ((gn > P.clip && gn > 0.0f) ? P.clip / gn : 1.0f) * (1.0f / P.loss_scale);
+    c.bc1             = 1.0f / (1.0f - powf(P.beta1, (float)t));
+    c.bc2             = 1.0f / (1.0f - powf(P.beta2, (float)t));
+    return c;
 }
 
-// :1537-1554 on fp32 masters with fp16 working copies.  The backward pass
-// overwrites both gradients every step, so they are not cleared here.
-__global__ __launch_bounds__(256) void k_adam(TrainParams P, const TrainDevState* S, float* __restrict__ w, half_t* __restrict__ w16, const float* __restrict__ g, float* __restrict__ m, float* __restrict__ v, uint64_t n) {
-    const bool skip       = S->skip != 0u;
-    const float lr = S->lr, gs = S->grad_scale * S->inv_ls, bc1 = S->inv_bc1, bc2 = S->inv_bc2;
-    const float b1 = P.beta1, b2 = P.beta2, eps = P.eps;
+struct AdamSeg {
+    float* w;
+    half_t* w16;
+    const float* g;
+    float* m;
+    float* v;
+};
+
+__device__ __forceinline__ float adam_one(const AdamCoef& c, const TrainParams& P, float& w, float g, float& m, float& v) {
+    const float gr = g * c.gs;
+    m              = P.beta1 * m + (1.0f - P.beta1) * gr;
+    v              = P.beta2 * v + (1.0f - P.beta2) * gr * gr;
+    w              = w - c.lr * (m * c.bc1) / (sqrtf(v * c.bc2) + P.eps);
+    return w;
+}
+
+// :1537-1554 on fp32 masters with fp16 working copies, all parameters in one
+// launch: the hash table four at a time (n_table is a multiple of 4), then
+// the density and colour MLPs (contiguous masters, moments and gradients;
+// separate fp16 copies).  Every workgroup derives the step's coefficients
+// itself.  The backward pass overwrites the gradients every step, so they
+// are not cleared here.
+__global__ __launch_bounds__(256) void k_adam(TrainParams P, TrainDevState* S, AdamSeg table, uint64_t n_table, AdamSeg mlp, half_t* __restrict__ w16_color, uint32_t n_density, uint32_t n_mlp) {
+    __shared__ AdamCoef coef;
+    if (threadIdx.x == 0u) {
+        coef = adam_coef(P, S);
+        if (blockIdx.x == 0u) S->skip = coef.skip;
+    }
+    __syncthreads();
+    const AdamCoef c = coef;
+    if (c.skip) return;
     const uint64_t step = (uint64_t)gridDim.x * blockDim.x;
-    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += step) {
-        if (skip) break;
-        const float gr = g[i] * gs;
-        const float mi = b1 * m[i] + (1.0f - b1) * gr;
-        const float vi = b2 * v[i] + (1.0f - b2) * gr * gr;
-        const float wi = w[i] - lr * (mi * bc1) / (sqrtf(vi * bc2) + eps);
-        m[i]           = mi;
-        v[i]           = vi;
-        w[i]           = wi;
-        w16[i]         = to_half_rne(wi);
+    const uint64_t n4 = n_table / 4u, total = n4 + n_mlp;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += step) {
+        if (i < n4) {
+            float4 w = reinterpret_cast<const float4*>(table.w)[i], m = reinterpret_cast<const float4*>(table.m)[i], v = reinterpret_cast<const float4*>(table.v)[i];
+            const float4 g = reinterpret_cast<const float4*>(table.g)[i];
+            adam_one(c, P, w.x, g.x, m.x, v.x);
+            adam_one(c, P, w.y, g.y, m.y, v.y);
+            adam_one(c, P, w.z, g.z, m.z, v.z);
+            adam_one(c, P, w.w, g.w, m.w, v.w);
+            reinterpret_cast<float4*>(table.w)[i] = w;
+            reinterpret_cast<float4*>(table.m)[i] = m;
+            reinterpret_cast<float4*>(table.v)[i] = v;
+            half4_t h = {to_half_rne(w.x), to_half_rne(w.y), to_half_rne(w.z), to_half_rne(w.w)};
+            reinterpret_cast<half4_t*>(table.w16)[i] = h;
+        } else {
+            const uint32_t j = (uint32_t)(i - n4);
+            float w = mlp.w[j], m = mlp.m[j], v = mlp.v[j];
+            adam_one(c, P, w, mlp.g[j], m, v);
+            mlp.w[j] = w;
+            mlp.m[j] = m;
+            mlp.v[j] = v;
+            if (j < n_density) mlp.w16[j] = to_half_rne(w);
+            else w16_color[j - n_density] = to_half_rne(w);
+        }
     }
 }
 
@@ -1039,21 +1094,20 @@ hipError_t launch_mlp_backward(const TrainParams& P, const TrainBuffers& B, hipS
                                                    reinterpret_cast<float2*>(B.table_grad) + (uint64_t)B.n_dense * B.grid.table_size, B.state);
     }
     k_dw_gemm<<<kDwBlocks, kThreads, 0, st>>>(P, B.state, B.dw_stage, B.dw_partials);
-    k_dw_reduce<<<(kMlpParams + 63u) / 64u, 256, 0, st>>>(B.dw_partials, kDwBlocks, B.mlp_grad);
+    k_dw_reduce<<<(kMlpParams + 63u) / 64u, 256, 0, st>>>(B.dw_partials, kDwBlocks, B.mlp_grad, B.state);
     return hipGetLastError();
 }
 
 hipError_t launch_adam(const TrainParams& P, const TrainBuffers& B, hipStream_t st) {
     const uint32_t cap = device_cu_count() * 16u;
-    const uint64_t dense_elems = (uint64_t)B.n_dense * B.grid.table_size * 2u;  // hashed levels: counted by k_bin_accumulate
+    // The dense levels' gradient statistics; the binned levels' and the MLP's
+    // were taken when those gradients were written.
+    const uint64_t dense_elems = (uint64_t)B.n_dense * B.grid.table_size * 2u;
     if (dense_elems) k_grad_stats<<<grid_for(dense_elems / 4u, cap), 256, 0, st>>>(B.table_grad, dense_elems, B.state);
-    k_grad_stats<<<grid_for(kMlpParams, cap), 256, 0, st>>>(B.mlp_grad, kMlpParams, B.state);
-    k_adam_prepare<<<1, 64, 0, st>>>(P, B.state);
-    k_adam<<<grid_for(B.table_elems, cap), 256, 0, st>>>(P, B.state, B.table_f32, B.table, B.table_grad, B.table_m, B.table_v, B.table_elems);
-    // MLP masters: density then colour, fp16 copies in two separate arrays.
-    k_adam<<<grid_for(NERF_EXT_DENSITY_PARAMS, cap), 256, 0, st>>>(P, B.state, B.mlp_f32, B.dparams, B.mlp_grad, B.mlp_m, B.mlp_v, NERF_EXT_DENSITY_PARAMS);
-    k_adam<<<grid_for(NERF_EXT_COLOR_PARAMS, cap), 256, 0, st>>>(P, B.state, B.mlp_f32 + NERF_EXT_DENSITY_PARAMS, B.cparams, B.mlp_grad + NERF_EXT_DENSITY_PARAMS, B.mlp_m + NERF_EXT_DENSITY_PARAMS,
-                                                                B.mlp_v + NERF_EXT_DENSITY_PARAMS, NERF_EXT_COLOR_PARAMS);
+    if (B.table_elems % 4u) return hipErrorInvalidValue;
+    const AdamSeg table{B.table_f32, B.table, B.table_grad, B.table_m, B.table_v};
+    const AdamSeg mlp{B.mlp_f32, B.dparams, B.mlp_grad, B.mlp_m, B.mlp_v};
+    k_adam<<<grid_for(B.table_elems / 4u + kMlpParams, cap), 256, 0, st>>>(P, B.state, table, B.table_elems, mlp, B.cparams, NERF_EXT_DENSITY_PARAMS, kMlpParams);
     return hipGetLastError();
 }
 
