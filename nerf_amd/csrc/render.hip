@@ -341,6 +341,37 @@ __global__ __launch_bounds__(256) void k_scan_apply(const uint32_t* __restrict__
     }
 }
 
+// Apply pass for up to kScanDirect blocks, which sums the preceding block
+// totals itself (k_scan_sums is then not needed); the last block writes the
+// grand total.
+constexpr uint32_t kScanDirect = 2048u;
+__global__ __launch_bounds__(256) void k_scan_apply_direct(const uint32_t* __restrict__ in, uint32_t n, const uint32_t* __restrict__ block_sums, uint32_t* __restrict__ out, unsigned long long* __restrict__ total_out) {
+    __shared__ uint32_t lds4[4];
+    __shared__ unsigned long long wsum[4];
+    unsigned long long before = 0ull;  // 64-bit: the grand total may pass 2^32
+    for (uint32_t b = threadIdx.x; b < blockIdx.x; b += 256u) before += block_sums[b];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) before += __shfl_xor(before, o, 64);
+    if ((threadIdx.x & 63u) == 0u) wsum[threadIdx.x >> 6] = before;
+    __syncthreads();
+    const unsigned long long prefix = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+    const uint64_t base = (uint64_t)blockIdx.x * kScanBlock + 4u * threadIdx.x;
+    uint32_t v[4], s = 0u;
+#pragma unroll
+    for (uint32_t k = 0; k < 4u; ++k) {
+        v[k] = base + k < n ? in[base + k] : 0u;
+        s += v[k];
+    }
+    uint32_t total;
+    uint32_t run = block_exclusive_scan(s, lds4, &total) + (uint32_t)prefix;
+#pragma unroll
+    for (uint32_t k = 0; k < 4u; ++k) {
+        if (base + k < n) out[base + k] = run;
+        run += v[k];
+    }
+    if (blockIdx.x == gridDim.x - 1u && threadIdx.x == 0u) *total_out = prefix + total;
+}
+
 }  // namespace
 
 uint64_t scan_tmp_words(uint32_t n) { return (n + kScanBlock - 1u) / kScanBlock + 2u; }
@@ -349,8 +380,12 @@ hipError_t exclusive_scan_u32(const uint32_t* in, uint32_t* out, uint32_t n, uin
     const uint32_t blocks = (n + kScanBlock - 1u) / kScanBlock;
     if (blocks == 0u) return hipMemsetAsync(total, 0, sizeof(unsigned long long), stream);
     k_scan_reduce<<<blocks, 256, 0, stream>>>(in, n, tmp);
-    k_scan_sums<<<1, 256, 0, stream>>>(tmp, blocks, total);
-    k_scan_apply<<<blocks, 256, 0, stream>>>(in, n, tmp, out);
+    if (blocks <= kScanDirect) {
+        k_scan_apply_direct<<<blocks, 256, 0, stream>>>(in, n, tmp, out, total);
+    } else {
+        k_scan_sums<<<1, 256, 0, stream>>>(tmp, blocks, total);
+        k_scan_apply<<<blocks, 256, 0, stream>>>(in, n, tmp, out);
+    }
     return hipGetLastError();
 }
 

@@ -904,32 +904,44 @@ __global__ __launch_bounds__(256) void k_backward_clear(float* __restrict__ p, u
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) p[i] = 0.0f;
 }
 
-// Sum of the per-workgroup partials: workgroup x sums 64 parameters, its 4
-// waves each a quarter of the partials (independent loads in flight), then
-// the quarters are added in a fixed order.
-// The MLP gradient's share of the squared norm and the non-finite flag are
-// taken here, from the values written.
+// Sum of the per-workgroup partials: a workgroup takes 16 columns of 4
+// parameters; its 16 slices of 16 threads each add every 16th partial (16
+// independent four-wide loads per thread), then the slices are added in a
+// fixed order.  The MLP gradient's share of the squared norm and the
+// non-finite flag are taken here, from the values written.
+constexpr uint32_t kReduceSlices = 16u;
 __global__ __launch_bounds__(256) void k_dw_reduce(const float* __restrict__ partials, uint32_t blocks, float* __restrict__ grad, TrainDevState* S) {
-    __shared__ float part[4][64];
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    const uint32_t i    = blockIdx.x * 64u + lane;
-    float s             = 0.0f;
-    if (i < kMlpParams)
-        for (uint32_t b = wave; b < blocks; b += 4u) s += partials[(uint64_t)b * kMlpParams + i];
-    part[wave][lane] = s;
+    static_assert(kMlpParams % 64u == 0u, "whole columns per workgroup");
+    __shared__ float4 part[kReduceSlices][16];
+    const uint32_t col = threadIdx.x & 15u, slice = threadIdx.x >> 4;
+    const uint32_t c   = blockIdx.x * 16u + col;  // float4 column
+    const float4* p4   = reinterpret_cast<const float4*>(partials);
+    float4 s           = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (uint32_t b = slice; b < blocks; b += kReduceSlices) {
+        const float4 v = p4[(uint64_t)b * (kMlpParams / 4u) + c];
+        s.x += v.x;
+        s.y += v.y;
+        s.z += v.z;
+        s.w += v.w;
+    }
+    part[slice][col] = s;
     __syncthreads();
-    if (wave != 0u) return;
+    if (threadIdx.x >= 64u) return;
+    // Thread t < 64: parameter 4 * (blockIdx.x * 16) + t.
+    const uint32_t cc = threadIdx.x >> 2, e = threadIdx.x & 3u;
+    float gi          = 0.0f;
+    for (uint32_t k = 0; k < kReduceSlices; ++k) {
+        const float4 v = part[k][cc];
+        gi += e == 0u ? v.x : e == 1u ? v.y : e == 2u ? v.z : v.w;
+    }
+    grad[blockIdx.x * 64u + threadIdx.x] = gi;
     double sq = 0.0;
     bool bad  = false;
-    if (i < kMlpParams) {
-        const float gi = (part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]);
-        grad[i]        = gi;
-        if (isfinite(gi)) sq = (double)gi * (double)gi;
-        else bad = true;
-    }
+    if (isfinite(gi)) sq = (double)gi * (double)gi;
+    else bad = true;
     sq = wave_sum_d(sq);
-    if (__ballot(bad) != 0ull && lane == 0u) atomicOr(&S->nonfinite, 1u);
-    if (lane == 0u && sq != 0.0) atomicAdd(&S->grad_sumsq, sq);
+    if (__ballot(bad) != 0ull && threadIdx.x == 0u) atomicOr(&S->nonfinite, 1u);
+    if (threadIdx.x == 0u && sq != 0.0) atomicAdd(&S->grad_sumsq, sq);
 }
 
 // ------------------------------------------------------------------ Adam
@@ -1094,7 +1106,7 @@ hipError_t launch_mlp_backward(const TrainParams& P, const TrainBuffers& B, hipS
                                                    reinterpret_cast<float2*>(B.table_grad) + (uint64_t)B.n_dense * B.grid.table_size, B.state);
     }
     k_dw_gemm<<<kDwBlocks, kThreads, 0, st>>>(P, B.state, B.dw_stage, B.dw_partials);
-    k_dw_reduce<<<(kMlpParams + 63u) / 64u, 256, 0, st>>>(B.dw_partials, kDwBlocks, B.mlp_grad, B.state);
+    k_dw_reduce<<<kMlpParams / 64u, 256, 0, st>>>(B.dw_partials, kDwBlocks, B.mlp_grad, B.state);
     return hipGetLastError();
 }
 
