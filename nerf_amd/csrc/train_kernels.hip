@@ -648,8 +648,12 @@ __device__ __forceinline__ uint2 pack_record(float v0, float v1, uint32_t entry)
 __device__ __forceinline__ uint32_t record_entry(uint2 r) { return (r.x & 63u) | ((r.y & 63u) << 6); }
 __device__ __forceinline__ float2 record_value(uint2 r) { return make_float2(__uint_as_float(r.x & ~63u), __uint_as_float(r.y & ~63u)); }
 
+// 16 waves per workgroup: the 128 KiB of LDS counters allow one workgroup
+// per CU, and the LDS atomics and record stores need several waves per SIMD
+// to hide their latency.
+constexpr uint32_t kBinThreads = 1024u;
 template <bool kFill>
-__global__ __launch_bounds__(256) void k_bin_pass(TrainParams P, GridParams g, const TrainDevState* S, const float2* __restrict__ samples, const uint32_t* __restrict__ sample_ray, const float4* __restrict__ rays,
+__global__ __launch_bounds__(kBinThreads) void k_bin_pass(TrainParams P, GridParams g, const TrainDevState* S, const float2* __restrict__ samples, const uint32_t* __restrict__ sample_ray, const float4* __restrict__ rays,
                                                   const float* __restrict__ dfeat, uint32_t n_dense, uint32_t n_bins, uint32_t* __restrict__ hist, uint2* __restrict__ rec,
                                                   uint32_t* __restrict__ bin_max) {
     __shared__ uint32_t cursor[kMaxBins];
@@ -1098,10 +1102,10 @@ hipError_t launch_mlp_backward(const TrainParams& P, const TrainBuffers& B, hipS
     k_bwd_dx<<<cus * 2u, kThreads, kDxLds, st>>>(P, B.grid, B.state, B.dparams, B.cparams, B.features, B.draw, B.samples, B.sample_ray, B.rays, B.dfeat, B.n_dense, B.table_grad, B.dw_stage);
     // Hashed levels: binned.
     if (B.n_bins) {
-        k_bin_pass<false><<<kBinBlocks, 256, 0, st>>>(P, B.grid, B.state, B.samples, B.sample_ray, B.rays, B.dfeat, B.n_dense, B.n_bins, B.bin_hist, nullptr, nullptr);
+        k_bin_pass<false><<<kBinBlocks, kBinThreads, 0, st>>>(P, B.grid, B.state, B.samples, B.sample_ray, B.rays, B.dfeat, B.n_dense, B.n_bins, B.bin_hist, nullptr, nullptr);
         const hipError_t e = exclusive_scan_u32(B.bin_hist, B.bin_off, B.n_bins * kBinBlocks, B.bin_scan_tmp, B.bin_total, st);
         if (e != hipSuccess) return e;
-        k_bin_pass<true><<<kBinBlocks, 256, 0, st>>>(P, B.grid, B.state, B.samples, B.sample_ray, B.rays, B.dfeat, B.n_dense, B.n_bins, B.bin_off, B.rec, B.bin_max);
+        k_bin_pass<true><<<kBinBlocks, kBinThreads, 0, st>>>(P, B.grid, B.state, B.samples, B.sample_ray, B.rays, B.dfeat, B.n_dense, B.n_bins, B.bin_off, B.rec, B.bin_max);
         k_bin_accumulate<<<B.n_bins, 512, 0, st>>>(B.bin_off, kBinBlocks, B.n_bins, B.bin_total, B.rec, B.bin_max, (uint64_t)(B.grid.n_levels - B.n_dense) * B.grid.table_size,
                                                    reinterpret_cast<float2*>(B.table_grad) + (uint64_t)B.n_dense * B.grid.table_size, B.state);
     }
