@@ -414,12 +414,42 @@ struct TileGrad {
 
 // Recomputes the forward of one tile and back-propagates (loss-scaled fp16
 // deltas, fp32 MFMA accumulation): the chain of the oracle's orc_mlp_backward.
-__device__ __forceinline__ void tile_backward(const half_t* dp, const half_t* cp, const DensityFrags& fd, const half8_t x, const float d[3], const float4 g, float ls, uint32_t grp, TileGrad& T) {
+// Every A operand of the tile's products, in MFMA fragment order: fragment
+// f of lane l is the 16 bytes at F[64 f + l], so each is one conflict-free
+// 128-bit LDS read.
+enum : uint32_t {
+    kFragCF1 = 0,   // colour layer 1 (ColorIn map), blocks 0..3
+    kFragCF2 = 4,   // colour layer 2, [2 block + k-step]
+    kFragC3T = 12,  // colour output, transposed, blocks 0..3
+    kFragC2T = 16,  // colour layer 2, transposed, [2 block + k-step]
+    kFragC1T = 24,  // colour layer 1, transposed, k-steps 0..1
+    kFragD2T = 26,  // density output, transposed, blocks 0..3
+    kFragD1T = 30,  // density layer 1, transposed, [2 block + k-step]
+    kFragDW1 = 34,  // density layer 1, blocks 0..3
+    kFragDW2 = 38,  // density output, k-steps 0..1
+    kFrags   = 40,
+};
+__device__ half8_t build_frag(uint32_t f, const half_t* dp, const half_t* cp, uint32_t lane) {
+    if (f < kFragCF2) return load_a(cp, 32u, f - kFragCF1, 0u, KMap::ColorIn, lane);
+    if (f < kFragC3T) return load_a(cp + 2048, 64u, (f - kFragCF2) >> 1, (f - kFragCF2) & 1u, KMap::Hidden, lane);
+    if (f < kFragC2T) return frag_c3t(cp, f - kFragC3T, lane);
+    if (f < kFragC1T) return frag_hidden_t(cp + 2048, 64u, (f - kFragC2T) >> 1, (f - kFragC2T) & 1u, lane);
+    if (f < kFragD2T) return frag_c1t(cp, f - kFragC1T, lane);
+    if (f < kFragD1T) return frag_d2t(dp, f - kFragD2T, lane);
+    if (f < kFragDW1) return frag_hidden_t(dp, 32u, (f - kFragD1T) >> 1, (f - kFragD1T) & 1u, lane);
+    if (f < kFragDW2) return load_a(dp, 32u, f - kFragDW1, 0u, KMap::Identity, lane);
+    return load_a(dp + 2048, 64u, 0u, f - kFragDW2, KMap::Hidden, lane);
+}
+
+__device__ __forceinline__ void tile_backward(const half8_t* F, const half8_t x, const float d[3], const float4 g, float ls, uint32_t grp, TileGrad& T) {
     const floatx4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
     const uint32_t lane = threadIdx.x & 63u;
+    auto frag = [&](uint32_t f) { return F[64u * f + lane]; };
     T.x = x;
-    layer_32_64(fd.w1, x, T.hd);
-    const floatx4 o = layer_64_16(fd.w2, T.hd);
+    const half8_t dw1[4] = {frag(kFragDW1), frag(kFragDW1 + 1u), frag(kFragDW1 + 2u), frag(kFragDW1 + 3u)};
+    const half8_t dw2[2] = {frag(kFragDW2), frag(kFragDW2 + 1u)};
+    layer_32_64(dw1, x, T.hd);
+    const floatx4 o = layer_64_16(dw2, T.hd);
     float sh[4];
     sh4_quad(d, grp, sh);
 #pragma unroll
@@ -428,13 +458,13 @@ __device__ __forceinline__ void tile_backward(const half_t* dp, const half_t* cp
         T.xc[4 + e] = (half_t)sh[e];
     }
     if (grp == 0u) T.xc[0] = (half_t)0.0f;
-    // colour forward (weights straight from LDS)
+    // colour forward
 #pragma unroll
-    for (uint32_t b = 0; b < 4u; ++b) T.h1[b] = relu_half(mfma16x16x32(load_a(cp, 32u, b, 0u, KMap::ColorIn, lane), T.xc, zero));
+    for (uint32_t b = 0; b < 4u; ++b) T.h1[b] = relu_half(mfma16x16x32(frag(kFragCF1 + b), T.xc, zero));
 #pragma unroll
     for (uint32_t b = 0; b < 4u; ++b) {
-        floatx4 a = mfma16x16x32(load_a(cp + 2048, 64u, b, 0u, KMap::Hidden, lane), cat(T.h1[0], T.h1[1]), zero);
-        a         = mfma16x16x32(load_a(cp + 2048, 64u, b, 1u, KMap::Hidden, lane), cat(T.h1[2], T.h1[3]), a);
+        floatx4 a = mfma16x16x32(frag(kFragCF2 + 2u * b), cat(T.h1[0], T.h1[1]), zero);
+        a         = mfma16x16x32(frag(kFragCF2 + 2u * b + 1u), cat(T.h1[2], T.h1[3]), a);
         T.h2[b]   = relu_half(a);
     }
     // colour backward
@@ -445,26 +475,26 @@ __device__ __forceinline__ void tile_backward(const half_t* dp, const half_t* cp
         T.do3[e]         = to_half_rne(ls * v);
     }
 #pragma unroll
-    for (uint32_t b = 0; b < 4u; ++b) T.dh2[b] = mask_half(mfma16x16x32(frag_c3t(cp, b, lane), T.do3, zero), T.h2[b]);
+    for (uint32_t b = 0; b < 4u; ++b) T.dh2[b] = mask_half(mfma16x16x32(frag(kFragC3T + b), T.do3, zero), T.h2[b]);
 #pragma unroll
     for (uint32_t b = 0; b < 4u; ++b) {
-        floatx4 a = mfma16x16x32(frag_hidden_t(cp + 2048, 64u, b, 0u, lane), cat(T.dh2[0], T.dh2[1]), zero);
-        a         = mfma16x16x32(frag_hidden_t(cp + 2048, 64u, b, 1u, lane), cat(T.dh2[2], T.dh2[3]), a);
+        floatx4 a = mfma16x16x32(frag(kFragC2T + 2u * b), cat(T.dh2[0], T.dh2[1]), zero);
+        a         = mfma16x16x32(frag(kFragC2T + 2u * b + 1u), cat(T.dh2[2], T.dh2[3]), a);
         T.dh1[b]  = mask_half(a, T.h1[b]);
     }
-    floatx4 dgeo = mfma16x16x32(frag_c1t(cp, 0u, lane), cat(T.dh1[0], T.dh1[1]), zero);
-    dgeo         = mfma16x16x32(frag_c1t(cp, 1u, lane), cat(T.dh1[2], T.dh1[3]), dgeo);
+    floatx4 dgeo = mfma16x16x32(frag(kFragC1T), cat(T.dh1[0], T.dh1[1]), zero);
+    dgeo         = mfma16x16x32(frag(kFragC1T + 1u), cat(T.dh1[2], T.dh1[3]), dgeo);
     // density backward
 #pragma unroll
     for (int e = 0; e < 4; ++e) T.dout[e] = (half_t)dgeo[e];
     if (grp == 0u) T.dout[0] = to_half_rne(ls * g.x);
     const half4_t z4 = {(half_t)0.0f, (half_t)0.0f, (half_t)0.0f, (half_t)0.0f};
 #pragma unroll
-    for (uint32_t b = 0; b < 4u; ++b) T.dhd[b] = mask_half(mfma16x16x32(frag_d2t(dp, b, lane), cat(T.dout, z4), zero), T.hd[b]);
+    for (uint32_t b = 0; b < 4u; ++b) T.dhd[b] = mask_half(mfma16x16x32(frag(kFragD2T + b), cat(T.dout, z4), zero), T.hd[b]);
 #pragma unroll
     for (uint32_t b = 0; b < 2u; ++b) {
-        floatx4 a = mfma16x16x32(frag_hidden_t(dp, 32u, b, 0u, lane), cat(T.dhd[0], T.dhd[1]), zero);
-        T.dx[b]   = mfma16x16x32(frag_hidden_t(dp, 32u, b, 1u, lane), cat(T.dhd[2], T.dhd[3]), a);
+        floatx4 a = mfma16x16x32(frag(kFragD1T + 2u * b), cat(T.dhd[0], T.dhd[1]), zero);
+        T.dx[b]   = mfma16x16x32(frag(kFragD1T + 2u * b + 1u), cat(T.dhd[2], T.dhd[3]), a);
     }
 }
 
@@ -554,29 +584,48 @@ __device__ __forceinline__ void scatter_level(const GridParams& g, float* __rest
 // would take every sample's records) are scattered here with row-combined
 // atomics.  Lane (g, s) holds features 16b + 4g + e of
 // sample s, i.e. levels 2g, 2g+1 (b = 0) and 8+2g, 9+2g (b = 1).
-// Rows 16b + 4g + e, column s16 of a 16-column tile region.
+// The staging tile of a wave holds half of the tile's 480 operand rows at a
+// time (rows [240 h, 240 h + 240)), 16 samples each, rows padded to 40 bytes:
+// the four rows one 16-bit store instruction writes (rows r + 4g of lane
+// group g) then fall in four disjoint groups of 8 banks.
+constexpr uint32_t kHalfRows   = kStageRows / 2u;
+constexpr uint32_t kStagePitch = 20u;  // halves per LDS row
+constexpr uint32_t kDxFragBytes  = kFrags * 64u * 16u;
+constexpr uint32_t kDxStageBytes = kWaves * kHalfRows * kStagePitch * 2u;
+constexpr uint32_t kDxLds        = kDxFragBytes + kDxStageBytes;  // bytes of dynamic LDS: two workgroups per CU
+static_assert(kDxLds <= 81920u, "two workgroups per CU");
+static_assert(kMlpParams * 2u <= kDxStageBytes, "raw weights are staged in the operand area");
+
+// Row r (global staging row) of lane (g, s16) in a 16-column region.
+__device__ __forceinline__ void put_row(half_t* L, uint32_t row, uint32_t s16, half_t v) { L[row * kStagePitch + s16] = v; }
+// Rows 16b + 4g + e of a 64-row block starting at local row row0.
 __device__ __forceinline__ void put16(half_t* L, uint32_t row0, const half4_t v[4], uint32_t s16, uint32_t grp) {
 #pragma unroll
     for (uint32_t b = 0; b < 4u; ++b)
 #pragma unroll
-        for (uint32_t e = 0; e < 4u; ++e) L[(row0 + 16u * b + 4u * grp + e) * 16u + s16] = v[b][e];
+        for (uint32_t e = 0; e < 4u; ++e) put_row(L, row0 + 16u * b + 4u * grp + e, s16, v[b][e]);
 }
-
-constexpr uint32_t kDxLds = (kMlpParams + kWaves * kStageRows * 16u) * 2u;  // bytes of dynamic LDS
+// One half of the tile's operand rows, LDS -> dw_stage rows [240 h, 240 h + 240).
+__device__ __forceinline__ void copy_half(const half_t* L, half_t* __restrict__ stage_tile, uint32_t h, uint32_t lane) {
+    uint2* dst = reinterpret_cast<uint2*>(stage_tile + (uint64_t)h * kHalfRows * 16u);
+    for (uint32_t j = lane; j < kHalfRows * 4u; j += 64u) dst[j] = *reinterpret_cast<const uint2*>(L + (j >> 2) * kStagePitch + 4u * (j & 3u));
+}
 
 __global__ __launch_bounds__(kThreads) void k_bwd_dx(TrainParams P, GridParams g, const TrainDevState* S, const half_t* __restrict__ dparams, const half_t* __restrict__ cparams, const half_t* __restrict__ features,
                                                      const float4* __restrict__ draw, const float2* __restrict__ samples, const uint32_t* __restrict__ sample_ray, const float4* __restrict__ rays, float* __restrict__ dfeat, uint32_t n_dense,
                                                      float* __restrict__ table_grad, half_t* __restrict__ dw_stage) {
     extern __shared__ __align__(16) half_t dyn[];
-    half_t* sp = dyn;
-    for (uint32_t i = threadIdx.x; i < NERF_EXT_DENSITY_PARAMS; i += blockDim.x) sp[i] = dparams[i];
-    for (uint32_t i = threadIdx.x; i < NERF_EXT_COLOR_PARAMS; i += blockDim.x) sp[NERF_EXT_DENSITY_PARAMS + i] = cparams[i];
+    half8_t* F    = reinterpret_cast<half8_t*>(dyn);
+    half_t* stage = dyn + kDxFragBytes / 2u;
+    // Raw weights into the operand area, then every fragment built once.
+    for (uint32_t i = threadIdx.x; i < NERF_EXT_DENSITY_PARAMS; i += blockDim.x) stage[i] = dparams[i];
+    for (uint32_t i = threadIdx.x; i < NERF_EXT_COLOR_PARAMS; i += blockDim.x) stage[NERF_EXT_DENSITY_PARAMS + i] = cparams[i];
+    __syncthreads();
+    const uint32_t lane = threadIdx.x & 63u, grp = lane >> 4, s16 = lane & 15u;
+    for (uint32_t f = threadIdx.x >> 6; f < kFrags; f += kWaves) F[64u * f + lane] = build_frag(f, stage, stage + NERF_EXT_DENSITY_PARAMS, lane);
     __syncthreads();
     const uint32_t n = min(S->n_samples, P.sample_cap);
-    const uint32_t lane = threadIdx.x & 63u, grp = lane >> 4, s16 = lane & 15u;
-    half_t* W = dyn + kMlpParams + (threadIdx.x >> 6) * kStageRows * 16u;  // this wave's staging tile
-    DensityFrags fd;
-    load_density(sp, fd, lane);
+    half_t* W        = stage + (threadIdx.x >> 6) * kHalfRows * kStagePitch;  // this wave's staging rows
     const uint32_t tiles = (n + 15u) / 16u;
     for (uint32_t tile = blockIdx.x * kWaves + (threadIdx.x >> 6); tile < tiles; tile += gridDim.x * kWaves) {
         const uint32_t s = tile * 16u + s16;
@@ -588,37 +637,42 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dx(TrainParams P, GridParams g
         float4 gr       = draw[q];
         if (!live) gr = make_float4(0.0f, 0.0f, 0.0f, 0.0f);  // padding samples add nothing to the weight gradients
         TileGrad T;
-        tile_backward(sp, sp + NERF_EXT_DENSITY_PARAMS, fd, x, d, gr, P.loss_scale, grp, T);
+        tile_backward(F, x, d, gr, P.loss_scale, grp, T);
         if (live) {
             float4* o = reinterpret_cast<float4*>(dfeat + (uint64_t)s * 32u);
             o[grp]      = make_float4(T.dx[0][0], T.dx[0][1], T.dx[0][2], T.dx[0][3]);
             o[4u + grp] = make_float4(T.dx[1][0], T.dx[1][1], T.dx[1][2], T.dx[1][3]);
         }
-        // Weight-gradient operands of this tile, neuron-major through LDS,
-        // then one contiguous 15 KB copy to dw_stage.
+        // Weight-gradient operands of this tile, neuron-major through LDS in
+        // two halves, each copied to dw_stage as 7.5 KB of contiguous rows.
+        half_t* stage_tile = dw_stage + (uint64_t)tile * kStageRows * 16u;
         wave_lds_sync();
         put16(W, kRowDh2, T.dh2, s16, grp);
         put16(W, kRowH1, T.h1, s16, grp);
         put16(W, kRowDh1, T.dh1, s16, grp);
-        put16(W, kRowH2, T.h2, s16, grp);
-        put16(W, kRowDhd, T.dhd, s16, grp);
-        put16(W, kRowHd, T.hd, s16, grp);
 #pragma unroll
         for (uint32_t e = 0; e < 8u; ++e) {  // colour input in logical order; row 31 is the zero pad
             const int k = logical_k(KMap::ColorIn, 0u, grp, e);
-            W[(kRowXc + (k < 0 ? 31u : (uint32_t)k)) * 16u + s16] = k < 0 ? (half_t)0.0f : T.xc[e];
-            if (8u * grp + e < 16u) W[(kRowDo3 + 8u * grp + e) * 16u + s16] = T.do3[e];
-            W[(kRowX + 8u * grp + e) * 16u + s16] = T.x[e];
+            put_row(W, kRowXc + (k < 0 ? 31u : (uint32_t)k), s16, k < 0 ? (half_t)0.0f : T.xc[e]);
+            if (8u * grp + e < 16u) put_row(W, kRowDo3 + 8u * grp + e, s16, T.do3[e]);
         }
-#pragma unroll
-        for (uint32_t e = 0; e < 4u; ++e) W[(kRowDout + 4u * grp + e) * 16u + s16] = T.dout[e];
         wave_lds_sync();
-        const uint4* src = reinterpret_cast<const uint4*>(W);
-        uint4* dst       = reinterpret_cast<uint4*>(dw_stage + (uint64_t)tile * kStageRows * 16u);
-        for (uint32_t i = lane; i < kStageRows * 2u; i += 64u) dst[i] = src[i];
-        if (n_dense > 0u) {  // uniform: the dense levels are the first n_dense levels
+        copy_half(W, stage_tile, 0u, lane);
+        wave_lds_sync();
+        put16(W, kRowH2 - kHalfRows, T.h2, s16, grp);
+        put16(W, kRowDhd - kHalfRows, T.dhd, s16, grp);
+        put16(W, kRowHd - kHalfRows, T.hd, s16, grp);
 #pragma unroll
-            for (uint32_t b = 0; b < 2u; ++b) {
+        for (uint32_t e = 0; e < 8u; ++e) put_row(W, kRowX - kHalfRows + 8u * grp + e, s16, T.x[e]);
+#pragma unroll
+        for (uint32_t e = 0; e < 4u; ++e) put_row(W, kRowDout - kHalfRows + 4u * grp + e, s16, T.dout[e]);
+        wave_lds_sync();
+        copy_half(W, stage_tile, 1u, lane);
+        // The atomic levels are the first n_dense; lane group g holds levels
+        // 2g, 2g + 1 (b = 0) and 8 + 2g, 9 + 2g (b = 1).
+#pragma unroll
+        for (uint32_t b = 0; b < 2u; ++b) {
+            if (8u * b < n_dense) {  // uniform
                 const uint32_t l0 = 8u * b + 2u * grp;
                 scatter_level(g, table_grad, l0, p, T.dx[b][0], T.dx[b][1], live && l0 < n_dense);
                 scatter_level(g, table_grad, l0 + 1u, p, T.dx[b][2], T.dx[b][3], live && l0 + 1u < n_dense);
