@@ -66,7 +66,6 @@ struct TrainBuffers {
     half_t* features;            // [sample_cap][32]
     float4* draw;                // [sample_cap] (d sigma_raw, d r, d g, d b)
     float* dfeat;                // [sample_cap][32] d(features), loss-scaled
-    half_t* dw_stage;            // [tile][kStageRows][16 samples] fp16 operands of the weight gradients
     // binned hash-grid scatter: records (entry within bin, 2 values) grouped
     // by bin of kBinEntries table entries
     uint32_t* bin_hist;          // [n_bins][kBinBlocks] record counts
@@ -91,15 +90,11 @@ struct TrainBuffers {
     float* mlp_grad;             // 10240, loss-scaled
     float* mlp_m;
     float* mlp_v;
-    float* dw_partials;          // [kDwBlocks][10240]
+    float* dw_partials;          // [kDxMaxBlocks][10240] per-workgroup weight-gradient partials
     uint64_t table_elems;
 };
 
-constexpr uint32_t kDwBlocks   = 256;   // workgroups of the weight-gradient pass
-// Rows of one 16-sample tile in dw_stage: the deltas and activations whose
-// products over samples are the weight gradients (neuron-major, 16 samples
-// per row).
-constexpr uint32_t kRowDh2 = 0, kRowH1 = 64, kRowDh1 = 128, kRowXc = 192, kRowDo3 = 224, kRowH2 = 240, kRowDhd = 304, kRowX = 368, kRowDout = 400, kRowHd = 416, kStageRows = 480;
+constexpr uint32_t kDxMaxBlocks = 1024;  // workgroups of the input-gradient pass (two per CU)
 constexpr uint32_t kBinEntries = 4096;  // table entries per scatter bin (64 KiB of int64 pairs in LDS)
 constexpr uint32_t kBinBlocks  = 256;   // workgroups of the bin count / fill passes
 constexpr uint32_t kAtomicMaxEntries = 1u << 15;  // largest level scattered with atomics

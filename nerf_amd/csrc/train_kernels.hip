@@ -6,8 +6,9 @@
 // ray sampling + march      :422-533                       k_train_rays, scan, k_train_samples
 // field forward             :1328-1339                     launch_field (field.hip)
 // composite fwd/bwd + loss  :1095-1182 (MSE)               k_composite_train (Huber)
-// MLP backward              :784-909, 1267-1301 (cuBLAS)   k_bwd_dx (+ hash scatter, dW operands), k_dw_gemm, k_dw_reduce
-// grad stats, Adam          :1447-1554                     k_grad_stats, k_adam_prepare, k_adam
+// MLP backward              :784-909, 1267-1301 (cuBLAS)   k_bwd_dx (dfeat, dW partials, coarse-level atomics), k_dw_reduce
+// hash-table backward       (hash-grid model)              k_bin_pass (count, fill), scan, k_bin_accumulate
+// grad stats, Adam          :1447-1554                     k_grad_stats, k_adam
 // end step                  :1495-1512                     k_step_end
 //
 // MI355X choices: every count lives in device memory and every launch has a
@@ -15,11 +16,11 @@
 // HIP has no conditional graph nodes, so the reference's bucket switch
 // (:1489-1494) becomes kernels that read their counts and exit early).  The
 // MLP backward recomputes the forward per 16-sample tile in registers (MFMA
-// is cheap next to moving activations through HBM); the input-gradient pass
-// scatters straight into the hash-table gradient; the weight gradients run as
-// three recompute passes whose per-tile sample axis is moved onto the MFMA
-// reduction axis through a per-wave LDS transpose, with deterministic
-// per-workgroup partials.
+// is cheap next to moving activations through HBM) and, in the same pass,
+// moves each tile's deltas and activations through LDS onto the MFMA
+// reduction axis for the weight gradients (deterministic per-workgroup
+// partials); the hash-table gradient goes through sorted bins with exact
+// fixed-point sums.
 #include "mlp_device.hpp"
 #include "wave.hpp"
 #include "train.hpp"
@@ -584,53 +585,77 @@ __device__ __forceinline__ void scatter_level(const GridParams& g, float* __rest
 // would take every sample's records) are scattered here with row-combined
 // atomics.  Lane (g, s) holds features 16b + 4g + e of
 // sample s, i.e. levels 2g, 2g+1 (b = 0) and 8+2g, 9+2g (b = 1).
-// The staging tile of a wave holds half of the tile's 480 operand rows at a
-// time (rows [240 h, 240 h + 240)), 16 samples each, rows padded to 40 bytes:
-// the four rows one 16-bit store instruction writes (rows r + 4g of lane
-// group g) then fall in four disjoint groups of 8 banks.
-constexpr uint32_t kHalfRows   = kStageRows / 2u;
-constexpr uint32_t kStagePitch = 20u;  // halves per LDS row
+// Weight gradients inside the same pass.  dW = sum over samples of delta
+// act^T needs the sample axis on the MFMA reduction axis, so each phase every
+// wave puts its tile's deltas and activations of some layers into LDS,
+// neuron-major (row = neuron, 16 samples per row); after a barrier the four
+// tiles (64 samples = two k-steps of 32) are multiplied out.  The 40 16x16
+// blocks of the five weight matrices are split 10 per wave: wave w owns
+// output block w of the colour hidden, colour input and density input
+// layers and input block w of the two 16-wide output layers, and keeps them
+// in registers for the whole pass; the workgroup writes one partial per
+// parameter at the end (fixed order throughout, so the result is
+// deterministic).  Phases (rows per tile):
+//   1: dh2 [0,64) h1 [64,128)
+//   2: dh1 [0,64) xc [64,96) do3 [96,112) h2 [112,176)
+//   3: dhd [0,64) x  [64,96) dout [96,112) hd [112,176)
+// Rows are 48 bytes (16 samples + pad): 16-byte aligned fragment reads, and
+// the four rows one 16-bit store instruction writes (r + 4g) fall in two
+// bank groups.
+constexpr uint32_t kPhaseRows    = 176u;
+constexpr uint32_t kOpPitch      = 24u;  // halves per LDS row
 constexpr uint32_t kDxFragBytes  = kFrags * 64u * 16u;
-constexpr uint32_t kDxStageBytes = kWaves * kHalfRows * kStagePitch * 2u;
-constexpr uint32_t kDxLds        = kDxFragBytes + kDxStageBytes;  // bytes of dynamic LDS: two workgroups per CU
+constexpr uint32_t kDxOpBytes    = kWaves * kPhaseRows * kOpPitch * 2u;
+constexpr uint32_t kDxLds        = kDxFragBytes + kDxOpBytes;  // bytes of dynamic LDS: two workgroups per CU
 static_assert(kDxLds <= 81920u, "two workgroups per CU");
-static_assert(kMlpParams * 2u <= kDxStageBytes, "raw weights are staged in the operand area");
+static_assert(kMlpParams * 2u <= kDxOpBytes, "raw weights are staged in the operand area");
 
-// Row r (global staging row) of lane (g, s16) in a 16-column region.
-__device__ __forceinline__ void put_row(half_t* L, uint32_t row, uint32_t s16, half_t v) { L[row * kStagePitch + s16] = v; }
-// Rows 16b + 4g + e of a 64-row block starting at local row row0.
+__device__ __forceinline__ void put_row(half_t* L, uint32_t row, uint32_t s16, half_t v) { L[row * kOpPitch + s16] = v; }
+// Rows 16b + 4g + e of a 64-row block starting at row0.
 __device__ __forceinline__ void put16(half_t* L, uint32_t row0, const half4_t v[4], uint32_t s16, uint32_t grp) {
 #pragma unroll
     for (uint32_t b = 0; b < 4u; ++b)
 #pragma unroll
         for (uint32_t e = 0; e < 4u; ++e) put_row(L, row0 + 16u * b + 4u * grp + e, s16, v[b][e]);
 }
-// One half of the tile's operand rows, LDS -> dw_stage rows [240 h, 240 h + 240).
-__device__ __forceinline__ void copy_half(const half_t* L, half_t* __restrict__ stage_tile, uint32_t h, uint32_t lane) {
-    uint2* dst = reinterpret_cast<uint2*>(stage_tile + (uint64_t)h * kHalfRows * 16u);
-    for (uint32_t j = lane; j < kHalfRows * 4u; j += 64u) dst[j] = *reinterpret_cast<const uint2*>(L + (j >> 2) * kStagePitch + 4u * (j & 3u));
+// A or B fragment of rows [row0, row0 + 16) over k-step ks: lane (r, g) takes
+// row r, samples 8 (g & 1) .. + 7 of the tile of wave 2 ks + (g >> 1).
+__device__ __forceinline__ half8_t op_frag(const half_t* ops, uint32_t row0, uint32_t ks, uint32_t lane) {
+    const uint32_t r = lane & 15u, g = lane >> 4;
+    const half_t* region = ops + (2u * ks + (g >> 1)) * kPhaseRows * kOpPitch;
+    return *reinterpret_cast<const half8_t*>(region + (row0 + r) * kOpPitch + 8u * (g & 1u));
 }
 
 __global__ __launch_bounds__(kThreads) void k_bwd_dx(TrainParams P, GridParams g, const TrainDevState* S, const half_t* __restrict__ dparams, const half_t* __restrict__ cparams, const half_t* __restrict__ features,
                                                      const float4* __restrict__ draw, const float2* __restrict__ samples, const uint32_t* __restrict__ sample_ray, const float4* __restrict__ rays, float* __restrict__ dfeat, uint32_t n_dense,
-                                                     float* __restrict__ table_grad, half_t* __restrict__ dw_stage) {
+                                                     float* __restrict__ table_grad, float* __restrict__ partials) {
     extern __shared__ __align__(16) half_t dyn[];
-    half8_t* F    = reinterpret_cast<half8_t*>(dyn);
-    half_t* stage = dyn + kDxFragBytes / 2u;
+    half8_t* F  = reinterpret_cast<half8_t*>(dyn);
+    half_t* ops = dyn + kDxFragBytes / 2u;
     // Raw weights into the operand area, then every fragment built once.
-    for (uint32_t i = threadIdx.x; i < NERF_EXT_DENSITY_PARAMS; i += blockDim.x) stage[i] = dparams[i];
-    for (uint32_t i = threadIdx.x; i < NERF_EXT_COLOR_PARAMS; i += blockDim.x) stage[NERF_EXT_DENSITY_PARAMS + i] = cparams[i];
+    for (uint32_t i = threadIdx.x; i < NERF_EXT_DENSITY_PARAMS; i += blockDim.x) ops[i] = dparams[i];
+    for (uint32_t i = threadIdx.x; i < NERF_EXT_COLOR_PARAMS; i += blockDim.x) ops[NERF_EXT_DENSITY_PARAMS + i] = cparams[i];
     __syncthreads();
-    const uint32_t lane = threadIdx.x & 63u, grp = lane >> 4, s16 = lane & 15u;
-    for (uint32_t f = threadIdx.x >> 6; f < kFrags; f += kWaves) F[64u * f + lane] = build_frag(f, stage, stage + NERF_EXT_DENSITY_PARAMS, lane);
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u, grp = lane >> 4, s16 = lane & 15u;
+    for (uint32_t f = wave; f < kFrags; f += kWaves) F[64u * f + lane] = build_frag(f, ops, ops + NERF_EXT_DENSITY_PARAMS, lane);
     __syncthreads();
-    const uint32_t n = min(S->n_samples, P.sample_cap);
-    half_t* W        = stage + (threadIdx.x >> 6) * kHalfRows * kStagePitch;  // this wave's staging rows
+    const uint32_t n     = min(S->n_samples, P.sample_cap);
     const uint32_t tiles = (n + 15u) / 16u;
-    for (uint32_t tile = blockIdx.x * kWaves + (threadIdx.x >> 6); tile < tiles; tile += gridDim.x * kWaves) {
-        const uint32_t s = tile * 16u + s16;
-        const bool live  = s < n;
-        const uint32_t q = live ? s : n - 1u;
+    half_t* W            = ops + wave * kPhaseRows * kOpPitch;  // this wave's operand rows
+    const floatx4 zero   = {0.0f, 0.0f, 0.0f, 0.0f};
+    floatx4 acc_h[4], acc_ci[2], acc_di[2], acc_co = zero, acc_do = zero;
+#pragma unroll
+    for (uint32_t i = 0; i < 4u; ++i) acc_h[i] = zero;
+    acc_ci[0] = acc_ci[1] = acc_di[0] = acc_di[1] = zero;
+    // Every wave of the workgroup runs the same number of iterations (the
+    // barriers); a wave past the last tile runs one with zero deltas.
+    const uint32_t first = blockIdx.x * kWaves, stride = gridDim.x * kWaves;
+    const uint32_t iters = tiles > first ? (tiles - first + stride - 1u) / stride : 0u;
+    for (uint32_t it = 0; it < iters; ++it) {
+        const uint32_t tile = first + wave + it * stride;
+        const uint32_t s    = tile * 16u + s16;
+        const bool live     = tile < tiles && s < n;
+        const uint32_t q    = live ? s : n - 1u;  // n > 0 here
         float p[3], d[3];
         sample_geometry(samples, sample_ray, rays, P.bmin, P.bmax, q, p, d);
         const half8_t x = *reinterpret_cast<const half8_t*>(features + (uint64_t)q * 32u + 8u * grp);
@@ -643,31 +668,51 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dx(TrainParams P, GridParams g
             o[grp]      = make_float4(T.dx[0][0], T.dx[0][1], T.dx[0][2], T.dx[0][3]);
             o[4u + grp] = make_float4(T.dx[1][0], T.dx[1][1], T.dx[1][2], T.dx[1][3]);
         }
-        // Weight-gradient operands of this tile, neuron-major through LDS in
-        // two halves, each copied to dw_stage as 7.5 KB of contiguous rows.
-        half_t* stage_tile = dw_stage + (uint64_t)tile * kStageRows * 16u;
-        wave_lds_sync();
-        put16(W, kRowDh2, T.dh2, s16, grp);
-        put16(W, kRowH1, T.h1, s16, grp);
-        put16(W, kRowDh1, T.dh1, s16, grp);
+        // Phase 1: colour hidden layer.
+        put16(W, 0u, T.dh2, s16, grp);
+        put16(W, 64u, T.h1, s16, grp);
+        __syncthreads();
+#pragma unroll
+        for (uint32_t ks = 0; ks < 2u; ++ks) {
+            const half8_t a = op_frag(ops, 16u * wave, ks, lane);
+#pragma unroll
+            for (uint32_t ib = 0; ib < 4u; ++ib) acc_h[ib] = mfma16x16x32(a, op_frag(ops, 64u + 16u * ib, ks, lane), acc_h[ib]);
+        }
+        __syncthreads();
+        // Phase 2: colour input and output layers.
+        put16(W, 0u, T.dh1, s16, grp);
 #pragma unroll
         for (uint32_t e = 0; e < 8u; ++e) {  // colour input in logical order; row 31 is the zero pad
             const int k = logical_k(KMap::ColorIn, 0u, grp, e);
-            put_row(W, kRowXc + (k < 0 ? 31u : (uint32_t)k), s16, k < 0 ? (half_t)0.0f : T.xc[e]);
-            if (8u * grp + e < 16u) put_row(W, kRowDo3 + 8u * grp + e, s16, T.do3[e]);
+            put_row(W, 64u + (k < 0 ? 31u : (uint32_t)k), s16, k < 0 ? (half_t)0.0f : T.xc[e]);
+            if (8u * grp + e < 16u) put_row(W, 96u + 8u * grp + e, s16, T.do3[e]);
         }
-        wave_lds_sync();
-        copy_half(W, stage_tile, 0u, lane);
-        wave_lds_sync();
-        put16(W, kRowH2 - kHalfRows, T.h2, s16, grp);
-        put16(W, kRowDhd - kHalfRows, T.dhd, s16, grp);
-        put16(W, kRowHd - kHalfRows, T.hd, s16, grp);
+        put16(W, 112u, T.h2, s16, grp);
+        __syncthreads();
 #pragma unroll
-        for (uint32_t e = 0; e < 8u; ++e) put_row(W, kRowX - kHalfRows + 8u * grp + e, s16, T.x[e]);
+        for (uint32_t ks = 0; ks < 2u; ++ks) {
+            const half8_t a = op_frag(ops, 16u * wave, ks, lane);
 #pragma unroll
-        for (uint32_t e = 0; e < 4u; ++e) put_row(W, kRowDout - kHalfRows + 4u * grp + e, s16, T.dout[e]);
-        wave_lds_sync();
-        copy_half(W, stage_tile, 1u, lane);
+            for (uint32_t ib = 0; ib < 2u; ++ib) acc_ci[ib] = mfma16x16x32(a, op_frag(ops, 64u + 16u * ib, ks, lane), acc_ci[ib]);
+            acc_co = mfma16x16x32(op_frag(ops, 96u, ks, lane), op_frag(ops, 112u + 16u * wave, ks, lane), acc_co);
+        }
+        __syncthreads();
+        // Phase 3: density input and output layers.
+        put16(W, 0u, T.dhd, s16, grp);
+#pragma unroll
+        for (uint32_t e = 0; e < 8u; ++e) put_row(W, 64u + 8u * grp + e, s16, T.x[e]);
+#pragma unroll
+        for (uint32_t e = 0; e < 4u; ++e) put_row(W, 96u + 4u * grp + e, s16, T.dout[e]);
+        put16(W, 112u, T.hd, s16, grp);
+        __syncthreads();
+#pragma unroll
+        for (uint32_t ks = 0; ks < 2u; ++ks) {
+            const half8_t a = op_frag(ops, 16u * wave, ks, lane);
+#pragma unroll
+            for (uint32_t ib = 0; ib < 2u; ++ib) acc_di[ib] = mfma16x16x32(a, op_frag(ops, 64u + 16u * ib, ks, lane), acc_di[ib]);
+            acc_do = mfma16x16x32(op_frag(ops, 96u, ks, lane), op_frag(ops, 112u + 16u * wave, ks, lane), acc_do);
+        }
+        __syncthreads();
         // The atomic levels are the first n_dense; lane group g holds levels
         // 2g, 2g + 1 (b = 0) and 8 + 2g, 9 + 2g (b = 1).
 #pragma unroll
@@ -678,6 +723,25 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dx(TrainParams P, GridParams g
                 scatter_level(g, table_grad, l0 + 1u, p, T.dx[b][2], T.dx[b][3], live && l0 + 1u < n_dense);
             }
         }
+    }
+    // This workgroup's partial of every weight gradient (parameter order:
+    // density 0..3071, colour 3072..10239).  Lane (g, s16) of a block holds
+    // rows 4g + e (delta neurons), column s16 (activation neurons).
+    float* out = partials + (uint64_t)blockIdx.x * kMlpParams;
+    constexpr uint32_t D = NERF_EXT_DENSITY_PARAMS;
+#pragma unroll
+    for (uint32_t e = 0; e < 4u; ++e) {
+        const uint32_t o = 16u * wave + 4u * grp + e;  // output neuron of the 64-wide layers
+#pragma unroll
+        for (uint32_t ib = 0; ib < 4u; ++ib) out[D + 2048u + o * 64u + 16u * ib + s16] = acc_h[ib][e];
+#pragma unroll
+        for (uint32_t ib = 0; ib < 2u; ++ib) {
+            out[D + o * 32u + 16u * ib + s16] = acc_ci[ib][e];
+            out[o * 32u + 16u * ib + s16]     = acc_di[ib][e];
+        }
+        const uint32_t o16 = 4u * grp + e;  // output of the 16-wide layers
+        out[D + 6144u + o16 * 64u + 16u * wave + s16] = acc_co[e];
+        out[2048u + o16 * 64u + 16u * wave + s16]     = acc_do[e];
     }
 }
 
@@ -856,98 +920,6 @@ __global__ __launch_bounds__(512) void k_bin_accumulate(const uint32_t* __restri
         for (uint32_t w = 0; w < blockDim.x / 64u; ++w) b += wsq[w];
         if (b != 0.0) atomicAdd(&S->grad_sumsq, b);
     }
-}
-
-// Weight gradients as one pass of products over samples: dW = sum_s delta_s
-// act_s^T for the five layers, on the operands k_bwd_dx staged per tile.  A
-// wave takes pairs of tiles (32 samples = the k of one 16x16x32 MFMA); lane
-// (r, g) loads row r, samples 8g..8g+7 of the pair, which is both the A
-// fragment (deltas, rows = neurons) and the B fragment (activations, rows =
-// inputs).  40 accumulator blocks: colour hidden 16, colour input 8 + output
-// 4, density input 8 + output 4.  The 4 waves of a workgroup are reduced in
-// LDS in a fixed order, one partial per workgroup.
-__device__ __forceinline__ half8_t stage_frag(const half_t* __restrict__ stage, uint32_t tiles, uint32_t pair, uint32_t row0, uint32_t lane) {
-    const uint32_t r = lane & 15u, g = lane >> 4;
-    const uint32_t tile = 2u * pair + (g >> 1);
-    if (tile >= tiles) return half8_t{};
-    return *reinterpret_cast<const half8_t*>(stage + ((uint64_t)tile * kStageRows + row0 + r) * 16u + 8u * (g & 1u));
-}
-
-__global__ __launch_bounds__(kThreads) void k_dw_gemm(TrainParams P, const TrainDevState* S, const half_t* __restrict__ stage, float* __restrict__ partials) {
-    __shared__ float red[kMlpParams];
-    const uint32_t n     = min(S->n_samples, P.sample_cap);
-    const uint32_t tiles = (n + 15u) / 16u, pairs = (tiles + 1u) / 2u;
-    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u, grp = lane >> 4, s16 = lane & 15u;
-    floatx4 a0[16], a1[12], a2[12];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) a0[i] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int i = 0; i < 12; ++i) a1[i] = a2[i] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-    for (uint32_t pair = blockIdx.x * kWaves + wave; pair < pairs; pair += gridDim.x * kWaves) {
-        half8_t bh1[4], bh2[4], bhd[4], bxc[2], bx[2];
-#pragma unroll
-        for (uint32_t i = 0; i < 4u; ++i) {
-            bh1[i] = stage_frag(stage, tiles, pair, kRowH1 + 16u * i, lane);
-            bh2[i] = stage_frag(stage, tiles, pair, kRowH2 + 16u * i, lane);
-            bhd[i] = stage_frag(stage, tiles, pair, kRowHd + 16u * i, lane);
-        }
-#pragma unroll
-        for (uint32_t i = 0; i < 2u; ++i) {
-            bxc[i] = stage_frag(stage, tiles, pair, kRowXc + 16u * i, lane);
-            bx[i]  = stage_frag(stage, tiles, pair, kRowX + 16u * i, lane);
-        }
-#pragma unroll
-        for (uint32_t ob = 0; ob < 4u; ++ob) {
-            const half8_t dh2 = stage_frag(stage, tiles, pair, kRowDh2 + 16u * ob, lane);
-            const half8_t dh1 = stage_frag(stage, tiles, pair, kRowDh1 + 16u * ob, lane);
-            const half8_t dhd = stage_frag(stage, tiles, pair, kRowDhd + 16u * ob, lane);
-#pragma unroll
-            for (uint32_t ib = 0; ib < 4u; ++ib) a0[4u * ob + ib] = mfma16x16x32(dh2, bh1[ib], a0[4u * ob + ib]);
-#pragma unroll
-            for (uint32_t ib = 0; ib < 2u; ++ib) {
-                a1[2u * ob + ib] = mfma16x16x32(dh1, bxc[ib], a1[2u * ob + ib]);
-                a2[2u * ob + ib] = mfma16x16x32(dhd, bx[ib], a2[2u * ob + ib]);
-            }
-        }
-        const half8_t do3  = stage_frag(stage, tiles, pair, kRowDo3, lane);
-        const half8_t dout = stage_frag(stage, tiles, pair, kRowDout, lane);
-#pragma unroll
-        for (uint32_t ib = 0; ib < 4u; ++ib) {
-            a1[8u + ib] = mfma16x16x32(do3, bh2[ib], a1[8u + ib]);
-            a2[8u + ib] = mfma16x16x32(dout, bhd[ib], a2[8u + ib]);
-        }
-    }
-    // Fixed-order reduction of the 4 waves, in parameter order (density
-    // 0..3071, colour 3072..10239).
-    for (uint32_t i = threadIdx.x; i < kMlpParams; i += blockDim.x) red[i] = 0.0f;
-    __syncthreads();
-    for (uint32_t w = 0; w < kWaves; ++w) {
-        if (wave == w) {
-#pragma unroll
-            for (uint32_t e = 0; e < 4u; ++e) {
-#pragma unroll
-                for (uint32_t ob = 0; ob < 4u; ++ob) {
-                    const uint32_t o = 16u * ob + 4u * grp + e;
-#pragma unroll
-                    for (uint32_t ib = 0; ib < 4u; ++ib) red[NERF_EXT_DENSITY_PARAMS + 2048u + o * 64u + 16u * ib + s16] += a0[4u * ob + ib][e];
-#pragma unroll
-                    for (uint32_t ib = 0; ib < 2u; ++ib) {
-                        red[NERF_EXT_DENSITY_PARAMS + o * 32u + 16u * ib + s16] += a1[2u * ob + ib][e];
-                        red[o * 32u + 16u * ib + s16] += a2[2u * ob + ib][e];
-                    }
-                }
-                const uint32_t o = 4u * grp + e;
-#pragma unroll
-                for (uint32_t ib = 0; ib < 4u; ++ib) {
-                    red[NERF_EXT_DENSITY_PARAMS + 6144u + o * 64u + 16u * ib + s16] += a1[8u + ib][e];
-                    red[2048u + o * 64u + 16u * ib + s16] += a2[8u + ib][e];
-                }
-            }
-        }
-        __syncthreads();
-    }
-    float* out = partials + (uint64_t)blockIdx.x * kMlpParams;
-    for (uint32_t i = threadIdx.x; i < kMlpParams; i += blockDim.x) out[i] = red[i];
 }
 
 // Start of the backward stage: clears the dense-level gradient slab (its
@@ -1153,7 +1125,8 @@ hipError_t launch_mlp_backward(const TrainParams& P, const TrainBuffers& B, hipS
         if (e != hipSuccess) return e;
         lds_set = true;
     }
-    k_bwd_dx<<<cus * 2u, kThreads, kDxLds, st>>>(P, B.grid, B.state, B.dparams, B.cparams, B.features, B.draw, B.samples, B.sample_ray, B.rays, B.dfeat, B.n_dense, B.table_grad, B.dw_stage);
+    const uint32_t dx_blocks = min(cus * 2u, kDxMaxBlocks);  // two per CU (LDS)
+    k_bwd_dx<<<dx_blocks, kThreads, kDxLds, st>>>(P, B.grid, B.state, B.dparams, B.cparams, B.features, B.draw, B.samples, B.sample_ray, B.rays, B.dfeat, B.n_dense, B.table_grad, B.dw_partials);
     // Hashed levels: binned.
     if (B.n_bins) {
         k_bin_pass<false><<<kBinBlocks, kBinThreads, 0, st>>>(P, B.grid, B.state, B.samples, B.sample_ray, B.rays, B.dfeat, B.n_dense, B.n_bins, B.bin_hist, nullptr, nullptr);
@@ -1163,8 +1136,7 @@ hipError_t launch_mlp_backward(const TrainParams& P, const TrainBuffers& B, hipS
         k_bin_accumulate<<<B.n_bins, 512, 0, st>>>(B.bin_off, kBinBlocks, B.n_bins, B.bin_total, B.rec, B.bin_max, (uint64_t)(B.grid.n_levels - B.n_dense) * B.grid.table_size,
                                                    reinterpret_cast<float2*>(B.table_grad) + (uint64_t)B.n_dense * B.grid.table_size, B.state);
     }
-    k_dw_gemm<<<kDwBlocks, kThreads, 0, st>>>(P, B.state, B.dw_stage, B.dw_partials);
-    k_dw_reduce<<<kMlpParams / 64u, 256, 0, st>>>(B.dw_partials, kDwBlocks, B.mlp_grad, B.state);
+    k_dw_reduce<<<kMlpParams / 64u, 256, 0, st>>>(B.dw_partials, dx_blocks, B.mlp_grad, B.state);
     return hipGetLastError();
 }
 

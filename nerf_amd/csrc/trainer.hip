@@ -121,7 +121,6 @@ NerfStatus trainer_create(const NerfExtTrainDesc* d, const BorrowedModel* borrow
     NERF_HIP_TRY(alloc(T, B.features, 32ull * P.sample_cap));
     NERF_HIP_TRY(alloc(T, B.draw, P.sample_cap));
     NERF_HIP_TRY(alloc(T, B.dfeat, 32ull * P.sample_cap));
-    NERF_HIP_TRY(alloc(T, B.dw_stage, (uint64_t)(P.sample_cap + 15u) / 16u * kStageRows * 16u));
     // Leading dense levels of at most kAtomicMaxEntries entries take row-
     // combined atomics; binned, the records of every sample would crowd into
     // their few bins.  Every other level is binned.
@@ -145,7 +144,7 @@ NerfStatus trainer_create(const NerfExtTrainDesc* d, const BorrowedModel* borrow
     NERF_HIP_TRY(alloc(T, B.mlp_grad, kMlpParams));
     NERF_HIP_TRY(alloc(T, B.mlp_m, kMlpParams));
     NERF_HIP_TRY(alloc(T, B.mlp_v, kMlpParams));
-    NERF_HIP_TRY(alloc(T, B.dw_partials, (uint64_t)kDwBlocks * kMlpParams));
+    NERF_HIP_TRY(alloc(T, B.dw_partials, (uint64_t)kDxMaxBlocks * kMlpParams));
     if (borrowed) {
         B.table     = borrowed->table;
         B.table_f32 = borrowed->table_f32;
