@@ -177,7 +177,9 @@ __global__ __launch_bounds__(kBlockThreads) void k_field_forward(GridParams g, c
 }
 
 // MLP pass on given encodings: lane (g, s) loads features 8g..8g+7 of
-// sample s (one 16-byte load), the B operand of the density MLP.
+// sample s (one 16-byte load), the B operand of the density MLP.  The next
+// tile's features and directions are loaded before the current tile is
+// computed, so their latency overlaps the products.
 __global__ __launch_bounds__(kBlockThreads) void k_field_mlp(const half_t* __restrict__ dparams, const half_t* __restrict__ cparams, const half_t* __restrict__ features, const float* __restrict__ dirs, uint32_t n,
                                                             float4* __restrict__ out) {
     __shared__ half_t sp[NERF_EXT_DENSITY_PARAMS + NERF_EXT_COLOR_PARAMS];
@@ -191,11 +193,23 @@ __global__ __launch_bounds__(kBlockThreads) void k_field_mlp(const half_t* __res
     load_color(sp + NERF_EXT_DENSITY_PARAMS, fc, lane);
     const uint32_t tiles  = (n + 15u) / 16u;
     const uint32_t nwaves = gridDim.x * kBlockWaves;
-    for (uint32_t tile = blockIdx.x * kBlockWaves + (threadIdx.x >> 6); tile < tiles; tile += nwaves) {
-        const uint32_t s = tile * 16u + s16;
+    half8_t xn{};
+    float dn[3] = {0.0f, 0.0f, 0.0f};
+    auto fetch = [&](uint32_t t) {
+        const uint32_t s = t * 16u + s16;
         const uint32_t q = s < n ? s : n - 1u;
-        const half8_t x  = *reinterpret_cast<const half8_t*>(features + (uint64_t)q * 32u + 8u * grp);
-        const float d[3] = {dirs[3ull * q], dirs[3ull * q + 1u], dirs[3ull * q + 2u]};
+        xn               = *reinterpret_cast<const half8_t*>(features + (uint64_t)q * 32u + 8u * grp);
+        dn[0]            = dirs[3ull * q];
+        dn[1]            = dirs[3ull * q + 1u];
+        dn[2]            = dirs[3ull * q + 2u];
+    };
+    uint32_t tile = blockIdx.x * kBlockWaves + (threadIdx.x >> 6);
+    if (tile < tiles) fetch(tile);
+    for (; tile < tiles; tile += nwaves) {
+        const uint32_t s = tile * 16u + s16;
+        const half8_t x  = xn;
+        const float d[3] = {dn[0], dn[1], dn[2]};
+        if (tile + nwaves < tiles) fetch(tile + nwaves);
         const floatx4 o  = density_mlp(fd, x);
         const floatx4 c  = color_mlp(fc, color_input(o, d, grp));
         const float v = field_channel(o, c, grp, s16);

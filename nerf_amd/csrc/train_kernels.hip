@@ -947,12 +947,21 @@ __global__ __launch_bounds__(256) void k_dw_reduce(const float* __restrict__ par
     const uint32_t c   = blockIdx.x * 16u + col;  // float4 column
     const float4* p4   = reinterpret_cast<const float4*>(partials);
     float4 s           = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    for (uint32_t b = slice; b < blocks; b += kReduceSlices) {
-        const float4 v = p4[(uint64_t)b * (kMlpParams / 4u) + c];
-        s.x += v.x;
-        s.y += v.y;
-        s.z += v.z;
-        s.w += v.w;
+    // Batches of 8 loads in flight, added in partial order.
+    for (uint32_t b0 = slice; b0 < blocks; b0 += 8u * kReduceSlices) {
+        float4 v[8];
+#pragma unroll
+        for (uint32_t k = 0; k < 8u; ++k) {
+            const uint32_t b = b0 + k * kReduceSlices;
+            v[k]             = b < blocks ? p4[(uint64_t)b * (kMlpParams / 4u) + c] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < 8u; ++k) {
+            s.x += v[k].x;
+            s.y += v[k].y;
+            s.z += v[k].z;
+            s.w += v[k].w;
+        }
     }
     part[slice][col] = s;
     __syncthreads();
