@@ -67,18 +67,14 @@ __device__ __forceinline__ half8_t color_input(const floatx4 o, const float d[3]
     return xc;
 }
 
-// Output activation spread over the wave: the raw outputs of sample s sit in
-// lane (0, s) (density output 0, colour outputs 0..2); lane (g, s) takes
-// channel g (g = 0: sigma = exp, g = 1..3: sigmoid of colour g - 1), so each
-// lane evaluates one transcendental and the 16 samples leave in one 256-byte
-// store.
+// Output activation spread over the wave: lane (g, s) holds channel g of
+// sample s in element 0 (sigma from the density output, colour g - 1 from the
+// row-permuted colour output) and applies its activation (g = 0: exp, else
+// sigmoid), so each lane evaluates one transcendental and the 16 samples
+// leave in one 256-byte store.
 __device__ __forceinline__ float field_channel(const floatx4 o, const floatx4 c, uint32_t grp, uint32_t s16) {
-    const float v0 = __shfl(o[0], (int)s16, 64);
-    const float v1 = __shfl(c[0], (int)s16, 64);
-    const float v2 = __shfl(c[1], (int)s16, 64);
-    const float v3 = __shfl(c[2], (int)s16, 64);
-    const float x  = grp == 0u ? v0 : grp == 1u ? v1 : grp == 2u ? v2 : v3;
-    return grp == 0u ? __expf(x) : __frcp_rn(1.0f + __expf(-x));
+    (void)s16;
+    return grp == 0u ? __expf(o[0]) : __frcp_rn(1.0f + __expf(-c[0]));
 }
 
 // ---------------------------------------------------------------- kernels

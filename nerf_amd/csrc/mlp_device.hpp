@@ -71,8 +71,16 @@ __device__ __forceinline__ void load_color(const half_t* P, ColorFrags& f, uint3
     for (uint32_t b = 0; b < 4u; ++b)
 #pragma unroll
         for (uint32_t t = 0; t < 2u; ++t) f.w2[2u * b + t] = load_a(P + 2048, 64u, b, t, KMap::Hidden, lane);
+    // Colour output: MFMA row 4c (c = 1..3) computes output c - 1 and every
+    // other row is zero, so lane group c holds colour c - 1 in element 0 (and
+    // lane group 0 takes sigma from the density output, row 0).
+    const uint32_t i = lane & 15u, g = lane >> 4;
+    const bool used  = (i & 3u) == 0u && i != 0u;
+    const half_t* row = P + 2048 + 4096 + (used ? (i / 4u - 1u) : 0u) * 64u;
 #pragma unroll
-    for (uint32_t t = 0; t < 2u; ++t) f.w3[t] = load_a(P + 2048 + 4096, 64u, 0u, t, KMap::Hidden, lane);
+    for (uint32_t t = 0; t < 2u; ++t)
+#pragma unroll
+        for (uint32_t e = 0; e < 8u; ++e) f.w3[t][e] = used ? row[logical_k(KMap::Hidden, t, g, e)] : (half_t)0.0f;
 }
 
 // ReLU in fp16 after the conversion (packed convert, packed max): the same
