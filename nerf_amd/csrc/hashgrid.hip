@@ -86,6 +86,52 @@ __global__ __launch_bounds__(256) void k_encode_tile(GridParams g, const TableT*
     for (uint32_t i = threadIdx.x; i < count * width; i += blockDim.x) o[i] = tile[i];
 }
 
+// One level with the x-neighbour corners of each (y, z) edge fetched as one
+// 16-byte load when they are the two entries of an aligned pair (index i and
+// i ^ 1: always for an even x on a hashed level, x's prime being 1), else as
+// two 8-byte loads.  Same entries, same weights, same summation order as
+// encode_level.
+template <typename TableT>
+__device__ __forceinline__ void encode_level_xpair(const GridParams& g, const TableT* __restrict__ table, const float p[3], uint32_t level, uint32_t N, bool dense, float& a0, float& a1) {
+    const LevelCell c  = level_cell(p, N);
+    const TableT* base = table + (uint64_t)level * g.table_size * 2u;
+    float v0[8], v1[8];
+#pragma unroll
+    for (uint32_t e = 0; e < 4u; ++e) {  // (y, z) edge e: corners 2e (x) and 2e + 1 (x + 1)
+        const uint32_t i0 = corner_index(c, 2u * e, N, dense, g.table_size - 1u);
+        const uint32_t i1 = corner_index(c, 2u * e + 1u, N, dense, g.table_size - 1u);
+        if (i1 == (i0 ^ 1u)) {
+            const uint32_t lo = i0 & ~1u;
+            float q[4];
+            if constexpr (sizeof(TableT) == 4) {
+                const float4 w = *reinterpret_cast<const float4*>(base + 2u * lo);
+                q[0] = w.x; q[1] = w.y; q[2] = w.z; q[3] = w.w;
+            } else {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) q[k] = (float)base[2u * lo + k];
+            }
+            const bool odd = (i0 & 1u) != 0u;
+            v0[2u * e]      = odd ? q[2] : q[0];
+            v1[2u * e]      = odd ? q[3] : q[1];
+            v0[2u * e + 1u] = odd ? q[0] : q[2];
+            v1[2u * e + 1u] = odd ? q[1] : q[3];
+        } else {
+            v0[2u * e]      = (float)base[2u * i0];
+            v1[2u * e]      = (float)base[2u * i0 + 1u];
+            v0[2u * e + 1u] = (float)base[2u * i1];
+            v1[2u * e + 1u] = (float)base[2u * i1 + 1u];
+        }
+    }
+    a0 = 0.0f;
+    a1 = 0.0f;
+#pragma unroll
+    for (uint32_t k = 0; k < 8u; ++k) {
+        const float w = corner_weight(c, k);
+        a0            = a0 + w * v0[k];
+        a1            = a1 + w * v1[k];
+    }
+}
+
 // XCD-aware encode.  Workgroup b runs on XCD b % 8 (the dispatcher's round
 // robin) and gathers only the levels of pair b % 8 (levels 2x, 2x + 1), so
 // each XCD's L2 holds two levels of the table rather than all of them; the
@@ -105,8 +151,8 @@ __global__ __launch_bounds__(256) void k_encode_split(GridParams g, const TableT
     for (uint32_t i = slot * blockDim.x + threadIdx.x; i < n; i += slots * blockDim.x) {
         const float x[3] = {pos[3ull * i], pos[3ull * i + 1], pos[3ull * i + 2]};
         float a0, a1, b0 = 0.0f, b1 = 0.0f;
-        encode_level(g, table, x, l0, N0, d0, a0, a1);
-        if (has1) encode_level(g, table, x, l1, N1, d1, b0, b1);
+        encode_level_xpair(g, table, x, l0, N0, d0, a0, a1);
+        if (has1) encode_level_xpair(g, table, x, l1, N1, d1, b0, b1);
         OutT* o = out + (uint64_t)i * width + 2u * l0;
         if (has1) {
             store_value(o, a0);
