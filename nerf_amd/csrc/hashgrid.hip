@@ -107,8 +107,9 @@ __device__ __forceinline__ void encode_level_xpair(const GridParams& g, const Ta
                 const float4 w = *reinterpret_cast<const float4*>(base + 2u * lo);
                 q[0] = w.x; q[1] = w.y; q[2] = w.z; q[3] = w.w;
             } else {
+                const half4_t w = *reinterpret_cast<const half4_t*>(base + 2u * lo);
 #pragma unroll
-                for (int k = 0; k < 4; ++k) q[k] = (float)base[2u * lo + k];
+                for (int k = 0; k < 4; ++k) q[k] = (float)w[k];
             }
             const bool odd = (i0 & 1u) != 0u;
             v0[2u * e]      = odd ? q[2] : q[0];
@@ -138,8 +139,11 @@ __device__ __forceinline__ void encode_level_xpair(const GridParams& g, const Ta
 // workgroups of one XCD stride over the points, one point per thread, and
 // each thread writes its 4 features as one vector store.  The placement is
 // a locality choice only: any workgroup-to-XCD mapping gives the same
-// result.
-template <typename TableT, typename OutT>
+// result.  Positions arrive as one 12-byte load; the features leave as
+// scalar stores (measured faster than one 16-byte store per thread here).
+// With kPair (the table aligned to an entry pair) x-neighbour corners are
+// fetched in pairs.
+template <typename TableT, typename OutT, bool kPair>
 __global__ __launch_bounds__(256) void k_encode_split(GridParams g, const TableT* __restrict__ table, const float* __restrict__ pos, uint32_t n, OutT* __restrict__ out) {
     const uint32_t pair = blockIdx.x & 7u, slot = blockIdx.x >> 3, slots = gridDim.x >> 3;
     const uint32_t l0 = 2u * pair, l1 = l0 + 1u;
@@ -149,10 +153,16 @@ __global__ __launch_bounds__(256) void k_encode_split(GridParams g, const TableT
     const bool d0 = g.dense[l0] != 0u, d1 = has1 && g.dense[l1] != 0u;
     const uint32_t width = 2u * g.n_levels;
     for (uint32_t i = slot * blockDim.x + threadIdx.x; i < n; i += slots * blockDim.x) {
-        const float x[3] = {pos[3ull * i], pos[3ull * i + 1], pos[3ull * i + 2]};
+        const float3 xp  = *reinterpret_cast<const float3*>(pos + 3ull * i);
+        const float x[3] = {xp.x, xp.y, xp.z};
         float a0, a1, b0 = 0.0f, b1 = 0.0f;
-        encode_level_xpair(g, table, x, l0, N0, d0, a0, a1);
-        if (has1) encode_level_xpair(g, table, x, l1, N1, d1, b0, b1);
+        if constexpr (kPair) {
+            encode_level_xpair(g, table, x, l0, N0, d0, a0, a1);
+            if (has1) encode_level_xpair(g, table, x, l1, N1, d1, b0, b1);
+        } else {
+            encode_level(g, table, x, l0, N0, d0, a0, a1);
+            if (has1) encode_level(g, table, x, l1, N1, d1, b0, b1);
+        }
         OutT* o = out + (uint64_t)i * width + 2u * l0;
         if (has1) {
             store_value(o, a0);
@@ -232,10 +242,15 @@ NERF_API NerfStatus nerf_ext_encode_forward(const NerfExtGridDesc* grid, const v
     const uint32_t per_xcd    = (n + 255u) / 256u;
     const uint32_t cap        = device_cu_count() / 8u * 8u;  // 8 workgroups per CU of one XCD
     const dim3 grid_dim = split ? dim3(8u * (per_xcd < cap ? per_xcd : (cap > 0u ? cap : 1u))) : dim3((n + kEncPoints - 1u) / kEncPoints);
+    // Pair loads need the table aligned to an entry pair: 16 bytes for fp32,
+    // 8 for fp16 (device allocations are).
+    const bool pair = ((uintptr_t)table & (g.table_dtype == NERF_EXT_F32 ? 15u : 7u)) == 0u;
 #define NERF_ENC(TT, OT)                                                                                                   \
     do {                                                                                                                   \
-        if (split)                                                                                                         \
-            k_encode_split<TT, OT><<<grid_dim, 256, 0, st>>>(g, (const TT*)table, positions, n, (OT*)features);            \
+        if (split && pair)                                                                                                 \
+            k_encode_split<TT, OT, true><<<grid_dim, 256, 0, st>>>(g, (const TT*)table, positions, n, (OT*)features);      \
+        else if (split)                                                                                                    \
+            k_encode_split<TT, OT, false><<<grid_dim, 256, 0, st>>>(g, (const TT*)table, positions, n, (OT*)features);     \
         else                                                                                                               \
             k_encode_tile<TT, OT><<<grid_dim, 256, 0, st>>>(g, (const TT*)table, positions, n, (OT*)features);             \
     } while (0)
