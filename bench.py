@@ -178,9 +178,92 @@ def train_bench(steps: int, warmup: int, views: int = 100):
            "loss_last": round(float(s1.last.loss), 6), "nonfinite": int(s1.last.has_nonfinite), "batch_target": batch, "views": views,
            "workload": f"{views} 800x800 views, 32-Gaussian scene, hash grid T=2^19 fp16, 128^3 occupancy, 2^18-sample batches, <=1024 steps/ray"}
     out["loss_first_timed"] = round(float(s0.last.loss), 6)
+    out["stages"] = train_stages(tr, _On, reps=20)
     out["render_trained"] = render_trained(tr)
     tr.close()
     return out
+
+
+# Algorithmic work per training stage (per sample unless noted): the march
+# writes a 16-byte sample and reads a 32-byte ray; the field forward gathers a
+# 588-byte f16 encoding and runs 18,688 MLP flops; compositing reads and writes
+# 44 bytes; the backward scatters the encoding gradient (2,124 bytes counting
+# read-modify-write) and runs 37,376 MLP flops; Adam moves 30 bytes per
+# parameter.
+TRAIN_MARCH_B_SAMPLE, TRAIN_MARCH_B_RAY = 16, 32
+TRAIN_ENCODE_B = 12 + 16 * 8 * 2 * 2 + 32 * 2
+TRAIN_COMPOSITE_B = 44
+TRAIN_ENC_BWD_B = 12 + 64 + 2 * (16 * 8 * 2 * 4)
+TRAIN_BWD_FLOPS = 2 * FIELD_FLOPS_PER_SAMPLE
+ADAM_B_PARAM = 30
+
+
+def train_stages(tr, on, reps: int):
+    """Per-stage times of `reps` further steps, each stage bracketed by HIP
+    events on the trainer's stream, with each stage's roofline fraction."""
+    from nerf_amd import _lib as L
+    from nerf_amd.device import Event
+
+    groups = [("sample", L.NERF_EXT_STAGE_BEGIN, L.NERF_EXT_STAGE_SAMPLE), ("forward", L.NERF_EXT_STAGE_FORWARD, L.NERF_EXT_STAGE_FORWARD),
+              ("composite", L.NERF_EXT_STAGE_COMPOSITE, L.NERF_EXT_STAGE_COMPOSITE), ("backward", L.NERF_EXT_STAGE_BACKWARD, L.NERF_EXT_STAGE_BACKWARD),
+              ("adam", L.NERF_EXT_STAGE_ADAM, L.NERF_EXT_STAGE_END)]
+    evs = [[Event() for _ in range(len(groups) + 1)] for _ in range(reps)]
+    s0 = tr.stats()
+    for r in range(reps):
+        evs[r][0].record(on)
+        for k, (_, a, b) in enumerate(groups):
+            tr.run_stages(a, b)
+            evs[r][k + 1].record(on)
+    s1 = tr.stats()
+    ms = {name: sum(evs[r][k].elapsed_ms(evs[r][k + 1]) for r in range(reps)) / reps for k, (name, _, _) in enumerate(groups)}
+    n = (s1.samples_total - s0.samples_total) / reps
+    rays = s1.rays
+    params = 16 * (1 << 19) * 2 + 10240
+
+    def hbm(b, t):
+        return {"achieved": round(b / (t / 1e3) / 1e9, 1), "unit": "GB/s", "frac": round(b / (t / 1e3) / 1e9 / HBM_PEAK_GBS, 4), "bound": "hbm"}
+
+    def mfma(f, t):
+        return {"achieved": round(f / (t / 1e3) / 1e12, 1), "unit": "TFLOP/s", "frac": round(f / (t / 1e3) / 1e12 / MFMA_FP16_PEAK_TFS, 4), "bound": "mfma"}
+
+    out = {"reps": reps, "samples_per_step": round(n, 1), "rays_last_step": rays,
+           "sample": {"ms": round(ms["sample"], 4), **hbm(n * TRAIN_MARCH_B_SAMPLE + rays * TRAIN_MARCH_B_RAY, ms["sample"]), "work": "16 B/sample + 32 B/ray (march, scan, compaction; occupancy refresh every 16 steps)"},
+           "forward": {"ms": round(ms["forward"], 4), **mfma(n * FIELD_FLOPS_PER_SAMPLE, ms["forward"]), "hbm": hbm(n * TRAIN_ENCODE_B, ms["forward"]), "work": "18,688 flop + 588 B/sample"},
+           "composite": {"ms": round(ms["composite"], 4), **hbm(n * TRAIN_COMPOSITE_B, ms["composite"]), "work": "44 B/sample"},
+           "backward": {"ms": round(ms["backward"], 4), **hbm(n * TRAIN_ENC_BWD_B, ms["backward"]), "mfma": mfma(n * TRAIN_BWD_FLOPS, ms["backward"]), "work": "2,124 B + 37,376 flop/sample"},
+           "adam": {"ms": round(ms["adam"], 4), **hbm(params * ADAM_B_PARAM, ms["adam"]), "work": "30 B/parameter, 16.8 M parameters"}}
+    return out
+
+
+def abi_render(model_seed: int = 0, reps: int = 5):
+    """The 800x800 render through the reference ABI's nerf_inference, timed by
+    wall clock around the call (RGBA8 returned in host memory).  The context
+    holds a random-init model and, before training is configured, no
+    occupancy grid: every cell of the unit box counts as occupied, so this is
+    a heavier workload than the headline render's 128^3 scene occupancy."""
+    from nerf_amd import _lib as L, ext
+
+    cam = ext.camera_orbit(0, 0, RADIUS, CENTRE, W, H, FOCAL)
+    img = np.zeros((1, H, W), np.uint32)
+    mat = np.zeros((1, 4, 4), np.float32)
+    mat[0, :3, :] = np.array(cam.c2w[:], np.float32).reshape(3, 4)
+    mat[0, 3, 3] = 1.0
+    d = L.NerfCreateDesc(128, 1 << 20, 4096, 256, img.ctypes.data, img.nbytes, mat.ctypes.data, mat.nbytes, 1, W, H, cam.fx, cam.fy, cam.cx, cam.cy)
+    h = C.c_void_p()
+    L.call("nerf_create_context", C.byref(d), C.byref(h))
+    try:
+        out = np.zeros((H, W), np.uint32)
+        req = L.NerfInferenceRequest(0, MAX_STEPS, L.NERF_MEMORY_HOST, out.ctypes.data, out.nbytes)
+        info = L.NerfInferenceInfo()
+        L.call("nerf_inference", h, C.byref(req), C.byref(info))
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            L.call("nerf_inference", h, C.byref(req), C.byref(info))
+        wall = (time.perf_counter() - t0) / reps
+    finally:
+        L.call("nerf_destroy_context", h)
+    return {"value": round(W * H / wall / 1e6, 3), "unit": "Mrays/s", "ms_per_render": round(wall * 1e3, 3), "reps": reps,
+            "workload": f"{W}x{H} through nerf_inference (wall clock, RGBA8 to host): random-init model, every cell of the unit box occupied, <={MAX_STEPS} steps/ray"}
 
 
 def render_trained(tr, reps: int = 5):
@@ -346,6 +429,7 @@ def main() -> int:
     }
     if not args.no_stage_rooflines:
         line["stage_rooflines"] = kernel_rooflines()
+        line["abi_render"] = abi_render()
     if args.train_steps > 0:
         line["train"] = train_bench(args.train_steps, args.train_warmup)
     if not args.no_cpu_baseline:
