@@ -72,21 +72,20 @@ __device__ __forceinline__ uint32_t march(float4 ro, float4 rd, float cone, uint
     // The G steps run unconditionally, branch-free: once t reaches tf the
     // step is clamped to zero, so t stays put and every later step of the run
     // is marked dead, which leaves t and dt of the live steps bit-identical
-    // to the conditional loop.
+    // to the conditional loop.  Each lane keeps only the t at which its own
+    // step starts (one select per step) and recomputes that step's dt, mid
+    // point and liveness from it afterwards with the same operations.
+    auto step_dt = [&](float tt) { return fminf(fmaxf(dt_min, tt * cone), fmaxf(tf - tt, 0.0f)); };
     auto run = [&](float& tm_out, float& dt_out, bool& has_out, uint32_t& idx_out, uint32_t& word_out) {
-        float my_tm = 0.0f, my_dt = 0.0f;
-        bool live = false;
+        float t_own = tf;
 #pragma unroll
         for (uint32_t j = 0; j < G; ++j) {
-            const float dt = fminf(fmaxf(dt_min, t * cone), fmaxf(tf - t, 0.0f));
-            if (j_own == j) {
-                my_tm = t + 0.5f * dt;
-                my_dt = dt;
-                live  = t < tf;
-            }
-            t += dt;
+            if (j_own == j) t_own = t;
+            t += step_dt(t);
         }
-        const bool has      = live && i + j_own < max_steps;
+        const float my_dt   = step_dt(t_own);
+        const float my_tm   = t_own + 0.5f * my_dt;
+        const bool has      = t_own < tf && i + j_own < max_steps;
         i += G;
         const float p[3]    = {ro.x + my_tm * rd.x, ro.y + my_tm * rd.y, ro.z + my_tm * rd.z};
         const uint32_t idx  = has ? cell(p) : kOutside;
