@@ -59,6 +59,9 @@ struct TrainBuffers {
     uint32_t* counts;            // [max_rays] occupied samples
     uint32_t* kept;              // [max_rays] samples kept (0 if cut)
     uint32_t* offsets;           // [max_rays]
+    float* seg_t;                // [max_rays][segs] t at the start of each kSegSteps-step segment of the march
+    uint32_t* seg_seen;          // [max_rays][segs] occupied steps before the segment (count past the end)
+    uint32_t segs;               // ceil(max_steps / kSegSteps)
     uint32_t* scan_tmp;
     float2* samples;             // [sample_cap] (t_mid, dt)
     uint32_t* sample_ray;        // [sample_cap]
@@ -97,6 +100,7 @@ struct TrainBuffers {
 constexpr uint32_t kDxMaxBlocks = 1024;  // workgroups of the input-gradient pass (two per CU)
 constexpr uint32_t kBinEntries = 4096;  // table entries per scatter bin (64 KiB of int64 pairs in LDS)
 constexpr uint32_t kBinBlocks  = 256;   // workgroups of the bin count / fill passes
+constexpr uint32_t kSegSteps = 64;  // march steps per resumable segment of the training sampler
 constexpr uint32_t kAtomicMaxEntries = 1u << 15;  // largest level scattered with atomics
 constexpr uint32_t kMaxBins    = 16384; // bins; the fill pass keeps a cursor and a maximum per bin in LDS (128 KiB)
 constexpr uint32_t kMlpParams  = NERF_EXT_DENSITY_PARAMS + NERF_EXT_COLOR_PARAMS;

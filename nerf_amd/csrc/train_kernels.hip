@@ -186,14 +186,14 @@ __device__ __forceinline__ float cone_of(const NerfExtCamera& c) {  // :333-337
 constexpr uint32_t kTrainGroup = 16u;  // lanes per ray in the training march (4 rays per wave)
 
 __global__ __launch_bounds__(256) void k_train_rays(TrainParams P, const TrainDevState* S, const NerfExtCamera* __restrict__ cams, const uint8_t* __restrict__ images, const uint32_t* __restrict__ bits, float4* __restrict__ rays, float4* __restrict__ gt,
-                                                     uint32_t* __restrict__ counts) {
+                                                     uint32_t* __restrict__ counts, float* __restrict__ seg_t, uint32_t* __restrict__ seg_seen, uint32_t segs) {
     constexpr uint32_t kPer = 64u / kTrainGroup;  // rays per wave
     const uint32_t lane = threadIdx.x & 63u, stride = gridDim.x * kWaves * kPer;
     const uint32_t n_rays = S->n_rays, cam_idx = S->camera, frame = S->frame;
     const NerfExtCamera cam = cams[cam_idx];
     const float cone        = cone_of(cam);
     for (uint32_t r = (blockIdx.x * kWaves + (threadIdx.x >> 6)) * kPer + lane / kTrainGroup; r < P.max_rays; r += stride) {
-        uint32_t count = 0u;
+        uint32_t count = 0u, reached = 0u;
         float4 ro = make_float4(0.0f, 0.0f, 0.0f, 0.0f), rd = make_float4(0.0f, 0.0f, 0.0f, 0.0f), g4 = make_float4(1.0f, 1.0f, 1.0f, 0.0f);
         if (r < n_rays) {
             const uint32_t seed = frame * 1315423911u ^ r * 9781u;
@@ -204,7 +204,18 @@ __global__ __launch_bounds__(256) void k_train_rays(TrainParams P, const TrainDe
             if (make_ray(cam, px, pyf, P.bmin, P.bmax, ray)) {
                 ro    = make_float4(ray.o[0], ray.o[1], ray.o[2], ray.tn);
                 rd    = make_float4(ray.d[0], ray.d[1], ray.d[2], ray.tf);
-                count = wave::march<kTrainGroup>(ro, rd, cone, P.max_steps, ~0u, bits, [&](const float p[3]) { return occ_cell_at(P, p); }, [](uint32_t, float, float) {});
+                // Checkpoints every kSegSteps steps (t and the occupied steps
+                // before), from which k_train_samples resumes each segment.
+                count = wave::march<kTrainGroup>(ro, rd, cone, P.max_steps, ~0u, bits, [&](const float p[3]) { return occ_cell_at(P, p); }, [](uint32_t, float, float) {},
+                                                 [&](uint32_t i0, float t0, uint32_t seen) {
+                                                     if (i0 % kSegSteps == 0u) {
+                                                         reached = i0 / kSegSteps + 1u;
+                                                         if (lane % kTrainGroup == 0u) {
+                                                             seg_t[(uint64_t)r * segs + i0 / kSegSteps]    = t0;
+                                                             seg_seen[(uint64_t)r * segs + i0 / kSegSteps] = seen;
+                                                         }
+                                                     }
+                                                 });
             }
             if (count > 0u) {
                 const uint8_t* img = images + (uint64_t)cam_idx * P.width * P.height * 4u;
@@ -234,6 +245,8 @@ __global__ __launch_bounds__(256) void k_train_rays(TrainParams P, const TrainDe
             rays[2ull * r + 1u] = rd;
             gt[r]               = g4;
             counts[r]           = count;
+            if (r < n_rays)
+                for (uint32_t k = reached; k < segs; ++k) seg_seen[(uint64_t)r * segs + k] = count;  // segments past the end: empty
         }
     }
 }
@@ -242,26 +255,47 @@ __global__ __launch_bounds__(256) void k_train_rays(TrainParams P, const TrainDe
 // kept[r] is its count or 0.  The kept rays form a prefix (offsets grow with
 // r), so n_samples = max(offset + count) over kept rays.  kTrainGroup lanes
 // per ray.
+// Emission pass: one unit per (ray, segment of kSegSteps steps), resumed from
+// the checkpoint k_train_rays left, so the serial step chain of a unit is
+// kSegSteps long rather than the whole ray.  A ray is kept only if all its
+// samples fit under the capacity (its offset + count); unit (r, 0) records
+// the ray's kept count and the step totals.
 __global__ __launch_bounds__(256) void k_train_samples(TrainParams P, TrainDevState* S, const NerfExtCamera* __restrict__ cams, const uint32_t* __restrict__ bits, const float4* __restrict__ rays, const uint32_t* __restrict__ counts,
-                                                        const uint32_t* __restrict__ offsets, uint32_t* __restrict__ kept, float2* __restrict__ samples, uint32_t* __restrict__ sample_ray) {
+                                                        const uint32_t* __restrict__ offsets, const float* __restrict__ seg_t, const uint32_t* __restrict__ seg_seen, uint32_t segs, uint32_t* __restrict__ kept,
+                                                        float2* __restrict__ samples, uint32_t* __restrict__ sample_ray) {
     constexpr uint32_t kPer = 64u / kTrainGroup;
     const uint32_t lane = threadIdx.x & 63u, stride = gridDim.x * kWaves * kPer;
-    const float cone    = cone_of(cams[S->camera]);
-    for (uint32_t r = (blockIdx.x * kWaves + (threadIdx.x >> 6)) * kPer + lane / kTrainGroup; r < P.max_rays; r += stride) {
+    const bool leader   = lane % kTrainGroup == 0u;
+    const uint32_t n_rays = min(S->n_rays, P.max_rays);
+    const float cone      = cone_of(cams[S->camera]);
+    for (uint32_t r = blockIdx.x * blockDim.x + threadIdx.x; r < P.max_rays; r += gridDim.x * blockDim.x)
+        if (r >= n_rays) kept[r] = 0u;
+    const uint64_t units = (uint64_t)n_rays * segs;
+    for (uint64_t u = (uint64_t)(blockIdx.x * kWaves + (threadIdx.x >> 6)) * kPer + lane / kTrainGroup; u < units; u += stride) {
+        const uint32_t r = (uint32_t)(u / segs), sg = (uint32_t)(u % segs);
         const uint32_t count = counts[r];
         const uint32_t base  = offsets[r];
         const bool fits      = count > 0u && (uint64_t)base + count <= (uint64_t)P.sample_cap;
-        const bool leader    = lane % kTrainGroup == 0u;
-        if (leader) kept[r] = fits ? count : 0u;
-        if (!fits) continue;
-        wave::march<kTrainGroup>(rays[2ull * r], rays[2ull * r + 1u], cone, P.max_steps, count, bits, [&](const float p[3]) { return occ_cell_at(P, p); }, [&](uint32_t k, float tm, float dt) {
-            samples[base + k]    = make_float2(tm, dt);
-            sample_ray[base + k] = r;
-        });
-        if (leader) {
-            atomicMax(&S->n_samples, base + count);
-            atomicAdd(&S->n_active, 1u);
+        if (sg == 0u && leader) {
+            kept[r] = fits ? count : 0u;
+            if (fits) {
+                atomicMax(&S->n_samples, base + count);
+                atomicAdd(&S->n_active, 1u);
+            }
         }
+        if (!fits) continue;
+        const uint32_t s0 = seg_seen[u], s1 = sg + 1u < segs ? seg_seen[u + 1u] : count;
+        if (s1 <= s0) continue;
+        const float4 ro = rays[2ull * r], rd = rays[2ull * r + 1u];
+        const float dt_min = (rd.w - ro.w) / (float)P.max_steps;  // as in wave::march
+        const uint32_t i0 = sg * kSegSteps, i1 = min(i0 + kSegSteps, P.max_steps);
+        const uint32_t at = base + s0;
+        wave::march_range<kTrainGroup>(ro, rd, cone, dt_min, seg_t[u], i0, i1, s1 - s0, bits, [&](const float p[3]) { return occ_cell_at(P, p); },
+                                       [&](uint32_t k, float tm, float dt) {
+                                           samples[at + k]    = make_float2(tm, dt);
+                                           sample_ray[at + k] = r;
+                                       },
+                                       [](uint32_t, float, uint32_t) {});
     }
 }
 
@@ -1174,10 +1208,11 @@ hipError_t launch_train_stage(const TrainParams& P, const TrainBuffers& B, uint3
         }
         break;
     case NERF_EXT_STAGE_SAMPLE: {
-        k_train_rays<<<ray_wave_blocks(P.max_rays), 256, 0, st>>>(P, B.state, B.cams, B.images, B.bits, B.rays, B.gt, B.counts);
+        k_train_rays<<<ray_wave_blocks(P.max_rays), 256, 0, st>>>(P, B.state, B.cams, B.images, B.bits, B.rays, B.gt, B.counts, B.seg_t, B.seg_seen, B.segs);
         const hipError_t e = exclusive_scan_u32(B.counts, B.offsets, P.max_rays, B.scan_tmp, &B.state->total, st);
         if (e != hipSuccess) return e;
-        k_train_samples<<<ray_wave_blocks(P.max_rays), 256, 0, st>>>(P, B.state, B.cams, B.bits, B.rays, B.counts, B.offsets, B.kept, B.samples, B.sample_ray);
+        k_train_samples<<<ray_wave_blocks(P.max_rays * B.segs), 256, 0, st>>>(P, B.state, B.cams, B.bits, B.rays, B.counts, B.offsets, B.seg_t, B.seg_seen, B.segs, B.kept, B.samples,
+                                                                              B.sample_ray);
         break;
     }
     case NERF_EXT_STAGE_FORWARD: {

@@ -55,19 +55,25 @@ constexpr uint32_t kOutside = 0xFFFFFFFFu;
 // kOutside, and bit (index & 31) of bits[index >> 5] marks it occupied (a
 // null bitfield marks every cell inside the box).  The loads of run k + 1 are
 // issued before the cells of run k are consumed, so their latency overlaps
-// the recurrence.  emit(k, t_mid, dt) is called by the lanes holding the k-th
-// occupied step with k < limit, consecutive k on consecutive lanes.  Returns
-// the number of occupied steps seen (all of them when limit is ~0u).
-template <uint32_t G, typename Cell, typename Emit>
-__device__ __forceinline__ uint32_t march(float4 ro, float4 rd, float cone, uint32_t max_steps, uint32_t limit, const uint32_t* __restrict__ bits, Cell cell, Emit emit) {
+// the recurrence.
+//
+// march_range covers steps [i_begin, i_end) starting from t = t_begin (any t
+// the full march passes at step i_begin: the recurrence depends on t alone,
+// so a march resumed there is bit-identical).  emit(k, t_mid, dt) is called by
+// the lanes holding the k-th occupied step of the range with k < limit,
+// consecutive k on consecutive lanes; mark(i, t, seen) is called by every
+// lane of the group at the start of each run, with the occupied steps seen
+// before it.  Returns the number of occupied steps seen (all of them when
+// limit is ~0u).
+template <uint32_t G, typename Cell, typename Emit, typename Mark>
+__device__ __forceinline__ uint32_t march_range(float4 ro, float4 rd, float cone, float dt_min, float t_begin, uint32_t i_begin, uint32_t i_end, uint32_t limit, const uint32_t* __restrict__ bits, Cell cell, Emit emit,
+                                                Mark mark) {
     static_assert(G >= 1u && G <= 64u && 64u % G == 0u, "group size must divide 64");
     const uint32_t lane = lane_id(), j_own = lane % G, shift = lane - j_own;
     const uint64_t group_bits = G == 64u ? ~0ull : ((1ull << G) - 1ull);
-    const float tn = ro.w, tf = rd.w;
-    if (!(tf - tn > 0.0f)) return 0u;
-    const float dt_min = (tf - tn) / (float)max_steps;
-    float t = tn;
-    uint32_t i = 0u, seen = 0u;
+    const float tf = rd.w;
+    float t        = t_begin;
+    uint32_t i = i_begin, seen = 0u;
     // One run of G steps: this lane's step (if any) and its cell word in flight.
     // The G steps run unconditionally, branch-free: once t reaches tf the
     // step is clamped to zero, so t stays put and every later step of the run
@@ -76,46 +82,57 @@ __device__ __forceinline__ uint32_t march(float4 ro, float4 rd, float cone, uint
     // step starts (one select per step) and recomputes that step's dt, mid
     // point and liveness from it afterwards with the same operations.
     auto step_dt = [&](float tt) { return fminf(fmaxf(dt_min, tt * cone), fmaxf(tf - tt, 0.0f)); };
-    auto run = [&](float& tm_out, float& dt_out, bool& has_out, uint32_t& idx_out, uint32_t& word_out) {
+    struct Run {
+        float tm, dt, t0;
+        uint32_t i0, idx, word;
+        bool has;
+    };
+    auto run = [&](Run& r) {
+        r.t0        = t;
+        r.i0        = i;
         float t_own = tf;
 #pragma unroll
         for (uint32_t j = 0; j < G; ++j) {
             if (j_own == j) t_own = t;
             t += step_dt(t);
         }
-        const float my_dt   = step_dt(t_own);
-        const float my_tm   = t_own + 0.5f * my_dt;
-        const bool has      = t_own < tf && i + j_own < max_steps;
+        r.dt             = step_dt(t_own);
+        r.tm             = t_own + 0.5f * r.dt;
+        r.has            = t_own < tf && i + j_own < i_end;
         i += G;
-        const float p[3]    = {ro.x + my_tm * rd.x, ro.y + my_tm * rd.y, ro.z + my_tm * rd.z};
-        const uint32_t idx  = has ? cell(p) : kOutside;
-        tm_out              = my_tm;
-        dt_out              = my_dt;
-        has_out             = has;
-        idx_out             = idx;
-        word_out            = (idx != kOutside && bits) ? bits[idx >> 5] : 0u;
+        const float p[3] = {ro.x + r.tm * rd.x, ro.y + r.tm * rd.y, ro.z + r.tm * rd.z};
+        r.idx            = r.has ? cell(p) : kOutside;
+        r.word           = (r.idx != kOutside && bits) ? bits[r.idx >> 5] : 0u;
     };
-    float tm0 = 0.0f, dt0 = 0.0f, tm1 = 0.0f, dt1 = 0.0f;
-    bool has0 = false, has1 = false;
-    uint32_t idx0 = kOutside, idx1 = kOutside, word0 = 0u, word1 = 0u;
-    bool more = t < tf && i < max_steps;  // uniform per group
-    if (more) run(tm0, dt0, has0, idx0, word0);
+    Run cur{}, nxt{};
+    bool more = t < tf && i < i_end;  // uniform per group
+    if (more) run(cur);
     while (more) {
-        const bool next = t < tf && i < max_steps;
-        if (next) run(tm1, dt1, has1, idx1, word1);
-        const bool hit      = has0 && idx0 != kOutside && (!bits || ((word0 >> (idx0 & 31u)) & 1u));
+        const bool next = t < tf && i < i_end;
+        if (next) run(nxt);
+        mark(cur.i0, cur.t0, seen);
+        const bool hit      = cur.has && cur.idx != kOutside && (!bits || ((cur.word >> (cur.idx & 31u)) & 1u));
         const uint64_t mask = (__ballot(hit) >> shift) & group_bits;
         const uint32_t k    = seen + (uint32_t)__popcll(mask & ((1ull << j_own) - 1ull));
-        if (hit && k < limit) emit(k, tm0, dt0);
+        if (hit && k < limit) emit(k, cur.tm, cur.dt);
         seen += (uint32_t)__popcll(mask);
         more = next && seen < limit;
-        tm0 = tm1;
-        dt0 = dt1;
-        has0 = has1;
-        idx0 = idx1;
-        word0 = word1;
+        cur  = nxt;
     }
     return seen;
+}
+
+// The whole march of a ray: steps [0, max_steps) from t_near = ro.w.
+template <uint32_t G, typename Cell, typename Emit, typename Mark>
+__device__ __forceinline__ uint32_t march(float4 ro, float4 rd, float cone, uint32_t max_steps, uint32_t limit, const uint32_t* __restrict__ bits, Cell cell, Emit emit, Mark mark) {
+    const float tn = ro.w, tf = rd.w;
+    if (!(tf - tn > 0.0f)) return 0u;
+    const float dt_min = (tf - tn) / (float)max_steps;
+    return march_range<G>(ro, rd, cone, dt_min, tn, 0u, max_steps, limit, bits, cell, emit, mark);
+}
+template <uint32_t G, typename Cell, typename Emit>
+__device__ __forceinline__ uint32_t march(float4 ro, float4 rd, float cone, uint32_t max_steps, uint32_t limit, const uint32_t* __restrict__ bits, Cell cell, Emit emit) {
+    return march<G>(ro, rd, cone, max_steps, limit, bits, cell, emit, [](uint32_t, float, uint32_t) {});
 }
 
 }  // namespace wave
