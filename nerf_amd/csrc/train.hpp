@@ -60,7 +60,8 @@ struct TrainBuffers {
     uint32_t* kept;              // [max_rays] samples kept (0 if cut)
     uint32_t* offsets;           // [max_rays]
     float* seg_t;                // [max_rays][segs] t at the start of each kSegSteps-step segment of the march
-    uint32_t* seg_seen;          // [max_rays][segs] occupied steps before the segment (count past the end)
+    uint32_t* seg_seen;          // [max_rays][segs] occupied steps before the segment
+    uint32_t* seg_reached;       // [max_rays] segments the march started
     uint32_t segs;               // ceil(max_steps / kSegSteps)
     uint32_t* scan_tmp;
     float2* samples;             // [sample_cap] (t_mid, dt)

@@ -186,7 +186,7 @@ __device__ __forceinline__ float cone_of(const NerfExtCamera& c) {  // :333-337
 constexpr uint32_t kTrainGroup = 16u;  // lanes per ray in the training march (4 rays per wave)
 
 __global__ __launch_bounds__(256) void k_train_rays(TrainParams P, const TrainDevState* S, const NerfExtCamera* __restrict__ cams, const uint8_t* __restrict__ images, const uint32_t* __restrict__ bits, float4* __restrict__ rays, float4* __restrict__ gt,
-                                                     uint32_t* __restrict__ counts, float* __restrict__ seg_t, uint32_t* __restrict__ seg_seen, uint32_t segs) {
+                                                     uint32_t* __restrict__ counts, float* __restrict__ seg_t, uint32_t* __restrict__ seg_seen, uint32_t* __restrict__ seg_reached, uint32_t segs) {
     constexpr uint32_t kPer = 64u / kTrainGroup;  // rays per wave
     const uint32_t lane = threadIdx.x & 63u, stride = gridDim.x * kWaves * kPer;
     const uint32_t n_rays = S->n_rays, cam_idx = S->camera, frame = S->frame;
@@ -245,8 +245,7 @@ __global__ __launch_bounds__(256) void k_train_rays(TrainParams P, const TrainDe
             rays[2ull * r + 1u] = rd;
             gt[r]               = g4;
             counts[r]           = count;
-            if (r < n_rays)
-                for (uint32_t k = reached; k < segs; ++k) seg_seen[(uint64_t)r * segs + k] = count;  // segments past the end: empty
+            seg_reached[r]      = reached;
         }
     }
 }
@@ -261,7 +260,8 @@ __global__ __launch_bounds__(256) void k_train_rays(TrainParams P, const TrainDe
 // samples fit under the capacity (its offset + count); unit (r, 0) records
 // the ray's kept count and the step totals.
 __global__ __launch_bounds__(256) void k_train_samples(TrainParams P, TrainDevState* S, const NerfExtCamera* __restrict__ cams, const uint32_t* __restrict__ bits, const float4* __restrict__ rays, const uint32_t* __restrict__ counts,
-                                                        const uint32_t* __restrict__ offsets, const float* __restrict__ seg_t, const uint32_t* __restrict__ seg_seen, uint32_t segs, uint32_t* __restrict__ kept,
+                                                        const uint32_t* __restrict__ offsets, const float* __restrict__ seg_t, const uint32_t* __restrict__ seg_seen, const uint32_t* __restrict__ seg_reached, uint32_t segs,
+                                                        uint32_t* __restrict__ kept,
                                                         float2* __restrict__ samples, uint32_t* __restrict__ sample_ray) {
     constexpr uint32_t kPer = 64u / kTrainGroup;
     const uint32_t lane = threadIdx.x & 63u, stride = gridDim.x * kWaves * kPer;
@@ -283,8 +283,9 @@ __global__ __launch_bounds__(256) void k_train_samples(TrainParams P, TrainDevSt
                 atomicAdd(&S->n_active, 1u);
             }
         }
-        if (!fits) continue;
-        const uint32_t s0 = seg_seen[u], s1 = sg + 1u < segs ? seg_seen[u + 1u] : count;
+        const uint32_t reached = seg_reached[r];
+        if (!fits || sg >= reached) continue;
+        const uint32_t s0 = seg_seen[u], s1 = sg + 1u < reached ? seg_seen[u + 1u] : count;
         if (s1 <= s0) continue;
         const float4 ro = rays[2ull * r], rd = rays[2ull * r + 1u];
         const float dt_min = (rd.w - ro.w) / (float)P.max_steps;  // as in wave::march
@@ -1208,10 +1209,10 @@ hipError_t launch_train_stage(const TrainParams& P, const TrainBuffers& B, uint3
         }
         break;
     case NERF_EXT_STAGE_SAMPLE: {
-        k_train_rays<<<ray_wave_blocks(P.max_rays), 256, 0, st>>>(P, B.state, B.cams, B.images, B.bits, B.rays, B.gt, B.counts, B.seg_t, B.seg_seen, B.segs);
+        k_train_rays<<<ray_wave_blocks(P.max_rays), 256, 0, st>>>(P, B.state, B.cams, B.images, B.bits, B.rays, B.gt, B.counts, B.seg_t, B.seg_seen, B.seg_reached, B.segs);
         const hipError_t e = exclusive_scan_u32(B.counts, B.offsets, P.max_rays, B.scan_tmp, &B.state->total, st);
         if (e != hipSuccess) return e;
-        k_train_samples<<<ray_wave_blocks(P.max_rays * B.segs), 256, 0, st>>>(P, B.state, B.cams, B.bits, B.rays, B.counts, B.offsets, B.seg_t, B.seg_seen, B.segs, B.kept, B.samples,
+        k_train_samples<<<ray_wave_blocks(P.max_rays * B.segs), 256, 0, st>>>(P, B.state, B.cams, B.bits, B.rays, B.counts, B.offsets, B.seg_t, B.seg_seen, B.seg_reached, B.segs, B.kept, B.samples,
                                                                               B.sample_ray);
         break;
     }
