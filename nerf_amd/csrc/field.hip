@@ -224,7 +224,12 @@ uint32_t persistent_blocks(uint32_t n, uint32_t per_cu) {
 
 hipError_t launch_field(const GridParams& g, const void* table, const FieldWeights& w, const FieldInputs& in, uint32_t n, float4* out4, hipStream_t stream) {
     if (n == 0u) return hipSuccess;
-    const uint32_t blocks   = (persistent_blocks(n, 8u) + 7u) / 8u * 8u;  // whole XCD rounds
+    // Workgroups per CU: 8 for large launches (renders: more tiles in flight
+    // per XCD keep its L2 busy), 3 for training-sized batches (<= 2^20
+    // samples: every workgroup stages the weights, so fewer, longer-lived
+    // ones; 3 is also what the register budget keeps resident).
+    const uint32_t per_cu   = n <= (1u << 20) ? 3u : 8u;
+    const uint32_t blocks   = (persistent_blocks(n, per_cu) + 7u) / 8u * 8u;  // whole XCD rounds
     const bool from_samples = in.samples != nullptr;
     if (g.table_dtype == NERF_EXT_F32) {
         if (from_samples)
