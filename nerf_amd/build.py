@@ -5,6 +5,10 @@ and linked into one shared library exporting the C ABI of include/nerf.h and
 include/nerf_ext.h.  Flags that matter for correctness:
   -ffp-contract=off     no implicit FMA: bit-exact indices, bits and counts
   -packed-fp32-ops off  no v_pk_*_f32 generation
+The host harness (nerf_amd/harness, plain C++20 built with g++) gives
+libnerf_host.so (PNG, JSON, dataset loading and PSNR behind a C API, no GPU
+needed) and nerf_bench, the reference host program's counterpart linked
+against libnerf.so.
 Run:  python -m nerf_amd.build   (or via __graft_entry__.build()).
 """
 from __future__ import annotations
@@ -21,6 +25,10 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libnerf.so"
+HARNESS = PKG / "harness"
+HOST_LIB = PKG / "libnerf_host.so"
+BENCH_EXE = PKG / "nerf_bench"
+GXX_FLAGS = ["-std=c++20", "-O2", "-fPIC", "-ffp-contract=off", "-Wall", "-Wextra", "-fvisibility=hidden"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",
@@ -73,9 +81,34 @@ def build_library(jobs: int = 8) -> Path:
     return LIB
 
 
+def build_harness(jobs: int = 8) -> tuple[Path, Path]:
+    """libnerf_host.so and nerf_bench (needs libnerf.so for the latter)."""
+    gxx = shutil.which("g++") or "g++"
+    BUILD.mkdir(exist_ok=True)
+    parts = ["png", "json", "dataset"]
+
+    def compile_one(stem: str) -> Path:
+        obj = BUILD / f"harness_{stem}.o"
+        _run([gxx, *GXX_FLAGS, "-c", str(HARNESS / f"{stem}.cpp"), "-o", str(obj)])
+        return obj
+
+    with cf.ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
+        objs = list(ex.map(compile_one, parts + ["host_capi", "nerf_bench"]))
+    common, capi, main_obj = objs[:3], objs[3], objs[4]
+    tmp = HOST_LIB.with_suffix(".so.tmp")
+    _run([gxx, "-shared", "-o", str(tmp), *map(str, common), str(capi)])
+    os.replace(tmp, HOST_LIB)
+    tmp = BENCH_EXE.with_suffix(".tmp")
+    _run([gxx, "-o", str(tmp), str(main_obj), *map(str, common), f"-L{PKG}", "-lnerf", "-Wl,-rpath,$ORIGIN"])
+    os.replace(tmp, BENCH_EXE)
+    return HOST_LIB, BENCH_EXE
+
+
 def main() -> None:
     lib = build_library()
     print(f"built {lib}")
+    for p in build_harness():
+        print(f"built {p}")
 
 
 if __name__ == "__main__":
