@@ -74,7 +74,10 @@ __device__ __forceinline__ half8_t color_input(const floatx4 o, const float d[3]
 // leave in one 256-byte store.
 __device__ __forceinline__ float field_channel(const floatx4 o, const floatx4 c, uint32_t grp, uint32_t s16) {
     (void)s16;
-    return grp == 0u ? __expf(o[0]) : __frcp_rn(1.0f + __expf(-c[0]));
+    // Both activations share one exp; bit selects keep the wave convergent.
+    const bool sigma = grp == 0u;
+    const float e    = __expf(select_bits(sigma, o[0], -c[0]));
+    return select_bits(sigma, e, __frcp_rn(1.0f + e));
 }
 
 // ---------------------------------------------------------------- kernels

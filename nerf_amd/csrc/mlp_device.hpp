@@ -156,6 +156,12 @@ __device__ __forceinline__ half8_t to_half8(const float f[8]) {
 }
 
 // Real SH bands 0..3 (Sloan 2008), coefficients 4g..4g+3 of a unit direction.
+// c ? a : b as a bit blend (no branch; exact).
+__device__ __forceinline__ float select_bits(bool c, float a, float b) {
+    const uint32_t m = 0u - (uint32_t)c;
+    return __uint_as_float((__float_as_uint(a) & m) | (__float_as_uint(b) & ~m));
+}
+
 __device__ __forceinline__ void sh4_quad(const float d[3], uint32_t grp, float out[4]) {
     const float x = d[0], y = d[1], z = d[2];
     const float xy = x * y, yz = y * z, xz = x * z;
@@ -177,8 +183,14 @@ __device__ __forceinline__ void sh4_quad(const float d[3], uint32_t grp, float o
     s[13] = 0.45704579946446572f * x * (1.0f - 5.0f * z2);
     s[14] = 1.4453057213202769f * z * (x2 - y2);
     s[15] = 0.59004358992664352f * x * (3.0f * y2 - x2);
+    // Lane group g takes s[4g .. 4g + 3]: bitwise selects, so the four groups
+    // of a wave never take divergent branches.
 #pragma unroll
-    for (uint32_t e = 0; e < 4u; ++e) out[e] = grp == 0u ? s[e] : grp == 1u ? s[4u + e] : grp == 2u ? s[8u + e] : s[12u + e];
+    for (uint32_t e = 0; e < 4u; ++e) {
+        const float lo = select_bits((grp & 1u) != 0u, s[4u + e], s[e]);
+        const float hi = select_bits((grp & 1u) != 0u, s[12u + e], s[8u + e]);
+        out[e]         = select_bits((grp & 2u) != 0u, hi, lo);
+    }
 }
 
 }  // namespace mlp
