@@ -47,6 +47,26 @@ struct TrainParams {
     uint32_t occ_cells;
 };
 
+// The coarse dense levels' gradient is summed in LDS: workgroup (chunk c,
+// slab k) adds the contributions of sample chunk c to entries [begin, begin +
+// count) of one level and writes them to row c of the partials, where the
+// levels lie one after another (level l from level_part[l], its entry count
+// rounded up to even).  A level of more than kCoarseSlabEntries entries takes
+// several slabs.
+constexpr uint32_t kCoarseMaxEntries  = 1u << 15;  // largest level on the slab path
+constexpr uint32_t kCoarseSlabEntries = 1u << 14;  // entries per slab: 128 KiB of int32 pairs in LDS
+constexpr uint32_t kCoarseChunks      = 64u;       // sample chunks, a multiple of 8 (the slabs of a chunk share an XCD)
+constexpr uint32_t kCoarseMaxSlabs    = NERF_EXT_MAX_LEVELS * (kCoarseMaxEntries / kCoarseSlabEntries);
+struct CoarsePlan {
+    uint32_t n_slabs;
+    uint32_t row;                                  // entries of a partial row (even)
+    uint32_t level[kCoarseMaxSlabs];               // per slab: level
+    uint32_t begin[kCoarseMaxSlabs];               // first entry within the level
+    uint32_t count[kCoarseMaxSlabs];               // entries (even)
+    uint32_t level_part[NERF_EXT_MAX_LEVELS + 1];  // per level: first entry in the partial row
+    uint32_t level_entries[NERF_EXT_MAX_LEVELS];   // (N + 1)^3
+};
+
 // Device buffers of a run.
 struct TrainBuffers {
     TrainDevState* state;
@@ -69,7 +89,7 @@ struct TrainBuffers {
     float4* field;               // [sample_cap] (sigma, r, g, b)
     half_t* features;            // [sample_cap][32]
     float4* draw;                // [sample_cap] (d sigma_raw, d r, d g, d b)
-    float* dfeat;                // [sample_cap][32] d(features), loss-scaled
+    float2* dfeat;               // [16 levels][sample_cap] d(features), loss-scaled
     // binned hash-grid scatter: records (entry within bin, 2 values) grouped
     // by bin of kBinEntries table entries
     uint32_t* bin_hist;          // [n_bins][kBinBlocks] record counts
@@ -78,9 +98,11 @@ struct TrainBuffers {
     uint32_t* bin_scan_tmp;
     unsigned long long* bin_total;
     uint2* rec;                  // [rec_cap] packed (entry within bin, 2 values)
-    uint32_t n_bins;             // bins of the hashed levels
-    uint32_t n_dense;            // leading levels scattered with atomics (dense, <= kAtomicMaxEntries entries)
+    uint32_t n_bins;             // bins of the levels past the coarse ones
+    uint32_t n_dense;            // leading (coarse) levels accumulated in LDS slabs (dense, <= kCoarseMaxEntries entries)
     uint64_t rec_cap;
+    CoarsePlan coarse;           // slabs of the coarse levels
+    float2* coarse_partials;     // [kCoarseChunks][coarse.row] per-chunk sums of the coarse levels' gradient
     // model
     GridParams grid;
     half_t* table;               // fp16 working copy [L][T][2]
@@ -95,6 +117,7 @@ struct TrainBuffers {
     float* mlp_m;
     float* mlp_v;
     float* dw_partials;          // [kDxMaxBlocks][10240] per-workgroup weight-gradient partials
+    double* norm_partials;       // [norm_partial_count] per-workgroup squared-gradient-norm partials
     uint64_t table_elems;
 };
 
@@ -102,9 +125,13 @@ constexpr uint32_t kDxMaxBlocks = 1024;  // workgroups of the input-gradient pas
 constexpr uint32_t kBinEntries = 4096;  // table entries per scatter bin (64 KiB of int64 pairs in LDS)
 constexpr uint32_t kBinBlocks  = 256;   // workgroups of the bin count / fill passes
 constexpr uint32_t kSegSteps = 64;  // march steps per resumable segment of the training sampler
-constexpr uint32_t kAtomicMaxEntries = 1u << 15;  // largest level scattered with atomics
 constexpr uint32_t kMaxBins    = 16384; // bins; the fill pass keeps a cursor and a maximum per bin in LDS (128 KiB)
 constexpr uint32_t kMlpParams  = NERF_EXT_DENSITY_PARAMS + NERF_EXT_COLOR_PARAMS;
+
+// Workgroups of the coarse-level reduction (16 columns of two entries each).
+inline uint32_t coarse_reduce_blocks(const CoarsePlan& C) { return (C.row / 2u + 15u) / 16u; }
+// Squared-norm partials of a step: coarse reduction, bins, weight gradients.
+inline uint32_t norm_partial_count(const TrainBuffers& B) { return coarse_reduce_blocks(B.coarse) + B.n_bins + kMlpParams / 64u; }
 
 // Launches one stage (NERF_EXT_STAGE_*) of a training step on `stream`.
 // `occupancy_update` selects the occupancy-maintenance kernels (the schedule

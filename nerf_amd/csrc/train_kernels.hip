@@ -6,9 +6,10 @@
 // ray sampling + march      :422-533                       k_train_rays, scan, k_train_samples
 // field forward             :1328-1339                     launch_field (field.hip)
 // composite fwd/bwd + loss  :1095-1182 (MSE)               k_composite_train (Huber)
-// MLP backward              :784-909, 1267-1301 (cuBLAS)   k_bwd_dx (dfeat, dW partials, coarse-level atomics), k_dw_reduce
-// hash-table backward       (hash-grid model)              k_bin_pass (count, fill), scan, k_bin_accumulate
-// grad stats, Adam          :1447-1554                     k_grad_stats, k_adam
+// MLP backward              :784-909, 1267-1301 (cuBLAS)   k_bwd_dx (dfeat, dW partials), k_dw_reduce
+// hash-table backward       (hash-grid model)              k_coarse_scatter, k_coarse_reduce (coarse levels);
+//                                                          k_bin_pass (count, fill), scan, k_bin_accumulate
+// grad stats, Adam          :1447-1554                     in the gradient writers; k_adam
 // end step                  :1495-1512                     k_step_end
 //
 // MI355X choices: every count lives in device memory and every launch has a
@@ -534,6 +535,11 @@ __device__ __forceinline__ void tile_backward(const half8_t* F, const half8_t x,
     }
 }
 
+__device__ __forceinline__ void sample_position(float t, float4 ro, float4 rd, const float* bmin, const float* bmax, float p[3]) {
+    const float w[3] = {ro.x + t * rd.x, ro.y + t * rd.y, ro.z + t * rd.z};
+#pragma unroll
+    for (int a = 0; a < 3; ++a) p[a] = (w[a] - bmin[a]) / (bmax[a] - bmin[a]);
+}
 __device__ __forceinline__ void sample_geometry(const float2* samples, const uint32_t* sample_ray, const float4* rays, const float* bmin, const float* bmax, uint32_t q, float p[3], float d[3]) {
     const float2 td  = samples[q];
     const uint32_t r = sample_ray[q];
@@ -541,9 +547,7 @@ __device__ __forceinline__ void sample_geometry(const float2* samples, const uin
     d[0] = rd.x;
     d[1] = rd.y;
     d[2] = rd.z;
-    const float w[3] = {ro.x + td.x * rd.x, ro.y + td.x * rd.y, ro.z + td.x * rd.z};
-#pragma unroll
-    for (int a = 0; a < 3; ++a) p[a] = (w[a] - bmin[a]) / (bmax[a] - bmin[a]);
+    sample_position(td.x, ro, rd, bmin, bmax, p);
 }
 
 // Value of lane i + o of the same 16-lane row (0 past the row's end): DPP
@@ -568,58 +572,144 @@ __device__ __forceinline__ void combine_step(float v[16], uint32_t seg) {
     }
 }
 
-// Scatter-add of d(feature) into the fp32 table gradient for one dense level,
-// with the contributions of a 16-lane row combined first.  Each row holds 16
-// consecutive samples (mostly of one ray) at the same level; runs of samples
-// in the same grid cell touch the same 8 corners, so their 16 corner values
-// (8 corners x 2 features) are summed across the run with a segmented suffix
-// scan over DPP row shifts and only the run's first lane issues atomics.
-// Runs are long on coarse levels, where the atomics would otherwise queue on
-// a few hot addresses.  All 64 lanes must call this (the level may differ
-// between rows); lanes with live == false contribute nothing.
-__device__ __forceinline__ void scatter_level(const GridParams& g, float* __restrict__ grad, uint32_t level, const float p[3], float d0, float d1, bool live) {
-    const uint32_t lane = threadIdx.x & 63u, s16 = lane & 15u;
-    const uint32_t lv   = level < g.n_levels ? level : 0u;
-    const uint32_t N    = g.resolution[lv];
-    const bool dense    = g.dense[lv] != 0u;
-    live                = live && level < g.n_levels;
-    const LevelCell c   = level_cell(p, N);
-    // Cell key; dead lanes get a key no live lane has.
-    const uint32_t kx = live ? c.i0[0] : 0xFFFFFFFFu, ky = c.i0[1], kz = c.i0[2];
-    const uint32_t px = __shfl_up(kx, 1, 16), py = __shfl_up(ky, 1, 16), pz = __shfl_up(kz, 1, 16);
-    const bool head   = s16 == 0u || kx != px || ky != py || kz != pz || !live;
-    const uint64_t heads = __ballot(head);
-    float v[16];
+// Coarse-level hash-grid backward: the first n_dense levels (dense, at most
+// kCoarseMaxEntries entries).  Consecutive samples mostly share cells there,
+// so binned records would crowd into a few bins and global atomics would
+// queue on a few hot addresses.  Instead workgroup (chunk, slab) adds the
+// contributions of one chunk of samples to the slab's entries in LDS and
+// writes them to the chunk's row of the partials, which k_coarse_reduce adds
+// in chunk order.  Runs of consecutive samples of a 16-lane row in the same
+// cell touch the same 8 corners: their 16 corner values (8 corners x 2
+// features) are summed across the run with a segmented suffix scan over DPP
+// row shifts, and only the run's first lane adds to LDS.
+// The LDS sums are int32 fixed point (fp32 LDS atomics run at a twelfth of
+// the rate of integer ones, and 32-bit entries let a slab hold a whole level
+// of up to 2^14 entries): a first pass over the chunk's d(feature) pairs of
+// the level bounds every entry's sum by S = sum of max(|d0|, |d1|) (the
+// corner weights of a sample add to 1), values are scaled by 2^e with
+// S * 2^e < 2^30 and rounded to integers, and each entry's exact sum is
+// scaled back once; the rounding of a value is at most 2^-31 S, below the
+// rounding of the fp16 gradients the reference accumulates.  A non-finite S
+// makes the slab's partials NaN, which the statistics report as non-finite.
+constexpr uint32_t kCoarseThreads = 1024u;
+constexpr uint32_t kCoarseBatch   = 4u;
+__global__ __launch_bounds__(kCoarseThreads) void k_coarse_scatter(TrainParams P, GridParams g, CoarsePlan C, const TrainDevState* S, const float2* __restrict__ samples, const uint32_t* __restrict__ sample_ray,
+                                                                   const float4* __restrict__ rays, const float2* __restrict__ dfeat, float2* __restrict__ partials) {
+    extern __shared__ __align__(16) uint32_t slab[];  // [count][2], two's complement
+    __shared__ float wsum[kCoarseThreads / 64u];
+    // Workgroup b runs on XCD b % 8: the slabs of one chunk share an XCD, and
+    // with it the L2 lines of the chunk's samples.
+    const uint32_t xcd = blockIdx.x & 7u, r = blockIdx.x >> 3;
+    const uint32_t k = r % C.n_slabs, chunk = (r / C.n_slabs) * 8u + xcd;
+    const uint32_t level = C.level[k], e0 = C.begin[k], ne = C.count[k];
+    for (uint32_t i = threadIdx.x; i < 2u * ne; i += blockDim.x) slab[i] = 0u;
+    const uint32_t n   = min(S->n_samples, P.sample_cap);
+    const uint32_t per = (n + kCoarseChunks - 1u) / kCoarseChunks;
+    const uint32_t s0 = min(n, chunk * per), s1 = min(n, s0 + per);
+    const float2* df_level = dfeat + (uint64_t)level * P.sample_cap;
+    // kCoarseBatch samples per thread have their loads in flight together.
+    float bound = 0.0f;
+    for (uint32_t q0 = s0 + threadIdx.x; q0 < s1; q0 += kCoarseBatch * kCoarseThreads) {
+        float2 df[kCoarseBatch];
 #pragma unroll
-    for (uint32_t k = 0; k < 8u; ++k) {
-        const float w = live ? corner_weight(c, k) : 0.0f;
-        v[2u * k]      = w * d0;
-        v[2u * k + 1u] = w * d1;
-    }
-    if (heads != ~0ull) {  // some run longer than one sample somewhere in the wave
-        const uint32_t row_heads = (uint32_t)(heads >> (lane & 48u)) & 0xFFFFu;
-        const uint32_t seg       = (uint32_t)__popc(row_heads & ((2u << s16) - 1u));
-        combine_step<1>(v, seg);
-        combine_step<2>(v, seg);
-        combine_step<4>(v, seg);
-        combine_step<8>(v, seg);
-    }
-    if (!(live && head)) return;
-    float* base = grad + (uint64_t)lv * g.table_size * 2u;
+        for (uint32_t b = 0; b < kCoarseBatch; ++b) {
+            const uint32_t q = q0 + b * kCoarseThreads;
+            df[b]            = q < s1 ? df_level[q] : make_float2(0.0f, 0.0f);
+        }
 #pragma unroll
-    for (uint32_t k = 0; k < 8u; ++k) {
-        const uint32_t idx = corner_index(c, k, N, dense, g.table_size - 1u);
-        atomicAdd(base + 2u * idx, v[2u * k]);
-        atomicAdd(base + 2u * idx + 1u, v[2u * k + 1u]);
+        for (uint32_t b = 0; b < kCoarseBatch; ++b) {
+            bound += fmaxf(fabsf(df[b].x), fabsf(df[b].y));
+            if (!isfinite(df[b].x) || !isfinite(df[b].y)) bound = __builtin_inff();  // fmaxf would drop a NaN
+        }
+    }
+    bound = wave_sum(bound);
+    if ((threadIdx.x & 63u) == 0u) wsum[threadIdx.x >> 6] = bound;
+    __syncthreads();
+    bound = 0.0f;
+    for (uint32_t w = 0; w < kCoarseThreads / 64u; ++w) bound += wsum[w];
+    float4* out = reinterpret_cast<float4*>(partials + (uint64_t)chunk * C.row + C.level_part[level] + e0);
+    if (!isfinite(bound)) {  // uniform
+        const float nan = __builtin_nanf("");
+        for (uint32_t i = threadIdx.x; i < ne / 2u; i += blockDim.x) out[i] = make_float4(nan, nan, nan, nan);
+        return;
+    }
+    const int e = bound > 0.0f ? 29 - ilogbf(bound) : 0;  // bound * 2^e < 2^30
+    const uint32_t N = g.resolution[level], s16 = threadIdx.x & 15u;
+    for (uint32_t base = s0; base < s1; base += kCoarseBatch * kCoarseThreads) {  // uniform over the workgroup
+        float2 td[kCoarseBatch], df[kCoarseBatch];
+        uint32_t ray[kCoarseBatch];
+#pragma unroll
+        for (uint32_t b = 0; b < kCoarseBatch; ++b) {
+            const uint32_t q = base + b * kCoarseThreads + threadIdx.x;
+            const bool live  = q < s1;
+            td[b]            = samples[live ? q : s0];
+            ray[b]           = sample_ray[live ? q : s0];
+            df[b]            = live ? df_level[q] : make_float2(0.0f, 0.0f);
+        }
+        float4 ro[kCoarseBatch], rd[kCoarseBatch];
+#pragma unroll
+        for (uint32_t b = 0; b < kCoarseBatch; ++b) {
+            ro[b] = rays[2ull * ray[b]];
+            rd[b] = rays[2ull * ray[b] + 1u];
+        }
+#pragma unroll
+        for (uint32_t b = 0; b < kCoarseBatch; ++b) {
+            const bool live = base + b * kCoarseThreads + threadIdx.x < s1;
+            float p[3];
+            sample_position(td[b].x, ro[b], rd[b], P.bmin, P.bmax, p);
+            const LevelCell c = level_cell(p, N);
+            // The cell's corners span entries [lo, lo + 1 + (N + 1) + (N + 1)^2];
+            // a wave none of whose cells reach the slab skips the rest (the
+            // samples of a wave are mostly one ray, in a few slabs).
+            const uint32_t lo = corner_index(c, 0u, N, true, 0u), hi = lo + 1u + (N + 1u) * (N + 2u);
+            if (__ballot(live && hi >= e0 && lo < e0 + ne) == 0ull) continue;  // uniform per wave
+            // Cell key; dead lanes get a key no live lane has.
+            const uint32_t kx = live ? c.i0[0] : 0xFFFFFFFFu, ky = c.i0[1], kz = c.i0[2];
+            const uint32_t px = __shfl_up(kx, 1, 16), py = __shfl_up(ky, 1, 16), pz = __shfl_up(kz, 1, 16);
+            const bool head      = s16 == 0u || kx != px || ky != py || kz != pz || !live;
+            const uint64_t heads = __ballot(head);
+            float v[16];
+#pragma unroll
+            for (uint32_t j = 0; j < 8u; ++j) {
+                const float w  = corner_weight(c, j);
+                v[2u * j]      = w * df[b].x;
+                v[2u * j + 1u] = w * df[b].y;
+            }
+            if (heads != ~0ull) {  // some run longer than one sample in the wave
+                const uint32_t lane      = threadIdx.x & 63u;
+                const uint32_t row_heads = (uint32_t)(heads >> (lane & 48u)) & 0xFFFFu;
+                const uint32_t seg       = (uint32_t)__popc(row_heads & ((2u << s16) - 1u));
+                combine_step<1>(v, seg);
+                combine_step<2>(v, seg);
+                combine_step<4>(v, seg);
+                combine_step<8>(v, seg);
+            }
+            if (live && head) {
+#pragma unroll
+                for (uint32_t j = 0; j < 8u; ++j) {
+                    const uint32_t idx = corner_index(c, j, N, true, 0u) - e0;  // wraps past ne below the slab
+                    if (idx < ne) {
+                        atomicAdd(&slab[2u * idx], (uint32_t)(int32_t)rintf(ldexpf(v[2u * j], e)));
+                        atomicAdd(&slab[2u * idx + 1u], (uint32_t)(int32_t)rintf(ldexpf(v[2u * j + 1u], e)));
+                    }
+                }
+            }
+        }
+    }
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < ne / 2u; i += blockDim.x) {
+        float f[4];
+#pragma unroll
+        for (uint32_t m = 0; m < 4u; ++m) f[m] = ldexpf((float)(int32_t)slab[4u * i + m], -e);
+        out[i] = make_float4(f[0], f[1], f[2], f[3]);
     }
 }
 
 // Input-gradient pass: d(features) of each tile, loss-scaled, to dfeat
-// [n][32] for the binned scatter; the first n_dense levels (the coarsest
-// dense ones, where runs of consecutive samples share cells and a few bins
-// would take every sample's records) are scattered here with row-combined
-// atomics.  Lane (g, s) holds features 16b + 4g + e of
-// sample s, i.e. levels 2g, 2g+1 (b = 0) and 8+2g, 9+2g (b = 1).
+// (level-major: [level][sample] pairs) for the coarse-slab and binned table
+// scatters.  Lane (g, s) holds
+// features 16b + 4g + e of sample s, i.e. levels 2g, 2g+1 (b = 0) and 8+2g,
+// 9+2g (b = 1).
 // Weight gradients inside the same pass.  dW = sum over samples of delta
 // act^T needs the sample axis on the MFMA reduction axis, so each phase every
 // wave puts its tile's deltas and activations of some layers into LDS,
@@ -661,9 +751,8 @@ __device__ __forceinline__ half8_t op_frag(const half_t* ops, uint32_t row0, uin
     return *reinterpret_cast<const half8_t*>(region + (row0 + r) * kOpPitch + 8u * (g & 1u));
 }
 
-__global__ __launch_bounds__(kThreads) void k_bwd_dx(TrainParams P, GridParams g, const TrainDevState* S, const half_t* __restrict__ dparams, const half_t* __restrict__ cparams, const half_t* __restrict__ features,
-                                                     const float4* __restrict__ draw, const float2* __restrict__ samples, const uint32_t* __restrict__ sample_ray, const float4* __restrict__ rays, float* __restrict__ dfeat, uint32_t n_dense,
-                                                     float* __restrict__ table_grad, float* __restrict__ partials) {
+__global__ __launch_bounds__(kThreads) void k_bwd_dx(TrainParams P, const TrainDevState* S, const half_t* __restrict__ dparams, const half_t* __restrict__ cparams, const half_t* __restrict__ features, const float4* __restrict__ draw,
+                                                     const float2* __restrict__ samples, const uint32_t* __restrict__ sample_ray, const float4* __restrict__ rays, float2* __restrict__ dfeat, float* __restrict__ partials) {
     extern __shared__ __align__(16) half_t dyn[];
     half8_t* F  = reinterpret_cast<half8_t*>(dyn);
     half_t* ops = dyn + kDxFragBytes / 2u;
@@ -699,9 +788,12 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dx(TrainParams P, GridParams g
         TileGrad T;
         tile_backward(F, x, d, gr, P.loss_scale, grp, T);
         if (live) {
-            float4* o = reinterpret_cast<float4*>(dfeat + (uint64_t)s * 32u);
-            o[grp]      = make_float4(T.dx[0][0], T.dx[0][1], T.dx[0][2], T.dx[0][3]);
-            o[4u + grp] = make_float4(T.dx[1][0], T.dx[1][1], T.dx[1][2], T.dx[1][3]);
+#pragma unroll
+            for (uint32_t b = 0; b < 2u; ++b) {
+                const uint64_t l = 8u * b + 2u * grp;
+                dfeat[l * P.sample_cap + s]        = make_float2(T.dx[b][0], T.dx[b][1]);
+                dfeat[(l + 1u) * P.sample_cap + s] = make_float2(T.dx[b][2], T.dx[b][3]);
+            }
         }
         // Phase 1: colour hidden layer.
         put16(W, 0u, T.dh2, s16, grp);
@@ -748,16 +840,6 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dx(TrainParams P, GridParams g
             acc_do = mfma16x16x32(op_frag(ops, 96u, ks, lane), op_frag(ops, 112u + 16u * wave, ks, lane), acc_do);
         }
         __syncthreads();
-        // The atomic levels are the first n_dense; lane group g holds levels
-        // 2g, 2g + 1 (b = 0) and 8 + 2g, 9 + 2g (b = 1).
-#pragma unroll
-        for (uint32_t b = 0; b < 2u; ++b) {
-            if (8u * b < n_dense) {  // uniform
-                const uint32_t l0 = 8u * b + 2u * grp;
-                scatter_level(g, table_grad, l0, p, T.dx[b][0], T.dx[b][1], live && l0 < n_dense);
-                scatter_level(g, table_grad, l0 + 1u, p, T.dx[b][2], T.dx[b][3], live && l0 + 1u < n_dense);
-            }
-        }
     }
     // This workgroup's partial of every weight gradient (parameter order:
     // density 0..3071, colour 3072..10239).  Lane (g, s16) of a block holds
@@ -807,7 +889,7 @@ __device__ __forceinline__ float2 record_value(uint2 r) { return make_float2(__u
 constexpr uint32_t kBinThreads = 1024u;
 template <bool kFill>
 __global__ __launch_bounds__(kBinThreads) void k_bin_pass(TrainParams P, GridParams g, const TrainDevState* S, const float2* __restrict__ samples, const uint32_t* __restrict__ sample_ray, const float4* __restrict__ rays,
-                                                  const float* __restrict__ dfeat, uint32_t n_dense, uint32_t n_bins, uint32_t* __restrict__ hist, uint2* __restrict__ rec,
+                                                  const float2* __restrict__ dfeat, uint32_t n_dense, uint32_t n_bins, uint32_t* __restrict__ hist, uint2* __restrict__ rec,
                                                   uint32_t* __restrict__ bin_max) {
     __shared__ uint32_t cursor[kMaxBins];
     __shared__ uint32_t vmax[kFill ? kMaxBins : 1u];  // bits of the largest |record value| per bin
@@ -820,7 +902,7 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_pass(TrainParams P, GridPar
     const uint32_t mask = g.table_size - 1u;
     const uint32_t lane = threadIdx.x & 63u, s16 = lane & 15u;
     // Waves take 64 consecutive samples; all lanes stay active (rows of 16
-    // combine runs of samples in the same cell, as in scatter_level, and only
+    // combine runs of samples in the same cell, as in k_coarse_scatter, and only
     // a run's first lane emits its 8 records).
     for (uint32_t base = blockIdx.x * blockDim.x + (threadIdx.x & ~63u); base < n; base += gridDim.x * blockDim.x) {
         const uint32_t s = base + lane;
@@ -838,8 +920,8 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_pass(TrainParams P, GridPar
             const bool head   = s16 == 0u || kx != px || ky != py || kz != pz || !live;
             float v[16];
             if constexpr (kFill) {
-                const float* df = dfeat + (uint64_t)q * 32u;
-                const float d0 = live ? df[2u * l] : 0.0f, d1 = live ? df[2u * l + 1u] : 0.0f;
+                const float2 df = live ? dfeat[(uint64_t)l * P.sample_cap + q] : make_float2(0.0f, 0.0f);
+                const float d0 = df.x, d1 = df.y;
 #pragma unroll
                 for (uint32_t k = 0; k < 8u; ++k) {
                     const float w  = corner_weight(c, k);
@@ -886,7 +968,7 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_pass(TrainParams P, GridPar
 // NaN, which the gradient statistics report as non-finite.
 // grad points at the first hashed level; entries = hashed levels x T.
 __global__ __launch_bounds__(512) void k_bin_accumulate(const uint32_t* __restrict__ offsets, uint32_t n_blocks, uint32_t n_bins, const unsigned long long* __restrict__ total, const uint2* __restrict__ rec,
-                                                        const uint32_t* __restrict__ bin_max, uint64_t entries, float2* __restrict__ grad, TrainDevState* S) {
+                                                        const uint32_t* __restrict__ bin_max, uint64_t entries, float2* __restrict__ grad, double* __restrict__ norm) {
     __shared__ unsigned long long acc[2u * kBinEntries];
     __shared__ uint32_t wmax[16];
     __shared__ double wsq[16];
@@ -910,7 +992,7 @@ __global__ __launch_bounds__(512) void k_bin_accumulate(const uint32_t* __restri
     if (mb >= 0x7F800000u) {  // NaN or inf among the records
         for (uint32_t i = threadIdx.x; i < kBinEntries; i += blockDim.x)
             if (base + i < entries) grad[base + i] = make_float2(__builtin_nanf(""), __builtin_nanf(""));
-        if (threadIdx.x == 0u) atomicOr(&S->nonfinite, 1u);
+        if (threadIdx.x == 0u) norm[bin] = -1.0;
         return;
     }
     const int e        = mx > 0.0f ? 39 - ilogbf(mx) : 0;  // mx * 2^e in [2^39, 2^40)
@@ -937,8 +1019,8 @@ __global__ __launch_bounds__(512) void k_bin_accumulate(const uint32_t* __restri
         }
     }
     __syncthreads();
-    // The bin's gradient, and its share of the squared gradient norm (the
-    // statistics k_grad_stats takes of the other gradients).
+    // The bin's gradient, and its share of the squared gradient norm (one
+    // partial per workgroup, added by k_grad_norm).
     const double inv = ldexp(1.0, -e);
     double sq        = 0.0;
     for (uint32_t i = threadIdx.x; i < kBinEntries; i += blockDim.x)
@@ -953,29 +1035,17 @@ __global__ __launch_bounds__(512) void k_bin_accumulate(const uint32_t* __restri
     if (threadIdx.x == 0u) {
         double b = 0.0;
         for (uint32_t w = 0; w < blockDim.x / 64u; ++w) b += wsq[w];
-        if (b != 0.0) atomicAdd(&S->grad_sumsq, b);
+        norm[bin] = b;
     }
-}
-
-// Start of the backward stage: clears the dense-level gradient slab (its
-// atomics accumulate into it) and the gradient statistics, which the hashed-
-// level accumulation and k_grad_stats then add to.
-__global__ __launch_bounds__(256) void k_backward_clear(float* __restrict__ p, uint64_t n, TrainDevState* S) {
-    if (blockIdx.x == 0u && threadIdx.x == 0u) {
-        S->grad_sumsq = 0.0;
-        S->nonfinite  = 0u;
-    }
-    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
-    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) p[i] = 0.0f;
 }
 
 // Sum of the per-workgroup partials: a workgroup takes 16 columns of 4
 // parameters; its 16 slices of 16 threads each add every 16th partial (16
 // independent four-wide loads per thread), then the slices are added in a
-// fixed order.  The MLP gradient's share of the squared norm and the
-// non-finite flag are taken here, from the values written.
+// fixed order.  The MLP gradient's share of the squared norm is taken here,
+// from the values written: one partial per workgroup, added by k_grad_norm.
 constexpr uint32_t kReduceSlices = 16u;
-__global__ __launch_bounds__(256) void k_dw_reduce(const float* __restrict__ partials, uint32_t blocks, float* __restrict__ grad, TrainDevState* S) {
+__global__ __launch_bounds__(256) void k_dw_reduce(const float* __restrict__ partials, uint32_t blocks, float* __restrict__ grad, double* __restrict__ norm) {
     static_assert(kMlpParams % 64u == 0u, "whole columns per workgroup");
     __shared__ float4 part[kReduceSlices][16];
     const uint32_t col = threadIdx.x & 15u, slice = threadIdx.x >> 4;
@@ -1009,50 +1079,91 @@ __global__ __launch_bounds__(256) void k_dw_reduce(const float* __restrict__ par
         gi += e == 0u ? v.x : e == 1u ? v.y : e == 2u ? v.z : v.w;
     }
     grad[blockIdx.x * 64u + threadIdx.x] = gi;
-    double sq = 0.0;
-    bool bad  = false;
-    if (isfinite(gi)) sq = (double)gi * (double)gi;
-    else bad = true;
-    sq = wave_sum_d(sq);
-    if (__ballot(bad) != 0ull && threadIdx.x == 0u) atomicOr(&S->nonfinite, 1u);
-    if (threadIdx.x == 0u && sq != 0.0) atomicAdd(&S->grad_sumsq, sq);
+    const bool finite = isfinite(gi);
+    const double sq   = wave_sum_d(finite ? (double)gi * (double)gi : 0.0);
+    if (threadIdx.x == 0u) norm[blockIdx.x] = __ballot(!finite) != 0ull ? -1.0 - sq : sq;
 }
 
-// ------------------------------------------------------------------ Adam
-// Squared norm and non-finite flag of the gradients accumulated with atomics
-// (dense hash levels, MLP); the hashed levels' share comes from
-// k_bin_accumulate.  Four-wide loads, fp32 per load, fp64 across loads.
-__global__ __launch_bounds__(256) void k_grad_stats(const float* __restrict__ g, uint64_t n, TrainDevState* S) {
-    __shared__ double ws[kWaves];
+// Sum of the coarse levels' chunk partials, in chunk order (the same layout
+// of work as k_dw_reduce: 16 columns of two entries per workgroup, 16 slices
+// of the chunks), written to the levels' gradient; their share of the squared
+// norm is taken from the values written, as in k_dw_reduce.  Entries
+// past a level's (N + 1)^3 are never written and stay zero.
+static_assert(kCoarseChunks % kReduceSlices == 0u, "whole slices of chunks");
+__global__ __launch_bounds__(256) void k_coarse_reduce(const float2* __restrict__ partials, CoarsePlan C, uint32_t n_levels, uint32_t table_size, float* __restrict__ grad, double* __restrict__ norm) {
+    __shared__ float4 part[kReduceSlices][16];
+    const uint32_t col = threadIdx.x & 15u, slice = threadIdx.x >> 4;
+    const uint32_t cols = C.row / 2u;
+    const uint32_t c    = blockIdx.x * 16u + col;  // entries 2c, 2c + 1 of a partial row
+    const float4* p4    = reinterpret_cast<const float4*>(partials);
+    float4 s            = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (c < cols) {
+        constexpr uint32_t kPer = kCoarseChunks / kReduceSlices;
+        float4 v[kPer];
+#pragma unroll
+        for (uint32_t k = 0; k < kPer; ++k) v[k] = p4[(uint64_t)(slice + k * kReduceSlices) * cols + c];
+#pragma unroll
+        for (uint32_t k = 0; k < kPer; ++k) {
+            s.x += v[k].x;
+            s.y += v[k].y;
+            s.z += v[k].z;
+            s.w += v[k].w;
+        }
+    }
+    part[slice][col] = s;
+    __syncthreads();
+    if (threadIdx.x >= 64u) return;
+    // Thread t < 64: component t & 3 (entry t >> 1 & 1, feature t & 1) of column t >> 2.
+    const uint32_t cc = threadIdx.x >> 2, comp = threadIdx.x & 3u;
+    float gi          = 0.0f;
+    for (uint32_t k = 0; k < kReduceSlices; ++k) {
+        const float4 v = part[k][cc];
+        gi += comp == 0u ? v.x : comp == 1u ? v.y : comp == 2u ? v.z : v.w;
+    }
+    const uint32_t e = 2u * (blockIdx.x * 16u + cc) + (comp >> 1);  // entry of the partial row
+    uint32_t l       = 0u;
+    while (l + 1u < n_levels && e >= C.level_part[l + 1u]) ++l;
+    const uint32_t el = e - C.level_part[l];
+    const bool valid  = e < C.row && el < C.level_entries[l];
+    if (valid) grad[((uint64_t)l * table_size + el) * 2u + (comp & 1u)] = gi;
+    const bool finite = !valid || isfinite(gi);
+    const double sq   = wave_sum_d(valid && finite ? (double)gi * (double)gi : 0.0);
+    if (threadIdx.x == 0u) norm[blockIdx.x] = __ballot(!finite) != 0ull ? -1.0 - sq : sq;
+}
+
+// The step's squared gradient norm: the sum, in a fixed order, of the
+// per-workgroup partials of k_coarse_reduce, k_bin_accumulate and k_dw_reduce.
+// A partial is the sum of squares of the workgroup's finite gradient values,
+// or -1 minus that sum when one of its values is not finite (the statistics
+// of backend-cuda.cu:1451-1476: finite values summed, a separate flag).
+// Per-workgroup atomics on one address would serialize; this sum is also
+// independent of the order the workgroups ran in.
+constexpr uint32_t kNormThreads = 1024u;
+__global__ __launch_bounds__(kNormThreads) void k_grad_norm(const double* __restrict__ norm, uint32_t n, TrainDevState* S) {
+    __shared__ double ws[kNormThreads / 64u];
     __shared__ uint32_t bad;
     if (threadIdx.x == 0u) bad = 0u;
     __syncthreads();
-    double acc          = 0.0;
-    uint32_t nonfinite  = 0u;
-    const uint64_t step = (uint64_t)gridDim.x * blockDim.x;
-    const uint64_t n4   = n / 4u;
-    const float4* g4    = reinterpret_cast<const float4*>(g);
-    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += step) {
-        const float4 v = g4[i];
-        if (!isfinite(v.x) || !isfinite(v.y) || !isfinite(v.z) || !isfinite(v.w)) nonfinite = 1u;
-        else acc += (double)v.x * (double)v.x + (double)v.y * (double)v.y + (double)v.z * (double)v.z + (double)v.w * (double)v.w;
+    double acc      = 0.0;
+    bool nonfinite  = false;
+    for (uint32_t i = threadIdx.x; i < n; i += kNormThreads) {
+        const double v = norm[i];
+        nonfinite      = nonfinite || v < 0.0;
+        acc += v < 0.0 ? -1.0 - v : v;
     }
-    for (uint64_t i = 4u * n4 + (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += step) {
-        const float v = g[i];
-        if (!isfinite(v)) nonfinite = 1u;
-        else acc += (double)v * (double)v;
-    }
-    const double w = wave_sum_d(acc);
-    if ((threadIdx.x & 63u) == 0u) ws[threadIdx.x >> 6] = w;
-    if (nonfinite) atomicOr(&bad, 1u);
+    acc = wave_sum_d(acc);
+    if ((threadIdx.x & 63u) == 0u) ws[threadIdx.x >> 6] = acc;
+    if (nonfinite) bad = 1u;
     __syncthreads();
     if (threadIdx.x == 0u) {
-        const double b = ws[0] + ws[1] + ws[2] + ws[3];
-        if (b != 0.0) atomicAdd(&S->grad_sumsq, b);
-        if (bad) atomicOr(&S->nonfinite, 1u);
+        double t = 0.0;
+        for (uint32_t w = 0; w < kNormThreads / 64u; ++w) t += ws[w];
+        S->grad_sumsq = t;
+        S->nonfinite  = bad;
     }
 }
 
+// ------------------------------------------------------------------ Adam
 // :1513-1536: skip guard, lr decay, clip factor, bias corrections, from the
 // step's gradient statistics.
 struct AdamCoef {
@@ -1160,17 +1271,23 @@ hipError_t launch_composite_train(const TrainParams& P, const TrainBuffers& B, h
 hipError_t launch_mlp_backward(const TrainParams& P, const TrainBuffers& B, hipStream_t st) {
     const uint32_t cus = device_cu_count();
     if (B.grid.table_dtype != NERF_EXT_F16) return hipErrorInvalidValue;
-    // Dense levels: cleared, then row-combined atomics inside k_bwd_dx.
-    const uint64_t dense_elems = (uint64_t)B.n_dense * B.grid.table_size * 2u;
-    k_backward_clear<<<grid_for(dense_elems, cus * 4u), 256, 0, st>>>(B.table_grad, dense_elems, B.state);
-    static bool lds_set = false;  // once per process: the kernel's dynamic LDS exceeds the 64 KiB default
+    static bool lds_set = false;  // once per process: the kernels' dynamic LDS exceeds the 64 KiB default
     if (!lds_set) {
-        const hipError_t e = hipFuncSetAttribute((const void*)k_bwd_dx, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDxLds);
+        hipError_t e = hipFuncSetAttribute((const void*)k_bwd_dx, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDxLds);
+        if (e == hipSuccess) e = hipFuncSetAttribute((const void*)k_coarse_scatter, hipFuncAttributeMaxDynamicSharedMemorySize, (int)(kCoarseSlabEntries * 2u * sizeof(uint32_t)));
         if (e != hipSuccess) return e;
         lds_set = true;
     }
     const uint32_t dx_blocks = min(cus * 2u, kDxMaxBlocks);  // two per CU (LDS)
-    k_bwd_dx<<<dx_blocks, kThreads, kDxLds, st>>>(P, B.grid, B.state, B.dparams, B.cparams, B.features, B.draw, B.samples, B.sample_ray, B.rays, B.dfeat, B.n_dense, B.table_grad, B.dw_partials);
+    k_bwd_dx<<<dx_blocks, kThreads, kDxLds, st>>>(P, B.state, B.dparams, B.cparams, B.features, B.draw, B.samples, B.sample_ray, B.rays, B.dfeat, B.dw_partials);
+    // Coarse levels: LDS slabs per chunk of samples, then the chunks added.
+    if (B.n_dense) {
+        const CoarsePlan& C = B.coarse;
+        uint32_t lds_entries = 0u;
+        for (uint32_t k = 0; k < C.n_slabs; ++k) lds_entries = max(lds_entries, C.count[k]);
+        k_coarse_scatter<<<kCoarseChunks * C.n_slabs, kCoarseThreads, lds_entries * 2u * sizeof(uint32_t), st>>>(P, B.grid, C, B.state, B.samples, B.sample_ray, B.rays, B.dfeat, B.coarse_partials);
+        k_coarse_reduce<<<coarse_reduce_blocks(C), 256, 0, st>>>(B.coarse_partials, C, B.n_dense, B.grid.table_size, B.table_grad, B.norm_partials);
+    }
     // Hashed levels: binned.
     if (B.n_bins) {
         k_bin_pass<false><<<kBinBlocks, kBinThreads, 0, st>>>(P, B.grid, B.state, B.samples, B.sample_ray, B.rays, B.dfeat, B.n_dense, B.n_bins, B.bin_hist, nullptr, nullptr);
@@ -1178,18 +1295,16 @@ hipError_t launch_mlp_backward(const TrainParams& P, const TrainBuffers& B, hipS
         if (e != hipSuccess) return e;
         k_bin_pass<true><<<kBinBlocks, kBinThreads, 0, st>>>(P, B.grid, B.state, B.samples, B.sample_ray, B.rays, B.dfeat, B.n_dense, B.n_bins, B.bin_off, B.rec, B.bin_max);
         k_bin_accumulate<<<B.n_bins, 512, 0, st>>>(B.bin_off, kBinBlocks, B.n_bins, B.bin_total, B.rec, B.bin_max, (uint64_t)(B.grid.n_levels - B.n_dense) * B.grid.table_size,
-                                                   reinterpret_cast<float2*>(B.table_grad) + (uint64_t)B.n_dense * B.grid.table_size, B.state);
+                                                   reinterpret_cast<float2*>(B.table_grad) + (uint64_t)B.n_dense * B.grid.table_size, B.norm_partials + coarse_reduce_blocks(B.coarse));
     }
-    k_dw_reduce<<<kMlpParams / 64u, 256, 0, st>>>(B.dw_partials, dx_blocks, B.mlp_grad, B.state);
+    k_dw_reduce<<<kMlpParams / 64u, 256, 0, st>>>(B.dw_partials, dx_blocks, B.mlp_grad, B.norm_partials + coarse_reduce_blocks(B.coarse) + B.n_bins);
+    k_grad_norm<<<1, kNormThreads, 0, st>>>(B.norm_partials, norm_partial_count(B), B.state);
     return hipGetLastError();
 }
 
 hipError_t launch_adam(const TrainParams& P, const TrainBuffers& B, hipStream_t st) {
     const uint32_t cap = device_cu_count() * 16u;
-    // The dense levels' gradient statistics; the binned levels' and the MLP's
-    // were taken when those gradients were written.
-    const uint64_t dense_elems = (uint64_t)B.n_dense * B.grid.table_size * 2u;
-    if (dense_elems) k_grad_stats<<<grid_for(dense_elems / 4u, cap), 256, 0, st>>>(B.table_grad, dense_elems, B.state);
+    // The gradient statistics were taken when the gradients were written.
     if (B.table_elems % 4u) return hipErrorInvalidValue;
     const AdamSeg table{B.table_f32, B.table, B.table_grad, B.table_m, B.table_v};
     const AdamSeg mlp{B.mlp_f32, B.dparams, B.mlp_grad, B.mlp_m, B.mlp_v};

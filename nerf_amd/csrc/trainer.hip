@@ -124,16 +124,31 @@ NerfStatus trainer_create(const NerfExtTrainDesc* d, const BorrowedModel* borrow
     NERF_HIP_TRY(alloc(T, B.field, P.sample_cap));
     NERF_HIP_TRY(alloc(T, B.features, 32ull * P.sample_cap));
     NERF_HIP_TRY(alloc(T, B.draw, P.sample_cap));
-    NERF_HIP_TRY(alloc(T, B.dfeat, 32ull * P.sample_cap));
-    // Leading dense levels of at most kAtomicMaxEntries entries take row-
-    // combined atomics; binned, the records of every sample would crowd into
-    // their few bins.  Every other level is binned.
-    B.n_dense = 0u;
+    NERF_HIP_TRY(alloc(T, B.dfeat, 16ull * P.sample_cap));
+    // Leading dense levels of at most kCoarseMaxEntries entries are summed in
+    // LDS slabs; binned, the records of every sample would crowd into their
+    // few bins.  Every other level is binned.
+    B.n_dense          = 0u;
+    CoarsePlan& C      = B.coarse;
+    C                  = CoarsePlan{};
     while (B.n_dense < g.n_levels && g.dense[B.n_dense]) {
         const uint64_t v = (uint64_t)g.resolution[B.n_dense] + 1u;
-        if (v * v * v > kAtomicMaxEntries) break;
-        ++B.n_dense;
+        if (v * v * v > kCoarseMaxEntries) break;
+        const uint32_t l     = B.n_dense++;
+        const uint32_t e     = (uint32_t)(v * v * v);
+        const uint32_t e_pad = (e + 1u) & ~1u;
+        C.level_entries[l]   = e;
+        C.level_part[l]      = C.row;
+        for (uint32_t b = 0; b < e_pad; b += kCoarseSlabEntries) {
+            C.level[C.n_slabs] = l;
+            C.begin[C.n_slabs] = b;
+            C.count[C.n_slabs] = e_pad - b < kCoarseSlabEntries ? e_pad - b : kCoarseSlabEntries;
+            ++C.n_slabs;
+        }
+        C.row += e_pad;
     }
+    C.level_part[B.n_dense] = C.row;
+    if (C.row) NERF_HIP_TRY(alloc(T, B.coarse_partials, (uint64_t)kCoarseChunks * C.row));
     B.n_bins  = (uint32_t)(((uint64_t)(g.n_levels - B.n_dense) * g.table_size + kBinEntries - 1u) / kBinEntries);
     B.rec_cap = (uint64_t)P.sample_cap * (g.n_levels - B.n_dense) * 8u;
     NERF_HIP_TRY(alloc(T, B.bin_hist, (uint64_t)B.n_bins * kBinBlocks));
@@ -149,6 +164,7 @@ NerfStatus trainer_create(const NerfExtTrainDesc* d, const BorrowedModel* borrow
     NERF_HIP_TRY(alloc(T, B.mlp_m, kMlpParams));
     NERF_HIP_TRY(alloc(T, B.mlp_v, kMlpParams));
     NERF_HIP_TRY(alloc(T, B.dw_partials, (uint64_t)kDxMaxBlocks * kMlpParams));
+    NERF_HIP_TRY(alloc(T, B.norm_partials, norm_partial_count(B)));
     if (borrowed) {
         B.table     = borrowed->table;
         B.table_f32 = borrowed->table_f32;

@@ -183,8 +183,9 @@ def _frob(got, want):
     return float(np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-30))
 
 
-# T = 2^14: the dense levels take atomics, the hashed ones bins.  T = 2^17:
-# the coarsest dense levels take atomics, the finer dense ones bins as well.
+# T = 2^14: the dense levels take the coarse LDS slabs, the hashed ones bins.
+# T = 2^17: the coarsest dense levels take the slabs (the largest one two of
+# them), the finer dense ones bins as well.
 @pytest.mark.parametrize("log2_table", [14, 17])
 def test_backward_stage(dataset, log2_table):
     announce(f"train backward stage, T=2^{log2_table}")
