@@ -32,11 +32,6 @@ using namespace mlp;
 
 namespace {
 
-__device__ __forceinline__ void stage_params(half_t* lds, const half_t* src, uint32_t count) {
-    for (uint32_t i = threadIdx.x; i < count; i += blockDim.x) lds[i] = src[i];
-    __syncthreads();
-}
-
 // Position (normalised by the AABB) and direction of march sample q.
 __device__ __forceinline__ void sample_point(const FieldInputs& in, uint32_t q, float p[3], float d[3]) {
     const float2 td  = in.samples[q];
@@ -51,40 +46,19 @@ __device__ __forceinline__ void sample_point(const FieldInputs& in, uint32_t q, 
     for (int a = 0; a < 3; ++a) p[a] = (w[a] - in.bmin[a]) / (in.bmax[a] - in.bmin[a]);
 }
 
-// Colour input of lane group grp from density outputs 4g..4g+3 and SH
-// coefficients 4g..4g+3; the slot of density output 0 (sigma) carries a zero
-// weight and a zero value.
-__device__ __forceinline__ half8_t color_input(const floatx4 o, const float d[3], uint32_t grp) {
+// Colour input from per-sample fp32 SH coefficients (lane group grp's four).
+__device__ __forceinline__ half8_t color_input_dir(const floatx4 o, const float d[3], uint32_t grp) {
     float sh[4];
     sh4_quad(d, grp, sh);
-    half8_t xc;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        xc[e]     = (half_t)o[e];
-        xc[4 + e] = (half_t)sh[e];
-    }
-    if (grp == 0u) xc[0] = (half_t)0.0f;
-    return xc;
-}
-
-// Output activation spread over the wave: lane (g, s) holds channel g of
-// sample s in element 0 (sigma from the density output, colour g - 1 from the
-// row-permuted colour output) and applies its activation (g = 0: exp, else
-// sigmoid), so each lane evaluates one transcendental and the 16 samples
-// leave in one 256-byte store.
-__device__ __forceinline__ float field_channel(const floatx4 o, const floatx4 c, uint32_t grp, uint32_t s16) {
-    (void)s16;
-    // Both activations share one exp; bit selects keep the wave convergent.
-    const bool sigma = grp == 0u;
-    const float e    = __expf(select_bits(sigma, o[0], -c[0]));
-    return select_bits(sigma, e, __frcp_rn(1.0f + e));
+    return color_input(o, half4_t{(half_t)sh[0], (half_t)sh[1], (half_t)sh[2], (half_t)sh[3]}, grp);
 }
 
 // ---------------------------------------------------------------- kernels
 // Density MLP on fp16 features [n][32] -> raw outputs [n][16].
 __global__ __launch_bounds__(kBlockThreads) void k_density_mlp(const half_t* __restrict__ params, const half_t* __restrict__ features, uint32_t n, float* __restrict__ out) {
-    __shared__ half_t sp[NERF_EXT_DENSITY_PARAMS];
-    stage_params(sp, params, NERF_EXT_DENSITY_PARAMS);
+    __shared__ __align__(16) half_t sp[NERF_EXT_DENSITY_PARAMS];
+    stage_density<kBlockThreads>(sp, params);
+    __syncthreads();
     const uint32_t lane = threadIdx.x & 63u, grp = lane >> 4, s16 = lane & 15u;
     DensityFrags f;
     load_density(sp, f, lane);
@@ -107,8 +81,9 @@ __global__ __launch_bounds__(kBlockThreads) void k_density_mlp(const half_t* __r
 // Fused encode + density MLP on points: out [n][16] = (exp(raw0), raw1..15).
 template <typename TableT>
 __global__ __launch_bounds__(kBlockThreads) void k_density_forward(GridParams g, const TableT* __restrict__ table, const half_t* __restrict__ params, const float* __restrict__ pos, uint32_t n, float* __restrict__ out) {
-    __shared__ half_t sp[NERF_EXT_DENSITY_PARAMS];
-    stage_params(sp, params, NERF_EXT_DENSITY_PARAMS);
+    __shared__ __align__(16) half_t sp[NERF_EXT_DENSITY_PARAMS];
+    stage_density<kBlockThreads>(sp, params);
+    __syncthreads();
     const uint32_t lane = threadIdx.x & 63u, grp = lane >> 4, s16 = lane & 15u;
     DensityFrags f;
     load_density(sp, f, lane);
@@ -131,9 +106,8 @@ __global__ __launch_bounds__(kBlockThreads) void k_density_forward(GridParams g,
 template <typename TableT, bool kFromSamples>
 __global__ __launch_bounds__(kBlockThreads) void k_field_forward(GridParams g, const TableT* __restrict__ table, const half_t* __restrict__ dparams, const half_t* __restrict__ cparams, FieldInputs in, uint32_t n_cap, float4* __restrict__ out) {
     const uint32_t n = in.n_dev ? min(*in.n_dev, n_cap) : n_cap;
-    __shared__ half_t sp[NERF_EXT_DENSITY_PARAMS + NERF_EXT_COLOR_PARAMS];
-    for (uint32_t i = threadIdx.x; i < NERF_EXT_DENSITY_PARAMS; i += blockDim.x) sp[i] = dparams[i];
-    for (uint32_t i = threadIdx.x; i < NERF_EXT_COLOR_PARAMS; i += blockDim.x) sp[NERF_EXT_DENSITY_PARAMS + i] = cparams[i];
+    __shared__ __align__(16) half_t sp[NERF_EXT_DENSITY_PARAMS + NERF_EXT_COLOR_PARAMS];
+    stage_weights<kBlockThreads>(sp, dparams, cparams);
     __syncthreads();
     const uint32_t lane = threadIdx.x & 63u, grp = lane >> 4, s16 = lane & 15u;
     DensityFrags fd;
@@ -169,50 +143,63 @@ __global__ __launch_bounds__(kBlockThreads) void k_field_forward(GridParams g, c
         const half8_t x = to_half8(feat);
         if (in.features_out && s < n) *reinterpret_cast<half8_t*>(in.features_out + (uint64_t)s * 32u + 8u * grp) = x;
         const floatx4 o = density_mlp(fd, x);
-        const floatx4 c = color_mlp(fc, color_input(o, d, grp));
-        const float v = field_channel(o, c, grp, s16);
+        const floatx4 c = color_mlp(fc, color_input_dir(o, d, grp));
+        const float v   = field_channel(o, c, grp);
         if (s < n) reinterpret_cast<float*>(out)[4ull * dst + grp] = v;
     }
 }
 
-// MLP pass on given encodings: lane (g, s) loads features 8g..8g+7 of
-// sample s (one 16-byte load), the B operand of the density MLP.  The next
-// tile's features and directions are loaded before the current tile is
-// computed, so their latency overlaps the products.
+// MLP pass on given encodings, in groups of 64 samples (four 16-sample
+// tiles) per wave.  Lane l first evaluates all 16 SH coefficients of sample
+// l of the group and leaves them in LDS as fp16; lane (g, s) of tile t then
+// reads coefficients 4g..4g+3 of sample 16t + s back (8 bytes) instead of
+// evaluating the 16 polynomials and selecting four.  Lane (g, s) loads
+// features 8g..8g+7 of sample s of each tile (one 16-byte load), the B
+// operand of the density MLP.  The stores follow all four tiles, so the four
+// chains share one basic block.
+constexpr uint32_t kGroupSamples = 64u;
 __global__ __launch_bounds__(kBlockThreads) void k_field_mlp(const half_t* __restrict__ dparams, const half_t* __restrict__ cparams, const half_t* __restrict__ features, const float* __restrict__ dirs, uint32_t n,
                                                             float4* __restrict__ out) {
-    __shared__ half_t sp[NERF_EXT_DENSITY_PARAMS + NERF_EXT_COLOR_PARAMS];
-    for (uint32_t i = threadIdx.x; i < NERF_EXT_DENSITY_PARAMS; i += blockDim.x) sp[i] = dparams[i];
-    for (uint32_t i = threadIdx.x; i < NERF_EXT_COLOR_PARAMS; i += blockDim.x) sp[NERF_EXT_DENSITY_PARAMS + i] = cparams[i];
+    __shared__ __align__(16) half_t sp[NERF_EXT_DENSITY_PARAMS + NERF_EXT_COLOR_PARAMS];
+    __shared__ half4_t shl[kBlockWaves][kGroupSamples][4];
+    stage_weights<kBlockThreads>(sp, dparams, cparams);
     __syncthreads();
-    const uint32_t lane = threadIdx.x & 63u, grp = lane >> 4, s16 = lane & 15u;
+    const uint32_t lane = threadIdx.x & 63u, grp = lane >> 4, s16 = lane & 15u, wv = threadIdx.x >> 6;
     DensityFrags fd;
     ColorFrags fc;
     load_density(sp, fd, lane);
     load_color(sp + NERF_EXT_DENSITY_PARAMS, fc, lane);
-    const uint32_t tiles  = (n + 15u) / 16u;
+    const uint32_t groups = (n + kGroupSamples - 1u) / kGroupSamples;
     const uint32_t nwaves = gridDim.x * kBlockWaves;
-    half8_t xn{};
-    float dn[3] = {0.0f, 0.0f, 0.0f};
-    auto fetch = [&](uint32_t t) {
-        const uint32_t s = t * 16u + s16;
-        const uint32_t q = s < n ? s : n - 1u;
-        xn               = *reinterpret_cast<const half8_t*>(features + (uint64_t)q * 32u + 8u * grp);
-        dn[0]            = dirs[3ull * q];
-        dn[1]            = dirs[3ull * q + 1u];
-        dn[2]            = dirs[3ull * q + 2u];
-    };
-    uint32_t tile = blockIdx.x * kBlockWaves + (threadIdx.x >> 6);
-    if (tile < tiles) fetch(tile);
-    for (; tile < tiles; tile += nwaves) {
-        const uint32_t s = tile * 16u + s16;
-        const half8_t x  = xn;
-        const float d[3] = {dn[0], dn[1], dn[2]};
-        if (tile + nwaves < tiles) fetch(tile + nwaves);
-        const floatx4 o  = density_mlp(fd, x);
-        const floatx4 c  = color_mlp(fc, color_input(o, d, grp));
-        const float v = field_channel(o, c, grp, s16);
-        if (s < n) reinterpret_cast<float*>(out)[4ull * s + grp] = v;
+    for (uint32_t gi = blockIdx.x * kBlockWaves + wv; gi < groups; gi += nwaves) {
+        const uint32_t base = gi * kGroupSamples;
+        half8_t x[4];
+#pragma unroll
+        for (uint32_t t = 0; t < 4u; ++t) {
+            const uint32_t q = min(base + 16u * t + s16, n - 1u);
+            x[t]             = *reinterpret_cast<const half8_t*>(features + (uint64_t)q * 32u + 8u * grp);
+        }
+        const uint32_t ql = min(base + lane, n - 1u);
+        const float d[3]  = {dirs[3ull * ql], dirs[3ull * ql + 1u], dirs[3ull * ql + 2u]};
+        float sh[16];
+        sh16(d, sh);
+#pragma unroll
+        for (uint32_t j = 0; j < 4u; ++j)
+            shl[wv][lane][j] = half4_t{to_half_rne(sh[4u * j]), to_half_rne(sh[4u * j + 1u]), to_half_rne(sh[4u * j + 2u]), to_half_rne(sh[4u * j + 3u])};
+        __builtin_amdgcn_wave_barrier();  // LDS traffic of one wave completes in order
+        float v[4];
+#pragma unroll
+        for (uint32_t t = 0; t < 4u; ++t) {
+            const floatx4 o = density_mlp(fd, x[t]);
+            const floatx4 c = color_mlp(fc, color_input(o, shl[wv][16u * t + s16][grp], grp));
+            v[t]            = field_channel(o, c, grp);
+        }
+#pragma unroll
+        for (uint32_t t = 0; t < 4u; ++t) {
+            const uint32_t s = base + 16u * t + s16;
+            if (s < n) reinterpret_cast<float*>(out)[4ull * s + grp] = v[t];
+        }
+        __builtin_amdgcn_wave_barrier();
     }
 }
 
@@ -332,7 +319,11 @@ NERF_API NerfStatus nerf_ext_field_mlp(const uint16_t* density_params, const uin
     if (n == 0u) return NERF_STATUS_OK;
     NERF_CHECK_ARG(density_params && color_params && features && directions && out, "nerf_ext_field_mlp: null pointer");
     NERF_CHECK_ARG(((uintptr_t)features & 15u) == 0u, "nerf_ext_field_mlp: features must be 16-byte aligned");
-    k_field_mlp<<<persistent_blocks(n, 8u), kBlockThreads, 0, (hipStream_t)stream>>>((const half_t*)density_params, (const half_t*)color_params, (const half_t*)features, directions, n, reinterpret_cast<float4*>(out));
+    // Three workgroups per CU: what the register budget keeps resident, so
+    // every workgroup stages the weights once and stays.
+    const uint32_t groups = (n + kGroupSamples - 1u) / kGroupSamples;
+    const uint32_t blocks = min((groups + kBlockWaves - 1u) / kBlockWaves, device_cu_count() * 3u);
+    k_field_mlp<<<blocks, kBlockThreads, 0, (hipStream_t)stream>>>((const half_t*)density_params, (const half_t*)color_params, (const half_t*)features, directions, n, reinterpret_cast<float4*>(out));
     NERF_LAUNCH_CHECK("k_field_mlp");
     return NERF_STATUS_OK;
 }

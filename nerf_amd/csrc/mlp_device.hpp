@@ -57,30 +57,96 @@ struct ColorFrags {
     half8_t w3[2];  // 16 x 64
 };
 
+// Fragments of layers whose k-map is Identity or Hidden are contiguous runs
+// of the weight row (8 halves, or two runs of 4), so they are read from LDS
+// as one 16-byte or two 8-byte loads.  P must be 16-byte aligned.
+__device__ __forceinline__ half8_t frag_identity(const half_t* W, uint32_t n_in, uint32_t b, uint32_t t, uint32_t lane) {
+    const uint32_t i = lane & 15u, g = lane >> 4;
+    return *reinterpret_cast<const half8_t*>(W + (16u * b + i) * n_in + 32u * t + 8u * g);
+}
+__device__ __forceinline__ half8_t frag_hidden(const half_t* row, uint32_t g) {
+    const half4_t lo = *reinterpret_cast<const half4_t*>(row + 4u * g);
+    const half4_t hi = *reinterpret_cast<const half4_t*>(row + 16u + 4u * g);
+    return half8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
 __device__ __forceinline__ void load_density(const half_t* P, DensityFrags& f, uint32_t lane) {
+    const uint32_t i = lane & 15u, g = lane >> 4;
 #pragma unroll
-    for (uint32_t b = 0; b < 4u; ++b) f.w1[b] = load_a(P, 32u, b, 0u, KMap::Identity, lane);
+    for (uint32_t b = 0; b < 4u; ++b) f.w1[b] = frag_identity(P, 32u, b, 0u, lane);
 #pragma unroll
-    for (uint32_t t = 0; t < 2u; ++t) f.w2[t] = load_a(P + 2048, 64u, 0u, t, KMap::Hidden, lane);
+    for (uint32_t t = 0; t < 2u; ++t) f.w2[t] = frag_hidden(P + 2048 + i * 64u + 32u * t, g);
 }
 
 __device__ __forceinline__ void load_color(const half_t* P, ColorFrags& f, uint32_t lane) {
+    const uint32_t i = lane & 15u, g = lane >> 4;
 #pragma unroll
     for (uint32_t b = 0; b < 4u; ++b) f.w1[b] = load_a(P, 32u, b, 0u, KMap::ColorIn, lane);
 #pragma unroll
     for (uint32_t b = 0; b < 4u; ++b)
 #pragma unroll
-        for (uint32_t t = 0; t < 2u; ++t) f.w2[2u * b + t] = load_a(P + 2048, 64u, b, t, KMap::Hidden, lane);
+        for (uint32_t t = 0; t < 2u; ++t) f.w2[2u * b + t] = frag_hidden(P + 2048 + (16u * b + i) * 64u + 32u * t, g);
     // Colour output: MFMA row 4c (c = 1..3) computes output c - 1 and every
     // other row is zero, so lane group c holds colour c - 1 in element 0 (and
     // lane group 0 takes sigma from the density output, row 0).
-    const uint32_t i = lane & 15u, g = lane >> 4;
-    const bool used  = (i & 3u) == 0u && i != 0u;
+    const bool used   = (i & 3u) == 0u && i != 0u;
     const half_t* row = P + 2048 + 4096 + (used ? (i / 4u - 1u) : 0u) * 64u;
+    const half8_t z   = {};
 #pragma unroll
-    for (uint32_t t = 0; t < 2u; ++t)
+    for (uint32_t t = 0; t < 2u; ++t) {
+        const half8_t v = frag_hidden(row + 32u * t, g);
+        f.w3[t]         = used ? v : z;
+    }
+}
+
+// Copies the density (3072) and colour (7168) fp16 parameters into LDS,
+// colour after density, as 1,280 16-byte chunks; every thread issues all of
+// its loads before its first LDS store, so the copy costs about one memory
+// latency instead of one per element.  Element copies when a source is not
+// 16-byte aligned.  The caller synchronises the workgroup afterwards.
+template <uint32_t kThreads>
+__device__ __forceinline__ void stage_weights(half_t* lds, const half_t* __restrict__ dp, const half_t* __restrict__ cp) {
+    constexpr uint32_t kD = NERF_EXT_DENSITY_PARAMS / 8u, kN = kD + NERF_EXT_COLOR_PARAMS / 8u;
+    constexpr uint32_t kPer = (kN + kThreads - 1u) / kThreads;
+    if (((reinterpret_cast<uintptr_t>(dp) | reinterpret_cast<uintptr_t>(cp)) & 15u) == 0u) {
+        const uint4* d4 = reinterpret_cast<const uint4*>(dp);
+        const uint4* c4 = reinterpret_cast<const uint4*>(cp);
+        uint4 r[kPer];
 #pragma unroll
-        for (uint32_t e = 0; e < 8u; ++e) f.w3[t][e] = used ? row[logical_k(KMap::Hidden, t, g, e)] : (half_t)0.0f;
+        for (uint32_t k = 0; k < kPer; ++k) {
+            const uint32_t c = threadIdx.x + kThreads * k;
+            if (c < kN) r[k] = c < kD ? d4[c] : c4[c - kD];
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < kPer; ++k) {
+            const uint32_t c = threadIdx.x + kThreads * k;
+            if (c < kN) reinterpret_cast<uint4*>(lds)[c] = r[k];
+        }
+    } else {
+        for (uint32_t i = threadIdx.x; i < NERF_EXT_DENSITY_PARAMS; i += kThreads) lds[i] = dp[i];
+        for (uint32_t i = threadIdx.x; i < NERF_EXT_COLOR_PARAMS; i += kThreads) lds[NERF_EXT_DENSITY_PARAMS + i] = cp[i];
+    }
+}
+
+// The density parameters alone (3072 halves, 384 chunks).
+template <uint32_t kThreads>
+__device__ __forceinline__ void stage_density(half_t* lds, const half_t* __restrict__ dp) {
+    constexpr uint32_t kN = NERF_EXT_DENSITY_PARAMS / 8u, kPer = (kN + kThreads - 1u) / kThreads;
+    if ((reinterpret_cast<uintptr_t>(dp) & 15u) == 0u) {
+        uint4 r[kPer];
+#pragma unroll
+        for (uint32_t k = 0; k < kPer; ++k) {
+            const uint32_t c = threadIdx.x + kThreads * k;
+            if (c < kN) r[k] = reinterpret_cast<const uint4*>(dp)[c];
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < kPer; ++k) {
+            const uint32_t c = threadIdx.x + kThreads * k;
+            if (c < kN) reinterpret_cast<uint4*>(lds)[c] = r[k];
+        }
+    } else {
+        for (uint32_t i = threadIdx.x; i < NERF_EXT_DENSITY_PARAMS; i += kThreads) lds[i] = dp[i];
+    }
 }
 
 // ReLU in fp16 after the conversion (packed convert, packed max): the same
@@ -162,11 +228,11 @@ __device__ __forceinline__ float select_bits(bool c, float a, float b) {
     return __uint_as_float((__float_as_uint(a) & m) | (__float_as_uint(b) & ~m));
 }
 
-__device__ __forceinline__ void sh4_quad(const float d[3], uint32_t grp, float out[4]) {
+// All 16 coefficients of a unit direction.
+__device__ __forceinline__ void sh16(const float d[3], float s[16]) {
     const float x = d[0], y = d[1], z = d[2];
     const float xy = x * y, yz = y * z, xz = x * z;
     const float x2 = x * x, y2 = y * y, z2 = z * z;
-    float s[16];
     s[0]  = 0.28209479177387814f;
     s[1]  = -0.48860251190291987f * y;
     s[2]  = 0.48860251190291987f * z;
@@ -183,6 +249,12 @@ __device__ __forceinline__ void sh4_quad(const float d[3], uint32_t grp, float o
     s[13] = 0.45704579946446572f * x * (1.0f - 5.0f * z2);
     s[14] = 1.4453057213202769f * z * (x2 - y2);
     s[15] = 0.59004358992664352f * x * (3.0f * y2 - x2);
+}
+
+// Coefficients 4g..4g+3 (lane group g) of a unit direction.
+__device__ __forceinline__ void sh4_quad(const float d[3], uint32_t grp, float out[4]) {
+    float s[16];
+    sh16(d, s);
     // Lane group g takes s[4g .. 4g + 3]: bitwise selects, so the four groups
     // of a wave never take divergent branches.
 #pragma unroll
@@ -191,6 +263,32 @@ __device__ __forceinline__ void sh4_quad(const float d[3], uint32_t grp, float o
         const float hi = select_bits((grp & 1u) != 0u, s[12u + e], s[8u + e]);
         out[e]         = select_bits((grp & 2u) != 0u, hi, lo);
     }
+}
+
+// Output activation spread over the wave: lane (g, s) holds channel g of
+// sample s in element 0 (sigma from the density output o, colour g - 1 from
+// the row-permuted colour output c) and applies its activation (g = 0: exp,
+// else sigmoid 1 / (1 + exp(-c)) with the hardware reciprocal, 1 ulp), so
+// each lane evaluates one exponential and one reciprocal; bit selects keep
+// the wave convergent.
+__device__ __forceinline__ float field_channel(const floatx4 o, const floatx4 c, uint32_t grp) {
+    const bool sigma = grp == 0u;
+    const float e    = __expf(select_bits(sigma, o[0], -c[0]));
+    return select_bits(sigma, e, __builtin_amdgcn_rcpf(1.0f + e));
+}
+
+// Colour input of lane group grp from density outputs 4g..4g+3 and the four
+// fp16 SH coefficients 4g..4g+3; the slot of density output 0 (sigma) carries
+// a zero weight and a zero value.
+__device__ __forceinline__ half8_t color_input(const floatx4 o, const half4_t sh, uint32_t grp) {
+    half8_t xc;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        xc[e]     = (half_t)o[e];
+        xc[4 + e] = sh[e];
+    }
+    if (grp == 0u) xc[0] = (half_t)0.0f;
+    return xc;
 }
 
 }  // namespace mlp

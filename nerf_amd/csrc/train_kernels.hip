@@ -120,10 +120,10 @@ __global__ __launch_bounds__(256) void k_occ_decay(TrainParams P, const TrainDev
 // rotating window of cells_per_update cells (:1575-1627).
 template <typename TableT>
 __global__ __launch_bounds__(kThreads) void k_occ_eval(TrainParams P, GridParams g, const TableT* __restrict__ table, const half_t* __restrict__ dparams, const TrainDevState* S, float* density) {
-    __shared__ half_t sp[NERF_EXT_DENSITY_PARAMS];
-    for (uint32_t i = threadIdx.x; i < NERF_EXT_DENSITY_PARAMS; i += blockDim.x) sp[i] = dparams[i];
-    __syncthreads();
     if (S->occ_mode != kOccRefresh) return;  // uniform across the grid
+    __shared__ __align__(16) half_t sp[NERF_EXT_DENSITY_PARAMS];
+    stage_density<kThreads>(sp, dparams);
+    __syncthreads();
     const uint32_t lane = threadIdx.x & 63u, grp = lane >> 4, s16 = lane & 15u;
     DensityFrags f;
     load_density(sp, f, lane);
@@ -757,8 +757,7 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dx(TrainParams P, const TrainD
     half8_t* F  = reinterpret_cast<half8_t*>(dyn);
     half_t* ops = dyn + kDxFragBytes / 2u;
     // Raw weights into the operand area, then every fragment built once.
-    for (uint32_t i = threadIdx.x; i < NERF_EXT_DENSITY_PARAMS; i += blockDim.x) ops[i] = dparams[i];
-    for (uint32_t i = threadIdx.x; i < NERF_EXT_COLOR_PARAMS; i += blockDim.x) ops[NERF_EXT_DENSITY_PARAMS + i] = cparams[i];
+    stage_weights<kThreads>(ops, dparams, cparams);
     __syncthreads();
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u, grp = lane >> 4, s16 = lane & 15u;
     for (uint32_t f = wave; f < kFrags; f += kWaves) F[64u * f + lane] = build_frag(f, ops, ops + NERF_EXT_DENSITY_PARAMS, lane);
