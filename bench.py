@@ -125,7 +125,7 @@ def kernel_rooflines(reps_small: int = 200):
         feats = DeviceArray((n, 32), np.float32)
         ms = timed(lambda: L.call("nerf_ext_encode_forward", C.byref(desc), table.ptr, pos.ptr, n, feats.ptr, L.NERF_EXT_F32, st.handle), reps)
         gbs = n * ENCODE_BYTES_PER_POINT / (ms / 1e3) / 1e9
-        out[label] = {"kernel": "k_encode_split (nerf_ext_encode_forward, level pair per XCD)", "points": n, "table": "16 x 2^16 x 2 fp32", "ms": round(ms, 5), "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+        out[label] = {"kernel": "k_encode_split (nerf_ext_encode_forward, four levels per XCD, one point per thread)", "points": n, "table": "16 x 2^16 x 2 fp32", "ms": round(ms, 5), "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                       "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_point": ENCODE_BYTES_PER_POINT, "reps": reps}
     n = 1 << 22
     rng = np.random.default_rng(0)

@@ -86,11 +86,31 @@ __global__ __launch_bounds__(256) void k_encode_tile(GridParams g, const TableT*
     for (uint32_t i = threadIdx.x; i < count * width; i += blockDim.x) o[i] = tile[i];
 }
 
-// One level with the x-neighbour corners of each (y, z) edge fetched as one
-// 16-byte load when they are the two entries of an aligned pair (index i and
-// i ^ 1: always for an even x on a hashed level, x's prime being 1), else as
-// two 8-byte loads.  Same entries, same weights, same summation order as
-// encode_level.
+// One level with the x-neighbour corners of each (y, z) edge (corners 2e and
+// 2e + 1) fetched by as few loads as the index structure allows:
+//   * dense level: the two entries are adjacent (i1 = i0 + 1): one load of
+//     two entries at i0 (entry aligned, not necessarily pair aligned; the
+//     hardware serves unaligned dword loads);
+//   * hashed level: when x is even, i1 = i0 ^ 1 (x's prime is 1), one load
+//     of that aligned entry pair; otherwise two single-entry loads.
+// Same entries, weights and summation order as encode_level.
+template <typename TableT>
+__device__ __forceinline__ void load_entry_pair(const TableT* p, float q[4]) {
+    if constexpr (sizeof(TableT) == 4) {
+        float4 w;
+        __builtin_memcpy(&w, p, 16);
+        q[0] = w.x;
+        q[1] = w.y;
+        q[2] = w.z;
+        q[3] = w.w;
+    } else {
+        half4_t w;
+        __builtin_memcpy(&w, p, 8);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) q[k] = (float)w[k];
+    }
+}
+
 template <typename TableT>
 __device__ __forceinline__ void encode_level_xpair(const GridParams& g, const TableT* __restrict__ table, const float p[3], uint32_t level, uint32_t N, bool dense, float& a0, float& a1) {
     const LevelCell c  = level_cell(p, N);
@@ -100,18 +120,16 @@ __device__ __forceinline__ void encode_level_xpair(const GridParams& g, const Ta
     for (uint32_t e = 0; e < 4u; ++e) {  // (y, z) edge e: corners 2e (x) and 2e + 1 (x + 1)
         const uint32_t i0 = corner_index(c, 2u * e, N, dense, g.table_size - 1u);
         const uint32_t i1 = corner_index(c, 2u * e + 1u, N, dense, g.table_size - 1u);
-        if (i1 == (i0 ^ 1u)) {
-            const uint32_t lo = i0 & ~1u;
-            float q[4];
-            if constexpr (sizeof(TableT) == 4) {
-                const float4 w = *reinterpret_cast<const float4*>(base + 2u * lo);
-                q[0] = w.x; q[1] = w.y; q[2] = w.z; q[3] = w.w;
-            } else {
-                const half4_t w = *reinterpret_cast<const half4_t*>(base + 2u * lo);
-#pragma unroll
-                for (int k = 0; k < 4; ++k) q[k] = (float)w[k];
-            }
-            const bool odd = (i0 & 1u) != 0u;
+        float q[4];
+        if (dense) {
+            load_entry_pair(base + 2u * i0, q);
+            v0[2u * e]      = q[0];
+            v1[2u * e]      = q[1];
+            v0[2u * e + 1u] = q[2];
+            v1[2u * e + 1u] = q[3];
+        } else if (i1 == (i0 ^ 1u)) {
+            load_entry_pair(base + 2u * (i0 & ~1u), q);
+            const bool odd  = (i0 & 1u) != 0u;
             v0[2u * e]      = odd ? q[2] : q[0];
             v1[2u * e]      = odd ? q[3] : q[1];
             v0[2u * e + 1u] = odd ? q[0] : q[2];
@@ -134,44 +152,47 @@ __device__ __forceinline__ void encode_level_xpair(const GridParams& g, const Ta
 }
 
 // XCD-aware encode.  Workgroup b runs on XCD b % 8 (the dispatcher's round
-// robin) and gathers only the levels of pair b % 8 (levels 2x, 2x + 1), so
-// each XCD's L2 holds two levels of the table rather than all of them; the
-// workgroups of one XCD stride over the points, one point per thread, and
-// each thread writes its 4 features as one vector store.  The placement is
-// a locality choice only: any workgroup-to-XCD mapping gives the same
-// result.  Positions arrive as one 12-byte load; the features leave as
-// scalar stores (measured faster than one 16-byte store per thread here).
-// With kPair (the table aligned to an entry pair) x-neighbour corners are
-// fetched in pairs.
-template <typename TableT, typename OutT, bool kPair>
+// robin) and gathers only kLevels levels of the table, so each XCD's L2
+// holds those levels rather than all of them:
+//   * kLevels = 2: XCD x takes levels 2x, 2x + 1 for every point;
+//   * kLevels = 4 (16 levels): XCD x takes levels 4 (x % 4) .. + 3 for the
+//     points of every other 256-point block (x / 4 picks which), so a point's
+//     position is read by 4 XCDs instead of 8 and each thread writes 32
+//     contiguous bytes of the output row instead of 16.
+// One point per thread (the launch gives every thread exactly one).  The
+// placement is a locality choice only: any workgroup-to-XCD mapping gives
+// the same result.  With kPair (the table aligned to an entry pair)
+// x-neighbour corners are fetched in pairs.
+template <typename TableT, typename OutT, bool kPair, uint32_t kLevels>
 __global__ __launch_bounds__(256) void k_encode_split(GridParams g, const TableT* __restrict__ table, const float* __restrict__ pos, uint32_t n, OutT* __restrict__ out) {
-    const uint32_t pair = blockIdx.x & 7u, slot = blockIdx.x >> 3, slots = gridDim.x >> 3;
-    const uint32_t l0 = 2u * pair, l1 = l0 + 1u;
+    constexpr uint32_t kParts = kLevels / 2u;  // XCDs sharing one level group
+    const uint32_t xcd = blockIdx.x & 7u, group = xcd % (8u / kParts), part = xcd / (8u / kParts);
+    const uint32_t slot = blockIdx.x >> 3, slots = gridDim.x >> 3;
+    const uint32_t l0 = kLevels * group;
     if (l0 >= g.n_levels) return;  // uniform per workgroup
-    const bool has1   = l1 < g.n_levels;
-    const uint32_t N0 = g.resolution[l0], N1 = has1 ? g.resolution[l1] : 1u;
-    const bool d0 = g.dense[l0] != 0u, d1 = has1 && g.dense[l1] != 0u;
     const uint32_t width = 2u * g.n_levels;
-    for (uint32_t i = slot * blockDim.x + threadIdx.x; i < n; i += slots * blockDim.x) {
+    for (uint32_t blk = slot * kParts + part; blk * 256u < n; blk += slots * kParts) {
+        const uint32_t i = blk * 256u + threadIdx.x;
+        if (i >= n) break;
         const float3 xp  = *reinterpret_cast<const float3*>(pos + 3ull * i);
         const float x[3] = {xp.x, xp.y, xp.z};
-        float a0, a1, b0 = 0.0f, b1 = 0.0f;
-        if constexpr (kPair) {
-            encode_level_xpair(g, table, x, l0, N0, d0, a0, a1);
-            if (has1) encode_level_xpair(g, table, x, l1, N1, d1, b0, b1);
-        } else {
-            encode_level(g, table, x, l0, N0, d0, a0, a1);
-            if (has1) encode_level(g, table, x, l1, N1, d1, b0, b1);
+        float f[2u * kLevels];
+#pragma unroll
+        for (uint32_t j = 0; j < kLevels; ++j) {
+            const uint32_t l = l0 + j;
+            f[2u * j] = f[2u * j + 1u] = 0.0f;
+            if (l < g.n_levels) {
+                if constexpr (kPair) encode_level_xpair(g, table, x, l, g.resolution[l], g.dense[l] != 0u, f[2u * j], f[2u * j + 1u]);
+                else encode_level(g, table, x, l, g.resolution[l], g.dense[l] != 0u, f[2u * j], f[2u * j + 1u]);
+            }
         }
         OutT* o = out + (uint64_t)i * width + 2u * l0;
-        if (has1) {
-            store_value(o, a0);
-            store_value(o + 1, a1);
-            store_value(o + 2, b0);
-            store_value(o + 3, b1);
-        } else {
-            store_value(o, a0);
-            store_value(o + 1, a1);
+#pragma unroll
+        for (uint32_t j = 0; j < kLevels; ++j) {
+            if (l0 + j < g.n_levels) {
+                store_value(o + 2u * j, f[2u * j]);
+                store_value(o + 2u * j + 1u, f[2u * j + 1u]);
+            }
         }
     }
 }
@@ -236,21 +257,27 @@ NERF_API NerfStatus nerf_ext_encode_forward(const NerfExtGridDesc* grid, const v
     NERF_CHECK_ARG(features_dtype == NERF_EXT_F32 || features_dtype == NERF_EXT_F16, "nerf_ext_encode_forward: bad features dtype");
     hipStream_t st = (hipStream_t)stream;
     // Level split when two levels of the table fit in half of one XCD's L2
-    // (4 MiB); otherwise every workgroup gathers all levels.
-    const uint64_t pair_bytes = 2ull * g.table_size * g.n_features * (g.table_dtype == NERF_EXT_F32 ? 4u : 2u);
-    const bool split          = pair_bytes <= (2ull << 20);
-    const uint32_t per_xcd    = (n + 255u) / 256u;
-    const uint32_t cap        = device_cu_count() / 8u * 8u;  // 8 workgroups per CU of one XCD
-    const dim3 grid_dim = split ? dim3(8u * (per_xcd < cap ? per_xcd : (cap > 0u ? cap : 1u))) : dim3((n + kEncPoints - 1u) / kEncPoints);
+    // (4 MiB), four levels per XCD when four fit (16-level grids only);
+    // otherwise every workgroup gathers all levels.
+    const uint64_t level_bytes = (uint64_t)g.table_size * g.n_features * (g.table_dtype == NERF_EXT_F32 ? 4u : 2u);
+    const bool split           = 2u * level_bytes <= (2ull << 20);
+    const bool quad            = split && g.n_levels == 16u && 4u * level_bytes <= (2ull << 20);
+    // One point per thread (no persistent grid): workgroups that finish early
+    // are replaced by new ones, so the CUs stay full to the end instead of
+    // draining through a long tail of the oldest-first wave scheduling.
+    const uint32_t blocks_256 = (n + 255u) / 256u;
+    const dim3 grid_dim = quad ? dim3(8u * ((blocks_256 + 1u) / 2u)) : split ? dim3(8u * blocks_256) : dim3((n + kEncPoints - 1u) / kEncPoints);
     // Pair loads need the table aligned to an entry pair: 16 bytes for fp32,
     // 8 for fp16 (device allocations are).
     const bool pair = ((uintptr_t)table & (g.table_dtype == NERF_EXT_F32 ? 15u : 7u)) == 0u;
 #define NERF_ENC(TT, OT)                                                                                                   \
     do {                                                                                                                   \
-        if (split && pair)                                                                                                 \
-            k_encode_split<TT, OT, true><<<grid_dim, 256, 0, st>>>(g, (const TT*)table, positions, n, (OT*)features);      \
+        if (quad && pair)                                                                                                  \
+            k_encode_split<TT, OT, true, 4u><<<grid_dim, 256, 0, st>>>(g, (const TT*)table, positions, n, (OT*)features);  \
+        else if (split && pair)                                                                                            \
+            k_encode_split<TT, OT, true, 2u><<<grid_dim, 256, 0, st>>>(g, (const TT*)table, positions, n, (OT*)features);  \
         else if (split)                                                                                                    \
-            k_encode_split<TT, OT, false><<<grid_dim, 256, 0, st>>>(g, (const TT*)table, positions, n, (OT*)features);     \
+            k_encode_split<TT, OT, false, 2u><<<grid_dim, 256, 0, st>>>(g, (const TT*)table, positions, n, (OT*)features); \
         else                                                                                                               \
             k_encode_tile<TT, OT><<<grid_dim, 256, 0, st>>>(g, (const TT*)table, positions, n, (OT*)features);             \
     } while (0)

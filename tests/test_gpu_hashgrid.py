@@ -42,9 +42,22 @@ def test_indices_bit_exact(log2_t, finest):
     assert np.array_equal(d_w.numpy().view(np.uint32), w.view(np.uint32))
 
 
-@pytest.mark.parametrize("table_dtype,out_dtype,log2_t", [(L.NERF_EXT_F32, np.float32, 16), (L.NERF_EXT_F16, np.float32, 19), (L.NERF_EXT_F16, np.float16, 19)])
-def test_encode_forward(table_dtype, out_dtype, log2_t):
-    n = 1 << 16
+# Launch shapes covered: four levels per XCD (fp32 T = 2^16, fp16 T = 2^17),
+# two levels per XCD (fp32 T = 2^17), all levels per workgroup (fp16
+# T = 2^19); point counts that are and are not multiples of the 256-point
+# blocks.
+@pytest.mark.parametrize(
+    "table_dtype,out_dtype,log2_t,n",
+    [
+        (L.NERF_EXT_F32, np.float32, 16, 1 << 16),
+        (L.NERF_EXT_F32, np.float32, 16, 1000),
+        (L.NERF_EXT_F16, np.float16, 17, 777),
+        (L.NERF_EXT_F32, np.float32, 17, 3001),
+        (L.NERF_EXT_F16, np.float32, 19, 1 << 16),
+        (L.NERF_EXT_F16, np.float16, 19, 1 << 16),
+    ],
+)
+def test_encode_forward(table_dtype, out_dtype, log2_t, n):
     announce(f"encode forward n={n} table={table_dtype} out={np.dtype(out_dtype).name} log2_t={log2_t}")
     desc = ext.grid_desc(log2_t, table_dtype)
     table = ext.init_table(desc, seed=3, value_range=1.0)
