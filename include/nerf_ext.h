@@ -154,16 +154,32 @@ NERF_API NerfStatus nerf_ext_scene_gaussians(const NerfExtSceneDesc* desc, NerfE
 /* density(p) = sum_g A_g exp(-|p - c_g|^2 / (2 sigma_g^2)), host/device bit-identical. */
 NERF_API NerfStatus nerf_ext_scene_density(const NerfExtGaussian* gaussians, uint32_t count, const float* positions, uint32_t n, float* out, void* stream);
 
+/* Occupancy grid (reference bitfield backend-cuda.cu:338-351) over one box
+ * or over nested cascades for unbounded scenes.  Cascade 0 is the box
+ * [aabb_min, aabb_max]; cascade c > 0 is that box scaled by 2^c about its
+ * centre: centre = 0.5 (min + max), half = 0.5 (max - min), bounds
+ * centre -/+ half * 2^c (fp32).  A point belongs to the first cascade c whose
+ * box holds it (r = (p - lo_c) / (hi_c - lo_c) in [0, 1) on every axis) and
+ * to its cell min(res - 1, floor(r * res)) there; points outside every
+ * cascade are unoccupied.  Rays are clipped to the outermost box.  Cascade c
+ * occupies words [c * W, (c + 1) * W), W = ceil(res^3 / 32), of the
+ * bitfield, cell x + y res + z res^2 at bit (index & 31) of word index >> 5. */
 typedef struct NerfExtOccupancy {
-    uint32_t* bitfield;  /* device, ceil(res^3 / 32) words, bit x + y res + z res^2, LSB first */
+    uint32_t* bitfield;  /* device, cascades * ceil(res^3 / 32) words */
     uint32_t resolution;
     float aabb_min[3];
     float aabb_max[3];
+    uint32_t cascades;   /* 0 or 1: one grid over the box; at most 8 */
 } NerfExtOccupancy;
 
 /* Bit set iff density(cell centre) > threshold (reference cell centres
- * backend-cuda.cu:1607-1608, strict threshold :1632). */
+ * backend-cuda.cu:1607-1608, strict threshold :1632), every cascade. */
 NERF_API NerfStatus nerf_ext_occupancy_from_scene(const NerfExtGaussian* gaussians, uint32_t count, float threshold, const NerfExtOccupancy* occupancy, void* stream);
+/* Uniform-density background shell: sets (ORs) the bit of every cell, in
+ * every cascade, whose centre q has r_inner^2 <= |q - centre|^2 <= r_outer^2
+ * (fp32, (dx dx + dy dy) + dz dz) — the occupancy of a shell whose density
+ * exceeds the threshold. */
+NERF_API NerfStatus nerf_ext_occupancy_mark_shell(const NerfExtOccupancy* occupancy, const float* centre3, float r_inner, float r_outer, void* stream);
 
 /* ----------------------------------------------------------- rays and march */
 typedef struct NerfExtCamera {

@@ -198,6 +198,7 @@ class NerfExtOccupancy(C.Structure):
         ("resolution", C.c_uint32),
         ("aabb_min", C.c_float * 3),
         ("aabb_max", C.c_float * 3),
+        ("cascades", C.c_uint32),
     ]
 
 
@@ -332,6 +333,7 @@ PROTOTYPES: dict[str, tuple] = {
     "nerf_ext_scene_gaussians": (_S, [C.POINTER(NerfExtSceneDesc), _P]),
     "nerf_ext_scene_density": (_S, [_P, _U32, _P, _U32, _P, _P]),
     "nerf_ext_occupancy_from_scene": (_S, [_P, _U32, _F, C.POINTER(NerfExtOccupancy), _P]),
+    "nerf_ext_occupancy_mark_shell": (_S, [C.POINTER(NerfExtOccupancy), _P, _F, _F, _P]),
     # cameras, march, render
     "nerf_ext_camera_orbit": (_S, [_U64, _U32, _F, _P, _U32, _U32, _F, C.POINTER(NerfExtCamera)]),
     "nerf_ext_march_count": (_S, [C.POINTER(NerfExtCamera), C.POINTER(NerfExtOccupancy), _U32, _P, _P]),

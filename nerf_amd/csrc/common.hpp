@@ -139,6 +139,69 @@ __device__ __forceinline__ void encode_level(const GridParams& g, const TableT* 
     }
 }
 
+// ------------------------------------------------------------- occupancy
+// Occupancy grid over one box or over nested cascades (NerfExtOccupancy in
+// include/nerf_ext.h): cascade 0 is [bmin, bmax], cascade c > 0 that box
+// scaled by 2^c about its centre; a point belongs to the first cascade whose
+// box holds it.  Scalar fp32 throughout, the same operations as the oracle,
+// so cells (and with them occupancy bits and sample counts) are bit-exact.
+struct OccView {
+    const uint32_t* bits;  // cascades * words words, or null: every cell occupied
+    uint32_t res;
+    uint32_t cascades;     // >= 1
+    uint32_t words;        // per cascade: ceil(res^3 / 32)
+    float bmin[3], bmax[3];  // cascade 0
+    float omin[3], omax[3];  // outermost cascade: the box rays are clipped to
+};
+
+constexpr uint32_t kCellOutside = 0xFFFFFFFFu;
+
+__device__ __forceinline__ void occ_box(const OccView& o, uint32_t c, float lo[3], float hi[3]) {
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+        if (c == 0u) {
+            lo[a] = o.bmin[a];
+            hi[a] = o.bmax[a];
+        } else {
+            const float centre = 0.5f * (o.bmin[a] + o.bmax[a]);
+            const float half   = 0.5f * (o.bmax[a] - o.bmin[a]);
+            const float s      = (float)(1u << c);
+            lo[a]              = centre - half * s;
+            hi[a]              = centre + half * s;
+        }
+    }
+}
+
+// Bit index of the cell holding p (cascade c: c * 32 * words + x + y res +
+// z res^2; cell rule of backend-cuda.cu:338-351 within the cascade's box),
+// or kCellOutside.
+__device__ __forceinline__ uint32_t occ_cell(const OccView& o, const float p[3]) {
+    for (uint32_t c = 0; c < o.cascades; ++c) {
+        float lo[3], hi[3];
+        occ_box(o, c, lo, hi);
+        const float rx = (p[0] - lo[0]) / (hi[0] - lo[0]);
+        const float ry = (p[1] - lo[1]) / (hi[1] - lo[1]);
+        const float rz = (p[2] - lo[2]) / (hi[2] - lo[2]);
+        if (rx < 0.0f || rx >= 1.0f || ry < 0.0f || ry >= 1.0f || rz < 0.0f || rz >= 1.0f) continue;
+        const uint32_t ix = min(o.res - 1u, (uint32_t)(rx * (float)o.res));
+        const uint32_t iy = min(o.res - 1u, (uint32_t)(ry * (float)o.res));
+        const uint32_t iz = min(o.res - 1u, (uint32_t)(rz * (float)o.res));
+        return c * 32u * o.words + ix + iy * o.res + iz * o.res * o.res;
+    }
+    return kCellOutside;
+}
+
+__device__ __forceinline__ bool occ_occupied(const OccView& o, const float p[3]) {
+    const uint32_t idx = occ_cell(o, p);
+    if (idx == kCellOutside) return false;
+    return !o.bits || ((o.bits[idx >> 5] >> (idx & 31u)) & 1u);
+}
+
+// Host: view of a NerfExtOccupancy (cascades 0 means 1), with the outermost
+// box computed by the same fp32 operations as occ_box; false if the box is
+// empty, the cascade count is above 8 or the bit indices overflow 32 bits.
+bool make_occ_view(const NerfExtOccupancy& o, OccView& v);
+
 // --------------------------------------------------------------- cameras
 struct Ray {
     float o[3];

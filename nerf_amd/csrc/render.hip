@@ -27,31 +27,6 @@ namespace nerf_hip {
 
 namespace {
 
-struct OccView {
-    const uint32_t* bits;
-    uint32_t res;
-    float bmin[3], bmax[3];
-};
-
-// Cell index of p in the grid over the box, or wave::kOutside
-// (backend-cuda.cu:338-351).
-__device__ __forceinline__ uint32_t occ_cell(const OccView& o, const float p[3]) {
-    const float sx = o.bmax[0] - o.bmin[0], sy = o.bmax[1] - o.bmin[1], sz = o.bmax[2] - o.bmin[2];
-    const float rx = (p[0] - o.bmin[0]) / sx, ry = (p[1] - o.bmin[1]) / sy, rz = (p[2] - o.bmin[2]) / sz;
-    if (rx < 0.0f || rx >= 1.0f || ry < 0.0f || ry >= 1.0f || rz < 0.0f || rz >= 1.0f) return wave::kOutside;
-    const uint32_t ix = min(o.res - 1u, (uint32_t)(rx * (float)o.res));
-    const uint32_t iy = min(o.res - 1u, (uint32_t)(ry * (float)o.res));
-    const uint32_t iz = min(o.res - 1u, (uint32_t)(rz * (float)o.res));
-    return ix + iy * o.res + iz * o.res * o.res;
-}
-
-// backend-cuda.cu:338-351 (a null bitfield marks every cell of the box occupied).
-__device__ __forceinline__ bool occupied(const OccView& o, const float p[3]) {
-    const uint32_t idx = occ_cell(o, p);
-    if (idx == wave::kOutside) return false;
-    return !o.bits || ((o.bits[idx >> 5] >> (idx & 31u)) & 1u);
-}
-
 __device__ __forceinline__ float cone_angle(const NerfExtCamera& c) {
     const float ifx = c.fx > 0.0f ? 1.0f / c.fx : 0.0f;
     const float ify = c.fy > 0.0f ? 1.0f / c.fy : 0.0f;
@@ -71,7 +46,7 @@ __device__ __forceinline__ uint32_t march_ray(const float4 ro, const float4 rd, 
         const float dt   = fminf(fmaxf(dt_min, t * cone), tf - t);
         const float tm   = t + 0.5f * dt;
         const float p[3] = {ro.x + tm * rd.x, ro.y + tm * rd.y, ro.z + tm * rd.z};
-        if (occupied(occ, p)) {
+        if (occ_occupied(occ, p)) {
             emit(count, tm, dt);
             ++count;
         }
@@ -89,7 +64,7 @@ __global__ __launch_bounds__(256) void k_march_count(const NerfExtCamera* __rest
     Ray r;
     float4 ro = make_float4(0.0f, 0.0f, 0.0f, 0.0f), rd = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     uint32_t count = 0u;
-    if (pixel_ray(cam, ray - view * pixels_per_view, occ.bmin, occ.bmax, r)) {
+    if (pixel_ray(cam, ray - view * pixels_per_view, occ.omin, occ.omax, r)) {
         ro    = make_float4(r.o[0], r.o[1], r.o[2], r.tn);
         rd    = make_float4(r.d[0], r.d[1], r.d[2], r.tf);
         count = march_ray(ro, rd, cone_angle(cam), max_steps, occ, [](uint32_t, float, float) {});
@@ -513,7 +488,8 @@ NERF_API NerfStatus nerf_ext_march_count(const NerfExtCamera* camera, const Nerf
     NERF_HIP_TRY(hipMallocAsync((void**)&dcam, sizeof(NerfExtCamera), st));
     NERF_HIP_TRY(hipMallocAsync((void**)&rays, sizeof(float4) * 2ull * n, st));
     NERF_HIP_TRY(hipMemcpyAsync(dcam, camera, sizeof(NerfExtCamera), hipMemcpyHostToDevice, st));
-    OccView occ{occupancy->bitfield, occupancy->resolution, {occupancy->aabb_min[0], occupancy->aabb_min[1], occupancy->aabb_min[2]}, {occupancy->aabb_max[0], occupancy->aabb_max[1], occupancy->aabb_max[2]}};
+    OccView occ;
+    NERF_CHECK_ARG(make_occ_view(*occupancy, occ), "nerf_ext_march_count: bad occupancy (empty box, more than 8 cascades or too many cells)");
     k_march_count<<<(n + 255u) / 256u, 256, 0, st>>>(dcam, n, n, occ, max_steps, rays, counts);
     NERF_LAUNCH_CHECK("k_march_count");
     NERF_HIP_TRY(hipFreeAsync(rays, st));
@@ -545,8 +521,8 @@ NERF_API NerfStatus nerf_ext_render(NerfExtRenderer* R, const NerfExtRenderDesc*
     NERF_HIP_TRY(R->total.reserve(1));
     NERF_HIP_TRY(hipMemcpyAsync(R->cams.ptr, d->cameras, sizeof(NerfExtCamera) * d->view_count, hipMemcpyHostToDevice, st));
 
-    const NerfExtOccupancy& o = *d->occupancy;
-    const OccView occ{o.bitfield, o.resolution, {o.aabb_min[0], o.aabb_min[1], o.aabb_min[2]}, {o.aabb_max[0], o.aabb_max[1], o.aabb_max[2]}};
+    OccView occ;
+    NERF_CHECK_ARG(make_occ_view(*d->occupancy, occ), "nerf_ext_render: bad occupancy (empty box, more than 8 cascades or too many cells)");
     const uint32_t ppv    = W * H;
     const uint32_t blocks = (n_rays + 255u) / 256u;
     const bool timed      = stats != nullptr;
@@ -577,9 +553,9 @@ NERF_API NerfStatus nerf_ext_render(NerfExtRenderer* R, const NerfExtRenderDesc*
     in.samples    = R->samples.ptr;
     in.sample_ray = R->sample_ray.ptr;
     in.rays       = R->rays.ptr;
-    for (int a = 0; a < 3; ++a) {
-        in.bmin[a] = o.aabb_min[a];
-        in.bmax[a] = o.aabb_max[a];
+    for (int a = 0; a < 3; ++a) {  // the field's box is the outermost cascade's
+        in.bmin[a] = occ.omin[a];
+        in.bmax[a] = occ.omax[a];
     }
     const FieldWeights w{(const half_t*)d->model->density_params, (const half_t*)d->model->color_params};
     const float3 bg = make_float3(d->background[0], d->background[1], d->background[2]);

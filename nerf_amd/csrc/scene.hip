@@ -54,31 +54,68 @@ __global__ __launch_bounds__(256) void k_scene_density(const NerfExtGaussian* __
     if (i < n) out[i] = acc;
 }
 
-__global__ __launch_bounds__(256) void k_occupancy_from_scene(const NerfExtGaussian* __restrict__ gaussians, uint32_t count, float threshold, uint32_t res, float3 bmin, float3 bmax, uint32_t* __restrict__ bits, uint64_t cells, uint64_t words) {
+// Cell c of cascade blockIdx.y: centre lo + (i + 0.5) * ((hi - lo) / res) per
+// axis.
+__device__ __forceinline__ void cell_centre(const OccView& o, uint32_t cascade, uint64_t cell, float p[3]) {
+    const uint64_t rr  = (uint64_t)o.res * o.res;
+    const uint32_t z   = (uint32_t)(cell / rr);
+    const uint32_t rem = (uint32_t)(cell - (uint64_t)z * rr);
+    const uint32_t y   = rem / o.res;
+    const uint32_t x   = rem - y * o.res;
+    float lo[3], hi[3];
+    occ_box(o, cascade, lo, hi);
+    const float sx = (hi[0] - lo[0]) / (float)o.res, sy = (hi[1] - lo[1]) / (float)o.res, sz = (hi[2] - lo[2]) / (float)o.res;
+    p[0] = lo[0] + ((float)x + 0.5f) * sx;
+    p[1] = lo[1] + ((float)y + 0.5f) * sy;
+    p[2] = lo[2] + ((float)z + 0.5f) * sz;
+}
+
+// Each wavefront ballots 64 consecutive cells of one cascade into two words
+// (kOr: ORed into the existing words, else stored); cascades start at word
+// boundaries, so a word never mixes cascades.
+template <bool kOr>
+__device__ __forceinline__ void store_ballot(const OccView& o, uint32_t* bits, uint32_t cascade, bool occ) {
+    const uint64_t ballot    = __ballot(occ);
+    const uint32_t lane      = threadIdx.x & 63u;
+    const uint64_t wave_base = ((uint64_t)blockIdx.x * 256u + (threadIdx.x & ~63u)) >> 5;  // first word of this wave in the cascade
+    uint32_t* w              = bits + (uint64_t)cascade * o.words;
+    if (lane == 0u) {
+#pragma unroll
+        for (uint32_t k = 0; k < 2u; ++k) {
+            if (wave_base + k >= o.words) break;
+            const uint32_t v = (uint32_t)(ballot >> (32u * k));
+            if constexpr (kOr) {
+                if (v) w[wave_base + k] |= v;
+            } else {
+                w[wave_base + k] = v;
+            }
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void k_occupancy_from_scene(const NerfExtGaussian* __restrict__ gaussians, uint32_t count, float threshold, OccView o, uint32_t* __restrict__ bits) {
     __shared__ GaussLds lds[kMaxSceneLds];
-    const uint64_t cell = (uint64_t)blockIdx.x * 256u + threadIdx.x;
-    const uint64_t rr   = (uint64_t)res * res;
-    const uint64_t cq   = cell < cells ? cell : cells - 1u;
-    const uint32_t z    = (uint32_t)(cq / rr);
-    const uint32_t rem  = (uint32_t)(cq - (uint64_t)z * rr);
-    const uint32_t y    = rem / res;
-    const uint32_t x    = rem - y * res;
-    const float sx = (bmax.x - bmin.x) / (float)res, sy = (bmax.y - bmin.y) / (float)res, sz = (bmax.z - bmin.z) / (float)res;
-    const float p[3] = {bmin.x + ((float)x + 0.5f) * sx, bmin.y + ((float)y + 0.5f) * sy, bmin.z + ((float)z + 0.5f) * sz};
-    float acc        = 0.0f;
+    const uint64_t cells = (uint64_t)o.res * o.res * o.res;
+    const uint64_t cell  = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+    float p[3];
+    cell_centre(o, blockIdx.y, cell < cells ? cell : cells - 1u, p);
+    float acc = 0.0f;
     for (uint32_t b = 0; b < count; b += kMaxSceneLds) {
         const uint32_t c = count - b < kMaxSceneLds ? count - b : kMaxSceneLds;
         stage_gaussians(lds, gaussians, b, c);
         acc = eval_density(lds, c, p, acc);
     }
-    const bool occ          = cell < cells && acc > threshold;
-    const uint64_t ballot   = __ballot(occ);
-    const uint32_t lane     = threadIdx.x & 63u;
-    const uint64_t wave_base = ((uint64_t)blockIdx.x * 256u + (threadIdx.x & ~63u)) >> 5;  // first word of this wave
-    if (lane == 0u) {
-        if (wave_base < words) bits[wave_base] = (uint32_t)ballot;
-        if (wave_base + 1u < words) bits[wave_base + 1u] = (uint32_t)(ballot >> 32);
-    }
+    store_ballot<false>(o, bits, blockIdx.y, cell < cells && acc > threshold);
+}
+
+__global__ __launch_bounds__(256) void k_occupancy_mark_shell(OccView o, float3 centre, float r2_inner, float r2_outer, uint32_t* __restrict__ bits) {
+    const uint64_t cells = (uint64_t)o.res * o.res * o.res;
+    const uint64_t cell  = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+    float p[3];
+    cell_centre(o, blockIdx.y, cell < cells ? cell : cells - 1u, p);
+    const float dx = p[0] - centre.x, dy = p[1] - centre.y, dz = p[2] - centre.z;
+    const float d2 = (dx * dx + dy * dy) + dz * dz;
+    store_ballot<true>(o, bits, blockIdx.y, cell < cells && d2 >= r2_inner && d2 <= r2_outer);
 }
 
 struct GaussColorLds {
@@ -134,6 +171,38 @@ __global__ __launch_bounds__(256) void k_scene_render(const NerfExtGaussian* __r
 }
 
 }  // namespace
+
+bool make_occ_view(const NerfExtOccupancy& o, OccView& v) {
+    const uint32_t casc = o.cascades == 0u ? 1u : o.cascades;
+    if (casc > 8u || o.resolution == 0u) return false;
+    for (int a = 0; a < 3; ++a)
+        if (!(o.aabb_max[a] > o.aabb_min[a])) return false;
+    const uint64_t cells = (uint64_t)o.resolution * o.resolution * o.resolution;
+    const uint64_t words = (cells + 31u) / 32u;
+    if ((uint64_t)casc * words * 32u >= 0xFFFFFFFFull) return false;
+    v.bits     = o.bitfield;
+    v.res      = o.resolution;
+    v.cascades = casc;
+    v.words    = (uint32_t)words;
+    for (int a = 0; a < 3; ++a) {
+        v.bmin[a] = o.aabb_min[a];
+        v.bmax[a] = o.aabb_max[a];
+        // The device's occ_box for the last cascade, on the host (same fp32
+        // operations; this file is built with -ffp-contract=off).
+        if (casc == 1u) {
+            v.omin[a] = v.bmin[a];
+            v.omax[a] = v.bmax[a];
+        } else {
+            const float centre = 0.5f * (v.bmin[a] + v.bmax[a]);
+            const float half   = 0.5f * (v.bmax[a] - v.bmin[a]);
+            const float s      = (float)(1u << (casc - 1u));
+            v.omin[a]          = centre - half * s;
+            v.omax[a]          = centre + half * s;
+        }
+    }
+    return true;
+}
+
 }  // namespace nerf_hip
 
 using namespace nerf_hip;
@@ -170,12 +239,25 @@ NERF_API NerfStatus nerf_ext_scene_density(const NerfExtGaussian* gaussians, uin
 NERF_API NerfStatus nerf_ext_occupancy_from_scene(const NerfExtGaussian* gaussians, uint32_t count, float threshold, const NerfExtOccupancy* occ, void* stream) {
     NERF_CHECK_ARG(occ && occ->bitfield && gaussians, "nerf_ext_occupancy_from_scene: null pointer");
     NERF_CHECK_ARG(occ->resolution >= 1u && occ->resolution <= 2048u, "nerf_ext_occupancy_from_scene: resolution must be 1..2048");
-    const uint64_t cells  = (uint64_t)occ->resolution * occ->resolution * occ->resolution;
-    const uint64_t words  = (cells + 31u) / 32u;
-    const uint64_t blocks = (cells + 255u) / 256u;
-    k_occupancy_from_scene<<<(uint32_t)blocks, 256, 0, (hipStream_t)stream>>>(gaussians, count, threshold, occ->resolution, make_float3(occ->aabb_min[0], occ->aabb_min[1], occ->aabb_min[2]),
-        make_float3(occ->aabb_max[0], occ->aabb_max[1], occ->aabb_max[2]), occ->bitfield, cells, words);
+    OccView v;
+    NERF_CHECK_ARG(make_occ_view(*occ, v), "nerf_ext_occupancy_from_scene: empty box, more than 8 cascades or too many cells");
+    const uint64_t cells = (uint64_t)v.res * v.res * v.res;
+    const dim3 grid((uint32_t)((cells + 255u) / 256u), v.cascades);
+    k_occupancy_from_scene<<<grid, 256, 0, (hipStream_t)stream>>>(gaussians, count, threshold, v, occ->bitfield);
     NERF_LAUNCH_CHECK("k_occupancy_from_scene");
+    return NERF_STATUS_OK;
+}
+
+NERF_API NerfStatus nerf_ext_occupancy_mark_shell(const NerfExtOccupancy* occ, const float* centre3, float r_inner, float r_outer, void* stream) {
+    NERF_CHECK_ARG(occ && occ->bitfield && centre3, "nerf_ext_occupancy_mark_shell: null pointer");
+    NERF_CHECK_ARG(occ->resolution >= 1u && occ->resolution <= 2048u, "nerf_ext_occupancy_mark_shell: resolution must be 1..2048");
+    NERF_CHECK_ARG(r_inner >= 0.0f && r_outer >= r_inner, "nerf_ext_occupancy_mark_shell: need 0 <= r_inner <= r_outer");
+    OccView v;
+    NERF_CHECK_ARG(make_occ_view(*occ, v), "nerf_ext_occupancy_mark_shell: empty box, more than 8 cascades or too many cells");
+    const uint64_t cells = (uint64_t)v.res * v.res * v.res;
+    const dim3 grid((uint32_t)((cells + 255u) / 256u), v.cascades);
+    k_occupancy_mark_shell<<<grid, 256, 0, (hipStream_t)stream>>>(v, make_float3(centre3[0], centre3[1], centre3[2]), r_inner * r_inner, r_outer * r_outer, occ->bitfield);
+    NERF_LAUNCH_CHECK("k_occupancy_mark_shell");
     return NERF_STATUS_OK;
 }
 

@@ -341,6 +341,7 @@ NERF_API NerfStatus nerf_ext_trainer_model(NerfExtTrainer* trainer, NerfExtModel
     if (occ) {
         occ->bitfield   = t.B.bits;
         occ->resolution = t.P.occ_res;
+        occ->cascades   = 1u;
         for (int a = 0; a < 3; ++a) {
             occ->aabb_min[a] = t.P.bmin[a];
             occ->aabb_max[a] = t.P.bmax[a];

@@ -82,16 +82,26 @@ def scene_gaussians(count: int, seed: int = 0, centre=(0.2, 0.8), sigma=(0.02, 0
     return np.frombuffer(out, dtype=np.float32).reshape(count, 8).copy()
 
 
-def occupancy_struct(bits: DeviceArray, res: int, aabb_min=(0.0, 0.0, 0.0), aabb_max=(1.0, 1.0, 1.0)) -> L.NerfExtOccupancy:
-    return L.NerfExtOccupancy(bits.ptr, res, (C.c_float * 3)(*aabb_min), (C.c_float * 3)(*aabb_max))
+def occupancy_struct(bits: DeviceArray, res: int, aabb_min=(0.0, 0.0, 0.0), aabb_max=(1.0, 1.0, 1.0), cascades: int = 1) -> L.NerfExtOccupancy:
+    return L.NerfExtOccupancy(bits.ptr, res, (C.c_float * 3)(*aabb_min), (C.c_float * 3)(*aabb_max), cascades)
 
 
-def occupancy_from_scene(gaussians: np.ndarray, res: int, threshold: float = 0.01, aabb_min=(0.0, 0.0, 0.0), aabb_max=(1.0, 1.0, 1.0)) -> DeviceArray:
-    words = (res ** 3 + 31) // 32
-    bits = DeviceArray.zeros((words,), np.uint32)
+def occupancy_words(res: int, cascades: int = 1) -> int:
+    """Bitfield length: one word-aligned grid of res^3 bits per cascade."""
+    return cascades * ((res ** 3 + 31) // 32)
+
+
+def occupancy_from_scene(gaussians: np.ndarray, res: int, threshold: float = 0.01, aabb_min=(0.0, 0.0, 0.0), aabb_max=(1.0, 1.0, 1.0), cascades: int = 1, shell=None) -> DeviceArray:
+    """Bitfield of the scene's density > threshold at cell centres, every
+    cascade; shell = (centre3, r_inner, r_outer) also marks a uniform shell."""
+    bits = DeviceArray.zeros((occupancy_words(res, cascades),), np.uint32)
     g = DeviceArray.from_numpy(np.ascontiguousarray(gaussians, np.float32))
-    occ = occupancy_struct(bits, res, aabb_min, aabb_max)
+    occ = occupancy_struct(bits, res, aabb_min, aabb_max, cascades)
     L.call("nerf_ext_occupancy_from_scene", g.ptr, gaussians.shape[0], threshold, C.byref(occ), None)
+    if shell is not None:
+        centre, r_in, r_out = shell
+        c3 = (C.c_float * 3)(*centre)
+        L.call("nerf_ext_occupancy_mark_shell", C.byref(occ), C.cast(c3, C.c_void_p), r_in, r_out, None)
     return bits
 
 

@@ -378,20 +378,127 @@ extern "C" void orc_scene_density(const float* gs, uint32_t count, const float* 
     for (uint32_t i = 0; i < n; ++i) out[i] = scene_density(gs, count, pos + 3ull * i);
 }
 
-// Bit (x + y*res + z*res^2) is set iff density(cell centre) > threshold, with
-// centre = min + (i + 0.5) * ((max - min) / res) per axis (backend-cuda.cu
-// :1607-1608 cell centres, :1632-1633 strict threshold, :347-350 packing).
-extern "C" void orc_occupancy_from_scene(const float* gs, uint32_t count, uint32_t res, const float* aabb, float threshold, uint32_t* bits) {
+// ---------------------------------------------------------------------------
+// Occupancy grid over one box or nested cascades: cascade 0 is the box,
+// cascade c > 0 the box scaled by 2^c about its centre (centre -/+ half * 2^c,
+// fp32); a point belongs to the first cascade whose box holds it, and to the
+// cell min(res - 1, floor(r * res)) of r = (p - lo) / (hi - lo) there
+// (backend-cuda.cu:338-351 within one box).  Cascade c occupies words
+// [c W, (c + 1) W), W = ceil(res^3 / 32).
+// ---------------------------------------------------------------------------
+struct OrcOcc {
+    const uint32_t* bits;
+    uint32_t res, cascades, words;
+    float bmin[3], bmax[3], omin[3], omax[3];
+};
+
+static void occ_box(const OrcOcc& o, uint32_t c, float* lo, float* hi) {
+    for (int a = 0; a < 3; ++a) {
+        if (c == 0u) {
+            lo[a] = o.bmin[a];
+            hi[a] = o.bmax[a];
+        } else {
+            const float centre = 0.5f * (o.bmin[a] + o.bmax[a]);
+            const float half   = 0.5f * (o.bmax[a] - o.bmin[a]);
+            const float sc     = (float)(1u << c);
+            lo[a]              = centre - half * sc;
+            hi[a]              = centre + half * sc;
+        }
+    }
+}
+
+static OrcOcc make_occ(const uint32_t* bits, uint32_t res, uint32_t cascades, const float* aabb) {
+    OrcOcc o;
+    o.bits     = bits;
+    o.res      = res;
+    o.cascades = cascades == 0u ? 1u : cascades;
+    o.words    = (uint32_t)(((uint64_t)res * res * res + 31u) / 32u);
+    for (int a = 0; a < 3; ++a) {
+        o.bmin[a] = aabb[a];
+        o.bmax[a] = aabb[3 + a];
+    }
+    occ_box(o, o.cascades - 1u, o.omin, o.omax);
+    return o;
+}
+
+static const uint32_t kOrcOutside = 0xFFFFFFFFu;
+
+static uint32_t occ_cell(const OrcOcc& o, const float* p) {
+    for (uint32_t c = 0; c < o.cascades; ++c) {
+        float lo[3], hi[3];
+        occ_box(o, c, lo, hi);
+        const float rx = (p[0] - lo[0]) / (hi[0] - lo[0]);
+        const float ry = (p[1] - lo[1]) / (hi[1] - lo[1]);
+        const float rz = (p[2] - lo[2]) / (hi[2] - lo[2]);
+        if (rx < 0.0f || rx >= 1.0f || ry < 0.0f || ry >= 1.0f || rz < 0.0f || rz >= 1.0f) continue;
+        const uint32_t ix = std::min(o.res - 1u, (uint32_t)(rx * (float)o.res));
+        const uint32_t iy = std::min(o.res - 1u, (uint32_t)(ry * (float)o.res));
+        const uint32_t iz = std::min(o.res - 1u, (uint32_t)(rz * (float)o.res));
+        return c * 32u * o.words + ix + iy * o.res + iz * o.res * o.res;
+    }
+    return kOrcOutside;
+}
+
+// A null bitfield marks every cell of every cascade occupied.
+static bool occ_occupied(const OrcOcc& o, const float* p) {
+    const uint32_t idx = occ_cell(o, p);
+    if (idx == kOrcOutside) return false;
+    return !o.bits || (o.bits[idx >> 5] & (1u << (idx & 31u))) != 0u;
+}
+
+// Cell index (as above) of each point; kOrcOutside outside every cascade.
+extern "C" void orc_occ_cell(uint32_t res, uint32_t cascades, const float* aabb, const float* pos, uint32_t n, uint32_t* out) {
+    const OrcOcc o = make_occ(nullptr, res, cascades, aabb);
+    for (uint32_t i = 0; i < n; ++i) out[i] = occ_cell(o, pos + 3ull * i);
+}
+
+// Centre of cell (x, y, z) of cascade c: lo + (i + 0.5) * ((hi - lo) / res).
+static void cell_centre(const OrcOcc& o, uint32_t c, uint64_t cell, float* p) {
+    const uint64_t rr = (uint64_t)o.res * o.res;
+    const uint32_t z  = (uint32_t)(cell / rr);
+    const uint32_t r  = (uint32_t)(cell - (uint64_t)z * rr);
+    const uint32_t y  = r / o.res;
+    const uint32_t x  = r - y * o.res;
+    float lo[3], hi[3];
+    occ_box(o, c, lo, hi);
+    const float step[3] = {(hi[0] - lo[0]) / (float)o.res, (hi[1] - lo[1]) / (float)o.res, (hi[2] - lo[2]) / (float)o.res};
+    p[0] = lo[0] + ((float)x + 0.5f) * step[0];
+    p[1] = lo[1] + ((float)y + 0.5f) * step[1];
+    p[2] = lo[2] + ((float)z + 0.5f) * step[2];
+}
+
+// Bit (x + y*res + z*res^2) of cascade c is set iff density(cell centre) >
+// threshold (backend-cuda.cu :1607-1608 cell centres, :1632-1633 strict
+// threshold, :347-350 packing).  bits: cascades * W words.
+extern "C" void orc_occupancy_from_scene(const float* gs, uint32_t count, uint32_t res, uint32_t cascades, const float* aabb, float threshold, uint32_t* bits) {
+    const OrcOcc o       = make_occ(nullptr, res, cascades, aabb);
     const uint64_t cells = (uint64_t)res * res * res;
-    memset(bits, 0, ((cells + 31) / 32) * 4);
-    const float step[3] = {(aabb[3] - aabb[0]) / (float)res, (aabb[4] - aabb[1]) / (float)res, (aabb[5] - aabb[2]) / (float)res};
-    for (uint64_t c = 0; c < cells; ++c) {
-        const uint32_t z = (uint32_t)(c / ((uint64_t)res * res));
-        const uint32_t r = (uint32_t)(c - (uint64_t)z * res * res);
-        const uint32_t y = r / res;
-        const uint32_t x = r - y * res;
-        const float p[3] = {aabb[0] + ((float)x + 0.5f) * step[0], aabb[1] + ((float)y + 0.5f) * step[1], aabb[2] + ((float)z + 0.5f) * step[2]};
-        if (scene_density(gs, count, p) > threshold) bits[c >> 5] |= 1u << (c & 31u);
+    memset(bits, 0, (uint64_t)o.cascades * o.words * 4u);
+    for (uint32_t c = 0; c < o.cascades; ++c) {
+        uint32_t* w = bits + (uint64_t)c * o.words;
+        for (uint64_t k = 0; k < cells; ++k) {
+            float p[3];
+            cell_centre(o, c, k, p);
+            if (scene_density(gs, count, p) > threshold) w[k >> 5] |= 1u << (k & 31u);
+        }
+    }
+}
+
+// Uniform background shell: ORs the bit of every cell (every cascade) whose
+// centre q has r_inner^2 <= |q - centre|^2 <= r_outer^2.
+extern "C" void orc_occupancy_mark_shell(uint32_t res, uint32_t cascades, const float* aabb, const float* centre, float r_inner, float r_outer, uint32_t* bits) {
+    const OrcOcc o       = make_occ(nullptr, res, cascades, aabb);
+    const uint64_t cells = (uint64_t)res * res * res;
+    const float r2i = r_inner * r_inner, r2o = r_outer * r_outer;
+    for (uint32_t c = 0; c < o.cascades; ++c) {
+        uint32_t* w = bits + (uint64_t)c * o.words;
+        for (uint64_t k = 0; k < cells; ++k) {
+            float p[3];
+            cell_centre(o, c, k, p);
+            const float dx = p[0] - centre[0], dy = p[1] - centre[1], dz = p[2] - centre[2];
+            const float d2 = (dx * dx + dy * dy) + dz * dz;
+            if (d2 >= r2i && d2 <= r2o) w[k >> 5] |= 1u << (k & 31u);
+        }
     }
 }
 
@@ -410,7 +517,7 @@ struct OrcRay {
 
 // backend-cuda.cu:373-390 (ray direction; 1/sqrtf instead of rsqrtf) and
 // :391-408 (slab test).
-static bool make_ray(const OrcCamera& c, float px, float py_flipped, const float* aabb, OrcRay& r) {
+static bool make_ray(const OrcCamera& c, float px, float py_flipped, const float* lo, const float* hi, OrcRay& r) {
     const float dcx = (px - c.cx) / c.fx;
     const float dcy = (py_flipped - c.cy) / c.fy;
     const float dcz = -1.0f;
@@ -427,8 +534,8 @@ static bool make_ray(const OrcCamera& c, float px, float py_flipped, const float
     float tmins[3], tmaxs[3];
     for (int a = 0; a < 3; ++a) {
         const float inv_d = fabsf(r.d[a]) > 1e-8f ? 1.0f / r.d[a] : (r.d[a] >= 0.0f ? 1e8f : -1e8f);
-        const float t0    = (aabb[a] - r.o[a]) * inv_d;
-        const float t1    = (aabb[3 + a] - r.o[a]) * inv_d;
+        const float t0    = (lo[a] - r.o[a]) * inv_d;
+        const float t1    = (hi[a] - r.o[a]) * inv_d;
         tmins[a]          = fminf(t0, t1);
         tmaxs[a]          = fmaxf(t0, t1);
     }
@@ -441,29 +548,16 @@ static bool make_ray(const OrcCamera& c, float px, float py_flipped, const float
     return true;
 }
 
-// backend-cuda.cu:338-351.  A null bitfield marks every cell of the box occupied.
-static inline bool occupied(const uint32_t* bits, uint32_t res, const float* aabb, const float* p) {
-    const float sx = aabb[3] - aabb[0], sy = aabb[4] - aabb[1], sz = aabb[5] - aabb[2];
-    const float rx = (p[0] - aabb[0]) / sx, ry = (p[1] - aabb[1]) / sy, rz = (p[2] - aabb[2]) / sz;
-    if (rx < 0.0f || rx >= 1.0f || ry < 0.0f || ry >= 1.0f || rz < 0.0f || rz >= 1.0f) return false;
-    if (!bits) return true;  // no bitfield: every cell of the box is occupied
-    const uint32_t ix  = std::min(res - 1u, (uint32_t)(rx * (float)res));
-    const uint32_t iy  = std::min(res - 1u, (uint32_t)(ry * (float)res));
-    const uint32_t iz  = std::min(res - 1u, (uint32_t)(rz * (float)res));
-    const uint32_t idx = ix + iy * res + iz * res * res;
-    return (bits[idx >> 5] & (1u << (idx & 31u))) != 0u;
-}
-
 // Inference ray of pixel (x, y): pixel centre, y flipped (backend-cuda.cu:561-563).
-static bool pixel_ray(const OrcCamera& c, uint32_t x, uint32_t y, const float* aabb, OrcRay& r) {
+static bool pixel_ray(const OrcCamera& c, uint32_t x, uint32_t y, const float* lo, const float* hi, OrcRay& r) {
     const float px = (float)x + 0.5f;
     const float py = (float)y + 0.5f;
-    return make_ray(c, px, (float)c.height - 1.0f - py, aabb, r);
+    return make_ray(c, px, (float)c.height - 1.0f - py, lo, hi, r);
 }
 
 // March of backend-cuda.cu:448-469; emit(t_mid, dt) for occupied steps.
 template <typename Emit>
-static uint32_t march(const OrcCamera& c, const OrcRay& r, const uint32_t* bits, uint32_t res, const float* aabb, uint32_t max_steps, Emit emit) {
+static uint32_t march(const OrcCamera& c, const OrcRay& r, const OrcOcc& occ, uint32_t max_steps, Emit emit) {
     const float t_range = r.tf - r.tn;
     if (!(t_range > 0.0f)) return 0u;
     const float dt_min = t_range / (float)max_steps;
@@ -476,7 +570,7 @@ static uint32_t march(const OrcCamera& c, const OrcRay& r, const uint32_t* bits,
         const float dt    = fminf(fmaxf(dt_min, t * cone), r.tf - t);
         const float tm    = t + 0.5f * dt;
         const float p[3]  = {r.o[0] + tm * r.d[0], r.o[1] + tm * r.d[1], r.o[2] + tm * r.d[2]};
-        if (occupied(bits, res, aabb, p)) {
+        if (occ_occupied(occ, p)) {
             emit(count, tm, dt);
             ++count;
         }
@@ -486,22 +580,25 @@ static uint32_t march(const OrcCamera& c, const OrcRay& r, const uint32_t* bits,
     return count;
 }
 
-// Per-ray occupied-sample counts for rays [ray_begin, ray_begin + n) of one view.
-extern "C" void orc_march_count(const OrcCamera* cam, const uint32_t* bits, uint32_t res, const float* aabb, uint32_t max_steps, uint32_t ray_begin, uint32_t n, uint32_t* counts) {
+// Per-ray occupied-sample counts for rays [ray_begin, ray_begin + n) of one
+// view; rays are clipped to the outermost cascade's box.
+extern "C" void orc_march_count(const OrcCamera* cam, const uint32_t* bits, uint32_t res, uint32_t cascades, const float* aabb, uint32_t max_steps, uint32_t ray_begin, uint32_t n, uint32_t* counts) {
+    const OrcOcc occ = make_occ(bits, res, cascades, aabb);
     for (uint32_t k = 0; k < n; ++k) {
         const uint32_t ray = ray_begin + k;
         OrcRay r;
         counts[k] = 0u;
-        if (!pixel_ray(*cam, ray % cam->width, ray / cam->width, aabb, r)) continue;
-        counts[k] = march(*cam, r, bits, res, aabb, max_steps, [](uint32_t, float, float) {});
+        if (!pixel_ray(*cam, ray % cam->width, ray / cam->width, occ.omin, occ.omax, r)) continue;
+        counts[k] = march(*cam, r, occ, max_steps, [](uint32_t, float, float) {});
     }
 }
 
 // Samples (t_mid, dt) of one ray, up to cap; returns the count.
-extern "C" uint32_t orc_march_ray(const OrcCamera* cam, const uint32_t* bits, uint32_t res, const float* aabb, uint32_t max_steps, uint32_t ray, float* t_dt, uint32_t cap) {
+extern "C" uint32_t orc_march_ray(const OrcCamera* cam, const uint32_t* bits, uint32_t res, uint32_t cascades, const float* aabb, uint32_t max_steps, uint32_t ray, float* t_dt, uint32_t cap) {
+    const OrcOcc occ = make_occ(bits, res, cascades, aabb);
     OrcRay r;
-    if (!pixel_ray(*cam, ray % cam->width, ray / cam->width, aabb, r)) return 0u;
-    return march(*cam, r, bits, res, aabb, max_steps, [&](uint32_t k, float tm, float dt) {
+    if (!pixel_ray(*cam, ray % cam->width, ray / cam->width, occ.omin, occ.omax, r)) return 0u;
+    return march(*cam, r, occ, max_steps, [&](uint32_t k, float tm, float dt) {
         if (k < cap) {
             t_dt[2 * k]     = tm;
             t_dt[2 * k + 1] = dt;
@@ -509,10 +606,11 @@ extern "C" uint32_t orc_march_ray(const OrcCamera* cam, const uint32_t* bits, ui
     });
 }
 
-// Ray origin/direction/t-range of one pixel ray; returns 0 if it misses.
+// Ray origin/direction/t-range of one pixel ray against a box; returns 0 if
+// it misses.
 extern "C" int orc_pixel_ray(const OrcCamera* cam, uint32_t ray, const float* aabb, float* out8) {
     OrcRay r;
-    if (!pixel_ray(*cam, ray % cam->width, ray / cam->width, aabb, r)) return 0;
+    if (!pixel_ray(*cam, ray % cam->width, ray / cam->width, aabb, aabb + 3, r)) return 0;
     for (int a = 0; a < 3; ++a) {
         out8[a]     = r.o[a];
         out8[3 + a] = r.d[a];
@@ -561,9 +659,12 @@ struct OrcModel {
     const uint16_t* color_params;
 };
 
-extern "C" void orc_render_rays(const OrcModel* model, const OrcCamera* cam, const uint32_t* bits, uint32_t res, const float* aabb, uint32_t max_steps, float t_stop, const float* bg, const uint32_t* rays, uint32_t n_rays, float* rgb_out, uint32_t* rgba8_out,
-    uint32_t* counts_out, uint32_t n_threads) {
+// The field sees positions normalised to the outermost cascade's box,
+// (w - lo) / (hi - lo) per axis (exact for the unit box).
+extern "C" void orc_render_rays(const OrcModel* model, const OrcCamera* cam, const uint32_t* bits, uint32_t res, uint32_t cascades, const float* aabb, uint32_t max_steps, float t_stop, const float* bg, const uint32_t* rays, uint32_t n_rays,
+    float* rgb_out, uint32_t* rgba8_out, uint32_t* counts_out, uint32_t n_threads) {
     if (n_threads == 0u) n_threads = 1u;
+    const OrcOcc occ = make_occ(bits, res, cascades, aabb);
     auto work = [&](uint32_t begin, uint32_t end) {
         std::vector<float> t_dt, sig, dts;
         for (uint32_t k = begin; k < end; ++k) {
@@ -571,8 +672,8 @@ extern "C" void orc_render_rays(const OrcModel* model, const OrcCamera* cam, con
             OrcRay r;
             uint32_t count = 0;
             t_dt.clear();
-            if (pixel_ray(*cam, ray % cam->width, ray / cam->width, aabb, r)) {
-                count = march(*cam, r, bits, res, aabb, max_steps, [&](uint32_t, float tm, float dt) {
+            if (pixel_ray(*cam, ray % cam->width, ray / cam->width, occ.omin, occ.omax, r)) {
+                count = march(*cam, r, occ, max_steps, [&](uint32_t, float tm, float dt) {
                     t_dt.push_back(tm);
                     t_dt.push_back(dt);
                 });
@@ -581,7 +682,9 @@ extern "C" void orc_render_rays(const OrcModel* model, const OrcCamera* cam, con
             for (uint32_t i = 0; i < count; ++i) {
                 const float tm   = t_dt[2 * i];
                 const float dt   = t_dt[2 * i + 1];
-                const float p[3] = {r.o[0] + tm * r.d[0], r.o[1] + tm * r.d[1], r.o[2] + tm * r.d[2]};
+                const float wp[3] = {r.o[0] + tm * r.d[0], r.o[1] + tm * r.d[1], r.o[2] + tm * r.d[2]};
+                float p[3];
+                for (int a = 0; a < 3; ++a) p[a] = (wp[a] - occ.omin[a]) / (occ.omax[a] - occ.omin[a]);
                 float s4[4];
                 field_point(model->grid, model->table, model->density_params, model->color_params, p, r.d, s4);
                 const float a = 1.0f - expf(-(s4[0] * fmaxf(dt, 0.0f)));
@@ -836,8 +939,8 @@ extern "C" void orc_train_rays(const OrcCamera* cam, const uint8_t* image, const
         OrcRay ray;
         uint32_t count = 0;
         offsets[r]     = off;
-        if (make_ray(*cam, px, (float)H - 1.0f - py, aabb, ray)) {
-            count = march(*cam, ray, bits, res, aabb, max_steps, [&](uint32_t k, float tm, float dt) {
+        if (make_ray(*cam, px, (float)H - 1.0f - py, aabb, aabb + 3, ray)) {
+            count = march(*cam, ray, make_occ(bits, res, 1u, aabb), max_steps, [&](uint32_t k, float tm, float dt) {
                 if (off + k < cap) {
                     t_dt[2 * (off + k)]     = tm;
                     t_dt[2 * (off + k) + 1] = dt;
@@ -887,7 +990,7 @@ extern "C" void orc_scene_render(const float* gs, uint32_t count, const OrcCamer
         for (uint32_t x = 0; x < W; ++x) {
             OrcRay r;
             float T = 1.0f, Cc[3] = {0.0f, 0.0f, 0.0f};
-            if (pixel_ray(*cam, x, y, aabb, r)) {
+            if (pixel_ray(*cam, x, y, aabb, aabb + 3, r)) {
                 const float dt = (r.tf - r.tn) / (float)steps;
                 for (uint32_t i = 0; i < steps && dt > 0.0f; ++i) {
                     const float t    = r.tn + ((float)i + 0.5f) * dt;

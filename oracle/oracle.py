@@ -73,9 +73,11 @@ _PROTOS = {
     "orc_det_expf": (_F, [_F]),
     "orc_det_expf_array": (None, [_P, _U64, _P]),
     "orc_scene_density": (None, [_P, _U32, _P, _U32, _P]),
-    "orc_occupancy_from_scene": (None, [_P, _U32, _U32, _P, _F, _P]),
-    "orc_march_count": (None, [C.POINTER(OrcCamera), _P, _U32, _P, _U32, _U32, _U32, _P]),
-    "orc_march_ray": (_U32, [C.POINTER(OrcCamera), _P, _U32, _P, _U32, _U32, _P, _U32]),
+    "orc_occupancy_from_scene": (None, [_P, _U32, _U32, _U32, _P, _F, _P]),
+    "orc_occupancy_mark_shell": (None, [_U32, _U32, _P, _P, _F, _F, _P]),
+    "orc_occ_cell": (None, [_U32, _U32, _P, _P, _U32, _P]),
+    "orc_march_count": (None, [C.POINTER(OrcCamera), _P, _U32, _U32, _P, _U32, _U32, _U32, _P]),
+    "orc_march_ray": (_U32, [C.POINTER(OrcCamera), _P, _U32, _U32, _P, _U32, _U32, _P, _U32]),
     "orc_pixel_ray": (C.c_int, [C.POINTER(OrcCamera), _U32, _P, _P]),
     "orc_composite_ray": (_U32, [_P, _P, _U32, _F, _P, _P, _P]),
     "orc_composite_backward_ray": (C.c_double, [_P, _P, _P, _U32, _P, _P, _F, _F, _P, _P, _P]),
@@ -87,7 +89,7 @@ _PROTOS = {
     "orc_train_camera": (_U32, [_U32, _U32]),
     "orc_field_mlp": (None, [_P, _P, _P, _P, _U32, _P]),
     "orc_scene_render": (None, [_P, _U32, C.POINTER(OrcCamera), _P, _U32, _P]),
-    "orc_render_rays": (None, [C.POINTER(OrcModel), C.POINTER(OrcCamera), _P, _U32, _P, _U32, _F, _P, _P, _U32, _P, _P, _P, _U32]),
+    "orc_render_rays": (None, [C.POINTER(OrcModel), C.POINTER(OrcCamera), _P, _U32, _U32, _P, _U32, _F, _P, _P, _U32, _P, _P, _P, _U32]),
 }
 
 _lib = None
@@ -222,12 +224,31 @@ def scene_density(gaussians: np.ndarray, pos: np.ndarray) -> np.ndarray:
     return out
 
 
-def occupancy_from_scene(gaussians: np.ndarray, res: int, aabb=(0, 0, 0, 1, 1, 1), threshold: float = 0.01) -> np.ndarray:
+def occupancy_words(res: int, cascades: int = 1) -> int:
+    return cascades * ((res ** 3 + 31) // 32)
+
+
+def occupancy_from_scene(gaussians: np.ndarray, res: int, aabb=(0, 0, 0, 1, 1, 1), threshold: float = 0.01, cascades: int = 1, shell=None) -> np.ndarray:
+    """Bits of density(cell centre) > threshold for every cascade; shell =
+    (centre3, r_inner, r_outer) also marks a uniform shell."""
     g = np.ascontiguousarray(gaussians, np.float32)
     box = np.array(aabb, np.float32)
-    bits = np.zeros((res ** 3 + 31) // 32, np.uint32)
-    lib().orc_occupancy_from_scene(_p(g), g.shape[0], res, _p(box), threshold, _p(bits))
+    bits = np.zeros(occupancy_words(res, cascades), np.uint32)
+    lib().orc_occupancy_from_scene(_p(g), g.shape[0], res, cascades, _p(box), threshold, _p(bits))
+    if shell is not None:
+        centre, r_in, r_out = shell
+        c3 = np.array(centre, np.float32)
+        lib().orc_occupancy_mark_shell(res, cascades, _p(box), _p(c3), r_in, r_out, _p(bits))
     return bits
+
+
+def occ_cell(res: int, cascades: int, aabb, pos: np.ndarray) -> np.ndarray:
+    """Bit index of each point's cell (0xFFFFFFFF outside every cascade)."""
+    box = np.array(aabb, np.float32)
+    p = np.ascontiguousarray(pos, np.float32)
+    out = np.empty(p.shape[0], np.uint32)
+    lib().orc_occ_cell(res, cascades, _p(box), _p(p), p.shape[0], _p(out))
+    return out
 
 
 def camera(c2w12, fx, fy, cx, cy, width, height) -> OrcCamera:
@@ -246,20 +267,20 @@ def camera_from_bytes(raw: bytes) -> OrcCamera:
     return cam
 
 
-def march_count(cam: OrcCamera, bits: np.ndarray | None, res: int, aabb, max_steps: int, ray_begin: int = 0, n: int | None = None) -> np.ndarray:
+def march_count(cam: OrcCamera, bits: np.ndarray | None, res: int, aabb, max_steps: int, ray_begin: int = 0, n: int | None = None, cascades: int = 1) -> np.ndarray:
     if n is None:
         n = cam.width * cam.height - ray_begin
     box = np.array(aabb, np.float32)
     out = np.empty(n, np.uint32)
-    lib().orc_march_count(C.byref(cam), _p(bits) if bits is not None else None, res, _p(box), max_steps, ray_begin, n, _p(out))
+    lib().orc_march_count(C.byref(cam), _p(bits) if bits is not None else None, res, cascades, _p(box), max_steps, ray_begin, n, _p(out))
     return out
 
 
-def march_ray(cam: OrcCamera, bits: np.ndarray | None, res: int, aabb, max_steps: int, ray: int) -> np.ndarray:
+def march_ray(cam: OrcCamera, bits: np.ndarray | None, res: int, aabb, max_steps: int, ray: int, cascades: int = 1) -> np.ndarray:
     box = np.array(aabb, np.float32)
     cap = max_steps
     buf = np.empty((cap, 2), np.float32)
-    k = lib().orc_march_ray(C.byref(cam), _p(bits) if bits is not None else None, res, _p(box), max_steps, ray, _p(buf), cap)
+    k = lib().orc_march_ray(C.byref(cam), _p(bits) if bits is not None else None, res, cascades, _p(box), max_steps, ray, _p(buf), cap)
     return buf[:k].copy()
 
 
@@ -281,7 +302,7 @@ def composite_ray(sigma_rgb: np.ndarray, dt: np.ndarray, t_stop: float = 1e-4, b
 
 
 def render_rays(grid: OrcGrid, table: np.ndarray, dparams_bits: np.ndarray, cparams_bits: np.ndarray, cam: OrcCamera, bits: np.ndarray | None, res: int, aabb, max_steps: int, rays: np.ndarray, t_stop: float = 1e-4, bg=(1.0, 1.0, 1.0),
-                threads: int = 1):
+                threads: int = 1, cascades: int = 1):
     model = OrcModel()
     model.grid = grid
     model.table = _p(table)
@@ -293,7 +314,7 @@ def render_rays(grid: OrcGrid, table: np.ndarray, dparams_bits: np.ndarray, cpar
     rgb = np.empty((rays.size, 3), np.float32)
     rgba = np.empty(rays.size, np.uint32)
     counts = np.empty(rays.size, np.uint32)
-    lib().orc_render_rays(C.byref(model), C.byref(cam), _p(bits) if bits is not None else None, res, _p(box), max_steps, t_stop, _p(b), _p(rays), rays.size, _p(rgb), _p(rgba), _p(counts), threads)
+    lib().orc_render_rays(C.byref(model), C.byref(cam), _p(bits) if bits is not None else None, res, cascades, _p(box), max_steps, t_stop, _p(b), _p(rays), rays.size, _p(rgb), _p(rgba), _p(counts), threads)
     return rgb, rgba, counts
 
 
