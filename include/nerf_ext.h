@@ -208,6 +208,12 @@ typedef struct NerfExtRenderDesc {
     float min_transmittance;        /* early stop threshold, e.g. 1e-4 */
     float background[3];            /* composited as C + T * background */
     void* stream;
+    uint64_t chunk_samples;         /* 0: 2^29.  Rays are marched, shaded and
+                                       composited in chunks of whole blocks of
+                                       1024 rays holding at most this many
+                                       samples (a block is never split), so
+                                       the sample buffers (32 B per sample)
+                                       hold one chunk */
 } NerfExtRenderDesc;
 
 typedef struct NerfExtRenderStats {
@@ -224,7 +230,8 @@ typedef struct NerfExtRenderStats {
 
 NERF_API NerfStatus nerf_ext_renderer_create(NerfExtRenderer** out);
 NERF_API NerfStatus nerf_ext_renderer_destroy(NerfExtRenderer* renderer);
-/* Renders view_count views into rgba8 [view][H][W] (device).  Optional device
+/* Renders view_count views into rgba8 [view][H][W] (device), max_steps at
+ * most 2^19.  Optional device
  * outputs: rgb_f32 [view][H][W][3] (unclamped composite) and counts
  * [view][H][W] (occupied samples per ray).  With stats != NULL the call
  * synchronises and times each stage with HIP events on desc->stream. */

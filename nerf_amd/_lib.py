@@ -224,6 +224,7 @@ class NerfExtRenderDesc(C.Structure):
         ("min_transmittance", C.c_float),
         ("background", C.c_float * 3),
         ("stream", C.c_void_p),
+        ("chunk_samples", C.c_uint64),
     ]
 
 

@@ -81,10 +81,10 @@ __global__ __launch_bounds__(256) void k_march_count(const NerfExtCamera* __rest
 // inside the ray's slice.
 constexpr uint32_t kMarchGroup = 8u;
 
-__global__ __launch_bounds__(256) void k_march_samples(const NerfExtCamera* __restrict__ cams, uint32_t pixels_per_view, uint32_t n_rays, OccView occ, uint32_t max_steps, const float4* __restrict__ rays, const uint32_t* __restrict__ counts,
-    const uint32_t* __restrict__ offsets, float2* __restrict__ samples, uint32_t* __restrict__ sample_ray) {
-    const uint32_t ray = (blockIdx.x * 256u + threadIdx.x) / kMarchGroup;
-    if (ray >= n_rays) return;
+__global__ __launch_bounds__(256) void k_march_samples(const NerfExtCamera* __restrict__ cams, uint32_t pixels_per_view, uint32_t ray0, uint32_t ray_end, OccView occ, uint32_t max_steps, const float4* __restrict__ rays,
+                                                      const uint32_t* __restrict__ counts, const uint32_t* __restrict__ offsets, float2* __restrict__ samples, uint32_t* __restrict__ sample_ray) {
+    const uint32_t ray = ray0 + (blockIdx.x * 256u + threadIdx.x) / kMarchGroup;
+    if (ray >= ray_end) return;
     const uint32_t count = counts[ray];
     if (count == 0u) return;
     const uint32_t view = ray / pixels_per_view;
@@ -124,10 +124,10 @@ __device__ __forceinline__ void write_pixel(uint32_t ray, float cr, float cg, fl
 
 // Rays without samples get the background; the others start the first
 // round's list (wave-aggregated appends) with T = 1, C = 0.
-__global__ __launch_bounds__(256) void k_round_init(uint32_t n_rays, const uint32_t* __restrict__ counts, float3 bg, uint32_t* __restrict__ rgba8, float* __restrict__ rgb_out, float4* __restrict__ state,
+__global__ __launch_bounds__(256) void k_round_init(uint32_t ray0, uint32_t ray_end, const uint32_t* __restrict__ counts, float3 bg, uint32_t* __restrict__ rgba8, float* __restrict__ rgb_out, float4* __restrict__ state,
                                                    uint32_t* __restrict__ list, uint32_t* __restrict__ n_active) {
-    const uint32_t ray = blockIdx.x * 256u + threadIdx.x;
-    const bool valid   = ray < n_rays;
+    const uint32_t ray = ray0 + blockIdx.x * 256u + threadIdx.x;
+    const bool valid   = ray < ray_end;
     const bool take    = valid && counts[ray] > 0u;
     const uint64_t m   = __ballot(take);
     const uint32_t lane = threadIdx.x & 63u;
@@ -351,6 +351,14 @@ __global__ __launch_bounds__(256) void k_scan_apply_direct(const uint32_t* __res
 
 uint64_t scan_tmp_words(uint32_t n) { return (n + kScanBlock - 1u) / kScanBlock + 2u; }
 
+// Sums of in[] over consecutive blocks of 1024 elements (the scan's first pass).
+hipError_t block_sums_u32(const uint32_t* in, uint32_t n, uint32_t* sums, hipStream_t stream) {
+    const uint32_t blocks = (n + kScanBlock - 1u) / kScanBlock;
+    if (blocks) k_scan_reduce<<<blocks, 256, 0, stream>>>(in, n, sums);
+    return hipGetLastError();
+}
+static_assert(kScanBlock == 1024u, "the renderer plans chunks in blocks of 1024 rays");
+
 hipError_t exclusive_scan_u32(const uint32_t* in, uint32_t* out, uint32_t n, uint32_t* tmp, unsigned long long* total, hipStream_t stream) {
     const uint32_t blocks = (n + kScanBlock - 1u) / kScanBlock;
     if (blocks == 0u) return hipMemsetAsync(total, 0, sizeof(unsigned long long), stream);
@@ -368,6 +376,9 @@ hipError_t exclusive_scan_u32(const uint32_t* in, uint32_t* out, uint32_t n, uin
 
 // ----------------------------------------------------------------- renderer
 constexpr uint32_t kFirstRound = 256u;  // samples per ray in the first round (a multiple of 64)
+constexpr uint32_t kScanBlockRays = 1024u;        // rays per block of the chunk plan (the scan's block)
+constexpr uint64_t kChunkSamples  = 1ull << 29;   // samples per chunk: 32 B each in the stream buffers (16 GiB)
+constexpr uint32_t kMaxSteps      = 1u << 19;     // so that a block of rays holds at most kChunkSamples samples
 constexpr uint32_t kMaxRounds  = 24u;   // K doubles from 256: covers any max_steps < 2^24
 
 struct NerfExtRenderer {
@@ -405,7 +416,7 @@ struct NerfExtRenderer {
     Buf<unsigned long long> round_total;
     hipEvent_t ev[6] = {};
     hipEvent_t fev[2 * kMaxRounds] = {};
-    unsigned long long* host_total = nullptr;
+    std::vector<uint32_t> host_sums;  // per-block sample counts (chunk plan)
 
     ~NerfExtRenderer() {
         cams.release();
@@ -429,7 +440,6 @@ struct NerfExtRenderer {
             if (e) (void)hipEventDestroy(e);
         for (hipEvent_t& e : ev)
             if (e) (void)hipEventDestroy(e);
-        if (host_total) (void)hipHostFree(host_total);
     }
 };
 
@@ -458,11 +468,6 @@ NERF_API NerfStatus nerf_ext_renderer_create(NerfExtRenderer** out) {
             delete r;
             return hip_fail(err, "hipEventCreate");
         }
-    }
-    const hipError_t err = hipHostMalloc((void**)&r->host_total, sizeof(unsigned long long), hipHostMallocDefault);
-    if (err != hipSuccess) {
-        delete r;
-        return hip_fail(err, "hipHostMalloc");
     }
     *out = r;
     return NERF_STATUS_OK;
@@ -500,7 +505,7 @@ NERF_API NerfStatus nerf_ext_march_count(const NerfExtCamera* camera, const Nerf
 NERF_API NerfStatus nerf_ext_render(NerfExtRenderer* R, const NerfExtRenderDesc* d, uint32_t* rgba8, float* rgb_f32, uint32_t* counts_out, NerfExtRenderStats* stats) {
     NERF_CHECK_ARG(R && d && d->model && d->occupancy && d->cameras && rgba8, "nerf_ext_render: null argument");
     NERF_CHECK_ARG(d->view_count >= 1u, "nerf_ext_render: view_count must be >= 1");
-    NERF_CHECK_ARG(d->max_steps >= 1u, "nerf_ext_render: max_steps must be >= 1");
+    NERF_CHECK_ARG(d->max_steps >= 1u && d->max_steps <= kMaxSteps, "nerf_ext_render: max_steps must be 1..2^19");
     GridParams g;
     const NerfStatus gs = make_grid(&d->model->grid, g);
     if (gs != NERF_STATUS_OK) return gs;
@@ -531,24 +536,38 @@ NERF_API NerfStatus nerf_ext_render(NerfExtRenderer* R, const NerfExtRenderDesc*
     k_march_count<<<blocks, 256, 0, st>>>(R->cams.ptr, ppv, n_rays, occ, d->max_steps, R->rays.ptr, R->counts.ptr);
     NERF_LAUNCH_CHECK("k_march_count");
     if (timed) NERF_HIP_TRY(hipEventRecord(R->ev[1], st));
-    NERF_HIP_TRY(exclusive_scan_u32(R->counts.ptr, R->offsets.ptr, n_rays, R->scan_tmp.ptr, R->total.ptr, st));
-    if (timed) NERF_HIP_TRY(hipEventRecord(R->ev[2], st));
-    NERF_HIP_TRY(hipMemcpyAsync(R->host_total, R->total.ptr, sizeof(unsigned long long), hipMemcpyDeviceToHost, st));
+    // Chunk plan: the per-ray counts summed over blocks of kScanBlock rays
+    // (exact; at most kScanBlock * 2^19 < 2^32 each), copied to the host,
+    // which groups whole blocks into chunks of at most kChunkSamples samples.
+    // Each chunk is marched, shaded and composited on its own, so the sample
+    // buffers hold one chunk; offsets are relative to the chunk.
+    const uint32_t n_blocks = (n_rays + kScanBlockRays - 1u) / kScanBlockRays;
+    NERF_HIP_TRY(R->scan_tmp.reserve(std::max<uint64_t>(scan_tmp_words(n_rays), n_blocks)));
+    NERF_HIP_TRY(block_sums_u32(R->counts.ptr, n_rays, R->scan_tmp.ptr, st));
+    R->host_sums.resize(n_blocks);
+    NERF_HIP_TRY(hipMemcpyAsync(R->host_sums.data(), R->scan_tmp.ptr, sizeof(uint32_t) * n_blocks, hipMemcpyDeviceToHost, st));
     NERF_HIP_TRY(hipStreamSynchronize(st));
-    const uint64_t total = *R->host_total;
-    if (total >= (1ull << 32)) {
-        set_error("nerf_ext_render: more than 2^32 samples in one call; render fewer views per call");
-        return NERF_STATUS_INVALID_USAGE;
+    if (timed) NERF_HIP_TRY(hipEventRecord(R->ev[2], st));
+    struct Chunk {
+        uint32_t ray0, ray_end;
+        uint64_t samples;
+    };
+    std::vector<Chunk> chunks;
+    const uint64_t budget = d->chunk_samples ? std::min<uint64_t>(d->chunk_samples, kChunkSamples) : kChunkSamples;
+    uint64_t total = 0, biggest = 0;
+    for (uint32_t b = 0; b < n_blocks;) {
+        Chunk c{b * kScanBlockRays, 0u, 0u};
+        while (b < n_blocks && (c.ray0 == (uint64_t)b * kScanBlockRays || c.samples + R->host_sums[b] <= budget)) c.samples += R->host_sums[b++];
+        c.ray_end = std::min<uint64_t>((uint64_t)b * kScanBlockRays, n_rays);
+        total += c.samples;
+        biggest = std::max(biggest, c.samples);
+        chunks.push_back(c);
     }
-    const uint32_t n_samples = (uint32_t)total;
-    NERF_HIP_TRY(R->samples.reserve(n_samples));
-    NERF_HIP_TRY(R->sample_ray.reserve(n_samples));
-    NERF_HIP_TRY(R->field.reserve(n_samples));
+    NERF_HIP_TRY(R->samples.reserve(biggest));
+    NERF_HIP_TRY(R->sample_ray.reserve(biggest));
+    NERF_HIP_TRY(R->field.reserve(biggest));
+    NERF_HIP_TRY(R->qlist.reserve(biggest));
 
-    if (timed) NERF_HIP_TRY(hipEventRecord(R->ev[3], st));
-    k_march_samples<<<(n_rays + 256u / kMarchGroup - 1u) / (256u / kMarchGroup), 256, 0, st>>>(R->cams.ptr, ppv, n_rays, occ, d->max_steps, R->rays.ptr, R->counts.ptr, R->offsets.ptr, R->samples.ptr, R->sample_ray.ptr);
-    NERF_LAUNCH_CHECK("k_march_samples");
-    if (timed) NERF_HIP_TRY(hipEventRecord(R->ev[4], st));
     FieldInputs in{};
     in.samples    = R->samples.ptr;
     in.sample_ray = R->sample_ray.ptr;
@@ -568,38 +587,69 @@ NERF_API NerfStatus nerf_ext_render(NerfExtRenderer* R, const NerfExtRenderDesc*
         Ks[n_rounds] = (uint32_t)K;
         ++n_rounds;
     }
+    const uint32_t chunk_rays_max = n_rays;
     NERF_HIP_TRY(R->state.reserve(n_rays));
-    NERF_HIP_TRY(R->list[0].reserve(n_rays));
-    NERF_HIP_TRY(R->list[1].reserve(n_rays));
+    NERF_HIP_TRY(R->list[0].reserve(chunk_rays_max));
+    NERF_HIP_TRY(R->list[1].reserve(chunk_rays_max));
     NERF_HIP_TRY(R->n_active.reserve(2));
-    NERF_HIP_TRY(R->cnt.reserve(n_rays));
-    NERF_HIP_TRY(R->off.reserve(n_rays));
-    NERF_HIP_TRY(R->qlist.reserve(n_samples));
+    NERF_HIP_TRY(R->cnt.reserve(chunk_rays_max));
+    NERF_HIP_TRY(R->off.reserve(chunk_rays_max));
     NERF_HIP_TRY(R->round_total.reserve(kMaxRounds));
     in.sample_index = R->qlist.ptr;
-    uint32_t* n_cur  = R->n_active.ptr;
-    uint32_t* n_nxt  = R->n_active.ptr + 1;
-    uint32_t* l_cur  = R->list[0].ptr;
-    uint32_t* l_nxt  = R->list[1].ptr;
-    k_fill_u32<<<1, 64, 0, st>>>(n_cur, 2u, 0u);
-    k_round_init<<<blocks, 256, 0, st>>>(n_rays, R->counts.ptr, bg, rgba8, rgb_f32, R->state.ptr, l_cur, n_cur);
-    NERF_LAUNCH_CHECK("k_round_init");
-    const uint32_t ray_waves = std::min<uint32_t>((n_rays + 3u) / 4u, device_cu_count() * 16u);  // workgroups of one-wave-per-slot kernels
-    for (uint32_t r = 0; r < n_rounds; ++r) {
-        k_round_counts<<<blocks, 256, 0, st>>>(n_rays, l_cur, n_cur, R->counts.ptr, Ss[r], Ks[r], R->cnt.ptr, n_nxt);
-        NERF_HIP_TRY(exclusive_scan_u32(R->cnt.ptr, R->off.ptr, n_rays, R->scan_tmp.ptr, R->round_total.ptr + r, st));
-        k_round_list<<<ray_waves, 256, 0, st>>>(l_cur, n_cur, R->offsets.ptr, Ss[r], R->cnt.ptr, R->off.ptr, R->qlist.ptr);
-        NERF_LAUNCH_CHECK("k_round_list");
-        // The field reads this round's sample count on the device: the low
-        // word of the 64-bit scan total (little-endian; totals < 2^32).
-        in.n_dev = reinterpret_cast<const uint32_t*>(R->round_total.ptr + r);
-        if (timed) NERF_HIP_TRY(hipEventRecord(R->fev[2u * r], st));
-        NERF_HIP_TRY(launch_field(g, d->model->table, w, in, n_samples, R->field.ptr, st));
-        if (timed) NERF_HIP_TRY(hipEventRecord(R->fev[2u * r + 1u], st));
-        k_round_composite<<<ray_waves, 256, 0, st>>>(l_cur, n_cur, R->counts.ptr, R->offsets.ptr, R->samples.ptr, R->field.ptr, Ss[r], Ks[r], d->min_transmittance, bg, R->state.ptr, rgba8, rgb_f32, l_nxt, n_nxt);
-        NERF_LAUNCH_CHECK("k_round_composite");
-        std::swap(l_cur, l_nxt);
-        std::swap(n_cur, n_nxt);
+
+    float ms_scan = 0.0f, ms_samples = 0.0f, field_ms = 0.0f;
+    uint64_t shaded = 0;
+    for (const Chunk& c : chunks) {
+        const uint32_t nr = c.ray_end - c.ray0;
+        if (timed) NERF_HIP_TRY(hipEventRecord(R->ev[3], st));
+        NERF_HIP_TRY(exclusive_scan_u32(R->counts.ptr + c.ray0, R->offsets.ptr + c.ray0, nr, R->scan_tmp.ptr, R->total.ptr, st));
+        if (timed) NERF_HIP_TRY(hipEventRecord(R->ev[4], st));
+        k_march_samples<<<(nr + 256u / kMarchGroup - 1u) / (256u / kMarchGroup), 256, 0, st>>>(R->cams.ptr, ppv, c.ray0, c.ray_end, occ, d->max_steps, R->rays.ptr, R->counts.ptr, R->offsets.ptr, R->samples.ptr,
+                                                                                               R->sample_ray.ptr);
+        NERF_LAUNCH_CHECK("k_march_samples");
+        if (timed) NERF_HIP_TRY(hipEventRecord(R->ev[5], st));
+        uint32_t* n_cur = R->n_active.ptr;
+        uint32_t* n_nxt = R->n_active.ptr + 1;
+        uint32_t* l_cur = R->list[0].ptr;
+        uint32_t* l_nxt = R->list[1].ptr;
+        const uint32_t cblocks = (nr + 255u) / 256u;
+        k_fill_u32<<<1, 64, 0, st>>>(n_cur, 2u, 0u);
+        k_round_init<<<cblocks, 256, 0, st>>>(c.ray0, c.ray_end, R->counts.ptr, bg, rgba8, rgb_f32, R->state.ptr, l_cur, n_cur);
+        NERF_LAUNCH_CHECK("k_round_init");
+        const uint32_t ray_waves = std::min<uint32_t>((nr + 3u) / 4u, device_cu_count() * 16u);  // workgroups of one-wave-per-slot kernels
+        for (uint32_t r = 0; r < n_rounds; ++r) {
+            k_round_counts<<<cblocks, 256, 0, st>>>(nr, l_cur, n_cur, R->counts.ptr, Ss[r], Ks[r], R->cnt.ptr, n_nxt);
+            NERF_HIP_TRY(exclusive_scan_u32(R->cnt.ptr, R->off.ptr, nr, R->scan_tmp.ptr, R->round_total.ptr + r, st));
+            k_round_list<<<ray_waves, 256, 0, st>>>(l_cur, n_cur, R->offsets.ptr, Ss[r], R->cnt.ptr, R->off.ptr, R->qlist.ptr);
+            NERF_LAUNCH_CHECK("k_round_list");
+            // The field reads this round's sample count on the device: the low
+            // word of the 64-bit scan total (little-endian; totals < 2^32).
+            in.n_dev = reinterpret_cast<const uint32_t*>(R->round_total.ptr + r);
+            if (timed) NERF_HIP_TRY(hipEventRecord(R->fev[2u * r], st));
+            NERF_HIP_TRY(launch_field(g, d->model->table, w, in, (uint32_t)c.samples, R->field.ptr, st));
+            if (timed) NERF_HIP_TRY(hipEventRecord(R->fev[2u * r + 1u], st));
+            k_round_composite<<<ray_waves, 256, 0, st>>>(l_cur, n_cur, R->counts.ptr, R->offsets.ptr, R->samples.ptr, R->field.ptr, Ss[r], Ks[r], d->min_transmittance, bg, R->state.ptr, rgba8, rgb_f32, l_nxt, n_nxt);
+            NERF_LAUNCH_CHECK("k_round_composite");
+            std::swap(l_cur, l_nxt);
+            std::swap(n_cur, n_nxt);
+        }
+        if (timed) {
+            // Per-chunk stage times (the events are reused by the next chunk).
+            NERF_HIP_TRY(hipStreamSynchronize(st));
+            float t_scan = 0.0f, t_samp = 0.0f;
+            NERF_HIP_TRY(hipEventElapsedTime(&t_scan, R->ev[3], R->ev[4]));
+            NERF_HIP_TRY(hipEventElapsedTime(&t_samp, R->ev[4], R->ev[5]));
+            ms_scan += t_scan;
+            ms_samples += t_samp;
+            for (uint32_t r = 0; r < n_rounds; ++r) {
+                float f = 0.0f;
+                NERF_HIP_TRY(hipEventElapsedTime(&f, R->fev[2u * r], R->fev[2u * r + 1u]));
+                field_ms += f;
+            }
+            std::vector<unsigned long long> totals(n_rounds);
+            NERF_HIP_TRY(hipMemcpy(totals.data(), R->round_total.ptr, sizeof(unsigned long long) * n_rounds, hipMemcpyDeviceToHost));
+            for (unsigned long long t : totals) shaded += t;
+        }
     }
     if (counts_out) NERF_HIP_TRY(hipMemcpyAsync(counts_out, R->counts.ptr, sizeof(uint32_t) * n_rays, hipMemcpyDeviceToDevice, st));
     if (timed) {
@@ -607,29 +657,19 @@ NERF_API NerfStatus nerf_ext_render(NerfExtRenderer* R, const NerfExtRenderDesc*
         NERF_HIP_TRY(hipEventCreate(&end));
         NERF_HIP_TRY(hipEventRecord(end, st));
         NERF_HIP_TRY(hipEventSynchronize(end));
-        float ms[3], field_ms = 0.0f, total_ms = 0.0f;
-        NERF_HIP_TRY(hipEventElapsedTime(&ms[0], R->ev[0], R->ev[1]));
-        NERF_HIP_TRY(hipEventElapsedTime(&ms[1], R->ev[1], R->ev[2]));
-        NERF_HIP_TRY(hipEventElapsedTime(&ms[2], R->ev[3], R->ev[4]));
-        for (uint32_t r = 0; r < n_rounds; ++r) {
-            float f = 0.0f;
-            NERF_HIP_TRY(hipEventElapsedTime(&f, R->fev[2u * r], R->fev[2u * r + 1u]));
-            field_ms += f;
-        }
+        float ms_count = 0.0f, ms_plan = 0.0f, total_ms = 0.0f;
+        NERF_HIP_TRY(hipEventElapsedTime(&ms_count, R->ev[0], R->ev[1]));
+        NERF_HIP_TRY(hipEventElapsedTime(&ms_plan, R->ev[1], R->ev[2]));
         NERF_HIP_TRY(hipEventElapsedTime(&total_ms, R->ev[0], end));
         (void)hipEventDestroy(end);
-        std::vector<unsigned long long> totals(n_rounds);
-        NERF_HIP_TRY(hipMemcpy(totals.data(), R->round_total.ptr, sizeof(unsigned long long) * n_rounds, hipMemcpyDeviceToHost));
-        uint64_t shaded = 0;
-        for (unsigned long long t : totals) shaded += t;
         stats->rays           = n_rays;
-        stats->samples        = n_samples;
+        stats->samples        = total;
         stats->samples_shaded = shaded;
-        stats->ms_count       = ms[0];
-        stats->ms_scan        = ms[1];
-        stats->ms_samples     = ms[2];
+        stats->ms_count       = ms_count;
+        stats->ms_scan        = ms_plan + ms_scan;
+        stats->ms_samples     = ms_samples;
         stats->ms_field       = field_ms;
-        stats->ms_composite   = total_ms - ms[0] - ms[1] - ms[2] - field_ms;
+        stats->ms_composite   = total_ms - stats->ms_count - stats->ms_scan - ms_samples - field_ms;
         stats->ms_total       = total_ms;
     }
     return NERF_STATUS_OK;

@@ -84,3 +84,25 @@ def test_render_parity(w, h, views):
     rgba2, _ = r.render(model, occ, cams, 1024)
     synchronize()
     assert np.array_equal(rgba2.numpy(), rgba.numpy())
+
+
+def test_render_in_chunks_matches_one_chunk():
+    # 2 views of 64x48 = 6 blocks of 1024 rays; a small sample budget splits
+    # the render into one chunk per block.  Rays are independent, so the
+    # images, counts and statistics are identical.
+    announce("render in chunks: 2 views 64x48, chunk budget 1 sample")
+    g, bits = _scene_setup()
+    desc = ext.grid_desc(19, L.NERF_EXT_F16)
+    model = ext.Model.create(desc, seed=0, table_range=1.0)
+    cams = [ext.camera_orbit(0, i, 1.32, CENTRE, 64, 48, 1111.0 * 64 / 800.0) for i in range(2)]
+    occ = ext.occupancy_struct(bits, 128)
+    outs = []
+    for chunk in (0, 1):
+        rgb = DeviceArray((2, 48, 64, 3), np.float32)
+        counts = DeviceArray((2, 48, 64), np.uint32)
+        rgba, stats = ext.Renderer().render(model, occ, cams, 1024, rgb=rgb, counts=counts, timed=True, chunk_samples=chunk)
+        synchronize()
+        outs.append((rgba.numpy(), rgb.numpy(), counts.numpy(), stats.samples, stats.samples_shaded))
+    (a0, r0, c0, s0, h0), (a1, r1, c1, s1, h1) = outs
+    assert np.array_equal(a0, a1) and np.array_equal(r0.view(np.uint32), r1.view(np.uint32)) and np.array_equal(c0, c1)
+    assert s0 == s1 == int(c0.sum()) and h0 == h1 and s0 > 0
