@@ -127,19 +127,20 @@ def kernel_rooflines(reps_small: int = 200):
         gbs = n * ENCODE_BYTES_PER_POINT / (ms / 1e3) / 1e9
         out[label] = {"kernel": "k_encode_split (nerf_ext_encode_forward, four levels per XCD, one point per thread)", "points": n, "table": "16 x 2^16 x 2 fp32", "ms": round(ms, 5), "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                       "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_point": ENCODE_BYTES_PER_POINT, "reps": reps}
-    n = 1 << 22
     rng = np.random.default_rng(0)
-    feats = DeviceArray.from_numpy(rng.uniform(-1.0, 1.0, size=(n, 32)).astype(np.float16))
-    d = rng.normal(size=(n, 3)).astype(np.float32)
-    dirs = DeviceArray.from_numpy(d / np.linalg.norm(d, axis=1, keepdims=True))
-    res = DeviceArray((n, 4), np.float32)
     dp = DeviceArray.from_numpy(ext.mlp_init(0).astype(np.float16))
     cp = DeviceArray.from_numpy(ext.mlp_init(1).astype(np.float16))
-    ms = timed(lambda: L.call("nerf_ext_field_mlp", dp.ptr, cp.ptr, feats.ptr, dirs.ptr, n, res.ptr, st.handle), 20)
-    tfs = n * FIELD_FLOPS_PER_SAMPLE / (ms / 1e3) / 1e12
-    io_gbs = n * (64 + 12 + 16) / (ms / 1e3) / 1e9
-    out["field_mlp"] = {"kernel": "k_field_mlp (density 32-64-16 + colour 32-64-64-16, fp16 MFMA)", "samples": n, "ms": round(ms, 4), "bound": "mfma", "achieved": round(tfs, 1), "peak": MFMA_FP16_PEAK_TFS, "unit": "TFLOP/s",
-                        "frac": round(tfs / MFMA_FP16_PEAK_TFS, 4), "flops_per_sample": FIELD_FLOPS_PER_SAMPLE, "io_GBps": round(io_gbs, 1)}
+    for n, label in ((1 << 22, "field_mlp"), (1 << 24, "field_mlp_2p24")):
+        feats = DeviceArray.from_numpy(rng.uniform(-1.0, 1.0, size=(n, 32)).astype(np.float16))
+        d = rng.normal(size=(n, 3)).astype(np.float32)
+        dirs = DeviceArray.from_numpy(d / np.linalg.norm(d, axis=1, keepdims=True))
+        res = DeviceArray((n, 4), np.float32)
+        ms = timed(lambda: L.call("nerf_ext_field_mlp", dp.ptr, cp.ptr, feats.ptr, dirs.ptr, n, res.ptr, st.handle), 20)
+        tfs = n * FIELD_FLOPS_PER_SAMPLE / (ms / 1e3) / 1e12
+        io_gbs = n * (64 + 12 + 16) / (ms / 1e3) / 1e9
+        out[label] = {"kernel": "k_field_mlp (density 32-64-16 + colour 32-64-64-16, fp16 MFMA)", "samples": n, "ms": round(ms, 4), "bound": "mfma", "achieved": round(tfs, 1), "peak": MFMA_FP16_PEAK_TFS, "unit": "TFLOP/s",
+                      "frac": round(tfs / MFMA_FP16_PEAK_TFS, 4), "flops_per_sample": FIELD_FLOPS_PER_SAMPLE, "io_GBps": round(io_gbs, 1)}
+        del feats, dirs, res
     return out
 
 
@@ -302,6 +303,52 @@ def render_trained(tr, reps: int = 5):
             "workload": "800x800 view of the trained model (analytic 128^3 occupancy, <=1024 steps/ray, early stop T<1e-4)"}
 
 
+def config_renders(reps: int = 2):
+    """The two large configurations as whole renders (one warm-up, then reps
+    timed by wall clock around synchronised calls):
+      C4: 1920x1080, hash grid T=2^22 fp16 with finest resolution 4096, 256
+          Gaussians (as the headline scene), 256^3 occupancy, <=2048 steps/ray,
+          focal 1111 * 1920 / 800 (the headline field of view);
+      C5: 8 views of 1280x720 in one call (one compacted sample stream per
+          chunk of rays), unbounded scene of 512 Gaussians over [-16, 16]^3
+          (sigma U(0.3, 1.5), amplitude U(5, 50)) plus a uniform shell of radii
+          12..15.5, 5 nested 128^3 cascades over [-1, 1]^3 .. [-16, 16]^3, hash
+          grid T=2^21 fp16, <=4096 steps/ray, orbit radius 4, focal
+          1111 * 1280 / 800.
+    Random-init models, early stop at T < 1e-4."""
+    from nerf_amd import _lib as L, ext
+    from nerf_amd.device import synchronize
+
+    def run(model, occ, cams, steps):
+        r = ext.Renderer()
+        r.render(model, occ, cams, steps, T_STOP)
+        synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            _, st = r.render(model, occ, cams, steps, T_STOP, timed=True)
+        wall = (time.perf_counter() - t0) / reps
+        n = len(cams) * cams[0].width * cams[0].height
+        return {"value": round(n / wall / 1e6, 3), "unit": "Mrays/s", "ms_per_render": round(wall * 1e3, 2), "field_ms": round(st.ms_field, 2), "samples_marched": int(st.samples),
+                "samples_shaded": int(st.samples_shaded), "reps": reps}
+
+    out = {}
+    g = ext.scene_gaussians(256, seed=4)
+    bits = ext.occupancy_from_scene(g, 256, 0.01)
+    model = ext.Model.create(ext.grid_desc(22, L.NERF_EXT_F16, finest=4096), seed=0)
+    cam = ext.camera_orbit(0, 0, RADIUS, CENTRE, 1920, 1080, FOCAL * 1920 / 800.0)
+    out["C4"] = run(model, ext.occupancy_struct(bits, 256), [cam], 2048)
+    out["C4"]["workload"] = "1920x1080, T=2^22 fp16 (finest 4096), 256 Gaussians, 256^3 occupancy, <=2048 steps/ray"
+    del model, bits
+    g = ext.scene_gaussians(512, seed=5, centre=(-16.0, 16.0), sigma=(0.3, 1.5), amplitude=(5.0, 50.0))
+    bits = ext.occupancy_from_scene(g, 128, 0.01, (-1.0, -1.0, -1.0), (1.0, 1.0, 1.0), 5, shell=((0.0, 0.0, 0.0), 12.0, 15.5))
+    model = ext.Model.create(ext.grid_desc(21, L.NERF_EXT_F16), seed=0)
+    occ = ext.occupancy_struct(bits, 128, (-1.0, -1.0, -1.0), (1.0, 1.0, 1.0), 5)
+    cams = [ext.camera_orbit(5, i, 4.0, (0.0, 0.0, 0.0), 1280, 720, FOCAL * 1280 / 800.0) for i in range(8)]
+    out["C5"] = run(model, occ, cams, 4096)
+    out["C5"]["workload"] = "8 x 1280x720 in one call, 5 x 128^3 cascades, 512 Gaussians over radius 16 + shell, T=2^21 fp16, <=4096 steps/ray"
+    return out
+
+
 def cpu_baseline(desc, model, cam, bits, budget_s: float = 15.0):
     """Scalar oracle on a deterministic ray subset (every k-th ray of the view)."""
     from oracle import oracle as orc
@@ -339,6 +386,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-stage-rooflines", action="store_true", help="skip the encode / MLP stage measurements")
+    ap.add_argument("--no-configs", action="store_true", help="skip the C4 (1920x1080, T=2^22) and C5 (8 views, 5 cascades) renders")
     ap.add_argument("--train-steps", type=int, default=100, help="timed training steps (0: skip the training leg)")
     ap.add_argument("--train-warmup", type=int, default=30)
     ap.add_argument("--width", type=int, default=W, help="render width (the metric is quoted at 800)")
@@ -432,6 +480,8 @@ def main() -> int:
         line["abi_render"] = abi_render()
     if args.train_steps > 0:
         line["train"] = train_bench(args.train_steps, args.train_warmup)
+    if not args.no_configs:
+        line["configs"] = config_renders()
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(desc, model, cam, bits)
     print(json.dumps(line), flush=True)
