@@ -202,6 +202,73 @@ __device__ __forceinline__ bool occ_occupied(const OccView& o, const float p[3])
 // empty, the cascade count is above 8 or the bit indices overflow 32 bits.
 bool make_occ_view(const NerfExtOccupancy& o, OccView& v);
 
+// One level with the x-neighbour corners of each (y, z) edge (corners 2e and
+// 2e + 1) fetched by as few loads as the index structure allows:
+//   * dense level: the two entries are adjacent (i1 = i0 + 1): one load of
+//     two entries at i0 (entry aligned, not necessarily pair aligned; the
+//     hardware serves unaligned dword loads);
+//   * hashed level: when x is even, i1 = i0 ^ 1 (x's prime is 1): one load
+//     of that aligned entry pair; otherwise two single-entry loads (also
+//     merging the odd-x cases whose entries happen to be adjacent measured
+//     no faster).
+// Same entries, weights and summation order as encode_level.
+template <typename TableT>
+__device__ __forceinline__ void load_entry_pair(const TableT* p, float q[4]) {
+    if constexpr (sizeof(TableT) == 4) {
+        float4 w;
+        __builtin_memcpy(&w, p, 16);
+        q[0] = w.x;
+        q[1] = w.y;
+        q[2] = w.z;
+        q[3] = w.w;
+    } else {
+        half4_t w;
+        __builtin_memcpy(&w, p, 8);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) q[k] = (float)w[k];
+    }
+}
+
+template <typename TableT, bool kHashPairs = true>
+__device__ __forceinline__ void encode_level_xpair(const GridParams& g, const TableT* __restrict__ table, const float p[3], uint32_t level, uint32_t N, bool dense, float& a0, float& a1) {
+    const LevelCell c  = level_cell(p, N);
+    const TableT* base = table + (uint64_t)level * g.table_size * 2u;
+    float v0[8], v1[8];
+#pragma unroll
+    for (uint32_t e = 0; e < 4u; ++e) {  // (y, z) edge e: corners 2e (x) and 2e + 1 (x + 1)
+        const uint32_t i0 = corner_index(c, 2u * e, N, dense, g.table_size - 1u);
+        const uint32_t i1 = corner_index(c, 2u * e + 1u, N, dense, g.table_size - 1u);
+        float q[4];
+        if (dense) {
+            load_entry_pair(base + 2u * i0, q);
+            v0[2u * e]      = q[0];
+            v1[2u * e]      = q[1];
+            v0[2u * e + 1u] = q[2];
+            v1[2u * e + 1u] = q[3];
+        } else if (kHashPairs && i1 == (i0 ^ 1u)) {
+            load_entry_pair(base + 2u * (i0 & ~1u), q);
+            const bool odd  = (i0 & 1u) != 0u;
+            v0[2u * e]      = odd ? q[2] : q[0];
+            v1[2u * e]      = odd ? q[3] : q[1];
+            v0[2u * e + 1u] = odd ? q[0] : q[2];
+            v1[2u * e + 1u] = odd ? q[1] : q[3];
+        } else {
+            v0[2u * e]      = (float)base[2u * i0];
+            v1[2u * e]      = (float)base[2u * i0 + 1u];
+            v0[2u * e + 1u] = (float)base[2u * i1];
+            v1[2u * e + 1u] = (float)base[2u * i1 + 1u];
+        }
+    }
+    a0 = 0.0f;
+    a1 = 0.0f;
+#pragma unroll
+    for (uint32_t k = 0; k < 8u; ++k) {
+        const float w = corner_weight(c, k);
+        a0            = a0 + w * v0[k];
+        a1            = a1 + w * v1[k];
+    }
+}
+
 // --------------------------------------------------------------- cameras
 struct Ray {
     float o[3];

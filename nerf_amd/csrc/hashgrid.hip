@@ -86,71 +86,6 @@ __global__ __launch_bounds__(256) void k_encode_tile(GridParams g, const TableT*
     for (uint32_t i = threadIdx.x; i < count * width; i += blockDim.x) o[i] = tile[i];
 }
 
-// One level with the x-neighbour corners of each (y, z) edge (corners 2e and
-// 2e + 1) fetched by as few loads as the index structure allows:
-//   * dense level: the two entries are adjacent (i1 = i0 + 1): one load of
-//     two entries at i0 (entry aligned, not necessarily pair aligned; the
-//     hardware serves unaligned dword loads);
-//   * hashed level: when x is even, i1 = i0 ^ 1 (x's prime is 1), one load
-//     of that aligned entry pair; otherwise two single-entry loads.
-// Same entries, weights and summation order as encode_level.
-template <typename TableT>
-__device__ __forceinline__ void load_entry_pair(const TableT* p, float q[4]) {
-    if constexpr (sizeof(TableT) == 4) {
-        float4 w;
-        __builtin_memcpy(&w, p, 16);
-        q[0] = w.x;
-        q[1] = w.y;
-        q[2] = w.z;
-        q[3] = w.w;
-    } else {
-        half4_t w;
-        __builtin_memcpy(&w, p, 8);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) q[k] = (float)w[k];
-    }
-}
-
-template <typename TableT>
-__device__ __forceinline__ void encode_level_xpair(const GridParams& g, const TableT* __restrict__ table, const float p[3], uint32_t level, uint32_t N, bool dense, float& a0, float& a1) {
-    const LevelCell c  = level_cell(p, N);
-    const TableT* base = table + (uint64_t)level * g.table_size * 2u;
-    float v0[8], v1[8];
-#pragma unroll
-    for (uint32_t e = 0; e < 4u; ++e) {  // (y, z) edge e: corners 2e (x) and 2e + 1 (x + 1)
-        const uint32_t i0 = corner_index(c, 2u * e, N, dense, g.table_size - 1u);
-        const uint32_t i1 = corner_index(c, 2u * e + 1u, N, dense, g.table_size - 1u);
-        float q[4];
-        if (dense) {
-            load_entry_pair(base + 2u * i0, q);
-            v0[2u * e]      = q[0];
-            v1[2u * e]      = q[1];
-            v0[2u * e + 1u] = q[2];
-            v1[2u * e + 1u] = q[3];
-        } else if (i1 == (i0 ^ 1u)) {
-            load_entry_pair(base + 2u * (i0 & ~1u), q);
-            const bool odd  = (i0 & 1u) != 0u;
-            v0[2u * e]      = odd ? q[2] : q[0];
-            v1[2u * e]      = odd ? q[3] : q[1];
-            v0[2u * e + 1u] = odd ? q[0] : q[2];
-            v1[2u * e + 1u] = odd ? q[1] : q[3];
-        } else {
-            v0[2u * e]      = (float)base[2u * i0];
-            v1[2u * e]      = (float)base[2u * i0 + 1u];
-            v0[2u * e + 1u] = (float)base[2u * i1];
-            v1[2u * e + 1u] = (float)base[2u * i1 + 1u];
-        }
-    }
-    a0 = 0.0f;
-    a1 = 0.0f;
-#pragma unroll
-    for (uint32_t k = 0; k < 8u; ++k) {
-        const float w = corner_weight(c, k);
-        a0            = a0 + w * v0[k];
-        a1            = a1 + w * v1[k];
-    }
-}
-
 // XCD-aware encode.  Workgroup b runs on XCD b % 8 (the dispatcher's round
 // robin) and gathers only kLevels levels of the table, so each XCD's L2
 // holds those levels rather than all of them:
@@ -161,8 +96,9 @@ __device__ __forceinline__ void encode_level_xpair(const GridParams& g, const Ta
 //     contiguous bytes of the output row instead of 16.
 // One point per thread (the launch gives every thread exactly one).  The
 // placement is a locality choice only: any workgroup-to-XCD mapping gives
-// the same result.  With kPair (the table aligned to an entry pair)
-// x-neighbour corners are fetched in pairs.
+// the same result.  With kPair, x-neighbour corners that are adjacent
+// entries are fetched by one load (dense levels always; hashed levels for
+// even x).
 template <typename TableT, typename OutT, bool kPair, uint32_t kLevels>
 __global__ __launch_bounds__(256) void k_encode_split(GridParams g, const TableT* __restrict__ table, const float* __restrict__ pos, uint32_t n, OutT* __restrict__ out) {
     constexpr uint32_t kParts = kLevels / 2u;  // XCDs sharing one level group
@@ -267,17 +203,12 @@ NERF_API NerfStatus nerf_ext_encode_forward(const NerfExtGridDesc* grid, const v
     // draining through a long tail of the oldest-first wave scheduling.
     const uint32_t blocks_256 = (n + 255u) / 256u;
     const dim3 grid_dim = quad ? dim3(8u * ((blocks_256 + 1u) / 2u)) : split ? dim3(8u * blocks_256) : dim3((n + kEncPoints - 1u) / kEncPoints);
-    // Pair loads need the table aligned to an entry pair: 16 bytes for fp32,
-    // 8 for fp16 (device allocations are).
-    const bool pair = ((uintptr_t)table & (g.table_dtype == NERF_EXT_F32 ? 15u : 7u)) == 0u;
 #define NERF_ENC(TT, OT)                                                                                                   \
     do {                                                                                                                   \
-        if (quad && pair)                                                                                                  \
+        if (quad)                                                                                                          \
             k_encode_split<TT, OT, true, 4u><<<grid_dim, 256, 0, st>>>(g, (const TT*)table, positions, n, (OT*)features);  \
-        else if (split && pair)                                                                                            \
-            k_encode_split<TT, OT, true, 2u><<<grid_dim, 256, 0, st>>>(g, (const TT*)table, positions, n, (OT*)features);  \
         else if (split)                                                                                                    \
-            k_encode_split<TT, OT, false, 2u><<<grid_dim, 256, 0, st>>>(g, (const TT*)table, positions, n, (OT*)features); \
+            k_encode_split<TT, OT, true, 2u><<<grid_dim, 256, 0, st>>>(g, (const TT*)table, positions, n, (OT*)features);  \
         else                                                                                                               \
             k_encode_tile<TT, OT><<<grid_dim, 256, 0, st>>>(g, (const TT*)table, positions, n, (OT*)features);             \
     } while (0)
