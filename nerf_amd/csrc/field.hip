@@ -149,6 +149,93 @@ __global__ __launch_bounds__(kBlockThreads) void k_field_forward(GridParams g, c
     }
 }
 
+// Full field, level-major gather.  A wave takes 64 samples at a time, lane l
+// owning sample l: it gathers the 16 levels of its sample one level after
+// another, so every load instruction of the wave reads one level for 64
+// consecutive samples (neighbouring samples share the lines of the coarse
+// levels within one instruction) and a level's dense/hashed branch is
+// uniform across the wave (dense levels take one load per x-neighbour
+// pair; hashed levels one load per corner: pairing their even-x corners as
+// the encode kernel does measured 11 % slower here).  The fp16 features go through LDS (rows of 80 bytes: 16-byte
+// stores of four levels, 16-byte reads of lane group g's levels 4g..4g+3,
+// no bank conflicts) into the MLP's B-operand layout, four 16-sample tiles
+// per group; the SH coefficients go through LDS as in k_field_mlp.
+constexpr uint32_t kFeatPitch = 40u;  // halves per LDS feature row (80 bytes)
+template <typename TableT, bool kFromSamples>
+__global__ __launch_bounds__(kBlockThreads) void k_field_forward_lv(GridParams g, const TableT* __restrict__ table, const half_t* __restrict__ dparams, const half_t* __restrict__ cparams, FieldInputs in, uint32_t n_cap,
+                                                                   float4* __restrict__ out) {
+    const uint32_t n = in.n_dev ? min(*in.n_dev, n_cap) : n_cap;
+    __shared__ __align__(16) half_t sp[NERF_EXT_DENSITY_PARAMS + NERF_EXT_COLOR_PARAMS];
+    __shared__ __align__(16) half_t feat[kBlockWaves][64 * kFeatPitch];
+    __shared__ half4_t shl[kBlockWaves][64][4];
+    stage_weights<kBlockThreads>(sp, dparams, cparams);
+    __syncthreads();
+    const uint32_t lane = threadIdx.x & 63u, grp = lane >> 4, s16 = lane & 15u, wv = threadIdx.x >> 6;
+    DensityFrags fd;
+    ColorFrags fc;
+    load_density(sp, fd, lane);
+    load_color(sp + NERF_EXT_DENSITY_PARAMS, fc, lane);
+    half_t* F = feat[wv];
+    // Round r covers groups [r * W, (r + 1) * W) (W = all waves), XCD x
+    // (workgroups b with b % 8 == x) taking the x-th eighth of it.
+    const uint32_t groups  = (n + 63u) / 64u;
+    const uint32_t per_xcd = (gridDim.x >> 3) * kBlockWaves;
+    const uint32_t first   = (blockIdx.x & 7u) * per_xcd + (blockIdx.x >> 3) * kBlockWaves + wv;
+    for (uint32_t gi = first; gi < groups; gi += 8u * per_xcd) {
+        const uint32_t s = gi * 64u + lane;
+        const uint32_t q = s < n ? s : n - 1u;
+        float p[3], d[3];
+        if constexpr (kFromSamples) {
+            const uint32_t qs = in.sample_index ? in.sample_index[q] : q;
+            sample_point(in, qs, p, d);
+        } else {
+#pragma unroll
+            for (int a = 0; a < 3; ++a) {
+                p[a] = in.positions[3ull * q + a];
+                d[a] = in.directions[3ull * q + a];
+            }
+        }
+        float sh[16];
+        sh16(d, sh);
+#pragma unroll
+        for (uint32_t j = 0; j < 4u; ++j) shl[wv][lane][j] = half4_t{to_half_rne(sh[4u * j]), to_half_rne(sh[4u * j + 1u]), to_half_rne(sh[4u * j + 2u]), to_half_rne(sh[4u * j + 3u])};
+        // Gather, four levels per 16-byte LDS store.
+#pragma unroll
+        for (uint32_t k = 0; k < 4u; ++k) {
+            half8_t h;
+#pragma unroll
+            for (uint32_t j = 0; j < 4u; ++j) {
+                const uint32_t l = 4u * k + j;
+                float a0 = 0.0f, a1 = 0.0f;
+                if (l < g.n_levels) encode_level_xpair<TableT, false>(g, table, p, l, g.resolution[l], g.dense[l] != 0u, a0, a1);
+                h[2u * j]      = to_half_rne(a0);
+                h[2u * j + 1u] = to_half_rne(a1);
+            }
+            *reinterpret_cast<half8_t*>(F + lane * kFeatPitch + 8u * k) = h;
+            if (in.features_out && s < n) *reinterpret_cast<half8_t*>(in.features_out + (uint64_t)s * 32u + 8u * k) = h;
+        }
+        __builtin_amdgcn_wave_barrier();  // LDS traffic of one wave completes in order
+        float v[4];
+#pragma unroll
+        for (uint32_t t = 0; t < 4u; ++t) {
+            const uint32_t row = 16u * t + s16;
+            const half8_t x    = *reinterpret_cast<const half8_t*>(F + row * kFeatPitch + 8u * grp);
+            const floatx4 o    = density_mlp(fd, x);
+            const floatx4 c    = color_mlp(fc, color_input(o, shl[wv][row][grp], grp));
+            v[t]               = field_channel(o, c, grp);
+        }
+#pragma unroll
+        for (uint32_t t = 0; t < 4u; ++t) {
+            const uint32_t st = gi * 64u + 16u * t + s16;
+            if (st < n) {
+                const uint32_t dst = (kFromSamples && in.sample_index) ? in.sample_index[st] : st;
+                reinterpret_cast<float*>(out)[4ull * dst + grp] = v[t];
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+}
+
 // MLP pass on given encodings, in groups of 64 samples (four 16-sample
 // tiles) per wave.  Lane l first evaluates all 16 SH coefficients of sample
 // l of the group and leaves them in LDS as fp16; lane (g, s) of tile t then
@@ -214,24 +301,29 @@ uint32_t persistent_blocks(uint32_t n, uint32_t per_cu) {
 
 hipError_t launch_field(const GridParams& g, const void* table, const FieldWeights& w, const FieldInputs& in, uint32_t n, float4* out4, hipStream_t stream) {
     if (n == 0u) return hipSuccess;
-    // Workgroups per CU: 8 for large launches (renders: more tiles in flight
-    // per XCD keep its L2 busy), 3 for training-sized batches (<= 2^20
-    // samples: every workgroup stages the weights, so fewer, longer-lived
-    // ones; 3 is also what the register budget keeps resident).
-    const uint32_t per_cu   = n <= (1u << 20) ? 3u : 8u;
-    const uint32_t blocks   = (persistent_blocks(n, per_cu) + 7u) / 8u * 8u;  // whole XCD rounds
+    // Renders (more than 2^20 samples) take the level-major kernel, 3
+    // workgroups per CU (its LDS and register budget); training-sized
+    // batches the tile kernel, whose 16-sample tiles leave a shorter tail
+    // when a launch is only one or two rounds of work (2^18 samples: 84 vs
+    // 115 us; 800x800 render: 119 vs 116 ms).  The tile kernel uses 3
+    // workgroups per CU there (every workgroup stages the weights, so fewer,
+    // longer-lived ones; 3 is also what the register budget keeps resident).
+    const bool level_major  = n > (1u << 20);
+    const uint32_t blocks   = (persistent_blocks(n, 3u) + 7u) / 8u * 8u;  // whole XCD rounds
     const bool from_samples = in.samples != nullptr;
-    if (g.table_dtype == NERF_EXT_F32) {
-        if (from_samples)
-            k_field_forward<float, true><<<blocks, kBlockThreads, 0, stream>>>(g, (const float*)table, w.density, w.color, in, n, out4);
-        else
-            k_field_forward<float, false><<<blocks, kBlockThreads, 0, stream>>>(g, (const float*)table, w.density, w.color, in, n, out4);
-    } else {
-        if (from_samples)
-            k_field_forward<half_t, true><<<blocks, kBlockThreads, 0, stream>>>(g, (const half_t*)table, w.density, w.color, in, n, out4);
-        else
-            k_field_forward<half_t, false><<<blocks, kBlockThreads, 0, stream>>>(g, (const half_t*)table, w.density, w.color, in, n, out4);
-    }
+#define NERF_FIELD_LAUNCH(K)                                                                                                                   \
+    do {                                                                                                                                       \
+        if (g.table_dtype == NERF_EXT_F32) {                                                                                                   \
+            if (from_samples) K<float, true><<<blocks, kBlockThreads, 0, stream>>>(g, (const float*)table, w.density, w.color, in, n, out4);      \
+            else K<float, false><<<blocks, kBlockThreads, 0, stream>>>(g, (const float*)table, w.density, w.color, in, n, out4);                \
+        } else {                                                                                                                               \
+            if (from_samples) K<half_t, true><<<blocks, kBlockThreads, 0, stream>>>(g, (const half_t*)table, w.density, w.color, in, n, out4);  \
+            else K<half_t, false><<<blocks, kBlockThreads, 0, stream>>>(g, (const half_t*)table, w.density, w.color, in, n, out4);              \
+        }                                                                                                                                      \
+    } while (0)
+    if (level_major) NERF_FIELD_LAUNCH(k_field_forward_lv);
+    else NERF_FIELD_LAUNCH(k_field_forward);
+#undef NERF_FIELD_LAUNCH
     return hipGetLastError();
 }
 

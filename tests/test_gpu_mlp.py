@@ -93,6 +93,25 @@ def test_field_forward(log2_t, dtype):
     assert_rel(d_o.numpy(), want, what="field forward")
 
 
+def test_field_forward_level_major_launch():
+    # More than 2^20 points take the level-major field kernel (renders); the
+    # smaller launches above take the tile kernel.  Rows compared on a sample.
+    n = (1 << 20) + 4099
+    announce(f"field forward level-major n={n}")
+    desc = ext.grid_desc(19, L.NERF_EXT_F16)
+    model = ext.Model.create(desc, seed=2, table_range=0.5)
+    pos = points(n, seed=13)
+    dirs = unit_dirs(n, seed=14)
+    d_pos, d_dir, d_o = DeviceArray.from_numpy(pos), DeviceArray.from_numpy(dirs), DeviceArray((n, 4), np.float32)
+    ms = model.struct()
+    L.call("nerf_ext_field_forward", byref(ms), d_pos.ptr, d_dir.ptr, n, d_o.ptr, None)
+    synchronize()
+    rows = np.unique(np.concatenate([np.random.default_rng(5).integers(0, n, 4000), np.arange(n - 70, n)]))
+    dp, cp = host_params(model)
+    want = orc.field_forward(oracle_grid(desc), host_table(model), dp, cp, np.ascontiguousarray(pos[rows]), np.ascontiguousarray(dirs[rows]))
+    assert_rel(d_o.numpy()[rows], want, what="field forward (level-major)")
+
+
 @pytest.mark.parametrize("n", [65536, 1000])
 def test_field_mlp_on_features(n):
     announce(f"field mlp on features n={n}")
