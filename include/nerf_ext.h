@@ -34,6 +34,11 @@ extern "C" {
 enum { NERF_EXT_F32 = 0, NERF_EXT_F16 = 1 };
 enum { NERF_EXT_H2D = 1, NERF_EXT_D2H = 2, NERF_EXT_D2D = 3 };
 enum { NERF_EXT_DENSITY_PARAMS = 3072, NERF_EXT_COLOR_PARAMS = 7168 };
+/* Parameter counts of the reference's own network (reference-model mode):
+ * density 128x64 + 4 x 128x128 + 16x128, colour 128x48 + 2 x 128x128 + 16x128. */
+enum { NERF_EXT_REF_DENSITY_PARAMS = 75776, NERF_EXT_REF_COLOR_PARAMS = 40960 };
+/* NerfExtModel.kind */
+enum { NERF_EXT_MODEL_HASHGRID = 0, NERF_EXT_MODEL_REFERENCE = 1 };
 enum { NERF_EXT_MAX_LEVELS = 16 };
 
 /* ---------------------------------------------------------------- runtime */
@@ -118,13 +123,30 @@ NERF_API NerfStatus nerf_ext_density_forward(const NerfExtGridDesc* grid, const 
 typedef struct NerfExtModel {
     NerfExtGridDesc grid;
     const void* table;              /* device, [L][T][F] */
-    const uint16_t* density_params; /* device, 3072 fp16 */
-    const uint16_t* color_params;   /* device, 7168 fp16 */
+    const uint16_t* density_params; /* device, 3072 fp16 (reference model: 75776) */
+    const uint16_t* color_params;   /* device, 7168 fp16 (reference model: 40960) */
+    uint32_t kind;                  /* NERF_EXT_MODEL_HASHGRID (0) or
+                                       NERF_EXT_MODEL_REFERENCE: the reference's
+                                       own network (grid and table unused; field
+                                       positions are world coordinates) */
+    uint32_t reserved;
 } NerfExtModel;
 
 /* Full field at points with view directions: out [n][4] = (sigma, r, g, b),
- * sigma = exp(density raw 0), rgb = sigmoid(colour raw 0..2). */
+ * sigma = exp(density raw 0), rgb = sigmoid(colour raw 0..2); positions in
+ * the unit cube of the grid.  A model of kind NERF_EXT_MODEL_REFERENCE runs
+ * nerf_ext_ref_field_forward instead (world positions, softplus sigma). */
 NERF_API NerfStatus nerf_ext_field_forward(const NerfExtModel* model, const float* positions, const float* directions, uint32_t n, float* out, void* stream);
+/* Reference-model mode: the reference's own network (backend-cuda.cu:23-54).
+ * Frequency encoding of the world position (10 levels) and of the direction
+ * (4 levels) (:252-277); density 64 -> 128 -> 128 x 4 -> 16; colour
+ * [raw density 1..15 | direction encoding 27 | 0 x 6] -> 128 -> 128 x 2 -> 16
+ * (3 used) (:918-943); fp16 weights packed [out][in], input layer first
+ * (:828-834, :1213-1241).  out [n][4] = (softplus(raw density 0), sigmoid of
+ * raw colour 0..2) (:909-917); raw (optional) [n][4] = the fp16-rounded raw
+ * outputs.  Init: :1810-1847 on these shapes. */
+NERF_API NerfStatus nerf_ext_ref_mlp_init(uint32_t network /* 0 density, 1 colour */, float* params_host);
+NERF_API NerfStatus nerf_ext_ref_field_forward(const uint16_t* density_params, const uint16_t* color_params, const float* positions, const float* directions, uint32_t n, float* out, float* raw, void* stream);
 /* The density and colour MLPs of nerf_ext_field_forward on given encodings:
  * features fp16 [n][32], unit directions [n][3] -> out [n][4] = (sigma, r, g, b).
  * The fused fp16-MFMA MLP pass on its own (no table gathers). */

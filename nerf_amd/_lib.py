@@ -122,6 +122,10 @@ class NerfCheckpointFileDesc(C.Structure):
 # ------------------------------------------------------------- nerf_ext.h
 NERF_EXT_F32 = 0
 NERF_EXT_F16 = 1
+NERF_EXT_MODEL_HASHGRID = 0
+NERF_EXT_MODEL_REFERENCE = 1
+NERF_EXT_REF_DENSITY_PARAMS = 75776
+NERF_EXT_REF_COLOR_PARAMS = 40960
 NERF_EXT_H2D = 1
 NERF_EXT_D2H = 2
 NERF_EXT_D2D = 3
@@ -171,6 +175,8 @@ class NerfExtModel(C.Structure):
         ("table", C.c_void_p),
         ("density_params", C.c_void_p),
         ("color_params", C.c_void_p),
+        ("kind", C.c_uint32),
+        ("reserved", C.c_uint32),
     ]
 
 
@@ -330,6 +336,8 @@ PROTOTYPES: dict[str, tuple] = {
     "nerf_ext_density_forward": (_S, [C.POINTER(NerfExtGridDesc), _P, _P, _P, _U32, _P, _P]),
     "nerf_ext_field_mlp": (_S, [_P, _P, _P, _P, _U32, _P, _P]),
     "nerf_ext_field_forward": (_S, [C.POINTER(NerfExtModel), _P, _P, _U32, _P, _P]),
+    "nerf_ext_ref_mlp_init": (_S, [_U32, _P]),
+    "nerf_ext_ref_field_forward": (_S, [_P, _P, _P, _P, _U32, _P, _P, _P]),
     # scene
     "nerf_ext_scene_gaussians": (_S, [C.POINTER(NerfExtSceneDesc), _P]),
     "nerf_ext_scene_density": (_S, [_P, _U32, _P, _U32, _P, _P]),

@@ -422,6 +422,8 @@ NERF_API NerfStatus nerf_ext_field_mlp(const uint16_t* density_params, const uin
 
 NERF_API NerfStatus nerf_ext_field_forward(const NerfExtModel* model, const float* positions, const float* directions, uint32_t n, float* out, void* stream) {
     NERF_CHECK_ARG(model, "nerf_ext_field_forward: null model");
+    NERF_CHECK_ARG(model->kind <= NERF_EXT_MODEL_REFERENCE, "nerf_ext_field_forward: unknown model kind");
+    if (model->kind == NERF_EXT_MODEL_REFERENCE) return nerf_ext_ref_field_forward(model->density_params, model->color_params, positions, directions, n, out, nullptr, stream);
     GridParams g;
     const NerfStatus s = make_grid(&model->grid, g);
     if (s != NERF_STATUS_OK) return s;

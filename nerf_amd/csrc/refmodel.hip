@@ -1,0 +1,340 @@
+// refmodel.hip — reference-model mode: the reference's own network
+// (backend-cuda.cu:23-54) behind the same field interface as the hash-grid
+// model.
+//
+//   encoding   frequency encoding of the world position, 10 levels, and of the
+//              ray direction, 4 levels (:252-277): [x, y, z, then per level
+//              sin x, sin y, sin z, cos x, cos y, cos z]
+//   density    64 (63 encoded values and a zero, :918-927) -> 128 -> 128 x 4
+//              -> 16, ReLU between layers, no biases
+//   colour     48 = [raw density outputs 1..15 | direction encoding (27) |
+//              0 x 6] (:928-943) -> 128 -> 128 x 2 -> 16 (3 used)
+//   outputs    sigma = softplus(raw density 0) (:913-917), rgb = sigmoid
+//              (:910-912)
+//
+// Rounding points: fp16 inputs, fp16 hidden activations, fp16 raw outputs
+// (the reference's output buffers are fp16); MFMA accumulation in fp32.
+//
+// Layout.  A layer computes out^T = W . in^T on v_mfma_f32_16x16x32_f16 with
+// 16 output rows of W as the A operand and 16 samples as the B operand, as the
+// hash-grid model's MLPs do: a layer's fp32 results, rounded to fp16 and
+// ReLU'd, are directly the next layer's B operand when the next layer's
+// weights are read with the matching k-permutation (KMap::Hidden).  The 128 x
+// 128 layers do not fit in registers or LDS (232 KiB of weights in all), so
+// the weights are packed once per call into A-fragment order — fragment
+// (row block r, k-block q) is 64 lanes x 8 halves = 1 KiB, contiguous — and
+// every A fragment is one coalesced 16-byte load per lane from L2.  A wave
+// works on 64 samples (four 16-sample tiles) per pass, so each A fragment
+// loaded serves four MFMAs: 232 KiB of weight reads per 64 samples.
+//
+// Encoding.  Lane l of a wave evaluates the 30 + 12 sincos pairs of sample l
+// of its group once and writes the sample's density input (64 halves) and
+// direction encoding (27 halves and zeros) as one LDS row; lane (g, s) of
+// tile t then reads its B operands back with 16-byte LDS loads.
+#include "mlp_device.hpp"
+
+namespace nerf_hip {
+namespace {
+
+using namespace mlp;
+
+constexpr uint32_t kRefDensityParams = NERF_EXT_REF_DENSITY_PARAMS;
+constexpr uint32_t kRefColorParams   = NERF_EXT_REF_COLOR_PARAMS;
+
+// Layers in consumption order: (rows out, columns in, k-blocks, row blocks,
+// k-map, first fragment, offset of W in its parameter set).
+enum RefMap : uint32_t { kMapIdentity = 0u, kMapHidden = 1u, kMapColorIn = 2u };
+struct RefLayer {
+    uint32_t n_out, n_in, kb, rb, map, frag0, w_off, network;
+};
+constexpr RefLayer kRefLayers[10] = {
+    {128u, 64u, 2u, 8u, kMapIdentity, 0u, 0u, 0u},    {128u, 128u, 4u, 8u, kMapHidden, 16u, 8192u, 0u},  {128u, 128u, 4u, 8u, kMapHidden, 48u, 24576u, 0u},
+    {128u, 128u, 4u, 8u, kMapHidden, 80u, 40960u, 0u}, {128u, 128u, 4u, 8u, kMapHidden, 112u, 57344u, 0u}, {16u, 128u, 4u, 1u, kMapHidden, 144u, 73728u, 0u},
+    {128u, 48u, 2u, 8u, kMapColorIn, 148u, 0u, 1u},    {128u, 128u, 4u, 8u, kMapHidden, 164u, 6144u, 1u}, {128u, 128u, 4u, 8u, kMapHidden, 196u, 22528u, 1u},
+    {16u, 128u, 4u, 1u, kMapHidden, 228u, 38912u, 1u},
+};
+static_assert(kRefLayers[5].w_off + 16u * 128u == kRefDensityParams, "density layout");
+static_assert(kRefLayers[9].w_off + 16u * 128u == kRefColorParams, "colour layout");
+
+// Input column of W for element j of lane group g in k-block q (-1: zero).
+__device__ __forceinline__ int ref_column(uint32_t map, uint32_t q, uint32_t g, uint32_t j) {
+    if (map == kMapIdentity) return (int)(32u * q + 8u * g + j);
+    if (map == kMapHidden) return (int)(32u * q + (j < 4u ? 4u * g + j : 16u + 4u * g + (j - 4u)));
+    if (q == 0u) {
+        if (j < 4u) {
+            const uint32_t o = 4u * g + j;  // raw density output o; output 0 (sigma) is not a colour input
+            return o == 0u ? -1 : (int)(o - 1u);
+        }
+        return (int)(15u + 4u * g + (j - 4u));  // direction encoding 4g .. 4g + 3
+    }
+    const uint32_t e = 16u + 8u * g + j;  // direction encoding 16 .. 47 (27 used)
+    return e < 27u ? (int)(15u + e) : -1;
+}
+
+// One workgroup of 64 threads per fragment.
+__global__ __launch_bounds__(64) void k_ref_pack(const half_t* __restrict__ dparams, const half_t* __restrict__ cparams, half8_t* __restrict__ frags) {
+    const uint32_t f = blockIdx.x, lane = threadIdx.x;
+    uint32_t li = 0u;
+#pragma unroll
+    for (uint32_t k = 1u; k < 10u; ++k)
+        if (f >= kRefLayers[k].frag0) li = k;
+    const RefLayer L   = kRefLayers[li];
+    const uint32_t loc = f - L.frag0, r = loc / L.kb, q = loc - r * L.kb;
+    const uint32_t i = lane & 15u, g = lane >> 4;
+    const half_t* row = (L.network == 0u ? dparams : cparams) + L.w_off + (16u * r + i) * L.n_in;
+    half8_t a;
+#pragma unroll
+    for (uint32_t j = 0; j < 8u; ++j) {
+        const int c = ref_column(L.map, q, g, j);
+        a[j]        = c < 0 ? (half_t)0.0f : row[c];
+    }
+    frags[(uint64_t)f * 64u + lane] = a;
+}
+
+// Weight fragments are read with buffer loads: one VGPR (lane * 16) and a
+// scalar fragment offset per load.  With plain pointers the compiler hoists
+// the 232 fragment addresses (two VGPRs each) out of the sample loop and
+// spills.  Word 3 of the descriptor is the gfx9-family raw-buffer format;
+// loads past num_records return zero.
+struct FragSrc {
+    __amdgpu_buffer_rsrc_t rsrc;
+    uint32_t voff;  // lane * 16
+};
+
+__device__ __forceinline__ FragSrc frag_src(const half8_t* frags, uint32_t lane) {
+    return FragSrc{__builtin_amdgcn_make_buffer_rsrc((void*)frags, (short)0, (int)(kRefFragments * 1024u), 0x00020000), lane * 16u};
+}
+
+__device__ __forceinline__ half8_t frag_load(const FragSrc& S, uint32_t f) {
+    return __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(S.rsrc, S.voff, f * 1024u, 0));
+}
+
+// A layer of 128 outputs (8 row blocks) on KB k-blocks of input, four tiles;
+// its fragments start at f0.
+template <uint32_t KB>
+__device__ __forceinline__ void ref_hidden(const FragSrc& S, uint32_t f0, const half8_t (&in)[4][4], half8_t (&out)[4][4]) {
+    half4_t lo[4];  // fp16 results of the even row block, joined with the odd one
+#pragma unroll
+    for (uint32_t r = 0; r < 8u; ++r) {
+        half8_t a[KB];
+#pragma unroll
+        for (uint32_t q = 0; q < KB; ++q) a[q] = frag_load(S, f0 + r * KB + q);
+        floatx4 acc[4];
+#pragma unroll
+        for (uint32_t t = 0; t < 4u; ++t) {
+            acc[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (uint32_t q = 0; q < KB; ++q) acc[t] = mfma16x16x32(a[q], in[t][q], acc[t]);
+        }
+        // Each output vector is written whole (never element-wise into its
+        // previous contents, which would keep those alive across the layer).
+#pragma unroll
+        for (uint32_t t = 0; t < 4u; ++t) {
+            const half4_t h = half4_t{to_half_rne(fmaxf(acc[t][0], 0.0f)), to_half_rne(fmaxf(acc[t][1], 0.0f)), to_half_rne(fmaxf(acc[t][2], 0.0f)), to_half_rne(fmaxf(acc[t][3], 0.0f))};
+            if (r & 1u) out[t][r >> 1] = half8_t{lo[t][0], lo[t][1], lo[t][2], lo[t][3], h[0], h[1], h[2], h[3]};
+            else lo[t] = h;
+        }
+        // One row block's weights in flight at a time: without the fence the
+        // scheduler hoists the next blocks' fragment loads and spills.
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// The 16-output layer: raw accumulators of the four tiles.
+__device__ __forceinline__ void ref_output(const FragSrc& S, uint32_t f0, const half8_t (&in)[4][4], floatx4 (&o)[4]) {
+    half8_t a[4];
+#pragma unroll
+    for (uint32_t q = 0; q < 4u; ++q) a[q] = frag_load(S, f0 + q);
+#pragma unroll
+    for (uint32_t t = 0; t < 4u; ++t) {
+        o[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (uint32_t q = 0; q < 4u; ++q) o[t] = mfma16x16x32(a[q], in[t][q], o[t]);
+    }
+}
+
+__device__ __forceinline__ float softplus_ref(float x) {
+    if (x > 20.0f) return x;
+    if (x < -20.0f) return expf(x);
+    return log1pf(expf(x));
+}
+
+// LDS row of one sample: density input [0, 64), direction encoding [64, 96)
+// (27 values, then zeros); pitch 104 halves (208 bytes): the 16-byte reads of
+// the 16 lanes of a lane group fall on distinct bank quads.
+constexpr uint32_t kRefPitch = 104u;
+
+// Frequency encoding of v into row[0, 3 + 6 levels) as fp16.  The level loop
+// stays rolled (three sincos per iteration): unrolled, the scheduler
+// interleaves all of them and the kernel spills.
+__device__ __forceinline__ void freq_row(const float v[3], uint32_t levels, half_t* row) {
+    row[0] = to_half_rne(v[0]);
+    row[1] = to_half_rne(v[1]);
+    row[2] = to_half_rne(v[2]);
+    float f = 1.0f;
+#pragma unroll 1
+    for (uint32_t l = 0; l < levels; ++l) {
+#pragma unroll
+        for (uint32_t a = 0; a < 3u; ++a) {
+            float s, c;
+            sincosf(v[a] * f, &s, &c);  // v * 2^l is exact
+            row[3u + 6u * l + a]      = to_half_rne(s);
+            row[3u + 6u * l + 3u + a] = to_half_rne(c);
+        }
+        f *= 2.0f;
+    }
+}
+
+template <bool kFromSamples>
+__global__ __launch_bounds__(kBlockThreads) void k_ref_field(const half8_t* __restrict__ frags, FieldInputs in, uint32_t n_cap, float4* __restrict__ out, float4* __restrict__ raw_out) {
+    const uint32_t n = in.n_dev ? min(*in.n_dev, n_cap) : n_cap;
+    __shared__ __align__(16) half_t rows[kBlockWaves][64 * kRefPitch];
+    const uint32_t lane = threadIdx.x & 63u, g = lane >> 4, s16 = lane & 15u, wv = threadIdx.x >> 6;
+    half_t* R           = rows[wv];
+    const FragSrc S     = frag_src(frags, lane);
+    const uint32_t groups = (n + 63u) / 64u;
+    for (uint32_t gi = blockIdx.x * kBlockWaves + wv; gi < groups; gi += gridDim.x * kBlockWaves) {
+        // Encoding: lane = sample.
+        {
+            const uint32_t q = min(gi * 64u + lane, n - 1u);
+            float p[3], d[3];
+            if constexpr (kFromSamples) {
+                const uint32_t qs = in.sample_index ? in.sample_index[q] : q;
+                const float2 td   = in.samples[qs];
+                const uint32_t r  = in.sample_ray[qs];
+                const float4 ro = in.rays[2ull * r], rd = in.rays[2ull * r + 1ull];
+                d[0] = rd.x;
+                d[1] = rd.y;
+                d[2] = rd.z;
+                p[0] = ro.x + td.x * rd.x;
+                p[1] = ro.y + td.x * rd.y;
+                p[2] = ro.z + td.x * rd.z;
+            } else {
+#pragma unroll
+                for (uint32_t a = 0; a < 3u; ++a) {
+                    p[a] = in.positions[3ull * q + a];
+                    d[a] = in.directions[3ull * q + a];
+                }
+            }
+            half_t* row = R + lane * kRefPitch;
+            freq_row(p, 10u, row);
+            row[63] = (half_t)0.0f;
+            freq_row(d, 4u, row + 64u);
+#pragma unroll
+            for (uint32_t k = 64u + 27u; k < 96u; ++k) row[k] = (half_t)0.0f;
+        }
+        __builtin_amdgcn_wave_barrier();  // LDS traffic of one wave completes in order
+        half8_t x[4][4], y[4][4];
+#pragma unroll
+        for (uint32_t t = 0; t < 4u; ++t) {
+            const half_t* r = R + (16u * t + s16) * kRefPitch;
+            x[t][0]         = *reinterpret_cast<const half8_t*>(r + 8u * g);
+            x[t][1]         = *reinterpret_cast<const half8_t*>(r + 32u + 8u * g);
+            x[t][2] = x[t][3] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+        }
+        // Density network.
+        ref_hidden<2>(S, kRefLayers[0].frag0, x, y);
+        ref_hidden<4>(S, kRefLayers[1].frag0, y, x);
+        ref_hidden<4>(S, kRefLayers[2].frag0, x, y);
+        ref_hidden<4>(S, kRefLayers[3].frag0, y, x);
+        ref_hidden<4>(S, kRefLayers[4].frag0, x, y);
+        floatx4 dens[4];
+        ref_output(S, kRefLayers[5].frag0, y, dens);
+        // Colour input: raw density outputs 4g..4g+3 (fp16) and direction
+        // encoding 4g..4g+3; then direction encoding 16 + 8g .. + 7.
+#pragma unroll
+        for (uint32_t t = 0; t < 4u; ++t) {
+            const half_t* r  = R + (16u * t + s16) * kRefPitch + 64u;
+            const half4_t de = *reinterpret_cast<const half4_t*>(r + 4u * g);
+            x[t][0]          = half8_t{to_half_rne(dens[t][0]), to_half_rne(dens[t][1]), to_half_rne(dens[t][2]), to_half_rne(dens[t][3]), de[0], de[1], de[2], de[3]};
+            x[t][1]          = g < 2u ? *reinterpret_cast<const half8_t*>(r + 16u + 8u * g) : half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+        }
+        __builtin_amdgcn_wave_barrier();  // the rows are rewritten by the next pass
+        ref_hidden<2>(S, kRefLayers[6].frag0, x, y);
+        ref_hidden<4>(S, kRefLayers[7].frag0, y, x);
+        ref_hidden<4>(S, kRefLayers[8].frag0, x, y);
+        floatx4 col[4];
+        ref_output(S, kRefLayers[9].frag0, y, col);
+        // Lane group 0 holds raw outputs 0..3 of both networks.
+        if (g == 0u) {
+#pragma unroll
+            for (uint32_t t = 0; t < 4u; ++t) {
+                const uint32_t st = gi * 64u + 16u * t + s16;
+                if (st < n) {
+                    const uint32_t dst = (kFromSamples && in.sample_index) ? in.sample_index[st] : st;
+                    const float rs = (float)to_half_rne(dens[t][0]);
+                    const float rr = (float)to_half_rne(col[t][0]), rg = (float)to_half_rne(col[t][1]), rb = (float)to_half_rne(col[t][2]);
+                    out[dst]           = make_float4(softplus_ref(rs), 1.0f / (1.0f + expf(-rr)), 1.0f / (1.0f + expf(-rg)), 1.0f / (1.0f + expf(-rb)));
+                    if (raw_out) raw_out[dst] = make_float4(rs, rr, rg, rb);
+                }
+            }
+        }
+    }
+}
+
+// Host-side Xavier-uniform init of backend-cuda.cu:1810-1847 on the
+// reference's own shapes.
+void ref_mlp_init_host(uint32_t network, float* out) {
+    const uint64_t state0 = network == 0u ? nerf_math::stream_state(0x1234ull, 0x5678ull) : nerf_math::stream_state(0x9abcull, 0xdef0ull);
+    uint64_t draw = 0, off = 0;
+    for (const RefLayer& L : kRefLayers) {
+        if (L.network != network) continue;
+        const float scale    = sqrtf(6.0f / (float)(L.n_in + L.n_out));
+        const uint64_t count = (uint64_t)L.n_in * L.n_out;
+        for (uint64_t i = 0; i < count; ++i, ++draw) {
+            const uint64_t z = nerf_math::splitmix_at(state0, draw);
+            out[off + i]     = ((float)((uint32_t)(z >> 32) >> 8) * (1.0f / 16777216.0f) * 2.0f - 1.0f) * scale;
+        }
+        off += count;
+    }
+}
+
+}  // namespace
+
+hipError_t ref_pack_weights(const half_t* dparams, const half_t* cparams, half8_t* frags, hipStream_t stream) {
+    k_ref_pack<<<kRefFragments, 64, 0, stream>>>(dparams, cparams, frags);
+    return hipGetLastError();
+}
+
+hipError_t launch_ref_field(const half8_t* frags, const FieldInputs& in, uint32_t n, float4* out, float4* raw, hipStream_t stream) {
+    if (n == 0u) return hipSuccess;
+    const uint32_t groups = (n + 63u) / 64u;
+    const uint32_t need   = (groups + kBlockWaves - 1u) / kBlockWaves;
+    const uint32_t cap    = device_cu_count() * 2u;
+    const uint32_t blocks = need < cap ? need : cap;
+    if (in.samples) k_ref_field<true><<<blocks, kBlockThreads, 0, stream>>>(frags, in, n, out, raw);
+    else k_ref_field<false><<<blocks, kBlockThreads, 0, stream>>>(frags, in, n, out, raw);
+    return hipGetLastError();
+}
+
+}  // namespace nerf_hip
+
+using namespace nerf_hip;
+
+extern "C" {
+
+NERF_API NerfStatus nerf_ext_ref_mlp_init(uint32_t network, float* params_host) {
+    NERF_CHECK_ARG(network <= 1u, "nerf_ext_ref_mlp_init: network must be 0 (density) or 1 (colour)");
+    NERF_CHECK_ARG(params_host, "nerf_ext_ref_mlp_init: null output");
+    ref_mlp_init_host(network, params_host);
+    return NERF_STATUS_OK;
+}
+
+NERF_API NerfStatus nerf_ext_ref_field_forward(const uint16_t* density_params, const uint16_t* color_params, const float* positions, const float* directions, uint32_t n, float* out, float* raw, void* stream) {
+    if (n == 0u) return NERF_STATUS_OK;
+    NERF_CHECK_ARG(density_params && color_params && positions && directions && out, "nerf_ext_ref_field_forward: null pointer");
+    hipStream_t st  = (hipStream_t)stream;
+    half8_t* frags = nullptr;
+    NERF_HIP_TRY(hipMallocAsync((void**)&frags, sizeof(half8_t) * 64u * kRefFragments, st));
+    FieldInputs in{};
+    in.positions  = positions;
+    in.directions = directions;
+    hipError_t e  = ref_pack_weights((const half_t*)density_params, (const half_t*)color_params, frags, st);
+    if (e == hipSuccess) e = launch_ref_field(frags, in, n, (float4*)out, (float4*)raw, st);
+    const hipError_t f = hipFreeAsync(frags, st);
+    NERF_HIP_TRY(e);
+    NERF_HIP_TRY(f);
+    return NERF_STATUS_OK;
+}
+
+}  // extern "C"

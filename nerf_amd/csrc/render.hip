@@ -414,6 +414,7 @@ struct NerfExtRenderer {
     Buf<uint32_t> list[2], n_active;   // active rays of this / the next round, and their counts
     Buf<uint32_t> cnt, off, qlist;     // samples per slot, their offsets, stream indices
     Buf<unsigned long long> round_total;
+    Buf<nerf_hip::half8_t> ref_frags;           // reference-model weights in MFMA fragment order
     hipEvent_t ev[6] = {};
     hipEvent_t fev[2 * kMaxRounds] = {};
     std::vector<uint32_t> host_sums;  // per-block sample counts (chunk plan)
@@ -506,11 +507,15 @@ NERF_API NerfStatus nerf_ext_render(NerfExtRenderer* R, const NerfExtRenderDesc*
     NERF_CHECK_ARG(R && d && d->model && d->occupancy && d->cameras && rgba8, "nerf_ext_render: null argument");
     NERF_CHECK_ARG(d->view_count >= 1u, "nerf_ext_render: view_count must be >= 1");
     NERF_CHECK_ARG(d->max_steps >= 1u && d->max_steps <= kMaxSteps, "nerf_ext_render: max_steps must be 1..2^19");
-    GridParams g;
-    const NerfStatus gs = make_grid(&d->model->grid, g);
-    if (gs != NERF_STATUS_OK) return gs;
-    NERF_CHECK_ARG(g.n_levels * g.n_features == 32u, "nerf_ext_render: the density MLP takes 32 features (16 levels x 2)");
-    NERF_CHECK_ARG(d->model->table && d->model->density_params && d->model->color_params, "nerf_ext_render: model has null buffers");
+    NERF_CHECK_ARG(d->model->kind <= NERF_EXT_MODEL_REFERENCE, "nerf_ext_render: unknown model kind");
+    const bool ref_model = d->model->kind == NERF_EXT_MODEL_REFERENCE;
+    GridParams g{};
+    if (!ref_model) {
+        const NerfStatus gs = make_grid(&d->model->grid, g);
+        if (gs != NERF_STATUS_OK) return gs;
+        NERF_CHECK_ARG(g.n_levels * g.n_features == 32u, "nerf_ext_render: the density MLP takes 32 features (16 levels x 2)");
+    }
+    NERF_CHECK_ARG((ref_model || d->model->table) && d->model->density_params && d->model->color_params, "nerf_ext_render: model has null buffers");
     const uint32_t W = d->cameras[0].width, H = d->cameras[0].height;
     for (uint32_t v = 0; v < d->view_count; ++v) NERF_CHECK_ARG(d->cameras[v].width == W && d->cameras[v].height == H && W > 0u && H > 0u, "nerf_ext_render: all views must share a non-empty image size");
     const uint64_t n64 = (uint64_t)W * H * d->view_count;
@@ -577,6 +582,10 @@ NERF_API NerfStatus nerf_ext_render(NerfExtRenderer* R, const NerfExtRenderDesc*
         in.bmax[a] = occ.omax[a];
     }
     const FieldWeights w{(const half_t*)d->model->density_params, (const half_t*)d->model->color_params};
+    if (ref_model) {
+        NERF_HIP_TRY(R->ref_frags.reserve(64ull * kRefFragments));
+        NERF_HIP_TRY(ref_pack_weights(w.density, w.color, R->ref_frags.ptr, st));
+    }
     const float3 bg = make_float3(d->background[0], d->background[1], d->background[2]);
     // Rounds: slices of 256, 256, 512, 1024, ... samples per active ray until
     // every ray's stream (at most max_steps samples) is covered.
@@ -626,7 +635,8 @@ NERF_API NerfStatus nerf_ext_render(NerfExtRenderer* R, const NerfExtRenderDesc*
             // word of the 64-bit scan total (little-endian; totals < 2^32).
             in.n_dev = reinterpret_cast<const uint32_t*>(R->round_total.ptr + r);
             if (timed) NERF_HIP_TRY(hipEventRecord(R->fev[2u * r], st));
-            NERF_HIP_TRY(launch_field(g, d->model->table, w, in, (uint32_t)c.samples, R->field.ptr, st));
+            if (ref_model) NERF_HIP_TRY(launch_ref_field(R->ref_frags.ptr, in, (uint32_t)c.samples, R->field.ptr, nullptr, st));
+            else NERF_HIP_TRY(launch_field(g, d->model->table, w, in, (uint32_t)c.samples, R->field.ptr, st));
             if (timed) NERF_HIP_TRY(hipEventRecord(R->fev[2u * r + 1u], st));
             k_round_composite<<<ray_waves, 256, 0, st>>>(l_cur, n_cur, R->counts.ptr, R->offsets.ptr, R->samples.ptr, R->field.ptr, Ss[r], Ks[r], d->min_transmittance, bg, R->state.ptr, rgba8, rgb_f32, l_nxt, n_nxt);
             NERF_LAUNCH_CHECK("k_round_composite");

@@ -337,6 +337,8 @@ NERF_API NerfStatus nerf_ext_trainer_model(NerfExtTrainer* trainer, NerfExtModel
         model->table          = t.B.table;
         model->density_params = (const uint16_t*)t.B.dparams;
         model->color_params   = (const uint16_t*)t.B.cparams;
+        model->kind           = NERF_EXT_MODEL_HASHGRID;
+        model->reserved       = 0u;
     }
     if (occ) {
         occ->bitfield   = t.B.bits;

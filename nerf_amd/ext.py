@@ -74,6 +74,38 @@ class Model:
         return L.NerfExtModel(self.grid, self.table.ptr, self.density.ptr, self.color.ptr)
 
 
+def ref_mlp_init(network: int) -> np.ndarray:
+    """The reference's init (backend-cuda.cu:1810-1847) on its own network."""
+    n = L.NERF_EXT_REF_DENSITY_PARAMS if network == 0 else L.NERF_EXT_REF_COLOR_PARAMS
+    out = np.empty(n, np.float32)
+    L.call("nerf_ext_ref_mlp_init", network, out.ctypes.data)
+    return out
+
+
+@dataclass
+class RefModel:
+    """Reference-model mode: the reference's own network (frequency encoding,
+    128-wide MLPs, softplus density) with fp16 weights on the device."""
+
+    density_f32: np.ndarray
+    color_f32: np.ndarray
+    density: DeviceArray
+    color: DeviceArray
+
+    @classmethod
+    def create(cls, density_f32: np.ndarray | None = None, color_f32: np.ndarray | None = None) -> "RefModel":
+        d32 = ref_mlp_init(0) if density_f32 is None else np.asarray(density_f32, np.float32)
+        c32 = ref_mlp_init(1) if color_f32 is None else np.asarray(color_f32, np.float32)
+        return cls(d32, c32, DeviceArray.from_numpy(d32.astype(np.float16)), DeviceArray.from_numpy(c32.astype(np.float16)))
+
+    def struct(self) -> L.NerfExtModel:
+        m = L.NerfExtModel()
+        m.density_params = self.density.ptr
+        m.color_params = self.color.ptr
+        m.kind = L.NERF_EXT_MODEL_REFERENCE
+        return m
+
+
 def scene_gaussians(count: int, seed: int = 0, centre=(0.2, 0.8), sigma=(0.02, 0.1), amplitude=(5.0, 50.0)) -> np.ndarray:
     """Analytic scene records as a structured array (cx cy cz sigma A r g b)."""
     desc = L.NerfExtSceneDesc(count, 0, seed, centre[0], centre[1], sigma[0], sigma[1], amplitude[0], amplitude[1])
@@ -123,7 +155,7 @@ class Renderer:
         self._h = C.c_void_p()
         L.call("nerf_ext_renderer_create", C.byref(self._h))
 
-    def render(self, model: Model, occupancy: L.NerfExtOccupancy, cameras: list, max_steps: int, min_transmittance: float = 1e-4, background=(1.0, 1.0, 1.0), rgba8: DeviceArray | None = None, rgb: DeviceArray | None = None,
+    def render(self, model: "Model | RefModel", occupancy: L.NerfExtOccupancy, cameras: list, max_steps: int, min_transmittance: float = 1e-4, background=(1.0, 1.0, 1.0), rgba8: DeviceArray | None = None, rgb: DeviceArray | None = None,
                counts: DeviceArray | None = None, stream: Stream | None = None, timed: bool = False, chunk_samples: int = 0):
         n_views = len(cameras)
         w, h = cameras[0].width, cameras[0].height

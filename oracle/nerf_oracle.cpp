@@ -657,7 +657,10 @@ struct OrcModel {
     const void* table;
     const uint16_t* density_params;
     const uint16_t* color_params;
+    uint32_t kind;  // 0 hash grid, 1 the reference's own network (world positions)
 };
+
+static void ref_field_point(const uint16_t* dp, const uint16_t* cp, const float* p, const float* d, float* out4, float* raw4);
 
 // The field sees positions normalised to the outermost cascade's box,
 // (w - lo) / (hi - lo) per axis (exact for the unit box).
@@ -686,7 +689,8 @@ extern "C" void orc_render_rays(const OrcModel* model, const OrcCamera* cam, con
                 float p[3];
                 for (int a = 0; a < 3; ++a) p[a] = (wp[a] - occ.omin[a]) / (occ.omax[a] - occ.omin[a]);
                 float s4[4];
-                field_point(model->grid, model->table, model->density_params, model->color_params, p, r.d, s4);
+                if (model->kind == 1u) ref_field_point(model->density_params, model->color_params, wp, r.d, s4, nullptr);
+                else field_point(model->grid, model->table, model->density_params, model->color_params, p, r.d, s4);
                 const float a = 1.0f - expf(-(s4[0] * fmaxf(dt, 0.0f)));
                 const float w = T * a;
                 for (int c = 0; c < 3; ++c) C[c] += w * s4[1 + c];
@@ -1037,4 +1041,107 @@ extern "C" void orc_field_mlp(const uint16_t* dparams, const uint16_t* cparams, 
         out4[2]     = rgb[1];
         out4[3]     = rgb[2];
     }
+}
+
+// ===========================================================================
+// Reference-model mode: the reference's own network (backend-cuda.cu:23-54).
+// Frequency encoding of the world position (10 levels) and of the direction
+// (4 levels) (:252-277); density MLP 64 -> 128 -> 128 x 4 -> 16 on the 63
+// encoded values and a zero (:918-927); colour MLP on [raw density outputs
+// 1..15 | direction encoding (27) | 0 x 6] (:928-943) -> 128 -> 128 x 2 -> 16
+// (3 used); sigma = softplus(raw 0) (:913-917), rgb = sigmoid(raw) (:910-912).
+// Rounding points: fp16 inputs, fp16 hidden activations and fp16 raw outputs
+// (the reference's output buffers are fp16, :1063-1083); accumulation in fp64.
+// ===========================================================================
+static const uint32_t kRefDensity[6][2] = {{128u, 64u}, {128u, 128u}, {128u, 128u}, {128u, 128u}, {128u, 128u}, {16u, 128u}};
+static const uint32_t kRefColor[4][2]   = {{128u, 48u}, {128u, 128u}, {128u, 128u}, {16u, 128u}};
+
+extern "C" uint32_t orc_ref_param_count(uint32_t network) { return network == 0u ? 75776u : 40960u; }
+
+// The reference's Xavier-uniform init (:1810-1847) on its own shapes.
+extern "C" void orc_ref_mlp_init(uint32_t network, float* out) {
+    const uint32_t n_mat = network == 0u ? 6u : 4u;
+    uint64_t state       = network == 0u ? orc_stream_state(0x1234ull, 0x5678ull) : orc_stream_state(0x9abcull, 0xdef0ull);
+    uint64_t off         = 0;
+    for (uint32_t m = 0; m < n_mat; ++m) {
+        const uint32_t fan_out = network == 0u ? kRefDensity[m][0] : kRefColor[m][0];
+        const uint32_t fan_in  = network == 0u ? kRefDensity[m][1] : kRefColor[m][1];
+        const float scale      = sqrtf(6.0f / (float)(fan_in + fan_out));
+        for (uint64_t i = 0; i < (uint64_t)fan_in * fan_out; ++i) {
+            state += 0x9e3779b97f4a7c15ull;
+            uint64_t z = state;
+            z          = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+            z          = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+            z ^= z >> 31;
+            out[off + i] = ((float)((uint32_t)(z >> 32) >> 8) * (1.0f / 16777216.0f) * 2.0f - 1.0f) * scale;
+        }
+        off += (uint64_t)fan_in * fan_out;
+    }
+}
+
+// [x, y, z, then per level l: sin(2^l x), sin(2^l y), sin(2^l z), cos(2^l x),
+// cos(2^l y), cos(2^l z)] (:252-277).  The argument x * 2^l is exact in fp32;
+// sin and cos of it are correctly rounded to fp32 (fp64 evaluation).
+extern "C" void orc_freq_encode(const float* p, uint32_t levels, float* out) {
+    out[0] = p[0];
+    out[1] = p[1];
+    out[2] = p[2];
+    float freq = 1.0f;
+    for (uint32_t l = 0; l < levels; ++l) {
+        for (int a = 0; a < 3; ++a) {
+            const double arg    = (double)(p[a] * freq);
+            out[3 + 6 * l + a]     = (float)sin(arg);
+            out[3 + 6 * l + 3 + a] = (float)cos(arg);
+        }
+        freq *= 2.0f;
+    }
+}
+
+// softplus with the reference's branches (:913-917), evaluated in fp64.
+extern "C" float orc_softplus(float x) {
+    if (x > 20.0f) return x;
+    if (x < -20.0f) return (float)exp((double)x);
+    return (float)log1p(exp((double)x));
+}
+
+static float sigmoid64(float x) { return (float)(1.0 / (1.0 + exp(-(double)x))); }
+
+// Layers of one network on an fp16-valued input row; out = fp16-rounded raw
+// outputs of the last layer.
+static void ref_mlp_row(const uint16_t* W, const uint32_t (*shape)[2], uint32_t layers, const float* x_in, float* out) {
+    std::vector<float> a(x_in, x_in + shape[0][1]), b;
+    uint64_t off = 0;
+    for (uint32_t m = 0; m < layers; ++m) {
+        b.assign(shape[m][0], 0.0f);
+        matvec(W + off, shape[m][0], shape[m][1], a.data(), b.data());
+        off += (uint64_t)shape[m][0] * shape[m][1];
+        for (float& v : b) v = m + 1u < layers ? r16(fmaxf(v, 0.0f)) : r16(v);
+        a.swap(b);
+    }
+    std::copy(a.begin(), a.end(), out);
+}
+
+static void ref_field_point(const uint16_t* dp, const uint16_t* cp, const float* p, const float* d, float* out4, float* raw4) {
+    float pe[64], de[27], dens[16], ci[48], col[16];
+    orc_freq_encode(p, 10u, pe);
+    for (int k = 0; k < 63; ++k) pe[k] = r16(pe[k]);
+    pe[63] = 0.0f;
+    ref_mlp_row(dp, kRefDensity, 6u, pe, dens);
+    orc_freq_encode(d, 4u, de);
+    for (int k = 0; k < 15; ++k) ci[k] = dens[1 + k];
+    for (int k = 0; k < 27; ++k) ci[15 + k] = r16(de[k]);
+    for (int k = 42; k < 48; ++k) ci[k] = 0.0f;
+    ref_mlp_row(cp, kRefColor, 4u, ci, col);
+    out4[0] = orc_softplus(dens[0]);
+    for (int c = 0; c < 3; ++c) out4[1 + c] = sigmoid64(col[c]);
+    if (raw4) {
+        raw4[0] = dens[0];
+        for (int c = 0; c < 3; ++c) raw4[1 + c] = col[c];
+    }
+}
+
+// out [n][4] = (sigma, r, g, b); raw (optional) [n][4] = fp16-rounded raw
+// density output 0 and colour outputs 0..2.  Positions in world coordinates.
+extern "C" void orc_ref_field_forward(const uint16_t* dparams, const uint16_t* cparams, const float* pos, const float* dirs, uint32_t n, float* out, float* raw) {
+    for (uint32_t i = 0; i < n; ++i) ref_field_point(dparams, cparams, pos + 3ull * i, dirs + 3ull * i, out + 4ull * i, raw ? raw + 4ull * i : nullptr);
 }

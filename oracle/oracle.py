@@ -45,6 +45,7 @@ class OrcModel(C.Structure):
         ("table", C.c_void_p),
         ("density_params", C.c_void_p),
         ("color_params", C.c_void_p),
+        ("kind", C.c_uint32),
     ]
 
 
@@ -70,6 +71,11 @@ _PROTOS = {
     "orc_density_forward": (None, [C.POINTER(OrcGrid), _P, _P, _P, _U32, _P]),
     "orc_sh4": (None, [_P, _P]),
     "orc_field_forward": (None, [C.POINTER(OrcGrid), _P, _P, _P, _P, _P, _U32, _P]),
+    "orc_ref_param_count": (_U32, [_U32]),
+    "orc_ref_mlp_init": (None, [_U32, _P]),
+    "orc_freq_encode": (None, [_P, _U32, _P]),
+    "orc_softplus": (_F, [_F]),
+    "orc_ref_field_forward": (None, [_P, _P, _P, _P, _U32, _P, _P]),
     "orc_det_expf": (_F, [_F]),
     "orc_det_expf_array": (None, [_P, _U64, _P]),
     "orc_scene_density": (None, [_P, _U32, _P, _U32, _P]),
@@ -209,6 +215,41 @@ def field_forward(grid: OrcGrid, table: np.ndarray, dparams_bits: np.ndarray, cp
     return out
 
 
+def ref_param_count(network: int) -> int:
+    return int(lib().orc_ref_param_count(network))
+
+
+def ref_mlp_init(network: int) -> np.ndarray:
+    """The reference's init (backend-cuda.cu:1810-1847) on its own shapes."""
+    out = np.empty(lib().orc_ref_param_count(network), np.float32)
+    lib().orc_ref_mlp_init(network, _p(out))
+    return out
+
+
+def freq_encode(p: np.ndarray, levels: int) -> np.ndarray:
+    p = np.ascontiguousarray(p, np.float32).reshape(-1, 3)
+    out = np.empty((p.shape[0], 3 + 6 * levels), np.float32)
+    for i in range(p.shape[0]):
+        lib().orc_freq_encode(_p(p[i]), levels, _p(out[i]))
+    return out
+
+
+def softplus(x: float) -> float:
+    return float(lib().orc_softplus(float(x)))
+
+
+def ref_field_forward(dparams_bits: np.ndarray, cparams_bits: np.ndarray, pos: np.ndarray, dirs: np.ndarray):
+    """Reference-model field at world positions: (out [n][4] = (sigma, r, g,
+    b), raw [n][4] = fp16-rounded raw density 0 and colour 0..2)."""
+    pos = np.ascontiguousarray(pos, np.float32)
+    dirs = np.ascontiguousarray(dirs, np.float32)
+    n = pos.shape[0]
+    out = np.empty((n, 4), np.float32)
+    raw = np.empty((n, 4), np.float32)
+    lib().orc_ref_field_forward(_p(np.ascontiguousarray(dparams_bits)), _p(np.ascontiguousarray(cparams_bits)), _p(pos), _p(dirs), n, _p(out), _p(raw))
+    return out, raw
+
+
 def det_expf(x) -> np.ndarray:
     x = np.ascontiguousarray(x, np.float32)
     out = np.empty_like(x)
@@ -301,11 +342,15 @@ def composite_ray(sigma_rgb: np.ndarray, dt: np.ndarray, t_stop: float = 1e-4, b
     return rgb, int(rgba[0]), int(used)
 
 
-def render_rays(grid: OrcGrid, table: np.ndarray, dparams_bits: np.ndarray, cparams_bits: np.ndarray, cam: OrcCamera, bits: np.ndarray | None, res: int, aabb, max_steps: int, rays: np.ndarray, t_stop: float = 1e-4, bg=(1.0, 1.0, 1.0),
-                threads: int = 1, cascades: int = 1):
+def render_rays(grid: OrcGrid | None, table: np.ndarray | None, dparams_bits: np.ndarray, cparams_bits: np.ndarray, cam: OrcCamera, bits: np.ndarray | None, res: int, aabb, max_steps: int, rays: np.ndarray, t_stop: float = 1e-4,
+                bg=(1.0, 1.0, 1.0), threads: int = 1, cascades: int = 1, kind: int = 0):
+    """kind 0: hash-grid model (grid, table); kind 1: the reference's own
+    network (ref_* parameter sets; grid and table unused)."""
     model = OrcModel()
-    model.grid = grid
-    model.table = _p(table)
+    if grid is not None:
+        model.grid = grid
+    model.table = _p(table) if table is not None else None
+    model.kind = kind
     model.density_params = _p(dparams_bits)
     model.color_params = _p(cparams_bits)
     rays = np.ascontiguousarray(rays, np.uint32)

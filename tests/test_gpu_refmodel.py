@@ -1,0 +1,123 @@
+"""Reference-model mode on the GPU (the reference's own network,
+backend-cuda.cu:23-54): fused frequency encoding + 128-wide fp16 MFMA MLPs
+against the oracle (fp64 accumulation, same fp16 rounding points).
+
+Tolerance.  Ten layers of 128 fp16-rounded activations: where the GPU's fp32
+accumulation (or its sin/cos, within a few ulp) lands on the other side of an
+fp16 rounding tie than the oracle's fp64 sum, the 1-ulp difference is carried
+through the later layers.  Measured on 20,000 samples: 95 % of rows of raw
+outputs bit-identical, the rest spread over every lane (no layout pattern),
+max 0.9 % (reference init) / 1.4 % (weights x 1.5); (sigma, rgb) within
+3.1e-4 at the reference init.  So: (sigma, rgb) within 1e-3 relative at the
+reference init; raw outputs >= 90 % of rows bit-identical, 99th percentile
+of the row error <= 5e-3, max <= 3e-2.  Layouts are pinned exactly by
+structured weights with closed-form outputs."""
+import numpy as np
+import pytest
+
+from conftest import announce
+from helpers import L, ext, orc, DeviceArray, synchronize, byref, assert_rel
+from refmodel_cases import structured, structured_raw, unit_dirs, world_points
+
+pytestmark = pytest.mark.gpu
+
+BOX = (0.0, 0.0, 0.0, 1.0, 1.0, 1.0)
+CENTRE = (0.5, 0.5, 0.5)
+
+
+def _ref_model(scale=1.5):
+    return ext.RefModel.create(ext.ref_mlp_init(0) * scale, ext.ref_mlp_init(1) * scale)
+
+
+def _bits(m):
+    return m.density.numpy().view(np.uint16), m.color.numpy().view(np.uint16)
+
+
+def _forward(m, pos, dirs, use_model_kind=False):
+    n = pos.shape[0]
+    d_p, d_d = DeviceArray.from_numpy(pos), DeviceArray.from_numpy(dirs)
+    d_o, d_r = DeviceArray((n, 4), np.float32), DeviceArray((n, 4), np.float32)
+    if use_model_kind:
+        ms = m.struct()
+        L.call("nerf_ext_field_forward", byref(ms), d_p.ptr, d_d.ptr, n, d_o.ptr, None)
+        synchronize()
+        return d_o.numpy(), None
+    L.call("nerf_ext_ref_field_forward", m.density.ptr, m.color.ptr, d_p.ptr, d_d.ptr, n, d_o.ptr, d_r.ptr, None)
+    synchronize()
+    return d_o.numpy(), d_r.numpy()
+
+
+def assert_raw_parity(got, want, what, min_exact=0.9):
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    assert np.isfinite(got).all(), f"{what}: non-finite GPU output"
+    floor = max(0.1 * float(np.sqrt(np.mean(want ** 2))), 1e-6)
+    row = (np.abs(got - want) / np.maximum(np.abs(want), floor)).max(1)
+    exact = float(np.mean(row == 0))
+    assert exact >= min_exact and np.quantile(row, 0.99) <= 5e-3 and row.max() <= 3e-2, (what, exact, np.quantile(row, 0.99), row.max(), int(np.argmax(row)))
+
+
+def test_ref_init_bit_exact_with_oracle():
+    for net in (0, 1):
+        assert np.array_equal(ext.ref_mlp_init(net).view(np.uint32), orc.ref_mlp_init(net).view(np.uint32))
+
+
+@pytest.mark.parametrize("n", [4099, 1000, 64, 1])
+def test_ref_field_forward(n):
+    announce(f"reference-model field forward n={n}")
+    m = _ref_model()
+    pos, dirs = world_points(n, 21), unit_dirs(n, 22)
+    out, raw = _forward(m, pos, dirs)
+    want_out, want_raw = orc.ref_field_forward(*_bits(m), pos, dirs)
+    assert_raw_parity(raw, want_raw, "reference-model raw outputs, weights x 1.5")
+    # Activations in fp32 (expf, log1pf) differ from the oracle's fp64 in the
+    # last bits, so no bit-identical fraction is asked of them.
+    assert_raw_parity(out, want_out, "reference-model (sigma, rgb), weights x 1.5", min_exact=0.0)
+
+
+def test_ref_field_forward_init_weights_and_model_kind():
+    n = 3000
+    announce(f"reference-model field forward, reference init, via model kind n={n}")
+    m = ext.RefModel.create()
+    pos, dirs = world_points(n, 23), unit_dirs(n, 24)
+    out, raw = _forward(m, pos, dirs)
+    out_kind, _ = _forward(m, pos, dirs, use_model_kind=True)
+    assert np.array_equal(out.view(np.uint32), out_kind.view(np.uint32))
+    want_out, want_raw = orc.ref_field_forward(*_bits(m), pos, dirs)
+    assert_rel(out, want_out, what="reference-model (sigma, rgb), reference init")
+    assert_raw_parity(raw, want_raw, "reference-model raw outputs, reference init")
+
+
+def test_ref_structured_weights_closed_form():
+    n = 777
+    announce(f"reference-model structured weights n={n}")
+    dp, cp = structured()
+    m = ext.RefModel(None, None, DeviceArray.from_numpy(dp), DeviceArray.from_numpy(cp))
+    pos, dirs = world_points(n, 25, 0.05, 1.5), unit_dirs(n, 26)
+    _, raw = _forward(m, pos, dirs)
+    want = structured_raw(pos, dirs)
+    assert np.array_equal(raw[:, 1], want[:, 1]) and np.array_equal(raw[:, 3], want[:, 3])
+    # sin/cos on the GPU are within a few fp32 ulp of the correctly rounded
+    # value, so an fp16 rounding may differ by one fp16 ulp.
+    np.testing.assert_allclose(raw[:, [0, 2]], want[:, [0, 2]], rtol=1e-3, atol=1e-3)
+
+
+@pytest.mark.parametrize("w,h,views", [(24, 20, 1), (16, 12, 2)])
+def test_ref_render_parity(w, h, views):
+    announce(f"reference-model render {w}x{h} views={views}")
+    g = ext.scene_gaussians(32, seed=0)
+    bits = ext.occupancy_from_scene(g, 128)
+    m = _ref_model(1.0)
+    cams = [ext.camera_orbit(0, i, 1.32, CENTRE, w, h, 1111.0 * w / 800.0) for i in range(views)]
+    occ = ext.occupancy_struct(bits, 128)
+    rgb = DeviceArray((views, h, w, 3), np.float32)
+    counts = DeviceArray((views, h, w), np.uint32)
+    rgba, stats = ext.Renderer().render(m, occ, cams, 512, rgb=rgb, counts=counts, timed=True)
+    synchronize()
+    dp, cp = _bits(m)
+    got_rgb, got_counts = rgb.numpy().reshape(views, -1, 3), counts.numpy().reshape(views, -1)
+    assert stats.samples == int(got_counts.sum()) > 0
+    for v in range(views):
+        ocam = orc.camera_from_bytes(bytes(cams[v]))
+        want_rgb, _, want_counts = orc.render_rays(None, None, dp, cp, ocam, bits.numpy(), 128, BOX, 512, np.arange(w * h, dtype=np.uint32), threads=8, kind=1)
+        assert np.array_equal(got_counts[v], want_counts)
+        assert_rel(got_rgb[v], want_rgb, what=f"reference-model render rgb view {v}")

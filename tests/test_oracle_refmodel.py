@@ -1,0 +1,108 @@
+"""Oracle pins of the reference-model mode (the reference's own network,
+backend-cuda.cu:23-54): init = the reference loop restated, frequency
+encoding = closed forms, softplus branches, the MLP against an fp64 numpy
+GEMM with the same fp16 rounding points, and structured weights whose
+outputs have closed forms (input layouts of :918-943)."""
+import numpy as np
+
+from refmodel_cases import COLOR_SHAPES, DENSITY_SHAPES, structured, structured_raw, unit_dirs, world_points
+
+
+def test_ref_init_matches_reference_loop(orc):
+    for net, shapes, (a, b) in [(0, DENSITY_SHAPES, (0x1234, 0x5678)), (1, COLOR_SHAPES, (0x9ABC, 0xDEF0))]:
+        total = sum(o * i for o, i in shapes)
+        assert orc.ref_param_count(net) == total
+        z = orc.splitmix_sequence(orc.lib().orc_stream_state(a, b), total)
+        u = ((z >> np.uint64(32)).astype(np.uint32) >> np.uint32(8)).astype(np.float32) * np.float32(1.0 / 16777216.0)
+        want, off = [], 0
+        for o, i in shapes:
+            scale = np.sqrt(np.float32(6.0) / np.float32(o + i)).astype(np.float32)
+            want.append(((u[off:off + o * i] * np.float32(2.0) - np.float32(1.0)) * scale).astype(np.float32))
+            off += o * i
+        assert np.array_equal(orc.ref_mlp_init(net), np.concatenate(want))
+    assert orc.ref_param_count(0) == 75776 and orc.ref_param_count(1) == 40960
+
+
+def test_freq_encode_closed_forms(orc):
+    # Zero: sin = 0, cos = 1 on every level.
+    e = orc.freq_encode(np.zeros(3), 10)[0]
+    assert e.shape == (63,)
+    assert np.array_equal(e[:3], np.zeros(3)) and np.all(e[3:].reshape(10, 6)[:, :3] == 0) and np.all(e[3:].reshape(10, 6)[:, 3:] == 1)
+    # pi/4 on x: level l holds sin/cos of 2^l pi/4 (x first, then y, z).
+    p = np.array([np.pi / 4, 0.0, 0.0], np.float32)
+    e = orc.freq_encode(p, 4)[0].reshape(-1)
+    arg = [np.float32(p[0]) * np.float32(2.0 ** l) for l in range(4)]
+    for l in range(4):
+        assert e[3 + 6 * l] == np.float32(np.sin(np.float64(arg[l])))
+        assert e[3 + 6 * l + 3] == np.float32(np.cos(np.float64(arg[l])))
+        assert e[3 + 6 * l + 1] == 0 and e[3 + 6 * l + 4] == 1
+    assert abs(e[3 + 6 * 1] - 1.0) < 1e-7          # sin(pi/2)
+    assert abs(e[3 + 6 * 2 + 3] + 1.0) < 1e-7      # cos(pi)
+    # Random points: identity first, then sin^2 + cos^2 = 1 per axis/level.
+    pts = world_points(200, 1)
+    e = orc.freq_encode(pts, 10)
+    assert np.array_equal(e[:, :3], pts)
+    lv = e[:, 3:].reshape(-1, 10, 6).astype(np.float64)
+    assert np.abs(lv[..., :3] ** 2 + lv[..., 3:] ** 2 - 1).max() < 1e-6
+
+
+def test_softplus_branches(orc):
+    assert abs(orc.softplus(0.0) - np.log(2.0)) < 1e-7
+    assert orc.softplus(25.0) == 25.0
+    assert orc.softplus(-25.0) == np.float32(np.exp(-25.0))
+    assert abs(orc.softplus(20.0) - 20.0) < 1e-5
+    assert abs(orc.softplus(-3.0) - np.log1p(np.exp(-3.0))) < 1e-7
+
+
+def _f16(x):
+    return np.asarray(x, np.float32).astype(np.float16).astype(np.float32)
+
+
+def _numpy_ref(dp, cp, pos, dirs):
+    def net(bits, shapes, x):
+        W = bits.view(np.float16).astype(np.float64)
+        off = 0
+        for m, (o, i) in enumerate(shapes):
+            A = W[off:off + o * i].reshape(o, i)
+            off += o * i
+            y = (x.astype(np.float64) @ A.T).astype(np.float32)
+            x = _f16(np.maximum(y, 0) if m + 1 < len(shapes) else y)
+        return x
+    n = pos.shape[0]
+    lv = np.arange(10, dtype=np.float32)
+    args = pos[:, None, :] * (np.float32(2.0) ** lv)[None, :, None]          # [n][10][3], exact
+    pe = np.concatenate([pos, np.concatenate([np.sin(args.astype(np.float64)), np.cos(args.astype(np.float64))], 2).astype(np.float32).reshape(n, -1)], 1)
+    pe = _f16(np.concatenate([pe[:, :63], np.zeros((n, 1), np.float32)], 1))
+    dens = net(dp, DENSITY_SHAPES, pe)
+    dl = np.arange(4, dtype=np.float32)
+    dargs = dirs[:, None, :] * (np.float32(2.0) ** dl)[None, :, None]
+    de = np.concatenate([dirs, np.concatenate([np.sin(dargs.astype(np.float64)), np.cos(dargs.astype(np.float64))], 2).astype(np.float32).reshape(n, -1)], 1)
+    ci = np.concatenate([dens[:, 1:16], _f16(de), np.zeros((n, 6), np.float32)], 1)
+    col = net(cp, COLOR_SHAPES, ci)
+    raw = np.stack([dens[:, 0], col[:, 0], col[:, 1], col[:, 2]], 1)
+    x = raw[:, 0].astype(np.float64)
+    sp = np.where(x > 20, x, np.where(x < -20, np.exp(x), np.log1p(np.exp(np.clip(x, -20, 20)))))
+    out = np.concatenate([sp[:, None], 1.0 / (1.0 + np.exp(-raw[:, 1:].astype(np.float64)))], 1)
+    return out.astype(np.float32), raw
+
+
+def test_ref_field_matches_fp64_numpy(orc):
+    dp = orc.f32_to_f16_bits(orc.ref_mlp_init(0) * 1.5)   # larger weights: raw outputs of order 1
+    cp = orc.f32_to_f16_bits(orc.ref_mlp_init(1) * 1.5)
+    pos, dirs = world_points(300, 2), unit_dirs(300, 3)
+    out, raw = orc.ref_field_forward(dp, cp, pos, dirs)
+    want_out, want_raw = _numpy_ref(dp, cp, pos, dirs)
+    # fp64 accumulation on both sides; a rare fp16 tie of a hidden activation
+    # may round differently in the last place.
+    scale = np.abs(want_raw).max()
+    assert np.abs(raw - want_raw).max() <= 2e-3 * scale
+    assert np.median(np.abs(raw - want_raw)) == 0.0
+    np.testing.assert_allclose(out, want_out, rtol=2e-3, atol=1e-5)
+
+
+def test_ref_structured_weights_closed_form(orc):
+    dp, cp = structured()
+    pos = world_points(500, 4, 0.05, 1.5)          # x > 0
+    dirs = unit_dirs(500, 5)
+    _, raw = orc.ref_field_forward(dp, cp, pos, dirs)
+    assert np.array_equal(raw, structured_raw(pos, dirs))
