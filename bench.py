@@ -62,10 +62,14 @@ FIELD_FLOPS_PER_SAMPLE = 2 * (32 * 64 + 64 * 16) + 2 * (31 * 64 + 64 * 64 + 64 *
 # HBM traffic of the field kernel per sample on this workload, from rocprofv3
 # FETCH_SIZE (x 2.0) + WRITE_SIZE (x 1.0) on one 800x800 render, the factors
 # being what the same counters read on a plain conversion kernel of known
-# size (profiles/field_forward_800x800_hbm_traffic.md): 858.3 GB + 8.4 GB over
+# size (profiles/field_forward_800x800_hbm_traffic.md): 791.9 GB + 8.0 GB over
 # 486,308,861 samples, summed over the render's three rounds.  Every 4-byte table gather pulls a whole line from
 # beyond L2, hence the gap to the 540 algorithmic bytes.
-FIELD_TRAFFIC_BYTES_PER_SAMPLE = 1782
+FIELD_TRAFFIC_BYTES_PER_SAMPLE = 1645
+# Reference-model network per sample, on the reference's own padded shapes
+# (backend-cuda.cu:23-54): density 64x128 + 4 x 128x128 + 128x16, colour
+# 48x128 + 2 x 128x128 + 128x16, two flops per multiply-add.
+REF_FLOPS_PER_SAMPLE = 2 * (64 * 128 + 4 * 128 * 128 + 128 * 16) + 2 * (48 * 128 + 2 * 128 * 128 + 128 * 16)
 
 
 def build_workload():
@@ -141,7 +145,39 @@ def kernel_rooflines(reps_small: int = 200):
         out[label] = {"kernel": "k_field_mlp (density 32-64-16 + colour 32-64-64-16, fp16 MFMA)", "samples": n, "ms": round(ms, 4), "bound": "mfma", "achieved": round(tfs, 1), "peak": MFMA_FP16_PEAK_TFS, "unit": "TFLOP/s",
                       "frac": round(tfs / MFMA_FP16_PEAK_TFS, 4), "flops_per_sample": FIELD_FLOPS_PER_SAMPLE, "io_GBps": round(io_gbs, 1)}
         del feats, dirs, res
+    # Reference-model field (frequency encoding + the reference's 128-wide
+    # MLPs, fused), 2^22 world points in [-1.5, 1.5]^3.
+    rm = ext.RefModel.create()
+    n = 1 << 22
+    p = rng.uniform(-1.5, 1.5, size=(n, 3)).astype(np.float32)
+    d = rng.normal(size=(n, 3)).astype(np.float32)
+    pos, dirs = DeviceArray.from_numpy(p), DeviceArray.from_numpy(d / np.linalg.norm(d, axis=1, keepdims=True))
+    res = DeviceArray((n, 4), np.float32)
+    ms = timed(lambda: L.call("nerf_ext_ref_field_forward", rm.density.ptr, rm.color.ptr, pos.ptr, dirs.ptr, n, res.ptr, None, st.handle), 20)
+    tfs = n * REF_FLOPS_PER_SAMPLE / (ms / 1e3) / 1e12
+    out["ref_field_2p22"] = {"kernel": "k_ref_field (reference-model mode: frequency encoding, density 64-128x5-16, colour 48-128x3-16, fp16 MFMA)", "samples": n, "ms": round(ms, 4), "bound": "mfma", "achieved": round(tfs, 1),
+                             "peak": MFMA_FP16_PEAK_TFS, "unit": "TFLOP/s", "frac": round(tfs / MFMA_FP16_PEAK_TFS, 4), "flops_per_sample": REF_FLOPS_PER_SAMPLE}
     return out
+
+
+def ref_model_render(reps: int = 3):
+    """The headline 800x800 render with the reference's own network in place
+    of the hash-grid model (reference-model mode, the reference's init)."""
+    from nerf_amd import ext
+    from nerf_amd.device import synchronize
+    scene, bits, desc, model, cam, occ = build_workload()
+    rm = ext.RefModel.create()
+    r = ext.Renderer()
+    r.render(rm, occ, [cam], MAX_STEPS, T_STOP)
+    synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        _, st = r.render(rm, occ, [cam], MAX_STEPS, T_STOP, timed=True)
+    wall = (time.perf_counter() - t0) / reps
+    tfs = st.samples_shaded * REF_FLOPS_PER_SAMPLE / (st.ms_field / 1e3) / 1e12
+    return {"value": round(W * H / wall / 1e6, 3), "unit": "Mrays/s", "ms_per_render": round(wall * 1e3, 2), "field_ms": round(st.ms_field, 2), "samples_shaded": int(st.samples_shaded),
+            "field_tflops": round(tfs, 1), "field_mfma_frac": round(tfs / MFMA_FP16_PEAK_TFS, 4), "reps": reps,
+            "workload": "800x800, 32-Gaussian scene, 128^3 occupancy, <=1024 steps/ray, reference-model network (frequency encoding, 128-wide MLPs, softplus)"}
 
 
 def train_bench(steps: int, warmup: int, views: int = 100):
@@ -469,7 +505,7 @@ def main() -> int:
         "config": {"workload": f"{W}x{H} inference render, 32-Gaussian scene, 128^3 occupancy, hash grid T=2^19 fp16, <=1024 steps/ray, early stop T<1e-4",
                    "rays": rays, "samples_per_render": int(samples), "samples_shaded": int(shaded), "gpu_ms_per_render": round(gpu_ms, 4), "parallelism": "single GPU"},
         "stages_ms": {k: round(v, 4) for k, v in stage.items()},
-        "roofline": {"kernel": "k_field_forward (fused hash encode + density/colour MLP)", "bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+        "roofline": {"kernel": "k_field_forward_lv (fused hash encode + density/colour MLP, level-major gathers)", "bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved_gbs / HBM_PEAK_GBS, 4), "traffic": int(shaded * FIELD_TRAFFIC_BYTES_PER_SAMPLE),
                      "traffic_GBps": round(shaded * FIELD_TRAFFIC_BYTES_PER_SAMPLE / field_s / 1e9, 1), "mfma_tflops": round(field_tflops, 2), "mfma_frac": round(field_tflops / MFMA_FP16_PEAK_TFS, 4),
                      "bytes_per_sample": FIELD_BYTES_PER_SAMPLE, "flops_per_sample": FIELD_FLOPS_PER_SAMPLE},
@@ -482,6 +518,7 @@ def main() -> int:
         line["train"] = train_bench(args.train_steps, args.train_warmup)
     if not args.no_configs:
         line["configs"] = config_renders()
+        line["reference_model"] = ref_model_render()
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(desc, model, cam, bits)
     print(json.dumps(line), flush=True)
