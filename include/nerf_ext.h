@@ -147,6 +147,16 @@ NERF_API NerfStatus nerf_ext_field_forward(const NerfExtModel* model, const floa
  * outputs.  Init: :1810-1847 on these shapes. */
 NERF_API NerfStatus nerf_ext_ref_mlp_init(uint32_t network /* 0 density, 1 colour */, float* params_host);
 NERF_API NerfStatus nerf_ext_ref_field_forward(const uint16_t* density_params, const uint16_t* color_params, const float* positions, const float* directions, uint32_t n, float* out, float* raw, void* stream);
+/* Composite forward + backward with the reference's loss (backend-cuda.cu
+ * :1095-1182) for rays whose samples are stored contiguously: ray r owns
+ * samples [offsets[r], offsets[r] + counts[r]) of samples [n][2] = (t, dt)
+ * and field [n][4] = (sigma = softplus(raw), sigmoid rgb) as
+ * nerf_ext_ref_field_forward writes it; gt [n_rays][4] = (r, g, b) composited
+ * over white and alpha.  Loss per ray (0.1 + 0.9 clamp(alpha, 0, 1)) |pred -
+ * gt|^2, white background, output gradient 2 w (pred - gt) inv_norm.  draw
+ * [n][4] = d loss / d (raw sigma, raw r, raw g, raw b); the batch's loss is
+ * added to *loss_sum (device). */
+NERF_API NerfStatus nerf_ext_ref_composite_backward(const uint32_t* counts, const uint32_t* offsets, const float* samples, const float* field, const float* gt, uint32_t n_rays, float inv_norm, float* draw, float* loss_sum, void* stream);
 /* The density and colour MLPs of nerf_ext_field_forward on given encodings:
  * features fp16 [n][32], unit directions [n][3] -> out [n][4] = (sigma, r, g, b).
  * The fused fp16-MFMA MLP pass on its own (no table gathers). */

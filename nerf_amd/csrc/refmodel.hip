@@ -32,6 +32,7 @@
 // direction encoding (27 halves and zeros) as one LDS row; lane (g, s) of
 // tile t then reads its B operands back with 16-byte LDS loads.
 #include "mlp_device.hpp"
+#include "wave.hpp"
 
 namespace nerf_hip {
 namespace {
@@ -272,6 +273,85 @@ __global__ __launch_bounds__(kBlockThreads) void k_ref_field(const half8_t* __re
     }
 }
 
+// Composite forward + backward with the reference's loss (:1095-1182), one
+// wave per ray over 64-sample groups as in the training composite of the
+// hash-grid model: field = (sigma = softplus(raw), sigmoid rgb), white
+// background, ray weight w_r = 0.1 + 0.9 clamp(gt_a, 0, 1), loss
+// w_r |pred - gt|^2, g = 2 w_r (pred - gt) inv_norm.  d raw sigma = dt
+// (T_{i+1} c - S_i) . g sigmoid(raw), with sigmoid(raw) = 1 - e^-sigma for
+// sigma = softplus(raw), taken as -expm1(-sigma) (exact for small sigma); the
+// exact derivative where the reference divides by max(1 - alpha, 1e-6).
+__global__ __launch_bounds__(256) void k_ref_composite_train(uint32_t n_rays, const uint32_t* __restrict__ counts, const uint32_t* __restrict__ offsets, const float2* __restrict__ samples, const float4* __restrict__ field,
+                                                              const float4* __restrict__ gt, float inv_norm, float4* __restrict__ draw, float* __restrict__ loss_sum) {
+    __shared__ float wsum[kBlockWaves];
+    const uint32_t lane = threadIdx.x & 63u, nw = gridDim.x * kBlockWaves;
+    float wave_loss     = 0.0f;
+    for (uint32_t r = blockIdx.x * kBlockWaves + (threadIdx.x >> 6); r < n_rays; r += nw) {
+        const uint32_t count = counts[r];
+        if (count == 0u) continue;
+        const uint32_t base = offsets[r];
+        float T = 1.0f, C[3] = {0.0f, 0.0f, 0.0f};
+        for (uint32_t c0 = 0; c0 < count; c0 += 64u) {
+            const uint32_t i = c0 + lane;
+            const bool valid = i < count;
+            const float4 f   = valid ? field[base + i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            const float dt   = valid ? fmaxf(samples[base + i].y, 0.0f) : 0.0f;
+            const float a    = valid ? -expm1f(-(f.x * dt)) : 0.0f;
+            const float incl = wave::inclusive_product(1.0f - a);
+            float excl       = __shfl_up(incl, 1, 64);
+            excl             = lane == 0u ? 1.0f : excl;
+            const float w    = T * excl * a;
+            C[0] += w * f.y;
+            C[1] += w * f.z;
+            C[2] += w * f.w;
+            T *= wave::broadcast(incl, 63u);
+        }
+        const float4 g4    = gt[r];
+        const float gtv[3] = {g4.x, g4.y, g4.z};
+        const float wr     = 0.1f + 0.9f * fminf(1.0f, fmaxf(0.0f, g4.w));
+        float pred[3], gr[3], ray_loss = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+            pred[c]       = wave::sum(C[c]) + T;  // white background
+            const float x = pred[c] - gtv[c];
+            ray_loss += wr * x * x;
+            gr[c] = 2.0f * wr * x * inv_norm;
+        }
+        wave_loss += ray_loss;
+        T = 1.0f;
+        float carry[3] = {0.0f, 0.0f, 0.0f};
+        for (uint32_t c0 = 0; c0 < count; c0 += 64u) {
+            const uint32_t i  = c0 + lane;
+            const bool valid  = i < count;
+            const float4 f    = valid ? field[base + i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            const float dt    = valid ? fmaxf(samples[base + i].y, 0.0f) : 0.0f;
+            const float a     = valid ? -expm1f(-(f.x * dt)) : 0.0f;
+            const float incl  = wave::inclusive_product(1.0f - a);
+            float excl        = __shfl_up(incl, 1, 64);
+            excl              = lane == 0u ? 1.0f : excl;
+            const float w     = T * excl * a;
+            const float Tn    = T * incl;
+            const float c3[3] = {f.y, f.z, f.w};
+            float ds = 0.0f, dc[3];
+#pragma unroll
+            for (int c = 0; c < 3; ++c) {
+                const float prefix = carry[c] + wave::inclusive_sum(w * c3[c]);
+                ds += gr[c] * (Tn * c3[c] - (pred[c] - prefix));
+                dc[c]    = w * gr[c] * c3[c] * (1.0f - c3[c]);
+                carry[c] = wave::broadcast(prefix, 63u);
+            }
+            if (valid) draw[base + i] = make_float4(dt * ds * -expm1f(-f.x), dc[0], dc[1], dc[2]);
+            T *= wave::broadcast(incl, 63u);
+        }
+    }
+    if (lane == 0u) wsum[threadIdx.x >> 6] = wave_loss;
+    __syncthreads();
+    if (threadIdx.x == 0u) {
+        const float b = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+        if (b != 0.0f) atomicAdd(loss_sum, b);
+    }
+}
+
 // Host-side Xavier-uniform init of backend-cuda.cu:1810-1847 on the
 // reference's own shapes.
 void ref_mlp_init_host(uint32_t network, float* out) {
@@ -334,6 +414,17 @@ NERF_API NerfStatus nerf_ext_ref_field_forward(const uint16_t* density_params, c
     const hipError_t f = hipFreeAsync(frags, st);
     NERF_HIP_TRY(e);
     NERF_HIP_TRY(f);
+    return NERF_STATUS_OK;
+}
+
+NERF_API NerfStatus nerf_ext_ref_composite_backward(const uint32_t* counts, const uint32_t* offsets, const float* samples, const float* field, const float* gt, uint32_t n_rays, float inv_norm, float* draw, float* loss_sum,
+                                                  void* stream) {
+    if (n_rays == 0u) return NERF_STATUS_OK;
+    NERF_CHECK_ARG(counts && offsets && samples && field && gt && draw && loss_sum, "nerf_ext_ref_composite_backward: null pointer");
+    const uint32_t waves  = (n_rays + kBlockWaves - 1u) / kBlockWaves;
+    const uint32_t cap    = device_cu_count() * 16u;
+    k_ref_composite_train<<<waves < cap ? waves : cap, kBlockThreads, 0, (hipStream_t)stream>>>(n_rays, counts, offsets, (const float2*)samples, (const float4*)field, (const float4*)gt, inv_norm, (float4*)draw, loss_sum);
+    NERF_LAUNCH_CHECK("k_ref_composite_train");
     return NERF_STATUS_OK;
 }
 

@@ -1145,3 +1145,49 @@ static void ref_field_point(const uint16_t* dp, const uint16_t* cp, const float*
 extern "C" void orc_ref_field_forward(const uint16_t* dparams, const uint16_t* cparams, const float* pos, const float* dirs, uint32_t n, float* out, float* raw) {
     for (uint32_t i = 0; i < n; ++i) ref_field_point(dparams, cparams, pos + 3ull * i, dirs + 3ull * i, out + 4ull * i, raw ? raw + 4ull * i : nullptr);
 }
+
+// Composite forward + backward of one ray with the reference's loss
+// (:1095-1182): sigma = softplus(raw), rgb = sigmoid(raw), white background,
+// ray weight w_r = 0.1 + 0.9 clamp(gt_a, 0, 1), loss w_r |pred - gt|^2,
+// output gradient g = 2 w_r (pred - gt) inv_norm.  d raw sigma_i =
+// dt_i (T_{i+1} c_i - S_i) . g sigmoid(raw_i) with S_i the colour composited
+// behind sample i plus T_n (the exact derivative; the reference divides by
+// max(1 - alpha, 1e-6), equal wherever 1 - alpha >= 1e-6); d raw rgb_i =
+// T_i alpha_i g c (1 - c).  fp64 throughout; returns the ray's loss.
+extern "C" double orc_ref_composite_backward_ray(const float* sraw, const float* rgbraw, const float* dt, uint32_t n, const float* gt4, float inv_norm, float* dsraw, float* drgbraw, float* pred_out) {
+    auto softplus = [](double x) { return x > 20.0 ? x : (x < -20.0 ? exp(x) : log1p(exp(x))); };
+    auto sigm     = [](double x) { return 1.0 / (1.0 + exp(-x)); };
+    std::vector<double> T(n + 1), a(n), c(3ull * n), d(n);
+    T[0] = 1.0;
+    double pred[3] = {0.0, 0.0, 0.0};
+    for (uint32_t i = 0; i < n; ++i) {
+        d[i] = fmax((double)dt[i], 0.0);
+        a[i] = 1.0 - exp(-softplus(sraw[i]) * d[i]);
+        for (int k = 0; k < 3; ++k) {
+            c[3ull * i + k] = sigm(rgbraw[3ull * i + k]);
+            pred[k] += T[i] * a[i] * c[3ull * i + k];
+        }
+        T[i + 1] = T[i] * (1.0 - a[i]);
+    }
+    const double wr = 0.1 + 0.9 * fmin(1.0, fmax(0.0, (double)gt4[3]));
+    double loss = 0.0, g[3];
+    for (int k = 0; k < 3; ++k) {
+        pred[k] += T[n];
+        const double x = pred[k] - gt4[k];
+        loss += wr * x * x;
+        g[k] = 2.0 * wr * x * inv_norm;
+        if (pred_out) pred_out[k] = (float)pred[k];
+    }
+    double S[3] = {T[n], T[n], T[n]};  // composited behind sample i
+    for (int i = (int)n - 1; i >= 0; --i) {
+        double ds = 0.0;
+        for (int k = 0; k < 3; ++k) {
+            const double ck = c[3ull * i + k];
+            ds += g[k] * (T[i + 1] * ck - S[k]);
+            if (drgbraw) drgbraw[3ull * i + k] = (float)(T[i] * a[i] * g[k] * ck * (1.0 - ck));
+            S[k] += T[i] * a[i] * ck;
+        }
+        if (dsraw) dsraw[i] = (float)(d[i] * ds * sigm(sraw[i]));
+    }
+    return loss;
+}

@@ -76,6 +76,7 @@ _PROTOS = {
     "orc_freq_encode": (None, [_P, _U32, _P]),
     "orc_softplus": (_F, [_F]),
     "orc_ref_field_forward": (None, [_P, _P, _P, _P, _U32, _P, _P]),
+    "orc_ref_composite_backward_ray": (C.c_double, [_P, _P, _P, _U32, _P, _F, _P, _P, _P]),
     "orc_det_expf": (_F, [_F]),
     "orc_det_expf_array": (None, [_P, _U64, _P]),
     "orc_scene_density": (None, [_P, _U32, _P, _U32, _P]),
@@ -248,6 +249,19 @@ def ref_field_forward(dparams_bits: np.ndarray, cparams_bits: np.ndarray, pos: n
     raw = np.empty((n, 4), np.float32)
     lib().orc_ref_field_forward(_p(np.ascontiguousarray(dparams_bits)), _p(np.ascontiguousarray(cparams_bits)), _p(pos), _p(dirs), n, _p(out), _p(raw))
     return out, raw
+
+
+def ref_composite_backward_ray(sraw, rgbraw, dt, gt4, inv_norm: float = 1.0):
+    """The reference's loss on one ray (softplus, alpha-weighted MSE, white
+    background): (loss, d raw sigma [n], d raw rgb [n][3], pred [3])."""
+    sraw = np.ascontiguousarray(sraw, np.float32)
+    rgbraw = np.ascontiguousarray(rgbraw, np.float32).reshape(-1, 3)
+    dt = np.ascontiguousarray(dt, np.float32)
+    gt4 = np.ascontiguousarray(gt4, np.float32)
+    n = sraw.size
+    ds, dc, pred = np.zeros(n, np.float32), np.zeros((n, 3), np.float32), np.zeros(3, np.float32)
+    loss = lib().orc_ref_composite_backward_ray(_p(sraw), _p(rgbraw), _p(dt), n, _p(gt4), float(inv_norm), _p(ds), _p(dc), _p(pred))
+    return float(loss), ds, dc, pred
 
 
 def det_expf(x) -> np.ndarray:

@@ -121,3 +121,39 @@ def test_ref_render_parity(w, h, views):
         want_rgb, _, want_counts = orc.render_rays(None, None, dp, cp, ocam, bits.numpy(), 128, BOX, 512, np.arange(w * h, dtype=np.uint32), threads=8, kind=1)
         assert np.array_equal(got_counts[v], want_counts)
         assert_rel(got_rgb[v], want_rgb, what=f"reference-model render rgb view {v}")
+
+
+def test_ref_composite_backward():
+    # Rays of 0 .. 300 samples (several 64-sample groups, ragged ends) with
+    # the field as the reference-model forward writes it (softplus sigma,
+    # sigmoid rgb, fp32); the oracle works from the raw values in fp64.
+    counts = np.array([0, 1, 5, 63, 64, 65, 130, 200, 300, 17], np.uint32)
+    announce(f"reference-model composite backward rays={counts.size}")
+    rng = np.random.default_rng(31)
+    n = int(counts.sum())
+    offsets = np.concatenate([[0], np.cumsum(counts)[:-1]]).astype(np.uint32)
+    sraw = rng.normal(0, 2, n).astype(np.float32)
+    craw = rng.normal(0, 2, (n, 3)).astype(np.float32)
+    dt = rng.uniform(0.001, 0.05, n).astype(np.float32)
+    samples = np.stack([np.cumsum(dt), dt], 1).astype(np.float32)
+    sig = np.where(sraw > 20, sraw, np.where(sraw < -20, np.exp(sraw.astype(np.float64)), np.log1p(np.exp(np.clip(sraw, -20, 20).astype(np.float64)))))
+    field = np.concatenate([sig[:, None], 1 / (1 + np.exp(-craw.astype(np.float64)))], 1).astype(np.float32)
+    gt = np.concatenate([rng.uniform(0, 1, (counts.size, 3)), rng.uniform(-0.2, 1.2, (counts.size, 1))], 1).astype(np.float32)
+    inv_norm = 1.0 / np.count_nonzero(counts)
+    d = {k: DeviceArray.from_numpy(v) for k, v in (("c", counts), ("o", offsets), ("s", samples), ("f", field), ("g", gt))}
+    d_draw, d_loss = DeviceArray((n, 4), np.float32), DeviceArray((1,), np.float32)
+    d_loss.fill_bytes(0)
+    L.call("nerf_ext_ref_composite_backward", d["c"].ptr, d["o"].ptr, d["s"].ptr, d["f"].ptr, d["g"].ptr, counts.size, inv_norm, d_draw.ptr, d_loss.ptr, None)
+    synchronize()
+    got, loss = d_draw.numpy(), float(d_loss.numpy()[0])
+    want, want_loss = np.zeros((n, 4), np.float32), 0.0
+    for r in range(counts.size):
+        a, b = int(offsets[r]), int(offsets[r] + counts[r])
+        if a == b:
+            continue
+        l, ds, dc, _ = orc.ref_composite_backward_ray(sraw[a:b], craw[a:b], dt[a:b], gt[r], inv_norm)
+        want[a:b, 0], want[a:b, 1:] = ds, dc
+        want_loss += l
+    assert_rel(got[:, 0], want[:, 0], what="d raw sigma")
+    assert_rel(got[:, 1:], want[:, 1:], what="d raw rgb")
+    assert abs(loss - want_loss) <= 1e-4 * want_loss

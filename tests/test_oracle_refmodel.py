@@ -106,3 +106,51 @@ def test_ref_structured_weights_closed_form(orc):
     dirs = unit_dirs(500, 5)
     _, raw = orc.ref_field_forward(dp, cp, pos, dirs)
     assert np.array_equal(raw, structured_raw(pos, dirs))
+
+
+def _ray(n, seed):
+    rng = np.random.default_rng(seed)
+    return (rng.normal(0, 2, n).astype(np.float32), rng.normal(0, 2, (n, 3)).astype(np.float32), rng.uniform(0.001, 0.05, n).astype(np.float32),
+            np.array([*rng.uniform(0, 1, 3), rng.uniform(0, 1)], np.float32))
+
+
+def test_ref_composite_backward_finite_differences(orc):
+    # Central differences of the fp64 loss in the raw inputs (h on the fp32 grid).
+    for n, seed in ((1, 1), (7, 2), (150, 3)):
+        s, c, dt, gt = _ray(n, seed)
+        loss, ds, dc, _ = orc.ref_composite_backward_ray(s, c, dt, gt, inv_norm=1.0)
+        for i in range(0, n, max(1, n // 10)):
+            for k in (-1, 0, 1, 2):
+                h = np.float32(1e-2)
+                sp, sm, cp_, cm = s.copy(), s.copy(), c.copy(), c.copy()
+                if k < 0:
+                    sp[i] += h; sm[i] -= h
+                    h_eff = (np.float64(sp[i]) - np.float64(sm[i])) / 2
+                    got = ds[i]
+                else:
+                    cp_[i, k] += h; cm[i, k] -= h
+                    h_eff = (np.float64(cp_[i, k]) - np.float64(cm[i, k])) / 2
+                    got = dc[i, k]
+                lp = orc.ref_composite_backward_ray(sp, cp_, dt, gt)[0]
+                lm = orc.ref_composite_backward_ray(sm, cm, dt, gt)[0]
+                fd = (lp - lm) / (2 * h_eff)
+                assert abs(got - fd) <= 1e-4 * max(abs(fd), 1e-3), (n, i, k, got, fd)
+
+
+def test_ref_composite_alpha_weighting_and_closed_form(orc):
+    s, c, dt, gt = _ray(5, 4)
+    gt1, gt0 = gt.copy(), gt.copy()
+    gt1[3], gt0[3] = 1.0, 0.0
+    l1 = orc.ref_composite_backward_ray(s, c, dt, gt1)[0]
+    l0 = orc.ref_composite_backward_ray(s, c, dt, gt0)[0]
+    assert abs(l0 / l1 - 0.1) < 1e-12           # ray weight 0.1 + 0.9 alpha (:1131-1139)
+    # One sample: pred = a c + (1 - a), a = 1 - exp(-softplus(s) dt).
+    s1, c1, dt1 = np.array([0.3], np.float32), np.array([[0.5, -1.0, 2.0]], np.float32), np.array([0.2], np.float32)
+    g = np.array([0.2, 0.4, 0.6, 0.5], np.float32)
+    a = 1 - np.exp(-np.log1p(np.exp(np.float64(np.float32(0.3)))) * np.float64(np.float32(0.2)))
+    col = 1 / (1 + np.exp(-c1[0].astype(np.float64)))
+    pred = a * col + (1 - a)
+    loss, _, dc, p = orc.ref_composite_backward_ray(s1, c1, dt1, g, inv_norm=0.5)
+    w = 0.1 + 0.9 * np.float64(np.float32(0.5))
+    assert abs(loss - w * np.sum((pred - g[:3].astype(np.float64)) ** 2)) < 1e-12
+    np.testing.assert_allclose(dc[0], a * 2 * w * (pred - g[:3]) * 0.5 * col * (1 - col), rtol=1e-6)
