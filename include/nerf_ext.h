@@ -156,6 +156,14 @@ NERF_API NerfStatus nerf_ext_ref_field_forward(const uint16_t* density_params, c
  * gt|^2, white background, output gradient 2 w (pred - gt) inv_norm.  draw
  * [n][4] = d loss / d (raw sigma, raw r, raw g, raw b); the batch's loss is
  * added to *loss_sum (device). */
+/* MLP backward of the reference-model network (forward recomputed): weight
+ * gradients ddensity [75776], dcolor [40960] (fp32, device, overwritten) of
+ * the loss whose derivatives in the raw outputs are draw [n][4] = (raw sigma,
+ * raw r, g, b) (as nerf_ext_ref_composite_backward writes them), multiplied
+ * by loss_scale (:1066, :1079; Adam divides it out).  fp16 deltas, fp32
+ * accumulation; the colour network's input gradient flows into density
+ * outputs 1..15 (:1069-1083).  n <= 2^20 per call. */
+NERF_API NerfStatus nerf_ext_ref_backward(const uint16_t* density_params, const uint16_t* color_params, const float* positions, const float* directions, const float* draw, uint32_t n, float loss_scale, float* ddensity, float* dcolor, void* stream);
 NERF_API NerfStatus nerf_ext_ref_composite_backward(const uint32_t* counts, const uint32_t* offsets, const float* samples, const float* field, const float* gt, uint32_t n_rays, float inv_norm, float* draw, float* loss_sum, void* stream);
 /* The density and colour MLPs of nerf_ext_field_forward on given encodings:
  * features fp16 [n][32], unit directions [n][3] -> out [n][4] = (sigma, r, g, b).

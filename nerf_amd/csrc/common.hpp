@@ -353,9 +353,10 @@ hipError_t launch_density(const GridParams& g, const void* table, const half_t* 
 
 // Reference-model mode (refmodel.hip): the reference's own network.  Its
 // weights are packed into kRefFragments MFMA A fragments (64 lanes x 8 halves
-// each) by ref_pack_weights; launch_ref_field evaluates the field from them
-// (world positions), out4 = (softplus sigma, sigmoid rgb), raw4 optional.
-constexpr uint32_t kRefFragments = 232u;
+// each; the forward's first, then the backward's transposed ones) by
+// ref_pack_weights; launch_ref_field evaluates the field from them (world
+// positions), out4 = (softplus sigma, sigmoid rgb), raw4 optional.
+constexpr uint32_t kRefFragments = 444u;
 hipError_t ref_pack_weights(const half_t* dparams, const half_t* cparams, half8_t* frags, hipStream_t stream);
 hipError_t launch_ref_field(const half8_t* frags, const FieldInputs& in, uint32_t n, float4* out4, float4* raw4, hipStream_t stream);
 

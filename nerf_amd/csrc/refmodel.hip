@@ -56,6 +56,28 @@ constexpr RefLayer kRefLayers[10] = {
 };
 static_assert(kRefLayers[5].w_off + 16u * 128u == kRefDensityParams, "density layout");
 static_assert(kRefLayers[9].w_off + 16u * 128u == kRefColorParams, "colour layout");
+constexpr uint32_t kRefFwdFragments = 232u;
+
+// Backward products delta_in = W^T delta_out, in the order the backward
+// consumes them: transposed fragments of layer `src` — rows = its input
+// neurons, k = its output neurons under the hidden k-map (outputs >= n_out
+// are zero).  `geo`: the colour input layer restricted to the geometry
+// features, with row o = density output o (column o - 1; row 0 zero), so the
+// result lands where the density output layer's deltas live.
+struct RefTLayer {
+    uint32_t src, rb, kb, frag0, geo;
+};
+constexpr RefTLayer kRefT[9] = {{9u, 8u, 1u, 232u, 0u}, {8u, 8u, 4u, 240u, 0u}, {7u, 8u, 4u, 272u, 0u}, {6u, 1u, 4u, 304u, 1u}, {5u, 8u, 1u, 308u, 0u},
+                                {4u, 8u, 4u, 316u, 0u}, {3u, 8u, 4u, 348u, 0u}, {2u, 8u, 4u, 380u, 0u}, {1u, 8u, 4u, 412u, 0u}};
+static_assert(kRefT[8].frag0 + 32u == kRefFragments, "fragment count");
+
+// Rows of the neuron-major training buffers [row][np samples]: kActOff[l]
+// is the input of layer l (the encoding, hidden activations, the colour
+// input [geometry 15 | direction encoding 27 | 0 x 6]); kDltOff[l] the delta
+// of layer l's output.  dW_l = delta_l x input_l^T over the samples.
+constexpr uint32_t kActOff[10] = {0u, 64u, 192u, 320u, 448u, 576u, 704u, 752u, 880u, 1008u};
+constexpr uint32_t kDltOff[10] = {0u, 128u, 256u, 384u, 512u, 640u, 656u, 784u, 912u, 1040u};
+constexpr uint32_t kActRows = 1136u, kDltRows = 1056u;
 
 // Input column of W for element j of lane group g in k-block q (-1: zero).
 __device__ __forceinline__ int ref_column(uint32_t map, uint32_t q, uint32_t g, uint32_t j) {
@@ -75,6 +97,27 @@ __device__ __forceinline__ int ref_column(uint32_t map, uint32_t q, uint32_t g, 
 // One workgroup of 64 threads per fragment.
 __global__ __launch_bounds__(64) void k_ref_pack(const half_t* __restrict__ dparams, const half_t* __restrict__ cparams, half8_t* __restrict__ frags) {
     const uint32_t f = blockIdx.x, lane = threadIdx.x;
+    if (f >= kRefFwdFragments) {
+        uint32_t ti = 0u;
+#pragma unroll
+        for (uint32_t k = 1u; k < 9u; ++k)
+            if (f >= kRefT[k].frag0) ti = k;
+        const RefTLayer T  = kRefT[ti];
+        const RefLayer L   = kRefLayers[T.src];
+        const uint32_t loc = f - T.frag0, r = loc / T.kb, q = loc - r * T.kb;
+        const uint32_t i = lane & 15u, g = lane >> 4;
+        const half_t* W = (L.network == 0u ? dparams : cparams) + L.w_off;
+        half8_t a;
+#pragma unroll
+        for (uint32_t j = 0; j < 8u; ++j) {
+            const uint32_t o = (uint32_t)ref_column(kMapHidden, q, g, j);  // output neuron of layer src
+            const uint32_t row = 16u * r + i;                               // input neuron (geo: density output)
+            const bool ok = o < L.n_out && (!T.geo || (row >= 1u && row <= 15u));
+            a[j] = ok ? W[o * L.n_in + (T.geo ? row - 1u : row)] : (half_t)0.0f;
+        }
+        frags[(uint64_t)f * 64u + lane] = a;
+        return;
+    }
     uint32_t li = 0u;
 #pragma unroll
     for (uint32_t k = 1u; k < 10u; ++k)
@@ -110,10 +153,34 @@ __device__ __forceinline__ half8_t frag_load(const FragSrc& S, uint32_t f) {
     return __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(S.rsrc, S.voff, f * 1024u, 0));
 }
 
+// Where a training pass keeps a block of activations or deltas: the fp16
+// neuron-major buffer [row][np samples] through a buffer descriptor; rows
+// from `row0`, samples of this wave's group from s0; lane (g, s) of tile t
+// owns rows 16 r + 4 g + e of sample s0 + 16 t + s.  The lane's part of the
+// address (4 g rows, sample s0 + s) is one VGPR; the uniform row 16 r + e
+// goes in the scalar offset and the tile in the immediate — with plain
+// pointers the compiler keeps a 64-bit address per row live and spills.
+struct RowStore {
+    __amdgpu_buffer_rsrc_t rsrc;
+    uint32_t vbase;  // bytes: (4 g np + s0 + s) * 2
+    uint32_t np2;    // np * 2
+    uint32_t row0;
+    __device__ __forceinline__ void put(uint32_t row_u, uint32_t t, half_t v) const {
+        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, v), rsrc, vbase + 32u * t, (row0 + row_u) * np2, 0);
+    }
+    __device__ __forceinline__ half_t get(uint32_t row_u, uint32_t t) const {
+        return __builtin_bit_cast(half_t, __builtin_amdgcn_raw_buffer_load_b16(rsrc, vbase + 32u * t, (row0 + row_u) * np2, 0));
+    }
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(half_t* buf, uint32_t rows, uint32_t np) {
+    return __builtin_amdgcn_make_buffer_rsrc((void*)buf, (short)0, (int)(rows * np * 2u), 0x00020000);
+}
+
 // A layer of 128 outputs (8 row blocks) on KB k-blocks of input, four tiles;
-// its fragments start at f0.
-template <uint32_t KB>
-__device__ __forceinline__ void ref_hidden(const FragSrc& S, uint32_t f0, const half8_t (&in)[4][4], half8_t (&out)[4][4]) {
+// its fragments start at f0.  With kStore the fp16 outputs also go to st.
+template <uint32_t KB, bool kStore = false>
+__device__ __forceinline__ void ref_hidden(const FragSrc& S, uint32_t f0, const half8_t (&in)[4][4], half8_t (&out)[4][4], const RowStore& st = RowStore{}) {
     half4_t lo[4];  // fp16 results of the even row block, joined with the odd one
 #pragma unroll
     for (uint32_t r = 0; r < 8u; ++r) {
@@ -134,6 +201,10 @@ __device__ __forceinline__ void ref_hidden(const FragSrc& S, uint32_t f0, const 
             const half4_t h = half4_t{to_half_rne(fmaxf(acc[t][0], 0.0f)), to_half_rne(fmaxf(acc[t][1], 0.0f)), to_half_rne(fmaxf(acc[t][2], 0.0f)), to_half_rne(fmaxf(acc[t][3], 0.0f))};
             if (r & 1u) out[t][r >> 1] = half8_t{lo[t][0], lo[t][1], lo[t][2], lo[t][3], h[0], h[1], h[2], h[3]};
             else lo[t] = h;
+            if constexpr (kStore) {
+#pragma unroll
+                for (uint32_t e = 0; e < 4u; ++e) st.put(16u * r + e, t, h[e]);
+            }
         }
         // One row block's weights in flight at a time: without the fence the
         // scheduler hoists the next blocks' fragment loads and spills.
@@ -151,6 +222,40 @@ __device__ __forceinline__ void ref_output(const FragSrc& S, uint32_t f0, const 
         o[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (uint32_t q = 0; q < 4u; ++q) o[t] = mfma16x16x32(a[q], in[t][q], o[t]);
+    }
+}
+
+// One backward product of a 128-input layer: delta_in = mask . (W^T
+// delta_out) for the four tiles, mask = the stored forward activation of
+// those 128 rows > 0, rounded to fp16 as the next product's B operand and
+// stored for the weight gradients.
+template <uint32_t KB>
+__device__ __forceinline__ void ref_backward_layer(const FragSrc& S, uint32_t f0, const half8_t (&in)[4][4], half8_t (&out)[4][4], const RowStore& act, const RowStore& dlt) {
+    half4_t lo[4];
+#pragma unroll
+    for (uint32_t r = 0; r < 8u; ++r) {
+        half8_t a[KB];
+#pragma unroll
+        for (uint32_t q = 0; q < KB; ++q) a[q] = frag_load(S, f0 + r * KB + q);
+        floatx4 acc[4];
+#pragma unroll
+        for (uint32_t t = 0; t < 4u; ++t) {
+            acc[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (uint32_t q = 0; q < KB; ++q) acc[t] = mfma16x16x32(a[q], in[t][q], acc[t]);
+        }
+#pragma unroll
+        for (uint32_t t = 0; t < 4u; ++t) {
+            half4_t h;
+#pragma unroll
+            for (uint32_t e = 0; e < 4u; ++e) {
+                h[e] = (float)act.get(16u * r + e, t) > 0.0f ? to_half_rne(acc[t][e]) : (half_t)0.0f;
+                dlt.put(16u * r + e, t, h[e]);
+            }
+            if (r & 1u) out[t][r >> 1] = half8_t{lo[t][0], lo[t][1], lo[t][2], lo[t][3], h[0], h[1], h[2], h[3]};
+            else lo[t] = h;
+        }
+        __builtin_amdgcn_sched_barrier(0);
     }
 }
 
@@ -270,6 +375,190 @@ __global__ __launch_bounds__(kBlockThreads) void k_ref_field(const half8_t* __re
                 }
             }
         }
+    }
+}
+
+// MLP backward of the reference-model network for one batch (the forward is
+// recomputed, :784-909 semantics with fp32 accumulation).  Per 64-sample
+// group: the encoding and every layer's fp16 input go to `acts`, the fp16
+// deltas of every layer's output to `dlts` (neuron-major, np samples per
+// row) for k_ref_dw.  Output deltas: fp16(loss_scale x d raw) for colour
+// outputs 0..2; the geometry features' delta (colour input layer transposed,
+// rows shifted onto density outputs 1..15) and fp16(loss_scale x d raw
+// sigma) for the density outputs.  Samples past n get zero output deltas, so
+// all their deltas are zero.
+template <bool kFromSamples>
+__global__ __launch_bounds__(kBlockThreads) void k_ref_backward(const half8_t* __restrict__ frags, FieldInputs in, uint32_t n, const float4* __restrict__ draw, float loss_scale, half_t* __restrict__ acts,
+                                                                half_t* __restrict__ dlts, uint32_t np) {
+    __shared__ __align__(16) half_t rows[kBlockWaves][64 * kRefPitch];
+    const uint32_t lane = threadIdx.x & 63u, g = lane >> 4, s16 = lane & 15u, wv = threadIdx.x >> 6;
+    half_t* R       = rows[wv];
+    const FragSrc S = frag_src(frags, lane);
+    const uint32_t groups = np / 64u;
+    const __amdgpu_buffer_rsrc_t ra = row_rsrc(acts, kActRows, np), rd = row_rsrc(dlts, kDltRows, np);
+    for (uint32_t gi = blockIdx.x * kBlockWaves + wv; gi < groups; gi += gridDim.x * kBlockWaves) {
+        const uint32_t s0    = gi * 64u;
+        const uint32_t vbase = (4u * g * np + s0 + s16) * 2u;
+        auto A = [&](uint32_t l) { return RowStore{ra, vbase, 2u * np, kActOff[l]}; };
+        auto D = [&](uint32_t l) { return RowStore{rd, vbase, 2u * np, kDltOff[l]}; };
+        {
+            const uint32_t q = min(s0 + lane, n - 1u);
+            float p[3], d[3];
+            if constexpr (kFromSamples) {
+                const float2 td  = in.samples[q];
+                const uint32_t r = in.sample_ray[q];
+                const float4 ro = in.rays[2ull * r], rd = in.rays[2ull * r + 1ull];
+                d[0] = rd.x;
+                d[1] = rd.y;
+                d[2] = rd.z;
+                p[0] = ro.x + td.x * rd.x;
+                p[1] = ro.y + td.x * rd.y;
+                p[2] = ro.z + td.x * rd.z;
+            } else {
+#pragma unroll
+                for (uint32_t a = 0; a < 3u; ++a) {
+                    p[a] = in.positions[3ull * q + a];
+                    d[a] = in.directions[3ull * q + a];
+                }
+            }
+            half_t* row = R + lane * kRefPitch;
+            freq_row(p, 10u, row);
+            row[63] = (half_t)0.0f;
+            freq_row(d, 4u, row + 64u);
+#pragma unroll
+            for (uint32_t k = 64u + 27u; k < 96u; ++k) row[k] = (half_t)0.0f;
+            // Lane = sample: the encoding rows are stored one row per instruction.
+            const uint32_t vs = (s0 + lane) * 2u;
+            for (uint32_t k = 0; k < 64u; ++k) __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, row[k]), ra, vs, (kActOff[0] + k) * 2u * np, 0);
+            // Colour input columns 15..41: the direction encoding; 42..47: zero.
+            for (uint32_t k = 15u; k < 48u; ++k) {
+                const half_t v = k < 42u ? row[64u + (k - 15u)] : (half_t)0.0f;
+                __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, v), ra, vs, (kActOff[6] + k) * 2u * np, 0);
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+        half8_t x[4][4], y[4][4];
+#pragma unroll
+        for (uint32_t t = 0; t < 4u; ++t) {
+            const half_t* r = R + (16u * t + s16) * kRefPitch;
+            x[t][0]         = *reinterpret_cast<const half8_t*>(r + 8u * g);
+            x[t][1]         = *reinterpret_cast<const half8_t*>(r + 32u + 8u * g);
+            x[t][2] = x[t][3] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+        }
+        ref_hidden<2, true>(S, kRefLayers[0].frag0, x, y, A(1));
+        ref_hidden<4, true>(S, kRefLayers[1].frag0, y, x, A(2));
+        ref_hidden<4, true>(S, kRefLayers[2].frag0, x, y, A(3));
+        ref_hidden<4, true>(S, kRefLayers[3].frag0, y, x, A(4));
+        ref_hidden<4, true>(S, kRefLayers[4].frag0, x, y, A(5));
+        floatx4 dens[4];
+        ref_output(S, kRefLayers[5].frag0, y, dens);
+#pragma unroll
+        for (uint32_t t = 0; t < 4u; ++t) {
+            const half_t* r  = R + (16u * t + s16) * kRefPitch + 64u;
+            const half4_t de = *reinterpret_cast<const half4_t*>(r + 4u * g);
+            const half4_t h  = half4_t{to_half_rne(dens[t][0]), to_half_rne(dens[t][1]), to_half_rne(dens[t][2]), to_half_rne(dens[t][3])};
+#pragma unroll
+            for (uint32_t e = 0; e < 4u; ++e)
+                // Geometry = density outputs 1..15 at colour input row 4g + e - 1
+                // (the uniform part e - 1 wraps to -1 for e = 0: the row sum is
+                // taken modulo 2^32 and lands on 4g - 1).
+                if (4u * g + e >= 1u) A(6).put(e - 1u, t, h[e]);
+            x[t][0] = half8_t{h[0], h[1], h[2], h[3], de[0], de[1], de[2], de[3]};
+            x[t][1] = g < 2u ? *reinterpret_cast<const half8_t*>(r + 16u + 8u * g) : half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+        }
+        __builtin_amdgcn_wave_barrier();  // the rows are rewritten by the next pass
+        ref_hidden<2, true>(S, kRefLayers[6].frag0, x, y, A(7));
+        ref_hidden<4, true>(S, kRefLayers[7].frag0, y, x, A(8));
+        ref_hidden<4, true>(S, kRefLayers[8].frag0, x, y, A(9));
+        // Output deltas.  Lane group 0 holds outputs 0..3 of a sample.
+        float4 dr[4];
+#pragma unroll
+        for (uint32_t t = 0; t < 4u; ++t) {
+            const uint32_t st = s0 + 16u * t + s16;
+            dr[t]             = st < n ? draw[st] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            const half4_t h   = g == 0u ? half4_t{to_half_rne(loss_scale * dr[t].y), to_half_rne(loss_scale * dr[t].z), to_half_rne(loss_scale * dr[t].w), (half_t)0.0f} : half4_t{0, 0, 0, 0};
+#pragma unroll
+            for (uint32_t e = 0; e < 4u; ++e) D(9).put(e, t, h[e]);
+            x[t][0] = half8_t{h[0], h[1], h[2], h[3], 0, 0, 0, 0};
+            x[t][1] = x[t][2] = x[t][3] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+        }
+        ref_backward_layer<1>(S, kRefT[0].frag0, x, y, A(9), D(8));
+        ref_backward_layer<4>(S, kRefT[1].frag0, y, x, A(8), D(7));
+        ref_backward_layer<4>(S, kRefT[2].frag0, x, y, A(7), D(6));
+        // Geometry features -> density output deltas 1..15; output 0 = sigma.
+        {
+            floatx4 geo[4];
+            ref_output(S, kRefT[3].frag0, y, geo);
+#pragma unroll
+            for (uint32_t t = 0; t < 4u; ++t) {
+                half4_t h;
+#pragma unroll
+                for (uint32_t e = 0; e < 4u; ++e) h[e] = (g == 0u && e == 0u) ? to_half_rne(loss_scale * dr[t].x) : to_half_rne(geo[t][e]);
+#pragma unroll
+                for (uint32_t e = 0; e < 4u; ++e) D(5).put(e, t, h[e]);
+                x[t][0] = half8_t{h[0], h[1], h[2], h[3], 0, 0, 0, 0};
+                x[t][1] = x[t][2] = x[t][3] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+            }
+        }
+        ref_backward_layer<1>(S, kRefT[4].frag0, x, y, A(5), D(4));
+        ref_backward_layer<4>(S, kRefT[5].frag0, y, x, A(4), D(3));
+        ref_backward_layer<4>(S, kRefT[6].frag0, x, y, A(3), D(2));
+        ref_backward_layer<4>(S, kRefT[7].frag0, y, x, A(2), D(1));
+        ref_backward_layer<4>(S, kRefT[8].frag0, x, y, A(1), D(0));
+    }
+}
+
+// Weight gradients from the neuron-major buffers: dW_l[o][i] = sum over
+// samples of delta_l[o][s] input_l[i][s], the samples on the MFMA reduction
+// axis (A = delta rows, B = input rows, 32 samples per MFMA, 16-byte
+// fragment loads).  One wave per (16 x 16 block, chunk of samples); each
+// writes its block's partial for that chunk, and k_ref_dw_reduce sums the
+// chunks in order (deterministic).
+constexpr uint32_t kRefDwBlocks = 456u;  // sum over layers of (n_out / 16) x ceil(n_in / 16)
+__device__ __forceinline__ uint32_t ref_dw_layer(uint32_t b, uint32_t& local) {
+    uint32_t l = 0u, first = 0u;
+#pragma unroll
+    for (uint32_t k = 0; k < 10u; ++k) {
+        const uint32_t nb = (kRefLayers[k].n_out / 16u) * ((kRefLayers[k].n_in + 15u) / 16u);
+        if (b >= first && b < first + nb) {
+            l     = k;
+            local = b - first;
+        }
+        first += nb;
+    }
+    return l;
+}
+
+__global__ __launch_bounds__(kBlockThreads) void k_ref_dw(const half_t* __restrict__ acts, const half_t* __restrict__ dlts, uint32_t np, uint32_t chunk, uint32_t chunks, float* __restrict__ partial) {
+    const uint32_t lane = threadIdx.x & 63u, g = lane >> 4, i = lane & 15u;
+    const uint32_t w = blockIdx.x * kBlockWaves + (threadIdx.x >> 6);
+    if (w >= kRefDwBlocks * chunks) return;
+    const uint32_t blk = w % kRefDwBlocks, kc = w / kRefDwBlocks;
+    uint32_t local    = 0u;
+    const uint32_t l  = ref_dw_layer(blk, local);
+    const RefLayer L  = kRefLayers[l];
+    const uint32_t ib_n = (L.n_in + 15u) / 16u, ob = local / ib_n, ib = local - ob * ib_n;
+    const uint32_t k_begin = kc * chunk, k_end = min(np, k_begin + chunk);
+    const half_t* a = dlts + (uint64_t)(kDltOff[l] + 16u * ob + i) * np + 8u * g;
+    const half_t* b = acts + (uint64_t)(kActOff[l] + 16u * ib + i) * np + 8u * g;
+    floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t k0 = k_begin; k0 < k_end; k0 += 32u) acc = mfma16x16x32(*reinterpret_cast<const half8_t*>(a + k0), *reinterpret_cast<const half8_t*>(b + k0), acc);
+    // C lane (g, i): rows 4g + e of the delta block, column i of the input block.
+    float* dst = partial + (uint64_t)kc * (kRefDensityParams + kRefColorParams) + (L.network == 0u ? 0u : kRefDensityParams) + L.w_off;
+    const uint32_t col = 16u * ib + i;
+    if (col < L.n_in) {
+#pragma unroll
+        for (uint32_t e = 0; e < 4u; ++e) dst[(16u * ob + 4u * g + e) * L.n_in + col] = acc[e];
+    }
+}
+
+__global__ __launch_bounds__(256) void k_ref_dw_reduce(const float* __restrict__ partial, uint32_t chunks, float* __restrict__ ddensity, float* __restrict__ dcolor) {
+    constexpr uint32_t P = kRefDensityParams + kRefColorParams;
+    for (uint32_t j = blockIdx.x * 256u + threadIdx.x; j < P; j += gridDim.x * 256u) {
+        float v = 0.0f;
+        for (uint32_t c = 0; c < chunks; ++c) v += partial[(uint64_t)c * P + j];
+        if (j < kRefDensityParams) ddensity[j] = v;
+        else dcolor[j - kRefDensityParams] = v;
     }
 }
 
@@ -414,6 +703,45 @@ NERF_API NerfStatus nerf_ext_ref_field_forward(const uint16_t* density_params, c
     const hipError_t f = hipFreeAsync(frags, st);
     NERF_HIP_TRY(e);
     NERF_HIP_TRY(f);
+    return NERF_STATUS_OK;
+}
+
+NERF_API NerfStatus nerf_ext_ref_backward(const uint16_t* density_params, const uint16_t* color_params, const float* positions, const float* directions, const float* draw, uint32_t n, float loss_scale, float* ddensity,
+                                        float* dcolor, void* stream) {
+    if (n == 0u) return NERF_STATUS_OK;
+    NERF_CHECK_ARG(density_params && color_params && positions && directions && draw && ddensity && dcolor, "nerf_ext_ref_backward: null pointer");
+    NERF_CHECK_ARG(n <= (1u << 20), "nerf_ext_ref_backward: at most 2^20 samples per call (buffer descriptors address < 4 GiB)");
+    hipStream_t st        = (hipStream_t)stream;
+    const uint32_t np     = (n + 63u) / 64u * 64u;
+    const uint32_t chunk  = 8192u;
+    const uint32_t chunks = (np + chunk - 1u) / chunk;
+    half8_t* frags = nullptr;
+    half_t *acts = nullptr, *dlts = nullptr;
+    float* partial = nullptr;
+    NERF_HIP_TRY(hipMallocAsync((void**)&frags, sizeof(half8_t) * 64u * kRefFragments, st));
+    NERF_HIP_TRY(hipMallocAsync((void**)&acts, sizeof(half_t) * (uint64_t)kActRows * np, st));
+    NERF_HIP_TRY(hipMallocAsync((void**)&dlts, sizeof(half_t) * (uint64_t)kDltRows * np, st));
+    NERF_HIP_TRY(hipMallocAsync((void**)&partial, sizeof(float) * (uint64_t)chunks * (kRefDensityParams + kRefColorParams), st));
+    FieldInputs in{};
+    in.positions  = positions;
+    in.directions = directions;
+    hipError_t e  = ref_pack_weights((const half_t*)density_params, (const half_t*)color_params, frags, st);
+    if (e == hipSuccess) {
+        const uint32_t need = np / 64u / kBlockWaves + 1u, cap = device_cu_count() * 2u;
+        k_ref_backward<false><<<need < cap ? need : cap, kBlockThreads, 0, st>>>(frags, in, n, (const float4*)draw, loss_scale, acts, dlts, np);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess) {
+        k_ref_dw<<<(kRefDwBlocks * chunks + kBlockWaves - 1u) / kBlockWaves, kBlockThreads, 0, st>>>(acts, dlts, np, chunk, chunks, partial);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess) {
+        k_ref_dw_reduce<<<128, 256, 0, st>>>(partial, chunks, ddensity, dcolor);
+        e = hipGetLastError();
+    }
+    const hipError_t f[4] = {hipFreeAsync(partial, st), hipFreeAsync(dlts, st), hipFreeAsync(acts, st), hipFreeAsync(frags, st)};
+    NERF_HIP_TRY(e);
+    for (hipError_t x : f) NERF_HIP_TRY(x);
     return NERF_STATUS_OK;
 }
 

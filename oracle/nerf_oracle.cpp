@@ -1191,3 +1191,72 @@ extern "C" double orc_ref_composite_backward_ray(const float* sraw, const float*
     }
     return loss;
 }
+
+// MLP backward of the reference-model network for a batch: given d loss /
+// d raw outputs draw [n][4] (raw sigma, raw r, g, b), weight gradients
+// dD [75776], dC [40960] (accumulated in fp64, multiplied by loss_scale).
+// Rounding points as the product path: output deltas fp16(loss_scale x draw);
+// every propagated delta fp16(mask . W^T delta) with the mask from the
+// forward activation (> 0); the geometry features' delta
+// fp16((W_c0^T delta_c0) [0, 15)) becomes density output deltas 1..15
+// (:1069-1083); activations as the forward (fp16).
+extern "C" void orc_ref_mlp_backward(const uint16_t* dp, const uint16_t* cp, const float* pos, const float* dirs, const float* draw, uint32_t n, float loss_scale, double* dD, double* dC) {
+    auto W = [](const uint16_t* P, uint64_t off, uint32_t n_in, uint32_t o, uint32_t i) { return (double)orc_f16_to_f32(P[off + (uint64_t)o * n_in + i]); };
+    uint64_t doff[6], coff[4], o = 0;
+    for (int m = 0; m < 6; ++m) doff[m] = o, o += (uint64_t)kRefDensity[m][0] * kRefDensity[m][1];
+    o = 0;
+    for (int m = 0; m < 4; ++m) coff[m] = o, o += (uint64_t)kRefColor[m][0] * kRefColor[m][1];
+    // Forward with every layer's input kept: net input, then each layer's output.
+    auto forward = [&](const uint16_t* P, const uint32_t (*shape)[2], const uint64_t* off, uint32_t layers, std::vector<std::vector<float>>& acts) {
+        for (uint32_t m = 0; m < layers; ++m) {
+            const std::vector<float>& a = acts[m];
+            std::vector<float> b(shape[m][0]);
+            for (uint32_t q = 0; q < shape[m][0]; ++q) {
+                double acc = 0.0;
+                for (uint32_t k = 0; k < shape[m][1]; ++k) acc += W(P, off[m], shape[m][1], q, k) * (double)a[k];
+                b[q] = m + 1u < layers ? r16(fmaxf((float)acc, 0.0f)) : r16((float)acc);
+            }
+            acts.push_back(b);
+        }
+    };
+    // Backward from output delta; returns the delta of the network input (unmasked).
+    auto backward = [&](const uint16_t* P, const uint32_t (*shape)[2], const uint64_t* off, uint32_t layers, const std::vector<std::vector<float>>& acts, std::vector<float> delta, double* dW) {
+        std::vector<double> din;
+        for (int m = (int)layers - 1; m >= 0; --m) {
+            const uint32_t n_out = shape[m][0], n_in = shape[m][1];
+            const std::vector<float>& a = acts[m];
+            for (uint32_t q = 0; q < n_out; ++q)
+                for (uint32_t k = 0; k < n_in; ++k) dW[off[m] + (uint64_t)q * n_in + k] += (double)delta[q] * (double)a[k];
+            din.assign(n_in, 0.0);
+            for (uint32_t k = 0; k < n_in; ++k)
+                for (uint32_t q = 0; q < n_out; ++q) din[k] += W(P, off[m], n_in, q, k) * (double)delta[q];
+            if (m > 0) {
+                std::vector<float> nd(n_in);
+                for (uint32_t k = 0; k < n_in; ++k) nd[k] = a[k] > 0.0f ? r16((float)din[k]) : 0.0f;
+                delta.swap(nd);
+            }
+        }
+        return din;
+    };
+    for (uint32_t s = 0; s < n; ++s) {
+        float pe[64], de[27];
+        orc_freq_encode(pos + 3ull * s, 10u, pe);
+        for (int k = 0; k < 63; ++k) pe[k] = r16(pe[k]);
+        pe[63] = 0.0f;
+        std::vector<std::vector<float>> da{std::vector<float>(pe, pe + 64)};
+        forward(dp, kRefDensity, doff, 6u, da);
+        const std::vector<float>& dens = da.back();
+        orc_freq_encode(dirs + 3ull * s, 4u, de);
+        std::vector<float> ci(48, 0.0f);
+        for (int k = 0; k < 15; ++k) ci[k] = dens[1 + k];
+        for (int k = 0; k < 27; ++k) ci[15 + k] = r16(de[k]);
+        std::vector<std::vector<float>> ca{ci};
+        forward(cp, kRefColor, coff, 4u, ca);
+        std::vector<float> dc(16, 0.0f), dd(16, 0.0f);
+        for (int k = 0; k < 3; ++k) dc[k] = r16(loss_scale * draw[4ull * s + 1 + k]);
+        const std::vector<double> dci = backward(cp, kRefColor, coff, 4u, ca, dc, dC);
+        dd[0] = r16(loss_scale * draw[4ull * s]);
+        for (int k = 0; k < 15; ++k) dd[1 + k] = r16((float)dci[k]);
+        backward(dp, kRefDensity, doff, 6u, da, dd, dD);
+    }
+}

@@ -77,6 +77,7 @@ _PROTOS = {
     "orc_softplus": (_F, [_F]),
     "orc_ref_field_forward": (None, [_P, _P, _P, _P, _U32, _P, _P]),
     "orc_ref_composite_backward_ray": (C.c_double, [_P, _P, _P, _U32, _P, _F, _P, _P, _P]),
+    "orc_ref_mlp_backward": (None, [_P, _P, _P, _P, _P, _U32, _F, _P, _P]),
     "orc_det_expf": (_F, [_F]),
     "orc_det_expf_array": (None, [_P, _U64, _P]),
     "orc_scene_density": (None, [_P, _U32, _P, _U32, _P]),
@@ -262,6 +263,17 @@ def ref_composite_backward_ray(sraw, rgbraw, dt, gt4, inv_norm: float = 1.0):
     ds, dc, pred = np.zeros(n, np.float32), np.zeros((n, 3), np.float32), np.zeros(3, np.float32)
     loss = lib().orc_ref_composite_backward_ray(_p(sraw), _p(rgbraw), _p(dt), n, _p(gt4), float(inv_norm), _p(ds), _p(dc), _p(pred))
     return float(loss), ds, dc, pred
+
+
+def ref_mlp_backward(dparams_bits, cparams_bits, pos, dirs, draw, loss_scale: float = 1.0):
+    """Reference-model weight gradients (fp64, x loss_scale) for d loss / d raw
+    outputs draw [n][4]: (dD [75776], dC [40960])."""
+    pos = np.ascontiguousarray(pos, np.float32)
+    dirs = np.ascontiguousarray(dirs, np.float32)
+    draw = np.ascontiguousarray(draw, np.float32)
+    dD, dC = np.zeros(ref_param_count(0), np.float64), np.zeros(ref_param_count(1), np.float64)
+    lib().orc_ref_mlp_backward(_p(np.ascontiguousarray(dparams_bits)), _p(np.ascontiguousarray(cparams_bits)), _p(pos), _p(dirs), _p(draw), pos.shape[0], float(loss_scale), _p(dD), _p(dC))
+    return dD, dC
 
 
 def det_expf(x) -> np.ndarray:

@@ -157,3 +157,31 @@ def test_ref_composite_backward():
     assert_rel(got[:, 0], want[:, 0], what="d raw sigma")
     assert_rel(got[:, 1:], want[:, 1:], what="d raw rgb")
     assert abs(loss - want_loss) <= 1e-4 * want_loss
+
+
+@pytest.mark.parametrize("n", [1000, 9000])
+def test_ref_mlp_backward(n):
+    # Weight gradients (fp32, x loss_scale) against the oracle's fp64 sums
+    # with the same fp16 delta rounding: within 1e-2 relative Frobenius norm
+    # per layer (fp16 rounding flips of deltas, fp32 accumulation order).
+    # 9,000 samples span two chunks of the reduction.
+    announce(f"reference-model MLP backward n={n}")
+    m = _ref_model(1.0)
+    pos, dirs = world_points(n, 41), unit_dirs(n, 42)
+    draw = np.random.default_rng(43).normal(0, 1e-2, (n, 4)).astype(np.float32)
+    d_p, d_d, d_r = DeviceArray.from_numpy(pos), DeviceArray.from_numpy(dirs), DeviceArray.from_numpy(draw)
+    gD, gC = DeviceArray((75776,), np.float32), DeviceArray((40960,), np.float32)
+    L.call("nerf_ext_ref_backward", m.density.ptr, m.color.ptr, d_p.ptr, d_d.ptr, d_r.ptr, n, 128.0, gD.ptr, gC.ptr, None)
+    synchronize()
+    wD, wC = orc.ref_mlp_backward(*_bits(m), pos, dirs, draw, loss_scale=128.0)
+    from refmodel_cases import COLOR_SHAPES, DENSITY_SHAPES
+    for got, want, shapes, what in ((gD.numpy(), wD, DENSITY_SHAPES, "density"), (gC.numpy(), wC, COLOR_SHAPES, "colour")):
+        assert np.isfinite(got).all()
+        off = 0
+        for li, (o, i) in enumerate(shapes):
+            g, w = got[off:off + o * i].astype(np.float64), want[off:off + o * i]
+            off += o * i
+            if what == "colour" and li == 3:
+                assert np.all(g.reshape(16, 128)[3:] == 0)   # outputs 3..15 carry no gradient
+            rel = np.linalg.norm(g - w) / max(np.linalg.norm(w), 1e-30)
+            assert rel <= 1e-2, (what, li, rel)

@@ -58,6 +58,17 @@ def _f16(x):
     return np.asarray(x, np.float32).astype(np.float16).astype(np.float32)
 
 
+def _numpy_enc(pos, dirs):
+    """fp16 density input (63 values + 0) and direction encoding (27)."""
+    def enc(v, levels):
+        args = v[:, None, :] * (np.float32(2.0) ** np.arange(levels, dtype=np.float32))[None, :, None]   # exact
+        sc = np.concatenate([np.sin(args.astype(np.float64)), np.cos(args.astype(np.float64))], 2).astype(np.float32)
+        return np.concatenate([v, sc.reshape(v.shape[0], -1)], 1)
+    n = pos.shape[0]
+    pe = _f16(np.concatenate([enc(pos, 10)[:, :63], np.zeros((n, 1), np.float32)], 1))
+    return pe, _f16(enc(dirs, 4))
+
+
 def _numpy_ref(dp, cp, pos, dirs):
     def net(bits, shapes, x):
         W = bits.view(np.float16).astype(np.float64)
@@ -69,15 +80,9 @@ def _numpy_ref(dp, cp, pos, dirs):
             x = _f16(np.maximum(y, 0) if m + 1 < len(shapes) else y)
         return x
     n = pos.shape[0]
-    lv = np.arange(10, dtype=np.float32)
-    args = pos[:, None, :] * (np.float32(2.0) ** lv)[None, :, None]          # [n][10][3], exact
-    pe = np.concatenate([pos, np.concatenate([np.sin(args.astype(np.float64)), np.cos(args.astype(np.float64))], 2).astype(np.float32).reshape(n, -1)], 1)
-    pe = _f16(np.concatenate([pe[:, :63], np.zeros((n, 1), np.float32)], 1))
+    pe, de = _numpy_enc(pos, dirs)
     dens = net(dp, DENSITY_SHAPES, pe)
-    dl = np.arange(4, dtype=np.float32)
-    dargs = dirs[:, None, :] * (np.float32(2.0) ** dl)[None, :, None]
-    de = np.concatenate([dirs, np.concatenate([np.sin(dargs.astype(np.float64)), np.cos(dargs.astype(np.float64))], 2).astype(np.float32).reshape(n, -1)], 1)
-    ci = np.concatenate([dens[:, 1:16], _f16(de), np.zeros((n, 6), np.float32)], 1)
+    ci = np.concatenate([dens[:, 1:16], de, np.zeros((n, 6), np.float32)], 1)
     col = net(cp, COLOR_SHAPES, ci)
     raw = np.stack([dens[:, 0], col[:, 0], col[:, 1], col[:, 2]], 1)
     x = raw[:, 0].astype(np.float64)
@@ -154,3 +159,59 @@ def test_ref_composite_alpha_weighting_and_closed_form(orc):
     w = 0.1 + 0.9 * np.float64(np.float32(0.5))
     assert abs(loss - w * np.sum((pred - g[:3].astype(np.float64)) ** 2)) < 1e-12
     np.testing.assert_allclose(dc[0], a * 2 * w * (pred - g[:3]) * 0.5 * col * (1 - col), rtol=1e-6)
+
+
+def _numpy_ref_backward(dp, cp, pos, dirs, draw, ls):
+    """Matrix-form backward over the batch, same fp16 rounding points."""
+    def fwd(bits, shapes, x):
+        W = bits.view(np.float16).astype(np.float64)
+        acts, Ws, off = [x], [], 0
+        for m, (o, i) in enumerate(shapes):
+            A = W[off:off + o * i].reshape(o, i)
+            off += o * i
+            Ws.append(A)
+            y = (acts[-1].astype(np.float64) @ A.T).astype(np.float32)
+            acts.append(_f16(np.maximum(y, 0) if m + 1 < len(shapes) else y))
+        return acts, Ws
+
+    def bwd(acts, Ws, delta):
+        dWs, din = [None] * len(Ws), None
+        for m in reversed(range(len(Ws))):
+            a = acts[m].astype(np.float64)
+            dWs[m] = delta.astype(np.float64).T @ a
+            din = delta.astype(np.float64) @ Ws[m]
+            if m > 0:
+                delta = np.where(a > 0, _f16(din.astype(np.float32)), 0).astype(np.float32)
+        return np.concatenate([w.ravel() for w in dWs]), din
+
+    n = pos.shape[0]
+    pe, de = _numpy_enc(pos, dirs)
+    dacts, dWs = fwd(dp, DENSITY_SHAPES, pe)
+    ci = np.concatenate([dacts[-1][:, 1:16], de, np.zeros((n, 6), np.float32)], 1)
+    cacts, cWs = fwd(cp, COLOR_SHAPES, ci)
+    dc = np.zeros((n, 16), np.float32)
+    dc[:, :3] = _f16(np.float32(ls) * draw[:, 1:4])
+    gC, cdin = bwd(cacts, cWs, dc)
+    dd = np.zeros((n, 16), np.float32)
+    dd[:, 0] = _f16(np.float32(ls) * draw[:, 0])
+    dd[:, 1:16] = _f16(cdin[:, :15].astype(np.float32))
+    gD, _ = bwd(dacts, dWs, dd)
+    return gD, gC
+
+
+def test_ref_mlp_backward_matches_matrix_form(orc):
+    dp = orc.f32_to_f16_bits(orc.ref_mlp_init(0) * 1.5)
+    cp = orc.f32_to_f16_bits(orc.ref_mlp_init(1) * 1.5)
+    n = 60
+    pos, dirs = world_points(n, 7), unit_dirs(n, 8)
+    draw = np.random.default_rng(9).normal(0, 1e-2, (n, 4)).astype(np.float32)
+    dD, dC = orc.ref_mlp_backward(dp, cp, pos, dirs, draw, loss_scale=128.0)
+    gD, gC = _numpy_ref_backward(dp, cp, pos, dirs, draw, 128.0)
+    for got, want, what in ((dD, gD, "density"), (dC, gC, "colour")):
+        assert np.abs(want).max() > 0
+        # Same rounding points; fp64 sums in different orders may put a rare
+        # fp16 rounding of a delta on the other side of a tie.
+        assert np.linalg.norm(got - want) <= 1e-6 * np.linalg.norm(want), what
+    # Only the colour outputs 0..2 carry gradient: the last colour layer's
+    # rows 3..15 have none.
+    assert np.all(dC[38912 + 3 * 128:] == 0)
