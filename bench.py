@@ -70,6 +70,11 @@ FIELD_TRAFFIC_BYTES_PER_SAMPLE = 1645
 # (backend-cuda.cu:23-54): density 64x128 + 4 x 128x128 + 128x16, colour
 # 48x128 + 2 x 128x128 + 128x16, two flops per multiply-add.
 REF_FLOPS_PER_SAMPLE = 2 * (64 * 128 + 4 * 128 * 128 + 128 * 16) + 2 * (48 * 128 + 2 * 128 * 128 + 128 * 16)
+# Its MLP backward per sample: the forward recomputed (233,472), input
+# gradients of every layer but the density input (density 2 x (16x128 +
+# 4 x 128x128), colour 2 x (16x128 + 2 x 128x128), the colour input's 15
+# geometry columns 2 x 15x128: 208,640) and the weight gradients (233,472).
+REF_BACKWARD_FLOPS_PER_SAMPLE = REF_FLOPS_PER_SAMPLE + 2 * (16 * 128 + 4 * 128 * 128) + 2 * (16 * 128 + 2 * 128 * 128) + 2 * 15 * 128 + REF_FLOPS_PER_SAMPLE
 
 
 def build_workload():
@@ -155,6 +160,13 @@ def kernel_rooflines(reps_small: int = 200):
     res = DeviceArray((n, 4), np.float32)
     ms = timed(lambda: L.call("nerf_ext_ref_field_forward", rm.density.ptr, rm.color.ptr, pos.ptr, dirs.ptr, n, res.ptr, None, st.handle), 20)
     tfs = n * REF_FLOPS_PER_SAMPLE / (ms / 1e3) / 1e12
+    nb = 1 << 18
+    draw = DeviceArray.from_numpy(rng.normal(0, 1e-2, size=(nb, 4)).astype(np.float32))
+    gD, gC = DeviceArray((L.NERF_EXT_REF_DENSITY_PARAMS,), np.float32), DeviceArray((L.NERF_EXT_REF_COLOR_PARAMS,), np.float32)
+    ms_b = timed(lambda: L.call("nerf_ext_ref_backward", rm.density.ptr, rm.color.ptr, pos.ptr, dirs.ptr, draw.ptr, nb, 128.0, gD.ptr, gC.ptr, st.handle), 20)
+    tfs_b = nb * REF_BACKWARD_FLOPS_PER_SAMPLE / (ms_b / 1e3) / 1e12
+    out["ref_backward_2p18"] = {"kernel": "k_ref_backward + k_ref_dw + k_ref_dw_reduce (reference-model MLP backward: recompute, deltas, weight gradients)", "samples": nb, "ms": round(ms_b, 4), "bound": "mfma",
+                                "achieved": round(tfs_b, 1), "peak": MFMA_FP16_PEAK_TFS, "unit": "TFLOP/s", "frac": round(tfs_b / MFMA_FP16_PEAK_TFS, 4), "flops_per_sample": REF_BACKWARD_FLOPS_PER_SAMPLE}
     out["ref_field_2p22"] = {"kernel": "k_ref_field (reference-model mode: frequency encoding, density 64-128x5-16, colour 48-128x3-16, fp16 MFMA)", "samples": n, "ms": round(ms, 4), "bound": "mfma", "achieved": round(tfs, 1),
                              "peak": MFMA_FP16_PEAK_TFS, "unit": "TFLOP/s", "frac": round(tfs / MFMA_FP16_PEAK_TFS, 4), "flops_per_sample": REF_FLOPS_PER_SAMPLE}
     return out

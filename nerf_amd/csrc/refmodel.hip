@@ -178,9 +178,12 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(half_t* buf, uint32_t
 }
 
 // A layer of 128 outputs (8 row blocks) on KB k-blocks of input, four tiles;
-// its fragments start at f0.  With kStore the fp16 outputs also go to st.
+// its fragments start at f0.  With kStore the fp16 outputs also go to st and
+// their ReLU masks to mrow[4 slot + t] (LDS): bit 4 r + e = (row 16 r + 4 g +
+// e of tile t > 0), the lane's 32 rows of one tile in one word.
 template <uint32_t KB, bool kStore = false>
-__device__ __forceinline__ void ref_hidden(const FragSrc& S, uint32_t f0, const half8_t (&in)[4][4], half8_t (&out)[4][4], const RowStore& st = RowStore{}) {
+__device__ __forceinline__ void ref_hidden(const FragSrc& S, uint32_t f0, const half8_t (&in)[4][4], half8_t (&out)[4][4], const RowStore& st = RowStore{}, uint32_t* mrow = nullptr, uint32_t slot = 0u) {
+    uint32_t mb[4] = {0u, 0u, 0u, 0u};
     half4_t lo[4];  // fp16 results of the even row block, joined with the odd one
 #pragma unroll
     for (uint32_t r = 0; r < 8u; ++r) {
@@ -203,12 +206,19 @@ __device__ __forceinline__ void ref_hidden(const FragSrc& S, uint32_t f0, const 
             else lo[t] = h;
             if constexpr (kStore) {
 #pragma unroll
-                for (uint32_t e = 0; e < 4u; ++e) st.put(16u * r + e, t, h[e]);
+                for (uint32_t e = 0; e < 4u; ++e) {
+                    st.put(16u * r + e, t, h[e]);
+                    mb[t] |= ((float)h[e] > 0.0f ? 1u : 0u) << (4u * r + e);
+                }
             }
         }
         // One row block's weights in flight at a time: without the fence the
         // scheduler hoists the next blocks' fragment loads and spills.
         __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (kStore) {
+#pragma unroll
+        for (uint32_t t = 0; t < 4u; ++t) mrow[4u * slot + t] = mb[t];
     }
 }
 
@@ -226,11 +236,12 @@ __device__ __forceinline__ void ref_output(const FragSrc& S, uint32_t f0, const 
 }
 
 // One backward product of a 128-input layer: delta_in = mask . (W^T
-// delta_out) for the four tiles, mask = the stored forward activation of
-// those 128 rows > 0, rounded to fp16 as the next product's B operand and
-// stored for the weight gradients.
+// delta_out) for the four tiles, mask = the forward ReLU mask of those 128
+// rows (bits from ref_hidden), rounded to fp16 as the next product's B
+// operand and stored for the weight gradients.
 template <uint32_t KB>
-__device__ __forceinline__ void ref_backward_layer(const FragSrc& S, uint32_t f0, const half8_t (&in)[4][4], half8_t (&out)[4][4], const RowStore& act, const RowStore& dlt) {
+__device__ __forceinline__ void ref_backward_layer(const FragSrc& S, uint32_t f0, const half8_t (&in)[4][4], half8_t (&out)[4][4], const uint32_t* mrow, uint32_t slot, const RowStore& dlt) {
+    const uint32_t mb[4] = {mrow[4u * slot], mrow[4u * slot + 1u], mrow[4u * slot + 2u], mrow[4u * slot + 3u]};
     half4_t lo[4];
 #pragma unroll
     for (uint32_t r = 0; r < 8u; ++r) {
@@ -249,7 +260,7 @@ __device__ __forceinline__ void ref_backward_layer(const FragSrc& S, uint32_t f0
             half4_t h;
 #pragma unroll
             for (uint32_t e = 0; e < 4u; ++e) {
-                h[e] = (float)act.get(16u * r + e, t) > 0.0f ? to_half_rne(acc[t][e]) : (half_t)0.0f;
+                h[e] = ((mb[t] >> (4u * r + e)) & 1u) ? to_half_rne(acc[t][e]) : (half_t)0.0f;
                 dlt.put(16u * r + e, t, h[e]);
             }
             if (r & 1u) out[t][r >> 1] = half8_t{lo[t][0], lo[t][1], lo[t][2], lo[t][3], h[0], h[1], h[2], h[3]};
@@ -445,11 +456,16 @@ __global__ __launch_bounds__(kBlockThreads) void k_ref_backward(const half8_t* _
             x[t][1]         = *reinterpret_cast<const half8_t*>(r + 32u + 8u * g);
             x[t][2] = x[t][3] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
         }
-        ref_hidden<2, true>(S, kRefLayers[0].frag0, x, y, A(1));
-        ref_hidden<4, true>(S, kRefLayers[1].frag0, y, x, A(2));
-        ref_hidden<4, true>(S, kRefLayers[2].frag0, x, y, A(3));
-        ref_hidden<4, true>(S, kRefLayers[3].frag0, y, x, A(4));
-        ref_hidden<4, true>(S, kRefLayers[4].frag0, x, y, A(5));
+        // The density input part of each LDS row (128 bytes) is free once x is
+        // loaded: lane l keeps its 32 ReLU mask words (inputs of layers 1..5,
+        // 7..9 x four tiles) in row l.
+        __builtin_amdgcn_wave_barrier();
+        uint32_t* M = reinterpret_cast<uint32_t*>(R + lane * kRefPitch);
+        ref_hidden<2, true>(S, kRefLayers[0].frag0, x, y, A(1), M, 0u);
+        ref_hidden<4, true>(S, kRefLayers[1].frag0, y, x, A(2), M, 1u);
+        ref_hidden<4, true>(S, kRefLayers[2].frag0, x, y, A(3), M, 2u);
+        ref_hidden<4, true>(S, kRefLayers[3].frag0, y, x, A(4), M, 3u);
+        ref_hidden<4, true>(S, kRefLayers[4].frag0, x, y, A(5), M, 4u);
         floatx4 dens[4];
         ref_output(S, kRefLayers[5].frag0, y, dens);
 #pragma unroll
@@ -467,9 +483,9 @@ __global__ __launch_bounds__(kBlockThreads) void k_ref_backward(const half8_t* _
             x[t][1] = g < 2u ? *reinterpret_cast<const half8_t*>(r + 16u + 8u * g) : half8_t{0, 0, 0, 0, 0, 0, 0, 0};
         }
         __builtin_amdgcn_wave_barrier();  // the rows are rewritten by the next pass
-        ref_hidden<2, true>(S, kRefLayers[6].frag0, x, y, A(7));
-        ref_hidden<4, true>(S, kRefLayers[7].frag0, y, x, A(8));
-        ref_hidden<4, true>(S, kRefLayers[8].frag0, x, y, A(9));
+        ref_hidden<2, true>(S, kRefLayers[6].frag0, x, y, A(7), M, 5u);
+        ref_hidden<4, true>(S, kRefLayers[7].frag0, y, x, A(8), M, 6u);
+        ref_hidden<4, true>(S, kRefLayers[8].frag0, x, y, A(9), M, 7u);
         // Output deltas.  Lane group 0 holds outputs 0..3 of a sample.
         float4 dr[4];
 #pragma unroll
@@ -482,9 +498,9 @@ __global__ __launch_bounds__(kBlockThreads) void k_ref_backward(const half8_t* _
             x[t][0] = half8_t{h[0], h[1], h[2], h[3], 0, 0, 0, 0};
             x[t][1] = x[t][2] = x[t][3] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
         }
-        ref_backward_layer<1>(S, kRefT[0].frag0, x, y, A(9), D(8));
-        ref_backward_layer<4>(S, kRefT[1].frag0, y, x, A(8), D(7));
-        ref_backward_layer<4>(S, kRefT[2].frag0, x, y, A(7), D(6));
+        ref_backward_layer<1>(S, kRefT[0].frag0, x, y, M, 7u, D(8));
+        ref_backward_layer<4>(S, kRefT[1].frag0, y, x, M, 6u, D(7));
+        ref_backward_layer<4>(S, kRefT[2].frag0, x, y, M, 5u, D(6));
         // Geometry features -> density output deltas 1..15; output 0 = sigma.
         {
             floatx4 geo[4];
@@ -500,29 +516,31 @@ __global__ __launch_bounds__(kBlockThreads) void k_ref_backward(const half8_t* _
                 x[t][1] = x[t][2] = x[t][3] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
             }
         }
-        ref_backward_layer<1>(S, kRefT[4].frag0, x, y, A(5), D(4));
-        ref_backward_layer<4>(S, kRefT[5].frag0, y, x, A(4), D(3));
-        ref_backward_layer<4>(S, kRefT[6].frag0, x, y, A(3), D(2));
-        ref_backward_layer<4>(S, kRefT[7].frag0, y, x, A(2), D(1));
-        ref_backward_layer<4>(S, kRefT[8].frag0, x, y, A(1), D(0));
+        ref_backward_layer<1>(S, kRefT[4].frag0, x, y, M, 4u, D(4));
+        ref_backward_layer<4>(S, kRefT[5].frag0, y, x, M, 3u, D(3));
+        ref_backward_layer<4>(S, kRefT[6].frag0, x, y, M, 2u, D(2));
+        ref_backward_layer<4>(S, kRefT[7].frag0, y, x, M, 1u, D(1));
+        ref_backward_layer<4>(S, kRefT[8].frag0, x, y, M, 0u, D(0));
+        __builtin_amdgcn_wave_barrier();  // the next group rewrites the rows
     }
 }
 
 // Weight gradients from the neuron-major buffers: dW_l[o][i] = sum over
 // samples of delta_l[o][s] input_l[i][s], the samples on the MFMA reduction
 // axis (A = delta rows, B = input rows, 32 samples per MFMA, 16-byte
-// fragment loads).  One wave per (16 x 16 block, chunk of samples); each
-// writes its block's partial for that chunk, and k_ref_dw_reduce sums the
-// chunks in order (deterministic).
-constexpr uint32_t kRefDwBlocks = 456u;  // sum over layers of (n_out / 16) x ceil(n_in / 16)
-__device__ __forceinline__ uint32_t ref_dw_layer(uint32_t b, uint32_t& local) {
+// fragment loads).  One wave per (64 x 64 tile of a layer, chunk of
+// samples), 4 x 4 blocks of 16 x 16 in registers: 16 MFMAs per 8 fragment
+// loads.  Each wave writes its tile's partial for its chunk; k_ref_dw_reduce
+// sums the chunks in order (deterministic).
+constexpr uint32_t kRefDwItems = 32u;  // sum over layers of ceil(n_out / 64) x ceil(n_in / 64)
+__device__ __forceinline__ uint32_t ref_dw_layer(uint32_t item, uint32_t& local) {
     uint32_t l = 0u, first = 0u;
 #pragma unroll
     for (uint32_t k = 0; k < 10u; ++k) {
-        const uint32_t nb = (kRefLayers[k].n_out / 16u) * ((kRefLayers[k].n_in + 15u) / 16u);
-        if (b >= first && b < first + nb) {
+        const uint32_t nb = ((kRefLayers[k].n_out + 63u) / 64u) * ((kRefLayers[k].n_in + 63u) / 64u);
+        if (item >= first && item < first + nb) {
             l     = k;
-            local = b - first;
+            local = item - first;
         }
         first += nb;
     }
@@ -532,24 +550,47 @@ __device__ __forceinline__ uint32_t ref_dw_layer(uint32_t b, uint32_t& local) {
 __global__ __launch_bounds__(kBlockThreads) void k_ref_dw(const half_t* __restrict__ acts, const half_t* __restrict__ dlts, uint32_t np, uint32_t chunk, uint32_t chunks, float* __restrict__ partial) {
     const uint32_t lane = threadIdx.x & 63u, g = lane >> 4, i = lane & 15u;
     const uint32_t w = blockIdx.x * kBlockWaves + (threadIdx.x >> 6);
-    if (w >= kRefDwBlocks * chunks) return;
-    const uint32_t blk = w % kRefDwBlocks, kc = w / kRefDwBlocks;
-    uint32_t local    = 0u;
-    const uint32_t l  = ref_dw_layer(blk, local);
-    const RefLayer L  = kRefLayers[l];
-    const uint32_t ib_n = (L.n_in + 15u) / 16u, ob = local / ib_n, ib = local - ob * ib_n;
+    if (w >= kRefDwItems * chunks) return;
+    const uint32_t item = w % kRefDwItems, kc = w / kRefDwItems;
+    uint32_t local     = 0u;
+    const uint32_t l   = ref_dw_layer(item, local);
+    const RefLayer L   = kRefLayers[l];
+    const uint32_t ig_n = (L.n_in + 63u) / 64u, og = local / ig_n, ig = local - og * ig_n;
+    const uint32_t rb_n = min(4u, L.n_out / 16u - 4u * og), cb_n = min(4u, (L.n_in + 15u) / 16u - 4u * ig);  // uniform
     const uint32_t k_begin = kc * chunk, k_end = min(np, k_begin + chunk);
-    const half_t* a = dlts + (uint64_t)(kDltOff[l] + 16u * ob + i) * np + 8u * g;
-    const half_t* b = acts + (uint64_t)(kActOff[l] + 16u * ib + i) * np + 8u * g;
-    floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (uint32_t k0 = k_begin; k0 < k_end; k0 += 32u) acc = mfma16x16x32(*reinterpret_cast<const half8_t*>(a + k0), *reinterpret_cast<const half8_t*>(b + k0), acc);
+    const half_t* a = dlts + (uint64_t)(kDltOff[l] + 64u * og + i) * np + 8u * g;
+    const half_t* b = acts + (uint64_t)(kActOff[l] + 64u * ig + i) * np + 8u * g;
+    const uint64_t blk = 16ull * np;  // next 16-row block
+    floatx4 acc[4][4];
+#pragma unroll
+    for (uint32_t rb = 0; rb < 4u; ++rb)
+#pragma unroll
+        for (uint32_t cb = 0; cb < 4u; ++cb) acc[rb][cb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t k0 = k_begin; k0 < k_end; k0 += 32u) {
+        half8_t fa[4], fb[4];
+#pragma unroll
+        for (uint32_t q = 0; q < 4u; ++q) {
+            fa[q] = q < rb_n ? *reinterpret_cast<const half8_t*>(a + q * blk + k0) : half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+            fb[q] = q < cb_n ? *reinterpret_cast<const half8_t*>(b + q * blk + k0) : half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+        }
+#pragma unroll
+        for (uint32_t rb = 0; rb < 4u; ++rb)
+#pragma unroll
+            for (uint32_t cb = 0; cb < 4u; ++cb)
+                if (rb < rb_n && cb < cb_n) acc[rb][cb] = mfma16x16x32(fa[rb], fb[cb], acc[rb][cb]);
+    }
     // C lane (g, i): rows 4g + e of the delta block, column i of the input block.
     float* dst = partial + (uint64_t)kc * (kRefDensityParams + kRefColorParams) + (L.network == 0u ? 0u : kRefDensityParams) + L.w_off;
-    const uint32_t col = 16u * ib + i;
-    if (col < L.n_in) {
 #pragma unroll
-        for (uint32_t e = 0; e < 4u; ++e) dst[(16u * ob + 4u * g + e) * L.n_in + col] = acc[e];
-    }
+    for (uint32_t rb = 0; rb < 4u; ++rb)
+#pragma unroll
+        for (uint32_t cb = 0; cb < 4u; ++cb) {
+            const uint32_t col = 64u * ig + 16u * cb + i;
+            if (rb < rb_n && cb < cb_n && col < L.n_in) {
+#pragma unroll
+                for (uint32_t e = 0; e < 4u; ++e) dst[(64u * og + 16u * rb + 4u * g + e) * L.n_in + col] = acc[rb][cb][e];
+            }
+        }
 }
 
 __global__ __launch_bounds__(256) void k_ref_dw_reduce(const float* __restrict__ partial, uint32_t chunks, float* __restrict__ ddensity, float* __restrict__ dcolor) {
@@ -713,7 +754,7 @@ NERF_API NerfStatus nerf_ext_ref_backward(const uint16_t* density_params, const 
     NERF_CHECK_ARG(n <= (1u << 20), "nerf_ext_ref_backward: at most 2^20 samples per call (buffer descriptors address < 4 GiB)");
     hipStream_t st        = (hipStream_t)stream;
     const uint32_t np     = (n + 63u) / 64u * 64u;
-    const uint32_t chunk  = 8192u;
+    const uint32_t chunk  = 4096u;
     const uint32_t chunks = (np + chunk - 1u) / chunk;
     half8_t* frags = nullptr;
     half_t *acts = nullptr, *dlts = nullptr;
@@ -732,7 +773,7 @@ NERF_API NerfStatus nerf_ext_ref_backward(const uint16_t* density_params, const 
         e = hipGetLastError();
     }
     if (e == hipSuccess) {
-        k_ref_dw<<<(kRefDwBlocks * chunks + kBlockWaves - 1u) / kBlockWaves, kBlockThreads, 0, st>>>(acts, dlts, np, chunk, chunks, partial);
+        k_ref_dw<<<(kRefDwItems * chunks + kBlockWaves - 1u) / kBlockWaves, kBlockThreads, 0, st>>>(acts, dlts, np, chunk, chunks, partial);
         e = hipGetLastError();
     }
     if (e == hipSuccess) {
