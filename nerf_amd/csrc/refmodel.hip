@@ -185,11 +185,19 @@ template <uint32_t KB, bool kStore = false>
 __device__ __forceinline__ void ref_hidden(const FragSrc& S, uint32_t f0, const half8_t (&in)[4][4], half8_t (&out)[4][4], const RowStore& st = RowStore{}, uint32_t* mrow = nullptr, uint32_t slot = 0u) {
     uint32_t mb[4] = {0u, 0u, 0u, 0u};
     half4_t lo[4];  // fp16 results of the even row block, joined with the odd one
+    // Row block r + 1's fragments are requested before block r's MFMAs, so
+    // their L2 latency overlaps the block's 4 KB MFMAs.
+    half8_t nxt[KB];
+#pragma unroll
+    for (uint32_t q = 0; q < KB; ++q) nxt[q] = frag_load(S, f0 + q);
 #pragma unroll
     for (uint32_t r = 0; r < 8u; ++r) {
         half8_t a[KB];
 #pragma unroll
-        for (uint32_t q = 0; q < KB; ++q) a[q] = frag_load(S, f0 + r * KB + q);
+        for (uint32_t q = 0; q < KB; ++q) {
+            a[q] = nxt[q];
+            if (r + 1u < 8u) nxt[q] = frag_load(S, f0 + (r + 1u) * KB + q);
+        }
         floatx4 acc[4];
 #pragma unroll
         for (uint32_t t = 0; t < 4u; ++t) {
@@ -243,11 +251,19 @@ template <uint32_t KB>
 __device__ __forceinline__ void ref_backward_layer(const FragSrc& S, uint32_t f0, const half8_t (&in)[4][4], half8_t (&out)[4][4], const uint32_t* mrow, uint32_t slot, const RowStore& dlt) {
     const uint32_t mb[4] = {mrow[4u * slot], mrow[4u * slot + 1u], mrow[4u * slot + 2u], mrow[4u * slot + 3u]};
     half4_t lo[4];
+    // Row block r + 1's fragments are requested before block r's MFMAs, so
+    // their L2 latency overlaps the block's 4 KB MFMAs.
+    half8_t nxt[KB];
+#pragma unroll
+    for (uint32_t q = 0; q < KB; ++q) nxt[q] = frag_load(S, f0 + q);
 #pragma unroll
     for (uint32_t r = 0; r < 8u; ++r) {
         half8_t a[KB];
 #pragma unroll
-        for (uint32_t q = 0; q < KB; ++q) a[q] = frag_load(S, f0 + r * KB + q);
+        for (uint32_t q = 0; q < KB; ++q) {
+            a[q] = nxt[q];
+            if (r + 1u < 8u) nxt[q] = frag_load(S, f0 + (r + 1u) * KB + q);
+        }
         floatx4 acc[4];
 #pragma unroll
         for (uint32_t t = 0; t < 4u; ++t) {
