@@ -1302,7 +1302,9 @@ hipError_t launch_mlp_backward(const TrainParams& P, const TrainBuffers& B, hipS
 }
 
 hipError_t launch_adam(const TrainParams& P, const TrainBuffers& B, hipStream_t st) {
-    const uint32_t cap = device_cu_count() * 16u;
+    // One item (four table entries or one MLP weight) per thread: a grid
+    // that loops leaves its CUs draining unevenly at the end of the stream.
+    const uint32_t cap = 1u << 30;
     // The gradient statistics were taken when the gradients were written.
     if (B.table_elems % 4u) return hipErrorInvalidValue;
     const AdamSeg table{B.table_f32, B.table, B.table_grad, B.table_m, B.table_v};
