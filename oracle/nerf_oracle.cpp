@@ -1,6 +1,6 @@
 // nerf_oracle.cpp — scalar C++ CPU oracle of the NeRF hot path.
 //
-// TEST INFRASTRUCTURE ONLY.  This file is the checker: tests/, the smoke check
+// TEST INFRASTRUCTURE ONLY.  This file is the oracle: tests/, the smoke check
 // in __graft_entry__.py and the cpu_baseline leg of bench.py call it through
 // ctypes (oracle/liboracle.so).  The product (nerf_amd/libnerf.so) never links,
 // loads or calls it.

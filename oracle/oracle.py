@@ -1,4 +1,4 @@
-"""ctypes binding of oracle/liboracle.so — the scalar CPU checker.
+"""ctypes binding of oracle/liboracle.so — the scalar CPU oracle.
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, by the smoke check of
 __graft_entry__.py and by the cpu_baseline leg of bench.py.  The product
