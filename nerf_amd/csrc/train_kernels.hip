@@ -1223,16 +1223,23 @@ __global__ __launch_bounds__(256) void k_adam(TrainParams P, TrainDevState* S, A
     const uint64_t n4 = n_table / 4u, total = n4 + n_mlp;
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += step) {
         if (i < n4) {
-            float4 w = reinterpret_cast<const float4*>(table.w)[i], m = reinterpret_cast<const float4*>(table.m)[i], v = reinterpret_cast<const float4*>(table.v)[i];
-            const float4 g = reinterpret_cast<const float4*>(table.g)[i];
-            adam_one(c, P, w.x, g.x, m.x, v.x);
-            adam_one(c, P, w.y, g.y, m.y, v.y);
-            adam_one(c, P, w.z, g.z, m.z, v.z);
-            adam_one(c, P, w.w, g.w, m.w, v.w);
-            reinterpret_cast<float4*>(table.w)[i] = w;
-            reinterpret_cast<float4*>(table.m)[i] = m;
-            reinterpret_cast<float4*>(table.v)[i] = v;
-            half4_t h = {to_half_rne(w.x), to_half_rne(w.y), to_half_rne(w.z), to_half_rne(w.w)};
+            // The fp32 streams (64 MiB each) pass through once per step:
+            // non-temporal, so they do not sweep the caches.
+            floatx4 w = __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(table.w) + i), m = __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(table.m) + i);
+            floatx4 v = __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(table.v) + i);
+            const floatx4 g = __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(table.g) + i);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                float wk = w[k], mk = m[k], vk = v[k];
+                adam_one(c, P, wk, g[k], mk, vk);
+                w[k] = wk;
+                m[k] = mk;
+                v[k] = vk;
+            }
+            __builtin_nontemporal_store(w, reinterpret_cast<floatx4*>(table.w) + i);
+            __builtin_nontemporal_store(m, reinterpret_cast<floatx4*>(table.m) + i);
+            __builtin_nontemporal_store(v, reinterpret_cast<floatx4*>(table.v) + i);
+            half4_t h = {to_half_rne(w[0]), to_half_rne(w[1]), to_half_rne(w[2]), to_half_rne(w[3])};
             reinterpret_cast<half4_t*>(table.w16)[i] = h;
         } else {
             const uint32_t j = (uint32_t)(i - n4);
