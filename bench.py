@@ -62,10 +62,10 @@ FIELD_FLOPS_PER_SAMPLE = 2 * (32 * 64 + 64 * 16) + 2 * (31 * 64 + 64 * 64 + 64 *
 # HBM traffic of the field kernel per sample on this workload, from rocprofv3
 # FETCH_SIZE (x 2.0) + WRITE_SIZE (x 1.0) on one 800x800 render, the factors
 # being what the same counters read on a plain conversion kernel of known
-# size (profiles/field_forward_800x800_hbm_traffic.md): 793.1 GB + 8.0 GB over
+# size (profiles/field_forward_800x800_hbm_traffic.md): 788.5 GB + 8.0 GB over
 # 486,308,861 samples, summed over the render's three rounds.  Every 4-byte table gather pulls a whole line from
 # beyond L2, hence the gap to the 540 algorithmic bytes.
-FIELD_TRAFFIC_BYTES_PER_SAMPLE = 1647
+FIELD_TRAFFIC_BYTES_PER_SAMPLE = 1638
 # Reference-model network per sample, on the reference's own padded shapes
 # (backend-cuda.cu:23-54): density 64x128 + 4 x 128x128 + 128x16, colour
 # 48x128 + 2 x 128x128 + 128x16, two flops per multiply-add.
