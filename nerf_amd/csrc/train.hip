@@ -109,8 +109,10 @@ NERF_API NerfStatus nerf_configure_training(void* context, const NerfTrainingCon
 NERF_API NerfStatus nerf_train_step(void* context) {
     if (!context) return NERF_STATUS_INVALID_USAGE;
     Context* ctx = static_cast<Context*>(context);
-    if (!ctx->scene_ready || !ctx->training_configured || !ctx->train) return NERF_STATUS_STATE_ERROR;
+    // The trainer is replaced under the mutex (nerf_configure_training), so
+    // it is checked under the mutex too.
     std::scoped_lock lock(ctx->mutex);
+    if (!ctx->scene_ready || !ctx->training_configured || !ctx->train) return NERF_STATUS_STATE_ERROR;
     const NerfStatus s = ctx->train->run_stages(NERF_EXT_STAGE_BEGIN, NERF_EXT_STAGE_END);
     if (s != NERF_STATUS_OK) return NERF_STATUS_CUDA_ERROR;
     ++ctx->host_generation;
@@ -121,8 +123,8 @@ NERF_API NerfStatus nerf_train_step(void* context) {
 NERF_API NerfStatus nerf_read_train_stats(void* context, NerfTrainStats* out_stats) {
     if (!context || !out_stats) return NERF_STATUS_INVALID_USAGE;
     Context* ctx = static_cast<Context*>(context);
-    if (!ctx->training_configured || !ctx->train) return NERF_STATUS_STATE_ERROR;
     std::scoped_lock lock(ctx->mutex);
+    if (!ctx->training_configured || !ctx->train) return NERF_STATUS_STATE_ERROR;
     TrainDevState st{};
     if (ctx->train->read_state(st) != NERF_STATUS_OK) return NERF_STATUS_CUDA_ERROR;
     *out_stats           = st.stats;

@@ -151,11 +151,14 @@ __global__ __launch_bounds__(kThreads) void k_occ_eval(TrainParams P, GridParams
     }
 }
 
+// Warmup start: every word all ones, whatever the density (:1569-1571);
+// refresh: bit = density > threshold, strict (:1628-1634).
 __global__ __launch_bounds__(256) void k_occ_bits(TrainParams P, const TrainDevState* S, const float* density, uint32_t* bits) {
-    if (S->occ_mode == kOccNone) return;
+    const uint32_t mode = S->occ_mode;
+    if (mode == kOccNone) return;
     const uint32_t cell = blockIdx.x * 256u + threadIdx.x;
-    const bool occ      = cell < P.occ_cells && density[cell > P.occ_cells - 1u ? P.occ_cells - 1u : cell] > P.occ_threshold;  // :1632
-    const uint64_t b    = __ballot(occ);
+    const bool occ      = cell < P.occ_cells && (mode == kOccWarmupInit || density[cell > P.occ_cells - 1u ? P.occ_cells - 1u : cell] > P.occ_threshold);
+    const uint64_t b    = mode == kOccWarmupInit ? ~0ull : __ballot(occ);
     const uint32_t words = (P.occ_cells + 31u) / 32u;
     const uint32_t w0    = (blockIdx.x * 256u + (threadIdx.x & ~63u)) >> 5;
     if ((threadIdx.x & 63u) == 0u) {

@@ -48,6 +48,9 @@ NerfStatus trainer_create(const NerfExtTrainDesc* d, const BorrowedModel* borrow
     NERF_CHECK_ARG(d->image_count >= 1u && d->cameras && d->images_rgba8, "trainer: a dataset of at least one image is required");
     NERF_CHECK_ARG(d->grid.table_dtype == NERF_EXT_F16, "trainer: the hash table must be fp16");
     NERF_CHECK_ARG(d->max_rays >= 1u && d->sample_capacity >= 1u && d->max_steps_per_ray >= 1u, "trainer: capacities must be >= 1");
+    // Per-ray sample offsets are a u32 exclusive scan of counts of at most
+    // max_steps_per_ray each: the sum must not wrap.
+    NERF_CHECK_ARG((uint64_t)d->max_rays * d->max_steps_per_ray < (1ull << 32), "trainer: max_rays x max_steps_per_ray must stay below 2^32");
     NERF_CHECK_ARG(d->occupancy_res >= 1u && d->occupancy_res <= 1024u, "trainer: occupancy_res must be 1..1024");
     NERF_CHECK_ARG(d->hyper.loss_scale > 0.0f, "trainer: loss_scale must be > 0");
     const uint32_t W = d->cameras[0].width, H = d->cameras[0].height;

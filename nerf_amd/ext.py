@@ -184,6 +184,13 @@ def read_device(ptr: int, shape, dtype) -> np.ndarray:
     return out
 
 
+def write_device(ptr: int, values: np.ndarray) -> None:
+    """Copies a host array into device memory at a raw device pointer."""
+    values = np.ascontiguousarray(values)
+    if values.nbytes:
+        L.call("nerf_ext_memcpy", int(ptr), values.ctypes.data, values.nbytes, L.NERF_EXT_H2D)
+
+
 def scene_render(gaussians: np.ndarray, cameras: list, steps: int, aabb=(0.0, 0.0, 0.0, 1.0, 1.0, 1.0), stream: Stream | None = None) -> DeviceArray:
     """Renders the analytic scene into RGBA8 images [views][H][W] (alpha =
     1 - transmittance, composited over white)."""

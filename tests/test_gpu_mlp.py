@@ -21,7 +21,7 @@ def test_density_mlp_on_features():
     L.call("nerf_ext_density_mlp", d_w.ptr, d_f.ptr, n, d_o.ptr, None)
     synchronize()
     want = orc.density_mlp(w.view(np.uint16), feat.astype(np.float32))
-    assert_rel(d_o.numpy(), want, what="density mlp")
+    assert_rel(d_o.numpy(), want, what="density mlp", mlp=True)
 
 
 def test_density_mlp_structured_weights():
@@ -59,7 +59,7 @@ def test_density_forward_hash_grid_f32_2p16(n):
     L.call("nerf_ext_density_forward", byref(desc), model.table.ptr, model.density.ptr, d_pos.ptr, n, d_o.ptr, None)
     synchronize()
     want = orc.density_forward(oracle_grid(desc), host_table(model), host_params(model)[0], pos)
-    assert_rel(d_o.numpy(), want, what="density forward")
+    assert_rel(d_o.numpy(), want, what="density forward", mlp=True)
 
 
 def test_density_forward_large_table_values():
@@ -73,7 +73,7 @@ def test_density_forward_large_table_values():
     L.call("nerf_ext_density_forward", byref(desc), model.table.ptr, model.density.ptr, d_pos.ptr, n, d_o.ptr, None)
     synchronize()
     want = orc.density_forward(oracle_grid(desc), host_table(model), host_params(model)[0], pos)
-    assert_rel(d_o.numpy(), want, what="density forward O(1) table")
+    assert_rel(d_o.numpy(), want, what="density forward O(1) table", mlp=True)
 
 
 @pytest.mark.parametrize("log2_t,dtype", [(19, L.NERF_EXT_F16), (16, L.NERF_EXT_F32)])
@@ -90,7 +90,7 @@ def test_field_forward(log2_t, dtype):
     synchronize()
     dp, cp = host_params(model)
     want = orc.field_forward(oracle_grid(desc), host_table(model), dp, cp, pos, dirs)
-    assert_rel(d_o.numpy(), want, what="field forward")
+    assert_rel(d_o.numpy(), want, what="field forward", mlp=True)
 
 
 def test_field_forward_level_major_launch():
@@ -109,7 +109,7 @@ def test_field_forward_level_major_launch():
     rows = np.unique(np.concatenate([np.random.default_rng(5).integers(0, n, 4000), np.arange(n - 70, n)]))
     dp, cp = host_params(model)
     want = orc.field_forward(oracle_grid(desc), host_table(model), dp, cp, np.ascontiguousarray(pos[rows]), np.ascontiguousarray(dirs[rows]))
-    assert_rel(d_o.numpy()[rows], want, what="field forward (level-major)")
+    assert_rel(d_o.numpy()[rows], want, what="field forward (level-major)", mlp=True)
 
 
 @pytest.mark.parametrize("n", [65536, 1000])
@@ -125,4 +125,4 @@ def test_field_mlp_on_features(n):
     L.call("nerf_ext_field_mlp", d_dp.ptr, d_cp.ptr, d_f.ptr, d_d.ptr, n, d_o.ptr, None)
     synchronize()
     want = orc.field_mlp(dp, cp, feats.astype(np.float32), dirs)
-    assert_rel(d_o.numpy(), want, what="field mlp")
+    assert_rel(d_o.numpy(), want, what="field mlp", mlp=True)
