@@ -236,6 +236,17 @@ NERF_API NerfStatus nerf_ext_camera_orbit(uint64_t seed, uint32_t index, float r
  * y flipped: backend-cuda.cu:561-563; march :448-469).  counts [W*H]. */
 NERF_API NerfStatus nerf_ext_march_count(const NerfExtCamera* camera, const NerfExtOccupancy* occupancy, uint32_t max_steps, uint32_t* counts, void* stream);
 
+/* nerf_ext_march_count for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc); it has no counterpart in the reference.  Same arguments, same
+ * counts, bit for bit.  The camera and the per-ray records live in a static
+ * per-GPU scratch array of the library (32 MiB + 256 B, held by every GPU the
+ * library runs on until the process ends), so width x height is limited to
+ * 2^20 rays: larger images return NERF_STATUS_INVALID_USAGE.  Calls that
+ * overlap on one GPU (several streams or threads) share the scratch and race;
+ * serialise them. */
+NERF_API NerfStatus nerf_ext_march_count_noalloc(const NerfExtCamera* camera, const NerfExtOccupancy* occupancy, uint32_t max_steps, uint32_t* counts, void* stream);
+
 /* ------------------------------------------------------------------ render */
 typedef struct NerfExtRenderer NerfExtRenderer;
 

@@ -348,6 +348,7 @@ PROTOTYPES: dict[str, tuple] = {
     # cameras, march, render
     "nerf_ext_camera_orbit": (_S, [_U64, _U32, _F, _P, _U32, _U32, _F, C.POINTER(NerfExtCamera)]),
     "nerf_ext_march_count": (_S, [C.POINTER(NerfExtCamera), C.POINTER(NerfExtOccupancy), _U32, _P, _P]),
+    "nerf_ext_march_count_noalloc": (_S, [C.POINTER(NerfExtCamera), C.POINTER(NerfExtOccupancy), _U32, _P, _P]),
     "nerf_ext_renderer_create": (_S, [C.POINTER(_P)]),
     "nerf_ext_renderer_destroy": (_S, [_P]),
     "nerf_ext_render": (_S, [_P, C.POINTER(NerfExtRenderDesc), _P, _P, _P, C.POINTER(NerfExtRenderStats)]),

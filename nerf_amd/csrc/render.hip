@@ -18,6 +18,7 @@
 // test and no early stop (:534-600) and writes 28 B per step whether or not
 // the step is occupied.
 #include <algorithm>
+#include <mutex>
 #include <vector>
 
 #include "common.hpp"
@@ -72,6 +73,12 @@ __global__ __launch_bounds__(256) void k_march_count(const NerfExtCamera* __rest
     rays[2ull * ray]      = ro;
     rays[2ull * ray + 1u] = rd;
     counts[ray]           = count;
+}
+
+// Writes one camera, passed by value, to device memory (the allocation-free
+// march stages its camera this way instead of a host-to-device copy).
+__global__ void k_stage_camera(NerfExtCamera cam, NerfExtCamera* __restrict__ dst) {
+    if (threadIdx.x == 0u && blockIdx.x == 0u) *dst = cam;
 }
 
 // Eight rays per wave, eight lanes per ray (wave::march<8>): the step
@@ -444,6 +451,47 @@ struct NerfExtRenderer {
     }
 };
 
+namespace nerf_hip {
+namespace {
+
+// Scratch of nerf_ext_march_count_noalloc, one copy per GPU, held until the
+// process ends: the staged camera in the first 256 bytes, then the per-ray
+// records (o, t_near), (d, t_far) that k_march_count writes, 32 bytes per
+// ray, for at most kNoAllocMaxRays rays (32 MiB + 256 B).  In host code the
+// name `scratch` is a host-side stand-in, not a device address: kernels get
+// the address hipGetSymbolAddress returns for the current device.
+constexpr uint32_t kNoAllocMaxRays  = 1u << 20;
+constexpr uint64_t kNoAllocCamBytes = 256u;
+constexpr uint64_t kNoAllocBytes    = kNoAllocCamBytes + 2ull * sizeof(float4) * kNoAllocMaxRays;
+static_assert(sizeof(NerfExtCamera) <= kNoAllocCamBytes, "camera slot");
+__device__ __align__(256) unsigned char scratch[kNoAllocBytes];
+
+constexpr int kNoAllocMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kNoAllocMaxDevices];  // device address of each GPU's copy of `scratch`
+
+// Address of the current device's copy of `scratch`, looked up once per
+// device with that device current.
+hipError_t scratch_address(void** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kNoAllocMaxDevices) return hipErrorInvalidDevice;
+    std::scoped_lock lock(g_scratch_mutex);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e       = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        if (!p) return hipErrorInvalidSymbol;
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return hipSuccess;
+}
+
+}  // namespace
+}  // namespace nerf_hip
+
 using namespace nerf_hip;
 
 extern "C" {
@@ -500,6 +548,34 @@ NERF_API NerfStatus nerf_ext_march_count(const NerfExtCamera* camera, const Nerf
     NERF_LAUNCH_CHECK("k_march_count");
     NERF_HIP_TRY(hipFreeAsync(rays, st));
     NERF_HIP_TRY(hipFreeAsync(dcam, st));
+    return NERF_STATUS_OK;
+}
+
+// nerf_ext_march_count without any allocation: the camera and the ray
+// records live in the library's per-GPU scratch (at most 2^20 rays).  Calls
+// that overlap on one GPU share that scratch and race.
+NERF_API NerfStatus nerf_ext_march_count_noalloc(const NerfExtCamera* camera, const NerfExtOccupancy* occupancy, uint32_t max_steps, uint32_t* counts, void* stream) {
+    NERF_CHECK_ARG(camera && occupancy && counts, "nerf_ext_march_count_noalloc: null pointer");
+    NERF_CHECK_ARG(max_steps > 0u, "nerf_ext_march_count_noalloc: max_steps must be > 0");
+    NERF_CHECK_ARG(camera->width > 0u && camera->height > 0u, "nerf_ext_march_count_noalloc: empty image");
+    const uint64_t n64 = (uint64_t)camera->width * camera->height;
+    if (n64 > kNoAllocMaxRays) {
+        set_error("nerf_ext_march_count_noalloc: " + std::to_string(camera->width) + " x " + std::to_string(camera->height) + " = " + std::to_string(n64) +
+                  " rays exceeds the scratch maximum of 1048576 (2^20) rays; use nerf_ext_march_count");
+        return NERF_STATUS_INVALID_USAGE;
+    }
+    OccView occ;
+    NERF_CHECK_ARG(make_occ_view(*occupancy, occ), "nerf_ext_march_count_noalloc: bad occupancy (empty box, more than 8 cascades or too many cells)");
+    const uint32_t n = (uint32_t)n64;
+    hipStream_t st   = (hipStream_t)stream;
+    void* base       = nullptr;
+    NERF_HIP_TRY(scratch_address(&base));
+    NerfExtCamera* dcam = static_cast<NerfExtCamera*>(base);
+    float4* rays        = reinterpret_cast<float4*>(static_cast<unsigned char*>(base) + kNoAllocCamBytes);
+    k_stage_camera<<<1, 64, 0, st>>>(*camera, dcam);
+    NERF_LAUNCH_CHECK("k_stage_camera");
+    k_march_count<<<(n + 255u) / 256u, 256, 0, st>>>(dcam, n, n, occ, max_steps, rays, counts);
+    NERF_LAUNCH_CHECK("k_march_count");
     return NERF_STATUS_OK;
 }
 
