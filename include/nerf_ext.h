@@ -170,6 +170,33 @@ NERF_API NerfStatus nerf_ext_ref_composite_backward(const uint32_t* counts, cons
  * The fused fp16-MFMA MLP pass on its own (no table gathers). */
 NERF_API NerfStatus nerf_ext_field_mlp(const uint16_t* density_params, const uint16_t* color_params, const uint16_t* features, const float* directions, uint32_t n, float* out, void* stream);
 
+/* ------------------------------------------------------- context options */
+/* Options of a nerf.h context (void* from nerf_create_context); nerf.h itself
+ * cannot express them.
+ *   model_kind: NERF_EXT_MODEL_HASHGRID (the default) or
+ *     NERF_EXT_MODEL_REFERENCE, the reference's own network
+ *     (backend-cuda.cu:23-54) trained, rendered and checkpointed as the
+ *     reference does it.  Changing it replaces the model by a freshly
+ *     initialised one (the reference's init, :1810-1847), clears the
+ *     occupancy grid and, if training is configured, rebuilds the training
+ *     run with the same NerfTrainingConfig (step counter 0).
+ *     nerf_load_network_weights also switches it to the model a file holds
+ *     ("nerf/network-v1": the reference's; "nerf/hashgrid-network-v1").
+ *   inference_sampling: what nerf_inference's samples_per_ray means.
+ *     NERF_EXT_SAMPLING_UNIFORM: the reference's sampling (:534-635),
+ *     exactly samples_per_ray uniform samples over the box per ray, no
+ *     occupancy test, no early stop.  NERF_EXT_SAMPLING_MARCH: the
+ *     occupancy-grid march with samples_per_ray as the step budget and early
+ *     stop at transmittance 1e-4.  NERF_EXT_SAMPLING_DEFAULT: uniform for the
+ *     reference model, march for the hash grid. */
+enum { NERF_EXT_SAMPLING_DEFAULT = 0, NERF_EXT_SAMPLING_UNIFORM = 1, NERF_EXT_SAMPLING_MARCH = 2 };
+typedef struct NerfExtContextOptions {
+    uint32_t model_kind;
+    uint32_t inference_sampling;
+} NerfExtContextOptions;
+NERF_API NerfStatus nerf_ext_context_configure(void* context, const NerfExtContextOptions* options);
+NERF_API NerfStatus nerf_ext_context_options(void* context, NerfExtContextOptions* out);
+
 /* ---------------------------------------------------------- analytic scene */
 typedef struct NerfExtGaussian {
     float cx, cy, cz;   /* centre */
@@ -294,6 +321,17 @@ NERF_API NerfStatus nerf_ext_render(NerfExtRenderer* renderer, const NerfExtRend
  * alpha = 1 - T.  rgba8: device [view][H][W]. */
 NERF_API NerfStatus nerf_ext_scene_render(const NerfExtGaussian* gaussians, uint32_t count, const NerfExtCamera* cameras, uint32_t view_count, const float* aabb6, uint32_t steps, uint32_t* rgba8, void* stream);
 
+/* The reference's inference sampling (backend-cuda.cu:534-635) for
+ * view_count views of one size: per pixel ray (pixel centre, y flipped) clipped
+ * to the box aabb6 = (min xyz, max xyz), samples_per_ray (1..2^19) samples at
+ * t_near + (i + 0.5) dt, dt = (t_far - t_near) / samples_per_ray, no
+ * occupancy test; composite front to back over every sample, then
+ * C + T * background3 (NULL: white), clamped to RGBA8 (rgba8 [view][H][W],
+ * device) and, optionally, the unclamped RGB (rgb_f32 [view][H][W][3]).
+ * Either model kind; hash-grid positions are normalised by the box. */
+NERF_API NerfStatus nerf_ext_render_uniform(NerfExtRenderer* renderer, const NerfExtModel* model, const NerfExtCamera* cameras, uint32_t view_count, const float* aabb6, uint32_t samples_per_ray, const float* background3,
+                                          uint32_t* rgba8, float* rgb_f32, void* stream);
+
 /* ---------------------------------------------------------------- training */
 /* One training step (the reference's nerf_train_step, backend-cuda.cu:2405,
  * with the graph of :2199-2402): pick a camera (hash of the step, :1482),
@@ -321,9 +359,16 @@ typedef struct NerfExtTrainDesc {
     uint32_t target_samples;         /* 0: keep the ray count fixed */
     uint32_t sample_capacity;        /* sample-stream capacity */
     uint32_t max_steps_per_ray;      /* march step budget */
-    float huber_delta;
+    float huber_delta;               /* hash-grid model's Huber loss */
     float table_init_range;          /* hash table init U(-r, r) */
-    uint32_t reserved;
+    uint32_t model_kind;             /* NERF_EXT_MODEL_HASHGRID (0), or
+                                        NERF_EXT_MODEL_REFERENCE: the reference's
+                                        own network (grid unused), trained as the
+                                        reference trains it: its loss
+                                        (backend-cuda.cu:1095-1182), softplus
+                                        occupancy refresh (:1617-1627), Adam over
+                                        its 116,736 weights; sample_capacity at
+                                        most 2^20 */
     uint64_t seed;                   /* hash table init seed */
 } NerfExtTrainDesc;
 

@@ -124,6 +124,9 @@ NERF_EXT_F32 = 0
 NERF_EXT_F16 = 1
 NERF_EXT_MODEL_HASHGRID = 0
 NERF_EXT_MODEL_REFERENCE = 1
+NERF_EXT_SAMPLING_DEFAULT = 0
+NERF_EXT_SAMPLING_UNIFORM = 1
+NERF_EXT_SAMPLING_MARCH = 2
 NERF_EXT_REF_DENSITY_PARAMS = 75776
 NERF_EXT_REF_COLOR_PARAMS = 40960
 NERF_EXT_H2D = 1
@@ -248,6 +251,10 @@ class NerfExtRenderStats(C.Structure):
     ]
 
 
+class NerfExtContextOptions(C.Structure):
+    _fields_ = [("model_kind", C.c_uint32), ("inference_sampling", C.c_uint32)]
+
+
 class NerfExtTrainDesc(C.Structure):
     _fields_ = [
         ("grid", NerfExtGridDesc),
@@ -266,7 +273,7 @@ class NerfExtTrainDesc(C.Structure):
         ("max_steps_per_ray", C.c_uint32),
         ("huber_delta", C.c_float),
         ("table_init_range", C.c_float),
-        ("reserved", C.c_uint32),
+        ("model_kind", C.c_uint32),
         ("seed", C.c_uint64),
     ]
 
@@ -352,6 +359,9 @@ PROTOTYPES: dict[str, tuple] = {
     "nerf_ext_renderer_create": (_S, [C.POINTER(_P)]),
     "nerf_ext_renderer_destroy": (_S, [_P]),
     "nerf_ext_render": (_S, [_P, C.POINTER(NerfExtRenderDesc), _P, _P, _P, C.POINTER(NerfExtRenderStats)]),
+    "nerf_ext_render_uniform": (_S, [_P, C.POINTER(NerfExtModel), C.POINTER(NerfExtCamera), _U32, _P, _U32, _P, _P, _P, _P]),
+    "nerf_ext_context_configure": (_S, [_P, C.POINTER(NerfExtContextOptions)]),
+    "nerf_ext_context_options": (_S, [_P, C.POINTER(NerfExtContextOptions)]),
     "nerf_ext_scene_render": (_S, [_P, _U32, C.POINTER(NerfExtCamera), _U32, _P, _U32, _P, _P]),
     # training
     "nerf_ext_trainer_create": (_S, [C.POINTER(NerfExtTrainDesc), C.POINTER(_P)]),

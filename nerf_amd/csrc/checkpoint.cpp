@@ -144,26 +144,28 @@ struct Reader {
 
 }  // namespace
 
+// The header is written as the reference's JSON library writes it: compact,
+// object keys in byte order at every level (so a file saved here and one
+// saved by the reference for the same weights are byte-identical); tensor
+// data follows in the order of `tensors`.
 bool save(const char* path, const std::vector<Tensor>& tensors, const std::vector<std::pair<std::string, std::string>>& meta_strings, const std::vector<std::pair<std::string, uint64_t>>& meta_numbers) {
-    std::string h = "{\"__metadata__\":{";
-    bool first    = true;
-    for (const auto& kv : meta_strings) {
-        h += (first ? "" : ",") + std::string("\"") + kv.first + "\":\"" + kv.second + "\"";
-        first = false;
-    }
-    for (const auto& kv : meta_numbers) {
-        h += (first ? "" : ",") + std::string("\"") + kv.first + "\":" + std::to_string(kv.second);
-        first = false;
-    }
-    h += "}";
+    std::map<std::string, std::string> meta;  // key -> serialised value
+    for (const auto& kv : meta_strings) meta[kv.first] = "\"" + kv.second + "\"";
+    for (const auto& kv : meta_numbers) meta[kv.first] = std::to_string(kv.second);
+    std::map<std::string, std::string> top;
+    std::string m = "{";
+    for (const auto& kv : meta) m += (m.size() > 1 ? "," : "") + std::string("\"") + kv.first + "\":" + kv.second;
+    top["__metadata__"] = m + "}";
     uint64_t off = 0;
     for (const Tensor& t : tensors) {
         const uint64_t bytes = t.count() * sizeof(float);
-        h += ",\"" + t.name + "\":{\"dtype\":\"F32\",\"shape\":[";
-        for (size_t i = 0; i < t.shape.size(); ++i) h += (i ? "," : "") + std::to_string(t.shape[i]);
-        h += "],\"data_offsets\":[" + std::to_string(off) + "," + std::to_string(off + bytes) + "]}";
+        std::string e        = "{\"data_offsets\":[" + std::to_string(off) + "," + std::to_string(off + bytes) + "],\"dtype\":\"F32\",\"shape\":[";
+        for (size_t i = 0; i < t.shape.size(); ++i) e += (i ? "," : "") + std::to_string(t.shape[i]);
+        top[t.name] = e + "]}";
         off += bytes;
     }
+    std::string h = "{";
+    for (const auto& kv : top) h += (h.size() > 1 ? "," : "") + std::string("\"") + kv.first + "\":" + kv.second;
     h += "}";
     std::ofstream f(path, std::ios::binary | std::ios::trunc);
     if (!f) return false;
@@ -172,6 +174,44 @@ bool save(const char* path, const std::vector<Tensor>& tensors, const std::vecto
     f.write(h.data(), (std::streamsize)h.size());
     for (const Tensor& t : tensors) f.write((const char*)t.data, (std::streamsize)(t.count() * sizeof(float)));
     return (bool)f;
+}
+
+bool read_format(const char* path, std::string& format, std::string& err) {
+    std::ifstream f(path, std::ios::binary);
+    if (!f) {
+        err = "cannot open checkpoint";
+        return false;
+    }
+    uint64_t hl = 0;
+    f.read((char*)&hl, sizeof(hl));
+    if (!f || hl == 0 || hl > (64ull << 20)) {
+        err = "bad header length";
+        return false;
+    }
+    std::string h(hl, '\0');
+    f.read(h.data(), (std::streamsize)hl);
+    if (!f) {
+        err = "truncated header";
+        return false;
+    }
+    Reader r{h.data(), h.data() + h.size()};
+    const Json root = r.value();
+    if (!r.ok || root.kind != Json::Object) {
+        err = "header is not a JSON object";
+        return false;
+    }
+    auto meta = root.obj.find("__metadata__");
+    if (meta == root.obj.end() || meta->second.kind != Json::Object) {
+        err = "no __metadata__";
+        return false;
+    }
+    auto fmt = meta->second.obj.find("format");
+    if (fmt == meta->second.obj.end() || fmt->second.kind != Json::String) {
+        err = "no format in __metadata__";
+        return false;
+    }
+    format = fmt->second.str;
+    return true;
 }
 
 bool load(const char* path, std::vector<Tensor>& tensors, std::string& err) {

@@ -21,6 +21,8 @@ struct Tensor {
 };
 
 bool save(const char* path, const std::vector<Tensor>& tensors, const std::vector<std::pair<std::string, std::string>>& meta_strings, const std::vector<std::pair<std::string, uint64_t>>& meta_numbers);
+// The "format" string of a file's __metadata__.
+bool read_format(const char* path, std::string& format, std::string& err);
 // Fills each tensor's data (shapes must match the file); err explains a failure.
 bool load(const char* path, std::vector<Tensor>& tensors, std::string& err);
 

@@ -359,6 +359,32 @@ hipError_t launch_density(const GridParams& g, const void* table, const half_t* 
 constexpr uint32_t kRefFragments = 444u;
 hipError_t ref_pack_weights(const half_t* dparams, const half_t* cparams, half8_t* frags, hipStream_t stream);
 hipError_t launch_ref_field(const half8_t* frags, const FieldInputs& in, uint32_t n, float4* out4, float4* raw4, hipStream_t stream);
+// Training of the reference model (the trainer's stages).  Rows of the
+// neuron-major fp16 buffers the backward writes per sample: every layer's
+// input (acts) and output delta (dlts); weight-gradient partials per chunk of
+// kRefDwChunk samples; kRefReduceBlocks squared-norm partials.
+constexpr uint32_t kRefActRows = 1136u, kRefDltRows = 1056u;
+constexpr uint32_t kRefDwChunk = 4096u;
+constexpr uint32_t kRefReduceBlocks = 128u;
+constexpr uint32_t kRefParams = NERF_EXT_REF_DENSITY_PARAMS + NERF_EXT_REF_COLOR_PARAMS;
+constexpr uint32_t kRefMaxSamples = 1u << 20;  // per backward call: the buffers stay below 4 GiB (buffer-descriptor range)
+struct RefTrainLaunch {
+    half8_t* frags;    // 64 x kRefFragments
+    half_t* acts;      // [kRefActRows][np]
+    half_t* dlts;      // [kRefDltRows][np]
+    float* partial;    // [chunks][kRefParams]
+    uint32_t np;       // sample capacity rounded up to 64
+    uint32_t chunks;   // ceil(np / kRefDwChunk)
+    uint32_t max_rays;
+};
+// Composite forward/backward with the reference's loss on the trainer's
+// stream: counts = kept, ray and active-ray counts on the device.
+hipError_t launch_ref_composite_train(const RefTrainLaunch& T, const uint32_t* kept, const uint32_t* offsets, const float2* samples, const float4* field, const float4* gt, float4* draw, float* loss_sum,
+                                      const uint32_t* n_rays_dev, const uint32_t* n_active_dev, hipStream_t stream);
+// MLP backward (forward recomputed from the sample stream, in.n_dev samples)
+// and the weight gradients x loss_scale into grad [kRefParams] (density then
+// colour), with kRefReduceBlocks squared-norm partials in norm.
+hipError_t launch_ref_backward_train(const RefTrainLaunch& T, const FieldInputs& in, const float4* draw, float loss_scale, float* grad, double* norm, hipStream_t stream);
 
 // Number of compute units of the current device (cached).
 uint32_t device_cu_count();

@@ -33,7 +33,11 @@ struct Context {
     uint32_t max_sample_steps = 0, max_batch_rays = 0;
     uint64_t alignment = 0;
 
-    // model: fp32 masters + fp16 working copies
+    // model: fp32 masters + fp16 working copies.  NERF_EXT_MODEL_HASHGRID:
+    // table + 3,072 + 7,168 weights; NERF_EXT_MODEL_REFERENCE: the reference's
+    // own network, 75,776 + 40,960 weights, no table.
+    uint32_t model_kind         = NERF_EXT_MODEL_HASHGRID;
+    uint32_t inference_sampling = NERF_EXT_SAMPLING_DEFAULT;
     NerfExtGridDesc grid{};
     GridParams grid_params{};
     uint64_t table_elems = 0;
@@ -41,7 +45,7 @@ struct Context {
     float* table_f32     = nullptr;
     uint16_t* dparams    = nullptr;
     uint16_t* cparams    = nullptr;
-    float* mlp_f32       = nullptr;  // 3072 density then 7168 colour fp32 masters
+    float* mlp_f32       = nullptr;  // density then colour fp32 masters
 
     NerfExtRenderer* renderer = nullptr;
 
@@ -53,8 +57,19 @@ struct Context {
 
     ~Context();
     void release();
+    uint32_t density_params() const { return model_kind == NERF_EXT_MODEL_REFERENCE ? (uint32_t)NERF_EXT_REF_DENSITY_PARAMS : (uint32_t)NERF_EXT_DENSITY_PARAMS; }
+    uint32_t color_params() const { return model_kind == NERF_EXT_MODEL_REFERENCE ? (uint32_t)NERF_EXT_REF_COLOR_PARAMS : (uint32_t)NERF_EXT_COLOR_PARAMS; }
+    // Allocates and initialises a model of model_kind (the reference's init).
     NerfStatus init_model();
+    void free_model();
+    // Replaces the model by a freshly initialised one of `kind`, clears the
+    // occupancy grid and rebuilds a configured training run for it (caller
+    // holds the mutex).
+    NerfStatus switch_model(uint32_t kind);
     NerfStatus upload_weights(const float* mlp32, const float* t32);
+    NerfExtModel model() const;
+    // Builds the trainer for config c (caller holds the mutex).
+    NerfStatus train_configure_locked(const NerfTrainingConfig& c);
     // Zeroes optimiser moments, gradients, occupancy and the step counter.
     NerfStatus train_reset_state();
     void train_release();

@@ -415,13 +415,15 @@ __global__ __launch_bounds__(kBlockThreads) void k_ref_field(const half8_t* __re
 // sigma) for the density outputs.  Samples past n get zero output deltas, so
 // all their deltas are zero.
 template <bool kFromSamples>
-__global__ __launch_bounds__(kBlockThreads) void k_ref_backward(const half8_t* __restrict__ frags, FieldInputs in, uint32_t n, const float4* __restrict__ draw, float loss_scale, half_t* __restrict__ acts,
+__global__ __launch_bounds__(kBlockThreads) void k_ref_backward(const half8_t* __restrict__ frags, FieldInputs in, uint32_t n_cap, const float4* __restrict__ draw, float loss_scale, half_t* __restrict__ acts,
                                                                 half_t* __restrict__ dlts, uint32_t np) {
     __shared__ __align__(16) half_t rows[kBlockWaves][64 * kRefPitch];
     const uint32_t lane = threadIdx.x & 63u, g = lane >> 4, s16 = lane & 15u, wv = threadIdx.x >> 6;
     half_t* R       = rows[wv];
     const FragSrc S = frag_src(frags, lane);
-    const uint32_t groups = np / 64u;
+    // Samples: n_cap, or the count on the device (the trainer's) clamped to it.
+    const uint32_t n      = in.n_dev ? min(*in.n_dev, n_cap) : n_cap;
+    const uint32_t groups = (n + 63u) / 64u;
     const __amdgpu_buffer_rsrc_t ra = row_rsrc(acts, kActRows, np), rd = row_rsrc(dlts, kDltRows, np);
     for (uint32_t gi = blockIdx.x * kBlockWaves + wv; gi < groups; gi += gridDim.x * kBlockWaves) {
         const uint32_t s0    = gi * 64u;
@@ -563,7 +565,11 @@ __device__ __forceinline__ uint32_t ref_dw_layer(uint32_t item, uint32_t& local)
     return l;
 }
 
-__global__ __launch_bounds__(kBlockThreads) void k_ref_dw(const half_t* __restrict__ acts, const half_t* __restrict__ dlts, uint32_t np, uint32_t chunk, uint32_t chunks, float* __restrict__ partial) {
+// np is the row pitch of the buffers; with n_dev the rows hold
+// ceil(min(*n_dev, np) / 64) groups (the rest is stale) and later chunks
+// write zero partials.
+__global__ __launch_bounds__(kBlockThreads) void k_ref_dw(const half_t* __restrict__ acts, const half_t* __restrict__ dlts, uint32_t np, uint32_t chunk, uint32_t chunks, float* __restrict__ partial,
+                                                          const uint32_t* __restrict__ n_dev) {
     const uint32_t lane = threadIdx.x & 63u, g = lane >> 4, i = lane & 15u;
     const uint32_t w = blockIdx.x * kBlockWaves + (threadIdx.x >> 6);
     if (w >= kRefDwItems * chunks) return;
@@ -573,7 +579,8 @@ __global__ __launch_bounds__(kBlockThreads) void k_ref_dw(const half_t* __restri
     const RefLayer L   = kRefLayers[l];
     const uint32_t ig_n = (L.n_in + 63u) / 64u, og = local / ig_n, ig = local - og * ig_n;
     const uint32_t rb_n = min(4u, L.n_out / 16u - 4u * og), cb_n = min(4u, (L.n_in + 15u) / 16u - 4u * ig);  // uniform
-    const uint32_t k_begin = kc * chunk, k_end = min(np, k_begin + chunk);
+    const uint32_t n_used  = n_dev ? (min(*n_dev, np) + 63u) / 64u * 64u : np;
+    const uint32_t k_begin = kc * chunk, k_end = min(n_used, k_begin + chunk);
     const half_t* a = dlts + (uint64_t)(kDltOff[l] + 64u * og + i) * np + 8u * g;
     const half_t* b = acts + (uint64_t)(kActOff[l] + 64u * ig + i) * np + 8u * g;
     const uint64_t blk = 16ull * np;  // next 16-row block
@@ -609,13 +616,37 @@ __global__ __launch_bounds__(kBlockThreads) void k_ref_dw(const half_t* __restri
         }
 }
 
-__global__ __launch_bounds__(256) void k_ref_dw_reduce(const float* __restrict__ partial, uint32_t chunks, float* __restrict__ ddensity, float* __restrict__ dcolor) {
+// Chunk partials summed in chunk order.  With norm != NULL each workgroup
+// also leaves its share of the squared gradient norm in norm[blockIdx.x]:
+// the sum of squares of its finite values, or -1 minus that sum when one of
+// them is not finite (the trainer's gradient statistics, backend-cuda.cu
+// :1451-1476).
+__global__ __launch_bounds__(256) void k_ref_dw_reduce(const float* __restrict__ partial, uint32_t chunks, float* __restrict__ ddensity, float* __restrict__ dcolor, double* __restrict__ norm) {
     constexpr uint32_t P = kRefDensityParams + kRefColorParams;
+    __shared__ double wsq[4];
+    __shared__ uint32_t wbad[4];
+    double sq = 0.0;
+    bool bad  = false;
     for (uint32_t j = blockIdx.x * 256u + threadIdx.x; j < P; j += gridDim.x * 256u) {
         float v = 0.0f;
         for (uint32_t c = 0; c < chunks; ++c) v += partial[(uint64_t)c * P + j];
         if (j < kRefDensityParams) ddensity[j] = v;
         else dcolor[j - kRefDensityParams] = v;
+        if (isfinite(v)) sq += (double)v * (double)v;
+        else bad = true;
+    }
+    if (!norm) return;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) sq += __shfl_xor(sq, o, 64);
+    const bool wave_bad = __ballot(bad) != 0ull;
+    if ((threadIdx.x & 63u) == 0u) {
+        wsq[threadIdx.x >> 6]  = sq;
+        wbad[threadIdx.x >> 6] = wave_bad ? 1u : 0u;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0u) {
+        const double b = ((wsq[0] + wsq[1]) + wsq[2]) + wsq[3];
+        norm[blockIdx.x] = (wbad[0] | wbad[1] | wbad[2] | wbad[3]) ? -1.0 - b : b;
     }
 }
 
@@ -627,10 +658,17 @@ __global__ __launch_bounds__(256) void k_ref_dw_reduce(const float* __restrict__
 // (T_{i+1} c - S_i) . g sigmoid(raw), with sigmoid(raw) = 1 - e^-sigma for
 // sigma = softplus(raw), taken as -expm1(-sigma) (exact for small sigma); the
 // exact derivative where the reference divides by max(1 - alpha, 1e-6).
-__global__ __launch_bounds__(256) void k_ref_composite_train(uint32_t n_rays, const uint32_t* __restrict__ counts, const uint32_t* __restrict__ offsets, const float2* __restrict__ samples, const float4* __restrict__ field,
-                                                              const float4* __restrict__ gt, float inv_norm, float4* __restrict__ draw, float* __restrict__ loss_sum) {
+// With n_rays_dev / n_active_dev (the trainer) the ray count is
+// min(*n_rays_dev, n_rays) and inv_norm = 1 / *n_active_dev (0 without
+// active rays).
+__global__ __launch_bounds__(256) void k_ref_composite_train(uint32_t n_rays_cap, const uint32_t* __restrict__ counts, const uint32_t* __restrict__ offsets, const float2* __restrict__ samples, const float4* __restrict__ field,
+                                                              const float4* __restrict__ gt, float inv_norm_host, float4* __restrict__ draw, float* __restrict__ loss_sum, const uint32_t* __restrict__ n_rays_dev,
+                                                              const uint32_t* __restrict__ n_active_dev) {
     __shared__ float wsum[kBlockWaves];
     const uint32_t lane = threadIdx.x & 63u, nw = gridDim.x * kBlockWaves;
+    const uint32_t n_rays = n_rays_dev ? min(*n_rays_dev, n_rays_cap) : n_rays_cap;
+    const uint32_t active = n_active_dev ? *n_active_dev : 0u;
+    const float inv_norm  = n_active_dev ? (active ? 1.0f / (float)active : 0.0f) : inv_norm_host;
     float wave_loss     = 0.0f;
     for (uint32_t r = blockIdx.x * kBlockWaves + (threadIdx.x >> 6); r < n_rays; r += nw) {
         const uint32_t count = counts[r];
@@ -733,6 +771,28 @@ hipError_t launch_ref_field(const half8_t* frags, const FieldInputs& in, uint32_
     return hipGetLastError();
 }
 
+static_assert(kActRows == kRefActRows && kDltRows == kRefDltRows, "training buffer rows");
+
+hipError_t launch_ref_composite_train(const RefTrainLaunch& T, const uint32_t* kept, const uint32_t* offsets, const float2* samples, const float4* field, const float4* gt, float4* draw, float* loss_sum,
+                                      const uint32_t* n_rays_dev, const uint32_t* n_active_dev, hipStream_t st) {
+    const uint32_t waves = (T.max_rays + kBlockWaves - 1u) / kBlockWaves;
+    const uint32_t cap   = device_cu_count() * 16u;
+    k_ref_composite_train<<<waves < cap ? (waves ? waves : 1u) : cap, kBlockThreads, 0, st>>>(T.max_rays, kept, offsets, samples, field, gt, 0.0f, draw, loss_sum, n_rays_dev, n_active_dev);
+    return hipGetLastError();
+}
+
+hipError_t launch_ref_backward_train(const RefTrainLaunch& T, const FieldInputs& in, const float4* draw, float loss_scale, float* grad, double* norm, hipStream_t st) {
+    const uint32_t need = T.np / 64u / kBlockWaves + 1u, cap = device_cu_count() * 2u;
+    k_ref_backward<true><<<need < cap ? need : cap, kBlockThreads, 0, st>>>(T.frags, in, T.np, draw, loss_scale, T.acts, T.dlts, T.np);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    k_ref_dw<<<(kRefDwItems * T.chunks + kBlockWaves - 1u) / kBlockWaves, kBlockThreads, 0, st>>>(T.acts, T.dlts, T.np, kRefDwChunk, T.chunks, T.partial, in.n_dev);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    k_ref_dw_reduce<<<kRefReduceBlocks, 256, 0, st>>>(T.partial, T.chunks, grad, grad + kRefDensityParams, norm);
+    return hipGetLastError();
+}
+
 }  // namespace nerf_hip
 
 using namespace nerf_hip;
@@ -770,7 +830,7 @@ NERF_API NerfStatus nerf_ext_ref_backward(const uint16_t* density_params, const 
     NERF_CHECK_ARG(n <= (1u << 20), "nerf_ext_ref_backward: at most 2^20 samples per call (buffer descriptors address < 4 GiB)");
     hipStream_t st        = (hipStream_t)stream;
     const uint32_t np     = (n + 63u) / 64u * 64u;
-    const uint32_t chunk  = 4096u;
+    const uint32_t chunk  = kRefDwChunk;
     const uint32_t chunks = (np + chunk - 1u) / chunk;
     half8_t* frags = nullptr;
     half_t *acts = nullptr, *dlts = nullptr;
@@ -789,11 +849,11 @@ NERF_API NerfStatus nerf_ext_ref_backward(const uint16_t* density_params, const 
         e = hipGetLastError();
     }
     if (e == hipSuccess) {
-        k_ref_dw<<<(kRefDwItems * chunks + kBlockWaves - 1u) / kBlockWaves, kBlockThreads, 0, st>>>(acts, dlts, np, chunk, chunks, partial);
+        k_ref_dw<<<(kRefDwItems * chunks + kBlockWaves - 1u) / kBlockWaves, kBlockThreads, 0, st>>>(acts, dlts, np, chunk, chunks, partial, nullptr);
         e = hipGetLastError();
     }
     if (e == hipSuccess) {
-        k_ref_dw_reduce<<<128, 256, 0, st>>>(partial, chunks, ddensity, dcolor);
+        k_ref_dw_reduce<<<kRefReduceBlocks, 256, 0, st>>>(partial, chunks, ddensity, dcolor, nullptr);
         e = hipGetLastError();
     }
     const hipError_t f[4] = {hipFreeAsync(partial, st), hipFreeAsync(dlts, st), hipFreeAsync(acts, st), hipFreeAsync(frags, st)};
@@ -808,7 +868,8 @@ NERF_API NerfStatus nerf_ext_ref_composite_backward(const uint32_t* counts, cons
     NERF_CHECK_ARG(counts && offsets && samples && field && gt && draw && loss_sum, "nerf_ext_ref_composite_backward: null pointer");
     const uint32_t waves  = (n_rays + kBlockWaves - 1u) / kBlockWaves;
     const uint32_t cap    = device_cu_count() * 16u;
-    k_ref_composite_train<<<waves < cap ? waves : cap, kBlockThreads, 0, (hipStream_t)stream>>>(n_rays, counts, offsets, (const float2*)samples, (const float4*)field, (const float4*)gt, inv_norm, (float4*)draw, loss_sum);
+    k_ref_composite_train<<<waves < cap ? waves : cap, kBlockThreads, 0, (hipStream_t)stream>>>(n_rays, counts, offsets, (const float2*)samples, (const float4*)field, (const float4*)gt, inv_norm, (float4*)draw, loss_sum, nullptr,
+                                                                                                nullptr);
     NERF_LAUNCH_CHECK("k_ref_composite_train");
     return NERF_STATUS_OK;
 }

@@ -129,6 +129,87 @@ __device__ __forceinline__ void write_pixel(uint32_t ray, float cr, float cg, fl
     rgba8[ray]        = (255u << 24) | (ub << 16) | (ug << 8) | ur;
 }
 
+// ------------------------------------------------------- uniform sampling
+// The reference's inference sampling (backend-cuda.cu:534-600): spp samples
+// per pixel ray at t_near + (i + 0.5) dt, dt = (t_far - t_near) / spp, over
+// the box, no occupancy test; a ray that misses the box (or whose dt is not
+// positive) has none.  Composite (:601-635) without early stop.
+__global__ __launch_bounds__(256) void k_uniform_rays(const NerfExtCamera* __restrict__ cams, uint32_t pixels_per_view, uint32_t n_rays, float3 bmin, float3 bmax, uint32_t spp, float4* __restrict__ rays,
+                                                     uint32_t* __restrict__ counts) {
+    const uint32_t ray = blockIdx.x * 256u + threadIdx.x;
+    if (ray >= n_rays) return;
+    const uint32_t view     = ray / pixels_per_view;
+    const NerfExtCamera cam = cams[view];
+    const float lo[3] = {bmin.x, bmin.y, bmin.z}, hi[3] = {bmax.x, bmax.y, bmax.z};
+    Ray r;
+    float4 ro = make_float4(0.0f, 0.0f, 0.0f, 0.0f), rd = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    uint32_t count = 0u;
+    if (pixel_ray(cam, ray - view * pixels_per_view, lo, hi, r)) {
+        const float dt = (r.tf - r.tn) / (float)spp;
+        if (dt > 0.0f) {
+            ro    = make_float4(r.o[0], r.o[1], r.o[2], r.tn);
+            rd    = make_float4(r.d[0], r.d[1], r.d[2], r.tf);
+            count = spp;
+        }
+    }
+    rays[2ull * ray]      = ro;
+    rays[2ull * ray + 1u] = rd;
+    counts[ray]           = count;
+}
+
+// One wave per ray: lane j writes samples j, j + 64, ... (coalesced).
+__global__ __launch_bounds__(256) void k_uniform_samples(uint32_t ray0, uint32_t ray_end, const float4* __restrict__ rays, const uint32_t* __restrict__ counts, const uint32_t* __restrict__ offsets,
+                                                        float2* __restrict__ samples, uint32_t* __restrict__ sample_ray) {
+    const uint32_t lane = threadIdx.x & 63u, nw = gridDim.x * 4u;
+    for (uint32_t ray = ray0 + blockIdx.x * 4u + (threadIdx.x >> 6); ray < ray_end; ray += nw) {
+        const uint32_t count = counts[ray];
+        if (count == 0u) continue;
+        const float tn = rays[2ull * ray].w, tf = rays[2ull * ray + 1u].w;
+        const float dt = (tf - tn) / (float)count;
+        const uint32_t base = offsets[ray];
+        for (uint32_t i = lane; i < count; i += 64u) {
+            samples[base + i]    = make_float2(tn + ((float)i + 0.5f) * dt, dt);
+            sample_ray[base + i] = ray;
+        }
+    }
+}
+
+// One wave per ray, 64 samples per step, front to back onto the carried
+// transmittance (wave-wide exclusive product of 1 - alpha), every sample
+// composited; then C + T bg, clamped, to RGBA8.
+__global__ __launch_bounds__(256) void k_uniform_composite(uint32_t ray0, uint32_t ray_end, const uint32_t* __restrict__ counts, const uint32_t* __restrict__ offsets, const float2* __restrict__ samples,
+                                                          const float4* __restrict__ field, float3 bg, uint32_t* __restrict__ rgba8, float* __restrict__ rgb_out) {
+    const uint32_t lane = threadIdx.x & 63u, nw = gridDim.x * 4u;
+    for (uint32_t ray = ray0 + blockIdx.x * 4u + (threadIdx.x >> 6); ray < ray_end; ray += nw) {
+        const uint32_t count = counts[ray];
+        const uint32_t base  = count ? offsets[ray] : 0u;
+        float T = 1.0f, cr = 0.0f, cg = 0.0f, cb = 0.0f;
+        for (uint32_t c0 = 0; c0 < count; c0 += 64u) {
+            const uint32_t i = c0 + lane;
+            const bool valid = i < count;
+            float4 f         = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            float dt         = 0.0f;
+            if (valid) {
+                f  = field[base + i];
+                dt = fmaxf(samples[base + i].y, 0.0f);
+            }
+            const float al   = valid ? 1.0f - __expf(-(f.x * dt)) : 0.0f;
+            const float incl = wave::inclusive_product(1.0f - al);
+            float excl       = __shfl_up(incl, 1, 64);
+            excl             = lane == 0u ? 1.0f : excl;
+            const float w    = T * excl * al;
+            cr += w * f.y;
+            cg += w * f.z;
+            cb += w * f.w;
+            T *= wave::broadcast(incl, 63u);
+        }
+        cr = wave::sum(cr);
+        cg = wave::sum(cg);
+        cb = wave::sum(cb);
+        if (lane == 0u) write_pixel(ray, cr, cg, cb, T, bg, rgba8, rgb_out);
+    }
+}
+
 // Rays without samples get the background; the others start the first
 // round's list (wave-aggregated appends) with T = 1, C = 0.
 __global__ __launch_bounds__(256) void k_round_init(uint32_t ray0, uint32_t ray_end, const uint32_t* __restrict__ counts, float3 bg, uint32_t* __restrict__ rgba8, float* __restrict__ rgb_out, float4* __restrict__ state,
@@ -757,6 +838,76 @@ NERF_API NerfStatus nerf_ext_render(NerfExtRenderer* R, const NerfExtRenderDesc*
         stats->ms_field       = field_ms;
         stats->ms_composite   = total_ms - stats->ms_count - stats->ms_scan - ms_samples - field_ms;
         stats->ms_total       = total_ms;
+    }
+    return NERF_STATUS_OK;
+}
+
+// The reference's inference sampling (backend-cuda.cu:534-635) for any
+// model: rays in chunks of whole 1,024-ray blocks whose spp samples each fit
+// the chunk budget; per chunk the samples, the field, the composite.
+NERF_API NerfStatus nerf_ext_render_uniform(NerfExtRenderer* R, const NerfExtModel* model, const NerfExtCamera* cameras, uint32_t view_count, const float* aabb6, uint32_t samples_per_ray, const float* background3,
+                                          uint32_t* rgba8, float* rgb_f32, void* stream) {
+    NERF_CHECK_ARG(R && model && cameras && aabb6 && rgba8, "nerf_ext_render_uniform: null argument");
+    NERF_CHECK_ARG(view_count >= 1u, "nerf_ext_render_uniform: view_count must be >= 1");
+    NERF_CHECK_ARG(samples_per_ray >= 1u && samples_per_ray <= kMaxSteps, "nerf_ext_render_uniform: samples_per_ray must be 1..2^19");
+    NERF_CHECK_ARG(model->kind <= NERF_EXT_MODEL_REFERENCE, "nerf_ext_render_uniform: unknown model kind");
+    const bool ref_model = model->kind == NERF_EXT_MODEL_REFERENCE;
+    GridParams g{};
+    if (!ref_model) {
+        const NerfStatus gs = make_grid(&model->grid, g);
+        if (gs != NERF_STATUS_OK) return gs;
+        NERF_CHECK_ARG(g.n_levels * g.n_features == 32u, "nerf_ext_render_uniform: the density MLP takes 32 features (16 levels x 2)");
+    }
+    NERF_CHECK_ARG((ref_model || model->table) && model->density_params && model->color_params, "nerf_ext_render_uniform: model has null buffers");
+    for (int a = 0; a < 3; ++a) NERF_CHECK_ARG(aabb6[3 + a] > aabb6[a], "nerf_ext_render_uniform: empty box");
+    const uint32_t W = cameras[0].width, H = cameras[0].height;
+    for (uint32_t v = 0; v < view_count; ++v) NERF_CHECK_ARG(cameras[v].width == W && cameras[v].height == H && W > 0u && H > 0u, "nerf_ext_render_uniform: all views must share a non-empty image size");
+    const uint64_t n64 = (uint64_t)W * H * view_count;
+    NERF_CHECK_ARG(n64 < (1ull << 31), "nerf_ext_render_uniform: too many rays");
+    const uint32_t n_rays = (uint32_t)n64;
+    hipStream_t st        = (hipStream_t)stream;
+    // Chunk: whole blocks of kScanBlockRays rays, at most kChunkSamples samples.
+    const uint64_t blocks_per_chunk = std::max<uint64_t>(1u, kChunkSamples / ((uint64_t)samples_per_ray * kScanBlockRays));
+    const uint32_t chunk_rays       = (uint32_t)std::min<uint64_t>(blocks_per_chunk * kScanBlockRays, (uint64_t)(n_rays + kScanBlockRays - 1u) / kScanBlockRays * kScanBlockRays);
+    const uint64_t chunk_samples    = (uint64_t)chunk_rays * samples_per_ray;
+    NERF_HIP_TRY(R->cams.reserve(view_count));
+    NERF_HIP_TRY(R->rays.reserve(2ull * n_rays));
+    NERF_HIP_TRY(R->counts.reserve(n_rays));
+    NERF_HIP_TRY(R->offsets.reserve(n_rays));
+    NERF_HIP_TRY(R->scan_tmp.reserve(scan_tmp_words(chunk_rays)));
+    NERF_HIP_TRY(R->total.reserve(1));
+    NERF_HIP_TRY(R->samples.reserve(chunk_samples));
+    NERF_HIP_TRY(R->sample_ray.reserve(chunk_samples));
+    NERF_HIP_TRY(R->field.reserve(chunk_samples));
+    NERF_HIP_TRY(hipMemcpyAsync(R->cams.ptr, cameras, sizeof(NerfExtCamera) * view_count, hipMemcpyHostToDevice, st));
+    const float3 bmin = make_float3(aabb6[0], aabb6[1], aabb6[2]), bmax = make_float3(aabb6[3], aabb6[4], aabb6[5]);
+    k_uniform_rays<<<(n_rays + 255u) / 256u, 256, 0, st>>>(R->cams.ptr, W * H, n_rays, bmin, bmax, samples_per_ray, R->rays.ptr, R->counts.ptr);
+    NERF_LAUNCH_CHECK("k_uniform_rays");
+    FieldInputs in{};
+    in.samples    = R->samples.ptr;
+    in.sample_ray = R->sample_ray.ptr;
+    in.rays       = R->rays.ptr;
+    in.n_dev      = reinterpret_cast<const uint32_t*>(R->total.ptr);  // low word of the chunk's sample total
+    for (int a = 0; a < 3; ++a) {
+        in.bmin[a] = aabb6[a];
+        in.bmax[a] = aabb6[3 + a];
+    }
+    const FieldWeights w{(const half_t*)model->density_params, (const half_t*)model->color_params};
+    if (ref_model) {
+        NERF_HIP_TRY(R->ref_frags.reserve(64ull * kRefFragments));
+        NERF_HIP_TRY(ref_pack_weights(w.density, w.color, R->ref_frags.ptr, st));
+    }
+    const float3 bg = background3 ? make_float3(background3[0], background3[1], background3[2]) : make_float3(1.0f, 1.0f, 1.0f);
+    for (uint32_t ray0 = 0; ray0 < n_rays; ray0 += chunk_rays) {
+        const uint32_t ray_end = std::min(n_rays, ray0 + chunk_rays), nr = ray_end - ray0;
+        NERF_HIP_TRY(exclusive_scan_u32(R->counts.ptr + ray0, R->offsets.ptr + ray0, nr, R->scan_tmp.ptr, R->total.ptr, st));
+        const uint32_t waves = std::min<uint32_t>((nr + 3u) / 4u, device_cu_count() * 16u);
+        k_uniform_samples<<<waves, 256, 0, st>>>(ray0, ray_end, R->rays.ptr, R->counts.ptr, R->offsets.ptr, R->samples.ptr, R->sample_ray.ptr);
+        NERF_LAUNCH_CHECK("k_uniform_samples");
+        if (ref_model) NERF_HIP_TRY(launch_ref_field(R->ref_frags.ptr, in, (uint32_t)((uint64_t)nr * samples_per_ray), R->field.ptr, nullptr, st));
+        else NERF_HIP_TRY(launch_field(g, model->table, w, in, (uint32_t)((uint64_t)nr * samples_per_ray), R->field.ptr, st));
+        k_uniform_composite<<<waves, 256, 0, st>>>(ray0, ray_end, R->counts.ptr, R->offsets.ptr, R->samples.ptr, R->field.ptr, bg, rgba8, rgb_f32);
+        NERF_LAUNCH_CHECK("k_uniform_composite");
     }
     return NERF_STATUS_OK;
 }

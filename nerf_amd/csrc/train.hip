@@ -8,7 +8,8 @@
 // rays_per_batch * max_sample_steps_per_ray samples, so no ray is ever cut.
 // nerf_train_step enqueues one step asynchronously (:2417);
 // nerf_read_train_stats synchronises (:2431).  The loss is the Huber loss
-// (delta 0.1) of the hash-grid model, not the reference's alpha-weighted MSE.
+// (delta 0.1) for the hash-grid model, and the reference's alpha-weighted
+// squared error (:1095-1182) for the reference model.
 #include "context.hpp"
 #include "trainer.hpp"
 
@@ -18,6 +19,62 @@ void Context::train_release() {
     delete train;
     train               = nullptr;
     training_configured = false;
+}
+
+// The trainer of a validated NerfTrainingConfig: it borrows the context's
+// model and occupancy buffers; rays_per_batch rays per step,
+// max_sample_steps_per_ray as the march budget, a stream of rays_per_batch *
+// max_sample_steps_per_ray samples (no ray is ever cut).
+NerfStatus Context::train_configure_locked(const NerfTrainingConfig& c) {
+    train_release();
+    const uint64_t total = (uint64_t)c.rays_per_batch * c.max_sample_steps_per_ray;
+    std::vector<NerfExtCamera> cams(image_count);
+    for (uint32_t i = 0; i < image_count; ++i) {
+        const float* m = cameras.data() + 16ull * i;
+        for (int r = 0; r < 3; ++r)
+            for (int k = 0; k < 4; ++k) cams[i].c2w[4 * r + k] = m[4 * r + k];
+        cams[i].fx     = fx;
+        cams[i].fy     = fy;
+        cams[i].cx     = cx;
+        cams[i].cy     = cy;
+        cams[i].width  = width;
+        cams[i].height = height;
+    }
+    // The trainer takes the dataset from host memory; the context keeps its
+    // own device copy only for its lifetime, so copy the images back once.
+    std::vector<uint8_t> host_images((uint64_t)image_count * width * height * 4u);
+    if (!host_images.empty() && hipMemcpy(host_images.data(), images, host_images.size(), hipMemcpyDeviceToHost) != hipSuccess) return NERF_STATUS_CUDA_ERROR;
+    NerfExtTrainDesc d{};
+    d.grid          = grid;
+    d.images_rgba8  = host_images.data();
+    d.cameras       = cams.data();
+    d.image_count   = image_count;
+    d.occupancy_res = occupancy_res;
+    d.aabb_min[0]   = c.aabb_min_x;
+    d.aabb_min[1]   = c.aabb_min_y;
+    d.aabb_min[2]   = c.aabb_min_z;
+    d.aabb_max[0]   = c.aabb_max_x;
+    d.aabb_max[1]   = c.aabb_max_y;
+    d.aabb_max[2]   = c.aabb_max_z;
+    d.hyper             = c.hyper_params;
+    d.occupancy         = c.occupancy_params;
+    d.initial_rays      = c.rays_per_batch;
+    d.max_rays          = c.rays_per_batch;
+    d.target_samples    = 0u;
+    d.sample_capacity   = (uint32_t)total;
+    d.max_steps_per_ray = c.max_sample_steps_per_ray;
+    d.huber_delta       = 0.1f;
+    d.model_kind        = model_kind;
+    if (d.hyper.loss_scale <= 0.0f) d.hyper.loss_scale = 1.0f;
+    const BorrowedModel bm{(half_t*)table, table_f32, (half_t*)dparams, (half_t*)cparams, mlp_f32, bitfield, density_grid};
+    Trainer* t         = nullptr;
+    const NerfStatus s = trainer_create(&d, &bm, stream, &t);
+    if (s != NERF_STATUS_OK) return s == NERF_STATUS_INVALID_USAGE ? s : NERF_STATUS_CUDA_ERROR;
+    train               = t;
+    train_config        = c;
+    host_generation     = 0u;
+    training_configured = true;
+    return NERF_STATUS_OK;
 }
 
 NerfStatus Context::train_reset_state() {
@@ -56,53 +113,7 @@ NERF_API NerfStatus nerf_configure_training(void* context, const NerfTrainingCon
         return NERF_STATUS_INVALID_USAGE;
     }
     std::scoped_lock lock(ctx->mutex);
-    ctx->train_release();
-    std::vector<NerfExtCamera> cams(ctx->image_count);
-    for (uint32_t i = 0; i < ctx->image_count; ++i) {
-        const float* m = ctx->cameras.data() + 16ull * i;
-        for (int r = 0; r < 3; ++r)
-            for (int k = 0; k < 4; ++k) cams[i].c2w[4 * r + k] = m[4 * r + k];
-        cams[i].fx     = ctx->fx;
-        cams[i].fy     = ctx->fy;
-        cams[i].cx     = ctx->cx;
-        cams[i].cy     = ctx->cy;
-        cams[i].width  = ctx->width;
-        cams[i].height = ctx->height;
-    }
-    // The trainer takes the dataset from host memory; the context keeps its
-    // own device copy only for its lifetime, so copy the images back once.
-    std::vector<uint8_t> images((uint64_t)ctx->image_count * ctx->width * ctx->height * 4u);
-    if (!images.empty() && hipMemcpy(images.data(), ctx->images, images.size(), hipMemcpyDeviceToHost) != hipSuccess) return NERF_STATUS_CUDA_ERROR;
-    NerfExtTrainDesc d{};
-    d.grid         = ctx->grid;
-    d.images_rgba8 = images.data();
-    d.cameras      = cams.data();
-    d.image_count  = ctx->image_count;
-    d.occupancy_res = ctx->occupancy_res;
-    d.aabb_min[0] = c.aabb_min_x;
-    d.aabb_min[1] = c.aabb_min_y;
-    d.aabb_min[2] = c.aabb_min_z;
-    d.aabb_max[0] = c.aabb_max_x;
-    d.aabb_max[1] = c.aabb_max_y;
-    d.aabb_max[2] = c.aabb_max_z;
-    d.hyper             = c.hyper_params;
-    d.occupancy         = c.occupancy_params;
-    d.initial_rays      = c.rays_per_batch;
-    d.max_rays          = c.rays_per_batch;
-    d.target_samples    = 0u;
-    d.sample_capacity   = (uint32_t)total;
-    d.max_steps_per_ray = c.max_sample_steps_per_ray;
-    d.huber_delta       = 0.1f;
-    if (d.hyper.loss_scale <= 0.0f) d.hyper.loss_scale = 1.0f;
-    const BorrowedModel bm{(half_t*)ctx->table, ctx->table_f32, (half_t*)ctx->dparams, (half_t*)ctx->cparams, ctx->mlp_f32, ctx->bitfield, ctx->density_grid};
-    Trainer* t = nullptr;
-    const NerfStatus s = trainer_create(&d, &bm, ctx->stream, &t);
-    if (s != NERF_STATUS_OK) return s == NERF_STATUS_INVALID_USAGE ? s : NERF_STATUS_CUDA_ERROR;
-    ctx->train               = t;
-    ctx->train_config        = c;
-    ctx->host_generation     = 0u;
-    ctx->training_configured = true;
-    return NERF_STATUS_OK;
+    return ctx->train_configure_locked(c);
 }
 
 // backend-cuda.cu:2405-2420.

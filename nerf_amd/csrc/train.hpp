@@ -118,7 +118,18 @@ struct TrainBuffers {
     float* mlp_v;
     float* dw_partials;          // [kDxMaxBlocks][10240] per-workgroup weight-gradient partials
     double* norm_partials;       // [norm_partial_count] per-workgroup squared-gradient-norm partials
-    uint64_t table_elems;
+    uint64_t table_elems;        // 0 for the reference model (no hash grid)
+    // Which network trains: NERF_EXT_MODEL_HASHGRID (the buffers above) or
+    // NERF_EXT_MODEL_REFERENCE (the reference's own network: no table, no
+    // features; the backward's buffers below).
+    uint32_t model_kind;
+    uint32_t mlp_params;         // kMlpParams or kRefParams (masters, moments, gradients)
+    uint32_t density_params;     // the density network's share (first in mlp_f32)
+    RefTrainLaunch ref;          // reference model: packed weights, backward buffers
+    float* occ_points;           // reference model: [occ_window][3] world cell centres of a refresh
+    float* occ_dirs;             // [occ_window][3] (0, 0, 1)
+    float4* occ_field;           // [occ_window] field at those points
+    uint32_t occ_window;         // min(cells_per_update, cells)
 };
 
 constexpr uint32_t kDxMaxBlocks = 1024;  // workgroups of the input-gradient pass (two per CU)
@@ -130,8 +141,11 @@ constexpr uint32_t kMlpParams  = NERF_EXT_DENSITY_PARAMS + NERF_EXT_COLOR_PARAMS
 
 // Workgroups of the coarse-level reduction (16 columns of two entries each).
 inline uint32_t coarse_reduce_blocks(const CoarsePlan& C) { return (C.row / 2u + 15u) / 16u; }
-// Squared-norm partials of a step: coarse reduction, bins, weight gradients.
-inline uint32_t norm_partial_count(const TrainBuffers& B) { return coarse_reduce_blocks(B.coarse) + B.n_bins + kMlpParams / 64u; }
+// Squared-norm partials of a step: coarse reduction, bins, weight gradients
+// (the reference model: its weight-gradient reduction only).
+inline uint32_t norm_partial_count(const TrainBuffers& B) {
+    return B.model_kind == NERF_EXT_MODEL_REFERENCE ? kRefReduceBlocks : coarse_reduce_blocks(B.coarse) + B.n_bins + kMlpParams / 64u;
+}
 
 // Launches one stage (NERF_EXT_STAGE_*) of a training step on `stream`.
 // `occupancy_update` selects the occupancy-maintenance kernels (the schedule

@@ -167,6 +167,33 @@ __global__ __launch_bounds__(256) void k_occ_bits(TrainParams P, const TrainDevS
     }
 }
 
+// Reference model: the refresh window's cell centres in world coordinates
+// (:1575-1611; direction (0, 0, 1), which the density does not read), for a
+// field evaluation, then density[cell] = max(density[cell], sigma) with
+// sigma = softplus of the raw density output (:1617-1627).
+__global__ __launch_bounds__(256) void k_occ_points(TrainParams P, const TrainDevState* S, uint32_t window, float* __restrict__ points, float* __restrict__ dirs) {
+    const uint32_t k = blockIdx.x * 256u + threadIdx.x;
+    if (k >= window || S->occ_mode != kOccRefresh) return;
+    const uint32_t start = (uint32_t)((uint64_t)S->frame * window % P.occ_cells);
+    const uint32_t cell  = (start + k) % P.occ_cells;
+    const uint32_t res = P.occ_res, z = cell / (res * res), rem = cell - z * res * res, y = rem / res, x = rem - y * res;
+    const uint32_t c[3] = {x, y, z};
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+        const float step    = (P.bmax[a] - P.bmin[a]) / (float)res;
+        points[3u * k + a]  = P.bmin[a] + ((float)c[a] + 0.5f) * step;
+        dirs[3u * k + a]    = a == 2 ? 1.0f : 0.0f;
+    }
+}
+
+__global__ __launch_bounds__(256) void k_occ_apply_field(TrainParams P, const TrainDevState* S, uint32_t window, const float4* __restrict__ field, float* __restrict__ density) {
+    const uint32_t k = blockIdx.x * 256u + threadIdx.x;
+    if (k >= window || S->occ_mode != kOccRefresh) return;
+    const uint32_t start = (uint32_t)((uint64_t)S->frame * window % P.occ_cells);
+    const uint32_t cell  = (start + k) % P.occ_cells;
+    density[cell]        = fmaxf(density[cell], field[k].x);
+}
+
 // ---------------------------------------------------------------- sampling
 // Occupancy cell of p (backend-cuda.cu:338-351), or wave::kOutside.
 __device__ __forceinline__ uint32_t occ_cell_at(const TrainParams& P, const float p[3]) {
@@ -1319,12 +1346,72 @@ hipError_t launch_adam(const TrainParams& P, const TrainBuffers& B, hipStream_t 
     if (B.table_elems % 4u) return hipErrorInvalidValue;
     const AdamSeg table{B.table_f32, B.table, B.table_grad, B.table_m, B.table_v};
     const AdamSeg mlp{B.mlp_f32, B.dparams, B.mlp_grad, B.mlp_m, B.mlp_v};
-    k_adam<<<grid_for(B.table_elems / 4u + kMlpParams, cap), 256, 0, st>>>(P, B.state, table, B.table_elems, mlp, B.cparams, NERF_EXT_DENSITY_PARAMS, kMlpParams);
+    k_adam<<<grid_for(B.table_elems / 4u + B.mlp_params, cap), 256, 0, st>>>(P, B.state, table, B.table_elems, mlp, B.cparams, B.density_params, B.mlp_params);
+    return hipGetLastError();
+}
+
+// Stages both models share: the sampler, Adam (over whatever parameters the
+// run has) and the end of the step.
+static hipError_t launch_train_stage_common(const TrainParams& P, const TrainBuffers& B, uint32_t stage, hipStream_t st) {
+    switch (stage) {
+    case NERF_EXT_STAGE_SAMPLE: {
+        k_train_rays<<<ray_wave_blocks(P.max_rays), 256, 0, st>>>(P, B.state, B.cams, B.images, B.bits, B.rays, B.gt, B.counts, B.seg_t, B.seg_seen, B.seg_reached, B.segs);
+        const hipError_t e = exclusive_scan_u32(B.counts, B.offsets, P.max_rays, B.scan_tmp, &B.state->total, st);
+        if (e != hipSuccess) return e;
+        k_train_samples<<<ray_wave_blocks(P.max_rays * B.segs), 256, 0, st>>>(P, B.state, B.cams, B.bits, B.rays, B.counts, B.offsets, B.seg_t, B.seg_seen, B.seg_reached, B.segs, B.kept, B.samples,
+                                                                              B.sample_ray);
+        break;
+    }
+    case NERF_EXT_STAGE_ADAM: return launch_adam(P, B, st);
+    case NERF_EXT_STAGE_END: k_step_end<<<1, 64, 0, st>>>(P, B.state); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// Stages of the reference model: the same step with the reference's network
+// (packed into MFMA fragments once per step, at its start), its loss and its
+// backward; no hash table.
+static hipError_t launch_ref_train_stage(const TrainParams& P, const TrainBuffers& B, uint32_t stage, bool occupancy_update, hipStream_t st) {
+    FieldInputs in{};
+    in.samples    = B.samples;
+    in.sample_ray = B.sample_ray;
+    in.rays       = B.rays;
+    in.n_dev      = &B.state->n_samples;
+    switch (stage) {
+    case NERF_EXT_STAGE_BEGIN:
+        k_step_begin<<<1, 64, 0, st>>>(P, B.state);
+        return ref_pack_weights(B.dparams, B.cparams, B.ref.frags, st);
+    case NERF_EXT_STAGE_OCCUPANCY:
+        if (occupancy_update) {
+            k_occ_decay<<<(P.occ_cells + 255u) / 256u, 256, 0, st>>>(P, B.state, B.density);
+            const uint32_t wb = (B.occ_window + 255u) / 256u;
+            k_occ_points<<<wb, 256, 0, st>>>(P, B.state, B.occ_window, B.occ_points, B.occ_dirs);
+            FieldInputs q{};
+            q.positions  = B.occ_points;
+            q.directions = B.occ_dirs;
+            const hipError_t e = launch_ref_field(B.ref.frags, q, B.occ_window, B.occ_field, nullptr, st);
+            if (e != hipSuccess) return e;
+            k_occ_apply_field<<<wb, 256, 0, st>>>(P, B.state, B.occ_window, B.occ_field, B.density);
+            k_occ_bits<<<(P.occ_cells + 255u) / 256u, 256, 0, st>>>(P, B.state, B.density, B.bits);
+        }
+        break;
+    case NERF_EXT_STAGE_FORWARD: return launch_ref_field(B.ref.frags, in, P.sample_cap, B.field, nullptr, st);
+    case NERF_EXT_STAGE_COMPOSITE: return launch_ref_composite_train(B.ref, B.kept, B.offsets, B.samples, B.field, B.gt, B.draw, &B.state->loss_sum, &B.state->n_rays, &B.state->n_active, st);
+    case NERF_EXT_STAGE_BACKWARD: {
+        const hipError_t e = launch_ref_backward_train(B.ref, in, B.draw, P.loss_scale, B.mlp_grad, B.norm_partials, st);
+        if (e != hipSuccess) return e;
+        k_grad_norm<<<1, kNormThreads, 0, st>>>(B.norm_partials, norm_partial_count(B), B.state);
+        break;
+    }
+    default: return launch_train_stage_common(P, B, stage, st);
+    }
     return hipGetLastError();
 }
 
 hipError_t launch_train_stage(const TrainParams& P, const TrainBuffers& B, uint32_t stage, bool occupancy_update, hipStream_t st) {
-    const uint32_t cus        = device_cu_count();
+    if (B.model_kind == NERF_EXT_MODEL_REFERENCE) return launch_ref_train_stage(P, B, stage, occupancy_update, st);
+    const uint32_t cus = device_cu_count();
     switch (stage) {
     case NERF_EXT_STAGE_BEGIN: k_step_begin<<<1, 64, 0, st>>>(P, B.state); break;
     case NERF_EXT_STAGE_OCCUPANCY:
@@ -1334,14 +1421,6 @@ hipError_t launch_train_stage(const TrainParams& P, const TrainBuffers& B, uint3
             k_occ_bits<<<(P.occ_cells + 255u) / 256u, 256, 0, st>>>(P, B.state, B.density, B.bits);
         }
         break;
-    case NERF_EXT_STAGE_SAMPLE: {
-        k_train_rays<<<ray_wave_blocks(P.max_rays), 256, 0, st>>>(P, B.state, B.cams, B.images, B.bits, B.rays, B.gt, B.counts, B.seg_t, B.seg_seen, B.seg_reached, B.segs);
-        const hipError_t e = exclusive_scan_u32(B.counts, B.offsets, P.max_rays, B.scan_tmp, &B.state->total, st);
-        if (e != hipSuccess) return e;
-        k_train_samples<<<ray_wave_blocks(P.max_rays * B.segs), 256, 0, st>>>(P, B.state, B.cams, B.bits, B.rays, B.counts, B.offsets, B.seg_t, B.seg_seen, B.seg_reached, B.segs, B.kept, B.samples,
-                                                                              B.sample_ray);
-        break;
-    }
     case NERF_EXT_STAGE_FORWARD: {
         FieldInputs in{};
         in.samples      = B.samples;
@@ -1357,9 +1436,7 @@ hipError_t launch_train_stage(const TrainParams& P, const TrainBuffers& B, uint3
     }
     case NERF_EXT_STAGE_COMPOSITE: return launch_composite_train(P, B, st);
     case NERF_EXT_STAGE_BACKWARD: return launch_mlp_backward(P, B, st);
-    case NERF_EXT_STAGE_ADAM: return launch_adam(P, B, st);
-    case NERF_EXT_STAGE_END: k_step_end<<<1, 64, 0, st>>>(P, B.state); break;
-    default: return hipErrorInvalidValue;
+    default: return launch_train_stage_common(P, B, stage, st);
     }
     return hipGetLastError();
 }

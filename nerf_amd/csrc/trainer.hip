@@ -46,7 +46,10 @@ NerfStatus trainer_create(const NerfExtTrainDesc* d, const BorrowedModel* borrow
     NERF_CHECK_ARG(d && out, "trainer: null argument");
     *out = nullptr;
     NERF_CHECK_ARG(d->image_count >= 1u && d->cameras && d->images_rgba8, "trainer: a dataset of at least one image is required");
-    NERF_CHECK_ARG(d->grid.table_dtype == NERF_EXT_F16, "trainer: the hash table must be fp16");
+    NERF_CHECK_ARG(d->model_kind <= NERF_EXT_MODEL_REFERENCE, "trainer: unknown model_kind");
+    const bool ref = d->model_kind == NERF_EXT_MODEL_REFERENCE;
+    NERF_CHECK_ARG(ref || d->grid.table_dtype == NERF_EXT_F16, "trainer: the hash table must be fp16");
+    NERF_CHECK_ARG(!ref || d->sample_capacity <= kRefMaxSamples, "trainer: the reference model takes at most 2^20 samples per step (sample_capacity)");
     NERF_CHECK_ARG(d->max_rays >= 1u && d->sample_capacity >= 1u && d->max_steps_per_ray >= 1u, "trainer: capacities must be >= 1");
     // Per-ray sample offsets are a u32 exclusive scan of counts of at most
     // max_steps_per_ray each: the sum must not wrap.
@@ -58,12 +61,15 @@ NerfStatus trainer_create(const NerfExtTrainDesc* d, const BorrowedModel* borrow
     for (int a = 0; a < 3; ++a) NERF_CHECK_ARG(d->aabb_max[a] > d->aabb_min[a], "trainer: empty AABB");
 
     auto t = std::make_unique<Trainer>();
-    GridParams g;
-    NerfStatus st = make_grid(&d->grid, g);
-    if (st != NERF_STATUS_OK) return st;
-    NERF_CHECK_ARG(g.n_levels * g.n_features == 32u, "trainer: the density MLP takes 32 features (16 levels x 2)");
-    NERF_CHECK_ARG((uint64_t)g.n_levels * g.table_size <= (uint64_t)kMaxBins * kBinEntries, "trainer: at most 2^26 table entries (16 levels x 2^22)");
-    NERF_CHECK_ARG((uint64_t)d->sample_capacity * g.n_levels * 8u < (1ull << 32), "trainer: sample_capacity x 128 must stay below 2^32 gradient records");
+    GridParams g{};
+    NerfStatus st = NERF_STATUS_OK;
+    if (!ref) {
+        st = make_grid(&d->grid, g);
+        if (st != NERF_STATUS_OK) return st;
+        NERF_CHECK_ARG(g.n_levels * g.n_features == 32u, "trainer: the density MLP takes 32 features (16 levels x 2)");
+        NERF_CHECK_ARG((uint64_t)g.n_levels * g.table_size <= (uint64_t)kMaxBins * kBinEntries, "trainer: at most 2^26 table entries (16 levels x 2^22)");
+        NERF_CHECK_ARG((uint64_t)d->sample_capacity * g.n_levels * 8u < (1ull << 32), "trainer: sample_capacity x 128 must stay below 2^32 gradient records");
+    }
     if (stream) {
         t->stream = stream;
     } else {
@@ -101,9 +107,12 @@ NerfStatus trainer_create(const NerfExtTrainDesc* d, const BorrowedModel* borrow
     P.occ_warmup           = d->occupancy.warmup_steps;
     P.occ_cells            = d->occupancy_res * d->occupancy_res * d->occupancy_res;
 
-    TrainBuffers& B = t->B;
-    B.grid          = g;
-    B.table_elems   = (uint64_t)g.n_levels * g.table_size * g.n_features;
+    TrainBuffers& B    = t->B;
+    B.grid             = g;
+    B.model_kind       = d->model_kind;
+    B.table_elems      = ref ? 0ull : (uint64_t)g.n_levels * g.table_size * g.n_features;
+    B.mlp_params       = ref ? kRefParams : kMlpParams;
+    B.density_params   = ref ? (uint32_t)NERF_EXT_REF_DENSITY_PARAMS : (uint32_t)NERF_EXT_DENSITY_PARAMS;
     Trainer& T      = *t;
     NERF_HIP_TRY(alloc(T, B.state, 1));
     NerfExtCamera* cams = nullptr;
@@ -125,8 +134,27 @@ NerfStatus trainer_create(const NerfExtTrainDesc* d, const BorrowedModel* borrow
     NERF_HIP_TRY(alloc(T, B.samples, P.sample_cap));
     NERF_HIP_TRY(alloc(T, B.sample_ray, P.sample_cap));
     NERF_HIP_TRY(alloc(T, B.field, P.sample_cap));
-    NERF_HIP_TRY(alloc(T, B.features, 32ull * P.sample_cap));
     NERF_HIP_TRY(alloc(T, B.draw, P.sample_cap));
+    B.n_dense = 0u;
+    B.coarse  = CoarsePlan{};
+    B.n_bins  = 0u;
+    if (ref) {
+        RefTrainLaunch& R = B.ref;
+        R.np              = (P.sample_cap + 63u) / 64u * 64u;
+        R.chunks          = (R.np + kRefDwChunk - 1u) / kRefDwChunk;
+        R.max_rays        = P.max_rays;
+        NERF_HIP_TRY(alloc(T, R.frags, 64ull * kRefFragments));
+        NERF_HIP_TRY(alloc(T, R.acts, (uint64_t)kRefActRows * R.np));
+        NERF_HIP_TRY(alloc(T, R.dlts, (uint64_t)kRefDltRows * R.np));
+        NERF_HIP_TRY(alloc(T, R.partial, (uint64_t)R.chunks * kRefParams));
+        B.occ_window = P.occ_cells_per_update < P.occ_cells ? P.occ_cells_per_update : P.occ_cells;
+        NERF_HIP_TRY(alloc(T, B.occ_points, 3ull * B.occ_window));
+        NERF_HIP_TRY(alloc(T, B.occ_dirs, 3ull * B.occ_window));
+        NERF_HIP_TRY(alloc(T, B.occ_field, B.occ_window));
+        NERF_HIP_TRY(hipMemsetAsync(B.occ_points, 0, 12ull * B.occ_window, T.stream));
+        NERF_HIP_TRY(hipMemsetAsync(B.occ_dirs, 0, 12ull * B.occ_window, T.stream));
+    } else {
+    NERF_HIP_TRY(alloc(T, B.features, 32ull * P.sample_cap));
     NERF_HIP_TRY(alloc(T, B.dfeat, 16ull * P.sample_cap));
     // Leading dense levels of at most kCoarseMaxEntries entries are summed in
     // LDS slabs; binned, the records of every sample would crowd into their
@@ -160,13 +188,14 @@ NerfStatus trainer_create(const NerfExtTrainDesc* d, const BorrowedModel* borrow
     NERF_HIP_TRY(alloc(T, B.bin_scan_tmp, scan_tmp_words(B.n_bins * kBinBlocks + 1u)));
     NERF_HIP_TRY(alloc(T, B.bin_total, 1));
     NERF_HIP_TRY(alloc(T, B.rec, B.rec_cap));
+    NERF_HIP_TRY(alloc(T, B.dw_partials, (uint64_t)kDxMaxBlocks * kMlpParams));
+    }
     NERF_HIP_TRY(alloc(T, B.table_grad, B.table_elems));
     NERF_HIP_TRY(alloc(T, B.table_m, B.table_elems));
     NERF_HIP_TRY(alloc(T, B.table_v, B.table_elems));
-    NERF_HIP_TRY(alloc(T, B.mlp_grad, kMlpParams));
-    NERF_HIP_TRY(alloc(T, B.mlp_m, kMlpParams));
-    NERF_HIP_TRY(alloc(T, B.mlp_v, kMlpParams));
-    NERF_HIP_TRY(alloc(T, B.dw_partials, (uint64_t)kDxMaxBlocks * kMlpParams));
+    NERF_HIP_TRY(alloc(T, B.mlp_grad, B.mlp_params));
+    NERF_HIP_TRY(alloc(T, B.mlp_m, B.mlp_params));
+    NERF_HIP_TRY(alloc(T, B.mlp_v, B.mlp_params));
     NERF_HIP_TRY(alloc(T, B.norm_partials, norm_partial_count(B)));
     if (borrowed) {
         B.table     = borrowed->table;
@@ -179,9 +208,9 @@ NerfStatus trainer_create(const NerfExtTrainDesc* d, const BorrowedModel* borrow
     } else {
         NERF_HIP_TRY(alloc(T, B.table, B.table_elems));
         NERF_HIP_TRY(alloc(T, B.table_f32, B.table_elems));
-        NERF_HIP_TRY(alloc(T, B.dparams, NERF_EXT_DENSITY_PARAMS));
-        NERF_HIP_TRY(alloc(T, B.cparams, NERF_EXT_COLOR_PARAMS));
-        NERF_HIP_TRY(alloc(T, B.mlp_f32, kMlpParams));
+        NERF_HIP_TRY(alloc(T, B.dparams, B.density_params));
+        NERF_HIP_TRY(alloc(T, B.cparams, B.mlp_params - B.density_params));
+        NERF_HIP_TRY(alloc(T, B.mlp_f32, B.mlp_params));
         NERF_HIP_TRY(alloc(T, B.bits, (P.occ_cells + 31u) / 32u));
         NERF_HIP_TRY(alloc(T, B.density, P.occ_cells));
     }
@@ -192,19 +221,28 @@ NerfStatus trainer_create(const NerfExtTrainDesc* d, const BorrowedModel* borrow
     st             = T.reset();
     if (st != NERF_STATUS_OK) return st;
     if (!borrowed) {
-        NerfExtGridDesc g32 = d->grid;
-        g32.table_dtype     = NERF_EXT_F32;
-        st                  = nerf_ext_grid_init_table(&g32, d->seed, d->table_init_range, B.table_f32, s);
-        if (st != NERF_STATUS_OK) return st;
-        st = nerf_ext_float_to_half(B.table_f32, (uint16_t*)B.table, B.table_elems, s);
-        if (st != NERF_STATUS_OK) return st;
-        std::vector<float> w(kMlpParams);
-        nerf_ext_mlp_init(0u, w.data());
-        nerf_ext_mlp_init(1u, w.data() + NERF_EXT_DENSITY_PARAMS);
-        NERF_HIP_TRY(hipMemcpyAsync(B.mlp_f32, w.data(), sizeof(float) * kMlpParams, hipMemcpyHostToDevice, s));
+        if (!ref) {
+            NerfExtGridDesc g32 = d->grid;
+            g32.table_dtype     = NERF_EXT_F32;
+            st                  = nerf_ext_grid_init_table(&g32, d->seed, d->table_init_range, B.table_f32, s);
+            if (st != NERF_STATUS_OK) return st;
+            st = nerf_ext_float_to_half(B.table_f32, (uint16_t*)B.table, B.table_elems, s);
+            if (st != NERF_STATUS_OK) return st;
+        }
+        // The reference's Xavier init (backend-cuda.cu:1810-1847) on the
+        // network's shapes.
+        std::vector<float> w(B.mlp_params);
+        if (ref) {
+            nerf_ext_ref_mlp_init(0u, w.data());
+            nerf_ext_ref_mlp_init(1u, w.data() + B.density_params);
+        } else {
+            nerf_ext_mlp_init(0u, w.data());
+            nerf_ext_mlp_init(1u, w.data() + B.density_params);
+        }
+        NERF_HIP_TRY(hipMemcpyAsync(B.mlp_f32, w.data(), sizeof(float) * B.mlp_params, hipMemcpyHostToDevice, s));
         NERF_HIP_TRY(hipStreamSynchronize(s));
-        st = nerf_ext_float_to_half(B.mlp_f32, (uint16_t*)B.dparams, NERF_EXT_DENSITY_PARAMS, s);
-        if (st == NERF_STATUS_OK) st = nerf_ext_float_to_half(B.mlp_f32 + NERF_EXT_DENSITY_PARAMS, (uint16_t*)B.cparams, NERF_EXT_COLOR_PARAMS, s);
+        st = nerf_ext_float_to_half(B.mlp_f32, (uint16_t*)B.dparams, B.density_params, s);
+        if (st == NERF_STATUS_OK) st = nerf_ext_float_to_half(B.mlp_f32 + B.density_params, (uint16_t*)B.cparams, B.mlp_params - B.density_params, s);
         if (st != NERF_STATUS_OK) return st;
     }
     NERF_HIP_TRY(hipStreamSynchronize(s));
@@ -218,9 +256,9 @@ NerfStatus Trainer::reset() {
     NERF_HIP_TRY(hipMemsetAsync(B.table_grad, 0, B.table_elems * 4u, s));
     NERF_HIP_TRY(hipMemsetAsync(B.table_m, 0, B.table_elems * 4u, s));
     NERF_HIP_TRY(hipMemsetAsync(B.table_v, 0, B.table_elems * 4u, s));
-    NERF_HIP_TRY(hipMemsetAsync(B.mlp_grad, 0, kMlpParams * 4u, s));
-    NERF_HIP_TRY(hipMemsetAsync(B.mlp_m, 0, kMlpParams * 4u, s));
-    NERF_HIP_TRY(hipMemsetAsync(B.mlp_v, 0, kMlpParams * 4u, s));
+    NERF_HIP_TRY(hipMemsetAsync(B.mlp_grad, 0, B.mlp_params * 4ull, s));
+    NERF_HIP_TRY(hipMemsetAsync(B.mlp_m, 0, B.mlp_params * 4ull, s));
+    NERF_HIP_TRY(hipMemsetAsync(B.mlp_v, 0, B.mlp_params * 4ull, s));
     NERF_HIP_TRY(hipMemsetAsync(B.bits, 0, (P.occ_cells + 31u) / 32u * 4u, s));
     NERF_HIP_TRY(hipMemsetAsync(B.density, 0, (uint64_t)P.occ_cells * 4u, s));
     TrainDevState init{};
@@ -340,7 +378,7 @@ NERF_API NerfStatus nerf_ext_trainer_model(NerfExtTrainer* trainer, NerfExtModel
         model->table          = t.B.table;
         model->density_params = (const uint16_t*)t.B.dparams;
         model->color_params   = (const uint16_t*)t.B.cparams;
-        model->kind           = NERF_EXT_MODEL_HASHGRID;
+        model->kind           = t.B.model_kind;
         model->reserved       = 0u;
     }
     if (occ) {

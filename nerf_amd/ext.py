@@ -223,7 +223,8 @@ class Trainer:
     and the buffers of one step, all on the device."""
 
     def __init__(self, grid: L.NerfExtGridDesc, images_rgba8: np.ndarray, cameras: list, *, occupancy_res=128, aabb_min=(0.0, 0.0, 0.0), aabb_max=(1.0, 1.0, 1.0), hyper: L.NerfHyperParams | None = None,
-                 occupancy: L.NerfOccupancyParams | None = None, initial_rays=4096, max_rays=1 << 18, target_samples=0, sample_capacity=1 << 20, max_steps_per_ray=1024, huber_delta=0.1, table_init_range=1e-4, seed=0):
+                 occupancy: L.NerfOccupancyParams | None = None, initial_rays=4096, max_rays=1 << 18, target_samples=0, sample_capacity=1 << 20, max_steps_per_ray=1024, huber_delta=0.1, table_init_range=1e-4, seed=0,
+                 model_kind=L.NERF_EXT_MODEL_HASHGRID):
         images = np.ascontiguousarray(images_rgba8)
         n = len(cameras)
         self._cams = (L.NerfExtCamera * n)(*cameras)
@@ -245,6 +246,7 @@ class Trainer:
         d.huber_delta = huber_delta
         d.table_init_range = table_init_range
         d.seed = seed
+        d.model_kind = model_kind
         self.desc = d
         self._h = C.c_void_p()
         L.call("nerf_ext_trainer_create", C.byref(d), C.byref(self._h))

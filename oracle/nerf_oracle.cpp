@@ -716,6 +716,63 @@ extern "C" void orc_render_rays(const OrcModel* model, const OrcCamera* cam, con
 }
 
 
+// Inference with the reference's sampling (backend-cuda.cu:534-600): the
+// pixel-centre ray (y flipped, :561-563) clipped to the box; dt = (t_far -
+// t_near) / spp; no samples when the ray misses the box or dt is not
+// positive (:570-583), else spp samples at t_mid = t_near + (i + 0.5) dt,
+// position o + t_mid d (:585-599).  Composite of :601-635 over every sample
+// (no early stop): alpha = 1 - exp(-sigma max(dt, 0)), w = T alpha,
+// C += w c, T *= 1 - alpha; output C + T bg, clamped, rounded to RGBA8.
+// The field is the model's: the hash grid reads positions normalised by the
+// box, the reference's network world positions.
+extern "C" void orc_render_uniform(const OrcModel* model, const OrcCamera* cam, const float* aabb, uint32_t spp, const float* bg, const uint32_t* rays, uint32_t n_rays, float* rgb_out, uint32_t* rgba8_out,
+                                   uint32_t* counts_out, uint32_t n_threads) {
+    if (n_threads == 0u) n_threads = 1u;
+    auto work = [&](uint32_t begin, uint32_t end) {
+        for (uint32_t k = begin; k < end; ++k) {
+            const uint32_t ray = rays[k];
+            OrcRay r;
+            uint32_t count = 0;
+            float dt       = 0.0f;
+            if (pixel_ray(*cam, ray % cam->width, ray / cam->width, aabb, aabb + 3, r)) {
+                dt = (r.tf - r.tn) / (float)spp;
+                if (dt > 0.0f) count = spp;
+            }
+            float T = 1.0f, Cc[3] = {0, 0, 0};
+            for (uint32_t i = 0; i < count; ++i) {
+                const float tm    = r.tn + ((float)i + 0.5f) * dt;
+                const float wp[3] = {r.o[0] + tm * r.d[0], r.o[1] + tm * r.d[1], r.o[2] + tm * r.d[2]};
+                float s4[4];
+                if (model->kind == 1u) {
+                    ref_field_point(model->density_params, model->color_params, wp, r.d, s4, nullptr);
+                } else {
+                    float p[3];
+                    for (int a = 0; a < 3; ++a) p[a] = (wp[a] - aabb[a]) / (aabb[3 + a] - aabb[a]);
+                    field_point(model->grid, model->table, model->density_params, model->color_params, p, r.d, s4);
+                }
+                const float a = 1.0f - expf(-(s4[0] * fmaxf(dt, 0.0f)));
+                const float w = T * a;
+                for (int c = 0; c < 3; ++c) Cc[c] += w * s4[1 + c];
+                T *= 1.0f - a;
+            }
+            float rgb[3];
+            for (int c = 0; c < 3; ++c) rgb[c] = Cc[c] + T * bg[c];
+            if (rgb_out)
+                for (int c = 0; c < 3; ++c) rgb_out[3ull * k + c] = rgb[c];
+            if (rgba8_out) rgba8_out[k] = pack_rgba8(rgb);
+            if (counts_out) counts_out[k] = count;
+        }
+    };
+    std::vector<std::thread> pool;
+    const uint32_t chunk = (n_rays + n_threads - 1u) / n_threads;
+    for (uint32_t t = 0; t < n_threads; ++t) {
+        const uint32_t b = t * chunk, e = std::min(n_rays, b + chunk);
+        if (b >= e) break;
+        pool.emplace_back(work, b, e);
+    }
+    for (auto& th : pool) th.join();
+}
+
 // ===========================================================================
 // Training: composite backward with Huber loss, MLP backward, hash-grid
 // scatter-add, Adam.

@@ -98,6 +98,7 @@ _PROTOS = {
     "orc_field_mlp": (None, [_P, _P, _P, _P, _U32, _P]),
     "orc_scene_render": (None, [_P, _U32, C.POINTER(OrcCamera), _P, _U32, _P]),
     "orc_render_rays": (None, [C.POINTER(OrcModel), C.POINTER(OrcCamera), _P, _U32, _U32, _P, _U32, _F, _P, _P, _U32, _P, _P, _P, _U32]),
+    "orc_render_uniform": (None, [C.POINTER(OrcModel), C.POINTER(OrcCamera), _P, _U32, _P, _P, _U32, _P, _P, _P, _U32]),
 }
 
 _lib = None
@@ -386,6 +387,26 @@ def render_rays(grid: OrcGrid | None, table: np.ndarray | None, dparams_bits: np
     rgba = np.empty(rays.size, np.uint32)
     counts = np.empty(rays.size, np.uint32)
     lib().orc_render_rays(C.byref(model), C.byref(cam), _p(bits) if bits is not None else None, res, cascades, _p(box), max_steps, t_stop, _p(b), _p(rays), rays.size, _p(rgb), _p(rgba), _p(counts), threads)
+    return rgb, rgba, counts
+
+
+def render_uniform(grid: OrcGrid | None, table: np.ndarray | None, dparams_bits: np.ndarray, cparams_bits: np.ndarray, cam: OrcCamera, aabb, spp: int, rays: np.ndarray, bg=(1.0, 1.0, 1.0), threads: int = 1, kind: int = 0):
+    """The reference's inference sampling and composite for the given pixel
+    rays: (rgb [n][3], rgba8 [n], sample counts [n])."""
+    model = OrcModel()
+    if grid is not None:
+        model.grid = grid
+    model.table = _p(table) if table is not None else None
+    model.kind = kind
+    model.density_params = _p(dparams_bits)
+    model.color_params = _p(cparams_bits)
+    rays = np.ascontiguousarray(rays, np.uint32)
+    box = np.array(aabb, np.float32)
+    b = np.array(bg, np.float32)
+    rgb = np.empty((rays.size, 3), np.float32)
+    rgba = np.empty(rays.size, np.uint32)
+    counts = np.empty(rays.size, np.uint32)
+    lib().orc_render_uniform(C.byref(model), C.byref(cam), _p(box), spp, _p(b), _p(rays), rays.size, _p(rgb), _p(rgba), _p(counts), threads)
     return rgb, rgba, counts
 
 

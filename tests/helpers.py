@@ -43,7 +43,7 @@ def channel_floor(want: np.ndarray, frac: float = FLOOR_FRAC) -> np.ndarray | fl
 MLP_BULK_RTOL = 1e-4
 
 
-def assert_rel(got, want, rtol=RTOL, floor=None, what="", mlp=False):
+def assert_rel(got, want, rtol=RTOL, floor=None, what="", mlp=False, bulk_rtol=MLP_BULK_RTOL):
     got = np.asarray(got, np.float64)
     want = np.asarray(want, np.float64)
     assert got.shape == want.shape, (got.shape, want.shape)
@@ -52,7 +52,7 @@ def assert_rel(got, want, rtol=RTOL, floor=None, what="", mlp=False):
     err = np.abs(got - want) / np.maximum(np.abs(want), strict)
     bulk = float(np.quantile(err, 0.999)) if err.size else 0.0
     if mlp:
-        assert bulk <= MLP_BULK_RTOL, f"{what}: 99.9th percentile rel err {bulk:.3e} > {MLP_BULK_RTOL}"
+        assert bulk <= bulk_rtol, f"{what}: 99.9th percentile rel err {bulk:.3e} > {bulk_rtol}"
         err = np.abs(got - want) / np.maximum(np.abs(want), channel_floor(want, 1.0))
     worst = np.unravel_index(np.argmax(err), err.shape)
     print(f"[rel] {what}: max {err.max():.3e} p99.9 {bulk:.3e}", flush=True)

@@ -80,7 +80,10 @@ def _run_steps_checking_controller(t, steps, target, initial_rays, max_rays):
 
 def _load_scene_bits(t, bits):
     """Replaces the trainer's occupancy (all ones during warmup) by the
-    scene's, so that rays hold occupied runs separated by empty space."""
+    scene's, so that rays hold occupied runs separated by empty space.  The
+    copy runs on the null stream: the trainer's stream (whose warmup kernel
+    writes the bits) is drained first."""
+    t.synchronize()
     ext.write_device(t.buffers().bitfield, bits)
 
 
@@ -141,6 +144,7 @@ def c3_step(scene):
     dp = ext.read_device(m.density_params, (L.NERF_EXT_DENSITY_PARAMS,), np.uint16)
     cp = ext.read_device(m.color_params, (L.NERF_EXT_COLOR_PARAMS,), np.uint16)
     t.run_stages(L.NERF_EXT_STAGE_FORWARD, L.NERF_EXT_STAGE_BACKWARD)
+    t.synchronize()  # the trainer's stream does not order with the copies below
     n = s["stats"].samples
     out = dict(trainer=t, grid=grid, seen=seen, s=s, table=table, dp=dp, cp=cp, cap=cap,
                field=ext.read_device(B.field, (n, 4), np.float32),
