@@ -229,7 +229,131 @@ def train_bench(steps: int, warmup: int, views: int = 100):
     out["loss_first_timed"] = round(float(s0.last.loss), 6)
     out["stages"] = train_stages(tr, _On, reps=20)
     out["render_trained"] = render_trained(tr)
+    snap = train_snapshot(tr, cams, scene)
     tr.close()
+    return out, snap
+
+
+def train_snapshot(tr, cams, scene):
+    """The inputs of the trainer's next step, for the CPU oracle's timing of
+    the same step: step index, ray count, picked camera and its image, the
+    occupancy and the model."""
+    from nerf_amd import _lib as L, ext
+    from oracle import oracle as orc
+    st = tr.stats()
+    frame = st.last.completed_steps
+    view = orc.train_camera(frame, len(cams))
+    image = ext.scene_render(scene, [cams[view]], 512).numpy()[0].view(np.uint8)
+    m, _ = tr.model()
+    B = tr.buffers()
+    E = int(B.table_elems)
+    return {"frame": frame, "rays": int(st.rays), "cam": cams[view], "ocam": orc.camera_from_bytes(bytes(cams[view])), "image": np.ascontiguousarray(image),
+            "bits": ext.read_device(B.bitfield, (128 ** 3 // 32,), np.uint32), "grid": orc.make_grid(16, 19, 1), "table": ext.read_device(m.table, (E,), np.uint16),
+            "table32": ext.read_device(B.table_f32, (E,), np.float32), "dp": ext.read_device(m.density_params, (L.NERF_EXT_DENSITY_PARAMS,), np.uint16),
+            "cp": ext.read_device(m.color_params, (L.NERF_EXT_COLOR_PARAMS,), np.uint16)}
+
+
+def ref_train_bench(steps: int, warmup: int, views: int = 100):
+    """Training the reference's own network (frequency encoding, 128-wide
+    MLPs, softplus, its alpha-weighted loss) in the trainer on the training
+    leg's data and batch (2^18 samples, <=1024 steps/ray)."""
+    from nerf_amd import _lib as L, ext
+    from nerf_amd.device import Event
+
+    scene = ext.scene_gaussians(32, seed=0)
+    cams = [ext.camera_orbit(1, i, RADIUS, CENTRE, TRAIN_W, TRAIN_H, FOCAL) for i in range(views)]
+    images = ext.scene_render(scene, cams, 512).numpy()
+    hyper = ext.hyper_params(lr=5e-4, beta1=0.9, beta2=0.99, eps=1e-15, loss_scale=128.0)
+    occ = ext.occupancy_params(decay=0.95, threshold=0.01, cells_per_update=128 ** 3, update_interval=16, warmup_steps=16)
+    batch = 1 << 18
+    tr = ext.Trainer(ext.grid_desc(19, L.NERF_EXT_F16), images.view(np.uint8), cams, occupancy_res=128, hyper=hyper, occupancy=occ, initial_rays=4096, max_rays=batch, target_samples=batch,
+                     sample_capacity=batch, max_steps_per_ray=MAX_STEPS, seed=0, model_kind=L.NERF_EXT_MODEL_REFERENCE)
+    del images
+
+    class _On:
+        handle = tr.stream()
+
+    tr.step(warmup)
+    s0 = tr.stats()
+    t0 = time.perf_counter()
+    tr.step(steps)
+    s1 = tr.stats()
+    wall = time.perf_counter() - t0
+    n = (s1.samples_total - s0.samples_total) / steps
+    groups = [("sample", L.NERF_EXT_STAGE_BEGIN, L.NERF_EXT_STAGE_SAMPLE), ("forward", L.NERF_EXT_STAGE_FORWARD, L.NERF_EXT_STAGE_FORWARD), ("composite", L.NERF_EXT_STAGE_COMPOSITE, L.NERF_EXT_STAGE_COMPOSITE),
+              ("backward", L.NERF_EXT_STAGE_BACKWARD, L.NERF_EXT_STAGE_BACKWARD), ("adam", L.NERF_EXT_STAGE_ADAM, L.NERF_EXT_STAGE_END)]
+    reps = 10
+    evs = [[Event() for _ in range(len(groups) + 1)] for _ in range(reps)]
+    for r in range(reps):
+        evs[r][0].record(_On)
+        for k, (_, a, b) in enumerate(groups):
+            tr.run_stages(a, b)
+            evs[r][k + 1].record(_On)
+    tr.stats()
+    ms = {name: sum(evs[r][k].elapsed_ms(evs[r][k + 1]) for r in range(reps)) / reps for k, (name, _, _) in enumerate(groups)}
+    params = L.NERF_EXT_REF_DENSITY_PARAMS + L.NERF_EXT_REF_COLOR_PARAMS
+
+    def mfma(f, t):
+        return {"achieved": round(f / (t / 1e3) / 1e12, 1), "unit": "TFLOP/s", "frac": round(f / (t / 1e3) / 1e12 / MFMA_FP16_PEAK_TFS, 4), "bound": "mfma"}
+
+    out = {"samples_per_s": round(n * steps / wall, 1), "unit": "train samples/s", "steps": steps, "warmup": warmup, "ms_per_step": round(wall * 1e3 / steps, 4), "mean_samples_per_step": round(n, 1),
+           "loss_last": round(float(s1.last.loss), 6), "nonfinite": int(s1.last.has_nonfinite),
+           "stages": {"sample_ms": round(ms["sample"], 4), "forward": {"ms": round(ms["forward"], 4), **mfma(n * REF_FLOPS_PER_SAMPLE, ms["forward"])}, "composite_ms": round(ms["composite"], 4),
+                      "backward": {"ms": round(ms["backward"], 4), **mfma(n * REF_BACKWARD_FLOPS_PER_SAMPLE, ms["backward"])}, "adam_ms": round(ms["adam"], 4), "parameters": params},
+           "workload": f"{views} 800x800 views, 32-Gaussian scene, the reference's network (frequency encoding, density 64-128x5-16, colour 48-128x3-16), 2^18-sample batches, <=1024 steps/ray"}
+    tr.close()
+    return out
+
+
+def reference_host_bench(steps: int = 200, views: int = 100):
+    """The reference host program's workload (benchmark.cpp:305-546) through
+    nerf.h with the reference's own network: 4,096 rays per step, <= 64
+    steps per ray, its hyper-parameters and occupancy schedule; the metric it
+    prints, steps/s, and nerf_inference at its 64 samples per ray (the
+    reference's uniform sampling)."""
+    from nerf_amd import _lib as L, ext
+
+    scene = ext.scene_gaussians(32, seed=0)
+    cams = [ext.camera_orbit(1, i, RADIUS, CENTRE, TRAIN_W, TRAIN_H, FOCAL) for i in range(views)]
+    images = np.ascontiguousarray(ext.scene_render(scene, cams, 512).numpy())
+    mats = np.zeros((views, 4, 4), np.float32)
+    for i, c in enumerate(cams):
+        mats[i, :3, :] = np.array(c.c2w[:], np.float32).reshape(3, 4)
+        mats[i, 3, 3] = 1.0
+    d = L.NerfCreateDesc(128, 1 << 21, 1 << 16, 256, images.ctypes.data, images.nbytes, mats.ctypes.data, mats.nbytes, views, TRAIN_W, TRAIN_H, cams[0].fx, cams[0].fy, cams[0].cx, cams[0].cy)
+    h = C.c_void_p()
+    L.call("nerf_create_context", C.byref(d), C.byref(h))
+    out = {}
+    try:
+        for name, kind in (("reference_model", L.NERF_EXT_MODEL_REFERENCE), ("hashgrid_model", L.NERF_EXT_MODEL_HASHGRID)):
+            L.call("nerf_ext_context_configure", h, C.byref(L.NerfExtContextOptions(kind, L.NERF_EXT_SAMPLING_UNIFORM)))
+            hp = L.NerfHyperParams(5e-4, 0.9, 0.999, 1e-8, 1.0, 100.0, 128.0, 250)
+            occ = L.NerfOccupancyParams(0.98, 0.01, 65536, 1, 32)
+            L.call("nerf_configure_training", h, C.byref(L.NerfTrainingConfig(0.0, 0.0, 0.0, 1.0, 1.0, 1.0, hp, occ, 4096, 64)))
+            for _ in range(20):
+                L.call("nerf_train_step", h)
+            st = L.NerfTrainStats()
+            L.call("nerf_read_train_stats", h, C.byref(st))
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                L.call("nerf_train_step", h)
+            L.call("nerf_read_train_stats", h, C.byref(st))
+            wall = time.perf_counter() - t0
+            img = np.zeros((TRAIN_H, TRAIN_W), np.uint32)
+            req = L.NerfInferenceRequest(0, 64, L.NERF_MEMORY_HOST, img.ctypes.data, img.nbytes)
+            info = L.NerfInferenceInfo()
+            L.call("nerf_inference", h, C.byref(req), C.byref(info))
+            t1 = time.perf_counter()
+            reps = 3
+            for _ in range(reps):
+                L.call("nerf_inference", h, C.byref(req), C.byref(info))
+            iw = (time.perf_counter() - t1) / reps
+            out[name] = {"sps": round(steps / wall, 2), "unit": "train steps/s", "rays_per_s": round(4096 * steps / wall, 1), "steps": steps, "loss_last": round(float(st.loss), 6),
+                         "nonfinite": int(st.has_nonfinite), "inference_ms": round(iw * 1e3, 3), "inference_mrays_per_s": round(TRAIN_W * TRAIN_H / iw / 1e6, 3),
+                         "inference": "nerf_inference, 64 uniform samples per ray over the box (the reference's sampling), RGBA8 to host"}
+    finally:
+        L.call("nerf_destroy_context", h)
+    out["workload"] = f"benchmark.cpp defaults through nerf.h: {views} 800x800 views, 4096 rays/step, <=64 steps/ray, lr 5e-4, betas 0.9/0.999, eps 1e-8, clip 1, guard 100, loss scale 128, decay 250k; occupancy decay 0.98, 65536 cells/update every step after 32 warmup steps"
     return out
 
 
@@ -397,33 +521,145 @@ def config_renders(reps: int = 2):
     return out
 
 
-def cpu_baseline(desc, model, cam, bits, budget_s: float = 15.0):
-    """Scalar oracle on a deterministic ray subset (every k-th ray of the view)."""
-    from oracle import oracle as orc
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
-    sys.path.insert(0, str(ROOT / "tests"))
-    threads = min(16, os.cpu_count() or 1)
+
+def _split(n: int, parts: int):
+    step = (n + parts - 1) // parts
+    return [(b, min(n, b + step)) for b in range(0, n, step)]
+
+
+def _threaded(fn, n: int, threads: int):
+    """fn(begin, end) over `threads` slices of range(n) on Python threads (the
+    oracle's ctypes calls release the GIL), results in slice order."""
+    if threads <= 1:
+        return [fn(0, n)]
+    from concurrent.futures import ThreadPoolExecutor
+    with ThreadPoolExecutor(max_workers=threads) as ex:
+        return list(ex.map(lambda be: fn(*be), _split(n, threads)))
+
+
+def cpu_render_leg(model, cam, bits, threads: int, budget_s: float):
+    """The scalar oracle's render (march + field + composite) on a
+    deterministic ray subset of the headline view, sized to about budget_s."""
+    from oracle import oracle as orc
     g = orc.make_grid(16, 19, 1)
     table = model.table.numpy().view(np.uint16)
     dp = model.density.numpy().view(np.uint16)
     cp = model.color.numpy().view(np.uint16)
     ocam = orc.camera_from_bytes(bytes(cam))
     b = bits.numpy()
-    # Calibrate on a small subset, then size the timed subset to ~budget_s.
-    stride = 4099
+    stride = 4099 * max(1, 16 // threads)
     rays = np.arange(0, W * H, stride, dtype=np.uint32)
     t0 = time.perf_counter()
     orc.render_rays(g, table, dp, cp, ocam, b, 128, (0, 0, 0, 1, 1, 1), MAX_STEPS, rays, T_STOP, threads=threads)
-    dt = max(time.perf_counter() - t0, 1e-3)
-    per_ray = dt / rays.size
-    n_target = int(min(W * H, max(rays.size, budget_s / per_ray)))
-    stride = max(1, (W * H) // n_target)
+    per_ray = max(time.perf_counter() - t0, 1e-3) / rays.size
+    stride = max(1, (W * H) // int(min(W * H, max(rays.size, budget_s / per_ray))))
     rays = np.arange(0, W * H, stride, dtype=np.uint32)
     t0 = time.perf_counter()
     orc.render_rays(g, table, dp, cp, ocam, b, 128, (0, 0, 0, 1, 1, 1), MAX_STEPS, rays, T_STOP, threads=threads)
     dt = time.perf_counter() - t0
-    return {"value": rays.size / dt / 1e6, "unit": "Mrays/s", "cores": threads, "kind": "port",
-            "sample": f"{rays.size} rays (every {stride}th ray of the {W}x{H} view, full march+field+composite per ray), {dt:.1f} s"}
+    return {"value": round(rays.size / dt / 1e6, 6), "unit": "Mrays/s", "threads": threads, "seconds": round(dt, 2),
+            "sample": f"{rays.size} rays (every {stride}th ray of the {W}x{H} view: full march + field + composite per ray)"}
+
+
+def cpu_c1_leg(threads: int):
+    """C1 on the oracle: hash encode + density MLP of all 2^16 points (fp32
+    table T = 2^16, the parity tests' points and weights)."""
+    from nerf_amd import _lib as L, ext
+    from oracle import oracle as orc
+    n = 1 << 16
+    desc = ext.grid_desc(16, L.NERF_EXT_F32)
+    table = ext.init_table(desc, 0, 1e-4).numpy()
+    dp = ext.mlp_init(0).astype(np.float16).view(np.uint16)
+    pos = unit_points(n, seed=0)
+    g = orc.make_grid(16, 16, 0)
+    t0 = time.perf_counter()
+    _threaded(lambda b, e: orc.density_forward(g, table, dp, pos[b:e]), n, threads)
+    dt = time.perf_counter() - t0
+    return {"value": round(n / dt, 1), "unit": "points/s", "threads": threads, "seconds": round(dt, 3), "sample": "all 2^16 points of C1 (hash encode 16 x 2^16 fp32 + density MLP 32-64-16)"}
+
+
+def cpu_train_leg(snap, threads: int, ray_fraction: float = 1.0):
+    """One C3 training step on the oracle, fed the GPU trainer's own inputs
+    (camera image, occupancy, model, step index and ray count of a 2^18-sample
+    step): march (one thread: the per-ray seeds make it serial here), field
+    forward, Huber composite backward per ray, MLP backward, hash-grid
+    scatter-add, Adam over the 16.8 M parameters."""
+    from oracle import oracle as orc
+    n_rays = max(1, int(snap["rays"] * ray_fraction))
+    box = (0.0, 0.0, 0.0, 1.0, 1.0, 1.0)
+    times = {}
+    t0 = time.perf_counter()
+    cap = 1 << 18  # the GPU step's sample capacity: rays past it are cut whole
+    counts, gt, pix, offs, tdt = orc.train_rays(snap["ocam"], snap["image"], snap["bits"], 128, box, MAX_STEPS, snap["frame"], n_rays, cap)
+    counts = np.where(offs.astype(np.int64) + counts <= cap, counts, 0).astype(np.uint32)
+    n = int((offs.astype(np.int64) + counts)[counts > 0].max()) if (counts > 0).any() else 0
+    times["march"] = time.perf_counter() - t0
+    # Sample positions and directions (host numpy, like the GPU's o + t d).
+    c2w = np.array(snap["cam"].c2w[:], np.float32).reshape(3, 4)
+    cam = snap["cam"]
+    px, py = pix[:, 0], np.float32(cam.height) - np.float32(1.0) - pix[:, 1]
+    dcam = np.stack([(px - cam.cx) / cam.fx, (py - cam.cy) / cam.fy, -np.ones_like(px)], 1).astype(np.float32)
+    d = dcam @ c2w[:, :3].T
+    d = (d / np.linalg.norm(d, axis=1, keepdims=True)).astype(np.float32)
+    ray_of = np.repeat(np.arange(n_rays), counts)
+    dirs = np.ascontiguousarray(d[ray_of])
+    pos = np.clip(c2w[:, 3][None, :] + tdt[:n, 0:1] * dirs, 0.0, 1.0).astype(np.float32)
+    g, table, dp, cp = snap["grid"], snap["table"], snap["dp"], snap["cp"]
+    t0 = time.perf_counter()
+    field = np.concatenate(_threaded(lambda b, e: orc.field_forward(g, table, dp, cp, pos[b:e], dirs[b:e]), n, threads))
+    times["forward"] = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    draw = np.zeros((n, 4), np.float32)
+    inv = 1.0 / max(1, int((counts > 0).sum()))
+
+    def comp(rb, re):
+        for r in range(rb, re):
+            a, c = int(offs[r]), int(counts[r])
+            if c:
+                _, d1, d3, _ = orc.composite_backward_act(field[a:a + c, 0], field[a:a + c, 1:], tdt[a:a + c, 1], gt[r, :3], delta=0.1, inv_norm=inv)
+                draw[a:a + c, 0], draw[a:a + c, 1:] = d1, d3
+
+    _threaded(comp, n_rays, threads)
+    times["composite"] = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    feats = np.concatenate(_threaded(lambda b, e: orc.encode(g, table, pos[b:e]), n, threads))
+    parts = _threaded(lambda b, e: orc.mlp_backward(dp, cp, feats[b:e], dirs[b:e], draw[b:e, 0], draw[b:e, 1:], 128.0), n, threads)
+    dfeat = np.concatenate([p[0] for p in parts])
+    tg = None
+    for part in _threaded(lambda b, e: orc.encode_backward(g, pos[b:e], dfeat[b:e]), n, min(threads, 8)):
+        tg = part if tg is None else tg + part
+    times["backward"] = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    w = snap["table32"].copy()
+    m, v = np.zeros_like(w), np.zeros_like(w)
+    orc.adam(w, m, v, tg.astype(np.float32), 1e-2, 0.9, 0.99, 1e-15, 1e30, 1e30, 128.0, 0, 1, 1.0)
+    times["adam"] = time.perf_counter() - t0
+    total = sum(times.values())
+    return {"value": round(n / total, 1), "unit": "train samples/s", "threads": threads, "seconds": round(total, 2), "stage_seconds": {k: round(t, 3) for k, t in times.items()},
+            "sample": f"one training step: {int((counts > 0).sum())} rays with samples of {n_rays} marched ({n} samples, capacity 2^18) of the GPU trainer's step {snap['frame']} on the 800x800 camera it picked"
+                      + ("" if ray_fraction == 1.0 else f" (the first {ray_fraction:.3g} of its rays)")}
+
+
+def cpu_baseline(model, cam, bits, train_snap):
+    """The scalar C++ oracle (the same math, -O2 -ffp-contract=off, no SIMD
+    intrinsics) on the host: 1 thread and the host's thread share."""
+    threads = min(16, os.cpu_count() or 1)
+    legs = {"render_1t": cpu_render_leg(model, cam, bits, 1, 6.0), f"render_{threads}t": cpu_render_leg(model, cam, bits, threads, 6.0), "c1_1t": cpu_c1_leg(1), f"c1_{threads}t": cpu_c1_leg(threads)}
+    if train_snap is not None:
+        legs["train_1t"] = cpu_train_leg(train_snap, 1, ray_fraction=1.0 / 16)
+        legs[f"train_{threads}t"] = cpu_train_leg(train_snap, threads)
+    head = legs[f"render_{threads}t"]
+    return {"value": head["value"], "unit": "Mrays/s", "cores": threads, "kind": "port", "sample": head["sample"], "hardware_concurrency": os.cpu_count(), "cpu_model": _cpu_model(),
+            "threads_note": "the host's share of one GPU box is 16 threads (the all-threads legs use them); 1-thread legs alongside", "legs": legs}
 
 
 def main() -> int:
@@ -519,6 +755,7 @@ def main() -> int:
         "stages_ms": {k: round(v, 4) for k, v in stage.items()},
         "roofline": {"kernel": "k_field_forward_lv (fused hash encode + density/colour MLP, level-major gathers)", "bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved_gbs / HBM_PEAK_GBS, 4), "traffic": int(shaded * FIELD_TRAFFIC_BYTES_PER_SAMPLE),
+                     "traffic_source": f"profile-derived, not counted in this run: {FIELD_TRAFFIC_BYTES_PER_SAMPLE} B/sample from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE on this render (profiles/field_forward_800x800_hbm_traffic.md) x this run's shaded samples",
                      "traffic_GBps": round(shaded * FIELD_TRAFFIC_BYTES_PER_SAMPLE / field_s / 1e9, 1), "mfma_tflops": round(field_tflops, 2), "mfma_frac": round(field_tflops / MFMA_FP16_PEAK_TFS, 4),
                      "bytes_per_sample": FIELD_BYTES_PER_SAMPLE, "flops_per_sample": FIELD_FLOPS_PER_SAMPLE},
         "device": {"name": info.name.decode(), "arch": info.arch.decode(), "cus": info.compute_units},
@@ -526,13 +763,16 @@ def main() -> int:
     if not args.no_stage_rooflines:
         line["stage_rooflines"] = kernel_rooflines()
         line["abi_render"] = abi_render()
+    train_snap = None
     if args.train_steps > 0:
-        line["train"] = train_bench(args.train_steps, args.train_warmup)
+        line["train"], train_snap = train_bench(args.train_steps, args.train_warmup)
+        line["train_reference_model"] = ref_train_bench(max(10, args.train_steps // 2), 10)
+        line["reference_host"] = reference_host_bench()
     if not args.no_configs:
         line["configs"] = config_renders()
         line["reference_model"] = ref_model_render()
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(desc, model, cam, bits)
+        line["cpu_baseline"] = cpu_baseline(model, cam, bits, train_snap)
     print(json.dumps(line), flush=True)
     return 0
 

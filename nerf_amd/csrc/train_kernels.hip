@@ -98,9 +98,11 @@ __global__ void k_step_end(TrainParams P, TrainDevState* S) {
     S->stats.completed_steps   = S->frame + 1u;
     S->stats.last_train_camera = S->camera;
     S->samples_done            = S->samples_done + S->n_samples;
-    if (P.target_samples != 0u && S->n_samples > 0u) {
-        // Aim the next batch at target_samples (exponentially smoothed).
-        const float want = S->rays_f * (float)P.target_samples / (float)S->n_samples;
+    if (P.target_samples != 0u && S->total > 0ull) {
+        // Aim the next batch at target_samples (exponentially smoothed), from
+        // the occupied samples before the capacity cut: the kept count is
+        // capped, so it cannot show an overshoot.
+        const float want = S->rays_f * (float)P.target_samples / (float)S->total;
         S->rays_f        = 0.5f * S->rays_f + 0.5f * want;
         S->rays_f        = fminf(fmaxf(S->rays_f, (float)P.min_rays), (float)P.max_rays);
     }

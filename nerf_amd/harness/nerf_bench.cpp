@@ -84,7 +84,7 @@ bool parse_u32(std::string_view v, uint32_t& out) {
 }  // namespace
 
 int main(int argc, char** argv) {
-    std::string dataset_path, load_weights, save_weights, inference_out = "nerf_inference_final.png";
+    std::string dataset_path, load_weights, save_weights, inference_out = "nerf_inference_final.png", model_name = "hashgrid";
     uint32_t steps = 10000u, rays = 4096u, max_sample_steps = 64u, log_interval = 200u, inference_interval = 2000u, inference_camera = 0u, inference_samples = 64u;
     uint32_t synthetic = 0u, synthetic_size = 800u, synthetic_gaussians = 32u, seed = 0u;
 
@@ -94,7 +94,7 @@ int main(int argc, char** argv) {
                   << "\n  --inference-interval <N> default " << inference_interval << "\n  --inference-camera <N> default " << inference_camera << "\n  --inference-samples <N> default " << inference_samples
                   << "\n  --inference-out <path> default " << inference_out << "\n  --load-weights <path> optional\n  --save-weights <path> optional\n"
                   << "  --synthetic <views>: train on the analytic Gaussian scene instead of a dataset\n  --synthetic-size <N> default " << synthetic_size << "\n  --synthetic-gaussians <N> default " << synthetic_gaussians
-                  << "\n  --seed <N> default " << seed << "\n";
+                  << "\n  --seed <N> default " << seed << "\n  --model <hashgrid|reference> default hashgrid (reference: the reference's own network, nerf_ext_context_configure)\n";
     };
     for (int i = 1; i < argc; ++i) {
         const std::string_view key = argv[i];
@@ -128,6 +128,7 @@ int main(int argc, char** argv) {
         else if (key == "--load-weights") load_weights = value;
         else if (key == "--save-weights") save_weights = value;
         else if (key == "--inference-out") inference_out = value;
+        else if (key == "--model") model_name = value;
         else {
             std::cerr << "unknown argument: " << key << '\n';
             return 2;
@@ -135,6 +136,10 @@ int main(int argc, char** argv) {
     }
     if (dataset_path.empty() == (synthetic == 0u)) {
         std::cerr << "exactly one of --dataset and --synthetic is required\n";
+        return 2;
+    }
+    if (model_name != "hashgrid" && model_name != "reference") {
+        std::cerr << "--model must be hashgrid or reference\n";
         return 2;
     }
     if (log_interval == 0u || inference_interval == 0u) {
@@ -171,6 +176,10 @@ int main(int argc, char** argv) {
         cd.image_count = data.count, cd.image_width = data.width, cd.image_height = data.height;
         cd.fx = data.fx, cd.fy = data.fy, cd.cx = data.cx, cd.cy = data.cy;
         check(nerf_create_context(&cd, &ctx), "nerf_create_context");
+        if (model_name == "reference") {
+            const NerfExtContextOptions o{NERF_EXT_MODEL_REFERENCE, NERF_EXT_SAMPLING_DEFAULT};
+            check(nerf_ext_context_configure(ctx, &o), "nerf_ext_context_configure");
+        }
         if (!load_weights.empty()) {
             const NerfCheckpointFileDesc f{load_weights.c_str()};
             check(nerf_load_network_weights(ctx, &f), "nerf_load_network_weights");

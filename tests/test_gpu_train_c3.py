@@ -60,7 +60,8 @@ def _trainer(scene, *, target, initial_rays, max_rays, capacity, hyper=None):
 def _run_steps_checking_controller(t, steps, target, initial_rays, max_rays):
     """Runs whole steps one at a time; every step's ray count must follow the
     device controller's fp32 recurrence (half-way towards the ray count that
-    would have hit the target, clamped to [64, max_rays])."""
+    would have hit the target with the step's occupied samples before the
+    capacity cut, clamped to [64, max_rays])."""
     rf = np.float32(initial_rays)
     seen = []
     for k in range(steps):
@@ -69,12 +70,12 @@ def _run_steps_checking_controller(t, steps, target, initial_rays, max_rays):
         want_rays = min(max(int(np.float32(rf + np.float32(0.5))), 64), max_rays)
         assert st.rays == want_rays, f"step {k}: {st.rays} rays, controller recurrence gives {want_rays}"
         assert st.last.has_nonfinite == 0
-        n = st.samples
+        n = st.occupied_samples
         if n > 0:
             want = np.float32(np.float32(rf * np.float32(target)) / np.float32(n))
             rf = np.float32(np.float32(np.float32(0.5) * rf) + np.float32(np.float32(0.5) * want))
             rf = np.float32(min(max(rf, np.float32(64.0)), np.float32(max_rays)))
-        seen.append((st.rays, n))
+        seen.append((st.rays, st.samples, n))
     return seen, rf
 
 
@@ -267,7 +268,7 @@ def test_c3_target_2p18(scene):
     target, init, max_rays, cap = 1 << 18, 1024, 1 << 16, 1 << 19
     t, _ = _trainer(scene, target=target, initial_rays=init, max_rays=max_rays, capacity=cap)
     seen, _ = _run_steps_checking_controller(t, 4, target, init, max_rays)
-    assert abs(seen[-1][1] - target) < 0.5 * target, f"controller far from the target: {seen}"
+    assert abs(seen[-1][2] - target) < 0.5 * target, f"controller far from the target: {seen}"
     t.run_stages(L.NERF_EXT_STAGE_BEGIN, L.NERF_EXT_STAGE_OCCUPANCY)
     _load_scene_bits(t, scene[3])
     t.run_stages(L.NERF_EXT_STAGE_SAMPLE, L.NERF_EXT_STAGE_SAMPLE)
