@@ -210,12 +210,36 @@ __global__ __launch_bounds__(256) void k_uniform_composite(uint32_t ray0, uint32
     }
 }
 
+// Spatial order of the sample lists.  The field kernel evaluates 64
+// consecutive list entries per wave; its table gathers are served by the
+// caches only as far as those 64 samples are close in space.  So the first
+// round lists rays in tiles of kTile x kTile pixels (a wave's 64 rays are
+// four tiles side by side, a 16 x 4 pixel block), k_round_list emits each
+// group of 64 listed rays step by step (a wave's samples are 64 neighbouring
+// rays at one march step, then the next step), and k_round_composite keeps
+// each group's surviving rays together for the next round.  The order only
+// changes which samples share a wave; every value is the same.
+constexpr uint32_t kTile = 4u;
+
+// Tile-major enumeration of the rays [ray0, ray_end) of equally sized views
+// of width W: rays are numbered ray = row * W + x over rows of all views;
+// thread t covers tile t / 16 (tile rows from row0_tile, tiles_x per row),
+// pixel (t % 16) of it.  Threads that map outside the range are idle.
+__device__ __forceinline__ bool tiled_ray(uint32_t t, uint32_t W, uint32_t tiles_x, uint32_t row0_tile, uint32_t ray0, uint32_t ray_end, uint32_t& ray) {
+    const uint32_t tile = t / (kTile * kTile), in = t % (kTile * kTile);
+    const uint32_t x      = (tile % tiles_x) * kTile + in % kTile;
+    const uint64_t row    = (uint64_t)(row0_tile + tile / tiles_x) * kTile + in / kTile;
+    const uint64_t r      = row * W + x;
+    ray                   = (uint32_t)r;
+    return x < W && r >= ray0 && r < ray_end;
+}
+
 // Rays without samples get the background; the others start the first
-// round's list (wave-aggregated appends) with T = 1, C = 0.
-__global__ __launch_bounds__(256) void k_round_init(uint32_t ray0, uint32_t ray_end, const uint32_t* __restrict__ counts, float3 bg, uint32_t* __restrict__ rgba8, float* __restrict__ rgb_out, float4* __restrict__ state,
-                                                   uint32_t* __restrict__ list, uint32_t* __restrict__ n_active) {
-    const uint32_t ray = ray0 + blockIdx.x * 256u + threadIdx.x;
-    const bool valid   = ray < ray_end;
+// round's list (wave-aggregated appends, tile-major order) with T = 1, C = 0.
+__global__ __launch_bounds__(256) void k_round_init(uint32_t ray0, uint32_t ray_end, uint32_t W, uint32_t tiles_x, uint32_t row0_tile, const uint32_t* __restrict__ counts, float3 bg, uint32_t* __restrict__ rgba8,
+                                                   float* __restrict__ rgb_out, float4* __restrict__ state, uint32_t* __restrict__ list, uint32_t* __restrict__ n_active) {
+    uint32_t ray       = 0u;
+    const bool valid   = tiled_ray(blockIdx.x * 256u + threadIdx.x, W, tiles_x, row0_tile, ray0, ray_end, ray);
     const bool take    = valid && counts[ray] > 0u;
     const uint64_t m   = __ballot(take);
     const uint32_t lane = threadIdx.x & 63u;
@@ -246,14 +270,28 @@ __global__ __launch_bounds__(256) void k_round_counts(uint32_t n_slots, const ui
     cnt[a] = v;
 }
 
-// Stream indices of this round's samples, slot by slot (one wave per slot).
+// Stream indices of this round's samples.  One wave per group of 64 list
+// slots (lane = slot): the group's samples fill the same range of the list
+// as slot by slot (from off of its first slot), but step-major: step i of
+// every slot that has one, in slot order, then step i + 1.
 __global__ __launch_bounds__(256) void k_round_list(const uint32_t* __restrict__ list, const uint32_t* __restrict__ n_active, const uint32_t* __restrict__ offsets, uint32_t S, const uint32_t* __restrict__ cnt,
                                                    const uint32_t* __restrict__ off, uint32_t* __restrict__ qlist) {
     const uint32_t lane = threadIdx.x & 63u, nw = gridDim.x * 4u;
     const uint32_t n    = *n_active;
-    for (uint32_t a = blockIdx.x * 4u + (threadIdx.x >> 6); a < n; a += nw) {
-        const uint32_t q0 = offsets[list[a]] + S, dst = off[a], m = cnt[a];
-        for (uint32_t k = lane; k < m; k += 64u) qlist[dst + k] = q0 + k;
+    for (uint32_t g = blockIdx.x * 4u + (threadIdx.x >> 6); g * 64u < n; g += nw) {
+        const uint32_t a  = g * 64u + lane;
+        const bool slot   = a < n;
+        const uint32_t m  = slot ? cnt[a] : 0u;
+        const uint32_t q0 = slot && m ? offsets[list[a]] + S : 0u;
+        uint32_t dst      = off[g * 64u];
+        uint32_t steps    = m;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) steps = max(steps, (uint32_t)__shfl_xor((int)steps, o, 64));
+        for (uint32_t i = 0; i < steps; ++i) {
+            const uint64_t act = __ballot(i < m);
+            if (i < m) qlist[dst + wave::rank_below(act)] = q0 + i;
+            dst += (uint32_t)__popcll(act);
+        }
     }
 }
 
@@ -261,14 +299,17 @@ __global__ __launch_bounds__(256) void k_round_list(const uint32_t* __restrict__
 // groups of 64 (transmittance = carried T x exclusive product of 1 - alpha;
 // the first sample after which T < t_stop is the last one composited), then
 // write the pixel or carry (T, C) into the next round.  Kept rays are
-// buffered one per lane and appended 64 at a time.
+// buffered one per lane and appended once per group of 64 slots.
 __global__ __launch_bounds__(256) void k_round_composite(const uint32_t* __restrict__ list, const uint32_t* __restrict__ n_active, const uint32_t* __restrict__ counts, const uint32_t* __restrict__ offsets,
                                                         const float2* __restrict__ samples, const float4* __restrict__ field, uint32_t S, uint32_t K, float t_stop, float3 bg, float4* __restrict__ state,
                                                         uint32_t* __restrict__ rgba8, float* __restrict__ rgb_out, uint32_t* __restrict__ next_list, uint32_t* __restrict__ n_next) {
     const uint32_t lane = threadIdx.x & 63u, nw = gridDim.x * 4u;
     const uint32_t n    = *n_active;
-    uint32_t kept_ray   = 0u, n_kept = 0u;  // lane j holds the j-th kept ray
-    for (uint32_t a = blockIdx.x * 4u + (threadIdx.x >> 6); a < n; a += nw) {
+    // One wave per group of 64 list slots, slot after slot, so that the rays
+    // a group keeps enter the next list together and in order.
+    for (uint32_t g = blockIdx.x * 4u + (threadIdx.x >> 6); g * 64u < n; g += nw) {
+    uint32_t kept_ray = 0u, n_kept = 0u;  // lane j holds the j-th kept ray
+    for (uint32_t a = g * 64u; a < min(n, g * 64u + 64u); ++a) {
         const uint32_t ray   = list[a];
         const uint32_t count = counts[ray];
         const uint32_t base  = offsets[ray];
@@ -309,12 +350,7 @@ __global__ __launch_bounds__(256) void k_round_composite(const uint32_t* __restr
         } else {
             if (lane == 0u) state[ray] = make_float4(T, cr, cg, cb);
             if (lane == n_kept) kept_ray = ray;
-            if (++n_kept == 64u) {
-                uint32_t at = 0u;
-                if (lane == 0u) at = atomicAdd(n_next, 64u);
-                next_list[(uint32_t)__shfl((int)at, 0, 64) + lane] = kept_ray;
-                n_kept = 0u;
-            }
+            ++n_kept;  // at most 64: one group
         }
     }
     if (n_kept) {
@@ -322,6 +358,7 @@ __global__ __launch_bounds__(256) void k_round_composite(const uint32_t* __restr
         if (lane == 0u) at = atomicAdd(n_next, n_kept);
         at = (uint32_t)__shfl((int)at, 0, 64);
         if (lane < n_kept) next_list[at + lane] = kept_ray;
+    }
     }
 }
 
@@ -780,7 +817,11 @@ NERF_API NerfStatus nerf_ext_render(NerfExtRenderer* R, const NerfExtRenderDesc*
         uint32_t* l_nxt = R->list[1].ptr;
         const uint32_t cblocks = (nr + 255u) / 256u;
         k_fill_u32<<<1, 64, 0, st>>>(n_cur, 2u, 0u);
-        k_round_init<<<cblocks, 256, 0, st>>>(c.ray0, c.ray_end, R->counts.ptr, bg, rgba8, rgb_f32, R->state.ptr, l_cur, n_cur);
+        // Tile-major enumeration of the chunk's rays: tile rows from the
+        // chunk's first pixel row to its last.
+        const uint32_t tiles_x = (W + kTile - 1u) / kTile, row0_tile = (c.ray0 / W) / kTile, row1_tile = ((c.ray_end - 1u) / W) / kTile;
+        const uint64_t tile_threads = (uint64_t)(row1_tile - row0_tile + 1u) * tiles_x * kTile * kTile;
+        k_round_init<<<(uint32_t)((tile_threads + 255u) / 256u), 256, 0, st>>>(c.ray0, c.ray_end, W, tiles_x, row0_tile, R->counts.ptr, bg, rgba8, rgb_f32, R->state.ptr, l_cur, n_cur);
         NERF_LAUNCH_CHECK("k_round_init");
         const uint32_t ray_waves = std::min<uint32_t>((nr + 3u) / 4u, device_cu_count() * 16u);  // workgroups of one-wave-per-slot kernels
         for (uint32_t r = 0; r < n_rounds; ++r) {
