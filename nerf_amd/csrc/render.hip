@@ -256,12 +256,12 @@ __global__ __launch_bounds__(256) void k_round_init(uint32_t ray0, uint32_t ray_
 }
 
 // Samples of this round per list slot (zero past the active count, so the
-// scan runs over a fixed length); also clears the next round's counter.
+// scans run over a fixed length); keep flags start at zero.
 __global__ __launch_bounds__(256) void k_round_counts(uint32_t n_slots, const uint32_t* __restrict__ list, const uint32_t* __restrict__ n_active, const uint32_t* __restrict__ counts, uint32_t S, uint32_t K, uint32_t* __restrict__ cnt,
-                                                     uint32_t* __restrict__ n_next) {
+                                                     uint32_t* __restrict__ keep) {
     const uint32_t a = blockIdx.x * 256u + threadIdx.x;
-    if (a == 0u) *n_next = 0u;
     if (a >= n_slots) return;
+    keep[a] = 0u;
     uint32_t v = 0u;
     if (a < *n_active) {
         const uint32_t c = counts[list[a]];
@@ -298,18 +298,14 @@ __global__ __launch_bounds__(256) void k_round_list(const uint32_t* __restrict__
 // One wave per active ray: composite samples [S, min(count, S + K)) in
 // groups of 64 (transmittance = carried T x exclusive product of 1 - alpha;
 // the first sample after which T < t_stop is the last one composited), then
-// write the pixel or carry (T, C) into the next round.  Kept rays are
-// buffered one per lane and appended once per group of 64 slots.
+// write the pixel or carry (T, C) into the next round and flag the slot in
+// keep (k_round_compact then lists the kept rays in slot order).
 __global__ __launch_bounds__(256) void k_round_composite(const uint32_t* __restrict__ list, const uint32_t* __restrict__ n_active, const uint32_t* __restrict__ counts, const uint32_t* __restrict__ offsets,
                                                         const float2* __restrict__ samples, const float4* __restrict__ field, uint32_t S, uint32_t K, float t_stop, float3 bg, float4* __restrict__ state,
-                                                        uint32_t* __restrict__ rgba8, float* __restrict__ rgb_out, uint32_t* __restrict__ next_list, uint32_t* __restrict__ n_next) {
+                                                        uint32_t* __restrict__ rgba8, float* __restrict__ rgb_out, uint32_t* __restrict__ keep) {
     const uint32_t lane = threadIdx.x & 63u, nw = gridDim.x * 4u;
     const uint32_t n    = *n_active;
-    // One wave per group of 64 list slots, slot after slot, so that the rays
-    // a group keeps enter the next list together and in order.
-    for (uint32_t g = blockIdx.x * 4u + (threadIdx.x >> 6); g * 64u < n; g += nw) {
-    uint32_t kept_ray = 0u, n_kept = 0u;  // lane j holds the j-th kept ray
-    for (uint32_t a = g * 64u; a < min(n, g * 64u + 64u); ++a) {
+    for (uint32_t a = blockIdx.x * 4u + (threadIdx.x >> 6); a < n; a += nw) {
         const uint32_t ray   = list[a];
         const uint32_t count = counts[ray];
         const uint32_t base  = offsets[ray];
@@ -345,21 +341,23 @@ __global__ __launch_bounds__(256) void k_round_composite(const uint32_t* __restr
         cr = st0.y + wave::sum(cr);
         cg = st0.z + wave::sum(cg);
         cb = st0.w + wave::sum(cb);
-        if (stopped || end >= count) {
-            if (lane == 0u) write_pixel(ray, cr, cg, cb, T, bg, rgba8, rgb_out);
-        } else {
-            if (lane == 0u) state[ray] = make_float4(T, cr, cg, cb);
-            if (lane == n_kept) kept_ray = ray;
-            ++n_kept;  // at most 64: one group
+        const bool done = stopped || end >= count;
+        if (lane == 0u) {
+            if (done) write_pixel(ray, cr, cg, cb, T, bg, rgba8, rgb_out);
+            else state[ray] = make_float4(T, cr, cg, cb);
+            keep[a] = done ? 0u : 1u;
         }
     }
-    if (n_kept) {
-        uint32_t at = 0u;
-        if (lane == 0u) at = atomicAdd(n_next, n_kept);
-        at = (uint32_t)__shfl((int)at, 0, 64);
-        if (lane < n_kept) next_list[at + lane] = kept_ray;
-    }
-    }
+}
+
+// The next round's list: the kept slots' rays in slot order (kept groups
+// stay together), at positions from the exclusive scan of keep; the count
+// is the low word of the scan's 64-bit total.
+__global__ __launch_bounds__(256) void k_round_compact(const uint32_t* __restrict__ list, const uint32_t* __restrict__ n_active, const uint32_t* __restrict__ keep, const uint32_t* __restrict__ koff,
+                                                      const unsigned long long* __restrict__ total, uint32_t* __restrict__ next_list, uint32_t* __restrict__ n_next) {
+    const uint32_t a = blockIdx.x * 256u + threadIdx.x;
+    if (a == 0u) *n_next = (uint32_t)*total;
+    if (a < *n_active && keep[a]) next_list[koff[a]] = list[a];
 }
 
 }  // namespace
@@ -538,6 +536,8 @@ struct NerfExtRenderer {
     Buf<float4> state;                 // per ray (T, C.rgb)
     Buf<uint32_t> list[2], n_active;   // active rays of this / the next round, and their counts
     Buf<uint32_t> cnt, off, qlist;     // samples per slot, their offsets, stream indices
+    Buf<uint32_t> keep, koff;          // slots carried into the next round, their positions there
+    Buf<unsigned long long> keep_total;
     Buf<unsigned long long> round_total;
     Buf<nerf_hip::half8_t> ref_frags;           // reference-model weights in MFMA fragment order
     hipEvent_t ev[6] = {};
@@ -560,6 +560,9 @@ struct NerfExtRenderer {
         n_active.release();
         cnt.release();
         off.release();
+        keep.release();
+        koff.release();
+        keep_total.release();
         qlist.release();
         round_total.release();
         for (hipEvent_t& e : fev)
@@ -798,6 +801,9 @@ NERF_API NerfStatus nerf_ext_render(NerfExtRenderer* R, const NerfExtRenderDesc*
     NERF_HIP_TRY(R->cnt.reserve(chunk_rays_max));
     NERF_HIP_TRY(R->off.reserve(chunk_rays_max));
     NERF_HIP_TRY(R->round_total.reserve(kMaxRounds));
+    NERF_HIP_TRY(R->keep.reserve(chunk_rays_max));
+    NERF_HIP_TRY(R->koff.reserve(chunk_rays_max));
+    NERF_HIP_TRY(R->keep_total.reserve(1));
     in.sample_index = R->qlist.ptr;
 
     float ms_scan = 0.0f, ms_samples = 0.0f, field_ms = 0.0f;
@@ -825,7 +831,7 @@ NERF_API NerfStatus nerf_ext_render(NerfExtRenderer* R, const NerfExtRenderDesc*
         NERF_LAUNCH_CHECK("k_round_init");
         const uint32_t ray_waves = std::min<uint32_t>((nr + 3u) / 4u, device_cu_count() * 16u);  // workgroups of one-wave-per-slot kernels
         for (uint32_t r = 0; r < n_rounds; ++r) {
-            k_round_counts<<<cblocks, 256, 0, st>>>(nr, l_cur, n_cur, R->counts.ptr, Ss[r], Ks[r], R->cnt.ptr, n_nxt);
+            k_round_counts<<<cblocks, 256, 0, st>>>(nr, l_cur, n_cur, R->counts.ptr, Ss[r], Ks[r], R->cnt.ptr, R->keep.ptr);
             NERF_HIP_TRY(exclusive_scan_u32(R->cnt.ptr, R->off.ptr, nr, R->scan_tmp.ptr, R->round_total.ptr + r, st));
             k_round_list<<<ray_waves, 256, 0, st>>>(l_cur, n_cur, R->offsets.ptr, Ss[r], R->cnt.ptr, R->off.ptr, R->qlist.ptr);
             NERF_LAUNCH_CHECK("k_round_list");
@@ -836,8 +842,11 @@ NERF_API NerfStatus nerf_ext_render(NerfExtRenderer* R, const NerfExtRenderDesc*
             if (ref_model) NERF_HIP_TRY(launch_ref_field(R->ref_frags.ptr, in, (uint32_t)c.samples, R->field.ptr, nullptr, st));
             else NERF_HIP_TRY(launch_field(g, d->model->table, w, in, (uint32_t)c.samples, R->field.ptr, st));
             if (timed) NERF_HIP_TRY(hipEventRecord(R->fev[2u * r + 1u], st));
-            k_round_composite<<<ray_waves, 256, 0, st>>>(l_cur, n_cur, R->counts.ptr, R->offsets.ptr, R->samples.ptr, R->field.ptr, Ss[r], Ks[r], d->min_transmittance, bg, R->state.ptr, rgba8, rgb_f32, l_nxt, n_nxt);
+            k_round_composite<<<ray_waves, 256, 0, st>>>(l_cur, n_cur, R->counts.ptr, R->offsets.ptr, R->samples.ptr, R->field.ptr, Ss[r], Ks[r], d->min_transmittance, bg, R->state.ptr, rgba8, rgb_f32, R->keep.ptr);
             NERF_LAUNCH_CHECK("k_round_composite");
+            NERF_HIP_TRY(exclusive_scan_u32(R->keep.ptr, R->koff.ptr, nr, R->scan_tmp.ptr, R->keep_total.ptr, st));
+            k_round_compact<<<cblocks, 256, 0, st>>>(l_cur, n_cur, R->keep.ptr, R->koff.ptr, R->keep_total.ptr, l_nxt, n_nxt);
+            NERF_LAUNCH_CHECK("k_round_compact");
             std::swap(l_cur, l_nxt);
             std::swap(n_cur, n_nxt);
         }
