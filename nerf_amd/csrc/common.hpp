@@ -335,6 +335,10 @@ struct FieldInputs {
     // Optional (mode B): the j-th sample evaluated is stream sample
     // sample_index[j], and its output goes to out[sample_index[j]].
     const uint32_t* sample_index;
+    // Optional with sample_index (the level-major kernel): the owning ray of
+    // the j-th evaluated sample, read in order instead of sample_ray at a
+    // scattered stream index.
+    const uint32_t* sample_index_ray;
     // Mode B positions are world positions inside [bmin, bmax]; the grid
     // encodes the unit cube, so they are mapped by (p - bmin) / (bmax - bmin).
     float bmin[3];

@@ -33,9 +33,8 @@ using namespace mlp;
 namespace {
 
 // Position (normalised by the AABB) and direction of march sample q.
-__device__ __forceinline__ void sample_point(const FieldInputs& in, uint32_t q, float p[3], float d[3]) {
+__device__ __forceinline__ void sample_point(const FieldInputs& in, uint32_t q, uint32_t r, float p[3], float d[3]) {
     const float2 td  = in.samples[q];
-    const uint32_t r = in.sample_ray[q];
     const float4 ro  = in.rays[2ull * r];
     const float4 rd  = in.rays[2ull * r + 1ull];
     d[0]             = rd.x;
@@ -130,7 +129,7 @@ __global__ __launch_bounds__(kBlockThreads) void k_field_forward(GridParams g, c
         if constexpr (kFromSamples) {
             const uint32_t qs = in.sample_index ? in.sample_index[q] : q;
             dst               = in.sample_index ? qs : s;
-            sample_point(in, qs, p, d);
+            sample_point(in, qs, in.sample_ray[qs], p, d);
         } else {
 #pragma unroll
             for (int a = 0; a < 3; ++a) {
@@ -187,7 +186,8 @@ __global__ __launch_bounds__(kBlockThreads) void k_field_forward_lv(GridParams g
         float p[3], d[3];
         if constexpr (kFromSamples) {
             const uint32_t qs = in.sample_index ? in.sample_index[q] : q;
-            sample_point(in, qs, p, d);
+            const uint32_t r  = in.sample_index && in.sample_index_ray ? in.sample_index_ray[q] : in.sample_ray[qs];
+            sample_point(in, qs, r, p, d);
         } else {
 #pragma unroll
             for (int a = 0; a < 3; ++a) {

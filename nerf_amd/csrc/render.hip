@@ -275,21 +275,26 @@ __global__ __launch_bounds__(256) void k_round_counts(uint32_t n_slots, const ui
 // as slot by slot (from off of its first slot), but step-major: step i of
 // every slot that has one, in slot order, then step i + 1.
 __global__ __launch_bounds__(256) void k_round_list(const uint32_t* __restrict__ list, const uint32_t* __restrict__ n_active, const uint32_t* __restrict__ offsets, uint32_t S, const uint32_t* __restrict__ cnt,
-                                                   const uint32_t* __restrict__ off, uint32_t* __restrict__ qlist) {
+                                                   const uint32_t* __restrict__ off, uint32_t* __restrict__ qlist, uint32_t* __restrict__ qray) {
     const uint32_t lane = threadIdx.x & 63u, nw = gridDim.x * 4u;
     const uint32_t n    = *n_active;
     for (uint32_t g = blockIdx.x * 4u + (threadIdx.x >> 6); g * 64u < n; g += nw) {
         const uint32_t a  = g * 64u + lane;
         const bool slot   = a < n;
         const uint32_t m  = slot ? cnt[a] : 0u;
-        const uint32_t q0 = slot && m ? offsets[list[a]] + S : 0u;
+        const uint32_t ray = slot && m ? list[a] : 0u;
+        const uint32_t q0  = slot && m ? offsets[ray] + S : 0u;
         uint32_t dst      = off[g * 64u];
         uint32_t steps    = m;
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) steps = max(steps, (uint32_t)__shfl_xor((int)steps, o, 64));
         for (uint32_t i = 0; i < steps; ++i) {
             const uint64_t act = __ballot(i < m);
-            if (i < m) qlist[dst + wave::rank_below(act)] = q0 + i;
+            if (i < m) {
+                const uint32_t at = dst + wave::rank_below(act);
+                qlist[at]         = q0 + i;
+                qray[at]          = ray;
+            }
             dst += (uint32_t)__popcll(act);
         }
     }
@@ -536,6 +541,7 @@ struct NerfExtRenderer {
     Buf<float4> state;                 // per ray (T, C.rgb)
     Buf<uint32_t> list[2], n_active;   // active rays of this / the next round, and their counts
     Buf<uint32_t> cnt, off, qlist;     // samples per slot, their offsets, stream indices
+    Buf<uint32_t> qray;                // owning ray of each qlist entry
     Buf<uint32_t> keep, koff;          // slots carried into the next round, their positions there
     Buf<unsigned long long> keep_total;
     Buf<unsigned long long> round_total;
@@ -564,6 +570,7 @@ struct NerfExtRenderer {
         koff.release();
         keep_total.release();
         qlist.release();
+        qray.release();
         round_total.release();
         for (hipEvent_t& e : fev)
             if (e) (void)hipEventDestroy(e);
@@ -769,6 +776,7 @@ NERF_API NerfStatus nerf_ext_render(NerfExtRenderer* R, const NerfExtRenderDesc*
     NERF_HIP_TRY(R->sample_ray.reserve(biggest));
     NERF_HIP_TRY(R->field.reserve(biggest));
     NERF_HIP_TRY(R->qlist.reserve(biggest));
+    NERF_HIP_TRY(R->qray.reserve(biggest));
 
     FieldInputs in{};
     in.samples    = R->samples.ptr;
@@ -804,7 +812,8 @@ NERF_API NerfStatus nerf_ext_render(NerfExtRenderer* R, const NerfExtRenderDesc*
     NERF_HIP_TRY(R->keep.reserve(chunk_rays_max));
     NERF_HIP_TRY(R->koff.reserve(chunk_rays_max));
     NERF_HIP_TRY(R->keep_total.reserve(1));
-    in.sample_index = R->qlist.ptr;
+    in.sample_index     = R->qlist.ptr;
+    in.sample_index_ray = R->qray.ptr;
 
     float ms_scan = 0.0f, ms_samples = 0.0f, field_ms = 0.0f;
     uint64_t shaded = 0;
@@ -833,7 +842,7 @@ NERF_API NerfStatus nerf_ext_render(NerfExtRenderer* R, const NerfExtRenderDesc*
         for (uint32_t r = 0; r < n_rounds; ++r) {
             k_round_counts<<<cblocks, 256, 0, st>>>(nr, l_cur, n_cur, R->counts.ptr, Ss[r], Ks[r], R->cnt.ptr, R->keep.ptr);
             NERF_HIP_TRY(exclusive_scan_u32(R->cnt.ptr, R->off.ptr, nr, R->scan_tmp.ptr, R->round_total.ptr + r, st));
-            k_round_list<<<ray_waves, 256, 0, st>>>(l_cur, n_cur, R->offsets.ptr, Ss[r], R->cnt.ptr, R->off.ptr, R->qlist.ptr);
+            k_round_list<<<ray_waves, 256, 0, st>>>(l_cur, n_cur, R->offsets.ptr, Ss[r], R->cnt.ptr, R->off.ptr, R->qlist.ptr, R->qray.ptr);
             NERF_LAUNCH_CHECK("k_round_list");
             // The field reads this round's sample count on the device: the low
             // word of the 64-bit scan total (little-endian; totals < 2^32).
