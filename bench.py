@@ -673,6 +673,7 @@ def main() -> int:
     ap.add_argument("--no-configs", action="store_true", help="skip the C4 (1920x1080, T=2^22) and C5 (8 views, 5 cascades) renders")
     ap.add_argument("--train-steps", type=int, default=100, help="timed training steps (0: skip the training leg)")
     ap.add_argument("--train-warmup", type=int, default=30)
+    ap.add_argument("--no-reference-legs", action="store_true", help="skip the reference-model training, reference-host and reference-model render legs")
     ap.add_argument("--width", type=int, default=W, help="render width (the metric is quoted at 800)")
     ap.add_argument("--height", type=int, default=H, help="render height (the metric is quoted at 800)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -766,11 +767,13 @@ def main() -> int:
     train_snap = None
     if args.train_steps > 0:
         line["train"], train_snap = train_bench(args.train_steps, args.train_warmup)
-        line["train_reference_model"] = ref_train_bench(max(10, args.train_steps // 2), 10)
-        line["reference_host"] = reference_host_bench()
+        if not args.no_reference_legs:
+            line["train_reference_model"] = ref_train_bench(max(10, args.train_steps // 2), 10)
+            line["reference_host"] = reference_host_bench()
     if not args.no_configs:
         line["configs"] = config_renders()
-        line["reference_model"] = ref_model_render()
+        if not args.no_reference_legs:
+            line["reference_model"] = ref_model_render()
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(model, cam, bits, train_snap)
     print(json.dumps(line), flush=True)
