@@ -104,6 +104,25 @@ def build_harness(jobs: int = 8) -> tuple[Path, Path]:
     return HOST_LIB, BENCH_EXE
 
 
+SAN_FLAGS = ["-O1", "-g", "-fno-omit-frame-pointer", "-fsanitize=address,undefined", "-fno-sanitize-recover=undefined"]
+
+
+def build_harness_sanitized(out_dir: Path) -> Path:
+    """libnerf_host.so of the host harness (plain C++, g++) with
+    AddressSanitizer and UndefinedBehaviorSanitizer, into out_dir."""
+    gxx = shutil.which("g++") or "g++"
+    out_dir.mkdir(parents=True, exist_ok=True)
+    flags = [f for f in GXX_FLAGS if f != "-O2"] + SAN_FLAGS
+    objs = []
+    for stem in ("png", "json", "dataset", "host_capi"):
+        obj = out_dir / f"{stem}.o"
+        _run([gxx, *flags, "-c", str(HARNESS / f"{stem}.cpp"), "-o", str(obj)])
+        objs.append(obj)
+    lib = out_dir / "libnerf_host.so"
+    _run([gxx, "-shared", *SAN_FLAGS, "-o", str(lib), *map(str, objs)])
+    return lib
+
+
 def main() -> None:
     lib = build_library()
     print(f"built {lib}")

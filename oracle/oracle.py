@@ -7,6 +7,7 @@ __graft_entry__.py and by the cpu_baseline leg of bench.py.  The product
 from __future__ import annotations
 
 import ctypes as C
+import os
 import subprocess
 from pathlib import Path
 
@@ -111,9 +112,12 @@ def build() -> None:
 def lib() -> C.CDLL:
     global _lib
     if _lib is None:
-        if not LIB_PATH.exists():
+        # NERF_ORACLE_LIB selects another build of the same sources (the
+        # sanitizer build of tests/test_sanitizers.py).
+        path = Path(os.environ["NERF_ORACLE_LIB"]) if os.environ.get("NERF_ORACLE_LIB") else LIB_PATH
+        if not path.exists():
             build()
-        L = C.CDLL(str(LIB_PATH))
+        L = C.CDLL(str(path))
         for name, (res, args) in _PROTOS.items():
             f = getattr(L, name)
             f.restype = res

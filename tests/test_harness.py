@@ -6,6 +6,7 @@ against its closed form (benchmark.cpp:148-303: Blender world axes (x, -z, y),
 translation x 0.33 + 0.5); the dataset loader end to end; PSNR against its
 closed form (benchmark.cpp:47-86)."""
 import ctypes as C
+import os
 import json
 import math
 import struct
@@ -15,7 +16,9 @@ from pathlib import Path
 import numpy as np
 import pytest
 
-LIB_PATH = Path(__file__).resolve().parent.parent / "nerf_amd" / "libnerf_host.so"
+# NERF_HOST_LIB selects another build of the harness (the sanitizer build of
+# tests/test_sanitizers.py).
+LIB_PATH = Path(os.environ["NERF_HOST_LIB"]) if os.environ.get("NERF_HOST_LIB") else Path(__file__).resolve().parent.parent / "nerf_amd" / "libnerf_host.so"
 
 
 @pytest.fixture(scope="module")
