@@ -59,13 +59,14 @@ FIELD_BYTES_PER_SAMPLE = 12 + 16 * 8 * 2 * 2 + 16
 # Algorithmic MLP flops per sample: density 32x64 + 64x16, colour 31x64 +
 # 64x64 + 64x3, two flops per multiply-add.
 FIELD_FLOPS_PER_SAMPLE = 2 * (32 * 64 + 64 * 16) + 2 * (31 * 64 + 64 * 64 + 64 * 3)
-# HBM traffic of the field kernel per sample on this workload, from rocprofv3
-# FETCH_SIZE (x 2.0) + WRITE_SIZE (x 1.0) on one 800x800 render, the factors
-# being what the same counters read on a plain conversion kernel of known
-# size (profiles/field_forward_800x800_hbm_traffic.md): 788.5 GB + 8.0 GB over
-# 486,308,861 samples, summed over the render's three rounds.  Every 4-byte table gather pulls a whole line from
-# beyond L2, hence the gap to the 540 algorithmic bytes.
-FIELD_TRAFFIC_BYTES_PER_SAMPLE = 1638
+# Traffic beyond L2 of the field kernel per sample on this workload, from
+# rocprofv3 FETCH_SIZE (x 2.0) + WRITE_SIZE (x 1.0) on one 800x800 render, the
+# factors being what the same counters read on a plain conversion kernel of
+# known size (profiles/field_forward_800x800_counters.md): 135.18 GB + 8.92 GB
+# over 486,308,861 samples, summed over the render's three rounds.  The render
+# rounds list samples in spatial order, so neighbouring lanes share table lines
+# in L2 (65 % hit) and the traffic stays below the 540 algorithmic bytes.
+FIELD_TRAFFIC_BYTES_PER_SAMPLE = 296
 # Reference-model network per sample, on the reference's own padded shapes
 # (backend-cuda.cu:23-54): density 64x128 + 4 x 128x128 + 128x16, colour
 # 48x128 + 2 x 128x128 + 128x16, two flops per multiply-add.
@@ -697,8 +698,15 @@ def main() -> int:
         synchronize()
         print(json.dumps({"copy_calibration": {"elements": n, "read_bytes": 4 * n, "write_bytes": 2 * n, "kernel": "k_float_to_half", "launches": 3}}), flush=True)
         return 0
+    t_start = time.perf_counter()
+
+    def progress(what):
+        # One stderr line per finished leg (stdout keeps the single JSON line).
+        print(f"bench.py: {what} done at {time.perf_counter() - t_start:.1f} s", file=sys.stderr, flush=True)
+
     info = device_info()
     scene, bits, desc, model, cam, occ = build_workload()
+    progress("workload")
     stream = Stream()
     renderer = ext.Renderer()
     rgba = DeviceArray((1, H, W), np.uint32)
@@ -733,6 +741,7 @@ def main() -> int:
         samples = st.samples
         shaded = st.samples_shaded
     stage = {k: v / args.steps for k, v in stage.items()}
+    progress("render")
     field_s = stage["field"] / 1e3
     achieved_gbs = shaded * FIELD_BYTES_PER_SAMPLE / field_s / 1e9
     field_tflops = shaded * FIELD_FLOPS_PER_SAMPLE / field_s / 1e12
@@ -756,26 +765,34 @@ def main() -> int:
         "stages_ms": {k: round(v, 4) for k, v in stage.items()},
         "roofline": {"kernel": "k_field_forward_lv (fused hash encode + density/colour MLP, level-major gathers)", "bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved_gbs / HBM_PEAK_GBS, 4), "traffic": int(shaded * FIELD_TRAFFIC_BYTES_PER_SAMPLE),
-                     "traffic_source": f"profile-derived, not counted in this run: {FIELD_TRAFFIC_BYTES_PER_SAMPLE} B/sample from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE on this render (profiles/field_forward_800x800_hbm_traffic.md) x this run's shaded samples",
+                     "traffic_source": f"profile-derived, not counted in this run: {FIELD_TRAFFIC_BYTES_PER_SAMPLE} B/sample from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE on this render (profiles/field_forward_800x800_counters.md) x this run's shaded samples",
                      "traffic_GBps": round(shaded * FIELD_TRAFFIC_BYTES_PER_SAMPLE / field_s / 1e9, 1), "mfma_tflops": round(field_tflops, 2), "mfma_frac": round(field_tflops / MFMA_FP16_PEAK_TFS, 4),
                      "bytes_per_sample": FIELD_BYTES_PER_SAMPLE, "flops_per_sample": FIELD_FLOPS_PER_SAMPLE},
         "device": {"name": info.name.decode(), "arch": info.arch.decode(), "cus": info.compute_units},
     }
     if not args.no_stage_rooflines:
         line["stage_rooflines"] = kernel_rooflines()
+        progress("stage rooflines")
         line["abi_render"] = abi_render()
+        progress("ABI render")
     train_snap = None
     if args.train_steps > 0:
         line["train"], train_snap = train_bench(args.train_steps, args.train_warmup)
+        progress("training")
         if not args.no_reference_legs:
             line["train_reference_model"] = ref_train_bench(max(10, args.train_steps // 2), 10)
+            progress("reference-model training")
             line["reference_host"] = reference_host_bench()
+            progress("reference host")
     if not args.no_configs:
         line["configs"] = config_renders()
+        progress("C4/C5 renders")
         if not args.no_reference_legs:
             line["reference_model"] = ref_model_render()
+            progress("reference-model render")
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(model, cam, bits, train_snap)
+        progress("CPU baseline")
     print(json.dumps(line), flush=True)
     return 0
 
