@@ -213,19 +213,24 @@ __device__ __forceinline__ float cone_of(const NerfExtCamera& c) {  // :333-337
 }
 
 // Random pixel per ray (:438-441), ray, march count, bilinear ground truth
-// composited over white (:471-499).  kTrainGroup lanes per ray (wave::march); ray
+// composited over white (:471-499).  kRayGroup lanes per ray (wave::march); ray
 // slots from n_rays to max_rays get a zero count so the scan over all slots
 // stays valid.
-constexpr uint32_t kTrainGroup = 16u;  // lanes per ray in the training march (4 rays per wave)
+constexpr uint32_t kTrainGroup = 16u;  // lanes per ray in the emission pass (4 units per wave)
+// Lanes per ray in the count pass: a step has only a few hundred rays (one
+// wave each, under one per SIMD), so the pass is the t recurrence's latency
+// plus one occupancy-word load per run; 64-step runs hide each run's loads
+// behind the next run's recurrence (55.7 -> 35.0 us per step at 16 -> 64).
+constexpr uint32_t kRayGroup = 64u;
 
 __global__ __launch_bounds__(256) void k_train_rays(TrainParams P, const TrainDevState* S, const NerfExtCamera* __restrict__ cams, const uint8_t* __restrict__ images, const uint32_t* __restrict__ bits, float4* __restrict__ rays, float4* __restrict__ gt,
                                                      uint32_t* __restrict__ counts, float* __restrict__ seg_t, uint32_t* __restrict__ seg_seen, uint32_t* __restrict__ seg_reached, uint32_t segs) {
-    constexpr uint32_t kPer = 64u / kTrainGroup;  // rays per wave
+    constexpr uint32_t kPer = 64u / kRayGroup;  // rays per wave
     const uint32_t lane = threadIdx.x & 63u, stride = gridDim.x * kWaves * kPer;
     const uint32_t n_rays = S->n_rays, cam_idx = S->camera, frame = S->frame;
     const NerfExtCamera cam = cams[cam_idx];
     const float cone        = cone_of(cam);
-    for (uint32_t r = (blockIdx.x * kWaves + (threadIdx.x >> 6)) * kPer + lane / kTrainGroup; r < P.max_rays; r += stride) {
+    for (uint32_t r = (blockIdx.x * kWaves + (threadIdx.x >> 6)) * kPer + lane / kRayGroup; r < P.max_rays; r += stride) {
         uint32_t count = 0u, reached = 0u;
         float4 ro = make_float4(0.0f, 0.0f, 0.0f, 0.0f), rd = make_float4(0.0f, 0.0f, 0.0f, 0.0f), g4 = make_float4(1.0f, 1.0f, 1.0f, 0.0f);
         if (r < n_rays) {
@@ -239,11 +244,11 @@ __global__ __launch_bounds__(256) void k_train_rays(TrainParams P, const TrainDe
                 rd    = make_float4(ray.d[0], ray.d[1], ray.d[2], ray.tf);
                 // Checkpoints every kSegSteps steps (t and the occupied steps
                 // before), from which k_train_samples resumes each segment.
-                count = wave::march<kTrainGroup>(ro, rd, cone, P.max_steps, ~0u, bits, [&](const float p[3]) { return occ_cell_at(P, p); }, [](uint32_t, float, float) {},
+                count = wave::march<kRayGroup>(ro, rd, cone, P.max_steps, ~0u, bits, [&](const float p[3]) { return occ_cell_at(P, p); }, [](uint32_t, float, float) {},
                                                  [&](uint32_t i0, float t0, uint32_t seen) {
                                                      if (i0 % kSegSteps == 0u) {
                                                          reached = i0 / kSegSteps + 1u;
-                                                         if (lane % kTrainGroup == 0u) {
+                                                         if (lane % kRayGroup == 0u) {
                                                              seg_t[(uint64_t)r * segs + i0 / kSegSteps]    = t0;
                                                              seg_seen[(uint64_t)r * segs + i0 / kSegSteps] = seen;
                                                          }
@@ -273,7 +278,7 @@ __global__ __launch_bounds__(256) void k_train_rays(TrainParams P, const TrainDe
                 g4 = make_float4(c[0] * alpha + (1.0f - alpha), c[1] * alpha + (1.0f - alpha), c[2] * alpha + (1.0f - alpha), alpha);
             }
         }
-        if (lane % kTrainGroup == 0u) {
+        if (lane % kRayGroup == 0u) {
             rays[2ull * r]      = ro;
             rays[2ull * r + 1u] = rd;
             gt[r]               = g4;

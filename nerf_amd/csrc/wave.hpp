@@ -91,9 +91,15 @@ __device__ __forceinline__ uint32_t march_range(float4 ro, float4 rd, float cone
         r.t0        = t;
         r.i0        = i;
         float t_own = tf;
+        // The lane's step index, opaque to the compiler: otherwise it hoists
+        // the G compares out of the march into scalar masks, which spill for
+        // G >= 32 (two v_readlane per step); compared in place it is one
+        // v_cmp per step off the t chain.
+        uint32_t jo = j_own;
+        asm volatile("" : "+v"(jo));
 #pragma unroll
         for (uint32_t j = 0; j < G; ++j) {
-            if (j_own == j) t_own = t;
+            if (jo == j) t_own = t;
             t += step_dt(t);
         }
         r.dt             = step_dt(t_own);
