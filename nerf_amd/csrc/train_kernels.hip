@@ -215,12 +215,13 @@ __device__ __forceinline__ float cone_of(const NerfExtCamera& c) {  // :333-337
 // Random pixel per ray (:438-441), ray, march count, bilinear ground truth
 // composited over white (:471-499).  kRayGroup lanes per ray (wave::march); ray
 // slots from n_rays to max_rays get a zero count so the scan over all slots
-// stays valid.
+// stays valid (their ray, ground-truth and checkpoint records are not
+// written: every reader stops at n_rays).
 constexpr uint32_t kTrainGroup = 16u;  // lanes per ray in the emission pass (4 units per wave)
-// Lanes per ray in the count pass: a step has only a few hundred rays (one
-// wave each, under one per SIMD), so the pass is the t recurrence's latency
-// plus one occupancy-word load per run; 64-step runs hide each run's loads
-// behind the next run's recurrence (55.7 -> 35.0 us per step at 16 -> 64).
+// The count pass marches each ray with a whole wave: a step has only a few
+// hundred rays (a wave each, under one per SIMD), so the pass is the latency
+// of the t recurrence, which the three-instruction chain of
+// wave::march_range keeps near 22 cycles per step.
 constexpr uint32_t kRayGroup = 64u;
 
 __global__ __launch_bounds__(256) void k_train_rays(TrainParams P, const TrainDevState* S, const NerfExtCamera* __restrict__ cams, const uint8_t* __restrict__ images, const uint32_t* __restrict__ bits, float4* __restrict__ rays, float4* __restrict__ gt,
@@ -230,7 +231,13 @@ __global__ __launch_bounds__(256) void k_train_rays(TrainParams P, const TrainDe
     const uint32_t n_rays = S->n_rays, cam_idx = S->camera, frame = S->frame;
     const NerfExtCamera cam = cams[cam_idx];
     const float cone        = cone_of(cam);
-    for (uint32_t r = (blockIdx.x * kWaves + (threadIdx.x >> 6)) * kPer + lane / kRayGroup; r < P.max_rays; r += stride) {
+    const uint32_t n_live   = min(n_rays, P.max_rays);
+    // Slots past the step's rays get only their count (the scan runs over
+    // every slot), in coalesced stores; nothing reads their other records.
+    // (One lane writing four records per empty slot cost 30 us of a 36 us
+    // pass at 2^18 slots and ~320 rays.)
+    for (uint32_t r = n_live + blockIdx.x * blockDim.x + threadIdx.x; r < P.max_rays; r += gridDim.x * blockDim.x) counts[r] = 0u;
+    for (uint32_t r = (blockIdx.x * kWaves + (threadIdx.x >> 6)) * kPer + lane / kRayGroup; r < n_live; r += stride) {
         uint32_t count = 0u, reached = 0u;
         float4 ro = make_float4(0.0f, 0.0f, 0.0f, 0.0f), rd = make_float4(0.0f, 0.0f, 0.0f, 0.0f), g4 = make_float4(1.0f, 1.0f, 1.0f, 0.0f);
         if (r < n_rays) {

@@ -65,9 +65,9 @@ constexpr uint32_t kOutside = 0xFFFFFFFFu;
 // lane of the group at the start of each run, with the occupied steps seen
 // before it.  Returns the number of occupied steps seen (all of them when
 // limit is ~0u).
-template <uint32_t G, typename Cell, typename Emit, typename Mark>
-__device__ __forceinline__ uint32_t march_range(float4 ro, float4 rd, float cone, float dt_min, float t_begin, uint32_t i_begin, uint32_t i_end, uint32_t limit, const uint32_t* __restrict__ bits, Cell cell, Emit emit,
-                                                Mark mark) {
+template <uint32_t G, bool kMed3Chain, typename Cell, typename Emit, typename Mark>
+__device__ __forceinline__ uint32_t march_range_impl(float4 ro, float4 rd, float cone, float dt_min, float t_begin, uint32_t i_begin, uint32_t i_end, uint32_t limit, const uint32_t* __restrict__ bits, Cell cell,
+                                                     Emit emit, Mark mark) {
     static_assert(G >= 1u && G <= 64u && 64u % G == 0u, "group size must divide 64");
     const uint32_t lane = lane_id(), j_own = lane % G, shift = lane - j_own;
     const uint64_t group_bits = G == 64u ? ~0ull : ((1ull << G) - 1ull);
@@ -82,6 +82,20 @@ __device__ __forceinline__ uint32_t march_range(float4 ro, float4 rd, float cone
     // step starts (one select per step) and recomputes that step's dt, mid
     // point and liveness from it afterwards with the same operations.
     auto step_dt = [&](float tt) { return fminf(fmaxf(dt_min, tt * cone), fmaxf(tf - tt, 0.0f)); };
+    // With kMed3Chain the shared chain advances by med3(dt_min, t * cone,
+    // tf - t), three instructions per step instead of five.  It equals
+    // step_dt while the step stays short of tf (tf - t is then at least the
+    // clamped step) and whenever tf - t lies between the two candidates; when
+    // both candidates exceed tf - t, step_dt lands exactly on tf and med3
+    // beyond it, so the ray is dead either way and every live t is the same.
+    // (tf - t is exact there by Sterbenz's lemma: such a step starts beyond
+    // tf / (1 + cone) and beyond tf - dt_min, both above tf / 2 under the
+    // bounds march_range checks.)  Lanes recompute their own step with
+    // step_dt.
+    auto chain_dt = [&](float tt) { return kMed3Chain ? __builtin_amdgcn_fmed3f(dt_min, tt * cone, tf - tt) : step_dt(tt); };
+    // Lanes keeping step j of a run: lane j of every group.
+    constexpr uint64_t kOwnPattern = G == 64u ? 1ull : G == 32u ? 0x0000000100000001ull : G == 16u ? 0x0001000100010001ull : G == 8u ? 0x0101010101010101ull : 0ull;
+    static_assert(kOwnPattern != 0ull, "group size 8, 16, 32 or 64");
     struct Run {
         float tm, dt, t0;
         uint32_t i0, idx, word;
@@ -91,16 +105,13 @@ __device__ __forceinline__ uint32_t march_range(float4 ro, float4 rd, float cone
         r.t0        = t;
         r.i0        = i;
         float t_own = tf;
-        // The lane's step index, opaque to the compiler: otherwise it hoists
-        // the G compares out of the march into scalar masks, which spill for
-        // G >= 32 (two v_readlane per step); compared in place it is one
-        // v_cmp per step off the t chain.
-        uint32_t jo = j_own;
-        asm volatile("" : "+v"(jo));
 #pragma unroll
         for (uint32_t j = 0; j < G; ++j) {
-            if (jo == j) t_own = t;
-            t += step_dt(t);
+            // t_own = t on the lanes keeping step j: one v_cndmask on a
+            // constant lane mask (two scalar moves), where a compare against
+            // the lane index costs a v_cmp and a wait state more per step.
+            asm("v_cndmask_b32_e64 %0, %0, %1, %2" : "+v"(t_own) : "v"(t), "s"(kOwnPattern << j));
+            t += chain_dt(t);
         }
         r.dt             = step_dt(t_own);
         r.tm             = t_own + 0.5f * r.dt;
@@ -126,6 +137,17 @@ __device__ __forceinline__ uint32_t march_range(float4 ro, float4 rd, float cone
         cur  = nxt;
     }
     return seen;
+}
+
+template <uint32_t G, typename Cell, typename Emit, typename Mark>
+__device__ __forceinline__ uint32_t march_range(float4 ro, float4 rd, float cone, float dt_min, float t_begin, uint32_t i_begin, uint32_t i_end, uint32_t limit, const uint32_t* __restrict__ bits, Cell cell, Emit emit,
+                                                Mark mark) {
+    // The three-instruction chain where a step that reaches tf starts well
+    // beyond tf / 2 (cone <= 1/2: focal lengths of two pixels or more;
+    // dt_min <= tf / 4: four or more steps over [0, tf]); otherwise the exact
+    // one.
+    if (cone <= 0.5f && dt_min <= 0.25f * rd.w) return march_range_impl<G, true>(ro, rd, cone, dt_min, t_begin, i_begin, i_end, limit, bits, cell, emit, mark);
+    return march_range_impl<G, false>(ro, rd, cone, dt_min, t_begin, i_begin, i_end, limit, bits, cell, emit, mark);
 }
 
 // The whole march of a ray: steps [0, max_steps) from t_near = ro.w.
