@@ -661,6 +661,8 @@ __global__ __launch_bounds__(256) void k_ref_dw_reduce(const float* __restrict__
 // With n_rays_dev / n_active_dev (the trainer) the ray count is
 // min(*n_rays_dev, n_rays) and inv_norm = 1 / *n_active_dev (0 without
 // active rays).
+constexpr uint32_t kRefCompositeBatch = 8u;  // groups of 64 samples loaded together per ray
+
 __global__ __launch_bounds__(256) void k_ref_composite_train(uint32_t n_rays_cap, const uint32_t* __restrict__ counts, const uint32_t* __restrict__ offsets, const float2* __restrict__ samples, const float4* __restrict__ field,
                                                               const float4* __restrict__ gt, float inv_norm_host, float4* __restrict__ draw, float* __restrict__ loss_sum, const uint32_t* __restrict__ n_rays_dev,
                                                               const uint32_t* __restrict__ n_active_dev) {
@@ -674,21 +676,37 @@ __global__ __launch_bounds__(256) void k_ref_composite_train(uint32_t n_rays_cap
         const uint32_t count = counts[r];
         if (count == 0u) continue;
         const uint32_t base = offsets[r];
+        // kRefCompositeBatch groups of 64 samples loaded together before any
+        // is composited (a ray has only its own wave to cover the loads).
+        float4 fb[kRefCompositeBatch];
+        float db[kRefCompositeBatch];
+        auto load_batch = [&](uint32_t c0) {
+#pragma unroll
+            for (uint32_t b = 0; b < kRefCompositeBatch; ++b) {
+                const uint32_t i = c0 + 64u * b + lane;
+                const bool valid = i < count;
+                fb[b]            = valid ? field[base + i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                db[b]            = valid ? fmaxf(samples[base + i].y, 0.0f) : 0.0f;
+            }
+        };
         float T = 1.0f, C[3] = {0.0f, 0.0f, 0.0f};
-        for (uint32_t c0 = 0; c0 < count; c0 += 64u) {
-            const uint32_t i = c0 + lane;
-            const bool valid = i < count;
-            const float4 f   = valid ? field[base + i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            const float dt   = valid ? fmaxf(samples[base + i].y, 0.0f) : 0.0f;
-            const float a    = valid ? -expm1f(-(f.x * dt)) : 0.0f;
-            const float incl = wave::inclusive_product(1.0f - a);
-            float excl       = __shfl_up(incl, 1, 64);
-            excl             = lane == 0u ? 1.0f : excl;
-            const float w    = T * excl * a;
-            C[0] += w * f.y;
-            C[1] += w * f.z;
-            C[2] += w * f.w;
-            T *= wave::broadcast(incl, 63u);
+        for (uint32_t c00 = 0; c00 < count; c00 += 64u * kRefCompositeBatch) {
+            load_batch(c00);
+#pragma unroll
+            for (uint32_t b = 0; b < kRefCompositeBatch; ++b) {
+                if (c00 + 64u * b >= count) break;  // uniform
+                const bool valid = c00 + 64u * b + lane < count;
+                const float4 f   = fb[b];
+                const float dt   = db[b];
+                const float a    = valid ? -expm1f(-(f.x * dt)) : 0.0f;
+                const float incl = wave::inclusive_product(1.0f - a);
+                const float excl = wave::shift_up1(incl, 1.0f);
+                const float w    = T * excl * a;
+                C[0] += w * f.y;
+                C[1] += w * f.z;
+                C[2] += w * f.w;
+                T *= wave::broadcast(incl, 63u);
+            }
         }
         const float4 g4    = gt[r];
         const float gtv[3] = {g4.x, g4.y, g4.z};
@@ -704,28 +722,33 @@ __global__ __launch_bounds__(256) void k_ref_composite_train(uint32_t n_rays_cap
         wave_loss += ray_loss;
         T = 1.0f;
         float carry[3] = {0.0f, 0.0f, 0.0f};
-        for (uint32_t c0 = 0; c0 < count; c0 += 64u) {
-            const uint32_t i  = c0 + lane;
-            const bool valid  = i < count;
-            const float4 f    = valid ? field[base + i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            const float dt    = valid ? fmaxf(samples[base + i].y, 0.0f) : 0.0f;
-            const float a     = valid ? -expm1f(-(f.x * dt)) : 0.0f;
-            const float incl  = wave::inclusive_product(1.0f - a);
-            float excl        = __shfl_up(incl, 1, 64);
-            excl              = lane == 0u ? 1.0f : excl;
-            const float w     = T * excl * a;
-            const float Tn    = T * incl;
-            const float c3[3] = {f.y, f.z, f.w};
-            float ds = 0.0f, dc[3];
+        for (uint32_t c00 = 0; c00 < count; c00 += 64u * kRefCompositeBatch) {
+            load_batch(c00);
 #pragma unroll
-            for (int c = 0; c < 3; ++c) {
-                const float prefix = carry[c] + wave::inclusive_sum(w * c3[c]);
-                ds += gr[c] * (Tn * c3[c] - (pred[c] - prefix));
-                dc[c]    = w * gr[c] * c3[c] * (1.0f - c3[c]);
-                carry[c] = wave::broadcast(prefix, 63u);
+            for (uint32_t b = 0; b < kRefCompositeBatch; ++b) {
+                const uint32_t c0 = c00 + 64u * b;
+                if (c0 >= count) break;  // uniform
+                const uint32_t i  = c0 + lane;
+                const bool valid  = i < count;
+                const float4 f    = fb[b];
+                const float dt    = db[b];
+                const float a     = valid ? -expm1f(-(f.x * dt)) : 0.0f;
+                const float incl  = wave::inclusive_product(1.0f - a);
+                const float excl  = wave::shift_up1(incl, 1.0f);
+                const float w     = T * excl * a;
+                const float Tn    = T * incl;
+                const float c3[3] = {f.y, f.z, f.w};
+                float ds = 0.0f, dc[3];
+#pragma unroll
+                for (int c = 0; c < 3; ++c) {
+                    const float prefix = carry[c] + wave::inclusive_sum(w * c3[c]);
+                    ds += gr[c] * (Tn * c3[c] - (pred[c] - prefix));
+                    dc[c]    = w * gr[c] * c3[c] * (1.0f - c3[c]);
+                    carry[c] = wave::broadcast(prefix, 63u);
+                }
+                if (valid) draw[base + i] = make_float4(dt * ds * -expm1f(-f.x), dc[0], dc[1], dc[2]);
+                T *= wave::broadcast(incl, 63u);
             }
-            if (valid) draw[base + i] = make_float4(dt * ds * -expm1f(-f.x), dc[0], dc[1], dc[2]);
-            T *= wave::broadcast(incl, 63u);
         }
     }
     if (lane == 0u) wsum[threadIdx.x >> 6] = wave_loss;

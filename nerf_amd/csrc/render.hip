@@ -195,8 +195,7 @@ __global__ __launch_bounds__(256) void k_uniform_composite(uint32_t ray0, uint32
             }
             const float al   = valid ? 1.0f - __expf(-(f.x * dt)) : 0.0f;
             const float incl = wave::inclusive_product(1.0f - al);
-            float excl       = __shfl_up(incl, 1, 64);
-            excl             = lane == 0u ? 1.0f : excl;
+            const float excl = wave::shift_up1(incl, 1.0f);
             const float w    = T * excl * al;
             cr += w * f.y;
             cg += w * f.z;
@@ -329,8 +328,7 @@ __global__ __launch_bounds__(256) void k_round_composite(const uint32_t* __restr
             }
             const float al      = valid ? 1.0f - __expf(-(f.x * dt)) : 0.0f;
             const float incl    = wave::inclusive_product(1.0f - al);
-            float excl          = __shfl_up(incl, 1, 64);
-            excl                = lane == 0u ? 1.0f : excl;
+            const float excl    = wave::shift_up1(incl, 1.0f);
             const uint64_t stop = __ballot(valid && T * incl < t_stop);
             const uint32_t last = stop ? (uint32_t)__ffsll((long long)stop) - 1u : 63u;
             const float w       = lane <= last ? T * excl * al : 0.0f;

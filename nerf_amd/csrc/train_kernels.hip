@@ -352,6 +352,8 @@ __global__ __launch_bounds__(256) void k_train_samples(TrainParams P, TrainDevSt
 // from the carried T times the exclusive product of (1 - alpha) across the
 // group; the backward pass forms the suffix S_i = pred - prefix_i from an
 // inclusive scan of w c, so both passes run front to back.
+constexpr uint32_t kCompositeBatch = 8u;  // groups of 64 samples loaded together per ray
+
 __global__ __launch_bounds__(256) void k_composite_train(TrainParams P, TrainDevState* S, const uint32_t* __restrict__ kept, const uint32_t* __restrict__ offsets, const float2* __restrict__ samples, const float4* __restrict__ field,
                                                           const float4* __restrict__ gt, float4* __restrict__ draw) {
     __shared__ float wsum[kWaves];
@@ -365,21 +367,38 @@ __global__ __launch_bounds__(256) void k_composite_train(TrainParams P, TrainDev
         const uint32_t count = kept[r];
         if (count == 0u) continue;
         const uint32_t base = offsets[r];
+        // The field and step of kCompositeBatch groups of 64 samples are
+        // loaded together before any of them is composited: a ray has only
+        // its own wave, so each load round trip is exposed.
+        float4 fb[kCompositeBatch];
+        float db[kCompositeBatch];
+        auto load_batch = [&](uint32_t c0) {
+#pragma unroll
+            for (uint32_t b = 0; b < kCompositeBatch; ++b) {
+                const uint32_t i = c0 + 64u * b + lane;
+                const bool valid = i < count;
+                fb[b]            = valid ? field[base + i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                db[b]            = valid ? fmaxf(samples[base + i].y, 0.0f) : 0.0f;
+            }
+        };
         float T = 1.0f, C[3] = {0.0f, 0.0f, 0.0f};
-        for (uint32_t c0 = 0; c0 < count; c0 += 64u) {
-            const uint32_t i = c0 + lane;
-            const bool valid = i < count;
-            const float4 f   = valid ? field[base + i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            const float dt   = valid ? fmaxf(samples[base + i].y, 0.0f) : 0.0f;
-            const float a    = valid ? 1.0f - __expf(-(f.x * dt)) : 0.0f;
-            const float incl = wave::inclusive_product(1.0f - a);
-            float excl       = __shfl_up(incl, 1, 64);
-            excl             = lane == 0u ? 1.0f : excl;
-            const float w    = T * excl * a;
-            C[0] += w * f.y;
-            C[1] += w * f.z;
-            C[2] += w * f.w;
-            T *= wave::broadcast(incl, 63u);
+        for (uint32_t c0 = 0; c0 < count; c0 += 64u * kCompositeBatch) {
+            load_batch(c0);
+#pragma unroll
+            for (uint32_t b = 0; b < kCompositeBatch; ++b) {
+                if (c0 + 64u * b >= count) break;  // uniform
+                const bool valid = c0 + 64u * b + lane < count;
+                const float4 f   = fb[b];
+                const float dt   = db[b];
+                const float a    = valid ? 1.0f - __expf(-(f.x * dt)) : 0.0f;
+                const float incl = wave::inclusive_product(1.0f - a);
+                const float excl = wave::shift_up1(incl, 1.0f);
+                const float w    = T * excl * a;
+                C[0] += w * f.y;
+                C[1] += w * f.z;
+                C[2] += w * f.w;
+                T *= wave::broadcast(incl, 63u);
+            }
         }
         const float4 g4    = gt[r];
         const float gtv[3] = {g4.x, g4.y, g4.z};
@@ -396,28 +415,33 @@ __global__ __launch_bounds__(256) void k_composite_train(TrainParams P, TrainDev
         wave_loss += ray_loss;
         T = 1.0f;
         float carry[3] = {0.0f, 0.0f, 0.0f};
-        for (uint32_t c0 = 0; c0 < count; c0 += 64u) {
-            const uint32_t i  = c0 + lane;
-            const bool valid  = i < count;
-            const float4 f    = valid ? field[base + i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            const float dt    = valid ? fmaxf(samples[base + i].y, 0.0f) : 0.0f;
-            const float a     = valid ? 1.0f - __expf(-(f.x * dt)) : 0.0f;
-            const float incl  = wave::inclusive_product(1.0f - a);
-            float excl        = __shfl_up(incl, 1, 64);
-            excl              = lane == 0u ? 1.0f : excl;
-            const float w     = T * excl * a;
-            const float Tn    = T * incl;
-            const float c3[3] = {f.y, f.z, f.w};
-            float ds = 0.0f, dc[3];
+        for (uint32_t c00 = 0; c00 < count; c00 += 64u * kCompositeBatch) {
+            load_batch(c00);
 #pragma unroll
-            for (int c = 0; c < 3; ++c) {
-                const float prefix = carry[c] + wave::inclusive_sum(w * c3[c]);
-                ds += gr[c] * (Tn * c3[c] - (pred[c] - prefix));
-                dc[c]    = w * gr[c] * c3[c] * (1.0f - c3[c]);
-                carry[c] = wave::broadcast(prefix, 63u);
+            for (uint32_t b = 0; b < kCompositeBatch; ++b) {
+                const uint32_t c0 = c00 + 64u * b;
+                if (c0 >= count) break;  // uniform
+                const uint32_t i  = c0 + lane;
+                const bool valid  = i < count;
+                const float4 f    = fb[b];
+                const float dt    = db[b];
+                const float a     = valid ? 1.0f - __expf(-(f.x * dt)) : 0.0f;
+                const float incl  = wave::inclusive_product(1.0f - a);
+                const float excl  = wave::shift_up1(incl, 1.0f);
+                const float w     = T * excl * a;
+                const float Tn    = T * incl;
+                const float c3[3] = {f.y, f.z, f.w};
+                float ds = 0.0f, dc[3];
+#pragma unroll
+                for (int c = 0; c < 3; ++c) {
+                    const float prefix = carry[c] + wave::inclusive_sum(w * c3[c]);
+                    ds += gr[c] * (Tn * c3[c] - (pred[c] - prefix));
+                    dc[c]    = w * gr[c] * c3[c] * (1.0f - c3[c]);
+                    carry[c] = wave::broadcast(prefix, 63u);
+                }
+                if (valid) draw[base + i] = make_float4(dt * f.x * ds, dc[0], dc[1], dc[2]);
+                T *= wave::broadcast(incl, 63u);
             }
-            if (valid) draw[base + i] = make_float4(dt * f.x * ds, dc[0], dc[1], dc[2]);
-            T *= wave::broadcast(incl, 63u);
         }
     }
     if (lane == 0u) wsum[threadIdx.x >> 6] = wave_loss;

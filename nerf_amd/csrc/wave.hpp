@@ -9,34 +9,51 @@ namespace wave {
 
 __device__ __forceinline__ uint32_t lane_id() { return threadIdx.x & 63u; }
 
-// Inclusive scans over the 64 lanes (Hillis-Steele, log2(64) = 6 steps).
+// Wave-wide scans and broadcasts on DPP lane moves (VALU only, no LDS round
+// trip): an inclusive scan is four row shifts (1, 2, 4, 8 lanes within each
+// row of 16) and two row broadcasts (lane 15 of a row into the next row,
+// lane 31 into rows 2 and 3); a lane whose source is outside its row keeps
+// the identity.  With __shfl_up each of the six steps was a ds_bpermute and
+// a wait (about 25 serial LDS round trips per 64-sample group in the
+// composite backward).  The association differs from a sequential product
+// or sum by rounding only.
+namespace dpp {
+constexpr int kRowShr1 = 0x111, kRowShr2 = 0x112, kRowShr4 = 0x114, kRowShr8 = 0x118;
+constexpr int kRowBcast15 = 0x142, kRowBcast31 = 0x143, kWaveShr1 = 0x138;
+template <int kCtrl, int kRowMask = 0xf>
+__device__ __forceinline__ float move(float v, float fill) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(fill), __float_as_int(v), kCtrl, kRowMask, 0xf, false));
+}
+}  // namespace dpp
+
 __device__ __forceinline__ float inclusive_sum(float v) {
-    const uint32_t lane = lane_id();
-#pragma unroll
-    for (uint32_t d = 1; d < 64u; d <<= 1) {
-        const float o = __shfl_up(v, d, 64);
-        if (lane >= d) v += o;
-    }
+    v += dpp::move<dpp::kRowShr1>(v, 0.0f);
+    v += dpp::move<dpp::kRowShr2>(v, 0.0f);
+    v += dpp::move<dpp::kRowShr4>(v, 0.0f);
+    v += dpp::move<dpp::kRowShr8>(v, 0.0f);
+    v += dpp::move<dpp::kRowBcast15, 0xa>(v, 0.0f);
+    v += dpp::move<dpp::kRowBcast31, 0xc>(v, 0.0f);
     return v;
 }
 
 __device__ __forceinline__ float inclusive_product(float v) {
-    const uint32_t lane = lane_id();
-#pragma unroll
-    for (uint32_t d = 1; d < 64u; d <<= 1) {
-        const float o = __shfl_up(v, d, 64);
-        if (lane >= d) v *= o;
-    }
+    v *= dpp::move<dpp::kRowShr1>(v, 1.0f);
+    v *= dpp::move<dpp::kRowShr2>(v, 1.0f);
+    v *= dpp::move<dpp::kRowShr4>(v, 1.0f);
+    v *= dpp::move<dpp::kRowShr8>(v, 1.0f);
+    v *= dpp::move<dpp::kRowBcast15, 0xa>(v, 1.0f);
+    v *= dpp::move<dpp::kRowBcast31, 0xc>(v, 1.0f);
     return v;
 }
 
-__device__ __forceinline__ float sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
+// The value of the lane below (lane 0: fill), e.g. an exclusive scan from an
+// inclusive one.
+__device__ __forceinline__ float shift_up1(float v, float fill) { return dpp::move<dpp::kWaveShr1>(v, fill); }
 
-__device__ __forceinline__ float broadcast(float v, uint32_t lane) { return __shfl(v, (int)lane, 64); }
+// `lane` must be the same on every lane of the wave.
+__device__ __forceinline__ float broadcast(float v, uint32_t lane) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), (int)lane)); }
+
+__device__ __forceinline__ float sum(float v) { return broadcast(inclusive_sum(v), 63u); }
 
 // Number of set bits of `mask` below this lane.
 __device__ __forceinline__ uint32_t rank_below(uint64_t mask) {
