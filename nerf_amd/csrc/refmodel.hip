@@ -160,13 +160,38 @@ __device__ __forceinline__ half8_t frag_load(const FragSrc& S, uint32_t f) {
 // address (4 g rows, sample s0 + s) is one VGPR; the uniform row 16 r + e
 // goes in the scalar offset and the tile in the immediate — with plain
 // pointers the compiler keeps a 64-bit address per row live and spills.
+//
+// put_quad stores a lane's four rows of one tile (rows 16 r + 4 g + e of
+// sample s0 + 16 t + s) as one 8-byte store per lane: a 4 x 4 transpose
+// across each quad of lanes (lanes s = 4 k + j, samples 16 t + 4 k + j)
+// leaves lane j with row 16 r + 4 g + j at samples 16 t + 4 k .. + 3.  Two
+// DPP swaps (lane j ^ 1, then j ^ 2), two byte permutes and two selects
+// replace four 2-byte stores (a quarter of the store instructions, each a
+// full wave of lane addresses for the address path).
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 struct RowStore {
     __amdgpu_buffer_rsrc_t rsrc;
     uint32_t vbase;  // bytes: (4 g np + s0 + s) * 2
     uint32_t np2;    // np * 2
     uint32_t row0;
+    uint32_t vquad;  // bytes: ((4 g + j) np + s0 + 4 k) * 2, s = 4 k + j
     __device__ __forceinline__ void put(uint32_t row_u, uint32_t t, half_t v) const {
         __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, v), rsrc, vbase + 32u * t, (row0 + row_u) * np2, 0);
+    }
+    __device__ __forceinline__ void put_quad(uint32_t row_u, uint32_t t, half4_t h) const {
+        constexpr int kSwap1 = 0xB1, kSwap2 = 0x4E;  // quad_perm [1, 0, 3, 2] and [2, 3, 0, 1]
+        const uint32_t j = threadIdx.x & 3u;
+        const uint32_t a = __builtin_bit_cast(uint32_t, half2_t{h[0], h[1]}), b = __builtin_bit_cast(uint32_t, half2_t{h[2], h[3]});
+        const uint32_t a1 = (uint32_t)__builtin_amdgcn_mov_dpp((int)a, kSwap1, 0xf, 0xf, false);
+        const uint32_t b1 = (uint32_t)__builtin_amdgcn_mov_dpp((int)b, kSwap1, 0xf, 0xf, false);
+        // Even lanes: (own, next) of their first row; odd lanes: (previous,
+        // own) of their second row.
+        const uint32_t sel = (j & 1u) ? 0x03020706u : 0x05040100u;
+        const uint32_t c = __builtin_amdgcn_perm(a1, a, sel), d = __builtin_amdgcn_perm(b1, b, sel);
+        const uint32_t c2 = (uint32_t)__builtin_amdgcn_mov_dpp((int)c, kSwap2, 0xf, 0xf, false);
+        const uint32_t d2 = (uint32_t)__builtin_amdgcn_mov_dpp((int)d, kSwap2, 0xf, 0xf, false);
+        const bool first  = j < 2u;
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2{first ? c : d2, first ? c2 : d}, rsrc, vquad + 32u * t, (row0 + row_u) * np2, 0);
     }
     __device__ __forceinline__ half_t get(uint32_t row_u, uint32_t t) const {
         return __builtin_bit_cast(half_t, __builtin_amdgcn_raw_buffer_load_b16(rsrc, vbase + 32u * t, (row0 + row_u) * np2, 0));
@@ -213,11 +238,9 @@ __device__ __forceinline__ void ref_hidden(const FragSrc& S, uint32_t f0, const 
             if (r & 1u) out[t][r >> 1] = half8_t{lo[t][0], lo[t][1], lo[t][2], lo[t][3], h[0], h[1], h[2], h[3]};
             else lo[t] = h;
             if constexpr (kStore) {
+                st.put_quad(16u * r, t, h);
 #pragma unroll
-                for (uint32_t e = 0; e < 4u; ++e) {
-                    st.put(16u * r + e, t, h[e]);
-                    mb[t] |= ((float)h[e] > 0.0f ? 1u : 0u) << (4u * r + e);
-                }
+                for (uint32_t e = 0; e < 4u; ++e) mb[t] |= ((float)h[e] > 0.0f ? 1u : 0u) << (4u * r + e);
             }
         }
         // One row block's weights in flight at a time: without the fence the
@@ -275,10 +298,8 @@ __device__ __forceinline__ void ref_backward_layer(const FragSrc& S, uint32_t f0
         for (uint32_t t = 0; t < 4u; ++t) {
             half4_t h;
 #pragma unroll
-            for (uint32_t e = 0; e < 4u; ++e) {
-                h[e] = ((mb[t] >> (4u * r + e)) & 1u) ? to_half_rne(acc[t][e]) : (half_t)0.0f;
-                dlt.put(16u * r + e, t, h[e]);
-            }
+            for (uint32_t e = 0; e < 4u; ++e) h[e] = ((mb[t] >> (4u * r + e)) & 1u) ? to_half_rne(acc[t][e]) : (half_t)0.0f;
+            dlt.put_quad(16u * r, t, h);
             if (r & 1u) out[t][r >> 1] = half8_t{lo[t][0], lo[t][1], lo[t][2], lo[t][3], h[0], h[1], h[2], h[3]};
             else lo[t] = h;
         }
@@ -428,8 +449,9 @@ __global__ __launch_bounds__(kBlockThreads) void k_ref_backward(const half8_t* _
     for (uint32_t gi = blockIdx.x * kBlockWaves + wv; gi < groups; gi += gridDim.x * kBlockWaves) {
         const uint32_t s0    = gi * 64u;
         const uint32_t vbase = (4u * g * np + s0 + s16) * 2u;
-        auto A = [&](uint32_t l) { return RowStore{ra, vbase, 2u * np, kActOff[l]}; };
-        auto D = [&](uint32_t l) { return RowStore{rd, vbase, 2u * np, kDltOff[l]}; };
+        const uint32_t vquad = ((4u * g + (s16 & 3u)) * np + s0 + (s16 & ~3u)) * 2u;
+        auto A = [&](uint32_t l) { return RowStore{ra, vbase, 2u * np, kActOff[l], vquad}; };
+        auto D = [&](uint32_t l) { return RowStore{rd, vbase, 2u * np, kDltOff[l], vquad}; };
         {
             const uint32_t q = min(s0 + lane, n - 1u);
             float p[3], d[3];
