@@ -55,6 +55,28 @@ def test_march_counts_bit_exact(w, h, steps):
         assert want.max() > 0
 
 
+@pytest.mark.parametrize("focal,steps", [(1.5, 64), (1.5, 1024), (20.0, 2), (20.0, 3), (20.0, 5)])
+def test_march_counts_both_step_chains(focal, steps):
+    """The march advances its shared t chain by a three-instruction form
+    only where a step that reaches t_far starts beyond t_far / 2 (cone <= 1/2,
+    dt_min <= t_far / 4), else by the reference's clamp: a 1.5-pixel focal
+    length (cone 2/3) and 2, 3 and 5 steps per ray cover both sides of those
+    bounds.  Counts bit-exact against the oracle's sequential recurrence."""
+    announce(f"march count, focal {focal} px, {steps} steps")
+    g, bits = _scene_setup()
+    w, h = 40, 30
+    for index in range(2):
+        cam = ext.camera_orbit(0, index, 1.32, CENTRE, w, h, focal)
+        occ = ext.occupancy_struct(bits, 128)
+        d_counts = DeviceArray((w * h,), np.uint32)
+        L.call("nerf_ext_march_count", byref(cam), byref(occ), steps, d_counts.ptr, None)
+        synchronize()
+        want = orc.march_count(orc.camera_from_bytes(bytes(cam)), bits.numpy(), 128, BOX, steps)
+        got = d_counts.numpy()
+        assert np.array_equal(got, want), f"view {index}: {np.count_nonzero(got != want)} rays differ"
+        assert want.max() > 0
+
+
 @pytest.mark.parametrize("w,h,views", [(24, 20, 1), (16, 12, 3)])
 def test_render_parity(w, h, views):
     announce(f"render {w}x{h} views={views}")
