@@ -628,6 +628,9 @@ template <int o>
 __device__ __forceinline__ uint32_t row_next_u(uint32_t v) {
     return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x100 + o, 0xF, 0xF, false);
 }
+// Value of lane i - 1 of the same 16-lane row (`fill` on the row's first
+// lane): DPP row_shr:1, a VALU move rather than an LDS round trip.
+__device__ __forceinline__ uint32_t row_prev_u(uint32_t v, uint32_t fill) { return (uint32_t)__builtin_amdgcn_update_dpp((int)fill, (int)v, 0x111, 0xF, 0xF, false); }
 
 template <int o>
 __device__ __forceinline__ void combine_step(float v[16], uint32_t seg) {
@@ -733,7 +736,7 @@ __global__ __launch_bounds__(kCoarseThreads) void k_coarse_scatter(TrainParams P
             if (__ballot(live && hi >= e0 && lo < e0 + ne) == 0ull) continue;  // uniform per wave
             // Cell key; dead lanes get a key no live lane has.
             const uint32_t kx = live ? c.i0[0] : 0xFFFFFFFFu, ky = c.i0[1], kz = c.i0[2];
-            const uint32_t px = __shfl_up(kx, 1, 16), py = __shfl_up(ky, 1, 16), pz = __shfl_up(kz, 1, 16);
+            const uint32_t px = row_prev_u(kx, ~0u), py = row_prev_u(ky, ~0u), pz = row_prev_u(kz, ~0u);
             const bool head      = s16 == 0u || kx != px || ky != py || kz != pz || !live;
             const uint64_t heads = __ballot(head);
             float v[16];
@@ -983,7 +986,7 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_pass(TrainParams P, GridPar
             const uint32_t e0 = (l - n_dense) * g.table_size;
             const LevelCell c = level_cell(p, N);
             const uint32_t kx = live ? c.i0[0] : 0xFFFFFFFFu, ky = c.i0[1], kz = c.i0[2];
-            const uint32_t px = __shfl_up(kx, 1, 16), py = __shfl_up(ky, 1, 16), pz = __shfl_up(kz, 1, 16);
+            const uint32_t px = row_prev_u(kx, ~0u), py = row_prev_u(ky, ~0u), pz = row_prev_u(kz, ~0u);
             const bool head   = s16 == 0u || kx != px || ky != py || kz != pz || !live;
             float v[16];
             if constexpr (kFill) {
