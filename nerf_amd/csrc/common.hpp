@@ -269,6 +269,80 @@ __device__ __forceinline__ void encode_level_xpair(const GridParams& g, const Ta
     }
 }
 
+// One hashed level of one point per lane, with the x-neighbour corners of
+// each point fetched by a lane pair (lanes 2k and 2k + 1 of a wave, every
+// lane active).  x's prime is 1, so corners x and x + 1 of a (y, z) edge
+// have entries i and i ^ (x ^ (x + 1)) = i ^ (2^(t+1) - 1), t the trailing
+// ones of x: one 128-byte line holds both unless x ends in five or more
+// ones (fp16 entries; four for fp32).  Load e of a lane reads corner 2e + h
+// (h = lane parity) of the even lane's point, load 4 + e the same corner of
+// the odd lane's point, so each load instruction asks for one line per
+// point where one lane per point asks for two; a quad_perm swap per edge
+// then hands each lane the other half of its own point's corners.  Same
+// entries, weights and summation order as encode_level.
+__device__ __forceinline__ uint32_t pair_swap(uint32_t v) { return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xf, 0xf, false); }  // quad_perm [1, 0, 3, 2]
+
+template <typename TableT>
+__device__ __forceinline__ void encode_level_lanepair(const GridParams& g, const TableT* __restrict__ table, const float p[3], uint32_t level, uint32_t N, float& a0, float& a1) {
+    constexpr uint32_t kWords = sizeof(TableT) == 4 ? 2u : 1u;  // dwords per entry
+    const LevelCell c = level_cell(p, N);
+    const bool odd    = (threadIdx.x & 1u) != 0u;
+    const uint32_t h  = odd ? 1u : 0u;
+    LevelCell ce, co;  // cells of the even and the odd lane's point
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+        const uint32_t other = pair_swap(c.i0[a]);
+        ce.i0[a]             = odd ? other : c.i0[a];
+        co.i0[a]             = odd ? c.i0[a] : other;
+    }
+    const uint32_t mask    = g.table_size - 1u;
+    const uint32_t* base   = reinterpret_cast<const uint32_t*>(table + (uint64_t)level * g.table_size * 2u);
+    uint32_t ve[4][kWords], vo[4][kWords];
+#pragma unroll
+    for (uint32_t e = 0; e < 4u; ++e) {
+        const uint32_t ie = corner_index(ce, 2u * e + h, N, false, mask);
+#pragma unroll
+        for (uint32_t w = 0; w < kWords; ++w) ve[e][w] = base[kWords * ie + w];
+    }
+#pragma unroll
+    for (uint32_t e = 0; e < 4u; ++e) {
+        const uint32_t io = corner_index(co, 2u * e + h, N, false, mask);
+#pragma unroll
+        for (uint32_t w = 0; w < kWords; ++w) vo[e][w] = base[kWords * io + w];
+    }
+    float v0[8], v1[8];
+#pragma unroll
+    for (uint32_t e = 0; e < 4u; ++e) {
+        uint32_t lo[kWords], hi[kWords];  // corners 2e and 2e + 1 of this lane's point
+#pragma unroll
+        for (uint32_t w = 0; w < kWords; ++w) {
+            const uint32_t recv = pair_swap(odd ? ve[e][w] : vo[e][w]);
+            const uint32_t own  = odd ? vo[e][w] : ve[e][w];
+            lo[w]               = odd ? recv : own;
+            hi[w]               = odd ? own : recv;
+        }
+        if constexpr (sizeof(TableT) == 4) {
+            v0[2u * e]      = __uint_as_float(lo[0]);
+            v1[2u * e]      = __uint_as_float(lo[kWords - 1u]);
+            v0[2u * e + 1u] = __uint_as_float(hi[0]);
+            v1[2u * e + 1u] = __uint_as_float(hi[kWords - 1u]);
+        } else {
+            v0[2u * e]      = (float)__builtin_bit_cast(half_t, (uint16_t)(lo[0] & 0xffffu));
+            v1[2u * e]      = (float)__builtin_bit_cast(half_t, (uint16_t)(lo[0] >> 16));
+            v0[2u * e + 1u] = (float)__builtin_bit_cast(half_t, (uint16_t)(hi[0] & 0xffffu));
+            v1[2u * e + 1u] = (float)__builtin_bit_cast(half_t, (uint16_t)(hi[0] >> 16));
+        }
+    }
+    a0 = 0.0f;
+    a1 = 0.0f;
+#pragma unroll
+    for (uint32_t k = 0; k < 8u; ++k) {
+        const float w = corner_weight(c, k);
+        a0            = a0 + w * v0[k];
+        a1            = a1 + w * v1[k];
+    }
+}
+
 // --------------------------------------------------------------- cameras
 struct Ray {
     float o[3];

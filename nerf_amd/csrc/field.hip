@@ -153,9 +153,14 @@ __global__ __launch_bounds__(kBlockThreads) void k_field_forward(GridParams g, c
 // another, so every load instruction of the wave reads one level for 64
 // consecutive samples (neighbouring samples share the lines of the coarse
 // levels within one instruction) and a level's dense/hashed branch is
-// uniform across the wave (dense levels take one load per x-neighbour
-// pair; hashed levels one load per corner: pairing their even-x corners as
-// the encode kernel does measured 11 % slower here).  The fp16 features go through LDS (rows of 80 bytes: 16-byte
+// uniform across the wave.  Dense levels take one load per x-neighbour
+// pair.  On hashed levels the two lanes of a pair fetch the x-neighbour
+// corners of one sample in the same load instruction (encode_level_lanepair:
+// one 128-byte line per sample where a lane per sample asks for two), which
+// halves the cache-line lookups of the fine levels, the kernel's bound
+// (800x800 render: field 81.9 -> 54.8 ms; pairing only the even-x corners
+// in one 8-byte load, as the encode kernel does, measured 11 % slower).
+// The fp16 features go through LDS (rows of 80 bytes: 16-byte
 // stores of four levels, 16-byte reads of lane group g's levels 4g..4g+3,
 // no bank conflicts) into the MLP's B-operand layout, four 16-sample tiles
 // per group; the SH coefficients go through LDS as in k_field_mlp.
@@ -207,7 +212,10 @@ __global__ __launch_bounds__(kBlockThreads) void k_field_forward_lv(GridParams g
             for (uint32_t j = 0; j < 4u; ++j) {
                 const uint32_t l = 4u * k + j;
                 float a0 = 0.0f, a1 = 0.0f;
-                if (l < g.n_levels) encode_level_xpair<TableT, false>(g, table, p, l, g.resolution[l], g.dense[l] != 0u, a0, a1);
+                if (l < g.n_levels) {
+                    if (g.dense[l] != 0u) encode_level_xpair<TableT, false>(g, table, p, l, g.resolution[l], true, a0, a1);
+                    else encode_level_lanepair<TableT>(g, table, p, l, g.resolution[l], a0, a1);
+                }
                 h[2u * j]      = to_half_rne(a0);
                 h[2u * j + 1u] = to_half_rne(a1);
             }

@@ -93,23 +93,33 @@ def test_field_forward(log2_t, dtype):
     assert_rel(d_o.numpy(), want, what="field forward", mlp=True)
 
 
-def test_field_forward_level_major_launch():
+@pytest.mark.parametrize("log2_t,dtype", [(19, L.NERF_EXT_F16), (17, L.NERF_EXT_F32)])
+def test_field_forward_level_major_launch(log2_t, dtype):
     # More than 2^20 points take the level-major field kernel (renders); the
-    # smaller launches above take the tile kernel.  Rows compared on a sample.
+    # smaller launches above take the tile kernel.  Rows compared with the
+    # oracle on a sample; the first 2^20 rows bit for bit with the tile
+    # kernel (the same fp32 feature sums in the oracle's order, the same MFMA
+    # chain), whatever lanes fetch which corners.
     n = (1 << 20) + 4099
-    announce(f"field forward level-major n={n}")
-    desc = ext.grid_desc(19, L.NERF_EXT_F16)
+    announce(f"field forward level-major n={n} log2_t={log2_t} dtype={dtype}")
+    desc = ext.grid_desc(log2_t, dtype)
     model = ext.Model.create(desc, seed=2, table_range=0.5)
     pos = points(n, seed=13)
     dirs = unit_dirs(n, seed=14)
     d_pos, d_dir, d_o = DeviceArray.from_numpy(pos), DeviceArray.from_numpy(dirs), DeviceArray((n, 4), np.float32)
     ms = model.struct()
     L.call("nerf_ext_field_forward", byref(ms), d_pos.ptr, d_dir.ptr, n, d_o.ptr, None)
+    d_tile = DeviceArray((1 << 20, 4), np.float32)
+    L.call("nerf_ext_field_forward", byref(ms), d_pos.ptr, d_dir.ptr, 1 << 20, d_tile.ptr, None)
     synchronize()
+    got = d_o.numpy()
     rows = np.unique(np.concatenate([np.random.default_rng(5).integers(0, n, 4000), np.arange(n - 70, n)]))
     dp, cp = host_params(model)
     want = orc.field_forward(oracle_grid(desc), host_table(model), dp, cp, np.ascontiguousarray(pos[rows]), np.ascontiguousarray(dirs[rows]))
-    assert_rel(d_o.numpy()[rows], want, what="field forward (level-major)", mlp=True)
+    assert_rel(got[rows], want, what="field forward (level-major)", mlp=True)
+    tile = d_tile.numpy()
+    diff = np.count_nonzero(got[: 1 << 20].view(np.uint32) != tile.view(np.uint32))
+    assert diff == 0, f"{diff} values differ between the level-major and the tile kernel"
 
 
 @pytest.mark.parametrize("n", [65536, 1000])
