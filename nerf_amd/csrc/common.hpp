@@ -269,12 +269,13 @@ __device__ __forceinline__ void encode_level_xpair(const GridParams& g, const Ta
     }
 }
 
-// One hashed level of one point per lane, with the x-neighbour corners of
-// each point fetched by a lane pair (lanes 2k and 2k + 1 of a wave, every
-// lane active).  x's prime is 1, so corners x and x + 1 of a (y, z) edge
-// have entries i and i ^ (x ^ (x + 1)) = i ^ (2^(t+1) - 1), t the trailing
-// ones of x: one 128-byte line holds both unless x ends in five or more
-// ones (fp16 entries; four for fp32).  Load e of a lane reads corner 2e + h
+// One level of one point per lane, with the x-neighbour corners of each
+// point fetched by a lane pair (lanes 2k and 2k + 1 of a wave, both active,
+// same level).  On a hashed level x's prime is 1, so corners x and x + 1 of
+// a (y, z) edge have entries i and i ^ (x ^ (x + 1)) = i ^ (2^(t+1) - 1), t
+// the trailing ones of x: one 128-byte line holds both unless x ends in five
+// or more ones (fp16 entries; four for fp32); on a dense level they are
+// adjacent entries.  Load e of a lane reads corner 2e + h
 // (h = lane parity) of the even lane's point, load 4 + e the same corner of
 // the odd lane's point, so each load instruction asks for one line per
 // point where one lane per point asks for two; a quad_perm swap per edge
@@ -283,7 +284,7 @@ __device__ __forceinline__ void encode_level_xpair(const GridParams& g, const Ta
 __device__ __forceinline__ uint32_t pair_swap(uint32_t v) { return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xf, 0xf, false); }  // quad_perm [1, 0, 3, 2]
 
 template <typename TableT>
-__device__ __forceinline__ void encode_level_lanepair(const GridParams& g, const TableT* __restrict__ table, const float p[3], uint32_t level, uint32_t N, float& a0, float& a1) {
+__device__ __forceinline__ void encode_level_lanepair(const GridParams& g, const TableT* __restrict__ table, const float p[3], uint32_t level, uint32_t N, bool dense, float& a0, float& a1) {
     constexpr uint32_t kWords = sizeof(TableT) == 4 ? 2u : 1u;  // dwords per entry
     const LevelCell c = level_cell(p, N);
     const bool odd    = (threadIdx.x & 1u) != 0u;
@@ -300,13 +301,13 @@ __device__ __forceinline__ void encode_level_lanepair(const GridParams& g, const
     uint32_t ve[4][kWords], vo[4][kWords];
 #pragma unroll
     for (uint32_t e = 0; e < 4u; ++e) {
-        const uint32_t ie = corner_index(ce, 2u * e + h, N, false, mask);
+        const uint32_t ie = corner_index(ce, 2u * e + h, N, dense, mask);
 #pragma unroll
         for (uint32_t w = 0; w < kWords; ++w) ve[e][w] = base[kWords * ie + w];
     }
 #pragma unroll
     for (uint32_t e = 0; e < 4u; ++e) {
-        const uint32_t io = corner_index(co, 2u * e + h, N, false, mask);
+        const uint32_t io = corner_index(co, 2u * e + h, N, dense, mask);
 #pragma unroll
         for (uint32_t w = 0; w < kWords; ++w) vo[e][w] = base[kWords * io + w];
     }

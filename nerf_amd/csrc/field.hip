@@ -214,7 +214,7 @@ __global__ __launch_bounds__(kBlockThreads) void k_field_forward_lv(GridParams g
                 float a0 = 0.0f, a1 = 0.0f;
                 if (l < g.n_levels) {
                     if (g.dense[l] != 0u) encode_level_xpair<TableT, false>(g, table, p, l, g.resolution[l], true, a0, a1);
-                    else encode_level_lanepair<TableT>(g, table, p, l, g.resolution[l], a0, a1);
+                    else encode_level_lanepair<TableT>(g, table, p, l, g.resolution[l], false, a0, a1);
                 }
                 h[2u * j]      = to_half_rne(a0);
                 h[2u * j + 1u] = to_half_rne(a1);

@@ -74,12 +74,17 @@ __global__ __launch_bounds__(256) void k_encode_tile(GridParams g, const TableT*
     __syncthreads();
     const uint32_t p = threadIdx.x & (kEncPoints - 1u), level = threadIdx.x / kEncPoints;
     const uint32_t width = 2u * g.n_levels;
-    if (p < count && level < g.n_levels) {
-        const float x[3] = {sp[3u * p], sp[3u * p + 1u], sp[3u * p + 2u]};
+    if (level < g.n_levels) {  // uniform over the 16 lanes of a level
+        // Lanes p and p ^ 1 fetch each other's x-neighbour corners
+        // (encode_level_lanepair), so lanes past the last point gather too.
+        const uint32_t pq = p < count ? p : count - 1u;
+        const float x[3]  = {sp[3u * pq], sp[3u * pq + 1u], sp[3u * pq + 2u]};
         float a0, a1;
-        encode_level(g, table, x, level, g.resolution[level], g.dense[level] != 0u, a0, a1);
-        store_value(&tile[p * width + 2u * level], a0);
-        store_value(&tile[p * width + 2u * level + 1u], a1);
+        encode_level_lanepair(g, table, x, level, g.resolution[level], g.dense[level] != 0u, a0, a1);
+        if (p < count) {
+            store_value(&tile[p * width + 2u * level], a0);
+            store_value(&tile[p * width + 2u * level + 1u], a1);
+        }
     }
     __syncthreads();
     OutT* o = out + (uint64_t)first * width;
@@ -96,10 +101,12 @@ __global__ __launch_bounds__(256) void k_encode_tile(GridParams g, const TableT*
 //     contiguous bytes of the output row instead of 16.
 // One point per thread (the launch gives every thread exactly one).  The
 // placement is a locality choice only: any workgroup-to-XCD mapping gives
-// the same result.  With kPair, x-neighbour corners that are adjacent
-// entries are fetched by one load (dense levels always; hashed levels for
-// even x).
-template <typename TableT, typename OutT, bool kPair, uint32_t kLevels>
+// the same result.  The x-neighbour corners of a dense level are adjacent
+// entries, fetched by one load; on a hashed level the lanes of a pair fetch
+// them for each other's points in one load instruction (one cache line per
+// point and edge; encode_level_lanepair), so every lane runs the gathers and
+// only lanes holding a point store.
+template <typename TableT, typename OutT, uint32_t kLevels>
 __global__ __launch_bounds__(256) void k_encode_split(GridParams g, const TableT* __restrict__ table, const float* __restrict__ pos, uint32_t n, OutT* __restrict__ out, bool nt) {
     constexpr uint32_t kParts = kLevels / 2u;  // XCDs sharing one level group
     const uint32_t xcd = blockIdx.x & 7u, group = xcd % (8u / kParts), part = xcd / (8u / kParts);
@@ -108,9 +115,9 @@ __global__ __launch_bounds__(256) void k_encode_split(GridParams g, const TableT
     if (l0 >= g.n_levels) return;  // uniform per workgroup
     const uint32_t width = 2u * g.n_levels;
     for (uint32_t blk = slot * kParts + part; blk * 256u < n; blk += slots * kParts) {
-        const uint32_t i = blk * 256u + threadIdx.x;
-        if (i >= n) break;
-        const float3 xp  = *reinterpret_cast<const float3*>(pos + 3ull * i);
+        const uint32_t i  = blk * 256u + threadIdx.x;
+        const uint32_t iq = i < n ? i : n - 1u;
+        const float3 xp   = *reinterpret_cast<const float3*>(pos + 3ull * iq);
         const float x[3] = {xp.x, xp.y, xp.z};
         float f[2u * kLevels];
 #pragma unroll
@@ -118,10 +125,11 @@ __global__ __launch_bounds__(256) void k_encode_split(GridParams g, const TableT
             const uint32_t l = l0 + j;
             f[2u * j] = f[2u * j + 1u] = 0.0f;
             if (l < g.n_levels) {
-                if constexpr (kPair) encode_level_xpair(g, table, x, l, g.resolution[l], g.dense[l] != 0u, f[2u * j], f[2u * j + 1u]);
-                else encode_level(g, table, x, l, g.resolution[l], g.dense[l] != 0u, f[2u * j], f[2u * j + 1u]);
+                if (g.dense[l] != 0u) encode_level_xpair(g, table, x, l, g.resolution[l], true, f[2u * j], f[2u * j + 1u]);
+                else encode_level_lanepair(g, table, x, l, g.resolution[l], false, f[2u * j], f[2u * j + 1u]);
             }
         }
+        if (i >= n) continue;
         OutT* o = out + (uint64_t)i * width + 2u * l0;
         if (l0 + kLevels <= g.n_levels) {  // uniform: every level of the group exists
             // 16-byte stores.  With nt (large launches) non-temporal: the
@@ -237,9 +245,9 @@ NERF_API NerfStatus nerf_ext_encode_forward(const NerfExtGridDesc* grid, const v
 #define NERF_ENC(TT, OT)                                                                                                   \
     do {                                                                                                                   \
         if (quad)                                                                                                          \
-            k_encode_split<TT, OT, true, 4u><<<grid_dim, 256, 0, st>>>(g, (const TT*)table, positions, n, (OT*)features, nt);  \
+            k_encode_split<TT, OT, 4u><<<grid_dim, 256, 0, st>>>(g, (const TT*)table, positions, n, (OT*)features, nt);  \
         else if (split)                                                                                                    \
-            k_encode_split<TT, OT, true, 2u><<<grid_dim, 256, 0, st>>>(g, (const TT*)table, positions, n, (OT*)features, nt);  \
+            k_encode_split<TT, OT, 2u><<<grid_dim, 256, 0, st>>>(g, (const TT*)table, positions, n, (OT*)features, nt);  \
         else                                                                                                               \
             k_encode_tile<TT, OT><<<grid_dim, 256, 0, st>>>(g, (const TT*)table, positions, n, (OT*)features);             \
     } while (0)

@@ -208,10 +208,13 @@ __device__ __forceinline__ void encode_quad(const GridParams& g, const TableT* _
         const uint32_t dn = grp == 0u ? g.dense[l0] : grp == 1u ? g.dense[l1] : grp == 2u ? g.dense[l2] : g.dense[l3];
         const uint32_t level = 4u * grp + j;
         float a0 = 0.0f, a1 = 0.0f;
-        // One load per corner: the lane groups of a wave hold dense and hashed
-        // levels at once, so the x-pair loads of encode_level_xpair would
-        // run both branches (measured 1.5x slower here).
-        if (level < g.n_levels) encode_level(g, table, p, level, N, dn != 0u, a0, a1);
+        // Lanes s and s ^ 1 of a lane group hold the same level of two
+        // points, so they fetch each point's x-neighbour corners together
+        // (one cache line per point and edge), dense and hashed levels alike:
+        // the lane groups of a wave hold both kinds at once, and the 8-byte
+        // x-pair loads of encode_level_xpair ran both branches (measured 1.5x
+        // slower than one load per corner).
+        if (level < g.n_levels) encode_level_lanepair(g, table, p, level, N, dn != 0u, a0, a1);
         feat[2u * j]      = a0;
         feat[2u * j + 1u] = a1;
     }
