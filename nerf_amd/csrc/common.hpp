@@ -444,8 +444,8 @@ hipError_t launch_ref_field(const half8_t* frags, const FieldInputs& in, uint32_
 // kRefDwChunk samples; kRefReduceBlocks squared-norm partials.
 constexpr uint32_t kRefActRows = 1136u, kRefDltRows = 1056u;
 constexpr uint32_t kRefDwChunk = 4096u;
-constexpr uint32_t kRefReduceBlocks = 128u;
 constexpr uint32_t kRefParams = NERF_EXT_REF_DENSITY_PARAMS + NERF_EXT_REF_COLOR_PARAMS;
+constexpr uint32_t kRefReduceBlocks = (kRefParams + 255u) / 256u;  // one parameter per thread
 constexpr uint32_t kRefMaxSamples = 1u << 20;  // per backward call: the buffers stay below 4 GiB (buffer-descriptor range)
 struct RefTrainLaunch {
     half8_t* frags;    // 64 x kRefFragments
