@@ -567,62 +567,110 @@ __global__ __launch_bounds__(kBlockThreads) void k_ref_backward(const half8_t* _
 
 // Weight gradients from the neuron-major buffers: dW_l[o][i] = sum over
 // samples of delta_l[o][s] input_l[i][s], the samples on the MFMA reduction
-// axis (A = delta rows, B = input rows, 32 samples per MFMA, 16-byte
-// fragment loads).  One wave per (64 x 64 tile of a layer, chunk of
-// samples), 4 x 4 blocks of 16 x 16 in registers: 16 MFMAs per 8 fragment
-// loads.  Each wave writes its tile's partial for its chunk; k_ref_dw_reduce
-// sums the chunks in order (deterministic).
-constexpr uint32_t kRefDwItems = 32u;  // sum over layers of ceil(n_out / 64) x ceil(n_in / 64)
-__device__ __forceinline__ uint32_t ref_dw_layer(uint32_t item, uint32_t& local) {
-    uint32_t l = 0u, first = 0u;
-#pragma unroll
-    for (uint32_t k = 0; k < 10u; ++k) {
-        const uint32_t nb = ((kRefLayers[k].n_out + 63u) / 64u) * ((kRefLayers[k].n_in + 63u) / 64u);
-        if (item >= first && item < first + nb) {
-            l     = k;
-            local = item - first;
-        }
-        first += nb;
-    }
-    return l;
-}
+// axis (A = delta rows, B = input rows, 32 samples per MFMA).  One workgroup
+// per (layer, chunk of samples): per step of 32 samples it stages the
+// layer's n_out delta rows and n_in input rows (64 bytes each, at most
+// 16 KiB) in LDS once, double-buffered, and its four waves multiply their
+// parts of the n_out x n_in product from there (a 128 x 128 layer: 64 x 64
+// per wave, 4 x 4 blocks of 16 x 16 in registers).  With one wave per 64 x 64
+// tile reading its rows from memory, every row was read once per tile row or
+// column of its layer (2.2 times on average; 415 us per 2^18 samples).  Each workgroup writes its
+// layer's partial for its chunk; k_ref_dw_reduce sums the chunks in order
+// (deterministic; the same MFMA sequence per block as one wave per tile).
+constexpr uint32_t kRefDwRows  = 256u;  // largest n_out + n_in
+constexpr uint32_t kRefDwStage = kRefDwRows * 64u;  // bytes per step of 32 samples
 
 // np is the row pitch of the buffers; with n_dev the rows hold
 // ceil(min(*n_dev, np) / 64) groups (the rest is stale) and later chunks
 // write zero partials.
 __global__ __launch_bounds__(kBlockThreads) void k_ref_dw(const half_t* __restrict__ acts, const half_t* __restrict__ dlts, uint32_t np, uint32_t chunk, uint32_t chunks, float* __restrict__ partial,
                                                           const uint32_t* __restrict__ n_dev) {
-    const uint32_t lane = threadIdx.x & 63u, g = lane >> 4, i = lane & 15u;
-    const uint32_t w = blockIdx.x * kBlockWaves + (threadIdx.x >> 6);
-    if (w >= kRefDwItems * chunks) return;
-    const uint32_t item = w % kRefDwItems, kc = w / kRefDwItems;
-    uint32_t local     = 0u;
-    const uint32_t l   = ref_dw_layer(item, local);
-    const RefLayer L   = kRefLayers[l];
-    const uint32_t ig_n = (L.n_in + 63u) / 64u, og = local / ig_n, ig = local - og * ig_n;
-    const uint32_t rb_n = min(4u, L.n_out / 16u - 4u * og), cb_n = min(4u, (L.n_in + 15u) / 16u - 4u * ig);  // uniform
+    __shared__ __align__(16) unsigned char stage[2][kRefDwStage];
+    const uint32_t lane = threadIdx.x & 63u, g = lane >> 4, i = lane & 15u, wv = threadIdx.x >> 6;
+    const uint32_t l = blockIdx.x % 10u, kc = blockIdx.x / 10u;
+    if (kc >= chunks) return;  // uniform per workgroup
+    const RefLayer L    = kRefLayers[l];
+    const uint32_t rows = L.n_out + L.n_in;  // staged rows: deltas, then inputs
+    const uint32_t rb_all = L.n_out / 16u, cb_all = L.n_in / 16u;
+    // This wave's blocks: rows split in halves and columns in halves (n_out
+    // 128), or columns in quarters (n_out 16).
+    uint32_t r0, nr, c0, nc;
+    if (rb_all >= 2u) {
+        nr = rb_all / 2u;
+        r0 = (wv >> 1) * nr;
+        const uint32_t half = (cb_all + 1u) / 2u;
+        c0 = (wv & 1u) * half;
+        nc = min(half, cb_all - c0);
+    } else {
+        nr = 1u;
+        r0 = 0u;
+        nc = cb_all / 4u;
+        c0 = wv * nc;
+    }
     const uint32_t n_used  = n_dev ? (min(*n_dev, np) + 63u) / 64u * 64u : np;
-    const uint32_t k_begin = kc * chunk, k_end = min(n_used, k_begin + chunk);
-    const half_t* a = dlts + (uint64_t)(kDltOff[l] + 64u * og + i) * np + 8u * g;
-    const half_t* b = acts + (uint64_t)(kActOff[l] + 64u * ig + i) * np + 8u * g;
-    const uint64_t blk = 16ull * np;  // next 16-row block
+    const uint32_t k_begin = min(kc * chunk, n_used), k_end = min(n_used, kc * chunk + chunk);
+    // Staging: thread t copies 16 bytes (8 samples) of row t / 4 + 64 j.
+    const uint32_t srow = threadIdx.x >> 2, spart = threadIdx.x & 3u;
+    auto row_ptr = [&](uint32_t r) -> const half_t* {
+        return r < L.n_out ? dlts + (uint64_t)(kDltOff[l] + r) * np : acts + (uint64_t)(kActOff[l] + r - L.n_out) * np;
+    };
+    // Two steps of loads in flight: the rows of step s + 2 are requested
+    // before step s is multiplied (one step ahead left the workgroups
+    // waiting on each step's loads: 385 us per 2^18 samples).
+    auto fetch = [&](half8_t (&h)[4], uint32_t k0) {
+#pragma unroll
+        for (uint32_t j = 0; j < 4u; ++j) {
+            const uint32_t r = srow + 64u * j;
+            if (r < rows) h[j] = *reinterpret_cast<const half8_t*>(row_ptr(r) + k0 + 8u * spart);
+        }
+    };
+    auto put = [&](const half8_t (&h)[4], uint32_t b) {
+#pragma unroll
+        for (uint32_t j = 0; j < 4u; ++j) {
+            const uint32_t r = srow + 64u * j;
+            if (r < rows) *reinterpret_cast<half8_t*>(&stage[b][r * 64u + 16u * spart]) = h[j];
+        }
+    };
     floatx4 acc[4][4];
 #pragma unroll
     for (uint32_t rb = 0; rb < 4u; ++rb)
 #pragma unroll
         for (uint32_t cb = 0; cb < 4u; ++cb) acc[rb][cb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-    for (uint32_t k0 = k_begin; k0 < k_end; k0 += 32u) {
+    // A fragment of block rb: delta row 16 (r0 + rb) + i, samples 8g..8g+7;
+    // B fragment of block cb: input row 16 (c0 + cb) + i.
+    auto multiply = [&](uint32_t b) {
         half8_t fa[4], fb[4];
 #pragma unroll
         for (uint32_t q = 0; q < 4u; ++q) {
-            fa[q] = q < rb_n ? *reinterpret_cast<const half8_t*>(a + q * blk + k0) : half8_t{0, 0, 0, 0, 0, 0, 0, 0};
-            fb[q] = q < cb_n ? *reinterpret_cast<const half8_t*>(b + q * blk + k0) : half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+            fa[q] = q < nr ? *reinterpret_cast<const half8_t*>(&stage[b][(16u * (r0 + q) + i) * 64u + 16u * g]) : half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+            fb[q] = q < nc ? *reinterpret_cast<const half8_t*>(&stage[b][(L.n_out + 16u * (c0 + q) + i) * 64u + 16u * g]) : half8_t{0, 0, 0, 0, 0, 0, 0, 0};
         }
 #pragma unroll
         for (uint32_t rb = 0; rb < 4u; ++rb)
 #pragma unroll
             for (uint32_t cb = 0; cb < 4u; ++cb)
-                if (rb < rb_n && cb < cb_n) acc[rb][cb] = mfma16x16x32(fa[rb], fb[cb], acc[rb][cb]);
+                if (rb < nr && cb < nc) acc[rb][cb] = mfma16x16x32(fa[rb], fb[cb], acc[rb][cb]);
+    };
+    half8_t ha[4], hb[4];
+    // Step s (of `steps`) is multiplied from stage[s & 1]; its successor's rows
+    // are in ha (s even) or hb (s odd) until they are put into the other buffer.
+    const uint32_t steps = (k_end - k_begin) / 32u;
+    if (steps > 0u) {
+        fetch(ha, k_begin);
+        put(ha, 0u);
+    }
+    if (steps > 1u) fetch(ha, k_begin + 32u);
+    __syncthreads();
+    for (uint32_t s = 0; s < steps; s += 2u) {  // two steps per trip: ha and hb swap roles
+        if (s + 2u < steps) fetch(hb, k_begin + 32u * (s + 2u));
+        multiply(0u);
+        if (s + 1u < steps) put(ha, 1u);
+        __syncthreads();
+        if (s + 1u >= steps) break;  // uniform
+        if (s + 3u < steps) fetch(ha, k_begin + 32u * (s + 3u));
+        multiply(1u);
+        if (s + 2u < steps) put(hb, 0u);
+        __syncthreads();
     }
     // C lane (g, i): rows 4g + e of the delta block, column i of the input block.
     float* dst = partial + (uint64_t)kc * (kRefDensityParams + kRefColorParams) + (L.network == 0u ? 0u : kRefDensityParams) + L.w_off;
@@ -630,10 +678,10 @@ __global__ __launch_bounds__(kBlockThreads) void k_ref_dw(const half_t* __restri
     for (uint32_t rb = 0; rb < 4u; ++rb)
 #pragma unroll
         for (uint32_t cb = 0; cb < 4u; ++cb) {
-            const uint32_t col = 64u * ig + 16u * cb + i;
-            if (rb < rb_n && cb < cb_n && col < L.n_in) {
+            if (rb < nr && cb < nc) {
+                const uint32_t col = 16u * (c0 + cb) + i;
 #pragma unroll
-                for (uint32_t e = 0; e < 4u; ++e) dst[(64u * og + 16u * rb + 4u * g + e) * L.n_in + col] = acc[rb][cb][e];
+                for (uint32_t e = 0; e < 4u; ++e) dst[(16u * (r0 + rb) + 4u * g + e) * L.n_in + col] = acc[rb][cb][e];
             }
         }
 }
@@ -843,7 +891,7 @@ hipError_t launch_ref_backward_train(const RefTrainLaunch& T, const FieldInputs&
     k_ref_backward<true><<<need < cap ? need : cap, kBlockThreads, 0, st>>>(T.frags, in, T.np, draw, loss_scale, T.acts, T.dlts, T.np);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    k_ref_dw<<<(kRefDwItems * T.chunks + kBlockWaves - 1u) / kBlockWaves, kBlockThreads, 0, st>>>(T.acts, T.dlts, T.np, kRefDwChunk, T.chunks, T.partial, in.n_dev);
+    k_ref_dw<<<10u * T.chunks, kBlockThreads, 0, st>>>(T.acts, T.dlts, T.np, kRefDwChunk, T.chunks, T.partial, in.n_dev);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     k_ref_dw_reduce<<<kRefReduceBlocks, 256, 0, st>>>(T.partial, T.chunks, grad, grad + kRefDensityParams, norm);
@@ -906,7 +954,7 @@ NERF_API NerfStatus nerf_ext_ref_backward(const uint16_t* density_params, const 
         e = hipGetLastError();
     }
     if (e == hipSuccess) {
-        k_ref_dw<<<(kRefDwItems * chunks + kBlockWaves - 1u) / kBlockWaves, kBlockThreads, 0, st>>>(acts, dlts, np, chunk, chunks, partial, nullptr);
+        k_ref_dw<<<10u * chunks, kBlockThreads, 0, st>>>(acts, dlts, np, chunk, chunks, partial, nullptr);
         e = hipGetLastError();
     }
     if (e == hipSuccess) {
