@@ -439,7 +439,7 @@ constexpr uint32_t kRefFragments = 444u;
 hipError_t ref_pack_weights(const half_t* dparams, const half_t* cparams, half8_t* frags, hipStream_t stream);
 hipError_t launch_ref_field(const half8_t* frags, const FieldInputs& in, uint32_t n, float4* out4, float4* raw4, hipStream_t stream);
 // Training of the reference model (the trainer's stages).  Rows of the
-// neuron-major fp16 buffers the backward writes per sample: every layer's
+// neuron-major fp16 buffers (blocks of 32 samples) the backward writes per sample: every layer's
 // input (acts) and output delta (dlts); weight-gradient partials per chunk of
 // kRefDwChunk samples; kRefReduceBlocks squared-norm partials.
 constexpr uint32_t kRefActRows = 1136u, kRefDltRows = 1056u;

@@ -71,7 +71,8 @@ constexpr RefTLayer kRefT[9] = {{9u, 8u, 1u, 232u, 0u}, {8u, 8u, 4u, 240u, 0u}, 
                                 {4u, 8u, 4u, 316u, 0u}, {3u, 8u, 4u, 348u, 0u}, {2u, 8u, 4u, 380u, 0u}, {1u, 8u, 4u, 412u, 0u}};
 static_assert(kRefT[8].frag0 + 32u == kRefFragments, "fragment count");
 
-// Rows of the neuron-major training buffers [row][np samples]: kActOff[l]
+// Rows of the neuron-major training buffers (fp16, in blocks of 32 samples:
+// row r of sample s at element (s / 32 * rows + r) * 32 + s % 32): kActOff[l]
 // is the input of layer l (the encoding, hidden activations, the colour
 // input [geometry 15 | direction encoding 27 | 0 x 6]); kDltOff[l] the delta
 // of layer l's output.  dW_l = delta_l x input_l^T over the samples.
@@ -154,12 +155,13 @@ __device__ __forceinline__ half8_t frag_load(const FragSrc& S, uint32_t f) {
 }
 
 // Where a training pass keeps a block of activations or deltas: the fp16
-// neuron-major buffer [row][np samples] through a buffer descriptor; rows
-// from `row0`, samples of this wave's group from s0; lane (g, s) of tile t
-// owns rows 16 r + 4 g + e of sample s0 + 16 t + s.  The lane's part of the
-// address (4 g rows, sample s0 + s) is one VGPR; the uniform row 16 r + e
-// goes in the scalar offset and the tile in the immediate — with plain
-// pointers the compiler keeps a 64-bit address per row live and spills.
+// neuron-major buffer (blocks of 32 samples) through a buffer descriptor;
+// rows from `row0`, samples of this wave's group from s0; lane (g, s) of
+// tile t owns rows 16 r + 4 g + e of sample s0 + 16 t + s.  The lane's part
+// of the address (4 g rows, sample s) is one VGPR; the uniform row 16 r + e
+// and block go in the scalar offset and the half block in the immediate —
+// with plain pointers the compiler keeps a 64-bit address per row live and
+// spills.
 //
 // put_quad stores a lane's four rows of one tile (rows 16 r + 4 g + e of
 // sample s0 + 16 t + s) as one 8-byte store per lane: a 4 x 4 transpose
@@ -169,14 +171,20 @@ __device__ __forceinline__ half8_t frag_load(const FragSrc& S, uint32_t f) {
 // replace four 2-byte stores (a quarter of the store instructions, each a
 // full wave of lane addresses for the address path).
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+// One block of a layer's rows is one contiguous run for k_ref_dw (rows at a
+// stride of the sample count, 64 bytes per row and step, read back more
+// slowly), and a group's stores land in two blocks.  A wave's group of 64 samples is blocks blk and blk + 1; tile t (16
+// samples) is half t & 1 of block blk + t / 2.
 struct RowStore {
     __amdgpu_buffer_rsrc_t rsrc;
-    uint32_t vbase;  // bytes: (4 g np + s0 + s) * 2
-    uint32_t np2;    // np * 2
+    uint32_t vbase;  // bytes: 4 g * 64 + s16 * 2
+    uint32_t tile;   // bytes of one block: rows * 64
     uint32_t row0;
-    uint32_t vquad;  // bytes: ((4 g + j) np + s0 + 4 k) * 2, s = 4 k + j
+    uint32_t vquad;  // bytes: (4 g + j) * 64 + 4 k * 2, s16 = 4 k + j
+    uint32_t blk;    // first block of the group
+    __device__ __forceinline__ uint32_t soff(uint32_t row_u, uint32_t t) const { return (row0 + row_u) * 64u + (blk + (t >> 1)) * tile; }
     __device__ __forceinline__ void put(uint32_t row_u, uint32_t t, half_t v) const {
-        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, v), rsrc, vbase + 32u * t, (row0 + row_u) * np2, 0);
+        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, v), rsrc, vbase + 32u * (t & 1u), soff(row_u, t), 0);
     }
     __device__ __forceinline__ void put_quad(uint32_t row_u, uint32_t t, half4_t h) const {
         constexpr int kSwap1 = 0xB1, kSwap2 = 0x4E;  // quad_perm [1, 0, 3, 2] and [2, 3, 0, 1]
@@ -191,10 +199,10 @@ struct RowStore {
         const uint32_t c2 = (uint32_t)__builtin_amdgcn_mov_dpp((int)c, kSwap2, 0xf, 0xf, false);
         const uint32_t d2 = (uint32_t)__builtin_amdgcn_mov_dpp((int)d, kSwap2, 0xf, 0xf, false);
         const bool first  = j < 2u;
-        __builtin_amdgcn_raw_buffer_store_b64(u32x2{first ? c : d2, first ? c2 : d}, rsrc, vquad + 32u * t, (row0 + row_u) * np2, 0);
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2{first ? c : d2, first ? c2 : d}, rsrc, vquad + 32u * (t & 1u), soff(row_u, t), 0);
     }
     __device__ __forceinline__ half_t get(uint32_t row_u, uint32_t t) const {
-        return __builtin_bit_cast(half_t, __builtin_amdgcn_raw_buffer_load_b16(rsrc, vbase + 32u * t, (row0 + row_u) * np2, 0));
+        return __builtin_bit_cast(half_t, __builtin_amdgcn_raw_buffer_load_b16(rsrc, vbase + 32u * (t & 1u), soff(row_u, t), 0));
     }
 };
 
@@ -429,8 +437,8 @@ __global__ __launch_bounds__(kBlockThreads) void k_ref_field(const half8_t* __re
 // MLP backward of the reference-model network for one batch (the forward is
 // recomputed, :784-909 semantics with fp32 accumulation).  Per 64-sample
 // group: the encoding and every layer's fp16 input go to `acts`, the fp16
-// deltas of every layer's output to `dlts` (neuron-major, np samples per
-// row) for k_ref_dw.  Output deltas: fp16(loss_scale x d raw) for colour
+// deltas of every layer's output to `dlts` (neuron-major in 32-sample
+// blocks) for k_ref_dw.  Output deltas: fp16(loss_scale x d raw) for colour
 // outputs 0..2; the geometry features' delta (colour input layer transposed,
 // rows shifted onto density outputs 1..15) and fp16(loss_scale x d raw
 // sigma) for the density outputs.  Samples past n get zero output deltas, so
@@ -447,11 +455,11 @@ __global__ __launch_bounds__(kBlockThreads) void k_ref_backward(const half8_t* _
     const uint32_t groups = (n + 63u) / 64u;
     const __amdgpu_buffer_rsrc_t ra = row_rsrc(acts, kActRows, np), rd = row_rsrc(dlts, kDltRows, np);
     for (uint32_t gi = blockIdx.x * kBlockWaves + wv; gi < groups; gi += gridDim.x * kBlockWaves) {
-        const uint32_t s0    = gi * 64u;
-        const uint32_t vbase = (4u * g * np + s0 + s16) * 2u;
-        const uint32_t vquad = ((4u * g + (s16 & 3u)) * np + s0 + (s16 & ~3u)) * 2u;
-        auto A = [&](uint32_t l) { return RowStore{ra, vbase, 2u * np, kActOff[l], vquad}; };
-        auto D = [&](uint32_t l) { return RowStore{rd, vbase, 2u * np, kDltOff[l], vquad}; };
+        const uint32_t s0    = gi * 64u, blk = gi * 2u;
+        const uint32_t vbase = 4u * g * 64u + s16 * 2u;
+        const uint32_t vquad = (4u * g + (s16 & 3u)) * 64u + (s16 & ~3u) * 2u;
+        auto A = [&](uint32_t l) { return RowStore{ra, vbase, kActRows * 64u, kActOff[l], vquad, blk}; };
+        auto D = [&](uint32_t l) { return RowStore{rd, vbase, kDltRows * 64u, kDltOff[l], vquad, blk}; };
         {
             const uint32_t q = min(s0 + lane, n - 1u);
             float p[3], d[3];
@@ -479,12 +487,12 @@ __global__ __launch_bounds__(kBlockThreads) void k_ref_backward(const half8_t* _
 #pragma unroll
             for (uint32_t k = 64u + 27u; k < 96u; ++k) row[k] = (half_t)0.0f;
             // Lane = sample: the encoding rows are stored one row per instruction.
-            const uint32_t vs = (s0 + lane) * 2u;
-            for (uint32_t k = 0; k < 64u; ++k) __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, row[k]), ra, vs, (kActOff[0] + k) * 2u * np, 0);
+            const uint32_t vs = (lane >> 5) * (kActRows * 64u) + (lane & 31u) * 2u, sb = blk * (kActRows * 64u);
+            for (uint32_t k = 0; k < 64u; ++k) __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, row[k]), ra, vs, (kActOff[0] + k) * 64u + sb, 0);
             // Colour input columns 15..41: the direction encoding; 42..47: zero.
             for (uint32_t k = 15u; k < 48u; ++k) {
                 const half_t v = k < 42u ? row[64u + (k - 15u)] : (half_t)0.0f;
-                __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, v), ra, vs, (kActOff[6] + k) * 2u * np, 0);
+                __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, v), ra, vs, (kActOff[6] + k) * 64u + sb, 0);
             }
         }
         __builtin_amdgcn_wave_barrier();
@@ -574,7 +582,9 @@ __global__ __launch_bounds__(kBlockThreads) void k_ref_backward(const half8_t* _
 // parts of the n_out x n_in product from there (a 128 x 128 layer: 64 x 64
 // per wave, 4 x 4 blocks of 16 x 16 in registers).  With one wave per 64 x 64
 // tile reading its rows from memory, every row was read once per tile row or
-// column of its layer (2.2 times on average; 415 us per 2^18 samples).  Each workgroup writes its
+// column of its layer (2.2 times on average; 415 us per 2^18 samples; 361 us
+// staged in LDS with rows at a stride of the sample count, 301 us with the
+// rows in 32-sample blocks, where a step's rows are two contiguous runs).  Each workgroup writes its
 // layer's partial for its chunk; k_ref_dw_reduce sums the chunks in order
 // (deterministic; the same MFMA sequence per block as one wave per tile).
 constexpr uint32_t kRefDwRows  = 256u;  // largest n_out + n_in
@@ -611,8 +621,10 @@ __global__ __launch_bounds__(kBlockThreads) void k_ref_dw(const half_t* __restri
     const uint32_t k_begin = min(kc * chunk, n_used), k_end = min(n_used, kc * chunk + chunk);
     // Staging: thread t copies 16 bytes (8 samples) of row t / 4 + 64 j.
     const uint32_t srow = threadIdx.x >> 2, spart = threadIdx.x & 3u;
-    auto row_ptr = [&](uint32_t r) -> const half_t* {
-        return r < L.n_out ? dlts + (uint64_t)(kDltOff[l] + r) * np : acts + (uint64_t)(kActOff[l] + r - L.n_out) * np;
+    // Row r of step k0 (a whole 32-sample block): the layer's delta rows, then
+    // its input rows, each set one contiguous run of the block.
+    auto row_ptr = [&](uint32_t r, uint32_t k0) -> const half_t* {
+        return r < L.n_out ? dlts + ((uint64_t)(k0 / 32u) * kDltRows + kDltOff[l] + r) * 32u : acts + ((uint64_t)(k0 / 32u) * kActRows + kActOff[l] + r - L.n_out) * 32u;
     };
     // Two steps of loads in flight: the rows of step s + 2 are requested
     // before step s is multiplied (one step ahead left the workgroups
@@ -621,7 +633,7 @@ __global__ __launch_bounds__(kBlockThreads) void k_ref_dw(const half_t* __restri
 #pragma unroll
         for (uint32_t j = 0; j < 4u; ++j) {
             const uint32_t r = srow + 64u * j;
-            if (r < rows) h[j] = *reinterpret_cast<const half8_t*>(row_ptr(r) + k0 + 8u * spart);
+            if (r < rows) h[j] = *reinterpret_cast<const half8_t*>(row_ptr(r, k0) + 8u * spart);
         }
     };
     auto put = [&](const half8_t (&h)[4], uint32_t b) {
