@@ -442,9 +442,13 @@ __global__ __launch_bounds__(kBlockThreads) void k_ref_field(const half8_t* __re
 // outputs 0..2; the geometry features' delta (colour input layer transposed,
 // rows shifted onto density outputs 1..15) and fp16(loss_scale x d raw
 // sigma) for the density outputs.  Samples past n get zero output deltas, so
-// all their deltas are zero.
+// all their deltas are zero.  Register budget for two waves per SIMD: left
+// to itself the compiler used 256 VGPRs and 27 AGPRs (one wave per SIMD);
+// capped, it spills 77 VGPRs to scratch and the pass still runs faster
+// (503 -> 476 us per 2^18 samples): with one wave nothing hides the weight
+// fragment, LDS and MFMA latencies of the layer chain.
 template <bool kFromSamples>
-__global__ __launch_bounds__(kBlockThreads) void k_ref_backward(const half8_t* __restrict__ frags, FieldInputs in, uint32_t n_cap, const float4* __restrict__ draw, float loss_scale, half_t* __restrict__ acts,
+__global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_ref_backward(const half8_t* __restrict__ frags, FieldInputs in, uint32_t n_cap, const float4* __restrict__ draw, float loss_scale, half_t* __restrict__ acts,
                                                                 half_t* __restrict__ dlts, uint32_t np) {
     __shared__ __align__(16) half_t rows[kBlockWaves][64 * kRefPitch];
     const uint32_t lane = threadIdx.x & 63u, g = lane >> 4, s16 = lane & 15u, wv = threadIdx.x >> 6;
