@@ -129,7 +129,7 @@ __global__ __launch_bounds__(kBlockThreads) void k_field_forward(GridParams g, c
         if constexpr (kFromSamples) {
             const uint32_t qs = in.sample_index ? in.sample_index[q] : q;
             dst               = in.sample_index ? qs : s;
-            sample_point(in, qs, in.sample_ray[qs], p, d);
+            sample_point(in, qs, in.sample_index && in.sample_index_ray ? in.sample_index_ray[q] : in.sample_ray[qs], p, d);
         } else {
 #pragma unroll
             for (int a = 0; a < 3; ++a) {

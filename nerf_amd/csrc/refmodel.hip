@@ -363,7 +363,7 @@ __global__ __launch_bounds__(kBlockThreads) void k_ref_field(const half8_t* __re
             if constexpr (kFromSamples) {
                 const uint32_t qs = in.sample_index ? in.sample_index[q] : q;
                 const float2 td   = in.samples[qs];
-                const uint32_t r  = in.sample_ray[qs];
+                const uint32_t r  = in.sample_index && in.sample_index_ray ? in.sample_index_ray[q] : in.sample_ray[qs];
                 const float4 ro = in.rays[2ull * r], rd = in.rays[2ull * r + 1ull];
                 d[0] = rd.x;
                 d[1] = rd.y;

@@ -8,12 +8,15 @@
 //   2. scan            exclusive prefix sum of counts -> sample offsets.
 //   3. k_march_samples eight lanes per ray: re-marches from the stored ray
 //                      record 8 steps at a time and writes the compacted
-//                      stream (t_mid, dt) + owning ray, ray-major, in
-//                      contiguous segments.
-//   4. field           fused hash encode + MFMA MLPs -> (sigma, r, g, b).
-//   5. k_composite     one wave per ray, front to back (:601-635) over groups
-//                      of 64 samples with early stop at T < min_transmittance,
-//                      background C + T * bg, RGBA8.
+//                      stream (t_mid, dt), ray-major, in contiguous segments.
+//   4. rounds          k_round_list lists the next slice of every active
+//                      ray's samples (step-major per group of 64 rays, each
+//                      entry with its ray), the fused field (hash encode +
+//                      MFMA MLPs -> sigma, r, g, b) shades the list, and
+//                      k_round_composite (one wave per active ray, front to
+//                      back, :601-635) composites it onto the ray's carried
+//                      (T, C), retiring rays at T < min_transmittance or at
+//                      the end of their samples: background C + T * bg, RGBA8.
 // The reference instead samples spp uniform steps per ray with no occupancy
 // test and no early stop (:534-600) and writes 28 B per step whether or not
 // the step is occupied.
@@ -85,11 +88,12 @@ __global__ void k_stage_camera(NerfExtCamera cam, NerfExtCamera* __restrict__ ds
 // sequence is bit-identical to the count pass and the occupied steps of each
 // run of 8 are written contiguously, so samples leave in 64-byte segments
 // instead of one 8-byte store per ray and step; k < count keeps every write
-// inside the ray's slice.
+// inside the ray's slice.  Only (t_mid, dt) is written: the round lists carry
+// each entry's ray to the field and composite passes.
 constexpr uint32_t kMarchGroup = 8u;
 
 __global__ __launch_bounds__(256) void k_march_samples(const NerfExtCamera* __restrict__ cams, uint32_t pixels_per_view, uint32_t ray0, uint32_t ray_end, OccView occ, uint32_t max_steps, const float4* __restrict__ rays,
-                                                      const uint32_t* __restrict__ counts, const uint32_t* __restrict__ offsets, float2* __restrict__ samples, uint32_t* __restrict__ sample_ray) {
+                                                      const uint32_t* __restrict__ counts, const uint32_t* __restrict__ offsets, float2* __restrict__ samples) {
     const uint32_t ray = ray0 + (blockIdx.x * 256u + threadIdx.x) / kMarchGroup;
     if (ray >= ray_end) return;
     const uint32_t count = counts[ray];
@@ -98,8 +102,7 @@ __global__ __launch_bounds__(256) void k_march_samples(const NerfExtCamera* __re
     const float cone    = cone_angle(cams[view]);
     const uint32_t base = offsets[ray];
     wave::march<kMarchGroup>(rays[2ull * ray], rays[2ull * ray + 1u], cone, max_steps, count, occ.bits, [&](const float p[3]) { return occ_cell(occ, p); }, [&](uint32_t k, float tm, float dt) {
-        samples[base + k]    = make_float2(tm, dt);
-        sample_ray[base + k] = ray;
+        samples[base + k] = make_float2(tm, dt);
     });
 }
 
@@ -771,15 +774,15 @@ NERF_API NerfStatus nerf_ext_render(NerfExtRenderer* R, const NerfExtRenderDesc*
         chunks.push_back(c);
     }
     NERF_HIP_TRY(R->samples.reserve(biggest));
-    NERF_HIP_TRY(R->sample_ray.reserve(biggest));
     NERF_HIP_TRY(R->field.reserve(biggest));
     NERF_HIP_TRY(R->qlist.reserve(biggest));
     NERF_HIP_TRY(R->qray.reserve(biggest));
 
+    // Every field launch of the rounds reads its entries' rays from the round
+    // list (qray), so the march writes no per-sample ray index.
     FieldInputs in{};
-    in.samples    = R->samples.ptr;
-    in.sample_ray = R->sample_ray.ptr;
-    in.rays       = R->rays.ptr;
+    in.samples = R->samples.ptr;
+    in.rays    = R->rays.ptr;
     for (int a = 0; a < 3; ++a) {  // the field's box is the outermost cascade's
         in.bmin[a] = occ.omin[a];
         in.bmax[a] = occ.omax[a];
@@ -820,8 +823,7 @@ NERF_API NerfStatus nerf_ext_render(NerfExtRenderer* R, const NerfExtRenderDesc*
         if (timed) NERF_HIP_TRY(hipEventRecord(R->ev[3], st));
         NERF_HIP_TRY(exclusive_scan_u32(R->counts.ptr + c.ray0, R->offsets.ptr + c.ray0, nr, R->scan_tmp.ptr, R->total.ptr, st));
         if (timed) NERF_HIP_TRY(hipEventRecord(R->ev[4], st));
-        k_march_samples<<<(nr + 256u / kMarchGroup - 1u) / (256u / kMarchGroup), 256, 0, st>>>(R->cams.ptr, ppv, c.ray0, c.ray_end, occ, d->max_steps, R->rays.ptr, R->counts.ptr, R->offsets.ptr, R->samples.ptr,
-                                                                                               R->sample_ray.ptr);
+        k_march_samples<<<(nr + 256u / kMarchGroup - 1u) / (256u / kMarchGroup), 256, 0, st>>>(R->cams.ptr, ppv, c.ray0, c.ray_end, occ, d->max_steps, R->rays.ptr, R->counts.ptr, R->offsets.ptr, R->samples.ptr);
         NERF_LAUNCH_CHECK("k_march_samples");
         if (timed) NERF_HIP_TRY(hipEventRecord(R->ev[5], st));
         uint32_t* n_cur = R->n_active.ptr;
