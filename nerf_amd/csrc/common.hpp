@@ -394,6 +394,11 @@ __device__ __forceinline__ bool pixel_ray(const NerfExtCamera& c, uint32_t pix, 
 
 // ------------------------------------------------------------ field eval
 // Where the fused field kernel gets its sample positions and directions.
+// Opacity of a render sample from the field's density (backend-cuda.cu
+// :601-635 with dt clamped at zero); the renderer's rounds take it from the
+// field pass.
+__device__ __forceinline__ float render_alpha(float sigma, float dt) { return 1.0f - __expf(-(sigma * fmaxf(dt, 0.0f))); }
+
 struct FieldInputs {
     // Mode A: explicit positions [n][3] and directions [n][3].
     const float* positions;
@@ -410,10 +415,13 @@ struct FieldInputs {
     // Optional (mode B): the j-th sample evaluated is stream sample
     // sample_index[j], and its output goes to out[sample_index[j]].
     const uint32_t* sample_index;
-    // Optional with sample_index (the level-major kernel): the owning ray of
-    // the j-th evaluated sample, read in order instead of sample_ray at a
-    // scattered stream index.
+    // Optional with sample_index: the owning ray of the j-th evaluated
+    // sample, read in order instead of sample_ray at a scattered stream index.
     const uint32_t* sample_index_ray;
+    // With sample_index (the renderer's rounds): output j goes to out[j] in
+    // evaluation order as (alpha, r, g, b), alpha = 1 - exp(-sigma max(dt, 0))
+    // with the sample's dt, instead of (sigma, r, g, b) at out[sample_index[j]].
+    bool alpha_in_order;
     // Mode B positions are world positions inside [bmin, bmax]; the grid
     // encodes the unit cube, so they are mapped by (p - bmin) / (bmax - bmin).
     float bmin[3];

@@ -32,9 +32,10 @@ using namespace mlp;
 
 namespace {
 
-// Position (normalised by the AABB) and direction of march sample q.
-__device__ __forceinline__ void sample_point(const FieldInputs& in, uint32_t q, uint32_t r, float p[3], float d[3]) {
+// Position (normalised by the AABB), direction and dt of march sample q.
+__device__ __forceinline__ void sample_point(const FieldInputs& in, uint32_t q, uint32_t r, float p[3], float d[3], float& dt) {
     const float2 td  = in.samples[q];
+    dt               = td.y;
     const float4 ro  = in.rays[2ull * r];
     const float4 rd  = in.rays[2ull * r + 1ull];
     d[0]             = rd.x;
@@ -124,12 +125,12 @@ __global__ __launch_bounds__(kBlockThreads) void k_field_forward(GridParams g, c
     for (uint32_t tile = first; tile < tiles; tile += 8u * per_xcd) {
         const uint32_t s = tile * 16u + s16;
         const uint32_t q = s < n ? s : n - 1u;
-        float p[3], d[3];
+        float p[3], d[3], dt = 0.0f;
         uint32_t dst = s;  // output slot
         if constexpr (kFromSamples) {
             const uint32_t qs = in.sample_index ? in.sample_index[q] : q;
-            dst               = in.sample_index ? qs : s;
-            sample_point(in, qs, in.sample_index && in.sample_index_ray ? in.sample_index_ray[q] : in.sample_ray[qs], p, d);
+            dst               = in.sample_index && !in.alpha_in_order ? qs : s;
+            sample_point(in, qs, in.sample_index && in.sample_index_ray ? in.sample_index_ray[q] : in.sample_ray[qs], p, d, dt);
         } else {
 #pragma unroll
             for (int a = 0; a < 3; ++a) {
@@ -143,7 +144,8 @@ __global__ __launch_bounds__(kBlockThreads) void k_field_forward(GridParams g, c
         if (in.features_out && s < n) *reinterpret_cast<half8_t*>(in.features_out + (uint64_t)s * 32u + 8u * grp) = x;
         const floatx4 o = density_mlp(fd, x);
         const floatx4 c = color_mlp(fc, color_input_dir(o, d, grp));
-        const float v   = field_channel(o, c, grp);
+        float v         = field_channel(o, c, grp);
+        if (kFromSamples && in.alpha_in_order && grp == 0u) v = render_alpha(v, dt);
         if (s < n) reinterpret_cast<float*>(out)[4ull * dst + grp] = v;
     }
 }
@@ -172,6 +174,7 @@ __global__ __launch_bounds__(kBlockThreads) void k_field_forward_lv(GridParams g
     __shared__ __align__(16) half_t sp[NERF_EXT_DENSITY_PARAMS + NERF_EXT_COLOR_PARAMS];
     __shared__ __align__(16) half_t feat[kBlockWaves][64 * kFeatPitch];
     __shared__ half4_t shl[kBlockWaves][64][4];
+    __shared__ float dts[kBlockWaves][64];  // dt per sample (alpha_in_order)
     stage_weights<kBlockThreads>(sp, dparams, cparams);
     __syncthreads();
     const uint32_t lane = threadIdx.x & 63u, grp = lane >> 4, s16 = lane & 15u, wv = threadIdx.x >> 6;
@@ -192,7 +195,9 @@ __global__ __launch_bounds__(kBlockThreads) void k_field_forward_lv(GridParams g
         if constexpr (kFromSamples) {
             const uint32_t qs = in.sample_index ? in.sample_index[q] : q;
             const uint32_t r  = in.sample_index && in.sample_index_ray ? in.sample_index_ray[q] : in.sample_ray[qs];
-            sample_point(in, qs, r, p, d);
+            float dt;
+            sample_point(in, qs, r, p, d, dt);
+            dts[wv][lane] = dt;
         } else {
 #pragma unroll
             for (int a = 0; a < 3; ++a) {
@@ -231,12 +236,13 @@ __global__ __launch_bounds__(kBlockThreads) void k_field_forward_lv(GridParams g
             const floatx4 o    = density_mlp(fd, x);
             const floatx4 c    = color_mlp(fc, color_input(o, shl[wv][row][grp], grp));
             v[t]               = field_channel(o, c, grp);
+            if (kFromSamples && in.alpha_in_order && grp == 0u) v[t] = render_alpha(v[t], dts[wv][row]);
         }
 #pragma unroll
         for (uint32_t t = 0; t < 4u; ++t) {
             const uint32_t st = gi * 64u + 16u * t + s16;
             if (st < n) {
-                const uint32_t dst = (kFromSamples && in.sample_index) ? in.sample_index[st] : st;
+                const uint32_t dst = (kFromSamples && in.sample_index && !in.alpha_in_order) ? in.sample_index[st] : st;
                 reinterpret_cast<float*>(out)[4ull * dst + grp] = v[t];
             }
         }

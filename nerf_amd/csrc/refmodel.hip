@@ -351,6 +351,7 @@ template <bool kFromSamples>
 __global__ __launch_bounds__(kBlockThreads) void k_ref_field(const half8_t* __restrict__ frags, FieldInputs in, uint32_t n_cap, float4* __restrict__ out, float4* __restrict__ raw_out) {
     const uint32_t n = in.n_dev ? min(*in.n_dev, n_cap) : n_cap;
     __shared__ __align__(16) half_t rows[kBlockWaves][64 * kRefPitch];
+    __shared__ float dts[kBlockWaves][64];  // dt per sample (alpha_in_order)
     const uint32_t lane = threadIdx.x & 63u, g = lane >> 4, s16 = lane & 15u, wv = threadIdx.x >> 6;
     half_t* R           = rows[wv];
     const FragSrc S     = frag_src(frags, lane);
@@ -365,6 +366,7 @@ __global__ __launch_bounds__(kBlockThreads) void k_ref_field(const half8_t* __re
                 const float2 td   = in.samples[qs];
                 const uint32_t r  = in.sample_index && in.sample_index_ray ? in.sample_index_ray[q] : in.sample_ray[qs];
                 const float4 ro = in.rays[2ull * r], rd = in.rays[2ull * r + 1ull];
+                dts[wv][lane] = td.y;
                 d[0] = rd.x;
                 d[1] = rd.y;
                 d[2] = rd.z;
@@ -423,10 +425,12 @@ __global__ __launch_bounds__(kBlockThreads) void k_ref_field(const half8_t* __re
             for (uint32_t t = 0; t < 4u; ++t) {
                 const uint32_t st = gi * 64u + 16u * t + s16;
                 if (st < n) {
-                    const uint32_t dst = (kFromSamples && in.sample_index) ? in.sample_index[st] : st;
+                    const bool in_order = kFromSamples && in.sample_index && in.alpha_in_order;
+                    const uint32_t dst  = (kFromSamples && in.sample_index && !in_order) ? in.sample_index[st] : st;
                     const float rs = (float)to_half_rne(dens[t][0]);
                     const float rr = (float)to_half_rne(col[t][0]), rg = (float)to_half_rne(col[t][1]), rb = (float)to_half_rne(col[t][2]);
-                    out[dst]           = make_float4(softplus_ref(rs), 1.0f / (1.0f + expf(-rr)), 1.0f / (1.0f + expf(-rg)), 1.0f / (1.0f + expf(-rb)));
+                    const float sigma  = softplus_ref(rs);
+                    out[dst]           = make_float4(in_order ? render_alpha(sigma, dts[wv][16u * t + s16]) : sigma, 1.0f / (1.0f + expf(-rr)), 1.0f / (1.0f + expf(-rg)), 1.0f / (1.0f + expf(-rb)));
                     if (raw_out) raw_out[dst] = make_float4(rs, rr, rg, rb);
                 }
             }

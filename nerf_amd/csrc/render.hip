@@ -13,10 +13,11 @@
 //                      ray's samples (step-major per group of 64 rays, each
 //                      entry with its ray), the fused field (hash encode +
 //                      MFMA MLPs -> sigma, r, g, b) shades the list, and
-//                      k_round_composite (one wave per active ray, front to
-//                      back, :601-635) composites it onto the ray's carried
-//                      (T, C), retiring rays at T < min_transmittance or at
-//                      the end of their samples: background C + T * bg, RGBA8.
+//                      k_round_composite (lane = ray, replaying the list
+//                      order, front to back, :601-635) composites the field's
+//                      (alpha, rgb) onto the ray's carried (T, C), retiring
+//                      rays at T < min_transmittance or at the end of their
+//                      samples: background C + T * bg, RGBA8.
 // The reference instead samples spp uniform steps per ray with no occupancy
 // test and no early stop (:534-600) and writes 28 B per step whether or not
 // the step is occupied.
@@ -302,53 +303,58 @@ __global__ __launch_bounds__(256) void k_round_list(const uint32_t* __restrict__
     }
 }
 
-// One wave per active ray: composite samples [S, min(count, S + K)) in
-// groups of 64 (transmittance = carried T x exclusive product of 1 - alpha;
-// the first sample after which T < t_stop is the last one composited), then
-// write the pixel or carry (T, C) into the next round and flag the slot in
-// keep (k_round_compact then lists the kept rays in slot order).
-__global__ __launch_bounds__(256) void k_round_composite(const uint32_t* __restrict__ list, const uint32_t* __restrict__ n_active, const uint32_t* __restrict__ counts, const uint32_t* __restrict__ offsets,
-                                                        const float2* __restrict__ samples, const float4* __restrict__ field, uint32_t S, uint32_t K, float t_stop, float3 bg, float4* __restrict__ state,
-                                                        uint32_t* __restrict__ rgba8, float* __restrict__ rgb_out, uint32_t* __restrict__ keep) {
+// One wave per group of 64 list slots (lane = slot), the grouping of
+// k_round_list: the field pass left the group's entries of this round in
+// the order k_round_list listed them (step by step, compacted by ballot) as
+// (alpha, r, g, b), so the lanes replay that order and each composites its
+// own ray front to back (backend-cuda.cu:601-635: w = T alpha, C += w c,
+// T *= 1 - alpha; the sample after which T < t_stop is the last one
+// composited) onto the (T, C) the ray carries between rounds.  Then the
+// pixel is written or (T, C) carried, and the slot flagged in keep
+// (k_round_compact then lists the kept rays in slot order).  The entries of
+// eight steps are loaded before they are composited; each load reads the
+// group's entries of one step, consecutive in the output.
+__global__ __launch_bounds__(256) void k_round_composite(const uint32_t* __restrict__ list, const uint32_t* __restrict__ n_active, const uint32_t* __restrict__ counts, uint32_t S, const uint32_t* __restrict__ cnt,
+                                                        const uint32_t* __restrict__ off, const float4* __restrict__ field, float t_stop, float3 bg, float4* __restrict__ state, uint32_t* __restrict__ rgba8,
+                                                        float* __restrict__ rgb_out, uint32_t* __restrict__ keep) {
     const uint32_t lane = threadIdx.x & 63u, nw = gridDim.x * 4u;
     const uint32_t n    = *n_active;
-    for (uint32_t a = blockIdx.x * 4u + (threadIdx.x >> 6); a < n; a += nw) {
-        const uint32_t ray   = list[a];
-        const uint32_t count = counts[ray];
-        const uint32_t base  = offsets[ray];
-        const uint32_t end   = min(count, S + K);
-        const float4 st0     = state[ray];
-        float T = st0.x, cr = 0.0f, cg = 0.0f, cb = 0.0f;
-        bool stopped = false;
-        for (uint32_t c0 = S; c0 < end; c0 += 64u) {
-            const uint32_t i = c0 + lane;
-            const bool valid = i < end;
-            float4 f         = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            float dt         = 0.0f;
-            if (valid) {
-                f  = field[base + i];
-                dt = fmaxf(samples[base + i].y, 0.0f);
+    for (uint32_t g = blockIdx.x * 4u + (threadIdx.x >> 6); g * 64u < n; g += nw) {
+        const uint32_t a   = g * 64u + lane;
+        const bool slot    = a < n;
+        const uint32_t m   = slot ? cnt[a] : 0u;
+        const uint32_t ray = slot ? list[a] : 0u;
+        const float4 st0   = slot ? state[ray] : make_float4(1.0f, 0.0f, 0.0f, 0.0f);
+        float T = st0.x, cr = st0.y, cg = st0.z, cb = st0.w;
+        bool stopped   = false;
+        uint32_t dst   = off[g * 64u];
+        uint32_t steps = m;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) steps = max(steps, (uint32_t)__shfl_xor((int)steps, o, 64));
+        constexpr uint32_t kBatch = 8u;
+        for (uint32_t i0 = 0; i0 < steps; i0 += kBatch) {
+            float4 f[kBatch];
+#pragma unroll
+            for (uint32_t k = 0; k < kBatch; ++k) {
+                const uint32_t i   = i0 + k;
+                const uint64_t act = __ballot(i < m);
+                f[k]               = i < m && !stopped ? field[dst + wave::rank_below(act)] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                dst += (uint32_t)__popcll(act);
             }
-            const float al      = valid ? 1.0f - __expf(-(f.x * dt)) : 0.0f;
-            const float incl    = wave::inclusive_product(1.0f - al);
-            const float excl    = wave::shift_up1(incl, 1.0f);
-            const uint64_t stop = __ballot(valid && T * incl < t_stop);
-            const uint32_t last = stop ? (uint32_t)__ffsll((long long)stop) - 1u : 63u;
-            const float w       = lane <= last ? T * excl * al : 0.0f;
-            cr += w * f.y;
-            cg += w * f.z;
-            cb += w * f.w;
-            T *= wave::broadcast(incl, last);
-            if (stop) {
-                stopped = true;
-                break;
+#pragma unroll
+            for (uint32_t k = 0; k < kBatch; ++k) {
+                if (i0 + k < m && !stopped) {
+                    const float w = T * f[k].x;
+                    cr += w * f[k].y;
+                    cg += w * f[k].z;
+                    cb += w * f[k].w;
+                    T *= 1.0f - f[k].x;
+                    stopped = T < t_stop;
+                }
             }
         }
-        cr = st0.y + wave::sum(cr);
-        cg = st0.z + wave::sum(cg);
-        cb = st0.w + wave::sum(cb);
-        const bool done = stopped || end >= count;
-        if (lane == 0u) {
+        if (slot) {
+            const bool done = stopped || S + m >= counts[ray];
             if (done) write_pixel(ray, cr, cg, cb, T, bg, rgba8, rgb_out);
             else state[ray] = make_float4(T, cr, cg, cb);
             keep[a] = done ? 0u : 1u;
@@ -815,6 +821,7 @@ NERF_API NerfStatus nerf_ext_render(NerfExtRenderer* R, const NerfExtRenderDesc*
     NERF_HIP_TRY(R->keep_total.reserve(1));
     in.sample_index     = R->qlist.ptr;
     in.sample_index_ray = R->qray.ptr;
+    in.alpha_in_order   = true;  // k_round_composite reads (alpha, rgb) in list order
 
     float ms_scan = 0.0f, ms_samples = 0.0f, field_ms = 0.0f;
     uint64_t shaded = 0;
@@ -851,7 +858,7 @@ NERF_API NerfStatus nerf_ext_render(NerfExtRenderer* R, const NerfExtRenderDesc*
             if (ref_model) NERF_HIP_TRY(launch_ref_field(R->ref_frags.ptr, in, (uint32_t)c.samples, R->field.ptr, nullptr, st));
             else NERF_HIP_TRY(launch_field(g, d->model->table, w, in, (uint32_t)c.samples, R->field.ptr, st));
             if (timed) NERF_HIP_TRY(hipEventRecord(R->fev[2u * r + 1u], st));
-            k_round_composite<<<ray_waves, 256, 0, st>>>(l_cur, n_cur, R->counts.ptr, R->offsets.ptr, R->samples.ptr, R->field.ptr, Ss[r], Ks[r], d->min_transmittance, bg, R->state.ptr, rgba8, rgb_f32, R->keep.ptr);
+            k_round_composite<<<ray_waves, 256, 0, st>>>(l_cur, n_cur, R->counts.ptr, Ss[r], R->cnt.ptr, R->off.ptr, R->field.ptr, d->min_transmittance, bg, R->state.ptr, rgba8, rgb_f32, R->keep.ptr);
             NERF_LAUNCH_CHECK("k_round_composite");
             NERF_HIP_TRY(exclusive_scan_u32(R->keep.ptr, R->koff.ptr, nr, R->scan_tmp.ptr, R->keep_total.ptr, st));
             k_round_compact<<<cblocks, 256, 0, st>>>(l_cur, n_cur, R->keep.ptr, R->koff.ptr, R->keep_total.ptr, l_nxt, n_nxt);
