@@ -227,11 +227,17 @@ constexpr uint32_t kTile = 4u;
 // Tile-major enumeration of the rays [ray0, ray_end) of equally sized views
 // of width W: rays are numbered ray = row * W + x over rows of all views;
 // thread t covers tile t / 16 (tile rows from row0_tile, tiles_x per row),
-// pixel (t % 16) of it.  Threads that map outside the range are idle.
+// pixel (t % 16) of it in Z order.  Threads that map outside the range are
+// idle.
 __device__ __forceinline__ bool tiled_ray(uint32_t t, uint32_t W, uint32_t tiles_x, uint32_t row0_tile, uint32_t ray0, uint32_t ray_end, uint32_t& ray) {
     const uint32_t tile = t / (kTile * kTile), in = t % (kTile * kTile);
-    const uint32_t x      = (tile % tiles_x) * kTile + in % kTile;
-    const uint64_t row    = (uint64_t)(row0_tile + tile / tiles_x) * kTile + in / kTile;
+    // Z order inside the tile: each lane quad is a 2 x 2 pixel block, so the
+    // samples of a quad (the unit the texture address path handles at once)
+    // more often share cache lines (field 51.0 -> 49.8 ms against row-major
+    // tiles; 8 x 8 Z-order tiles: 52.1 ms).
+    const uint32_t ix = ((in >> 1) & 1u) | (((in >> 3) & 1u) << 1), iy = (in & 1u) | (((in >> 2) & 1u) << 1);
+    const uint32_t x      = (tile % tiles_x) * kTile + ix;
+    const uint64_t row    = (uint64_t)(row0_tile + tile / tiles_x) * kTile + iy;
     const uint64_t r      = row * W + x;
     ray                   = (uint32_t)r;
     return x < W && r >= ray0 && r < ray_end;
