@@ -83,7 +83,6 @@ struct TrainBuffers {
     uint32_t* seg_seen;          // [max_rays][segs] occupied steps before the segment
     uint32_t* seg_reached;       // [max_rays] segments the march started
     uint32_t segs;               // ceil(max_steps / kSegSteps)
-    uint32_t* scan_tmp;
     float2* samples;             // [sample_cap] (t_mid, dt)
     uint32_t* sample_ray;        // [sample_cap]
     float4* field;               // [sample_cap] (sigma, r, g, b)

@@ -305,24 +305,40 @@ __global__ __launch_bounds__(256) void k_train_rays(TrainParams P, const TrainDe
 // samples fit under the capacity (its offset + count); unit (r, 0) records
 // the ray's kept count and the step totals.
 __global__ __launch_bounds__(256) void k_train_samples(TrainParams P, TrainDevState* S, const NerfExtCamera* __restrict__ cams, const uint32_t* __restrict__ bits, const float4* __restrict__ rays, const uint32_t* __restrict__ counts,
-                                                        const uint32_t* __restrict__ offsets, const float* __restrict__ seg_t, const uint32_t* __restrict__ seg_seen, const uint32_t* __restrict__ seg_reached, uint32_t segs,
+                                                        uint32_t* __restrict__ offsets, const float* __restrict__ seg_t, const uint32_t* __restrict__ seg_seen, const uint32_t* __restrict__ seg_reached, uint32_t segs,
                                                         uint32_t* __restrict__ kept,
                                                         float2* __restrict__ samples, uint32_t* __restrict__ sample_ray) {
     constexpr uint32_t kPer = 64u / kTrainGroup;
-    const uint32_t lane = threadIdx.x & 63u, stride = gridDim.x * kWaves * kPer;
-    const bool leader   = lane % kTrainGroup == 0u;
+    const uint32_t lane = threadIdx.x & 63u, stride = gridDim.x * kWaves * kPer, j = lane % kTrainGroup;
+    const bool leader   = j == 0u;
     const uint32_t n_rays = min(S->n_rays, P.max_rays);
     const float cone      = cone_of(cams[S->camera]);
     for (uint32_t r = blockIdx.x * blockDim.x + threadIdx.x; r < P.max_rays; r += gridDim.x * blockDim.x)
         if (r >= n_rays) kept[r] = 0u;
+    // Sum of counts[0, end) by the kTrainGroup lanes of a unit (every lane
+    // gets it): the ray's offset in the stream is the sum over the rays
+    // before it, computed where it is used (a step has a few hundred rays;
+    // a separate scan took two launches, about 9 us).
+    auto count_sum = [&](uint32_t end) {
+        uint32_t part = 0u;
+        for (uint32_t k = j; k < end; k += kTrainGroup) part += counts[k];
+#pragma unroll
+        for (uint32_t o = kTrainGroup / 2u; o > 0u; o >>= 1) part += (uint32_t)__shfl_xor((int)part, (int)o, (int)kTrainGroup);
+        return part;
+    };
+    if (blockIdx.x == 0u && threadIdx.x < kTrainGroup) {
+        const uint32_t total = count_sum(n_rays);  // occupied samples before the capacity cut
+        if (leader) S->total = total;
+    }
     const uint64_t units = (uint64_t)n_rays * segs;
     for (uint64_t u = (uint64_t)(blockIdx.x * kWaves + (threadIdx.x >> 6)) * kPer + lane / kTrainGroup; u < units; u += stride) {
         const uint32_t r = (uint32_t)(u / segs), sg = (uint32_t)(u % segs);
         const uint32_t count = counts[r];
-        const uint32_t base  = offsets[r];
+        const uint32_t base  = count_sum(r);
         const bool fits      = count > 0u && (uint64_t)base + count <= (uint64_t)P.sample_cap;
         if (sg == 0u && leader) {
-            kept[r] = fits ? count : 0u;
+            offsets[r] = base;
+            kept[r]    = fits ? count : 0u;
             if (fits) {
                 atomicMax(&S->n_samples, base + count);
                 atomicAdd(&S->n_active, 1u);
@@ -1423,8 +1439,6 @@ static hipError_t launch_train_stage_common(const TrainParams& P, const TrainBuf
     switch (stage) {
     case NERF_EXT_STAGE_SAMPLE: {
         k_train_rays<<<ray_wave_blocks(P.max_rays), 256, 0, st>>>(P, B.state, B.cams, B.images, B.bits, B.rays, B.gt, B.counts, B.seg_t, B.seg_seen, B.seg_reached, B.segs);
-        const hipError_t e = exclusive_scan_u32(B.counts, B.offsets, P.max_rays, B.scan_tmp, &B.state->total, st);
-        if (e != hipSuccess) return e;
         k_train_samples<<<ray_wave_blocks(P.max_rays * B.segs), 256, 0, st>>>(P, B.state, B.cams, B.bits, B.rays, B.counts, B.offsets, B.seg_t, B.seg_seen, B.seg_reached, B.segs, B.kept, B.samples,
                                                                               B.sample_ray);
         break;

@@ -130,7 +130,6 @@ NerfStatus trainer_create(const NerfExtTrainDesc* d, const BorrowedModel* borrow
     NERF_HIP_TRY(alloc(T, B.seg_t, (uint64_t)P.max_rays * B.segs));
     NERF_HIP_TRY(alloc(T, B.seg_seen, (uint64_t)P.max_rays * B.segs));
     NERF_HIP_TRY(alloc(T, B.seg_reached, P.max_rays));
-    NERF_HIP_TRY(alloc(T, B.scan_tmp, scan_tmp_words(P.max_rays)));
     NERF_HIP_TRY(alloc(T, B.samples, P.sample_cap));
     NERF_HIP_TRY(alloc(T, B.sample_ray, P.sample_cap));
     NERF_HIP_TRY(alloc(T, B.field, P.sample_cap));
