@@ -214,6 +214,18 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(half_t* buf, uint32_t
 // its fragments start at f0.  With kStore the fp16 outputs also go to st and
 // their ReLU masks to mrow[4 slot + t] (LDS): bit 4 r + e = (row 16 r + 4 g +
 // e of tile t > 0), the lane's 32 rows of one tile in one word.
+// max(x, 0) rounded to fp16: the accumulators are rounded (RNE), then the
+// negative halves cleared as 16-bit integers — fp16 bit patterns order like
+// signed integers (negative values, -0 included, are below +0), so a packed
+// integer max with 0 gives exactly fp16(max(x, 0)) for every non-NaN x (two
+// conversions and two packed maxima instead of four fp32 maxima and two
+// conversions).
+__device__ __forceinline__ half4_t relu_half4(const floatx4& a) {
+    typedef short short4_t __attribute__((ext_vector_type(4)));
+    const short4_t b = __builtin_bit_cast(short4_t, __builtin_convertvector(a, half4_t));
+    return __builtin_bit_cast(half4_t, __builtin_elementwise_max(b, short4_t{0, 0, 0, 0}));
+}
+
 template <uint32_t KB, bool kStore = false>
 __device__ __forceinline__ void ref_hidden(const FragSrc& S, uint32_t f0, const half8_t (&in)[4][4], half8_t (&out)[4][4], const RowStore& st = RowStore{}, uint32_t* mrow = nullptr, uint32_t slot = 0u) {
     uint32_t mb[4] = {0u, 0u, 0u, 0u};
@@ -242,7 +254,7 @@ __device__ __forceinline__ void ref_hidden(const FragSrc& S, uint32_t f0, const 
         // previous contents, which would keep those alive across the layer).
 #pragma unroll
         for (uint32_t t = 0; t < 4u; ++t) {
-            const half4_t h = half4_t{to_half_rne(fmaxf(acc[t][0], 0.0f)), to_half_rne(fmaxf(acc[t][1], 0.0f)), to_half_rne(fmaxf(acc[t][2], 0.0f)), to_half_rne(fmaxf(acc[t][3], 0.0f))};
+            const half4_t h = relu_half4(acc[t]);
             if (r & 1u) out[t][r >> 1] = half8_t{lo[t][0], lo[t][1], lo[t][2], lo[t][3], h[0], h[1], h[2], h[3]};
             else lo[t] = h;
             if constexpr (kStore) {
@@ -329,6 +341,42 @@ constexpr uint32_t kRefPitch = 104u;
 // Frequency encoding of v into row[0, 3 + 6 levels) as fp16.  The level loop
 // stays rolled (three sincos per iteration): unrolled, the scheduler
 // interleaves all of them and the kernel spills.
+// sin and cos of a frequency-encoding argument y = v 2^l (|y| < 2^10: world
+// coordinates within 1.5 x 2^9, directions within 2^3).  Cody-Waite
+// reduction: k = rint(2y / pi), r = y - k pi/2 with pi/2 split into three
+// fp32 parts (pi/2 = C1 + C2 + C3 + 1.1e-23); C1 has 24 bits and k < 2^10, so
+// the first fused step is exact and the residue r (|r| <= pi/4) carries about
+// one rounding.  sin r and cos r are the Taylor polynomials to r^9 and r^10
+// (truncation below 0.1 ulp on [-pi/4, pi/4]), then the quadrant k mod 4
+// picks and signs them.  Every float in (0, 1024): at most 1.49 ulp from the
+// correctly rounded sin and cos, and the fp16 rounding of the result differs
+// from that of the correctly rounded value for 2 in 10^5 arguments (ties the
+// fp32 error crosses).  The library sincosf spent about twice the
+// instructions (full-range reduction and a large-argument branch); the
+// encoding was a third of this kernel's vector instructions.
+__device__ __forceinline__ void freq_sincos(float y, float& s_out, float& c_out) {
+    constexpr float kTwoOverPi = 0x1.45f306p-1f;
+    constexpr float kC1 = 0x1.921fb6p+0f, kC2 = -0x1.777a5cp-25f, kC3 = -0x1.ee59dap-50f;
+    const float k = __builtin_rintf(y * kTwoOverPi);
+    float r       = __builtin_fmaf(-k, kC1, y);
+    r             = __builtin_fmaf(-k, kC2, r);
+    r             = __builtin_fmaf(-k, kC3, r);
+    const float z = r * r;
+    float ps      = __builtin_fmaf(z, 0x1.71de3ap-19f, -0x1.a01a02p-13f);  // 1/9!, -1/7!
+    ps            = __builtin_fmaf(z, ps, 0x1.111112p-7f);                 // 1/5!
+    ps            = __builtin_fmaf(z, ps, -0x1.555556p-3f);                // -1/3!
+    const float s = __builtin_fmaf(r * z, ps, r);
+    float pc      = __builtin_fmaf(z, -0x1.27e4fcp-22f, 0x1.a01a02p-16f);  // -1/10!, 1/8!
+    pc            = __builtin_fmaf(z, pc, -0x1.6c16c2p-10f);               // -1/6!
+    pc            = __builtin_fmaf(z, pc, 0x1.555556p-5f);                 // 1/4!
+    pc            = __builtin_fmaf(z, pc, -0.5f);
+    const float c = __builtin_fmaf(z, pc, 1.0f);
+    const int q   = (int)k;
+    const float a = (q & 1) ? c : s, b = (q & 1) ? s : c;
+    s_out         = (q & 2) ? -a : a;
+    c_out         = ((q + 1) & 2) ? -b : b;
+}
+
 __device__ __forceinline__ void freq_row(const float v[3], uint32_t levels, half_t* row) {
     row[0] = to_half_rne(v[0]);
     row[1] = to_half_rne(v[1]);
@@ -339,7 +387,7 @@ __device__ __forceinline__ void freq_row(const float v[3], uint32_t levels, half
 #pragma unroll
         for (uint32_t a = 0; a < 3u; ++a) {
             float s, c;
-            sincosf(v[a] * f, &s, &c);  // v * 2^l is exact
+            freq_sincos(v[a] * f, s, c);  // v * 2^l is exact
             row[3u + 6u * l + a]      = to_half_rne(s);
             row[3u + 6u * l + 3u + a] = to_half_rne(c);
         }
@@ -348,16 +396,16 @@ __device__ __forceinline__ void freq_row(const float v[3], uint32_t levels, half
 }
 
 template <bool kFromSamples>
-__global__ __launch_bounds__(kBlockThreads) void k_ref_field(const half8_t* __restrict__ frags, FieldInputs in, uint32_t n_cap, float4* __restrict__ out, float4* __restrict__ raw_out) {
+__global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_ref_field(const half8_t* __restrict__ frags, FieldInputs in, uint32_t n_cap, float4* __restrict__ out, float4* __restrict__ raw_out) {
     const uint32_t n = in.n_dev ? min(*in.n_dev, n_cap) : n_cap;
     __shared__ __align__(16) half_t rows[kBlockWaves][64 * kRefPitch];
-    __shared__ float dts[kBlockWaves][64];  // dt per sample (alpha_in_order)
     const uint32_t lane = threadIdx.x & 63u, g = lane >> 4, s16 = lane & 15u, wv = threadIdx.x >> 6;
     half_t* R           = rows[wv];
     const FragSrc S     = frag_src(frags, lane);
     const uint32_t groups = (n + 63u) / 64u;
     for (uint32_t gi = blockIdx.x * kBlockWaves + wv; gi < groups; gi += gridDim.x * kBlockWaves) {
         // Encoding: lane = sample.
+        float dt = 0.0f;  // the sample's interval (alpha_in_order)
         {
             const uint32_t q = min(gi * 64u + lane, n - 1u);
             float p[3], d[3];
@@ -366,7 +414,7 @@ __global__ __launch_bounds__(kBlockThreads) void k_ref_field(const half8_t* __re
                 const float2 td   = in.samples[qs];
                 const uint32_t r  = in.sample_index && in.sample_index_ray ? in.sample_index_ray[q] : in.sample_ray[qs];
                 const float4 ro = in.rays[2ull * r], rd = in.rays[2ull * r + 1ull];
-                dts[wv][lane] = td.y;
+                dt = td.y;
                 d[0] = rd.x;
                 d[1] = rd.y;
                 d[2] = rd.z;
@@ -419,22 +467,27 @@ __global__ __launch_bounds__(kBlockThreads) void k_ref_field(const half8_t* __re
         ref_hidden<4>(S, kRefLayers[8].frag0, x, y);
         floatx4 col[4];
         ref_output(S, kRefLayers[9].frag0, y, col);
-        // Lane group 0 holds raw outputs 0..3 of both networks.
+        // Lane group 0 holds raw outputs 0..3 of both networks; they pass
+        // through LDS (the rows are free until the next group's encoding) so
+        // that the activations run once per wave with lane = sample, not once
+        // per tile on a quarter of the lanes.
+        float4* RF = reinterpret_cast<float4*>(R);
         if (g == 0u) {
 #pragma unroll
-            for (uint32_t t = 0; t < 4u; ++t) {
-                const uint32_t st = gi * 64u + 16u * t + s16;
-                if (st < n) {
-                    const bool in_order = kFromSamples && in.sample_index && in.alpha_in_order;
-                    const uint32_t dst  = (kFromSamples && in.sample_index && !in_order) ? in.sample_index[st] : st;
-                    const float rs = (float)to_half_rne(dens[t][0]);
-                    const float rr = (float)to_half_rne(col[t][0]), rg = (float)to_half_rne(col[t][1]), rb = (float)to_half_rne(col[t][2]);
-                    const float sigma  = softplus_ref(rs);
-                    out[dst]           = make_float4(in_order ? render_alpha(sigma, dts[wv][16u * t + s16]) : sigma, 1.0f / (1.0f + expf(-rr)), 1.0f / (1.0f + expf(-rg)), 1.0f / (1.0f + expf(-rb)));
-                    if (raw_out) raw_out[dst] = make_float4(rs, rr, rg, rb);
-                }
-            }
+            for (uint32_t t = 0; t < 4u; ++t)
+                RF[16u * t + s16] = make_float4((float)to_half_rne(dens[t][0]), (float)to_half_rne(col[t][0]), (float)to_half_rne(col[t][1]), (float)to_half_rne(col[t][2]));
         }
+        __builtin_amdgcn_wave_barrier();
+        const float4 rv   = RF[lane];
+        const uint32_t st = gi * 64u + lane;
+        if (st < n) {
+            const bool in_order = kFromSamples && in.sample_index && in.alpha_in_order;
+            const uint32_t dst  = (kFromSamples && in.sample_index && !in_order) ? in.sample_index[st] : st;
+            const float sigma   = softplus_ref(rv.x);
+            out[dst]            = make_float4(in_order ? render_alpha(sigma, dt) : sigma, 1.0f / (1.0f + expf(-rv.y)), 1.0f / (1.0f + expf(-rv.z)), 1.0f / (1.0f + expf(-rv.w)));
+            if (raw_out) raw_out[dst] = rv;
+        }
+        __builtin_amdgcn_wave_barrier();  // the read completes before the next encoding rewrites the rows
     }
 }
 
