@@ -21,9 +21,10 @@
 //   * The first B operand is the hash encoding itself: lane (g, s) encodes
 //     levels 4g..4g+3 of sample s (features 8g..8g+7), straight into
 //     registers.
-//   * Weights are staged once per workgroup into LDS, then each wave keeps its
-//     A fragments in VGPRs (80 VGPRs for both networks) and loops over tiles
-//     of 16 samples (persistent grid).
+//   * The 20 A fragments of both networks (1 KiB each) are built once per
+//     workgroup.  The level-major render kernel keeps them in VGPRs (80 per
+//     lane); the tile kernel and the MLP pass keep them in LDS in lane order
+//     and read each where it is used (one conflict-free 16-byte read).
 #include "mlp_device.hpp"
 
 namespace nerf_hip {
@@ -51,6 +52,56 @@ __device__ __forceinline__ half8_t color_input_dir(const floatx4 o, const float 
     float sh[4];
     sh4_quad(d, grp, sh);
     return color_input(o, half4_t{(half_t)sh[0], (half_t)sh[1], (half_t)sh[2], (half_t)sh[3]}, grp);
+}
+
+constexpr uint32_t kGroupSamples = 64u;
+constexpr uint32_t kFieldFrags   = 20u;  // density w1[4] w2[2], colour w1[4] w2[8] w3[2]
+constexpr uint32_t kMlpWaves     = 4u;   // waves per SIMD the register budget is built for
+
+// Fragment f of the two MLPs for lane `lane`, read from the global parameters
+// element by element (any alignment); same values as load_density /
+// load_color give from the staged copy.
+__device__ half8_t mlp_fragment(const half_t* __restrict__ dp, const half_t* __restrict__ cp, uint32_t f, uint32_t lane) {
+    const uint32_t i = lane & 15u;
+    if (f < 4u) return load_a(dp, 32u, f, 0u, KMap::Identity, lane);
+    if (f < 6u) return load_a(dp + 2048, 64u, 0u, f - 4u, KMap::Hidden, lane);
+    if (f < 10u) return load_a(cp, 32u, f - 6u, 0u, KMap::ColorIn, lane);
+    if (f < 18u) return load_a(cp + 2048, 64u, (f - 10u) >> 1, (f - 10u) & 1u, KMap::Hidden, lane);
+    // Colour output: row 4c (c = 1..3) of the MFMA computes colour c - 1,
+    // every other row is zero (see load_color).
+    const bool used = (i & 3u) == 0u && i != 0u;
+    const half8_t v = load_a(cp + 2048 + 4096 + (used ? (i / 4u - 1u) : 0u) * 64u, 64u, 0u, f - 18u, KMap::Hidden, lane & 48u);
+    const half8_t z = {};
+    return used ? v : z;
+}
+
+// The MLPs of one 16-sample tile with the 20 fragments in LDS in lane order
+// (W = &frag[0][0] + lane): density 32 -> 64 -> 16 from the encoding x, then
+// colour [geo | SH] -> 64 -> 64 -> 16 from the colour input that xc_of builds
+// out of the density outputs.  Same products and order as density_mlp /
+// color_mlp on register fragments.
+template <typename ColorIn>
+__device__ __forceinline__ void tile_mlp(const half8_t* W, const half8_t x, ColorIn xc_of, floatx4& o, floatx4& c) {
+    const floatx4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+    half4_t h[4], h2[4];
+#pragma unroll
+    for (uint32_t b = 0; b < 4u; ++b) h[b] = relu_half(mfma16x16x32(W[64u * b], x, zero));
+    o                = mfma16x16x32(W[64u * 5u], cat(h[2], h[3]), mfma16x16x32(W[64u * 4u], cat(h[0], h[1]), zero));
+    const half8_t xc = xc_of(o);
+#pragma unroll
+    for (uint32_t b = 0; b < 4u; ++b) h[b] = relu_half(mfma16x16x32(W[64u * (6u + b)], xc, zero));
+#pragma unroll
+    for (uint32_t b = 0; b < 4u; ++b) h2[b] = relu_half(mfma16x16x32(W[64u * (11u + 2u * b)], cat(h[2], h[3]), mfma16x16x32(W[64u * (10u + 2u * b)], cat(h[0], h[1]), zero)));
+    c = mfma16x16x32(W[64u * 19u], cat(h2[2], h2[3]), mfma16x16x32(W[64u * 18u], cat(h2[0], h2[1]), zero));
+}
+
+// Fragment base for this lane, through an opaque offset: with a visible lane
+// index the compiler hoists all 20 fragment reads out of the sample loop
+// into 80 VGPRs, which is what keeping them in LDS avoids.
+__device__ __forceinline__ const half8_t* lane_frags(const half8_t (&frag)[kFieldFrags][kWaveSize], uint32_t lane) {
+    uint32_t lo = lane;
+    asm volatile("" : "+v"(lo));
+    return &frag[0][0] + lo;
 }
 
 // ---------------------------------------------------------------- kernels
@@ -102,18 +153,18 @@ __global__ __launch_bounds__(kBlockThreads) void k_density_forward(GridParams g,
 }
 
 // Full field: sigma, rgb per sample.  Inputs either explicit (positions,
-// directions) or march samples (t_mid, dt, ray) with per-ray o, d.
+// directions) or march samples (t_mid, dt, ray) with per-ray o, d.  The
+// weight fragments stay in LDS (84 VGPRs instead of 157): on a training
+// batch (2^18 samples, one ray's consecutive samples per tile) the gathers
+// of a tile then get more registers in flight, 75 -> 71 us at the same 3
+// workgroups per CU.
 template <typename TableT, bool kFromSamples>
 __global__ __launch_bounds__(kBlockThreads) void k_field_forward(GridParams g, const TableT* __restrict__ table, const half_t* __restrict__ dparams, const half_t* __restrict__ cparams, FieldInputs in, uint32_t n_cap, float4* __restrict__ out) {
     const uint32_t n = in.n_dev ? min(*in.n_dev, n_cap) : n_cap;
-    __shared__ __align__(16) half_t sp[NERF_EXT_DENSITY_PARAMS + NERF_EXT_COLOR_PARAMS];
-    stage_weights<kBlockThreads>(sp, dparams, cparams);
-    __syncthreads();
+    __shared__ __align__(16) half8_t frag[kFieldFrags][kWaveSize];
     const uint32_t lane = threadIdx.x & 63u, grp = lane >> 4, s16 = lane & 15u;
-    DensityFrags fd;
-    ColorFrags fc;
-    load_density(sp, fd, lane);
-    load_color(sp + NERF_EXT_DENSITY_PARAMS, fc, lane);
+    for (uint32_t f = threadIdx.x >> 6; f < kFieldFrags; f += kBlockWaves) frag[f][lane] = mlp_fragment(dparams, cparams, f, lane);
+    __syncthreads();
     // Round r covers tiles [r * W, (r + 1) * W) of the stream (W = all waves),
     // XCD x (workgroups b with b % 8 == x) taking the x-th eighth of it, so
     // a ray's consecutive tiles share one XCD's L2 while the whole device
@@ -142,9 +193,9 @@ __global__ __launch_bounds__(kBlockThreads) void k_field_forward(GridParams g, c
         encode_quad(g, table, p, grp, feat);
         const half8_t x = to_half8(feat);
         if (in.features_out && s < n) *reinterpret_cast<half8_t*>(in.features_out + (uint64_t)s * 32u + 8u * grp) = x;
-        const floatx4 o = density_mlp(fd, x);
-        const floatx4 c = color_mlp(fc, color_input_dir(o, d, grp));
-        float v         = field_channel(o, c, grp);
+        floatx4 o, c;
+        tile_mlp(lane_frags(frag, lane), x, [&](const floatx4& od) { return color_input_dir(od, d, grp); }, o, c);
+        float v = field_channel(o, c, grp);
         if (kFromSamples && in.alpha_in_order && grp == 0u) v = render_alpha(v, dt);
         if (s < n) reinterpret_cast<float*>(out)[4ull * dst + grp] = v;
     }
@@ -265,27 +316,6 @@ __global__ __launch_bounds__(kBlockThreads) void k_field_forward_lv(GridParams g
 // costs 80 VGPRs per lane and limits the pass to 3 waves per SIMD; this way
 // it runs 4 (2^24 samples: 434 vs 445 us; 2^18: 12.4 vs 17.7 us, where
 // staging the weights once per workgroup dominated), with identical results.
-constexpr uint32_t kGroupSamples = 64u;
-constexpr uint32_t kFieldFrags   = 20u;  // density w1[4] w2[2], colour w1[4] w2[8] w3[2]
-constexpr uint32_t kMlpWaves     = 4u;   // waves per SIMD the register budget is built for
-
-// Fragment f of the two MLPs for lane `lane`, read from the global parameters
-// element by element (any alignment); same values as load_density /
-// load_color give from the staged copy.
-__device__ half8_t mlp_fragment(const half_t* __restrict__ dp, const half_t* __restrict__ cp, uint32_t f, uint32_t lane) {
-    const uint32_t i = lane & 15u;
-    if (f < 4u) return load_a(dp, 32u, f, 0u, KMap::Identity, lane);
-    if (f < 6u) return load_a(dp + 2048, 64u, 0u, f - 4u, KMap::Hidden, lane);
-    if (f < 10u) return load_a(cp, 32u, f - 6u, 0u, KMap::ColorIn, lane);
-    if (f < 18u) return load_a(cp + 2048, 64u, (f - 10u) >> 1, (f - 10u) & 1u, KMap::Hidden, lane);
-    // Colour output: row 4c (c = 1..3) of the MFMA computes colour c - 1,
-    // every other row is zero (see load_color).
-    const bool used = (i & 3u) == 0u && i != 0u;
-    const half8_t v = load_a(cp + 2048 + 4096 + (used ? (i / 4u - 1u) : 0u) * 64u, 64u, 0u, f - 18u, KMap::Hidden, lane & 48u);
-    const half8_t z = {};
-    return used ? v : z;
-}
-
 __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(kMlpWaves, 8))) void k_field_mlp(const half_t* __restrict__ dparams, const half_t* __restrict__ cparams, const half_t* __restrict__ features,
                                                                                                                   const float* __restrict__ dirs, uint32_t n, float4* __restrict__ out) {
     __shared__ __align__(16) half8_t frag[kFieldFrags][kWaveSize];
@@ -376,12 +406,15 @@ hipError_t launch_field(const GridParams& g, const void* table, const FieldWeigh
     // Renders (more than 2^20 samples) take the level-major kernel, 3
     // workgroups per CU (its LDS and register budget); training-sized
     // batches the tile kernel, whose 16-sample tiles leave a shorter tail
-    // when a launch is only one or two rounds of work (2^18 samples: 84 vs
-    // 115 us; 800x800 render: 119 vs 116 ms).  The tile kernel uses 3
-    // workgroups per CU there (every workgroup stages the weights, so fewer,
-    // longer-lived ones; 3 is also what the register budget keeps resident).
+    // when a launch is only one or two rounds of work (2^18 samples: 67 vs
+    // 93 us).  The tile kernel runs 4 workgroups per CU: 2^18 samples are
+    // 16,384 tiles, exactly 4 per wave (67 us; 3 per CU leave 5 or 6 tiles
+    // per wave, 71 us; 5 and 6 per CU, 77 us).  The level-major kernel
+    // measured no faster with its fragments in LDS (49.9 vs 49.8 ms per
+    // render) and slower with 8-wave workgroups at 4 waves per SIMD (52.5
+    // ms: more waves than its L1 serves).
     const bool level_major  = n > (1u << 20);
-    const uint32_t blocks   = (persistent_blocks(n, 3u) + 7u) / 8u * 8u;  // whole XCD rounds
+    const uint32_t blocks   = (persistent_blocks(n, level_major ? 3u : 4u) + 7u) / 8u * 8u;  // whole XCD rounds
     const bool from_samples = in.samples != nullptr;
 #define NERF_FIELD_LAUNCH(K)                                                                                                                   \
     do {                                                                                                                                       \
