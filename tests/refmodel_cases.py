@@ -49,6 +49,75 @@ def structured_raw(pos, dirs):
     return np.stack([np.maximum(cos4y, 0), f16(pos[:, 0]), f16(np.cos(np.float64(dirs[:, 0]))), np.zeros(len(pos), np.float32)], 1)
 
 
+def pos_entry(level, kind, axis):
+    """Position-encoding index of sin (kind 0) / cos (kind 1) of 2^level
+    times coordinate `axis`."""
+    return 3 + 6 * level + 3 * kind + axis
+
+
+def encoding_probe(d_entry, c_entries, c_from_dir):
+    """Weights whose four raw outputs are four frequency-encoding values:
+    raw density 0 = position entry d_entry, raw colour k = position entry
+    c_entries[k] (carried through raw density output k + 1, the colour
+    input's geometry column k) or, with c_from_dir, direction entry
+    c_entries[k].  Each value v enters as the neuron pair relu(v), relu(-v),
+    identity hidden layers carry both, and the linear output layer takes
+    their difference: every product is 1 x an fp16 value and every sum has
+    one nonzero term, so the raw outputs are the encoding's fp16 values
+    exactly."""
+    d = [np.zeros(s, np.float32) for s in DENSITY_SHAPES]
+    c = [np.zeros(s, np.float32) for s in COLOR_SHAPES]
+    d[0][0, d_entry], d[0][1, d_entry] = 1.0, -1.0
+    d[5][0, 0], d[5][0, 1] = 1.0, -1.0
+    for k in range(3):
+        if not c_from_dir:
+            d[0][2 + 2 * k, c_entries[k]], d[0][3 + 2 * k, c_entries[k]] = 1.0, -1.0
+            d[5][1 + k, 2 + 2 * k], d[5][1 + k, 3 + 2 * k] = 1.0, -1.0
+        col = 15 + c_entries[k] if c_from_dir else k
+        c[0][2 * k, col], c[0][2 * k + 1, col] = 1.0, -1.0
+        c[3][k, 2 * k], c[3][k, 2 * k + 1] = 1.0, -1.0
+    for m in d[1:5] + c[1:3]:
+        m[:, :] = np.eye(128)
+    return pack(d), pack(c)
+
+
+def encoding_values(v, levels):
+    """Frequency encoding of rows v [n][3] in numpy: sin and cos evaluated in
+    fp64 on the exact fp32 argument v 2^l, rounded to fp32, then to fp16."""
+    v = np.asarray(v, np.float32)
+    cols = [v[:, a].astype(np.float64) for a in range(3)]
+    for l in range(levels):
+        arg = [(v[:, a] * np.float32(2.0 ** l)).astype(np.float64) for a in range(3)]
+        cols += [np.sin(x) for x in arg] + [np.cos(x) for x in arg]
+    e = np.stack(cols, 1).astype(np.float32).astype(np.float16).astype(np.float32)
+    return e
+
+
+def encoding_probe_raw(pos, dirs, d_entry, c_entries, c_from_dir):
+    pe, de = encoding_values(pos, 10), encoding_values(dirs, 4)
+    src = de if c_from_dir else pe
+    return np.stack([pe[:, d_entry]] + [src[:, k] for k in c_entries], 1)
+
+
+# (density entry, three colour entries, colour entries from the direction):
+# sine and cosine on the finest levels (|2^9 x| up to 768) and the coarsest,
+# both networks, every axis.
+ENCODING_PROBES = [
+    (pos_entry(9, 0, 0), [pos_entry(9, 1, 1), pos_entry(8, 0, 2), pos_entry(7, 1, 0)], False),
+    (pos_entry(9, 1, 2), [pos_entry(0, 0, 1), pos_entry(3, 1, 0), pos_entry(5, 0, 2)], False),
+    (pos_entry(6, 0, 1), [3 + 6 * 3 + 2, 3 + 6 * 3 + 3, 3 + 6 * 2 + 4], True),
+    (1, [0, 3 + 1, 3 + 6 * 1 + 5], True),
+]
+
+
+def probe_points(n, seed):
+    """World points over the scene box plus edge values (0, the box faces,
+    tiny magnitudes, both signs)."""
+    p = world_points(n, seed)
+    edge = np.array([[0.0, -0.0, 1.5], [-1.5, 1e-7, -1e-7], [1.0, -1.0, 0.5], [np.pi / 4, np.pi / 2, -np.pi]], np.float32)
+    return np.concatenate([p, edge])
+
+
 def world_points(n, seed, lo=-1.5, hi=1.5):
     return np.random.default_rng(seed).uniform(lo, hi, (n, 3)).astype(np.float32)
 

@@ -17,7 +17,7 @@ import pytest
 
 from conftest import announce
 from helpers import L, ext, orc, DeviceArray, synchronize, byref, assert_rel
-from refmodel_cases import structured, structured_raw, unit_dirs, world_points
+from refmodel_cases import ENCODING_PROBES, encoding_probe, encoding_probe_raw, probe_points, structured, structured_raw, unit_dirs, world_points
 
 pytestmark = pytest.mark.gpu
 
@@ -99,6 +99,30 @@ def test_ref_structured_weights_closed_form():
     # sin/cos on the GPU are within a few fp32 ulp of the correctly rounded
     # value, so an fp16 rounding may differ by one fp16 ulp.
     np.testing.assert_allclose(raw[:, [0, 2]], want[:, [0, 2]], rtol=1e-3, atol=1e-3)
+
+
+@pytest.mark.parametrize("probe", range(len(ENCODING_PROBES)))
+def test_ref_frequency_encoding_values(probe):
+    # Weights that route four frequency-encoding values straight to the raw
+    # outputs (exact: every product is 1 x an fp16 value, every sum has one
+    # nonzero term) pin the kernel's sine and cosine, their level, axis and
+    # slot, against fp16 of the correctly rounded fp32 values.  The kernel's
+    # own reduction and polynomials are within 1.49 fp32 ulp, so a value
+    # whose fp32 result lies within that of an fp16 rounding tie may round
+    # the other way: measured over every float in (0, 1024), 2 arguments in
+    # 10^5.  Bar: at least 99.9 % exact, every value within one fp16 ulp.
+    d_entry, c_entries, from_dir = ENCODING_PROBES[probe]
+    n = 16384
+    announce(f"reference-model frequency encoding probe {probe} n={n}")
+    dp, cp = encoding_probe(d_entry, c_entries, from_dir)
+    m = ext.RefModel(None, None, DeviceArray.from_numpy(dp), DeviceArray.from_numpy(cp))
+    pos = probe_points(n, 31 + probe)
+    dirs = unit_dirs(pos.shape[0], 37 + probe)
+    _, raw = _forward(m, pos, dirs)
+    want = encoding_probe_raw(pos, dirs, d_entry, c_entries, from_dir)
+    exact = float(np.mean(raw == want))
+    ulp = np.spacing(np.abs(want).astype(np.float16)).astype(np.float32)
+    assert exact >= 0.999 and np.all(np.abs(raw - want) <= ulp), (exact, float(np.max(np.abs(raw - want) / ulp)))
 
 
 @pytest.mark.parametrize("w,h,views", [(24, 20, 1), (16, 12, 2)])

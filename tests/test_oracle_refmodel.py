@@ -5,7 +5,7 @@ GEMM with the same fp16 rounding points, and structured weights whose
 outputs have closed forms (input layouts of :918-943)."""
 import numpy as np
 
-from refmodel_cases import COLOR_SHAPES, DENSITY_SHAPES, structured, structured_raw, unit_dirs, world_points
+from refmodel_cases import COLOR_SHAPES, DENSITY_SHAPES, ENCODING_PROBES, encoding_probe, encoding_probe_raw, probe_points, structured, structured_raw, unit_dirs, world_points
 
 
 def test_ref_init_matches_reference_loop(orc):
@@ -215,3 +215,13 @@ def test_ref_mlp_backward_matches_matrix_form(orc):
     # Only the colour outputs 0..2 carry gradient: the last colour layer's
     # rows 3..15 have none.
     assert np.all(dC[38912 + 3 * 128:] == 0)
+
+
+def test_ref_encoding_probe_weights(orc):
+    # The probe weights route four encoding values to the raw outputs
+    # unchanged; the oracle's network gives the numpy closed form exactly.
+    pos, dirs = probe_points(500, 41), unit_dirs(504, 42)
+    for d_entry, c_entries, from_dir in ENCODING_PROBES:
+        dp, cp = encoding_probe(d_entry, c_entries, from_dir)
+        _, raw = orc.ref_field_forward(dp, cp, pos, dirs)
+        assert np.array_equal(raw, encoding_probe_raw(pos, dirs, d_entry, c_entries, from_dir)), (d_entry, c_entries, from_dir)
