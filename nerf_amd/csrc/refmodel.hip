@@ -409,22 +409,33 @@ __device__ __forceinline__ void freq_sincos(float y, float& s_out, float& c_out)
     c_out         = ((q + 1) & 2) ? -b : b;
 }
 
+// Written as 4-byte pairs (row is 4-byte aligned): level l fills positions
+// 3 + 6l .. 8 + 6l, so each level stores the previous level's last value
+// with its first, then two pairs, and carries its last value on; position
+// 3 + 6 levels (the first padding column) gets zero.
 __device__ __forceinline__ void freq_row(const float v[3], uint32_t levels, half_t* row) {
-    row[0] = to_half_rne(v[0]);
-    row[1] = to_half_rne(v[1]);
-    row[2] = to_half_rne(v[2]);
-    float f = 1.0f;
+    uint32_t* w = reinterpret_cast<uint32_t*>(row);
+    auto pack   = [](half_t a, half_t b) { return __builtin_bit_cast(uint32_t, half2_t{a, b}); };
+    w[0]        = pack(to_half_rne(v[0]), to_half_rne(v[1]));
+    half_t carry = to_half_rne(v[2]);
+    float f      = 1.0f;
 #pragma unroll 1
     for (uint32_t l = 0; l < levels; ++l) {
+        half_t sn[3], cs[3];
 #pragma unroll
         for (uint32_t a = 0; a < 3u; ++a) {
             float s, c;
             freq_sincos(v[a] * f, s, c);  // v * 2^l is exact
-            row[3u + 6u * l + a]      = to_half_rne(s);
-            row[3u + 6u * l + 3u + a] = to_half_rne(c);
+            sn[a] = to_half_rne(s);
+            cs[a] = to_half_rne(c);
         }
+        w[1u + 3u * l] = pack(carry, sn[0]);
+        w[2u + 3u * l] = pack(sn[1], sn[2]);
+        w[3u + 3u * l] = pack(cs[0], cs[1]);
+        carry          = cs[2];
         f *= 2.0f;
     }
+    w[1u + 3u * levels] = pack(carry, (half_t)0.0f);
 }
 
 template <bool kFromSamples>
