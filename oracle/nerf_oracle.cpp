@@ -23,10 +23,12 @@
 // injectivity; trilinear interpolation against exact reproduction of linear
 // tables; MLP against an fp64 numpy GEMM with the same rounding points; SH
 // against quadrature orthonormality; rays, AABB and march against analytic
-// axis-aligned cases; composite against the closed form for constant density.
-// hash_u32 (:321-328) has no published test vector: it is checked for
-// bijectivity through its inverse and for avalanche only ("parity unpinned"
-// beyond that; it is not on the inference path).
+// axis-aligned cases; composite against the closed form for constant density;
+// the Huber loss against a one-sample closed form in both branches.
+// hash_u32, rand01, the training pixel draws and the camera pick
+// (:321-332, :438-440, :1482) have no published test vector: they are pinned
+// by a numpy uint32 restatement of the reference's recurrences, compared bit
+// for bit (tests/test_oracle_rng_pins.py), plus bijectivity and avalanche.
 
 #include <math.h>
 #include <stdint.h>
