@@ -548,9 +548,13 @@ def _threaded(fn, n: int, threads: int):
         return list(ex.map(lambda be: fn(*be), _split(n, threads)))
 
 
-def cpu_render_leg(model, cam, bits, threads: int, budget_s: float):
+def cpu_render_leg(model, cam, bits, threads: int, budget_s: float, gpu_image=None):
     """The scalar oracle's render (march + field + composite) on a
-    deterministic ray subset of the headline view, sized to about budget_s."""
+    deterministic ray subset of the headline view, sized to about budget_s.
+    gpu_image = (rgba8 [H*W] u32, rgb [H*W][3] f32) of the GPU's render of the
+    same view: the subset's oracle pixels are compared with it (max RGBA8
+    difference, max RGB error relative to max(|want|, 10 % of the channel's
+    RMS), as the parity tests measure them)."""
     from oracle import oracle as orc
     g = orc.make_grid(16, 19, 1)
     table = model.table.numpy().view(np.uint16)
@@ -566,10 +570,18 @@ def cpu_render_leg(model, cam, bits, threads: int, budget_s: float):
     stride = max(1, (W * H) // int(min(W * H, max(rays.size, budget_s / per_ray))))
     rays = np.arange(0, W * H, stride, dtype=np.uint32)
     t0 = time.perf_counter()
-    orc.render_rays(g, table, dp, cp, ocam, b, 128, (0, 0, 0, 1, 1, 1), MAX_STEPS, rays, T_STOP, threads=threads)
+    want_rgb, want_rgba, _ = orc.render_rays(g, table, dp, cp, ocam, b, 128, (0, 0, 0, 1, 1, 1), MAX_STEPS, rays, T_STOP, threads=threads)
     dt = time.perf_counter() - t0
-    return {"value": round(rays.size / dt / 1e6, 6), "unit": "Mrays/s", "threads": threads, "seconds": round(dt, 2),
-            "sample": f"{rays.size} rays (every {stride}th ray of the {W}x{H} view: full march + field + composite per ray)"}
+    out = {"value": round(rays.size / dt / 1e6, 6), "unit": "Mrays/s", "threads": threads, "seconds": round(dt, 2),
+           "sample": f"{rays.size} rays (every {stride}th ray of the {W}x{H} view: full march + field + composite per ray)"}
+    if gpu_image is not None:
+        g_rgba, g_rgb = gpu_image
+        d8 = np.abs(g_rgba[rays].view(np.uint8).astype(int) - want_rgba.view(np.uint8).astype(int)).max()
+        wr = want_rgb.astype(np.float64)
+        floor = np.maximum(0.1 * np.sqrt(np.mean(wr ** 2, axis=0)), 1e-6)
+        rel = (np.abs(g_rgb[rays].astype(np.float64) - wr) / np.maximum(np.abs(wr), floor)).max()
+        out["parity_vs_gpu"] = {"rays": int(rays.size), "max_rgba8_diff": int(d8), "max_rgb_rel_err": float(f"{rel:.3e}")}
+    return out
 
 
 def cpu_c1_leg(threads: int):
@@ -651,16 +663,16 @@ def cpu_train_leg(snap, threads: int, ray_fraction: float = 1.0):
                       + ("" if ray_fraction == 1.0 else f" (the first {ray_fraction:.3g} of its rays)")}
 
 
-def cpu_baseline(model, cam, bits, train_snap):
+def cpu_baseline(model, cam, bits, train_snap, gpu_image=None):
     """The scalar C++ oracle (the same math, -O2 -ffp-contract=off, no SIMD
     intrinsics) on the host: 1 thread and the host's thread share."""
     threads = min(16, os.cpu_count() or 1)
-    legs = {"render_1t": cpu_render_leg(model, cam, bits, 1, 6.0), f"render_{threads}t": cpu_render_leg(model, cam, bits, threads, 6.0), "c1_1t": cpu_c1_leg(1), f"c1_{threads}t": cpu_c1_leg(threads)}
+    legs = {"render_1t": cpu_render_leg(model, cam, bits, 1, 6.0), f"render_{threads}t": cpu_render_leg(model, cam, bits, threads, 6.0, gpu_image), "c1_1t": cpu_c1_leg(1), f"c1_{threads}t": cpu_c1_leg(threads)}
     if train_snap is not None:
         legs["train_1t"] = cpu_train_leg(train_snap, 1, ray_fraction=1.0 / 16)
         legs[f"train_{threads}t"] = cpu_train_leg(train_snap, threads)
     head = legs[f"render_{threads}t"]
-    return {"value": head["value"], "unit": "Mrays/s", "cores": threads, "kind": "port", "sample": head["sample"], "hardware_concurrency": os.cpu_count(), "cpu_model": _cpu_model(),
+    return {"value": head["value"], "unit": "Mrays/s", "cores": threads, "kind": "port", "sample": head["sample"], "parity_vs_gpu": head.get("parity_vs_gpu"), "hardware_concurrency": os.cpu_count(), "cpu_model": _cpu_model(),
             "threads_note": "the host's share of one GPU box is 16 threads (the all-threads legs use them); 1-thread legs alongside", "legs": legs}
 
 
@@ -742,6 +754,13 @@ def main() -> int:
         samples = st.samples
         shaded = st.samples_shaded
     stage = {k: v / args.steps for k, v in stage.items()}
+    # The image of one more render, with its unclamped RGB, for the CPU leg's
+    # parity check (outside the timed region).
+    rgb_img = DeviceArray((1, H, W, 3), np.float32)
+    renderer.render(model, occ, [cam], MAX_STEPS, T_STOP, rgba8=rgba, rgb=rgb_img, stream=stream)
+    synchronize()
+    gpu_image = (rgba.numpy().reshape(-1), rgb_img.numpy().reshape(-1, 3))
+    del rgb_img
     progress("render")
     field_s = stage["field"] / 1e3
     achieved_gbs = shaded * FIELD_BYTES_PER_SAMPLE / field_s / 1e9
@@ -792,7 +811,7 @@ def main() -> int:
             line["reference_model"] = ref_model_render()
             progress("reference-model render")
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(model, cam, bits, train_snap)
+        line["cpu_baseline"] = cpu_baseline(model, cam, bits, train_snap, gpu_image)
         progress("CPU baseline")
     print(json.dumps(line), flush=True)
     return 0

@@ -292,6 +292,14 @@ typedef struct NerfExtRenderDesc {
                                        samples (a block is never split), so
                                        the sample buffers (32 B per sample)
                                        hold one chunk */
+    uint32_t* composited;           /* optional device [view][H][W]: samples
+                                       composited per ray, i.e. up to and
+                                       including the one after which T <
+                                       min_transmittance (all of them if T
+                                       stays above it) */
+    uint32_t* shaded;               /* optional device [view][H][W]: samples
+                                       the field evaluated per ray (whole
+                                       rounds: >= composited) */
 } NerfExtRenderDesc;
 
 typedef struct NerfExtRenderStats {

@@ -234,6 +234,8 @@ class NerfExtRenderDesc(C.Structure):
         ("background", C.c_float * 3),
         ("stream", C.c_void_p),
         ("chunk_samples", C.c_uint64),
+        ("composited", C.c_void_p),
+        ("shaded", C.c_void_p),
     ]
 
 

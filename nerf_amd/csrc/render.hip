@@ -113,12 +113,23 @@ __global__ void k_fill_u32(uint32_t* __restrict__ p, uint32_t n, uint32_t v) {
 
 // -------------------------------------------------------------- rounds
 // Shading and compositing run in rounds over slices of each ray's sample
-// stream: round r shades samples [S_r, S_r + K_r) of every active ray
-// (K = 256, 256, 512, ...: every S_r is a multiple of 64), composites them
-// front to back onto the ray's carried (T, C) (reference :601-635) and
-// retires the rays whose transmittance fell below t_stop or whose samples
-// are exhausted.  Only active rays are shaded: an opaque surface ends a ray's
-// field work within the round it is reached.
+// stream.  Every ray carries its progress p (samples composited so far) and
+// the quota q of its next round: round r shades samples [p, p + min(q, count
+// - p)) of every active ray, composites them front to back onto the ray's
+// carried (T, C) (reference :601-635) and retires the rays whose
+// transmittance fell below t_stop or whose samples are exhausted.  The
+// quota follows a schedule of round ends E_r = 256, 512, 1024, 2048, ...
+// (q = E_r - p catches a ray up with it), except where the ray's own decay
+// predicts its stop sooner: from T0 -> T1 over the m samples of the last
+// round the per-sample rate ln(T0 / T1) / m gives the samples still needed
+// to fall below t_stop, and the quota is that plus a margin when it is
+// smaller than the catch-up.  A ray whose prediction fell short catches up
+// in the following round, and the last round never predicts, so every ray
+// is done after the scheduled rounds plus two.  Only active rays are shaded:
+// an opaque surface ends a ray's field work within the round it is reached,
+// and a ray that thins out gradually stops close to its predicted sample.
+// The split into rounds changes which samples share a field launch, never a
+// value: images are the same for any quotas.
 
 __device__ __forceinline__ void write_pixel(uint32_t ray, float cr, float cg, float cb, float T, float3 bg, uint32_t* __restrict__ rgba8, float* __restrict__ rgb_out) {
     const float r = cr + T * bg.x, g = cg + T * bg.y, b = cb + T * bg.z;
@@ -244,9 +255,11 @@ __device__ __forceinline__ bool tiled_ray(uint32_t t, uint32_t W, uint32_t tiles
 }
 
 // Rays without samples get the background; the others start the first
-// round's list (wave-aggregated appends, tile-major order) with T = 1, C = 0.
+// round's list (wave-aggregated appends, tile-major order) with T = 1, C = 0,
+// progress 0 and the first round's quota.
 __global__ __launch_bounds__(256) void k_round_init(uint32_t ray0, uint32_t ray_end, uint32_t W, uint32_t tiles_x, uint32_t row0_tile, const uint32_t* __restrict__ counts, float3 bg, uint32_t* __restrict__ rgba8,
-                                                   float* __restrict__ rgb_out, float4* __restrict__ state, uint32_t* __restrict__ list, uint32_t* __restrict__ n_active) {
+                                                   float* __restrict__ rgb_out, float4* __restrict__ state, uint2* __restrict__ prog, uint32_t first_quota, uint32_t* __restrict__ list,
+                                                   uint32_t* __restrict__ n_active, uint32_t* __restrict__ composited, uint32_t* __restrict__ shaded) {
     uint32_t ray       = 0u;
     const bool valid   = tiled_ray(blockIdx.x * 256u + threadIdx.x, W, tiles_x, row0_tile, ray0, ray_end, ray);
     const bool take    = valid && counts[ray] > 0u;
@@ -259,22 +272,27 @@ __global__ __launch_bounds__(256) void k_round_init(uint32_t ray0, uint32_t ray_
     if (take) {
         list[base + wave::rank_below(m)] = ray;
         state[ray]                       = make_float4(1.0f, 0.0f, 0.0f, 0.0f);
+        prog[ray]                        = make_uint2(0u, first_quota);
     } else if (valid) {
         write_pixel(ray, 0.0f, 0.0f, 0.0f, 1.0f, bg, rgba8, rgb_out);
+        if (composited) composited[ray] = 0u;
+        if (shaded) shaded[ray] = 0u;
     }
 }
 
 // Samples of this round per list slot (zero past the active count, so the
 // scans run over a fixed length); keep flags start at zero.
-__global__ __launch_bounds__(256) void k_round_counts(uint32_t n_slots, const uint32_t* __restrict__ list, const uint32_t* __restrict__ n_active, const uint32_t* __restrict__ counts, uint32_t S, uint32_t K, uint32_t* __restrict__ cnt,
-                                                     uint32_t* __restrict__ keep) {
+__global__ __launch_bounds__(256) void k_round_counts(uint32_t n_slots, const uint32_t* __restrict__ list, const uint32_t* __restrict__ n_active, const uint32_t* __restrict__ counts, const uint2* __restrict__ prog,
+                                                     uint32_t* __restrict__ cnt, uint32_t* __restrict__ keep) {
     const uint32_t a = blockIdx.x * 256u + threadIdx.x;
     if (a >= n_slots) return;
     keep[a] = 0u;
     uint32_t v = 0u;
     if (a < *n_active) {
-        const uint32_t c = counts[list[a]];
-        v                = c > S ? min(K, c - S) : 0u;
+        const uint32_t ray = list[a];
+        const uint32_t c   = counts[ray];
+        const uint2 pq     = prog[ray];
+        v                  = c > pq.x ? min(pq.y, c - pq.x) : 0u;
     }
     cnt[a] = v;
 }
@@ -283,7 +301,7 @@ __global__ __launch_bounds__(256) void k_round_counts(uint32_t n_slots, const ui
 // slots (lane = slot): the group's samples fill the same range of the list
 // as slot by slot (from off of its first slot), but step-major: step i of
 // every slot that has one, in slot order, then step i + 1.
-__global__ __launch_bounds__(256) void k_round_list(const uint32_t* __restrict__ list, const uint32_t* __restrict__ n_active, const uint32_t* __restrict__ offsets, uint32_t S, const uint32_t* __restrict__ cnt,
+__global__ __launch_bounds__(256) void k_round_list(const uint32_t* __restrict__ list, const uint32_t* __restrict__ n_active, const uint32_t* __restrict__ offsets, const uint2* __restrict__ prog, const uint32_t* __restrict__ cnt,
                                                    const uint32_t* __restrict__ off, uint32_t* __restrict__ qlist, uint32_t* __restrict__ qray) {
     const uint32_t lane = threadIdx.x & 63u, nw = gridDim.x * 4u;
     const uint32_t n    = *n_active;
@@ -292,7 +310,7 @@ __global__ __launch_bounds__(256) void k_round_list(const uint32_t* __restrict__
         const bool slot   = a < n;
         const uint32_t m  = slot ? cnt[a] : 0u;
         const uint32_t ray = slot && m ? list[a] : 0u;
-        const uint32_t q0  = slot && m ? offsets[ray] + S : 0u;
+        const uint32_t q0  = slot && m ? offsets[ray] + prog[ray].x : 0u;
         uint32_t dst      = off[g * 64u];
         uint32_t steps    = m;
 #pragma unroll
@@ -319,10 +337,26 @@ __global__ __launch_bounds__(256) void k_round_list(const uint32_t* __restrict__
 // pixel is written or (T, C) carried, and the slot flagged in keep
 // (k_round_compact then lists the kept rays in slot order).  The entries of
 // eight steps are loaded before they are composited; each load reads the
-// group's entries of one step, consecutive in the output.
-__global__ __launch_bounds__(256) void k_round_composite(const uint32_t* __restrict__ list, const uint32_t* __restrict__ n_active, const uint32_t* __restrict__ counts, uint32_t S, const uint32_t* __restrict__ cnt,
+// group's entries of one step, consecutive in the output.  A kept ray's
+// progress and next quota are updated (next_end: the schedule's end of the
+// next round; predict: whether that round may take a predicted quota).  A
+// retiring ray optionally reports the samples it composited (the early-stop
+// index) and the samples the field evaluated for it (to the end of this
+// round).
+__device__ __forceinline__ uint32_t next_quota(float T0, float T1, uint32_t m, uint32_t p, uint32_t next_end, float t_stop, bool predict) {
+    const uint32_t catch_up = next_end - p;
+    if (!predict || !(T1 < T0) || m == 0u) return catch_up;
+    // Samples until T < t_stop at the last round's rate, with a margin of an
+    // eighth plus eight samples.  Only the amount of work depends on it.
+    const float need = (__logf(T1) - __logf(t_stop)) * (float)m / (__logf(T0) - __logf(T1));
+    const float q    = need * 1.125f + 8.0f;
+    return q < (float)catch_up ? max(1u, (uint32_t)q) : catch_up;
+}
+
+__global__ __launch_bounds__(256) void k_round_composite(const uint32_t* __restrict__ list, const uint32_t* __restrict__ n_active, const uint32_t* __restrict__ counts, uint2* __restrict__ prog, const uint32_t* __restrict__ cnt,
                                                         const uint32_t* __restrict__ off, const float4* __restrict__ field, float t_stop, float3 bg, float4* __restrict__ state, uint32_t* __restrict__ rgba8,
-                                                        float* __restrict__ rgb_out, uint32_t* __restrict__ keep) {
+                                                        float* __restrict__ rgb_out, uint32_t* __restrict__ keep, uint32_t next_end, uint32_t predict, uint32_t* __restrict__ composited,
+                                                        uint32_t* __restrict__ shaded) {
     const uint32_t lane = threadIdx.x & 63u, nw = gridDim.x * 4u;
     const uint32_t n    = *n_active;
     for (uint32_t g = blockIdx.x * 4u + (threadIdx.x >> 6); g * 64u < n; g += nw) {
@@ -333,6 +367,7 @@ __global__ __launch_bounds__(256) void k_round_composite(const uint32_t* __restr
         const float4 st0   = slot ? state[ray] : make_float4(1.0f, 0.0f, 0.0f, 0.0f);
         float T = st0.x, cr = st0.y, cg = st0.z, cb = st0.w;
         bool stopped   = false;
+        uint32_t used  = 0u;
         uint32_t dst   = off[g * 64u];
         uint32_t steps = m;
 #pragma unroll
@@ -356,13 +391,21 @@ __global__ __launch_bounds__(256) void k_round_composite(const uint32_t* __restr
                     cb += w * f[k].w;
                     T *= 1.0f - f[k].x;
                     stopped = T < t_stop;
+                    ++used;
                 }
             }
         }
         if (slot) {
-            const bool done = stopped || S + m >= counts[ray];
-            if (done) write_pixel(ray, cr, cg, cb, T, bg, rgba8, rgb_out);
-            else state[ray] = make_float4(T, cr, cg, cb);
+            const uint32_t p = prog[ray].x;
+            const bool done  = stopped || p + m >= counts[ray];
+            if (done) {
+                write_pixel(ray, cr, cg, cb, T, bg, rgba8, rgb_out);
+                if (composited) composited[ray] = p + used;
+                if (shaded) shaded[ray] = p + m;
+            } else {
+                state[ray] = make_float4(T, cr, cg, cb);
+                prog[ray]  = make_uint2(p + m, next_quota(st0.x, T, m, p + m, next_end, t_stop, predict != 0u));
+            }
             keep[a] = done ? 0u : 1u;
         }
     }
@@ -520,7 +563,7 @@ constexpr uint32_t kFirstRound = 256u;  // samples per ray in the first round (a
 constexpr uint32_t kScanBlockRays = 1024u;        // rays per block of the chunk plan (the scan's block)
 constexpr uint64_t kChunkSamples  = 1ull << 29;   // samples per chunk: 32 B each in the stream buffers (16 GiB)
 constexpr uint32_t kMaxSteps      = 1u << 19;     // so that a block of rays holds at most kChunkSamples samples
-constexpr uint32_t kMaxRounds  = 24u;   // K doubles from 256: covers any max_steps < 2^24
+constexpr uint32_t kMaxRounds  = 24u;   // round ends double from 256 (12 cover 2^19 steps), plus two
 
 struct NerfExtRenderer {
     template <typename T>
@@ -552,6 +595,7 @@ struct NerfExtRenderer {
     Buf<float4> field;
     // rounds
     Buf<float4> state;                 // per ray (T, C.rgb)
+    Buf<uint2> prog;                   // per ray (samples composited, quota of its next round)
     Buf<uint32_t> list[2], n_active;   // active rays of this / the next round, and their counts
     Buf<uint32_t> cnt, off, qlist;     // samples per slot, their offsets, stream indices
     Buf<uint32_t> qray;                // owning ray of each qlist entry
@@ -574,6 +618,7 @@ struct NerfExtRenderer {
         sample_ray.release();
         field.release();
         state.release();
+        prog.release();
         list[0].release();
         list[1].release();
         n_active.release();
@@ -805,17 +850,22 @@ NERF_API NerfStatus nerf_ext_render(NerfExtRenderer* R, const NerfExtRenderDesc*
         NERF_HIP_TRY(ref_pack_weights(w.density, w.color, R->ref_frags.ptr, st));
     }
     const float3 bg = make_float3(d->background[0], d->background[1], d->background[2]);
-    // Rounds: slices of 256, 256, 512, 1024, ... samples per active ray until
-    // every ray's stream (at most max_steps samples) is covered.
+    // Rounds: the schedule's round ends 256, 512, 1024, ... until every
+    // ray's stream (at most max_steps samples) is covered; when there is more
+    // than one, two more rounds at the last end let rays whose predicted
+    // quota fell short catch up.  Round r + 1 may take predicted quotas
+    // unless it is the last.
     uint32_t n_rounds = 0u;
-    uint32_t Ks[kMaxRounds], Ss[kMaxRounds];
-    for (uint64_t S = 0, K = kFirstRound; S < d->max_steps && n_rounds < kMaxRounds; S += K, K = S < kFirstRound ? kFirstRound : S) {
-        Ss[n_rounds] = (uint32_t)S;
-        Ks[n_rounds] = (uint32_t)K;
-        ++n_rounds;
+    uint32_t Es[kMaxRounds];
+    for (uint64_t E = kFirstRound;; E *= 2u) {
+        Es[n_rounds++] = (uint32_t)E;
+        if (E >= d->max_steps) break;
     }
+    if (n_rounds >= 2u)
+        for (int k = 0; k < 2; ++k, ++n_rounds) Es[n_rounds] = Es[n_rounds - 1u];
     const uint32_t chunk_rays_max = n_rays;
     NERF_HIP_TRY(R->state.reserve(n_rays));
+    NERF_HIP_TRY(R->prog.reserve(n_rays));
     NERF_HIP_TRY(R->list[0].reserve(chunk_rays_max));
     NERF_HIP_TRY(R->list[1].reserve(chunk_rays_max));
     NERF_HIP_TRY(R->n_active.reserve(2));
@@ -849,13 +899,13 @@ NERF_API NerfStatus nerf_ext_render(NerfExtRenderer* R, const NerfExtRenderDesc*
         // chunk's first pixel row to its last.
         const uint32_t tiles_x = (W + kTile - 1u) / kTile, row0_tile = (c.ray0 / W) / kTile, row1_tile = ((c.ray_end - 1u) / W) / kTile;
         const uint64_t tile_threads = (uint64_t)(row1_tile - row0_tile + 1u) * tiles_x * kTile * kTile;
-        k_round_init<<<(uint32_t)((tile_threads + 255u) / 256u), 256, 0, st>>>(c.ray0, c.ray_end, W, tiles_x, row0_tile, R->counts.ptr, bg, rgba8, rgb_f32, R->state.ptr, l_cur, n_cur);
+        k_round_init<<<(uint32_t)((tile_threads + 255u) / 256u), 256, 0, st>>>(c.ray0, c.ray_end, W, tiles_x, row0_tile, R->counts.ptr, bg, rgba8, rgb_f32, R->state.ptr, R->prog.ptr, Es[0], l_cur, n_cur, d->composited, d->shaded);
         NERF_LAUNCH_CHECK("k_round_init");
         const uint32_t ray_waves = std::min<uint32_t>((nr + 3u) / 4u, device_cu_count() * 16u);  // workgroups of one-wave-per-slot kernels
         for (uint32_t r = 0; r < n_rounds; ++r) {
-            k_round_counts<<<cblocks, 256, 0, st>>>(nr, l_cur, n_cur, R->counts.ptr, Ss[r], Ks[r], R->cnt.ptr, R->keep.ptr);
+            k_round_counts<<<cblocks, 256, 0, st>>>(nr, l_cur, n_cur, R->counts.ptr, R->prog.ptr, R->cnt.ptr, R->keep.ptr);
             NERF_HIP_TRY(exclusive_scan_u32(R->cnt.ptr, R->off.ptr, nr, R->scan_tmp.ptr, R->round_total.ptr + r, st));
-            k_round_list<<<ray_waves, 256, 0, st>>>(l_cur, n_cur, R->offsets.ptr, Ss[r], R->cnt.ptr, R->off.ptr, R->qlist.ptr, R->qray.ptr);
+            k_round_list<<<ray_waves, 256, 0, st>>>(l_cur, n_cur, R->offsets.ptr, R->prog.ptr, R->cnt.ptr, R->off.ptr, R->qlist.ptr, R->qray.ptr);
             NERF_LAUNCH_CHECK("k_round_list");
             // The field reads this round's sample count on the device: the low
             // word of the 64-bit scan total (little-endian; totals < 2^32).
@@ -864,7 +914,9 @@ NERF_API NerfStatus nerf_ext_render(NerfExtRenderer* R, const NerfExtRenderDesc*
             if (ref_model) NERF_HIP_TRY(launch_ref_field(R->ref_frags.ptr, in, (uint32_t)c.samples, R->field.ptr, nullptr, st));
             else NERF_HIP_TRY(launch_field(g, d->model->table, w, in, (uint32_t)c.samples, R->field.ptr, st));
             if (timed) NERF_HIP_TRY(hipEventRecord(R->fev[2u * r + 1u], st));
-            k_round_composite<<<ray_waves, 256, 0, st>>>(l_cur, n_cur, R->counts.ptr, Ss[r], R->cnt.ptr, R->off.ptr, R->field.ptr, d->min_transmittance, bg, R->state.ptr, rgba8, rgb_f32, R->keep.ptr);
+            const uint32_t nxt = std::min(r + 1u, n_rounds - 1u);
+            k_round_composite<<<ray_waves, 256, 0, st>>>(l_cur, n_cur, R->counts.ptr, R->prog.ptr, R->cnt.ptr, R->off.ptr, R->field.ptr, d->min_transmittance, bg, R->state.ptr, rgba8, rgb_f32, R->keep.ptr, Es[nxt],
+                                                         r + 2u < n_rounds ? 1u : 0u, d->composited, d->shaded);
             NERF_LAUNCH_CHECK("k_round_composite");
             NERF_HIP_TRY(exclusive_scan_u32(R->keep.ptr, R->koff.ptr, nr, R->scan_tmp.ptr, R->keep_total.ptr, st));
             k_round_compact<<<cblocks, 256, 0, st>>>(l_cur, n_cur, R->keep.ptr, R->koff.ptr, R->keep_total.ptr, l_nxt, n_nxt);

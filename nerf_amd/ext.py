@@ -156,14 +156,15 @@ class Renderer:
         L.call("nerf_ext_renderer_create", C.byref(self._h))
 
     def render(self, model: "Model | RefModel", occupancy: L.NerfExtOccupancy, cameras: list, max_steps: int, min_transmittance: float = 1e-4, background=(1.0, 1.0, 1.0), rgba8: DeviceArray | None = None, rgb: DeviceArray | None = None,
-               counts: DeviceArray | None = None, stream: Stream | None = None, timed: bool = False, chunk_samples: int = 0):
+               counts: DeviceArray | None = None, stream: Stream | None = None, timed: bool = False, chunk_samples: int = 0, composited: DeviceArray | None = None, shaded: DeviceArray | None = None):
         n_views = len(cameras)
         w, h = cameras[0].width, cameras[0].height
         if rgba8 is None:
             rgba8 = DeviceArray((n_views, h, w), np.uint32)
         cams = (L.NerfExtCamera * n_views)(*cameras)
         ms = model.struct()
-        desc = L.NerfExtRenderDesc(C.pointer(ms), C.pointer(occupancy), cams, n_views, max_steps, min_transmittance, (C.c_float * 3)(*background), stream.handle if stream else None, chunk_samples)
+        desc = L.NerfExtRenderDesc(C.pointer(ms), C.pointer(occupancy), cams, n_views, max_steps, min_transmittance, (C.c_float * 3)(*background), stream.handle if stream else None, chunk_samples,
+                                   composited.ptr if composited else None, shaded.ptr if shaded else None)
         stats = L.NerfExtRenderStats()
         L.call("nerf_ext_render", self._h, C.byref(desc), rgba8.ptr, rgb.ptr if rgb else None, counts.ptr if counts else None, C.byref(stats) if timed else None)
         return rgba8, (stats if timed else None)

@@ -666,8 +666,12 @@ static void ref_field_point(const uint16_t* dp, const uint16_t* cp, const float*
 
 // The field sees positions normalised to the outermost cascade's box,
 // (w - lo) / (hi - lo) per axis (exact for the unit box).
+// Optional per-ray outputs of the early stop: used_out = samples composited
+// (the sample after which T < t_stop is the last one, :601-635 plus the
+// stop), t_prev_out = T before the last composited sample, t_final_out = T
+// after it.
 extern "C" void orc_render_rays(const OrcModel* model, const OrcCamera* cam, const uint32_t* bits, uint32_t res, uint32_t cascades, const float* aabb, uint32_t max_steps, float t_stop, const float* bg, const uint32_t* rays, uint32_t n_rays,
-    float* rgb_out, uint32_t* rgba8_out, uint32_t* counts_out, uint32_t n_threads) {
+    float* rgb_out, uint32_t* rgba8_out, uint32_t* counts_out, uint32_t n_threads, uint32_t* used_out, float* t_prev_out, float* t_final_out) {
     if (n_threads == 0u) n_threads = 1u;
     const OrcOcc occ = make_occ(bits, res, cascades, aabb);
     auto work = [&](uint32_t begin, uint32_t end) {
@@ -683,7 +687,8 @@ extern "C" void orc_render_rays(const OrcModel* model, const OrcCamera* cam, con
                     t_dt.push_back(dt);
                 });
             }
-            float T = 1.0f, C[3] = {0, 0, 0};
+            float T = 1.0f, T_prev = 1.0f, C[3] = {0, 0, 0};
+            uint32_t used = 0;
             for (uint32_t i = 0; i < count; ++i) {
                 const float tm   = t_dt[2 * i];
                 const float dt   = t_dt[2 * i + 1];
@@ -696,9 +701,14 @@ extern "C" void orc_render_rays(const OrcModel* model, const OrcCamera* cam, con
                 const float a = 1.0f - expf(-(s4[0] * fmaxf(dt, 0.0f)));
                 const float w = T * a;
                 for (int c = 0; c < 3; ++c) C[c] += w * s4[1 + c];
+                T_prev = T;
                 T *= 1.0f - a;
+                ++used;
                 if (T < t_stop) break;
             }
+            if (used_out) used_out[k] = used;
+            if (t_prev_out) t_prev_out[k] = T_prev;
+            if (t_final_out) t_final_out[k] = T;
             float rgb[3];
             for (int c = 0; c < 3; ++c) rgb[c] = C[c] + T * bg[c];
             if (rgb_out)

@@ -98,7 +98,7 @@ _PROTOS = {
     "orc_train_camera": (_U32, [_U32, _U32]),
     "orc_field_mlp": (None, [_P, _P, _P, _P, _U32, _P]),
     "orc_scene_render": (None, [_P, _U32, C.POINTER(OrcCamera), _P, _U32, _P]),
-    "orc_render_rays": (None, [C.POINTER(OrcModel), C.POINTER(OrcCamera), _P, _U32, _U32, _P, _U32, _F, _P, _P, _U32, _P, _P, _P, _U32]),
+    "orc_render_rays": (None, [C.POINTER(OrcModel), C.POINTER(OrcCamera), _P, _U32, _U32, _P, _U32, _F, _P, _P, _U32, _P, _P, _P, _U32, _P, _P, _P]),
     "orc_render_uniform": (None, [C.POINTER(OrcModel), C.POINTER(OrcCamera), _P, _U32, _P, _P, _U32, _P, _P, _P, _U32]),
 }
 
@@ -374,9 +374,12 @@ def composite_ray(sigma_rgb: np.ndarray, dt: np.ndarray, t_stop: float = 1e-4, b
 
 
 def render_rays(grid: OrcGrid | None, table: np.ndarray | None, dparams_bits: np.ndarray, cparams_bits: np.ndarray, cam: OrcCamera, bits: np.ndarray | None, res: int, aabb, max_steps: int, rays: np.ndarray, t_stop: float = 1e-4,
-                bg=(1.0, 1.0, 1.0), threads: int = 1, cascades: int = 1, kind: int = 0):
+                bg=(1.0, 1.0, 1.0), threads: int = 1, cascades: int = 1, kind: int = 0, stop: bool = False):
     """kind 0: hash-grid model (grid, table); kind 1: the reference's own
-    network (ref_* parameter sets; grid and table unused)."""
+    network (ref_* parameter sets; grid and table unused).  Returns (rgb,
+    rgba8, counts); with stop=True also (used, t_prev, t_final) per ray: the
+    samples composited before the early stop, and the transmittance before and
+    after the last of them."""
     model = OrcModel()
     if grid is not None:
         model.grid = grid
@@ -390,7 +393,13 @@ def render_rays(grid: OrcGrid | None, table: np.ndarray | None, dparams_bits: np
     rgb = np.empty((rays.size, 3), np.float32)
     rgba = np.empty(rays.size, np.uint32)
     counts = np.empty(rays.size, np.uint32)
-    lib().orc_render_rays(C.byref(model), C.byref(cam), _p(bits) if bits is not None else None, res, cascades, _p(box), max_steps, t_stop, _p(b), _p(rays), rays.size, _p(rgb), _p(rgba), _p(counts), threads)
+    used = np.empty(rays.size, np.uint32) if stop else None
+    t_prev = np.empty(rays.size, np.float32) if stop else None
+    t_final = np.empty(rays.size, np.float32) if stop else None
+    lib().orc_render_rays(C.byref(model), C.byref(cam), _p(bits) if bits is not None else None, res, cascades, _p(box), max_steps, t_stop, _p(b), _p(rays), rays.size, _p(rgb), _p(rgba), _p(counts), threads,
+                          _p(used) if stop else None, _p(t_prev) if stop else None, _p(t_final) if stop else None)
+    if stop:
+        return rgb, rgba, counts, used, t_prev, t_final
     return rgb, rgba, counts
 
 

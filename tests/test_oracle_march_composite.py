@@ -84,3 +84,30 @@ def test_composite_early_stop(orc):
     # T after k samples = exp(-5 k) < 1e-4 first at k = 2
     assert used == 2
     np.testing.assert_allclose(got, [1.0, np.exp(-10.0), np.exp(-10.0)], rtol=1e-4, atol=1e-6)
+
+
+def test_render_rays_stop_index(orc):
+    """Zero density-MLP weights give raw density 0, sigma = exp(0) = 1 at every
+    sample whatever the table, so an axis ray through an all-occupied box of
+    side 20 marched in 256 uniform steps of dt = 20/256 (exact in fp32) has
+    T = exp(-k dt) after k samples: the first k with T < 1e-4 is 118
+    (k dt = 9.21875; 117 steps leave T = 1.075e-4)."""
+    grid = orc.make_grid(16, 12, 0)
+    table = np.zeros(16 * (1 << 12) * 2, np.float32)
+    dp = np.zeros(3072, np.uint16)
+    cp = orc.f32_to_f16_bits(orc.mlp_init(1))
+    c2w = [1, 0, 0, 10.0, 0, 1, 0, 10.0, 0, 0, 1, 30.0]
+    cam = orc.camera(c2w, 1e30, 1e30, 0.5, 0.5, 2, 2)
+    box = (0, 0, 0, 20, 20, 20)
+    rgb, _, counts, used, t_prev, t_final = orc.render_rays(grid, table, dp, cp, cam, None, 16, box, 256, np.array([0], np.uint32), stop=True)
+    assert counts[0] == 256 and used[0] == 118
+    assert t_prev[0] >= 1e-4 > t_final[0]
+    np.testing.assert_allclose(t_final[0], np.exp(-118 * 20.0 / 256), rtol=1e-5)
+    np.testing.assert_allclose(t_prev[0], np.exp(-117 * 20.0 / 256), rtol=1e-5)
+    # Without the stop every sample is composited and T is the full chord's.
+    _, _, _, used0, _, t0 = orc.render_rays(grid, table, dp, cp, cam, None, 16, box, 256, np.array([0], np.uint32), t_stop=0.0, stop=True)
+    assert used0[0] == 256
+    np.testing.assert_allclose(t0[0], np.exp(-20.0), rtol=1e-4)
+    # The stop leaves T_final of the background in the pixel: rgb = C + T bg.
+    rgb0, *_ = orc.render_rays(grid, table, dp, cp, cam, None, 16, box, 256, np.array([0], np.uint32), t_stop=0.0)
+    assert np.all(np.abs(rgb - rgb0) < 2e-4)
