@@ -416,6 +416,9 @@ typedef struct NerfExtTrainBuffers {
     uint32_t max_rays;
     uint32_t sample_capacity;
     uint64_t table_elems;
+    float* dfeat;                    /* [16 levels][cap][2] d loss / d features,
+                                        loss-scaled, level-major (hash-grid
+                                        model; NULL for the reference model) */
 } NerfExtTrainBuffers;
 
 enum {

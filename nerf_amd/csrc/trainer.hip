@@ -366,6 +366,7 @@ NERF_API NerfStatus nerf_ext_trainer_buffers(NerfExtTrainer* trainer, NerfExtTra
     o->max_rays        = trainer->t->P.max_rays;
     o->sample_capacity = trainer->t->P.sample_cap;
     o->table_elems     = B.table_elems;
+    o->dfeat           = (float*)B.dfeat;
     return NERF_STATUS_OK;
 }
 

@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 
 from conftest import announce
-from helpers import L, ext, orc, oracle_grid, assert_rel, assert_adam_step
+from helpers import L, ext, orc, oracle_grid, assert_rel, assert_adam_step, assert_table_grad, assert_rel_rows, fixed_point_floor
 
 pytestmark = pytest.mark.gpu
 
@@ -209,12 +209,19 @@ def test_backward_stage(dataset, log2_table):
     for name, got, want in (("density input", mlp_grad[:2048], dD[:2048]), ("density output", mlp_grad[2048:3072], dD[2048:]), ("colour input", mlp_grad[3072:5120], dC[:2048]),
                             ("colour hidden", mlp_grad[5120:9216], dC[2048:6144]), ("colour output", mlp_grad[9216:], dC[6144:])):
         err = _frob(got, want)
-        assert err < 1e-2, f"{name} dW: relative Frobenius error {err:.3e}"
-    want_t = orc.encode_backward(oracle_grid(grid), p, dfeat)
-    err = _frob(table_grad, want_t)
-    assert err < 1e-2, f"table gradient: relative Frobenius error {err:.3e}"
-    # Support: every touched entry is touched on both sides.
-    assert np.array_equal(table_grad != 0, want_t != 0) or (np.count_nonzero((table_grad != 0) != (want_t != 0)) < 1e-4 * table_grad.size)
+        print(f"[grad] {name} dW: relative Frobenius {err:.3e}", flush=True)
+        assert err < 1e-3, f"{name} dW: relative Frobenius error {err:.3e}"
+    # The MLP's input gradient (fp16 deltas at the oracle's rounding points).
+    gpu_dfeat = ext.read_device(B.dfeat, (16, int(B.sample_capacity), 2), np.float32)[:, :n, :].transpose(1, 0, 2).reshape(n, 32)
+    assert_rel_rows(gpu_dfeat, dfeat, what="d features")
+    og = oracle_grid(grid)
+    # The scatter-add alone, on the GPU's own d features: exact fixed-point
+    # bins and slabs, 17-bit records.
+    floor = fixed_point_floor(gpu_dfeat)
+    assert_table_grad(table_grad, orc.encode_backward(og, p, gpu_dfeat), 16, f"table gradient (scatter), T=2^{log2_table}", frob_tol=1e-3, floor=floor)
+    # End to end from the oracle's d features: the samples whose ReLU mask
+    # flipped (bounded above) move the few entries they touch.
+    assert_table_grad(table_grad, orc.encode_backward(og, p, dfeat), 16, f"table gradient (end to end), T=2^{log2_table}", frob_tol=1e-3, floor=floor, entry_frac=1e-4)
 
 
 @pytest.mark.parametrize("log2_table", [14, 17])

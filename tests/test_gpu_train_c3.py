@@ -21,7 +21,7 @@ import numpy as np
 import pytest
 
 from conftest import announce
-from helpers import L, ext, orc, oracle_grid, assert_rel, assert_adam_step
+from helpers import L, ext, orc, oracle_grid, assert_rel, assert_adam_step, assert_table_grad, assert_rel_rows, fixed_point_floor
 
 pytestmark = pytest.mark.gpu
 
@@ -152,7 +152,8 @@ def c3_step(scene):
                features=ext.read_device(B.features, (n, 32), np.float16).astype(np.float32),
                draw=ext.read_device(B.draw, (n, 4), np.float32),
                mlp_grad=ext.read_device(B.mlp_grad, (10240,), np.float32),
-               table_grad=ext.read_device(B.table_grad, (int(B.table_elems),), np.float32))
+               table_grad=ext.read_device(B.table_grad, (int(B.table_elems),), np.float32),
+               dfeat=ext.read_device(B.dfeat, (16, int(B.sample_capacity), 2), np.float32)[:, :n, :].transpose(1, 0, 2).reshape(n, 32))
     return out
 
 
@@ -224,12 +225,17 @@ def test_backward_stage(c3_step):
     dfeat, dD, dC = orc.mlp_backward(c3_step["dp"], c3_step["cp"], c3_step["features"], d, draw[:, 0], draw[:, 1:], LOSS_SCALE)
     g = c3_step["mlp_grad"]
     assert np.isfinite(g).all() and np.isfinite(c3_step["table_grad"]).all()
-    for name, got, want in (("density", g[:3072], dD), ("colour", g[3072:], dC)):
+    for name, got, want in (("density input", g[:2048], dD[:2048]), ("density output", g[2048:3072], dD[2048:]), ("colour input", g[3072:5120], dC[:2048]),
+                            ("colour hidden", g[5120:9216], dC[2048:6144]), ("colour output", g[9216:], dC[6144:])):
         err = _frob(got, want)
-        assert err < 1e-2, f"{name} dW: relative Frobenius error {err:.3e}"
-    want_t = orc.encode_backward(oracle_grid(c3_step["grid"]), p, dfeat)
-    err = _frob(c3_step["table_grad"], want_t)
-    assert err < 1e-2, f"table gradient: relative Frobenius error {err:.3e}"
+        print(f"[grad] C3 {name} dW: relative Frobenius {err:.3e}", flush=True)
+        assert err < 1e-3, f"{name} dW: relative Frobenius error {err:.3e}"
+    assert_rel_rows(c3_step["dfeat"], dfeat, what="C3 d features")
+    og = oracle_grid(c3_step["grid"])
+    floor = fixed_point_floor(c3_step["dfeat"])
+    assert_table_grad(c3_step["table_grad"], orc.encode_backward(og, p, c3_step["dfeat"]), 16, "C3 table gradient (scatter)", frob_tol=1e-3, floor=floor)
+    # End to end: the samples whose ReLU mask flipped move the few entries they touch.
+    assert_table_grad(c3_step["table_grad"], orc.encode_backward(og, p, dfeat), 16, "C3 table gradient (end to end)", frob_tol=1e-3, floor=floor, entry_frac=1e-4)
 
 
 def test_adam_reference_settings(scene):
