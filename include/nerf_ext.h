@@ -164,6 +164,21 @@ NERF_API NerfStatus nerf_ext_ref_field_forward(const uint16_t* density_params, c
  * accumulation; the colour network's input gradient flows into density
  * outputs 1..15 (:1069-1083).  n <= 2^20 per call. */
 NERF_API NerfStatus nerf_ext_ref_backward(const uint16_t* density_params, const uint16_t* color_params, const float* positions, const float* directions, const float* draw, uint32_t n, float loss_scale, float* ddensity, float* dcolor, void* stream);
+/* nerf_ext_ref_backward that also leaves the backward's per-layer fp16 rows
+ * for inspection, in caller-allocated device buffers: acts [1136][np] (the
+ * input of every layer, recomputed), dlts [1056][np] (the delta of every
+ * layer's output), np = n rounded up to 64, neuron-major in blocks of 32
+ * samples: row r of sample s at element (s / 32 * rows + r) * 32 + s % 32,
+ * rows = 1136 or 1056.  Layers 0..9 in the order density 64->128, 128->128
+ * x 4, 128->16, colour 48->128, 128->128 x 2, 128->16; layer l's input rows
+ * start at acts row {0, 64, 192, 320, 448, 576, 704, 752, 880, 1008}[l]
+ * (layer 0: the position encoding 63 + 1 zero; layer 6: [raw density 1..15 |
+ * direction encoding 27 | 0 x 6]) and its output delta rows at dlts row
+ * {0, 128, 256, 384, 512, 640, 656, 784, 912, 1040}[l] (layer 5: output 0 =
+ * fp16(loss_scale d raw sigma), outputs 1..15 = the colour input's geometry
+ * deltas; layer 9: fp16(loss_scale d raw r, g, b), then zeros). */
+NERF_API NerfStatus nerf_ext_ref_backward_rows(const uint16_t* density_params, const uint16_t* color_params, const float* positions, const float* directions, const float* draw, uint32_t n, float loss_scale, float* ddensity,
+                                             float* dcolor, uint16_t* acts, uint16_t* dlts, void* stream);
 NERF_API NerfStatus nerf_ext_ref_composite_backward(const uint32_t* counts, const uint32_t* offsets, const float* samples, const float* field, const float* gt, uint32_t n_rays, float inv_norm, float* draw, float* loss_sum, void* stream);
 /* The density and colour MLPs of nerf_ext_field_forward on given encodings:
  * features fp16 [n][32], unit directions [n][3] -> out [n][4] = (sigma, r, g, b).

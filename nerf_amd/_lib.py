@@ -349,6 +349,7 @@ PROTOTYPES: dict[str, tuple] = {
     "nerf_ext_ref_field_forward": (_S, [_P, _P, _P, _P, _U32, _P, _P, _P]),
     "nerf_ext_ref_composite_backward": (_S, [_P, _P, _P, _P, _P, _U32, _F, _P, _P, _P]),
     "nerf_ext_ref_backward": (_S, [_P, _P, _P, _P, _P, _U32, _F, _P, _P, _P]),
+    "nerf_ext_ref_backward_rows": (_S, [_P, _P, _P, _P, _P, _U32, _F, _P, _P, _P, _P, _P]),
     # scene
     "nerf_ext_scene_gaussians": (_S, [C.POINTER(NerfExtSceneDesc), _P]),
     "nerf_ext_scene_density": (_S, [_P, _U32, _P, _U32, _P, _P]),

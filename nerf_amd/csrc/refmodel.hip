@@ -1046,21 +1046,26 @@ NERF_API NerfStatus nerf_ext_ref_field_forward(const uint16_t* density_params, c
     return NERF_STATUS_OK;
 }
 
-NERF_API NerfStatus nerf_ext_ref_backward(const uint16_t* density_params, const uint16_t* color_params, const float* positions, const float* directions, const float* draw, uint32_t n, float loss_scale, float* ddensity,
-                                        float* dcolor, void* stream) {
+}  // extern "C"
+
+namespace {
+// nerf_ext_ref_backward, with the neuron-major rows in the caller's buffers
+// when acts_out / dlts_out are given (else in temporary ones).
+NerfStatus ref_backward(const char* who, const uint16_t* density_params, const uint16_t* color_params, const float* positions, const float* directions, const float* draw, uint32_t n, float loss_scale, float* ddensity,
+                        float* dcolor, uint16_t* acts_out, uint16_t* dlts_out, void* stream) {
     if (n == 0u) return NERF_STATUS_OK;
-    NERF_CHECK_ARG(density_params && color_params && positions && directions && draw && ddensity && dcolor, "nerf_ext_ref_backward: null pointer");
-    NERF_CHECK_ARG(n <= (1u << 20), "nerf_ext_ref_backward: at most 2^20 samples per call (buffer descriptors address < 4 GiB)");
+    NERF_CHECK_ARG(density_params && color_params && positions && directions && draw && ddensity && dcolor, std::string(who) + ": null pointer");
+    NERF_CHECK_ARG(n <= (1u << 20), std::string(who) + ": at most 2^20 samples per call (buffer descriptors address < 4 GiB)");
     hipStream_t st        = (hipStream_t)stream;
     const uint32_t np     = (n + 63u) / 64u * 64u;
     const uint32_t chunk  = kRefDwChunk;
     const uint32_t chunks = (np + chunk - 1u) / chunk;
     half8_t* frags = nullptr;
-    half_t *acts = nullptr, *dlts = nullptr;
+    half_t *acts = (half_t*)acts_out, *dlts = (half_t*)dlts_out;
     float* partial = nullptr;
     NERF_HIP_TRY(hipMallocAsync((void**)&frags, sizeof(half8_t) * 64u * kRefFragments, st));
-    NERF_HIP_TRY(hipMallocAsync((void**)&acts, sizeof(half_t) * (uint64_t)kActRows * np, st));
-    NERF_HIP_TRY(hipMallocAsync((void**)&dlts, sizeof(half_t) * (uint64_t)kDltRows * np, st));
+    if (!acts_out) NERF_HIP_TRY(hipMallocAsync((void**)&acts, sizeof(half_t) * (uint64_t)kActRows * np, st));
+    if (!dlts_out) NERF_HIP_TRY(hipMallocAsync((void**)&dlts, sizeof(half_t) * (uint64_t)kDltRows * np, st));
     NERF_HIP_TRY(hipMallocAsync((void**)&partial, sizeof(float) * (uint64_t)chunks * (kRefDensityParams + kRefColorParams), st));
     FieldInputs in{};
     in.positions  = positions;
@@ -1079,10 +1084,24 @@ NERF_API NerfStatus nerf_ext_ref_backward(const uint16_t* density_params, const 
         k_ref_dw_reduce<<<kRefReduceBlocks, 256, 0, st>>>(partial, chunks, ddensity, dcolor, nullptr);
         e = hipGetLastError();
     }
-    const hipError_t f[4] = {hipFreeAsync(partial, st), hipFreeAsync(dlts, st), hipFreeAsync(acts, st), hipFreeAsync(frags, st)};
+    const hipError_t f[4] = {hipFreeAsync(partial, st), dlts_out ? hipSuccess : hipFreeAsync(dlts, st), acts_out ? hipSuccess : hipFreeAsync(acts, st), hipFreeAsync(frags, st)};
     NERF_HIP_TRY(e);
     for (hipError_t x : f) NERF_HIP_TRY(x);
     return NERF_STATUS_OK;
+}
+}  // namespace
+
+extern "C" {
+
+NERF_API NerfStatus nerf_ext_ref_backward(const uint16_t* density_params, const uint16_t* color_params, const float* positions, const float* directions, const float* draw, uint32_t n, float loss_scale, float* ddensity,
+                                        float* dcolor, void* stream) {
+    return ref_backward("nerf_ext_ref_backward", density_params, color_params, positions, directions, draw, n, loss_scale, ddensity, dcolor, nullptr, nullptr, stream);
+}
+
+NERF_API NerfStatus nerf_ext_ref_backward_rows(const uint16_t* density_params, const uint16_t* color_params, const float* positions, const float* directions, const float* draw, uint32_t n, float loss_scale, float* ddensity,
+                                             float* dcolor, uint16_t* acts, uint16_t* dlts, void* stream) {
+    NERF_CHECK_ARG(n == 0u || (acts && dlts), "nerf_ext_ref_backward_rows: null row buffer");
+    return ref_backward("nerf_ext_ref_backward_rows", density_params, color_params, positions, directions, draw, n, loss_scale, ddensity, dcolor, acts, dlts, stream);
 }
 
 NERF_API NerfStatus nerf_ext_ref_composite_backward(const uint32_t* counts, const uint32_t* offsets, const float* samples, const float* field, const float* gt, uint32_t n_rays, float inv_norm, float* draw, float* loss_sum,

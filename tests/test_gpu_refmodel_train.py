@@ -107,7 +107,8 @@ def test_ref_forward_stage(step):
     # Ten fp16-rounded 128-wide layers: a rounding flip early on reaches every
     # later layer, so the bars are 2e-3 of the channel scale and 1e-3 for
     # 99.9 % of outputs (measured after one Adam step: 1.1e-3 and 7.9e-4)
-    # rather than the small MLPs' 1e-3 and 1e-4.
+    # rather than the small MLPs' 1e-3 and 1e-4.  Each layer on its own is
+    # held to one fp16 ulp in tests/test_gpu_refmodel_layers.py.
     assert_rel(step["field"], want, rtol=2e-3, what="reference-model field (sigma, rgb) in the trainer", mlp=True, bulk_rtol=1e-3)
 
 
