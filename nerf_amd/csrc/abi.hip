@@ -75,14 +75,39 @@ NerfStatus Context::upload_weights(const float* mlp32, const float* t32) {
     return NERF_STATUS_OK;
 }
 
-void Context::free_model() {
-    for (void* p : {(void*)table, (void*)table_f32, (void*)dparams, (void*)cparams, (void*)mlp_f32})
-        if (p) (void)hipFree(p);
+Context::ModelSlot Context::take_model() {
+    const ModelSlot m{model_kind, grid, grid_params, table_elems, table, table_f32, dparams, cparams, mlp_f32};
     table     = nullptr;
     table_f32 = nullptr;
     dparams = cparams = nullptr;
     mlp_f32     = nullptr;
     table_elems = 0;
+    return m;
+}
+
+void Context::put_model(const ModelSlot& m) {
+    model_kind  = m.kind;
+    grid        = m.grid;
+    grid_params = m.grid_params;
+    table_elems = m.table_elems;
+    table       = m.table;
+    table_f32   = m.table_f32;
+    dparams     = m.dparams;
+    cparams     = m.cparams;
+    mlp_f32     = m.mlp_f32;
+}
+
+void Context::free_slot(ModelSlot& m) {
+    for (void* p : {(void*)m.table, (void*)m.table_f32, (void*)m.dparams, (void*)m.cparams, (void*)m.mlp_f32})
+        if (p) (void)hipFree(p);
+    m.table = m.table_f32 = nullptr;
+    m.dparams = m.cparams = nullptr;
+    m.mlp_f32 = nullptr;
+}
+
+void Context::free_model() {
+    ModelSlot m = take_model();
+    free_slot(m);
 }
 
 NerfStatus Context::init_model() {
@@ -118,14 +143,26 @@ NerfStatus Context::init_model() {
 
 NerfStatus Context::switch_model(uint32_t kind) {
     if (kind == model_kind) return NERF_STATUS_OK;
-    const bool was_training        = training_configured;
-    const NerfTrainingConfig saved = train_config;
-    train_release();
     if (stream) NERF_HIP_TRY(hipStreamSynchronize(stream));
-    free_model();
-    model_kind   = kind;
-    NerfStatus s = init_model();
-    if (s != NERF_STATUS_OK) return s;
+    // Build the new model (and, when training is configured, its trainer for
+    // the same config) beside the current ones; commit only if all of it
+    // succeeds.
+    ModelSlot old = take_model();
+    model_kind    = kind;
+    NerfStatus s  = init_model();
+    Trainer* nt   = nullptr;
+    if (s == NERF_STATUS_OK && training_configured) s = train_build(train_config, &nt);
+    if (s != NERF_STATUS_OK) {
+        if (stream) (void)hipStreamSynchronize(stream);
+        free_model();
+        put_model(old);
+        return s;
+    }
+    const bool was_training = training_configured;
+    train_release();  // the previous run borrowed the previous model
+    train               = nt;
+    training_configured = was_training;
+    free_slot(old);
     const uint64_t cells = (uint64_t)occupancy_res * occupancy_res * occupancy_res;
     if (cells) {
         NERF_HIP_TRY(hipMemsetAsync(bitfield, 0, (cells + 31u) / 32u * 4u, stream));
@@ -133,7 +170,7 @@ NerfStatus Context::switch_model(uint32_t kind) {
         NERF_HIP_TRY(hipStreamSynchronize(stream));
     }
     host_generation = 0u;
-    return was_training ? train_configure_locked(saved) : NERF_STATUS_OK;
+    return NERF_STATUS_OK;
 }
 
 NerfExtModel Context::model() const {
@@ -400,8 +437,8 @@ NERF_API NerfStatus nerf_ext_context_configure(void* context, const NerfExtConte
     NERF_CHECK_ARG(options->inference_sampling <= NERF_EXT_SAMPLING_MARCH, "nerf_ext_context_configure: unknown inference_sampling");
     Context* ctx = static_cast<Context*>(context);
     std::scoped_lock lock(ctx->mutex);
-    const NerfStatus s      = ctx->switch_model(options->model_kind);
-    ctx->inference_sampling = options->inference_sampling;
+    const NerfStatus s = ctx->switch_model(options->model_kind);
+    if (s == NERF_STATUS_OK) ctx->inference_sampling = options->inference_sampling;  // a failed switch changes nothing
     return s;
 }
 

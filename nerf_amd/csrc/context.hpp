@@ -64,11 +64,31 @@ struct Context {
     void free_model();
     // Replaces the model by a freshly initialised one of `kind`, clears the
     // occupancy grid and rebuilds a configured training run for it (caller
-    // holds the mutex).
+    // holds the mutex).  Atomic: the new model and trainer are built beside
+    // the current ones, and on any failure the context is left as it was.
     NerfStatus switch_model(uint32_t kind);
     NerfStatus upload_weights(const float* mlp32, const float* t32);
     NerfExtModel model() const;
-    // Builds the trainer for config c (caller holds the mutex).
+    // The model's buffers, moved out of (take) or into (put) the context.
+    struct ModelSlot {
+        uint32_t kind;
+        NerfExtGridDesc grid;
+        GridParams grid_params;
+        uint64_t table_elems;
+        void* table;
+        float* table_f32;
+        uint16_t* dparams;
+        uint16_t* cparams;
+        float* mlp_f32;
+    };
+    ModelSlot take_model();
+    void put_model(const ModelSlot& m);
+    static void free_slot(ModelSlot& m);
+    // Builds a trainer for config c and the current model without changing
+    // the context (caller holds the mutex).
+    NerfStatus train_build(const NerfTrainingConfig& c, Trainer** out);
+    // Replaces the training run by one for config c; on failure the previous
+    // run stays (caller holds the mutex).
     NerfStatus train_configure_locked(const NerfTrainingConfig& c);
     // Zeroes optimiser moments, gradients, occupancy and the step counter.
     NerfStatus train_reset_state();

@@ -21,12 +21,13 @@ void Context::train_release() {
     training_configured = false;
 }
 
-// The trainer of a validated NerfTrainingConfig: it borrows the context's
-// model and occupancy buffers; rays_per_batch rays per step,
+// The trainer of a validated NerfTrainingConfig for the context's current
+// model, built without touching the context: it borrows the context's model,
+// occupancy buffers and device images; rays_per_batch rays per step,
 // max_sample_steps_per_ray as the march budget, a stream of rays_per_batch *
 // max_sample_steps_per_ray samples (no ray is ever cut).
-NerfStatus Context::train_configure_locked(const NerfTrainingConfig& c) {
-    train_release();
+NerfStatus Context::train_build(const NerfTrainingConfig& c, Trainer** out) {
+    *out = nullptr;
     const uint64_t total = (uint64_t)c.rays_per_batch * c.max_sample_steps_per_ray;
     std::vector<NerfExtCamera> cams(image_count);
     for (uint32_t i = 0; i < image_count; ++i) {
@@ -40,13 +41,9 @@ NerfStatus Context::train_configure_locked(const NerfTrainingConfig& c) {
         cams[i].width  = width;
         cams[i].height = height;
     }
-    // The trainer takes the dataset from host memory; the context keeps its
-    // own device copy only for its lifetime, so copy the images back once.
-    std::vector<uint8_t> host_images((uint64_t)image_count * width * height * 4u);
-    if (!host_images.empty() && hipMemcpy(host_images.data(), images, host_images.size(), hipMemcpyDeviceToHost) != hipSuccess) return NERF_STATUS_CUDA_ERROR;
     NerfExtTrainDesc d{};
     d.grid          = grid;
-    d.images_rgba8  = host_images.data();
+    d.images_rgba8  = nullptr;  // borrowed on the device below
     d.cameras       = cams.data();
     d.image_count   = image_count;
     d.occupancy_res = occupancy_res;
@@ -66,10 +63,18 @@ NerfStatus Context::train_configure_locked(const NerfTrainingConfig& c) {
     d.huber_delta       = 0.1f;
     d.model_kind        = model_kind;
     if (d.hyper.loss_scale <= 0.0f) d.hyper.loss_scale = 1.0f;
-    const BorrowedModel bm{(half_t*)table, table_f32, (half_t*)dparams, (half_t*)cparams, mlp_f32, bitfield, density_grid};
+    const BorrowedModel bm{(half_t*)table, table_f32, (half_t*)dparams, (half_t*)cparams, mlp_f32, bitfield, density_grid, images};
+    const NerfStatus s = trainer_create(&d, &bm, stream, out);
+    return s == NERF_STATUS_OK || s == NERF_STATUS_INVALID_USAGE ? s : NERF_STATUS_CUDA_ERROR;
+}
+
+// Replaces the training run by one for config c; on failure the previous
+// run stays configured.
+NerfStatus Context::train_configure_locked(const NerfTrainingConfig& c) {
     Trainer* t         = nullptr;
-    const NerfStatus s = trainer_create(&d, &bm, stream, &t);
-    if (s != NERF_STATUS_OK) return s == NERF_STATUS_INVALID_USAGE ? s : NERF_STATUS_CUDA_ERROR;
+    const NerfStatus s = train_build(c, &t);
+    if (s != NERF_STATUS_OK) return s;
+    train_release();
     train               = t;
     train_config        = c;
     host_generation     = 0u;

@@ -45,7 +45,7 @@ NerfStatus Trainer::run_stages(uint32_t first, uint32_t last) {
 NerfStatus trainer_create(const NerfExtTrainDesc* d, const BorrowedModel* borrowed, hipStream_t stream, Trainer** out) {
     NERF_CHECK_ARG(d && out, "trainer: null argument");
     *out = nullptr;
-    NERF_CHECK_ARG(d->image_count >= 1u && d->cameras && d->images_rgba8, "trainer: a dataset of at least one image is required");
+    NERF_CHECK_ARG(d->image_count >= 1u && d->cameras && (d->images_rgba8 || (borrowed && borrowed->images)), "trainer: a dataset of at least one image is required");
     NERF_CHECK_ARG(d->model_kind <= NERF_EXT_MODEL_REFERENCE, "trainer: unknown model_kind");
     const bool ref = d->model_kind == NERF_EXT_MODEL_REFERENCE;
     NERF_CHECK_ARG(ref || d->grid.table_dtype == NERF_EXT_F16, "trainer: the hash table must be fp16");
@@ -118,9 +118,13 @@ NerfStatus trainer_create(const NerfExtTrainDesc* d, const BorrowedModel* borrow
     NerfExtCamera* cams = nullptr;
     NERF_HIP_TRY(alloc(T, cams, d->image_count));
     B.cams = cams;
-    uint8_t* images = nullptr;
-    NERF_HIP_TRY(alloc(T, images, (uint64_t)d->image_count * W * H * 4u));
-    B.images = images;
+    uint8_t* images = nullptr;  // the trainer's own copy, unless the dataset is borrowed on the device
+    if (borrowed && borrowed->images) {
+        B.images = borrowed->images;
+    } else {
+        NERF_HIP_TRY(alloc(T, images, (uint64_t)d->image_count * W * H * 4u));
+        B.images = images;
+    }
     NERF_HIP_TRY(alloc(T, B.rays, 2ull * P.max_rays));
     NERF_HIP_TRY(alloc(T, B.gt, P.max_rays));
     NERF_HIP_TRY(alloc(T, B.counts, P.max_rays));
@@ -215,7 +219,7 @@ NerfStatus trainer_create(const NerfExtTrainDesc* d, const BorrowedModel* borrow
     }
     hipStream_t s = T.stream;
     NERF_HIP_TRY(hipMemcpyAsync(cams, d->cameras, sizeof(NerfExtCamera) * d->image_count, hipMemcpyHostToDevice, s));
-    NERF_HIP_TRY(hipMemcpyAsync(images, d->images_rgba8, (uint64_t)d->image_count * W * H * 4u, hipMemcpyHostToDevice, s));
+    if (images) NERF_HIP_TRY(hipMemcpyAsync(images, d->images_rgba8, (uint64_t)d->image_count * W * H * 4u, hipMemcpyHostToDevice, s));
     T.initial_rays = (float)(d->initial_rays ? d->initial_rays : 1u);
     st             = T.reset();
     if (st != NERF_STATUS_OK) return st;

@@ -18,6 +18,7 @@ struct BorrowedModel {
     float* mlp_f32;
     uint32_t* bits;
     float* density;
+    const uint8_t* images;  // device RGBA8 dataset, or null: the trainer copies desc->images_rgba8 (host)
 };
 
 struct Trainer {

@@ -216,3 +216,50 @@ def test_render_uniform_views_and_background(dataset):
         g = got_rgb[v].reshape(-1, 3)[rays]
         assert np.max(np.abs(g - want_rgb) / np.maximum(np.abs(want_rgb), 1e-3)) <= 1e-3
         _close_rgba(rgba.numpy()[v].ravel()[rays], want_rgba)
+
+
+def test_failed_model_switch_leaves_the_context(dataset, tmp_path):
+    """A switch that the new model cannot take (the reference model trains on
+    at most 2^20 samples per step; this context trains the hash grid on
+    8,192 x 256 = 2^21) fails as a whole: the model, its weights, the
+    training run and the inference sampling stay as they were, whether the
+    switch comes from nerf_ext_context_configure or from loading a reference
+    checkpoint."""
+    cams, imgs, mats = dataset
+    announce("nerf.h context: failed model switch (2^21 samples per step) leaves the context unchanged")
+    ref_ctx = Context(dataset)
+    try:
+        _configure(ref_ctx, L.NERF_EXT_MODEL_REFERENCE)
+        ref_path = tmp_path / "ref.ckpt"
+        ref_ctx.save(ref_path)
+    finally:
+        ref_ctx.close()
+    ctx = Context.__new__(Context)
+    ctx._keep = (imgs, mats)
+    d = L.NerfCreateDesc(32, 1 << 22, 8192, 256, imgs.ctypes.data, imgs.nbytes, mats.ctypes.data, mats.nbytes, VIEWS, W, H, cams[0].fx, cams[0].fy, cams[0].cx, cams[0].cy)
+    ctx.h = C.c_void_p()
+    L.call("nerf_create_context", C.byref(d), C.byref(ctx.h))
+    try:
+        L.call("nerf_configure_training", ctx.h, C.byref(_config(rays=8192, steps=256)))
+        for _ in range(2):
+            L.call("nerf_train_step", ctx.h)
+        before = tmp_path / "before.ckpt"
+        ctx.save(before)
+        img0, _ = ctx.infer(1, samples=64)
+        assert ctx.status("nerf_ext_context_configure", C.byref(L.NerfExtContextOptions(L.NERF_EXT_MODEL_REFERENCE, L.NERF_EXT_SAMPLING_UNIFORM))) == L.NERF_STATUS_INVALID_USAGE
+        assert "2^20" in L.last_error()
+        assert _options(ctx) == (L.NERF_EXT_MODEL_HASHGRID, L.NERF_EXT_SAMPLING_DEFAULT)
+        assert ctx.load(ref_path) == L.NERF_STATUS_INVALID_USAGE
+        assert _options(ctx) == (L.NERF_EXT_MODEL_HASHGRID, L.NERF_EXT_SAMPLING_DEFAULT)
+        after = tmp_path / "after.ckpt"
+        ctx.save(after)
+        assert open(after, "rb").read() == open(before, "rb").read(), "the weights changed"
+        img1, _ = ctx.infer(1, samples=64)
+        assert np.array_equal(img0, img1)
+        # Training is still configured and continues from its step count.
+        L.call("nerf_train_step", ctx.h)
+        st = L.NerfTrainStats()
+        L.call("nerf_read_train_stats", ctx.h, C.byref(st))
+        assert st.completed_steps == 3 and st.has_nonfinite == 0
+    finally:
+        ctx.close()
