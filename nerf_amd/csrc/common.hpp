@@ -426,6 +426,46 @@ struct FieldInputs {
     // encodes the unit cube, so they are mapped by (p - bmin) / (bmax - bmin).
     float bmin[3];
     float bmax[3];
+    // Mode B with features_out, fp16 table: the samples are far apart (a few
+    // march steps per ray), so caches see no reuse between them and the
+    // table is gathered level group by level group, each on its own XCD
+    // (whose L2 then holds those levels), followed by the MLPs as a pass over
+    // the features.  Same values as the fused kernel.
+    bool sparse;
+};
+
+struct PointsFromSamples {
+    const float2* samples;
+    const uint32_t* sample_ray;
+    const float4* rays;
+    const uint32_t* n_dev;
+    uint32_t cap;
+    float bmin[3], bmax[3];
+    __device__ __forceinline__ uint32_t count() const { return n_dev ? min(*n_dev, cap) : cap; }
+    __device__ __forceinline__ void at(uint32_t q, float x[3]) const {
+        const float2 td  = samples[q];
+        const uint32_t r = sample_ray[q];
+        const float4 ro  = rays[2ull * r];
+        const float4 rd  = rays[2ull * r + 1ull];
+        const float w[3] = {ro.x + td.x * rd.x, ro.y + td.x * rd.y, ro.z + td.x * rd.z};
+#pragma unroll
+        for (int a = 0; a < 3; ++a) x[a] = (w[a] - bmin[a]) / (bmax[a] - bmin[a]);
+    }
+};
+
+// Point sources of the XCD-split encode (hashgrid.hip): positions in the
+// grid's unit cube from an array, or from a march sample stream (FieldInputs
+// mode B, the same operations as the field kernels use).
+struct PointsFromArray {
+    const float* pos;
+    uint32_t n;
+    __device__ __forceinline__ uint32_t count() const { return n; }
+    __device__ __forceinline__ void at(uint32_t i, float x[3]) const {
+        const float3 p = *reinterpret_cast<const float3*>(pos + 3ull * i);
+        x[0]           = p.x;
+        x[1]           = p.y;
+        x[2]           = p.z;
+    }
 };
 
 struct FieldWeights {
@@ -433,6 +473,9 @@ struct FieldWeights {
     const half_t* color;    // 7168
 };
 
+// XCD-split encode of a sample stream's positions into fp16 features [n][32]
+// (16-level grids, fp16 table), the sample count read on the device.
+hipError_t launch_encode_samples(const GridParams& g, const half_t* table, const FieldInputs& in, uint32_t cap, half_t* features, hipStream_t stream);
 // out4 [n] float4 (sigma, r, g, b).
 hipError_t launch_field(const GridParams& g, const void* table, const FieldWeights& w, const FieldInputs& in, uint32_t n, float4* out4, hipStream_t stream);
 // Density network only, on points or on fp16 features: out [n][16] = (exp(raw0), raw1..15).

@@ -316,8 +316,37 @@ __global__ __launch_bounds__(kBlockThreads) void k_field_forward_lv(GridParams g
 // costs 80 VGPRs per lane and limits the pass to 3 waves per SIMD; this way
 // it runs 4 (2^24 samples: 434 vs 445 us; 2^18: 12.4 vs 17.7 us, where
 // staging the weights once per workgroup dominated), with identical results.
+//
+// Directions come from a source: an array [n][3], or the owning rays of a
+// march sample stream whose count is read on the device.
+struct DirsFromArray {
+    const float* dirs;
+    uint32_t n;
+    __device__ __forceinline__ uint32_t count() const { return n; }
+    __device__ __forceinline__ void at(uint32_t q, float d[3]) const {
+#pragma unroll
+        for (int a = 0; a < 3; ++a) d[a] = dirs[3ull * q + a];
+    }
+};
+
+struct DirsFromSamples {
+    const uint32_t* sample_ray;
+    const float4* rays;
+    const uint32_t* n_dev;
+    uint32_t cap;
+    __device__ __forceinline__ uint32_t count() const { return n_dev ? min(*n_dev, cap) : cap; }
+    __device__ __forceinline__ void at(uint32_t q, float d[3]) const {
+        const float4 rd = rays[2ull * sample_ray[q] + 1ull];
+        d[0]            = rd.x;
+        d[1]            = rd.y;
+        d[2]            = rd.z;
+    }
+};
+
+template <typename Dirs>
 __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(kMlpWaves, 8))) void k_field_mlp(const half_t* __restrict__ dparams, const half_t* __restrict__ cparams, const half_t* __restrict__ features,
-                                                                                                                  const float* __restrict__ dirs, uint32_t n, float4* __restrict__ out) {
+                                                                                                                  Dirs dirs, float4* __restrict__ out) {
+    const uint32_t n = dirs.count();
     __shared__ __align__(16) half8_t frag[kFieldFrags][kWaveSize];
     __shared__ half4_t shl[kBlockWaves][kGroupSamples][4];
     const uint32_t lane = threadIdx.x & 63u, grp = lane >> 4, s16 = lane & 15u, wv = threadIdx.x >> 6;
@@ -339,8 +368,8 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
             const uint32_t q = min(base + 16u * t + s16, n - 1u);
             x[t]             = *reinterpret_cast<const half8_t*>(features + (uint64_t)q * 32u + 8u * grp);
         }
-        const uint32_t ql = min(base + lane, n - 1u);
-        const float d[3]  = {dirs[3ull * ql], dirs[3ull * ql + 1u], dirs[3ull * ql + 2u]};
+        float d[3];
+        dirs.at(min(base + lane, n - 1u), d);
         float sh[16];
         sh16(d, sh);
 #pragma unroll
@@ -392,6 +421,13 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
     }
 }
 
+// One workgroup per CU for each wave per SIMD the MLP pass's register budget
+// keeps resident, so every workgroup builds the fragments once and stays.
+uint32_t mlp_pass_blocks(uint32_t n) {
+    const uint32_t groups = (n + kGroupSamples - 1u) / kGroupSamples;
+    return max(1u, min((groups + kBlockWaves - 1u) / kBlockWaves, device_cu_count() * kMlpWaves));
+}
+
 uint32_t persistent_blocks(uint32_t n, uint32_t per_cu) {
     const uint32_t tiles  = (n + 15u) / 16u;
     const uint32_t needed = (tiles + kBlockWaves - 1u) / kBlockWaves;
@@ -416,6 +452,14 @@ hipError_t launch_field(const GridParams& g, const void* table, const FieldWeigh
     const bool level_major  = n > (1u << 20);
     const uint32_t blocks   = (persistent_blocks(n, level_major ? 3u : 4u) + 7u) / 8u * 8u;  // whole XCD rounds
     const bool from_samples = in.samples != nullptr;
+    if (in.sparse && from_samples && in.features_out && !in.sample_index && !in.alpha_in_order && g.table_dtype != NERF_EXT_F32 && g.n_levels == 16u) {
+        // Sparse samples: encode level group by level group, one group per
+        // XCD, into features_out, then the MLPs over those features.
+        const hipError_t e = launch_encode_samples(g, (const half_t*)table, in, n, in.features_out, stream);
+        if (e != hipSuccess) return e;
+        k_field_mlp<<<mlp_pass_blocks(n), kBlockThreads, 0, stream>>>(w.density, w.color, in.features_out, DirsFromSamples{in.sample_ray, in.rays, in.n_dev, n}, out4);
+        return hipGetLastError();
+    }
 #define NERF_FIELD_LAUNCH(K)                                                                                                                   \
     do {                                                                                                                                       \
         if (g.table_dtype == NERF_EXT_F32) {                                                                                                   \
@@ -516,11 +560,7 @@ NERF_API NerfStatus nerf_ext_field_mlp(const uint16_t* density_params, const uin
     if (n == 0u) return NERF_STATUS_OK;
     NERF_CHECK_ARG(density_params && color_params && features && directions && out, "nerf_ext_field_mlp: null pointer");
     NERF_CHECK_ARG(((uintptr_t)features & 15u) == 0u, "nerf_ext_field_mlp: features must be 16-byte aligned");
-    // One workgroup per CU for each wave per SIMD the register budget keeps
-    // resident, so every workgroup builds the fragments once and stays.
-    const uint32_t groups = (n + kGroupSamples - 1u) / kGroupSamples;
-    const uint32_t blocks = min((groups + kBlockWaves - 1u) / kBlockWaves, device_cu_count() * kMlpWaves);
-    k_field_mlp<<<blocks, kBlockThreads, 0, (hipStream_t)stream>>>((const half_t*)density_params, (const half_t*)color_params, (const half_t*)features, directions, n, reinterpret_cast<float4*>(out));
+    k_field_mlp<<<mlp_pass_blocks(n), kBlockThreads, 0, (hipStream_t)stream>>>((const half_t*)density_params, (const half_t*)color_params, (const half_t*)features, DirsFromArray{directions, n}, reinterpret_cast<float4*>(out));
     NERF_LAUNCH_CHECK("k_field_mlp");
     return NERF_STATUS_OK;
 }

@@ -106,19 +106,22 @@ __global__ __launch_bounds__(256) void k_encode_tile(GridParams g, const TableT*
 // them for each other's points in one load instruction (one cache line per
 // point and edge; encode_level_lanepair), so every lane runs the gathers and
 // only lanes holding a point store.
-template <typename TableT, typename OutT, uint32_t kLevels>
-__global__ __launch_bounds__(256) void k_encode_split(GridParams g, const TableT* __restrict__ table, const float* __restrict__ pos, uint32_t n, OutT* __restrict__ out, bool nt) {
+// Points come from a source (PointsFromArray, PointsFromSamples) whose count
+// may be read on the device.
+template <typename TableT, typename OutT, uint32_t kLevels, typename Points>
+__global__ __launch_bounds__(256) void k_encode_split(GridParams g, const TableT* __restrict__ table, Points src, OutT* __restrict__ out, bool nt) {
     constexpr uint32_t kParts = kLevels / 2u;  // XCDs sharing one level group
     const uint32_t xcd = blockIdx.x & 7u, group = xcd % (8u / kParts), part = xcd / (8u / kParts);
     const uint32_t slot = blockIdx.x >> 3, slots = gridDim.x >> 3;
     const uint32_t l0 = kLevels * group;
     if (l0 >= g.n_levels) return;  // uniform per workgroup
+    const uint32_t n = src.count();
     const uint32_t width = 2u * g.n_levels;
     for (uint32_t blk = slot * kParts + part; blk * 256u < n; blk += slots * kParts) {
         const uint32_t i  = blk * 256u + threadIdx.x;
         const uint32_t iq = i < n ? i : n - 1u;
-        const float3 xp   = *reinterpret_cast<const float3*>(pos + 3ull * iq);
-        const float x[3] = {xp.x, xp.y, xp.z};
+        float x[3];
+        src.at(iq, x);
         float f[2u * kLevels];
 #pragma unroll
         for (uint32_t j = 0; j < kLevels; ++j) {
@@ -186,6 +189,20 @@ __global__ __launch_bounds__(256) void k_encode_indices(GridParams g, const floa
     }
 }
 
+hipError_t launch_encode_samples(const GridParams& g, const half_t* table, const FieldInputs& in, uint32_t cap, half_t* features, hipStream_t stream) {
+    if (cap == 0u) return hipSuccess;
+    if (g.n_levels != 16u || g.table_dtype != NERF_EXT_F16) return hipErrorInvalidValue;
+    PointsFromSamples src{in.samples, in.sample_ray, in.rays, in.n_dev, cap, {in.bmin[0], in.bmin[1], in.bmin[2]}, {in.bmax[0], in.bmax[1], in.bmax[2]}};
+    const uint64_t level_bytes = (uint64_t)g.table_size * g.n_features * 2u;
+    const uint32_t blocks_256  = (cap + 255u) / 256u;
+    // Four levels per XCD when four fit in half of its L2, else two.
+    if (4u * level_bytes <= (2ull << 20))
+        k_encode_split<half_t, half_t, 4u><<<8u * ((blocks_256 + 1u) / 2u), 256, 0, stream>>>(g, table, src, features, false);
+    else
+        k_encode_split<half_t, half_t, 2u><<<8u * blocks_256, 256, 0, stream>>>(g, table, src, features, false);
+    return hipGetLastError();
+}
+
 }  // namespace nerf_hip
 
 using namespace nerf_hip;
@@ -230,11 +247,13 @@ NERF_API NerfStatus nerf_ext_encode_forward(const NerfExtGridDesc* grid, const v
     NERF_CHECK_ARG(table && positions && features, "nerf_ext_encode_forward: null pointer");
     NERF_CHECK_ARG(features_dtype == NERF_EXT_F32 || features_dtype == NERF_EXT_F16, "nerf_ext_encode_forward: bad features dtype");
     hipStream_t st = (hipStream_t)stream;
-    // Level split when two levels of the table fit in half of one XCD's L2
-    // (4 MiB), four levels per XCD when four fit (16-level grids only);
-    // otherwise every workgroup gathers all levels.
+    // Level split when two levels of the table fit in one XCD's L2 (4 MiB),
+    // four levels per XCD when four fit in half of it (16-level grids only);
+    // otherwise every workgroup gathers all levels.  (fp16 T = 2^19, two 2 MiB
+    // levels per XCD: 2^18 random points 188 -> 113 us against all levels
+    // per workgroup.)
     const uint64_t level_bytes = (uint64_t)g.table_size * g.n_features * (g.table_dtype == NERF_EXT_F32 ? 4u : 2u);
-    const bool split           = 2u * level_bytes <= (2ull << 20);
+    const bool split           = 2u * level_bytes <= (4ull << 20);
     const bool quad            = split && g.n_levels == 16u && 4u * level_bytes <= (2ull << 20);
     // One point per thread (no persistent grid): workgroups that finish early
     // are replaced by new ones, so the CUs stay full to the end instead of
@@ -245,9 +264,9 @@ NERF_API NerfStatus nerf_ext_encode_forward(const NerfExtGridDesc* grid, const v
 #define NERF_ENC(TT, OT)                                                                                                   \
     do {                                                                                                                   \
         if (quad)                                                                                                          \
-            k_encode_split<TT, OT, 4u><<<grid_dim, 256, 0, st>>>(g, (const TT*)table, positions, n, (OT*)features, nt);  \
+            k_encode_split<TT, OT, 4u><<<grid_dim, 256, 0, st>>>(g, (const TT*)table, PointsFromArray{positions, n}, (OT*)features, nt);  \
         else if (split)                                                                                                    \
-            k_encode_split<TT, OT, 2u><<<grid_dim, 256, 0, st>>>(g, (const TT*)table, positions, n, (OT*)features, nt);  \
+            k_encode_split<TT, OT, 2u><<<grid_dim, 256, 0, st>>>(g, (const TT*)table, PointsFromArray{positions, n}, (OT*)features, nt);  \
         else                                                                                                               \
             k_encode_tile<TT, OT><<<grid_dim, 256, 0, st>>>(g, (const TT*)table, positions, n, (OT*)features);             \
     } while (0)

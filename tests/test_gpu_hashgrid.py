@@ -43,9 +43,9 @@ def test_indices_bit_exact(log2_t, finest):
 
 
 # Launch shapes covered: four levels per XCD (fp32 T = 2^16, fp16 T = 2^17),
-# two levels per XCD (fp32 T = 2^17), all levels per workgroup (fp16
-# T = 2^19); point counts that are and are not multiples of the 256-point
-# blocks.
+# two levels per XCD (fp32 T = 2^17 and 2^18, fp16 T = 2^19), all levels per
+# workgroup (fp16 T = 2^20); point counts that are and are not multiples of
+# the 256-point blocks.
 @pytest.mark.parametrize(
     "table_dtype,out_dtype,log2_t,n",
     [
@@ -55,6 +55,8 @@ def test_indices_bit_exact(log2_t, finest):
         (L.NERF_EXT_F32, np.float32, 17, 3001),
         (L.NERF_EXT_F16, np.float32, 19, 1 << 16),
         (L.NERF_EXT_F16, np.float16, 19, 1 << 16),
+        (L.NERF_EXT_F32, np.float32, 18, 4099),
+        (L.NERF_EXT_F16, np.float16, 20, 5000),
     ],
 )
 def test_encode_forward(table_dtype, out_dtype, log2_t, n):

@@ -136,3 +136,26 @@ def test_field_mlp_on_features(n):
     synchronize()
     want = orc.field_mlp(dp, cp, feats.astype(np.float32), dirs)
     assert_rel(d_o.numpy(), want, what="field mlp", mlp=True)
+
+
+@pytest.mark.parametrize("log2_t", [17, 19])
+def test_split_encode_then_mlp_equals_fused_field(log2_t):
+    """The sparse training forward (level-split encode into fp16 features,
+    then the MLP pass) gives the fused tile kernel's outputs bit for bit:
+    same corner entries, weights and summation order, same fp16 rounding of
+    the features and SH coefficients, same MFMA chain.  T = 2^17 takes four
+    levels per XCD, T = 2^19 two."""
+    n = 1 << 16
+    announce(f"split encode + field mlp vs fused field forward, T=2^{log2_t}, n={n}")
+    desc = ext.grid_desc(log2_t, L.NERF_EXT_F16)
+    model = ext.Model.create(desc, seed=2, table_range=1.0)
+    pos, dirs = points(n, seed=21), unit_dirs(n, seed=22)
+    d_pos, d_dir = DeviceArray.from_numpy(pos), DeviceArray.from_numpy(dirs)
+    feats = DeviceArray((n, 32), np.float16)
+    split, fused = DeviceArray((n, 4), np.float32), DeviceArray((n, 4), np.float32)
+    ext.encode_forward(desc, model.table, d_pos, n, feats)
+    L.call("nerf_ext_field_mlp", model.density.ptr, model.color.ptr, feats.ptr, d_dir.ptr, n, split.ptr, None)
+    L.call("nerf_ext_field_forward", byref(model.struct()), d_pos.ptr, d_dir.ptr, n, fused.ptr, None)
+    synchronize()
+    diff = np.count_nonzero(split.numpy().view(np.uint32) != fused.numpy().view(np.uint32))
+    assert diff == 0, f"{diff} of {4 * n} values differ"
