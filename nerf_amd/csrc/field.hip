@@ -421,11 +421,14 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
     }
 }
 
-// One workgroup per CU for each wave per SIMD the MLP pass's register budget
-// keeps resident, so every workgroup builds the fragments once and stays.
+// Twice as many workgroups as stay resident (4 per CU at 4 waves per SIMD):
+// the second half refills CUs whose first workgroups finish early, which
+// evens out the end of the pass (2^22 samples: 4 per CU 103-110 us, 6 per CU
+// 96-100 us, 8 per CU 97-99 us, 16 per CU 99 us); the fragment build per
+// workgroup (20 KiB from L2) stays small beside the groups each one runs.
 uint32_t mlp_pass_blocks(uint32_t n) {
     const uint32_t groups = (n + kGroupSamples - 1u) / kGroupSamples;
-    return max(1u, min((groups + kBlockWaves - 1u) / kBlockWaves, device_cu_count() * kMlpWaves));
+    return max(1u, min((groups + kBlockWaves - 1u) / kBlockWaves, device_cu_count() * 2u * kMlpWaves));
 }
 
 uint32_t persistent_blocks(uint32_t n, uint32_t per_cu) {

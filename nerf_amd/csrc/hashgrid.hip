@@ -98,7 +98,9 @@ __global__ __launch_bounds__(256) void k_encode_tile(GridParams g, const TableT*
 //   * kLevels = 4 (16 levels): XCD x takes levels 4 (x % 4) .. + 3 for the
 //     points of every other 256-point block (x / 4 picks which), so a point's
 //     position is read by 4 XCDs instead of 8 and each thread writes 32
-//     contiguous bytes of the output row instead of 16.
+//     contiguous bytes of the output row instead of 16;
+//   * kLevels = 1 (16 levels, two launches): XCD x takes level x + 8 phase
+//     for every point, so its L2 holds one level.
 // One point per thread (the launch gives every thread exactly one).  The
 // placement is a locality choice only: any workgroup-to-XCD mapping gives
 // the same result.  The x-neighbour corners of a dense level are adjacent
@@ -109,11 +111,11 @@ __global__ __launch_bounds__(256) void k_encode_tile(GridParams g, const TableT*
 // Points come from a source (PointsFromArray, PointsFromSamples) whose count
 // may be read on the device.
 template <typename TableT, typename OutT, uint32_t kLevels, typename Points>
-__global__ __launch_bounds__(256) void k_encode_split(GridParams g, const TableT* __restrict__ table, Points src, OutT* __restrict__ out, bool nt) {
-    constexpr uint32_t kParts = kLevels / 2u;  // XCDs sharing one level group
+__global__ __launch_bounds__(256) void k_encode_split(GridParams g, const TableT* __restrict__ table, Points src, OutT* __restrict__ out, bool nt, uint32_t phase) {
+    constexpr uint32_t kParts = kLevels >= 2u ? kLevels / 2u : 1u;  // XCDs sharing one level group
     const uint32_t xcd = blockIdx.x & 7u, group = xcd % (8u / kParts), part = xcd / (8u / kParts);
     const uint32_t slot = blockIdx.x >> 3, slots = gridDim.x >> 3;
-    const uint32_t l0 = kLevels * group;
+    const uint32_t l0 = kLevels * group + (kLevels == 1u ? 8u * phase : 0u);
     if (l0 >= g.n_levels) return;  // uniform per workgroup
     const uint32_t n = src.count();
     const uint32_t width = 2u * g.n_levels;
@@ -157,8 +159,8 @@ __global__ __launch_bounds__(256) void k_encode_split(GridParams g, const TableT
                 if constexpr (kLevels % 4u != 0u) {
 #pragma unroll
                     for (uint32_t j = 4u * (kLevels / 4u); j < kLevels; ++j) {
-                        store_value(o + 2u * j, f[2u * j]);
-                        store_value(o + 2u * j + 1u, f[2u * j + 1u]);
+                        const uint32_t v = (uint32_t)__builtin_bit_cast(uint16_t, to_half_rne(f[2u * j])) | ((uint32_t)__builtin_bit_cast(uint16_t, to_half_rne(f[2u * j + 1u])) << 16);
+                        *reinterpret_cast<uint32_t*>(o + 2u * j) = v;
                     }
                 }
             }
@@ -195,11 +197,18 @@ hipError_t launch_encode_samples(const GridParams& g, const half_t* table, const
     PointsFromSamples src{in.samples, in.sample_ray, in.rays, in.n_dev, cap, {in.bmin[0], in.bmin[1], in.bmin[2]}, {in.bmax[0], in.bmax[1], in.bmax[2]}};
     const uint64_t level_bytes = (uint64_t)g.table_size * g.n_features * 2u;
     const uint32_t blocks_256  = (cap + 255u) / 256u;
-    // Four levels per XCD when four fit in half of its L2, else two.
-    if (4u * level_bytes <= (2ull << 20))
-        k_encode_split<half_t, half_t, 4u><<<8u * ((blocks_256 + 1u) / 2u), 256, 0, stream>>>(g, table, src, features, false);
-    else
-        k_encode_split<half_t, half_t, 2u><<<8u * blocks_256, 256, 0, stream>>>(g, table, src, features, false);
+    // Four levels per XCD when four fit in half of its L2; else one level per
+    // XCD in two launches (levels 0-7, then 8-15): with T = 2^19 fp16 a level
+    // is 2 MiB, and two of them (4 MiB) left no room in the XCD's L2 for the
+    // feature rows streaming through it (the reference host's 4,096 rays x
+    // <= 64 steps: 117 us for one launch of two levels per XCD, 95 us for
+    // the two launches).
+    if (4u * level_bytes <= (2ull << 20)) {
+        k_encode_split<half_t, half_t, 4u><<<8u * ((blocks_256 + 1u) / 2u), 256, 0, stream>>>(g, table, src, features, false, 0u);
+    } else {
+        k_encode_split<half_t, half_t, 1u><<<8u * blocks_256, 256, 0, stream>>>(g, table, src, features, false, 0u);
+        k_encode_split<half_t, half_t, 1u><<<8u * blocks_256, 256, 0, stream>>>(g, table, src, features, false, 1u);
+    }
     return hipGetLastError();
 }
 
@@ -264,9 +273,9 @@ NERF_API NerfStatus nerf_ext_encode_forward(const NerfExtGridDesc* grid, const v
 #define NERF_ENC(TT, OT)                                                                                                   \
     do {                                                                                                                   \
         if (quad)                                                                                                          \
-            k_encode_split<TT, OT, 4u><<<grid_dim, 256, 0, st>>>(g, (const TT*)table, PointsFromArray{positions, n}, (OT*)features, nt);  \
+            k_encode_split<TT, OT, 4u><<<grid_dim, 256, 0, st>>>(g, (const TT*)table, PointsFromArray{positions, n}, (OT*)features, nt, 0u);  \
         else if (split)                                                                                                    \
-            k_encode_split<TT, OT, 2u><<<grid_dim, 256, 0, st>>>(g, (const TT*)table, PointsFromArray{positions, n}, (OT*)features, nt);  \
+            k_encode_split<TT, OT, 2u><<<grid_dim, 256, 0, st>>>(g, (const TT*)table, PointsFromArray{positions, n}, (OT*)features, nt, 0u);  \
         else                                                                                                               \
             k_encode_tile<TT, OT><<<grid_dim, 256, 0, st>>>(g, (const TT*)table, positions, n, (OT*)features);             \
     } while (0)

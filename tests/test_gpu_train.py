@@ -134,9 +134,13 @@ def test_sample_stage_bit_exact(dataset, capacity):
     assert np.array_equal(s["sample_ray"], want_ray)
 
 
-def test_forward_stage(dataset):
-    announce("train forward stage")
-    t, grid = _trainer(dataset)
+@pytest.mark.parametrize("log2_table", [14, 19])
+def test_forward_stage(dataset, log2_table):
+    """At 64 steps per ray the forward takes the level-split encode and the
+    MLP pass: four levels per XCD at T = 2^14, one level per XCD in two
+    launches at T = 2^19."""
+    announce(f"train forward stage, T=2^{log2_table}")
+    t, grid = _trainer(dataset, log2_table=log2_table)
     t.run_stages(L.NERF_EXT_STAGE_BEGIN, L.NERF_EXT_STAGE_FORWARD)
     s = _sample_state(t)
     n = s["stats"].samples
