@@ -99,8 +99,9 @@ __global__ __launch_bounds__(256) void k_encode_tile(GridParams g, const TableT*
 //     points of every other 256-point block (x / 4 picks which), so a point's
 //     position is read by 4 XCDs instead of 8 and each thread writes 32
 //     contiguous bytes of the output row instead of 16;
-//   * kLevels = 1 (16 levels, two launches): XCD x takes level x + 8 phase
-//     for every point, so its L2 holds one level.
+//   * kLevels = 1 (16 levels): XCD x takes level x + 8 phase for every
+//     point, so its L2 holds one level; phase 2 runs phase 0 on the first
+//     half of the workgroups and phase 1 on the second.
 // One point per thread (the launch gives every thread exactly one).  The
 // placement is a locality choice only: any workgroup-to-XCD mapping gives
 // the same result.  The x-neighbour corners of a dense level are adjacent
@@ -114,7 +115,12 @@ template <typename TableT, typename OutT, uint32_t kLevels, typename Points>
 __global__ __launch_bounds__(256) void k_encode_split(GridParams g, const TableT* __restrict__ table, Points src, OutT* __restrict__ out, bool nt, uint32_t phase) {
     constexpr uint32_t kParts = kLevels >= 2u ? kLevels / 2u : 1u;  // XCDs sharing one level group
     const uint32_t xcd = blockIdx.x & 7u, group = xcd % (8u / kParts), part = xcd / (8u / kParts);
-    const uint32_t slot = blockIdx.x >> 3, slots = gridDim.x >> 3;
+    uint32_t slot = blockIdx.x >> 3, slots = gridDim.x >> 3;
+    if (kLevels == 1u && phase > 1u) {  // both phases in one launch: the first half of the slots, then the second
+        slots /= 2u;
+        phase = slot >= slots ? 1u : 0u;
+        slot -= phase * slots;
+    }
     const uint32_t l0 = kLevels * group + (kLevels == 1u ? 8u * phase : 0u);
     if (l0 >= g.n_levels) return;  // uniform per workgroup
     const uint32_t n = src.count();
@@ -198,16 +204,16 @@ hipError_t launch_encode_samples(const GridParams& g, const half_t* table, const
     const uint64_t level_bytes = (uint64_t)g.table_size * g.n_features * 2u;
     const uint32_t blocks_256  = (cap + 255u) / 256u;
     // Four levels per XCD when four fit in half of its L2; else one level per
-    // XCD in two launches (levels 0-7, then 8-15): with T = 2^19 fp16 a level
-    // is 2 MiB, and two of them (4 MiB) left no room in the XCD's L2 for the
-    // feature rows streaming through it (the reference host's 4,096 rays x
-    // <= 64 steps: 117 us for one launch of two levels per XCD, 95 us for
-    // the two launches).
+    // XCD in two phases (levels 0-7, then 8-15; one launch whose second half
+    // of workgroups, dispatched after the first, takes the second phase):
+    // with T = 2^19 fp16 a level is 2 MiB, and two of them (4 MiB) left no
+    // room in the XCD's L2 for the feature rows streaming through it (the
+    // reference host's 4,096 rays x <= 64 steps: 117 us for two levels per
+    // XCD, 95 us for the two phases as two launches).
     if (4u * level_bytes <= (2ull << 20)) {
         k_encode_split<half_t, half_t, 4u><<<8u * ((blocks_256 + 1u) / 2u), 256, 0, stream>>>(g, table, src, features, false, 0u);
     } else {
-        k_encode_split<half_t, half_t, 1u><<<8u * blocks_256, 256, 0, stream>>>(g, table, src, features, false, 0u);
-        k_encode_split<half_t, half_t, 1u><<<8u * blocks_256, 256, 0, stream>>>(g, table, src, features, false, 1u);
+        k_encode_split<half_t, half_t, 1u><<<16u * blocks_256, 256, 0, stream>>>(g, table, src, features, false, 2u);
     }
     return hipGetLastError();
 }

@@ -139,7 +139,7 @@ constexpr uint32_t kMaxBins    = 16384; // bins; the fill pass keeps a cursor an
 constexpr uint32_t kMlpParams  = NERF_EXT_DENSITY_PARAMS + NERF_EXT_COLOR_PARAMS;
 
 // Workgroups of the coarse-level reduction (16 columns of two entries each).
-inline uint32_t coarse_reduce_blocks(const CoarsePlan& C) { return (C.row / 2u + 15u) / 16u; }
+__host__ __device__ inline uint32_t coarse_reduce_blocks(const CoarsePlan& C) { return (C.row / 2u + 15u) / 16u; }
 // Squared-norm partials of a step: coarse reduction, bins, weight gradients
 // (the reference model: its weight-gradient reduction only).
 inline uint32_t norm_partial_count(const TrainBuffers& B) {

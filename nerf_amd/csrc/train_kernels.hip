@@ -1100,6 +1100,163 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_pass(TrainParams P, GridPar
     }
 }
 
+// Fill pass with the records staged in LDS, for grids whose per-bin state
+// fits beside the stage (n_bins <= kStagedMaxBins).  The workgroup takes one
+// level of its chunk of samples per round: every head lane reserves its
+// records' slots as in k_bin_pass<true> (the same slots, since the cursors
+// advance the same way), then the round's records are placed in LDS by bin
+// (an exclusive scan of the round's per-bin counts) and written out in that
+// order, so consecutive lanes store consecutive slots of one bin's range
+// instead of one scattered 8-byte store per record.  (Left out, those
+// stores were half of k_bin_pass<true>: 74 -> 38 us at 2^18 samples of 1,024
+// steps, 136 -> 32 us at 4,096 rays of 64 steps; staged: 90 and 98 us.)
+// Records, slots and the per-bin maxima are those of k_bin_pass<true>; only
+// the order in which they reach memory differs.
+constexpr uint32_t kStageRecords  = kBinThreads * 8u;  // at most 8 records per lane and level
+constexpr uint32_t kStageBytes    = kStageRecords * (sizeof(uint2) + sizeof(uint32_t));
+constexpr uint32_t kStagedMaxBins = (160u * 1024u - kStageBytes - 1024u) / (4u * sizeof(uint32_t));
+__host__ __device__ constexpr uint32_t staged_fill_lds(uint32_t n_bins) { return kStageBytes + 4u * sizeof(uint32_t) * ((n_bins + 1u) & ~1u); }
+
+// Workgroup barrier for LDS data only: waits for this wave's LDS operations,
+// not for its global loads and stores (which __syncthreads also drains).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+__global__ __launch_bounds__(kBinThreads) void k_bin_fill_staged(TrainParams P, GridParams g, const TrainDevState* S, const float2* __restrict__ samples, const uint32_t* __restrict__ sample_ray,
+                                                                 const float4* __restrict__ rays, const float2* __restrict__ dfeat, uint32_t n_dense, uint32_t n_bins, const uint32_t* __restrict__ hist,
+                                                                 uint2* __restrict__ rec, uint32_t* __restrict__ bin_max) {
+    extern __shared__ __align__(16) uint32_t lds_words[];
+    uint2* st_rec      = reinterpret_cast<uint2*>(lds_words);  // [kStageRecords]
+    uint32_t* st_slot  = lds_words + 2u * kStageRecords;       // [kStageRecords] global slot of each staged record
+    const uint32_t nb2 = (n_bins + 1u) & ~1u;
+    uint32_t* cursor   = st_slot + kStageRecords;  // [n_bins] next global slot of each bin's range
+    uint32_t* vmax     = cursor + nb2;             // [n_bins] bits of the largest |record value|
+    uint32_t* start    = vmax + nb2;               // [n_bins] the round's first slot
+    uint32_t* pos      = start + nb2;              // [n_bins] LDS position of slot x of bin b: x + pos[b]
+    __shared__ uint32_t wave_tot[kBinThreads / 64u];
+    for (uint32_t i = threadIdx.x; i < n_bins; i += blockDim.x) {
+        const uint32_t h = hist[(uint64_t)i * gridDim.x + blockIdx.x];
+        cursor[i]        = h;
+        start[i]         = h;
+        vmax[i]          = 0u;
+    }
+    __syncthreads();
+    const uint32_t n    = min(S->n_samples, P.sample_cap);
+    const uint32_t mask = g.table_size - 1u;
+    const uint32_t lane = threadIdx.x & 63u, s16 = lane & 15u, wave = threadIdx.x >> 6;
+    const uint32_t per  = (n_bins + blockDim.x - 1u) / blockDim.x;  // bins per thread in the scan
+    // Chunks of blockDim.x consecutive samples, the same samples per wave as
+    // k_bin_pass (wave w of the workgroup holds samples chunk + 64 w ..).
+    for (uint32_t chunk = blockIdx.x * blockDim.x; chunk < n; chunk += gridDim.x * blockDim.x) {
+        const uint32_t s = chunk + threadIdx.x;
+        const bool live  = s < n;
+        const uint32_t q = live ? s : n - 1u;
+        float p[3], d[3];
+        sample_geometry(samples, sample_ray, rays, P.bmin, P.bmax, q, p, d);
+        // d(features) of the next level are loaded a round ahead.
+        float2 df_next = live ? dfeat[(uint64_t)n_dense * P.sample_cap + q] : make_float2(0.0f, 0.0f);
+        for (uint32_t l = n_dense; l < g.n_levels; ++l) {
+            const float2 df = df_next;
+            if (l + 1u < g.n_levels) df_next = live ? dfeat[(uint64_t)(l + 1u) * P.sample_cap + q] : make_float2(0.0f, 0.0f);
+            const uint32_t N  = g.resolution[l];
+            const bool dense  = g.dense[l] != 0u;
+            const uint32_t e0 = (l - n_dense) * g.table_size;
+            const LevelCell c = level_cell(p, N);
+            const uint32_t kx = live ? c.i0[0] : 0xFFFFFFFFu, ky = c.i0[1], kz = c.i0[2];
+            const uint32_t px = row_prev_u(kx, ~0u), py = row_prev_u(ky, ~0u), pz = row_prev_u(kz, ~0u);
+            const bool head   = s16 == 0u || kx != px || ky != py || kz != pz || !live;
+            float v[16];
+#pragma unroll
+            for (uint32_t k = 0; k < 8u; ++k) {
+                const float w  = corner_weight(c, k);
+                v[2u * k]      = w * df.x;
+                v[2u * k + 1u] = w * df.y;
+            }
+            const uint64_t heads = __ballot(head);
+            if (heads != ~0ull) {
+                const uint32_t row_heads = (uint32_t)(heads >> (lane & 48u)) & 0xFFFFu;
+                const uint32_t seg       = (uint32_t)__popc(row_heads & ((2u << s16) - 1u));
+                combine_step<1>(v, seg);
+                combine_step<2>(v, seg);
+                combine_step<4>(v, seg);
+                combine_step<8>(v, seg);
+            }
+            const bool emits = live && head;
+            // This lane's records: the corners of edge (y, z) k / 2 as records k, k + 1.
+            uint2 r[8];
+            uint32_t rbin[8], rslot[8];
+#pragma unroll
+            for (uint32_t k = 0; k < 8u; k += 2u) {
+                rbin[k] = rbin[k + 1u] = 0xFFFFFFFFu;
+                if (!emits) continue;
+                const uint32_t ea = e0 + corner_index(c, k, N, dense, mask);
+                const uint32_t eb = e0 + corner_index(c, k + 1u, N, dense, mask);
+                const uint32_t ba = ea / kBinEntries, bb = eb / kBinEntries;
+                uint32_t sa, sb;
+                const uint32_t ma = max(__float_as_uint(v[2u * k]) & 0x7FFFFFFFu, __float_as_uint(v[2u * k + 1u]) & 0x7FFFFFFFu);
+                const uint32_t mb = max(__float_as_uint(v[2u * k + 2u]) & 0x7FFFFFFFu, __float_as_uint(v[2u * k + 3u]) & 0x7FFFFFFFu);
+                if (ba == bb) {
+                    sa = atomicAdd(&cursor[ba], 2u);
+                    sb = sa + 1u;
+                    atomicMax(&vmax[ba], max(ma, mb));
+                } else {
+                    sa = atomicAdd(&cursor[ba], 1u);
+                    sb = atomicAdd(&cursor[bb], 1u);
+                    atomicMax(&vmax[ba], ma);
+                    atomicMax(&vmax[bb], mb);
+                }
+                r[k]          = pack_record(v[2u * k], v[2u * k + 1u], ea % kBinEntries);
+                r[k + 1u]     = pack_record(v[2u * k + 2u], v[2u * k + 3u], eb % kBinEntries);
+                rbin[k]       = ba;
+                rbin[k + 1u]  = bb;
+                rslot[k]      = sa;
+                rslot[k + 1u] = sb;
+            }
+            lds_barrier();
+            // Exclusive scan of the round's per-bin counts: thread t sums bins
+            // [t per, (t + 1) per), waves scan the thread sums, the wave totals
+            // are added in LDS; each bin's round then starts at its cursor.
+            const uint32_t b0 = min(threadIdx.x * per, n_bins), b1 = min(b0 + per, n_bins);
+            uint32_t own = 0u;
+            for (uint32_t b = b0; b < b1; ++b) own += cursor[b] - start[b];
+            uint32_t inc = own;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const uint32_t up = (uint32_t)__shfl_up((int)inc, o, 64);
+                if (lane >= (uint32_t)o) inc += up;
+            }
+            if (lane == 63u) wave_tot[wave] = inc;
+            lds_barrier();
+            uint32_t before = 0u, total = 0u;
+            for (uint32_t w = 0; w < blockDim.x / 64u; ++w) {
+                const uint32_t t = wave_tot[w];
+                before += w < wave ? t : 0u;
+                total += t;
+            }
+            uint32_t off = before + inc - own;
+            for (uint32_t b = b0; b < b1; ++b) {
+                const uint32_t first = start[b], end = cursor[b];
+                pos[b]   = off - first;
+                start[b] = end;
+                off += end - first;
+            }
+            lds_barrier();
+#pragma unroll
+            for (uint32_t k = 0; k < 8u; ++k) {
+                if (rbin[k] == 0xFFFFFFFFu) continue;
+                const uint32_t at = rslot[k] + pos[rbin[k]];
+                st_rec[at]        = r[k];
+                st_slot[at]       = rslot[k];
+            }
+            lds_barrier();
+            for (uint32_t i = threadIdx.x; i < total; i += blockDim.x) rec[st_slot[i]] = st_rec[i];
+            // The next round's atomics touch only the cursors, and its stage
+            // writes come after two more barriers.
+        }
+    }
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < n_bins; i += blockDim.x) bin_max[(uint64_t)i * gridDim.x + blockIdx.x] = vmax[i];
+}
+
 // One bin per workgroup.  fp32 LDS atomics run at a twelfth of the rate of
 // 64-bit integer ones on gfx950, so the bin is accumulated in fixed point:
 // a first pass over the bin's records finds max |v|, every value is scaled
@@ -1109,13 +1266,10 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_pass(TrainParams P, GridPar
 // largest one round to zero.  A non-finite record makes the whole slice
 // NaN, which the gradient statistics report as non-finite.
 // grad points at the first hashed level; entries = hashed levels x T.
-__global__ __launch_bounds__(512) void k_bin_accumulate(const uint32_t* __restrict__ offsets, uint32_t n_blocks, uint32_t n_bins, const unsigned long long* __restrict__ total, const uint2* __restrict__ rec,
-                                                        const uint32_t* __restrict__ bin_max, uint64_t entries, float2* __restrict__ grad, double* __restrict__ norm) {
-    __shared__ unsigned long long acc[2u * kBinEntries];
-    __shared__ uint32_t wmax[16];
-    __shared__ double wsq[16];
+// acc: 2 kBinEntries int64 of LDS; wmax, wsq: 16 each.
+__device__ void bin_accumulate(uint32_t bin, const uint32_t* __restrict__ offsets, uint32_t n_blocks, uint32_t n_bins, const unsigned long long* __restrict__ total, const uint2* __restrict__ rec,
+                               const uint32_t* __restrict__ bin_max, uint64_t entries, float2* __restrict__ grad, double* __restrict__ norm, unsigned long long* acc, uint32_t* wmax, double* wsq) {
     for (uint32_t i = threadIdx.x; i < 2u * kBinEntries; i += blockDim.x) acc[i] = 0ull;
-    const uint32_t bin   = blockIdx.x;
     const uint32_t begin = offsets[(uint64_t)bin * n_blocks];
     const uint32_t end   = bin + 1u < n_bins ? offsets[(uint64_t)(bin + 1u) * n_blocks] : (uint32_t)*total;
     // Largest |record value| of the bin, as bits: the maximum of the fill
@@ -1187,15 +1341,20 @@ __global__ __launch_bounds__(512) void k_bin_accumulate(const uint32_t* __restri
 // fixed order.  The MLP gradient's share of the squared norm is taken here,
 // from the values written: one partial per workgroup, added by k_grad_norm.
 constexpr uint32_t kReduceSlices = 16u;
-__global__ __launch_bounds__(256) void k_dw_reduce(const float* __restrict__ partials, uint32_t blocks, float* __restrict__ grad, double* __restrict__ norm) {
+// Part vb of the MLP weight-gradient reduction, run by the 256 threads t of
+// half h of a 512-thread workgroup (each half has its own slice sums; both
+// halves reach the barrier, an out-of-range part only takes part in it).
+// part_h: LDS of 2 x kReduceSlices x 16 float4.
+__device__ void dw_reduce(uint32_t vb, uint32_t t, uint32_t h, const float* __restrict__ partials, uint32_t blocks, float* __restrict__ grad, double* __restrict__ norm, float4 (*part_h)[kReduceSlices][16]) {
     static_assert(kMlpParams % 64u == 0u, "whole columns per workgroup");
-    __shared__ float4 part[kReduceSlices][16];
-    const uint32_t col = threadIdx.x & 15u, slice = threadIdx.x >> 4;
-    const uint32_t c   = blockIdx.x * 16u + col;  // float4 column
+    float4 (*part)[16] = part_h[h];
+    const bool valid   = vb < kMlpParams / 64u;
+    const uint32_t col = t & 15u, slice = t >> 4;
+    const uint32_t c   = vb * 16u + col;  // float4 column
     const float4* p4   = reinterpret_cast<const float4*>(partials);
     float4 s           = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     // Batches of 8 loads in flight, added in partial order.
-    for (uint32_t b0 = slice; b0 < blocks; b0 += 8u * kReduceSlices) {
+    for (uint32_t b0 = slice; valid && b0 < blocks; b0 += 8u * kReduceSlices) {
         float4 v[8];
 #pragma unroll
         for (uint32_t k = 0; k < 8u; ++k) {
@@ -1212,18 +1371,18 @@ __global__ __launch_bounds__(256) void k_dw_reduce(const float* __restrict__ par
     }
     part[slice][col] = s;
     __syncthreads();
-    if (threadIdx.x >= 64u) return;
-    // Thread t < 64: parameter 4 * (blockIdx.x * 16) + t.
-    const uint32_t cc = threadIdx.x >> 2, e = threadIdx.x & 3u;
+    if (t >= 64u || !valid) return;
+    // Thread t < 64: parameter 4 * (vb * 16) + t.
+    const uint32_t cc = t >> 2, e = t & 3u;
     float gi          = 0.0f;
     for (uint32_t k = 0; k < kReduceSlices; ++k) {
         const float4 v = part[k][cc];
         gi += e == 0u ? v.x : e == 1u ? v.y : e == 2u ? v.z : v.w;
     }
-    grad[blockIdx.x * 64u + threadIdx.x] = gi;
+    grad[vb * 64u + t] = gi;
     const bool finite = isfinite(gi);
     const double sq   = wave_sum_d(finite ? (double)gi * (double)gi : 0.0);
-    if (threadIdx.x == 0u) norm[blockIdx.x] = __ballot(!finite) != 0ull ? -1.0 - sq : sq;
+    if (t == 0u) norm[vb] = __ballot(!finite) != 0ull ? -1.0 - sq : sq;
 }
 
 // Sum of the coarse levels' chunk partials, in chunk order (the same layout
@@ -1232,14 +1391,18 @@ __global__ __launch_bounds__(256) void k_dw_reduce(const float* __restrict__ par
 // norm is taken from the values written, as in k_dw_reduce.  Entries
 // past a level's (N + 1)^3 are never written and stay zero.
 static_assert(kCoarseChunks % kReduceSlices == 0u, "whole slices of chunks");
-__global__ __launch_bounds__(256) void k_coarse_reduce(const float2* __restrict__ partials, CoarsePlan C, uint32_t n_levels, uint32_t table_size, float* __restrict__ grad, double* __restrict__ norm) {
-    __shared__ float4 part[kReduceSlices][16];
-    const uint32_t col = threadIdx.x & 15u, slice = threadIdx.x >> 4;
+// Part vb of the coarse levels' reduction, by the 256 threads t of half h of
+// a 512-thread workgroup, as dw_reduce.
+__device__ void coarse_reduce(uint32_t vb, uint32_t t, uint32_t h, const float2* __restrict__ partials, const CoarsePlan& C, uint32_t n_levels, uint32_t table_size, float* __restrict__ grad, double* __restrict__ norm,
+                              float4 (*part_h)[kReduceSlices][16]) {
+    float4 (*part)[16] = part_h[h];
+    const bool in_range = vb < coarse_reduce_blocks(C);
+    const uint32_t col = t & 15u, slice = t >> 4;
     const uint32_t cols = C.row / 2u;
-    const uint32_t c    = blockIdx.x * 16u + col;  // entries 2c, 2c + 1 of a partial row
+    const uint32_t c    = vb * 16u + col;  // entries 2c, 2c + 1 of a partial row
     const float4* p4    = reinterpret_cast<const float4*>(partials);
     float4 s            = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if (c < cols) {
+    if (in_range && c < cols) {
         constexpr uint32_t kPer = kCoarseChunks / kReduceSlices;
         float4 v[kPer];
 #pragma unroll
@@ -1254,15 +1417,15 @@ __global__ __launch_bounds__(256) void k_coarse_reduce(const float2* __restrict_
     }
     part[slice][col] = s;
     __syncthreads();
-    if (threadIdx.x >= 64u) return;
+    if (t >= 64u || !in_range) return;
     // Thread t < 64: component t & 3 (entry t >> 1 & 1, feature t & 1) of column t >> 2.
-    const uint32_t cc = threadIdx.x >> 2, comp = threadIdx.x & 3u;
+    const uint32_t cc = t >> 2, comp = t & 3u;
     float gi          = 0.0f;
     for (uint32_t k = 0; k < kReduceSlices; ++k) {
         const float4 v = part[k][cc];
         gi += comp == 0u ? v.x : comp == 1u ? v.y : comp == 2u ? v.z : v.w;
     }
-    const uint32_t e = 2u * (blockIdx.x * 16u + cc) + (comp >> 1);  // entry of the partial row
+    const uint32_t e = 2u * (vb * 16u + cc) + (comp >> 1);  // entry of the partial row
     uint32_t l       = 0u;
     while (l + 1u < n_levels && e >= C.level_part[l + 1u]) ++l;
     const uint32_t el = e - C.level_part[l];
@@ -1270,7 +1433,57 @@ __global__ __launch_bounds__(256) void k_coarse_reduce(const float2* __restrict_
     if (valid) grad[((uint64_t)l * table_size + el) * 2u + (comp & 1u)] = gi;
     const bool finite = !valid || isfinite(gi);
     const double sq   = wave_sum_d(valid && finite ? (double)gi * (double)gi : 0.0);
-    if (threadIdx.x == 0u) norm[blockIdx.x] = __ballot(!finite) != 0ull ? -1.0 - sq : sq;
+    if (t == 0u) norm[vb] = __ballot(!finite) != 0ull ? -1.0 - sq : sq;
+}
+
+// The gradient reductions of a step in one launch of 512-thread workgroups
+// (each launch costs about 4.5 us here, and the three parts are independent):
+// the first workgroups take pairs of coarse-level parts, the next pairs of
+// MLP weight-gradient parts (two 256-thread parts per workgroup; first, so
+// that these short parts run beside the bins rather than after them), the
+// rest one bin each.  norm gets one partial per part: coarse parts first,
+// then the bins, then the MLP parts.
+struct GradReduceArgs {
+    const uint32_t* bin_off;
+    uint32_t n_bins;
+    const unsigned long long* bin_total;
+    const uint2* rec;
+    const uint32_t* bin_max;
+    uint64_t hashed_entries;
+    float2* hashed_grad;
+    const float2* coarse_partials;
+    CoarsePlan coarse;
+    uint32_t n_dense;
+    uint32_t table_size;
+    float* table_grad;
+    const float* dw_partials;
+    uint32_t dw_blocks;
+    float* mlp_grad;
+    double* norm;
+};
+__global__ __launch_bounds__(512) void k_grad_reduce(GradReduceArgs a) {
+    // One LDS allocation for every part (the bins' 64 KiB of sums, which the
+    // reduction parts reuse for their slice sums), so two workgroups fit a CU.
+    __shared__ unsigned long long acc[2u * kBinEntries];
+    __shared__ uint32_t wmax[16];
+    __shared__ double wsq[16];
+    static_assert(2u * kReduceSlices * 16u * sizeof(float4) <= sizeof(acc), "slice sums fit the bins' LDS");
+    float4 (*part_h)[kReduceSlices][16] = reinterpret_cast<float4 (*)[kReduceSlices][16]>(acc);
+    const uint32_t coarse_parts = coarse_reduce_blocks(a.coarse);  // norm partials of the coarse levels
+    const uint32_t coarse_pairs = a.n_dense ? (coarse_parts + 1u) / 2u : 0u;
+    const uint32_t t = threadIdx.x & 255u, h = threadIdx.x >> 8;
+    const uint32_t b = blockIdx.x;
+    if (b < coarse_pairs) {
+        const uint32_t vb = 2u * b + h;
+        coarse_reduce(vb < coarse_parts ? vb : 0xFFFFFFFFu, t, h, a.coarse_partials, a.coarse, a.n_dense, a.table_size, a.table_grad, a.norm, part_h);
+        return;
+    }
+    if (b < coarse_pairs + kMlpParams / 128u) {
+        dw_reduce(2u * (b - coarse_pairs) + h, t, h, a.dw_partials, a.dw_blocks, a.mlp_grad, a.norm + coarse_parts + a.n_bins, part_h);
+        return;
+    }
+    const uint32_t bin = b - coarse_pairs - kMlpParams / 128u;
+    bin_accumulate(bin, a.bin_off, kBinBlocks, a.n_bins, a.bin_total, a.rec, a.bin_max, a.hashed_entries, a.hashed_grad, a.norm + coarse_parts, acc, wmax, wsq);
 }
 
 // The step's squared gradient norm: the sum, in a fixed order, of the
@@ -1424,6 +1637,7 @@ hipError_t launch_mlp_backward(const TrainParams& P, const TrainBuffers& B, hipS
     if (!lds_set) {
         hipError_t e = hipFuncSetAttribute((const void*)k_bwd_dx, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDxLds);
         if (e == hipSuccess) e = hipFuncSetAttribute((const void*)k_coarse_scatter, hipFuncAttributeMaxDynamicSharedMemorySize, (int)(kCoarseSlabEntries * 2u * sizeof(uint32_t)));
+        if (e == hipSuccess) e = hipFuncSetAttribute((const void*)k_bin_fill_staged, hipFuncAttributeMaxDynamicSharedMemorySize, (int)staged_fill_lds(kStagedMaxBins));
         if (e != hipSuccess) return e;
         lds_set = true;
     }
@@ -1435,18 +1649,43 @@ hipError_t launch_mlp_backward(const TrainParams& P, const TrainBuffers& B, hipS
         uint32_t lds_entries = 0u;
         for (uint32_t k = 0; k < C.n_slabs; ++k) lds_entries = max(lds_entries, C.count[k]);
         k_coarse_scatter<<<kCoarseChunks * C.n_slabs, kCoarseThreads, lds_entries * 2u * sizeof(uint32_t), st>>>(P, B.grid, C, B.state, B.samples, B.sample_ray, B.rays, B.dfeat, B.coarse_partials);
-        k_coarse_reduce<<<coarse_reduce_blocks(C), 256, 0, st>>>(B.coarse_partials, C, B.n_dense, B.grid.table_size, B.table_grad, B.norm_partials);
     }
     // Hashed levels: binned.
     if (B.n_bins) {
         k_bin_pass<false><<<kBinBlocks, kBinThreads, 0, st>>>(P, B.grid, B.state, B.samples, B.sample_ray, B.rays, B.dfeat, B.n_dense, B.n_bins, B.bin_hist, nullptr, nullptr);
         const hipError_t e = exclusive_scan_u32(B.bin_hist, B.bin_off, B.n_bins * kBinBlocks, B.bin_scan_tmp, B.bin_total, st);
         if (e != hipSuccess) return e;
-        k_bin_pass<true><<<kBinBlocks, kBinThreads, 0, st>>>(P, B.grid, B.state, B.samples, B.sample_ray, B.rays, B.dfeat, B.n_dense, B.n_bins, B.bin_off, B.rec, B.bin_max);
-        k_bin_accumulate<<<B.n_bins, 512, 0, st>>>(B.bin_off, kBinBlocks, B.n_bins, B.bin_total, B.rec, B.bin_max, (uint64_t)(B.grid.n_levels - B.n_dense) * B.grid.table_size,
-                                                   reinterpret_cast<float2*>(B.table_grad) + (uint64_t)B.n_dense * B.grid.table_size, B.norm_partials + coarse_reduce_blocks(B.coarse));
+        // Staged for sparse batches (<= 128 steps per ray: records rarely
+        // combine and the scattered stores dominate: 4,096 rays of 64 steps
+        // 136 -> 98 us); dense batches keep the direct stores, whose records
+        // are fewer and whose pass is shorter than the staging rounds (2^18
+        // samples of 1,024 steps: 74 us direct, 90 us staged).
+        if (P.max_steps <= 128u && B.n_bins <= kStagedMaxBins)
+            k_bin_fill_staged<<<kBinBlocks, kBinThreads, staged_fill_lds(B.n_bins), st>>>(P, B.grid, B.state, B.samples, B.sample_ray, B.rays, B.dfeat, B.n_dense, B.n_bins, B.bin_off, B.rec, B.bin_max);
+        else
+            k_bin_pass<true><<<kBinBlocks, kBinThreads, 0, st>>>(P, B.grid, B.state, B.samples, B.sample_ray, B.rays, B.dfeat, B.n_dense, B.n_bins, B.bin_off, B.rec, B.bin_max);
     }
-    k_dw_reduce<<<kMlpParams / 64u, 256, 0, st>>>(B.dw_partials, dx_blocks, B.mlp_grad, B.norm_partials + coarse_reduce_blocks(B.coarse) + B.n_bins);
+    // Bin accumulation, the coarse levels' chunk sums and the MLP weight
+    // gradients' partial sums, in one launch.
+    GradReduceArgs a{};
+    a.bin_off         = B.bin_off;
+    a.n_bins          = B.n_bins;
+    a.bin_total       = B.bin_total;
+    a.rec             = B.rec;
+    a.bin_max         = B.bin_max;
+    a.hashed_entries  = (uint64_t)(B.grid.n_levels - B.n_dense) * B.grid.table_size;
+    a.hashed_grad     = reinterpret_cast<float2*>(B.table_grad) + (uint64_t)B.n_dense * B.grid.table_size;
+    a.coarse_partials = B.coarse_partials;
+    a.coarse          = B.coarse;
+    a.n_dense         = B.n_dense;
+    a.table_size      = B.grid.table_size;
+    a.table_grad      = B.table_grad;
+    a.dw_partials     = B.dw_partials;
+    a.dw_blocks       = dx_blocks;
+    a.mlp_grad        = B.mlp_grad;
+    a.norm            = B.norm_partials;
+    const uint32_t coarse_pairs = B.n_dense ? (coarse_reduce_blocks(B.coarse) + 1u) / 2u : 0u;
+    k_grad_reduce<<<B.n_bins + coarse_pairs + kMlpParams / 128u, 512, 0, st>>>(a);
     k_grad_norm<<<1, kNormThreads, 0, st>>>(B.norm_partials, norm_partial_count(B), B.state);
     return hipGetLastError();
 }
