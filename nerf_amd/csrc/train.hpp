@@ -146,14 +146,27 @@ inline uint32_t norm_partial_count(const TrainBuffers& B) {
     return B.model_kind == NERF_EXT_MODEL_REFERENCE ? kRefReduceBlocks : coarse_reduce_blocks(B.coarse) + B.n_bins + kMlpParams / 64u;
 }
 
+// A second stream beside a step's own: the hash table's record count and its
+// scan depend only on the step's samples, so the sample stage starts them
+// there and the backward waits for them, instead of running them between
+// the MLP backward and the record fill.  counted is true once a count has
+// been started after the latest sample stage.
+struct StepStreams {
+    hipStream_t aux    = nullptr;
+    hipEvent_t sampled = nullptr;  // the sample stage's end, on the step's stream
+    hipEvent_t done    = nullptr;  // the count and scan's end, on aux
+    bool counted       = false;
+};
+
 // Launches one stage (NERF_EXT_STAGE_*) of a training step on `stream`.
 // `occupancy_update` selects the occupancy-maintenance kernels (the schedule
-// is a function of the step index, which the host tracks).
-hipError_t launch_train_stage(const TrainParams& P, const TrainBuffers& B, uint32_t stage, bool occupancy_update, hipStream_t stream);
+// is a function of the step index, which the host tracks).  ss may be null
+// (then the count runs in the backward, on `stream`).
+hipError_t launch_train_stage(const TrainParams& P, const TrainBuffers& B, uint32_t stage, bool occupancy_update, hipStream_t stream, StepStreams* ss);
 
 // Individual stages, exposed for the parity tests through nerf_ext.h.
 hipError_t launch_composite_train(const TrainParams& P, const TrainBuffers& B, hipStream_t stream);
-hipError_t launch_mlp_backward(const TrainParams& P, const TrainBuffers& B, hipStream_t stream);
+hipError_t launch_mlp_backward(const TrainParams& P, const TrainBuffers& B, hipStream_t stream, StepStreams* ss);
 hipError_t launch_adam(const TrainParams& P, const TrainBuffers& B, hipStream_t stream);
 
 uint64_t scan_tmp_words(uint32_t n);

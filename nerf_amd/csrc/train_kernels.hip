@@ -1630,7 +1630,14 @@ hipError_t launch_composite_train(const TrainParams& P, const TrainBuffers& B, h
     return hipGetLastError();
 }
 
-hipError_t launch_mlp_backward(const TrainParams& P, const TrainBuffers& B, hipStream_t st) {
+// The hashed levels' record count per (bin, workgroup) and its exclusive
+// scan (the record ranges of the fill pass).
+static hipError_t launch_bin_count(const TrainParams& P, const TrainBuffers& B, hipStream_t st) {
+    k_bin_pass<false><<<kBinBlocks, kBinThreads, 0, st>>>(P, B.grid, B.state, B.samples, B.sample_ray, B.rays, B.dfeat, B.n_dense, B.n_bins, B.bin_hist, nullptr, nullptr);
+    return exclusive_scan_u32(B.bin_hist, B.bin_off, B.n_bins * kBinBlocks, B.bin_scan_tmp, B.bin_total, st);
+}
+
+hipError_t launch_mlp_backward(const TrainParams& P, const TrainBuffers& B, hipStream_t st, StepStreams* ss) {
     const uint32_t cus = device_cu_count();
     if (B.grid.table_dtype != NERF_EXT_F16) return hipErrorInvalidValue;
     static bool lds_set = false;  // once per process: the kernels' dynamic LDS exceeds the 64 KiB default
@@ -1652,8 +1659,9 @@ hipError_t launch_mlp_backward(const TrainParams& P, const TrainBuffers& B, hipS
     }
     // Hashed levels: binned.
     if (B.n_bins) {
-        k_bin_pass<false><<<kBinBlocks, kBinThreads, 0, st>>>(P, B.grid, B.state, B.samples, B.sample_ray, B.rays, B.dfeat, B.n_dense, B.n_bins, B.bin_hist, nullptr, nullptr);
-        const hipError_t e = exclusive_scan_u32(B.bin_hist, B.bin_off, B.n_bins * kBinBlocks, B.bin_scan_tmp, B.bin_total, st);
+        // The count started beside the forward pass by the sample stage, or
+        // here when no count followed the latest sample stage.
+        const hipError_t e = ss && ss->counted ? hipStreamWaitEvent(st, ss->done, 0) : launch_bin_count(P, B, st);
         if (e != hipSuccess) return e;
         // Staged for sparse batches (<= 128 steps per ray: records rarely
         // combine and the scattered stores dominate: 4,096 rays of 64 steps
@@ -1759,7 +1767,7 @@ static hipError_t launch_ref_train_stage(const TrainParams& P, const TrainBuffer
     return hipGetLastError();
 }
 
-hipError_t launch_train_stage(const TrainParams& P, const TrainBuffers& B, uint32_t stage, bool occupancy_update, hipStream_t st) {
+hipError_t launch_train_stage(const TrainParams& P, const TrainBuffers& B, uint32_t stage, bool occupancy_update, hipStream_t st, StepStreams* ss) {
     if (B.model_kind == NERF_EXT_MODEL_REFERENCE) return launch_ref_train_stage(P, B, stage, occupancy_update, st);
     const uint32_t cus = device_cu_count();
     switch (stage) {
@@ -1789,7 +1797,21 @@ hipError_t launch_train_stage(const TrainParams& P, const TrainBuffers& B, uint3
         return launch_field(B.grid, B.table, FieldWeights{B.dparams, B.cparams}, in, P.sample_cap, B.field, st);
     }
     case NERF_EXT_STAGE_COMPOSITE: return launch_composite_train(P, B, st);
-    case NERF_EXT_STAGE_BACKWARD: return launch_mlp_backward(P, B, st);
+    case NERF_EXT_STAGE_SAMPLE: {
+        hipError_t e = launch_train_stage_common(P, B, stage, st);
+        if (e != hipSuccess || !ss || !ss->aux || !B.n_bins) return e;
+        // The record count needs only the samples: it runs on the second
+        // stream while this one runs the forward pass, the composite and the
+        // MLP backward (2^18 samples: 17.5 + 9.5 us off the step's chain).
+        ss->counted = false;
+        if ((e = hipEventRecord(ss->sampled, st)) != hipSuccess) return e;
+        if ((e = hipStreamWaitEvent(ss->aux, ss->sampled, 0)) != hipSuccess) return e;
+        if ((e = launch_bin_count(P, B, ss->aux)) != hipSuccess) return e;
+        if ((e = hipEventRecord(ss->done, ss->aux)) != hipSuccess) return e;
+        ss->counted = true;
+        return hipSuccess;
+    }
+    case NERF_EXT_STAGE_BACKWARD: return launch_mlp_backward(P, B, st, ss);
     default: return launch_train_stage_common(P, B, stage, st);
     }
     return hipGetLastError();

@@ -13,7 +13,11 @@
 namespace nerf_hip {
 
 Trainer::~Trainer() {
+    if (side.aux) (void)hipStreamSynchronize(side.aux);
     if (stream) (void)hipStreamSynchronize(stream);
+    if (side.sampled) (void)hipEventDestroy(side.sampled);
+    if (side.done) (void)hipEventDestroy(side.done);
+    if (side.aux) (void)hipStreamDestroy(side.aux);
     for (void* p : owned)
         if (p) (void)hipFree(p);
     if (stream && own_stream) (void)hipStreamDestroy(stream);
@@ -36,7 +40,7 @@ bool Trainer::occupancy_due(uint32_t frame) const {
 
 NerfStatus Trainer::run_stages(uint32_t first, uint32_t last) {
     for (uint32_t s = first; s <= last; ++s) {
-        NERF_HIP_TRY(launch_train_stage(P, B, s, occupancy_due(host_frame), stream));
+        NERF_HIP_TRY(launch_train_stage(P, B, s, occupancy_due(host_frame), stream, &side));
         if (s == NERF_EXT_STAGE_END) ++host_frame;
     }
     return NERF_STATUS_OK;
@@ -192,6 +196,11 @@ NerfStatus trainer_create(const NerfExtTrainDesc* d, const BorrowedModel* borrow
     NERF_HIP_TRY(alloc(T, B.bin_total, 1));
     NERF_HIP_TRY(alloc(T, B.rec, B.rec_cap));
     NERF_HIP_TRY(alloc(T, B.dw_partials, (uint64_t)kDxMaxBlocks * kMlpParams));
+    if (B.n_bins) {
+        NERF_HIP_TRY(hipStreamCreateWithFlags(&T.side.aux, hipStreamNonBlocking));
+        NERF_HIP_TRY(hipEventCreateWithFlags(&T.side.sampled, hipEventDisableTiming));
+        NERF_HIP_TRY(hipEventCreateWithFlags(&T.side.done, hipEventDisableTiming));
+    }
     }
     NERF_HIP_TRY(alloc(T, B.table_grad, B.table_elems));
     NERF_HIP_TRY(alloc(T, B.table_m, B.table_elems));

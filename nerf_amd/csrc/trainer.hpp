@@ -27,6 +27,7 @@ struct Trainer {
     NerfExtGridDesc grid_desc{};
     hipStream_t stream = nullptr;
     bool own_stream    = false;
+    StepStreams side;  // the second stream of a step (hash-grid model)
     uint32_t host_frame = 0;  // steps enqueued so far (drives the occupancy schedule)
     float initial_rays  = 1.0f;
     std::vector<void*> owned;
