@@ -378,6 +378,104 @@ __global__ __launch_bounds__(256) void k_train_samples(TrainParams P, TrainDevSt
     }
 }
 
+// Rays of one segment (at most kSegSteps steps, the reference host's 64):
+// one workgroup scans the step's counts into the offsets, the kept counts and
+// the step totals (what the leading units of k_train_samples record), and
+// k_train_samples_one marches each ray with a whole wave (one run of 64
+// steps: one cell-word round trip instead of four) from its offset.  At
+// 4,096 rays of 64 steps the per-wave prefix sums of k_train_samples cost
+// more than the march (31 us for the pass; this pair 7.4 + 5.9 us).
+constexpr uint32_t kOffsetThreads = 1024u;
+__global__ __launch_bounds__(kOffsetThreads) void k_ray_offsets(TrainParams P, TrainDevState* S, const uint32_t* __restrict__ counts, uint32_t* __restrict__ offsets, uint32_t* __restrict__ kept) {
+    __shared__ uint32_t wsum[kOffsetThreads / 64u];
+    __shared__ uint32_t wend[kOffsetThreads / 64u];
+    __shared__ uint32_t wact[kOffsetThreads / 64u];
+    const uint32_t n_rays = min(S->n_rays, P.max_rays);
+    const uint32_t lane = threadIdx.x & 63u, wv = threadIdx.x >> 6;
+    uint32_t carry = 0u, end_max = 0u, active = 0u;
+    for (uint32_t r0 = 0; r0 < n_rays; r0 += 4u * kOffsetThreads) {
+        uint32_t c[4], own = 0u;
+#pragma unroll
+        for (uint32_t k = 0; k < 4u; ++k) {
+            const uint32_t r = r0 + 4u * threadIdx.x + k;
+            c[k]             = r < n_rays ? counts[r] : 0u;
+            own += c[k];
+        }
+        uint32_t inc = own;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t up = (uint32_t)__shfl_up((int)inc, o, 64);
+            if (lane >= (uint32_t)o) inc += up;
+        }
+        if (lane == 63u) wsum[wv] = inc;
+        __syncthreads();
+        uint32_t before = 0u, chunk = 0u;
+        for (uint32_t w = 0; w < kOffsetThreads / 64u; ++w) {
+            before += w < wv ? wsum[w] : 0u;
+            chunk += wsum[w];
+        }
+        uint32_t base = carry + before + inc - own;
+#pragma unroll
+        for (uint32_t k = 0; k < 4u; ++k) {
+            const uint32_t r = r0 + 4u * threadIdx.x + k;
+            if (r < n_rays) {
+                const bool fits = c[k] > 0u && (uint64_t)base + c[k] <= (uint64_t)P.sample_cap;
+                offsets[r]      = base;
+                kept[r]         = fits ? c[k] : 0u;
+                if (fits) {
+                    end_max = max(end_max, base + c[k]);
+                    ++active;
+                }
+            }
+            base += c[k];
+        }
+        carry += chunk;
+        __syncthreads();  // wsum is rewritten by the next chunk
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        end_max = max(end_max, (uint32_t)__shfl_xor((int)end_max, o, 64));
+        active += (uint32_t)__shfl_xor((int)active, o, 64);
+    }
+    if (lane == 0u) {
+        wend[wv] = end_max;
+        wact[wv] = active;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0u) {
+        uint32_t e = 0u, a = 0u;
+        for (uint32_t w = 0; w < kOffsetThreads / 64u; ++w) {
+            e = max(e, wend[w]);
+            a += wact[w];
+        }
+        S->n_samples = e;
+        S->n_active  = a;
+        S->total     = carry;  // occupied samples before the capacity cut
+    }
+}
+
+__global__ __launch_bounds__(256) void k_train_samples_one(TrainParams P, const TrainDevState* S, const NerfExtCamera* __restrict__ cams, const uint32_t* __restrict__ bits, const float4* __restrict__ rays,
+                                                            const uint32_t* __restrict__ offsets, uint32_t* __restrict__ kept, const float* __restrict__ seg_t, float2* __restrict__ samples,
+                                                            uint32_t* __restrict__ sample_ray) {
+    const uint32_t n_rays = min(S->n_rays, P.max_rays);
+    const float cone      = cone_of(cams[S->camera]);
+    for (uint32_t r = blockIdx.x * blockDim.x + threadIdx.x; r < P.max_rays; r += gridDim.x * blockDim.x)
+        if (r >= n_rays) kept[r] = 0u;
+    for (uint32_t r = blockIdx.x * kWaves + (threadIdx.x >> 6); r < n_rays; r += gridDim.x * kWaves) {
+        const uint32_t count = kept[r];
+        if (count == 0u) continue;
+        const uint32_t at = offsets[r];
+        const float4 ro = rays[2ull * r], rd = rays[2ull * r + 1u];
+        const float dt_min = (rd.w - ro.w) / (float)P.max_steps;  // as in wave::march
+        wave::march_range<64u>(ro, rd, cone, dt_min, seg_t[r], 0u, P.max_steps, count, bits, [&](const float p[3]) { return occ_cell_at(P, p); },
+                               [&](uint32_t k, float tm, float dt) {
+                                   samples[at + k]    = make_float2(tm, dt);
+                                   sample_ray[at + k] = r;
+                               },
+                               [](uint32_t, float, uint32_t) {});
+    }
+}
+
 // ----------------------------------------------------- composite fwd + bwd
 // Huber loss (Huber 1964) on the white-composited RGB; gradients with respect
 // to the raw network outputs (see the oracle's orc_composite_backward_ray for
@@ -1716,8 +1814,13 @@ static hipError_t launch_train_stage_common(const TrainParams& P, const TrainBuf
     switch (stage) {
     case NERF_EXT_STAGE_SAMPLE: {
         k_train_rays<<<ray_wave_blocks(P.max_rays), 256, 0, st>>>(P, B.state, B.cams, B.images, B.bits, B.rays, B.gt, B.counts, B.seg_t, B.seg_seen, B.seg_reached, B.segs);
-        k_train_samples<<<ray_wave_blocks(P.max_rays * B.segs), 256, 0, st>>>(P, B.state, B.cams, B.bits, B.rays, B.counts, B.offsets, B.seg_t, B.seg_seen, B.seg_reached, B.segs, B.kept, B.samples,
-                                                                              B.sample_ray);
+        if (B.segs == 1u) {
+            k_ray_offsets<<<1, kOffsetThreads, 0, st>>>(P, B.state, B.counts, B.offsets, B.kept);
+            k_train_samples_one<<<ray_wave_blocks(P.max_rays), 256, 0, st>>>(P, B.state, B.cams, B.bits, B.rays, B.offsets, B.kept, B.seg_t, B.samples, B.sample_ray);
+        } else {
+            k_train_samples<<<ray_wave_blocks(P.max_rays * B.segs), 256, 0, st>>>(P, B.state, B.cams, B.bits, B.rays, B.counts, B.offsets, B.seg_t, B.seg_seen, B.seg_reached, B.segs, B.kept, B.samples,
+                                                                                  B.sample_ray);
+        }
         break;
     }
     case NERF_EXT_STAGE_ADAM: return launch_adam(P, B, st);
