@@ -2,7 +2,7 @@
 //
 // Stage                     reference                      here
 // begin step / camera       backend-cuda.cu:1479-1488      k_step_begin
-// occupancy maintenance     :1555-1634                     k_occ_decay, k_occ_eval, k_occ_bits
+// occupancy maintenance     :1555-1634                     k_occ_eval (window), k_occ_bits (decay, bits)
 // ray sampling + march      :422-533                       k_train_rays, scan, k_train_samples
 // field forward             :1328-1339                     launch_field (field.hip)
 // composite fwd/bwd + loss  :1095-1182 (MSE)               k_composite_train (Huber)
@@ -110,16 +110,17 @@ __global__ void k_step_end(TrainParams P, TrainDevState* S) {
 }
 
 // ----------------------------------------------------------- occupancy grid
-__global__ __launch_bounds__(256) void k_occ_decay(TrainParams P, const TrainDevState* S, float* density) {
-    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
-    if (i >= P.occ_cells) return;
-    const uint32_t mode = S->occ_mode;
-    if (mode == kOccWarmupInit) density[i] = 1.0f;          // :1559-1561
-    else if (mode == kOccRefresh) density[i] *= P.occ_decay; // :1563
+// A refresh decays every cell (:1563) and then takes, over the rotating
+// window of cells_per_update cells, max(density, sigma(cell centre))
+// (:1575-1627).  The window's cells are decayed by the kernel that evaluates
+// them and every other cell by k_occ_bits, which then sets the bits, so the
+// refresh is two launches: the same products and maxima as a decay pass
+// before the evaluation.
+__device__ __forceinline__ bool occ_in_window(uint32_t cell, uint32_t start, uint32_t window, uint32_t cells) {
+    return (cell >= start ? cell - start : cell + cells - start) < window;
 }
 
-// density[cell] = max(density[cell], exp(raw sigma(cell centre))) over the
-// rotating window of cells_per_update cells (:1575-1627).
+// density[cell] = max(decay x density[cell], exp(raw sigma(cell centre))).
 template <typename TableT>
 __global__ __launch_bounds__(kThreads) void k_occ_eval(TrainParams P, GridParams g, const TableT* __restrict__ table, const half_t* __restrict__ dparams, const TrainDevState* S, float* density) {
     if (S->occ_mode != kOccRefresh) return;  // uniform across the grid
@@ -148,18 +149,34 @@ __global__ __launch_bounds__(kThreads) void k_occ_eval(TrainParams P, GridParams
         const floatx4 o = density_mlp(f, to_half8(feat));
         if (grp == 0u && k < count) {
             const float sigma = expf(o[0]);
-            density[cell]     = fmaxf(density[cell], sigma);
+            density[cell]     = fmaxf(density[cell] * P.occ_decay, sigma);
         }
     }
 }
 
-// Warmup start: every word all ones, whatever the density (:1569-1571);
-// refresh: bit = density > threshold, strict (:1628-1634).
-__global__ __launch_bounds__(256) void k_occ_bits(TrainParams P, const TrainDevState* S, const float* density, uint32_t* bits) {
+// Warmup start: density 1 and every word all ones (:1559-1561, :1569-1571);
+// refresh: the decay of the cells outside the window, then bit = density >
+// threshold, strict (:1628-1634).  window: the refresh window's size (the
+// window's own cells were decayed when they were evaluated).
+__global__ __launch_bounds__(256) void k_occ_bits(TrainParams P, const TrainDevState* S, uint32_t window, float* density, uint32_t* bits) {
     const uint32_t mode = S->occ_mode;
     if (mode == kOccNone) return;
     const uint32_t cell = blockIdx.x * 256u + threadIdx.x;
-    const bool occ      = cell < P.occ_cells && (mode == kOccWarmupInit || density[cell > P.occ_cells - 1u ? P.occ_cells - 1u : cell] > P.occ_threshold);
+    bool occ            = false;
+    if (cell < P.occ_cells) {
+        if (mode == kOccWarmupInit) {
+            density[cell] = 1.0f;
+            occ           = true;
+        } else {
+            const uint32_t start = (uint32_t)((uint64_t)S->frame * window % P.occ_cells);
+            float d              = density[cell];
+            if (!occ_in_window(cell, start, window, P.occ_cells)) {
+                d *= P.occ_decay;
+                density[cell] = d;
+            }
+            occ = d > P.occ_threshold;
+        }
+    }
     const uint64_t b    = mode == kOccWarmupInit ? ~0ull : __ballot(occ);
     const uint32_t words = (P.occ_cells + 31u) / 32u;
     const uint32_t w0    = (blockIdx.x * 256u + (threadIdx.x & ~63u)) >> 5;
@@ -193,7 +210,7 @@ __global__ __launch_bounds__(256) void k_occ_apply_field(TrainParams P, const Tr
     if (k >= window || S->occ_mode != kOccRefresh) return;
     const uint32_t start = (uint32_t)((uint64_t)S->frame * window % P.occ_cells);
     const uint32_t cell  = (start + k) % P.occ_cells;
-    density[cell]        = fmaxf(density[cell], field[k].x);
+    density[cell]        = fmaxf(density[cell] * P.occ_decay, field[k].x);
 }
 
 // ---------------------------------------------------------------- sampling
@@ -1845,7 +1862,6 @@ static hipError_t launch_ref_train_stage(const TrainParams& P, const TrainBuffer
         return ref_pack_weights(B.dparams, B.cparams, B.ref.frags, st);
     case NERF_EXT_STAGE_OCCUPANCY:
         if (occupancy_update) {
-            k_occ_decay<<<(P.occ_cells + 255u) / 256u, 256, 0, st>>>(P, B.state, B.density);
             const uint32_t wb = (B.occ_window + 255u) / 256u;
             k_occ_points<<<wb, 256, 0, st>>>(P, B.state, B.occ_window, B.occ_points, B.occ_dirs);
             FieldInputs q{};
@@ -1854,7 +1870,7 @@ static hipError_t launch_ref_train_stage(const TrainParams& P, const TrainBuffer
             const hipError_t e = launch_ref_field(B.ref.frags, q, B.occ_window, B.occ_field, nullptr, st);
             if (e != hipSuccess) return e;
             k_occ_apply_field<<<wb, 256, 0, st>>>(P, B.state, B.occ_window, B.occ_field, B.density);
-            k_occ_bits<<<(P.occ_cells + 255u) / 256u, 256, 0, st>>>(P, B.state, B.density, B.bits);
+            k_occ_bits<<<(P.occ_cells + 255u) / 256u, 256, 0, st>>>(P, B.state, B.occ_window, B.density, B.bits);
         }
         break;
     case NERF_EXT_STAGE_FORWARD: return launch_ref_field(B.ref.frags, in, P.sample_cap, B.field, nullptr, st);
@@ -1877,9 +1893,8 @@ hipError_t launch_train_stage(const TrainParams& P, const TrainBuffers& B, uint3
     case NERF_EXT_STAGE_BEGIN: k_step_begin<<<1, 64, 0, st>>>(P, B.state); break;
     case NERF_EXT_STAGE_OCCUPANCY:
         if (occupancy_update) {
-            k_occ_decay<<<(P.occ_cells + 255u) / 256u, 256, 0, st>>>(P, B.state, B.density);
             k_occ_eval<half_t><<<cus * 4u, kThreads, 0, st>>>(P, B.grid, B.table, B.dparams, B.state, B.density);
-            k_occ_bits<<<(P.occ_cells + 255u) / 256u, 256, 0, st>>>(P, B.state, B.density, B.bits);
+            k_occ_bits<<<(P.occ_cells + 255u) / 256u, 256, 0, st>>>(P, B.state, min(P.occ_cells_per_update, P.occ_cells), B.density, B.bits);
         }
         break;
     case NERF_EXT_STAGE_FORWARD: {
