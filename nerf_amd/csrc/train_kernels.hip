@@ -3,13 +3,16 @@
 // Stage                     reference                      here
 // begin step / camera       backend-cuda.cu:1479-1488      k_step_begin
 // occupancy maintenance     :1555-1634                     k_occ_eval (window), k_occ_bits (decay, bits)
-// ray sampling + march      :422-533                       k_train_rays, scan, k_train_samples
+// ray sampling + march      :422-533                       k_train_rays, k_train_samples (or, for rays of
+//                                                          one segment, k_ray_offsets, k_train_samples_one)
 // field forward             :1328-1339                     launch_field (field.hip)
 // composite fwd/bwd + loss  :1095-1182 (MSE)               k_composite_train (Huber)
-// MLP backward              :784-909, 1267-1301 (cuBLAS)   k_bwd_dx (dfeat, dW partials), k_dw_reduce
-// hash-table backward       (hash-grid model)              k_coarse_scatter, k_coarse_reduce (coarse levels);
-//                                                          k_bin_pass (count, fill), scan, k_bin_accumulate
-// grad stats, Adam          :1447-1554                     in the gradient writers; k_adam
+// MLP backward              :784-909, 1267-1301 (cuBLAS)   k_bwd_dx (dfeat, dW partials)
+// hash-table backward       (hash-grid model)              k_coarse_scatter (coarse levels); k_bin_pass
+//                                                          (count, on a second stream; fill) or
+//                                                          k_bin_fill_staged, scan
+// gradient sums             :1286-1301                     k_grad_reduce (bins, coarse chunks, dW partials)
+// grad stats, Adam          :1447-1554                     in the gradient writers, k_grad_norm; k_adam
 // end step                  :1495-1512                     k_step_end
 //
 // MI355X choices: every count lives in device memory and every launch has a
