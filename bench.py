@@ -690,6 +690,9 @@ def main() -> int:
     ap.add_argument("--no-reference-legs", action="store_true", help="skip the reference-model training, reference-host and reference-model render legs")
     ap.add_argument("--width", type=int, default=W, help="render width (the metric is quoted at 800)")
     ap.add_argument("--height", type=int, default=H, help="render height (the metric is quoted at 800)")
+    ap.add_argument("--only", choices=["render", "stages", "train", "reftrain", "refhost", "configs", "refrender"], default=None,
+                    help="run one leg only and print its result (for profiling a leg under rocprofv3): the headline render (3 renders), the stage rooflines, "
+                         "training (30 + 30 steps), reference-model training, the reference host's workload, the C4/C5 renders, the reference-model render")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain fp32->fp16 conversion over MIB MiB of input (reads 4 B, writes 2 B per element) to calibrate HBM counters, then exit")
     args = ap.parse_args()
@@ -710,6 +713,28 @@ def main() -> int:
             L.call("nerf_ext_float_to_half", src.ptr, dst.ptr, n, None)
         synchronize()
         print(json.dumps({"copy_calibration": {"elements": n, "read_bytes": 4 * n, "write_bytes": 2 * n, "kernel": "k_float_to_half", "launches": 3}}), flush=True)
+        return 0
+    if args.only:
+        if args.only == "render":
+            scene, bits, desc, model, cam, occ = build_workload()
+            renderer = ext.Renderer()
+            for _ in range(3):
+                renderer.render(model, occ, [cam], MAX_STEPS, T_STOP)
+            synchronize()
+            result = {"renders": 3}
+        elif args.only == "stages":
+            result = kernel_rooflines(reps_small=50)
+        elif args.only == "train":
+            result, _ = train_bench(30, 30)
+        elif args.only == "reftrain":
+            result = ref_train_bench(20, 10)
+        elif args.only == "refhost":
+            result = reference_host_bench(steps=60)
+        elif args.only == "configs":
+            result = config_renders(reps=1)
+        else:
+            result = ref_model_render(reps=1)
+        print(json.dumps({"leg": args.only, "result": result}), flush=True)
         return 0
     t_start = time.perf_counter()
 

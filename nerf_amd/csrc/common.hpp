@@ -432,6 +432,10 @@ struct FieldInputs {
     // (whose L2 then holds those levels), followed by the MLPs as a pass over
     // the features.  Same values as the fused kernel.
     bool sparse;
+    // With sparse: level-major scratch [16][capacity] of fp16 feature pairs,
+    // which the level-split encode writes (each XCD whole lines of its
+    // levels) and the MLP pass reads, writing features_out row by row.
+    uint32_t* features_lm;
 };
 
 struct PointsFromSamples {
@@ -475,7 +479,9 @@ struct FieldWeights {
 
 // XCD-split encode of a sample stream's positions into fp16 features [n][32]
 // (16-level grids, fp16 table), the sample count read on the device.
-hipError_t launch_encode_samples(const GridParams& g, const half_t* table, const FieldInputs& in, uint32_t cap, half_t* features, hipStream_t stream);
+// Level-split encode of a march sample stream: features [cap][32] fp16 rows,
+// or with lm, level-major fp16 pairs lm[level * cap + sample].
+hipError_t launch_encode_samples(const GridParams& g, const half_t* table, const FieldInputs& in, uint32_t cap, half_t* features, uint32_t* lm, hipStream_t stream);
 // out4 [n] float4 (sigma, r, g, b).
 hipError_t launch_field(const GridParams& g, const void* table, const FieldWeights& w, const FieldInputs& in, uint32_t n, float4* out4, hipStream_t stream);
 // Density network only, on points or on fp16 features: out [n][16] = (exp(raw0), raw1..15).

@@ -343,8 +343,29 @@ struct DirsFromSamples {
     }
 };
 
-template <typename Dirs>
-__global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(kMlpWaves, 8))) void k_field_mlp(const half_t* __restrict__ dparams, const half_t* __restrict__ cparams, const half_t* __restrict__ features,
+// Features come from rows [n][32] or from level-major fp16 pairs (the
+// sparse training batch's encode), whose rows the pass then writes for the
+// backward.
+struct FeatsFromRows {
+    const half_t* rows;
+    __device__ __forceinline__ half8_t at(uint32_t q, uint32_t grp, bool) const { return *reinterpret_cast<const half8_t*>(rows + (uint64_t)q * 32u + 8u * grp); }
+};
+struct FeatsFromLevels {
+    const uint32_t* lm;  // [16][stride]
+    uint32_t stride;
+    half_t* rows;        // [n][32], written
+    __device__ __forceinline__ half8_t at(uint32_t q, uint32_t grp, bool store) const {
+        uint32_t v[4];
+#pragma unroll
+        for (uint32_t j = 0; j < 4u; ++j) v[j] = lm[(uint64_t)(4u * grp + j) * stride + q];
+        const half8_t h = __builtin_bit_cast(half8_t, v);
+        if (store) *reinterpret_cast<half8_t*>(rows + (uint64_t)q * 32u + 8u * grp) = h;
+        return h;
+    }
+};
+
+template <typename Dirs, typename Feats>
+__global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(kMlpWaves, 8))) void k_field_mlp(const half_t* __restrict__ dparams, const half_t* __restrict__ cparams, Feats features,
                                                                                                                   Dirs dirs, float4* __restrict__ out) {
     const uint32_t n = dirs.count();
     __shared__ __align__(16) half8_t frag[kFieldFrags][kWaveSize];
@@ -366,7 +387,7 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
 #pragma unroll
         for (uint32_t t = 0; t < 4u; ++t) {
             const uint32_t q = min(base + 16u * t + s16, n - 1u);
-            x[t]             = *reinterpret_cast<const half8_t*>(features + (uint64_t)q * 32u + 8u * grp);
+            x[t]             = features.at(q, grp, base + 16u * t + s16 < n);
         }
         float d[3];
         dirs.at(min(base + lane, n - 1u), d);
@@ -458,9 +479,13 @@ hipError_t launch_field(const GridParams& g, const void* table, const FieldWeigh
     if (in.sparse && from_samples && in.features_out && !in.sample_index && !in.alpha_in_order && g.table_dtype != NERF_EXT_F32 && g.n_levels == 16u) {
         // Sparse samples: encode level group by level group, one group per
         // XCD, into features_out, then the MLPs over those features.
-        const hipError_t e = launch_encode_samples(g, (const half_t*)table, in, n, in.features_out, stream);
+        const hipError_t e = launch_encode_samples(g, (const half_t*)table, in, n, in.features_out, in.features_lm, stream);
         if (e != hipSuccess) return e;
-        k_field_mlp<<<mlp_pass_blocks(n), kBlockThreads, 0, stream>>>(w.density, w.color, in.features_out, DirsFromSamples{in.sample_ray, in.rays, in.n_dev, n}, out4);
+        const DirsFromSamples dirs{in.sample_ray, in.rays, in.n_dev, n};
+        if (in.features_lm)
+            k_field_mlp<<<mlp_pass_blocks(n), kBlockThreads, 0, stream>>>(w.density, w.color, FeatsFromLevels{in.features_lm, n, in.features_out}, dirs, out4);
+        else
+            k_field_mlp<<<mlp_pass_blocks(n), kBlockThreads, 0, stream>>>(w.density, w.color, FeatsFromRows{in.features_out}, dirs, out4);
         return hipGetLastError();
     }
 #define NERF_FIELD_LAUNCH(K)                                                                                                                   \
@@ -563,7 +588,8 @@ NERF_API NerfStatus nerf_ext_field_mlp(const uint16_t* density_params, const uin
     if (n == 0u) return NERF_STATUS_OK;
     NERF_CHECK_ARG(density_params && color_params && features && directions && out, "nerf_ext_field_mlp: null pointer");
     NERF_CHECK_ARG(((uintptr_t)features & 15u) == 0u, "nerf_ext_field_mlp: features must be 16-byte aligned");
-    k_field_mlp<<<mlp_pass_blocks(n), kBlockThreads, 0, (hipStream_t)stream>>>((const half_t*)density_params, (const half_t*)color_params, (const half_t*)features, DirsFromArray{directions, n}, reinterpret_cast<float4*>(out));
+    k_field_mlp<<<mlp_pass_blocks(n), kBlockThreads, 0, (hipStream_t)stream>>>((const half_t*)density_params, (const half_t*)color_params, FeatsFromRows{(const half_t*)features}, DirsFromArray{directions, n},
+                                                                                reinterpret_cast<float4*>(out));
     NERF_LAUNCH_CHECK("k_field_mlp");
     return NERF_STATUS_OK;
 }

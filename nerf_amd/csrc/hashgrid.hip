@@ -111,8 +111,14 @@ __global__ __launch_bounds__(256) void k_encode_tile(GridParams g, const TableT*
 // only lanes holding a point store.
 // Points come from a source (PointsFromArray, PointsFromSamples) whose count
 // may be read on the device.
+// With lm (fp16 output only), the features go level-major instead: level
+// l's pair of sample i at lm[l * lm_stride + i] (a workgroup writes whole
+// lines; rows of [n][32] would collect their 16 levels from 8 XCDs' L2s as
+// partial lines: 134 MB written per 4,096 x 64-step batch for 16 MB of
+// features).
 template <typename TableT, typename OutT, uint32_t kLevels, typename Points>
-__global__ __launch_bounds__(256) void k_encode_split(GridParams g, const TableT* __restrict__ table, Points src, OutT* __restrict__ out, bool nt, uint32_t phase) {
+__global__ __launch_bounds__(256) void k_encode_split(GridParams g, const TableT* __restrict__ table, Points src, OutT* __restrict__ out, bool nt, uint32_t phase, uint32_t* __restrict__ lm = nullptr,
+                                                      uint32_t lm_stride = 0u) {
     constexpr uint32_t kParts = kLevels >= 2u ? kLevels / 2u : 1u;  // XCDs sharing one level group
     const uint32_t xcd = blockIdx.x & 7u, group = xcd % (8u / kParts), part = xcd / (8u / kParts);
     uint32_t slot = blockIdx.x >> 3, slots = gridDim.x >> 3;
@@ -141,6 +147,16 @@ __global__ __launch_bounds__(256) void k_encode_split(GridParams g, const TableT
             }
         }
         if (i >= n) continue;
+        if constexpr (sizeof(OutT) == 2u) {
+            if (lm) {
+#pragma unroll
+                for (uint32_t j = 0; j < kLevels; ++j)
+                    if (l0 + j < g.n_levels)
+                        lm[(uint64_t)(l0 + j) * lm_stride + i] =
+                            (uint32_t)__builtin_bit_cast(uint16_t, to_half_rne(f[2u * j])) | ((uint32_t)__builtin_bit_cast(uint16_t, to_half_rne(f[2u * j + 1u])) << 16);
+                continue;
+            }
+        }
         OutT* o = out + (uint64_t)i * width + 2u * l0;
         if (l0 + kLevels <= g.n_levels) {  // uniform: every level of the group exists
             // 16-byte stores.  With nt (large launches) non-temporal: the
@@ -197,7 +213,7 @@ __global__ __launch_bounds__(256) void k_encode_indices(GridParams g, const floa
     }
 }
 
-hipError_t launch_encode_samples(const GridParams& g, const half_t* table, const FieldInputs& in, uint32_t cap, half_t* features, hipStream_t stream) {
+hipError_t launch_encode_samples(const GridParams& g, const half_t* table, const FieldInputs& in, uint32_t cap, half_t* features, uint32_t* lm, hipStream_t stream) {
     if (cap == 0u) return hipSuccess;
     if (g.n_levels != 16u || g.table_dtype != NERF_EXT_F16) return hipErrorInvalidValue;
     PointsFromSamples src{in.samples, in.sample_ray, in.rays, in.n_dev, cap, {in.bmin[0], in.bmin[1], in.bmin[2]}, {in.bmax[0], in.bmax[1], in.bmax[2]}};
@@ -211,9 +227,9 @@ hipError_t launch_encode_samples(const GridParams& g, const half_t* table, const
     // reference host's 4,096 rays x <= 64 steps: 117 us for two levels per
     // XCD, 95 us for the two phases as two launches).
     if (4u * level_bytes <= (2ull << 20)) {
-        k_encode_split<half_t, half_t, 4u><<<8u * ((blocks_256 + 1u) / 2u), 256, 0, stream>>>(g, table, src, features, false, 0u);
+        k_encode_split<half_t, half_t, 4u><<<8u * ((blocks_256 + 1u) / 2u), 256, 0, stream>>>(g, table, src, features, false, 0u, lm, cap);
     } else {
-        k_encode_split<half_t, half_t, 1u><<<16u * blocks_256, 256, 0, stream>>>(g, table, src, features, false, 2u);
+        k_encode_split<half_t, half_t, 1u><<<16u * blocks_256, 256, 0, stream>>>(g, table, src, features, false, 2u, lm, cap);
     }
     return hipGetLastError();
 }

@@ -87,6 +87,7 @@ struct TrainBuffers {
     uint32_t* sample_ray;        // [sample_cap]
     float4* field;               // [sample_cap] (sigma, r, g, b)
     half_t* features;            // [sample_cap][32]
+    uint32_t* features_lm;         // [16][sample_cap] fp16 feature pairs, level-major (sparse batches' encode)
     float4* draw;                // [sample_cap] (d sigma_raw, d r, d g, d b)
     float2* dfeat;               // [16 levels][sample_cap] d(features), loss-scaled
     // binned hash-grid scatter: records (entry within bin, 2 values) grouped

@@ -1914,7 +1914,8 @@ hipError_t launch_train_stage(const TrainParams& P, const TrainBuffers& B, uint3
         // At up to 128 steps per ray a ray's samples are spread over the
         // whole box (neighbouring samples rarely share a fine-level cell), so
         // the batch takes the level-split encode and a separate MLP pass.
-        in.sparse = P.max_steps <= 128u;
+        in.sparse      = P.max_steps <= 128u;
+        in.features_lm = B.features_lm;
         return launch_field(B.grid, B.table, FieldWeights{B.dparams, B.cparams}, in, P.sample_cap, B.field, st);
     }
     case NERF_EXT_STAGE_COMPOSITE: return launch_composite_train(P, B, st);

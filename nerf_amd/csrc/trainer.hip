@@ -162,6 +162,7 @@ NerfStatus trainer_create(const NerfExtTrainDesc* d, const BorrowedModel* borrow
         NERF_HIP_TRY(hipMemsetAsync(B.occ_dirs, 0, 12ull * B.occ_window, T.stream));
     } else {
     NERF_HIP_TRY(alloc(T, B.features, 32ull * P.sample_cap));
+    NERF_HIP_TRY(alloc(T, B.features_lm, 16ull * P.sample_cap));
     NERF_HIP_TRY(alloc(T, B.dfeat, 16ull * P.sample_cap));
     // Leading dense levels of at most kCoarseMaxEntries entries are summed in
     // LDS slabs; binned, the records of every sample would crowd into their
