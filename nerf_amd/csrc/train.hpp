@@ -26,6 +26,12 @@ struct TrainDevState {
     float loss_sum;       // sum of per-ray Huber losses
     float rays_f;         // adaptive ray count
     NerfTrainStats stats; // last completed step
+    // Adam's copy of the gradient statistics, taken with them: a pipelined
+    // run starts the next step (whose begin clears the fields above) while
+    // Adam still runs.
+    double adam_sumsq;
+    uint32_t adam_nonfinite;
+    uint32_t adam_t;      // optimizer step (frame + 1 of the step that took the gradients)
 };
 
 // Fixed parameters of a configured run (kernel argument).
@@ -151,11 +157,14 @@ inline uint32_t norm_partial_count(const TrainBuffers& B) {
 // scan depend only on the step's samples, so the sample stage starts them
 // there and the backward waits for them, instead of running them between
 // the MLP backward and the record fill.  counted is true once a count has
-// been started after the latest sample stage.
+// been started after the latest sample stage.  A run of several steps also
+// puts each step's begin, occupancy and sample stages there, after the
+// previous step's end (`ready`), so that they overlap its Adam pass.
 struct StepStreams {
     hipStream_t aux    = nullptr;
-    hipEvent_t sampled = nullptr;  // the sample stage's end, on the step's stream
+    hipEvent_t sampled = nullptr;  // the sample stage's end, on the stream it ran on
     hipEvent_t done    = nullptr;  // the count and scan's end, on aux
+    hipEvent_t ready   = nullptr;  // what the next step's first stages wait for, on the step's stream
     bool counted       = false;
 };
 

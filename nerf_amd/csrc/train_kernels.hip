@@ -1631,8 +1631,11 @@ __global__ __launch_bounds__(kNormThreads) void k_grad_norm(const double* __rest
     if (threadIdx.x == 0u) {
         double t = 0.0;
         for (uint32_t w = 0; w < kNormThreads / 64u; ++w) t += ws[w];
-        S->grad_sumsq = t;
-        S->nonfinite  = bad;
+        S->grad_sumsq     = t;
+        S->nonfinite      = bad;
+        S->adam_sumsq     = t;
+        S->adam_nonfinite = bad;
+        S->adam_t         = S->frame + 1u;
     }
 }
 
@@ -1643,11 +1646,13 @@ struct AdamCoef {
     float lr, gs, bc1, bc2;  // gs: clip factor / loss scale
     uint32_t skip;
 };
+// Reads Adam's copy of the statistics (k_grad_norm), which the next step's
+// begin leaves alone.
 __device__ AdamCoef adam_coef(const TrainParams& P, const TrainDevState* S) {
-    const float gn   = (float)sqrt(S->grad_sumsq > 0.0 ? S->grad_sumsq : 0.0) / P.loss_scale;
-    const uint32_t t = S->frame + 1u;  // optimizer step
+    const float gn   = (float)sqrt(S->adam_sumsq > 0.0 ? S->adam_sumsq : 0.0) / P.loss_scale;
+    const uint32_t t = S->adam_t;  // optimizer step
     AdamCoef c;
-    c.skip = (S->nonfinite != 0u || !isfinite(gn) || gn > P.guard) ? 1u : 0u;
+    c.skip = (S->adam_nonfinite != 0u || !isfinite(gn) || gn > P.guard) ? 1u : 0u;
     if (c.skip) {
         c.lr = 0.0f;
         c.gs = 1.0f / P.loss_scale;
@@ -1927,7 +1932,7 @@ hipError_t launch_train_stage(const TrainParams& P, const TrainBuffers& B, uint3
         // MLP backward (2^18 samples: 17.5 + 9.5 us off the step's chain).
         ss->counted = false;
         if ((e = hipEventRecord(ss->sampled, st)) != hipSuccess) return e;
-        if ((e = hipStreamWaitEvent(ss->aux, ss->sampled, 0)) != hipSuccess) return e;
+        if (st != ss->aux && (e = hipStreamWaitEvent(ss->aux, ss->sampled, 0)) != hipSuccess) return e;
         if ((e = launch_bin_count(P, B, ss->aux)) != hipSuccess) return e;
         if ((e = hipEventRecord(ss->done, ss->aux)) != hipSuccess) return e;
         ss->counted = true;

@@ -17,6 +17,7 @@ Trainer::~Trainer() {
     if (stream) (void)hipStreamSynchronize(stream);
     if (side.sampled) (void)hipEventDestroy(side.sampled);
     if (side.done) (void)hipEventDestroy(side.done);
+    if (side.ready) (void)hipEventDestroy(side.ready);
     if (side.aux) (void)hipStreamDestroy(side.aux);
     for (void* p : owned)
         if (p) (void)hipFree(p);
@@ -42,6 +43,42 @@ NerfStatus Trainer::run_stages(uint32_t first, uint32_t last) {
     for (uint32_t s = first; s <= last; ++s) {
         NERF_HIP_TRY(launch_train_stage(P, B, s, occupancy_due(host_frame), stream, &side));
         if (s == NERF_EXT_STAGE_END) ++host_frame;
+    }
+    return NERF_STATUS_OK;
+}
+
+// Several whole steps.  With a second stream each step's begin, occupancy
+// and sample stages (and the record count) run there, after the previous
+// step's end, so that they overlap its Adam pass: Adam is the last stage on
+// the step's stream, after the end of the step, and reads its own copy of the
+// gradient statistics and step index (TrainDevState::adam_*).  The next
+// step's stages touch nothing Adam reads or writes, except the occupancy
+// refresh, which evaluates the field with the weights Adam writes: a step that
+// refreshes waits for the whole previous step.  The first step waits for all
+// the work already on the step's stream, so the overlap stays inside one call
+// and work a caller enqueues between calls is ordered as before.  Every
+// stage of a step still ends before the step's stream passes its forward
+// pass, so synchronizing that stream covers the whole run.
+NerfStatus Trainer::run_steps(uint32_t steps) {
+    if (!side.aux || !side.ready || steps < 2u) {
+        for (uint32_t i = 0; i < steps; ++i) {
+            const NerfStatus s = run_stages(NERF_EXT_STAGE_BEGIN, NERF_EXT_STAGE_END);
+            if (s != NERF_STATUS_OK) return s;
+        }
+        return NERF_STATUS_OK;
+    }
+    NERF_HIP_TRY(hipEventRecord(side.ready, stream));
+    for (uint32_t i = 0; i < steps; ++i) {
+        const bool occ = occupancy_due(host_frame);
+        if (occ) NERF_HIP_TRY(hipEventRecord(side.ready, stream));  // after the previous step's Adam
+        NERF_HIP_TRY(hipStreamWaitEvent(side.aux, side.ready, 0));
+        for (uint32_t s = NERF_EXT_STAGE_BEGIN; s <= NERF_EXT_STAGE_SAMPLE; ++s) NERF_HIP_TRY(launch_train_stage(P, B, s, occ, side.aux, &side));
+        NERF_HIP_TRY(hipStreamWaitEvent(stream, side.sampled, 0));
+        for (uint32_t s = NERF_EXT_STAGE_FORWARD; s <= NERF_EXT_STAGE_BACKWARD; ++s) NERF_HIP_TRY(launch_train_stage(P, B, s, occ, stream, &side));
+        NERF_HIP_TRY(launch_train_stage(P, B, NERF_EXT_STAGE_END, occ, stream, &side));
+        ++host_frame;
+        NERF_HIP_TRY(hipEventRecord(side.ready, stream));
+        NERF_HIP_TRY(launch_train_stage(P, B, NERF_EXT_STAGE_ADAM, occ, stream, &side));
     }
     return NERF_STATUS_OK;
 }
@@ -201,6 +238,7 @@ NerfStatus trainer_create(const NerfExtTrainDesc* d, const BorrowedModel* borrow
         NERF_HIP_TRY(hipStreamCreateWithFlags(&T.side.aux, hipStreamNonBlocking));
         NERF_HIP_TRY(hipEventCreateWithFlags(&T.side.sampled, hipEventDisableTiming));
         NERF_HIP_TRY(hipEventCreateWithFlags(&T.side.done, hipEventDisableTiming));
+        NERF_HIP_TRY(hipEventCreateWithFlags(&T.side.ready, hipEventDisableTiming));
     }
     }
     NERF_HIP_TRY(alloc(T, B.table_grad, B.table_elems));
@@ -318,11 +356,7 @@ NERF_API NerfStatus nerf_ext_trainer_destroy(NerfExtTrainer* trainer) {
 
 NERF_API NerfStatus nerf_ext_trainer_step(NerfExtTrainer* trainer, uint32_t steps) {
     NERF_CHECK_ARG(trainer && trainer->t, "nerf_ext_trainer_step: null trainer");
-    for (uint32_t i = 0; i < steps; ++i) {
-        const NerfStatus s = trainer->t->run_stages(NERF_EXT_STAGE_BEGIN, NERF_EXT_STAGE_END);
-        if (s != NERF_STATUS_OK) return s;
-    }
-    return NERF_STATUS_OK;
+    return trainer->t->run_steps(steps);
 }
 
 NERF_API NerfStatus nerf_ext_trainer_run_stages(NerfExtTrainer* trainer, uint32_t first, uint32_t last) {

@@ -35,6 +35,7 @@ struct Trainer {
     ~Trainer();
     bool occupancy_due(uint32_t frame) const;
     NerfStatus run_stages(uint32_t first, uint32_t last);
+    NerfStatus run_steps(uint32_t steps);  // whole steps, consecutive ones overlapped
     NerfStatus read_state(TrainDevState& host);
     // Zeroes gradients, Adam moments, the occupancy grid and the step state
     // (frame 0, initial ray count); the weights are left as they are.

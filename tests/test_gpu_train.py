@@ -446,3 +446,34 @@ def test_gradients_deterministic(dataset):
     assert np.array_equal(grads[0][2], grads[1][2]), "weights after two steps differ between runs"
     assert np.array_equal(grads[0][0], grads[1][0]), "table gradients differ between runs"
     assert np.array_equal(grads[0][1], grads[1][1]), "MLP weight gradients differ between runs"
+
+
+def test_pipelined_steps_match_stage_by_stage(dataset):
+    """Whole steps from one call (each step's begin and sampler overlapping
+    the previous step's Adam on the trainer's second stream) leave the same
+    weights, moments, occupancy and step state bit for bit as the same steps
+    enqueued one stage range at a time.  Ten steps cross the warm-up and two
+    occupancy refreshes (frames 4 and 8), which wait for the previous Adam."""
+    announce("train: pipelined steps vs stage by stage, 10 steps")
+    runs = []
+    for pipelined in (True, False):
+        t, _ = _trainer(dataset, log2_table=17, target_samples=RAYS * 24)
+        if pipelined:
+            t.step(10)
+        else:
+            for _ in range(10):
+                t.run_stages(L.NERF_EXT_STAGE_BEGIN, L.NERF_EXT_STAGE_END)
+        st = t.stats()
+        B = t.buffers()
+        E = int(B.table_elems)
+        cells = OCC_RES ** 3
+        runs.append({"table_f32": ext.read_device(B.table_f32, (E,), np.uint32), "table_m": ext.read_device(B.table_m, (E,), np.uint32), "table_v": ext.read_device(B.table_v, (E,), np.uint32),
+                     "mlp_f32": ext.read_device(B.mlp_f32, (10240,), np.uint32), "mlp_v": ext.read_device(B.mlp_v, (10240,), np.uint32),
+                     "density": ext.read_device(B.density_grid, (cells,), np.uint32), "bits": ext.read_device(B.bitfield, (cells // 32,), np.uint32),
+                     "stats": (st.last.completed_steps, st.last.last_train_camera, st.rays, st.samples_total, st.skipped, st.last.has_nonfinite,
+                               np.float32(st.last.loss).view(np.uint32), np.float32(st.last.grad_norm).view(np.uint32))})
+        t.close()
+    a, b = runs
+    assert a["stats"][0] == 10
+    for k in a:
+        assert np.array_equal(np.asarray(a[k]), np.asarray(b[k])), f"{k} differs between pipelined and stage-by-stage steps"
