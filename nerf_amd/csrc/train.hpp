@@ -168,15 +168,26 @@ struct StepStreams {
     bool counted       = false;
 };
 
+// Folds of a step's one-thread stages into their neighbours, for callers that
+// enqueue the neighbours too (each launch costs a few microseconds whatever
+// it does).  kFoldBegin: the begin stage launches nothing and the step's
+// first kernel (the occupancy refresh, else the ray pass; hash-grid model)
+// does the begin.  kFoldEnd: the end stage launches nothing and the
+// backward's gradient-norm kernel does the end (before Adam, which reads its
+// own copy of the step index).
+enum : uint32_t { kFoldBegin = 1u, kFoldEnd = 2u };
+
 // Launches one stage (NERF_EXT_STAGE_*) of a training step on `stream`.
 // `occupancy_update` selects the occupancy-maintenance kernels (the schedule
 // is a function of the step index, which the host tracks).  ss may be null
-// (then the count runs in the backward, on `stream`).
-hipError_t launch_train_stage(const TrainParams& P, const TrainBuffers& B, uint32_t stage, bool occupancy_update, hipStream_t stream, StepStreams* ss);
+// (then the count runs in the backward, on `stream`).  fold: kFold* bits,
+// passed to the stages on either side of the one folded away.
+hipError_t launch_train_stage(const TrainParams& P, const TrainBuffers& B, uint32_t stage, bool occupancy_update, hipStream_t stream, StepStreams* ss, uint32_t fold = 0u);
 
 // Individual stages, exposed for the parity tests through nerf_ext.h.
 hipError_t launch_composite_train(const TrainParams& P, const TrainBuffers& B, hipStream_t stream);
-hipError_t launch_mlp_backward(const TrainParams& P, const TrainBuffers& B, hipStream_t stream, StepStreams* ss);
+// end: the gradient-norm kernel also ends the step (kFoldEnd).
+hipError_t launch_mlp_backward(const TrainParams& P, const TrainBuffers& B, hipStream_t stream, StepStreams* ss, bool end = false);
 hipError_t launch_adam(const TrainParams& P, const TrainBuffers& B, hipStream_t stream);
 
 uint64_t scan_tmp_words(uint32_t n);

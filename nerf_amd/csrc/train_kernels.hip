@@ -12,7 +12,8 @@
 //                                                          (count, on a second stream; fill) or
 //                                                          k_bin_fill_staged, scan
 // gradient sums             :1286-1301                     k_grad_reduce (bins, coarse chunks, dW partials)
-// grad stats, Adam          :1447-1554                     in the gradient writers, k_grad_norm; k_adam
+// grad stats, Adam          :1447-1554                     in the gradient writers, the last workgroup of
+//                                                          k_grad_reduce (k_grad_norm: reference model); k_adam
 // end step                  :1495-1512                     k_step_end
 //
 // MI355X choices: every count lives in device memory and every launch has a
@@ -71,27 +72,55 @@ __device__ __forceinline__ void wave_lds_sync() {
 }
 
 // ------------------------------------------------------------ step control
-__global__ void k_step_begin(TrainParams P, TrainDevState* S) {
-    if (threadIdx.x != 0u || blockIdx.x != 0u) return;
+// What the start of a step decides (:1479-1488): its camera, its occupancy
+// work and its ray count, from the step index and the adaptive ray count.
+struct StepBegin {
+    uint32_t camera, occ_mode, n_rays;
+};
+__device__ __forceinline__ StepBegin step_begin_values(const TrainParams& P, const TrainDevState* S) {
     const uint32_t f = S->frame;
-    S->camera        = hash_u32(f * 747796405u + 2891336453u) % P.image_count;  // :1482
+    StepBegin b;
+    b.camera = hash_u32(f * 747796405u + 2891336453u) % P.image_count;  // :1482
     if (f < P.occ_warmup)
-        S->occ_mode = f == 0u ? kOccWarmupInit : kOccNone;                     // :1483-1485
+        b.occ_mode = f == 0u ? kOccWarmupInit : kOccNone;                // :1483-1485
     else
-        S->occ_mode = (P.occ_interval != 0u && f % P.occ_interval == 0u) ? kOccRefresh : kOccNone;
-    uint32_t rays = (uint32_t)(S->rays_f + 0.5f);
-    rays          = rays < P.min_rays ? P.min_rays : (rays > P.max_rays ? P.max_rays : rays);
-    S->n_rays     = rays;
+        b.occ_mode = (P.occ_interval != 0u && f % P.occ_interval == 0u) ? kOccRefresh : kOccNone;
+    const uint32_t rays = (uint32_t)(S->rays_f + 0.5f);
+    b.n_rays            = rays < P.min_rays ? P.min_rays : (rays > P.max_rays ? P.max_rays : rays);
+    return b;
+}
+__device__ __forceinline__ void step_begin_store(TrainDevState* S, const StepBegin& b) {
+    S->camera     = b.camera;
+    S->occ_mode   = b.occ_mode;
+    S->n_rays     = b.n_rays;
     S->n_samples  = 0u;
     S->n_active   = 0u;
-    S->nonfinite  = 0u;
     S->total      = 0ull;
+    S->nonfinite  = 0u;
     S->grad_sumsq = 0.0;
     S->loss_sum   = 0.0f;
 }
+// A step's first kernel may do the begin itself (begin = true): every
+// workgroup derives the values from the step index and the ray count, which
+// only the end of a step changes, and workgroup 0 stores them; later kernels
+// read them from the state.
+__device__ __forceinline__ StepBegin step_begin_in(const TrainParams& P, TrainDevState* S, bool begin) {
+    if (!begin) return StepBegin{S->camera, S->occ_mode, S->n_rays};
+    const StepBegin b = step_begin_values(P, S);
+    if (blockIdx.x == 0u && threadIdx.x == 0u) step_begin_store(S, b);
+    return b;
+}
 
-__global__ void k_step_end(TrainParams P, TrainDevState* S) {
+__global__ void k_step_begin(TrainParams P, TrainDevState* S) {
     if (threadIdx.x != 0u || blockIdx.x != 0u) return;
+    step_begin_store(S, step_begin_values(P, S));
+}
+
+// :1495-1512 and the ray-count adaptation.  Reads only what the step's
+// kernels up to the gradient norm wrote, and Adam reads none of what it
+// writes (its step index is its own copy), so the gradient-norm kernel may
+// run it (end = true in k_grad_norm).
+__device__ __forceinline__ void step_end(const TrainParams& P, TrainDevState* S) {
     const float inv = S->n_active ? 1.0f / (float)S->n_active : 0.0f;
     const float loss = S->loss_sum * inv;                                          // :1499
     const float gn   = (float)sqrt(S->grad_sumsq > 0.0 ? S->grad_sumsq : 0.0) / P.loss_scale;
@@ -112,6 +141,11 @@ __global__ void k_step_end(TrainParams P, TrainDevState* S) {
     S->frame = S->frame + 1u;
 }
 
+__global__ void k_step_end(TrainParams P, TrainDevState* S) {
+    if (threadIdx.x != 0u || blockIdx.x != 0u) return;
+    step_end(P, S);
+}
+
 // ----------------------------------------------------------- occupancy grid
 // A refresh decays every cell (:1563) and then takes, over the rotating
 // window of cells_per_update cells, max(density, sigma(cell centre))
@@ -125,8 +159,8 @@ __device__ __forceinline__ bool occ_in_window(uint32_t cell, uint32_t start, uin
 
 // density[cell] = max(decay x density[cell], exp(raw sigma(cell centre))).
 template <typename TableT>
-__global__ __launch_bounds__(kThreads) void k_occ_eval(TrainParams P, GridParams g, const TableT* __restrict__ table, const half_t* __restrict__ dparams, const TrainDevState* S, float* density) {
-    if (S->occ_mode != kOccRefresh) return;  // uniform across the grid
+__global__ __launch_bounds__(kThreads) void k_occ_eval(TrainParams P, GridParams g, const TableT* __restrict__ table, const half_t* __restrict__ dparams, TrainDevState* S, bool begin, float* density) {
+    if (step_begin_in(P, S, begin).occ_mode != kOccRefresh) return;  // uniform across the grid
     __shared__ __align__(16) half_t sp[NERF_EXT_DENSITY_PARAMS];
     stage_density<kThreads>(sp, dparams);
     __syncthreads();
@@ -244,11 +278,12 @@ constexpr uint32_t kTrainGroup = 16u;  // lanes per ray in the emission pass (4 
 // wave::march_range keeps near 22 cycles per step.
 constexpr uint32_t kRayGroup = 64u;
 
-__global__ __launch_bounds__(256) void k_train_rays(TrainParams P, const TrainDevState* S, const NerfExtCamera* __restrict__ cams, const uint8_t* __restrict__ images, const uint32_t* __restrict__ bits, float4* __restrict__ rays, float4* __restrict__ gt,
-                                                     uint32_t* __restrict__ counts, float* __restrict__ seg_t, uint32_t* __restrict__ seg_seen, uint32_t* __restrict__ seg_reached, uint32_t segs) {
+__global__ __launch_bounds__(256) void k_train_rays(TrainParams P, TrainDevState* S, bool begin, const NerfExtCamera* __restrict__ cams, const uint8_t* __restrict__ images, const uint32_t* __restrict__ bits, float4* __restrict__ rays,
+                                                     float4* __restrict__ gt, uint32_t* __restrict__ counts, float* __restrict__ seg_t, uint32_t* __restrict__ seg_seen, uint32_t* __restrict__ seg_reached, uint32_t segs) {
     constexpr uint32_t kPer = 64u / kRayGroup;  // rays per wave
     const uint32_t lane = threadIdx.x & 63u, stride = gridDim.x * kWaves * kPer;
-    const uint32_t n_rays = S->n_rays, cam_idx = S->camera, frame = S->frame;
+    const StepBegin sb = step_begin_in(P, S, begin);
+    const uint32_t n_rays = sb.n_rays, cam_idx = sb.camera, frame = S->frame;
     const NerfExtCamera cam = cams[cam_idx];
     const float cone        = cone_of(cam);
     const uint32_t n_live   = min(n_rays, P.max_rays);
@@ -407,13 +442,12 @@ __global__ __launch_bounds__(256) void k_train_samples(TrainParams P, TrainDevSt
 // more than the march (31 us for the pass; this pair 7.4 + 5.9 us).
 constexpr uint32_t kOffsetThreads = 1024u;
 __global__ __launch_bounds__(kOffsetThreads) void k_ray_offsets(TrainParams P, TrainDevState* S, const uint32_t* __restrict__ counts, uint32_t* __restrict__ offsets, uint32_t* __restrict__ kept) {
-    __shared__ uint32_t wsum[kOffsetThreads / 64u];
-    __shared__ uint32_t wend[kOffsetThreads / 64u];
-    __shared__ uint32_t wact[kOffsetThreads / 64u];
+    constexpr uint32_t kT = kOffsetThreads;
+    __shared__ uint32_t wsum[kT / 64u], wend[kT / 64u], wact[kT / 64u];
     const uint32_t n_rays = min(S->n_rays, P.max_rays);
     const uint32_t lane = threadIdx.x & 63u, wv = threadIdx.x >> 6;
     uint32_t carry = 0u, end_max = 0u, active = 0u;
-    for (uint32_t r0 = 0; r0 < n_rays; r0 += 4u * kOffsetThreads) {
+    for (uint32_t r0 = 0; r0 < n_rays; r0 += 4u * kT) {
         uint32_t c[4], own = 0u;
 #pragma unroll
         for (uint32_t k = 0; k < 4u; ++k) {
@@ -430,7 +464,7 @@ __global__ __launch_bounds__(kOffsetThreads) void k_ray_offsets(TrainParams P, T
         if (lane == 63u) wsum[wv] = inc;
         __syncthreads();
         uint32_t before = 0u, chunk = 0u;
-        for (uint32_t w = 0; w < kOffsetThreads / 64u; ++w) {
+        for (uint32_t w = 0; w < kT / 64u; ++w) {
             before += w < wv ? wsum[w] : 0u;
             chunk += wsum[w];
         }
@@ -464,7 +498,7 @@ __global__ __launch_bounds__(kOffsetThreads) void k_ray_offsets(TrainParams P, T
     __syncthreads();
     if (threadIdx.x == 0u) {
         uint32_t e = 0u, a = 0u;
-        for (uint32_t w = 0; w < kOffsetThreads / 64u; ++w) {
+        for (uint32_t w = 0; w < kT / 64u; ++w) {
             e = max(e, wend[w]);
             a += wact[w];
         }
@@ -1434,7 +1468,7 @@ __device__ void bin_accumulate(uint32_t bin, const uint32_t* __restrict__ offset
     }
     __syncthreads();
     // The bin's gradient, and its share of the squared gradient norm (one
-    // partial per workgroup, added by k_grad_norm).
+    // partial per workgroup, added by the last workgroup to finish).
     const double inv = ldexp(1.0, -e);
     double sq        = 0.0;
     for (uint32_t i = threadIdx.x; i < kBinEntries; i += blockDim.x)
@@ -1457,7 +1491,8 @@ __device__ void bin_accumulate(uint32_t bin, const uint32_t* __restrict__ offset
 // parameters; its 16 slices of 16 threads each add every 16th partial (16
 // independent four-wide loads per thread), then the slices are added in a
 // fixed order.  The MLP gradient's share of the squared norm is taken here,
-// from the values written: one partial per workgroup, added by k_grad_norm.
+// from the values written: one partial per workgroup, added by the last
+// workgroup to finish.
 constexpr uint32_t kReduceSlices = 16u;
 // Part vb of the MLP weight-gradient reduction, run by the 256 threads t of
 // half h of a 512-thread workgroup (each half has its own slice sums; both
@@ -1594,25 +1629,26 @@ __global__ __launch_bounds__(512) void k_grad_reduce(GradReduceArgs a) {
     if (b < coarse_pairs) {
         const uint32_t vb = 2u * b + h;
         coarse_reduce(vb < coarse_parts ? vb : 0xFFFFFFFFu, t, h, a.coarse_partials, a.coarse, a.n_dense, a.table_size, a.table_grad, a.norm, part_h);
-        return;
-    }
-    if (b < coarse_pairs + kMlpParams / 128u) {
+    } else if (b < coarse_pairs + kMlpParams / 128u) {
         dw_reduce(2u * (b - coarse_pairs) + h, t, h, a.dw_partials, a.dw_blocks, a.mlp_grad, a.norm + coarse_parts + a.n_bins, part_h);
-        return;
+    } else {
+        bin_accumulate(b - coarse_pairs - kMlpParams / 128u, a.bin_off, kBinBlocks, a.n_bins, a.bin_total, a.rec, a.bin_max, a.hashed_entries, a.hashed_grad, a.norm + coarse_parts, acc, wmax,
+                       wsq);
     }
-    const uint32_t bin = b - coarse_pairs - kMlpParams / 128u;
-    bin_accumulate(bin, a.bin_off, kBinBlocks, a.n_bins, a.bin_total, a.rec, a.bin_max, a.hashed_entries, a.hashed_grad, a.norm + coarse_parts, acc, wmax, wsq);
 }
 
 // The step's squared gradient norm: the sum, in a fixed order, of the
-// per-workgroup partials of k_coarse_reduce, k_bin_accumulate and k_dw_reduce.
-// A partial is the sum of squares of the workgroup's finite gradient values,
-// or -1 minus that sum when one of its values is not finite (the statistics
-// of backend-cuda.cu:1451-1476: finite values summed, a separate flag).
+// per-workgroup partials of the gradient sums (coarse chunks, bins, weight
+// gradients; the reference model's weight-gradient reduction).  A partial is
+// the sum of squares of the workgroup's finite gradient values, or -1 minus
+// that sum when one of its values is not finite (the statistics of
+// backend-cuda.cu:1451-1476: finite values summed, a separate flag).
 // Per-workgroup atomics on one address would serialize; this sum is also
-// independent of the order the workgroups ran in.
+// independent of the order the workgroups ran in.  Each thread adds every
+// kNormThreads-th partial, then the waves are added in order.  Writes the
+// statistics and Adam's copy of them; end: then the end of the step.
 constexpr uint32_t kNormThreads = 1024u;
-__global__ __launch_bounds__(kNormThreads) void k_grad_norm(const double* __restrict__ norm, uint32_t n, TrainDevState* S) {
+__global__ __launch_bounds__(kNormThreads) void k_grad_norm(TrainParams P, const double* __restrict__ norm, uint32_t n, TrainDevState* S, bool end) {
     __shared__ double ws[kNormThreads / 64u];
     __shared__ uint32_t bad;
     if (threadIdx.x == 0u) bad = 0u;
@@ -1636,6 +1672,7 @@ __global__ __launch_bounds__(kNormThreads) void k_grad_norm(const double* __rest
         S->adam_sumsq     = t;
         S->adam_nonfinite = bad;
         S->adam_t         = S->frame + 1u;
+        if (end) step_end(P, S);
     }
 }
 
@@ -1760,7 +1797,7 @@ static hipError_t launch_bin_count(const TrainParams& P, const TrainBuffers& B, 
     return exclusive_scan_u32(B.bin_hist, B.bin_off, B.n_bins * kBinBlocks, B.bin_scan_tmp, B.bin_total, st);
 }
 
-hipError_t launch_mlp_backward(const TrainParams& P, const TrainBuffers& B, hipStream_t st, StepStreams* ss) {
+hipError_t launch_mlp_backward(const TrainParams& P, const TrainBuffers& B, hipStream_t st, StepStreams* ss, bool end) {
     const uint32_t cus = device_cu_count();
     if (B.grid.table_dtype != NERF_EXT_F16) return hipErrorInvalidValue;
     static bool lds_set = false;  // once per process: the kernels' dynamic LDS exceeds the 64 KiB default
@@ -1817,7 +1854,7 @@ hipError_t launch_mlp_backward(const TrainParams& P, const TrainBuffers& B, hipS
     a.norm            = B.norm_partials;
     const uint32_t coarse_pairs = B.n_dense ? (coarse_reduce_blocks(B.coarse) + 1u) / 2u : 0u;
     k_grad_reduce<<<B.n_bins + coarse_pairs + kMlpParams / 128u, 512, 0, st>>>(a);
-    k_grad_norm<<<1, kNormThreads, 0, st>>>(B.norm_partials, norm_partial_count(B), B.state);
+    k_grad_norm<<<1, kNormThreads, 0, st>>>(P, B.norm_partials, norm_partial_count(B), B.state, end);
     return hipGetLastError();
 }
 
@@ -1835,10 +1872,10 @@ hipError_t launch_adam(const TrainParams& P, const TrainBuffers& B, hipStream_t 
 
 // Stages both models share: the sampler, Adam (over whatever parameters the
 // run has) and the end of the step.
-static hipError_t launch_train_stage_common(const TrainParams& P, const TrainBuffers& B, uint32_t stage, hipStream_t st) {
+static hipError_t launch_train_stage_common(const TrainParams& P, const TrainBuffers& B, uint32_t stage, hipStream_t st, uint32_t fold) {
     switch (stage) {
     case NERF_EXT_STAGE_SAMPLE: {
-        k_train_rays<<<ray_wave_blocks(P.max_rays), 256, 0, st>>>(P, B.state, B.cams, B.images, B.bits, B.rays, B.gt, B.counts, B.seg_t, B.seg_seen, B.seg_reached, B.segs);
+        k_train_rays<<<ray_wave_blocks(P.max_rays), 256, 0, st>>>(P, B.state, (fold & kFoldBegin) != 0u, B.cams, B.images, B.bits, B.rays, B.gt, B.counts, B.seg_t, B.seg_seen, B.seg_reached, B.segs);
         if (B.segs == 1u) {
             k_ray_offsets<<<1, kOffsetThreads, 0, st>>>(P, B.state, B.counts, B.offsets, B.kept);
             k_train_samples_one<<<ray_wave_blocks(P.max_rays), 256, 0, st>>>(P, B.state, B.cams, B.bits, B.rays, B.offsets, B.kept, B.seg_t, B.samples, B.sample_ray);
@@ -1849,7 +1886,9 @@ static hipError_t launch_train_stage_common(const TrainParams& P, const TrainBuf
         break;
     }
     case NERF_EXT_STAGE_ADAM: return launch_adam(P, B, st);
-    case NERF_EXT_STAGE_END: k_step_end<<<1, 64, 0, st>>>(P, B.state); break;
+    case NERF_EXT_STAGE_END:
+        if (!(fold & kFoldEnd)) k_step_end<<<1, 64, 0, st>>>(P, B.state);
+        break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -1858,7 +1897,7 @@ static hipError_t launch_train_stage_common(const TrainParams& P, const TrainBuf
 // Stages of the reference model: the same step with the reference's network
 // (packed into MFMA fragments once per step, at its start), its loss and its
 // backward; no hash table.
-static hipError_t launch_ref_train_stage(const TrainParams& P, const TrainBuffers& B, uint32_t stage, bool occupancy_update, hipStream_t st) {
+static hipError_t launch_ref_train_stage(const TrainParams& P, const TrainBuffers& B, uint32_t stage, bool occupancy_update, hipStream_t st, uint32_t fold) {
     FieldInputs in{};
     in.samples    = B.samples;
     in.sample_ray = B.sample_ray;
@@ -1886,22 +1925,24 @@ static hipError_t launch_ref_train_stage(const TrainParams& P, const TrainBuffer
     case NERF_EXT_STAGE_BACKWARD: {
         const hipError_t e = launch_ref_backward_train(B.ref, in, B.draw, P.loss_scale, B.mlp_grad, B.norm_partials, st);
         if (e != hipSuccess) return e;
-        k_grad_norm<<<1, kNormThreads, 0, st>>>(B.norm_partials, norm_partial_count(B), B.state);
+        k_grad_norm<<<1, kNormThreads, 0, st>>>(P, B.norm_partials, norm_partial_count(B), B.state, (fold & kFoldEnd) != 0u);
         break;
     }
-    default: return launch_train_stage_common(P, B, stage, st);
+    default: return launch_train_stage_common(P, B, stage, st, fold & kFoldEnd);
     }
     return hipGetLastError();
 }
 
-hipError_t launch_train_stage(const TrainParams& P, const TrainBuffers& B, uint32_t stage, bool occupancy_update, hipStream_t st, StepStreams* ss) {
-    if (B.model_kind == NERF_EXT_MODEL_REFERENCE) return launch_ref_train_stage(P, B, stage, occupancy_update, st);
+hipError_t launch_train_stage(const TrainParams& P, const TrainBuffers& B, uint32_t stage, bool occupancy_update, hipStream_t st, StepStreams* ss, uint32_t fold) {
+    if (B.model_kind == NERF_EXT_MODEL_REFERENCE) return launch_ref_train_stage(P, B, stage, occupancy_update, st, fold);
     const uint32_t cus = device_cu_count();
     switch (stage) {
-    case NERF_EXT_STAGE_BEGIN: k_step_begin<<<1, 64, 0, st>>>(P, B.state); break;
+    case NERF_EXT_STAGE_BEGIN:
+        if (!(fold & kFoldBegin)) k_step_begin<<<1, 64, 0, st>>>(P, B.state);
+        break;
     case NERF_EXT_STAGE_OCCUPANCY:
         if (occupancy_update) {
-            k_occ_eval<half_t><<<cus * 4u, kThreads, 0, st>>>(P, B.grid, B.table, B.dparams, B.state, B.density);
+            k_occ_eval<half_t><<<cus * 4u, kThreads, 0, st>>>(P, B.grid, B.table, B.dparams, B.state, (fold & kFoldBegin) != 0u, B.density);
             k_occ_bits<<<(P.occ_cells + 255u) / 256u, 256, 0, st>>>(P, B.state, min(P.occ_cells_per_update, P.occ_cells), B.density, B.bits);
         }
         break;
@@ -1925,7 +1966,7 @@ hipError_t launch_train_stage(const TrainParams& P, const TrainBuffers& B, uint3
     }
     case NERF_EXT_STAGE_COMPOSITE: return launch_composite_train(P, B, st);
     case NERF_EXT_STAGE_SAMPLE: {
-        hipError_t e = launch_train_stage_common(P, B, stage, st);
+        hipError_t e = launch_train_stage_common(P, B, stage, st, fold);
         if (e != hipSuccess || !ss || !ss->aux || !B.n_bins) return e;
         // The record count needs only the samples: it runs on the second
         // stream while this one runs the forward pass, the composite and the
@@ -1938,8 +1979,8 @@ hipError_t launch_train_stage(const TrainParams& P, const TrainBuffers& B, uint3
         ss->counted = true;
         return hipSuccess;
     }
-    case NERF_EXT_STAGE_BACKWARD: return launch_mlp_backward(P, B, st, ss);
-    default: return launch_train_stage_common(P, B, stage, st);
+    case NERF_EXT_STAGE_BACKWARD: return launch_mlp_backward(P, B, st, ss, (fold & kFoldEnd) != 0u);
+    default: return launch_train_stage_common(P, B, stage, st, fold);
     }
     return hipGetLastError();
 }

@@ -39,9 +39,22 @@ bool Trainer::occupancy_due(uint32_t frame) const {
     return P.occ_interval != 0u && frame % P.occ_interval == 0u;       // :1487
 }
 
+// The fold bits for stage s of a range that starts at `first` and ends at
+// `last` (kFoldBegin: hash-grid model, the range holds the begin and the
+// step's first kernel; kFoldEnd: the range holds the backward and the end).
+uint32_t Trainer::fold_for(uint32_t s, uint32_t first, uint32_t last, bool occ) const {
+    uint32_t fold = 0u;
+    if (B.model_kind != NERF_EXT_MODEL_REFERENCE && first == NERF_EXT_STAGE_BEGIN && last >= NERF_EXT_STAGE_SAMPLE &&
+        (s == NERF_EXT_STAGE_BEGIN || s == (occ ? NERF_EXT_STAGE_OCCUPANCY : NERF_EXT_STAGE_SAMPLE)))
+        fold |= kFoldBegin;
+    if (first <= NERF_EXT_STAGE_BACKWARD && last == NERF_EXT_STAGE_END && (s == NERF_EXT_STAGE_BACKWARD || s == NERF_EXT_STAGE_END)) fold |= kFoldEnd;
+    return fold;
+}
+
 NerfStatus Trainer::run_stages(uint32_t first, uint32_t last) {
     for (uint32_t s = first; s <= last; ++s) {
-        NERF_HIP_TRY(launch_train_stage(P, B, s, occupancy_due(host_frame), stream, &side));
+        const bool occ = occupancy_due(host_frame);
+        NERF_HIP_TRY(launch_train_stage(P, B, s, occ, stream, &side, fold_for(s, first, last, occ)));
         if (s == NERF_EXT_STAGE_END) ++host_frame;
     }
     return NERF_STATUS_OK;
@@ -50,8 +63,9 @@ NerfStatus Trainer::run_stages(uint32_t first, uint32_t last) {
 // Several whole steps.  With a second stream each step's begin, occupancy
 // and sample stages (and the record count) run there, after the previous
 // step's end, so that they overlap its Adam pass: Adam is the last stage on
-// the step's stream, after the end of the step, and reads its own copy of the
-// gradient statistics and step index (TrainDevState::adam_*).  The next
+// the step's stream, after the end of the step (which the backward's
+// gradient-norm kernel does), and reads its own copy of the gradient
+// statistics and step index (TrainDevState::adam_*).  The next
 // step's stages touch nothing Adam reads or writes, except the occupancy
 // refresh, which evaluates the field with the weights Adam writes: a step that
 // refreshes waits for the whole previous step.  The first step waits for all
@@ -72,10 +86,11 @@ NerfStatus Trainer::run_steps(uint32_t steps) {
         const bool occ = occupancy_due(host_frame);
         if (occ) NERF_HIP_TRY(hipEventRecord(side.ready, stream));  // after the previous step's Adam
         NERF_HIP_TRY(hipStreamWaitEvent(side.aux, side.ready, 0));
-        for (uint32_t s = NERF_EXT_STAGE_BEGIN; s <= NERF_EXT_STAGE_SAMPLE; ++s) NERF_HIP_TRY(launch_train_stage(P, B, s, occ, side.aux, &side));
+        for (uint32_t s = NERF_EXT_STAGE_BEGIN; s <= NERF_EXT_STAGE_SAMPLE; ++s)
+            NERF_HIP_TRY(launch_train_stage(P, B, s, occ, side.aux, &side, fold_for(s, NERF_EXT_STAGE_BEGIN, NERF_EXT_STAGE_SAMPLE, occ)));
         NERF_HIP_TRY(hipStreamWaitEvent(stream, side.sampled, 0));
-        for (uint32_t s = NERF_EXT_STAGE_FORWARD; s <= NERF_EXT_STAGE_BACKWARD; ++s) NERF_HIP_TRY(launch_train_stage(P, B, s, occ, stream, &side));
-        NERF_HIP_TRY(launch_train_stage(P, B, NERF_EXT_STAGE_END, occ, stream, &side));
+        for (uint32_t s = NERF_EXT_STAGE_FORWARD; s <= NERF_EXT_STAGE_BACKWARD; ++s)
+            NERF_HIP_TRY(launch_train_stage(P, B, s, occ, stream, &side, fold_for(s, NERF_EXT_STAGE_BEGIN, NERF_EXT_STAGE_END, occ)));  // the backward ends the step
         ++host_frame;
         NERF_HIP_TRY(hipEventRecord(side.ready, stream));
         NERF_HIP_TRY(launch_train_stage(P, B, NERF_EXT_STAGE_ADAM, occ, stream, &side));

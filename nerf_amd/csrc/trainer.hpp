@@ -34,6 +34,7 @@ struct Trainer {
 
     ~Trainer();
     bool occupancy_due(uint32_t frame) const;
+    uint32_t fold_for(uint32_t stage, uint32_t first, uint32_t last, bool occupancy_update) const;
     NerfStatus run_stages(uint32_t first, uint32_t last);
     NerfStatus run_steps(uint32_t steps);  // whole steps, consecutive ones overlapped
     NerfStatus read_state(TrainDevState& host);
