@@ -416,7 +416,8 @@ typedef struct NerfExtTrainBuffers {
     float* samples;                  /* [cap][2] (t_mid, dt) */
     uint32_t* sample_ray;            /* [cap] */
     float* field;                    /* [cap][4] (sigma, r, g, b) */
-    uint16_t* features;              /* [cap][32] fp16 */
+    uint16_t* features;              /* [cap][32] fp16 (not written when
+                                        features_lm is set) */
     float* draw;                     /* [cap][4] d loss / d raw outputs */
     float* table_grad;               /* [L][T][2] fp32, loss-scaled */
     float* mlp_grad;                 /* [3072 + 7168] fp32, loss-scaled */
@@ -434,6 +435,10 @@ typedef struct NerfExtTrainBuffers {
     float* dfeat;                    /* [16 levels][cap][2] d loss / d features,
                                         loss-scaled, level-major (hash-grid
                                         model; NULL for the reference model) */
+    uint32_t* features_lm;           /* [16 levels][cap] fp16 feature pairs,
+                                        level-major: where the step's features
+                                        are kept for batches of at most 128
+                                        steps per ray; NULL otherwise */
 } NerfExtTrainBuffers;
 
 enum {

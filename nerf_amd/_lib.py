@@ -294,7 +294,8 @@ class NerfExtTrainStats(C.Structure):
 
 class NerfExtTrainBuffers(C.Structure):
     _fields_ = [(k, C.c_void_p) for k in ("state", "rays", "gt", "counts", "kept", "offsets", "samples", "sample_ray", "field", "features", "draw", "table_grad", "mlp_grad", "table_f32", "mlp_f32",
-                                          "table_m", "table_v", "mlp_m", "mlp_v", "bitfield", "density_grid")] + [("max_rays", C.c_uint32), ("sample_capacity", C.c_uint32), ("table_elems", C.c_uint64), ("dfeat", C.c_void_p)]
+                                          "table_m", "table_v", "mlp_m", "mlp_v", "bitfield", "density_grid")] + [("max_rays", C.c_uint32), ("sample_capacity", C.c_uint32), ("table_elems", C.c_uint64), ("dfeat", C.c_void_p),
+                                                                                                                                       ("features_lm", C.c_void_p)]
 
 
 NERF_EXT_STAGE_BEGIN, NERF_EXT_STAGE_OCCUPANCY, NERF_EXT_STAGE_SAMPLE, NERF_EXT_STAGE_FORWARD, NERF_EXT_STAGE_COMPOSITE, NERF_EXT_STAGE_BACKWARD, NERF_EXT_STAGE_ADAM, NERF_EXT_STAGE_END = range(8)

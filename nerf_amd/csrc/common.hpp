@@ -432,9 +432,9 @@ struct FieldInputs {
     // (whose L2 then holds those levels), followed by the MLPs as a pass over
     // the features.  Same values as the fused kernel.
     bool sparse;
-    // With sparse: level-major scratch [16][capacity] of fp16 feature pairs,
-    // which the level-split encode writes (each XCD whole lines of its
-    // levels) and the MLP pass reads, writing features_out row by row.
+    // With sparse: level-major [16][capacity] fp16 feature pairs, which the
+    // level-split encode writes (each XCD whole lines of its levels) instead
+    // of features_out, and the MLP pass reads.
     uint32_t* features_lm;
 };
 

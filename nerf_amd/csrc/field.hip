@@ -344,8 +344,7 @@ struct DirsFromSamples {
 };
 
 // Features come from rows [n][32] or from level-major fp16 pairs (the
-// sparse training batch's encode), whose rows the pass then writes for the
-// backward.
+// sparse training batch's encode, which the backward reads too).
 struct FeatsFromRows {
     const half_t* rows;
     __device__ __forceinline__ half8_t at(uint32_t q, uint32_t grp, bool) const { return *reinterpret_cast<const half8_t*>(rows + (uint64_t)q * 32u + 8u * grp); }
@@ -353,14 +352,11 @@ struct FeatsFromRows {
 struct FeatsFromLevels {
     const uint32_t* lm;  // [16][stride]
     uint32_t stride;
-    half_t* rows;        // [n][32], written
-    __device__ __forceinline__ half8_t at(uint32_t q, uint32_t grp, bool store) const {
+    __device__ __forceinline__ half8_t at(uint32_t q, uint32_t grp, bool) const {
         uint32_t v[4];
 #pragma unroll
         for (uint32_t j = 0; j < 4u; ++j) v[j] = lm[(uint64_t)(4u * grp + j) * stride + q];
-        const half8_t h = __builtin_bit_cast(half8_t, v);
-        if (store) *reinterpret_cast<half8_t*>(rows + (uint64_t)q * 32u + 8u * grp) = h;
-        return h;
+        return __builtin_bit_cast(half8_t, v);
     }
 };
 
@@ -483,7 +479,7 @@ hipError_t launch_field(const GridParams& g, const void* table, const FieldWeigh
         if (e != hipSuccess) return e;
         const DirsFromSamples dirs{in.sample_ray, in.rays, in.n_dev, n};
         if (in.features_lm)
-            k_field_mlp<<<mlp_pass_blocks(n), kBlockThreads, 0, stream>>>(w.density, w.color, FeatsFromLevels{in.features_lm, n, in.features_out}, dirs, out4);
+            k_field_mlp<<<mlp_pass_blocks(n), kBlockThreads, 0, stream>>>(w.density, w.color, FeatsFromLevels{in.features_lm, n}, dirs, out4);
         else
             k_field_mlp<<<mlp_pass_blocks(n), kBlockThreads, 0, stream>>>(w.density, w.color, FeatsFromRows{in.features_out}, dirs, out4);
         return hipGetLastError();

@@ -138,6 +138,13 @@ struct TrainBuffers {
     uint32_t occ_window;         // min(cells_per_update, cells)
 };
 
+// Batches of at most 128 steps per ray (sparse samples) keep the step's
+// features level-major only (features_lm): the level-split encode writes
+// them, the MLP pass and the input-gradient pass read them.
+inline bool sparse_features(const TrainParams& P, const TrainBuffers& B) {
+    return B.model_kind != NERF_EXT_MODEL_REFERENCE && P.max_steps <= 128u && B.grid.n_levels == 16u && B.features_lm != nullptr;
+}
+
 constexpr uint32_t kDxMaxBlocks = 1024;  // workgroups of the input-gradient pass (two per CU)
 constexpr uint32_t kBinEntries = 4096;  // table entries per scatter bin (64 KiB of int64 pairs in LDS)
 constexpr uint32_t kBinBlocks  = 256;   // workgroups of the bin count / fill passes

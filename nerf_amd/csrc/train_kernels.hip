@@ -57,6 +57,16 @@ __device__ __forceinline__ float wave_sum(float v) {
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
     return v;
 }
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += (uint32_t)__shfl_xor((int)v, o, 64);
+    return v;
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o, 64));
+    return v;
+}
 __device__ __forceinline__ double wave_sum_d(double v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
@@ -528,6 +538,103 @@ __global__ __launch_bounds__(256) void k_train_samples_one(TrainParams P, const 
                                },
                                [](uint32_t, float, uint32_t) {});
     }
+}
+
+// Rays of one segment with at most kPrefixRays ray slots (the reference
+// host's 4,096 rays of 64 steps): one launch instead of k_ray_offsets and
+// k_train_samples_one.  Workgroup b owns rays 4b..4b+3, a wave each; it adds
+// the counts of the rays before them itself (at 4,096 rays 8 MB of L2 reads
+// over the whole grid, against a launch of its own for the scan), and the
+// workgroup that owns the last ray scans all counts for the step totals.
+// The kept rays are those whose samples all fit the capacity, a prefix of
+// the rays with samples (offsets only grow): the kept count is the largest
+// inclusive prefix sum within the capacity.
+constexpr uint32_t kPrefixRays = 8192u;
+__global__ __launch_bounds__(256) void k_train_samples_prefix(TrainParams P, TrainDevState* S, const NerfExtCamera* __restrict__ cams, const uint32_t* __restrict__ bits, const float4* __restrict__ rays,
+                                                               const uint32_t* __restrict__ counts, uint32_t* __restrict__ offsets, uint32_t* __restrict__ kept, const float* __restrict__ seg_t,
+                                                               float2* __restrict__ samples, uint32_t* __restrict__ sample_ray) {
+    __shared__ uint32_t red[3][kWaves];
+    const uint32_t n_rays = min(S->n_rays, P.max_rays);
+    const uint32_t lane = threadIdx.x & 63u, wv = threadIdx.x >> 6;
+    const uint32_t r0 = blockIdx.x * kWaves, r = r0 + wv;
+    // Counts before this workgroup's rays (r0 is a multiple of 4: 16-byte loads).
+    uint32_t before = 0u;
+    const uint32_t upto = min(r0, n_rays & ~3u);
+    for (uint32_t i = 4u * threadIdx.x; i < upto; i += 4u * blockDim.x) {
+        const uint4 c = *reinterpret_cast<const uint4*>(counts + i);
+        before += c.x + c.y + c.z + c.w;
+    }
+    for (uint32_t i = upto + threadIdx.x; i < min(r0, n_rays); i += blockDim.x) before += counts[i];
+    before = wave_sum_u32(before);
+    if (lane == 0u) red[0][wv] = before;
+    __syncthreads();
+    uint32_t base = 0u;
+    for (uint32_t w = 0; w < kWaves; ++w) base += red[0][w];
+    for (uint32_t w = 0; w < wv; ++w) base += r0 + w < n_rays ? counts[r0 + w] : 0u;
+    const uint32_t count = r < n_rays ? counts[r] : 0u;
+    const bool fits      = count > 0u && (uint64_t)base + count <= (uint64_t)P.sample_cap;
+    if (r < P.max_rays && lane == 0u) {
+        kept[r] = fits ? count : 0u;
+        if (r < n_rays) offsets[r] = base;
+    }
+    if (n_rays > 0u && blockIdx.x == (n_rays - 1u) / kWaves) {
+        // Step totals: thread t takes a run of `per` counts, the runs' sums
+        // are scanned across the workgroup, then each thread walks its run.
+        const uint32_t per = (n_rays + blockDim.x - 1u) / blockDim.x;
+        const uint32_t a = min(threadIdx.x * per, n_rays), e = min(a + per, n_rays);
+        uint32_t own = 0u;
+        for (uint32_t i = a; i < e; ++i) own += counts[i];
+        uint32_t inc = own;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t up = (uint32_t)__shfl_up((int)inc, o, 64);
+            if (lane >= (uint32_t)o) inc += up;
+        }
+        __syncthreads();  // red[0] was read above
+        if (lane == 63u) red[0][wv] = inc;
+        __syncthreads();
+        uint32_t run = inc - own, total = 0u;
+        for (uint32_t w = 0; w < kWaves; ++w) {
+            run += w < wv ? red[0][w] : 0u;
+            total += red[0][w];
+        }
+        uint32_t end_max = 0u, active = 0u;
+        for (uint32_t i = a; i < e; ++i) {
+            const uint32_t c = counts[i];
+            run += c;
+            if (c > 0u && (uint64_t)run <= (uint64_t)P.sample_cap) {
+                end_max = run;
+                ++active;
+            }
+        }
+        end_max = wave_max_u32(end_max);
+        active  = wave_sum_u32(active);
+        if (lane == 0u) {
+            red[1][wv] = end_max;
+            red[2][wv] = active;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0u) {
+            uint32_t em = 0u, ac = 0u;
+            for (uint32_t w = 0; w < kWaves; ++w) {
+                em = max(em, red[1][w]);
+                ac += red[2][w];
+            }
+            S->n_samples = em;
+            S->n_active  = ac;
+            S->total     = total;  // occupied samples before the capacity cut
+        }
+    }
+    if (!fits) return;
+    const float cone   = cone_of(cams[S->camera]);
+    const float4 ro = rays[2ull * r], rd = rays[2ull * r + 1u];
+    const float dt_min = (rd.w - ro.w) / (float)P.max_steps;  // as in wave::march
+    wave::march_range<64u>(ro, rd, cone, dt_min, seg_t[r], 0u, P.max_steps, count, bits, [&](const float p[3]) { return occ_cell_at(P, p); },
+                           [&](uint32_t k, float tm, float dt) {
+                               samples[base + k]    = make_float2(tm, dt);
+                               sample_ray[base + k] = r;
+                           },
+                           [](uint32_t, float, uint32_t) {});
 }
 
 // ----------------------------------------------------- composite fwd + bwd
@@ -1020,7 +1127,10 @@ __device__ __forceinline__ half8_t op_frag(const half_t* ops, uint32_t row0, uin
     return *reinterpret_cast<const half8_t*>(region + (row0 + r) * kOpPitch + 8u * (g & 1u));
 }
 
-__global__ __launch_bounds__(kThreads) void k_bwd_dx(TrainParams P, const TrainDevState* S, const half_t* __restrict__ dparams, const half_t* __restrict__ cparams, const half_t* __restrict__ features, const float4* __restrict__ draw,
+// features: rows [n][32], or (features_lm non-null) level-major pairs
+// [16][sample_cap].
+__global__ __launch_bounds__(kThreads) void k_bwd_dx(TrainParams P, const TrainDevState* S, const half_t* __restrict__ dparams, const half_t* __restrict__ cparams, const half_t* __restrict__ features,
+                                                     const uint32_t* __restrict__ features_lm, const float4* __restrict__ draw,
                                                      const float2* __restrict__ samples, const uint32_t* __restrict__ sample_ray, const float4* __restrict__ rays, float2* __restrict__ dfeat, float* __restrict__ partials) {
     extern __shared__ __align__(16) half_t dyn[];
     half8_t* F  = reinterpret_cast<half8_t*>(dyn);
@@ -1050,7 +1160,15 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dx(TrainParams P, const TrainD
         const uint32_t q    = live ? s : n - 1u;  // n > 0 here
         float p[3], d[3];
         sample_geometry(samples, sample_ray, rays, P.bmin, P.bmax, q, p, d);
-        const half8_t x = *reinterpret_cast<const half8_t*>(features + (uint64_t)q * 32u + 8u * grp);
+        half8_t x;
+        if (features_lm) {
+            uint32_t v[4];
+#pragma unroll
+            for (uint32_t j = 0; j < 4u; ++j) v[j] = features_lm[(uint64_t)(4u * grp + j) * P.sample_cap + q];
+            x = __builtin_bit_cast(half8_t, v);
+        } else {
+            x = *reinterpret_cast<const half8_t*>(features + (uint64_t)q * 32u + 8u * grp);
+        }
         float4 gr       = draw[q];
         if (!live) gr = make_float4(0.0f, 0.0f, 0.0f, 0.0f);  // padding samples add nothing to the weight gradients
         TileGrad T;
@@ -1809,7 +1927,7 @@ hipError_t launch_mlp_backward(const TrainParams& P, const TrainBuffers& B, hipS
         lds_set = true;
     }
     const uint32_t dx_blocks = min(cus * 2u, kDxMaxBlocks);  // two per CU (LDS)
-    k_bwd_dx<<<dx_blocks, kThreads, kDxLds, st>>>(P, B.state, B.dparams, B.cparams, B.features, B.draw, B.samples, B.sample_ray, B.rays, B.dfeat, B.dw_partials);
+    k_bwd_dx<<<dx_blocks, kThreads, kDxLds, st>>>(P, B.state, B.dparams, B.cparams, B.features, sparse_features(P, B) ? B.features_lm : nullptr, B.draw, B.samples, B.sample_ray, B.rays, B.dfeat, B.dw_partials);
     // Coarse levels: LDS slabs per chunk of samples, then the chunks added.
     if (B.n_dense) {
         const CoarsePlan& C = B.coarse;
@@ -1876,7 +1994,9 @@ static hipError_t launch_train_stage_common(const TrainParams& P, const TrainBuf
     switch (stage) {
     case NERF_EXT_STAGE_SAMPLE: {
         k_train_rays<<<ray_wave_blocks(P.max_rays), 256, 0, st>>>(P, B.state, (fold & kFoldBegin) != 0u, B.cams, B.images, B.bits, B.rays, B.gt, B.counts, B.seg_t, B.seg_seen, B.seg_reached, B.segs);
-        if (B.segs == 1u) {
+        if (B.segs == 1u && P.max_rays <= kPrefixRays) {
+            k_train_samples_prefix<<<(P.max_rays + kWaves - 1u) / kWaves, 256, 0, st>>>(P, B.state, B.cams, B.bits, B.rays, B.counts, B.offsets, B.kept, B.seg_t, B.samples, B.sample_ray);
+        } else if (B.segs == 1u) {
             k_ray_offsets<<<1, kOffsetThreads, 0, st>>>(P, B.state, B.counts, B.offsets, B.kept);
             k_train_samples_one<<<ray_wave_blocks(P.max_rays), 256, 0, st>>>(P, B.state, B.cams, B.bits, B.rays, B.offsets, B.kept, B.seg_t, B.samples, B.sample_ray);
         } else {
@@ -1960,8 +2080,8 @@ hipError_t launch_train_stage(const TrainParams& P, const TrainBuffers& B, uint3
         // At up to 128 steps per ray a ray's samples are spread over the
         // whole box (neighbouring samples rarely share a fine-level cell), so
         // the batch takes the level-split encode and a separate MLP pass.
-        in.sparse      = P.max_steps <= 128u;
-        in.features_lm = B.features_lm;
+        in.sparse      = sparse_features(P, B);
+        in.features_lm = in.sparse ? B.features_lm : nullptr;
         return launch_field(B.grid, B.table, FieldWeights{B.dparams, B.cparams}, in, P.sample_cap, B.field, st);
     }
     case NERF_EXT_STAGE_COMPOSITE: return launch_composite_train(P, B, st);

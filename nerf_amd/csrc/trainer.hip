@@ -430,6 +430,7 @@ NERF_API NerfStatus nerf_ext_trainer_buffers(NerfExtTrainer* trainer, NerfExtTra
     o->sample_capacity = trainer->t->P.sample_cap;
     o->table_elems     = B.table_elems;
     o->dfeat           = (float*)B.dfeat;
+    o->features_lm     = sparse_features(trainer->t->P, B) ? B.features_lm : nullptr;
     return NERF_STATUS_OK;
 }
 

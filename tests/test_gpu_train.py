@@ -70,6 +70,16 @@ def _sample_state(t):
     )
 
 
+def _features(t, n):
+    """The step's fp16 features [n][32]: rows, or the level-major pairs that
+    batches of at most 128 steps per ray keep instead."""
+    B = t.buffers()
+    if B.features_lm:
+        lm = ext.read_device(B.features_lm, (16, B.sample_capacity), np.uint32)[:, :n]
+        return np.ascontiguousarray(lm.T).view(np.float16).reshape(n, 32).astype(np.float32)
+    return ext.read_device(B.features, (n, 32), np.float16).astype(np.float32)
+
+
 def _positions(s):
     """Normalised sample positions and directions, in the fp32 order the field kernel uses."""
     r = s["sample_ray"]
@@ -153,7 +163,8 @@ def test_forward_stage(dataset, log2_table):
     n = s["stats"].samples
     B = t.buffers()
     field = ext.read_device(B.field, (n, 4), np.float32)
-    feats = ext.read_device(B.features, (n, 32), np.float16).astype(np.float32)
+    assert B.features_lm, "64 steps per ray keep the features level-major"
+    feats = _features(t, n)
     table, dp, cp = _model_host(t)
     p, d = _positions(s)
     og = oracle_grid(grid)
@@ -209,7 +220,7 @@ def test_backward_stage(dataset, log2_table):
     s = _sample_state(t)
     n = s["stats"].samples
     B = t.buffers()
-    feats = ext.read_device(B.features, (n, 32), np.float16).astype(np.float32)
+    feats = _features(t, n)
     draw = ext.read_device(B.draw, (n, 4), np.float32)
     mlp_grad = ext.read_device(B.mlp_grad, (10240,), np.float32)
     table_grad = ext.read_device(B.table_grad, (B.table_elems,), np.float32)

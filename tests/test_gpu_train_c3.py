@@ -147,6 +147,7 @@ def c3_step(scene):
     t.run_stages(L.NERF_EXT_STAGE_FORWARD, L.NERF_EXT_STAGE_BACKWARD)
     t.synchronize()  # the trainer's stream does not order with the copies below
     n = s["stats"].samples
+    assert not B.features_lm, "1,024 steps per ray keep the features as rows"
     out = dict(trainer=t, grid=grid, seen=seen, s=s, table=table, dp=dp, cp=cp, cap=cap,
                field=ext.read_device(B.field, (n, 4), np.float32),
                features=ext.read_device(B.features, (n, 32), np.float16).astype(np.float32),
