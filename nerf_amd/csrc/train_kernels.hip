@@ -168,21 +168,60 @@ __device__ __forceinline__ bool occ_in_window(uint32_t cell, uint32_t start, uin
 }
 
 // density[cell] = max(decay x density[cell], exp(raw sigma(cell centre))).
+// bits non-null (whole words: cells and window multiples of 32): the whole
+// occupancy stage in one launch, without k_occ_bits: for a refresh the
+// workgroups first decay the cells of the words outside the window and set
+// those words' bits, then evaluate the window four tiles (64 cells, two
+// words) per workgroup at a time and set the window's words from the new
+// densities; the warm-up start as in k_occ_bits.
 template <typename TableT>
-__global__ __launch_bounds__(kThreads) void k_occ_eval(TrainParams P, GridParams g, const TableT* __restrict__ table, const half_t* __restrict__ dparams, TrainDevState* S, bool begin, float* density) {
-    if (step_begin_in(P, S, begin).occ_mode != kOccRefresh) return;  // uniform across the grid
+__global__ __launch_bounds__(kThreads) void k_occ_eval(TrainParams P, GridParams g, const TableT* __restrict__ table, const half_t* __restrict__ dparams, TrainDevState* S, bool begin, float* density,
+                                                       uint32_t* __restrict__ bits) {
+    const uint32_t mode = step_begin_in(P, S, begin).occ_mode;  // uniform across the grid
+    if (bits && mode == kOccWarmupInit) {  // as k_occ_bits
+        for (uint32_t c = blockIdx.x * blockDim.x + threadIdx.x; c < P.occ_cells; c += gridDim.x * blockDim.x) density[c] = 1.0f;
+        for (uint32_t w = blockIdx.x * blockDim.x + threadIdx.x; w < P.occ_cells / 32u; w += gridDim.x * blockDim.x) bits[w] = ~0u;
+        return;
+    }
+    if (mode != kOccRefresh) return;
     __shared__ __align__(16) half_t sp[NERF_EXT_DENSITY_PARAMS];
+    __shared__ uint32_t half_words[kWaves];
     stage_density<kThreads>(sp, dparams);
-    __syncthreads();
-    const uint32_t lane = threadIdx.x & 63u, grp = lane >> 4, s16 = lane & 15u;
-    DensityFrags f;
-    load_density(sp, f, lane);
+    const uint32_t lane = threadIdx.x & 63u, grp = lane >> 4, s16 = lane & 15u, wave = threadIdx.x >> 6;
     const uint32_t count = P.occ_cells_per_update < P.occ_cells ? P.occ_cells_per_update : P.occ_cells;
     const uint32_t start = (uint32_t)((uint64_t)S->frame * count % P.occ_cells);
+    if (bits) {
+        const uint32_t words = P.occ_cells / 32u, w_start = start / 32u, w_count = count / 32u;
+        for (uint32_t w = blockIdx.x * blockDim.x + threadIdx.x; w < words - w_count; w += gridDim.x * blockDim.x) {
+            const uint32_t word = (w_start + w_count + w) % words;  // the words after the window, wrapping
+            float4* d4          = reinterpret_cast<float4*>(density + 32ull * word);
+            uint32_t b          = 0u;
+#pragma unroll
+            for (uint32_t k = 0; k < 8u; ++k) {
+                float4 v = d4[k];
+                v.x *= P.occ_decay;
+                v.y *= P.occ_decay;
+                v.z *= P.occ_decay;
+                v.w *= P.occ_decay;
+                d4[k] = v;
+                b |= (v.x > P.occ_threshold ? 1u : 0u) << (4u * k);
+                b |= (v.y > P.occ_threshold ? 1u : 0u) << (4u * k + 1u);
+                b |= (v.z > P.occ_threshold ? 1u : 0u) << (4u * k + 2u);
+                b |= (v.w > P.occ_threshold ? 1u : 0u) << (4u * k + 3u);
+            }
+            bits[word] = b;
+        }
+    }
+    __syncthreads();
+    DensityFrags f;
+    load_density(sp, f, lane);
     const uint32_t res   = P.occ_res;
     const float step[3]  = {(P.bmax[0] - P.bmin[0]) / (float)res, (P.bmax[1] - P.bmin[1]) / (float)res, (P.bmax[2] - P.bmin[2]) / (float)res};
     const uint32_t tiles = (count + 15u) / 16u;
-    for (uint32_t tile = blockIdx.x * kWaves + (threadIdx.x >> 6); tile < tiles; tile += gridDim.x * kWaves) {
+    // Chunks of kWaves consecutive tiles per workgroup (a loop uniform across
+    // the workgroup: the word assembly below has barriers).
+    for (uint32_t chunk = blockIdx.x; chunk * kWaves < tiles; chunk += gridDim.x) {
+        const uint32_t tile = chunk * kWaves + wave;
         const uint32_t k    = tile * 16u + s16;
         const uint32_t kq   = k < count ? k : count - 1u;
         const uint32_t cell = (start + kq) % P.occ_cells;
@@ -194,9 +233,22 @@ __global__ __launch_bounds__(kThreads) void k_occ_eval(TrainParams P, GridParams
         float feat[8];
         encode_quad(g, table, p, grp, feat);
         const floatx4 o = density_mlp(f, to_half8(feat));
+        bool occ        = false;
         if (grp == 0u && k < count) {
             const float sigma = expf(o[0]);
-            density[cell]     = fmaxf(density[cell] * P.occ_decay, sigma);
+            const float d     = fmaxf(density[cell] * P.occ_decay, sigma);
+            density[cell]     = d;
+            occ               = d > P.occ_threshold;
+        }
+        if (bits) {
+            const uint32_t b = (uint32_t)__ballot(occ) & 0xFFFFu;  // lanes 0..15: cells 16 tile .. 16 tile + 15
+            if (lane == 0u) half_words[wave] = b;
+            __syncthreads();
+            if (threadIdx.x < kWaves / 2u) {
+                const uint32_t k0 = (chunk * kWaves + 2u * threadIdx.x) * 16u;  // first cell of the word within the window
+                if (k0 < count) bits[(start + k0) % P.occ_cells / 32u] = half_words[2u * threadIdx.x] | (half_words[2u * threadIdx.x + 1u] << 16);
+            }
+            __syncthreads();
         }
     }
 }
@@ -2062,8 +2114,11 @@ hipError_t launch_train_stage(const TrainParams& P, const TrainBuffers& B, uint3
         break;
     case NERF_EXT_STAGE_OCCUPANCY:
         if (occupancy_update) {
-            k_occ_eval<half_t><<<cus * 4u, kThreads, 0, st>>>(P, B.grid, B.table, B.dparams, B.state, (fold & kFoldBegin) != 0u, B.density);
-            k_occ_bits<<<(P.occ_cells + 255u) / 256u, 256, 0, st>>>(P, B.state, min(P.occ_cells_per_update, P.occ_cells), B.density, B.bits);
+            // Refreshes over whole bit words take one launch.
+            const uint32_t window = min(P.occ_cells_per_update, P.occ_cells);
+            const bool one        = P.occ_cells % 32u == 0u && window % 32u == 0u;
+            k_occ_eval<half_t><<<cus * 4u, kThreads, 0, st>>>(P, B.grid, B.table, B.dparams, B.state, (fold & kFoldBegin) != 0u, B.density, one ? B.bits : nullptr);
+            if (!one) k_occ_bits<<<(P.occ_cells + 255u) / 256u, 256, 0, st>>>(P, B.state, window, B.density, B.bits);
         }
         break;
     case NERF_EXT_STAGE_FORWARD: {

@@ -408,13 +408,15 @@ def test_nonfinite_gradient_skips_update(dataset):
     assert st.skipped == 0 and st.last.has_nonfinite == 0
 
 
-def test_occupancy_window_rotates(dataset):
+# 20,000 cells: whole bit words (one launch evaluates, decays and sets the
+# bits); 20,001: the window's edges split words (a bit pass of its own).
+@pytest.mark.parametrize("count", [20000, 20001])
+def test_occupancy_window_rotates(dataset, count):
     """cells_per_update below the cell count: each refresh decays every cell
     and re-evaluates the window starting at frame x count mod cells, wrapping
     past the last cell (:1575-1627); two refreshes (frames 4 and 8)."""
-    announce("train occupancy refresh, rotating window")
+    announce(f"train occupancy refresh, rotating window of {count}")
     cells = OCC_RES ** 3
-    count = 20000
     occ = ext.occupancy_params(warmup_steps=2, update_interval=4, cells_per_update=count, threshold=0.01, decay=0.95)
     t, grid = _trainer(dataset, occ=occ)
     B = t.buffers()
