@@ -141,9 +141,9 @@ NERF_API NerfStatus nerf_read_train_stats(void* context, NerfTrainStats* out_sta
     Context* ctx = static_cast<Context*>(context);
     std::scoped_lock lock(ctx->mutex);
     if (!ctx->training_configured || !ctx->train) return NERF_STATUS_STATE_ERROR;
-    TrainDevState st{};
-    if (ctx->train->read_state(st) != NERF_STATUS_OK) return NERF_STATUS_CUDA_ERROR;
-    *out_stats           = st.stats;
+    TrainDevState st{}, last{};
+    if (ctx->train->read_state(st, &last) != NERF_STATUS_OK) return NERF_STATUS_CUDA_ERROR;
+    *out_stats           = last.stats;
     ctx->host_generation = out_stats->completed_steps;
     return NERF_STATUS_OK;
 }

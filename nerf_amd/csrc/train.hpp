@@ -10,9 +10,12 @@ enum : uint32_t { kOccNone = 0u, kOccWarmupInit = 1u, kOccRefresh = 2u };
 // Per-step scalars kept in device memory, so that every kernel of a step reads
 // its counts on the device (fixed launch shapes: the step can be captured in
 // a HIP graph).  Mirrors the reference's TrainingDeviceState
-// (backend-cuda.cu:79-85) plus the batch counters and Adam scalars.
+// (backend-cuda.cu:79-85) plus the batch counters and Adam scalars.  Steps
+// alternate between two of these (step k in slot k % 2): a step's begin
+// reads the previous step's slot, so the next step can sample while this
+// one still trains.
 struct TrainDevState {
-    uint32_t frame;       // steps completed so far (reference frame_index)
+    uint32_t frame;       // this step's index (reference frame_index): the previous step's + 1
     uint32_t camera;      // camera of the current step
     uint32_t occ_mode;    // kOcc* of the current step
     uint32_t n_rays;      // rays marched this step
@@ -21,17 +24,18 @@ struct TrainDevState {
     uint32_t nonfinite;   // gradient contains inf/nan
     uint32_t skip;        // Adam update skipped
     unsigned long long total;  // occupied samples before the capacity cut
-    unsigned long long samples_done;  // samples trained on since the last reset
+    unsigned long long samples_done;  // samples trained on since the last reset, this step's included
     double grad_sumsq;    // sum of squared (loss-scaled) gradients
     float loss_sum;       // sum of per-ray Huber losses
-    float rays_f;         // adaptive ray count
+    float rays_f;         // this step's adaptive ray count
+    float rays_next;      // the next step's, from this step's occupied samples
     NerfTrainStats stats; // last completed step
     // Adam's copy of the gradient statistics, taken with them: a pipelined
     // run starts the next step (whose begin clears the fields above) while
     // Adam still runs.
     double adam_sumsq;
     uint32_t adam_nonfinite;
-    uint32_t adam_t;      // optimizer step (frame + 1 of the step that took the gradients)
+    uint32_t adam_t;      // optimizer step (frame + 1)
 };
 
 // Fixed parameters of a configured run (kernel argument).
@@ -75,7 +79,8 @@ struct CoarsePlan {
 
 // Device buffers of a run.
 struct TrainBuffers {
-    TrainDevState* state;
+    TrainDevState* state;        // this step's slot
+    TrainDevState* prev;         // the previous step's slot
     const NerfExtCamera* cams;   // [image_count]
     const uint8_t* images;       // [image_count][H][W][4]
     uint32_t* bits;              // occupancy bitfield
@@ -99,10 +104,10 @@ struct TrainBuffers {
     // binned hash-grid scatter: records (entry within bin, 2 values) grouped
     // by bin of kBinEntries table entries
     uint32_t* bin_hist;          // [n_bins][kBinBlocks] record counts
-    uint32_t* bin_off;           // [n_bins][kBinBlocks] exclusive scan of bin_hist
+    uint32_t* bin_off;           // [n_bins][kBinBlocks] exclusive scan of bin_hist (one per slot)
     uint32_t* bin_max;           // [n_bins][kBinBlocks] bits of the largest |record value|
     uint32_t* bin_scan_tmp;
-    unsigned long long* bin_total;
+    unsigned long long* bin_total;  // one per slot
     uint2* rec;                  // [rec_cap] packed (entry within bin, 2 values)
     uint32_t n_bins;             // bins of the levels past the coarse ones
     uint32_t n_dense;            // leading (coarse) levels accumulated in LDS slabs (dense, <= kCoarseMaxEntries entries)
@@ -163,16 +168,20 @@ inline uint32_t norm_partial_count(const TrainBuffers& B) {
 // A second stream beside a step's own: the hash table's record count and its
 // scan depend only on the step's samples, so the sample stage starts them
 // there and the backward waits for them, instead of running them between
-// the MLP backward and the record fill.  counted is true once a count has
-// been started after the latest sample stage.  A run of several steps also
-// puts each step's begin, occupancy and sample stages there, after the
-// previous step's end (`ready`), so that they overlap its Adam pass.
+// the MLP backward and the record fill.  counted[s] is true once a count has
+// been started for the step in slot s.  A run of several steps also puts
+// each step's begin, occupancy and sample stages there, after the previous
+// step's record fill (`filled`: the last reader of the sample stream), so
+// that they overlap its gradient sums and Adam pass.
 struct StepStreams {
-    hipStream_t aux    = nullptr;
-    hipEvent_t sampled = nullptr;  // the sample stage's end, on the stream it ran on
-    hipEvent_t done    = nullptr;  // the count and scan's end, on aux
-    hipEvent_t ready   = nullptr;  // what the next step's first stages wait for, on the step's stream
-    bool counted       = false;
+    hipStream_t aux       = nullptr;
+    hipEvent_t sampled[2] = {nullptr, nullptr};  // per slot: the sample stage's end, on the stream it ran on
+    hipEvent_t done[2]    = {nullptr, nullptr};  // per slot: the count and scan's end, on aux
+    hipEvent_t ready      = nullptr;             // a point on the step's stream the second stream waits for
+    hipEvent_t filled     = nullptr;             // the record fill's end, on the step's stream (record_filled)
+    bool counted[2]       = {false, false};
+    bool record_filled    = false;
+    uint32_t slot         = 0u;                  // the slot of the step being enqueued
 };
 
 // Folds of a step's one-thread stages into their neighbours, for callers that

@@ -82,24 +82,33 @@ __device__ __forceinline__ void wave_lds_sync() {
 }
 
 // ------------------------------------------------------------ step control
-// What the start of a step decides (:1479-1488): its camera, its occupancy
-// work and its ray count, from the step index and the adaptive ray count.
+// What the start of a step decides (:1479-1488): its index, camera,
+// occupancy work and ray count, from the previous step's index and the ray
+// count its sampler chose.
 struct StepBegin {
-    uint32_t camera, occ_mode, n_rays;
+    uint32_t frame, camera, occ_mode, n_rays;
+    float rays_f;
+    uint32_t skip;  // the latest Adam's, carried until this step's Adam
 };
-__device__ __forceinline__ StepBegin step_begin_values(const TrainParams& P, const TrainDevState* S) {
-    const uint32_t f = S->frame;
+__device__ __forceinline__ StepBegin step_begin_values(const TrainParams& P, const TrainDevState* prev) {
     StepBegin b;
+    const uint32_t f = prev->frame + 1u;
+    b.frame          = f;
     b.camera = hash_u32(f * 747796405u + 2891336453u) % P.image_count;  // :1482
     if (f < P.occ_warmup)
         b.occ_mode = f == 0u ? kOccWarmupInit : kOccNone;                // :1483-1485
     else
         b.occ_mode = (P.occ_interval != 0u && f % P.occ_interval == 0u) ? kOccRefresh : kOccNone;
-    const uint32_t rays = (uint32_t)(S->rays_f + 0.5f);
+    b.rays_f            = prev->rays_next;
+    b.skip              = prev->skip;
+    const uint32_t rays = (uint32_t)(b.rays_f + 0.5f);
     b.n_rays            = rays < P.min_rays ? P.min_rays : (rays > P.max_rays ? P.max_rays : rays);
     return b;
 }
 __device__ __forceinline__ void step_begin_store(TrainDevState* S, const StepBegin& b) {
+    S->frame      = b.frame;
+    S->rays_f     = b.rays_f;
+    S->skip       = b.skip;
     S->camera     = b.camera;
     S->occ_mode   = b.occ_mode;
     S->n_rays     = b.n_rays;
@@ -111,26 +120,39 @@ __device__ __forceinline__ void step_begin_store(TrainDevState* S, const StepBeg
     S->loss_sum   = 0.0f;
 }
 // A step's first kernel may do the begin itself (begin = true): every
-// workgroup derives the values from the step index and the ray count, which
-// only the end of a step changes, and workgroup 0 stores them; later kernels
-// read them from the state.
-__device__ __forceinline__ StepBegin step_begin_in(const TrainParams& P, TrainDevState* S, bool begin) {
-    if (!begin) return StepBegin{S->camera, S->occ_mode, S->n_rays};
-    const StepBegin b = step_begin_values(P, S);
+// workgroup derives the values from the previous step's slot, which nothing
+// changes meanwhile, and workgroup 0 stores them; later kernels read them
+// from the state.
+__device__ __forceinline__ StepBegin step_begin_in(const TrainParams& P, TrainDevState* S, const TrainDevState* prev, bool begin) {
+    if (!begin) return StepBegin{S->frame, S->camera, S->occ_mode, S->n_rays, S->rays_f, S->skip};
+    const StepBegin b = step_begin_values(P, prev);
     if (blockIdx.x == 0u && threadIdx.x == 0u) step_begin_store(S, b);
     return b;
 }
 
-__global__ void k_step_begin(TrainParams P, TrainDevState* S) {
+__global__ void k_step_begin(TrainParams P, TrainDevState* S, const TrainDevState* prev) {
     if (threadIdx.x != 0u || blockIdx.x != 0u) return;
-    step_begin_store(S, step_begin_values(P, S));
+    step_begin_store(S, step_begin_values(P, prev));
 }
 
-// :1495-1512 and the ray-count adaptation.  Reads only what the step's
-// kernels up to the gradient norm wrote, and Adam reads none of what it
-// writes (its step index is its own copy), so the gradient-norm kernel may
-// run it (end = true in k_grad_norm).
-__device__ __forceinline__ void step_end(const TrainParams& P, TrainDevState* S) {
+// The ray-count adaptation, once the step's occupied samples are known (the
+// sampler's totals): aim the next batch at target_samples (exponentially
+// smoothed), from the occupied samples before the capacity cut (the kept
+// count is capped, so it cannot show an overshoot).
+__device__ __forceinline__ void ray_count_next(const TrainParams& P, TrainDevState* S, unsigned long long total) {
+    float r = S->rays_f;
+    if (P.target_samples != 0u && total > 0ull) {
+        const float want = r * (float)P.target_samples / (float)total;
+        r                = 0.5f * r + 0.5f * want;
+        r                = fminf(fmaxf(r, (float)P.min_rays), (float)P.max_rays);
+    }
+    S->rays_next = r;
+}
+
+// :1495-1512.  Reads only what the step's kernels up to the gradient norm
+// wrote and the previous step's sample total, and Adam reads none of what it
+// writes, so the gradient-norm kernel may run it (end = true in k_grad_norm).
+__device__ __forceinline__ void step_end(const TrainParams& P, TrainDevState* S, const TrainDevState* prev) {
     const float inv = S->n_active ? 1.0f / (float)S->n_active : 0.0f;
     const float loss = S->loss_sum * inv;                                          // :1499
     const float gn   = (float)sqrt(S->grad_sumsq > 0.0 ? S->grad_sumsq : 0.0) / P.loss_scale;
@@ -139,21 +161,12 @@ __device__ __forceinline__ void step_end(const TrainParams& P, TrainDevState* S)
     S->stats.has_nonfinite     = (S->nonfinite || !isfinite(loss) || !isfinite(gn)) ? 1u : 0u;
     S->stats.completed_steps   = S->frame + 1u;
     S->stats.last_train_camera = S->camera;
-    S->samples_done            = S->samples_done + S->n_samples;
-    if (P.target_samples != 0u && S->total > 0ull) {
-        // Aim the next batch at target_samples (exponentially smoothed), from
-        // the occupied samples before the capacity cut: the kept count is
-        // capped, so it cannot show an overshoot.
-        const float want = S->rays_f * (float)P.target_samples / (float)S->total;
-        S->rays_f        = 0.5f * S->rays_f + 0.5f * want;
-        S->rays_f        = fminf(fmaxf(S->rays_f, (float)P.min_rays), (float)P.max_rays);
-    }
-    S->frame = S->frame + 1u;
+    S->samples_done            = prev->samples_done + S->n_samples;
 }
 
-__global__ void k_step_end(TrainParams P, TrainDevState* S) {
+__global__ void k_step_end(TrainParams P, TrainDevState* S, const TrainDevState* prev) {
     if (threadIdx.x != 0u || blockIdx.x != 0u) return;
-    step_end(P, S);
+    step_end(P, S, prev);
 }
 
 // ----------------------------------------------------------- occupancy grid
@@ -171,13 +184,15 @@ __device__ __forceinline__ bool occ_in_window(uint32_t cell, uint32_t start, uin
 // bits non-null (whole words: cells and window multiples of 32): the whole
 // occupancy stage in one launch, without k_occ_bits: for a refresh the
 // workgroups first decay the cells of the words outside the window and set
-// those words' bits, then evaluate the window four tiles (64 cells, two
-// words) per workgroup at a time and set the window's words from the new
-// densities; the warm-up start as in k_occ_bits.
+// those words' bits, then evaluate the window a tile of 16 cells (half a
+// word, stored as 16 bits) per wave; the warm-up start as in k_occ_bits.
+// (Words assembled from two waves' tiles through LDS took two workgroup
+// barriers per four tiles: 2^21 cells 225 -> 284 us.)
 template <typename TableT>
-__global__ __launch_bounds__(kThreads) void k_occ_eval(TrainParams P, GridParams g, const TableT* __restrict__ table, const half_t* __restrict__ dparams, TrainDevState* S, bool begin, float* density,
-                                                       uint32_t* __restrict__ bits) {
-    const uint32_t mode = step_begin_in(P, S, begin).occ_mode;  // uniform across the grid
+__global__ __launch_bounds__(kThreads) void k_occ_eval(TrainParams P, GridParams g, const TableT* __restrict__ table, const half_t* __restrict__ dparams, TrainDevState* S, const TrainDevState* prev,
+                                                       bool begin, float* density, uint32_t* __restrict__ bits) {
+    const StepBegin sb  = step_begin_in(P, S, prev, begin);
+    const uint32_t mode = sb.occ_mode;  // uniform across the grid
     if (bits && mode == kOccWarmupInit) {  // as k_occ_bits
         for (uint32_t c = blockIdx.x * blockDim.x + threadIdx.x; c < P.occ_cells; c += gridDim.x * blockDim.x) density[c] = 1.0f;
         for (uint32_t w = blockIdx.x * blockDim.x + threadIdx.x; w < P.occ_cells / 32u; w += gridDim.x * blockDim.x) bits[w] = ~0u;
@@ -185,11 +200,10 @@ __global__ __launch_bounds__(kThreads) void k_occ_eval(TrainParams P, GridParams
     }
     if (mode != kOccRefresh) return;
     __shared__ __align__(16) half_t sp[NERF_EXT_DENSITY_PARAMS];
-    __shared__ uint32_t half_words[kWaves];
     stage_density<kThreads>(sp, dparams);
     const uint32_t lane = threadIdx.x & 63u, grp = lane >> 4, s16 = lane & 15u, wave = threadIdx.x >> 6;
     const uint32_t count = P.occ_cells_per_update < P.occ_cells ? P.occ_cells_per_update : P.occ_cells;
-    const uint32_t start = (uint32_t)((uint64_t)S->frame * count % P.occ_cells);
+    const uint32_t start = (uint32_t)((uint64_t)sb.frame * count % P.occ_cells);
     if (bits) {
         const uint32_t words = P.occ_cells / 32u, w_start = start / 32u, w_count = count / 32u;
         for (uint32_t w = blockIdx.x * blockDim.x + threadIdx.x; w < words - w_count; w += gridDim.x * blockDim.x) {
@@ -218,10 +232,7 @@ __global__ __launch_bounds__(kThreads) void k_occ_eval(TrainParams P, GridParams
     const uint32_t res   = P.occ_res;
     const float step[3]  = {(P.bmax[0] - P.bmin[0]) / (float)res, (P.bmax[1] - P.bmin[1]) / (float)res, (P.bmax[2] - P.bmin[2]) / (float)res};
     const uint32_t tiles = (count + 15u) / 16u;
-    // Chunks of kWaves consecutive tiles per workgroup (a loop uniform across
-    // the workgroup: the word assembly below has barriers).
-    for (uint32_t chunk = blockIdx.x; chunk * kWaves < tiles; chunk += gridDim.x) {
-        const uint32_t tile = chunk * kWaves + wave;
+    for (uint32_t tile = blockIdx.x * kWaves + wave; tile < tiles; tile += gridDim.x * kWaves) {
         const uint32_t k    = tile * 16u + s16;
         const uint32_t kq   = k < count ? k : count - 1u;
         const uint32_t cell = (start + kq) % P.occ_cells;
@@ -241,14 +252,10 @@ __global__ __launch_bounds__(kThreads) void k_occ_eval(TrainParams P, GridParams
             occ               = d > P.occ_threshold;
         }
         if (bits) {
-            const uint32_t b = (uint32_t)__ballot(occ) & 0xFFFFu;  // lanes 0..15: cells 16 tile .. 16 tile + 15
-            if (lane == 0u) half_words[wave] = b;
-            __syncthreads();
-            if (threadIdx.x < kWaves / 2u) {
-                const uint32_t k0 = (chunk * kWaves + 2u * threadIdx.x) * 16u;  // first cell of the word within the window
-                if (k0 < count) bits[(start + k0) % P.occ_cells / 32u] = half_words[2u * threadIdx.x] | (half_words[2u * threadIdx.x + 1u] << 16);
-            }
-            __syncthreads();
+            // The tile's 16 cells are one half of a bit word (the window
+            // starts on a word): lanes 0..15 hold them, stored as 16 bits.
+            const uint32_t b = (uint32_t)__ballot(occ) & 0xFFFFu;
+            if (lane == 0u) reinterpret_cast<uint16_t*>(bits)[(start + tile * 16u) % P.occ_cells / 16u] = (uint16_t)b;
         }
     }
 }
@@ -340,12 +347,12 @@ constexpr uint32_t kTrainGroup = 16u;  // lanes per ray in the emission pass (4 
 // wave::march_range keeps near 22 cycles per step.
 constexpr uint32_t kRayGroup = 64u;
 
-__global__ __launch_bounds__(256) void k_train_rays(TrainParams P, TrainDevState* S, bool begin, const NerfExtCamera* __restrict__ cams, const uint8_t* __restrict__ images, const uint32_t* __restrict__ bits, float4* __restrict__ rays,
+__global__ __launch_bounds__(256) void k_train_rays(TrainParams P, TrainDevState* S, const TrainDevState* prev, bool begin, const NerfExtCamera* __restrict__ cams, const uint8_t* __restrict__ images, const uint32_t* __restrict__ bits, float4* __restrict__ rays,
                                                      float4* __restrict__ gt, uint32_t* __restrict__ counts, float* __restrict__ seg_t, uint32_t* __restrict__ seg_seen, uint32_t* __restrict__ seg_reached, uint32_t segs) {
     constexpr uint32_t kPer = 64u / kRayGroup;  // rays per wave
     const uint32_t lane = threadIdx.x & 63u, stride = gridDim.x * kWaves * kPer;
-    const StepBegin sb = step_begin_in(P, S, begin);
-    const uint32_t n_rays = sb.n_rays, cam_idx = sb.camera, frame = S->frame;
+    const StepBegin sb = step_begin_in(P, S, prev, begin);
+    const uint32_t n_rays = sb.n_rays, cam_idx = sb.camera, frame = sb.frame;
     const NerfExtCamera cam = cams[cam_idx];
     const float cone        = cone_of(cam);
     const uint32_t n_live   = min(n_rays, P.max_rays);
@@ -455,7 +462,10 @@ __global__ __launch_bounds__(256) void k_train_samples(TrainParams P, TrainDevSt
     };
     if (blockIdx.x == 0u && threadIdx.x < 64u) {
         const uint32_t total = wave_count_sum(n_rays);  // occupied samples before the capacity cut
-        if (threadIdx.x == 0u) S->total = total;
+        if (threadIdx.x == 0u) {
+            S->total = total;
+            ray_count_next(P, S, total);
+        }
     }
     const uint64_t units = (uint64_t)n_rays * segs;
     // The loop runs per wave (every lane takes part in the wave's sum); lane
@@ -567,6 +577,7 @@ __global__ __launch_bounds__(kOffsetThreads) void k_ray_offsets(TrainParams P, T
         S->n_samples = e;
         S->n_active  = a;
         S->total     = carry;  // occupied samples before the capacity cut
+        ray_count_next(P, S, carry);
     }
 }
 
@@ -675,6 +686,7 @@ __global__ __launch_bounds__(256) void k_train_samples_prefix(TrainParams P, Tra
             S->n_samples = em;
             S->n_active  = ac;
             S->total     = total;  // occupied samples before the capacity cut
+            ray_count_next(P, S, total);
         }
     }
     if (!fits) return;
@@ -1818,7 +1830,7 @@ __global__ __launch_bounds__(512) void k_grad_reduce(GradReduceArgs a) {
 // kNormThreads-th partial, then the waves are added in order.  Writes the
 // statistics and Adam's copy of them; end: then the end of the step.
 constexpr uint32_t kNormThreads = 1024u;
-__global__ __launch_bounds__(kNormThreads) void k_grad_norm(TrainParams P, const double* __restrict__ norm, uint32_t n, TrainDevState* S, bool end) {
+__global__ __launch_bounds__(kNormThreads) void k_grad_norm(TrainParams P, const double* __restrict__ norm, uint32_t n, TrainDevState* S, const TrainDevState* prev, bool end) {
     __shared__ double ws[kNormThreads / 64u];
     __shared__ uint32_t bad;
     if (threadIdx.x == 0u) bad = 0u;
@@ -1842,7 +1854,7 @@ __global__ __launch_bounds__(kNormThreads) void k_grad_norm(TrainParams P, const
         S->adam_sumsq     = t;
         S->adam_nonfinite = bad;
         S->adam_t         = S->frame + 1u;
-        if (end) step_end(P, S);
+        if (end) step_end(P, S, prev);
     }
 }
 
@@ -1990,9 +2002,11 @@ hipError_t launch_mlp_backward(const TrainParams& P, const TrainBuffers& B, hipS
     // Hashed levels: binned.
     if (B.n_bins) {
         // The count started beside the forward pass by the sample stage, or
-        // here when no count followed the latest sample stage.
-        const hipError_t e = ss && ss->counted ? hipStreamWaitEvent(st, ss->done, 0) : launch_bin_count(P, B, st);
+        // here when no count followed the step's sample stage.
+        const uint32_t sl = ss ? ss->slot : 0u;
+        hipError_t e      = ss && ss->counted[sl] ? hipStreamWaitEvent(st, ss->done[sl], 0) : launch_bin_count(P, B, st);
         if (e != hipSuccess) return e;
+        if (ss) ss->counted[sl] = false;  // consumed
         // Staged for sparse batches (<= 128 steps per ray: records rarely
         // combine and the scattered stores dominate: 4,096 rays of 64 steps
         // 136 -> 98 us); dense batches keep the direct stores, whose records
@@ -2002,6 +2016,8 @@ hipError_t launch_mlp_backward(const TrainParams& P, const TrainBuffers& B, hipS
             k_bin_fill_staged<<<kBinBlocks, kBinThreads, staged_fill_lds(B.n_bins), st>>>(P, B.grid, B.state, B.samples, B.sample_ray, B.rays, B.dfeat, B.n_dense, B.n_bins, B.bin_off, B.rec, B.bin_max);
         else
             k_bin_pass<true><<<kBinBlocks, kBinThreads, 0, st>>>(P, B.grid, B.state, B.samples, B.sample_ray, B.rays, B.dfeat, B.n_dense, B.n_bins, B.bin_off, B.rec, B.bin_max);
+        // The fill is the step's last reader of its sample stream.
+        if (ss && ss->record_filled && (e = hipEventRecord(ss->filled, st)) != hipSuccess) return e;
     }
     // Bin accumulation, the coarse levels' chunk sums and the MLP weight
     // gradients' partial sums, in one launch.
@@ -2024,7 +2040,7 @@ hipError_t launch_mlp_backward(const TrainParams& P, const TrainBuffers& B, hipS
     a.norm            = B.norm_partials;
     const uint32_t coarse_pairs = B.n_dense ? (coarse_reduce_blocks(B.coarse) + 1u) / 2u : 0u;
     k_grad_reduce<<<B.n_bins + coarse_pairs + kMlpParams / 128u, 512, 0, st>>>(a);
-    k_grad_norm<<<1, kNormThreads, 0, st>>>(P, B.norm_partials, norm_partial_count(B), B.state, end);
+    k_grad_norm<<<1, kNormThreads, 0, st>>>(P, B.norm_partials, norm_partial_count(B), B.state, B.prev, end);
     return hipGetLastError();
 }
 
@@ -2045,7 +2061,8 @@ hipError_t launch_adam(const TrainParams& P, const TrainBuffers& B, hipStream_t 
 static hipError_t launch_train_stage_common(const TrainParams& P, const TrainBuffers& B, uint32_t stage, hipStream_t st, uint32_t fold) {
     switch (stage) {
     case NERF_EXT_STAGE_SAMPLE: {
-        k_train_rays<<<ray_wave_blocks(P.max_rays), 256, 0, st>>>(P, B.state, (fold & kFoldBegin) != 0u, B.cams, B.images, B.bits, B.rays, B.gt, B.counts, B.seg_t, B.seg_seen, B.seg_reached, B.segs);
+        k_train_rays<<<ray_wave_blocks(P.max_rays), 256, 0, st>>>(P, B.state, B.prev, (fold & kFoldBegin) != 0u, B.cams, B.images, B.bits, B.rays, B.gt, B.counts, B.seg_t, B.seg_seen, B.seg_reached,
+                                                                  B.segs);
         if (B.segs == 1u && P.max_rays <= kPrefixRays) {
             k_train_samples_prefix<<<(P.max_rays + kWaves - 1u) / kWaves, 256, 0, st>>>(P, B.state, B.cams, B.bits, B.rays, B.counts, B.offsets, B.kept, B.seg_t, B.samples, B.sample_ray);
         } else if (B.segs == 1u) {
@@ -2059,7 +2076,7 @@ static hipError_t launch_train_stage_common(const TrainParams& P, const TrainBuf
     }
     case NERF_EXT_STAGE_ADAM: return launch_adam(P, B, st);
     case NERF_EXT_STAGE_END:
-        if (!(fold & kFoldEnd)) k_step_end<<<1, 64, 0, st>>>(P, B.state);
+        if (!(fold & kFoldEnd)) k_step_end<<<1, 64, 0, st>>>(P, B.state, B.prev);
         break;
     default: return hipErrorInvalidValue;
     }
@@ -2077,7 +2094,7 @@ static hipError_t launch_ref_train_stage(const TrainParams& P, const TrainBuffer
     in.n_dev      = &B.state->n_samples;
     switch (stage) {
     case NERF_EXT_STAGE_BEGIN:
-        k_step_begin<<<1, 64, 0, st>>>(P, B.state);
+        k_step_begin<<<1, 64, 0, st>>>(P, B.state, B.prev);
         return ref_pack_weights(B.dparams, B.cparams, B.ref.frags, st);
     case NERF_EXT_STAGE_OCCUPANCY:
         if (occupancy_update) {
@@ -2097,7 +2114,7 @@ static hipError_t launch_ref_train_stage(const TrainParams& P, const TrainBuffer
     case NERF_EXT_STAGE_BACKWARD: {
         const hipError_t e = launch_ref_backward_train(B.ref, in, B.draw, P.loss_scale, B.mlp_grad, B.norm_partials, st);
         if (e != hipSuccess) return e;
-        k_grad_norm<<<1, kNormThreads, 0, st>>>(P, B.norm_partials, norm_partial_count(B), B.state, (fold & kFoldEnd) != 0u);
+        k_grad_norm<<<1, kNormThreads, 0, st>>>(P, B.norm_partials, norm_partial_count(B), B.state, B.prev, (fold & kFoldEnd) != 0u);
         break;
     }
     default: return launch_train_stage_common(P, B, stage, st, fold & kFoldEnd);
@@ -2110,14 +2127,14 @@ hipError_t launch_train_stage(const TrainParams& P, const TrainBuffers& B, uint3
     const uint32_t cus = device_cu_count();
     switch (stage) {
     case NERF_EXT_STAGE_BEGIN:
-        if (!(fold & kFoldBegin)) k_step_begin<<<1, 64, 0, st>>>(P, B.state);
+        if (!(fold & kFoldBegin)) k_step_begin<<<1, 64, 0, st>>>(P, B.state, B.prev);
         break;
     case NERF_EXT_STAGE_OCCUPANCY:
         if (occupancy_update) {
             // Refreshes over whole bit words take one launch.
             const uint32_t window = min(P.occ_cells_per_update, P.occ_cells);
             const bool one        = P.occ_cells % 32u == 0u && window % 32u == 0u;
-            k_occ_eval<half_t><<<cus * 4u, kThreads, 0, st>>>(P, B.grid, B.table, B.dparams, B.state, (fold & kFoldBegin) != 0u, B.density, one ? B.bits : nullptr);
+            k_occ_eval<half_t><<<cus * 4u, kThreads, 0, st>>>(P, B.grid, B.table, B.dparams, B.state, B.prev, (fold & kFoldBegin) != 0u, B.density, one ? B.bits : nullptr);
             if (!one) k_occ_bits<<<(P.occ_cells + 255u) / 256u, 256, 0, st>>>(P, B.state, window, B.density, B.bits);
         }
         break;
@@ -2146,12 +2163,13 @@ hipError_t launch_train_stage(const TrainParams& P, const TrainBuffers& B, uint3
         // The record count needs only the samples: it runs on the second
         // stream while this one runs the forward pass, the composite and the
         // MLP backward (2^18 samples: 17.5 + 9.5 us off the step's chain).
-        ss->counted = false;
-        if ((e = hipEventRecord(ss->sampled, st)) != hipSuccess) return e;
-        if (st != ss->aux && (e = hipStreamWaitEvent(ss->aux, ss->sampled, 0)) != hipSuccess) return e;
+        const uint32_t sl = ss->slot;
+        ss->counted[sl] = false;
+        if ((e = hipEventRecord(ss->sampled[sl], st)) != hipSuccess) return e;
+        if (st != ss->aux && (e = hipStreamWaitEvent(ss->aux, ss->sampled[sl], 0)) != hipSuccess) return e;
         if ((e = launch_bin_count(P, B, ss->aux)) != hipSuccess) return e;
-        if ((e = hipEventRecord(ss->done, ss->aux)) != hipSuccess) return e;
-        ss->counted = true;
+        if ((e = hipEventRecord(ss->done[sl], ss->aux)) != hipSuccess) return e;
+        ss->counted[sl] = true;
         return hipSuccess;
     }
     case NERF_EXT_STAGE_BACKWARD: return launch_mlp_backward(P, B, st, ss, (fold & kFoldEnd) != 0u);

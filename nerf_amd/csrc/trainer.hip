@@ -15,9 +15,12 @@ namespace nerf_hip {
 Trainer::~Trainer() {
     if (side.aux) (void)hipStreamSynchronize(side.aux);
     if (stream) (void)hipStreamSynchronize(stream);
-    if (side.sampled) (void)hipEventDestroy(side.sampled);
-    if (side.done) (void)hipEventDestroy(side.done);
+    for (int k = 0; k < 2; ++k) {
+        if (side.sampled[k]) (void)hipEventDestroy(side.sampled[k]);
+        if (side.done[k]) (void)hipEventDestroy(side.done[k]);
+    }
     if (side.ready) (void)hipEventDestroy(side.ready);
+    if (side.filled) (void)hipEventDestroy(side.filled);
     if (side.aux) (void)hipStreamDestroy(side.aux);
     for (void* p : owned)
         if (p) (void)hipFree(p);
@@ -51,50 +54,89 @@ uint32_t Trainer::fold_for(uint32_t s, uint32_t first, uint32_t last, bool occ) 
     return fold;
 }
 
+TrainBuffers Trainer::at(uint32_t step) const {
+    TrainBuffers b = B;
+    b.state        = slot_state[step & 1u];
+    b.prev         = slot_state[(step + 1u) & 1u];
+    b.bin_off      = slot_bin_off[step & 1u];
+    b.bin_total    = slot_bin_total[step & 1u];
+    return b;
+}
+
 NerfStatus Trainer::run_stages(uint32_t first, uint32_t last) {
     for (uint32_t s = first; s <= last; ++s) {
         const bool occ = occupancy_due(host_frame);
-        NERF_HIP_TRY(launch_train_stage(P, B, s, occ, stream, &side, fold_for(s, first, last, occ)));
+        side.slot      = host_frame & 1u;
+        NERF_HIP_TRY(launch_train_stage(P, at(host_frame), s, occ, stream, &side, fold_for(s, first, last, occ)));
+        open = s != NERF_EXT_STAGE_END;
         if (s == NERF_EXT_STAGE_END) ++host_frame;
     }
     return NERF_STATUS_OK;
 }
 
 // Several whole steps.  With a second stream each step's begin, occupancy
-// and sample stages (and the record count) run there, after the previous
-// step's end, so that they overlap its Adam pass: Adam is the last stage on
-// the step's stream, after the end of the step (which the backward's
-// gradient-norm kernel does), and reads its own copy of the gradient
-// statistics and step index (TrainDevState::adam_*).  The next
-// step's stages touch nothing Adam reads or writes, except the occupancy
-// refresh, which evaluates the field with the weights Adam writes: a step that
-// refreshes waits for the whole previous step.  The first step waits for all
-// the work already on the step's stream, so the overlap stays inside one call
-// and work a caller enqueues between calls is ordered as before.  Every
-// stage of a step still ends before the step's stream passes its forward
-// pass, so synchronizing that stream covers the whole run.
+// and sample stages and its record count run there; the step's own stream
+// waits for the samples before its forward pass and for the count before
+// its record fill (the count runs beside the forward: beside the gradient
+// sums and Adam it slowed them and ended after them).  Step k + 1's are
+// enqueued there after step k's record fill, the last reader of the sample
+// stream, so they run beside step k's gradient sums and Adam pass: the two
+// steps' counters live in different state slots (TrainBuffers::state and
+// prev) and their record ranges in different bin-offset buffers.  A step that
+// refreshes the occupancy grid evaluates the weights the previous step's Adam
+// writes, so its stages wait for that Adam instead.  The first step waits for
+// all the work already on the step's stream, so the overlap stays inside one
+// call and work a caller enqueues between calls is ordered as before.  Every
+// stage of a step ends before the step's stream passes its forward pass, so
+// synchronizing that stream covers the whole run.
 NerfStatus Trainer::run_steps(uint32_t steps) {
-    if (!side.aux || !side.ready || steps < 2u) {
+    if (!side.aux || !side.ready || !side.filled || steps < 2u) {
         for (uint32_t i = 0; i < steps; ++i) {
             const NerfStatus s = run_stages(NERF_EXT_STAGE_BEGIN, NERF_EXT_STAGE_END);
             if (s != NERF_STATUS_OK) return s;
         }
         return NERF_STATUS_OK;
     }
+    auto sample_aux = [&](uint32_t k) -> hipError_t {
+        const bool occ = occupancy_due(k);
+        side.slot      = k & 1u;
+        for (uint32_t s = NERF_EXT_STAGE_BEGIN; s <= NERF_EXT_STAGE_SAMPLE; ++s) {
+            const hipError_t e = launch_train_stage(P, at(k), s, occ, side.aux, &side, fold_for(s, NERF_EXT_STAGE_BEGIN, NERF_EXT_STAGE_SAMPLE, occ));
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    };
     NERF_HIP_TRY(hipEventRecord(side.ready, stream));
+    NERF_HIP_TRY(hipStreamWaitEvent(side.aux, side.ready, 0));
+    NERF_HIP_TRY(sample_aux(host_frame));
+    open = true;
     for (uint32_t i = 0; i < steps; ++i) {
-        const bool occ = occupancy_due(host_frame);
-        if (occ) NERF_HIP_TRY(hipEventRecord(side.ready, stream));  // after the previous step's Adam
-        NERF_HIP_TRY(hipStreamWaitEvent(side.aux, side.ready, 0));
-        for (uint32_t s = NERF_EXT_STAGE_BEGIN; s <= NERF_EXT_STAGE_SAMPLE; ++s)
-            NERF_HIP_TRY(launch_train_stage(P, B, s, occ, side.aux, &side, fold_for(s, NERF_EXT_STAGE_BEGIN, NERF_EXT_STAGE_SAMPLE, occ)));
-        NERF_HIP_TRY(hipStreamWaitEvent(stream, side.sampled, 0));
+        const uint32_t k    = host_frame;
+        const bool more     = i + 1u < steps;
+        const bool occ_next = more && occupancy_due(k + 1u);
+        const TrainBuffers Bk = at(k);
+        side.slot = k & 1u;
+        // The step's samples; its record count, which runs beside the forward
+        // pass, is waited for by the backward before the fill.
+        NERF_HIP_TRY(hipStreamWaitEvent(stream, side.sampled[k & 1u], 0));
+        side.record_filled = more && !occ_next;
         for (uint32_t s = NERF_EXT_STAGE_FORWARD; s <= NERF_EXT_STAGE_BACKWARD; ++s)
-            NERF_HIP_TRY(launch_train_stage(P, B, s, occ, stream, &side, fold_for(s, NERF_EXT_STAGE_BEGIN, NERF_EXT_STAGE_END, occ)));  // the backward ends the step
+            NERF_HIP_TRY(launch_train_stage(P, Bk, s, false, stream, &side, fold_for(s, NERF_EXT_STAGE_BEGIN, NERF_EXT_STAGE_END, false)));  // the backward ends the step
+        side.record_filled = false;
         ++host_frame;
-        NERF_HIP_TRY(hipEventRecord(side.ready, stream));
-        NERF_HIP_TRY(launch_train_stage(P, B, NERF_EXT_STAGE_ADAM, occ, stream, &side));
+        if (more && !occ_next) {
+            NERF_HIP_TRY(hipStreamWaitEvent(side.aux, side.filled, 0));
+            NERF_HIP_TRY(sample_aux(k + 1u));
+        }
+        side.slot = k & 1u;
+        NERF_HIP_TRY(launch_train_stage(P, Bk, NERF_EXT_STAGE_ADAM, false, stream, &side));
+        if (occ_next) {
+            NERF_HIP_TRY(hipEventRecord(side.ready, stream));  // after this step's Adam
+            NERF_HIP_TRY(hipStreamWaitEvent(side.aux, side.ready, 0));
+            NERF_HIP_TRY(sample_aux(k + 1u));
+        }
     }
+    open = false;
     return NERF_STATUS_OK;
 }
 
@@ -170,7 +212,10 @@ NerfStatus trainer_create(const NerfExtTrainDesc* d, const BorrowedModel* borrow
     B.mlp_params       = ref ? kRefParams : kMlpParams;
     B.density_params   = ref ? (uint32_t)NERF_EXT_REF_DENSITY_PARAMS : (uint32_t)NERF_EXT_DENSITY_PARAMS;
     Trainer& T      = *t;
-    NERF_HIP_TRY(alloc(T, B.state, 1));
+    NERF_HIP_TRY(alloc(T, T.slot_state[0], 2));
+    T.slot_state[1] = T.slot_state[0] + 1;
+    B.state         = T.slot_state[0];
+    B.prev          = T.slot_state[1];
     NerfExtCamera* cams = nullptr;
     NERF_HIP_TRY(alloc(T, cams, d->image_count));
     B.cams = cams;
@@ -243,17 +288,24 @@ NerfStatus trainer_create(const NerfExtTrainDesc* d, const BorrowedModel* borrow
     B.n_bins  = (uint32_t)(((uint64_t)(g.n_levels - B.n_dense) * g.table_size + kBinEntries - 1u) / kBinEntries);
     B.rec_cap = (uint64_t)P.sample_cap * (g.n_levels - B.n_dense) * 8u;
     NERF_HIP_TRY(alloc(T, B.bin_hist, (uint64_t)B.n_bins * kBinBlocks));
-    NERF_HIP_TRY(alloc(T, B.bin_off, (uint64_t)B.n_bins * kBinBlocks));
+    NERF_HIP_TRY(alloc(T, T.slot_bin_off[0], 2ull * B.n_bins * kBinBlocks));
+    T.slot_bin_off[1] = T.slot_bin_off[0] + (uint64_t)B.n_bins * kBinBlocks;
+    B.bin_off         = T.slot_bin_off[0];
     NERF_HIP_TRY(alloc(T, B.bin_max, (uint64_t)B.n_bins * kBinBlocks));
     NERF_HIP_TRY(alloc(T, B.bin_scan_tmp, scan_tmp_words(B.n_bins * kBinBlocks + 1u)));
-    NERF_HIP_TRY(alloc(T, B.bin_total, 1));
+    NERF_HIP_TRY(alloc(T, T.slot_bin_total[0], 2));
+    T.slot_bin_total[1] = T.slot_bin_total[0] + 1;
+    B.bin_total         = T.slot_bin_total[0];
     NERF_HIP_TRY(alloc(T, B.rec, B.rec_cap));
     NERF_HIP_TRY(alloc(T, B.dw_partials, (uint64_t)kDxMaxBlocks * kMlpParams));
     if (B.n_bins) {
         NERF_HIP_TRY(hipStreamCreateWithFlags(&T.side.aux, hipStreamNonBlocking));
-        NERF_HIP_TRY(hipEventCreateWithFlags(&T.side.sampled, hipEventDisableTiming));
-        NERF_HIP_TRY(hipEventCreateWithFlags(&T.side.done, hipEventDisableTiming));
+        for (int k = 0; k < 2; ++k) {
+            NERF_HIP_TRY(hipEventCreateWithFlags(&T.side.sampled[k], hipEventDisableTiming));
+            NERF_HIP_TRY(hipEventCreateWithFlags(&T.side.done[k], hipEventDisableTiming));
+        }
         NERF_HIP_TRY(hipEventCreateWithFlags(&T.side.ready, hipEventDisableTiming));
+        NERF_HIP_TRY(hipEventCreateWithFlags(&T.side.filled, hipEventDisableTiming));
     }
     }
     NERF_HIP_TRY(alloc(T, B.table_grad, B.table_elems));
@@ -327,17 +379,28 @@ NerfStatus Trainer::reset() {
     NERF_HIP_TRY(hipMemsetAsync(B.mlp_v, 0, B.mlp_params * 4ull, s));
     NERF_HIP_TRY(hipMemsetAsync(B.bits, 0, (P.occ_cells + 31u) / 32u * 4u, s));
     NERF_HIP_TRY(hipMemsetAsync(B.density, 0, (uint64_t)P.occ_cells * 4u, s));
-    TrainDevState init{};
-    init.rays_f = initial_rays;
-    NERF_HIP_TRY(hipMemcpyAsync(B.state, &init, sizeof(init), hipMemcpyHostToDevice, s));
+    // Slot 1 stands for the step before step 0: index -1, the initial ray
+    // count as its choice for the next step, no samples yet.
+    TrainDevState init[2]{};
+    init[1].frame     = 0xFFFFFFFFu;
+    init[1].rays_f    = initial_rays;
+    init[1].rays_next = initial_rays;
+    NERF_HIP_TRY(hipMemcpyAsync(slot_state[0], init, sizeof(init), hipMemcpyHostToDevice, s));
     NERF_HIP_TRY(hipStreamSynchronize(s));
     host_frame = 0u;
+    open       = false;
+    for (int k = 0; k < 2; ++k) side.counted[k] = false;
     return NERF_STATUS_OK;
 }
 
-NerfStatus Trainer::read_state(TrainDevState& host) {
+// The state of the step in progress (some of its stages enqueued), else of
+// the last completed step.
+TrainDevState* Trainer::current_state() const { return slot_state[(open ? host_frame : host_frame - 1u) & 1u]; }
+
+NerfStatus Trainer::read_state(TrainDevState& host, TrainDevState* last) {
     NERF_HIP_TRY(hipStreamSynchronize(stream));
-    NERF_HIP_TRY(hipMemcpy(&host, B.state, sizeof(host), hipMemcpyDeviceToHost));
+    NERF_HIP_TRY(hipMemcpy(&host, current_state(), sizeof(host), hipMemcpyDeviceToHost));
+    if (last) NERF_HIP_TRY(hipMemcpy(last, slot_state[(host_frame - 1u) & 1u], sizeof(*last), hipMemcpyDeviceToHost));
     return NERF_STATUS_OK;
 }
 
@@ -388,16 +451,18 @@ NERF_API NerfStatus nerf_ext_trainer_synchronize(NerfExtTrainer* trainer) {
 
 NERF_API NerfStatus nerf_ext_trainer_stats(NerfExtTrainer* trainer, NerfExtTrainStats* out) {
     NERF_CHECK_ARG(trainer && trainer->t && out, "nerf_ext_trainer_stats: null argument");
-    TrainDevState s{};
-    const NerfStatus st = trainer->t->read_state(s);
+    // The step in progress (or the last one) for its counters; the last
+    // completed step for its statistics and the running sample total.
+    TrainDevState s{}, done{};
+    const NerfStatus st = trainer->t->read_state(s, &done);
     if (st != NERF_STATUS_OK) return st;
-    out->last             = s.stats;
+    out->last             = done.stats;
     out->rays             = s.n_rays;
     out->samples          = s.n_samples;
     out->active_rays      = s.n_active;
     out->skipped          = s.skip;
     out->occupied_samples = s.total;
-    out->samples_total    = s.samples_done;
+    out->samples_total    = done.samples_done;
     return NERF_STATUS_OK;
 }
 
@@ -405,7 +470,7 @@ NERF_API NerfStatus nerf_ext_trainer_buffers(NerfExtTrainer* trainer, NerfExtTra
     NERF_CHECK_ARG(trainer && trainer->t && o, "nerf_ext_trainer_buffers: null argument");
     const TrainBuffers& B = trainer->t->B;
     memset(o, 0, sizeof(*o));
-    o->state           = B.state;
+    o->state           = trainer->t->current_state();
     o->rays            = (float*)B.rays;
     o->gt              = (float*)B.gt;
     o->counts          = B.counts;

@@ -23,7 +23,11 @@ struct BorrowedModel {
 
 struct Trainer {
     TrainParams P{};
-    TrainBuffers B{};
+    TrainBuffers B{};  // the buffers; at(k) gives step k's view (its state slot, the previous one, its bin ranges)
+    TrainDevState* slot_state[2]            = {nullptr, nullptr};
+    uint32_t* slot_bin_off[2]               = {nullptr, nullptr};
+    unsigned long long* slot_bin_total[2]   = {nullptr, nullptr};
+    bool open = false;  // stages of step host_frame have been enqueued, its end not yet
     NerfExtGridDesc grid_desc{};
     hipStream_t stream = nullptr;
     bool own_stream    = false;
@@ -34,10 +38,14 @@ struct Trainer {
 
     ~Trainer();
     bool occupancy_due(uint32_t frame) const;
+    TrainBuffers at(uint32_t step) const;
     uint32_t fold_for(uint32_t stage, uint32_t first, uint32_t last, bool occupancy_update) const;
     NerfStatus run_stages(uint32_t first, uint32_t last);
     NerfStatus run_steps(uint32_t steps);  // whole steps, consecutive ones overlapped
-    NerfStatus read_state(TrainDevState& host);
+    TrainDevState* current_state() const;
+    // The state of the step in progress, else of the last completed step;
+    // last: also the last completed step's.
+    NerfStatus read_state(TrainDevState& host, TrainDevState* last = nullptr);
     // Zeroes gradients, Adam moments, the occupancy grid and the step state
     // (frame 0, initial ray count); the weights are left as they are.
     NerfStatus reset();
