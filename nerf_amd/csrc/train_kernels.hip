@@ -8,12 +8,12 @@
 // field forward             :1328-1339                     launch_field (field.hip)
 // composite fwd/bwd + loss  :1095-1182 (MSE)               k_composite_train (Huber)
 // MLP backward              :784-909, 1267-1301 (cuBLAS)   k_bwd_dx (dfeat, dW partials)
-// hash-table backward       (hash-grid model)              k_coarse_scatter (coarse levels); k_bin_pass
-//                                                          (count, on a second stream; fill) or
-//                                                          k_bin_fill_staged, scan
+// hash-table backward       (hash-grid model)              k_bin_pass<false> (record count, on a second
+//                                                          stream) and its scan; k_scatter_fill (coarse-level
+//                                                          slabs and the record fill, direct or staged)
 // gradient sums             :1286-1301                     k_grad_reduce (bins, coarse chunks, dW partials)
-// grad stats, Adam          :1447-1554                     in the gradient writers, the last workgroup of
-//                                                          k_grad_reduce (k_grad_norm: reference model); k_adam
+// grad stats, Adam          :1447-1554                     in the gradient writers, summed by k_grad_norm
+//                                                          (which may also end the step); k_adam
 // end step                  :1495-1512                     k_step_end
 //
 // MI355X choices: every count lives in device memory and every launch has a
@@ -1020,13 +1020,13 @@ __device__ __forceinline__ void combine_step(float v[16], uint32_t seg) {
 // makes the slab's partials NaN, which the statistics report as non-finite.
 constexpr uint32_t kCoarseThreads = 1024u;
 constexpr uint32_t kCoarseBatch   = 4u;
-__global__ __launch_bounds__(kCoarseThreads) void k_coarse_scatter(TrainParams P, GridParams g, CoarsePlan C, const TrainDevState* S, const float2* __restrict__ samples, const uint32_t* __restrict__ sample_ray,
-                                                                   const float4* __restrict__ rays, const float2* __restrict__ dfeat, float2* __restrict__ partials) {
-    extern __shared__ __align__(16) uint32_t slab[];  // [count][2], two's complement
-    __shared__ float wsum[kCoarseThreads / 64u];
+// Workgroup blk of the coarse scatter; slab: [count][2] LDS words (two's
+// complement), wsum: kCoarseThreads / 64 floats.
+__device__ __forceinline__ void coarse_scatter_wg(const TrainParams& P, const GridParams& g, const CoarsePlan& C, const TrainDevState* S, const float2* __restrict__ samples, const uint32_t* __restrict__ sample_ray,
+                                                  const float4* __restrict__ rays, const float2* __restrict__ dfeat, float2* __restrict__ partials, uint32_t blk, uint32_t* slab, float* wsum) {
     // Workgroup b runs on XCD b % 8: the slabs of one chunk share an XCD, and
     // with it the L2 lines of the chunk's samples.
-    const uint32_t xcd = blockIdx.x & 7u, r = blockIdx.x >> 3;
+    const uint32_t xcd = blk & 7u, r = blk >> 3;
     const uint32_t k = r % C.n_slabs, chunk = (r / C.n_slabs) * 8u + xcd;
     const uint32_t level = C.level[k], e0 = C.begin[k], ne = C.count[k];
     for (uint32_t i = threadIdx.x; i < 2u * ne; i += blockDim.x) slab[i] = 0u;
@@ -1130,6 +1130,13 @@ __global__ __launch_bounds__(kCoarseThreads) void k_coarse_scatter(TrainParams P
         for (uint32_t m = 0; m < 4u; ++m) f[m] = ldexpf((float)(int32_t)slab[4u * i + m], -e);
         out[i] = make_float4(f[0], f[1], f[2], f[3]);
     }
+}
+
+__global__ __launch_bounds__(kCoarseThreads) void k_coarse_scatter(TrainParams P, GridParams g, CoarsePlan C, const TrainDevState* S, const float2* __restrict__ samples, const uint32_t* __restrict__ sample_ray,
+                                                                   const float4* __restrict__ rays, const float2* __restrict__ dfeat, float2* __restrict__ partials) {
+    extern __shared__ __align__(16) uint32_t slab[];
+    __shared__ float wsum[kCoarseThreads / 64u];
+    coarse_scatter_wg(P, g, C, S, samples, sample_ray, rays, dfeat, partials, blockIdx.x, slab, wsum);
 }
 
 // Input-gradient pass: d(features) of each tile, loss-scaled, to dfeat
@@ -1339,14 +1346,14 @@ __device__ __forceinline__ float2 record_value(uint2 r) { return make_float2(__u
 // bins with two workgroups per CU (236 vs 229 us for the backward), 16-byte
 // stores of each x-neighbour record pair (bins padded to even counts).
 constexpr uint32_t kBinThreads = 1024u;
+// Workgroup blk of nblk; cursor: n_bins LDS words, vmax (kFill): n_bins
+// LDS words, the bits of the largest |record value| per bin.
 template <bool kFill>
-__global__ __launch_bounds__(kBinThreads) void k_bin_pass(TrainParams P, GridParams g, const TrainDevState* S, const float2* __restrict__ samples, const uint32_t* __restrict__ sample_ray, const float4* __restrict__ rays,
-                                                  const float2* __restrict__ dfeat, uint32_t n_dense, uint32_t n_bins, uint32_t* __restrict__ hist, uint2* __restrict__ rec,
-                                                  uint32_t* __restrict__ bin_max) {
-    __shared__ uint32_t cursor[kMaxBins];
-    __shared__ uint32_t vmax[kFill ? kMaxBins : 1u];  // bits of the largest |record value| per bin
+__device__ __forceinline__ void bin_pass_wg(const TrainParams& P, const GridParams& g, const TrainDevState* S, const float2* __restrict__ samples, const uint32_t* __restrict__ sample_ray,
+                                            const float4* __restrict__ rays, const float2* __restrict__ dfeat, uint32_t n_dense, uint32_t n_bins, uint32_t* __restrict__ hist, uint2* __restrict__ rec,
+                                            uint32_t* __restrict__ bin_max, uint32_t blk, uint32_t nblk, uint32_t* cursor, uint32_t* vmax) {
     for (uint32_t i = threadIdx.x; i < n_bins; i += blockDim.x) {
-        cursor[i] = kFill ? hist[(uint64_t)i * gridDim.x + blockIdx.x] : 0u;
+        cursor[i] = kFill ? hist[(uint64_t)i * nblk + blk] : 0u;
         if constexpr (kFill) vmax[i] = 0u;
     }
     __syncthreads();
@@ -1356,7 +1363,7 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_pass(TrainParams P, GridPar
     // Waves take 64 consecutive samples; all lanes stay active (rows of 16
     // combine runs of samples in the same cell, as in k_coarse_scatter, and only
     // a run's first lane emits its 8 records).
-    for (uint32_t base = blockIdx.x * blockDim.x + (threadIdx.x & ~63u); base < n; base += gridDim.x * blockDim.x) {
+    for (uint32_t base = blk * blockDim.x + (threadIdx.x & ~63u); base < n; base += nblk * blockDim.x) {
         const uint32_t s = base + lane;
         const bool live  = s < n;
         const uint32_t q = live ? s : n - 1u;
@@ -1429,9 +1436,18 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_pass(TrainParams P, GridPar
     }
     __syncthreads();
     for (uint32_t i = threadIdx.x; i < n_bins; i += blockDim.x) {
-        if constexpr (kFill) bin_max[(uint64_t)i * gridDim.x + blockIdx.x] = vmax[i];
-        else hist[(uint64_t)i * gridDim.x + blockIdx.x] = cursor[i];
+        if constexpr (kFill) bin_max[(uint64_t)i * nblk + blk] = vmax[i];
+        else hist[(uint64_t)i * nblk + blk] = cursor[i];
     }
+}
+
+template <bool kFill>
+__global__ __launch_bounds__(kBinThreads) void k_bin_pass(TrainParams P, GridParams g, const TrainDevState* S, const float2* __restrict__ samples, const uint32_t* __restrict__ sample_ray, const float4* __restrict__ rays,
+                                                  const float2* __restrict__ dfeat, uint32_t n_dense, uint32_t n_bins, uint32_t* __restrict__ hist, uint2* __restrict__ rec,
+                                                  uint32_t* __restrict__ bin_max) {
+    __shared__ uint32_t cursor[kMaxBins];
+    __shared__ uint32_t vmax[kFill ? kMaxBins : 1u];
+    bin_pass_wg<kFill>(P, g, S, samples, sample_ray, rays, dfeat, n_dense, n_bins, hist, rec, bin_max, blockIdx.x, gridDim.x, cursor, vmax);
 }
 
 // Fill pass with the records staged in LDS, for grids whose per-bin state
@@ -1455,10 +1471,11 @@ __host__ __device__ constexpr uint32_t staged_fill_lds(uint32_t n_bins) { return
 // not for its global loads and stores (which __syncthreads also drains).
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-__global__ __launch_bounds__(kBinThreads) void k_bin_fill_staged(TrainParams P, GridParams g, const TrainDevState* S, const float2* __restrict__ samples, const uint32_t* __restrict__ sample_ray,
-                                                                 const float4* __restrict__ rays, const float2* __restrict__ dfeat, uint32_t n_dense, uint32_t n_bins, const uint32_t* __restrict__ hist,
-                                                                 uint2* __restrict__ rec, uint32_t* __restrict__ bin_max) {
-    extern __shared__ __align__(16) uint32_t lds_words[];
+// Workgroup blk of nblk; lds_words: staged_fill_lds(n_bins) bytes; wave_tot:
+// kBinThreads / 64 LDS words.
+__device__ __forceinline__ void bin_fill_staged_wg(const TrainParams& P, const GridParams& g, const TrainDevState* S, const float2* __restrict__ samples, const uint32_t* __restrict__ sample_ray,
+                                                   const float4* __restrict__ rays, const float2* __restrict__ dfeat, uint32_t n_dense, uint32_t n_bins, const uint32_t* __restrict__ hist,
+                                                   uint2* __restrict__ rec, uint32_t* __restrict__ bin_max, uint32_t blk, uint32_t nblk, uint32_t* lds_words, uint32_t* wave_tot) {
     uint2* st_rec      = reinterpret_cast<uint2*>(lds_words);  // [kStageRecords]
     uint32_t* st_slot  = lds_words + 2u * kStageRecords;       // [kStageRecords] global slot of each staged record
     const uint32_t nb2 = (n_bins + 1u) & ~1u;
@@ -1466,9 +1483,8 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_fill_staged(TrainParams P, 
     uint32_t* vmax     = cursor + nb2;             // [n_bins] bits of the largest |record value|
     uint32_t* start    = vmax + nb2;               // [n_bins] the round's first slot
     uint32_t* pos      = start + nb2;              // [n_bins] LDS position of slot x of bin b: x + pos[b]
-    __shared__ uint32_t wave_tot[kBinThreads / 64u];
     for (uint32_t i = threadIdx.x; i < n_bins; i += blockDim.x) {
-        const uint32_t h = hist[(uint64_t)i * gridDim.x + blockIdx.x];
+        const uint32_t h = hist[(uint64_t)i * nblk + blk];
         cursor[i]        = h;
         start[i]         = h;
         vmax[i]          = 0u;
@@ -1480,7 +1496,7 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_fill_staged(TrainParams P, 
     const uint32_t per  = (n_bins + blockDim.x - 1u) / blockDim.x;  // bins per thread in the scan
     // Chunks of blockDim.x consecutive samples, the same samples per wave as
     // k_bin_pass (wave w of the workgroup holds samples chunk + 64 w ..).
-    for (uint32_t chunk = blockIdx.x * blockDim.x; chunk < n; chunk += gridDim.x * blockDim.x) {
+    for (uint32_t chunk = blk * blockDim.x; chunk < n; chunk += nblk * blockDim.x) {
         const uint32_t s = chunk + threadIdx.x;
         const bool live  = s < n;
         const uint32_t q = live ? s : n - 1u;
@@ -1588,7 +1604,29 @@ __global__ __launch_bounds__(kBinThreads) void k_bin_fill_staged(TrainParams P, 
         }
     }
     __syncthreads();
-    for (uint32_t i = threadIdx.x; i < n_bins; i += blockDim.x) bin_max[(uint64_t)i * gridDim.x + blockIdx.x] = vmax[i];
+    for (uint32_t i = threadIdx.x; i < n_bins; i += blockDim.x) bin_max[(uint64_t)i * nblk + blk] = vmax[i];
+}
+
+// The coarse levels' scatter and the record fill in one launch: the first
+// n_coarse workgroups take the coarse slabs (their dynamic LDS is the slab),
+// the other kBinBlocks the fill (the same LDS as its cursors and maxima, or
+// its stage).  One launch instead of two: the fill's workgroups start on each
+// CU as the coarse ones finish there.
+template <bool kStaged>
+__global__ __launch_bounds__(kBinThreads) void k_scatter_fill(TrainParams P, GridParams g, CoarsePlan C, const TrainDevState* S, const float2* __restrict__ samples, const uint32_t* __restrict__ sample_ray,
+                                                              const float4* __restrict__ rays, const float2* __restrict__ dfeat, float2* __restrict__ partials, uint32_t n_coarse, uint32_t n_dense,
+                                                              uint32_t n_bins, uint32_t* __restrict__ hist, uint2* __restrict__ rec, uint32_t* __restrict__ bin_max) {
+    static_assert(kCoarseThreads == kBinThreads, "one workgroup size for both parts");
+    extern __shared__ __align__(16) uint32_t lds_words[];
+    __shared__ float wsum[kBinThreads / 64u];
+    __shared__ uint32_t wave_tot[kBinThreads / 64u];
+    if (blockIdx.x < n_coarse) {
+        coarse_scatter_wg(P, g, C, S, samples, sample_ray, rays, dfeat, partials, blockIdx.x, lds_words, wsum);
+        return;
+    }
+    const uint32_t blk = blockIdx.x - n_coarse;
+    if constexpr (kStaged) bin_fill_staged_wg(P, g, S, samples, sample_ray, rays, dfeat, n_dense, n_bins, hist, rec, bin_max, blk, kBinBlocks, lds_words, wave_tot);
+    else bin_pass_wg<true>(P, g, S, samples, sample_ray, rays, dfeat, n_dense, n_bins, hist, rec, bin_max, blk, kBinBlocks, lds_words, lds_words + n_bins);
 }
 
 // One bin per workgroup.  fp32 LDS atomics run at a twelfth of the rate of
@@ -1986,20 +2024,23 @@ hipError_t launch_mlp_backward(const TrainParams& P, const TrainBuffers& B, hipS
     if (!lds_set) {
         hipError_t e = hipFuncSetAttribute((const void*)k_bwd_dx, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDxLds);
         if (e == hipSuccess) e = hipFuncSetAttribute((const void*)k_coarse_scatter, hipFuncAttributeMaxDynamicSharedMemorySize, (int)(kCoarseSlabEntries * 2u * sizeof(uint32_t)));
-        if (e == hipSuccess) e = hipFuncSetAttribute((const void*)k_bin_fill_staged, hipFuncAttributeMaxDynamicSharedMemorySize, (int)staged_fill_lds(kStagedMaxBins));
+        const uint32_t slab_lds = kCoarseSlabEntries * 2u * sizeof(uint32_t);
+        if (e == hipSuccess) e = hipFuncSetAttribute((const void*)k_scatter_fill<true>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)max(slab_lds, staged_fill_lds(kStagedMaxBins)));
+        if (e == hipSuccess) e = hipFuncSetAttribute((const void*)k_scatter_fill<false>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)max(slab_lds, 2u * kMaxBins * (uint32_t)sizeof(uint32_t)));
         if (e != hipSuccess) return e;
         lds_set = true;
     }
     const uint32_t dx_blocks = min(cus * 2u, kDxMaxBlocks);  // two per CU (LDS)
     k_bwd_dx<<<dx_blocks, kThreads, kDxLds, st>>>(P, B.state, B.dparams, B.cparams, B.features, sparse_features(P, B) ? B.features_lm : nullptr, B.draw, B.samples, B.sample_ray, B.rays, B.dfeat, B.dw_partials);
-    // Coarse levels: LDS slabs per chunk of samples, then the chunks added.
-    if (B.n_dense) {
-        const CoarsePlan& C = B.coarse;
-        uint32_t lds_entries = 0u;
-        for (uint32_t k = 0; k < C.n_slabs; ++k) lds_entries = max(lds_entries, C.count[k]);
-        k_coarse_scatter<<<kCoarseChunks * C.n_slabs, kCoarseThreads, lds_entries * 2u * sizeof(uint32_t), st>>>(P, B.grid, C, B.state, B.samples, B.sample_ray, B.rays, B.dfeat, B.coarse_partials);
-    }
-    // Hashed levels: binned.
+    // Coarse levels: LDS slabs per chunk of samples, summed over the chunks
+    // by the gradient reduction; hashed levels: binned.  One launch when both
+    // are present.
+    const CoarsePlan& C = B.coarse;
+    uint32_t lds_entries = 0u;
+    for (uint32_t k = 0; k < C.n_slabs; ++k) lds_entries = max(lds_entries, C.count[k]);
+    const uint32_t n_coarse = B.n_dense ? kCoarseChunks * C.n_slabs : 0u, slab_lds = lds_entries * 2u * (uint32_t)sizeof(uint32_t);
+    if (!B.n_bins && n_coarse)
+        k_coarse_scatter<<<n_coarse, kCoarseThreads, slab_lds, st>>>(P, B.grid, C, B.state, B.samples, B.sample_ray, B.rays, B.dfeat, B.coarse_partials);
     if (B.n_bins) {
         // The count started beside the forward pass by the sample stage, or
         // here when no count followed the step's sample stage.
@@ -2013,9 +2054,11 @@ hipError_t launch_mlp_backward(const TrainParams& P, const TrainBuffers& B, hipS
         // are fewer and whose pass is shorter than the staging rounds (2^18
         // samples of 1,024 steps: 74 us direct, 90 us staged).
         if (P.max_steps <= 128u && B.n_bins <= kStagedMaxBins)
-            k_bin_fill_staged<<<kBinBlocks, kBinThreads, staged_fill_lds(B.n_bins), st>>>(P, B.grid, B.state, B.samples, B.sample_ray, B.rays, B.dfeat, B.n_dense, B.n_bins, B.bin_off, B.rec, B.bin_max);
+            k_scatter_fill<true><<<n_coarse + kBinBlocks, kBinThreads, max(slab_lds, staged_fill_lds(B.n_bins)), st>>>(P, B.grid, C, B.state, B.samples, B.sample_ray, B.rays, B.dfeat, B.coarse_partials, n_coarse, B.n_dense,
+                                                                                                                        B.n_bins, B.bin_off, B.rec, B.bin_max);
         else
-            k_bin_pass<true><<<kBinBlocks, kBinThreads, 0, st>>>(P, B.grid, B.state, B.samples, B.sample_ray, B.rays, B.dfeat, B.n_dense, B.n_bins, B.bin_off, B.rec, B.bin_max);
+            k_scatter_fill<false><<<n_coarse + kBinBlocks, kBinThreads, max(slab_lds, 2u * B.n_bins * (uint32_t)sizeof(uint32_t)), st>>>(P, B.grid, C, B.state, B.samples, B.sample_ray, B.rays, B.dfeat, B.coarse_partials,
+                                                                                                                                     n_coarse, B.n_dense, B.n_bins, B.bin_off, B.rec, B.bin_max);
         // The fill is the step's last reader of its sample stream.
         if (ss && ss->record_filled && (e = hipEventRecord(ss->filled, st)) != hipSuccess) return e;
     }
