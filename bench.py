@@ -307,6 +307,20 @@ def ref_train_bench(steps: int, warmup: int, views: int = 100):
     return out
 
 
+def leg_in_child(leg: str, extra: list) -> dict:
+    """One leg run by `bench.py --only LEG` in a child process of its own (a
+    fresh HIP context), as the reference's benchmark program runs on its own;
+    its JSON result, with the process noted."""
+    import subprocess
+    proc = subprocess.run([sys.executable, os.path.abspath(__file__), "--only", leg, *extra], capture_output=True, text=True, timeout=900)
+    lines = [x for x in proc.stdout.splitlines() if x.startswith('{"leg"')]
+    if proc.returncode != 0 or not lines:
+        raise RuntimeError(f"bench.py --only {leg} failed ({proc.returncode}): {proc.stderr[-2000:]}")
+    result = json.loads(lines[-1])["result"]
+    result["process"] = "a child process of its own (bench.py --only " + " ".join([leg, *extra]) + "), as benchmark.cpp runs"
+    return result
+
+
 def reference_host_bench(steps: int = 200, views: int = 100):
     """The reference host program's workload (benchmark.cpp:305-546) through
     nerf.h with the reference's own network: 4,096 rays per step, <= 64
@@ -693,6 +707,7 @@ def main() -> int:
     ap.add_argument("--only", choices=["render", "stages", "train", "reftrain", "refhost", "configs", "refrender"], default=None,
                     help="run one leg only and print its result (for profiling a leg under rocprofv3): the headline render (3 renders), the stage rooflines, "
                          "training (30 + 30 steps), reference-model training, the reference host's workload, the C4/C5 renders, the reference-model render")
+    ap.add_argument("--refhost-steps", type=int, default=60, help="timed steps of the reference-host leg with --only refhost (the full run times 200 in a child process)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain fp32->fp16 conversion over MIB MiB of input (reads 4 B, writes 2 B per element) to calibrate HBM counters, then exit")
     args = ap.parse_args()
@@ -729,7 +744,7 @@ def main() -> int:
         elif args.only == "reftrain":
             result = ref_train_bench(20, 10)
         elif args.only == "refhost":
-            result = reference_host_bench(steps=60)
+            result = reference_host_bench(steps=args.refhost_steps)
         elif args.only == "configs":
             result = config_renders(reps=1)
         else:
@@ -827,7 +842,7 @@ def main() -> int:
         if not args.no_reference_legs:
             line["train_reference_model"] = ref_train_bench(max(10, args.train_steps // 2), 10)
             progress("reference-model training")
-            line["reference_host"] = reference_host_bench()
+            line["reference_host"] = leg_in_child("refhost", ["--refhost-steps", "200"])
             progress("reference host")
     if not args.no_configs:
         line["configs"] = config_renders()
