@@ -29,13 +29,7 @@ struct TrainDevState {
     float loss_sum;       // sum of per-ray Huber losses
     float rays_f;         // this step's adaptive ray count
     float rays_next;      // the next step's, from this step's occupied samples
-    NerfTrainStats stats; // last completed step
-    // Adam's copy of the gradient statistics, taken with them: a pipelined
-    // run starts the next step (whose begin clears the fields above) while
-    // Adam still runs.
-    double adam_sumsq;
-    uint32_t adam_nonfinite;
-    uint32_t adam_t;      // optimizer step (frame + 1)
+    NerfTrainStats stats; // this step's, once it has ended
 };
 
 // Fixed parameters of a configured run (kernel argument).

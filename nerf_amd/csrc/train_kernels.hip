@@ -1889,9 +1889,6 @@ __global__ __launch_bounds__(kNormThreads) void k_grad_norm(TrainParams P, const
         for (uint32_t w = 0; w < kNormThreads / 64u; ++w) t += ws[w];
         S->grad_sumsq     = t;
         S->nonfinite      = bad;
-        S->adam_sumsq     = t;
-        S->adam_nonfinite = bad;
-        S->adam_t         = S->frame + 1u;
         if (end) step_end(P, S, prev);
     }
 }
@@ -1903,13 +1900,12 @@ struct AdamCoef {
     float lr, gs, bc1, bc2;  // gs: clip factor / loss scale
     uint32_t skip;
 };
-// Reads Adam's copy of the statistics (k_grad_norm), which the next step's
-// begin leaves alone.
+// From the step's own state slot (the next step's begin writes the other).
 __device__ AdamCoef adam_coef(const TrainParams& P, const TrainDevState* S) {
-    const float gn   = (float)sqrt(S->adam_sumsq > 0.0 ? S->adam_sumsq : 0.0) / P.loss_scale;
-    const uint32_t t = S->adam_t;  // optimizer step
+    const float gn   = (float)sqrt(S->grad_sumsq > 0.0 ? S->grad_sumsq : 0.0) / P.loss_scale;
+    const uint32_t t = S->frame + 1u;  // optimizer step
     AdamCoef c;
-    c.skip = (S->adam_nonfinite != 0u || !isfinite(gn) || gn > P.guard) ? 1u : 0u;
+    c.skip = (S->nonfinite != 0u || !isfinite(gn) || gn > P.guard) ? 1u : 0u;
     if (c.skip) {
         c.lr = 0.0f;
         c.gs = 1.0f / P.loss_scale;
