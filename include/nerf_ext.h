@@ -397,8 +397,9 @@ typedef struct NerfExtTrainDesc {
 
 typedef struct NerfExtTrainStats {
     NerfTrainStats last;             /* last completed step */
-    uint32_t rays;                   /* rays marched in the last step */
-    uint32_t samples;                /* samples kept in the last step */
+    uint32_t rays;                   /* rays marched in the step in progress (some of
+                                        its stages enqueued), else in the last step */
+    uint32_t samples;                /* samples kept in that step */
     uint32_t active_rays;
     uint32_t skipped;                /* Adam update skipped */
     uint64_t occupied_samples;       /* before the capacity cut */
@@ -449,12 +450,16 @@ enum {
     NERF_EXT_STAGE_COMPOSITE = 4, /* composite fwd/bwd + loss */
     NERF_EXT_STAGE_BACKWARD = 5,  /* MLP backward, hash scatter-add, dW */
     NERF_EXT_STAGE_ADAM = 6,      /* grad stats, Adam, fp16 copies */
-    NERF_EXT_STAGE_END = 7        /* stats, ray-count adaptation, step++ */
+    NERF_EXT_STAGE_END = 7        /* stats, sample total, step++ (the ray-count
+                                     adaptation runs in the sample stage) */
 };
 
 NERF_API NerfStatus nerf_ext_trainer_create(const NerfExtTrainDesc* desc, NerfExtTrainer** out);
 NERF_API NerfStatus nerf_ext_trainer_destroy(NerfExtTrainer* trainer);
-/* Enqueues `steps` full training steps (asynchronous). */
+/* Enqueues `steps` full training steps (asynchronous).  Consecutive steps of
+   one call overlap on the trainer's second stream (each step samples beside
+   the previous step's gradient sums and Adam); the results are those of the
+   steps enqueued one stage at a time, bit for bit. */
 NERF_API NerfStatus nerf_ext_trainer_step(NerfExtTrainer* trainer, uint32_t steps);
 /* Enqueues stages first..last of the current step (parity tests). */
 NERF_API NerfStatus nerf_ext_trainer_run_stages(NerfExtTrainer* trainer, uint32_t first, uint32_t last);
