@@ -139,6 +139,49 @@ __device__ __forceinline__ void encode_level(const GridParams& g, const TableT* 
     }
 }
 
+// ------------------------------------------------- box-relative coordinates
+// (p - lo) / (hi - lo) per axis, bit-identical to the three fp32 divisions.
+// A divisor fixed over many divisions (a box size) lets the division become
+// four FMAs and a multiply: r = the refined reciprocal of d (v_rcp_f32, then
+// one Newton step r0 + r0 (1 - d r0)), q0 = x r, then two residual
+// corrections q <- q + (x - d q) r (Markstein's method).  That is the
+// operation sequence hipcc emits for a correctly rounded x / d on gfx950,
+// less its operand scaling (v_div_scale) and special-value fix-up
+// (v_div_fixup), which change nothing while d and 1 / d are normal, x is
+// finite with |x| >= 2^-103, and 2^-126 <= |x / d| < 2^95.  The fast
+// quotients are kept when d lies in [2^-20, 2^20] (the reciprocal and its
+// refinement are then loop invariants for the cascade-0 box) and every
+// computed |q| lies in [2^-80, 2^80]: operands outside those ranges cannot
+// give a computed quotient there.  Otherwise (a degenerate box, a point on
+// or within 2^-80 box lengths of a face, non-finite input) all three axes
+// are divided.  The march's cell test had spent 33 of its 65 instructions
+// per step on the divisions.
+__device__ __forceinline__ float quotient_by(float x, float d, float r) {
+    const float q0 = x * r;
+    const float q1 = __builtin_fmaf(__builtin_fmaf(-d, q0, x), r, q0);
+    return __builtin_fmaf(__builtin_fmaf(-d, q1, x), r, q1);
+}
+
+__device__ __forceinline__ void box_relative(const float p[3], const float lo[3], const float hi[3], float q[3]) {
+    float d[3], x[3];
+    bool d_ok = true;
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+        d[a] = hi[a] - lo[a];
+        x[a] = p[a] - lo[a];
+        d_ok = d_ok && d[a] >= 0x1p-20f && d[a] <= 0x1p20f;
+        const float r0 = __builtin_amdgcn_rcpf(d[a]);
+        const float r  = __builtin_fmaf(__builtin_fmaf(-d[a], r0, 1.0f), r0, r0);
+        q[a]           = quotient_by(x[a], d[a], r);
+    }
+    const float lo_q = fminf(fminf(fabsf(q[0]), fabsf(q[1])), fabsf(q[2]));
+    const float sum  = fabsf(q[0]) + fabsf(q[1]) + fabsf(q[2]);  // NaN if any q is
+    if (!(d_ok && lo_q >= 0x1p-80f && sum <= 0x1p80f)) {
+#pragma unroll
+        for (int a = 0; a < 3; ++a) q[a] = x[a] / d[a];
+    }
+}
+
 // ------------------------------------------------------------- occupancy
 // Occupancy grid over one box or over nested cascades (NerfExtOccupancy in
 // include/nerf_ext.h): cascade 0 is [bmin, bmax], cascade c > 0 that box
@@ -177,11 +220,10 @@ __device__ __forceinline__ void occ_box(const OccView& o, uint32_t c, float lo[3
 // or kCellOutside.
 __device__ __forceinline__ uint32_t occ_cell(const OccView& o, const float p[3]) {
     for (uint32_t c = 0; c < o.cascades; ++c) {
-        float lo[3], hi[3];
+        float lo[3], hi[3], rel[3];
         occ_box(o, c, lo, hi);
-        const float rx = (p[0] - lo[0]) / (hi[0] - lo[0]);
-        const float ry = (p[1] - lo[1]) / (hi[1] - lo[1]);
-        const float rz = (p[2] - lo[2]) / (hi[2] - lo[2]);
+        box_relative(p, lo, hi, rel);
+        const float rx = rel[0], ry = rel[1], rz = rel[2];
         if (rx < 0.0f || rx >= 1.0f || ry < 0.0f || ry >= 1.0f || rz < 0.0f || rz >= 1.0f) continue;
         const uint32_t ix = min(o.res - 1u, (uint32_t)(rx * (float)o.res));
         const uint32_t iy = min(o.res - 1u, (uint32_t)(ry * (float)o.res));

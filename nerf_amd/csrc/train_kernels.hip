@@ -322,8 +322,9 @@ __global__ __launch_bounds__(256) void k_occ_apply_field(TrainParams P, const Tr
 // ---------------------------------------------------------------- sampling
 // Occupancy cell of p (backend-cuda.cu:338-351), or wave::kOutside.
 __device__ __forceinline__ uint32_t occ_cell_at(const TrainParams& P, const float p[3]) {
-    const float sx = P.bmax[0] - P.bmin[0], sy = P.bmax[1] - P.bmin[1], sz = P.bmax[2] - P.bmin[2];
-    const float rx = (p[0] - P.bmin[0]) / sx, ry = (p[1] - P.bmin[1]) / sy, rz = (p[2] - P.bmin[2]) / sz;
+    float rel[3];
+    box_relative(p, P.bmin, P.bmax, rel);
+    const float rx = rel[0], ry = rel[1], rz = rel[2];
     if (rx < 0.0f || rx >= 1.0f || ry < 0.0f || ry >= 1.0f || rz < 0.0f || rz >= 1.0f) return wave::kOutside;
     const uint32_t res = P.occ_res;
     const uint32_t ix = min(res - 1u, (uint32_t)(rx * (float)res)), iy = min(res - 1u, (uint32_t)(ry * (float)res)), iz = min(res - 1u, (uint32_t)(rz * (float)res));
