@@ -274,6 +274,12 @@ typedef struct NerfExtCamera {
  * direction from the splitmix64 stream (0xca3e, seed), draw index 2*index. */
 NERF_API NerfStatus nerf_ext_camera_orbit(uint64_t seed, uint32_t index, float radius, const float* centre3, uint32_t width, uint32_t height, float focal, NerfExtCamera* out);
 
+/* The occupancy cell rule's box-relative coordinates (p - lo) / (hi - lo) of
+ * n points (device [n][3] in and out; box_lo, box_hi: host float[3]), as the
+ * march kernels compute them: bit-identical to fp32 division (the reference
+ * divides inline, backend-cuda.cu:342).  For tests of that computation. */
+NERF_API NerfStatus nerf_ext_box_relative(const float* points, uint32_t n, const float* box_lo, const float* box_hi, float* out, void* stream);
+
 /* Per-ray occupied-step counts of the pixel rays of one view (pixel centres,
  * y flipped: backend-cuda.cu:561-563; march :448-469).  counts [W*H]. */
 NERF_API NerfStatus nerf_ext_march_count(const NerfExtCamera* camera, const NerfExtOccupancy* occupancy, uint32_t max_steps, uint32_t* counts, void* stream);

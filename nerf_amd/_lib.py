@@ -358,6 +358,7 @@ PROTOTYPES: dict[str, tuple] = {
     "nerf_ext_occupancy_mark_shell": (_S, [C.POINTER(NerfExtOccupancy), _P, _F, _F, _P]),
     # cameras, march, render
     "nerf_ext_camera_orbit": (_S, [_U64, _U32, _F, _P, _U32, _U32, _F, C.POINTER(NerfExtCamera)]),
+    "nerf_ext_box_relative": (_S, [_P, _U32, C.POINTER(C.c_float), C.POINTER(C.c_float), _P, _P]),
     "nerf_ext_march_count": (_S, [C.POINTER(NerfExtCamera), C.POINTER(NerfExtOccupancy), _U32, _P, _P]),
     "nerf_ext_march_count_noalloc": (_S, [C.POINTER(NerfExtCamera), C.POINTER(NerfExtOccupancy), _U32, _P, _P]),
     "nerf_ext_renderer_create": (_S, [C.POINTER(_P)]),

@@ -107,6 +107,18 @@ __global__ __launch_bounds__(256) void k_march_samples(const NerfExtCamera* __re
     });
 }
 
+// box_relative on n points [n][3] -> [n][3] (nerf_ext_box_relative).
+__global__ __launch_bounds__(256) void k_box_relative(const float* __restrict__ pts, uint32_t n, float3 lo, float3 hi, float* __restrict__ out) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i >= n) return;
+    const float p[3] = {pts[3ull * i], pts[3ull * i + 1u], pts[3ull * i + 2u]};
+    const float l[3] = {lo.x, lo.y, lo.z}, h[3] = {hi.x, hi.y, hi.z};
+    float q[3];
+    box_relative(p, l, h, q);
+#pragma unroll
+    for (int a = 0; a < 3; ++a) out[3ull * i + a] = q[a];
+}
+
 __global__ void k_fill_u32(uint32_t* __restrict__ p, uint32_t n, uint32_t v) {
     for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) p[i] = v;
 }
@@ -715,6 +727,14 @@ NERF_API NerfStatus nerf_ext_renderer_destroy(NerfExtRenderer* renderer) {
     if (!renderer) return NERF_STATUS_OK;
     (void)hipDeviceSynchronize();
     delete renderer;
+    return NERF_STATUS_OK;
+}
+
+NERF_API NerfStatus nerf_ext_box_relative(const float* points, uint32_t n, const float* box_lo, const float* box_hi, float* out, void* stream) {
+    NERF_CHECK_ARG(points && box_lo && box_hi && out, "nerf_ext_box_relative: null argument");
+    if (n == 0u) return NERF_STATUS_OK;
+    k_box_relative<<<(n + 255u) / 256u, 256, 0, (hipStream_t)stream>>>(points, n, make_float3(box_lo[0], box_lo[1], box_lo[2]), make_float3(box_hi[0], box_hi[1], box_hi[2]), out);
+    NERF_LAUNCH_CHECK("k_box_relative");
     return NERF_STATUS_OK;
 }
 
