@@ -140,7 +140,9 @@ __device__ __forceinline__ void encode_level(const GridParams& g, const TableT* 
 }
 
 // ------------------------------------------------- box-relative coordinates
-// (p - lo) / (hi - lo) per axis, bit-identical to the three fp32 divisions.
+// (p - lo) / (hi - lo) per axis, bit-identical to the three fp32 divisions:
+// the occupancy cell rule's coordinates and the hash grid's unit-cube
+// positions of march samples.
 // A divisor fixed over many divisions (a box size) lets the division become
 // four FMAs and a multiply: r = the refined reciprocal of d (v_rcp_f32, then
 // one Newton step r0 + r0 (1 - d r0)), q0 = x r, then two residual
@@ -494,8 +496,7 @@ struct PointsFromSamples {
         const float4 ro  = rays[2ull * r];
         const float4 rd  = rays[2ull * r + 1ull];
         const float w[3] = {ro.x + td.x * rd.x, ro.y + td.x * rd.y, ro.z + td.x * rd.z};
-#pragma unroll
-        for (int a = 0; a < 3; ++a) x[a] = (w[a] - bmin[a]) / (bmax[a] - bmin[a]);
+        box_relative(w, bmin, bmax, x);
     }
 };
 

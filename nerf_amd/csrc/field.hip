@@ -43,8 +43,7 @@ __device__ __forceinline__ void sample_point(const FieldInputs& in, uint32_t q, 
     d[1]             = rd.y;
     d[2]             = rd.z;
     const float w[3] = {ro.x + td.x * rd.x, ro.y + td.x * rd.y, ro.z + td.x * rd.z};
-#pragma unroll
-    for (int a = 0; a < 3; ++a) p[a] = (w[a] - in.bmin[a]) / (in.bmax[a] - in.bmin[a]);
+    box_relative(w, in.bmin, in.bmax, p);
 }
 
 // Colour input from per-sample fp32 SH coefficients (lane group grp's four).

@@ -239,8 +239,8 @@ __global__ __launch_bounds__(kThreads) void k_occ_eval(TrainParams P, GridParams
         const uint32_t z = cell / (res * res), rem = cell - z * res * res, y = rem / res, x = rem - y * res;
         float p[3] = {P.bmin[0] + ((float)x + 0.5f) * step[0], P.bmin[1] + ((float)y + 0.5f) * step[1], P.bmin[2] + ((float)z + 0.5f) * step[2]};
         // The hash grid encodes the unit cube: normalise by the AABB.
-#pragma unroll
-        for (int a = 0; a < 3; ++a) p[a] = (p[a] - P.bmin[a]) / (P.bmax[a] - P.bmin[a]);
+        const float w[3] = {p[0], p[1], p[2]};
+        box_relative(w, P.bmin, P.bmax, p);
         float feat[8];
         encode_quad(g, table, p, grp, feat);
         const floatx4 o = density_mlp(f, to_half8(feat));
@@ -962,8 +962,7 @@ __device__ __forceinline__ void tile_backward(const half8_t* F, const half8_t x,
 
 __device__ __forceinline__ void sample_position(float t, float4 ro, float4 rd, const float* bmin, const float* bmax, float p[3]) {
     const float w[3] = {ro.x + t * rd.x, ro.y + t * rd.y, ro.z + t * rd.z};
-#pragma unroll
-    for (int a = 0; a < 3; ++a) p[a] = (w[a] - bmin[a]) / (bmax[a] - bmin[a]);
+    box_relative(w, bmin, bmax, p);
 }
 __device__ __forceinline__ void sample_geometry(const float2* samples, const uint32_t* sample_ray, const float4* rays, const float* bmin, const float* bmax, uint32_t q, float p[3], float d[3]) {
     const float2 td  = samples[q];
