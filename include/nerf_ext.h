@@ -312,7 +312,10 @@ typedef struct NerfExtRenderDesc {
                                        1024 rays holding at most this many
                                        samples (a block is never split), so
                                        the sample buffers (32 B per sample)
-                                       hold one chunk */
+                                       hold one chunk.  With 0 a render of at
+                                       most 2^30 ray steps (rays x max_steps)
+                                       is one chunk marched once into per-ray
+                                       slots (32 B per ray step) */
     uint32_t* composited;           /* optional device [view][H][W]: samples
                                        composited per ray, i.e. up to and
                                        including the one after which T <

@@ -1,7 +1,9 @@
 // render.hip — inference rendering: occupancy march with compacted sample
 // streams, fused field evaluation, front-to-back compositing to RGBA8.
 //
-// Stages (one HIP stream):
+// Stages (one HIP stream); renders of at most kSlotSamples ray steps with
+// the default chunk size replace 1-3 by one pass, k_march_slots (eight lanes
+// per ray, the whole march, samples into per-ray slots of max_steps):
 //   1. k_march_count   one thread per ray: pixel ray + AABB (backend-cuda.cu
 //                      :373-408, :561-563), occupancy march (:448-469),
 //                      per-ray occupied-step count; ray record (o, tn, d, tf).
@@ -117,6 +119,38 @@ __global__ __launch_bounds__(256) void k_box_relative(const float* __restrict__ 
     box_relative(p, l, h, q);
 #pragma unroll
     for (int a = 0; a < 3; ++a) out[3ull * i + a] = q[a];
+}
+
+// One march per ray into per-ray slots (renders whose rays x max_steps fit
+// kSlotSamples): ray r's samples at [r * max_steps, + count), its count and
+// that offset, and its ray record, all from one pass of wave::march<8> to
+// the end of the ray (no count is known beforehand).  The same steps, cells
+// and samples as k_march_count followed by k_march_samples; the slots are
+// 8 KiB-aligned per ray at 1,024 steps, so each run's 64-byte segment falls
+// within one cache line.
+__global__ __launch_bounds__(256) void k_march_slots(const NerfExtCamera* __restrict__ cams, uint32_t pixels_per_view, uint32_t n_rays, OccView occ, uint32_t max_steps, float4* __restrict__ rays,
+                                                    uint32_t* __restrict__ counts, uint32_t* __restrict__ offsets, float2* __restrict__ samples) {
+    const uint32_t ray = (blockIdx.x * 256u + threadIdx.x) / kMarchGroup;
+    if (ray >= n_rays) return;
+    const uint32_t view     = ray / pixels_per_view;
+    const NerfExtCamera cam = cams[view];
+    Ray r;
+    float4 ro = make_float4(0.0f, 0.0f, 0.0f, 0.0f), rd = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    uint32_t count = 0u;
+    if (pixel_ray(cam, ray - view * pixels_per_view, occ.omin, occ.omax, r)) {
+        ro             = make_float4(r.o[0], r.o[1], r.o[2], r.tn);
+        rd             = make_float4(r.d[0], r.d[1], r.d[2], r.tf);
+        float2* slot   = samples + (uint64_t)ray * max_steps;
+        count          = wave::march<kMarchGroup>(ro, rd, cone_angle(cam), max_steps, ~0u, occ.bits, [&](const float p[3]) { return occ_cell(occ, p); }, [&](uint32_t k, float tm, float dt) {
+            slot[k] = make_float2(tm, dt);
+        });
+    }
+    if ((threadIdx.x & (kMarchGroup - 1u)) == 0u) {
+        rays[2ull * ray]      = ro;
+        rays[2ull * ray + 1u] = rd;
+        counts[ray]           = count;
+        offsets[ray]          = ray * max_steps;
+    }
 }
 
 __global__ void k_fill_u32(uint32_t* __restrict__ p, uint32_t n, uint32_t v) {
@@ -577,6 +611,7 @@ hipError_t exclusive_scan_u32(const uint32_t* in, uint32_t* out, uint32_t n, uin
 constexpr uint32_t kFirstRound = 256u;  // samples per ray in the first round (a multiple of 64)
 constexpr uint32_t kScanBlockRays = 1024u;        // rays per block of the chunk plan (the scan's block)
 constexpr uint64_t kChunkSamples  = 1ull << 29;   // samples per chunk: 32 B each in the stream buffers (16 GiB)
+constexpr uint64_t kSlotSamples   = 1ull << 30;   // default-chunk renders of at most this many ray steps march once, into per-ray slots
 constexpr uint32_t kMaxSteps      = 1u << 19;     // so that a block of rays holds at most kChunkSamples samples
 constexpr uint32_t kMaxRounds  = 24u;   // round ends double from 256 (12 cover 2^19 steps), plus two
 
@@ -823,35 +858,51 @@ NERF_API NerfStatus nerf_ext_render(NerfExtRenderer* R, const NerfExtRenderDesc*
     const bool timed      = stats != nullptr;
 
     if (timed) NERF_HIP_TRY(hipEventRecord(R->ev[0], st));
-    k_march_count<<<blocks, 256, 0, st>>>(R->cams.ptr, ppv, n_rays, occ, d->max_steps, R->rays.ptr, R->counts.ptr);
-    NERF_LAUNCH_CHECK("k_march_count");
-    if (timed) NERF_HIP_TRY(hipEventRecord(R->ev[1], st));
-    // Chunk plan: the per-ray counts summed over blocks of kScanBlock rays
-    // (exact; at most kScanBlock * 2^19 < 2^32 each), copied to the host,
-    // which groups whole blocks into chunks of at most kChunkSamples samples.
-    // Each chunk is marched, shaded and composited on its own, so the sample
-    // buffers hold one chunk; offsets are relative to the chunk.
-    const uint32_t n_blocks = (n_rays + kScanBlockRays - 1u) / kScanBlockRays;
-    NERF_HIP_TRY(R->scan_tmp.reserve(std::max<uint64_t>(scan_tmp_words(n_rays), n_blocks)));
-    NERF_HIP_TRY(block_sums_u32(R->counts.ptr, n_rays, R->scan_tmp.ptr, st));
-    R->host_sums.resize(n_blocks);
-    NERF_HIP_TRY(hipMemcpyAsync(R->host_sums.data(), R->scan_tmp.ptr, sizeof(uint32_t) * n_blocks, hipMemcpyDeviceToHost, st));
-    NERF_HIP_TRY(hipStreamSynchronize(st));
-    if (timed) NERF_HIP_TRY(hipEventRecord(R->ev[2], st));
     struct Chunk {
         uint32_t ray0, ray_end;
         uint64_t samples;
     };
     std::vector<Chunk> chunks;
-    const uint64_t budget = d->chunk_samples ? std::min<uint64_t>(d->chunk_samples, kChunkSamples) : kChunkSamples;
     uint64_t total = 0, biggest = 0;
-    for (uint32_t b = 0; b < n_blocks;) {
-        Chunk c{b * kScanBlockRays, 0u, 0u};
-        while (b < n_blocks && (c.ray0 == (uint64_t)b * kScanBlockRays || c.samples + R->host_sums[b] <= budget)) c.samples += R->host_sums[b++];
-        c.ray_end = std::min<uint64_t>((uint64_t)b * kScanBlockRays, n_rays);
-        total += c.samples;
-        biggest = std::max(biggest, c.samples);
-        chunks.push_back(c);
+    const uint32_t n_blocks = (n_rays + kScanBlockRays - 1u) / kScanBlockRays;
+    NERF_HIP_TRY(R->scan_tmp.reserve(std::max<uint64_t>(scan_tmp_words(n_rays), n_blocks)));
+    // With the default chunk size a render of at most kSlotSamples ray steps
+    // is one chunk marched once, into per-ray slots (k_march_slots): no count
+    // pass, no plan on the host, no scan.  Its buffers are sized by rays x
+    // max_steps.
+    const bool slots = !d->chunk_samples && (uint64_t)n_rays * d->max_steps <= kSlotSamples;
+    if (slots) {
+        biggest = (uint64_t)n_rays * d->max_steps;
+        NERF_HIP_TRY(R->samples.reserve(biggest));
+        k_march_slots<<<(n_rays + 256u / kMarchGroup - 1u) / (256u / kMarchGroup), 256, 0, st>>>(R->cams.ptr, ppv, n_rays, occ, d->max_steps, R->rays.ptr, R->counts.ptr, R->offsets.ptr, R->samples.ptr);
+        NERF_LAUNCH_CHECK("k_march_slots");
+        if (timed) NERF_HIP_TRY(hipEventRecord(R->ev[1], st));
+        if (timed) NERF_HIP_TRY(hipEventRecord(R->ev[2], st));
+        chunks.push_back(Chunk{0u, n_rays, biggest});
+    } else {
+        k_march_count<<<blocks, 256, 0, st>>>(R->cams.ptr, ppv, n_rays, occ, d->max_steps, R->rays.ptr, R->counts.ptr);
+        NERF_LAUNCH_CHECK("k_march_count");
+        if (timed) NERF_HIP_TRY(hipEventRecord(R->ev[1], st));
+        // Chunk plan: the per-ray counts summed over blocks of kScanBlock rays
+        // (exact; at most kScanBlock * 2^19 < 2^32 each), copied to the host,
+        // which groups whole blocks into chunks of at most kChunkSamples
+        // samples.  Each chunk is marched, shaded and composited on its own,
+        // so the sample buffers hold one chunk; offsets are relative to the
+        // chunk.
+        NERF_HIP_TRY(block_sums_u32(R->counts.ptr, n_rays, R->scan_tmp.ptr, st));
+        R->host_sums.resize(n_blocks);
+        NERF_HIP_TRY(hipMemcpyAsync(R->host_sums.data(), R->scan_tmp.ptr, sizeof(uint32_t) * n_blocks, hipMemcpyDeviceToHost, st));
+        NERF_HIP_TRY(hipStreamSynchronize(st));
+        if (timed) NERF_HIP_TRY(hipEventRecord(R->ev[2], st));
+        const uint64_t budget = d->chunk_samples ? std::min<uint64_t>(d->chunk_samples, kChunkSamples) : kChunkSamples;
+        for (uint32_t b = 0; b < n_blocks;) {
+            Chunk c{b * kScanBlockRays, 0u, 0u};
+            while (b < n_blocks && (c.ray0 == (uint64_t)b * kScanBlockRays || c.samples + R->host_sums[b] <= budget)) c.samples += R->host_sums[b++];
+            c.ray_end = std::min<uint64_t>((uint64_t)b * kScanBlockRays, n_rays);
+            total += c.samples;
+            biggest = std::max(biggest, c.samples);
+            chunks.push_back(c);
+        }
     }
     NERF_HIP_TRY(R->samples.reserve(biggest));
     NERF_HIP_TRY(R->field.reserve(biggest));
@@ -907,10 +958,12 @@ NERF_API NerfStatus nerf_ext_render(NerfExtRenderer* R, const NerfExtRenderDesc*
     for (const Chunk& c : chunks) {
         const uint32_t nr = c.ray_end - c.ray0;
         if (timed) NERF_HIP_TRY(hipEventRecord(R->ev[3], st));
-        NERF_HIP_TRY(exclusive_scan_u32(R->counts.ptr + c.ray0, R->offsets.ptr + c.ray0, nr, R->scan_tmp.ptr, R->total.ptr, st));
+        if (!slots) NERF_HIP_TRY(exclusive_scan_u32(R->counts.ptr + c.ray0, R->offsets.ptr + c.ray0, nr, R->scan_tmp.ptr, R->total.ptr, st));
         if (timed) NERF_HIP_TRY(hipEventRecord(R->ev[4], st));
-        k_march_samples<<<(nr + 256u / kMarchGroup - 1u) / (256u / kMarchGroup), 256, 0, st>>>(R->cams.ptr, ppv, c.ray0, c.ray_end, occ, d->max_steps, R->rays.ptr, R->counts.ptr, R->offsets.ptr, R->samples.ptr);
-        NERF_LAUNCH_CHECK("k_march_samples");
+        if (!slots) {
+            k_march_samples<<<(nr + 256u / kMarchGroup - 1u) / (256u / kMarchGroup), 256, 0, st>>>(R->cams.ptr, ppv, c.ray0, c.ray_end, occ, d->max_steps, R->rays.ptr, R->counts.ptr, R->offsets.ptr, R->samples.ptr);
+            NERF_LAUNCH_CHECK("k_march_samples");
+        }
         if (timed) NERF_HIP_TRY(hipEventRecord(R->ev[5], st));
         uint32_t* n_cur = R->n_active.ptr;
         uint32_t* n_nxt = R->n_active.ptr + 1;
@@ -976,6 +1029,13 @@ NERF_API NerfStatus nerf_ext_render(NerfExtRenderer* R, const NerfExtRenderDesc*
         NERF_HIP_TRY(hipEventElapsedTime(&ms_plan, R->ev[1], R->ev[2]));
         NERF_HIP_TRY(hipEventElapsedTime(&total_ms, R->ev[0], end));
         (void)hipEventDestroy(end);
+        if (slots) {  // the marched total, from the per-block sums of the counts
+            NERF_HIP_TRY(block_sums_u32(R->counts.ptr, n_rays, R->scan_tmp.ptr, st));
+            R->host_sums.resize(n_blocks);
+            NERF_HIP_TRY(hipMemcpyAsync(R->host_sums.data(), R->scan_tmp.ptr, sizeof(uint32_t) * n_blocks, hipMemcpyDeviceToHost, st));
+            NERF_HIP_TRY(hipStreamSynchronize(st));
+            for (uint32_t b = 0; b < n_blocks; ++b) total += R->host_sums[b];
+        }
         stats->rays           = n_rays;
         stats->samples        = total;
         stats->samples_shaded = shaded;
