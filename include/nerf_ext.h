@@ -307,15 +307,16 @@ typedef struct NerfExtRenderDesc {
     float min_transmittance;        /* early stop threshold, e.g. 1e-4 */
     float background[3];            /* composited as C + T * background */
     void* stream;
-    uint64_t chunk_samples;         /* 0: 2^29.  Rays are marched, shaded and
+    uint64_t chunk_samples;         /* Rays are marched, shaded and
                                        composited in chunks of whole blocks of
-                                       1024 rays holding at most this many
-                                       samples (a block is never split), so
-                                       the sample buffers (32 B per sample)
-                                       hold one chunk.  With 0 a render of at
-                                       most 2^30 ray steps (rays x max_steps)
-                                       is one chunk marched once into per-ray
-                                       slots (32 B per ray step) */
+                                       1024 rays (a block is never split).
+                                       0: chunks of at most 2^30 ray steps
+                                       (rays x max_steps), each marched once
+                                       into per-ray slots (32 B per ray step
+                                       in the buffers).  Else: chunks of at
+                                       most this many samples (capped at
+                                       2^29) after a count pass over all
+                                       rays (32 B per sample) */
     uint32_t* composited;           /* optional device [view][H][W]: samples
                                        composited per ray, i.e. up to and
                                        including the one after which T <

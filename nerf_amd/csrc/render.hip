@@ -1,9 +1,10 @@
 // render.hip — inference rendering: occupancy march with compacted sample
 // streams, fused field evaluation, front-to-back compositing to RGBA8.
 //
-// Stages (one HIP stream); renders of at most kSlotSamples ray steps with
-// the default chunk size replace 1-3 by one pass, k_march_slots (eight lanes
-// per ray, the whole march, samples into per-ray slots of max_steps):
+// Stages (one HIP stream); with the default chunk size 1-3 are one pass per
+// chunk of at most kSlotSamples ray steps, k_march_slots (eight lanes per
+// ray, the whole march, samples into per-ray slots of max_steps); with an
+// explicit sample budget per chunk:
 //   1. k_march_count   one thread per ray: pixel ray + AABB (backend-cuda.cu
 //                      :373-408, :561-563), occupancy march (:448-469),
 //                      per-ray occupied-step count; ray record (o, tn, d, tf).
@@ -121,17 +122,18 @@ __global__ __launch_bounds__(256) void k_box_relative(const float* __restrict__ 
     for (int a = 0; a < 3; ++a) out[3ull * i + a] = q[a];
 }
 
-// One march per ray into per-ray slots (renders whose rays x max_steps fit
-// kSlotSamples): ray r's samples at [r * max_steps, + count), its count and
-// that offset, and its ray record, all from one pass of wave::march<8> to
-// the end of the ray (no count is known beforehand).  The same steps, cells
+// One march per ray into per-ray slots (the default chunking: chunks of at
+// most kSlotSamples ray steps): ray r's samples at [(r - ray0) max_steps,
+// + count) of the chunk's buffer, its count and that offset, and its ray
+// record, all from one pass of wave::march<8> to the end of the ray (no
+// count is known beforehand).  The same steps, cells
 // and samples as k_march_count followed by k_march_samples; the slots are
 // 8 KiB-aligned per ray at 1,024 steps, so each run's 64-byte segment falls
 // within one cache line.
-__global__ __launch_bounds__(256) void k_march_slots(const NerfExtCamera* __restrict__ cams, uint32_t pixels_per_view, uint32_t n_rays, OccView occ, uint32_t max_steps, float4* __restrict__ rays,
+__global__ __launch_bounds__(256) void k_march_slots(const NerfExtCamera* __restrict__ cams, uint32_t pixels_per_view, uint32_t ray0, uint32_t ray_end, OccView occ, uint32_t max_steps, float4* __restrict__ rays,
                                                     uint32_t* __restrict__ counts, uint32_t* __restrict__ offsets, float2* __restrict__ samples) {
-    const uint32_t ray = (blockIdx.x * 256u + threadIdx.x) / kMarchGroup;
-    if (ray >= n_rays) return;
+    const uint32_t ray = ray0 + (blockIdx.x * 256u + threadIdx.x) / kMarchGroup;
+    if (ray >= ray_end) return;
     const uint32_t view     = ray / pixels_per_view;
     const NerfExtCamera cam = cams[view];
     Ray r;
@@ -140,7 +142,7 @@ __global__ __launch_bounds__(256) void k_march_slots(const NerfExtCamera* __rest
     if (pixel_ray(cam, ray - view * pixels_per_view, occ.omin, occ.omax, r)) {
         ro             = make_float4(r.o[0], r.o[1], r.o[2], r.tn);
         rd             = make_float4(r.d[0], r.d[1], r.d[2], r.tf);
-        float2* slot   = samples + (uint64_t)ray * max_steps;
+        float2* slot   = samples + (uint64_t)(ray - ray0) * max_steps;
         count          = wave::march<kMarchGroup>(ro, rd, cone_angle(cam), max_steps, ~0u, occ.bits, [&](const float p[3]) { return occ_cell(occ, p); }, [&](uint32_t k, float tm, float dt) {
             slot[k] = make_float2(tm, dt);
         });
@@ -149,7 +151,7 @@ __global__ __launch_bounds__(256) void k_march_slots(const NerfExtCamera* __rest
         rays[2ull * ray]      = ro;
         rays[2ull * ray + 1u] = rd;
         counts[ray]           = count;
-        offsets[ray]          = ray * max_steps;
+        offsets[ray]          = (ray - ray0) * max_steps;
     }
 }
 
@@ -611,7 +613,7 @@ hipError_t exclusive_scan_u32(const uint32_t* in, uint32_t* out, uint32_t n, uin
 constexpr uint32_t kFirstRound = 256u;  // samples per ray in the first round (a multiple of 64)
 constexpr uint32_t kScanBlockRays = 1024u;        // rays per block of the chunk plan (the scan's block)
 constexpr uint64_t kChunkSamples  = 1ull << 29;   // samples per chunk: 32 B each in the stream buffers (16 GiB)
-constexpr uint64_t kSlotSamples   = 1ull << 30;   // default-chunk renders of at most this many ray steps march once, into per-ray slots
+constexpr uint64_t kSlotSamples   = 1ull << 30;   // ray steps (rays x max_steps) per chunk of the default chunking, marched once into per-ray slots
 constexpr uint32_t kMaxSteps      = 1u << 19;     // so that a block of rays holds at most kChunkSamples samples
 constexpr uint32_t kMaxRounds  = 24u;   // round ends double from 256 (12 cover 2^19 steps), plus two
 
@@ -866,19 +868,20 @@ NERF_API NerfStatus nerf_ext_render(NerfExtRenderer* R, const NerfExtRenderDesc*
     uint64_t total = 0, biggest = 0;
     const uint32_t n_blocks = (n_rays + kScanBlockRays - 1u) / kScanBlockRays;
     NERF_HIP_TRY(R->scan_tmp.reserve(std::max<uint64_t>(scan_tmp_words(n_rays), n_blocks)));
-    // With the default chunk size a render of at most kSlotSamples ray steps
-    // is one chunk marched once, into per-ray slots (k_march_slots): no count
-    // pass, no plan on the host, no scan.  Its buffers are sized by rays x
-    // max_steps.
-    const bool slots = !d->chunk_samples && (uint64_t)n_rays * d->max_steps <= kSlotSamples;
+    // With the default chunk size the chunks are whole blocks of rays holding
+    // at most kSlotSamples ray steps (rays x max_steps), each marched once,
+    // into per-ray slots (k_march_slots): no count pass, no plan on the host,
+    // no scan.  Their buffers are sized by rays x max_steps.
+    const bool slots = !d->chunk_samples;
     if (slots) {
-        biggest = (uint64_t)n_rays * d->max_steps;
-        NERF_HIP_TRY(R->samples.reserve(biggest));
-        k_march_slots<<<(n_rays + 256u / kMarchGroup - 1u) / (256u / kMarchGroup), 256, 0, st>>>(R->cams.ptr, ppv, n_rays, occ, d->max_steps, R->rays.ptr, R->counts.ptr, R->offsets.ptr, R->samples.ptr);
-        NERF_LAUNCH_CHECK("k_march_slots");
         if (timed) NERF_HIP_TRY(hipEventRecord(R->ev[1], st));
         if (timed) NERF_HIP_TRY(hipEventRecord(R->ev[2], st));
-        chunks.push_back(Chunk{0u, n_rays, biggest});
+        const uint32_t per_chunk = std::max<uint32_t>(1u, (uint32_t)(kSlotSamples / ((uint64_t)d->max_steps * kScanBlockRays))) * kScanBlockRays;
+        for (uint32_t r0 = 0; r0 < n_rays; r0 += std::min(per_chunk, n_rays - r0)) {
+            const uint32_t r1 = r0 + std::min(per_chunk, n_rays - r0);
+            chunks.push_back(Chunk{r0, r1, (uint64_t)(r1 - r0) * d->max_steps});
+            biggest = std::max(biggest, (uint64_t)(r1 - r0) * d->max_steps);
+        }
     } else {
         k_march_count<<<blocks, 256, 0, st>>>(R->cams.ptr, ppv, n_rays, occ, d->max_steps, R->rays.ptr, R->counts.ptr);
         NERF_LAUNCH_CHECK("k_march_count");
@@ -960,7 +963,10 @@ NERF_API NerfStatus nerf_ext_render(NerfExtRenderer* R, const NerfExtRenderDesc*
         if (timed) NERF_HIP_TRY(hipEventRecord(R->ev[3], st));
         if (!slots) NERF_HIP_TRY(exclusive_scan_u32(R->counts.ptr + c.ray0, R->offsets.ptr + c.ray0, nr, R->scan_tmp.ptr, R->total.ptr, st));
         if (timed) NERF_HIP_TRY(hipEventRecord(R->ev[4], st));
-        if (!slots) {
+        if (slots) {
+            k_march_slots<<<(nr + 256u / kMarchGroup - 1u) / (256u / kMarchGroup), 256, 0, st>>>(R->cams.ptr, ppv, c.ray0, c.ray_end, occ, d->max_steps, R->rays.ptr, R->counts.ptr, R->offsets.ptr, R->samples.ptr);
+            NERF_LAUNCH_CHECK("k_march_slots");
+        } else {
             k_march_samples<<<(nr + 256u / kMarchGroup - 1u) / (256u / kMarchGroup), 256, 0, st>>>(R->cams.ptr, ppv, c.ray0, c.ray_end, occ, d->max_steps, R->rays.ptr, R->counts.ptr, R->offsets.ptr, R->samples.ptr);
             NERF_LAUNCH_CHECK("k_march_samples");
         }

@@ -1,7 +1,8 @@
 """Parity of the benchmarked renders at their full size, and of the early stop.
 
 Each test renders a whole benchmarked view (or, for C5, all eight views in
-one call: 45 chunks of whole 1,024-ray blocks, rounds with per-ray quotas)
+one call: 29 chunks of whole 1,024-ray blocks, each marched once into
+per-ray slots, rounds with per-ray quotas)
 and compares a deterministic ray subset with the oracle's render of the same
 rays (backend-cuda.cu:601-635 composite, :1870-1909 whole-image loop):
 - per-ray occupied sample counts bit-exact (over the whole view for the
