@@ -462,6 +462,10 @@ struct FieldInputs {
     // Optional with sample_index: the owning ray of the j-th evaluated
     // sample, read in order instead of sample_ray at a scattered stream index.
     const uint32_t* sample_index_ray;
+    // With slot_rays the samples sit in per-ray slots of 2^slot_shift: stream
+    // sample q belongs to ray slot_ray0 + (q >> slot_shift) (no ray array).
+    bool slot_rays;
+    uint32_t slot_shift, slot_ray0;
     // With sample_index (the renderer's rounds): output j goes to out[j] in
     // evaluation order as (alpha, r, g, b), alpha = 1 - exp(-sigma max(dt, 0))
     // with the sample's dt, instead of (sigma, r, g, b) at out[sample_index[j]].
@@ -481,6 +485,12 @@ struct FieldInputs {
     // of features_out, and the MLP pass reads.
     uint32_t* features_lm;
 };
+
+// Owning ray of evaluated sample j (stream index qs), per FieldInputs.
+__device__ __forceinline__ uint32_t sample_owner(const FieldInputs& in, uint32_t j, uint32_t qs) {
+    if (in.slot_rays) return in.slot_ray0 + (qs >> in.slot_shift);
+    return in.sample_index && in.sample_index_ray ? in.sample_index_ray[j] : in.sample_ray[qs];
+}
 
 struct PointsFromSamples {
     const float2* samples;

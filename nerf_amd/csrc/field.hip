@@ -180,7 +180,7 @@ __global__ __launch_bounds__(kBlockThreads) void k_field_forward(GridParams g, c
         if constexpr (kFromSamples) {
             const uint32_t qs = in.sample_index ? in.sample_index[q] : q;
             dst               = in.sample_index && !in.alpha_in_order ? qs : s;
-            sample_point(in, qs, in.sample_index && in.sample_index_ray ? in.sample_index_ray[q] : in.sample_ray[qs], p, d, dt);
+            sample_point(in, qs, sample_owner(in, q, qs), p, d, dt);
         } else {
 #pragma unroll
             for (int a = 0; a < 3; ++a) {
@@ -244,7 +244,7 @@ __global__ __launch_bounds__(kBlockThreads) void k_field_forward_lv(GridParams g
         float p[3], d[3];
         if constexpr (kFromSamples) {
             const uint32_t qs = in.sample_index ? in.sample_index[q] : q;
-            const uint32_t r  = in.sample_index && in.sample_index_ray ? in.sample_index_ray[q] : in.sample_ray[qs];
+            const uint32_t r  = sample_owner(in, q, qs);
             float dt;
             sample_point(in, qs, r, p, d, dt);
             dts[wv][lane] = dt;

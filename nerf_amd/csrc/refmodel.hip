@@ -455,7 +455,7 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(2
             if constexpr (kFromSamples) {
                 const uint32_t qs = in.sample_index ? in.sample_index[q] : q;
                 const float2 td   = in.samples[qs];
-                const uint32_t r  = in.sample_index && in.sample_index_ray ? in.sample_index_ray[q] : in.sample_ray[qs];
+                const uint32_t r  = sample_owner(in, q, qs);
                 const float4 ro = in.rays[2ull * r], rd = in.rays[2ull * r + 1ull];
                 dt = td.y;
                 d[0] = rd.x;

@@ -123,15 +123,15 @@ __global__ __launch_bounds__(256) void k_box_relative(const float* __restrict__ 
 }
 
 // One march per ray into per-ray slots (the default chunking: chunks of at
-// most kSlotSamples ray steps): ray r's samples at [(r - ray0) max_steps,
-// + count) of the chunk's buffer, its count and that offset, and its ray
-// record, all from one pass of wave::march<8> to the end of the ray (no
-// count is known beforehand).  The same steps, cells
-// and samples as k_march_count followed by k_march_samples; the slots are
-// 8 KiB-aligned per ray at 1,024 steps, so each run's 64-byte segment falls
-// within one cache line.
-__global__ __launch_bounds__(256) void k_march_slots(const NerfExtCamera* __restrict__ cams, uint32_t pixels_per_view, uint32_t ray0, uint32_t ray_end, OccView occ, uint32_t max_steps, float4* __restrict__ rays,
-                                                    uint32_t* __restrict__ counts, uint32_t* __restrict__ offsets, float2* __restrict__ samples) {
+// most kSlotSamples slot entries): ray r's samples at [(r - ray0) 2^shift,
+// + count) of the chunk's buffer (2^shift >= max_steps, so a sample's index
+// also names its ray), its count and that offset, and its ray record, all
+// from one pass of wave::march<8> to the end of the ray (no count is known
+// beforehand).  The same steps, cells and samples as k_march_count followed
+// by k_march_samples; the slots are 8 KiB-aligned per ray at 1,024 steps, so
+// each run's 64-byte segment falls within one cache line.
+__global__ __launch_bounds__(256) void k_march_slots(const NerfExtCamera* __restrict__ cams, uint32_t pixels_per_view, uint32_t ray0, uint32_t ray_end, OccView occ, uint32_t max_steps, uint32_t shift,
+                                                    float4* __restrict__ rays, uint32_t* __restrict__ counts, uint32_t* __restrict__ offsets, float2* __restrict__ samples) {
     const uint32_t ray = ray0 + (blockIdx.x * 256u + threadIdx.x) / kMarchGroup;
     if (ray >= ray_end) return;
     const uint32_t view     = ray / pixels_per_view;
@@ -142,7 +142,7 @@ __global__ __launch_bounds__(256) void k_march_slots(const NerfExtCamera* __rest
     if (pixel_ray(cam, ray - view * pixels_per_view, occ.omin, occ.omax, r)) {
         ro             = make_float4(r.o[0], r.o[1], r.o[2], r.tn);
         rd             = make_float4(r.d[0], r.d[1], r.d[2], r.tf);
-        float2* slot   = samples + (uint64_t)(ray - ray0) * max_steps;
+        float2* slot   = samples + ((uint64_t)(ray - ray0) << shift);
         count          = wave::march<kMarchGroup>(ro, rd, cone_angle(cam), max_steps, ~0u, occ.bits, [&](const float p[3]) { return occ_cell(occ, p); }, [&](uint32_t k, float tm, float dt) {
             slot[k] = make_float2(tm, dt);
         });
@@ -151,7 +151,7 @@ __global__ __launch_bounds__(256) void k_march_slots(const NerfExtCamera* __rest
         rays[2ull * ray]      = ro;
         rays[2ull * ray + 1u] = rd;
         counts[ray]           = count;
-        offsets[ray]          = (ray - ray0) * max_steps;
+        offsets[ray]          = (ray - ray0) << shift;
     }
 }
 
@@ -345,10 +345,12 @@ __global__ __launch_bounds__(256) void k_round_counts(uint32_t n_slots, const ui
     cnt[a] = v;
 }
 
-// Stream indices of this round's samples.  One wave per group of 64 list
-// slots (lane = slot): the group's samples fill the same range of the list
-// as slot by slot (from off of its first slot), but step-major: step i of
-// every slot that has one, in slot order, then step i + 1.
+// Stream indices of this round's samples, and with qray non-null each
+// entry's ray (samples in per-ray slots need none: the index names the ray).
+// One wave per group of 64 list slots (lane = slot): the group's samples
+// fill the same range of the list as slot by slot (from off of its first
+// slot), but step-major: step i of every slot that has one, in slot order,
+// then step i + 1.
 __global__ __launch_bounds__(256) void k_round_list(const uint32_t* __restrict__ list, const uint32_t* __restrict__ n_active, const uint32_t* __restrict__ offsets, const uint2* __restrict__ prog, const uint32_t* __restrict__ cnt,
                                                    const uint32_t* __restrict__ off, uint32_t* __restrict__ qlist, uint32_t* __restrict__ qray) {
     const uint32_t lane = threadIdx.x & 63u, nw = gridDim.x * 4u;
@@ -368,7 +370,7 @@ __global__ __launch_bounds__(256) void k_round_list(const uint32_t* __restrict__
             if (i < m) {
                 const uint32_t at = dst + wave::rank_below(act);
                 qlist[at]         = q0 + i;
-                qray[at]          = ray;
+                if (qray) qray[at] = ray;
             }
             dst += (uint32_t)__popcll(act);
         }
@@ -873,14 +875,16 @@ NERF_API NerfStatus nerf_ext_render(NerfExtRenderer* R, const NerfExtRenderDesc*
     // into per-ray slots (k_march_slots): no count pass, no plan on the host,
     // no scan.  Their buffers are sized by rays x max_steps.
     const bool slots = !d->chunk_samples;
+    uint32_t slot_shift = 0u;  // slots of 2^slot_shift >= max_steps samples
+    while ((1u << slot_shift) < d->max_steps) ++slot_shift;
     if (slots) {
         if (timed) NERF_HIP_TRY(hipEventRecord(R->ev[1], st));
         if (timed) NERF_HIP_TRY(hipEventRecord(R->ev[2], st));
-        const uint32_t per_chunk = std::max<uint32_t>(1u, (uint32_t)(kSlotSamples / ((uint64_t)d->max_steps * kScanBlockRays))) * kScanBlockRays;
+        const uint32_t per_chunk = std::max<uint32_t>(1u, (uint32_t)(kSlotSamples / ((1ull << slot_shift) * kScanBlockRays))) * kScanBlockRays;
         for (uint32_t r0 = 0; r0 < n_rays; r0 += std::min(per_chunk, n_rays - r0)) {
             const uint32_t r1 = r0 + std::min(per_chunk, n_rays - r0);
-            chunks.push_back(Chunk{r0, r1, (uint64_t)(r1 - r0) * d->max_steps});
-            biggest = std::max(biggest, (uint64_t)(r1 - r0) * d->max_steps);
+            chunks.push_back(Chunk{r0, r1, (uint64_t)(r1 - r0) << slot_shift});
+            biggest = std::max(biggest, (uint64_t)(r1 - r0) << slot_shift);
         }
     } else {
         k_march_count<<<blocks, 256, 0, st>>>(R->cams.ptr, ppv, n_rays, occ, d->max_steps, R->rays.ptr, R->counts.ptr);
@@ -910,7 +914,7 @@ NERF_API NerfStatus nerf_ext_render(NerfExtRenderer* R, const NerfExtRenderDesc*
     NERF_HIP_TRY(R->samples.reserve(biggest));
     NERF_HIP_TRY(R->field.reserve(biggest));
     NERF_HIP_TRY(R->qlist.reserve(biggest));
-    NERF_HIP_TRY(R->qray.reserve(biggest));
+    if (!slots) NERF_HIP_TRY(R->qray.reserve(biggest));
 
     // Every field launch of the rounds reads its entries' rays from the round
     // list (qray), so the march writes no per-sample ray index.
@@ -953,18 +957,21 @@ NERF_API NerfStatus nerf_ext_render(NerfExtRenderer* R, const NerfExtRenderDesc*
     NERF_HIP_TRY(R->koff.reserve(chunk_rays_max));
     NERF_HIP_TRY(R->keep_total.reserve(1));
     in.sample_index     = R->qlist.ptr;
-    in.sample_index_ray = R->qray.ptr;
+    in.sample_index_ray = slots ? nullptr : R->qray.ptr;  // slots: the ray from the index
+    in.slot_rays        = slots;
+    in.slot_shift       = slot_shift;
     in.alpha_in_order   = true;  // k_round_composite reads (alpha, rgb) in list order
 
     float ms_scan = 0.0f, ms_samples = 0.0f, field_ms = 0.0f;
     uint64_t shaded = 0;
     for (const Chunk& c : chunks) {
         const uint32_t nr = c.ray_end - c.ray0;
+        in.slot_ray0       = c.ray0;
         if (timed) NERF_HIP_TRY(hipEventRecord(R->ev[3], st));
         if (!slots) NERF_HIP_TRY(exclusive_scan_u32(R->counts.ptr + c.ray0, R->offsets.ptr + c.ray0, nr, R->scan_tmp.ptr, R->total.ptr, st));
         if (timed) NERF_HIP_TRY(hipEventRecord(R->ev[4], st));
         if (slots) {
-            k_march_slots<<<(nr + 256u / kMarchGroup - 1u) / (256u / kMarchGroup), 256, 0, st>>>(R->cams.ptr, ppv, c.ray0, c.ray_end, occ, d->max_steps, R->rays.ptr, R->counts.ptr, R->offsets.ptr, R->samples.ptr);
+            k_march_slots<<<(nr + 256u / kMarchGroup - 1u) / (256u / kMarchGroup), 256, 0, st>>>(R->cams.ptr, ppv, c.ray0, c.ray_end, occ, d->max_steps, slot_shift, R->rays.ptr, R->counts.ptr, R->offsets.ptr, R->samples.ptr);
             NERF_LAUNCH_CHECK("k_march_slots");
         } else {
             k_march_samples<<<(nr + 256u / kMarchGroup - 1u) / (256u / kMarchGroup), 256, 0, st>>>(R->cams.ptr, ppv, c.ray0, c.ray_end, occ, d->max_steps, R->rays.ptr, R->counts.ptr, R->offsets.ptr, R->samples.ptr);
@@ -987,7 +994,7 @@ NERF_API NerfStatus nerf_ext_render(NerfExtRenderer* R, const NerfExtRenderDesc*
         for (uint32_t r = 0; r < n_rounds; ++r) {
             k_round_counts<<<cblocks, 256, 0, st>>>(nr, l_cur, n_cur, R->counts.ptr, R->prog.ptr, R->cnt.ptr, R->keep.ptr);
             NERF_HIP_TRY(exclusive_scan_u32(R->cnt.ptr, R->off.ptr, nr, R->scan_tmp.ptr, R->round_total.ptr + r, st));
-            k_round_list<<<ray_waves, 256, 0, st>>>(l_cur, n_cur, R->offsets.ptr, R->prog.ptr, R->cnt.ptr, R->off.ptr, R->qlist.ptr, R->qray.ptr);
+            k_round_list<<<ray_waves, 256, 0, st>>>(l_cur, n_cur, R->offsets.ptr, R->prog.ptr, R->cnt.ptr, R->off.ptr, R->qlist.ptr, slots ? nullptr : R->qray.ptr);
             NERF_LAUNCH_CHECK("k_round_list");
             // The field reads this round's sample count on the device: the low
             // word of the 64-bit scan total (little-endian; totals < 2^32).
