@@ -62,12 +62,12 @@ FIELD_FLOPS_PER_SAMPLE = 2 * (32 * 64 + 64 * 16) + 2 * (31 * 64 + 64 * 64 + 64 *
 # Traffic beyond L2 of the field kernel per sample on this workload, from
 # rocprofv3 FETCH_SIZE (x 2.0) + WRITE_SIZE (x 1.0) on one 800x800 render, the
 # factors being what the same counters read on a plain conversion kernel of
-# known size (profiles/field_forward_800x800_counters.md): 226.76 GB + 7.83 GB
+# known size (profiles/field_forward_800x800_counters.md): 217.52 GB + 7.83 GB
 # over 486,308,861 samples, summed over the render's dispatches.  The render
 # rounds list samples in spatial order, so neighbouring lanes share the coarse
 # levels' table lines and the traffic stays near the 540 algorithmic bytes
-# (57 % L2 hit).
-FIELD_TRAFFIC_BYTES_PER_SAMPLE = 482
+# (58 % L2 hit).
+FIELD_TRAFFIC_BYTES_PER_SAMPLE = 463
 # Reference-model network per sample, on the reference's own padded shapes
 # (backend-cuda.cu:23-54): density 64x128 + 4 x 128x128 + 128x16, colour
 # 48x128 + 2 x 128x128 + 128x16, two flops per multiply-add.
