@@ -310,10 +310,11 @@ typedef struct NerfExtRenderDesc {
     uint64_t chunk_samples;         /* Rays are marched, shaded and
                                        composited in chunks of whole blocks of
                                        1024 rays (a block is never split).
-                                       0: chunks of at most 2^30 ray steps
-                                       (rays x max_steps), each marched once
-                                       into per-ray slots (32 B per ray step
-                                       in the buffers).  Else: chunks of at
+                                       0: chunks of at most 2^30 slot
+                                       entries (rays x max_steps rounded up
+                                       to a power of two), each marched once
+                                       into per-ray slots (28 B per entry in
+                                       the buffers).  Else: chunks of at
                                        most this many samples (capped at
                                        2^29) after a count pass over all
                                        rays (32 B per sample) */
