@@ -2,9 +2,9 @@
 // streams, fused field evaluation, front-to-back compositing to RGBA8.
 //
 // Stages (one HIP stream); with the default chunk size 1-3 are one pass per
-// chunk of at most kSlotSamples ray steps, k_march_slots (eight lanes per
-// ray, the whole march, samples into per-ray slots of max_steps); with an
-// explicit sample budget per chunk:
+// chunk of at most kSlotSamples slot entries, k_march_slots (eight lanes per
+// ray, the whole march, samples into per-ray slots of max_steps rounded up
+// to a power of two); with an explicit sample budget per chunk:
 //   1. k_march_count   one thread per ray: pixel ray + AABB (backend-cuda.cu
 //                      :373-408, :561-563), occupancy march (:448-469),
 //                      per-ray occupied-step count; ray record (o, tn, d, tf).
@@ -615,7 +615,7 @@ hipError_t exclusive_scan_u32(const uint32_t* in, uint32_t* out, uint32_t n, uin
 constexpr uint32_t kFirstRound = 256u;  // samples per ray in the first round (a multiple of 64)
 constexpr uint32_t kScanBlockRays = 1024u;        // rays per block of the chunk plan (the scan's block)
 constexpr uint64_t kChunkSamples  = 1ull << 29;   // samples per chunk: 32 B each in the stream buffers (16 GiB)
-constexpr uint64_t kSlotSamples   = 1ull << 30;   // ray steps (rays x max_steps) per chunk of the default chunking, marched once into per-ray slots
+constexpr uint64_t kSlotSamples   = 1ull << 30;   // slot entries (rays x max_steps rounded up to a power of two) per chunk of the default chunking
 constexpr uint32_t kMaxSteps      = 1u << 19;     // so that a block of rays holds at most kChunkSamples samples
 constexpr uint32_t kMaxRounds  = 24u;   // round ends double from 256 (12 cover 2^19 steps), plus two
 
@@ -871,9 +871,9 @@ NERF_API NerfStatus nerf_ext_render(NerfExtRenderer* R, const NerfExtRenderDesc*
     const uint32_t n_blocks = (n_rays + kScanBlockRays - 1u) / kScanBlockRays;
     NERF_HIP_TRY(R->scan_tmp.reserve(std::max<uint64_t>(scan_tmp_words(n_rays), n_blocks)));
     // With the default chunk size the chunks are whole blocks of rays holding
-    // at most kSlotSamples ray steps (rays x max_steps), each marched once,
-    // into per-ray slots (k_march_slots): no count pass, no plan on the host,
-    // no scan.  Their buffers are sized by rays x max_steps.
+    // at most kSlotSamples slot entries, each marched once into per-ray
+    // slots of 2^slot_shift (k_march_slots): no count pass, no plan on the
+    // host, no scan.  Their buffers are sized by rays x 2^slot_shift.
     const bool slots = !d->chunk_samples;
     uint32_t slot_shift = 0u;  // slots of 2^slot_shift >= max_steps samples
     while ((1u << slot_shift) < d->max_steps) ++slot_shift;
