@@ -220,55 +220,58 @@ __global__ __launch_bounds__(256) void k_uniform_rays(const NerfExtCamera* __res
     counts[ray]           = count;
 }
 
-// One wave per ray: lane j writes samples j, j + 64, ... (coalesced).
-__global__ __launch_bounds__(256) void k_uniform_samples(uint32_t ray0, uint32_t ray_end, const float4* __restrict__ rays, const uint32_t* __restrict__ counts, const uint32_t* __restrict__ offsets,
-                                                        float2* __restrict__ samples, uint32_t* __restrict__ sample_ray) {
+// Sample layout of a chunk: its rays in groups of 64 neighbouring pixels
+// (lane = ray), each group's spp samples step-major, sample i of ray
+// ray0 + 64 g + l at (g spp + i) 64 + l, so that the field pass evaluates 64
+// neighbouring rays at one step per wave (in ray-major order every wave's
+// gathers were one ray's segment, whose fine-level corners are all fresh
+// lines).  One wave per group writes the (t_mid, dt) of :588-594 and the
+// owning ray; lanes past the chunk or of rays that miss the box get (0, 0)
+// and a valid ray (the field evaluates them, the composite skips them).
+__global__ __launch_bounds__(256) void k_uniform_samples(uint32_t ray0, uint32_t ray_end, uint32_t spp, const float4* __restrict__ rays, const uint32_t* __restrict__ counts, float2* __restrict__ samples,
+                                                        uint32_t* __restrict__ sample_ray) {
     const uint32_t lane = threadIdx.x & 63u, nw = gridDim.x * 4u;
-    for (uint32_t ray = ray0 + blockIdx.x * 4u + (threadIdx.x >> 6); ray < ray_end; ray += nw) {
-        const uint32_t count = counts[ray];
-        if (count == 0u) continue;
-        const float tn = rays[2ull * ray].w, tf = rays[2ull * ray + 1u].w;
-        const float dt = (tf - tn) / (float)count;
-        const uint32_t base = offsets[ray];
-        for (uint32_t i = lane; i < count; i += 64u) {
-            samples[base + i]    = make_float2(tn + ((float)i + 0.5f) * dt, dt);
-            sample_ray[base + i] = ray;
+    const uint32_t groups = (ray_end - ray0 + 63u) / 64u;
+    for (uint32_t g = blockIdx.x * 4u + (threadIdx.x >> 6); g < groups; g += nw) {
+        const uint32_t ray   = ray0 + g * 64u + lane;
+        const bool live      = ray < ray_end && counts[ray] > 0u;
+        const float tn       = live ? rays[2ull * ray].w : 0.0f;
+        const float tf       = live ? rays[2ull * ray + 1u].w : 0.0f;
+        const float dt       = live ? (tf - tn) / (float)spp : 0.0f;  // a live ray has spp samples
+        const uint32_t owner = ray < ray_end ? ray : ray_end - 1u;
+        const uint64_t base  = (uint64_t)g * spp * 64u + lane;
+        for (uint32_t i = 0; i < spp; ++i) {
+            samples[base + 64ull * i]    = live ? make_float2(tn + ((float)i + 0.5f) * dt, dt) : make_float2(0.0f, 0.0f);
+            sample_ray[base + 64ull * i] = owner;
         }
     }
 }
 
-// One wave per ray, 64 samples per step, front to back onto the carried
-// transmittance (wave-wide exclusive product of 1 - alpha), every sample
-// composited; then C + T bg, clamped, to RGBA8.
-__global__ __launch_bounds__(256) void k_uniform_composite(uint32_t ray0, uint32_t ray_end, const uint32_t* __restrict__ counts, const uint32_t* __restrict__ offsets, const float2* __restrict__ samples,
-                                                          const float4* __restrict__ field, float3 bg, uint32_t* __restrict__ rgba8, float* __restrict__ rgb_out) {
+// One wave per group of 64 rays (lane = ray), each lane compositing its
+// ray's samples front to back (:601-635, every sample composited), then
+// C + T bg, clamped, to RGBA8.  A step's loads are 64 consecutive outputs.
+__global__ __launch_bounds__(256) void k_uniform_composite(uint32_t ray0, uint32_t ray_end, uint32_t spp, const uint32_t* __restrict__ counts, const float2* __restrict__ samples, const float4* __restrict__ field,
+                                                          float3 bg, uint32_t* __restrict__ rgba8, float* __restrict__ rgb_out) {
     const uint32_t lane = threadIdx.x & 63u, nw = gridDim.x * 4u;
-    for (uint32_t ray = ray0 + blockIdx.x * 4u + (threadIdx.x >> 6); ray < ray_end; ray += nw) {
+    const uint32_t groups = (ray_end - ray0 + 63u) / 64u;
+    for (uint32_t g = blockIdx.x * 4u + (threadIdx.x >> 6); g < groups; g += nw) {
+        const uint32_t ray = ray0 + g * 64u + lane;
+        if (ray >= ray_end) continue;
         const uint32_t count = counts[ray];
-        const uint32_t base  = count ? offsets[ray] : 0u;
+        const uint64_t base  = (uint64_t)g * spp * 64u + lane;
         float T = 1.0f, cr = 0.0f, cg = 0.0f, cb = 0.0f;
-        for (uint32_t c0 = 0; c0 < count; c0 += 64u) {
-            const uint32_t i = c0 + lane;
-            const bool valid = i < count;
-            float4 f         = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            float dt         = 0.0f;
-            if (valid) {
-                f  = field[base + i];
-                dt = fmaxf(samples[base + i].y, 0.0f);
-            }
-            const float al   = valid ? 1.0f - __expf(-(f.x * dt)) : 0.0f;
-            const float incl = wave::inclusive_product(1.0f - al);
-            const float excl = wave::shift_up1(incl, 1.0f);
-            const float w    = T * excl * al;
+#pragma unroll 8
+        for (uint32_t i = 0; i < count; ++i) {
+            const float4 f = field[base + 64ull * i];
+            const float dt = fmaxf(samples[base + 64ull * i].y, 0.0f);
+            const float al = 1.0f - __expf(-(f.x * dt));
+            const float w  = T * al;
             cr += w * f.y;
             cg += w * f.z;
             cb += w * f.w;
-            T *= wave::broadcast(incl, 63u);
+            T *= 1.0f - al;
         }
-        cr = wave::sum(cr);
-        cg = wave::sum(cg);
-        cb = wave::sum(cb);
-        if (lane == 0u) write_pixel(ray, cr, cg, cb, T, bg, rgba8, rgb_out);
+        write_pixel(ray, cr, cg, cb, T, bg, rgba8, rgb_out);
     }
 }
 
@@ -1107,7 +1110,6 @@ NERF_API NerfStatus nerf_ext_render_uniform(NerfExtRenderer* R, const NerfExtMod
     in.samples    = R->samples.ptr;
     in.sample_ray = R->sample_ray.ptr;
     in.rays       = R->rays.ptr;
-    in.n_dev      = reinterpret_cast<const uint32_t*>(R->total.ptr);  // low word of the chunk's sample total
     for (int a = 0; a < 3; ++a) {
         in.bmin[a] = aabb6[a];
         in.bmax[a] = aabb6[3 + a];
@@ -1120,13 +1122,13 @@ NERF_API NerfStatus nerf_ext_render_uniform(NerfExtRenderer* R, const NerfExtMod
     const float3 bg = background3 ? make_float3(background3[0], background3[1], background3[2]) : make_float3(1.0f, 1.0f, 1.0f);
     for (uint32_t ray0 = 0; ray0 < n_rays; ray0 += chunk_rays) {
         const uint32_t ray_end = std::min(n_rays, ray0 + chunk_rays), nr = ray_end - ray0;
-        NERF_HIP_TRY(exclusive_scan_u32(R->counts.ptr + ray0, R->offsets.ptr + ray0, nr, R->scan_tmp.ptr, R->total.ptr, st));
-        const uint32_t waves = std::min<uint32_t>((nr + 3u) / 4u, device_cu_count() * 16u);
-        k_uniform_samples<<<waves, 256, 0, st>>>(ray0, ray_end, R->rays.ptr, R->counts.ptr, R->offsets.ptr, R->samples.ptr, R->sample_ray.ptr);
+        const uint32_t groups = (nr + 63u) / 64u, waves = std::min<uint32_t>((groups + 3u) / 4u, device_cu_count() * 16u);
+        const uint32_t n_smp  = (uint32_t)((uint64_t)groups * 64u * samples_per_ray);  // the groups' whole layout
+        k_uniform_samples<<<waves, 256, 0, st>>>(ray0, ray_end, samples_per_ray, R->rays.ptr, R->counts.ptr, R->samples.ptr, R->sample_ray.ptr);
         NERF_LAUNCH_CHECK("k_uniform_samples");
-        if (ref_model) NERF_HIP_TRY(launch_ref_field(R->ref_frags.ptr, in, (uint32_t)((uint64_t)nr * samples_per_ray), R->field.ptr, nullptr, st));
-        else NERF_HIP_TRY(launch_field(g, model->table, w, in, (uint32_t)((uint64_t)nr * samples_per_ray), R->field.ptr, st));
-        k_uniform_composite<<<waves, 256, 0, st>>>(ray0, ray_end, R->counts.ptr, R->offsets.ptr, R->samples.ptr, R->field.ptr, bg, rgba8, rgb_f32);
+        if (ref_model) NERF_HIP_TRY(launch_ref_field(R->ref_frags.ptr, in, n_smp, R->field.ptr, nullptr, st));
+        else NERF_HIP_TRY(launch_field(g, model->table, w, in, n_smp, R->field.ptr, st));
+        k_uniform_composite<<<waves, 256, 0, st>>>(ray0, ray_end, samples_per_ray, R->counts.ptr, R->samples.ptr, R->field.ptr, bg, rgba8, rgb_f32);
         NERF_LAUNCH_CHECK("k_uniform_composite");
     }
     return NERF_STATUS_OK;
