@@ -310,12 +310,13 @@ typedef struct NerfExtRenderDesc {
     uint64_t chunk_samples;         /* Rays are marched, shaded and
                                        composited in chunks of whole blocks of
                                        1024 rays (a block is never split).
-                                       0: chunks of at most 2^30 slot
-                                       entries (rays x max_steps rounded up
-                                       to a power of two), each marched once
-                                       into per-ray slots (28 B per entry in
-                                       the buffers).  Else: chunks of at
-                                       most this many samples (capped at
+                                       0 with max_steps <= 8192: chunks of
+                                       at most 2^30 slot entries (rays x
+                                       max_steps rounded up to a power of
+                                       two), each marched once into per-ray
+                                       slots (28 B per entry in the
+                                       buffers).  Else: chunks of at most
+                                       this many samples (0: 2^29; capped at
                                        2^29) after a count pass over all
                                        rays (32 B per sample) */
     uint32_t* composited;           /* optional device [view][H][W]: samples

@@ -618,6 +618,7 @@ hipError_t exclusive_scan_u32(const uint32_t* in, uint32_t* out, uint32_t n, uin
 constexpr uint32_t kFirstRound = 256u;  // samples per ray in the first round (a multiple of 64)
 constexpr uint32_t kScanBlockRays = 1024u;        // rays per block of the chunk plan (the scan's block)
 constexpr uint64_t kChunkSamples  = 1ull << 29;   // samples per chunk: 32 B each in the stream buffers (16 GiB)
+constexpr uint32_t kSlotMaxSteps  = 8192u;       // steps per ray up to which the default chunking uses slots
 constexpr uint64_t kSlotSamples   = 1ull << 30;   // slot entries (rays x max_steps rounded up to a power of two) per chunk of the default chunking
 constexpr uint32_t kMaxSteps      = 1u << 19;     // so that a block of rays holds at most kChunkSamples samples
 constexpr uint32_t kMaxRounds  = 24u;   // round ends double from 256 (12 cover 2^19 steps), plus two
@@ -873,11 +874,14 @@ NERF_API NerfStatus nerf_ext_render(NerfExtRenderer* R, const NerfExtRenderDesc*
     uint64_t total = 0, biggest = 0;
     const uint32_t n_blocks = (n_rays + kScanBlockRays - 1u) / kScanBlockRays;
     NERF_HIP_TRY(R->scan_tmp.reserve(std::max<uint64_t>(scan_tmp_words(n_rays), n_blocks)));
-    // With the default chunk size the chunks are whole blocks of rays holding
-    // at most kSlotSamples slot entries, each marched once into per-ray
-    // slots of 2^slot_shift (k_march_slots): no count pass, no plan on the
-    // host, no scan.  Their buffers are sized by rays x 2^slot_shift.
-    const bool slots = !d->chunk_samples;
+    // With the default chunk size and at most kSlotMaxSteps steps per ray the
+    // chunks are whole blocks of rays holding at most kSlotSamples slot
+    // entries, each marched once into per-ray slots of 2^slot_shift
+    // (k_march_slots): no count pass, no plan on the host, no scan.  Their
+    // buffers are sized by rays x 2^slot_shift, so longer marches (whose
+    // samples rarely fill their slots) keep the count pass and buffers sized
+    // by the samples.
+    const bool slots = !d->chunk_samples && d->max_steps <= kSlotMaxSteps;
     uint32_t slot_shift = 0u;  // slots of 2^slot_shift >= max_steps samples
     while ((1u << slot_shift) < d->max_steps) ++slot_shift;
     if (slots) {
